@@ -1,0 +1,106 @@
+#ifndef JAMHIP_H
+#define JAMHIP_H
+
+/* jamhip — jam's quantized matmul R = W @ Aᵀ on one AMD Instinct MI355X (gfx950).
+ *
+ * The drop-in boundary for jam's JAM SPI: a new jam backend ("hip") binds these entry points through
+ * Panama FFM exactly as NativeJAM binds libjam's jam_mm (jam/jam-native/src/main/java/com/qxotic/jam/
+ * NativeJAM.java:174-231). Plain C types only; every pointer is a raw address.
+ *
+ *   semantics : identical to jam_mm (jam/jam-native/include/jam.h:118-143). W [m×k] weights in a GGUF
+ *               block layout selected by `wt`, row stride ldw ELEMENTS; A [n×k] f32, stride lda; C f32
+ *               TOKEN-major: C[j*ldc + i] = dot(W[i,:], A[j,:]), ldc >= m, columns [m, ldc) untouched.
+ *               Activations are quantized to int8 exactly as jam's CPU path does: per-32 "F1"
+ *               (jam_q8_0_requant, jam_kernels_generic.c:71-94) for n < 8, per-32 "F2" with per-16 f32
+ *               sums (quantize_row_q8s, jam_kernels_q4k_avx512.c:25-37) for n >= 8, and each dtype's
+ *               per-block combine follows the matching jam kernel's decomposition.
+ *   dtypes    : W in {Q8_0, Q4_0, Q4_K, Q6_K, MXFP4}; A and C F32. Anything else -> JAMHIP_EUNSUPPORTED
+ *               (jinfer falls through to the next backend, MatMul.java:1822-1828).
+ *   residency : weights live on the GPU once pinned (jamhip_weight_pin). jamhip_mm on an unpinned W
+ *               stages it for that call only (correct, slow). Pinning uploads and repacks once into the
+ *               device layout; it is keyed by host address range, so the caller evicts before freeing or
+ *               rewriting a pinned range.
+ *   streams   : a context owns one HIP stream and its scratch: a SERIAL stream, as a jam_ctx is
+ *               (jam.h:16-20). A concurrent call on a busy context returns JAMHIP_EBUSY.
+ */
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* dtype tags: numerically jam_dtype / ggml_type (jam/jam-native/include/jam.h:59-77). */
+enum {
+    JAMHIP_F32 = 0, JAMHIP_F16 = 1, JAMHIP_Q4_0 = 2, JAMHIP_Q8_0 = 8, JAMHIP_Q4_K = 12,
+    JAMHIP_Q5_K = 13, JAMHIP_Q6_K = 14, JAMHIP_BF16 = 30, JAMHIP_MXFP4 = 39
+};
+
+/* status: numerically jam_status (jam.h:81-86; JAM.java:87). */
+typedef enum {
+    JAMHIP_OK = 0,
+    JAMHIP_EINVAL = 1,        /* null pointer, m/n/k <= 0, ldw < k, lda < k, ldc < m, HIP failure */
+    JAMHIP_EUNSUPPORTED = 2,  /* dtype combination or block misalignment; caller falls back */
+    JAMHIP_EBUSY = 3          /* another call is in flight on this context */
+} jamhip_status;
+
+typedef struct jamhip_ctx jamhip_ctx;
+
+/* 1 if a gfx950 device is visible and usable, else 0. Replaces the JAM.Provider.isAvailable probe
+ * (NativeJAMProvider.java:15-21 / JAM.java:65-71). Env JAM_HIP_DISABLE=1 forces 0. */
+int jamhip_device_available(void);
+
+/* Context on `device` (-1 = current). NULL on failure (see jamhip_last_error(NULL)).
+ * Mirrors jam_ctx_create/jam_ctx_destroy (jam.h:110-111). */
+jamhip_ctx* jamhip_ctx_create(int device);
+void        jamhip_ctx_destroy(jamhip_ctx* ctx);
+
+/* The device architecture string ("gfx950"); stands in for jam_active_isa/jam_isa_name (jam.h:146,92). */
+const char* jamhip_ctx_arch(const jamhip_ctx* ctx);
+
+/* Last error message of `ctx` (or of the last failed create when ctx == NULL). Never NULL. */
+const char* jamhip_last_error(const jamhip_ctx* ctx);
+
+/* The matmul, host pointers (jam_mm, jam.h:139-143; FFM descriptor NativeJAM.java:225-230).
+ * Synchronous: C is written when it returns. */
+jamhip_status jamhip_mm(jamhip_ctx* ctx,
+                        const void* w, int wt, int ldw,
+                        const void* a, int at, int lda,
+                        void*       c, int ct, int ldc,
+                        int m, int n, int k);
+
+/* Weight residency (no counterpart in jam: jam_mm borrows host memory per call, jam.h:24-25).
+ * pin: upload rows [0, m) of a host weight tensor (m rows of ldw elements, dtype wt) and repack it into
+ * the device layout; later calls whose W lies inside [w, w + span) at a row boundary with the same
+ * (wt, ldw) read the device copy. evict: drop the entry that starts at w. */
+jamhip_status jamhip_weight_pin(jamhip_ctx* ctx, const void* w, int wt, int ldw, int m);
+jamhip_status jamhip_weight_evict(jamhip_ctx* ctx, const void* w);
+/* Bytes of device memory held by pinned weights. */
+int64_t       jamhip_weight_bytes(const jamhip_ctx* ctx);
+
+/* Device-resident variant of jamhip_mm: W is a pinned host address (the registry key); A and C are
+ * device pointers; the work is queued on the context stream and NOT synchronized. Same validation and
+ * status codes as jamhip_mm. For callers that keep activations on the GPU (graph capture, benches). */
+jamhip_status jamhip_mm_device(jamhip_ctx* ctx,
+                               const void* w, int wt, int ldw,
+                               const void* a_dev, int at, int lda,
+                               void*       c_dev, int ct, int ldc,
+                               int m, int n, int k);
+
+/* jam's activation quantizers alone (device pointers, context stream, not synchronized); the matmul
+ * entry points run the same kernels internally. flavour 1 = F1 (jam_kernels_generic.c:71-94):
+ * q[n][k] int8, d[n][k/32], s[n][k/32] = (float)Σq. flavour 2 = F2 (jam_kernels_q4k_avx512.c:25-37):
+ * q[n][k], d[n][k/32], s[n][k/16] = raw f32 Σx per 16. k % 32 == 0. */
+jamhip_status jamhip_quantize_device(jamhip_ctx* ctx, int flavour, const void* a_dev, int lda, int n, int k,
+                                     void* q_dev, void* d_dev, void* s_dev);
+
+/* Use `stream` (a hipStream_t; NULL = the context's own) for subsequent work of this context. */
+jamhip_status jamhip_ctx_set_stream(jamhip_ctx* ctx, void* stream);
+void*         jamhip_ctx_stream(const jamhip_ctx* ctx);
+jamhip_status jamhip_ctx_synchronize(jamhip_ctx* ctx);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* JAMHIP_H */

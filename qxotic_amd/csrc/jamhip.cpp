@@ -1,0 +1,405 @@
+// C-ABI of the MI355X jam backend (include/jamhip.h): context, device weight registry, argument
+// validation in jam_mm's order, and dispatch to the HIP kernels. Host-side C++; compiled by hipcc.
+#include "jamhip.h"
+
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "common.h"
+#include "launch.h"
+
+using namespace jamhip;
+
+namespace {
+
+struct DevBuf {
+    void* p = nullptr;
+    size_t cap = 0;
+    hipError_t ensure(size_t bytes) {
+        if (bytes <= cap) return hipSuccess;
+        if (p) (void) hipFree(p);
+        p = nullptr;
+        cap = 0;
+        size_t want = bytes + bytes / 4;
+        hipError_t e = hipMalloc(&p, want);
+        if (e == hipSuccess) cap = want;
+        return e;
+    }
+    void release() {
+        if (p) (void) hipFree(p);
+        p = nullptr;
+        cap = 0;
+    }
+};
+
+struct Pin {
+    uintptr_t host;     // registry key: [host, host + span)
+    int64_t span;
+    int dt, ldw;
+    int64_t rows, rb;   // rows and blocks per row of the device copy
+    uint8_t* dev;       // plane 0
+    uint8_t* sc;        // plane 1 (nullptr for Q4_K)
+    int64_t bytes;      // device bytes held
+};
+
+constexpr int64_t align256(int64_t v) { return (v + 255) & ~int64_t(255); }
+
+bool supported_w(int dt) { return dt == Q8_0 || dt == Q4_0 || dt == Q4_K || dt == Q6_K || dt == MXFP4; }
+
+thread_local std::string g_create_error = "";
+
+}  // namespace
+
+struct jamhip_ctx {
+    int device = 0;
+    hipStream_t own = nullptr;
+    hipStream_t stream = nullptr;
+    std::atomic<int> busy{0};
+    std::string err;
+    char arch[64] = {0};
+    std::mutex pin_mu;
+    std::vector<Pin> pins;
+    DevBuf act, a_stage, c_stage, w_raw, w_stage;
+};
+
+namespace {
+
+jamhip_status fail(jamhip_ctx* ctx, jamhip_status st, const std::string& msg) {
+    if (ctx) ctx->err = msg;
+    return st;
+}
+
+jamhip_status hip_fail(jamhip_ctx* ctx, hipError_t e, const char* what) {
+    return fail(ctx, JAMHIP_EINVAL, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+struct Busy {   // the serial-stream guard of jam_mm (jam/jam-native/src/jam.c:777-783)
+    jamhip_ctx* c;
+    bool ok;
+    explicit Busy(jamhip_ctx* ctx) : c(ctx), ok(ctx->busy.exchange(1, std::memory_order_acquire) == 0) {}
+    ~Busy() {
+        if (ok) c->busy.store(0, std::memory_order_release);
+    }
+};
+
+// jam_mm's EINVAL contract (jam.c:771-775), then the dtype/alignment EUNSUPPORTED classes (jam.c:759-762).
+jamhip_status validate(jamhip_ctx* ctx, const void* w, int wt, int ldw, const void* a, int at, int lda, void* c,
+                       int ct, int ldc, int m, int n, int k) {
+    if (!ctx) return JAMHIP_EINVAL;
+    if (!w || !a || !c) return fail(ctx, JAMHIP_EINVAL, "null operand");
+    if (m <= 0 || n <= 0 || k <= 0) return fail(ctx, JAMHIP_EINVAL, "m, n, k must be positive");
+    if (ldw < k || lda < k || ldc < m) return fail(ctx, JAMHIP_EINVAL, "stride below extent (ldw<k, lda<k or ldc<m)");
+    if (at != F32 || ct != F32) return fail(ctx, JAMHIP_EUNSUPPORTED, "A and C must be F32");
+    if (!supported_w(wt)) return fail(ctx, JAMHIP_EUNSUPPORTED, "weight dtype not supported on the GPU backend");
+    const int be = block_elems(wt);
+    if (k % be || ldw % be) return fail(ctx, JAMHIP_EUNSUPPORTED, "k and ldw must be multiples of the block size");
+    return JAMHIP_OK;
+}
+
+int64_t row_bytes(int dt, int64_t elems) { return elems / block_elems(dt) * block_bytes(dt); }
+
+// Registry lookup: W inside a pinned range, on a row boundary, same (dtype, ldw), rows [r0, r0+m) held.
+bool lookup(jamhip_ctx* ctx, const void* w, int dt, int ldw, int m, WeightView* out) {
+    std::lock_guard<std::mutex> lk(ctx->pin_mu);
+    const uintptr_t p = reinterpret_cast<uintptr_t>(w);
+    for (const Pin& pin : ctx->pins) {
+        if (pin.dt != dt || pin.ldw != ldw || p < pin.host || p >= pin.host + (uintptr_t) pin.span) continue;
+        const int64_t off = (int64_t) (p - pin.host), rbytes = row_bytes(dt, ldw);
+        if (off % rbytes) continue;
+        const int64_t r0 = off / rbytes;
+        if (r0 + m > pin.rows) continue;
+        out->qs = pin.dev + r0 * pin.rb * qs_bytes(dt);
+        out->sc = pin.sc ? pin.sc + r0 * pin.rb * sc_bytes(dt) : nullptr;
+        out->rb = pin.rb;
+        return true;
+    }
+    return false;
+}
+
+// Upload `rows` raw host rows (stride raw_stride bytes, rb blocks used per row) into a device-layout
+// buffer at dst (plane 0) / dst_sc (plane 1) via a staging copy and the repack kernel.
+jamhip_status upload(jamhip_ctx* ctx, const uint8_t* host, int dt, int64_t raw_stride, int64_t rows, int64_t rb,
+                     uint8_t* dst, uint8_t* dst_sc) {
+    const int64_t span = (rows - 1) * raw_stride + rb * block_bytes(dt);
+    hipError_t e;
+    if (dt == Q4_K) {   // whole blocks are the device layout
+        if (raw_stride == rb * 144) {
+            e = hipMemcpyAsync(dst, host, (size_t) span, hipMemcpyHostToDevice, ctx->stream);
+        } else {
+            e = hipMemcpy2DAsync(dst, (size_t) (rb * 144), host, (size_t) raw_stride, (size_t) (rb * 144),
+                                 (size_t) rows, hipMemcpyHostToDevice, ctx->stream);
+        }
+        if (e != hipSuccess) return hip_fail(ctx, e, "weight upload");
+        return JAMHIP_OK;
+    }
+    if ((e = ctx->w_raw.ensure((size_t) span)) != hipSuccess) return hip_fail(ctx, e, "weight staging alloc");
+    if ((e = hipMemcpyAsync(ctx->w_raw.p, host, (size_t) span, hipMemcpyHostToDevice, ctx->stream)) != hipSuccess)
+        return hip_fail(ctx, e, "weight upload");
+    if ((e = launch_repack(dt, (const uint8_t*) ctx->w_raw.p, raw_stride, rows, rb, dst, dst_sc, ctx->stream)) !=
+        hipSuccess)
+        return hip_fail(ctx, e, "weight repack");
+    return JAMHIP_OK;
+}
+
+// Resolve W to a device view: the registry, else a per-call staged copy of rows [0, m), k elements each.
+jamhip_status resolve_w(jamhip_ctx* ctx, const void* w, int dt, int ldw, int m, int k, WeightView* wv) {
+    if (lookup(ctx, w, dt, ldw, m, wv)) return JAMHIP_OK;
+    const int64_t rb = k / block_elems(dt);
+    const int64_t qsz = align256((int64_t) m * rb * qs_bytes(dt)), ssz = (int64_t) m * rb * sc_bytes(dt);
+    hipError_t e = ctx->w_stage.ensure((size_t) (qsz + ssz));
+    if (e != hipSuccess) return hip_fail(ctx, e, "weight stage alloc");
+    uint8_t* dst = (uint8_t*) ctx->w_stage.p;
+    uint8_t* dsc = sc_bytes(dt) ? dst + qsz : nullptr;
+    jamhip_status st = upload(ctx, (const uint8_t*) w, dt, row_bytes(dt, ldw), m, rb, dst, dsc);
+    if (st != JAMHIP_OK) return st;
+    wv->qs = dst;
+    wv->sc = dsc;
+    wv->rb = rb;
+    return JAMHIP_OK;
+}
+
+// Quantize A (device, f32 [n][lda]) and run the matmul into C (device, [n][ldc]). Decode-sized calls
+// are one fused launch and touch no scratch (safe under stream capture once W is pinned).
+jamhip_status compute(jamhip_ctx* ctx, int dt, const WeightView& wv, const float* a, int lda, float* c, int ldc,
+                      int m, int n, int k) {
+    hipError_t e;
+    if (gemv_fusable(n, k)) {
+        if ((e = launch_gemv(dt, 1, wv, ActQ{}, a, lda, k, m, n, c, ldc, ctx->stream)) != hipSuccess)
+            return hip_fail(ctx, e, "gemv launch");
+        return JAMHIP_OK;
+    }
+    const int64_t nb = k / 32;
+    const int64_t qb = align256((int64_t) n * k), db = align256(n * nb * 4), sb = align256((int64_t) n * (k / 16) * 4);
+    if ((e = ctx->act.ensure((size_t) (qb + db + 2 * sb))) != hipSuccess)
+        return hip_fail(ctx, e, "activation scratch alloc");
+    uint8_t* base = (uint8_t*) ctx->act.p;
+    int8_t* q = (int8_t*) base;
+    float* d = (float*) (base + qb);
+    float* s = (float*) (base + qb + db);
+    int* s16 = (int*) (base + qb + db + sb);
+    const ActQ A{q, d, s, s16};
+    if (n < 8) {
+        if ((e = launch_quant_f1(a, lda, n, k, q, d, s, s16, ctx->stream)) != hipSuccess)
+            return hip_fail(ctx, e, "quant_f1 launch");
+        if ((e = launch_gemv(dt, 1, wv, A, nullptr, 0, k, m, n, c, ldc, ctx->stream)) != hipSuccess)
+            return hip_fail(ctx, e, "gemv launch");
+        return JAMHIP_OK;
+    }
+    if ((e = launch_quant_f2(a, lda, n, k, q, d, s, ctx->stream)) != hipSuccess)
+        return hip_fail(ctx, e, "quant_f2 launch");
+    e = n >= 32 ? launch_gemm(dt, wv, A, k, m, n, c, ldc, ctx->stream) : hipErrorNotSupported;
+    if (e == hipErrorNotSupported) e = launch_gemv(dt, 2, wv, A, nullptr, 0, k, m, n, c, ldc, ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "matmul launch");
+    return JAMHIP_OK;
+}
+
+bool env_true(const char* name) {
+    const char* v = getenv(name);
+    return v && (!strcmp(v, "1") || !strcasecmp(v, "true") || !strcasecmp(v, "yes"));
+}
+
+}  // namespace
+
+extern "C" {
+
+int jamhip_device_available(void) {
+    if (env_true("JAM_HIP_DISABLE")) return 0;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return 0;
+    hipDeviceProp_t prop;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&prop, dev) != hipSuccess) return 0;
+    return strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : 0;
+}
+
+jamhip_ctx* jamhip_ctx_create(int device) {
+    if (env_true("JAM_HIP_DISABLE")) {
+        g_create_error = "disabled by JAM_HIP_DISABLE";
+        return nullptr;
+    }
+    int dev = device;
+    if (dev < 0 && hipGetDevice(&dev) != hipSuccess) {
+        g_create_error = "no HIP device";
+        return nullptr;
+    }
+    hipDeviceProp_t prop;
+    if (hipSetDevice(dev) != hipSuccess || hipGetDeviceProperties(&prop, dev) != hipSuccess) {
+        g_create_error = "hipSetDevice/hipGetDeviceProperties failed";
+        return nullptr;
+    }
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        g_create_error = std::string("unsupported device architecture ") + prop.gcnArchName + " (need gfx950)";
+        return nullptr;
+    }
+    auto* ctx = new jamhip_ctx();
+    ctx->device = dev;
+    snprintf(ctx->arch, sizeof ctx->arch, "%s", prop.gcnArchName);
+    if (hipStreamCreate(&ctx->own) != hipSuccess) {
+        g_create_error = "hipStreamCreate failed";
+        delete ctx;
+        return nullptr;
+    }
+    ctx->stream = ctx->own;
+    return ctx;
+}
+
+void jamhip_ctx_destroy(jamhip_ctx* ctx) {
+    if (!ctx) return;
+    (void) hipSetDevice(ctx->device);
+    (void) hipStreamSynchronize(ctx->stream);
+    for (Pin& p : ctx->pins) (void) hipFree(p.dev);
+    ctx->pins.clear();
+    ctx->act.release();
+    ctx->a_stage.release();
+    ctx->c_stage.release();
+    ctx->w_raw.release();
+    ctx->w_stage.release();
+    if (ctx->own) (void) hipStreamDestroy(ctx->own);
+    delete ctx;
+}
+
+const char* jamhip_ctx_arch(const jamhip_ctx* ctx) { return ctx ? ctx->arch : ""; }
+
+const char* jamhip_last_error(const jamhip_ctx* ctx) { return ctx ? ctx->err.c_str() : g_create_error.c_str(); }
+
+jamhip_status jamhip_mm(jamhip_ctx* ctx, const void* w, int wt, int ldw, const void* a, int at, int lda, void* c,
+                        int ct, int ldc, int m, int n, int k) {
+    jamhip_status st = validate(ctx, w, wt, ldw, a, at, lda, c, ct, ldc, m, n, k);
+    if (st != JAMHIP_OK) return st;
+    Busy guard(ctx);
+    if (!guard.ok) return fail(ctx, JAMHIP_EBUSY, "context busy");
+    (void) hipSetDevice(ctx->device);
+    WeightView wv;
+    if ((st = resolve_w(ctx, w, wt, ldw, m, k, &wv)) != JAMHIP_OK) return st;
+    hipError_t e;
+    if ((e = ctx->a_stage.ensure((size_t) n * k * 4)) != hipSuccess) return hip_fail(ctx, e, "A staging alloc");
+    if ((e = ctx->c_stage.ensure((size_t) n * m * 4)) != hipSuccess) return hip_fail(ctx, e, "C staging alloc");
+    if ((e = hipMemcpy2DAsync(ctx->a_stage.p, (size_t) k * 4, a, (size_t) lda * 4, (size_t) k * 4, (size_t) n,
+                              hipMemcpyHostToDevice, ctx->stream)) != hipSuccess)
+        return hip_fail(ctx, e, "A upload");
+    if ((st = compute(ctx, wt, wv, (const float*) ctx->a_stage.p, k, (float*) ctx->c_stage.p, m, m, n, k)) != JAMHIP_OK)
+        return st;
+    // C columns [m, ldc) stay untouched (jam.h:131-138): a pitched copy of m floats per token.
+    if ((e = hipMemcpy2DAsync(c, (size_t) ldc * 4, ctx->c_stage.p, (size_t) m * 4, (size_t) m * 4, (size_t) n,
+                              hipMemcpyDeviceToHost, ctx->stream)) != hipSuccess)
+        return hip_fail(ctx, e, "C download");
+    if ((e = hipStreamSynchronize(ctx->stream)) != hipSuccess) return hip_fail(ctx, e, "stream sync");
+    return JAMHIP_OK;
+}
+
+jamhip_status jamhip_mm_device(jamhip_ctx* ctx, const void* w, int wt, int ldw, const void* a_dev, int at, int lda,
+                               void* c_dev, int ct, int ldc, int m, int n, int k) {
+    jamhip_status st = validate(ctx, w, wt, ldw, a_dev, at, lda, c_dev, ct, ldc, m, n, k);
+    if (st != JAMHIP_OK) return st;
+    Busy guard(ctx);
+    if (!guard.ok) return fail(ctx, JAMHIP_EBUSY, "context busy");
+    (void) hipSetDevice(ctx->device);
+    WeightView wv;
+    if ((st = resolve_w(ctx, w, wt, ldw, m, k, &wv)) != JAMHIP_OK) return st;
+    return compute(ctx, wt, wv, (const float*) a_dev, lda, (float*) c_dev, ldc, m, n, k);
+}
+
+jamhip_status jamhip_weight_pin(jamhip_ctx* ctx, const void* w, int wt, int ldw, int m) {
+    if (!ctx) return JAMHIP_EINVAL;
+    if (!w || m <= 0 || ldw <= 0) return fail(ctx, JAMHIP_EINVAL, "pin: null weight or empty shape");
+    if (!supported_w(wt)) return fail(ctx, JAMHIP_EUNSUPPORTED, "pin: weight dtype not supported");
+    if (ldw % block_elems(wt)) return fail(ctx, JAMHIP_EUNSUPPORTED, "pin: ldw not a block multiple");
+    Busy guard(ctx);
+    if (!guard.ok) return fail(ctx, JAMHIP_EBUSY, "context busy");
+    (void) hipSetDevice(ctx->device);
+    const uintptr_t host = reinterpret_cast<uintptr_t>(w);
+    const int64_t rb = ldw / block_elems(wt), span = (int64_t) m * row_bytes(wt, ldw);
+    {
+        std::lock_guard<std::mutex> lk(ctx->pin_mu);
+        for (const Pin& p : ctx->pins) {
+            if (p.host == host && p.dt == wt && p.ldw == ldw && p.rows == m) return JAMHIP_OK;   // already pinned
+            if (host < p.host + (uintptr_t) p.span && p.host < host + (uintptr_t) span)
+                return fail(ctx, JAMHIP_EINVAL, "pin: range overlaps a pinned tensor (evict it first)");
+        }
+    }
+    const int64_t qsz = align256((int64_t) m * rb * qs_bytes(wt)), ssz = (int64_t) m * rb * sc_bytes(wt);
+    uint8_t* dev = nullptr;
+    hipError_t e = hipMalloc((void**) &dev, (size_t) (qsz + ssz));
+    if (e != hipSuccess) return hip_fail(ctx, e, "pin: device alloc");
+    uint8_t* sc = sc_bytes(wt) ? dev + qsz : nullptr;
+    jamhip_status st = upload(ctx, (const uint8_t*) w, wt, row_bytes(wt, ldw), m, rb, dev, sc);
+    if (st == JAMHIP_OK && (e = hipStreamSynchronize(ctx->stream)) != hipSuccess) st = hip_fail(ctx, e, "pin: sync");
+    if (st != JAMHIP_OK) {
+        (void) hipFree(dev);
+        return st;
+    }
+    ctx->w_raw.release();   // staging is sized to the tensor; do not hold it
+    std::lock_guard<std::mutex> lk(ctx->pin_mu);
+    ctx->pins.push_back(Pin{host, span, wt, ldw, m, rb, dev, sc, qsz + ssz});
+    return JAMHIP_OK;
+}
+
+jamhip_status jamhip_weight_evict(jamhip_ctx* ctx, const void* w) {
+    if (!ctx || !w) return JAMHIP_EINVAL;
+    Busy guard(ctx);
+    if (!guard.ok) return fail(ctx, JAMHIP_EBUSY, "context busy");
+    (void) hipSetDevice(ctx->device);
+    std::lock_guard<std::mutex> lk(ctx->pin_mu);
+    for (size_t i = 0; i < ctx->pins.size(); i++) {
+        if (ctx->pins[i].host == reinterpret_cast<uintptr_t>(w)) {
+            (void) hipStreamSynchronize(ctx->stream);
+            (void) hipFree(ctx->pins[i].dev);
+            ctx->pins.erase(ctx->pins.begin() + (long) i);
+            return JAMHIP_OK;
+        }
+    }
+    return fail(ctx, JAMHIP_EINVAL, "evict: no pinned tensor starts at this address");
+}
+
+int64_t jamhip_weight_bytes(const jamhip_ctx* ctx) {
+    if (!ctx) return 0;
+    int64_t s = 0;
+    for (const Pin& p : ctx->pins) s += p.bytes;
+    return s;
+}
+
+jamhip_status jamhip_quantize_device(jamhip_ctx* ctx, int flavour, const void* a_dev, int lda, int n, int k,
+                                     void* q_dev, void* d_dev, void* s_dev) {
+    if (!ctx) return JAMHIP_EINVAL;
+    if (!a_dev || !q_dev || !d_dev || !s_dev) return fail(ctx, JAMHIP_EINVAL, "quantize: null pointer");
+    if (n <= 0 || k <= 0 || lda < k) return fail(ctx, JAMHIP_EINVAL, "quantize: bad shape");
+    if (k % 32) return fail(ctx, JAMHIP_EUNSUPPORTED, "quantize: k must be a multiple of 32");
+    if (flavour != 1 && flavour != 2) return fail(ctx, JAMHIP_EINVAL, "quantize: flavour must be 1 or 2");
+    Busy guard(ctx);
+    if (!guard.ok) return fail(ctx, JAMHIP_EBUSY, "context busy");
+    (void) hipSetDevice(ctx->device);
+    hipError_t e;
+    if (flavour == 1) {
+        if ((e = ctx->act.ensure((size_t) n * (k / 16) * 4)) != hipSuccess) return hip_fail(ctx, e, "scratch alloc");
+        e = launch_quant_f1((const float*) a_dev, lda, n, k, (int8_t*) q_dev, (float*) d_dev, (float*) s_dev,
+                            (int*) ctx->act.p, ctx->stream);
+    } else {
+        e = launch_quant_f2((const float*) a_dev, lda, n, k, (int8_t*) q_dev, (float*) d_dev, (float*) s_dev,
+                            ctx->stream);
+    }
+    return e == hipSuccess ? JAMHIP_OK : hip_fail(ctx, e, "quantize launch");
+}
+
+jamhip_status jamhip_ctx_set_stream(jamhip_ctx* ctx, void* stream) {
+    if (!ctx) return JAMHIP_EINVAL;
+    ctx->stream = stream ? (hipStream_t) stream : ctx->own;
+    return JAMHIP_OK;
+}
+
+void* jamhip_ctx_stream(const jamhip_ctx* ctx) { return ctx ? (void*) ctx->stream : nullptr; }
+
+jamhip_status jamhip_ctx_synchronize(jamhip_ctx* ctx) {
+    if (!ctx) return JAMHIP_EINVAL;
+    (void) hipSetDevice(ctx->device);
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    return e == hipSuccess ? JAMHIP_OK : hip_fail(ctx, e, "sync");
+}
+
+}  // extern "C"

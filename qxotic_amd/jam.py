@@ -1,0 +1,256 @@
+"""Host-side mirror of jam's backend SPI for the MI355X backend.
+
+Mirrors, name for name, the Java contract a jam backend implements:
+
+* ``JAM`` constants and ``JAM.mm`` (jam/jam-core/src/main/java/com/qxotic/jam/JAM.java:74-115);
+* ``Provider`` / ``providers()`` discovery with ``jam.<id>.disabled`` (JAM.java:21-71), here read from
+  the environment as ``JAM_<ID>_DISABLED`` (the NativeLoader config convention,
+  jam/jam-native/src/main/java/com/qxotic/jam/NativeLoader.java:344-349);
+* ``HipJAM.mm`` with NativeJAM's argument handling (NativeJAM.java:63-152): heap (non-native) operands
+  raise ``IllegalArgumentError``; undersized operands raise ``IndexOutOfBoundsError`` before any native
+  call, sized by ``GGMLType.span_bytes``; concurrent callers serialize FIFO unless
+  ``JAM_HIP_SERIAL=false``, in which case a contended call returns ``EBUSY`` from the native guard.
+
+Operands are ``Segment`` objects: a raw host address plus byte size (what a ``MemorySegment`` carries
+across the FFM boundary). ``Segment.of(ndarray)`` wraps C-contiguous numpy memory.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import threading
+from dataclasses import dataclass
+from typing import Any
+
+import numpy as np
+
+from . import ggml
+from ._lib import lib
+
+
+class JAM:
+    """Constants of the JAM contract (JAM.java:74-87)."""
+
+    F32, F16, BF16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, MXFP4, NVFP4, Q1_0 = 0, 1, 30, 2, 8, 12, 13, 14, 39, 40, 41
+    OK, EINVAL, EUNSUPPORTED, EBUSY = 0, 1, 2, 3
+
+
+class IllegalArgumentError(ValueError):
+    """java.lang.IllegalArgumentException (NativeJAM.requireNative, NativeJAM.java:115-122)."""
+
+
+class IndexOutOfBoundsError(IndexError):
+    """java.lang.IndexOutOfBoundsException (NativeJAM.checkSegment, NativeJAM.java:130-152)."""
+
+
+@dataclass(frozen=True)
+class Segment:
+    """A native memory segment: address + byte size (+ an owner kept alive while referenced)."""
+
+    address: int
+    byte_size: int
+    native: bool = True
+    owner: Any = None
+
+    @staticmethod
+    def of(arr: np.ndarray) -> "Segment":
+        if not isinstance(arr, np.ndarray) or not arr.flags.c_contiguous:
+            return Segment(0, 0, native=False, owner=arr)
+        return Segment(arr.ctypes.data, arr.nbytes, True, arr)
+
+    @staticmethod
+    def heap(obj: Any) -> "Segment":
+        """A heap-backed segment: has no native address (rejected by mm)."""
+        return Segment(0, 0, native=False, owner=obj)
+
+    def is_native(self) -> bool:
+        return self.native
+
+
+def _config(key: str, default: str) -> str:
+    """`jam.x.y` property convention read as env JAM_X_Y (NativeLoader.java:344-349)."""
+    return os.environ.get(key.upper().replace(".", "_"), default)
+
+
+class _FairLock:
+    """FIFO lock (ReentrantLock(true) in NativeJAM.java:55)."""
+
+    def __init__(self):
+        self._cv = threading.Condition()
+        self._next = 0
+        self._serving = 0
+
+    def __enter__(self):
+        with self._cv:
+            ticket = self._next
+            self._next += 1
+            while ticket != self._serving:
+                self._cv.wait()
+
+    def __exit__(self, *exc):
+        with self._cv:
+            self._serving += 1
+            self._cv.notify_all()
+
+
+class HipJAM:
+    """The MI355X backend behind the JAM contract. One context = one HIP stream (a serial stream)."""
+
+    def __init__(self, device: int = -1):
+        L = lib()
+        self._ctx = L.jamhip_ctx_create(device)
+        if not self._ctx:
+            raise RuntimeError("jamhip_ctx_create: " + L.jamhip_last_error(None).decode())
+        self._serial = _config("jam.hip.serial", "true").lower() == "true"
+        self._lock = _FairLock() if self._serial else None
+
+    # -- lifecycle -------------------------------------------------------------------------------
+    def close(self):
+        if self._ctx:
+            lib().jamhip_ctx_destroy(self._ctx)
+            self._ctx = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def ctx(self) -> int:
+        return self._ctx
+
+    def arch(self) -> str:
+        return lib().jamhip_ctx_arch(self._ctx).decode()
+
+    def last_error(self) -> str:
+        return lib().jamhip_last_error(self._ctx).decode()
+
+    # -- the contract ----------------------------------------------------------------------------
+    def mm(self, w: Segment, w_off: int, wt: int, ldw: int, a: Segment, a_off: int, at: int, lda: int,
+           r: Segment, r_off: int, rt: int, ldr: int, m: int, n: int, k: int) -> int:
+        """R = W @ A^T; byte offsets, ELEMENT strides; returns a jam_status (JAM.java:95-110)."""
+        _require_native(w, "weight W")
+        _require_native(a, "activation A")
+        _require_native(r, "result R")
+        if m > 0 and n > 0 and k > 0 and ldw >= k and lda >= k and ldr >= m:   # else native -> EINVAL
+            _check_segment("weight W", w, w_off, wt, ldw, m, k)
+            _check_segment("activation A", a, a_off, at, lda, n, k)
+            _check_segment("result R", r, r_off, rt, ldr, n, m)
+        args = (self._ctx, w.address + w_off, wt, ldw, a.address + a_off, at, lda, r.address + r_off, rt, ldr, m, n, k)
+        if self._lock is not None:
+            with self._lock:
+                return lib().jamhip_mm(*args)
+        return lib().jamhip_mm(*args)
+
+    def mm_contiguous(self, w: Segment, a: Segment, r: Segment, wt: int, m: int, n: int, k: int) -> int:
+        """Offsets 0, strides k/k/m, F32 activations and result (JAM.java:113-115)."""
+        return self.mm(w, 0, wt, k, a, 0, JAM.F32, k, r, 0, JAM.F32, m, m, n, k)
+
+    # -- residency extensions (no JAM counterpart) -------------------------------------------------
+    def pin(self, w: Segment, wt: int, ldw: int, m: int) -> int:
+        _require_native(w, "weight W")
+        g = ggml.by_code(wt)
+        if g is not None and m > 0 and ldw > 0 and m * g.row_bytes(ldw) > w.byte_size:
+            raise IndexOutOfBoundsError(f"pin: weight segment too small — need {m * g.row_bytes(ldw)} B, "
+                                        f"segment is {w.byte_size} B")
+        return lib().jamhip_weight_pin(self._ctx, w.address, wt, ldw, m)
+
+    def evict(self, w: Segment) -> int:
+        return lib().jamhip_weight_evict(self._ctx, w.address)
+
+    def pinned_bytes(self) -> int:
+        return lib().jamhip_weight_bytes(self._ctx)
+
+    # -- device-resident path (torch tensors or raw device addresses) ------------------------------
+    def mm_device(self, w: Segment, wt: int, ldw: int, a_dev: int, lda: int, c_dev: int, ldc: int,
+                  m: int, n: int, k: int) -> int:
+        return lib().jamhip_mm_device(self._ctx, w.address, wt, ldw, a_dev, JAM.F32, lda, c_dev, JAM.F32, ldc,
+                                      m, n, k)
+
+    def quantize_device(self, flavour: int, a_dev: int, lda: int, n: int, k: int, q_dev: int, d_dev: int,
+                        s_dev: int) -> int:
+        return lib().jamhip_quantize_device(self._ctx, flavour, a_dev, lda, n, k, q_dev, d_dev, s_dev)
+
+    def set_stream(self, stream: int | None) -> int:
+        return lib().jamhip_ctx_set_stream(self._ctx, stream)
+
+    def stream(self) -> int:
+        return lib().jamhip_ctx_stream(self._ctx)
+
+    def synchronize(self) -> int:
+        return lib().jamhip_ctx_synchronize(self._ctx)
+
+
+def _require_native(seg: Segment, which: str) -> None:
+    if not isinstance(seg, Segment) or not seg.is_native():
+        raise IllegalArgumentError(f"jam.mm: {which} must be a NATIVE (off-heap) MemorySegment — heap/array-backed "
+                                   "has no native address")
+
+
+def _check_segment(which: str, seg: Segment, off: int, dt: int, stride: int, rows: int, row_elems: int) -> None:
+    g = ggml.by_code(dt)
+    if g is None:
+        return   # unrecognized dtype: native classifies it
+    need = g.span_bytes(rows, stride, row_elems)
+    if off < 0 or off > seg.byte_size - need:
+        raise IndexOutOfBoundsError(f"jam.mm: {which} segment too small — need {need} B at offset {off}, "
+                                    f"segment is {seg.byte_size} B")
+
+
+# ------------------------------------------------------------------------------------ discovery
+class Provider:
+    """JAM.Provider (JAM.java:21-38) for the MI355X backend."""
+
+    def id(self) -> str:
+        return "hip"
+
+    def priority(self) -> int:
+        return 2000   # above native (1000), vector (500), scalar (0)
+
+    def is_available(self) -> bool:
+        return bool(lib().jamhip_device_available())
+
+    def create(self) -> HipJAM:
+        return _shared()
+
+
+_SHARED: HipJAM | None = None
+_SHARED_LOCK = threading.Lock()
+
+
+def _shared() -> HipJAM:
+    global _SHARED
+    with _SHARED_LOCK:
+        if _SHARED is None:
+            _SHARED = HipJAM()
+        return _SHARED
+
+
+def _disabled(p) -> bool:
+    return _config(f"jam.{p.id()}.disabled", "false").lower() == "true"
+
+
+def _available(p) -> bool:
+    try:
+        return bool(p.is_available())
+    except Exception:
+        return False
+
+
+def providers(candidates=None) -> list:
+    """Available providers, highest priority first; disabled ones are dropped BEFORE probing
+    (JAM.java:52-71)."""
+    ps = [Provider()] if candidates is None else list(candidates)
+    ps = [p for p in ps if not _disabled(p)]
+    ps = [p for p in ps if _available(p)]
+    return sorted(ps, key=lambda p: p.priority(), reverse=True)
+
+
+def addr(x) -> int:
+    """Device address of a torch tensor (or pass-through int)."""
+    return x if isinstance(x, int) else int(x.data_ptr())
+
+
+__all__ = ["JAM", "HipJAM", "Provider", "providers", "Segment", "IllegalArgumentError", "IndexOutOfBoundsError",
+           "addr", "C"]

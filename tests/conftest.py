@@ -1,0 +1,73 @@
+import subprocess
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+sys.path.insert(0, str(ROOT))
+
+from oracle import oracle as O  # noqa: E402  (test infrastructure)
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (run on the GPU box)")
+
+
+def _ensure_oracle():
+    if not O.ORACLE_SO.exists():
+        subprocess.run(["make", "-C", str(ROOT / "oracle"), "oracle"], check=True, capture_output=True)
+
+
+@pytest.fixture(scope="session")
+def oracle():
+    _ensure_oracle()
+    return O.Oracle()
+
+
+@pytest.fixture(scope="session")
+def refjam():
+    if not O.ref_available():
+        pytest.skip("oracle/_ref/libjam.so not built (reference sources absent when built)")
+    r = O.RefJam(nthreads=4)
+    yield r
+    r.close()
+
+
+@pytest.fixture(scope="session")
+def refjam_generic():
+    """libjam capped to its portable float floor (JAM_ISA_GENERIC): exact float dots of the dequantized
+    weights (jam_kernels_generic.c:42-321)."""
+    if not O.ref_available():
+        pytest.skip("oracle/_ref/libjam.so not built")
+    r = O.RefJam(nthreads=2, max_isa=1)
+    yield r
+    r.close()
+
+
+@pytest.fixture(scope="session")
+def hip():
+    from qxotic_amd.jam import HipJAM
+    h = HipJAM()
+    yield h
+    h.close()
+
+
+def adversarial_activations(k: int = 256) -> np.ndarray:
+    """Rows that stress the per-32 quantizers (jam_test.c:392-420, 355-390): zero block, all-equal,
+    tiny scale, exact .5 ties at d=1, saturation, mixed signs, huge range."""
+    rows = []
+    z = np.zeros(k, np.float32)
+    rows.append(z.copy())                                        # all zero -> d=0, q=0
+    rows.append(np.full(k, 0.75, np.float32))                    # all equal -> +127
+    rows.append(np.full(k, -3.0, np.float32))                    # all equal negative -> -127
+    rows.append((np.arange(k) % 7 - 3).astype(np.float32) * 1e-6)   # tiny scale
+    t = np.tile(np.array([127.0, 2.5, -2.5, 3.5, -0.5, 0.5, 1.5, -126.5] * 4, np.float32), k // 32)
+    rows.append(t)                                               # amax 127 -> d = 1: exact .5 ties
+    rows.append(np.tile(np.array([1e30, -1e30] + [1.0] * 30, np.float32), k // 32))   # huge dynamic range
+    s = np.where(np.arange(k) % 2 == 0, 1.0, -1.0).astype(np.float32) * 1e4
+    rows.append(s)                                               # saturation-scale magnitudes
+    rng = np.random.default_rng(1234)
+    rows.append(rng.standard_normal(k).astype(np.float32))
+    return np.stack(rows)

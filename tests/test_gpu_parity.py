@@ -1,0 +1,199 @@
+"""GPU parity: the HIP path through the C-ABI (libjamhip.so) against the pinned oracle.
+
+Tier 1 (same int8 semantics, f32 order differs): |gpu - oracle_int8| <= 1e-3*|oracle| + 1e-5*sumAbs.
+Tier 2 (jam's own bound, PRECISION.md:20-26): |gpu - float_ref| <= 1e-2*sumAbs + 1e-3, and the same
+bound against libjam itself when oracle/_ref is present.
+Activation quantization is checked bit for bit.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+from conftest import adversarial_activations
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(104, 1024), (100, 512), (70, 256), (64, 768)]   # JamBackendParityTest.java:204-252
+NS = [1, 2, 3, 4, 7, 8, 13, 16, 17, 33]
+
+
+def say(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def bits(x):
+    return np.ascontiguousarray(x).view(np.uint32)
+
+
+def tier1(got, ref, sa):
+    return np.abs(got - ref) <= 1e-3 * np.abs(ref) + 1e-5 * sa
+
+
+def run_mm(hip, dt, w, a, m, n, k, ldw=None, lda=None, ldc=None, out=None):
+    from qxotic_amd.jam import JAM, Segment
+    ldw = ldw or k
+    lda = lda or a.shape[-1]
+    ldc = ldc or m
+    c = out if out is not None else np.zeros((n, ldc), np.float32)
+    st = hip.mm(Segment.of(w), 0, dt, ldw, Segment.of(a), 0, JAM.F32, lda, Segment.of(c), 0, JAM.F32, ldc, m, n, k)
+    assert st == JAM.OK, hip.last_error()
+    return c
+
+
+# ----------------------------------------------------------------------------- activation quantizers
+@pytest.mark.parametrize("flavour", [1, 2])
+def test_quantizer_bit_exact(hip, oracle, flavour):
+    import torch
+    say(f"quantizer flavour {flavour}")
+    x = np.concatenate([adversarial_activations(4096), oracle.outliers(11, (64, 4096)), oracle.normal(12, (8, 4096))])
+    n, k = x.shape
+    a = torch.from_numpy(x).cuda()
+    q = torch.empty((n, k), dtype=torch.int8, device="cuda")
+    d = torch.empty((n, k // 32), dtype=torch.float32, device="cuda")
+    s = torch.empty((n, k // (32 if flavour == 1 else 16)), dtype=torch.float32, device="cuda")
+    assert hip.quantize_device(flavour, a.data_ptr(), k, n, k, q.data_ptr(), d.data_ptr(), s.data_ptr()) == 0
+    assert hip.synchronize() == 0
+    qo, do, so = (oracle.quant_f1 if flavour == 1 else oracle.quant_f2)(x)
+    assert np.array_equal(q.cpu().numpy(), qo)
+    assert np.array_equal(bits(d.cpu().numpy()), bits(do))
+    assert np.array_equal(bits(s.cpu().numpy()), bits(so))
+
+
+def test_quantizer_bit_exact_prefill_size(hip, oracle):
+    """Config 4's activations at full size (512 x 14336, 1% +-20 outliers), F2."""
+    import torch
+    x = oracle.outliers(0x5A11C0DE ^ 4, (512, 14336))
+    n, k = x.shape
+    a = torch.from_numpy(x).cuda()
+    q = torch.empty((n, k), dtype=torch.int8, device="cuda")
+    d = torch.empty((n, k // 32), dtype=torch.float32, device="cuda")
+    s = torch.empty((n, k // 16), dtype=torch.float32, device="cuda")
+    assert hip.quantize_device(2, a.data_ptr(), k, n, k, q.data_ptr(), d.data_ptr(), s.data_ptr()) == 0
+    hip.synchronize()
+    qo, do, so = oracle.quant_f2(x)
+    assert np.array_equal(q.cpu().numpy(), qo)
+    assert np.array_equal(bits(d.cpu().numpy()), bits(do))
+    assert np.array_equal(bits(s.cpu().numpy()), bits(so))
+
+
+# ------------------------------------------------------------------------------------- matmul parity
+@pytest.mark.parametrize("dt", O.QUANT_TYPES)
+def test_mm_parity_shapes(hip, oracle, dt):
+    for (m, k) in SHAPES:
+        if k % O.BLOCK[dt][0]:
+            continue
+        w = oracle.quantize(dt, oracle.normal(0x5A11C0DE ^ (m * 31 + k + dt), (m, k), 0.0, 0.02))
+        for n in NS:
+            say(f"mm {O.NAMES[dt]} m={m} n={n} k={k}")
+            a = oracle.outliers(1000 + n, (n, k))
+            got = run_mm(hip, dt, w, a, m, n, k)
+            ref = oracle.mm_int8(dt, w, a, m, n, k)
+            fref, sa = oracle.mm_ref(dt, w, a, m, n, k)
+            ok = tier1(got, ref, sa)
+            assert ok.all(), (O.NAMES[dt], m, n, k, float(np.max(np.abs(got - ref) / (np.abs(ref) + 1e-30))))
+            assert (np.abs(got - fref) <= 1e-2 * sa + 1e-3).all()
+
+
+@pytest.mark.parametrize("dt", O.QUANT_TYPES)
+def test_mm_matches_golden_libjam(hip, dt):
+    """Against libjam's own outputs committed as fixtures (PRECISION.md bound plus the tier-1 bound
+    relative to libjam's own answer)."""
+    from pathlib import Path
+    g = np.load(Path(__file__).resolve().parent / "golden" / "jam_golden.npz")
+    w, a = g[f"mm_{O.NAMES[dt]}_w"], g["mm_a"]
+    m, k = 32, 512
+    for n in (1, 3, 7, 8, 13, 16):
+        say(f"golden {O.NAMES[dt]} n={n}")
+        got = run_mm(hip, dt, w, a[:n].copy(), m, n, k)
+        want = g[f"mm_{O.NAMES[dt]}_n{n}"]
+        scale = np.abs(want).max()
+        assert (np.abs(got - want) <= 1e-3 * np.abs(want) + 1e-4 * scale).all(), (O.NAMES[dt], n)
+
+
+@pytest.mark.parametrize("dt", O.QUANT_TYPES)
+def test_layout_metamorphic(hip, oracle, dt):
+    """ldw > k (padding bytes 0xA5), lda > k, ldc > m gap untouched, rerun bit-identical
+    (jam_test.c:272-353)."""
+    be = O.BLOCK[dt][0]
+    m, k = 48, 512
+    ldw = k + 2 * max(be, 256)
+    wfull = oracle.quantize(dt, oracle.normal(5, (m, ldw), 0.0, 0.02))
+    rb = O.row_bytes(dt, k)
+    wpad = wfull.copy()
+    wpad[:, rb:] = 0xA5
+    for n in (1, 5, 8, 20):
+        say(f"layout {O.NAMES[dt]} n={n}")
+        a = np.full((n, k + 40), 7.0, np.float32)
+        a[:, :k] = oracle.normal(6 + n, (n, k))
+        ldc = m + 9
+        c = np.full((n, ldc), -12345.0, np.float32)
+        run_mm(hip, dt, wpad, a, m, n, k, ldw=ldw, lda=k + 40, ldc=ldc, out=c)
+        assert (c[:, m:] == -12345.0).all()
+        ref = run_mm(hip, dt, np.ascontiguousarray(wfull[:, :rb]), np.ascontiguousarray(a[:, :k]), m, n, k)
+        assert np.array_equal(bits(c[:, :m]), bits(ref[:, :m]))
+        again = run_mm(hip, dt, wpad, a, m, n, k, ldw=ldw, lda=k + 40)
+        assert np.array_equal(bits(again[:, :m]), bits(c[:, :m]))
+
+
+@pytest.mark.parametrize("dt", O.QUANT_TYPES)
+def test_pinned_matches_staged_and_slices(hip, oracle, dt):
+    """Pinned (device-resident) weights give the staged answer bit for bit, also for row slices at
+    non-zero offsets into one stacked tensor (the MoE expert pattern, GptOss.java:677-684)."""
+    from qxotic_amd.jam import JAM, Segment
+    experts, rows, k = 4, 64, 512
+    w = oracle.quantize(dt, oracle.normal(17, (experts * rows, k), 0.0, 0.02))
+    rb = O.row_bytes(dt, k)
+    a = oracle.normal(18, (9, k))
+    staged = [run_mm(hip, dt, np.ascontiguousarray(w[e * rows:(e + 1) * rows]), a[:n], rows, n, k)
+              for e in range(experts) for n in (1, 9)]
+    assert hip.pin(Segment.of(w), dt, k, experts * rows) == JAM.OK, hip.last_error()
+    try:
+        i = 0
+        for e in range(experts):
+            for n in (1, 9):
+                say(f"pinned {O.NAMES[dt]} expert={e} n={n}")
+                c = np.zeros((n, rows), np.float32)
+                st = hip.mm(Segment.of(w), e * rows * rb, dt, k, Segment.of(a), 0, JAM.F32, k, Segment.of(c), 0,
+                            JAM.F32, rows, rows, n, k)
+                assert st == JAM.OK
+                assert np.array_equal(bits(c), bits(staged[i]))
+                i += 1
+    finally:
+        assert hip.evict(Segment.of(w)) == JAM.OK
+
+
+def test_status_codes(hip, oracle):
+    from qxotic_amd.jam import JAM, Segment, IllegalArgumentError, IndexOutOfBoundsError
+    w = oracle.quantize(O.Q8_0, oracle.normal(1, (32, 64), 0.0, 0.02))
+    a = oracle.normal(2, (2, 64))
+    c = np.zeros((2, 32), np.float32)
+    W, A, R = Segment.of(w), Segment.of(a), Segment.of(c)
+    assert hip.mm(W, 0, JAM.Q8_0, 64, A, 0, JAM.F32, 64, R, 0, JAM.F32, 32, 32, 2, 64) == JAM.OK
+    assert hip.mm(W, 0, JAM.Q8_0, 64, A, 0, JAM.F32, 64, R, 0, JAM.F32, 32, 0, 2, 64) == JAM.EINVAL
+    assert hip.mm(W, 0, JAM.Q8_0, 32, A, 0, JAM.F32, 64, R, 0, JAM.F32, 32, 32, 2, 64) == JAM.EINVAL   # ldw < k
+    assert hip.mm(W, 0, JAM.Q8_0, 64, A, 0, JAM.F32, 64, R, 0, JAM.F32, 16, 32, 2, 64) == JAM.EINVAL   # ldc < m
+    assert hip.mm(W, 0, JAM.Q5_K, 256, A, 0, JAM.F32, 64, R, 0, JAM.F32, 32, 1, 1, 64) != JAM.OK
+    assert hip.mm(W, 0, JAM.Q8_0, 64, A, 0, JAM.F16, 64, R, 0, JAM.F32, 32, 32, 1, 64) == JAM.EUNSUPPORTED
+    assert hip.mm(W, 0, JAM.Q8_0, 48, A, 0, JAM.F32, 48, R, 0, JAM.F32, 32, 16, 1, 48) == JAM.EUNSUPPORTED
+    with pytest.raises(IllegalArgumentError):
+        hip.mm(Segment.heap([0]), 0, JAM.Q8_0, 64, A, 0, JAM.F32, 64, R, 0, JAM.F32, 32, 32, 2, 64)
+    with pytest.raises(IndexOutOfBoundsError):
+        hip.mm(W, 34, JAM.Q8_0, 64, A, 0, JAM.F32, 64, R, 0, JAM.F32, 32, 32, 2, 64)
+
+
+# ------------------------------------------------------------------------------- BASELINE full sizes
+FULL = [(O.Q4_K, 14336, 4096, 1), (O.Q6_K, 4096, 14336, 1), (O.Q8_0, 4096, 4096, 1),
+        (O.Q4_0, 14336, 4096, 4), (O.Q4_0, 4096, 14336, 8), (O.MXFP4, 2880, 2880, 3)]
+
+
+@pytest.mark.parametrize("dt,m,k,n", FULL)
+def test_full_size_decode(hip, oracle, dt, m, k, n):
+    say(f"full {O.NAMES[dt]} {m}x{k} n={n}")
+    w = oracle.quantize(dt, oracle.normal(0x5A11C0DE ^ dt, (m, k), 0.0, 0.02))
+    a = oracle.normal(0x5A11C0DE ^ 99, (n, k))
+    got = run_mm(hip, dt, w, a, m, n, k)
+    ref = oracle.mm_int8(dt, w, a, m, n, k)
+    _, sa = oracle.mm_ref(dt, w, a, m, n, k)
+    assert tier1(got, ref, sa).all()
