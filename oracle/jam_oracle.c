@@ -502,10 +502,26 @@ static int int8_supported(int dt) {
     return dt == JO_Q8_0 || dt == JO_Q4_0 || dt == JO_MXFP4 || dt == JO_Q4_K || dt == JO_Q6_K;
 }
 
+/* Exact float dot of one dequantized weight row with an f32 activation row (double accumulation): the
+ * "<16-row tail: scalar exact dot" every n>=8 band runs on its last m%16 rows (q4k_avx512.c:185-188,
+ * 314-317, 417-420, 551-554, 654-657, 790-793), whose own f32 order differs only by rounding. */
+static double row_float(int dt, const uint8_t* w, const float* x, int k) {
+    double* row = (double*) malloc(sizeof(double) * (size_t) k);
+    jo_dequant_row_f64(dt, w, k, row);
+    double s = 0.0;
+    for (int e = 0; e < k; e++) s += row[e] * x[e];
+    free(row);
+    return s;
+}
+
 int jo_mm_int8(int dt, const uint8_t* w, int ldw, const float* a, int lda, float* c, int ldc,
                int m, int n, int k, int flavour) {
     if (!int8_supported(dt) || k % jo_block_elems(dt) || ldw % jo_block_elems(dt)) return -1;
+    /* flavour 0 = jam's own routing on an AVX-512-VNNI host (jam.c:469-499, 544-560, 682-730): n < 8 runs
+     * F1 on every row; n >= 8 runs the 16-row F2 bands and leaves the last m % 16 rows to a float dot. */
+    const int jam_rule = flavour == 0;
     if (flavour == 0) flavour = n < 8 ? 1 : 2;
+    const int m_int8 = jam_rule && flavour == 2 ? m - m % 16 : m;
     int nb = k / 32;
     int8_t* q = (int8_t*) malloc((size_t) n * k);
     float* d = (float*) malloc(sizeof(float) * (size_t) n * nb);
@@ -518,7 +534,8 @@ int jo_mm_int8(int dt, const uint8_t* w, int ldw, const float* a, int lda, float
     for (int i = 0; i < m; i++) {
         const uint8_t* wr = w + (int64_t) i * wstride;
         for (int j = 0; j < n; j++) {
-            double v = flavour == 1
+            double v = i >= m_int8 ? row_float(dt, wr, a + (size_t) j * lda, k)
+                : flavour == 1
                 ? row_f1(dt, wr, q + (size_t) j * k, d + (size_t) j * nb, s + (size_t) j * nb, k)
                 : row_f2(dt, wr, q + (size_t) j * k, d + (size_t) j * nb, s + (size_t) j * nb * 2, k);
             c[(size_t) j * ldc + i] = (float) v;

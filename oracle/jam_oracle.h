@@ -64,7 +64,9 @@ void jo_quant_f2(const float* x, int k, int8_t* q, float* d, float* xsum16);
 
 /* jam's int8 pipeline, C[j*ldc+i] for i<m, j<n. flavour 1 = the n<8 decode decomposition (F1 quant;
  * jam.c:469-481 with the per-dtype kernels named in jam_oracle.c), flavour 2 = the n>=8 band
- * decomposition (F2 quant; jam.c:489-499, 544-560). flavour 0 picks jam's own rule (n<8 -> 1).
+ * decomposition (F2 quant; jam.c:489-499, 544-560). flavour 0 picks jam's own rule: n<8 -> 1 on every
+ * row; n>=8 -> 2 on rows [0, m - m%16) and an exact float dot on the last m%16 rows, as every 16-row
+ * band kernel does for its tail (jam_kernels_q4k_avx512.c:185-188).
  * Per-block terms are formed in f32 exactly as jam forms its scale products, and summed in double.
  * Returns 0, or -1 for an unsupported dtype/shape. */
 int jo_mm_int8(int dtype, const uint8_t* w, int ldw, const float* a, int lda, float* c, int ldc,

@@ -29,12 +29,27 @@ SIGNATURES = [
 ]
 
 
+def _adopt_torch_runtime() -> None:
+    """Load PyTorch's HIP runtime first when PyTorch is installed.
+
+    torch ships its own libamdhip64 (SONAME libamdhip64.so.7) and its libc10_hip asks for it under the
+    name "libamdhip64.so". If libjamhip.so were loaded first it would pull /opt/rocm's copy (same SONAME,
+    other file) and torch would then load a second runtime that finds no GPU. Importing torch first makes
+    the dynamic loader resolve libjamhip's libamdhip64.so.7 to the runtime already in the process, so both
+    share one HIP runtime, one device context and one set of streams."""
+    try:
+        import torch  # noqa: F401
+    except Exception:
+        pass
+
+
 def lib() -> C.CDLL:
     """The loaded library; raises RuntimeError if it has not been built."""
     global _lib
     if _lib is None:
         if not LIB_PATH.exists():
             raise RuntimeError(f"{LIB_PATH} is not built: run `python -m qxotic_amd.build` (no CPU fallback)")
+        _adopt_torch_runtime()
         L = C.CDLL(str(LIB_PATH))
         for name, res, args in SIGNATURES:
             fn = getattr(L, name)

@@ -87,13 +87,20 @@ def test_mm_parity_shapes(hip, oracle, dt):
         w = oracle.quantize(dt, oracle.normal(0x5A11C0DE ^ (m * 31 + k + dt), (m, k), 0.0, 0.02))
         for n in NS:
             say(f"mm {O.NAMES[dt]} m={m} n={n} k={k}")
+            # tier 1 on config 4's activation mix (1% +-20 outliers stress the per-32 scales)
             a = oracle.outliers(1000 + n, (n, k))
             got = run_mm(hip, dt, w, a, m, n, k)
             ref = oracle.mm_int8(dt, w, a, m, n, k)
-            fref, sa = oracle.mm_ref(dt, w, a, m, n, k)
+            _, sa = oracle.mm_ref(dt, w, a, m, n, k)
             ok = tier1(got, ref, sa)
             assert ok.all(), (O.NAMES[dt], m, n, k, float(np.max(np.abs(got - ref) / (np.abs(ref) + 1e-30))))
-            assert (np.abs(got - fref) <= 1e-2 * sa + 1e-3).all()
+            # tier 2, jam's own bound, holds for the N(0,1) activations it was written for: an outlier
+            # inflates its block's int8 step 20x, which jam's CPU path shares (PRECISION.md:8-26)
+            a = oracle.normal(2000 + n, (n, k))
+            got = run_mm(hip, dt, w, a, m, n, k)
+            fref, sa = oracle.mm_ref(dt, w, a, m, n, k)
+            assert tier1(got, oracle.mm_int8(dt, w, a, m, n, k), sa).all()
+            assert (np.abs(got - fref) <= 1e-2 * sa + 1e-3).all(), (O.NAMES[dt], m, n, k)
 
 
 @pytest.mark.parametrize("dt", O.QUANT_TYPES)

@@ -158,15 +158,31 @@ def test_int8_pipeline_matches_golden(oracle, dt):
 
 
 @pytest.mark.parametrize("dt", O.QUANT_TYPES)
-@pytest.mark.parametrize("n", [1, 2, 7, 8, 9, 16])
-def test_int8_pipeline_matches_libjam(oracle, refjam, dt, n):
-    m, k = 96, 1024   # m % 16 == 0: jam's n>=8 bands run every row through the int8 path
+@pytest.mark.parametrize("n", [1, 2, 7, 8, 9, 16, 33])
+@pytest.mark.parametrize("m", [96, 104, 77])
+def test_int8_pipeline_matches_libjam(oracle, refjam, dt, n, m):
+    """m % 16 != 0 included: jam's n>=8 bands leave the last m % 16 rows to a float dot."""
+    k = 1024
     w = oracle.quantize(dt, oracle.normal(77 + dt, (m, k), 0.0, 0.02))
     a = oracle.outliers(5 + n, (n, k))
     want = refjam.mm(dt, w, a, m, n, k)
     got = oracle.mm_int8(dt, w, a, m, n, k)
     _, sa = oracle.mm_ref(dt, w, a, m, n, k)
     assert (np.abs(got - want) <= tol_int8(got, sa)).all()
+
+
+def test_tail_rule_is_discriminating(oracle, refjam):
+    """The float-dot tail is observable: computing the last m % 16 rows with F2 int8 instead misses
+    libjam's answer there by more than the tolerance (outlier activations make the int8 error large)."""
+    m, k, n = 104, 1024, 9
+    for dt in O.QUANT_TYPES:
+        w = oracle.quantize(dt, oracle.normal(31 + dt, (m, k), 0.0, 0.02))
+        a = oracle.outliers(32, (n, k))
+        want = refjam.mm(dt, w, a, m, n, k)
+        all_int8 = oracle.mm_int8(dt, w, a, m, n, k, flavour=2)
+        _, sa = oracle.mm_ref(dt, w, a, m, n, k)
+        ok = np.abs(all_int8 - want) <= tol_int8(all_int8, sa)
+        assert ok[:, :96].all() and not ok[:, 96:].all(), O.NAMES[dt]
 
 
 def test_int8_flavour_is_discriminating(oracle, refjam):
