@@ -18,27 +18,33 @@ __host__ __device__ constexpr int block_bytes(int dt) {
          : dt == Q6_K ? 210 : dt == F32 ? 4 : 2;
 }
 
-// Device layout of a pinned weight tensor of `rows` rows and `rb` blocks per row.
-//   plane 0 ("qs")   : rows × rb × qs_bytes  — the 16-byte-aligned part of every block
-//   plane 1 ("sc")   : rows × rb × sc_bytes  — the scalar scale (fp16 d, or the E8M0 byte)
-// Q4_K's 144-byte blocks are already 16-byte multiples and stay whole in plane 0 (sc_bytes 0).
-//   Q8_0 : qs 32 (int8 q)                 | d fp16
-//   Q4_0 : qs 16 (nibbles)                | d fp16
-//   MXFP4: qs 16 (nibbles)                | e8m0
-//   Q6_K : ql 128 | qh 64 | scales 16 = 208 | d fp16
-//   Q4_K : whole block 144                | —
-// Bytes are exactly the GGUF bytes; only their order changes.
-__host__ __device__ constexpr int qs_bytes(int dt) {
-    return dt == Q8_0 ? 32 : dt == Q4_0 ? 16 : dt == MXFP4 ? 16 : dt == Q6_K ? 208 : dt == Q4_K ? 144 : 0;
+// Device layout of a pinned weight tensor ("chunk-major groups"). A row of k elements is cut into groups
+// of 256 elements (one super-block, or 8 blocks of 32; a row whose block count is not a multiple of 8
+// ends in a zero-padded group). A group's packed quants are NC 16-byte chunks and its scales SB bytes:
+//   Q4_K : NC 8  chunk c = nibble bytes 16c..16c+15            | SB 16: d, dmin fp16, 12 scale bytes
+//   Q6_K : NC 13 chunks 0-7 ql, 8-11 qh, 12 the 16 int8 scales | SB 2 : d fp16
+//   Q8_0 : NC 16 chunk c = half c&1 of block c>>1 (int8 q)     | SB 16: the 8 blocks' fp16 d
+//   Q4_0 : NC 8  chunk c = block c's 16 nibble bytes           | SB 16: the 8 blocks' fp16 d
+//   MXFP4: NC 8  chunk c = block c's 16 nibble bytes           | SB 8 : the 8 blocks' e8m0
+// Plane 0 ("qs") holds, per row, chunk c of group g at byte (c·G + g)·16 (G = groups per row), so the
+// lanes of a wave that own consecutive groups of a row read chunk c from contiguous memory; plane 1
+// ("sc") holds, per row, group g's scales at byte g·SB. Every GGUF byte is kept; only the order changes.
+__host__ __device__ constexpr int group_chunks(int dt) {
+    return dt == Q4_K ? 8 : dt == Q6_K ? 13 : dt == Q8_0 ? 16 : dt == Q4_0 ? 8 : dt == MXFP4 ? 8 : 0;
 }
-__host__ __device__ constexpr int sc_bytes(int dt) {
-    return dt == Q8_0 ? 2 : dt == Q4_0 ? 2 : dt == MXFP4 ? 1 : dt == Q6_K ? 2 : 0;
+__host__ __device__ constexpr int group_scale_bytes(int dt) {
+    return dt == Q4_K ? 16 : dt == Q6_K ? 2 : dt == Q8_0 ? 16 : dt == Q4_0 ? 16 : dt == MXFP4 ? 8 : 0;
+}
+__host__ __device__ constexpr int blocks_per_group(int dt) { return 256 / block_elems(dt); }
+// groups per row for a row of `blocks` blocks
+__host__ __device__ constexpr int64_t groups_of(int dt, int64_t blocks) {
+    return (blocks + blocks_per_group(dt) - 1) / blocks_per_group(dt);
 }
 
 struct WeightView {
     const uint8_t* qs;   // plane 0 at row 0 of the view
-    const uint8_t* sc;   // plane 1 at row 0 of the view (nullptr for Q4_K)
-    int64_t rb;          // blocks per row in the device layout
+    const uint8_t* sc;   // plane 1 at row 0 of the view
+    int64_t G;           // groups per row of the device layout (the row stride, in groups)
 };
 
 // Activation quantization outputs (per token row j of k elements, nb = k/32 blocks).
@@ -55,10 +61,29 @@ JAMHIP_DEV float h2f(uint32_t bits16) { return (float) __builtin_bit_cast(_Float
 
 JAMHIP_DEV int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
+template <int CTRL> JAMHIP_DEV float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+JAMHIP_DEV float lane_f(float v, int l) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l)); }
+
+// Sum over each row of 16 lanes, the same value in all 16 lanes, in a fixed order: a DPP butterfly
+// (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror).
+JAMHIP_DEV float row16_sum(float v) {
+    v += dpp<0xB1>(v);
+    v += dpp<0x4E>(v);
+    v += dpp<0x141>(v);
+    return v + dpp<0x140>(v);
+}
+
+// Sum over the 64 lanes of a wave, the same value in every lane, in a fixed order (reruns are bit-identical).
+// Within each row of 16 lanes a DPP butterfly (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror,
+// row_mirror) leaves the row sum in all 16 lanes; the four row sums are then read back with v_readlane.
 JAMHIP_DEV float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
+    v += dpp<0xB1>(v);
+    v += dpp<0x4E>(v);
+    v += dpp<0x141>(v);
+    v += dpp<0x140>(v);
+    return (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
 }
 
 // E8M0 -> 2^(e-128) (jam/jam-native/src/kernels/jam_mxfp4.h:17-24): e=0 -> 2^-128, e=255 -> +Inf.

@@ -1,66 +1,45 @@
-// Weight-streaming matmul for few tokens: decode GEMV (n < 8, jam's F1 decomposition) and the skinny
-// n >= 8 fallback (F2 decomposition, 8 tokens per launch row). HBM-bound: every weight byte is read once
-// per launch with 128-bit loads; int8 dots run on v_dot4_i32_i8; the per-block f32 combine follows the
-// jam kernel named at each dot below.
+// Weight-streaming matmul for few tokens: the decode GEMV (n < 8, jam's F1 decomposition) and the skinny
+// n >= 8 path (F2 decomposition). HBM-bound: every weight byte is read once per launch with aligned
+// 128-bit loads; int8 dots run on v_dot4_i32_i8; the per-block f32 combine follows the jam kernel named
+// at each dot below.
 //
-// Work split: a 256-thread workgroup = 4 waves; a wave owns ROWS consecutive weight rows; lane l owns the
-// "unit" u = pass*64 + l of every one of those rows, where a unit is 64 elements (Q4_K: one scale pair
-// of a super-block) or 32 elements (Q8_0/Q4_0/MXFP4: one block; Q6_K: one 16-byte ql slice). A wave reads
-// contiguous row bytes, then folds its 64 lane partials with xor-shuffles.
+// Work split. A lane owns whole 256-element groups of the chunk-major device layout (common.h): 16 lanes
+// (one DPP row) share a weight row and take its groups li, li+16, ...; the 4 rows of a wave's "quad" sit
+// in the wave's 4 lane rows. For each chunk index c the 64 lanes read 4 rows x 16 consecutive groups of
+// 16 bytes, i.e. four contiguous 256-byte runs, and one group's scales come in one more load. An item is
+// one such group-slot of a quad; each wave keeps DEPTH items in flight in a register ring with
+// unconditional loads (the compiler then waits with vmcnt(count) instead of draining the queue), folds
+// a row's 16 lane partials with a DPP butterfly once its last group is done, and a 256-thread workgroup
+// (4 waves) owns a contiguous range of rows, its quads dealt round-robin to the waves. In the fused F1
+// variant the workgroup first quantizes A into LDS (bit-exact F1), once for all of its rows, while its
+// first weight loads are already in flight.
 #include "common.h"
 #include "launch.h"
 #include "quant.h"
 
 namespace jamhip {
 
-template <int DT> constexpr int unit_elems() { return DT == Q4_K ? 64 : 32; }
-
 // -------------------------------------------------------------------------------------------- weights
-struct WQ4K { uint4 h, q0, q1; };
-struct WQ8 { uint4 q0, q1; uint32_t d; };
-struct WQ4 { uint4 q; uint32_t d; };        // Q4_0 and MXFP4 (d = fp16 bits or the e8m0 byte)
-struct WQ6 { uint4 ql, qh, sc; uint32_t d; };
+template <int DT> struct Group {
+    uint4 q[group_chunks(DT)];
+    uint4 s;   // the group's scale bytes (Q4_K header; Q8_0/Q4_0 8 x fp16; MXFP4 8 x e8m0; Q6_K d in s.x)
+};
 
-template <int DT> struct WRegs;
-template <> struct WRegs<Q4_K> { using T = WQ4K; };
-template <> struct WRegs<Q8_0> { using T = WQ8; };
-template <> struct WRegs<Q4_0> { using T = WQ4; };
-template <> struct WRegs<MXFP4> { using T = WQ4; };
-template <> struct WRegs<Q6_K> { using T = WQ6; };
+JAMHIP_DEV uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
 
-JAMHIP_DEV uint4 ld16(const uint8_t* p) { return *reinterpret_cast<const uint4*>(p); }
-
-template <int DT> JAMHIP_DEV typename WRegs<DT>::T load_w(const WeightView& w, int64_t row, int u) {
-    typename WRegs<DT>::T r;
-    if constexpr (DT == Q4_K) {
-        const uint8_t* p = w.qs + (row * w.rb + (u >> 2)) * 144;
-        const int g = u & 3;
-        r.h = ld16(p);
-        r.q0 = ld16(p + 16 + 32 * g);
-        r.q1 = ld16(p + 32 + 32 * g);
-    } else if constexpr (DT == Q8_0) {
-        const int64_t i = row * w.rb + u;
-        r.q0 = ld16(w.qs + i * 32);
-        r.q1 = ld16(w.qs + i * 32 + 16);
-        r.d = *reinterpret_cast<const uint16_t*>(w.sc + i * 2);
-    } else if constexpr (DT == Q4_0) {
-        const int64_t i = row * w.rb + u;
-        r.q = ld16(w.qs + i * 16);
-        r.d = *reinterpret_cast<const uint16_t*>(w.sc + i * 2);
+// Group g of a row (plane pointers of that row, Gs groups per row in the layout).
+template <int DT>
+JAMHIP_DEV void load_group(Group<DT>& r, const uint8_t* rq, const uint8_t* rs, int64_t Gs, int g) {
+#pragma unroll
+    for (int c = 0; c < group_chunks(DT); c++) r.q[c] = ld16(rq + ((int64_t) c * Gs + g) * 16);
+    if constexpr (DT == Q6_K) {
+        r.s.x = *reinterpret_cast<const uint16_t*>(rs + 2 * (int64_t) g);
     } else if constexpr (DT == MXFP4) {
-        const int64_t i = row * w.rb + u;
-        r.q = ld16(w.qs + i * 16);
-        r.d = w.sc[i];
-    } else {   // Q6_K: unit t = u & 7 of super-block u >> 3
-        const int64_t i = row * w.rb + (u >> 3);
-        const int t = u & 7, h = t >> 2, jj = (t >> 1) & 1, lh = t & 1;
-        const uint8_t* body = w.qs + i * 208;
-        r.ql = ld16(body + 64 * h + 32 * jj + 16 * lh);
-        r.qh = ld16(body + 128 + 32 * h + 16 * lh);
-        r.sc = ld16(body + 192);
-        r.d = *reinterpret_cast<const uint16_t*>(w.sc + i * 2);
+        const uint2 v = *reinterpret_cast<const uint2*>(rs + 8 * (int64_t) g);
+        r.s = make_uint4(v.x, v.y, 0u, 0u);
+    } else {
+        r.s = ld16(rs + 16 * (int64_t) g);
     }
-    return r;
 }
 
 // ------------------------------------------------------------------------------------- int8 helpers
@@ -72,6 +51,9 @@ JAMHIP_DEV int dot16(const uint4 w, const uint4 a, int c) {
 }
 JAMHIP_DEV uint4 and4(uint4 v, uint32_t m) { return make_uint4(v.x & m, v.y & m, v.z & m, v.w & m); }
 JAMHIP_DEV uint4 shr4(uint4 v, int s) { return make_uint4(v.x >> s, v.y >> s, v.z >> s, v.w >> s); }
+JAMHIP_DEV uint4 lo_nib(uint4 v) { return and4(v, 0x0f0f0f0fu); }
+JAMHIP_DEV uint4 hi_nib(uint4 v) { return and4(shr4(v, 4), 0x0f0f0f0fu); }
+JAMHIP_DEV uint32_t word(const uint4& v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
 
 // MXFP4 nibble -> signed int8 code (value x2: 0,1,2,3,4,6,8,12 and negatives; jam_mxfp4.h:14-15),
 // four at a time: v_perm picks the magnitude and its negation from 8-entry tables, bit 3 selects.
@@ -86,257 +68,403 @@ JAMHIP_DEV uint4 mxfp4_codes4(uint4 n) {
     return make_uint4(mxfp4_codes(n.x), mxfp4_codes(n.y), mxfp4_codes(n.z), mxfp4_codes(n.w));
 }
 
-// Q4_K 6-bit (scale, min) of sub-blocks 2g and 2g+1 (jam/jam-native/src/jam_kquant.h:26-33), from the
-// three scale words (bytes 4..15 of the block).
-JAMHIP_DEV void q4k_pair_scales(const uint4 h, int g, int& sc0, int& sc1, int& mn0, int& mn1) {
-    const uint32_t u0 = h.y, u1 = h.z, u2 = h.w;
-    const uint32_t scA = u0 & 0x3f3f3f3fu, mnA = u1 & 0x3f3f3f3fu;
-    const uint32_t scB = (u2 & 0x0f0f0f0fu) | (((u0 >> 6) & 0x03030303u) << 4);
-    const uint32_t mnB = ((u2 >> 4) & 0x0f0f0f0fu) | (((u1 >> 6) & 0x03030303u) << 4);
-    const uint32_t scw = g < 2 ? scA : scB, mnw = g < 2 ? mnA : mnB;
-    const int sh = (g & 1) * 16;
-    sc0 = (scw >> sh) & 0xff;
-    sc1 = (scw >> (sh + 8)) & 0xff;
-    mn0 = (mnw >> sh) & 0xff;
-    mn1 = (mnw >> (sh + 8)) & 0xff;
+// Q4_K 6-bit scale and min of sub-block s (jam/jam-native/src/jam_kquant.h:26-33) from the header words.
+JAMHIP_DEV void q4k_sm(const uint4 h, int s, int& sc, int& mn) {
+    const uint32_t u0 = h.y, u1 = h.z, u2 = h.w;   // scale bytes 0-3, 4-7, 8-11
+    const int sh = 8 * (s & 3);
+    if (s < 4) {
+        sc = (u0 >> sh) & 63;
+        mn = (u1 >> sh) & 63;
+    } else {
+        sc = ((u2 >> sh) & 15) | ((((u0 >> sh) >> 6) & 3) << 4);
+        mn = (((u2 >> sh) >> 4) & 15) | ((((u1 >> sh) >> 6) & 3) << 4);
+    }
 }
 
 JAMHIP_DEV int sbyte(uint32_t w, int b) { return (int) (int8_t) (w >> (8 * b)); }
 
-// -------------------------------------------------------------------------------- per-unit partials
-// F1: activations from jam_q8_0_requant — q, d per 32, asum per 32 (float), s16 per 16 (int).
-template <int DT>
-JAMHIP_DEV float unit_f1(const typename WRegs<DT>::T& w, int u, const ActQ& A, int t, int k) {
-    const int nb = k >> 5;
-    const int8_t* aq = A.q + (int64_t) t * k;
-    const float* ad = A.d + (int64_t) t * nb;
+// Q6_K 6-bit codes of ql chunk c with the matching qh chunk: the low-nibble group and the high one.
+JAMHIP_DEV void q6k_codes(const uint4 ql, const uint4 qh, int jj, uint4& qa, uint4& qb) {
+    const uint4 hia = and4(shr4(qh, 2 * jj), 0x03030303u), hib = and4(shr4(qh, 2 * jj + 4), 0x03030303u);
+    const uint4 lo = lo_nib(ql), hi = hi_nib(ql);
+    qa = make_uint4(lo.x | (hia.x << 4), lo.y | (hia.y << 4), lo.z | (hia.z << 4), lo.w | (hia.w << 4));
+    qb = make_uint4(hi.x | (hib.x << 4), hi.y | (hib.y << 4), hi.z | (hib.z << 4), hi.w | (hib.w << 4));
+}
+
+// -------------------------------------------------------------------------------- per-group partials
+// Activations of one token for one group: aq -> the group's 256 int8 codes, ad -> its 8 block scales,
+// as -> F1: 8 block sums (float Σq) / F2: 16 raw f32 sums Σx per 16, s16 -> F1: 16 int Σq per 16.
+// nbv = blocks of the group inside the call's k (8 but for a row's last group of a 32-element type);
+// blocks past it contribute nothing and read the last valid block's activations.
+template <int DT, int FL>
+JAMHIP_DEV float group_dot(const Group<DT>& w, const int8_t* aq, const float* ad, const float* as, const int* s16,
+                           int nbv) {
     if constexpr (DT == Q4_K) {
-        // jam_mm_q4k_avx512vnni (jam_kernels_q4k_avx512.c:956-1054):
-        //   Σ_s I_s·fl(fl(ad·sc)·d)  −  dmin·Σ_s mn·fl(asum·ad)
-        const int sb = u >> 2, g = u & 3, base = sb * 256 + 64 * g, bl = sb * 8 + 2 * g;
-        const uint4 a0 = ld16((const uint8_t*) aq + base), a1 = ld16((const uint8_t*) aq + base + 16);
-        const uint4 a2 = ld16((const uint8_t*) aq + base + 32), a3 = ld16((const uint8_t*) aq + base + 48);
-        int ilo = dot16(and4(w.q0, 0x0f0f0f0fu), a0, 0);
-        ilo = dot16(and4(w.q1, 0x0f0f0f0fu), a1, ilo);
-        int ihi = dot16(and4(shr4(w.q0, 4), 0x0f0f0f0fu), a2, 0);
-        ihi = dot16(and4(shr4(w.q1, 4), 0x0f0f0f0fu), a3, ihi);
-        int sc0, sc1, mn0, mn1;
-        q4k_pair_scales(w.h, g, sc0, sc1, mn0, mn1);
-        const float d = h2f(w.h.x & 0xffffu), dmin = h2f(w.h.x >> 16);
-        const float ad0 = ad[bl], ad1 = ad[bl + 1];
-        const float as0 = A.s[(int64_t) t * nb + bl], as1 = A.s[(int64_t) t * nb + bl + 1];
-        const float f0 = (ad0 * (float) sc0) * d, f1 = (ad1 * (float) sc1) * d;
-        return (float) ilo * f0 + (float) ihi * f1 - dmin * ((float) mn0 * (as0 * ad0) + (float) mn1 * (as1 * ad1));
-    } else if constexpr (DT == Q8_0) {
-        // jam_mm_q8_0_gemv_avx512 / q256 engine (avx512.c:374-390, jam_gemm_q256.inc:28-36): fl(d·ad)·Σq·aq
-        const uint4 a0 = ld16((const uint8_t*) aq + 32 * u), a1 = ld16((const uint8_t*) aq + 32 * u + 16);
-        const int I = dot16(w.q1, a1, dot16(w.q0, a0, 0));
-        return (float) I * (h2f(w.d) * ad[u]);
-    } else if constexpr (DT == Q4_0) {
-        // jam_decode_q4_0_256 + q256 engine: fl(d·ad)·Σ(nib-8)·aq, with Σ(nib-8)·aq = Σnib·aq - 8·Σaq
-        const uint4 a0 = ld16((const uint8_t*) aq + 32 * u), a1 = ld16((const uint8_t*) aq + 32 * u + 16);
-        int I = dot16(and4(w.q, 0x0f0f0f0fu), a0, 0);
-        I = dot16(and4(shr4(w.q, 4), 0x0f0f0f0fu), a1, I);
-        I -= 8 * (int) A.s[(int64_t) t * nb + u];
-        return (float) I * (h2f(w.d) * ad[u]);
-    } else if constexpr (DT == MXFP4) {
-        // jam_decode_mxfp4_256 + q256 engine: fl(dhalf·ad)·Σcode·aq
-        const uint4 a0 = ld16((const uint8_t*) aq + 32 * u), a1 = ld16((const uint8_t*) aq + 32 * u + 16);
-        int I = dot16(mxfp4_codes4(and4(w.q, 0x0f0f0f0fu)), a0, 0);
-        I = dot16(mxfp4_codes4(and4(shr4(w.q, 4), 0x0f0f0f0fu)), a1, I);
-        return (float) I * (e8m0_half(w.d) * ad[u]);
+        const uint4 h = w.s;
+        const float d = h2f(h.x & 0xffffu), dmin = h2f(h.x >> 16);
+        float acc = 0.0f, msum = 0.0f;
+#pragma unroll
+        for (int s = 0; s < 8; s++) {   // sub-block s: chunks 2(s>>1), 2(s>>1)+1, low nibbles if s even
+            const int c0 = 2 * (s >> 1);
+            const uint4 w0 = (s & 1) ? hi_nib(w.q[c0]) : lo_nib(w.q[c0]);
+            const uint4 w1 = (s & 1) ? hi_nib(w.q[c0 + 1]) : lo_nib(w.q[c0 + 1]);
+            const int I = dot16(w1, ld16(aq + 32 * s + 16), dot16(w0, ld16(aq + 32 * s), 0));
+            int sc, mn;
+            q4k_sm(h, s, sc, mn);
+            if constexpr (FL == 1) {
+                // jam_mm_q4k_avx512vnni (jam_kernels_q4k_avx512.c:956-1054):
+                //   Σ_s I_s·fl(fl(ad·sc)·d)  −  dmin·Σ_s mn·fl(asum·ad)
+                acc += (float) I * ((ad[s] * (float) sc) * d);
+                msum += (float) mn * (as[s] * ad[s]);
+            } else {
+                // q4k_block16 (jam_kernels_q4k_avx512.c:76-95): fl(fl(d·sc)·dx)·I − fl(dmin·mn)·fl(xs0+xs1)
+                acc += (float) I * ((d * (float) sc) * ad[s]);
+                msum += (dmin * (float) mn) * (as[2 * s] + as[2 * s + 1]);
+            }
+        }
+        return FL == 1 ? acc - dmin * msum : acc - msum;
+    } else if constexpr (DT == Q6_K) {
+        const float d = h2f(w.s.x & 0xffffu);
+        const uint4 scv = w.q[12];
+        float blk[8];
+#pragma unroll
+        for (int b = 0; b < 8; b++) blk[b] = 0.0f;
+        float off = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 8; c++) {   // ql chunk c: half h, j = jj (low nibbles) and jj+2, l = 16lh..
+            const int h = c >> 2, jj = (c >> 1) & 1, lh = c & 1;
+            uint4 qa, qb;
+            q6k_codes(w.q[c], w.q[8 + 2 * h + lh], jj, qa, qb);
+            const int ta = 8 * h + 2 * jj + lh, tb = ta + 4;   // 16-element groups (= scale index)
+            const int ia = dot16(qa, ld16(aq + 16 * ta), 0), ib = dot16(qb, ld16(aq + 16 * tb), 0);
+            const float sa = d * (float) sbyte(word(scv, ta >> 2), ta & 3);
+            const float sb = d * (float) sbyte(word(scv, tb >> 2), tb & 3);
+            if constexpr (FL == 1) {
+                // jam_mm_q6k_sse3 (jam_kernels_kquant_sse3.c:125-169): ad·(fl(d·sc)·Σ(q6-32)·aq) per 16
+                blk[ta >> 1] += sa * (float) (ia - 32 * s16[ta]);
+                blk[tb >> 1] += sb * (float) (ib - 32 * s16[tb]);
+            } else {
+                // q6k_block16 (jam_kernels_q4k_avx512.c:222-236): fl(fl(d·sc)·dx)·Σq6·xq − fl(d·sc)·fl(32·xs16)
+                blk[ta >> 1] += (float) ia * (sa * ad[ta >> 1]);
+                blk[tb >> 1] += (float) ib * (sb * ad[tb >> 1]);
+                off += sa * (32.0f * as[ta]) + sb * (32.0f * as[tb]);
+            }
+        }
+        float acc = 0.0f;
+#pragma unroll
+        for (int b = 0; b < 8; b++) acc += FL == 1 ? ad[b] * blk[b] : blk[b];
+        return acc - off;
     } else {
-        // jam_mm_q6k_sse3 (jam_kernels_kquant_sse3.c:125-169): ad·(fl(d·sc)·Σ(q6-32)·aq) per 16-half,
-        // with Σ(q6-32)·aq = Σq6·aq - 32·Σaq (exact ints).
-        const int sb = u >> 3, tt = u & 7, h = tt >> 2, jj = (tt >> 1) & 1, lh = tt & 1;
-        const int blka = sb * 8 + 4 * h + jj, blkb = blka + 2;
-        const uint4 aa = ld16((const uint8_t*) aq + 32 * blka + 16 * lh);
-        const uint4 ab = ld16((const uint8_t*) aq + 32 * blkb + 16 * lh);
-        const uint4 hia = and4(shr4(w.qh, 2 * jj), 0x03030303u), hib = and4(shr4(w.qh, 2 * jj + 4), 0x03030303u);
-        const uint4 lo = and4(w.ql, 0x0f0f0f0fu), hi = and4(shr4(w.ql, 4), 0x0f0f0f0fu);
-        const uint4 qa = make_uint4(lo.x | (hia.x << 4), lo.y | (hia.y << 4), lo.z | (hia.z << 4), lo.w | (hia.w << 4));
-        const uint4 qb = make_uint4(hi.x | (hib.x << 4), hi.y | (hib.y << 4), hi.z | (hib.z << 4), hi.w | (hib.w << 4));
-        const int* s16 = A.s16 + (int64_t) t * (k >> 4);
-        const int ia = dot16(qa, aa, 0) - 32 * s16[2 * blka + lh];
-        const int ib = dot16(qb, ab, 0) - 32 * s16[2 * blkb + lh];
-        const int byte = 2 * jj + lh;
-        const int sca = sbyte(h ? w.sc.z : w.sc.x, byte), scb = sbyte(h ? w.sc.w : w.sc.y, byte);
-        const float d = h2f(w.d);
-        return ad[blka] * ((d * (float) sca) * (float) ia) + ad[blkb] * ((d * (float) scb) * (float) ib);
+        float acc = 0.0f;
+#pragma unroll
+        for (int b = 0; b < 8; b++) {
+            const int bb = b < nbv ? b : nbv - 1;   // stay inside the token's activations
+            int I;
+            float sw;
+            if constexpr (DT == Q8_0) {
+                I = dot16(w.q[2 * b + 1], ld16(aq + 32 * bb + 16), dot16(w.q[2 * b], ld16(aq + 32 * bb), 0));
+                sw = h2f((word(w.s, b >> 1) >> (16 * (b & 1))) & 0xffffu);
+            } else if constexpr (DT == Q4_0) {
+                I = dot16(hi_nib(w.q[b]), ld16(aq + 32 * bb + 16), dot16(lo_nib(w.q[b]), ld16(aq + 32 * bb), 0));
+                sw = h2f((word(w.s, b >> 1) >> (16 * (b & 1))) & 0xffffu);
+                if constexpr (FL == 1) I -= 8 * (s16[2 * bb] + s16[2 * bb + 1]);
+            } else {
+                I = dot16(mxfp4_codes4(hi_nib(w.q[b])), ld16(aq + 32 * bb + 16),
+                          dot16(mxfp4_codes4(lo_nib(w.q[b])), ld16(aq + 32 * bb), 0));
+                sw = e8m0_half((word(w.s, b >> 2) >> (8 * (b & 3))) & 0xffu);
+            }
+            // F1 (q256 engine, jam_gemm_q256.inc:28-36) and F2 (q8/q4_0/mxfp4_block16): fl(sw·da)·I;
+            // Q4_0 under F2 also takes − fl(8·d)·fl(xs0+xs1) (jam_kernels_q4k_avx512.c:463-480)
+            float v = (float) I * (sw * ad[bb]);
+            if constexpr (DT == Q4_0 && FL == 2) v -= (8.0f * sw) * (as[2 * bb] + as[2 * bb + 1]);
+            acc += b < nbv ? v : 0.0f;
+        }
+        return acc;
     }
 }
 
-// F2: activations from quantize_row_q8s — q, d per 32, raw f32 Σx per 16 (A.s).
-template <int DT>
-JAMHIP_DEV float unit_f2(const typename WRegs<DT>::T& w, int u, const ActQ& A, int t, int k) {
-    const int nb = k >> 5;
-    const int8_t* aq = A.q + (int64_t) t * k;
-    const float* dx = A.d + (int64_t) t * nb;
-    const float* xs = A.s + (int64_t) t * (k >> 4);
-    if constexpr (DT == Q4_K) {
-        // q4k_block16 (jam_kernels_q4k_avx512.c:76-95): fl(fl(d·sc)·dx)·I − fl(dmin·mn)·fl(xs0+xs1)
-        const int sb = u >> 2, g = u & 3, base = sb * 256 + 64 * g, bl = sb * 8 + 2 * g;
-        const uint4 a0 = ld16((const uint8_t*) aq + base), a1 = ld16((const uint8_t*) aq + base + 16);
-        const uint4 a2 = ld16((const uint8_t*) aq + base + 32), a3 = ld16((const uint8_t*) aq + base + 48);
-        int ilo = dot16(and4(w.q0, 0x0f0f0f0fu), a0, 0);
-        ilo = dot16(and4(w.q1, 0x0f0f0f0fu), a1, ilo);
-        int ihi = dot16(and4(shr4(w.q0, 4), 0x0f0f0f0fu), a2, 0);
-        ihi = dot16(and4(shr4(w.q1, 4), 0x0f0f0f0fu), a3, ihi);
-        int sc0, sc1, mn0, mn1;
-        q4k_pair_scales(w.h, g, sc0, sc1, mn0, mn1);
-        const float d = h2f(w.h.x & 0xffffu), dmin = h2f(w.h.x >> 16);
-        const float dw0 = d * (float) sc0, dw1 = d * (float) sc1, mw0 = dmin * (float) mn0, mw1 = dmin * (float) mn1;
-        return (float) ilo * (dw0 * dx[bl]) - mw0 * (xs[2 * bl] + xs[2 * bl + 1])
-             + (float) ihi * (dw1 * dx[bl + 1]) - mw1 * (xs[2 * bl + 2] + xs[2 * bl + 3]);
-    } else if constexpr (DT == Q8_0) {
-        // q8_block16 (jam_kernels_q4k_avx512.c:347-362): fl(d·dx)·Σq·xq
-        const uint4 a0 = ld16((const uint8_t*) aq + 32 * u), a1 = ld16((const uint8_t*) aq + 32 * u + 16);
-        const int I = dot16(w.q1, a1, dot16(w.q0, a0, 0));
-        return (float) I * (h2f(w.d) * dx[u]);
-    } else if constexpr (DT == Q4_0) {
-        // q4_0_block16 (jam_kernels_q4k_avx512.c:463-480): fl(d·dx)·Σnib·xq − fl(8d)·fl(xs0+xs1)
-        const uint4 a0 = ld16((const uint8_t*) aq + 32 * u), a1 = ld16((const uint8_t*) aq + 32 * u + 16);
-        int I = dot16(and4(w.q, 0x0f0f0f0fu), a0, 0);
-        I = dot16(and4(shr4(w.q, 4), 0x0f0f0f0fu), a1, I);
-        const float d = h2f(w.d);
-        return (float) I * (d * dx[u]) - (8.0f * d) * (xs[2 * u] + xs[2 * u + 1]);
-    } else if constexpr (DT == MXFP4) {
-        // mxfp4_block16 (jam_kernels_q4k_avx512.c:692-711): fl(dhalf·dx)·Σcode·xq
-        const uint4 a0 = ld16((const uint8_t*) aq + 32 * u), a1 = ld16((const uint8_t*) aq + 32 * u + 16);
-        int I = dot16(mxfp4_codes4(and4(w.q, 0x0f0f0f0fu)), a0, 0);
-        I = dot16(mxfp4_codes4(and4(shr4(w.q, 4), 0x0f0f0f0fu)), a1, I);
-        return (float) I * (e8m0_half(w.d) * dx[u]);
-    } else {
-        // q6k_block16 (jam_kernels_q4k_avx512.c:222-236): fl(fl(d·sc)·dx)·Σq6·xq − fl(d·sc)·fl(32·xs16)
-        const int sb = u >> 3, tt = u & 7, h = tt >> 2, jj = (tt >> 1) & 1, lh = tt & 1;
-        const int blka = sb * 8 + 4 * h + jj, blkb = blka + 2;
-        const uint4 aa = ld16((const uint8_t*) aq + 32 * blka + 16 * lh);
-        const uint4 ab = ld16((const uint8_t*) aq + 32 * blkb + 16 * lh);
-        const uint4 hia = and4(shr4(w.qh, 2 * jj), 0x03030303u), hib = and4(shr4(w.qh, 2 * jj + 4), 0x03030303u);
-        const uint4 lo = and4(w.ql, 0x0f0f0f0fu), hi = and4(shr4(w.ql, 4), 0x0f0f0f0fu);
-        const uint4 qa = make_uint4(lo.x | (hia.x << 4), lo.y | (hia.y << 4), lo.z | (hia.z << 4), lo.w | (hia.w << 4));
-        const uint4 qb = make_uint4(hi.x | (hib.x << 4), hi.y | (hib.y << 4), hi.z | (hib.z << 4), hi.w | (hib.w << 4));
-        const int ia = dot16(qa, aa, 0), ib = dot16(qb, ab, 0);
-        const int byte = 2 * jj + lh;
-        const int sca = sbyte(h ? w.sc.z : w.sc.x, byte), scb = sbyte(h ? w.sc.w : w.sc.y, byte);
-        const float d = h2f(w.d);
-        const float dwa = d * (float) sca, dwb = d * (float) scb;
-        return (float) ia * (dwa * dx[blka]) - dwa * (32.0f * xs[2 * blka + lh])
-             + (float) ib * (dwb * dx[blkb]) - dwb * (32.0f * xs[2 * blkb + lh]);
+// ------------------------------------------------------------------------------ fused F1 prologue
+// Quantizes NT activation rows into LDS with jam's F1 (quant.h) in the group layout: per token and group
+// 256 int8 codes padded to QS_LDS bytes (conflict-free reads), 8 block scales, 8 block sums, 16 Σq per 16.
+// One thread per 16-element half-block; the halves of a 32-block sit in adjacent lanes, which exchange
+// their |x| maxima and Σq. Elements past k (a partial last group) quantize as zeros.
+constexpr int QS_LDS = 272;
+
+template <int NT>
+JAMHIP_DEV void f1_to_lds(const float* __restrict__ a, int lda, int k, int Gk, int8_t* lq, float* ld, float* las,
+                          int* ls16) {
+    const int halves = 16 * Gk, total = NT * halves;
+    for (int h = threadIdx.x; h < total; h += 256) {
+        const int j = h / halves, hh = h - j * halves, e0 = 16 * hh;
+        const float* src = a + (int64_t) j * lda + e0;
+        float x[16];
+#pragma unroll
+        for (int e = 0; e < 16; e++) x[e] = e0 + e < k ? src[e] : 0.0f;
+        float am = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 16; e++) am = fmaxf(am, fabsf(x[e]));
+        am = fmaxf(am, __shfl_xor(am, 1));
+        const float db = am / 127.0f;
+        const float id = db > 0.0f ? 1.0f / db : 0.0f;
+        uint32_t pk[4];
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            uint32_t v = 0;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                // lrintf then clamp; a NaN product (non-finite input) lands on -128 like LONG_MIN does
+                const int q = (int) fminf(fmaxf(rintf(x[4 * g + e] * id), -128.0f), 127.0f);
+                v |= (uint32_t) (q & 0xff) << (8 * e);
+            }
+            pk[g] = v;
+        }
+        int s = dot4((int) pk[0], 0x01010101, 0);
+        s = dot4((int) pk[1], 0x01010101, s);
+        s = dot4((int) pk[2], 0x01010101, s);
+        s = dot4((int) pk[3], 0x01010101, s);
+        const int s32 = s + __shfl_xor(s, 1);
+        const int grp = hh >> 4;
+        *reinterpret_cast<uint4*>(lq + (int64_t) (j * Gk + grp) * QS_LDS + 16 * (hh & 15)) =
+            make_uint4(pk[0], pk[1], pk[2], pk[3]);
+        ls16[j * halves + hh] = s;
+        if ((hh & 1) == 0) {
+            ld[j * 8 * Gk + (hh >> 1)] = db;
+            las[j * 8 * Gk + (hh >> 1)] = (float) s32;
+        }
     }
 }
 
 // ------------------------------------------------------------------------------------------ kernel
-// FL = 1 (n < 8): NT is the exact token count. FL = 2 (skinny n >= 8): blockIdx.y picks 8 tokens,
-// the last group may hold fewer (ntv). FUSE (FL = 1 only): the workgroup quantizes A into LDS itself
-// (F1, bit-exact) while its first weight loads are in flight, so a decode matmul is a single launch.
-template <int DT, int FL, int NT, int ROWS, bool FUSE>
-__global__ void __launch_bounds__(256) gemv_kernel(WeightView w, ActQ A, const float* __restrict__ a, int lda,
-                                                   int k, int m, int n, float* __restrict__ c, int ldc) {
-    const int lane = threadIdx.x & 63;
-    const int64_t row0 = ((int64_t) blockIdx.x * 4 + (threadIdx.x >> 6)) * ROWS;
+// FL = 1: F1 activations, NT = n (1..7). FUSE: quantized into LDS by this workgroup; else read from A.
+// FL = 2: F2 activations from A; blockIdx.y picks NT tokens, the last group may hold fewer (ntv).
+template <int DT, int FL, int NT, int DEPTH, bool FUSE>
+__global__ void __launch_bounds__(256) mv_kernel(WeightView w, ActQ A, const float* __restrict__ a, int lda,
+                                                 int k, int m, int n, float* __restrict__ c, int ldc, int rows_per_wg) {
+    constexpr int NC = group_chunks(DT), SB = group_scale_bytes(DT), BPG = blocks_per_group(DT);
+    const int lane = threadIdx.x & 63, rq = lane >> 4, li = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nb = k >> 5;                       // 32-blocks in the call
+    const int Gk = (nb + 7) >> 3;                // groups in the call
+    const int64_t Gs = w.G;                      // groups per row in the layout
+    const int J = (Gk + 15) >> 4;                // group slots per lane and row
+    const int64_t r_begin = (int64_t) blockIdx.x * rows_per_wg;
+    const int64_t r_end = r_begin + rows_per_wg < m ? r_begin + rows_per_wg : m;
+    const int64_t quads = (r_end - r_begin + 3) / 4;
+    const int64_t my_quads = quads - wave > 0 ? (quads - wave + 3) / 4 : 0;
+    const int64_t items = my_quads * J;
     const int t0 = blockIdx.y * NT;
     const int ntv = n - t0 < NT ? n - t0 : NT;
-    constexpr int UE = unit_elems<DT>();
-    const int units = k / UE;
 
-    typename WRegs<DT>::T wr[ROWS];
+    // the item DEPTH ahead of the one being computed: quad index qd_ld, slot j_ld. Loads are unconditional
+    // (past the wave's last item they repeat it; a lane past the row's last group re-reads that group,
+    // a lane past the range's last row re-reads that row; those partials are discarded).
+    Group<DT> buf[DEPTH];
+    int64_t qd_ld = 0;
+    int j_ld = 0;
+    auto issue = [&](Group<DT>& dst) {
+        const int64_t qd = qd_ld < my_quads ? qd_ld : (my_quads > 0 ? my_quads - 1 : 0);
+        int64_t row = r_begin + 4 * (wave + 4 * qd) + rq;
+        row = row < r_end ? row : r_end - 1;
+        const int g = 16 * j_ld + li < Gk ? 16 * j_ld + li : Gk - 1;
+        load_group<DT>(dst, w.qs + row * (NC * 16 * Gs), w.sc + row * (SB * Gs), Gs, g);
+        if (++j_ld == J) {
+            j_ld = 0;
+            qd_ld++;
+        }
+    };
+#pragma unroll
+    for (int d = 0; d < DEPTH; d++) issue(buf[d]);
+
+    // activation views: group stride QS bytes of codes, per-token strides
+    const int8_t* aq = A.q;
+    const float* ad = A.d;
+    const float* as = A.s;
+    const int* s16 = A.s16;
+    int64_t tq = k, td = nb, ts = FL == 1 ? nb : 2 * nb, t16 = 2 * nb;
+    int QS = 256;
     if constexpr (FUSE) {
         extern __shared__ __align__(16) unsigned char smem[];
-        const int nb = k >> 5;
         int8_t* lq = reinterpret_cast<int8_t*>(smem);
-        float* ld = reinterpret_cast<float*>(smem + NT * k);
-        float* las = ld + NT * nb;
-        int* ls16 = reinterpret_cast<int*>(las + NT * nb);
-        if (lane < units && row0 < m) {   // first weight loads go out before the quantization
-#pragma unroll
-            for (int r = 0; r < ROWS; r++) wr[r] = load_w<DT>(w, row0 + r < m ? row0 + r : m - 1, lane);
-        }
-        for (int e = threadIdx.x; e < NT * k; e += 256) {   // 32-lane groups are whole blocks
-            const int j = e / k, ee = e - j * k;
-            float db;
-            int h16, h32;
-            lq[e] = (int8_t) f1_lane(a[(int64_t) j * lda + ee], db, h16, h32);
-            if ((ee & 15) == 0) ls16[j * (k >> 4) + (ee >> 4)] = h16;
-            if ((ee & 31) == 0) {
-                ld[j * nb + (ee >> 5)] = db;
-                las[j * nb + (ee >> 5)] = (float) h32;
-            }
-        }
+        float* ld = reinterpret_cast<float*>(smem + NT * Gk * QS_LDS);
+        float* las = ld + NT * 8 * Gk;
+        int* ls16 = reinterpret_cast<int*>(las + NT * 8 * Gk);
+        f1_to_lds<NT>(a, lda, k, Gk, lq, ld, las, ls16);
         __syncthreads();
-        A = ActQ{lq, ld, las, ls16};
+        aq = lq;
+        ad = ld;
+        as = las;
+        s16 = ls16;
+        tq = (int64_t) Gk * QS_LDS;
+        td = ts = 8 * Gk;
+        t16 = 16 * Gk;
+        QS = QS_LDS;
     }
-    if (row0 >= m) return;
 
-    float acc[ROWS][NT];
+    float acc[NT];
 #pragma unroll
-    for (int r = 0; r < ROWS; r++)
+    for (int t = 0; t < NT; t++) acc[t] = 0.0f;
+    int64_t qd_cu = 0;
+    int j_cu = 0;
+    for (int64_t it = 0; it < items; it += DEPTH) {
 #pragma unroll
-        for (int t = 0; t < NT; t++) acc[r][t] = 0.0f;
-
-    bool loaded = FUSE;
-    for (int u = lane; u < units; u += 64) {
-        if (!loaded) {
+        for (int d = 0; d < DEPTH; d++) {
+            if (it + d < items) {   // wave-uniform
+                const int g = 16 * j_cu + li;
+                const bool live = g < Gk;
+                const int gg = live ? g : Gk - 1;
+                const int nbv = nb - BPG * gg < BPG ? nb - BPG * gg : BPG;
 #pragma unroll
-            for (int r = 0; r < ROWS; r++) wr[r] = load_w<DT>(w, row0 + r < m ? row0 + r : m - 1, u);  // clamp: in bounds
-        }
-        loaded = false;
+                for (int t = 0; t < NT; t++) {
+                    if (FL == 2 && t >= ntv) break;
+                    const int tt = FUSE ? t : t0 + t;
+                    const float part = group_dot<DT, FL>(
+                        buf[d], aq + tt * tq + (int64_t) gg * QS, ad + tt * td + 8 * gg,
+                        as + tt * ts + (FL == 1 ? 8 : 16) * gg, s16 + tt * t16 + 16 * gg, nbv);
+                    acc[t] += live ? part : 0.0f;
+                }
+                if (++j_cu == J) {
+                    const int64_t row = r_begin + 4 * (wave + 4 * qd_cu) + rq;
 #pragma unroll
-        for (int t = 0; t < NT; t++) {
-            if (FL == 2 && t >= ntv) break;
-            const int tt = FUSE ? t : t0 + t;
-#pragma unroll
-            for (int r = 0; r < ROWS; r++)
-                acc[r][t] += FL == 1 ? unit_f1<DT>(wr[r], u, A, tt, k) : unit_f2<DT>(wr[r], u, A, tt, k);
+                    for (int t = 0; t < NT; t++) {
+                        if (FL == 2 && t >= ntv) break;
+                        const float v = row16_sum(acc[t]);
+                        if (li == t && row < r_end) c[(int64_t) (t0 + t) * ldc + row] = v;
+                        acc[t] = 0.0f;
+                    }
+                    j_cu = 0;
+                    qd_cu++;
+                }
+            }
+            issue(buf[d]);
         }
     }
-#pragma unroll
-    for (int r = 0; r < ROWS; r++)
-#pragma unroll
-        for (int t = 0; t < NT; t++) {
-            if (FL == 2 && t >= ntv) break;
-            const float v = wave_sum(acc[r][t]);
-            if (lane == 0 && row0 + r < m) c[(int64_t) (t0 + t) * ldc + row0 + r] = v;
-        }
 }
 
-// Fused F1 quantization keeps A's int8 copy in LDS: 1.5 bytes per element (q, d, asum, Σ16).
-constexpr int kFuseMaxElems = 32768;
+// ----------------------------------------------------------------------------- float-dot tail rows
+// The last m % 16 rows of an n >= 8 call: jam's bands compute them with an exact float dot of the
+// dequantized weight against the f32 activations ("<16-row tail: scalar exact dot",
+// jam_kernels_q4k_avx512.c:185-188 and its siblings). One wave per (row, 8-token group); lane l takes
+// the 32-element chunks l, l+64, ...; products accumulate in f32.
+template <int DT>
+JAMHIP_DEV float deq(const WeightView& w, int64_t row, int elem) {
+    constexpr int NC = group_chunks(DT), SB = group_scale_bytes(DT);
+    const int64_t g = elem >> 8;
+    const int e = elem & 255;
+    const uint8_t* q = w.qs + row * (NC * 16 * w.G);
+    const uint8_t* s = w.sc + row * (SB * w.G) + g * SB;
+    auto qb = [&](int byte) { return q[((int64_t) (byte >> 4) * w.G + g) * 16 + (byte & 15)]; };   // group byte
+    auto f16 = [&](const uint8_t* p) { return h2f((uint32_t) p[0] | ((uint32_t) p[1] << 8)); };
+    if constexpr (DT == Q8_0) {
+        return f16(s + 2 * (e >> 5)) * (float) (int8_t) qb(e);
+    } else if constexpr (DT == Q4_0) {
+        const uint8_t b = qb(16 * (e >> 5) + (e & 15));
+        return f16(s + 2 * (e >> 5)) * (float) (((e & 31) < 16 ? b & 15 : b >> 4) - 8);
+    } else if constexpr (DT == MXFP4) {
+        const uint8_t b = qb(16 * (e >> 5) + (e & 15));
+        const uint32_t code = mxfp4_codes((e & 31) < 16 ? b & 15 : b >> 4);
+        return e8m0_half(s[e >> 5]) * (float) (int8_t) (code & 0xff);
+    } else if constexpr (DT == Q4_K) {
+        const int gp = e >> 6, half = (e >> 5) & 1, l = e & 31, sb = 2 * gp + half;
+        const uint8_t b = qb(32 * gp + l);
+        const uint4 h = make_uint4(s[0] | s[1] << 8 | s[2] << 16 | (uint32_t) s[3] << 24,
+                                   s[4] | s[5] << 8 | s[6] << 16 | (uint32_t) s[7] << 24,
+                                   s[8] | s[9] << 8 | s[10] << 16 | (uint32_t) s[11] << 24,
+                                   s[12] | s[13] << 8 | s[14] << 16 | (uint32_t) s[15] << 24);
+        int sc, mn;
+        q4k_sm(h, sb, sc, mn);
+        return f16(s) * (float) sc * (float) (half ? b >> 4 : b & 15) - f16(s + 2) * (float) mn;
+    } else {
+        const int hh = e >> 7, j = (e & 127) >> 5, l = e & 31;
+        const uint8_t qlb = qb(64 * hh + (j & 1) * 32 + l);
+        const int q6 = (j < 2 ? qlb & 15 : qlb >> 4) | (((qb(128 + 32 * hh + l) >> (2 * j)) & 3) << 4);
+        const int sc = (int) (int8_t) qb(192 + 8 * hh + 2 * j + l / 16);
+        return f16(s) * (float) sc * (float) (q6 - 32);
+    }
+}
 
-template <int DT, int FL, int NT, int ROWS>
+template <int DT>
+__global__ void __launch_bounds__(64) rows_float_kernel(WeightView w, const float* __restrict__ a, int lda, int k,
+                                                        int r0, int n, float* __restrict__ c, int ldc) {
+    const int64_t row = r0 + blockIdx.x;
+    const int t0 = blockIdx.y * 8, nt = n - t0 < 8 ? n - t0 : 8;
+    const int lane = threadIdx.x;
+    float acc[8];
+#pragma unroll
+    for (int t = 0; t < 8; t++) acc[t] = 0.0f;
+    for (int chunk = lane; chunk < k / 32; chunk += 64) {   // 32 consecutive elements per lane and step
+        for (int e = 32 * chunk; e < 32 * chunk + 32; e++) {
+            const float v = deq<DT>(w, row, e);
+#pragma unroll
+            for (int t = 0; t < 8; t++)
+                if (t < nt) acc[t] += v * a[(int64_t) (t0 + t) * lda + e];
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < 8; t++) {
+        const float v = wave_sum(acc[t]);
+        if (lane == 0 && t < nt) c[(int64_t) (t0 + t) * ldc + row] = v;
+    }
+}
+
+// ---------------------------------------------------------------------------------------- launchers
+// Fused F1 quantization keeps A's codes, scales and sums in LDS: 400 bytes per token and group.
+constexpr int kFuseMaxBytes = 96 * 1024;
+static size_t fuse_lds(int n, int k) { return (size_t) n * ((k / 32 + 7) / 8) * (QS_LDS + 32 + 32 + 64); }
+
+// Workgroups per launch. Each takes a contiguous range of rows; the fused variant pays its F1 prologue
+// once per workgroup, so it runs fewer, longer-lived ones. JAM_HIP_MV_WGS overrides (tuning sweeps).
+static int mv_wgs(int64_t m, bool fused) {
+    const char* v = getenv("JAM_HIP_MV_WGS");
+    const int over = v ? atoi(v) : 0;
+    const int64_t want = over > 0 ? over : (fused ? 512 : 1024);
+    const int64_t most = (m + 3) / 4;   // at least one row quad per workgroup
+    return (int) (want < most ? want : most);
+}
+
+template <int DT, int FL, int NT, int DEPTH>
 static hipError_t go(const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m, int n, float* c,
                      int ldc, hipStream_t st) {
-    const int waves = (m + ROWS - 1) / ROWS;
-    dim3 grid((waves + 3) / 4, FL == 1 ? 1 : (n + NT - 1) / NT);
-    if (FL == 1 && a != nullptr) {
-        const size_t lds = (size_t) NT * k + (size_t) NT * (k / 32) * 8 + (size_t) NT * (k / 16) * 4;
-        gemv_kernel<DT, FL, NT, ROWS, true><<<grid, 256, lds, st>>>(w, A, a, lda, k, m, n, c, ldc);
-    } else {
-        gemv_kernel<DT, FL, NT, ROWS, false><<<grid, 256, 0, st>>>(w, A, a, lda, k, m, n, c, ldc);
+    const bool fuse = FL == 1 && a != nullptr;
+    const int wgs = mv_wgs(m, fuse);
+    int rows_per_wg = (m + wgs - 1) / wgs;
+    rows_per_wg = (rows_per_wg + 3) & ~3;   // whole quads per workgroup
+    dim3 grid((m + rows_per_wg - 1) / rows_per_wg, FL == 1 ? 1 : (n + NT - 1) / NT);
+    if constexpr (FL == 1) {
+        if (fuse) {
+            mv_kernel<DT, FL, NT, DEPTH, true><<<grid, 256, fuse_lds(NT, k), st>>>(w, A, a, lda, k, m, n, c, ldc,
+                                                                                   rows_per_wg);
+            return hipGetLastError();
+        }
     }
+    mv_kernel<DT, FL, NT, DEPTH, false><<<grid, 256, 0, st>>>(w, A, a, lda, k, m, n, c, ldc, rows_per_wg);
     return hipGetLastError();
 }
 
 template <int DT>
 static hipError_t gemv_dt(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m,
                           int n, float* c, int ldc, hipStream_t st) {
-    if (flavour == 2) return go<DT, 2, 8, 1>(w, A, nullptr, 0, k, m, n, c, ldc, st);
-    const bool big = m >= 8192;
+    constexpr int D = DT == Q8_0 || DT == Q6_K ? 2 : 3;   // ring depth within the register budget
+    if (flavour == 2) return go<DT, 2, 8, 2>(w, A, nullptr, 0, k, m, n, c, ldc, st);
     switch (n) {
-    case 1:
-        return big ? go<DT, 1, 1, 4>(w, A, a, lda, k, m, n, c, ldc, st) : go<DT, 1, 1, 1>(w, A, a, lda, k, m, n, c, ldc, st);
-    case 2:
-        return big ? go<DT, 1, 2, 2>(w, A, a, lda, k, m, n, c, ldc, st) : go<DT, 1, 2, 1>(w, A, a, lda, k, m, n, c, ldc, st);
-    case 3: return go<DT, 1, 3, 1>(w, A, a, lda, k, m, n, c, ldc, st);
-    case 4: return go<DT, 1, 4, 1>(w, A, a, lda, k, m, n, c, ldc, st);
-    case 5: return go<DT, 1, 5, 1>(w, A, a, lda, k, m, n, c, ldc, st);
-    case 6: return go<DT, 1, 6, 1>(w, A, a, lda, k, m, n, c, ldc, st);
-    case 7: return go<DT, 1, 7, 1>(w, A, a, lda, k, m, n, c, ldc, st);
+    case 1: {
+        const char* v = getenv("JAM_HIP_MV_DEPTH");   // items in flight per wave (tuning sweeps)
+        const int depth = v ? atoi(v) : D;
+        if (depth == 1) return go<DT, 1, 1, 1>(w, A, a, lda, k, m, n, c, ldc, st);
+        if (depth == 2) return go<DT, 1, 1, 2>(w, A, a, lda, k, m, n, c, ldc, st);
+        if (depth == 4) return go<DT, 1, 1, 4>(w, A, a, lda, k, m, n, c, ldc, st);
+        return go<DT, 1, 1, 3>(w, A, a, lda, k, m, n, c, ldc, st);
+    }
+    case 2: return go<DT, 1, 2, D>(w, A, a, lda, k, m, n, c, ldc, st);
+    case 3: return go<DT, 1, 3, 2>(w, A, a, lda, k, m, n, c, ldc, st);
+    case 4: return go<DT, 1, 4, 2>(w, A, a, lda, k, m, n, c, ldc, st);
+    case 5: return go<DT, 1, 5, 2>(w, A, a, lda, k, m, n, c, ldc, st);
+    case 6: return go<DT, 1, 6, 2>(w, A, a, lda, k, m, n, c, ldc, st);
+    case 7: return go<DT, 1, 7, 2>(w, A, a, lda, k, m, n, c, ldc, st);
     default: return hipErrorInvalidValue;
     }
 }
 
-bool gemv_fusable(int n, int k) { return n < 8 && (int64_t) n * k <= kFuseMaxElems; }
+bool gemv_fusable(int n, int k) { return n < 8 && fuse_lds(n, k) <= (size_t) kFuseMaxBytes; }
 
 hipError_t launch_gemv(int dt, int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m,
                        int n, float* c, int ldc, hipStream_t st) {
@@ -348,6 +476,21 @@ hipError_t launch_gemv(int dt, int flavour, const WeightView& w, const ActQ& A, 
     case MXFP4: return gemv_dt<MXFP4>(flavour, w, A, a, lda, k, m, n, c, ldc, st);
     default: return hipErrorInvalidValue;
     }
+}
+
+hipError_t launch_rows_float(int dt, const WeightView& w, const float* a, int lda, int k, int r0, int rows, int n,
+                             float* c, int ldc, hipStream_t st) {
+    if (rows <= 0) return hipSuccess;
+    const dim3 grid((unsigned) rows, (unsigned) ((n + 7) / 8));
+    switch (dt) {
+    case Q4_K: rows_float_kernel<Q4_K><<<grid, 64, 0, st>>>(w, a, lda, k, r0, n, c, ldc); break;
+    case Q6_K: rows_float_kernel<Q6_K><<<grid, 64, 0, st>>>(w, a, lda, k, r0, n, c, ldc); break;
+    case Q8_0: rows_float_kernel<Q8_0><<<grid, 64, 0, st>>>(w, a, lda, k, r0, n, c, ldc); break;
+    case Q4_0: rows_float_kernel<Q4_0><<<grid, 64, 0, st>>>(w, a, lda, k, r0, n, c, ldc); break;
+    case MXFP4: rows_float_kernel<MXFP4><<<grid, 64, 0, st>>>(w, a, lda, k, r0, n, c, ldc); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
 }
 
 }  // namespace jamhip

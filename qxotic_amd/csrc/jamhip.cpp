@@ -43,9 +43,9 @@ struct Pin {
     uintptr_t host;     // registry key: [host, host + span)
     int64_t span;
     int dt, ldw;
-    int64_t rows, rb;   // rows and blocks per row of the device copy
+    int64_t rows, G;    // rows and groups per row of the device copy
     uint8_t* dev;       // plane 0
-    uint8_t* sc;        // plane 1 (nullptr for Q4_K)
+    uint8_t* sc;        // plane 1
     int64_t bytes;      // device bytes held
 };
 
@@ -115,34 +115,24 @@ bool lookup(jamhip_ctx* ctx, const void* w, int dt, int ldw, int m, WeightView* 
         if (off % rbytes) continue;
         const int64_t r0 = off / rbytes;
         if (r0 + m > pin.rows) continue;
-        out->qs = pin.dev + r0 * pin.rb * qs_bytes(dt);
-        out->sc = pin.sc ? pin.sc + r0 * pin.rb * sc_bytes(dt) : nullptr;
-        out->rb = pin.rb;
+        out->qs = pin.dev + r0 * pin.G * group_chunks(dt) * 16;
+        out->sc = pin.sc + r0 * pin.G * group_scale_bytes(dt);
+        out->G = pin.G;
         return true;
     }
     return false;
 }
 
 // Upload `rows` raw host rows (stride raw_stride bytes, rb blocks used per row) into a device-layout
-// buffer at dst (plane 0) / dst_sc (plane 1) via a staging copy and the repack kernel.
+// buffer of G groups per row at dst (plane 0) / dst_sc (plane 1) via a staging copy and the repack kernel.
 jamhip_status upload(jamhip_ctx* ctx, const uint8_t* host, int dt, int64_t raw_stride, int64_t rows, int64_t rb,
-                     uint8_t* dst, uint8_t* dst_sc) {
+                     int64_t G, uint8_t* dst, uint8_t* dst_sc) {
     const int64_t span = (rows - 1) * raw_stride + rb * block_bytes(dt);
     hipError_t e;
-    if (dt == Q4_K) {   // whole blocks are the device layout
-        if (raw_stride == rb * 144) {
-            e = hipMemcpyAsync(dst, host, (size_t) span, hipMemcpyHostToDevice, ctx->stream);
-        } else {
-            e = hipMemcpy2DAsync(dst, (size_t) (rb * 144), host, (size_t) raw_stride, (size_t) (rb * 144),
-                                 (size_t) rows, hipMemcpyHostToDevice, ctx->stream);
-        }
-        if (e != hipSuccess) return hip_fail(ctx, e, "weight upload");
-        return JAMHIP_OK;
-    }
     if ((e = ctx->w_raw.ensure((size_t) span)) != hipSuccess) return hip_fail(ctx, e, "weight staging alloc");
     if ((e = hipMemcpyAsync(ctx->w_raw.p, host, (size_t) span, hipMemcpyHostToDevice, ctx->stream)) != hipSuccess)
         return hip_fail(ctx, e, "weight upload");
-    if ((e = launch_repack(dt, (const uint8_t*) ctx->w_raw.p, raw_stride, rows, rb, dst, dst_sc, ctx->stream)) !=
+    if ((e = launch_repack(dt, (const uint8_t*) ctx->w_raw.p, raw_stride, rows, rb, G, dst, dst_sc, ctx->stream)) !=
         hipSuccess)
         return hip_fail(ctx, e, "weight repack");
     return JAMHIP_OK;
@@ -151,17 +141,17 @@ jamhip_status upload(jamhip_ctx* ctx, const uint8_t* host, int dt, int64_t raw_s
 // Resolve W to a device view: the registry, else a per-call staged copy of rows [0, m), k elements each.
 jamhip_status resolve_w(jamhip_ctx* ctx, const void* w, int dt, int ldw, int m, int k, WeightView* wv) {
     if (lookup(ctx, w, dt, ldw, m, wv)) return JAMHIP_OK;
-    const int64_t rb = k / block_elems(dt);
-    const int64_t qsz = align256((int64_t) m * rb * qs_bytes(dt)), ssz = (int64_t) m * rb * sc_bytes(dt);
+    const int64_t rb = k / block_elems(dt), G = groups_of(dt, rb);
+    const int64_t qsz = align256((int64_t) m * G * group_chunks(dt) * 16), ssz = (int64_t) m * G * group_scale_bytes(dt);
     hipError_t e = ctx->w_stage.ensure((size_t) (qsz + ssz));
     if (e != hipSuccess) return hip_fail(ctx, e, "weight stage alloc");
     uint8_t* dst = (uint8_t*) ctx->w_stage.p;
-    uint8_t* dsc = sc_bytes(dt) ? dst + qsz : nullptr;
-    jamhip_status st = upload(ctx, (const uint8_t*) w, dt, row_bytes(dt, ldw), m, rb, dst, dsc);
+    uint8_t* dsc = dst + qsz;
+    jamhip_status st = upload(ctx, (const uint8_t*) w, dt, row_bytes(dt, ldw), m, rb, G, dst, dsc);
     if (st != JAMHIP_OK) return st;
     wv->qs = dst;
     wv->sc = dsc;
-    wv->rb = rb;
+    wv->G = G;
     return JAMHIP_OK;
 }
 
@@ -192,11 +182,18 @@ jamhip_status compute(jamhip_ctx* ctx, int dt, const WeightView& wv, const float
             return hip_fail(ctx, e, "gemv launch");
         return JAMHIP_OK;
     }
-    if ((e = launch_quant_f2(a, lda, n, k, q, d, s, ctx->stream)) != hipSuccess)
-        return hip_fail(ctx, e, "quant_f2 launch");
-    e = n >= 32 ? launch_gemm(dt, wv, A, k, m, n, c, ldc, ctx->stream) : hipErrorNotSupported;
-    if (e == hipErrorNotSupported) e = launch_gemv(dt, 2, wv, A, nullptr, 0, k, m, n, c, ldc, ctx->stream);
-    if (e != hipSuccess) return hip_fail(ctx, e, "matmul launch");
+    // n >= 8: jam's 16-row F2 bands on rows [0, m16); the last m % 16 rows take the band's float-dot tail
+    // (jam_kernels_q4k_avx512.c:185-188).
+    const int m16 = m - m % 16;
+    if (m16 > 0) {
+        if ((e = launch_quant_f2(a, lda, n, k, q, d, s, ctx->stream)) != hipSuccess)
+            return hip_fail(ctx, e, "quant_f2 launch");
+        e = n >= 32 ? launch_gemm(dt, wv, A, k, m16, n, c, ldc, ctx->stream) : hipErrorNotSupported;
+        if (e == hipErrorNotSupported) e = launch_gemv(dt, 2, wv, A, nullptr, 0, k, m16, n, c, ldc, ctx->stream);
+        if (e != hipSuccess) return hip_fail(ctx, e, "matmul launch");
+    }
+    if ((e = launch_rows_float(dt, wv, a, lda, k, m16, m - m16, n, c, ldc, ctx->stream)) != hipSuccess)
+        return hip_fail(ctx, e, "tail rows launch");
     return JAMHIP_OK;
 }
 
@@ -315,7 +312,7 @@ jamhip_status jamhip_weight_pin(jamhip_ctx* ctx, const void* w, int wt, int ldw,
     if (!guard.ok) return fail(ctx, JAMHIP_EBUSY, "context busy");
     (void) hipSetDevice(ctx->device);
     const uintptr_t host = reinterpret_cast<uintptr_t>(w);
-    const int64_t rb = ldw / block_elems(wt), span = (int64_t) m * row_bytes(wt, ldw);
+    const int64_t rb = ldw / block_elems(wt), G = groups_of(wt, rb), span = (int64_t) m * row_bytes(wt, ldw);
     {
         std::lock_guard<std::mutex> lk(ctx->pin_mu);
         for (const Pin& p : ctx->pins) {
@@ -324,12 +321,12 @@ jamhip_status jamhip_weight_pin(jamhip_ctx* ctx, const void* w, int wt, int ldw,
                 return fail(ctx, JAMHIP_EINVAL, "pin: range overlaps a pinned tensor (evict it first)");
         }
     }
-    const int64_t qsz = align256((int64_t) m * rb * qs_bytes(wt)), ssz = (int64_t) m * rb * sc_bytes(wt);
+    const int64_t qsz = align256((int64_t) m * G * group_chunks(wt) * 16), ssz = (int64_t) m * G * group_scale_bytes(wt);
     uint8_t* dev = nullptr;
     hipError_t e = hipMalloc((void**) &dev, (size_t) (qsz + ssz));
     if (e != hipSuccess) return hip_fail(ctx, e, "pin: device alloc");
-    uint8_t* sc = sc_bytes(wt) ? dev + qsz : nullptr;
-    jamhip_status st = upload(ctx, (const uint8_t*) w, wt, row_bytes(wt, ldw), m, rb, dev, sc);
+    uint8_t* sc = dev + qsz;
+    jamhip_status st = upload(ctx, (const uint8_t*) w, wt, row_bytes(wt, ldw), m, rb, G, dev, sc);
     if (st == JAMHIP_OK && (e = hipStreamSynchronize(ctx->stream)) != hipSuccess) st = hip_fail(ctx, e, "pin: sync");
     if (st != JAMHIP_OK) {
         (void) hipFree(dev);
@@ -337,7 +334,7 @@ jamhip_status jamhip_weight_pin(jamhip_ctx* ctx, const void* w, int wt, int ldw,
     }
     ctx->w_raw.release();   // staging is sized to the tensor; do not hold it
     std::lock_guard<std::mutex> lk(ctx->pin_mu);
-    ctx->pins.push_back(Pin{host, span, wt, ldw, m, rb, dev, sc, qsz + ssz});
+    ctx->pins.push_back(Pin{host, span, wt, ldw, m, G, dev, sc, qsz + ssz});
     return JAMHIP_OK;
 }
 

@@ -38,29 +38,58 @@ __global__ void __launch_bounds__(256) quant_f2_kernel(const float* __restrict__
     if ((e & 31) == 0) d[(int64_t) j * (k >> 5) + (e >> 5)] = db;
 }
 
-// Weight repack: raw GGUF rows (stride raw_stride bytes, rb blocks) -> the two-plane device layout
-// described in common.h. One thread per block; runs once per pinned tensor.
+// Weight repack: raw GGUF rows (stride raw_stride bytes, rb blocks) -> the chunk-major group layout of
+// common.h. One thread per (row, group); a group past the row's last block is zero-filled. Runs once per
+// pinned tensor.
 template <int DT>
 __global__ void __launch_bounds__(256) repack_kernel(const uint8_t* __restrict__ raw, int64_t raw_stride,
-                                                     int64_t rows, int64_t rb, uint8_t* __restrict__ qs,
+                                                     int64_t rows, int64_t rb, int64_t G, uint8_t* __restrict__ qs,
                                                      uint8_t* __restrict__ sc) {
+    constexpr int NC = group_chunks(DT), SB = group_scale_bytes(DT), BPG = blocks_per_group(DT);
     const int64_t i = (int64_t) blockIdx.x * 256 + threadIdx.x;
-    if (i >= rows * rb) return;
-    const int64_t r = i / rb, b = i - r * rb;
-    const uint8_t* src = raw + r * raw_stride + b * block_bytes(DT);
-    uint8_t* dq = qs + i * qs_bytes(DT);
-    uint8_t* ds = sc + i * sc_bytes(DT);
-    if constexpr (DT == Q8_0 || DT == Q4_0) {          // d fp16 @0, payload @2
-        ds[0] = src[0];
-        ds[1] = src[1];
-        for (int t = 0; t < qs_bytes(DT); t++) dq[t] = src[2 + t];
-    } else if constexpr (DT == MXFP4) {                // e8m0 @0, nibbles @1
-        ds[0] = src[0];
-        for (int t = 0; t < 16; t++) dq[t] = src[1 + t];
-    } else if constexpr (DT == Q6_K) {                 // ql/qh/scales @0..207, d fp16 @208
-        for (int t = 0; t < 208; t++) dq[t] = src[t];
-        ds[0] = src[208];
-        ds[1] = src[209];
+    if (i >= rows * G) return;
+    const int64_t r = i / G, g = i - r * G;
+    const uint8_t* row = raw + r * raw_stride;
+    uint8_t* dq = qs + r * (NC * 16 * G) + g * 16;   // chunk c at dq + c·16·G
+    uint8_t* ds = sc + r * (SB * G) + g * SB;
+    auto chunk = [&](int c) { return dq + (int64_t) c * 16 * G; };
+    if constexpr (DT == Q4_K) {                        // d, dmin, scales @0..15, nibbles @16..143
+        const uint8_t* b = row + g * 144;
+        for (int t = 0; t < 16; t++) ds[t] = b[t];
+        for (int c = 0; c < 8; c++)
+            for (int t = 0; t < 16; t++) chunk(c)[t] = b[16 + 16 * c + t];
+    } else if constexpr (DT == Q6_K) {                 // ql @0..127, qh @128..191, scales @192..207, d @208
+        const uint8_t* b = row + g * 210;
+        for (int c = 0; c < 13; c++)
+            for (int t = 0; t < 16; t++) chunk(c)[t] = b[16 * c + t];
+        ds[0] = b[208];
+        ds[1] = b[209];
+    } else {
+        for (int j = 0; j < BPG; j++) {
+            const int64_t blk = g * BPG + j;
+            uint8_t q[32] = {0}, s[2] = {0, 0};   // a block past the row end stays zero (never read)
+            if (blk < rb) {
+                const uint8_t* b = row + blk * block_bytes(DT);
+                const int sbytes = DT == MXFP4 ? 1 : 2, qbytes = DT == Q8_0 ? 32 : 16;
+                for (int t = 0; t < sbytes; t++) s[t] = b[t];
+                for (int t = 0; t < qbytes; t++) q[t] = b[sbytes + t];
+            }
+            if constexpr (DT == Q8_0) {                // d fp16 @0, q @2..33
+                ds[2 * j] = s[0];
+                ds[2 * j + 1] = s[1];
+                for (int t = 0; t < 16; t++) {
+                    chunk(2 * j)[t] = q[t];
+                    chunk(2 * j + 1)[t] = q[16 + t];
+                }
+            } else if constexpr (DT == Q4_0) {         // d fp16 @0, nibbles @2..17
+                ds[2 * j] = s[0];
+                ds[2 * j + 1] = s[1];
+                for (int t = 0; t < 16; t++) chunk(j)[t] = q[t];
+            } else {                                   // MXFP4: e8m0 @0, nibbles @1..16
+                ds[j] = s[0];
+                for (int t = 0; t < 16; t++) chunk(j)[t] = q[t];
+            }
+        }
     }
 }
 
@@ -78,15 +107,16 @@ hipError_t launch_quant_f2(const float* a, int lda, int n, int k, int8_t* q, flo
     return hipGetLastError();
 }
 
-hipError_t launch_repack(int dt, const uint8_t* raw, int64_t raw_stride, int64_t rows, int64_t rb, uint8_t* qs,
-                         uint8_t* sc, hipStream_t st) {
-    const int64_t n = rows * rb;
+hipError_t launch_repack(int dt, const uint8_t* raw, int64_t raw_stride, int64_t rows, int64_t rb, int64_t G,
+                         uint8_t* qs, uint8_t* sc, hipStream_t st) {
+    const int64_t n = rows * G;
     const dim3 grid((unsigned) ((n + 255) / 256));
     switch (dt) {
-    case Q8_0: repack_kernel<Q8_0><<<grid, 256, 0, st>>>(raw, raw_stride, rows, rb, qs, sc); break;
-    case Q4_0: repack_kernel<Q4_0><<<grid, 256, 0, st>>>(raw, raw_stride, rows, rb, qs, sc); break;
-    case MXFP4: repack_kernel<MXFP4><<<grid, 256, 0, st>>>(raw, raw_stride, rows, rb, qs, sc); break;
-    case Q6_K: repack_kernel<Q6_K><<<grid, 256, 0, st>>>(raw, raw_stride, rows, rb, qs, sc); break;
+    case Q8_0: repack_kernel<Q8_0><<<grid, 256, 0, st>>>(raw, raw_stride, rows, rb, G, qs, sc); break;
+    case Q4_0: repack_kernel<Q4_0><<<grid, 256, 0, st>>>(raw, raw_stride, rows, rb, G, qs, sc); break;
+    case MXFP4: repack_kernel<MXFP4><<<grid, 256, 0, st>>>(raw, raw_stride, rows, rb, G, qs, sc); break;
+    case Q6_K: repack_kernel<Q6_K><<<grid, 256, 0, st>>>(raw, raw_stride, rows, rb, G, qs, sc); break;
+    case Q4_K: repack_kernel<Q4_K><<<grid, 256, 0, st>>>(raw, raw_stride, rows, rb, G, qs, sc); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -203,7 +203,10 @@ class Provider:
     """JAM.Provider (JAM.java:21-38) for the MI355X backend."""
 
     def id(self) -> str:
-        return "hip"
+        """`native` by default: jinfer asks only for ids `native` and `vector` (MatMul.java:1770-1771),
+        so answering to `native` above jam-native's priority puts the GPU under an unedited caller;
+        `JAM_HIP_ID=hip` (jam.hip.id) opts out."""
+        return _config("jam.hip.id", "native")
 
     def priority(self) -> int:
         return 2000   # above native (1000), vector (500), scalar (0)

@@ -16,7 +16,7 @@ from oracle import oracle as O
 pytestmark = pytest.mark.gpu
 
 SHAPES = [(104, 1024), (100, 512), (70, 256), (64, 768)]   # JamBackendParityTest.java:204-252
-NS = [1, 2, 3, 4, 7, 8, 13, 16, 17, 33]
+NS = [1, 2, 3, 4, 7, 8, 13, 16, 17, 32, 33, 64, 100]
 
 
 def say(*a):
@@ -204,3 +204,44 @@ def test_full_size_decode(hip, oracle, dt, m, k, n):
     ref = oracle.mm_int8(dt, w, a, m, n, k)
     _, sa = oracle.mm_ref(dt, w, a, m, n, k)
     assert tier1(got, ref, sa).all()
+
+
+# ------------------------------------------------------------------------------------ prefill GEMM
+PREFILL = [(O.Q4_K, 14336, 4096), (O.Q6_K, 4096, 14336)]
+
+
+@pytest.mark.parametrize("dt,m,k", PREFILL)
+def test_prefill_full_size(hip, oracle, dt, m, k):
+    """Config 4 (M=512, 1% +-20 outliers) at full size on the MFMA GEMM. The oracle checks a seeded sample of
+    192 rows against all 512 tokens; the whole output is checked for rerun bit-identity and finiteness."""
+    n = 512
+    say(f"prefill {O.NAMES[dt]} {m}x{k} n={n}")
+    w = oracle.quantize(dt, oracle.normal(0x5A11C0DE ^ 4 ^ dt, (m, k), 0.0, 0.02))
+    a = oracle.outliers(0x5A11C0DE ^ 4, (n, k))
+    got = run_mm(hip, dt, w, a, m, n, k)
+    again = run_mm(hip, dt, w, a, m, n, k)
+    assert np.isfinite(got).all()
+    assert np.array_equal(bits(got), bits(again))
+    rows = np.sort(np.random.default_rng(dt).choice(m, 192, replace=False))
+    ws = np.ascontiguousarray(w[rows])
+    ref = oracle.mm_int8(dt, ws, a, len(rows), n, k)
+    _, sa = oracle.mm_ref(dt, ws, a, len(rows), n, k)
+    ok = tier1(got[:, rows], ref, sa)
+    assert ok.all(), (int((~ok).sum()), float(np.max(np.abs(got[:, rows] - ref) / (np.abs(ref) + 1e-30))))
+
+
+@pytest.mark.parametrize("dt", O.QUANT_TYPES)
+def test_prefill_ragged_shapes(hip, oracle, dt):
+    """GEMM edge tiles: m not a multiple of the row tile (and of 16: float-dot tail), n not a multiple of the
+    token tile, k with a partial 256-element chunk for the 32-element block types."""
+    be = O.BLOCK[dt][0]
+    for (m, n, k) in [(200, 37, 512), (130, 64, 1024), (47, 96, 256 if be == 256 else 288), (16, 33, 2304)]:
+        if k % be:
+            continue
+        say(f"ragged {O.NAMES[dt]} m={m} n={n} k={k}")
+        w = oracle.quantize(dt, oracle.normal(m + n + k, (m, k), 0.0, 0.02))
+        a = oracle.outliers(m * n, (n, k))
+        got = run_mm(hip, dt, w, a, m, n, k)
+        ref = oracle.mm_int8(dt, w, a, m, n, k)
+        _, sa = oracle.mm_ref(dt, w, a, m, n, k)
+        assert tier1(got, ref, sa).all(), (O.NAMES[dt], m, n, k)
