@@ -4,15 +4,12 @@
 // at each dot below.
 //
 // Work split. A lane owns whole 256-element groups of the chunk-major device layout (common.h): 16 lanes
-// (one DPP row) share a weight row and take its groups li, li+16, ...; the 4 rows of a wave's "quad" sit
-// in the wave's 4 lane rows. For each chunk index c the 64 lanes read 4 rows x 16 consecutive groups of
-// 16 bytes, i.e. four contiguous 256-byte runs, and one group's scales come in one more load. An item is
-// one such group-slot of a quad; each wave keeps DEPTH items in flight in a register ring with
-// unconditional loads (the compiler then waits with vmcnt(count) instead of draining the queue), folds
-// a row's 16 lane partials with a DPP butterfly once its last group is done, and a 256-thread workgroup
-// (4 waves) owns a contiguous range of rows, its quads dealt round-robin to the waves. In the fused F1
-// variant the workgroup first quantizes A into LDS (bit-exact F1), once for all of its rows, while its
-// first weight loads are already in flight.
+// (one DPP row) share a weight row and take 16 of its groups per slot, the 4 lane rows of a wave take 4
+// consecutive rows (a "quad"). For each chunk index c the 64 lanes read 4 rows x 16 consecutive groups of
+// 16 bytes, i.e. four contiguous 256-byte runs, and one group's scales come in one more load. Eight waves
+// share a workgroup, the activation prologue and the LDS in which a row's partials from several waves are
+// combined (see mv_kernel). In the fused F1 variant the workgroup quantizes A into LDS (bit-exact F1) once
+// for all of its rows; its activation loads go out first and its weight stream right behind them.
 #include "common.h"
 #include "launch.h"
 #include "quant.h"
@@ -189,17 +186,51 @@ JAMHIP_DEV float group_dot(const Group<DT>& w, const int8_t* aq, const float* ad
 // One thread per 16-element half-block; the halves of a 32-block sit in adjacent lanes, which exchange
 // their |x| maxima and Σq. Elements past k (a partial last group) quantize as zeros.
 constexpr int QS_LDS = 272;
+constexpr int MV_WAVES = 8;   // waves per GEMV workgroup (512 threads)
 
-template <int NT>
-JAMHIP_DEV void f1_to_lds(const float* __restrict__ a, int lda, int k, int Gk, int8_t* lq, float* ld, float* las,
-                          int* ls16) {
+// The prologue runs in two steps so that its activation loads go out before the weight stream: a_load
+// issues HP unconditional half-block loads per thread (indices clamped; halves past k read as zero),
+// f1_store quantizes them and writes LDS. HP = ceil(NT·16·Gk / 512) half-blocks per thread.
+template <int HP> struct APre { float x[HP][16]; };
+
+template <int NT, int HP>
+JAMHIP_DEV void a_load(APre<HP>& pre, const float* __restrict__ a, int lda, int k, int Gk) {
+    // four 16-byte loads per half-block (the launcher checks a and lda for 16-byte alignment); a half past
+    // the token's last element (a partial last group) re-reads the token's last half, zeroed by f1_store
+    // (zeroing here would make the wave wait for these loads before issuing the weight loads)
+    const int halves = 16 * Gk, total = NT * halves, kh = k >> 4;
+#pragma unroll
+    for (int i = 0; i < HP; i++) {
+        const int h0 = threadIdx.x + 64 * MV_WAVES * i, h = h0 < total ? h0 : total - 1;
+        const int j = h / halves, hh = h - j * halves;
+        const bool in = hh < kh;   // clamp only; the zeroing happens in f1_store
+        const float4* src = reinterpret_cast<const float4*>(a + (int64_t) j * lda + 16 * (in ? hh : kh - 1));
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const float4 f = src[v];
+            pre.x[i][4 * v + 0] = f.x;
+            pre.x[i][4 * v + 1] = f.y;
+            pre.x[i][4 * v + 2] = f.z;
+            pre.x[i][4 * v + 3] = f.w;
+        }
+    }
+}
+
+template <int NT, int HP>
+JAMHIP_DEV void f1_store(const APre<HP>& pre, int k, int Gk, int8_t* lq, float* ld, float* las, int* ls16, char* dummy) {
+    // branch-free: a thread past the last half-block (its loads were clamped) quantizes anyway and writes to
+    // a dummy LDS slot; pairs stay aligned because the half-block count is even
     const int halves = 16 * Gk, total = NT * halves;
-    for (int h = threadIdx.x; h < total; h += 256) {
-        const int j = h / halves, hh = h - j * halves, e0 = 16 * hh;
-        const float* src = a + (int64_t) j * lda + e0;
+#pragma unroll
+    for (int i = 0; i < HP; i++) {
+        const int h0 = threadIdx.x + 64 * MV_WAVES * i;
+        const bool valid = h0 < total;
+        const int h = valid ? h0 : 0;
+        const int j = h / halves, hh = h - j * halves;
+        const bool in = hh < (k >> 4);
         float x[16];
 #pragma unroll
-        for (int e = 0; e < 16; e++) x[e] = e0 + e < k ? src[e] : 0.0f;
+        for (int e = 0; e < 16; e++) x[e] = in ? pre.x[i][e] : 0.0f;
         float am = 0.0f;
 #pragma unroll
         for (int e = 0; e < 16; e++) am = fmaxf(am, fabsf(x[e]));
@@ -223,59 +254,66 @@ JAMHIP_DEV void f1_to_lds(const float* __restrict__ a, int lda, int k, int Gk, i
         s = dot4((int) pk[2], 0x01010101, s);
         s = dot4((int) pk[3], 0x01010101, s);
         const int s32 = s + __shfl_xor(s, 1);
-        const int grp = hh >> 4;
-        *reinterpret_cast<uint4*>(lq + (int64_t) (j * Gk + grp) * QS_LDS + 16 * (hh & 15)) =
-            make_uint4(pk[0], pk[1], pk[2], pk[3]);
-        ls16[j * halves + hh] = s;
-        if ((hh & 1) == 0) {
-            ld[j * 8 * Gk + (hh >> 1)] = db;
-            las[j * 8 * Gk + (hh >> 1)] = (float) s32;
-        }
+        int8_t* pq = valid ? lq + (int64_t) (j * Gk + (hh >> 4)) * QS_LDS + 16 * (hh & 15) : (int8_t*) dummy;
+        int* p16 = valid ? ls16 + j * halves + hh : (int*) (dummy + 16);
+        const bool first = (hh & 1) == 0;
+        float* pd = valid && first ? ld + j * 8 * Gk + (hh >> 1) : (float*) (dummy + 20);
+        float* ps = valid && first ? las + j * 8 * Gk + (hh >> 1) : (float*) (dummy + 24);
+        *reinterpret_cast<uint4*>(pq) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+        *p16 = s;
+        *pd = db;
+        *ps = (float) s32;
     }
 }
 
 // ------------------------------------------------------------------------------------------ kernel
-// FL = 1: F1 activations, NT = n (1..7). FUSE: quantized into LDS by this workgroup; else read from A.
-// FL = 2: F2 activations from A; blockIdx.y picks NT tokens, the last group may hold fewer (ntv).
-template <int DT, int FL, int NT, int DEPTH, bool FUSE>
-__global__ void __launch_bounds__(256) mv_kernel(WeightView w, ActQ A, const float* __restrict__ a, int lda,
-                                                 int k, int m, int n, float* __restrict__ c, int ldc, int rows_per_wg) {
+// One workgroup (8 waves) computes one block of rows with straight-line code: the compiler can then count
+// every outstanding load exactly (a branch between a load and its use makes it drain the whole queue).
+// An item is a 16-group slot of a row quad; a block is QB quads x J slots = at most 8·ITEMS items, and
+// wave w takes items w·ITEMS .. w·ITEMS+ITEMS-1 (an item past the block re-reads a real group and adds
+// nothing). Order: the activation loads, then every weight load of the wave, then the F1 quantization
+// into LDS (waiting for the activations only), a barrier, the items in order, and finally each row's
+// partials — folded across its 16 lanes by the DPP butterfly and parked in LDS — summed over its slots
+// in a fixed order (deterministic, no atomics).
+// FL = 1: F1 activations, NT = n (1..7). HP > 0: quantized into LDS by this workgroup (HP half-blocks
+// per thread); HP = 0: read from A. FL = 2: F2 activations from A; blockIdx.y picks NT tokens, the last
+// group may hold fewer (ntv).
+template <int DT, int FL, int NT, int HP, int ITEMS>
+__global__ void __launch_bounds__(64 * MV_WAVES) mv_kernel(WeightView w, ActQ A, const float* __restrict__ a,
+                                                          int lda, int k, int m, int n, float* __restrict__ c,
+                                                          int ldc) {
     constexpr int NC = group_chunks(DT), SB = group_scale_bytes(DT), BPG = blocks_per_group(DT);
+    constexpr bool FUSE = HP > 0;
     const int lane = threadIdx.x & 63, rq = lane >> 4, li = lane & 15;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nb = k >> 5;                       // 32-blocks in the call
     const int Gk = (nb + 7) >> 3;                // groups in the call
     const int64_t Gs = w.G;                      // groups per row in the layout
-    const int J = (Gk + 15) >> 4;                // group slots per lane and row
-    const int64_t r_begin = (int64_t) blockIdx.x * rows_per_wg;
-    const int64_t r_end = r_begin + rows_per_wg < m ? r_begin + rows_per_wg : m;
-    const int64_t quads = (r_end - r_begin + 3) / 4;
-    const int64_t my_quads = quads - wave > 0 ? (quads - wave + 3) / 4 : 0;
-    const int64_t items = my_quads * J;
+    const int J = (Gk + 15) >> 4;                // 16-group slots per row
+    const int QB = MV_WAVES * ITEMS / J;         // quads per block (the launcher keeps J <= 8·ITEMS)
+    const int64_t q0 = (int64_t) blockIdx.x * QB;
     const int t0 = blockIdx.y * NT;
     const int ntv = n - t0 < NT ? n - t0 : NT;
 
-    // the item DEPTH ahead of the one being computed: quad index qd_ld, slot j_ld. Loads are unconditional
-    // (past the wave's last item they repeat it; a lane past the row's last group re-reads that group,
-    // a lane past the range's last row re-reads that row; those partials are discarded).
-    Group<DT> buf[DEPTH];
-    int64_t qd_ld = 0;
-    int j_ld = 0;
-    auto issue = [&](Group<DT>& dst) {
-        const int64_t qd = qd_ld < my_quads ? qd_ld : (my_quads > 0 ? my_quads - 1 : 0);
-        int64_t row = r_begin + 4 * (wave + 4 * qd) + rq;
-        row = row < r_end ? row : r_end - 1;
-        const int g = 16 * j_ld + li < Gk ? 16 * j_ld + li : Gk - 1;
-        load_group<DT>(dst, w.qs + row * (NC * 16 * Gs), w.sc + row * (SB * Gs), Gs, g);
-        if (++j_ld == J) {
-            j_ld = 0;
-            qd_ld++;
-        }
-    };
-#pragma unroll
-    for (int d = 0; d < DEPTH; d++) issue(buf[d]);
+    APre<FUSE ? HP : 1> pre;
+    if constexpr (FUSE) a_load<NT, HP>(pre, a, lda, k, Gk);   // first in the load queue
+    __builtin_amdgcn_sched_barrier(0);                        // ... and kept there by the scheduler
 
-    // activation views: group stride QS bytes of codes, per-token strides
+    // item i of this wave: quad q0 + it / J, slot it % J with it = wave·ITEMS + i (clamped into the tensor)
+    Group<DT> buf[ITEMS];
+#pragma unroll
+    for (int i = 0; i < ITEMS; i++) {
+        const int it = wave * ITEMS + i;
+        int64_t row = 4 * (q0 + it / J) + rq;
+        row = row < m ? row : m - 1;
+        int g = 16 * (it % J) + li;
+        g = g < Gk ? g : Gk - 1;
+        load_group<DT>(buf[i], w.qs + row * (NC * 16 * Gs), w.sc + row * (SB * Gs), Gs, g);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    extern __shared__ __align__(16) unsigned char smem[];
+    float* part = reinterpret_cast<float*>(smem);   // [8·ITEMS][4][NT] item partials
     const int8_t* aq = A.q;
     const float* ad = A.d;
     const float* as = A.s;
@@ -283,13 +321,12 @@ __global__ void __launch_bounds__(256) mv_kernel(WeightView w, ActQ A, const flo
     int64_t tq = k, td = nb, ts = FL == 1 ? nb : 2 * nb, t16 = 2 * nb;
     int QS = 256;
     if constexpr (FUSE) {
-        extern __shared__ __align__(16) unsigned char smem[];
-        int8_t* lq = reinterpret_cast<int8_t*>(smem);
-        float* ld = reinterpret_cast<float*>(smem + NT * Gk * QS_LDS);
+        char* dummy = reinterpret_cast<char*>(smem + MV_WAVES * ITEMS * 4 * NT * 4);   // 32 bytes
+        int8_t* lq = reinterpret_cast<int8_t*>(dummy + 32);
+        float* ld = reinterpret_cast<float*>(lq + NT * Gk * QS_LDS);
         float* las = ld + NT * 8 * Gk;
         int* ls16 = reinterpret_cast<int*>(las + NT * 8 * Gk);
-        f1_to_lds<NT>(a, lda, k, Gk, lq, ld, las, ls16);
-        __syncthreads();
+        f1_store<NT, HP>(pre, k, Gk, lq, ld, las, ls16, dummy);
         aq = lq;
         ad = ld;
         as = las;
@@ -298,45 +335,35 @@ __global__ void __launch_bounds__(256) mv_kernel(WeightView w, ActQ A, const flo
         td = ts = 8 * Gk;
         t16 = 16 * Gk;
         QS = QS_LDS;
+        __syncthreads();
     }
 
-    float acc[NT];
 #pragma unroll
-    for (int t = 0; t < NT; t++) acc[t] = 0.0f;
-    int64_t qd_cu = 0;
-    int j_cu = 0;
-    for (int64_t it = 0; it < items; it += DEPTH) {
-#pragma unroll
-        for (int d = 0; d < DEPTH; d++) {
-            if (it + d < items) {   // wave-uniform
-                const int g = 16 * j_cu + li;
-                const bool live = g < Gk;
-                const int gg = live ? g : Gk - 1;
-                const int nbv = nb - BPG * gg < BPG ? nb - BPG * gg : BPG;
-#pragma unroll
-                for (int t = 0; t < NT; t++) {
-                    if (FL == 2 && t >= ntv) break;
-                    const int tt = FUSE ? t : t0 + t;
-                    const float part = group_dot<DT, FL>(
-                        buf[d], aq + tt * tq + (int64_t) gg * QS, ad + tt * td + 8 * gg,
-                        as + tt * ts + (FL == 1 ? 8 : 16) * gg, s16 + tt * t16 + 16 * gg, nbv);
-                    acc[t] += live ? part : 0.0f;
-                }
-                if (++j_cu == J) {
-                    const int64_t row = r_begin + 4 * (wave + 4 * qd_cu) + rq;
-#pragma unroll
-                    for (int t = 0; t < NT; t++) {
-                        if (FL == 2 && t >= ntv) break;
-                        const float v = row16_sum(acc[t]);
-                        if (li == t && row < r_end) c[(int64_t) (t0 + t) * ldc + row] = v;
-                        acc[t] = 0.0f;
-                    }
-                    j_cu = 0;
-                    qd_cu++;
-                }
-            }
-            issue(buf[d]);
+    for (int i = 0; i < ITEMS; i++) {
+        const int it = wave * ITEMS + i;
+        const int g = 16 * (it % J) + li;
+        const bool live = g < Gk && it < QB * J && 4 * (q0 + it / J) + rq < m;
+        const int gg = g < Gk ? g : Gk - 1;
+        const int nbv = nb - BPG * gg < BPG ? nb - BPG * gg : BPG;
+        constexpr int TU = NT > 2 ? 1 : NT;   // keep several tokens' temporaries out of the register file
+#pragma unroll TU
+        for (int t = 0; t < NT; t++) {
+            if (FL == 2 && t >= ntv) break;
+            const int tt = FUSE ? t : t0 + t;
+            float p = group_dot<DT, FL>(buf[i], aq + tt * tq + (int64_t) gg * QS, ad + tt * td + 8 * gg,
+                                        as + tt * ts + (FL == 1 ? 8 : 16) * gg, s16 + tt * t16 + 16 * gg, nbv);
+            p = row16_sum(live ? p : 0.0f);
+            if (li == t) part[(it * 4 + rq) * NT + t] = p;
         }
+    }
+    __syncthreads();
+    const int tid = threadIdx.x;
+    if (tid < QB * 4 * NT) {   // (quad, row, token) of the block: sum its J slots in order
+        const int q = tid / (4 * NT), r = (tid / NT) & 3, t = tid % NT;
+        float v = 0.0f;
+        for (int j = 0; j < J; j++) v += part[((q * J + j) * 4 + r) * NT + t];
+        const int64_t row = 4 * (q0 + q) + r;
+        if (row < m && (FL == 1 || t < ntv)) c[(int64_t) (t0 + t) * ldc + row] = v;
     }
 }
 
@@ -407,64 +434,80 @@ __global__ void __launch_bounds__(64) rows_float_kernel(WeightView w, const floa
 }
 
 // ---------------------------------------------------------------------------------------- launchers
-// Fused F1 quantization keeps A's codes, scales and sums in LDS: 400 bytes per token and group.
+// Fused F1 quantization keeps A's codes, scales and sums in LDS: 400 bytes per token and group; its
+// prologue holds up to 4 half-blocks of A per thread in registers.
 constexpr int kFuseMaxBytes = 96 * 1024;
 static size_t fuse_lds(int n, int k) { return (size_t) n * ((k / 32 + 7) / 8) * (QS_LDS + 32 + 32 + 64); }
+static int fuse_hp(int n, int k) { return (n * 16 * ((k / 32 + 7) / 8) + 64 * MV_WAVES - 1) / (64 * MV_WAVES); }
 
-// Workgroups per launch. Each takes a contiguous range of rows; the fused variant pays its F1 prologue
-// once per workgroup, so it runs fewer, longer-lived ones. JAM_HIP_MV_WGS overrides (tuning sweeps).
-static int mv_wgs(int64_t m, bool fused) {
-    const char* v = getenv("JAM_HIP_MV_WGS");
-    const int over = v ? atoi(v) : 0;
-    const int64_t want = over > 0 ? over : (fused ? 512 : 1024);
-    const int64_t most = (m + 3) / 4;   // at least one row quad per workgroup
-    return (int) (want < most ? want : most);
+// Items per wave: enough that one launch's blocks fill the GPU about once, at least ceil(J / 8) so a row
+// quad fits in one block, at most 4 (register budget). JAM_HIP_MV_ITEMS overrides (tuning sweeps).
+static int mv_items(int m, int k) {
+    const int J = ((k / 32 + 7) / 8 + 15) / 16;
+    const int64_t items = (((int64_t) m + 3) / 4) * J;
+    const char* v = getenv("JAM_HIP_MV_ITEMS");
+    int it = v ? atoi(v) : (int) ((items + 256 * MV_WAVES - 1) / (256 * MV_WAVES));
+    const int lo = (J + MV_WAVES - 1) / MV_WAVES;
+    it = it < lo ? lo : it;
+    return it <= 1 ? 1 : it <= 2 ? 2 : 4;
 }
 
-template <int DT, int FL, int NT, int DEPTH>
+template <int DT, int FL, int NT, int HP, int ITEMS>
+static void launch_items(dim3 grid, size_t lds, const WeightView& w, const ActQ& A, const float* a, int lda, int k,
+                         int m, int n, float* c, int ldc, hipStream_t st) {
+    mv_kernel<DT, FL, NT, HP, ITEMS><<<grid, 64 * MV_WAVES, lds, st>>>(w, A, a, lda, k, m, n, c, ldc);
+}
+
+template <int DT, int FL, int NT, int HP>
+static hipError_t go_hp(int items, int k, int m, int n, const WeightView& w, const ActQ& A, const float* a, int lda,
+                        float* c, int ldc, hipStream_t st) {
+    const int J = ((k / 32 + 7) / 8 + 15) / 16;
+    if (J > MV_WAVES * items) return hipErrorInvalidValue;   // mv_items keeps this from happening
+    const int QB = MV_WAVES * items / J;
+    const int64_t quads = ((int64_t) m + 3) / 4;
+    const dim3 grid((unsigned) ((quads + QB - 1) / QB), FL == 1 ? 1 : (n + NT - 1) / NT);
+    const size_t lds = (size_t) MV_WAVES * items * 4 * NT * sizeof(float) + (HP > 0 ? 32 + fuse_lds(NT, k) : 0);
+    if (items == 1) launch_items<DT, FL, NT, HP, 1>(grid, lds, w, A, a, lda, k, m, n, c, ldc, st);
+    else if (items == 2) launch_items<DT, FL, NT, HP, 2>(grid, lds, w, A, a, lda, k, m, n, c, ldc, st);
+    else launch_items<DT, FL, NT, HP, 4>(grid, lds, w, A, a, lda, k, m, n, c, ldc, st);
+    return hipGetLastError();
+}
+
+template <int DT, int FL, int NT>
 static hipError_t go(const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m, int n, float* c,
                      int ldc, hipStream_t st) {
-    const bool fuse = FL == 1 && a != nullptr;
-    const int wgs = mv_wgs(m, fuse);
-    int rows_per_wg = (m + wgs - 1) / wgs;
-    rows_per_wg = (rows_per_wg + 3) & ~3;   // whole quads per workgroup
-    dim3 grid((m + rows_per_wg - 1) / rows_per_wg, FL == 1 ? 1 : (n + NT - 1) / NT);
+    const int items = mv_items(m, k);
     if constexpr (FL == 1) {
-        if (fuse) {
-            mv_kernel<DT, FL, NT, DEPTH, true><<<grid, 256, fuse_lds(NT, k), st>>>(w, A, a, lda, k, m, n, c, ldc,
-                                                                                   rows_per_wg);
-            return hipGetLastError();
+        if (a != nullptr) {
+            const int hp = fuse_hp(NT, k);
+            if (hp <= 1) return go_hp<DT, FL, NT, 1>(items, k, m, n, w, A, a, lda, c, ldc, st);
+            if (hp == 2) return go_hp<DT, FL, NT, 2>(items, k, m, n, w, A, a, lda, c, ldc, st);
+            return go_hp<DT, FL, NT, 4>(items, k, m, n, w, A, a, lda, c, ldc, st);
         }
     }
-    mv_kernel<DT, FL, NT, DEPTH, false><<<grid, 256, 0, st>>>(w, A, a, lda, k, m, n, c, ldc, rows_per_wg);
-    return hipGetLastError();
+    return go_hp<DT, FL, NT, 0>(items, k, m, n, w, A, a, lda, c, ldc, st);
 }
 
 template <int DT>
 static hipError_t gemv_dt(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m,
                           int n, float* c, int ldc, hipStream_t st) {
-    constexpr int D = DT == Q8_0 || DT == Q6_K ? 2 : 3;   // ring depth within the register budget
-    if (flavour == 2) return go<DT, 2, 8, 2>(w, A, nullptr, 0, k, m, n, c, ldc, st);
+    if (flavour == 2) return go<DT, 2, 8>(w, A, nullptr, 0, k, m, n, c, ldc, st);
     switch (n) {
-    case 1: {
-        const char* v = getenv("JAM_HIP_MV_DEPTH");   // items in flight per wave (tuning sweeps)
-        const int depth = v ? atoi(v) : D;
-        if (depth == 1) return go<DT, 1, 1, 1>(w, A, a, lda, k, m, n, c, ldc, st);
-        if (depth == 2) return go<DT, 1, 1, 2>(w, A, a, lda, k, m, n, c, ldc, st);
-        if (depth == 4) return go<DT, 1, 1, 4>(w, A, a, lda, k, m, n, c, ldc, st);
-        return go<DT, 1, 1, 3>(w, A, a, lda, k, m, n, c, ldc, st);
-    }
-    case 2: return go<DT, 1, 2, D>(w, A, a, lda, k, m, n, c, ldc, st);
-    case 3: return go<DT, 1, 3, 2>(w, A, a, lda, k, m, n, c, ldc, st);
-    case 4: return go<DT, 1, 4, 2>(w, A, a, lda, k, m, n, c, ldc, st);
-    case 5: return go<DT, 1, 5, 2>(w, A, a, lda, k, m, n, c, ldc, st);
-    case 6: return go<DT, 1, 6, 2>(w, A, a, lda, k, m, n, c, ldc, st);
-    case 7: return go<DT, 1, 7, 2>(w, A, a, lda, k, m, n, c, ldc, st);
+    case 1: return go<DT, 1, 1>(w, A, a, lda, k, m, n, c, ldc, st);
+    case 2: return go<DT, 1, 2>(w, A, a, lda, k, m, n, c, ldc, st);
+    case 3: return go<DT, 1, 3>(w, A, a, lda, k, m, n, c, ldc, st);
+    case 4: return go<DT, 1, 4>(w, A, a, lda, k, m, n, c, ldc, st);
+    case 5: return go<DT, 1, 5>(w, A, a, lda, k, m, n, c, ldc, st);
+    case 6: return go<DT, 1, 6>(w, A, a, lda, k, m, n, c, ldc, st);
+    case 7: return go<DT, 1, 7>(w, A, a, lda, k, m, n, c, ldc, st);
     default: return hipErrorInvalidValue;
     }
 }
 
-bool gemv_fusable(int n, int k) { return n < 8 && fuse_lds(n, k) <= (size_t) kFuseMaxBytes; }
+bool gemv_fusable(int n, int k, const float* a, int lda) {
+    return n < 8 && fuse_lds(n, k) <= (size_t) kFuseMaxBytes && fuse_hp(n, k) <= 4 &&
+           (reinterpret_cast<uintptr_t>(a) & 15) == 0 && (lda & 3) == 0;
+}
 
 hipError_t launch_gemv(int dt, int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m,
                        int n, float* c, int ldc, hipStream_t st) {

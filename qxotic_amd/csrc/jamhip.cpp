@@ -160,7 +160,7 @@ jamhip_status resolve_w(jamhip_ctx* ctx, const void* w, int dt, int ldw, int m, 
 jamhip_status compute(jamhip_ctx* ctx, int dt, const WeightView& wv, const float* a, int lda, float* c, int ldc,
                       int m, int n, int k) {
     hipError_t e;
-    if (gemv_fusable(n, k)) {
+    if (gemv_fusable(n, k, a, lda)) {
         if ((e = launch_gemv(dt, 1, wv, ActQ{}, a, lda, k, m, n, c, ldc, ctx->stream)) != hipSuccess)
             return hip_fail(ctx, e, "gemv launch");
         return JAMHIP_OK;

@@ -21,7 +21,7 @@ hipError_t launch_repack(int dt, const uint8_t* raw, int64_t raw_stride, int64_t
 // flavour 1: n in [1, 7], F1 activations; with `a` non-null the kernel quantizes A itself (requires
 // gemv_fusable(n, k)), else it reads A's quantized copy from `A`. flavour 2: any n >= 1, F2
 // activations from `A`, 8 tokens per grid row.
-bool gemv_fusable(int n, int k);
+bool gemv_fusable(int n, int k, const float* a, int lda);   // a, lda: the f32 activations (16-byte aligned rows)
 hipError_t launch_gemv(int dt, int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m,
                        int n, float* c, int ldc, hipStream_t st);
 
