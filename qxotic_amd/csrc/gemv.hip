@@ -440,13 +440,14 @@ constexpr int kFuseMaxBytes = 96 * 1024;
 static size_t fuse_lds(int n, int k) { return (size_t) n * ((k / 32 + 7) / 8) * (QS_LDS + 32 + 32 + 64); }
 static int fuse_hp(int n, int k) { return (n * 16 * ((k / 32 + 7) / 8) + 64 * MV_WAVES - 1) / (64 * MV_WAVES); }
 
-// Items per wave: enough that one launch's blocks fill the GPU about once, at least ceil(J / 8) so a row
-// quad fits in one block, at most 4 (register budget). JAM_HIP_MV_ITEMS overrides (tuning sweeps).
+// Items per wave: the fewest that fit a row quad in one block, ceil(J / 8). More items per wave only add
+// registers (2 already spills for several types, 4 for all) and measured slower at every shape; 4 serves
+// k above 32768 (J > 16). JAM_HIP_MV_ITEMS overrides (tuning sweeps).
 static int mv_items(int m, int k) {
+    (void) m;
     const int J = ((k / 32 + 7) / 8 + 15) / 16;
-    const int64_t items = (((int64_t) m + 3) / 4) * J;
     const char* v = getenv("JAM_HIP_MV_ITEMS");
-    int it = v ? atoi(v) : (int) ((items + 256 * MV_WAVES - 1) / (256 * MV_WAVES));
+    int it = v ? atoi(v) : 1;
     const int lo = (J + MV_WAVES - 1) / MV_WAVES;
     it = it < lo ? lo : it;
     return it <= 1 ? 1 : it <= 2 ? 2 : 4;
