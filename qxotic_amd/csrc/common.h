@@ -18,7 +18,7 @@ __host__ __device__ constexpr int block_bytes(int dt) {
          : dt == Q6_K ? 210 : dt == F32 ? 4 : 2;
 }
 
-// Device layout of a pinned weight tensor ("chunk-major groups"). A row of k elements is cut into groups
+// Device layout of a pinned weight tensor ("row-tiled groups"). A row of k elements is cut into groups
 // of 256 elements (one super-block, or 8 blocks of 32; a row whose block count is not a multiple of 8
 // ends in a zero-padded group). A group's packed quants are NC 16-byte chunks and its scales SB bytes:
 //   Q4_K : NC 8  chunk c = nibble bytes 16c..16c+15            | SB 16: d, dmin fp16, 12 scale bytes
@@ -26,9 +26,13 @@ __host__ __device__ constexpr int block_bytes(int dt) {
 //   Q8_0 : NC 16 chunk c = half c&1 of block c>>1 (int8 q)     | SB 16: the 8 blocks' fp16 d
 //   Q4_0 : NC 8  chunk c = block c's 16 nibble bytes           | SB 16: the 8 blocks' fp16 d
 //   MXFP4: NC 8  chunk c = block c's 16 nibble bytes           | SB 8 : the 8 blocks' e8m0
-// Plane 0 ("qs") holds, per row, chunk c of group g at byte (c·G + g)·16 (G = groups per row), so the
-// lanes of a wave that own consecutive groups of a row read chunk c from contiguous memory; plane 1
-// ("sc") holds, per row, group g's scales at byte g·SB. Every GGUF byte is kept; only the order changes.
+// Rows are taken in tiles of 32 (the row count is padded up to a multiple of 32 with zero rows). Plane 0
+// ("qs") holds chunk c of group g of row r at byte ((T·G + g)·NC + c)·512 + (r mod 32)·16 with T = r / 32
+// and G = groups per row: for a fixed (tile, group, chunk) the 32 rows' chunks are 512 contiguous bytes,
+// which is both the A-operand fragment of a 32-row matrix-core tile and, for 4..32 consecutive rows, a
+// fully used 64..512-byte segment for the decode kernels. Plane 1 ("sc") holds group g's scales of row r
+// at byte ((T·G + g)·32 + r mod 32)·SB. Every GGUF byte is kept; only the order changes.
+constexpr int ROW_TILE = 32;   // the shifts below assume 32
 __host__ __device__ constexpr int group_chunks(int dt) {
     return dt == Q4_K ? 8 : dt == Q6_K ? 13 : dt == Q8_0 ? 16 : dt == Q4_0 ? 8 : dt == MXFP4 ? 8 : 0;
 }
@@ -40,12 +44,26 @@ __host__ __device__ constexpr int blocks_per_group(int dt) { return 256 / block_
 __host__ __device__ constexpr int64_t groups_of(int dt, int64_t blocks) {
     return (blocks + blocks_per_group(dt) - 1) / blocks_per_group(dt);
 }
+// rows held by a device copy of m rows (whole 32-row tiles)
+__host__ __device__ constexpr int64_t tiled_rows(int64_t m) { return (m + ROW_TILE - 1) / ROW_TILE * ROW_TILE; }
 
 struct WeightView {
-    const uint8_t* qs;   // plane 0 at row 0 of the view
-    const uint8_t* sc;   // plane 1 at row 0 of the view
-    int64_t G;           // groups per row of the device layout (the row stride, in groups)
+    const uint8_t* qs;   // plane 0 of the device copy
+    const uint8_t* sc;   // plane 1 of the device copy
+    int64_t G;           // groups per row of the device layout
+    int64_t r0;          // device-copy row of the view's row 0
 };
+
+// Plane-0 address of chunk 0 of group g of view row `row` (chunk c at +c·512), and its plane-1 address.
+template <int DT> __host__ __device__ inline const uint8_t* group_q(const WeightView& w, int64_t row, int64_t g) {
+    const int64_t r = w.r0 + row;
+    return w.qs + ((r >> 5) * w.G + g) * (group_chunks(DT) * 16 * ROW_TILE) + (r & 31) * 16;   // r >= 0
+}
+template <int DT> __host__ __device__ inline const uint8_t* group_s(const WeightView& w, int64_t row, int64_t g) {
+    const int64_t r = w.r0 + row;
+    return w.sc + ((r >> 5) * w.G + g) * (group_scale_bytes(DT) * ROW_TILE) + (r & 31) * group_scale_bytes(DT);
+}
+constexpr int CHUNK_STRIDE = 16 * ROW_TILE;   // bytes between chunks c and c+1 of one row's group
 
 // Activation quantization outputs (per token row j of k elements, nb = k/32 blocks).
 struct ActQ {
@@ -65,15 +83,6 @@ template <int CTRL> JAMHIP_DEV float dpp(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
 }
 JAMHIP_DEV float lane_f(float v, int l) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l)); }
-
-// Sum over each row of 16 lanes, the same value in all 16 lanes, in a fixed order: a DPP butterfly
-// (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror).
-JAMHIP_DEV float row16_sum(float v) {
-    v += dpp<0xB1>(v);
-    v += dpp<0x4E>(v);
-    v += dpp<0x141>(v);
-    return v + dpp<0x140>(v);
-}
 
 // Sum over the 64 lanes of a wave, the same value in every lane, in a fixed order (reruns are bit-identical).
 // Within each row of 16 lanes a DPP butterfly (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror,

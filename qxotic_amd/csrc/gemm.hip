@@ -88,14 +88,13 @@ JAMHIP_DEV int mx_code(int nib) {   // e2m1 value x2 (jam_mxfp4.h:14-15)
 // LDS. Unit u of a row is 32 elements: Q4_K chunk u, Q6_K ql chunk u (+ its qh chunk), or block u.
 template <int DT, int BM, int BN>
 JAMHIP_DEV void stage_w(GemmSmem<DT, BM, BN>& S, const WeightView& w, int64_t m0, int m, int kc, int nblk) {
-    constexpr int NC = group_chunks(DT), SB = group_scale_bytes(DT);
     const int64_t g = kc / 256;
     for (int ui = threadIdx.x; ui < BM * 8; ui += 256) {
         const int row = ui >> 3, u = ui & 7;
         const int64_t grow = m0 + row < m ? m0 + row : m - 1;   // clamp: in bounds, never stored
-        const uint8_t* rq = w.qs + grow * (NC * 16 * w.G) + g * 16;   // chunk c at rq + c·16·G
-        const uint8_t* rs = w.sc + grow * (SB * w.G) + g * SB;
-        auto chunk = [&](int c) { return gld16(rq + (int64_t) c * 16 * w.G); };
+        const uint8_t* rq = group_q<DT>(w, grow, g);
+        const uint8_t* rs = group_s<DT>(w, grow, g);
+        auto chunk = [&](int c) { return gld16(rq + c * CHUNK_STRIDE); };
         float v[16], v2[16];
         if constexpr (DT == Q4_K) {
             const uint4 q = chunk(u);

@@ -3,12 +3,11 @@
 // 128-bit loads; int8 dots run on v_dot4_i32_i8; the per-block f32 combine follows the jam kernel named
 // at each dot below.
 //
-// Work split. A lane owns whole 256-element groups of the chunk-major device layout (common.h): 16 lanes
-// (one DPP row) share a weight row and take 16 of its groups per slot, the 4 lane rows of a wave take 4
-// consecutive rows (a "quad"). For each chunk index c the 64 lanes read 4 rows x 16 consecutive groups of
-// 16 bytes, i.e. four contiguous 256-byte runs, and one group's scales come in one more load. Eight waves
-// share a workgroup, the activation prologue and the LDS in which a row's partials from several waves are
-// combined (see mv_kernel). In the fused F1 variant the workgroup quantizes A into LDS (bit-exact F1) once
+// Work split. A lane owns whole 256-element groups of the row-tiled device layout (common.h): the 64 lanes
+// of a wave take 8 consecutive rows (a "band") x 8 groups, so for each chunk index c they read 8 groups x 8
+// rows of 16 bytes, i.e. eight full 128-byte lines, and one group's scales come in one more load. Eight
+// waves share a workgroup, the activation prologue and the LDS in which every lane's per-group partial is
+// parked and each row's partials are summed (see mv_kernel). In the fused F1 variant the workgroup quantizes A into LDS (bit-exact F1) once
 // for all of its rows; its activation loads go out first and its weight stream right behind them.
 #include "common.h"
 #include "launch.h"
@@ -24,18 +23,20 @@ template <int DT> struct Group {
 
 JAMHIP_DEV uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
 
-// Group g of a row (plane pointers of that row, Gs groups per row in the layout).
+// Group g of view row `row` (row-tiled layout of common.h: chunk c at +c·512 from chunk 0).
 template <int DT>
-JAMHIP_DEV void load_group(Group<DT>& r, const uint8_t* rq, const uint8_t* rs, int64_t Gs, int g) {
+JAMHIP_DEV void load_group(Group<DT>& r, const WeightView& w, int64_t row, int g) {
+    const uint8_t* q = group_q<DT>(w, row, g);
+    const uint8_t* s = group_s<DT>(w, row, g);
 #pragma unroll
-    for (int c = 0; c < group_chunks(DT); c++) r.q[c] = ld16(rq + ((int64_t) c * Gs + g) * 16);
+    for (int c = 0; c < group_chunks(DT); c++) r.q[c] = ld16(q + c * CHUNK_STRIDE);
     if constexpr (DT == Q6_K) {
-        r.s.x = *reinterpret_cast<const uint16_t*>(rs + 2 * (int64_t) g);
+        r.s.x = *reinterpret_cast<const uint16_t*>(s);
     } else if constexpr (DT == MXFP4) {
-        const uint2 v = *reinterpret_cast<const uint2*>(rs + 8 * (int64_t) g);
+        const uint2 v = *reinterpret_cast<const uint2*>(s);
         r.s = make_uint4(v.x, v.y, 0u, 0u);
     } else {
-        r.s = ld16(rs + 16 * (int64_t) g);
+        r.s = ld16(s);
     }
 }
 
@@ -269,28 +270,29 @@ JAMHIP_DEV void f1_store(const APre<HP>& pre, int k, int Gk, int8_t* lq, float* 
 // ------------------------------------------------------------------------------------------ kernel
 // One workgroup (8 waves) computes one block of rows with straight-line code: the compiler can then count
 // every outstanding load exactly (a branch between a load and its use makes it drain the whole queue).
-// An item is a 16-group slot of a row quad; a block is QB quads x J slots = at most 8·ITEMS items, and
-// wave w takes items w·ITEMS .. w·ITEMS+ITEMS-1 (an item past the block re-reads a real group and adds
-// nothing). Order: the activation loads, then every weight load of the wave, then the F1 quantization
-// into LDS (waiting for the activations only), a barrier, the items in order, and finally each row's
-// partials — folded across its 16 lanes by the DPP butterfly and parked in LDS — summed over its slots
-// in a fixed order (deterministic, no atomics).
+// Lanes: RB consecutive rows (lane % RB) x GS = 64 / RB group slots (lane / RB), so chunk c of an item is
+// GS runs of 16·RB contiguous bytes in the row-tiled layout. An item is a band of RB rows x GS groups; a
+// row band needs J = ceil(Gk / GS) items and a block is QB bands x J items = at most 8·ITEMS items, wave w
+// taking items w·ITEMS .. w·ITEMS+ITEMS-1 (an item past the block re-reads a real group and adds nothing).
+// Order: the activation loads, then every weight load of the wave, then the F1 quantization into LDS
+// (waiting for the activations only), a barrier, the items in order, each lane parking its per-group
+// partial in LDS, and finally each row's J·GS partials summed in a fixed order (deterministic, no
+// atomics, no cross-lane shuffles).
 // FL = 1: F1 activations, NT = n (1..7). HP > 0: quantized into LDS by this workgroup (HP half-blocks
 // per thread); HP = 0: read from A. FL = 2: F2 activations from A; blockIdx.y picks NT tokens, the last
 // group may hold fewer (ntv).
-template <int DT, int FL, int NT, int HP, int ITEMS>
+template <int DT, int FL, int NT, int HP, int RB, int ITEMS>
 __global__ void __launch_bounds__(64 * MV_WAVES) mv_kernel(WeightView w, ActQ A, const float* __restrict__ a,
                                                           int lda, int k, int m, int n, float* __restrict__ c,
                                                           int ldc) {
-    constexpr int NC = group_chunks(DT), SB = group_scale_bytes(DT), BPG = blocks_per_group(DT);
+    constexpr int BPG = blocks_per_group(DT), GS = 64 / RB;
     constexpr bool FUSE = HP > 0;
-    const int lane = threadIdx.x & 63, rq = lane >> 4, li = lane & 15;
+    const int lane = threadIdx.x & 63, rr = lane % RB, gs = lane / RB;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nb = k >> 5;                       // 32-blocks in the call
     const int Gk = (nb + 7) >> 3;                // groups in the call
-    const int64_t Gs = w.G;                      // groups per row in the layout
-    const int J = (Gk + 15) >> 4;                // 16-group slots per row
-    const int QB = MV_WAVES * ITEMS / J;         // quads per block (the launcher keeps J <= 8·ITEMS)
+    const int J = (Gk + GS - 1) / GS;            // items per row band
+    const int QB = MV_WAVES * ITEMS / J;         // bands per block (the launcher keeps J <= 8·ITEMS)
     const int64_t q0 = (int64_t) blockIdx.x * QB;
     const int t0 = blockIdx.y * NT;
     const int ntv = n - t0 < NT ? n - t0 : NT;
@@ -299,21 +301,21 @@ __global__ void __launch_bounds__(64 * MV_WAVES) mv_kernel(WeightView w, ActQ A,
     if constexpr (FUSE) a_load<NT, HP>(pre, a, lda, k, Gk);   // first in the load queue
     __builtin_amdgcn_sched_barrier(0);                        // ... and kept there by the scheduler
 
-    // item i of this wave: quad q0 + it / J, slot it % J with it = wave·ITEMS + i (clamped into the tensor)
+    // item i of this wave: band q0 + it / J, group slot it % J with it = wave·ITEMS + i (clamped)
     Group<DT> buf[ITEMS];
 #pragma unroll
     for (int i = 0; i < ITEMS; i++) {
         const int it = wave * ITEMS + i;
-        int64_t row = 4 * (q0 + it / J) + rq;
+        int64_t row = RB * (q0 + it / J) + rr;
         row = row < m ? row : m - 1;
-        int g = 16 * (it % J) + li;
+        int g = GS * (it % J) + gs;
         g = g < Gk ? g : Gk - 1;
-        load_group<DT>(buf[i], w.qs + row * (NC * 16 * Gs), w.sc + row * (SB * Gs), Gs, g);
+        load_group<DT>(buf[i], w, row, g);
     }
     __builtin_amdgcn_sched_barrier(0);
 
     extern __shared__ __align__(16) unsigned char smem[];
-    float* part = reinterpret_cast<float*>(smem);   // [8·ITEMS][4][NT] item partials
+    float* part = reinterpret_cast<float*>(smem);   // [8·ITEMS][GS][RB][NT] lane partials
     const int8_t* aq = A.q;
     const float* ad = A.d;
     const float* as = A.s;
@@ -321,7 +323,7 @@ __global__ void __launch_bounds__(64 * MV_WAVES) mv_kernel(WeightView w, ActQ A,
     int64_t tq = k, td = nb, ts = FL == 1 ? nb : 2 * nb, t16 = 2 * nb;
     int QS = 256;
     if constexpr (FUSE) {
-        char* dummy = reinterpret_cast<char*>(smem + MV_WAVES * ITEMS * 4 * NT * 4);   // 32 bytes
+        char* dummy = reinterpret_cast<char*>(smem + MV_WAVES * ITEMS * 64 * NT * 4);   // 32 bytes
         int8_t* lq = reinterpret_cast<int8_t*>(dummy + 32);
         float* ld = reinterpret_cast<float*>(lq + NT * Gk * QS_LDS);
         float* las = ld + NT * 8 * Gk;
@@ -341,28 +343,30 @@ __global__ void __launch_bounds__(64 * MV_WAVES) mv_kernel(WeightView w, ActQ A,
 #pragma unroll
     for (int i = 0; i < ITEMS; i++) {
         const int it = wave * ITEMS + i;
-        const int g = 16 * (it % J) + li;
-        const bool live = g < Gk && it < QB * J && 4 * (q0 + it / J) + rq < m;
+        const int g = GS * (it % J) + gs;
+        const bool live = g < Gk && it < QB * J && RB * (q0 + it / J) + rr < m;
         const int gg = g < Gk ? g : Gk - 1;
         const int nbv = nb - BPG * gg < BPG ? nb - BPG * gg : BPG;
+        float* pp = part + (it * 64 + lane) * NT;
         constexpr int TU = NT > 2 ? 1 : NT;   // keep several tokens' temporaries out of the register file
 #pragma unroll TU
         for (int t = 0; t < NT; t++) {
             if (FL == 2 && t >= ntv) break;
             const int tt = FUSE ? t : t0 + t;
-            float p = group_dot<DT, FL>(buf[i], aq + tt * tq + (int64_t) gg * QS, ad + tt * td + 8 * gg,
-                                        as + tt * ts + (FL == 1 ? 8 : 16) * gg, s16 + tt * t16 + 16 * gg, nbv);
-            p = row16_sum(live ? p : 0.0f);
-            if (li == t) part[(it * 4 + rq) * NT + t] = p;
+            const float p = group_dot<DT, FL>(buf[i], aq + tt * tq + (int64_t) gg * QS, ad + tt * td + 8 * gg,
+                                              as + tt * ts + (FL == 1 ? 8 : 16) * gg, s16 + tt * t16 + 16 * gg, nbv);
+            pp[t] = live ? p : 0.0f;
         }
     }
     __syncthreads();
-    const int tid = threadIdx.x;
-    if (tid < QB * 4 * NT) {   // (quad, row, token) of the block: sum its J slots in order
-        const int q = tid / (4 * NT), r = (tid / NT) & 3, t = tid % NT;
+    // (band, row, token) of the block: sum its J x GS partials in order; QB·RB·NT can exceed the 512 threads
+    for (int tid = threadIdx.x; tid < QB * RB * NT; tid += 64 * MV_WAVES) {
+        const int q = tid / (RB * NT), r = (tid / NT) % RB, t = tid % NT;
         float v = 0.0f;
-        for (int j = 0; j < J; j++) v += part[((q * J + j) * 4 + r) * NT + t];
-        const int64_t row = 4 * (q0 + q) + r;
+        for (int j = 0; j < J; j++)
+#pragma unroll
+            for (int s2 = 0; s2 < GS; s2++) v += part[(((q * J + j) * 64) + s2 * RB + r) * NT + t];
+        const int64_t row = RB * (q0 + q) + r;
         if (row < m && (FL == 1 || t < ntv)) c[(int64_t) (t0 + t) * ldc + row] = v;
     }
 }
@@ -374,12 +378,11 @@ __global__ void __launch_bounds__(64 * MV_WAVES) mv_kernel(WeightView w, ActQ A,
 // the 32-element chunks l, l+64, ...; products accumulate in f32.
 template <int DT>
 JAMHIP_DEV float deq(const WeightView& w, int64_t row, int elem) {
-    constexpr int NC = group_chunks(DT), SB = group_scale_bytes(DT);
     const int64_t g = elem >> 8;
     const int e = elem & 255;
-    const uint8_t* q = w.qs + row * (NC * 16 * w.G);
-    const uint8_t* s = w.sc + row * (SB * w.G) + g * SB;
-    auto qb = [&](int byte) { return q[((int64_t) (byte >> 4) * w.G + g) * 16 + (byte & 15)]; };   // group byte
+    const uint8_t* q = group_q<DT>(w, row, g);
+    const uint8_t* s = group_s<DT>(w, row, g);
+    auto qb = [&](int byte) { return q[(byte >> 4) * CHUNK_STRIDE + (byte & 15)]; };   // group byte
     auto f16 = [&](const uint8_t* p) { return h2f((uint32_t) p[0] | ((uint32_t) p[1] << 8)); };
     if constexpr (DT == Q8_0) {
         return f16(s + 2 * (e >> 5)) * (float) (int8_t) qb(e);
@@ -440,53 +443,57 @@ constexpr int kFuseMaxBytes = 96 * 1024;
 static size_t fuse_lds(int n, int k) { return (size_t) n * ((k / 32 + 7) / 8) * (QS_LDS + 32 + 32 + 64); }
 static int fuse_hp(int n, int k) { return (n * 16 * ((k / 32 + 7) / 8) + 64 * MV_WAVES - 1) / (64 * MV_WAVES); }
 
-// Items per wave: the fewest that fit a row quad in one block, ceil(J / 8). More items per wave only add
-// registers (2 already spills for several types, 4 for all) and measured slower at every shape; 4 serves
-// k above 32768 (J > 16). JAM_HIP_MV_ITEMS overrides (tuning sweeps).
-static int mv_items(int m, int k) {
-    (void) m;
-    const int J = ((k / 32 + 7) / 8 + 15) / 16;
-    const char* v = getenv("JAM_HIP_MV_ITEMS");
-    int it = v ? atoi(v) : 1;
+// Work split: bands of RB = 8 rows (x 8 group slots: chunk loads are 128-byte lines; 16-row bands measured
+// slower at every BASELINE shape) and the fewest items per wave that fit a band in one block, 1, 2 or 4
+// for k up to 16384, 32768, 65536. More items per wave only add registers. JAM_HIP_MV_ITEMS overrides
+// (tuning sweeps). Returns false past k = 65536.
+constexpr int MV_RB = 8;
+static bool mv_items(int k, int* items) {
+    const int Gk = (k / 32 + 7) / 8, J = (Gk + 64 / MV_RB - 1) / (64 / MV_RB);
+    const char* vi = getenv("JAM_HIP_MV_ITEMS");
+    int it = vi ? atoi(vi) : 1;
     const int lo = (J + MV_WAVES - 1) / MV_WAVES;
     it = it < lo ? lo : it;
-    return it <= 1 ? 1 : it <= 2 ? 2 : 4;
+    it = it <= 1 ? 1 : it <= 2 ? 2 : 4;
+    *items = it;
+    return J <= MV_WAVES * it;
 }
 
-template <int DT, int FL, int NT, int HP, int ITEMS>
-static void launch_items(dim3 grid, size_t lds, const WeightView& w, const ActQ& A, const float* a, int lda, int k,
-                         int m, int n, float* c, int ldc, hipStream_t st) {
-    mv_kernel<DT, FL, NT, HP, ITEMS><<<grid, 64 * MV_WAVES, lds, st>>>(w, A, a, lda, k, m, n, c, ldc);
+template <int DT, int FL, int NT, int HP, int RB, int ITEMS>
+static void launch_shape(int k, int m, int n, const WeightView& w, const ActQ& A, const float* a, int lda, float* c,
+                         int ldc, hipStream_t st) {
+    constexpr int GS = 64 / RB;
+    const int Gk = (k / 32 + 7) / 8, J = (Gk + GS - 1) / GS;
+    const int QB = MV_WAVES * ITEMS / J;
+    const int64_t bands = ((int64_t) m + RB - 1) / RB;
+    const dim3 grid((unsigned) ((bands + QB - 1) / QB), FL == 1 ? 1 : (n + NT - 1) / NT);
+    const size_t lds = (size_t) MV_WAVES * ITEMS * 64 * NT * sizeof(float) + (HP > 0 ? 32 + fuse_lds(NT, k) : 0);
+    mv_kernel<DT, FL, NT, HP, RB, ITEMS><<<grid, 64 * MV_WAVES, lds, st>>>(w, A, a, lda, k, m, n, c, ldc);
 }
 
 template <int DT, int FL, int NT, int HP>
-static hipError_t go_hp(int items, int k, int m, int n, const WeightView& w, const ActQ& A, const float* a, int lda,
-                        float* c, int ldc, hipStream_t st) {
-    const int J = ((k / 32 + 7) / 8 + 15) / 16;
-    if (J > MV_WAVES * items) return hipErrorInvalidValue;   // mv_items keeps this from happening
-    const int QB = MV_WAVES * items / J;
-    const int64_t quads = ((int64_t) m + 3) / 4;
-    const dim3 grid((unsigned) ((quads + QB - 1) / QB), FL == 1 ? 1 : (n + NT - 1) / NT);
-    const size_t lds = (size_t) MV_WAVES * items * 4 * NT * sizeof(float) + (HP > 0 ? 32 + fuse_lds(NT, k) : 0);
-    if (items == 1) launch_items<DT, FL, NT, HP, 1>(grid, lds, w, A, a, lda, k, m, n, c, ldc, st);
-    else if (items == 2) launch_items<DT, FL, NT, HP, 2>(grid, lds, w, A, a, lda, k, m, n, c, ldc, st);
-    else launch_items<DT, FL, NT, HP, 4>(grid, lds, w, A, a, lda, k, m, n, c, ldc, st);
+static hipError_t go_hp(int k, int m, int n, const WeightView& w, const ActQ& A, const float* a, int lda, float* c,
+                        int ldc, hipStream_t st) {
+    int items;
+    if (!mv_items(k, &items)) return hipErrorNotSupported;
+    if (items == 1) launch_shape<DT, FL, NT, HP, MV_RB, 1>(k, m, n, w, A, a, lda, c, ldc, st);
+    else if (items == 2) launch_shape<DT, FL, NT, HP, MV_RB, 2>(k, m, n, w, A, a, lda, c, ldc, st);
+    else launch_shape<DT, FL, NT, HP, MV_RB, 4>(k, m, n, w, A, a, lda, c, ldc, st);
     return hipGetLastError();
 }
 
 template <int DT, int FL, int NT>
 static hipError_t go(const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m, int n, float* c,
                      int ldc, hipStream_t st) {
-    const int items = mv_items(m, k);
     if constexpr (FL == 1) {
         if (a != nullptr) {
             const int hp = fuse_hp(NT, k);
-            if (hp <= 1) return go_hp<DT, FL, NT, 1>(items, k, m, n, w, A, a, lda, c, ldc, st);
-            if (hp == 2) return go_hp<DT, FL, NT, 2>(items, k, m, n, w, A, a, lda, c, ldc, st);
-            return go_hp<DT, FL, NT, 4>(items, k, m, n, w, A, a, lda, c, ldc, st);
+            if (hp <= 1) return go_hp<DT, FL, NT, 1>(k, m, n, w, A, a, lda, c, ldc, st);
+            if (hp == 2) return go_hp<DT, FL, NT, 2>(k, m, n, w, A, a, lda, c, ldc, st);
+            return go_hp<DT, FL, NT, 4>(k, m, n, w, A, a, lda, c, ldc, st);
         }
     }
-    return go_hp<DT, FL, NT, 0>(items, k, m, n, w, A, a, lda, c, ldc, st);
+    return go_hp<DT, FL, NT, 0>(k, m, n, w, A, a, lda, c, ldc, st);
 }
 
 template <int DT>

@@ -77,7 +77,10 @@ jamhip_status fail(jamhip_ctx* ctx, jamhip_status st, const std::string& msg) {
 }
 
 jamhip_status hip_fail(jamhip_ctx* ctx, hipError_t e, const char* what) {
-    return fail(ctx, JAMHIP_EINVAL, std::string(what) + ": " + hipGetErrorString(e));
+    // a shape no kernel here covers (hipErrorNotSupported from a launcher) is jam's EUNSUPPORTED: the
+    // caller falls through to the next backend
+    return fail(ctx, e == hipErrorNotSupported ? JAMHIP_EUNSUPPORTED : JAMHIP_EINVAL,
+                std::string(what) + ": " + hipGetErrorString(e));
 }
 
 struct Busy {   // the serial-stream guard of jam_mm (jam/jam-native/src/jam.c:777-783)
@@ -115,9 +118,10 @@ bool lookup(jamhip_ctx* ctx, const void* w, int dt, int ldw, int m, WeightView* 
         if (off % rbytes) continue;
         const int64_t r0 = off / rbytes;
         if (r0 + m > pin.rows) continue;
-        out->qs = pin.dev + r0 * pin.G * group_chunks(dt) * 16;
-        out->sc = pin.sc + r0 * pin.G * group_scale_bytes(dt);
+        out->qs = pin.dev;
+        out->sc = pin.sc;
         out->G = pin.G;
+        out->r0 = r0;
         return true;
     }
     return false;
@@ -142,7 +146,7 @@ jamhip_status upload(jamhip_ctx* ctx, const uint8_t* host, int dt, int64_t raw_s
 jamhip_status resolve_w(jamhip_ctx* ctx, const void* w, int dt, int ldw, int m, int k, WeightView* wv) {
     if (lookup(ctx, w, dt, ldw, m, wv)) return JAMHIP_OK;
     const int64_t rb = k / block_elems(dt), G = groups_of(dt, rb);
-    const int64_t qsz = align256((int64_t) m * G * group_chunks(dt) * 16), ssz = (int64_t) m * G * group_scale_bytes(dt);
+    const int64_t qsz = align256(tiled_rows(m) * G * group_chunks(dt) * 16), ssz = tiled_rows(m) * G * group_scale_bytes(dt);
     hipError_t e = ctx->w_stage.ensure((size_t) (qsz + ssz));
     if (e != hipSuccess) return hip_fail(ctx, e, "weight stage alloc");
     uint8_t* dst = (uint8_t*) ctx->w_stage.p;
@@ -152,6 +156,7 @@ jamhip_status resolve_w(jamhip_ctx* ctx, const void* w, int dt, int ldw, int m, 
     wv->qs = dst;
     wv->sc = dsc;
     wv->G = G;
+    wv->r0 = 0;
     return JAMHIP_OK;
 }
 
@@ -321,7 +326,7 @@ jamhip_status jamhip_weight_pin(jamhip_ctx* ctx, const void* w, int wt, int ldw,
                 return fail(ctx, JAMHIP_EINVAL, "pin: range overlaps a pinned tensor (evict it first)");
         }
     }
-    const int64_t qsz = align256((int64_t) m * G * group_chunks(wt) * 16), ssz = (int64_t) m * G * group_scale_bytes(wt);
+    const int64_t qsz = align256(tiled_rows(m) * G * group_chunks(wt) * 16), ssz = tiled_rows(m) * G * group_scale_bytes(wt);
     uint8_t* dev = nullptr;
     hipError_t e = hipMalloc((void**) &dev, (size_t) (qsz + ssz));
     if (e != hipSuccess) return hip_fail(ctx, e, "pin: device alloc");

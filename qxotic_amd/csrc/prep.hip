@@ -38,37 +38,39 @@ __global__ void __launch_bounds__(256) quant_f2_kernel(const float* __restrict__
     if ((e & 31) == 0) d[(int64_t) j * (k >> 5) + (e >> 5)] = db;
 }
 
-// Weight repack: raw GGUF rows (stride raw_stride bytes, rb blocks) -> the chunk-major group layout of
-// common.h. One thread per (row, group); a group past the row's last block is zero-filled. Runs once per
-// pinned tensor.
+// Weight repack: raw GGUF rows (stride raw_stride bytes, rb blocks) -> the row-tiled group layout of
+// common.h. One thread per (tile, group, row of the tile), consecutive threads on consecutive rows so each
+// chunk store of 32 threads fills 512 contiguous bytes; a group past the row's last block, and every row
+// past `rows` in the last tile, is zero-filled. Runs once per pinned tensor.
 template <int DT>
 __global__ void __launch_bounds__(256) repack_kernel(const uint8_t* __restrict__ raw, int64_t raw_stride,
                                                      int64_t rows, int64_t rb, int64_t G, uint8_t* __restrict__ qs,
                                                      uint8_t* __restrict__ sc) {
     constexpr int NC = group_chunks(DT), SB = group_scale_bytes(DT), BPG = blocks_per_group(DT);
     const int64_t i = (int64_t) blockIdx.x * 256 + threadIdx.x;
-    if (i >= rows * G) return;
-    const int64_t r = i / G, g = i - r * G;
-    const uint8_t* row = raw + r * raw_stride;
-    uint8_t* dq = qs + r * (NC * 16 * G) + g * 16;   // chunk c at dq + c·16·G
-    uint8_t* ds = sc + r * (SB * G) + g * SB;
-    auto chunk = [&](int c) { return dq + (int64_t) c * 16 * G; };
+    if (i >= tiled_rows(rows) * G) return;
+    const int64_t rr = i & 31, tg = i >> 5, T = tg / G, g = tg - T * G, r = 32 * T + rr;
+    const bool live = r < rows;
+    const uint8_t* row = raw + (live ? r : 0) * raw_stride;
+    uint8_t* dq = qs + (T * G + g) * (NC * CHUNK_STRIDE) + rr * 16;   // chunk c at dq + c·512
+    uint8_t* ds = sc + (T * G + g) * (SB * ROW_TILE) + rr * SB;
+    auto chunk = [&](int c) { return dq + (int64_t) c * CHUNK_STRIDE; };
     if constexpr (DT == Q4_K) {                        // d, dmin, scales @0..15, nibbles @16..143
         const uint8_t* b = row + g * 144;
-        for (int t = 0; t < 16; t++) ds[t] = b[t];
+        for (int t = 0; t < 16; t++) ds[t] = live ? b[t] : 0;
         for (int c = 0; c < 8; c++)
-            for (int t = 0; t < 16; t++) chunk(c)[t] = b[16 + 16 * c + t];
+            for (int t = 0; t < 16; t++) chunk(c)[t] = live ? b[16 + 16 * c + t] : 0;
     } else if constexpr (DT == Q6_K) {                 // ql @0..127, qh @128..191, scales @192..207, d @208
         const uint8_t* b = row + g * 210;
         for (int c = 0; c < 13; c++)
-            for (int t = 0; t < 16; t++) chunk(c)[t] = b[16 * c + t];
-        ds[0] = b[208];
-        ds[1] = b[209];
+            for (int t = 0; t < 16; t++) chunk(c)[t] = live ? b[16 * c + t] : 0;
+        ds[0] = live ? b[208] : 0;
+        ds[1] = live ? b[209] : 0;
     } else {
         for (int j = 0; j < BPG; j++) {
             const int64_t blk = g * BPG + j;
-            uint8_t q[32] = {0}, s[2] = {0, 0};   // a block past the row end stays zero (never read)
-            if (blk < rb) {
+            uint8_t q[32] = {0}, s[2] = {0, 0};   // a block past the row end, or a padding row, stays zero
+            if (live && blk < rb) {
                 const uint8_t* b = row + blk * block_bytes(DT);
                 const int sbytes = DT == MXFP4 ? 1 : 2, qbytes = DT == Q8_0 ? 32 : 16;
                 for (int t = 0; t < sbytes; t++) s[t] = b[t];
@@ -109,7 +111,7 @@ hipError_t launch_quant_f2(const float* a, int lda, int n, int k, int8_t* q, flo
 
 hipError_t launch_repack(int dt, const uint8_t* raw, int64_t raw_stride, int64_t rows, int64_t rb, int64_t G,
                          uint8_t* qs, uint8_t* sc, hipStream_t st) {
-    const int64_t n = rows * G;
+    const int64_t n = tiled_rows(rows) * G;
     const dim3 grid((unsigned) ((n + 255) / 256));
     switch (dt) {
     case Q8_0: repack_kernel<Q8_0><<<grid, 256, 0, st>>>(raw, raw_stride, rows, rb, G, qs, sc); break;
