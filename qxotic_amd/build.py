@@ -28,6 +28,7 @@ UNITS = {   # source -> extra flags
     "prep.hip": ["-ffp-contract=off"],
     "gemv.hip": [],
     "gemm.hip": [],
+    "mma.hip": [],
     "jamhip.cpp": ["-x", "hip"],
 }
 

@@ -66,7 +66,7 @@ struct jamhip_ctx {
     char arch[64] = {0};
     std::mutex pin_mu;
     std::vector<Pin> pins;
-    DevBuf act, a_stage, c_stage, w_raw, w_stage;
+    DevBuf act, gact, a_stage, c_stage, w_raw, w_stage;
 };
 
 namespace {
@@ -160,6 +160,17 @@ jamhip_status resolve_w(jamhip_ctx* ctx, const void* w, int dt, int ldw, int m, 
     return JAMHIP_OK;
 }
 
+bool env_true(const char* name) {
+    const char* v = getenv(name);
+    return v && (!strcmp(v, "1") || !strcasecmp(v, "true") || !strcasecmp(v, "yes"));
+}
+
+// The matrix-core GEMM covers the K-quants on 32-row-aligned views (launch_gemm_mma).
+bool mma_path(int dt, int k, const WeightView& wv) {
+    if (env_true("JAM_HIP_NO_MMA")) return false;
+    return (dt == Q4_K || dt == Q6_K) && k % 256 == 0 && (wv.r0 & 31) == 0;
+}
+
 // Quantize A (device, f32 [n][lda]) and run the matmul into C (device, [n][ldc]). Decode-sized calls
 // are one fused launch and touch no scratch (safe under stream capture once W is pinned).
 jamhip_status compute(jamhip_ctx* ctx, int dt, const WeightView& wv, const float* a, int lda, float* c, int ldc,
@@ -168,6 +179,21 @@ jamhip_status compute(jamhip_ctx* ctx, int dt, const WeightView& wv, const float
     if (gemv_fusable(n, k, a, lda)) {
         if ((e = launch_gemv(dt, 1, wv, ActQ{}, a, lda, k, m, n, c, ldc, ctx->stream)) != hipSuccess)
             return hip_fail(ctx, e, "gemv launch");
+        return JAMHIP_OK;
+    }
+    // n >= 8: jam's 16-row F2 bands on rows [0, m16); the last m % 16 rows take the band's float-dot tail
+    // (jam_kernels_q4k_avx512.c:185-188).
+    const int m16 = m - m % 16;
+    if (n >= 32 && m16 > 0 && mma_path(dt, k, wv)) {
+        GemmAct G;
+        if ((e = ctx->gact.ensure(gemm_act_bytes(dt, n, k))) != hipSuccess)
+            return hip_fail(ctx, e, "gemm activation scratch alloc");
+        if ((e = launch_gemm_prep(dt, a, lda, n, k, ctx->gact.p, &G, ctx->stream)) != hipSuccess)
+            return hip_fail(ctx, e, "gemm prep launch");
+        if ((e = launch_gemm_mma(dt, wv, G, k, m16, n, c, ldc, ctx->stream)) != hipSuccess)
+            return hip_fail(ctx, e, "gemm launch");
+        if ((e = launch_rows_float(dt, wv, a, lda, k, m16, m - m16, n, c, ldc, ctx->stream)) != hipSuccess)
+            return hip_fail(ctx, e, "tail rows launch");
         return JAMHIP_OK;
     }
     const int64_t nb = k / 32;
@@ -187,9 +213,6 @@ jamhip_status compute(jamhip_ctx* ctx, int dt, const WeightView& wv, const float
             return hip_fail(ctx, e, "gemv launch");
         return JAMHIP_OK;
     }
-    // n >= 8: jam's 16-row F2 bands on rows [0, m16); the last m % 16 rows take the band's float-dot tail
-    // (jam_kernels_q4k_avx512.c:185-188).
-    const int m16 = m - m % 16;
     if (m16 > 0) {
         if ((e = launch_quant_f2(a, lda, n, k, q, d, s, ctx->stream)) != hipSuccess)
             return hip_fail(ctx, e, "quant_f2 launch");
@@ -200,11 +223,6 @@ jamhip_status compute(jamhip_ctx* ctx, int dt, const WeightView& wv, const float
     if ((e = launch_rows_float(dt, wv, a, lda, k, m16, m - m16, n, c, ldc, ctx->stream)) != hipSuccess)
         return hip_fail(ctx, e, "tail rows launch");
     return JAMHIP_OK;
-}
-
-bool env_true(const char* name) {
-    const char* v = getenv(name);
-    return v && (!strcmp(v, "1") || !strcasecmp(v, "true") || !strcasecmp(v, "yes"));
 }
 
 }  // namespace
@@ -259,6 +277,7 @@ void jamhip_ctx_destroy(jamhip_ctx* ctx) {
     for (Pin& p : ctx->pins) (void) hipFree(p.dev);
     ctx->pins.clear();
     ctx->act.release();
+    ctx->gact.release();
     ctx->a_stage.release();
     ctx->c_stage.release();
     ctx->w_raw.release();

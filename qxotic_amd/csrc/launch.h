@@ -34,4 +34,27 @@ hipError_t launch_rows_float(int dt, const WeightView& w, const float* a, int ld
 hipError_t launch_gemm(int dt, const WeightView& w, const ActQ& A, int k, int m, int n, float* c, int ldc,
                        hipStream_t st);
 
+// Activations of the matrix-core GEMM, written by launch_gemm_prep: jam's F2 quantization of n tokens
+// (bit-exact codes and scales) laid out for the MFMA operand loads. Tokens are padded to NP (a multiple
+// of 64) and k to Kp (a multiple of 256) with zeros. Token t carries a power of two 2^e_t chosen so that
+// its largest activation sum lies in [2^13, 2^14): the GEMM accumulates in units of 2^-e_t (the block
+// scales and sums below are pre-multiplied by it, exactly) and multiplies by 2^e_t on the way out.
+struct GemmAct {
+    const _Float16* b;     // [Kp/16][NP][16] activation codes; kstep k16 = 2·block + ks, slot 8q + i holds
+                           // element 32·block + 16q + 8ks + perm8(i)
+    const float* dx;       // [Kp/32][NP] block scale d · 2^-e_t
+    const _Float16* shi;   // per-32 sums (Q4_K, Q4_0) [Kp/256][NP][8] or per-16 sums (Q6_K) [Kp/256][NP][16],
+    const _Float16* slo;   //   · 2^-e_t, split as f16 high part + f16 remainder
+    const float* es;       // [NP] 2^e_t
+    int NP, Kp;
+};
+int gemm_sums_kind(int dt);   // 0 none, 1 per-32 sums, 2 per-16 sums
+size_t gemm_act_bytes(int dt, int n, int k);
+hipError_t launch_gemm_prep(int dt, const float* a, int lda, int n, int k, void* scratch, GemmAct* out,
+                            hipStream_t st);
+// Matrix-core GEMM over GemmAct (f16 MFMA on exact integer operands); hipErrorNotSupported for dtypes it
+// does not cover.
+hipError_t launch_gemm_mma(int dt, const WeightView& w, const GemmAct& A, int k, int m, int n, float* c, int ldc,
+                           hipStream_t st);
+
 }  // namespace jamhip

@@ -1,0 +1,439 @@
+// Matrix-core prefill GEMM for the K-quant weights (Q4_K, Q6_K): C[n][m] = W[m][k] · A[n][k]^T with jam's
+// F2 semantics (the n >= 8 bands of jam_kernels_q4k_avx512.c), activations from launch_gemm_prep.
+//
+// Arithmetic. Each 32-element block's integer dot runs on v_mfma_f32_32x32x16_f16 with integer operands
+// that f16 holds exactly: the activation codes (int8) and the weight codes with their integer sub-scale
+// folded in (Q4_K sc·nib <= 945; Q6_K sc·q6 / 4 in two planes, sc·(q6 & 15) / 4 and sc·(q6 & 48) / 4).
+// Every product and every 32-term sum is an exact f32 integer (a quarter-integer for Q6_K), so the MFMA
+// returns the block's exact dot; one f32 FMA per output then applies the block's activation scale, and
+// the super-block scale d is applied once per 256 elements. The super-block's other term runs on the
+// matrix cores too, with the activation sums split into an f16 high part and an f16 remainder (about 22
+// significant bits):
+//   Q4_K  −Σ_s fl(dmin·mn_s)·fl(xs0+xs1)_s   v_mfma_f32_32x32x8_f16 per super-block, −dmin·mn split the
+//                                             same way (hi·hi + hi·lo + lo·hi)   (q4k_avx512.c:76-95)
+//   Q6_K  −Σ_t fl(d·sc_t)·fl(32·xs_t)         one 32x32x16 step with A' = −8·sc_t (exact), summed into
+//                                             the super-block accumulator before d   (q4k_avx512.c:222-236)
+// The result equals jam's up to f32 summation order (the oracle tests bound it).
+//
+// Operands. With the 32-row tiles of the device layout, the A fragment of lane (r, q) (row r = lane % 32,
+// q = lane / 32) for K-step ks of a block is the low or high nibbles of bytes 8ks..8ks+7 of one 16-byte
+// chunk, turned into f16 pairs from bytes (0,2), (1,3), (4,6), (5,7) by mask-and-or with 0x6400 (1024 + v)
+// and one packed FMA with the scale (which removes the 1024). The activation codes are stored in that
+// same order (GemmAct::b), so no shuffle is needed on either side.
+//
+// Tiling. A workgroup of 4 waves owns 4·RT row tiles (32 rows each, wave w the RT tiles w·RT..) x CT token
+// tiles (32 tokens each) and walks k in stages of 128 elements (half a super-block). Each stage's weight
+// chunks, scales, activation codes, block scales and sums are copied global -> LDS by the waves
+// themselves with global_load_lds_dwordx4 (16 bytes per lane, no registers), double-buffered: stage s+1
+// is in flight while stage s is computed. Workgroups that share a row block are placed on one XCD so the
+// weight tile is read from HBM into that XCD's L2 once.
+#include "common.h"
+#include "launch.h"
+
+namespace jamhip {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void lds_void;
+
+constexpr int MMA_THREADS = 256;
+
+JAMHIP_DEV void dma16(const void* g, void* lds_base) {
+    // lane l's 16 bytes at g land at lds_base + 16·l (lds_base is wave-uniform)
+    __builtin_amdgcn_global_load_lds(g, (lds_void*) lds_base, 16, 0, 0);
+}
+
+JAMHIP_DEV uint32_t hbits(_Float16 h) { return (uint32_t) __builtin_bit_cast(uint16_t, h); }
+JAMHIP_DEV uint32_t pack2(_Float16 lo, _Float16 hi) { return hbits(lo) | (hbits(hi) << 16); }
+
+// f16 pair (1024 + v_a, 1024 + v_b) -> mul·pair + add (one v_pk_fma_f16, exact for these operands)
+JAMHIP_DEV uint32_t pkfma(uint32_t x, uint32_t mul, uint32_t add) {
+    const half2v r = __builtin_elementwise_fma(__builtin_bit_cast(half2v, x), __builtin_bit_cast(half2v, mul),
+                                               __builtin_bit_cast(half2v, add));
+    return __builtin_bit_cast(uint32_t, r);
+}
+
+// 8 f16 of one K-step from two words: nibble/bit field `mask` of bytes (0,2), (1,3) of w0 then of w1; the
+// field sits at bits 0-3 or 4-7 of each byte (sh selects which byte pair holds it after shifting).
+JAMHIP_DEV half8 frag8(uint32_t w0, uint32_t w1, uint32_t mask, uint32_t mul, uint32_t add) {
+    const uint32_t m = 0x64006400u;
+    const uint32_t p0 = pkfma((w0 & mask) | m, mul, add), p1 = pkfma(((w0 >> 8) & mask) | m, mul, add);
+    const uint32_t p2 = pkfma((w1 & mask) | m, mul, add), p3 = pkfma(((w1 >> 8) & mask) | m, mul, add);
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    return __builtin_bit_cast(half8, u32x4{p0, p1, p2, p3});
+}
+
+// Q4_K 6-bit scale and min of sub-block s (jam/jam-native/src/jam_kquant.h:26-33); h = the 16-byte header.
+JAMHIP_DEV void q4k_scmn(const uint4 h, int s, int& sc, int& mn) {
+    const uint32_t u0 = h.y, u1 = h.z, u2 = h.w;
+    const int sh = 8 * (s & 3);
+    if (s < 4) {
+        sc = (u0 >> sh) & 63;
+        mn = (u1 >> sh) & 63;
+    } else {
+        sc = ((u2 >> sh) & 15) | ((((u0 >> sh) >> 6) & 3) << 4);
+        mn = (((u2 >> sh) >> 4) & 15) | ((((u1 >> sh) >> 6) & 3) << 4);
+    }
+}
+
+JAMHIP_DEV float h2f_bits(uint32_t b) { return (float) __builtin_bit_cast(_Float16, (uint16_t) (b & 0xffffu)); }
+
+// ------------------------------------------------------------------------------------ stage layout
+// Per stage buffer (bytes): A chunks [TW][NCS][32][16], header [TW][32][HB], codes [8][BN][32],
+// block scales [4][BN] f32, sums hi/lo [BN][SW] f16 each.
+template <int DT, int RT, int CT> struct Stage {
+    static constexpr int TW = 4 * RT, BN = 32 * CT;
+    static constexpr int NCS = DT == Q4_K ? 4 : 7;           // chunks per stage (Q6_K: 4 ql, 2 qh, scales)
+    static constexpr int HB = DT == Q4_K ? 16 : 2;           // header bytes per row (Q6_K: d)
+    static constexpr int SW = DT == Q4_K ? 8 : 16;           // sums per token per super-block
+    static constexpr int A_OFF = 0;
+    static constexpr int H_OFF = A_OFF + TW * NCS * 512;
+    static constexpr int B_OFF = (H_OFF + TW * 32 * HB + 1023) / 1024 * 1024;
+    static constexpr int DX_OFF = B_OFF + 8 * BN * 32;
+    static constexpr int S_OFF = DX_OFF + 4 * BN * 4;
+    static constexpr int BYTES = S_OFF + 2 * BN * SW * 2;
+};
+
+// ------------------------------------------------------------------------------------------ kernel
+template <int DT, int RT, int CT>
+__global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, GemmAct A, int m, int n,
+                                                                 float* __restrict__ c, int ldc, int nrb, int ncb,
+                                                                 int64_t tiles) {
+    using S = Stage<DT, RT, CT>;
+    constexpr int TW = S::TW, BN = S::BN, NCS = S::NCS;
+    extern __shared__ __align__(1024) unsigned char smem[];
+
+    // XCD-aware placement: workgroup id i runs on XCD i % 8; give each XCD a contiguous run of
+    // (row block, token block) pairs so a row block's token blocks share one L2.
+    const int total = nrb * ncb, per = (total + 7) / 8;
+    const int lin = (int) (blockIdx.x % 8) * per + (int) (blockIdx.x / 8);
+    if (lin >= total) return;
+    const int rb = lin / ncb, cb = lin % ncb;
+    const int64_t T0 = (int64_t) rb * TW;        // first row tile of the workgroup
+    const int n0 = cb * BN;
+
+    const int lane = threadIdx.x & 63, r = lane & 31, q = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int G = (int) w.G, nsb = A.Kp / 256, nst = 2 * nsb;
+    const int64_t r0t = w.r0 >> 5;               // the view's first row is tile-aligned (launcher checks)
+
+    // ---- global -> LDS copy of one stage (every wave takes every 4th 1 KB piece)
+    auto issue = [&](int st, unsigned char* buf) {
+        const int g = st >> 1, h2 = st & 1;
+        int piece = 0;
+        auto mine = [&]() { return (piece++ & 3) == wave; };
+        // weight chunks: tile tt, chunk pair p: 1 KB contiguous
+        constexpr int NC = group_chunks(DT);
+        for (int tt = 0; tt < TW; tt++) {
+            int64_t T = T0 + tt;
+            T = T < tiles ? T : tiles - 1;
+            const uint8_t* gbase = w.qs + ((r0t + T) * G + g) * (NC * CHUNK_STRIDE);
+            unsigned char* lbase = buf + S::A_OFF + tt * NCS * 512;
+            if constexpr (DT == Q4_K) {
+#pragma unroll
+                for (int p = 0; p < 2; p++)
+                    if (mine()) dma16(gbase + (4 * h2 + 2 * p) * CHUNK_STRIDE + 16 * lane, lbase + 2 * p * 512);
+            } else {
+                // ql chunks 4h2..4h2+3 (2 pieces), qh chunks 8+2h2, 9+2h2 (1 piece), scales chunk 12 (half)
+#pragma unroll
+                for (int p = 0; p < 2; p++)
+                    if (mine()) dma16(gbase + (4 * h2 + 2 * p) * CHUNK_STRIDE + 16 * lane, lbase + 2 * p * 512);
+                if (mine()) dma16(gbase + (8 + 2 * h2) * CHUNK_STRIDE + 16 * lane, lbase + 4 * 512);
+                if (mine() && lane < 32) dma16(gbase + 12 * CHUNK_STRIDE + 16 * lane, lbase + 6 * 512);
+            }
+        }
+        // headers: Q4_K 16 B per row (2 tiles per piece); Q6_K d (2 B per row, 16 tiles per piece)
+        if constexpr (DT == Q4_K) {
+            for (int tp = 0; tp < TW / 2; tp++) {
+                if (!mine()) continue;
+                int64_t T = T0 + 2 * tp + q;
+                T = T < tiles ? T : tiles - 1;
+                dma16(w.sc + (((r0t + T) * G + g) * 32 + r) * 16, buf + S::H_OFF + tp * 1024);
+            }
+        } else if (h2 == 1) {
+            if (mine() && lane < 4 * TW) {
+                int64_t T = T0 + (lane >> 2);
+                T = T < tiles ? T : tiles - 1;
+                dma16(w.sc + (((r0t + T) * G + g) * 32 + 8 * (lane & 3)) * 2, buf + S::H_OFF);
+            }
+        }
+        // activation codes: ksteps 16g + 8h2 .. +7, BN tokens x 32 B each
+        for (int kk = 0; kk < 8; kk++) {
+            const _Float16* src = A.b + ((int64_t) (16 * g + 8 * h2 + kk) * A.NP + n0) * 16;
+#pragma unroll
+            for (int p = 0; p < BN / 32; p++)
+                if (mine()) dma16((const uint8_t*) src + p * 1024 + 16 * lane, buf + S::B_OFF + kk * BN * 32 + p * 1024);
+        }
+        // block scales: 4 blocks x BN tokens (f32)
+        for (int p = 0; p < BN / 64; p++) {
+            if (!mine()) continue;
+            const int blk = (p * 64 + lane) / (BN / 4), tok = 4 * ((p * 64 + lane) % (BN / 4));
+            dma16(A.dx + (int64_t) (8 * g + 4 * h2 + blk) * A.NP + n0 + tok, buf + S::DX_OFF + p * 1024);
+        }
+        // sums: Q4_K needs them at the super-block's end (odd stage), Q6_K at its start (even stage)
+        if ((DT == Q4_K) == (h2 == 1)) {
+            constexpr int SWB = S::SW * 2;   // bytes per token per plane
+            for (int pl = 0; pl < 2; pl++) {
+                const _Float16* src = (pl ? A.slo : A.shi) + ((int64_t) g * A.NP + n0) * S::SW;
+                for (int p = 0; p < BN * SWB / 1024; p++)
+                    if (mine())
+                        dma16((const uint8_t*) src + p * 1024 + 16 * lane, buf + S::S_OFF + pl * BN * SWB + p * 1024);
+            }
+        }
+    };
+
+    floatx16 acc[RT][CT], accs[RT][CT];
+#pragma unroll
+    for (int i = 0; i < RT; i++)
+#pragma unroll
+        for (int j = 0; j < CT; j++) acc[i][j] = floatx16{};
+
+    issue(0, smem);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+
+    for (int st = 0; st < nst; st++) {
+        unsigned char* buf = smem + (st & 1) * S::BYTES;
+        if (st + 1 < nst) issue(st + 1, smem + ((st + 1) & 1) * S::BYTES);
+        const int h2 = st & 1;
+        const unsigned char* LA = buf + S::A_OFF;
+        const unsigned char* LB = buf + S::B_OFF;
+        const float* LDX = reinterpret_cast<const float*>(buf + S::DX_OFF);
+
+        if constexpr (DT == Q4_K) {
+            if (h2 == 0) {
+#pragma unroll
+                for (int i = 0; i < RT; i++)
+#pragma unroll
+                    for (int j = 0; j < CT; j++) accs[i][j] = floatx16{};
+            }
+            uint4 hdr[RT];
+#pragma unroll
+            for (int i = 0; i < RT; i++)
+                hdr[i] = *reinterpret_cast<const uint4*>(buf + S::H_OFF + ((wave * RT + i) * 32 + r) * 16);
+#pragma unroll
+            for (int gpl = 0; gpl < 2; gpl++) {
+                uint4 ch[RT];
+#pragma unroll
+                for (int i = 0; i < RT; i++)
+                    ch[i] = *reinterpret_cast<const uint4*>(LA + ((wave * RT + i) * NCS + 2 * gpl + q) * 512 + 16 * r);
+#pragma unroll
+                for (int sub = 0; sub < 2; sub++) {
+                    const int s = 4 * h2 + 2 * gpl + sub, bl = 2 * gpl + sub;
+                    half8 af[RT][2];
+#pragma unroll
+                    for (int i = 0; i < RT; i++) {
+                        int sc, mn;
+                        q4k_scmn(hdr[i], s, sc, mn);
+                        // lo nibble: (1024 + v)·sc − 1024·sc; hi nibble (bits 4-7): (1024 + 16v)·sc/16 − 64·sc
+                        const float fm = sub ? (float) sc * 0.0625f : (float) sc;
+                        const float fa = sub ? -64.0f * (float) sc : -1024.0f * (float) sc;
+                        const uint32_t mul = pack2((_Float16) fm, (_Float16) fm), add = pack2((_Float16) fa, (_Float16) fa);
+                        const uint32_t mask = sub ? 0x00F000F0u : 0x000F000Fu;
+                        af[i][0] = frag8(ch[i].x, ch[i].y, mask, mul, add);
+                        af[i][1] = frag8(ch[i].z, ch[i].w, mask, mul, add);
+                    }
+                    half8 bf[CT][2];
+                    float dxv[CT];
+#pragma unroll
+                    for (int j = 0; j < CT; j++) {
+#pragma unroll
+                        for (int ks = 0; ks < 2; ks++)
+                            bf[j][ks] = *reinterpret_cast<const half8*>(LB + ((2 * bl + ks) * BN + 32 * j + r) * 32 + 16 * q);
+                        dxv[j] = LDX[bl * BN + 32 * j + r];
+                    }
+#pragma unroll
+                    for (int i = 0; i < RT; i++)
+#pragma unroll
+                        for (int j = 0; j < CT; j++) {
+                            floatx16 D = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i][0], bf[j][0], floatx16{}, 0, 0, 0);
+                            D = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i][1], bf[j][1], D, 0, 0, 0);
+#pragma unroll
+                            for (int e = 0; e < 16; e++) accs[i][j][e] = fmaf(D[e], dxv[j], accs[i][j][e]);
+                        }
+                }
+            }
+            if (h2 == 1) {   // super-block end: d, then the mins on the matrix cores
+#pragma unroll
+                for (int i = 0; i < RT; i++) {
+                    const unsigned char* H = buf + S::H_OFF + (wave * RT + i) * 32 * 16;
+                    float dd[16];
+#pragma unroll
+                    for (int e = 0; e < 16; e++) {
+                        const int row = 8 * (e >> 2) + 4 * q + (e & 3);
+                        dd[e] = h2f_bits(*reinterpret_cast<const uint16_t*>(H + row * 16));
+                    }
+#pragma unroll
+                    for (int j = 0; j < CT; j++)
+#pragma unroll
+                        for (int e = 0; e < 16; e++) acc[i][j][e] = fmaf(dd[e], accs[i][j][e], acc[i][j][e]);
+                    // A' = −dmin·mn_s for sub-blocks 4q..4q+3 of row r, split hi + lo
+                    const float dmin = h2f_bits(hdr[i].x >> 16);
+                    half4 ahi, alo;
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        int sc, mn;
+                        q4k_scmn(hdr[i], 4 * q + e, sc, mn);
+                        const float v = -(dmin * (float) mn);
+                        const _Float16 h = (_Float16) v;
+                        ahi[e] = h;
+                        alo[e] = (_Float16) (v - (float) h);
+                    }
+#pragma unroll
+                    for (int j = 0; j < CT; j++) {
+                        const unsigned char* SP = buf + S::S_OFF + (32 * j + r) * 16 + 8 * q;
+                        const half4 bhi = *reinterpret_cast<const half4*>(SP);
+                        const half4 blo = *reinterpret_cast<const half4*>(SP + BN * 16);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(ahi, bhi, acc[i][j], 0, 0, 0);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(ahi, blo, acc[i][j], 0, 0, 0);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(alo, bhi, acc[i][j], 0, 0, 0);
+                    }
+                }
+            }
+        } else {   // Q6_K: stage h2 = half h of the super-block, blocks j = 0..3 (elements 128h + 32j + l)
+            const int8_t* scb = reinterpret_cast<const int8_t*>(LA);   // + tile offset below
+            if (h2 == 0) {
+                // accs = −8·Σ_t sc_t·xs_t (the −32 offset, in units of 1/4), one 32x32x16 step hi + lo
+#pragma unroll
+                for (int i = 0; i < RT; i++) {
+                    const int8_t* sc16 = scb + ((wave * RT + i) * NCS + 6) * 512 + 16 * r + 8 * q;
+                    half8 ao;
+#pragma unroll
+                    for (int e = 0; e < 8; e++) ao[e] = (_Float16) (-8.0f * (float) sc16[e]);
+#pragma unroll
+                    for (int j = 0; j < CT; j++) {
+                        const unsigned char* SP = buf + S::S_OFF + (32 * j + r) * 32 + 16 * q;
+                        const half8 bhi = *reinterpret_cast<const half8*>(SP);
+                        const half8 blo = *reinterpret_cast<const half8*>(SP + BN * 32);
+                        accs[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ao, bhi, floatx16{}, 0, 0, 0);
+                        accs[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ao, blo, accs[i][j], 0, 0, 0);
+                    }
+                }
+            }
+            uint4 ql[RT][2], qh[RT];
+            int8_t scl[RT][4];
+#pragma unroll
+            for (int i = 0; i < RT; i++) {
+                const unsigned char* T = LA + (wave * RT + i) * NCS * 512 + 16 * r;
+                ql[i][0] = *reinterpret_cast<const uint4*>(T + (0 + q) * 512);
+                ql[i][1] = *reinterpret_cast<const uint4*>(T + (2 + q) * 512);
+                qh[i] = *reinterpret_cast<const uint4*>(T + (4 + q) * 512);
+                const int8_t* sc16 = reinterpret_cast<const int8_t*>(LA + ((wave * RT + i) * NCS + 6) * 512 + 16 * r);
+#pragma unroll
+                for (int jb = 0; jb < 4; jb++) scl[i][jb] = sc16[8 * h2 + 2 * jb + q];
+            }
+#pragma unroll
+            for (int jb = 0; jb < 4; jb++) {
+                half8 a1[RT][2], a2[RT][2];
+#pragma unroll
+                for (int i = 0; i < RT; i++) {
+                    const float sc = (float) scl[i][jb];
+                    // ql nibble: lo (1024 + v)·sc/4 − 256·sc; hi (1024 + 16v)·sc/64 − 16·sc
+                    const bool hi = jb >= 2;
+                    const float fm = hi ? sc * 0.015625f : sc * 0.25f, fa = hi ? -16.0f * sc : -256.0f * sc;
+                    const uint32_t mul1 = pack2((_Float16) fm, (_Float16) fm), add1 = pack2((_Float16) fa, (_Float16) fa);
+                    const uint4 L = ql[i][jb & 1];
+                    const uint32_t m1 = hi ? 0x00F000F0u : 0x000F000Fu;
+                    a1[i][0] = frag8(L.x, L.y, m1, mul1, add1);
+                    a1[i][1] = frag8(L.z, L.w, m1, mul1, add1);
+                    // qh bits 2jb..2jb+1 moved to bits 4-5: (1024 + 16v)·sc/4 − 256·sc = 4·sc·v = sc·(16v)/4
+                    const float fm2 = sc * 0.25f, fa2 = -256.0f * sc;
+                    const uint32_t mul2 = pack2((_Float16) fm2, (_Float16) fm2), add2 = pack2((_Float16) fa2, (_Float16) fa2);
+                    const uint4 Q = qh[i];
+                    const int sh = 2 * jb;   // bits 2jb..2jb+1 -> 4..5
+                    auto mv = [&](uint32_t x) { return sh <= 4 ? x << (4 - sh) : x >> (sh - 4); };
+                    a2[i][0] = frag8(mv(Q.x), mv(Q.y), 0x00300030u, mul2, add2);
+                    a2[i][1] = frag8(mv(Q.z), mv(Q.w), 0x00300030u, mul2, add2);
+                }
+                half8 bf[CT][2];
+                float dxv[CT];
+#pragma unroll
+                for (int j = 0; j < CT; j++) {
+#pragma unroll
+                    for (int ks = 0; ks < 2; ks++)
+                        bf[j][ks] = *reinterpret_cast<const half8*>(LB + ((2 * jb + ks) * BN + 32 * j + r) * 32 + 16 * q);
+                    dxv[j] = LDX[jb * BN + 32 * j + r];
+                }
+#pragma unroll
+                for (int i = 0; i < RT; i++)
+#pragma unroll
+                    for (int j = 0; j < CT; j++) {
+                        floatx16 D = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1[i][0], bf[j][0], floatx16{}, 0, 0, 0);
+                        D = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1[i][1], bf[j][1], D, 0, 0, 0);
+                        D = __builtin_amdgcn_mfma_f32_32x32x16_f16(a2[i][0], bf[j][0], D, 0, 0, 0);
+                        D = __builtin_amdgcn_mfma_f32_32x32x16_f16(a2[i][1], bf[j][1], D, 0, 0, 0);
+#pragma unroll
+                        for (int e = 0; e < 16; e++) accs[i][j][e] = fmaf(D[e], dxv[j], accs[i][j][e]);
+                    }
+            }
+            if (h2 == 1) {   // super-block end: acc += 4d · accs
+#pragma unroll
+                for (int i = 0; i < RT; i++) {
+                    const unsigned char* H = buf + S::H_OFF + (wave * RT + i) * 32 * 2;
+                    float dd[16];
+#pragma unroll
+                    for (int e = 0; e < 16; e++) {
+                        const int row = 8 * (e >> 2) + 4 * q + (e & 3);
+                        dd[e] = 4.0f * h2f_bits(*reinterpret_cast<const uint16_t*>(H + row * 2));
+                    }
+#pragma unroll
+                    for (int j = 0; j < CT; j++)
+#pragma unroll
+                        for (int e = 0; e < 16; e++) acc[i][j][e] = fmaf(dd[e], accs[i][j][e], acc[i][j][e]);
+                }
+            }
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+    }
+
+    // epilogue: lane holds token n0 + 32j + r, rows 8·(e/4) + 4q + e%4 of each tile; scale back by 2^e_t
+#pragma unroll
+    for (int j = 0; j < CT; j++) {
+        const int t = n0 + 32 * j + r;
+        if (t >= n) continue;
+        const float sc = A.es[t];
+        float* ct = c + (int64_t) t * ldc;
+#pragma unroll
+        for (int i = 0; i < RT; i++) {
+            const int64_t rowb = (T0 + wave * RT + i) * 32 + 4 * q;
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const int64_t row = rowb + 8 * (e >> 2) + (e & 3);
+                if (row < m) ct[row] = acc[i][j][e] * sc;
+            }
+        }
+    }
+}
+
+template <int DT, int RT, int CT>
+static hipError_t kq_go(const WeightView& w, const GemmAct& A, int m, int n, float* c, int ldc, hipStream_t st) {
+    using S = Stage<DT, RT, CT>;
+    const int nrb = (m + 32 * S::TW - 1) / (32 * S::TW), ncb = A.NP / S::BN;
+    const int64_t tiles = (w.r0 + tiled_rows(m)) / 32 - w.r0 / 32;   // tiles of the view that exist
+    const int total = nrb * ncb, grid = (total + 7) / 8 * 8;
+    const size_t lds = 2 * (size_t) S::BYTES;
+    static bool attr = false;
+    if (!attr) {
+        hipError_t e = hipFuncSetAttribute((const void*) kq_gemm_kernel<DT, RT, CT>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int) lds);
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
+    kq_gemm_kernel<DT, RT, CT><<<grid, MMA_THREADS, lds, st>>>(w, A, m, n, c, ldc, nrb, ncb, tiles);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemm_mma(int dt, const WeightView& w, const GemmAct& A, int k, int m, int n, float* c, int ldc,
+                           hipStream_t st) {
+    if (k % 256 || (w.r0 & 31) || A.NP % 64) return hipErrorNotSupported;
+    switch (dt) {
+    case Q4_K: return kq_go<Q4_K, 1, 2>(w, A, m, n, c, ldc, st);
+    case Q6_K: return kq_go<Q6_K, 1, 2>(w, A, m, n, c, ldc, st);
+    default: return hipErrorNotSupported;
+    }
+}
+
+}  // namespace jamhip

@@ -95,6 +95,105 @@ __global__ void __launch_bounds__(256) repack_kernel(const uint8_t* __restrict__
     }
 }
 
+// ------------------------------------------------------------------------- matrix-core GEMM activations
+// Position of element j of an 8-element run inside an A-operand fragment (its own inverse): the weight
+// dequantization builds f16 pairs from bytes (0,2), (1,3), (4,6), (5,7) of two 32-bit words.
+JAMHIP_DEV int perm8(int j) { return j == 1 ? 2 : j == 2 ? 1 : j == 5 ? 6 : j == 6 ? 5 : j; }
+
+int gemm_sums_kind(int dt) { return dt == Q4_K || dt == Q4_0 ? 1 : dt == Q6_K ? 2 : 0; }
+
+// One workgroup per (padded) token: jam's F2 quantization of every 32-element block (f2_lane, bit-exact),
+// the codes scattered into the fragment order of GemmAct::b, then the token's power-of-two scale and the
+// scaled block scales and sums. SK: 0 no sums, 1 per-32 sums xs0 + xs1 (jam's fl(xs0 + xs1)), 2 per-16.
+template <int SK>
+__global__ void __launch_bounds__(256) gemm_prep_kernel(const float* __restrict__ a, int lda, int n, int k, int Kp,
+                                                        int NP, _Float16* __restrict__ bq, float* __restrict__ dx,
+                                                        _Float16* __restrict__ shi, _Float16* __restrict__ slo,
+                                                        float* __restrict__ es) {
+    extern __shared__ float psm[];   // block scales [Kp/32], per-16 sums [Kp/16]
+    __shared__ float red[4];
+    const int t = blockIdx.x, nbp = Kp >> 5, nbk = k >> 5, e = threadIdx.x & 31;
+    float* sdb = psm;
+    float* sxs = psm + nbp;
+    const bool live = t < n;
+    for (int b = threadIdx.x >> 5; b < nbp; b += 8) {   // b is uniform in each 32-lane group
+        const float x = live && b < nbk ? a[(int64_t) t * lda + 32 * b + e] : 0.0f;
+        float db, xs16;
+        const int v = f2_lane(x, db, xs16);
+        const int q = e >> 4, ks = (e >> 3) & 1;
+        bq[((int64_t) (2 * b + ks) * NP + t) * 16 + 8 * q + perm8(e & 7)] = (_Float16) v;
+        if (e == 0) sdb[b] = db;
+        if ((e & 15) == 0) sxs[2 * b + q] = xs16;
+    }
+    __syncthreads();
+    float mx = 0.0f;
+    if constexpr (SK == 1)
+        for (int b = threadIdx.x; b < nbp; b += 256) mx = fmaxf(mx, fabsf(sxs[2 * b] + sxs[2 * b + 1]));
+    if constexpr (SK == 2)
+        for (int i = threadIdx.x; i < 2 * nbp; i += 256) mx = fmaxf(mx, fabsf(sxs[i]));
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    int ex = 0;
+    if (SK != 0 && mx > 0.0f && mx <= 3.0e38f) {   // zero or non-finite sums keep 2^0
+        frexpf(mx, &ex);                         // mx < 2^ex
+        ex -= 14;
+    }
+    const float down = ldexpf(1.0f, -ex);
+    if (threadIdx.x == 0) es[t] = ldexpf(1.0f, ex);
+    for (int b = threadIdx.x; b < nbp; b += 256) dx[(int64_t) b * NP + t] = sdb[b] * down;
+    if constexpr (SK == 1) {
+        for (int b = threadIdx.x; b < nbp; b += 256) {
+            const float v = (sxs[2 * b] + sxs[2 * b + 1]) * down;
+            const _Float16 h = (_Float16) v;
+            const int64_t o = ((int64_t) (b >> 3) * NP + t) * 8 + (b & 7);
+            shi[o] = h;
+            slo[o] = (_Float16) (v - (float) h);
+        }
+    }
+    if constexpr (SK == 2) {
+        for (int i = threadIdx.x; i < 2 * nbp; i += 256) {
+            const float v = sxs[i] * down;
+            const _Float16 h = (_Float16) v;
+            const int64_t o = ((int64_t) (i >> 4) * NP + t) * 16 + (i & 15);
+            shi[o] = h;
+            slo[o] = (_Float16) (v - (float) h);
+        }
+    }
+}
+
+static int64_t a256(int64_t v) { return (v + 255) & ~(int64_t) 255; }
+
+size_t gemm_act_bytes(int dt, int n, int k) {
+    const int64_t NP = (n + 63) / 64 * 64, Kp = (k + 255) / 256 * 256, sk = gemm_sums_kind(dt);
+    const int64_t sb = sk == 0 ? 0 : a256((Kp / 256) * NP * (sk == 1 ? 8 : 16) * 2);
+    return (size_t) (a256(Kp * NP * 2) + a256((Kp / 32) * NP * 4) + 2 * sb + a256(NP * 4));
+}
+
+hipError_t launch_gemm_prep(int dt, const float* a, int lda, int n, int k, void* scratch, GemmAct* out,
+                            hipStream_t st) {
+    const int NP = (n + 63) / 64 * 64, Kp = (k + 255) / 256 * 256, sk = gemm_sums_kind(dt);
+    uint8_t* p = (uint8_t*) scratch;
+    _Float16* bq = (_Float16*) p;
+    p += a256((int64_t) Kp * NP * 2);
+    float* dx = (float*) p;
+    p += a256((int64_t) (Kp / 32) * NP * 4);
+    const int64_t sb = sk == 0 ? 0 : a256((int64_t) (Kp / 256) * NP * (sk == 1 ? 8 : 16) * 2);
+    _Float16* shi = (_Float16*) p;
+    _Float16* slo = (_Float16*) (p + sb);
+    p += 2 * sb;
+    float* es = (float*) p;
+    *out = GemmAct{bq, dx, shi, slo, es, NP, Kp};
+    const size_t lds = (size_t) (Kp / 32) * 12;
+    if (lds > 64 * 1024) return hipErrorNotSupported;
+    if (sk == 1) gemm_prep_kernel<1><<<NP, 256, lds, st>>>(a, lda, n, k, Kp, NP, bq, dx, shi, slo, es);
+    else if (sk == 2) gemm_prep_kernel<2><<<NP, 256, lds, st>>>(a, lda, n, k, Kp, NP, bq, dx, shi, slo, es);
+    else gemm_prep_kernel<0><<<NP, 256, lds, st>>>(a, lda, n, k, Kp, NP, bq, dx, shi, slo, es);
+    return hipGetLastError();
+}
+
 hipError_t launch_quant_f1(const float* a, int lda, int n, int k, int8_t* q, float* d, float* asum, int* s16,
                            hipStream_t st) {
     dim3 grid((k + 255) / 256, n);
