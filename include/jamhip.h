@@ -95,6 +95,49 @@ jamhip_status jamhip_mm_device(jamhip_ctx* ctx,
 jamhip_status jamhip_quantize_device(jamhip_ctx* ctx, int flavour, const void* a_dev, int lda, int n, int k,
                                      void* q_dev, void* d_dev, void* s_dev);
 
+/* ---- Mixture-of-experts (device pointers, context stream, not synchronized) -------------------------
+ * These replace jinfer's host-side CSR dispatch (jinfer/jinfer-kernels/src/main/java/com/qxotic/jinfer/
+ * kernels/Moe.java:178-232) and its per-expert loop of jam calls (GptOss.java:290-314): the same
+ * routing order, gather, per-expert jam_mm semantics and fused-multiply-add combine, with the counts
+ * and offsets staying on the GPU. */
+
+/* Grouped matmul. The n_experts weight matrices are one tensor of n_experts·m rows at w (dtype wt, row
+ * stride ldw; expert e = rows [e·m, (e+1)·m)), pinned or staged like jamhip_mm's W. counts_dev[e]
+ * (int32) is expert e's row count; off = their exclusive prefix sum, computed on the device (written to
+ * offsets_dev[0..n_experts] when non-NULL). Expert e's rows are A/C rows [off[e], off[e] + counts[e])
+ * (CSR order, as Moe.dispatch gathers them); for each expert the result is jam_mm(W_e, A_e, C_e, m,
+ * counts[e], k) under jam's routing (F1 below 8 rows, 16-row F2 bands from 8). rows_cap is the number
+ * of rows A and C hold: rows past it (a prefix sum beyond rows_cap) are not computed and never read.
+ * m must be a multiple of 16 and n_experts <= 1024 (else JAMHIP_EUNSUPPORTED). Replaces the per-expert
+ * MatMul.gemm calls of Moe.dispatch's kernel closure (GptOss.java:295-314). */
+jamhip_status jamhip_mm_grouped(jamhip_ctx* ctx,
+                                const void* w, int wt, int ldw, int m, int n_experts,
+                                const void* counts_dev,
+                                const void* a_dev, int at, int lda,
+                                void*       c_dev, int ct, int ldc,
+                                int k, int rows_cap, void* offsets_dev);
+
+/* Moe.dispatch's CSR build (Moe.java:188-206) from route_expert_dev[seq·topk] (int32 expert of route
+ * s·topk + j, Moe.selectTopK's rowTopE): counts_dev[n_experts], offsets_dev[n_experts + 1], and the
+ * slot of every route in (s, j) order within its expert: slot_route_dev[slot] = route,
+ * route_slot_dev[route] = slot (-1 for an expert id outside [0, n_experts)). n_experts <= 1024. */
+jamhip_status jamhip_moe_route(jamhip_ctx* ctx, const void* route_expert_dev, int seq, int topk, int n_experts,
+                               void* counts_dev, void* offsets_dev, void* slot_route_dev, void* route_slot_dev);
+
+/* Moe.dispatch's gather (Moe.java:214-222): g[slot] = x[slot_route[slot] / topk] for the slots below
+ * offsets[n_experts]; dim floats per row, row strides ldx / ldg (elements). */
+jamhip_status jamhip_moe_gather(jamhip_ctx* ctx, const void* x_dev, int ldx, const void* slot_route_dev,
+                                const void* offsets_dev, int n_experts, int seq, int topk, int dim,
+                                void* g_dev, int ldg);
+
+/* Moe.dispatch's weighted scatter-add (Moe.java:208, 223-231; Ops.saxpyInPlace's fma, Ops.java:688-725):
+ * out[s] = 0, then for each route of s in ascending expert order (then route order),
+ * out[s] = fma(route_prob[route], y[route_slot[route]], out[s]). Bit-identical to the host loop.
+ * topk <= 16. */
+jamhip_status jamhip_moe_combine(jamhip_ctx* ctx, const void* y_dev, int ldy, const void* route_expert_dev,
+                                 const void* route_prob_dev, const void* route_slot_dev, int seq, int topk,
+                                 int n_experts, int dim, void* out_dev, int ldo);
+
 /* Use `stream` (a hipStream_t; NULL = the context's own) for subsequent work of this context. */
 jamhip_status jamhip_ctx_set_stream(jamhip_ctx* ctx, void* stream);
 void*         jamhip_ctx_stream(const jamhip_ctx* ctx);

@@ -29,6 +29,7 @@ UNITS = {   # source -> extra flags
     "gemv.hip": [],
     "gemm.hip": [],
     "mma.hip": [],
+    "moe.hip": [],
     "jamhip.cpp": ["-x", "hip"],
 }
 

@@ -25,7 +25,8 @@ __host__ __device__ constexpr int block_bytes(int dt) {
 //   Q6_K : NC 13 chunks 0-7 ql, 8-11 qh, 12 the 16 int8 scales | SB 2 : d fp16
 //   Q8_0 : NC 16 chunk c = half c&1 of block c>>1 (int8 q)     | SB 16: the 8 blocks' fp16 d
 //   Q4_0 : NC 8  chunk c = block c's 16 nibble bytes           | SB 16: the 8 blocks' fp16 d
-//   MXFP4: NC 8  chunk c = block c's 16 nibble bytes           | SB 8 : the 8 blocks' e8m0
+//   MXFP4: NC 8  chunk c = block c's 16 nibble bytes           | SB 16: the 8 blocks' e8m0, then their
+//                                                                maximum (the group's reference exponent)
 // Rows are taken in tiles of 32 (the row count is padded up to a multiple of 32 with zero rows). Plane 0
 // ("qs") holds chunk c of group g of row r at byte ((T·G + g)·NC + c)·512 + (r mod 32)·16 with T = r / 32
 // and G = groups per row: for a fixed (tile, group, chunk) the 32 rows' chunks are 512 contiguous bytes,
@@ -37,7 +38,7 @@ __host__ __device__ constexpr int group_chunks(int dt) {
     return dt == Q4_K ? 8 : dt == Q6_K ? 13 : dt == Q8_0 ? 16 : dt == Q4_0 ? 8 : dt == MXFP4 ? 8 : 0;
 }
 __host__ __device__ constexpr int group_scale_bytes(int dt) {
-    return dt == Q4_K ? 16 : dt == Q6_K ? 2 : dt == Q8_0 ? 16 : dt == Q4_0 ? 16 : dt == MXFP4 ? 8 : 0;
+    return dt == Q4_K ? 16 : dt == Q6_K ? 2 : dt == Q8_0 ? 16 : dt == Q4_0 ? 16 : dt == MXFP4 ? 16 : 0;
 }
 __host__ __device__ constexpr int blocks_per_group(int dt) { return 256 / block_elems(dt); }
 // groups per row for a row of `blocks` blocks

@@ -195,7 +195,7 @@ constexpr int MV_WAVES = 8;   // waves per GEMV workgroup (512 threads)
 template <int HP> struct APre { float x[HP][16]; };
 
 template <int NT, int HP>
-JAMHIP_DEV void a_load(APre<HP>& pre, const float* __restrict__ a, int lda, int k, int Gk) {
+JAMHIP_DEV void a_load(APre<HP>& pre, const float* __restrict__ a, int lda, int k, int Gk, int ntv) {
     // four 16-byte loads per half-block (the launcher checks a and lda for 16-byte alignment); a half past
     // the token's last element (a partial last group) re-reads the token's last half, zeroed by f1_store
     // (zeroing here would make the wave wait for these loads before issuing the weight loads)
@@ -203,9 +203,9 @@ JAMHIP_DEV void a_load(APre<HP>& pre, const float* __restrict__ a, int lda, int 
 #pragma unroll
     for (int i = 0; i < HP; i++) {
         const int h0 = threadIdx.x + 64 * MV_WAVES * i, h = h0 < total ? h0 : total - 1;
-        const int j = h / halves, hh = h - j * halves;
+        const int j = h / halves, hh = h - j * halves, jr = j < ntv ? j : ntv - 1;   // rows past ntv: clamp
         const bool in = hh < kh;   // clamp only; the zeroing happens in f1_store
-        const float4* src = reinterpret_cast<const float4*>(a + (int64_t) j * lda + 16 * (in ? hh : kh - 1));
+        const float4* src = reinterpret_cast<const float4*>(a + (int64_t) jr * lda + 16 * (in ? hh : kh - 1));
 #pragma unroll
         for (int v = 0; v < 4; v++) {
             const float4 f = src[v];
@@ -281,10 +281,12 @@ JAMHIP_DEV void f1_store(const APre<HP>& pre, int k, int Gk, int8_t* lq, float* 
 // FL = 1: F1 activations, NT = n (1..7). HP > 0: quantized into LDS by this workgroup (HP half-blocks
 // per thread); HP = 0: read from A. FL = 2: F2 activations from A; blockIdx.y picks NT tokens, the last
 // group may hold fewer (ntv).
-template <int DT, int FL, int NT, int HP, int RB, int ITEMS>
+// GR (grouped matmul): FL = 1 takes expert blockIdx.y if it has 1..7 rows (ntv of them, CSR rows from
+// off[e]); FL = 2 takes the 8-token tile blockIdx.y of map8. The expert's weight rows start at e·gm.
+template <int DT, int FL, int NT, int HP, int RB, int ITEMS, bool GR>
 __global__ void __launch_bounds__(64 * MV_WAVES) mv_kernel(WeightView w, ActQ A, const float* __restrict__ a,
                                                           int lda, int k, int m, int n, float* __restrict__ c,
-                                                          int ldc) {
+                                                          int ldc, Groups gp) {
     constexpr int BPG = blocks_per_group(DT), GS = 64 / RB;
     constexpr bool FUSE = HP > 0;
     const int lane = threadIdx.x & 63, rr = lane % RB, gs = lane / RB;
@@ -294,11 +296,35 @@ __global__ void __launch_bounds__(64 * MV_WAVES) mv_kernel(WeightView w, ActQ A,
     const int J = (Gk + GS - 1) / GS;            // items per row band
     const int QB = MV_WAVES * ITEMS / J;         // bands per block (the launcher keeps J <= 8·ITEMS)
     const int64_t q0 = (int64_t) blockIdx.x * QB;
-    const int t0 = blockIdx.y * NT;
-    const int ntv = n - t0 < NT ? n - t0 : NT;
+    int t0, ntv;
+    if constexpr (GR) {
+        int e, o, ne;
+        if constexpr (FL == 1) {
+            e = blockIdx.y;
+            o = __builtin_amdgcn_readfirstlane(gp.off[e]);
+            ne = __builtin_amdgcn_readfirstlane(gp.off[e + 1]) - o;
+            if (ne <= 0 || ne >= 8) return;   // whole workgroup, before any barrier
+            t0 = o;
+            ntv = ne;
+            a += (int64_t) o * lda;
+        } else {
+            e = __builtin_amdgcn_readfirstlane(gp.map8[blockIdx.y]);
+            if (e < 0) return;
+            const int local = (int) blockIdx.y * 8 - __builtin_amdgcn_readfirstlane(gp.poff8[e]);
+            o = __builtin_amdgcn_readfirstlane(gp.off[e]);
+            ne = __builtin_amdgcn_readfirstlane(gp.off[e + 1]) - o;
+            t0 = o + local;
+            ntv = ne - local < NT ? ne - local : NT;
+        }
+        w.r0 += (int64_t) e * gp.gm;
+        m = gp.gm;
+    } else {
+        t0 = blockIdx.y * NT;
+        ntv = n - t0 < NT ? n - t0 : NT;
+    }
 
     APre<FUSE ? HP : 1> pre;
-    if constexpr (FUSE) a_load<NT, HP>(pre, a, lda, k, Gk);   // first in the load queue
+    if constexpr (FUSE) a_load<NT, HP>(pre, a, lda, k, Gk, ntv);   // first in the load queue
     __builtin_amdgcn_sched_barrier(0);                        // ... and kept there by the scheduler
 
     // item i of this wave: band q0 + it / J, group slot it % J with it = wave·ITEMS + i (clamped)
@@ -351,7 +377,7 @@ __global__ void __launch_bounds__(64 * MV_WAVES) mv_kernel(WeightView w, ActQ A,
         constexpr int TU = NT > 2 ? 1 : NT;   // keep several tokens' temporaries out of the register file
 #pragma unroll TU
         for (int t = 0; t < NT; t++) {
-            if (FL == 2 && t >= ntv) break;
+            if (t >= ntv) break;
             const int tt = FUSE ? t : t0 + t;
             const float p = group_dot<DT, FL>(buf[i], aq + tt * tq + (int64_t) gg * QS, ad + tt * td + 8 * gg,
                                               as + tt * ts + (FL == 1 ? 8 : 16) * gg, s16 + tt * t16 + 16 * gg, nbv);
@@ -367,7 +393,7 @@ __global__ void __launch_bounds__(64 * MV_WAVES) mv_kernel(WeightView w, ActQ A,
 #pragma unroll
             for (int s2 = 0; s2 < GS; s2++) v += part[(((q * J + j) * 64) + s2 * RB + r) * NT + t];
         const int64_t row = RB * (q0 + q) + r;
-        if (row < m && (FL == 1 || t < ntv)) c[(int64_t) (t0 + t) * ldc + row] = v;
+        if (row < m && t < ntv) c[(int64_t) (t0 + t) * ldc + row] = v;
     }
 }
 
@@ -468,7 +494,55 @@ static void launch_shape(int k, int m, int n, const WeightView& w, const ActQ& A
     const int64_t bands = ((int64_t) m + RB - 1) / RB;
     const dim3 grid((unsigned) ((bands + QB - 1) / QB), FL == 1 ? 1 : (n + NT - 1) / NT);
     const size_t lds = (size_t) MV_WAVES * ITEMS * 64 * NT * sizeof(float) + (HP > 0 ? 32 + fuse_lds(NT, k) : 0);
-    mv_kernel<DT, FL, NT, HP, RB, ITEMS><<<grid, 64 * MV_WAVES, lds, st>>>(w, A, a, lda, k, m, n, c, ldc);
+    mv_kernel<DT, FL, NT, HP, RB, ITEMS, false><<<grid, 64 * MV_WAVES, lds, st>>>(w, A, a, lda, k, m, n, c, ldc,
+                                                                                 Groups{});
+}
+
+template <int DT, int FL, int NT, int HP, int RB, int ITEMS>
+static void launch_shape_grouped(int k, const Groups& g, int ny, const WeightView& w, const ActQ& A, const float* a,
+                                 int lda, float* c, int ldc, hipStream_t st) {
+    constexpr int GS = 64 / RB;
+    const int Gk = (k / 32 + 7) / 8, J = (Gk + GS - 1) / GS;
+    const int QB = MV_WAVES * ITEMS / J;
+    const int64_t bands = ((int64_t) g.gm + RB - 1) / RB;
+    const dim3 grid((unsigned) ((bands + QB - 1) / QB), (unsigned) ny);
+    const size_t lds = (size_t) MV_WAVES * ITEMS * 64 * NT * sizeof(float) + (HP > 0 ? 32 + fuse_lds(NT, k) : 0);
+    mv_kernel<DT, FL, NT, HP, RB, ITEMS, true><<<grid, 64 * MV_WAVES, lds, st>>>(w, A, a, lda, k, g.gm, 0, c, ldc, g);
+}
+
+template <int DT, int FL, int NT, int HP>
+static hipError_t go_grouped(int k, const Groups& g, int ny, const WeightView& w, const ActQ& A, const float* a,
+                             int lda, float* c, int ldc, hipStream_t st) {
+    int items;
+    if (!mv_items(k, &items)) return hipErrorNotSupported;
+    if (items == 1) launch_shape_grouped<DT, FL, NT, HP, MV_RB, 1>(k, g, ny, w, A, a, lda, c, ldc, st);
+    else if (items == 2) launch_shape_grouped<DT, FL, NT, HP, MV_RB, 2>(k, g, ny, w, A, a, lda, c, ldc, st);
+    else launch_shape_grouped<DT, FL, NT, HP, MV_RB, 4>(k, g, ny, w, A, a, lda, c, ldc, st);
+    return hipGetLastError();
+}
+
+template <int DT>
+static hipError_t gemv_grouped_dt(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k,
+                                  const Groups& g, int E, int cap8, float* c, int ldc, hipStream_t st) {
+    if (flavour == 2) return go_grouped<DT, 2, 8, 0>(k, g, cap8, w, A, nullptr, 0, c, ldc, st);
+    if (a == nullptr) return go_grouped<DT, 1, 7, 0>(k, g, E, w, A, nullptr, 0, c, ldc, st);
+    const int hp = fuse_hp(7, k);
+    if (hp <= 1) return go_grouped<DT, 1, 7, 1>(k, g, E, w, A, a, lda, c, ldc, st);
+    if (hp == 2) return go_grouped<DT, 1, 7, 2>(k, g, E, w, A, a, lda, c, ldc, st);
+    return go_grouped<DT, 1, 7, 4>(k, g, E, w, A, a, lda, c, ldc, st);
+}
+
+hipError_t launch_gemv_grouped(int dt, int flavour, const WeightView& w, const ActQ& A, const float* a, int lda,
+                               int k, const Groups& g, int E, int cap8, float* c, int ldc, hipStream_t st) {
+    if (flavour == 2 && cap8 <= 0) return hipSuccess;
+    switch (dt) {
+    case Q4_K: return gemv_grouped_dt<Q4_K>(flavour, w, A, a, lda, k, g, E, cap8, c, ldc, st);
+    case Q6_K: return gemv_grouped_dt<Q6_K>(flavour, w, A, a, lda, k, g, E, cap8, c, ldc, st);
+    case Q8_0: return gemv_grouped_dt<Q8_0>(flavour, w, A, a, lda, k, g, E, cap8, c, ldc, st);
+    case Q4_0: return gemv_grouped_dt<Q4_0>(flavour, w, A, a, lda, k, g, E, cap8, c, ldc, st);
+    case MXFP4: return gemv_grouped_dt<MXFP4>(flavour, w, A, a, lda, k, g, E, cap8, c, ldc, st);
+    default: return hipErrorInvalidValue;
+    }
 }
 
 template <int DT, int FL, int NT, int HP>

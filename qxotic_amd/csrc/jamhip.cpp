@@ -66,7 +66,7 @@ struct jamhip_ctx {
     char arch[64] = {0};
     std::mutex pin_mu;
     std::vector<Pin> pins;
-    DevBuf act, gact, a_stage, c_stage, w_raw, w_stage;
+    DevBuf act, gact, moe, a_stage, c_stage, w_raw, w_stage;
 };
 
 namespace {
@@ -165,10 +165,11 @@ bool env_true(const char* name) {
     return v && (!strcmp(v, "1") || !strcasecmp(v, "true") || !strcasecmp(v, "yes"));
 }
 
-// The matrix-core GEMM covers the K-quants on 32-row-aligned views (launch_gemm_mma).
+// The matrix-core GEMM covers Q4_K, Q6_K (k a multiple of 256) and MXFP4 on 32-row-aligned views
+// (launch_gemm_mma).
 bool mma_path(int dt, int k, const WeightView& wv) {
     if (env_true("JAM_HIP_NO_MMA")) return false;
-    return (dt == Q4_K || dt == Q6_K) && k % 256 == 0 && (wv.r0 & 31) == 0;
+    return (((dt == Q4_K || dt == Q6_K) && k % 256 == 0) || dt == MXFP4) && (wv.r0 & 31) == 0;
 }
 
 // Quantize A (device, f32 [n][lda]) and run the matmul into C (device, [n][ldc]). Decode-sized calls
@@ -278,6 +279,7 @@ void jamhip_ctx_destroy(jamhip_ctx* ctx) {
     ctx->pins.clear();
     ctx->act.release();
     ctx->gact.release();
+    ctx->moe.release();
     ctx->a_stage.release();
     ctx->c_stage.release();
     ctx->w_raw.release();
@@ -406,6 +408,138 @@ jamhip_status jamhip_quantize_device(jamhip_ctx* ctx, int flavour, const void* a
                             ctx->stream);
     }
     return e == hipSuccess ? JAMHIP_OK : hip_fail(ctx, e, "quantize launch");
+}
+
+jamhip_status jamhip_mm_grouped(jamhip_ctx* ctx, const void* w, int wt, int ldw, int m, int n_experts,
+                                const void* counts_dev, const void* a_dev, int at, int lda, void* c_dev, int ct,
+                                int ldc, int k, int rows_cap, void* offsets_dev) {
+    if (!ctx) return JAMHIP_EINVAL;
+    if (!w || !counts_dev || !a_dev || !c_dev) return fail(ctx, JAMHIP_EINVAL, "grouped: null operand");
+    if (m <= 0 || k <= 0 || n_experts <= 0 || rows_cap < 0)
+        return fail(ctx, JAMHIP_EINVAL, "grouped: m, k, n_experts must be positive and rows_cap >= 0");
+    if (ldw < k || lda < k || ldc < m) return fail(ctx, JAMHIP_EINVAL, "grouped: stride below extent");
+    if (at != F32 || ct != F32) return fail(ctx, JAMHIP_EUNSUPPORTED, "grouped: A and C must be F32");
+    if (!supported_w(wt)) return fail(ctx, JAMHIP_EUNSUPPORTED, "grouped: weight dtype not supported");
+    if (k % block_elems(wt) || ldw % block_elems(wt))
+        return fail(ctx, JAMHIP_EUNSUPPORTED, "grouped: k and ldw must be multiples of the block size");
+    if (m % 16) return fail(ctx, JAMHIP_EUNSUPPORTED, "grouped: m must be a multiple of 16");
+    if (n_experts > 1024) return fail(ctx, JAMHIP_EUNSUPPORTED, "grouped: at most 1024 experts");
+    if ((int64_t) m * n_experts > INT32_MAX) return fail(ctx, JAMHIP_EUNSUPPORTED, "grouped: too many rows");
+    Busy guard(ctx);
+    if (!guard.ok) return fail(ctx, JAMHIP_EBUSY, "context busy");
+    (void) hipSetDevice(ctx->device);
+    jamhip_status st;
+    WeightView wv;
+    if ((st = resolve_w(ctx, w, wt, ldw, m * n_experts, k, &wv)) != JAMHIP_OK) return st;
+    const int E = n_experts;
+    const int cap64 = (int) (((int64_t) rows_cap + 63 * E + 63) / 64), cap8 = (int) (((int64_t) rows_cap + 7 * E + 7) / 8);
+    hipError_t e;
+    if ((e = ctx->moe.ensure((size_t) (3 * (E + 1) + cap64 + cap8) * sizeof(int))) != hipSuccess)
+        return hip_fail(ctx, e, "grouped: scratch alloc");
+    int* off = (int*) ctx->moe.p;
+    int* poff64 = off + (E + 1);
+    int* poff8 = poff64 + (E + 1);
+    int* map64 = poff8 + (E + 1);
+    int* map8 = map64 + cap64;
+    if ((e = launch_moe_offsets((const int*) counts_dev, E, rows_cap, off, poff64, poff8, map64, cap64, map8, cap8,
+                                ctx->stream)) != hipSuccess)
+        return hip_fail(ctx, e, "grouped: offsets launch");
+    if (offsets_dev &&
+        (e = hipMemcpyAsync(offsets_dev, off, (size_t) (E + 1) * sizeof(int), hipMemcpyDeviceToDevice, ctx->stream)) !=
+            hipSuccess)
+        return hip_fail(ctx, e, "grouped: offsets copy");
+    if (rows_cap == 0) return JAMHIP_OK;
+    const Groups g{off, poff8, map8, poff64, map64, m};
+    const float* a = (const float*) a_dev;
+    float* c = (float*) c_dev;
+    // activation scratch for the decode kernels (rows_cap rows; F1 then F2 reuse it in stream order)
+    const int64_t nb = k / 32, n = rows_cap;
+    const int64_t qb = align256(n * k), db = align256(n * nb * 4), sb = align256(n * (k / 16) * 4);
+    auto actq = [&](ActQ* A) -> hipError_t {
+        hipError_t r = ctx->act.ensure((size_t) (qb + db + 2 * sb));
+        uint8_t* base = (uint8_t*) ctx->act.p;
+        *A = ActQ{(int8_t*) base, (float*) (base + qb), (float*) (base + qb + db), (int*) (base + qb + db + sb)};
+        return r;
+    };
+    // experts with 1..7 rows: jam's F1 decode path, one launch
+    if (gemv_fusable(7, k, a, lda)) {
+        if ((e = launch_gemv_grouped(wt, 1, wv, ActQ{}, a, lda, k, g, E, cap8, c, ldc, ctx->stream)) != hipSuccess)
+            return hip_fail(ctx, e, "grouped: gemv launch");
+    } else {
+        ActQ A;
+        if ((e = actq(&A)) != hipSuccess) return hip_fail(ctx, e, "grouped: activation scratch alloc");
+        if ((e = launch_quant_f1(a, lda, rows_cap, k, (int8_t*) A.q, (float*) A.d, (float*) A.s, (int*) A.s16,
+                                 ctx->stream)) != hipSuccess ||
+            (e = launch_gemv_grouped(wt, 1, wv, A, nullptr, 0, k, g, E, cap8, c, ldc, ctx->stream)) != hipSuccess)
+            return hip_fail(ctx, e, "grouped: gemv launch");
+    }
+    // experts with >= 8 rows: jam's F2 bands (m % 16 == 0: no float-dot tail rows)
+    if (mma_path(wt, k, wv) && m % 32 == 0) {
+        GemmAct G;
+        if ((e = ctx->gact.ensure(gemm_act_bytes_np(wt, cap64 * 64, k))) != hipSuccess)
+            return hip_fail(ctx, e, "grouped: gemm activation scratch alloc");
+        if ((e = launch_gemm_prep_grouped(wt, a, lda, k, g, cap64, ctx->gact.p, &G, ctx->stream)) != hipSuccess ||
+            (e = launch_gemm_mma_grouped(wt, wv, G, k, g, cap64, c, ldc, ctx->stream)) != hipSuccess)
+            return hip_fail(ctx, e, "grouped: gemm launch");
+    } else {
+        ActQ A;
+        if ((e = actq(&A)) != hipSuccess) return hip_fail(ctx, e, "grouped: activation scratch alloc");
+        if ((e = launch_quant_f2(a, lda, rows_cap, k, (int8_t*) A.q, (float*) A.d, (float*) A.s, ctx->stream)) !=
+                hipSuccess ||
+            (e = launch_gemv_grouped(wt, 2, wv, A, nullptr, 0, k, g, E, cap8, c, ldc, ctx->stream)) != hipSuccess)
+            return hip_fail(ctx, e, "grouped: band launch");
+    }
+    return JAMHIP_OK;
+}
+
+jamhip_status jamhip_moe_route(jamhip_ctx* ctx, const void* route_expert_dev, int seq, int topk, int n_experts,
+                               void* counts_dev, void* offsets_dev, void* slot_route_dev, void* route_slot_dev) {
+    if (!ctx) return JAMHIP_EINVAL;
+    if (!route_expert_dev || !counts_dev || !offsets_dev || !slot_route_dev || !route_slot_dev)
+        return fail(ctx, JAMHIP_EINVAL, "route: null pointer");
+    if (seq <= 0 || topk <= 0 || n_experts <= 0) return fail(ctx, JAMHIP_EINVAL, "route: bad shape");
+    if (n_experts > 1024) return fail(ctx, JAMHIP_EUNSUPPORTED, "route: at most 1024 experts");
+    if ((int64_t) seq * topk > INT32_MAX) return fail(ctx, JAMHIP_EUNSUPPORTED, "route: too many routes");
+    Busy guard(ctx);
+    if (!guard.ok) return fail(ctx, JAMHIP_EBUSY, "context busy");
+    (void) hipSetDevice(ctx->device);
+    const hipError_t e = launch_moe_route((const int*) route_expert_dev, seq * topk, n_experts, (int*) counts_dev,
+                                          (int*) offsets_dev, (int*) slot_route_dev, (int*) route_slot_dev, ctx->stream);
+    return e == hipSuccess ? JAMHIP_OK : hip_fail(ctx, e, "route launch");
+}
+
+jamhip_status jamhip_moe_gather(jamhip_ctx* ctx, const void* x_dev, int ldx, const void* slot_route_dev,
+                                const void* offsets_dev, int n_experts, int seq, int topk, int dim, void* g_dev,
+                                int ldg) {
+    if (!ctx) return JAMHIP_EINVAL;
+    if (!x_dev || !slot_route_dev || !offsets_dev || !g_dev) return fail(ctx, JAMHIP_EINVAL, "gather: null pointer");
+    if (seq <= 0 || topk <= 0 || dim <= 0 || n_experts <= 0 || ldx < dim || ldg < dim)
+        return fail(ctx, JAMHIP_EINVAL, "gather: bad shape");
+    Busy guard(ctx);
+    if (!guard.ok) return fail(ctx, JAMHIP_EBUSY, "context busy");
+    (void) hipSetDevice(ctx->device);
+    const hipError_t e = launch_moe_gather((const float*) x_dev, ldx, (const int*) slot_route_dev,
+                                           (const int*) offsets_dev, n_experts, seq * topk, topk, dim, (float*) g_dev,
+                                           ldg, ctx->stream);
+    return e == hipSuccess ? JAMHIP_OK : hip_fail(ctx, e, "gather launch");
+}
+
+jamhip_status jamhip_moe_combine(jamhip_ctx* ctx, const void* y_dev, int ldy, const void* route_expert_dev,
+                                 const void* route_prob_dev, const void* route_slot_dev, int seq, int topk,
+                                 int n_experts, int dim, void* out_dev, int ldo) {
+    if (!ctx) return JAMHIP_EINVAL;
+    if (!y_dev || !route_expert_dev || !route_prob_dev || !route_slot_dev || !out_dev)
+        return fail(ctx, JAMHIP_EINVAL, "combine: null pointer");
+    if (seq <= 0 || topk <= 0 || dim <= 0 || n_experts <= 0 || ldy < dim || ldo < dim)
+        return fail(ctx, JAMHIP_EINVAL, "combine: bad shape");
+    if (topk > 16) return fail(ctx, JAMHIP_EUNSUPPORTED, "combine: topk above 16");
+    Busy guard(ctx);
+    if (!guard.ok) return fail(ctx, JAMHIP_EBUSY, "context busy");
+    (void) hipSetDevice(ctx->device);
+    const hipError_t e = launch_moe_combine((const float*) y_dev, ldy, (const int*) route_expert_dev,
+                                            (const float*) route_prob_dev, (const int*) route_slot_dev, seq, topk,
+                                            n_experts, dim, (float*) out_dev, ldo, ctx->stream);
+    return e == hipSuccess ? JAMHIP_OK : hip_fail(ctx, e, "combine launch");
 }
 
 jamhip_status jamhip_ctx_set_stream(jamhip_ctx* ctx, void* stream) {

@@ -18,12 +18,31 @@ hipError_t launch_quant_f2(const float* a, int lda, int n, int k, int8_t* q, flo
 hipError_t launch_repack(int dt, const uint8_t* raw, int64_t raw_stride, int64_t rows, int64_t rb, int64_t G,
                          uint8_t* qs, uint8_t* sc, hipStream_t st);
 
+// Expert grouping of a grouped matmul (moe.hip): CSR row offsets off[E+1] of the experts' rows in A and
+// C, the 8-token tile map (poff8, map8) and the 64-token slot map (poff64, map64) of the experts with at
+// least 8 rows, and the weight rows per expert (expert e = view rows [e·gm, (e+1)·gm)). Device pointers.
+struct Groups {
+    const int* off;
+    const int* poff8;
+    const int* map8;
+    const int* poff64;
+    const int* map64;
+    int gm;
+};
+
 // flavour 1: n in [1, 7], F1 activations; with `a` non-null the kernel quantizes A itself (requires
 // gemv_fusable(n, k)), else it reads A's quantized copy from `A`. flavour 2: any n >= 1, F2
 // activations from `A`, 8 tokens per grid row.
 bool gemv_fusable(int n, int k, const float* a, int lda);   // a, lda: the f32 activations (16-byte aligned rows)
 hipError_t launch_gemv(int dt, int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m,
                        int n, float* c, int ldc, hipStream_t st);
+
+// Grouped forms (one launch for all experts). flavour 1: every expert with 1..7 rows, F1, the kernel
+// quantizing its expert's rows itself when `a` is non-null (then gemv_fusable(7, k, a, lda) must hold),
+// else reading them from A (CSR rows). flavour 2: the 8-token tiles of map8 (experts with >= 8 rows), F2
+// activations from A (CSR rows). m here is the rows per expert (g.gm).
+hipError_t launch_gemv_grouped(int dt, int flavour, const WeightView& w, const ActQ& A, const float* a, int lda,
+                               int k, const Groups& g, int E, int cap8, float* c, int ldc, hipStream_t st);
 
 // Rows [r0, r0 + rows) of an n >= 8 call as jam's bands compute their <16-row tail: an f32 dot of the
 // dequantized weight row with the f32 activations a [n][lda].
@@ -53,8 +72,25 @@ size_t gemm_act_bytes(int dt, int n, int k);
 hipError_t launch_gemm_prep(int dt, const float* a, int lda, int n, int k, void* scratch, GemmAct* out,
                             hipStream_t st);
 // Matrix-core GEMM over GemmAct (f16 MFMA on exact integer operands); hipErrorNotSupported for dtypes it
-// does not cover.
+// does not cover. Grouped form: GemmAct laid out by the 64-token slots of g (launch_gemm_prep_grouped),
+// cap64 slot blocks, m = g.gm rows per expert.
 hipError_t launch_gemm_mma(int dt, const WeightView& w, const GemmAct& A, int k, int m, int n, float* c, int ldc,
                            hipStream_t st);
+hipError_t launch_gemm_mma_grouped(int dt, const WeightView& w, const GemmAct& A, int k, const Groups& g, int cap64,
+                                   float* c, int ldc, hipStream_t st);
+size_t gemm_act_bytes_np(int dt, int NP, int k);
+hipError_t launch_gemm_prep_grouped(int dt, const float* a, int lda, int k, const Groups& g, int cap64,
+                                    void* scratch, GemmAct* out, hipStream_t st);
+
+// MoE bookkeeping (moe.hip)
+hipError_t launch_moe_offsets(const int* counts, int E, int rows_cap, int* off, int* poff64, int* poff8, int* map64,
+                              int cap64, int* map8, int cap8, hipStream_t st);
+hipError_t launch_moe_route(const int* route_expert, int R, int E, int* counts, int* off, int* slot_route,
+                            int* route_slot, hipStream_t st);
+hipError_t launch_moe_gather(const float* x, int ldx, const int* slot_route, const int* off, int E, int R, int topk,
+                             int dim, float* g, int ldg, hipStream_t st);
+hipError_t launch_moe_combine(const float* y, int ldy, const int* route_expert, const float* route_prob,
+                              const int* route_slot, int seq, int topk, int E, int dim, float* out, int ldo,
+                              hipStream_t st);
 
 }  // namespace jamhip

@@ -1,4 +1,4 @@
-// Matrix-core prefill GEMM for the K-quant weights (Q4_K, Q6_K): C[n][m] = W[m][k] · A[n][k]^T with jam's
+// Matrix-core prefill GEMM for Q4_K, Q6_K and MXFP4 weights: C[n][m] = W[m][k] · A[n][k]^T with jam's
 // F2 semantics (the n >= 8 bands of jam_kernels_q4k_avx512.c), activations from launch_gemm_prep.
 //
 // Arithmetic. Each 32-element block's integer dot runs on v_mfma_f32_32x32x16_f16 with integer operands
@@ -80,14 +80,39 @@ JAMHIP_DEV void q4k_scmn(const uint4 h, int s, int& sc, int& mn) {
 
 JAMHIP_DEV float h2f_bits(uint32_t b) { return (float) __builtin_bit_cast(_Float16, (uint16_t) (b & 0xffffu)); }
 
+// MXFP4: f16 pair (2^d, 2^d) for d = e_block − e_ref <= 0 (exact down to 2^-24, 0 below).
+JAMHIP_DEV uint32_t mx_scale2(int d) {
+    const uint32_t b = d >= -14 ? (uint32_t) (d + 15) << 10 : d >= -24 ? 1u << (d + 24) : 0u;
+    return b | (b << 16);
+}
+
+// MXFP4: 8 f16 of one K-step from two words of a block's nibble bytes; lane half q takes the low (q = 0,
+// elements 0-15) or high (elements 16-31) nibbles. The e2m1 value x2 (jam_mxfp4.h:14-15: 0,1,2,3,4,6,8,12,
+// sign in bit 3) is looked up as its f16 high byte with v_perm, the sign bit moved in, then scaled by s2.
+JAMHIP_DEV uint32_t mx_pair(uint32_t x, uint32_t hb, uint32_t sel, uint32_t sgnmask, int sgnshift, uint32_t s2) {
+    const uint32_t v = __builtin_amdgcn_perm(hb, 0u, sel) | ((x & sgnmask) << sgnshift);
+    const half2v r = __builtin_bit_cast(half2v, v) * __builtin_bit_cast(half2v, s2);
+    return __builtin_bit_cast(uint32_t, r);
+}
+JAMHIP_DEV half8 mx_frag(uint32_t w0, uint32_t w1, int q, uint32_t s2) {
+    const uint32_t x0 = (q ? w0 >> 4 : w0) & 0x0F0F0F0Fu, x1 = (q ? w1 >> 4 : w1) & 0x0F0F0F0Fu;
+    const uint32_t h0 = __builtin_amdgcn_perm(0x4A484644u, 0x42403C00u, x0 & 0x07070707u);
+    const uint32_t h1 = __builtin_amdgcn_perm(0x4A484644u, 0x42403C00u, x1 & 0x07070707u);
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    return __builtin_bit_cast(half8, u32x4{mx_pair(x0, h0, 0x060C040Cu, 0x00080008u, 12, s2),
+                                           mx_pair(x0, h0, 0x070C050Cu, 0x08000800u, 4, s2),
+                                           mx_pair(x1, h1, 0x060C040Cu, 0x00080008u, 12, s2),
+                                           mx_pair(x1, h1, 0x070C050Cu, 0x08000800u, 4, s2)});
+}
+
 // ------------------------------------------------------------------------------------ stage layout
 // Per stage buffer (bytes): A chunks [TW][NCS][32][16], header [TW][32][HB], codes [8][BN][32],
 // block scales [4][BN] f32, sums hi/lo [BN][SW] f16 each.
 template <int DT, int RT, int CT> struct Stage {
     static constexpr int TW = 4 * RT, BN = 32 * CT;
-    static constexpr int NCS = DT == Q4_K ? 4 : 7;           // chunks per stage (Q6_K: 4 ql, 2 qh, scales)
-    static constexpr int HB = DT == Q4_K ? 16 : 2;           // header bytes per row (Q6_K: d)
-    static constexpr int SW = DT == Q4_K ? 8 : 16;           // sums per token per super-block
+    static constexpr int NCS = DT == Q6_K ? 7 : 4;           // chunks per stage (Q6_K: 4 ql, 2 qh, scales)
+    static constexpr int HB = DT == Q6_K ? 2 : 16;           // header bytes per row (Q6_K: d)
+    static constexpr int SW = DT == Q4_K ? 8 : DT == Q6_K ? 16 : 0;   // sums per token per group
     static constexpr int A_OFF = 0;
     static constexpr int H_OFF = A_OFF + TW * NCS * 512;
     static constexpr int B_OFF = (H_OFF + TW * 32 * HB + 1023) / 1024 * 1024;
@@ -100,7 +125,7 @@ template <int DT, int RT, int CT> struct Stage {
 template <int DT, int RT, int CT>
 __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, GemmAct A, int m, int n,
                                                                  float* __restrict__ c, int ldc, int nrb, int ncb,
-                                                                 int64_t tiles) {
+                                                                 int64_t tiles, Groups gp) {
     using S = Stage<DT, RT, CT>;
     constexpr int TW = S::TW, BN = S::BN, NCS = S::NCS;
     extern __shared__ __align__(1024) unsigned char smem[];
@@ -112,12 +137,23 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
     if (lin >= total) return;
     const int rb = lin / ncb, cb = lin % ncb;
     const int64_t T0 = (int64_t) rb * TW;        // first row tile of the workgroup
-    const int n0 = cb * BN;
+    const int n0 = cb * BN;                      // first token slot of GemmAct
 
     const int lane = threadIdx.x & 63, r = lane & 31, q = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int G = (int) w.G, nsb = A.Kp / 256, nst = 2 * nsb;
-    const int64_t r0t = w.r0 >> 5;               // the view's first row is tile-aligned (launcher checks)
+    int64_t r0t = w.r0 >> 5;                     // the view's first row is tile-aligned (launcher checks)
+    int slot0 = 0, crow0 = 0, nvalid = n;        // token slot -> C row: crow0 + (slot - slot0), < nvalid
+    if (gp.map64 != nullptr) {                   // grouped: this slot block's expert
+        const int e = __builtin_amdgcn_readfirstlane(gp.map64[cb]);
+        if (e < 0) return;                       // whole workgroup, before any barrier
+        r0t = (w.r0 + (int64_t) e * gp.gm) >> 5;
+        tiles = gp.gm / 32;
+        m = gp.gm;
+        slot0 = __builtin_amdgcn_readfirstlane(gp.poff64[e]);
+        crow0 = __builtin_amdgcn_readfirstlane(gp.off[e]);
+        nvalid = __builtin_amdgcn_readfirstlane(gp.off[e + 1]) - crow0;
+    }
 
     // ---- global -> LDS copy of one stage (every wave takes every 4th 1 KB piece)
     auto issue = [&](int st, unsigned char* buf) {
@@ -131,7 +167,7 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
             T = T < tiles ? T : tiles - 1;
             const uint8_t* gbase = w.qs + ((r0t + T) * G + g) * (NC * CHUNK_STRIDE);
             unsigned char* lbase = buf + S::A_OFF + tt * NCS * 512;
-            if constexpr (DT == Q4_K) {
+            if constexpr (DT != Q6_K) {   // Q4_K chunks 4h2..4h2+3 (sub-block pairs), MXFP4 blocks 4h2..4h2+3
 #pragma unroll
                 for (int p = 0; p < 2; p++)
                     if (mine()) dma16(gbase + (4 * h2 + 2 * p) * CHUNK_STRIDE + 16 * lane, lbase + 2 * p * 512);
@@ -144,8 +180,8 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
                 if (mine() && lane < 32) dma16(gbase + 12 * CHUNK_STRIDE + 16 * lane, lbase + 6 * 512);
             }
         }
-        // headers: Q4_K 16 B per row (2 tiles per piece); Q6_K d (2 B per row, 16 tiles per piece)
-        if constexpr (DT == Q4_K) {
+        // headers: Q4_K / MXFP4 16 B per row (2 tiles per piece); Q6_K d (2 B per row, 16 tiles per piece)
+        if constexpr (DT != Q6_K) {
             for (int tp = 0; tp < TW / 2; tp++) {
                 if (!mine()) continue;
                 int64_t T = T0 + 2 * tp + q;
@@ -173,7 +209,7 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
             dma16(A.dx + (int64_t) (8 * g + 4 * h2 + blk) * A.NP + n0 + tok, buf + S::DX_OFF + p * 1024);
         }
         // sums: Q4_K needs them at the super-block's end (odd stage), Q6_K at its start (even stage)
-        if ((DT == Q4_K) == (h2 == 1)) {
+        if (S::SW > 0 && (DT == Q4_K) == (h2 == 1)) {
             constexpr int SWB = S::SW * 2;   // bytes per token per plane
             for (int pl = 0; pl < 2; pl++) {
                 const _Float16* src = (pl ? A.slo : A.shi) + ((int64_t) g * A.NP + n0) * S::SW;
@@ -292,6 +328,62 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
                     }
                 }
             }
+        } else if constexpr (DT == MXFP4) {   // group of 8 blocks; stage h2 = blocks 4h2..4h2+3
+            if (h2 == 0) {
+#pragma unroll
+                for (int i = 0; i < RT; i++)
+#pragma unroll
+                    for (int j = 0; j < CT; j++) accs[i][j] = floatx16{};
+            }
+            uint4 hdr[RT];
+#pragma unroll
+            for (int i = 0; i < RT; i++)
+                hdr[i] = *reinterpret_cast<const uint4*>(buf + S::H_OFF + ((wave * RT + i) * 32 + r) * 16);
+#pragma unroll
+            for (int bl = 0; bl < 4; bl++) {
+                half8 af[RT][2];
+#pragma unroll
+                for (int i = 0; i < RT; i++) {
+                    const uint4 ch = *reinterpret_cast<const uint4*>(LA + ((wave * RT + i) * NCS + bl) * 512 + 16 * r);
+                    const int b = 4 * h2 + bl;
+                    const int eb = (int) (((b < 4 ? hdr[i].x : hdr[i].y) >> (8 * (b & 3))) & 0xffu);
+                    const int er = (int) (hdr[i].z & 0xffu);
+                    const uint32_t s2 = mx_scale2(eb - er);
+                    af[i][0] = mx_frag(ch.x, ch.y, q, s2);
+                    af[i][1] = mx_frag(ch.z, ch.w, q, s2);
+                }
+                half8 bf[CT][2];
+                float dxv[CT];
+#pragma unroll
+                for (int j = 0; j < CT; j++) {
+#pragma unroll
+                    for (int ks = 0; ks < 2; ks++)
+                        bf[j][ks] = *reinterpret_cast<const half8*>(LB + ((2 * bl + ks) * BN + 32 * j + r) * 32 + 16 * q);
+                    dxv[j] = LDX[bl * BN + 32 * j + r];
+                }
+#pragma unroll
+                for (int i = 0; i < RT; i++)
+#pragma unroll
+                    for (int j = 0; j < CT; j++) {
+                        floatx16 D = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i][0], bf[j][0], floatx16{}, 0, 0, 0);
+                        D = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i][1], bf[j][1], D, 0, 0, 0);
+#pragma unroll
+                        for (int e = 0; e < 16; e++) accs[i][j][e] = fmaf(D[e], dxv[j], accs[i][j][e]);
+                    }
+            }
+            if (h2 == 1) {   // group end: acc += 2^(e_ref - 128) · accs
+#pragma unroll
+                for (int i = 0; i < RT; i++) {
+                    const unsigned char* H = buf + S::H_OFF + (wave * RT + i) * 32 * 16;
+                    float sg[16];
+#pragma unroll
+                    for (int e = 0; e < 16; e++) sg[e] = e8m0_half(H[(8 * (e >> 2) + 4 * q + (e & 3)) * 16 + 8]);
+#pragma unroll
+                    for (int j = 0; j < CT; j++)
+#pragma unroll
+                        for (int e = 0; e < 16; e++) acc[i][j][e] = fmaf(sg[e], accs[i][j][e], acc[i][j][e]);
+                }
+            }
         } else {   // Q6_K: stage h2 = half h of the super-block, blocks j = 0..3 (elements 128h + 32j + l)
             const int8_t* scb = reinterpret_cast<const int8_t*>(LA);   // + tile offset below
             if (h2 == 0) {
@@ -392,10 +484,10 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
     // epilogue: lane holds token n0 + 32j + r, rows 8·(e/4) + 4q + e%4 of each tile; scale back by 2^e_t
 #pragma unroll
     for (int j = 0; j < CT; j++) {
-        const int t = n0 + 32 * j + r;
-        if (t >= n) continue;
+        const int t = n0 + 32 * j + r, tl = t - slot0;
+        if (tl >= nvalid) continue;
         const float sc = A.es[t];
-        float* ct = c + (int64_t) t * ldc;
+        float* ct = c + (int64_t) (crow0 + tl) * ldc;
 #pragma unroll
         for (int i = 0; i < RT; i++) {
             const int64_t rowb = (T0 + wave * RT + i) * 32 + 4 * q;
@@ -409,7 +501,8 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
 }
 
 template <int DT, int RT, int CT>
-static hipError_t kq_go(const WeightView& w, const GemmAct& A, int m, int n, float* c, int ldc, hipStream_t st) {
+static hipError_t kq_go(const WeightView& w, const GemmAct& A, int m, int n, float* c, int ldc, hipStream_t st,
+                        const Groups& gp = Groups{}) {
     using S = Stage<DT, RT, CT>;
     const int nrb = (m + 32 * S::TW - 1) / (32 * S::TW), ncb = A.NP / S::BN;
     const int64_t tiles = (w.r0 + tiled_rows(m)) / 32 - w.r0 / 32;   // tiles of the view that exist
@@ -422,16 +515,29 @@ static hipError_t kq_go(const WeightView& w, const GemmAct& A, int m, int n, flo
         if (e != hipSuccess) return e;
         attr = true;
     }
-    kq_gemm_kernel<DT, RT, CT><<<grid, MMA_THREADS, lds, st>>>(w, A, m, n, c, ldc, nrb, ncb, tiles);
+    kq_gemm_kernel<DT, RT, CT><<<grid, MMA_THREADS, lds, st>>>(w, A, m, n, c, ldc, nrb, ncb, tiles, gp);
     return hipGetLastError();
 }
 
 hipError_t launch_gemm_mma(int dt, const WeightView& w, const GemmAct& A, int k, int m, int n, float* c, int ldc,
                            hipStream_t st) {
-    if (k % 256 || (w.r0 & 31) || A.NP % 64) return hipErrorNotSupported;
+    if ((dt != MXFP4 && k % 256) || (w.r0 & 31) || A.NP % 64) return hipErrorNotSupported;
     switch (dt) {
     case Q4_K: return kq_go<Q4_K, 1, 2>(w, A, m, n, c, ldc, st);
     case Q6_K: return kq_go<Q6_K, 1, 2>(w, A, m, n, c, ldc, st);
+    case MXFP4: return kq_go<MXFP4, 1, 2>(w, A, m, n, c, ldc, st);
+    default: return hipErrorNotSupported;
+    }
+}
+
+hipError_t launch_gemm_mma_grouped(int dt, const WeightView& w, const GemmAct& A, int k, const Groups& g, int cap64,
+                                   float* c, int ldc, hipStream_t st) {
+    if ((dt != MXFP4 && k % 256) || (w.r0 & 31) || (g.gm & 31) || A.NP != cap64 * 64) return hipErrorNotSupported;
+    if (cap64 <= 0) return hipSuccess;
+    switch (dt) {
+    case Q4_K: return kq_go<Q4_K, 1, 2>(w, A, g.gm, A.NP, c, ldc, st, g);
+    case Q6_K: return kq_go<Q6_K, 1, 2>(w, A, g.gm, A.NP, c, ldc, st, g);
+    case MXFP4: return kq_go<MXFP4, 1, 2>(w, A, g.gm, A.NP, c, ldc, st, g);
     default: return hipErrorNotSupported;
     }
 }

@@ -1,0 +1,195 @@
+// Device side of jinfer's CSR-grouped MoE dispatch (jinfer/jinfer-kernels/.../Moe.java:178-232) and the
+// bookkeeping of the grouped matmul: per-expert counts -> CSR offsets (device prefix sum), the route ->
+// slot assignment in dispatch's order, the row gather, and the prob-weighted combine in dispatch's
+// expert order. Everything is deterministic: no atomics, every sum in a fixed order.
+#include "common.h"
+#include "launch.h"
+
+namespace jamhip {
+
+constexpr int MOE_THREADS = 1024;
+
+// Exclusive scan of v over the workgroup's threads (v of thread i at position i), Hillis-Steele in LDS.
+JAMHIP_DEV int block_exclusive_scan(int v, int* tmp) {
+    const int t = threadIdx.x;
+    tmp[t] = v;
+    __syncthreads();
+    for (int o = 1; o < MOE_THREADS; o <<= 1) {
+        const int x = t >= o ? tmp[t - o] : 0;
+        __syncthreads();
+        tmp[t] += x;
+        __syncthreads();
+    }
+    const int incl = tmp[t];
+    __syncthreads();
+    return incl - v;
+}
+
+// counts[E] (device, clamped to >= 0 and so that the total stays within rows_cap) -> off[E+1] (CSR row
+// offsets), and for the experts with at least 8 rows (jam's band threshold, jam_kquant.h:23) the token
+// slots of the matrix-core activation layout (poff64: each expert padded to 64 slots) and of the 8-token
+// decode tiles (poff8), with the tile -> expert maps map64[cap64] / map8[cap8] (-1 = no expert).
+__global__ void __launch_bounds__(MOE_THREADS) moe_offsets_kernel(const int* __restrict__ counts, int E, int rows_cap,
+                                                                 int* __restrict__ off, int* __restrict__ poff64,
+                                                                 int* __restrict__ poff8, int* __restrict__ map64,
+                                                                 int cap64, int* __restrict__ map8, int cap8) {
+    __shared__ int tmp[MOE_THREADS];
+    const int e = threadIdx.x;
+    const int c0 = e < E ? max(counts[e], 0) : 0;
+    const int o = block_exclusive_scan(c0, tmp);
+    const int c = e < E ? max(0, min(c0, rows_cap - o)) : 0;   // rows past rows_cap are dropped
+    const int oc = block_exclusive_scan(c, tmp);
+    const int big = c >= 8;
+    const int p64 = block_exclusive_scan(big ? (c + 63) / 64 * 64 : 0, tmp);
+    const int p8 = block_exclusive_scan(big ? (c + 7) / 8 * 8 : 0, tmp);
+    for (int i = e; i < cap64; i += MOE_THREADS) map64[i] = -1;
+    for (int i = e; i < cap8; i += MOE_THREADS) map8[i] = -1;
+    __syncthreads();
+    if (e < E) {
+        off[e] = oc;
+        poff64[e] = p64;
+        poff8[e] = p8;
+        if (big) {
+            for (int t = p64 / 64; t < (p64 + (c + 63) / 64 * 64) / 64 && t < cap64; t++) map64[t] = e;
+            for (int t = p8 / 8; t < (p8 + (c + 7) / 8 * 8) / 8 && t < cap8; t++) map8[t] = e;
+        }
+        if (e == E - 1) {
+            off[E] = oc + c;
+            poff64[E] = p64 + (big ? (c + 63) / 64 * 64 : 0);
+            poff8[E] = p8 + (big ? (c + 7) / 8 * 8 : 0);
+        }
+    }
+}
+
+// Moe.dispatch's CSR build (Moe.java:188-206): counts per expert, off = exclusive prefix sum, then the
+// routes in (s, k) order each take the next slot of their expert: slot_route[slot] = route index s·topk+k,
+// route_slot[route] = slot. One workgroup; routes are taken in chunks of 1024 and each expert's slots are
+// handed out by an in-order scan of "route r is expert e" flags, so the order is exactly the cursor loop's.
+// Routes naming an expert outside [0, E) take no slot (route_slot = -1).
+__global__ void __launch_bounds__(MOE_THREADS) moe_route_kernel(const int* __restrict__ route_expert, int R, int E,
+                                                               int* __restrict__ counts, int* __restrict__ off,
+                                                               int* __restrict__ slot_route, int* __restrict__ route_slot) {
+    __shared__ int tmp[MOE_THREADS];
+    __shared__ int cnt[MOE_THREADS];
+    __shared__ int cur[MOE_THREADS];
+    const int t = threadIdx.x;
+    if (t < E) cnt[t] = 0;
+    __syncthreads();
+    // counts: expert e's thread walks the routes (R = seq x topk is small)
+    if (t < E) {
+        int c = 0;
+        for (int r = 0; r < R; r++) c += route_expert[r] == t;
+        cnt[t] = c;
+    }
+    __syncthreads();
+    const int c = t < E ? cnt[t] : 0;
+    const int o = block_exclusive_scan(c, tmp);
+    if (t < E) {
+        counts[t] = c;
+        off[t] = o;
+        cur[t] = o;
+        if (t == E - 1) off[E] = o + c;
+    }
+    __syncthreads();
+    for (int base = 0; base < R; base += MOE_THREADS) {
+        const int r = base + t;
+        const int e = r < R ? route_expert[r] : -1;
+        const bool ok = e >= 0 && e < E;
+        // rank of route r among the chunk's earlier routes with the same expert
+        int rank = 0;
+        for (int j = base; j < r; j++) rank += route_expert[j] == e;
+        if (r < R) {
+            const int slot = ok ? cur[e] + rank : -1;
+            route_slot[r] = slot;
+            if (ok) slot_route[slot] = r;
+        }
+        __syncthreads();
+        // advance each expert's cursor by its routes in this chunk
+        if (t < E) {
+            int k = 0;
+            for (int j = base; j < min(base + MOE_THREADS, R); j++) k += route_expert[j] == t;
+            cur[t] += k;
+        }
+        __syncthreads();
+    }
+}
+
+// Moe.dispatch's gather (Moe.java:214-222): g[slot] = x[slot_route[slot] / topk] (dim floats per row).
+// Slots past off[E] (routes with an expert id outside [0, E) leave them unassigned) are not written.
+__global__ void __launch_bounds__(256) moe_gather_kernel(const float* __restrict__ x, int ldx,
+                                                        const int* __restrict__ slot_route,
+                                                        const int* __restrict__ off, int E, int topk, int dim,
+                                                        float* __restrict__ g, int ldg) {
+    const int slot = blockIdx.x;
+    if (slot >= off[E]) return;
+    const int s = slot_route[slot] / topk;
+    for (int i = threadIdx.x; i < dim; i += 256) g[(int64_t) slot * ldg + i] = x[(int64_t) s * ldx + i];
+}
+
+// Moe.dispatch's weighted scatter-add (Moe.java:208, 223-231): out is zero-filled, then every expert in
+// ascending order adds prob·y to its rows with one fused multiply-add (Ops.saxpyInPlace's fma,
+// Ops.java:688-725). Here each output row sums its own routes, sorted by (expert, k) — the order in
+// which the expert loop reaches them — so the result is bit-identical and needs no atomics.
+__global__ void __launch_bounds__(256) moe_combine_kernel(const float* __restrict__ y, int ldy,
+                                                         const int* __restrict__ route_expert,
+                                                         const float* __restrict__ route_prob,
+                                                         const int* __restrict__ route_slot, int seq, int topk,
+                                                         int E, int dim, float* __restrict__ out, int ldo) {
+    const int s = blockIdx.x;
+    if (s >= seq) return;
+    int ord[16];
+    const int kk = topk < 16 ? topk : 16;
+    for (int k = 0; k < kk; k++) ord[k] = k;
+    for (int a = 1; a < kk; a++) {   // insertion sort by (expert, k): stable
+        const int v = ord[a];
+        const int ev = route_expert[s * topk + v];
+        int b = a - 1;
+        while (b >= 0 && route_expert[s * topk + ord[b]] > ev) {
+            ord[b + 1] = ord[b];
+            b--;
+        }
+        ord[b + 1] = v;
+    }
+    for (int i = threadIdx.x; i < dim; i += 256) {
+        float acc = 0.0f;
+        for (int j = 0; j < kk; j++) {
+            const int r = s * topk + ord[j];
+            const int e = route_expert[r], slot = route_slot[r];
+            if (e < 0 || e >= E || slot < 0) continue;
+            acc = fmaf(route_prob[r], y[(int64_t) slot * ldy + i], acc);
+        }
+        out[(int64_t) s * ldo + i] = acc;
+    }
+}
+
+hipError_t launch_moe_offsets(const int* counts, int E, int rows_cap, int* off, int* poff64, int* poff8, int* map64,
+                              int cap64, int* map8, int cap8, hipStream_t st) {
+    if (E < 1 || E > MOE_THREADS) return hipErrorNotSupported;
+    moe_offsets_kernel<<<1, MOE_THREADS, 0, st>>>(counts, E, rows_cap, off, poff64, poff8, map64, cap64, map8, cap8);
+    return hipGetLastError();
+}
+
+hipError_t launch_moe_route(const int* route_expert, int R, int E, int* counts, int* off, int* slot_route,
+                            int* route_slot, hipStream_t st) {
+    if (E < 1 || E > MOE_THREADS) return hipErrorNotSupported;
+    moe_route_kernel<<<1, MOE_THREADS, 0, st>>>(route_expert, R, E, counts, off, slot_route, route_slot);
+    return hipGetLastError();
+}
+
+hipError_t launch_moe_gather(const float* x, int ldx, const int* slot_route, const int* off, int E, int R, int topk,
+                             int dim, float* g, int ldg, hipStream_t st) {
+    if (R <= 0) return hipSuccess;
+    moe_gather_kernel<<<R, 256, 0, st>>>(x, ldx, slot_route, off, E, topk, dim, g, ldg);
+    return hipGetLastError();
+}
+
+hipError_t launch_moe_combine(const float* y, int ldy, const int* route_expert, const float* route_prob,
+                              const int* route_slot, int seq, int topk, int E, int dim, float* out, int ldo,
+                              hipStream_t st) {
+    if (topk > 16) return hipErrorNotSupported;
+    if (seq <= 0) return hipSuccess;
+    moe_combine_kernel<<<seq, 256, 0, st>>>(y, ldy, route_expert, route_prob, route_slot, seq, topk, E, dim, out, ldo);
+    return hipGetLastError();
+}
+
+}  // namespace jamhip

@@ -92,6 +92,12 @@ __global__ void __launch_bounds__(256) repack_kernel(const uint8_t* __restrict__
                 for (int t = 0; t < 16; t++) chunk(j)[t] = q[t];
             }
         }
+        if constexpr (DT == MXFP4) {                   // byte 8: the group's largest exponent; 9..15 zero
+            uint8_t mx = 0;
+            for (int j = 0; j < BPG; j++) mx = ds[j] > mx ? ds[j] : mx;
+            ds[8] = mx;
+            for (int t = 9; t < 16; t++) ds[t] = 0;
+        }
     }
 }
 
@@ -105,19 +111,32 @@ int gemm_sums_kind(int dt) { return dt == Q4_K || dt == Q4_0 ? 1 : dt == Q6_K ? 
 // One workgroup per (padded) token: jam's F2 quantization of every 32-element block (f2_lane, bit-exact),
 // the codes scattered into the fragment order of GemmAct::b, then the token's power-of-two scale and the
 // scaled block scales and sums. SK: 0 no sums, 1 per-32 sums xs0 + xs1 (jam's fl(xs0 + xs1)), 2 per-16.
+// Grouped form (gmap non-null): slot t belongs to expert gmap[t / 64] (-1: padding) and holds that
+// expert's row t - gpoff[e] (CSR row goff[e] + t - gpoff[e]) while that is below its row count.
 template <int SK>
 __global__ void __launch_bounds__(256) gemm_prep_kernel(const float* __restrict__ a, int lda, int n, int k, int Kp,
                                                         int NP, _Float16* __restrict__ bq, float* __restrict__ dx,
                                                         _Float16* __restrict__ shi, _Float16* __restrict__ slo,
-                                                        float* __restrict__ es) {
+                                                        float* __restrict__ es, const int* __restrict__ gmap,
+                                                        const int* __restrict__ goff, const int* __restrict__ gpoff) {
     extern __shared__ float psm[];   // block scales [Kp/32], per-16 sums [Kp/16]
     __shared__ float red[4];
     const int t = blockIdx.x, nbp = Kp >> 5, nbk = k >> 5, e = threadIdx.x & 31;
     float* sdb = psm;
     float* sxs = psm + nbp;
-    const bool live = t < n;
+    int src = t;
+    bool live = t < n;
+    if (gmap != nullptr) {
+        const int ex = gmap[t >> 6];
+        live = false;
+        if (ex >= 0) {
+            const int l = t - gpoff[ex];
+            live = l < goff[ex + 1] - goff[ex];
+            src = goff[ex] + l;
+        }
+    }
     for (int b = threadIdx.x >> 5; b < nbp; b += 8) {   // b is uniform in each 32-lane group
-        const float x = live && b < nbk ? a[(int64_t) t * lda + 32 * b + e] : 0.0f;
+        const float x = live && b < nbk ? a[(int64_t) src * lda + 32 * b + e] : 0.0f;
         float db, xs16;
         const int v = f2_lane(x, db, xs16);
         const int q = e >> 4, ks = (e >> 3) & 1;
@@ -166,15 +185,16 @@ __global__ void __launch_bounds__(256) gemm_prep_kernel(const float* __restrict_
 
 static int64_t a256(int64_t v) { return (v + 255) & ~(int64_t) 255; }
 
-size_t gemm_act_bytes(int dt, int n, int k) {
-    const int64_t NP = (n + 63) / 64 * 64, Kp = (k + 255) / 256 * 256, sk = gemm_sums_kind(dt);
+size_t gemm_act_bytes_np(int dt, int NP, int k) {
+    const int64_t Kp = (k + 255) / 256 * 256, sk = gemm_sums_kind(dt);
     const int64_t sb = sk == 0 ? 0 : a256((Kp / 256) * NP * (sk == 1 ? 8 : 16) * 2);
-    return (size_t) (a256(Kp * NP * 2) + a256((Kp / 32) * NP * 4) + 2 * sb + a256(NP * 4));
+    return (size_t) (a256(Kp * NP * 2) + a256((Kp / 32) * NP * 4) + 2 * sb + a256((int64_t) NP * 4));
 }
+size_t gemm_act_bytes(int dt, int n, int k) { return gemm_act_bytes_np(dt, (n + 63) / 64 * 64, k); }
 
-hipError_t launch_gemm_prep(int dt, const float* a, int lda, int n, int k, void* scratch, GemmAct* out,
-                            hipStream_t st) {
-    const int NP = (n + 63) / 64 * 64, Kp = (k + 255) / 256 * 256, sk = gemm_sums_kind(dt);
+static hipError_t prep_np(int dt, const float* a, int lda, int n, int NP, int k, void* scratch, GemmAct* out,
+                          const int* gmap, const int* goff, const int* gpoff, hipStream_t st) {
+    const int Kp = (k + 255) / 256 * 256, sk = gemm_sums_kind(dt);
     uint8_t* p = (uint8_t*) scratch;
     _Float16* bq = (_Float16*) p;
     p += a256((int64_t) Kp * NP * 2);
@@ -188,10 +208,24 @@ hipError_t launch_gemm_prep(int dt, const float* a, int lda, int n, int k, void*
     *out = GemmAct{bq, dx, shi, slo, es, NP, Kp};
     const size_t lds = (size_t) (Kp / 32) * 12;
     if (lds > 64 * 1024) return hipErrorNotSupported;
-    if (sk == 1) gemm_prep_kernel<1><<<NP, 256, lds, st>>>(a, lda, n, k, Kp, NP, bq, dx, shi, slo, es);
-    else if (sk == 2) gemm_prep_kernel<2><<<NP, 256, lds, st>>>(a, lda, n, k, Kp, NP, bq, dx, shi, slo, es);
-    else gemm_prep_kernel<0><<<NP, 256, lds, st>>>(a, lda, n, k, Kp, NP, bq, dx, shi, slo, es);
+    if (NP <= 0) return hipSuccess;
+    if (sk == 1)
+        gemm_prep_kernel<1><<<NP, 256, lds, st>>>(a, lda, n, k, Kp, NP, bq, dx, shi, slo, es, gmap, goff, gpoff);
+    else if (sk == 2)
+        gemm_prep_kernel<2><<<NP, 256, lds, st>>>(a, lda, n, k, Kp, NP, bq, dx, shi, slo, es, gmap, goff, gpoff);
+    else
+        gemm_prep_kernel<0><<<NP, 256, lds, st>>>(a, lda, n, k, Kp, NP, bq, dx, shi, slo, es, gmap, goff, gpoff);
     return hipGetLastError();
+}
+
+hipError_t launch_gemm_prep(int dt, const float* a, int lda, int n, int k, void* scratch, GemmAct* out,
+                            hipStream_t st) {
+    return prep_np(dt, a, lda, n, (n + 63) / 64 * 64, k, scratch, out, nullptr, nullptr, nullptr, st);
+}
+
+hipError_t launch_gemm_prep_grouped(int dt, const float* a, int lda, int k, const Groups& g, int cap64,
+                                    void* scratch, GemmAct* out, hipStream_t st) {
+    return prep_np(dt, a, lda, 0, cap64 * 64, k, scratch, out, g.map64, g.off, g.poff64, st);
 }
 
 hipError_t launch_quant_f1(const float* a, int lda, int n, int k, int8_t* q, float* d, float* asum, int* s16,

@@ -172,6 +172,32 @@ class HipJAM:
                         s_dev: int) -> int:
         return lib().jamhip_quantize_device(self._ctx, flavour, a_dev, lda, n, k, q_dev, d_dev, s_dev)
 
+    # -- mixture of experts (device pointers; jamhip.h) -------------------------------------------
+    def mm_grouped(self, w: Segment, wt: int, ldw: int, m: int, n_experts: int, counts_dev: int, a_dev: int,
+                   lda: int, c_dev: int, ldc: int, k: int, rows_cap: int, offsets_dev: int | None = None) -> int:
+        """One jam matmul per expert over CSR-grouped rows (Moe.dispatch's per-expert MatMul.gemm loop)."""
+        _require_native(w, "weight W")
+        return lib().jamhip_mm_grouped(self._ctx, w.address, wt, ldw, m, n_experts, counts_dev, a_dev, JAM.F32, lda,
+                                       c_dev, JAM.F32, ldc, k, rows_cap, offsets_dev)
+
+    def moe_route(self, route_expert_dev: int, seq: int, topk: int, n_experts: int, counts_dev: int,
+                  offsets_dev: int, slot_route_dev: int, route_slot_dev: int) -> int:
+        """Moe.dispatch's CSR build on the device (Moe.java:188-206)."""
+        return lib().jamhip_moe_route(self._ctx, route_expert_dev, seq, topk, n_experts, counts_dev, offsets_dev,
+                                      slot_route_dev, route_slot_dev)
+
+    def moe_gather(self, x_dev: int, ldx: int, slot_route_dev: int, offsets_dev: int, n_experts: int, seq: int,
+                   topk: int, dim: int, g_dev: int, ldg: int) -> int:
+        """Moe.dispatch's gather (Moe.java:214-222)."""
+        return lib().jamhip_moe_gather(self._ctx, x_dev, ldx, slot_route_dev, offsets_dev, n_experts, seq, topk, dim,
+                                       g_dev, ldg)
+
+    def moe_combine(self, y_dev: int, ldy: int, route_expert_dev: int, route_prob_dev: int, route_slot_dev: int,
+                    seq: int, topk: int, n_experts: int, dim: int, out_dev: int, ldo: int) -> int:
+        """Moe.dispatch's prob-weighted scatter-add (Moe.java:208, 223-231), bit-identical order."""
+        return lib().jamhip_moe_combine(self._ctx, y_dev, ldy, route_expert_dev, route_prob_dev, route_slot_dev, seq,
+                                        topk, n_experts, dim, out_dev, ldo)
+
     def set_stream(self, stream: int | None) -> int:
         return lib().jamhip_ctx_set_stream(self._ctx, stream)
 

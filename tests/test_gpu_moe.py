@@ -1,0 +1,166 @@
+"""GPU parity of the MoE entry points (jamhip_moe_route / _gather / _combine / jamhip_mm_grouped) against the
+restatement of jinfer's Moe.dispatch (oracle/moe.py) and per-expert jam matmuls (the int8 oracle).
+
+Routing, gather and combine are bit-exact; the grouped matmul meets the tier-1 bound of the single-matrix
+tests (|gpu - oracle| <= 1e-3*|oracle| + 1e-5*sumAbs) on every expert, whichever path (F1 decode, F2 bands
+on the matrix cores or on the decode kernels) its row count selects.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+from oracle import moe as M
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def routes(seed, seq, topk, E):
+    rng = np.random.default_rng(seed)
+    return np.stack([rng.permutation(E)[:topk] for _ in range(seq)]).astype(np.int32).ravel()
+
+
+def dev(x):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(x)).cuda()
+
+
+def test_route_gather_combine_bit_exact(hip):
+    import torch
+    for seed, seq, topk, E in ((1, 37, 4, 8), (2, 300, 2, 32), (3, 5, 1, 3), (4, 700, 4, 32)):
+        say(f"moe route seq={seq} topk={topk} E={E}")
+        re = routes(seed, seq, topk, E)
+        if seed == 3:
+            re[2] = E + 5                        # an id outside [0, E) takes no slot
+        R = seq * topk
+        counts = torch.zeros(E, dtype=torch.int32, device="cuda")
+        off = torch.zeros(E + 1, dtype=torch.int32, device="cuda")
+        slot_route = torch.full((R,), -1, dtype=torch.int32, device="cuda")
+        route_slot = torch.zeros(R, dtype=torch.int32, device="cuda")
+        re_d = dev(re)
+        assert hip.moe_route(re_d.data_ptr(), seq, topk, E, counts.data_ptr(), off.data_ptr(), slot_route.data_ptr(),
+                             route_slot.data_ptr()) == 0, hip.last_error()
+        hip.synchronize()
+        c_o, off_o, sr_o, rs_o = M.dispatch_csr(re, E)
+        total = int(off_o[-1])
+        assert np.array_equal(counts.cpu().numpy(), c_o)
+        assert np.array_equal(off.cpu().numpy(), off_o)
+        assert np.array_equal(slot_route.cpu().numpy()[:total], sr_o[:total])
+        assert np.array_equal(route_slot.cpu().numpy(), rs_o)
+
+        dim = 96
+        x = np.random.default_rng(seed + 10).standard_normal((seq, dim)).astype(np.float32)
+        g = torch.zeros((R, dim + 3), dtype=torch.float32, device="cuda")
+        assert hip.moe_gather(dev(x).data_ptr(), dim, slot_route.data_ptr(), off.data_ptr(), E, seq, topk, dim,
+                              g.data_ptr(), dim + 3) == 0, hip.last_error()
+        hip.synchronize()
+        assert np.array_equal(g.cpu().numpy()[:total, :dim], M.gather(x, sr_o, total, topk))
+
+        y = np.random.default_rng(seed + 20).standard_normal((R, dim)).astype(np.float32)
+        prob = np.random.default_rng(seed + 30).random(R).astype(np.float32)
+        out = torch.full((seq, dim + 1), 7.0, dtype=torch.float32, device="cuda")
+        assert hip.moe_combine(dev(y).data_ptr(), dim, re_d.data_ptr(), dev(prob).data_ptr(), route_slot.data_ptr(),
+                               seq, topk, E, dim, out.data_ptr(), dim + 1) == 0, hip.last_error()
+        hip.synchronize()
+        want = M.combine(y, re, prob, rs_o, seq, topk, E)
+        got = out.cpu().numpy()
+        assert np.array_equal(got[:, :dim].view(np.uint32), want.view(np.uint32))
+        assert (got[:, dim] == 7.0).all()           # the stride gap is untouched
+
+
+# (dtype, m rows per expert, k): m % 32 == 0 takes the matrix cores for Q4_K / Q6_K / MXFP4 (k % 256 for the
+# K-quants; MXFP4 pads k to 256); m = 48 and Q8_0 / Q4_0 take the decode kernels' F2 tiles.
+GROUPED = [(O.MXFP4, 64, 576), (O.MXFP4, 48, 320), (O.Q4_K, 96, 512), (O.Q6_K, 64, 256), (O.Q8_0, 64, 320),
+           (O.Q4_0, 48, 256)]
+COUNTS = [0, 1, 7, 8, 9, 33, 64, 70, 3]
+
+
+@pytest.mark.parametrize("dt,m,k", GROUPED)
+def test_mm_grouped_parity(hip, oracle, dt, m, k):
+    import torch
+    from qxotic_amd.jam import JAM, Segment
+    E = len(COUNTS)
+    say(f"grouped {O.NAMES[dt]} m={m} k={k} counts={COUNTS}")
+    w_e = [oracle.quantize(dt, oracle.normal(0x5A11C0DE ^ (100 * e + dt), (m, k), 0.0, 0.02)) for e in range(E)]
+    w = np.ascontiguousarray(np.concatenate(w_e, axis=0))
+    total = sum(COUNTS)
+    rows_cap = total + 5
+    a = oracle.outliers(77, (rows_cap, k))
+    assert hip.pin(Segment.of(w), dt, k, E * m) == JAM.OK, hip.last_error()
+    try:
+        a_d = dev(a)
+        c = torch.full((rows_cap, m + 2), -3.0, dtype=torch.float32, device="cuda")
+        cnt = dev(np.array(COUNTS, np.int32))
+        off = torch.zeros(E + 1, dtype=torch.int32, device="cuda")
+        st = hip.mm_grouped(Segment.of(w), dt, k, m, E, cnt.data_ptr(), a_d.data_ptr(), k, c.data_ptr(), m + 2, k,
+                            rows_cap, off.data_ptr())
+        assert st == JAM.OK, hip.last_error()
+        hip.synchronize()
+        got = c.cpu().numpy()
+        assert np.array_equal(off.cpu().numpy(), np.concatenate([[0], np.cumsum(COUNTS)]))
+        ref = M.mm_grouped(oracle, dt, w_e, a, COUNTS, m, k)
+        o = 0
+        for e, n in enumerate(COUNTS):
+            if n:
+                _, sa = oracle.mm_ref(dt, w_e[e], np.ascontiguousarray(a[o:o + n]), m, n, k)
+                r = ref[o:o + n]
+                ok = np.abs(got[o:o + n, :m] - r) <= 1e-3 * np.abs(r) + 1e-5 * sa
+                assert ok.all(), (O.NAMES[dt], e, n, float(np.max(np.abs(got[o:o + n, :m] - r))))
+            o += n
+        assert (got[:, m:] == -3.0).all()           # ldc gap untouched
+        assert (got[total:] == -3.0).all()          # rows past the counts untouched
+        # rerun bit-identity
+        c2 = torch.zeros_like(c)
+        assert hip.mm_grouped(Segment.of(w), dt, k, m, E, cnt.data_ptr(), a_d.data_ptr(), k, c2.data_ptr(), m + 2, k,
+                              rows_cap, None) == JAM.OK
+        hip.synchronize()
+        assert np.array_equal(c2.cpu().numpy()[:total, :m], got[:total, :m])
+    finally:
+        hip.evict(Segment.of(w))
+
+
+def test_mm_grouped_counts_past_rows_cap(hip, oracle):
+    """Counts whose sum exceeds rows_cap: the rows past rows_cap are neither read nor written."""
+    import torch
+    from qxotic_amd.jam import JAM, Segment
+    dt, m, k, E = O.MXFP4, 32, 256, 3
+    w_e = [oracle.quantize(dt, oracle.normal(900 + e, (m, k), 0.0, 0.02)) for e in range(E)]
+    w = np.ascontiguousarray(np.concatenate(w_e, axis=0))
+    counts = [10, 40, 30]
+    rows_cap = 45                                    # expert 1 keeps 35 rows, expert 2 none
+    a = oracle.normal(901, (rows_cap, k))
+    assert hip.pin(Segment.of(w), dt, k, E * m) == JAM.OK
+    try:
+        c = torch.full((rows_cap, m), -3.0, dtype=torch.float32, device="cuda")
+        off = torch.zeros(E + 1, dtype=torch.int32, device="cuda")
+        assert hip.mm_grouped(Segment.of(w), dt, k, m, E, dev(np.array(counts, np.int32)).data_ptr(),
+                              dev(a).data_ptr(), k, c.data_ptr(), m, k, rows_cap, off.data_ptr()) == JAM.OK
+        hip.synchronize()
+        assert off.cpu().numpy().tolist() == [0, 10, 45, 45]
+        ref = M.mm_grouped(oracle, dt, w_e, a, [10, 35, 0], m, k)
+        got = c.cpu().numpy()
+        _, sa = oracle.mm_ref(dt, w_e[1], np.ascontiguousarray(a[10:45]), m, 35, k)
+        assert (np.abs(got[10:45] - ref[10:45]) <= 1e-3 * np.abs(ref[10:45]) + 1e-5 * sa).all()
+    finally:
+        hip.evict(Segment.of(w))
+
+
+def test_grouped_status_codes(hip):
+    import torch
+    from qxotic_amd.jam import JAM, Segment
+    w = np.zeros(17 * 8 * 40, np.uint8)
+    z = torch.zeros(64, dtype=torch.int32, device="cuda")
+    f = torch.zeros((64, 64), dtype=torch.float32, device="cuda")
+    call = lambda **kw: hip.mm_grouped(Segment.of(w), kw.get("dt", JAM.MXFP4), 256, kw.get("m", 32), kw.get("E", 2),
+                                       z.data_ptr(), f.data_ptr(), 256, f.data_ptr(), kw.get("ldc", 32), 256,
+                                       kw.get("cap", 4), None)
+    assert call(m=24) == JAM.EUNSUPPORTED           # m % 16
+    assert call(E=2000) == JAM.EUNSUPPORTED         # more than 1024 experts
+    assert call(ldc=16) == JAM.EINVAL               # ldc < m
+    assert call(cap=-1) == JAM.EINVAL
+    assert call(dt=JAM.F16) == JAM.EUNSUPPORTED
