@@ -38,7 +38,7 @@ typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) void lds_void;
 
-constexpr int MMA_THREADS = 256;
+constexpr int MMA_WAVES = 4, MMA_THREADS = 64 * MMA_WAVES;
 
 JAMHIP_DEV void dma16(const void* g, void* lds_base) {
     // lane l's 16 bytes at g land at lds_base + 16·l (lds_base is wave-uniform)
@@ -109,7 +109,7 @@ JAMHIP_DEV half8 mx_frag(uint32_t w0, uint32_t w1, int q, uint32_t s2) {
 // Per stage buffer (bytes): A chunks [TW][NCS][32][16], header [TW][32][HB], codes [8][BN][32],
 // block scales [4][BN] f32, sums hi/lo [BN][SW] f16 each.
 template <int DT, int RT, int CT> struct Stage {
-    static constexpr int TW = 4 * RT, BN = 32 * CT;
+    static constexpr int TW = MMA_WAVES * RT, BN = 32 * CT;
     static constexpr int NCS = DT == Q6_K ? 7 : 4;           // chunks per stage (Q6_K: 4 ql, 2 qh, scales)
     static constexpr int HB = DT == Q6_K ? 2 : 16;           // header bytes per row (Q6_K: d)
     static constexpr int SW = DT == Q4_K ? 8 : DT == Q6_K ? 16 : 0;   // sums per token per group
@@ -159,7 +159,7 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
     auto issue = [&](int st, unsigned char* buf) {
         const int g = st >> 1, h2 = st & 1;
         int piece = 0;
-        auto mine = [&]() { return (piece++ & 3) == wave; };
+        auto mine = [&]() { return (piece++ % MMA_WAVES) == wave; };
         // weight chunks: tile tt, chunk pair p: 1 KB contiguous
         constexpr int NC = group_chunks(DT);
         for (int tt = 0; tt < TW; tt++) {

@@ -63,52 +63,68 @@ __global__ void __launch_bounds__(MOE_THREADS) moe_offsets_kernel(const int* __r
 
 // Moe.dispatch's CSR build (Moe.java:188-206): counts per expert, off = exclusive prefix sum, then the
 // routes in (s, k) order each take the next slot of their expert: slot_route[slot] = route index s·topk+k,
-// route_slot[route] = slot. One workgroup; routes are taken in chunks of 1024 and each expert's slots are
-// handed out by an in-order scan of "route r is expert e" flags, so the order is exactly the cursor loop's.
-// Routes naming an expert outside [0, E) take no slot (route_slot = -1).
+// route_slot[route] = slot. One workgroup of 16 waves over chunks of 1024 routes. Per chunk and wave, one
+// ballot per expert gives every route its rank among the wave's earlier routes of the same expert
+// (popcount below its lane) and the wave's count; a per-expert prefix over the waves plus the expert's
+// running cursor then give the slot — the reference's cursor order, with no atomics. Two passes: counts,
+// then slots. Routes naming an expert outside [0, E) take no slot (route_slot = -1).
+constexpr int ROUTE_WAVES = MOE_THREADS / 64;
 __global__ void __launch_bounds__(MOE_THREADS) moe_route_kernel(const int* __restrict__ route_expert, int R, int E,
                                                                int* __restrict__ counts, int* __restrict__ off,
                                                                int* __restrict__ slot_route, int* __restrict__ route_slot) {
     __shared__ int tmp[MOE_THREADS];
-    __shared__ int cnt[MOE_THREADS];
-    __shared__ int cur[MOE_THREADS];
-    const int t = threadIdx.x;
-    if (t < E) cnt[t] = 0;
-    __syncthreads();
-    // counts: expert e's thread walks the routes (R = seq x topk is small)
-    if (t < E) {
-        int c = 0;
-        for (int r = 0; r < R; r++) c += route_expert[r] == t;
-        cnt[t] = c;
-    }
-    __syncthreads();
-    const int c = t < E ? cnt[t] : 0;
-    const int o = block_exclusive_scan(c, tmp);
-    if (t < E) {
-        counts[t] = c;
-        off[t] = o;
-        cur[t] = o;
-        if (t == E - 1) off[E] = o + c;
-    }
-    __syncthreads();
-    for (int base = 0; base < R; base += MOE_THREADS) {
+    extern __shared__ int wsm[];   // per-wave counts of the chunk [ROUTE_WAVES][E], then the cursors [E]
+    int* wcnt = wsm;
+    int* curs = wsm + ROUTE_WAVES * E;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const uint64_t below = (1ull << lane) - 1ull;
+    int total = 0;
+    for (int base = 0; base < R; base += MOE_THREADS) {   // pass 1: counts
         const int r = base + t;
         const int e = r < R ? route_expert[r] : -1;
-        const bool ok = e >= 0 && e < E;
-        // rank of route r among the chunk's earlier routes with the same expert
-        int rank = 0;
-        for (int j = base; j < r; j++) rank += route_expert[j] == e;
-        if (r < R) {
-            const int slot = ok ? cur[e] + rank : -1;
-            route_slot[r] = slot;
-            if (ok) slot_route[slot] = r;
+        for (int x = 0; x < E; x++) {
+            const uint64_t m = __ballot(e == x);
+            if (lane == 0) wcnt[wave * E + x] = __popcll(m);
         }
         __syncthreads();
-        // advance each expert's cursor by its routes in this chunk
+        if (t < E)
+            for (int w = 0; w < ROUTE_WAVES; w++) total += wcnt[w * E + t];
+        __syncthreads();
+    }
+    const int o = block_exclusive_scan(t < E ? total : 0, tmp);
+    if (t < E) {
+        counts[t] = total;
+        off[t] = o;
+        curs[t] = o;
+        if (t == E - 1) off[E] = o + total;
+    }
+    __syncthreads();
+    for (int base = 0; base < R; base += MOE_THREADS) {   // pass 2: slots
+        const int r = base + t;
+        const int e = r < R ? route_expert[r] : -1;
+        int rank = 0;
+        for (int x = 0; x < E; x++) {
+            const uint64_t m = __ballot(e == x);
+            if (e == x) rank = __popcll(m & below);
+            if (lane == 0) wcnt[wave * E + x] = __popcll(m);
+        }
+        __syncthreads();
+        if (r < R) {
+            if (e >= 0 && e < E) {
+                int pre = 0;
+                for (int w = 0; w < wave; w++) pre += wcnt[w * E + e];
+                const int slot = curs[e] + pre + rank;
+                slot_route[slot] = r;
+                route_slot[r] = slot;
+            } else {
+                route_slot[r] = -1;
+            }
+        }
+        __syncthreads();
         if (t < E) {
-            int k = 0;
-            for (int j = base; j < min(base + MOE_THREADS, R); j++) k += route_expert[j] == t;
-            cur[t] += k;
+            int cnt = 0;
+            for (int w = 0; w < ROUTE_WAVES; w++) cnt += wcnt[w * E + t];
+            curs[t] += cnt;
         }
         __syncthreads();
     }
@@ -172,7 +188,16 @@ hipError_t launch_moe_offsets(const int* counts, int E, int rows_cap, int* off, 
 hipError_t launch_moe_route(const int* route_expert, int R, int E, int* counts, int* off, int* slot_route,
                             int* route_slot, hipStream_t st) {
     if (E < 1 || E > MOE_THREADS) return hipErrorNotSupported;
-    moe_route_kernel<<<1, MOE_THREADS, 0, st>>>(route_expert, R, E, counts, off, slot_route, route_slot);
+    const size_t lds = (size_t) (ROUTE_WAVES + 1) * E * sizeof(int);
+    static bool attr = false;
+    if (!attr) {
+        const hipError_t e = hipFuncSetAttribute((const void*) moe_route_kernel,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 (ROUTE_WAVES + 1) * MOE_THREADS * (int) sizeof(int));
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
+    moe_route_kernel<<<1, MOE_THREADS, lds, st>>>(route_expert, R, E, counts, off, slot_route, route_slot);
     return hipGetLastError();
 }
 

@@ -108,87 +108,120 @@ JAMHIP_DEV int perm8(int j) { return j == 1 ? 2 : j == 2 ? 1 : j == 5 ? 6 : j ==
 
 int gemm_sums_kind(int dt) { return dt == Q4_K || dt == Q4_0 ? 1 : dt == Q6_K ? 2 : 0; }
 
-// One workgroup per (padded) token: jam's F2 quantization of every 32-element block (f2_lane, bit-exact),
-// the codes scattered into the fragment order of GemmAct::b, then the token's power-of-two scale and the
-// scaled block scales and sums. SK: 0 no sums, 1 per-32 sums xs0 + xs1 (jam's fl(xs0 + xs1)), 2 per-16.
+// Two passes. Pass A, one workgroup per (256-element chunk, token slot): jam's F2 quantization of the
+// chunk's 8 blocks (f2_lane, bit-exact), the codes scattered into the fragment order of GemmAct::b, the
+// block scales and per-16 sums parked block-major in scratch, and the chunk's largest |sum| (SK 1: per-32
+// xs0 + xs1, jam's fl(xs0 + xs1); SK 2: per-16; SK 0: none). Pass B, one thread per (token slot, block):
+// the token's power of two from its chunks' maxima, then the scaled block scale and sums.
 // Grouped form (gmap non-null): slot t belongs to expert gmap[t / 64] (-1: padding) and holds that
 // expert's row t - gpoff[e] (CSR row goff[e] + t - gpoff[e]) while that is below its row count.
+JAMHIP_DEV int prep_src(int t, int n, const int* gmap, const int* goff, const int* gpoff) {
+    if (gmap == nullptr) return t < n ? t : -1;
+    const int ex = gmap[t >> 6];
+    if (ex < 0) return -1;
+    const int l = t - gpoff[ex];
+    return l < goff[ex + 1] - goff[ex] ? goff[ex] + l : -1;
+}
+
+// Pass A: each lane holds 4 consecutive elements of one block (8 lanes per block, a wave = one 256-element
+// chunk, 4 chunks per workgroup). F2 exactly as f2_lane: the block max over the 8 lanes, d = max/127,
+// inv = 127/max, q = sat8(rne(x·inv)) with NaN/overflow -> -128, and the per-16 sums in
+// _mm512_reduce_add_ps's pairing (distance 8, 4, 2, 1): distances 8 and 4 cross lanes (xor 2, xor 1),
+// 2 and 1 stay in the lane.
 template <int SK>
-__global__ void __launch_bounds__(256) gemm_prep_kernel(const float* __restrict__ a, int lda, int n, int k, int Kp,
-                                                        int NP, _Float16* __restrict__ bq, float* __restrict__ dx,
-                                                        _Float16* __restrict__ shi, _Float16* __restrict__ slo,
-                                                        float* __restrict__ es, const int* __restrict__ gmap,
-                                                        const int* __restrict__ goff, const int* __restrict__ gpoff) {
-    extern __shared__ float psm[];   // block scales [Kp/32], per-16 sums [Kp/16]
-    __shared__ float red[4];
-    const int t = blockIdx.x, nbp = Kp >> 5, nbk = k >> 5, e = threadIdx.x & 31;
-    float* sdb = psm;
-    float* sxs = psm + nbp;
-    int src = t;
-    bool live = t < n;
-    if (gmap != nullptr) {
-        const int ex = gmap[t >> 6];
-        live = false;
-        if (ex >= 0) {
-            const int l = t - gpoff[ex];
-            live = l < goff[ex + 1] - goff[ex];
-            src = goff[ex] + l;
+__global__ void __launch_bounds__(256) gemm_prep_a(const float* __restrict__ a, int lda, int n, int k, int Kp, int NP,
+                                                   _Float16* __restrict__ bq, float* __restrict__ tdb,
+                                                   float* __restrict__ txs, float* __restrict__ tmx,
+                                                   const int* __restrict__ gmap, const int* __restrict__ goff,
+                                                   const int* __restrict__ gpoff, int vec) {
+    const int t = blockIdx.y, nbk = k >> 5, lane = threadIdx.x & 63;
+    const int ch = blockIdx.x * 4 + (threadIdx.x >> 6);   // this wave's 256-element chunk
+    if (ch >= (Kp >> 8)) return;                           // whole wave
+    const int src = prep_src(t, n, gmap, goff, gpoff);
+    const int b = 8 * ch + (lane >> 3), j = lane & 7;      // block, lane within the block
+    float x[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (src >= 0 && b < nbk) {
+        const float* p = a + (int64_t) src * lda + 32 * b + 4 * j;
+        if (vec) {   // a and lda 16-byte aligned (the launcher checks)
+            const float4 v = *reinterpret_cast<const float4*>(p);
+            x[0] = v.x, x[1] = v.y, x[2] = v.z, x[3] = v.w;
+        } else {
+            x[0] = p[0], x[1] = p[1], x[2] = p[2], x[3] = p[3];
         }
     }
-    for (int b = threadIdx.x >> 5; b < nbp; b += 8) {   // b is uniform in each 32-lane group
-        const float x = live && b < nbk ? a[(int64_t) src * lda + 32 * b + e] : 0.0f;
-        float db, xs16;
-        const int v = f2_lane(x, db, xs16);
-        const int q = e >> 4, ks = (e >> 3) & 1;
-        bq[((int64_t) (2 * b + ks) * NP + t) * 16 + 8 * q + perm8(e & 7)] = (_Float16) v;
-        if (e == 0) sdb[b] = db;
-        if ((e & 15) == 0) sxs[2 * b + q] = xs16;
-    }
-    __syncthreads();
-    float mx = 0.0f;
-    if constexpr (SK == 1)
-        for (int b = threadIdx.x; b < nbp; b += 256) mx = fmaxf(mx, fabsf(sxs[2 * b] + sxs[2 * b + 1]));
-    if constexpr (SK == 2)
-        for (int i = threadIdx.x; i < 2 * nbp; i += 256) mx = fmaxf(mx, fabsf(sxs[i]));
+    float mx = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
+    mx = fmaxf(mx, __shfl_xor(mx, 4));
+    mx = fmaxf(mx, __shfl_xor(mx, 2));
+    mx = fmaxf(mx, __shfl_xor(mx, 1));
+    const float db = mx / 127.0f;
+    const float inv = mx > 0.0f ? 127.0f / mx : 0.0f;
+    int qv[4];
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    for (int u = 0; u < 4; u++) {
+        const float p = x[u] * inv;
+        qv[u] = !(p > -2147483648.0f && p < 2147483648.0f) ? -128 : (int) fminf(fmaxf(rintf(p), -128.0f), 127.0f);
+    }
+    // codes: elements 4j..4j+3 -> K-step (j >> 1) & 1, half j >> 2, slots 4(j & 1) + {0, 2, 1, 3}
+    typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+    const half4 hv = {(_Float16) qv[0], (_Float16) qv[2], (_Float16) qv[1], (_Float16) qv[3]};
+    *reinterpret_cast<half4*>(bq + ((int64_t) (2 * b + ((j >> 1) & 1)) * NP + t) * 16 + 8 * (j >> 2) + 4 * (j & 1)) = hv;
+    // per-16 sums: distance 8 (xor 2), distance 4 (xor 1), then in-lane distance 2 and 1
+    float s[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) s[u] = __shfl_xor(x[u], 2) + x[u];
+#pragma unroll
+    for (int u = 0; u < 4; u++) s[u] = __shfl_xor(s[u], 1) + s[u];
+    const float xs16 = (s[0] + s[2]) + (s[1] + s[3]);
+    if (j == 0) tdb[(int64_t) b * NP + t] = db;
+    if ((j & 3) == 0) txs[(int64_t) (2 * b + (j >> 2)) * NP + t] = xs16;
+    if constexpr (SK != 0) {
+        const float other = __shfl_xor(xs16, 4);   // the block's other half
+        float m2 = SK == 1 ? fabsf((j < 4) ? xs16 + other : other + xs16) : fabsf(xs16);
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) m2 = fmaxf(m2, __shfl_xor(m2, o));
+        if (lane == 0) tmx[(int64_t) ch * NP + t] = m2;
+    }
+}
+
+template <int SK>
+__global__ void __launch_bounds__(256) gemm_prep_b(int Kp, int NP, const float* __restrict__ tdb,
+                                                   const float* __restrict__ txs, const float* __restrict__ tmx,
+                                                   float* __restrict__ dx, _Float16* __restrict__ shi,
+                                                   _Float16* __restrict__ slo, float* __restrict__ es) {
+    const int t = blockIdx.x * 256 + threadIdx.x, b = blockIdx.y, nch = Kp >> 8;
+    if (t >= NP) return;
+    float mx = 0.0f;
+    if constexpr (SK != 0)
+        for (int c = 0; c < nch; c++) mx = fmaxf(mx, tmx[(int64_t) c * NP + t]);
     int ex = 0;
-    if (SK != 0 && mx > 0.0f && mx <= 3.0e38f) {   // zero or non-finite sums keep 2^0
-        frexpf(mx, &ex);                         // mx < 2^ex
+    if (SK != 0 && mx > 0.0f && mx <= 3.0e38f) {   // the largest |sum| lands in [2^13, 2^14); 0 / non-finite keep 2^0
+        frexpf(mx, &ex);
         ex -= 14;
     }
     const float down = ldexpf(1.0f, -ex);
-    if (threadIdx.x == 0) es[t] = ldexpf(1.0f, ex);
-    for (int b = threadIdx.x; b < nbp; b += 256) dx[(int64_t) b * NP + t] = sdb[b] * down;
-    if constexpr (SK == 1) {
-        for (int b = threadIdx.x; b < nbp; b += 256) {
-            const float v = (sxs[2 * b] + sxs[2 * b + 1]) * down;
-            const _Float16 h = (_Float16) v;
-            const int64_t o = ((int64_t) (b >> 3) * NP + t) * 8 + (b & 7);
-            shi[o] = h;
-            slo[o] = (_Float16) (v - (float) h);
-        }
-    }
+    if (b == 0) es[t] = ldexpf(1.0f, ex);
+    dx[(int64_t) b * NP + t] = tdb[(int64_t) b * NP + t] * down;
+    const float x0 = txs[(int64_t) (2 * b) * NP + t], x1 = txs[(int64_t) (2 * b + 1) * NP + t];
+    auto put = [&](int64_t o, float v) {
+        const _Float16 h = (_Float16) v;
+        shi[o] = h;
+        slo[o] = (_Float16) (v - (float) h);
+    };
+    if constexpr (SK == 1) put(((int64_t) (b >> 3) * NP + t) * 8 + (b & 7), (x0 + x1) * down);
     if constexpr (SK == 2) {
-        for (int i = threadIdx.x; i < 2 * nbp; i += 256) {
-            const float v = sxs[i] * down;
-            const _Float16 h = (_Float16) v;
-            const int64_t o = ((int64_t) (i >> 4) * NP + t) * 16 + (i & 15);
-            shi[o] = h;
-            slo[o] = (_Float16) (v - (float) h);
-        }
+        put(((int64_t) (b >> 3) * NP + t) * 16 + 2 * (b & 7), x0 * down);
+        put(((int64_t) (b >> 3) * NP + t) * 16 + 2 * (b & 7) + 1, x1 * down);
     }
 }
 
 static int64_t a256(int64_t v) { return (v + 255) & ~(int64_t) 255; }
 
+// GemmAct buffers, then the pass-A temporaries (block scales, per-16 sums, chunk maxima).
 size_t gemm_act_bytes_np(int dt, int NP, int k) {
     const int64_t Kp = (k + 255) / 256 * 256, sk = gemm_sums_kind(dt);
     const int64_t sb = sk == 0 ? 0 : a256((Kp / 256) * NP * (sk == 1 ? 8 : 16) * 2);
-    return (size_t) (a256(Kp * NP * 2) + a256((Kp / 32) * NP * 4) + 2 * sb + a256((int64_t) NP * 4));
+    const int64_t tmp = a256((Kp / 32) * NP * 4) + a256((Kp / 16) * NP * 4) + a256((Kp / 256) * NP * 4);
+    return (size_t) (a256(Kp * NP * 2) + a256((Kp / 32) * NP * 4) + 2 * sb + a256((int64_t) NP * 4) + tmp);
 }
 size_t gemm_act_bytes(int dt, int n, int k) { return gemm_act_bytes_np(dt, (n + 63) / 64 * 64, k); }
 
@@ -205,16 +238,26 @@ static hipError_t prep_np(int dt, const float* a, int lda, int n, int NP, int k,
     _Float16* slo = (_Float16*) (p + sb);
     p += 2 * sb;
     float* es = (float*) p;
+    p += a256((int64_t) NP * 4);
+    float* tdb = (float*) p;
+    p += a256((int64_t) (Kp / 32) * NP * 4);
+    float* txs = (float*) p;
+    p += a256((int64_t) (Kp / 16) * NP * 4);
+    float* tmx = (float*) p;
     *out = GemmAct{bq, dx, shi, slo, es, NP, Kp};
-    const size_t lds = (size_t) (Kp / 32) * 12;
-    if (lds > 64 * 1024) return hipErrorNotSupported;
     if (NP <= 0) return hipSuccess;
-    if (sk == 1)
-        gemm_prep_kernel<1><<<NP, 256, lds, st>>>(a, lda, n, k, Kp, NP, bq, dx, shi, slo, es, gmap, goff, gpoff);
-    else if (sk == 2)
-        gemm_prep_kernel<2><<<NP, 256, lds, st>>>(a, lda, n, k, Kp, NP, bq, dx, shi, slo, es, gmap, goff, gpoff);
-    else
-        gemm_prep_kernel<0><<<NP, 256, lds, st>>>(a, lda, n, k, Kp, NP, bq, dx, shi, slo, es, gmap, goff, gpoff);
+    const dim3 ga((Kp / 256 + 3) / 4, NP), gb((NP + 255) / 256, Kp / 32);
+    const int vec = ((reinterpret_cast<uintptr_t>(a) & 15) == 0 && (lda & 3) == 0) ? 1 : 0;
+    if (sk == 1) {
+        gemm_prep_a<1><<<ga, 256, 0, st>>>(a, lda, n, k, Kp, NP, bq, tdb, txs, tmx, gmap, goff, gpoff, vec);
+        gemm_prep_b<1><<<gb, 256, 0, st>>>(Kp, NP, tdb, txs, tmx, dx, shi, slo, es);
+    } else if (sk == 2) {
+        gemm_prep_a<2><<<ga, 256, 0, st>>>(a, lda, n, k, Kp, NP, bq, tdb, txs, tmx, gmap, goff, gpoff, vec);
+        gemm_prep_b<2><<<gb, 256, 0, st>>>(Kp, NP, tdb, txs, tmx, dx, shi, slo, es);
+    } else {
+        gemm_prep_a<0><<<ga, 256, 0, st>>>(a, lda, n, k, Kp, NP, bq, tdb, txs, tmx, gmap, goff, gpoff, vec);
+        gemm_prep_b<0><<<gb, 256, 0, st>>>(Kp, NP, tdb, txs, tmx, dx, shi, slo, es);
+    }
     return hipGetLastError();
 }
 
