@@ -94,8 +94,8 @@ JAMHIP_DEV uint32_t mx_pair(uint32_t x, uint32_t hb, uint32_t sel, uint32_t sgnm
     const half2v r = __builtin_bit_cast(half2v, v) * __builtin_bit_cast(half2v, s2);
     return __builtin_bit_cast(uint32_t, r);
 }
-JAMHIP_DEV half8 mx_frag(uint32_t w0, uint32_t w1, int q, uint32_t s2) {
-    const uint32_t x0 = (q ? w0 >> 4 : w0) & 0x0F0F0F0Fu, x1 = (q ? w1 >> 4 : w1) & 0x0F0F0F0Fu;
+JAMHIP_DEV half8 mx_frag(uint32_t w0, uint32_t w1, int q4, uint32_t s2) {   // q4 = 4·q
+    const uint32_t x0 = (w0 >> q4) & 0x0F0F0F0Fu, x1 = (w1 >> q4) & 0x0F0F0F0Fu;
     const uint32_t h0 = __builtin_amdgcn_perm(0x4A484644u, 0x42403C00u, x0 & 0x07070707u);
     const uint32_t h1 = __builtin_amdgcn_perm(0x4A484644u, 0x42403C00u, x1 & 0x07070707u);
     typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -220,11 +220,19 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
         }
     };
 
+    // nibble masks in VGPRs: with one operand in a VGPR the mask-and-or is a single v_and_or_b32
+    uint32_t vmask_lo, vmask_hi;
+    asm volatile("v_mov_b32 %0, 0x000F000F" : "=v"(vmask_lo));
+    asm volatile("v_mov_b32 %0, 0x00F000F0" : "=v"(vmask_hi));
+    uint32_t vmask_qh;
+    asm volatile("v_mov_b32 %0, 0x00300030" : "=v"(vmask_qh));
+    (void) vmask_qh;
+
     floatx16 acc[RT][CT], accs[RT][CT];
 #pragma unroll
     for (int i = 0; i < RT; i++)
 #pragma unroll
-        for (int j = 0; j < CT; j++) acc[i][j] = floatx16{};
+        for (int j = 0; j < CT; j++) acc[i][j] = accs[i][j] = floatx16{};
 
     issue(0, smem);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -238,17 +246,17 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
         const unsigned char* LB = buf + S::B_OFF;
         const float* LDX = reinterpret_cast<const float*>(buf + S::DX_OFF);
 
-        if constexpr (DT == Q4_K) {
-            if (h2 == 0) {
-#pragma unroll
-                for (int i = 0; i < RT; i++)
-#pragma unroll
-                    for (int j = 0; j < CT; j++) accs[i][j] = floatx16{};
-            }
+        if constexpr (DT == Q4_K) {   // accs starts at zero and is cleared where it is consumed
             uint4 hdr[RT];
+            uint32_t scs[RT];   // the stage's 4 sub-block scales (6-bit), one per byte
 #pragma unroll
-            for (int i = 0; i < RT; i++)
+            for (int i = 0; i < RT; i++) {
                 hdr[i] = *reinterpret_cast<const uint4*>(buf + S::H_OFF + ((wave * RT + i) * 32 + r) * 16);
+                // jam_kquant.h:26-33: sub-blocks 0-3 scale = byte & 63; 4-7 = low nibble of bytes 8-11 with
+                // the top 2 bits of bytes 0-3
+                scs[i] = h2 == 0 ? hdr[i].y & 0x3F3F3F3Fu
+                                 : (hdr[i].w & 0x0F0F0F0Fu) | ((hdr[i].y >> 2) & 0x30303030u);
+            }
 #pragma unroll
             for (int gpl = 0; gpl < 2; gpl++) {
                 uint4 ch[RT];
@@ -257,17 +265,18 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
                     ch[i] = *reinterpret_cast<const uint4*>(LA + ((wave * RT + i) * NCS + 2 * gpl + q) * 512 + 16 * r);
 #pragma unroll
                 for (int sub = 0; sub < 2; sub++) {
-                    const int s = 4 * h2 + 2 * gpl + sub, bl = 2 * gpl + sub;
+                    const int bl = 2 * gpl + sub;
                     half8 af[RT][2];
 #pragma unroll
                     for (int i = 0; i < RT; i++) {
-                        int sc, mn;
-                        q4k_scmn(hdr[i], s, sc, mn);
                         // lo nibble: (1024 + v)·sc − 1024·sc; hi nibble (bits 4-7): (1024 + 16v)·sc/16 − 64·sc
-                        const float fm = sub ? (float) sc * 0.0625f : (float) sc;
-                        const float fa = sub ? -64.0f * (float) sc : -1024.0f * (float) sc;
-                        const uint32_t mul = pack2((_Float16) fm, (_Float16) fm), add = pack2((_Float16) fa, (_Float16) fa);
-                        const uint32_t mask = sub ? 0x00F000F0u : 0x000F000Fu;
+                        const uint32_t sc = (scs[i] >> (8 * bl)) & 0xffu;
+                        const uint32_t dup = sc | (sc << 16) | 0x64006400u;   // f16 pair (1024 + sc, 1024 + sc)
+                        const half2v one = __builtin_bit_cast(half2v, dup) - __builtin_bit_cast(half2v, 0x64006400u);
+                        const half2v mulv = sub ? one * (_Float16) 0.0625f : one;
+                        const half2v addv = one * (sub ? (_Float16) -64.0f : (_Float16) -1024.0f);
+                        const uint32_t mul = __builtin_bit_cast(uint32_t, mulv), add = __builtin_bit_cast(uint32_t, addv);
+                        const uint32_t mask = sub ? vmask_hi : vmask_lo;
                         af[i][0] = frag8(ch[i].x, ch[i].y, mask, mul, add);
                         af[i][1] = frag8(ch[i].z, ch[i].w, mask, mul, add);
                     }
@@ -302,9 +311,11 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
                         dd[e] = h2f_bits(*reinterpret_cast<const uint16_t*>(H + row * 16));
                     }
 #pragma unroll
-                    for (int j = 0; j < CT; j++)
+                    for (int j = 0; j < CT; j++) {
 #pragma unroll
                         for (int e = 0; e < 16; e++) acc[i][j][e] = fmaf(dd[e], accs[i][j][e], acc[i][j][e]);
+                        accs[i][j] = floatx16{};
+                    }
                     // A' = −dmin·mn_s for sub-blocks 4q..4q+3 of row r, split hi + lo
                     const float dmin = h2f_bits(hdr[i].x >> 16);
                     half4 ahi, alo;
@@ -329,12 +340,6 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
                 }
             }
         } else if constexpr (DT == MXFP4) {   // group of 8 blocks; stage h2 = blocks 4h2..4h2+3
-            if (h2 == 0) {
-#pragma unroll
-                for (int i = 0; i < RT; i++)
-#pragma unroll
-                    for (int j = 0; j < CT; j++) accs[i][j] = floatx16{};
-            }
             uint4 hdr[RT];
 #pragma unroll
             for (int i = 0; i < RT; i++)
@@ -349,8 +354,8 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
                     const int eb = (int) (((b < 4 ? hdr[i].x : hdr[i].y) >> (8 * (b & 3))) & 0xffu);
                     const int er = (int) (hdr[i].z & 0xffu);
                     const uint32_t s2 = mx_scale2(eb - er);
-                    af[i][0] = mx_frag(ch.x, ch.y, q, s2);
-                    af[i][1] = mx_frag(ch.z, ch.w, q, s2);
+                    af[i][0] = mx_frag(ch.x, ch.y, 4 * q, s2);
+                    af[i][1] = mx_frag(ch.z, ch.w, 4 * q, s2);
                 }
                 half8 bf[CT][2];
                 float dxv[CT];
@@ -379,9 +384,11 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
 #pragma unroll
                     for (int e = 0; e < 16; e++) sg[e] = e8m0_half(H[(8 * (e >> 2) + 4 * q + (e & 3)) * 16 + 8]);
 #pragma unroll
-                    for (int j = 0; j < CT; j++)
+                    for (int j = 0; j < CT; j++) {
 #pragma unroll
                         for (int e = 0; e < 16; e++) acc[i][j][e] = fmaf(sg[e], accs[i][j][e], acc[i][j][e]);
+                        accs[i][j] = floatx16{};
+                    }
                 }
             }
         } else {   // Q6_K: stage h2 = half h of the super-block, blocks j = 0..3 (elements 128h + 32j + l)
@@ -427,7 +434,7 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
                     const float fm = hi ? sc * 0.015625f : sc * 0.25f, fa = hi ? -16.0f * sc : -256.0f * sc;
                     const uint32_t mul1 = pack2((_Float16) fm, (_Float16) fm), add1 = pack2((_Float16) fa, (_Float16) fa);
                     const uint4 L = ql[i][jb & 1];
-                    const uint32_t m1 = hi ? 0x00F000F0u : 0x000F000Fu;
+                    const uint32_t m1 = hi ? vmask_hi : vmask_lo;
                     a1[i][0] = frag8(L.x, L.y, m1, mul1, add1);
                     a1[i][1] = frag8(L.z, L.w, m1, mul1, add1);
                     // qh bits 2jb..2jb+1 moved to bits 4-5: (1024 + 16v)·sc/4 − 256·sc = 4·sc·v = sc·(16v)/4
@@ -436,8 +443,8 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
                     const uint4 Q = qh[i];
                     const int sh = 2 * jb;   // bits 2jb..2jb+1 -> 4..5
                     auto mv = [&](uint32_t x) { return sh <= 4 ? x << (4 - sh) : x >> (sh - 4); };
-                    a2[i][0] = frag8(mv(Q.x), mv(Q.y), 0x00300030u, mul2, add2);
-                    a2[i][1] = frag8(mv(Q.z), mv(Q.w), 0x00300030u, mul2, add2);
+                    a2[i][0] = frag8(mv(Q.x), mv(Q.y), vmask_qh, mul2, add2);
+                    a2[i][1] = frag8(mv(Q.z), mv(Q.w), vmask_qh, mul2, add2);
                 }
                 half8 bf[CT][2];
                 float dxv[CT];

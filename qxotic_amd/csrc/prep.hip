@@ -183,23 +183,37 @@ __global__ void __launch_bounds__(256) gemm_prep_a(const float* __restrict__ a, 
     }
 }
 
-template <int SK>
-__global__ void __launch_bounds__(256) gemm_prep_b(int Kp, int NP, const float* __restrict__ tdb,
-                                                   const float* __restrict__ txs, const float* __restrict__ tmx,
-                                                   float* __restrict__ dx, _Float16* __restrict__ shi,
-                                                   _Float16* __restrict__ slo, float* __restrict__ es) {
-    const int t = blockIdx.x * 256 + threadIdx.x, b = blockIdx.y, nch = Kp >> 8;
-    if (t >= NP) return;
+// Pass E: the token's power of two from its chunks' maxima (the largest |sum| lands in [2^13, 2^14); zero
+// or non-finite sums keep 2^0): es[t] = 2^e_t, down[t] = 2^-e_t. A workgroup takes 64 token slots, its 4
+// waves a quarter of the chunks each.
+__global__ void __launch_bounds__(256) gemm_prep_e(int Kp, int NP, int sk, const float* __restrict__ tmx,
+                                                   float* __restrict__ es, float* __restrict__ down) {
+    __shared__ float part[4][64];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, t = blockIdx.x * 64 + lane, nch = Kp >> 8;
     float mx = 0.0f;
-    if constexpr (SK != 0)
-        for (int c = 0; c < nch; c++) mx = fmaxf(mx, tmx[(int64_t) c * NP + t]);
+    if (sk != 0 && t < NP)
+        for (int c = wv; c < nch; c += 4) mx = fmaxf(mx, tmx[(int64_t) c * NP + t]);
+    part[wv][lane] = mx;
+    __syncthreads();
+    if (wv != 0 || t >= NP) return;
+    mx = fmaxf(fmaxf(part[0][lane], part[1][lane]), fmaxf(part[2][lane], part[3][lane]));
     int ex = 0;
-    if (SK != 0 && mx > 0.0f && mx <= 3.0e38f) {   // the largest |sum| lands in [2^13, 2^14); 0 / non-finite keep 2^0
+    if (mx > 0.0f && mx <= 3.0e38f) {
         frexpf(mx, &ex);
         ex -= 14;
     }
-    const float down = ldexpf(1.0f, -ex);
-    if (b == 0) es[t] = ldexpf(1.0f, ex);
+    es[t] = ldexpf(1.0f, ex);
+    down[t] = ldexpf(1.0f, -ex);
+}
+
+// Pass B, one thread per (token slot, block): the scaled block scale and sums.
+template <int SK>
+__global__ void __launch_bounds__(256) gemm_prep_b(int NP, const float* __restrict__ tdb, const float* __restrict__ txs,
+                                                   const float* __restrict__ down_t, float* __restrict__ dx,
+                                                   _Float16* __restrict__ shi, _Float16* __restrict__ slo) {
+    const int t = blockIdx.x * 256 + threadIdx.x, b = blockIdx.y;
+    if (t >= NP) return;
+    const float down = down_t[t];
     dx[(int64_t) b * NP + t] = tdb[(int64_t) b * NP + t] * down;
     const float x0 = txs[(int64_t) (2 * b) * NP + t], x1 = txs[(int64_t) (2 * b + 1) * NP + t];
     auto put = [&](int64_t o, float v) {
@@ -220,7 +234,8 @@ static int64_t a256(int64_t v) { return (v + 255) & ~(int64_t) 255; }
 size_t gemm_act_bytes_np(int dt, int NP, int k) {
     const int64_t Kp = (k + 255) / 256 * 256, sk = gemm_sums_kind(dt);
     const int64_t sb = sk == 0 ? 0 : a256((Kp / 256) * NP * (sk == 1 ? 8 : 16) * 2);
-    const int64_t tmp = a256((Kp / 32) * NP * 4) + a256((Kp / 16) * NP * 4) + a256((Kp / 256) * NP * 4);
+    const int64_t tmp = a256((Kp / 32) * NP * 4) + a256((Kp / 16) * NP * 4) + a256((Kp / 256) * NP * 4) +
+                        a256((int64_t) NP * 4);
     return (size_t) (a256(Kp * NP * 2) + a256((Kp / 32) * NP * 4) + 2 * sb + a256((int64_t) NP * 4) + tmp);
 }
 size_t gemm_act_bytes(int dt, int n, int k) { return gemm_act_bytes_np(dt, (n + 63) / 64 * 64, k); }
@@ -244,20 +259,19 @@ static hipError_t prep_np(int dt, const float* a, int lda, int n, int NP, int k,
     float* txs = (float*) p;
     p += a256((int64_t) (Kp / 16) * NP * 4);
     float* tmx = (float*) p;
+    p += a256((int64_t) (Kp / 256) * NP * 4);
+    float* down = (float*) p;
     *out = GemmAct{bq, dx, shi, slo, es, NP, Kp};
     if (NP <= 0) return hipSuccess;
     const dim3 ga((Kp / 256 + 3) / 4, NP), gb((NP + 255) / 256, Kp / 32);
     const int vec = ((reinterpret_cast<uintptr_t>(a) & 15) == 0 && (lda & 3) == 0) ? 1 : 0;
-    if (sk == 1) {
-        gemm_prep_a<1><<<ga, 256, 0, st>>>(a, lda, n, k, Kp, NP, bq, tdb, txs, tmx, gmap, goff, gpoff, vec);
-        gemm_prep_b<1><<<gb, 256, 0, st>>>(Kp, NP, tdb, txs, tmx, dx, shi, slo, es);
-    } else if (sk == 2) {
-        gemm_prep_a<2><<<ga, 256, 0, st>>>(a, lda, n, k, Kp, NP, bq, tdb, txs, tmx, gmap, goff, gpoff, vec);
-        gemm_prep_b<2><<<gb, 256, 0, st>>>(Kp, NP, tdb, txs, tmx, dx, shi, slo, es);
-    } else {
-        gemm_prep_a<0><<<ga, 256, 0, st>>>(a, lda, n, k, Kp, NP, bq, tdb, txs, tmx, gmap, goff, gpoff, vec);
-        gemm_prep_b<0><<<gb, 256, 0, st>>>(Kp, NP, tdb, txs, tmx, dx, shi, slo, es);
-    }
+    if (sk == 1) gemm_prep_a<1><<<ga, 256, 0, st>>>(a, lda, n, k, Kp, NP, bq, tdb, txs, tmx, gmap, goff, gpoff, vec);
+    else if (sk == 2) gemm_prep_a<2><<<ga, 256, 0, st>>>(a, lda, n, k, Kp, NP, bq, tdb, txs, tmx, gmap, goff, gpoff, vec);
+    else gemm_prep_a<0><<<ga, 256, 0, st>>>(a, lda, n, k, Kp, NP, bq, tdb, txs, tmx, gmap, goff, gpoff, vec);
+    gemm_prep_e<<<(NP + 63) / 64, 256, 0, st>>>(Kp, NP, sk, tmx, es, down);
+    if (sk == 1) gemm_prep_b<1><<<gb, 256, 0, st>>>(NP, tdb, txs, down, dx, shi, slo);
+    else if (sk == 2) gemm_prep_b<2><<<gb, 256, 0, st>>>(NP, tdb, txs, down, dx, shi, slo);
+    else gemm_prep_b<0><<<gb, 256, 0, st>>>(NP, tdb, txs, down, dx, shi, slo);
     return hipGetLastError();
 }
 
