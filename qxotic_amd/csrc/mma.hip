@@ -195,12 +195,15 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
                 dma16(w.sc + (((r0t + T) * G + g) * 32 + 8 * (lane & 3)) * 2, buf + S::H_OFF);
             }
         }
-        // activation codes: ksteps 16g + 8h2 .. +7, BN tokens x 32 B each
+        // activation codes: ksteps 16g + 8h2 .. +7; in LDS each K-step's two 8-element halves are split
+        // into planes [kk][half q][BN tokens][16 B] so a fragment read is 512 contiguous bytes per half-wave
+        // (conflict-free); the copy gathers the halves from the token-interleaved global layout
+        static_assert(BN == 64, "one 1 KB piece per K-step half");
         for (int kk = 0; kk < 8; kk++) {
-            const _Float16* src = A.b + ((int64_t) (16 * g + 8 * h2 + kk) * A.NP + n0) * 16;
+            const uint8_t* src = reinterpret_cast<const uint8_t*>(A.b + ((int64_t) (16 * g + 8 * h2 + kk) * A.NP + n0) * 16);
 #pragma unroll
-            for (int p = 0; p < BN / 32; p++)
-                if (mine()) dma16((const uint8_t*) src + p * 1024 + 16 * lane, buf + S::B_OFF + kk * BN * 32 + p * 1024);
+            for (int p = 0; p < 2; p++)
+                if (mine()) dma16(src + 32 * lane + 16 * p, buf + S::B_OFF + (2 * kk + p) * 1024);
         }
         // block scales: 4 blocks x BN tokens (f32)
         for (int p = 0; p < BN / 64; p++) {
@@ -240,7 +243,8 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
 
     for (int st = 0; st < nst; st++) {
         unsigned char* buf = smem + (st & 1) * S::BYTES;
-        if (st + 1 < nst) issue(st + 1, smem + ((st + 1) & 1) * S::BYTES);
+        // Q4_K issues the next stage's copy itself, after its last LDS read of this stage
+        if (DT != Q4_K && st + 1 < nst) issue(st + 1, smem + ((st + 1) & 1) * S::BYTES);
         const int h2 = st & 1;
         const unsigned char* LA = buf + S::A_OFF;
         const unsigned char* LB = buf + S::B_OFF;
@@ -257,12 +261,48 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
                 scs[i] = h2 == 0 ? hdr[i].y & 0x3F3F3F3Fu
                                  : (hdr[i].w & 0x0F0F0F0Fu) | ((hdr[i].y >> 2) & 0x30303030u);
             }
+            // every LDS read of the stage up front (the wave then works down an in-order queue)
+            uint4 chs[2][RT];
+            half8 bfs[4][CT][2];
+            float dxs[4][CT];
 #pragma unroll
-            for (int gpl = 0; gpl < 2; gpl++) {
-                uint4 ch[RT];
+            for (int gpl = 0; gpl < 2; gpl++)
 #pragma unroll
                 for (int i = 0; i < RT; i++)
-                    ch[i] = *reinterpret_cast<const uint4*>(LA + ((wave * RT + i) * NCS + 2 * gpl + q) * 512 + 16 * r);
+                    chs[gpl][i] = *reinterpret_cast<const uint4*>(LA + ((wave * RT + i) * NCS + 2 * gpl + q) * 512 + 16 * r);
+#pragma unroll
+            for (int bl = 0; bl < 4; bl++)
+#pragma unroll
+                for (int j = 0; j < CT; j++) {
+#pragma unroll
+                    for (int ks = 0; ks < 2; ks++)
+                        bfs[bl][j][ks] = *reinterpret_cast<const half8*>(LB + ((2 * bl + ks) * 2 + q) * BN * 16 + (32 * j + r) * 16);
+                    dxs[bl][j] = LDX[bl * BN + 32 * j + r];
+                }
+            // super-block end (odd stage): d of the 16 output rows this lane holds, and the sums' fragments
+            float dds[RT][16];
+            half4 shi[CT], slo[CT];
+            if (h2 == 1) {
+#pragma unroll
+                for (int i = 0; i < RT; i++) {
+                    const unsigned char* H = buf + S::H_OFF + (wave * RT + i) * 32 * 16;
+#pragma unroll
+                    for (int e = 0; e < 16; e++)
+                        dds[i][e] = h2f_bits(*reinterpret_cast<const uint16_t*>(H + (8 * (e >> 2) + 4 * q + (e & 3)) * 16));
+                }
+#pragma unroll
+                for (int j = 0; j < CT; j++) {
+                    const unsigned char* SP = buf + S::S_OFF + (32 * j + r) * 16 + 8 * q;
+                    shi[j] = *reinterpret_cast<const half4*>(SP);
+                    slo[j] = *reinterpret_cast<const half4*>(SP + BN * 16);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);   // keep the reads ahead of the compute
+            // this stage's LDS reads are all issued: start copying the next stage into the other buffer
+            if (st + 1 < nst) issue(st + 1, smem + ((st + 1) & 1) * S::BYTES);
+#pragma unroll
+            for (int gpl = 0; gpl < 2; gpl++) {
+                const uint4* ch = chs[gpl];
 #pragma unroll
                 for (int sub = 0; sub < 2; sub++) {
                     const int bl = 2 * gpl + sub;
@@ -280,40 +320,24 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
                         af[i][0] = frag8(ch[i].x, ch[i].y, mask, mul, add);
                         af[i][1] = frag8(ch[i].z, ch[i].w, mask, mul, add);
                     }
-                    half8 bf[CT][2];
-                    float dxv[CT];
-#pragma unroll
-                    for (int j = 0; j < CT; j++) {
-#pragma unroll
-                        for (int ks = 0; ks < 2; ks++)
-                            bf[j][ks] = *reinterpret_cast<const half8*>(LB + ((2 * bl + ks) * BN + 32 * j + r) * 32 + 16 * q);
-                        dxv[j] = LDX[bl * BN + 32 * j + r];
-                    }
 #pragma unroll
                     for (int i = 0; i < RT; i++)
 #pragma unroll
                         for (int j = 0; j < CT; j++) {
-                            floatx16 D = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i][0], bf[j][0], floatx16{}, 0, 0, 0);
-                            D = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i][1], bf[j][1], D, 0, 0, 0);
+                            floatx16 D = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i][0], bfs[bl][j][0], floatx16{}, 0, 0, 0);
+                            D = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i][1], bfs[bl][j][1], D, 0, 0, 0);
 #pragma unroll
-                            for (int e = 0; e < 16; e++) accs[i][j][e] = fmaf(D[e], dxv[j], accs[i][j][e]);
+                            for (int e = 0; e < 16; e++) accs[i][j][e] = fmaf(D[e], dxs[bl][j], accs[i][j][e]);
                         }
                 }
             }
             if (h2 == 1) {   // super-block end: d, then the mins on the matrix cores
 #pragma unroll
                 for (int i = 0; i < RT; i++) {
-                    const unsigned char* H = buf + S::H_OFF + (wave * RT + i) * 32 * 16;
-                    float dd[16];
-#pragma unroll
-                    for (int e = 0; e < 16; e++) {
-                        const int row = 8 * (e >> 2) + 4 * q + (e & 3);
-                        dd[e] = h2f_bits(*reinterpret_cast<const uint16_t*>(H + row * 16));
-                    }
 #pragma unroll
                     for (int j = 0; j < CT; j++) {
 #pragma unroll
-                        for (int e = 0; e < 16; e++) acc[i][j][e] = fmaf(dd[e], accs[i][j][e], acc[i][j][e]);
+                        for (int e = 0; e < 16; e++) acc[i][j][e] = fmaf(dds[i][e], accs[i][j][e], acc[i][j][e]);
                         accs[i][j] = floatx16{};
                     }
                     // A' = −dmin·mn_s for sub-blocks 4q..4q+3 of row r, split hi + lo
@@ -330,12 +354,9 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
                     }
 #pragma unroll
                     for (int j = 0; j < CT; j++) {
-                        const unsigned char* SP = buf + S::S_OFF + (32 * j + r) * 16 + 8 * q;
-                        const half4 bhi = *reinterpret_cast<const half4*>(SP);
-                        const half4 blo = *reinterpret_cast<const half4*>(SP + BN * 16);
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(ahi, bhi, acc[i][j], 0, 0, 0);
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(ahi, blo, acc[i][j], 0, 0, 0);
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(alo, bhi, acc[i][j], 0, 0, 0);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(ahi, shi[j], acc[i][j], 0, 0, 0);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(ahi, slo[j], acc[i][j], 0, 0, 0);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(alo, shi[j], acc[i][j], 0, 0, 0);
                     }
                 }
             }
@@ -363,7 +384,7 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
                 for (int j = 0; j < CT; j++) {
 #pragma unroll
                     for (int ks = 0; ks < 2; ks++)
-                        bf[j][ks] = *reinterpret_cast<const half8*>(LB + ((2 * bl + ks) * BN + 32 * j + r) * 32 + 16 * q);
+                        bf[j][ks] = *reinterpret_cast<const half8*>(LB + ((2 * bl + ks) * 2 + q) * BN * 16 + (32 * j + r) * 16);
                     dxv[j] = LDX[bl * BN + 32 * j + r];
                 }
 #pragma unroll
@@ -452,7 +473,7 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
                 for (int j = 0; j < CT; j++) {
 #pragma unroll
                     for (int ks = 0; ks < 2; ks++)
-                        bf[j][ks] = *reinterpret_cast<const half8*>(LB + ((2 * jb + ks) * BN + 32 * j + r) * 32 + 16 * q);
+                        bf[j][ks] = *reinterpret_cast<const half8*>(LB + ((2 * jb + ks) * 2 + q) * BN * 16 + (32 * j + r) * 16);
                     dxv[j] = LDX[jb * BN + 32 * j + r];
                 }
 #pragma unroll
