@@ -10,13 +10,15 @@ The same JSON line carries
   * ``roofline``: the GEMV kernel's algorithmic bytes per launch over its event-timed average duration,
     against MI355X's 8 TB/s, plus the HBM bytes per launch that rocprofv3's FETCH_SIZE/WRITE_SIZE counters
     measured for this command (read from the committed summary under profiles/);
+  * ``moe``: config 5, a gpt-oss-20B-shaped MoE layer (device routing, gather, two grouped MXFP4 matmuls,
+    combine) in TOPS and weight GB/s with their fractions of the int8 / fp4 MFMA and HBM peaks;
   * ``prefill``: the metric's second half, M=512 prefill TOPS of Q4_K 14336x4096 and Q6_K 4096x14336
     (activations 99% N(0,1) + 1% outliers at +-20, F2-quantized in the timed calls) against MI355X's dense
     int8 and f16 MFMA peaks;
   * ``cpu_baseline``: the reference's own libjam (oracle/_ref, built from the reference C sources) on the
     same decode workload on this machine's host cores.
 
-    python bench.py [--gpus 1] [--steps 2048] [--warmup 64] [--no-cpu] [--no-prefill]
+    python bench.py [--gpus 1] [--steps 2048] [--warmup 64] [--no-cpu] [--no-prefill] [--no-moe]
     profiling runs: --no-graph (plain stream launches) --calibrate-copy (three 256 MiB device copies first,
     the known-size reference for the FETCH_SIZE/WRITE_SIZE scale factors)
 """
@@ -113,9 +115,23 @@ def gpu_leg(args, w: np.ndarray, hip, torch, stream) -> dict:
         st = hip.mm_device(Segment.of(copies[last]), JAM.Q4_K, K, a.data_ptr(), K, ref.data_ptr(), M, M, N, K)
     torch.cuda.synchronize()
     assert st == JAM.OK and torch.equal(ref, c[last]), "timed output disagrees with a direct call"
+    # the host-pointer entry point (jamhip_mm: A staged host -> device, C copied back, synchronized), the
+    # PCIe-inclusive latency a caller passing host buffers sees; pinned weights, wall clock per call
+    a_h = a.cpu().numpy()
+    c_h = np.empty((N, M), np.float32)
+    for i in range(8):
+        hip.mm_contiguous(Segment.of(copies[i % COPIES]), Segment.of(a_h), Segment.of(c_h), JAM.Q4_K, M, N, K)
+    calls = 256
+    t0 = time.perf_counter()
+    for i in range(calls):
+        st = hip.mm_contiguous(Segment.of(copies[i % COPIES]), Segment.of(a_h), Segment.of(c_h), JAM.Q4_K, M, N, K)
+        if st != JAM.OK:
+            raise RuntimeError(hip.last_error())
+    host_us = (time.perf_counter() - t0) / calls * 1e6
+    assert np.array_equal(c_h, c[(calls - 1) % COPIES].cpu().numpy()), "host-pointer call disagrees"
     for cp in copies:
         hip.evict(Segment.of(cp))
-    return {"event_ms": ev_ms, "wall_s": wall}
+    return {"event_ms": ev_ms, "wall_s": wall, "host_us": host_us}
 
 
 def prefill_leg(hip, torch, stream, reps: int = 10) -> dict:
@@ -154,6 +170,85 @@ def prefill_leg(hip, torch, stream, reps: int = 10) -> dict:
     out["note"] = ("jam's F2 quantization + int8 products computed exactly on f16 MFMA (integer operands "
                    "<= 2048); peaks are MI355X dense int8 5.0 POP/s and f16 2.5 PFLOP/s")
     return out
+
+
+def moe_leg(hip, torch, stream, steps: int = 10) -> dict:
+    """Config 5: a gpt-oss-20B-shaped MoE layer on the device: 32 experts with an MXFP4 gate_up 5760x2880
+    and down 2880x2880, 512 tokens routed top-4 by Zipf(1.1) popularity (Gumbel-top-k on log p_e,
+    p_e ~ e^-1.1). One step = jamhip_moe_route + _gather + grouped gate_up + grouped down + _combine
+    (the down projection reads a synthetic 2880-wide hidden of the routed rows; the activation between
+    the two matmuls is not part of jam's path)."""
+    from qxotic_amd.jam import JAM, Segment
+
+    E, TOPK, SEQ, D, FF = 32, 4, 512, 2880, 5760
+    distinct = 2   # distinct expert matrices quantized from N(0,0.02); the 32 experts cycle through them
+    gu = [quantized("MXFP4", FF, D, 0xC0F5 + s) for s in range(distinct)]
+    dn = [quantized("MXFP4", D, D, 0xD0F5 + s) for s in range(distinct)]
+    copies = 2    # 2 x 423 MB of weights, over the 256 MB Infinity Cache
+    wg = [np.ascontiguousarray(np.concatenate([gu[e % distinct] for e in range(E)])) for _ in range(copies)]
+    wd = [np.ascontiguousarray(np.concatenate([dn[e % distinct] for e in range(E)])) for _ in range(copies)]
+    for x in wg:
+        assert hip.pin(Segment.of(x), JAM.MXFP4, D, E * FF) == JAM.OK, hip.last_error()
+    for x in wd:
+        assert hip.pin(Segment.of(x), JAM.MXFP4, D, E * D) == JAM.OK, hip.last_error()
+    rng = np.random.default_rng(0x5A11C0DE ^ 5)
+    logp = -1.1 * np.log(np.arange(1, E + 1))
+    sel = np.argsort(-(logp[None, :] + rng.gumbel(size=(SEQ, E))), axis=1)[:, :TOPK].astype(np.int32)
+    counts_h = np.bincount(sel.ravel(), minlength=E)
+    R = SEQ * TOPK
+    dev = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to("cuda")
+    re = dev(sel.ravel())
+    prob = dev(rng.random(R).astype(np.float32))
+    x = dev(rng.standard_normal((SEQ, D)).astype(np.float32))
+    hid = dev(rng.standard_normal((R, D)).astype(np.float32))
+    i32 = lambda nel: torch.zeros(nel, dtype=torch.int32, device="cuda")
+    counts, off, slot_route, route_slot = i32(E), i32(E + 1), i32(R), i32(R)
+    g = torch.empty((R, D), device="cuda")
+    h = torch.empty((R, FF), device="cuda")
+    y = torch.empty((R, D), device="cuda")
+    out = torch.empty((SEQ, D), device="cuda")
+
+    def layer(i):
+        cg, cd = wg[i % copies], wd[i % copies]
+        ok = hip.moe_route(re.data_ptr(), SEQ, TOPK, E, counts.data_ptr(), off.data_ptr(), slot_route.data_ptr(),
+                           route_slot.data_ptr()) == JAM.OK
+        ok &= hip.moe_gather(x.data_ptr(), D, slot_route.data_ptr(), off.data_ptr(), E, SEQ, TOPK, D, g.data_ptr(),
+                             D) == JAM.OK
+        ok &= hip.mm_grouped(Segment.of(cg), JAM.MXFP4, D, FF, E, counts.data_ptr(), g.data_ptr(), D, h.data_ptr(),
+                             FF, D, R, None) == JAM.OK
+        ok &= hip.mm_grouped(Segment.of(cd), JAM.MXFP4, D, D, E, counts.data_ptr(), hid.data_ptr(), D, y.data_ptr(),
+                             D, D, R, None) == JAM.OK
+        ok &= hip.moe_combine(y.data_ptr(), D, re.data_ptr(), prob.data_ptr(), route_slot.data_ptr(), SEQ, TOPK, E, D,
+                              out.data_ptr(), D) == JAM.OK
+        if not ok:
+            raise RuntimeError(hip.last_error())
+
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        for i in range(3):
+            layer(i)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for i in range(steps):
+            layer(i)
+        e1.record(stream)
+        torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / steps
+    assert np.array_equal(counts.cpu().numpy(), counts_h), "device routing counts disagree with the host's"
+    assert bool(torch.isfinite(out).all()), "moe output not finite"
+    for xx in wg + wd:
+        hip.evict(Segment.of(xx))
+    ops = 2.0 * R * (FF * D + D * D)
+    wbytes = E * (FF + D) * (D // 32) * 17
+    tops = ops / (us * 1e-6) / 1e12
+    gbs = wbytes / (us * 1e-6) / 1e9
+    return {"us_per_layer": round(us, 1), "TOPS": round(tops, 2), "weights_GBs": round(gbs, 1),
+            "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
+            "frac_fp4_peak": round(tops / 10070.0, 4), "routed_rows": R,
+            "counts": counts_h.tolist(),
+            "note": "32 experts x (5760x2880 + 2880x2880) MXFP4 (423 MB, 2 rotating copies; experts cycle through "
+                    "2 distinct N(0,0.02) quantizations), 512 tokens top-4 Zipf(1.1); ops = 2*routed_rows*"
+                    "(5760*2880 + 2880*2880)"}
 
 
 def cpu_leg(w: np.ndarray, budget_s: float = 4.0) -> dict | None:
@@ -203,6 +298,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-moe", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true")
     args = ap.parse_args()
@@ -230,6 +326,10 @@ def main() -> int:
     if not args.no_prefill:
         log("bench: prefill leg")
         pre = prefill_leg(hip, torch, stream)
+    moe = None
+    if not args.no_moe:
+        log("bench: moe leg")
+        moe = moe_leg(hip, torch, stream)
     hip.close()
     cpu = None
     if not args.no_cpu:
@@ -243,9 +343,13 @@ def main() -> int:
                                f"{COPIES} rotating HBM-resident weight copies ({COPIES * M * 16 * 144 / 1e9:.2f} GB)",
                    "weights": "N(0,0.02) quantized to Q4_K", "activations": "N(0,1) f32",
                    "graph_launches": 0 if args.no_graph else args.steps, "wall_s": round(g["wall_s"], 4)},
+        "host_pointer_call": {"us": round(g["host_us"], 2), "GBs": round(STEP_BYTES / (g["host_us"] * 1e-6) / 1e9, 1),
+                              "note": "jamhip_mm with host A and C (16 KiB H2D + 56 KiB D2H + sync per call), "
+                                      "pinned weights, wall clock; not the metric"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles()},
         "prefill": pre,
+        "moe": moe,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
