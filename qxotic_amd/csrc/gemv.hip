@@ -203,7 +203,7 @@ JAMHIP_DEV void a_load(APre<HP>& pre, const float* __restrict__ a, int lda, int 
 #pragma unroll
     for (int i = 0; i < HP; i++) {
         const int h0 = threadIdx.x + 64 * MV_WAVES * i, h = h0 < total ? h0 : total - 1;
-        const int j = h / halves, hh = h - j * halves, jr = j < ntv ? j : ntv - 1;   // rows past ntv: clamp
+        const int j = NT == 1 ? 0 : h / halves, hh = h - j * halves, jr = j < ntv ? j : ntv - 1;   // rows past ntv: clamp
         const bool in = hh < kh;   // clamp only; the zeroing happens in f1_store
         const float4* src = reinterpret_cast<const float4*>(a + (int64_t) jr * lda + 16 * (in ? hh : kh - 1));
 #pragma unroll
@@ -227,7 +227,7 @@ JAMHIP_DEV void f1_store(const APre<HP>& pre, int k, int Gk, int8_t* lq, float* 
         const int h0 = threadIdx.x + 64 * MV_WAVES * i;
         const bool valid = h0 < total;
         const int h = valid ? h0 : 0;
-        const int j = h / halves, hh = h - j * halves;
+        const int j = NT == 1 ? 0 : h / halves, hh = h - j * halves;
         const bool in = hh < (k >> 4);
         float x[16];
 #pragma unroll
@@ -323,9 +323,14 @@ __global__ void __launch_bounds__(64 * MV_WAVES) mv_kernel(WeightView w, ActQ A,
         ntv = n - t0 < NT ? n - t0 : NT;
     }
 
+    // Only waves that own at least one real half-block of the activations load and quantize them (the
+    // others would only write the dummy slot); the condition is wave-uniform. Their loads go first in the
+    // load queue and are kept there by the scheduler.
+    const bool pro = FUSE && wave * 64 < NT * 16 * Gk;
     APre<FUSE ? HP : 1> pre;
-    if constexpr (FUSE) a_load<NT, HP>(pre, a, lda, k, Gk, ntv);   // first in the load queue
-    __builtin_amdgcn_sched_barrier(0);                        // ... and kept there by the scheduler
+    if constexpr (FUSE)
+        if (pro) a_load<NT, HP>(pre, a, lda, k, Gk, ntv);
+    __builtin_amdgcn_sched_barrier(0);
 
     // item i of this wave: band q0 + it / J, group slot it % J with it = wave·ITEMS + i (clamped)
     Group<DT> buf[ITEMS];
@@ -354,7 +359,7 @@ __global__ void __launch_bounds__(64 * MV_WAVES) mv_kernel(WeightView w, ActQ A,
         float* ld = reinterpret_cast<float*>(lq + NT * Gk * QS_LDS);
         float* las = ld + NT * 8 * Gk;
         int* ls16 = reinterpret_cast<int*>(las + NT * 8 * Gk);
-        f1_store<NT, HP>(pre, k, Gk, lq, ld, las, ls16, dummy);
+        if (pro) f1_store<NT, HP>(pre, k, Gk, lq, ld, las, ls16, dummy);
         aq = lq;
         ad = ld;
         as = las;
