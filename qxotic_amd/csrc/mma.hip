@@ -155,71 +155,65 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
         nvalid = __builtin_amdgcn_readfirstlane(gp.off[e + 1]) - crow0;
     }
 
-    // ---- global -> LDS copy of one stage (every wave takes every 4th 1 KB piece)
+    // ---- global -> LDS copy of one stage. Every wave issues a fixed set of 1 KB pieces: the weight chunks
+    // of its own row tile, the activation codes of K-steps 2·wave and 2·wave + 1, and one of the small
+    // pieces (headers, block scales, sums). Base addresses are computed once; a stage only adds offsets.
+    static_assert(TW == MMA_WAVES, "one row tile per wave");
+    static_assert(BN == 64, "one 1 KB piece per K-step half");
+    constexpr int NC = group_chunks(DT);
+    const int64_t Tw = T0 + wave < tiles ? T0 + wave : tiles - 1;             // this wave's row tile
+    const uint8_t* a_src = w.qs + (r0t + Tw) * G * (NC * CHUNK_STRIDE) + 16 * lane;
+    const int a_dst = S::A_OFF + wave * NCS * 512;
+    // headers: Q4_K / MXFP4 16 B per row, tiles 2·wave + q (waves 0, 1); Q6_K d, 8 rows per lane (wave 0)
+    const uint8_t* h_src;
+    if constexpr (DT != Q6_K) {
+        const int64_t T = T0 + 2 * (wave & 1) + q < tiles ? T0 + 2 * (wave & 1) + q : tiles - 1;
+        h_src = w.sc + ((r0t + T) * G * 32 + r) * 16;
+    } else {
+        const int64_t T = T0 + (lane >> 2) < tiles ? T0 + (lane >> 2) : tiles - 1;
+        h_src = w.sc + ((r0t + T) * G * 32 + 8 * (lane & 3)) * 2;
+    }
+    // GemmAct::b holds 16 f16 (32 bytes) per (K-step, token slot)
+    const uint8_t* b_src = reinterpret_cast<const uint8_t*>(A.b) + ((int64_t) (2 * wave) * A.NP + n0) * 32 + 32 * lane;
+    const int64_t b_kstep = (int64_t) A.NP * 32;                                  // bytes per K-step
+    const float* dx_src = A.dx + (int64_t) (lane >> 4) * A.NP + n0 + 4 * (lane & 15);
+    constexpr int SWB = S::SW * 2;                                                // sum bytes per token per plane
+    constexpr int SPC = S::SW > 0 ? BN * SWB / 1024 : 0;                          // 1 KB pieces per plane
+    const int s_pl = SPC == 1 ? (wave >> 1) & 1 : wave >> 1, s_p = SPC == 1 ? 0 : wave & 1;
+    const uint8_t* s_src = S::SW > 0 ? reinterpret_cast<const uint8_t*>(s_pl ? A.slo : A.shi) + (int64_t) n0 * SWB + s_p * 1024 + 16 * lane
+                                     : nullptr;
     auto issue = [&](int st, unsigned char* buf) {
         const int g = st >> 1, h2 = st & 1;
-        int piece = 0;
-        auto mine = [&]() { return (piece++ % MMA_WAVES) == wave; };
-        // weight chunks: tile tt, chunk pair p: 1 KB contiguous
-        constexpr int NC = group_chunks(DT);
-        for (int tt = 0; tt < TW; tt++) {
-            int64_t T = T0 + tt;
-            T = T < tiles ? T : tiles - 1;
-            const uint8_t* gbase = w.qs + ((r0t + T) * G + g) * (NC * CHUNK_STRIDE);
-            unsigned char* lbase = buf + S::A_OFF + tt * NCS * 512;
-            if constexpr (DT != Q6_K) {   // Q4_K chunks 4h2..4h2+3 (sub-block pairs), MXFP4 blocks 4h2..4h2+3
+        const uint8_t* ag = a_src + (int64_t) g * (NC * CHUNK_STRIDE);
+        if constexpr (DT != Q6_K) {   // Q4_K chunks 4h2..4h2+3 (sub-block pairs), MXFP4 blocks 4h2..4h2+3
 #pragma unroll
-                for (int p = 0; p < 2; p++)
-                    if (mine()) dma16(gbase + (4 * h2 + 2 * p) * CHUNK_STRIDE + 16 * lane, lbase + 2 * p * 512);
-            } else {
-                // ql chunks 4h2..4h2+3 (2 pieces), qh chunks 8+2h2, 9+2h2 (1 piece), scales chunk 12 (half)
+            for (int p = 0; p < 2; p++) dma16(ag + (4 * h2 + 2 * p) * CHUNK_STRIDE, buf + a_dst + 2 * p * 512);
+        } else {   // ql chunks 4h2..4h2+3, qh chunks 8+2h2, 9+2h2, the scales chunk 12 (512 B)
 #pragma unroll
-                for (int p = 0; p < 2; p++)
-                    if (mine()) dma16(gbase + (4 * h2 + 2 * p) * CHUNK_STRIDE + 16 * lane, lbase + 2 * p * 512);
-                if (mine()) dma16(gbase + (8 + 2 * h2) * CHUNK_STRIDE + 16 * lane, lbase + 4 * 512);
-                if (mine() && lane < 32) dma16(gbase + 12 * CHUNK_STRIDE + 16 * lane, lbase + 6 * 512);
-            }
+            for (int p = 0; p < 2; p++) dma16(ag + (4 * h2 + 2 * p) * CHUNK_STRIDE, buf + a_dst + 2 * p * 512);
+            dma16(ag + (8 + 2 * h2) * CHUNK_STRIDE, buf + a_dst + 4 * 512);
+            if (lane < 32) dma16(ag + 12 * CHUNK_STRIDE, buf + a_dst + 6 * 512);
         }
-        // headers: Q4_K / MXFP4 16 B per row (2 tiles per piece); Q6_K d (2 B per row, 16 tiles per piece)
-        if constexpr (DT != Q6_K) {
-            for (int tp = 0; tp < TW / 2; tp++) {
-                if (!mine()) continue;
-                int64_t T = T0 + 2 * tp + q;
-                T = T < tiles ? T : tiles - 1;
-                dma16(w.sc + (((r0t + T) * G + g) * 32 + r) * 16, buf + S::H_OFF + tp * 1024);
-            }
-        } else if (h2 == 1) {
-            if (mine() && lane < 4 * TW) {
-                int64_t T = T0 + (lane >> 2);
-                T = T < tiles ? T : tiles - 1;
-                dma16(w.sc + (((r0t + T) * G + g) * 32 + 8 * (lane & 3)) * 2, buf + S::H_OFF);
-            }
-        }
-        // activation codes: ksteps 16g + 8h2 .. +7; in LDS each K-step's two 8-element halves are split
-        // into planes [kk][half q][BN tokens][16 B] so a fragment read is 512 contiguous bytes per half-wave
+        // activation codes: K-steps 8·st + 2·wave, +1; in LDS each K-step's two 8-element halves are split into
+        // planes [kk][half][BN tokens][16 B] so a fragment read is 512 contiguous bytes per half-wave
         // (conflict-free); the copy gathers the halves from the token-interleaved global layout
-        static_assert(BN == 64, "one 1 KB piece per K-step half");
-        for (int kk = 0; kk < 8; kk++) {
-            const uint8_t* src = reinterpret_cast<const uint8_t*>(A.b + ((int64_t) (16 * g + 8 * h2 + kk) * A.NP + n0) * 16);
+        const uint8_t* bs = b_src + (int64_t) (8 * st) * b_kstep;
+#pragma unroll
+        for (int kl = 0; kl < 2; kl++)
 #pragma unroll
             for (int p = 0; p < 2; p++)
-                if (mine()) dma16(src + 32 * lane + 16 * p, buf + S::B_OFF + (2 * kk + p) * 1024);
+                dma16(bs + kl * b_kstep + 16 * p, buf + S::B_OFF + (2 * (2 * wave + kl) + p) * 1024);
+        if constexpr (DT != Q6_K) {
+            if (wave < 2) dma16(h_src + (int64_t) g * 32 * 16, buf + S::H_OFF + wave * 1024);
+        } else {
+            if (wave == 0 && h2 == 1 && lane < 4 * TW) dma16(h_src + (int64_t) g * 32 * 2, buf + S::H_OFF);
         }
         // block scales: 4 blocks x BN tokens (f32)
-        for (int p = 0; p < BN / 64; p++) {
-            if (!mine()) continue;
-            const int blk = (p * 64 + lane) / (BN / 4), tok = 4 * ((p * 64 + lane) % (BN / 4));
-            dma16(A.dx + (int64_t) (8 * g + 4 * h2 + blk) * A.NP + n0 + tok, buf + S::DX_OFF + p * 1024);
-        }
+        if (wave == 2) dma16(dx_src + (int64_t) (4 * st) * A.NP, buf + S::DX_OFF);
         // sums: Q4_K needs them at the super-block's end (odd stage), Q6_K at its start (even stage)
-        if (S::SW > 0 && (DT == Q4_K) == (h2 == 1)) {
-            constexpr int SWB = S::SW * 2;   // bytes per token per plane
-            for (int pl = 0; pl < 2; pl++) {
-                const _Float16* src = (pl ? A.slo : A.shi) + ((int64_t) g * A.NP + n0) * S::SW;
-                for (int p = 0; p < BN * SWB / 1024; p++)
-                    if (mine())
-                        dma16((const uint8_t*) src + p * 1024 + 16 * lane, buf + S::S_OFF + pl * BN * SWB + p * 1024);
-            }
+        if constexpr (S::SW > 0) {
+            if ((DT == Q4_K) == (h2 == 1) && (SPC == 2 || wave == 1 || wave == 3))
+                dma16(s_src + (int64_t) g * A.NP * SWB, buf + S::S_OFF + s_pl * BN * SWB + s_p * 1024);
         }
     };
 
