@@ -294,12 +294,14 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
             __builtin_amdgcn_sched_barrier(0);   // keep the reads ahead of the compute
             // this stage's LDS reads are all issued: start copying the next stage into the other buffer
             if (st + 1 < nst) issue(st + 1, smem + ((st + 1) & 1) * S::BYTES);
+            // Software pipeline over the stage's 4 blocks: block bl's products go out on the matrix cores into
+            // D[bl & 1] before block bl-1's scale FMAs, which then run while the matrix cores work.
+            floatx16 Dp[2][RT][CT];
 #pragma unroll
-            for (int gpl = 0; gpl < 2; gpl++) {
-                const uint4* ch = chs[gpl];
-#pragma unroll
-                for (int sub = 0; sub < 2; sub++) {
-                    const int bl = 2 * gpl + sub;
+            for (int bl = 0; bl < 5; bl++) {
+                if (bl < 4) {
+                    const uint4* ch = chs[bl >> 1];
+                    const int sub = bl & 1;
                     half8 af[RT][2];
 #pragma unroll
                     for (int i = 0; i < RT; i++) {
@@ -319,10 +321,18 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
 #pragma unroll
                         for (int j = 0; j < CT; j++) {
                             floatx16 D = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i][0], bfs[bl][j][0], floatx16{}, 0, 0, 0);
-                            D = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i][1], bfs[bl][j][1], D, 0, 0, 0);
-#pragma unroll
-                            for (int e = 0; e < 16; e++) accs[i][j][e] = fmaf(D[e], dxs[bl][j], accs[i][j][e]);
+                            Dp[bl & 1][i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i][1], bfs[bl][j][1], D, 0, 0, 0);
                         }
+                }
+                if (bl > 0) {
+                    const int pb = bl - 1;
+#pragma unroll
+                    for (int i = 0; i < RT; i++)
+#pragma unroll
+                        for (int j = 0; j < CT; j++)
+#pragma unroll
+                            for (int e = 0; e < 16; e++)
+                                accs[i][j][e] = fmaf(Dp[pb & 1][i][j][e], dxs[pb][j], accs[i][j][e]);
                 }
             }
             if (h2 == 1) {   // super-block end: d, then the mins on the matrix cores
