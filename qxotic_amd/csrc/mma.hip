@@ -237,8 +237,8 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
 
     for (int st = 0; st < nst; st++) {
         unsigned char* buf = smem + (st & 1) * S::BYTES;
-        // Q4_K issues the next stage's copy itself, after its last LDS read of this stage
-        if (DT != Q4_K && st + 1 < nst) issue(st + 1, smem + ((st + 1) & 1) * S::BYTES);
+        // each type issues the next stage's copy itself, after its last LDS read of this stage: the compiler
+        // makes any LDS read that follows a global -> LDS copy wait for that copy
         const int h2 = st & 1;
         const unsigned char* LA = buf + S::A_OFF;
         const unsigned char* LB = buf + S::B_OFF;
@@ -365,89 +365,135 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
                 }
             }
         } else if constexpr (DT == MXFP4) {   // group of 8 blocks; stage h2 = blocks 4h2..4h2+3
-            uint4 hdr[RT];
+            // every LDS read of the stage up front, then the next stage's copy, then the compute
+            uint4 hdr[RT], chs[RT][4];
+            half8 bfs[4][CT][2];
+            float dxs[4][CT];
+            float sg[RT][16];
 #pragma unroll
-            for (int i = 0; i < RT; i++)
+            for (int i = 0; i < RT; i++) {
                 hdr[i] = *reinterpret_cast<const uint4*>(buf + S::H_OFF + ((wave * RT + i) * 32 + r) * 16);
 #pragma unroll
-            for (int bl = 0; bl < 4; bl++) {
-                half8 af[RT][2];
+                for (int bl = 0; bl < 4; bl++)
+                    chs[i][bl] = *reinterpret_cast<const uint4*>(LA + ((wave * RT + i) * NCS + bl) * 512 + 16 * r);
+            }
 #pragma unroll
-                for (int i = 0; i < RT; i++) {
-                    const uint4 ch = *reinterpret_cast<const uint4*>(LA + ((wave * RT + i) * NCS + bl) * 512 + 16 * r);
-                    const int b = 4 * h2 + bl;
-                    const int eb = (int) (((b < 4 ? hdr[i].x : hdr[i].y) >> (8 * (b & 3))) & 0xffu);
-                    const int er = (int) (hdr[i].z & 0xffu);
-                    const uint32_t s2 = mx_scale2(eb - er);
-                    af[i][0] = mx_frag(ch.x, ch.y, 4 * q, s2);
-                    af[i][1] = mx_frag(ch.z, ch.w, 4 * q, s2);
-                }
-                half8 bf[CT][2];
-                float dxv[CT];
+            for (int bl = 0; bl < 4; bl++)
 #pragma unroll
                 for (int j = 0; j < CT; j++) {
 #pragma unroll
                     for (int ks = 0; ks < 2; ks++)
-                        bf[j][ks] = *reinterpret_cast<const half8*>(LB + ((2 * bl + ks) * 2 + q) * BN * 16 + (32 * j + r) * 16);
-                    dxv[j] = LDX[bl * BN + 32 * j + r];
+                        bfs[bl][j][ks] = *reinterpret_cast<const half8*>(LB + ((2 * bl + ks) * 2 + q) * BN * 16 + (32 * j + r) * 16);
+                    dxs[bl][j] = LDX[bl * BN + 32 * j + r];
                 }
+            if (h2 == 1) {   // group end: 2^(e_ref - 128) of the 16 output rows this lane holds
+#pragma unroll
+                for (int i = 0; i < RT; i++) {
+                    const unsigned char* H = buf + S::H_OFF + (wave * RT + i) * 32 * 16;
+#pragma unroll
+                    for (int e = 0; e < 16; e++) sg[i][e] = e8m0_half(H[(8 * (e >> 2) + 4 * q + (e & 3)) * 16 + 8]);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            if (st + 1 < nst) issue(st + 1, smem + ((st + 1) & 1) * S::BYTES);
+            // software pipeline: block bl's products go out before block bl-1's scale FMAs
+            floatx16 Dp[2][RT][CT];
+#pragma unroll
+            for (int bl = 0; bl < 5; bl++) {
+                if (bl < 4) {
+                    half8 af[RT][2];
+#pragma unroll
+                    for (int i = 0; i < RT; i++) {
+                        const uint4 ch = chs[i][bl];
+                        const int b = 4 * h2 + bl;
+                        const int eb = (int) (((b < 4 ? hdr[i].x : hdr[i].y) >> (8 * (b & 3))) & 0xffu);
+                        const int er = (int) (hdr[i].z & 0xffu);
+                        const uint32_t s2 = mx_scale2(eb - er);
+                        af[i][0] = mx_frag(ch.x, ch.y, 4 * q, s2);
+                        af[i][1] = mx_frag(ch.z, ch.w, 4 * q, s2);
+                    }
+#pragma unroll
+                    for (int i = 0; i < RT; i++)
+#pragma unroll
+                        for (int j = 0; j < CT; j++) {
+                            floatx16 D = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i][0], bfs[bl][j][0], floatx16{}, 0, 0, 0);
+                            Dp[bl & 1][i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i][1], bfs[bl][j][1], D, 0, 0, 0);
+                        }
+                }
+                if (bl > 0) {
+                    const int pb = bl - 1;
+#pragma unroll
+                    for (int i = 0; i < RT; i++)
+#pragma unroll
+                        for (int j = 0; j < CT; j++)
+#pragma unroll
+                            for (int e = 0; e < 16; e++)
+                                accs[i][j][e] = fmaf(Dp[pb & 1][i][j][e], dxs[pb][j], accs[i][j][e]);
+                }
+            }
+            if (h2 == 1) {   // group end: acc += 2^(e_ref - 128) · accs
 #pragma unroll
                 for (int i = 0; i < RT; i++)
 #pragma unroll
                     for (int j = 0; j < CT; j++) {
-                        floatx16 D = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i][0], bf[j][0], floatx16{}, 0, 0, 0);
-                        D = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i][1], bf[j][1], D, 0, 0, 0);
 #pragma unroll
-                        for (int e = 0; e < 16; e++) accs[i][j][e] = fmaf(D[e], dxv[j], accs[i][j][e]);
-                    }
-            }
-            if (h2 == 1) {   // group end: acc += 2^(e_ref - 128) · accs
-#pragma unroll
-                for (int i = 0; i < RT; i++) {
-                    const unsigned char* H = buf + S::H_OFF + (wave * RT + i) * 32 * 16;
-                    float sg[16];
-#pragma unroll
-                    for (int e = 0; e < 16; e++) sg[e] = e8m0_half(H[(8 * (e >> 2) + 4 * q + (e & 3)) * 16 + 8]);
-#pragma unroll
-                    for (int j = 0; j < CT; j++) {
-#pragma unroll
-                        for (int e = 0; e < 16; e++) acc[i][j][e] = fmaf(sg[e], accs[i][j][e], acc[i][j][e]);
+                        for (int e = 0; e < 16; e++) acc[i][j][e] = fmaf(sg[i][e], accs[i][j][e], acc[i][j][e]);
                         accs[i][j] = floatx16{};
                     }
-                }
             }
         } else {   // Q6_K: stage h2 = half h of the super-block, blocks j = 0..3 (elements 128h + 32j + l)
-            const int8_t* scb = reinterpret_cast<const int8_t*>(LA);   // + tile offset below
-            if (h2 == 0) {
-                // accs = −8·Σ_t sc_t·xs_t (the −32 offset, in units of 1/4), one 32x32x16 step hi + lo
-#pragma unroll
-                for (int i = 0; i < RT; i++) {
-                    const int8_t* sc16 = scb + ((wave * RT + i) * NCS + 6) * 512 + 16 * r + 8 * q;
-                    half8 ao;
-#pragma unroll
-                    for (int e = 0; e < 8; e++) ao[e] = (_Float16) (-8.0f * (float) sc16[e]);
-#pragma unroll
-                    for (int j = 0; j < CT; j++) {
-                        const unsigned char* SP = buf + S::S_OFF + (32 * j + r) * 32 + 16 * q;
-                        const half8 bhi = *reinterpret_cast<const half8*>(SP);
-                        const half8 blo = *reinterpret_cast<const half8*>(SP + BN * 32);
-                        accs[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ao, bhi, floatx16{}, 0, 0, 0);
-                        accs[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ao, blo, accs[i][j], 0, 0, 0);
-                    }
-                }
-            }
+            // every LDS read of the stage up front, then the next stage's copy, then the compute
             uint4 ql[RT][2], qh[RT];
             int8_t scl[RT][4];
+            uint2 sco[RT];             // h2 = 0: the 8 scales of row r's 16-groups 8q..8q+7 (offset term)
+            half8 bhi[CT], blo[CT];    // h2 = 0: the sums' fragments
+            half8 bfs[4][CT][2];
+            float dxs[4][CT];
 #pragma unroll
             for (int i = 0; i < RT; i++) {
                 const unsigned char* T = LA + (wave * RT + i) * NCS * 512 + 16 * r;
                 ql[i][0] = *reinterpret_cast<const uint4*>(T + (0 + q) * 512);
                 ql[i][1] = *reinterpret_cast<const uint4*>(T + (2 + q) * 512);
                 qh[i] = *reinterpret_cast<const uint4*>(T + (4 + q) * 512);
-                const int8_t* sc16 = reinterpret_cast<const int8_t*>(LA + ((wave * RT + i) * NCS + 6) * 512 + 16 * r);
+                const int8_t* sc16 = reinterpret_cast<const int8_t*>(T + 6 * 512);
 #pragma unroll
                 for (int jb = 0; jb < 4; jb++) scl[i][jb] = sc16[8 * h2 + 2 * jb + q];
+                if (h2 == 0) sco[i] = *reinterpret_cast<const uint2*>(sc16 + 8 * q);
             }
+            if (h2 == 0) {
+#pragma unroll
+                for (int j = 0; j < CT; j++) {
+                    const unsigned char* SP = buf + S::S_OFF + (32 * j + r) * 32 + 16 * q;
+                    bhi[j] = *reinterpret_cast<const half8*>(SP);
+                    blo[j] = *reinterpret_cast<const half8*>(SP + BN * 32);
+                }
+            }
+#pragma unroll
+            for (int jb = 0; jb < 4; jb++)
+#pragma unroll
+                for (int j = 0; j < CT; j++) {
+#pragma unroll
+                    for (int ks = 0; ks < 2; ks++)
+                        bfs[jb][j][ks] = *reinterpret_cast<const half8*>(LB + ((2 * jb + ks) * 2 + q) * BN * 16 + (32 * j + r) * 16);
+                    dxs[jb][j] = LDX[jb * BN + 32 * j + r];
+                }
+            if (h2 == 0) {
+                // accs = −8·Σ_t sc_t·xs_t (the −32 offset, in units of 1/4), one 32x32x16 step hi + lo
+#pragma unroll
+                for (int i = 0; i < RT; i++) {
+                    half8 ao;
+#pragma unroll
+                    for (int e = 0; e < 8; e++)
+                        ao[e] = (_Float16) (-8.0f * (float) (int8_t) (((e < 4 ? sco[i].x : sco[i].y) >> (8 * (e & 3))) & 0xffu));
+#pragma unroll
+                    for (int j = 0; j < CT; j++) {
+                        accs[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ao, bhi[j], floatx16{}, 0, 0, 0);
+                        accs[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ao, blo[j], accs[i][j], 0, 0, 0);
+                    }
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            if (st + 1 < nst) issue(st + 1, smem + ((st + 1) & 1) * S::BYTES);
 #pragma unroll
             for (int jb = 0; jb < 4; jb++) {
                 half8 a1[RT][2], a2[RT][2];
@@ -471,28 +517,19 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
                     a2[i][0] = frag8(mv(Q.x), mv(Q.y), vmask_qh, mul2, add2);
                     a2[i][1] = frag8(mv(Q.z), mv(Q.w), vmask_qh, mul2, add2);
                 }
-                half8 bf[CT][2];
-                float dxv[CT];
-#pragma unroll
-                for (int j = 0; j < CT; j++) {
-#pragma unroll
-                    for (int ks = 0; ks < 2; ks++)
-                        bf[j][ks] = *reinterpret_cast<const half8*>(LB + ((2 * jb + ks) * 2 + q) * BN * 16 + (32 * j + r) * 16);
-                    dxv[j] = LDX[jb * BN + 32 * j + r];
-                }
 #pragma unroll
                 for (int i = 0; i < RT; i++)
 #pragma unroll
                     for (int j = 0; j < CT; j++) {
-                        floatx16 D = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1[i][0], bf[j][0], floatx16{}, 0, 0, 0);
-                        D = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1[i][1], bf[j][1], D, 0, 0, 0);
-                        D = __builtin_amdgcn_mfma_f32_32x32x16_f16(a2[i][0], bf[j][0], D, 0, 0, 0);
-                        D = __builtin_amdgcn_mfma_f32_32x32x16_f16(a2[i][1], bf[j][1], D, 0, 0, 0);
+                        floatx16 D = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1[i][0], bfs[jb][j][0], floatx16{}, 0, 0, 0);
+                        D = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1[i][1], bfs[jb][j][1], D, 0, 0, 0);
+                        D = __builtin_amdgcn_mfma_f32_32x32x16_f16(a2[i][0], bfs[jb][j][0], D, 0, 0, 0);
+                        D = __builtin_amdgcn_mfma_f32_32x32x16_f16(a2[i][1], bfs[jb][j][1], D, 0, 0, 0);
 #pragma unroll
-                        for (int e = 0; e < 16; e++) accs[i][j][e] = fmaf(D[e], dxv[j], accs[i][j][e]);
+                        for (int e = 0; e < 16; e++) accs[i][j][e] = fmaf(D[e], dxs[jb][j], accs[i][j][e]);
                     }
             }
-            if (h2 == 1) {   // super-block end: acc += 4d · accs
+            if (h2 == 1) {   // super-block end: acc += 4d · accs (d read here: the next copy has had the stage)
 #pragma unroll
                 for (int i = 0; i < RT; i++) {
                     const unsigned char* H = buf + S::H_OFF + (wave * RT + i) * 32 * 2;
