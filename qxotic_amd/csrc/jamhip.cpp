@@ -166,10 +166,10 @@ bool env_true(const char* name) {
 }
 
 // The matrix-core GEMM covers Q4_K, Q6_K (k a multiple of 256) and MXFP4 on 32-row-aligned views
-// (launch_gemm_mma).
+// (launch_gemm_mma), for k up to the activation prep's limit (gemm_prep_fits).
 bool mma_path(int dt, int k, const WeightView& wv) {
     if (env_true("JAM_HIP_NO_MMA")) return false;
-    return (((dt == Q4_K || dt == Q6_K) && k % 256 == 0) || dt == MXFP4) && (wv.r0 & 31) == 0;
+    return (((dt == Q4_K || dt == Q6_K) && k % 256 == 0) || dt == MXFP4) && (wv.r0 & 31) == 0 && gemm_prep_fits(k);
 }
 
 // Quantize A (device, f32 [n][lda]) and run the matmul into C (device, [n][ldc]). Decode-sized calls

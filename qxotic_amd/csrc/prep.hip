@@ -108,11 +108,11 @@ JAMHIP_DEV int perm8(int j) { return j == 1 ? 2 : j == 2 ? 1 : j == 5 ? 6 : j ==
 
 int gemm_sums_kind(int dt) { return dt == Q4_K || dt == Q4_0 ? 1 : dt == Q6_K ? 2 : 0; }
 
-// Two passes. Pass A, one workgroup per (256-element chunk, token slot): jam's F2 quantization of the
-// chunk's 8 blocks (f2_lane, bit-exact), the codes scattered into the fragment order of GemmAct::b, the
-// block scales and per-16 sums parked block-major in scratch, and the chunk's largest |sum| (SK 1: per-32
-// xs0 + xs1, jam's fl(xs0 + xs1); SK 2: per-16; SK 0: none). Pass B, one thread per (token slot, block):
-// the token's power of two from its chunks' maxima, then the scaled block scale and sums.
+// One workgroup per token slot (4 waves, a wave per 256-element chunk at a time): jam's F2 quantization of
+// the slot's activation row (f2_lane, bit-exact), the codes scattered into the fragment order of
+// GemmAct::b, the block scales and per-16 sums parked in LDS together with the row's largest |sum| (SK 1:
+// per-32 xs0 + xs1, jam's fl(xs0 + xs1); SK 2: per-16; SK 0: none); then the slot's power of two from that
+// maximum and the scaled block scales and sums.
 // Grouped form (gmap non-null): slot t belongs to expert gmap[t / 64] (-1: padding) and holds that
 // expert's row t - gpoff[e] (CSR row goff[e] + t - gpoff[e]) while that is below its row count.
 JAMHIP_DEV int prep_src(int t, int n, const int* gmap, const int* goff, const int* gpoff) {
@@ -123,126 +123,120 @@ JAMHIP_DEV int prep_src(int t, int n, const int* gmap, const int* goff, const in
     return l < goff[ex + 1] - goff[ex] ? goff[ex] + l : -1;
 }
 
-// Pass A: each lane holds 4 consecutive elements of one block (8 lanes per block, a wave = one 256-element
-// chunk, 4 chunks per workgroup). F2 exactly as f2_lane: the block max over the 8 lanes, d = max/127,
-// inv = 127/max, q = sat8(rne(x·inv)) with NaN/overflow -> -128, and the per-16 sums in
-// _mm512_reduce_add_ps's pairing (distance 8, 4, 2, 1): distances 8 and 4 cross lanes (xor 2, xor 1),
-// 2 and 1 stay in the lane.
+template <int CTRL> JAMHIP_DEV float dppf(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+constexpr int PREP_MAX_KP = 65536;   // LDS: Kp/32 + Kp/16 floats per slot
+
+// Per chunk: each lane holds 4 consecutive elements of one block (8 lanes per block, a wave = one
+// 256-element chunk). F2 exactly as f2_lane: the block max over the 8 lanes, d = max/127, inv = 127/max,
+// q = sat8(rne(x·inv)) with NaN/overflow -> -128, and the per-16 sums in _mm512_reduce_add_ps's pairing
+// (distance 8, 4, 2, 1): distances 8 and 4 cross lanes (xor 2, xor 1: DPP quad permutes), 2 and 1 stay in
+// the lane.
 template <int SK>
-__global__ void __launch_bounds__(256) gemm_prep_a(const float* __restrict__ a, int lda, int n, int k, int Kp, int NP,
-                                                   _Float16* __restrict__ bq, float* __restrict__ tdb,
-                                                   float* __restrict__ txs, float* __restrict__ tmx,
-                                                   const int* __restrict__ gmap, const int* __restrict__ goff,
-                                                   const int* __restrict__ gpoff, int vec) {
-    const int t = blockIdx.y, nbk = k >> 5, lane = threadIdx.x & 63;
-    const int ch = blockIdx.x * 4 + (threadIdx.x >> 6);   // this wave's 256-element chunk
-    if (ch >= (Kp >> 8)) return;                           // whole wave
+__global__ void __launch_bounds__(256) gemm_prep(const float* __restrict__ a, int lda, int n, int k, int Kp, int NP,
+                                                 _Float16* __restrict__ bq, float* __restrict__ dx,
+                                                 _Float16* __restrict__ shi, _Float16* __restrict__ slo,
+                                                 float* __restrict__ es, const int* __restrict__ gmap,
+                                                 const int* __restrict__ goff, const int* __restrict__ gpoff, int vec) {
+    extern __shared__ float lsm[];   // [Kp/32] block scales, [Kp/16] per-16 sums, [4] wave maxima
+    float* ldb = lsm;
+    float* lxs = lsm + (Kp >> 5);
+    float* lmx = lxs + (Kp >> 4);
+    const int t = blockIdx.x, nbk = k >> 5, lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nch = Kp >> 8;
     const int src = prep_src(t, n, gmap, goff, gpoff);
-    const int b = 8 * ch + (lane >> 3), j = lane & 7;      // block, lane within the block
-    float x[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (src >= 0 && b < nbk) {
-        const float* p = a + (int64_t) src * lda + 32 * b + 4 * j;
-        if (vec) {   // a and lda 16-byte aligned (the launcher checks)
-            const float4 v = *reinterpret_cast<const float4*>(p);
-            x[0] = v.x, x[1] = v.y, x[2] = v.z, x[3] = v.w;
-        } else {
-            x[0] = p[0], x[1] = p[1], x[2] = p[2], x[3] = p[3];
+    const int j = lane & 7;   // lane within the block
+    float m2 = 0.0f;
+    for (int ch = wave; ch < nch; ch += 4) {
+        const int b = 8 * ch + (lane >> 3);
+        float x[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (src >= 0 && b < nbk) {
+            const float* p = a + (int64_t) src * lda + 32 * b + 4 * j;
+            if (vec) {   // a and lda 16-byte aligned (the launcher checks)
+                const float4 v = *reinterpret_cast<const float4*>(p);
+                x[0] = v.x, x[1] = v.y, x[2] = v.z, x[3] = v.w;
+            } else {
+                x[0] = p[0], x[1] = p[1], x[2] = p[2], x[3] = p[3];
+            }
+        }
+        float mx = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
+        mx = fmaxf(mx, __shfl_xor(mx, 4));
+        mx = fmaxf(mx, dppf<0x4E>(mx));   // lane ^ 2
+        mx = fmaxf(mx, dppf<0xB1>(mx));   // lane ^ 1
+        const float db = mx / 127.0f;
+        const float inv = mx > 0.0f ? 127.0f / mx : 0.0f;
+        int qv[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const float p = x[u] * inv;
+            qv[u] = !(p > -2147483648.0f && p < 2147483648.0f) ? -128 : (int) fminf(fmaxf(rintf(p), -128.0f), 127.0f);
+        }
+        // codes: elements 4j..4j+3 -> K-step (j >> 1) & 1, half j >> 2, slots 4(j & 1) + {0, 2, 1, 3}
+        typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+        const half4 hv = {(_Float16) qv[0], (_Float16) qv[2], (_Float16) qv[1], (_Float16) qv[3]};
+        *reinterpret_cast<half4*>(bq + ((int64_t) (2 * b + ((j >> 1) & 1)) * NP + t) * 16 + 8 * (j >> 2) + 4 * (j & 1)) = hv;
+        // per-16 sums: distance 8 (xor 2), distance 4 (xor 1), then in-lane distance 2 and 1
+        float s[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) s[u] = dppf<0x4E>(x[u]) + x[u];
+#pragma unroll
+        for (int u = 0; u < 4; u++) s[u] = dppf<0xB1>(s[u]) + s[u];
+        const float xs16 = (s[0] + s[2]) + (s[1] + s[3]);
+        if (j == 0) ldb[b] = db;
+        if ((j & 3) == 0) lxs[2 * b + (j >> 2)] = xs16;
+        if constexpr (SK != 0) {
+            const float other = __shfl_xor(xs16, 4);   // the block's other half
+            m2 = fmaxf(m2, SK == 1 ? fabsf((j < 4) ? xs16 + other : other + xs16) : fabsf(xs16));
         }
     }
-    float mx = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
-    mx = fmaxf(mx, __shfl_xor(mx, 4));
-    mx = fmaxf(mx, __shfl_xor(mx, 2));
-    mx = fmaxf(mx, __shfl_xor(mx, 1));
-    const float db = mx / 127.0f;
-    const float inv = mx > 0.0f ? 127.0f / mx : 0.0f;
-    int qv[4];
-#pragma unroll
-    for (int u = 0; u < 4; u++) {
-        const float p = x[u] * inv;
-        qv[u] = !(p > -2147483648.0f && p < 2147483648.0f) ? -128 : (int) fminf(fmaxf(rintf(p), -128.0f), 127.0f);
-    }
-    // codes: elements 4j..4j+3 -> K-step (j >> 1) & 1, half j >> 2, slots 4(j & 1) + {0, 2, 1, 3}
-    typedef _Float16 half4 __attribute__((ext_vector_type(4)));
-    const half4 hv = {(_Float16) qv[0], (_Float16) qv[2], (_Float16) qv[1], (_Float16) qv[3]};
-    *reinterpret_cast<half4*>(bq + ((int64_t) (2 * b + ((j >> 1) & 1)) * NP + t) * 16 + 8 * (j >> 2) + 4 * (j & 1)) = hv;
-    // per-16 sums: distance 8 (xor 2), distance 4 (xor 1), then in-lane distance 2 and 1
-    float s[4];
-#pragma unroll
-    for (int u = 0; u < 4; u++) s[u] = __shfl_xor(x[u], 2) + x[u];
-#pragma unroll
-    for (int u = 0; u < 4; u++) s[u] = __shfl_xor(s[u], 1) + s[u];
-    const float xs16 = (s[0] + s[2]) + (s[1] + s[3]);
-    if (j == 0) tdb[(int64_t) b * NP + t] = db;
-    if ((j & 3) == 0) txs[(int64_t) (2 * b + (j >> 2)) * NP + t] = xs16;
     if constexpr (SK != 0) {
-        const float other = __shfl_xor(xs16, 4);   // the block's other half
-        float m2 = SK == 1 ? fabsf((j < 4) ? xs16 + other : other + xs16) : fabsf(xs16);
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) m2 = fmaxf(m2, __shfl_xor(m2, o));
-        if (lane == 0) tmx[(int64_t) ch * NP + t] = m2;
+        if (lane == 0) lmx[wave] = m2;
     }
-}
-
-// Pass E: the token's power of two from its chunks' maxima (the largest |sum| lands in [2^13, 2^14); zero
-// or non-finite sums keep 2^0): es[t] = 2^e_t, down[t] = 2^-e_t. A workgroup takes 64 token slots, its 4
-// waves a quarter of the chunks each.
-__global__ void __launch_bounds__(256) gemm_prep_e(int Kp, int NP, int sk, const float* __restrict__ tmx,
-                                                   float* __restrict__ es, float* __restrict__ down) {
-    __shared__ float part[4][64];
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, t = blockIdx.x * 64 + lane, nch = Kp >> 8;
-    float mx = 0.0f;
-    if (sk != 0 && t < NP)
-        for (int c = wv; c < nch; c += 4) mx = fmaxf(mx, tmx[(int64_t) c * NP + t]);
-    part[wv][lane] = mx;
     __syncthreads();
-    if (wv != 0 || t >= NP) return;
-    mx = fmaxf(fmaxf(part[0][lane], part[1][lane]), fmaxf(part[2][lane], part[3][lane]));
+    // the slot's power of two: the largest |sum| lands in [2^13, 2^14); zero or non-finite sums keep 2^0
     int ex = 0;
-    if (mx > 0.0f && mx <= 3.0e38f) {
-        frexpf(mx, &ex);
-        ex -= 14;
+    if constexpr (SK != 0) {
+        const float mx = fmaxf(fmaxf(lmx[0], lmx[1]), fmaxf(lmx[2], lmx[3]));
+        if (mx > 0.0f && mx <= 3.0e38f) {
+            frexpf(mx, &ex);
+            ex -= 14;
+        }
     }
-    es[t] = ldexpf(1.0f, ex);
-    down[t] = ldexpf(1.0f, -ex);
-}
-
-// Pass B, one thread per (token slot, block): the scaled block scale and sums.
-template <int SK>
-__global__ void __launch_bounds__(256) gemm_prep_b(int NP, const float* __restrict__ tdb, const float* __restrict__ txs,
-                                                   const float* __restrict__ down_t, float* __restrict__ dx,
-                                                   _Float16* __restrict__ shi, _Float16* __restrict__ slo) {
-    const int t = blockIdx.x * 256 + threadIdx.x, b = blockIdx.y;
-    if (t >= NP) return;
-    const float down = down_t[t];
-    dx[(int64_t) b * NP + t] = tdb[(int64_t) b * NP + t] * down;
-    const float x0 = txs[(int64_t) (2 * b) * NP + t], x1 = txs[(int64_t) (2 * b + 1) * NP + t];
+    const float down = ldexpf(1.0f, -ex);
+    if (threadIdx.x == 0) es[t] = ldexpf(1.0f, ex);
     auto put = [&](int64_t o, float v) {
         const _Float16 h = (_Float16) v;
         shi[o] = h;
         slo[o] = (_Float16) (v - (float) h);
     };
-    if constexpr (SK == 1) put(((int64_t) (b >> 3) * NP + t) * 8 + (b & 7), (x0 + x1) * down);
-    if constexpr (SK == 2) {
-        put(((int64_t) (b >> 3) * NP + t) * 16 + 2 * (b & 7), x0 * down);
-        put(((int64_t) (b >> 3) * NP + t) * 16 + 2 * (b & 7) + 1, x1 * down);
+    for (int b = threadIdx.x; b < (Kp >> 5); b += 256) {
+        dx[(int64_t) b * NP + t] = ldb[b] * down;
+        const float x0 = lxs[2 * b], x1 = lxs[2 * b + 1];
+        if constexpr (SK == 1) put(((int64_t) (b >> 3) * NP + t) * 8 + (b & 7), (x0 + x1) * down);
+        if constexpr (SK == 2) {
+            put(((int64_t) (b >> 3) * NP + t) * 16 + 2 * (b & 7), x0 * down);
+            put(((int64_t) (b >> 3) * NP + t) * 16 + 2 * (b & 7) + 1, x1 * down);
+        }
     }
 }
 
 static int64_t a256(int64_t v) { return (v + 255) & ~(int64_t) 255; }
 
-// GemmAct buffers, then the pass-A temporaries (block scales, per-16 sums, chunk maxima).
+// GemmAct buffers: codes, block scales, sums hi/lo, slot powers of two.
 size_t gemm_act_bytes_np(int dt, int NP, int k) {
     const int64_t Kp = (k + 255) / 256 * 256, sk = gemm_sums_kind(dt);
     const int64_t sb = sk == 0 ? 0 : a256((Kp / 256) * NP * (sk == 1 ? 8 : 16) * 2);
-    const int64_t tmp = a256((Kp / 32) * NP * 4) + a256((Kp / 16) * NP * 4) + a256((Kp / 256) * NP * 4) +
-                        a256((int64_t) NP * 4);
-    return (size_t) (a256(Kp * NP * 2) + a256((Kp / 32) * NP * 4) + 2 * sb + a256((int64_t) NP * 4) + tmp);
+    return (size_t) (a256(Kp * NP * 2) + a256((Kp / 32) * NP * 4) + 2 * sb + a256((int64_t) NP * 4));
 }
 size_t gemm_act_bytes(int dt, int n, int k) { return gemm_act_bytes_np(dt, (n + 63) / 64 * 64, k); }
+bool gemm_prep_fits(int k) { return (k + 255) / 256 * 256 <= PREP_MAX_KP; }
 
 static hipError_t prep_np(int dt, const float* a, int lda, int n, int NP, int k, void* scratch, GemmAct* out,
                           const int* gmap, const int* goff, const int* gpoff, hipStream_t st) {
     const int Kp = (k + 255) / 256 * 256, sk = gemm_sums_kind(dt);
+    if (Kp > PREP_MAX_KP) return hipErrorNotSupported;
     uint8_t* p = (uint8_t*) scratch;
     _Float16* bq = (_Float16*) p;
     p += a256((int64_t) Kp * NP * 2);
@@ -253,25 +247,21 @@ static hipError_t prep_np(int dt, const float* a, int lda, int n, int NP, int k,
     _Float16* slo = (_Float16*) (p + sb);
     p += 2 * sb;
     float* es = (float*) p;
-    p += a256((int64_t) NP * 4);
-    float* tdb = (float*) p;
-    p += a256((int64_t) (Kp / 32) * NP * 4);
-    float* txs = (float*) p;
-    p += a256((int64_t) (Kp / 16) * NP * 4);
-    float* tmx = (float*) p;
-    p += a256((int64_t) (Kp / 256) * NP * 4);
-    float* down = (float*) p;
     *out = GemmAct{bq, dx, shi, slo, es, NP, Kp};
     if (NP <= 0) return hipSuccess;
-    const dim3 ga((Kp / 256 + 3) / 4, NP), gb((NP + 255) / 256, Kp / 32);
     const int vec = ((reinterpret_cast<uintptr_t>(a) & 15) == 0 && (lda & 3) == 0) ? 1 : 0;
-    if (sk == 1) gemm_prep_a<1><<<ga, 256, 0, st>>>(a, lda, n, k, Kp, NP, bq, tdb, txs, tmx, gmap, goff, gpoff, vec);
-    else if (sk == 2) gemm_prep_a<2><<<ga, 256, 0, st>>>(a, lda, n, k, Kp, NP, bq, tdb, txs, tmx, gmap, goff, gpoff, vec);
-    else gemm_prep_a<0><<<ga, 256, 0, st>>>(a, lda, n, k, Kp, NP, bq, tdb, txs, tmx, gmap, goff, gpoff, vec);
-    gemm_prep_e<<<(NP + 63) / 64, 256, 0, st>>>(Kp, NP, sk, tmx, es, down);
-    if (sk == 1) gemm_prep_b<1><<<gb, 256, 0, st>>>(NP, tdb, txs, down, dx, shi, slo);
-    else if (sk == 2) gemm_prep_b<2><<<gb, 256, 0, st>>>(NP, tdb, txs, down, dx, shi, slo);
-    else gemm_prep_b<0><<<gb, 256, 0, st>>>(NP, tdb, txs, down, dx, shi, slo);
+    const size_t lds = ((size_t) (Kp / 32) + (size_t) (Kp / 16) + 4) * sizeof(float);
+    static bool attr[3] = {false, false, false};
+    const void* fn = sk == 1 ? (const void*) gemm_prep<1> : sk == 2 ? (const void*) gemm_prep<2> : (const void*) gemm_prep<0>;
+    if (!attr[sk]) {
+        const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 (int) ((PREP_MAX_KP / 32 + PREP_MAX_KP / 16 + 4) * sizeof(float)));
+        if (e != hipSuccess) return e;
+        attr[sk] = true;
+    }
+    if (sk == 1) gemm_prep<1><<<NP, 256, lds, st>>>(a, lda, n, k, Kp, NP, bq, dx, shi, slo, es, gmap, goff, gpoff, vec);
+    else if (sk == 2) gemm_prep<2><<<NP, 256, lds, st>>>(a, lda, n, k, Kp, NP, bq, dx, shi, slo, es, gmap, goff, gpoff, vec);
+    else gemm_prep<0><<<NP, 256, lds, st>>>(a, lda, n, k, Kp, NP, bq, dx, shi, slo, es, gmap, goff, gpoff, vec);
     return hipGetLastError();
 }
 
