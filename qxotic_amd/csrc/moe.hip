@@ -61,6 +61,49 @@ __global__ void __launch_bounds__(MOE_THREADS) moe_offsets_kernel(const int* __r
     }
 }
 
+// The same for E <= 64 in a single wave: the four exclusive scans are wave scans (shuffles, no barriers).
+JAMHIP_DEV int wave_exclusive_scan(int v) {
+    const int lane = threadIdx.x & 63;
+    int x = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(x, o);
+        if (lane >= o) x += y;
+    }
+    return x - v;
+}
+__global__ void __launch_bounds__(64) moe_offsets_wave_kernel(const int* __restrict__ counts, int E, int rows_cap,
+                                                             int* __restrict__ off, int* __restrict__ poff64,
+                                                             int* __restrict__ poff8, int* __restrict__ map64,
+                                                             int cap64, int* __restrict__ map8, int cap8) {
+    const int e = threadIdx.x;
+    const int c0 = e < E ? max(counts[e], 0) : 0;
+    const int o = wave_exclusive_scan(c0);
+    const int c = e < E ? max(0, min(c0, rows_cap - o)) : 0;   // rows past rows_cap are dropped
+    const int oc = wave_exclusive_scan(c);
+    const int big = c >= 8;
+    const int a64 = big ? (c + 63) / 64 * 64 : 0, a8 = big ? (c + 7) / 8 * 8 : 0;
+    const int p64 = wave_exclusive_scan(a64);
+    const int p8 = wave_exclusive_scan(a8);
+    for (int i = e; i < cap64; i += 64) map64[i] = -1;
+    for (int i = e; i < cap8; i += 64) map8[i] = -1;
+    __syncthreads();
+    if (e < E) {
+        off[e] = oc;
+        poff64[e] = p64;
+        poff8[e] = p8;
+        if (big) {
+            for (int t = p64 / 64; t < (p64 + a64) / 64 && t < cap64; t++) map64[t] = e;
+            for (int t = p8 / 8; t < (p8 + a8) / 8 && t < cap8; t++) map8[t] = e;
+        }
+        if (e == E - 1) {
+            off[E] = oc + c;
+            poff64[E] = p64 + a64;
+            poff8[E] = p8 + a8;
+        }
+    }
+}
+
 // Moe.dispatch's CSR build (Moe.java:188-206): counts per expert, off = exclusive prefix sum, then the
 // routes in (s, k) order each take the next slot of their expert: slot_route[slot] = route index s·topk+k,
 // route_slot[route] = slot. One workgroup of 16 waves over chunks of 1024 routes. Per chunk and wave, one
@@ -131,7 +174,9 @@ __global__ void __launch_bounds__(MOE_THREADS) moe_route_kernel(const int* __res
 }
 
 // Moe.dispatch's gather (Moe.java:214-222): g[slot] = x[slot_route[slot] / topk] (dim floats per row).
-// Slots past off[E] (routes with an expert id outside [0, E) leave them unassigned) are not written.
+// Slots past off[E] (routes with an expert id outside [0, E) leave them unassigned) are not written. V4:
+// rows copied as float4 (the launcher checks 16-byte alignment of both rows and dim % 4 == 0).
+template <bool V4>
 __global__ void __launch_bounds__(256) moe_gather_kernel(const float* __restrict__ x, int ldx,
                                                         const int* __restrict__ slot_route,
                                                         const int* __restrict__ off, int E, int topk, int dim,
@@ -139,49 +184,92 @@ __global__ void __launch_bounds__(256) moe_gather_kernel(const float* __restrict
     const int slot = blockIdx.x;
     if (slot >= off[E]) return;
     const int s = slot_route[slot] / topk;
-    for (int i = threadIdx.x; i < dim; i += 256) g[(int64_t) slot * ldg + i] = x[(int64_t) s * ldx + i];
+    const float* src = x + (int64_t) s * ldx;
+    float* dst = g + (int64_t) slot * ldg;
+    if constexpr (V4) {
+        for (int i = threadIdx.x; i < dim / 4; i += 256)
+            reinterpret_cast<float4*>(dst)[i] = reinterpret_cast<const float4*>(src)[i];
+    } else {
+        for (int i = threadIdx.x; i < dim; i += 256) dst[i] = src[i];
+    }
 }
 
 // Moe.dispatch's weighted scatter-add (Moe.java:208, 223-231): out is zero-filled, then every expert in
 // ascending order adds prob·y to its rows with one fused multiply-add (Ops.saxpyInPlace's fma,
 // Ops.java:688-725). Here each output row sums its own routes, sorted by (expert, k) — the order in
-// which the expert loop reaches them — so the result is bit-identical and needs no atomics.
+// which the expert loop reaches them — so the result is bit-identical and needs no atomics. The row's
+// routes are loaded once into LDS; one thread drops the ones without a slot and sorts the rest (stable
+// insertion sort on the expert id) into (slot, prob) lists; then every thread runs the fma chain for its
+// columns (four at a time when V4: rows 16-byte aligned, dim % 4 == 0).
+template <bool V4>
 __global__ void __launch_bounds__(256) moe_combine_kernel(const float* __restrict__ y, int ldy,
                                                          const int* __restrict__ route_expert,
                                                          const float* __restrict__ route_prob,
                                                          const int* __restrict__ route_slot, int seq, int topk,
                                                          int E, int dim, float* __restrict__ out, int ldo) {
+    __shared__ int r_ex[16], r_slot[16], l_ex[16], l_slot[16];
+    __shared__ float r_prob[16], l_prob[16];
+    __shared__ int l_n;
     const int s = blockIdx.x;
     if (s >= seq) return;
-    int ord[16];
     const int kk = topk < 16 ? topk : 16;
-    for (int k = 0; k < kk; k++) ord[k] = k;
-    for (int a = 1; a < kk; a++) {   // insertion sort by (expert, k): stable
-        const int v = ord[a];
-        const int ev = route_expert[s * topk + v];
-        int b = a - 1;
-        while (b >= 0 && route_expert[s * topk + ord[b]] > ev) {
-            ord[b + 1] = ord[b];
-            b--;
-        }
-        ord[b + 1] = v;
+    if (threadIdx.x < kk) {
+        r_ex[threadIdx.x] = route_expert[s * topk + threadIdx.x];
+        r_slot[threadIdx.x] = route_slot[s * topk + threadIdx.x];
+        r_prob[threadIdx.x] = route_prob[s * topk + threadIdx.x];
     }
-    for (int i = threadIdx.x; i < dim; i += 256) {
-        float acc = 0.0f;
-        for (int j = 0; j < kk; j++) {
-            const int r = s * topk + ord[j];
-            const int e = route_expert[r], slot = route_slot[r];
-            if (e < 0 || e >= E || slot < 0) continue;
-            acc = fmaf(route_prob[r], y[(int64_t) slot * ldy + i], acc);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int nv = 0;
+        for (int k = 0; k < kk; k++) {
+            const int e = r_ex[k], sl = r_slot[k];
+            if (e < 0 || e >= E || sl < 0) continue;
+            int b = nv - 1;   // insert after every kept route with a smaller or equal expert id (stable)
+            while (b >= 0 && l_ex[b] > e) {
+                l_ex[b + 1] = l_ex[b];
+                l_slot[b + 1] = l_slot[b];
+                l_prob[b + 1] = l_prob[b];
+                b--;
+            }
+            l_ex[b + 1] = e;
+            l_slot[b + 1] = sl;
+            l_prob[b + 1] = r_prob[k];
+            nv++;
         }
-        out[(int64_t) s * ldo + i] = acc;
+        l_n = nv;
+    }
+    __syncthreads();
+    const int nv = l_n;
+    float* o = out + (int64_t) s * ldo;
+    if constexpr (V4) {
+        for (int i = threadIdx.x; i < dim / 4; i += 256) {
+            float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            for (int j = 0; j < nv; j++) {
+                const float p = l_prob[j];
+                const float4 v = reinterpret_cast<const float4*>(y + (int64_t) l_slot[j] * ldy)[i];
+                acc.x = fmaf(p, v.x, acc.x);
+                acc.y = fmaf(p, v.y, acc.y);
+                acc.z = fmaf(p, v.z, acc.z);
+                acc.w = fmaf(p, v.w, acc.w);
+            }
+            reinterpret_cast<float4*>(o)[i] = acc;
+        }
+    } else {
+        for (int i = threadIdx.x; i < dim; i += 256) {
+            float acc = 0.0f;
+            for (int j = 0; j < nv; j++) acc = fmaf(l_prob[j], y[(int64_t) l_slot[j] * ldy + i], acc);
+            o[i] = acc;
+        }
     }
 }
 
 hipError_t launch_moe_offsets(const int* counts, int E, int rows_cap, int* off, int* poff64, int* poff8, int* map64,
                               int cap64, int* map8, int cap8, hipStream_t st) {
     if (E < 1 || E > MOE_THREADS) return hipErrorNotSupported;
-    moe_offsets_kernel<<<1, MOE_THREADS, 0, st>>>(counts, E, rows_cap, off, poff64, poff8, map64, cap64, map8, cap8);
+    if (E <= 64)
+        moe_offsets_wave_kernel<<<1, 64, 0, st>>>(counts, E, rows_cap, off, poff64, poff8, map64, cap64, map8, cap8);
+    else
+        moe_offsets_kernel<<<1, MOE_THREADS, 0, st>>>(counts, E, rows_cap, off, poff64, poff8, map64, cap64, map8, cap8);
     return hipGetLastError();
 }
 
@@ -201,10 +289,17 @@ hipError_t launch_moe_route(const int* route_expert, int R, int E, int* counts, 
     return hipGetLastError();
 }
 
+static bool rows16(const float* p, int ld, int dim) {
+    return (reinterpret_cast<uintptr_t>(p) & 15) == 0 && (ld & 3) == 0 && (dim & 3) == 0;
+}
+
 hipError_t launch_moe_gather(const float* x, int ldx, const int* slot_route, const int* off, int E, int R, int topk,
                              int dim, float* g, int ldg, hipStream_t st) {
     if (R <= 0) return hipSuccess;
-    moe_gather_kernel<<<R, 256, 0, st>>>(x, ldx, slot_route, off, E, topk, dim, g, ldg);
+    if (rows16(x, ldx, dim) && rows16(g, ldg, dim))
+        moe_gather_kernel<true><<<R, 256, 0, st>>>(x, ldx, slot_route, off, E, topk, dim, g, ldg);
+    else
+        moe_gather_kernel<false><<<R, 256, 0, st>>>(x, ldx, slot_route, off, E, topk, dim, g, ldg);
     return hipGetLastError();
 }
 
@@ -213,7 +308,12 @@ hipError_t launch_moe_combine(const float* y, int ldy, const int* route_expert, 
                               hipStream_t st) {
     if (topk > 16) return hipErrorNotSupported;
     if (seq <= 0) return hipSuccess;
-    moe_combine_kernel<<<seq, 256, 0, st>>>(y, ldy, route_expert, route_prob, route_slot, seq, topk, E, dim, out, ldo);
+    if (rows16(y, ldy, dim) && rows16(out, ldo, dim))
+        moe_combine_kernel<true><<<seq, 256, 0, st>>>(y, ldy, route_expert, route_prob, route_slot, seq, topk, E, dim,
+                                                      out, ldo);
+    else
+        moe_combine_kernel<false><<<seq, 256, 0, st>>>(y, ldy, route_expert, route_prob, route_slot, seq, topk, E, dim,
+                                                       out, ldo);
     return hipGetLastError();
 }
 

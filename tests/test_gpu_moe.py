@@ -72,6 +72,17 @@ def test_route_gather_combine_bit_exact(hip):
         assert np.array_equal(got[:, :dim].view(np.uint32), want.view(np.uint32))
         assert (got[:, dim] == 7.0).all()           # the stride gap is untouched
 
+        # contiguous 16-byte-aligned rows (the four-wide copy and fma paths)
+        g4 = torch.zeros((R, dim), dtype=torch.float32, device="cuda")
+        assert hip.moe_gather(dev(x).data_ptr(), dim, slot_route.data_ptr(), off.data_ptr(), E, seq, topk, dim,
+                              g4.data_ptr(), dim) == 0, hip.last_error()
+        out4 = torch.zeros((seq, dim), dtype=torch.float32, device="cuda")
+        assert hip.moe_combine(dev(y).data_ptr(), dim, re_d.data_ptr(), dev(prob).data_ptr(), route_slot.data_ptr(),
+                               seq, topk, E, dim, out4.data_ptr(), dim) == 0, hip.last_error()
+        hip.synchronize()
+        assert np.array_equal(g4.cpu().numpy()[:total], M.gather(x, sr_o, total, topk))
+        assert np.array_equal(out4.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
 
 # (dtype, m rows per expert, k): m % 32 == 0 takes the matrix cores for Q4_K / Q6_K / MXFP4 (k % 256 for the
 # K-quants; MXFP4 pads k to 256); m = 48 and Q8_0 / Q4_0 take the decode kernels' F2 tiles.
