@@ -147,46 +147,59 @@ __global__ void __launch_bounds__(256) gemm_prep(const float* __restrict__ a, in
     const int src = prep_src(t, n, gmap, goff, gpoff);
     const int j = lane & 7;   // lane within the block
     float m2 = 0.0f;
-    for (int ch = wave; ch < nch; ch += 4) {
-        const int b = 8 * ch + (lane >> 3);
-        float x[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (src >= 0 && b < nbk) {
-            const float* p = a + (int64_t) src * lda + 32 * b + 4 * j;
-            if (vec) {   // a and lda 16-byte aligned (the launcher checks)
-                const float4 v = *reinterpret_cast<const float4*>(p);
-                x[0] = v.x, x[1] = v.y, x[2] = v.z, x[3] = v.w;
-            } else {
-                x[0] = p[0], x[1] = p[1], x[2] = p[2], x[3] = p[3];
-            }
-        }
-        float mx = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
-        mx = fmaxf(mx, __shfl_xor(mx, 4));
-        mx = fmaxf(mx, dppf<0x4E>(mx));   // lane ^ 2
-        mx = fmaxf(mx, dppf<0xB1>(mx));   // lane ^ 1
-        const float db = mx / 127.0f;
-        const float inv = mx > 0.0f ? 127.0f / mx : 0.0f;
-        int qv[4];
+    // batches of 4 chunks per wave: the batch's loads go out together, then the chunks are quantized
+    for (int c0 = wave; c0 < nch; c0 += 16) {
+        float xb[4][4];
 #pragma unroll
         for (int u = 0; u < 4; u++) {
-            const float p = x[u] * inv;
-            qv[u] = !(p > -2147483648.0f && p < 2147483648.0f) ? -128 : (int) fminf(fmaxf(rintf(p), -128.0f), 127.0f);
+            const int b = 8 * (c0 + 4 * u) + (lane >> 3);
+#pragma unroll
+            for (int v = 0; v < 4; v++) xb[u][v] = 0.0f;
+            if (src >= 0 && b < nbk) {
+                const float* p = a + (int64_t) src * lda + 32 * b + 4 * j;
+                if (vec) {   // a and lda 16-byte aligned (the launcher checks)
+                    const float4 v = *reinterpret_cast<const float4*>(p);
+                    xb[u][0] = v.x, xb[u][1] = v.y, xb[u][2] = v.z, xb[u][3] = v.w;
+                } else {
+                    xb[u][0] = p[0], xb[u][1] = p[1], xb[u][2] = p[2], xb[u][3] = p[3];
+                }
+            }
         }
-        // codes: elements 4j..4j+3 -> K-step (j >> 1) & 1, half j >> 2, slots 4(j & 1) + {0, 2, 1, 3}
-        typedef _Float16 half4 __attribute__((ext_vector_type(4)));
-        const half4 hv = {(_Float16) qv[0], (_Float16) qv[2], (_Float16) qv[1], (_Float16) qv[3]};
-        *reinterpret_cast<half4*>(bq + ((int64_t) (2 * b + ((j >> 1) & 1)) * NP + t) * 16 + 8 * (j >> 2) + 4 * (j & 1)) = hv;
-        // per-16 sums: distance 8 (xor 2), distance 4 (xor 1), then in-lane distance 2 and 1
-        float s[4];
 #pragma unroll
-        for (int u = 0; u < 4; u++) s[u] = dppf<0x4E>(x[u]) + x[u];
+        for (int cb = 0; cb < 4; cb++) {
+            const int ch = c0 + 4 * cb;
+            if (ch >= nch) break;   // wave-uniform
+            const int b = 8 * ch + (lane >> 3);
+            const float* x = xb[cb];
+            float mx = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
+            mx = fmaxf(mx, __shfl_xor(mx, 4));
+            mx = fmaxf(mx, dppf<0x4E>(mx));   // lane ^ 2
+            mx = fmaxf(mx, dppf<0xB1>(mx));   // lane ^ 1
+            const float db = mx / 127.0f;
+            const float inv = mx > 0.0f ? 127.0f / mx : 0.0f;
+            int qv[4];
 #pragma unroll
-        for (int u = 0; u < 4; u++) s[u] = dppf<0xB1>(s[u]) + s[u];
-        const float xs16 = (s[0] + s[2]) + (s[1] + s[3]);
-        if (j == 0) ldb[b] = db;
-        if ((j & 3) == 0) lxs[2 * b + (j >> 2)] = xs16;
-        if constexpr (SK != 0) {
-            const float other = __shfl_xor(xs16, 4);   // the block's other half
-            m2 = fmaxf(m2, SK == 1 ? fabsf((j < 4) ? xs16 + other : other + xs16) : fabsf(xs16));
+            for (int u = 0; u < 4; u++) {
+                const float p = x[u] * inv;
+                qv[u] = !(p > -2147483648.0f && p < 2147483648.0f) ? -128 : (int) fminf(fmaxf(rintf(p), -128.0f), 127.0f);
+            }
+            // codes: elements 4j..4j+3 -> K-step (j >> 1) & 1, half j >> 2, slots 4(j & 1) + {0, 2, 1, 3}
+            typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+            const half4 hv = {(_Float16) qv[0], (_Float16) qv[2], (_Float16) qv[1], (_Float16) qv[3]};
+            *reinterpret_cast<half4*>(bq + ((int64_t) (2 * b + ((j >> 1) & 1)) * NP + t) * 16 + 8 * (j >> 2) + 4 * (j & 1)) = hv;
+            // per-16 sums: distance 8 (xor 2), distance 4 (xor 1), then in-lane distance 2 and 1
+            float s[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) s[u] = dppf<0x4E>(x[u]) + x[u];
+#pragma unroll
+            for (int u = 0; u < 4; u++) s[u] = dppf<0xB1>(s[u]) + s[u];
+            const float xs16 = (s[0] + s[2]) + (s[1] + s[3]);
+            if (j == 0) ldb[b] = db;
+            if ((j & 3) == 0) lxs[2 * b + (j >> 2)] = xs16;
+            if constexpr (SK != 0) {
+                const float other = __shfl_xor(xs16, 4);   // the block's other half
+                m2 = fmaxf(m2, SK == 1 ? fabsf((j < 4) ? xs16 + other : other + xs16) : fabsf(xs16));
+            }
         }
     }
     if constexpr (SK != 0) {
