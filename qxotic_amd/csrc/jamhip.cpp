@@ -66,7 +66,7 @@ struct jamhip_ctx {
     char arch[64] = {0};
     std::mutex pin_mu;
     std::vector<Pin> pins;
-    DevBuf act, gact, moe, a_stage, c_stage, w_raw, w_stage;
+    DevBuf act, gact, part, moe, a_stage, c_stage, w_raw, w_stage;
 };
 
 namespace {
@@ -172,6 +172,14 @@ bool mma_path(int dt, int k, const WeightView& wv) {
     return (((dt == Q4_K || dt == Q6_K) && k % 256 == 0) || dt == MXFP4) && (wv.r0 & 31) == 0 && gemm_prep_fits(k);
 }
 
+// Smallest n that takes the matrix cores (n >= 8 is F2 either way; small grids split K): measured on the
+// BASELINE shapes, from 8 tokens for Q4_K / Q6_K and 16 for MXFP4. JAM_HIP_MMA_MIN_N overrides (tuning).
+static int mma_min_n(int dt) {
+    const char* v = getenv("JAM_HIP_MMA_MIN_N");
+    const int x = v ? atoi(v) : dt == MXFP4 ? 16 : 8;
+    return x < 8 ? 8 : x;
+}
+
 // Quantize A (device, f32 [n][lda]) and run the matmul into C (device, [n][ldc]). Decode-sized calls
 // are one fused launch and touch no scratch (safe under stream capture once W is pinned).
 jamhip_status compute(jamhip_ctx* ctx, int dt, const WeightView& wv, const float* a, int lda, float* c, int ldc,
@@ -185,13 +193,19 @@ jamhip_status compute(jamhip_ctx* ctx, int dt, const WeightView& wv, const float
     // n >= 8: jam's 16-row F2 bands on rows [0, m16); the last m % 16 rows take the band's float-dot tail
     // (jam_kernels_q4k_avx512.c:185-188).
     const int m16 = m - m % 16;
-    if (n >= 32 && m16 > 0 && mma_path(dt, k, wv)) {
+    if (n >= mma_min_n(dt) && m16 > 0 && mma_path(dt, k, wv)) {
         GemmAct G;
         if ((e = ctx->gact.ensure(gemm_act_bytes(dt, n, k))) != hipSuccess)
             return hip_fail(ctx, e, "gemm activation scratch alloc");
         if ((e = launch_gemm_prep(dt, a, lda, n, k, ctx->gact.p, &G, ctx->stream)) != hipSuccess)
             return hip_fail(ctx, e, "gemm prep launch");
-        if ((e = launch_gemm_mma(dt, wv, G, k, m16, n, c, ldc, ctx->stream)) != hipSuccess)
+        float* part = nullptr;
+        if (const size_t pf = gemm_mma_split_floats(dt, k, m16, n)) {
+            if ((e = ctx->part.ensure(pf * sizeof(float))) != hipSuccess)
+                return hip_fail(ctx, e, "gemm split scratch alloc");
+            part = (float*) ctx->part.p;
+        }
+        if ((e = launch_gemm_mma(dt, wv, G, k, m16, n, c, ldc, ctx->stream, part)) != hipSuccess)
             return hip_fail(ctx, e, "gemm launch");
         if ((e = launch_rows_float(dt, wv, a, lda, k, m16, m - m16, n, c, ldc, ctx->stream)) != hipSuccess)
             return hip_fail(ctx, e, "tail rows launch");
@@ -279,6 +293,7 @@ void jamhip_ctx_destroy(jamhip_ctx* ctx) {
     ctx->pins.clear();
     ctx->act.release();
     ctx->gact.release();
+    ctx->part.release();
     ctx->moe.release();
     ctx->a_stage.release();
     ctx->c_stage.release();

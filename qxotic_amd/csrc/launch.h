@@ -75,8 +75,11 @@ hipError_t launch_gemm_prep(int dt, const float* a, int lda, int n, int k, void*
 // Matrix-core GEMM over GemmAct (f16 MFMA on exact integer operands); hipErrorNotSupported for dtypes it
 // does not cover. Grouped form: GemmAct laid out by the 64-token slots of g (launch_gemm_prep_grouped),
 // cap64 slot blocks, m = g.gm rows per expert.
+// Small grids split K over extra workgroups (partials in `part`, gemm_mma_split_floats(dt, k, m, n) floats,
+// summed in a fixed order; part == nullptr: no split).
+size_t gemm_mma_split_floats(int dt, int k, int m, int n);
 hipError_t launch_gemm_mma(int dt, const WeightView& w, const GemmAct& A, int k, int m, int n, float* c, int ldc,
-                           hipStream_t st);
+                           hipStream_t st, float* part = nullptr);
 hipError_t launch_gemm_mma_grouped(int dt, const WeightView& w, const GemmAct& A, int k, const Groups& g, int cap64,
                                    float* c, int ldc, hipStream_t st);
 size_t gemm_act_bytes_np(int dt, int NP, int k);

@@ -125,7 +125,8 @@ template <int DT, int RT, int CT> struct Stage {
 template <int DT, int RT, int CT>
 __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, GemmAct A, int m, int n,
                                                                  float* __restrict__ c, int ldc, int nrb, int ncb,
-                                                                 int64_t tiles, Groups gp) {
+                                                                 int64_t tiles, Groups gp, int sb_per,
+                                                                 int64_t c_slice) {
     using S = Stage<DT, RT, CT>;
     constexpr int TW = S::TW, BN = S::BN, NCS = S::NCS;
     extern __shared__ __align__(1024) unsigned char smem[];
@@ -141,7 +142,11 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
 
     const int lane = threadIdx.x & 63, r = lane & 31, q = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int G = (int) w.G, nsb = A.Kp / 256, nst = 2 * nsb;
+    const int G = (int) w.G, nsb = A.Kp / 256;
+    // split K (sb_per > 0): slice blockIdx.y takes super-blocks [sb_per·y, sb_per·(y + 1)) and writes its
+    // partial result to c + y·c_slice (summed by split_reduce_kernel); stages are half super-blocks
+    const int st0 = sb_per > 0 ? 2 * sb_per * (int) blockIdx.y : 0;
+    const int nst = sb_per > 0 ? min(2 * nsb, st0 + 2 * sb_per) : 2 * nsb;
     int64_t r0t = w.r0 >> 5;                     // the view's first row is tile-aligned (launcher checks)
     int slot0 = 0, crow0 = 0, nvalid = n;        // token slot -> C row: crow0 + (slot - slot0), < nvalid
     if (gp.map64 != nullptr) {                   // grouped: this slot block's expert
@@ -231,11 +236,11 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
 #pragma unroll
         for (int j = 0; j < CT; j++) acc[i][j] = accs[i][j] = floatx16{};
 
-    issue(0, smem);
+    issue(st0, smem);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
 
-    for (int st = 0; st < nst; st++) {
+    for (int st = st0; st < nst; st++) {
         unsigned char* buf = smem + (st & 1) * S::BYTES;
         // each type issues the next stage's copy itself, after its last LDS read of this stage: the compiler
         // makes any LDS read that follows a global -> LDS copy wait for that copy
@@ -556,7 +561,7 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
         const int t = n0 + 32 * j + r, tl = t - slot0;
         if (tl >= nvalid) continue;
         const float sc = A.es[t];
-        float* ct = c + (int64_t) (crow0 + tl) * ldc;
+        float* ct = c + (int64_t) blockIdx.y * c_slice + (int64_t) (crow0 + tl) * ldc;
 #pragma unroll
         for (int i = 0; i < RT; i++) {
             const int64_t rowb = (T0 + wave * RT + i) * 32 + 4 * q;
@@ -569,9 +574,28 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
     }
 }
 
+// Deterministic sum of the split-K partials: c[t][row] = Σ_s part[s][t][row] in slice order.
+__global__ void __launch_bounds__(256) split_reduce_kernel(const float* __restrict__ part, int ns, int64_t slice,
+                                                          int m, float* __restrict__ c, int ldc) {
+    const int row = blockIdx.x * 256 + threadIdx.x, t = blockIdx.y;
+    if (row >= m) return;
+    const float* p = part + (int64_t) t * m + row;
+    float v = p[0];
+    for (int s = 1; s < ns; s++) v += p[(int64_t) s * slice];
+    c[(int64_t) t * ldc + row] = v;
+}
+
+// K slices for a grid of `total` workgroups: enough for about two workgroups per CU, whole super-blocks each.
+static void split_plan(int total, int nsb, int* ns, int* sb_per) {
+    int want = total >= 384 ? 1 : (512 + total - 1) / total;
+    want = want < nsb ? want : nsb;
+    *sb_per = want > 1 ? (nsb + want - 1) / want : 0;
+    *ns = want > 1 ? (nsb + *sb_per - 1) / *sb_per : 1;
+}
+
 template <int DT, int RT, int CT>
 static hipError_t kq_go(const WeightView& w, const GemmAct& A, int m, int n, float* c, int ldc, hipStream_t st,
-                        const Groups& gp = Groups{}) {
+                        const Groups& gp = Groups{}, float* part = nullptr) {
     using S = Stage<DT, RT, CT>;
     const int nrb = (m + 32 * S::TW - 1) / (32 * S::TW), ncb = A.NP / S::BN;
     const int64_t tiles = (w.r0 + tiled_rows(m)) / 32 - w.r0 / 32;   // tiles of the view that exist
@@ -584,17 +608,34 @@ static hipError_t kq_go(const WeightView& w, const GemmAct& A, int m, int n, flo
         if (e != hipSuccess) return e;
         attr = true;
     }
-    kq_gemm_kernel<DT, RT, CT><<<grid, MMA_THREADS, lds, st>>>(w, A, m, n, c, ldc, nrb, ncb, tiles, gp);
+    int ns = 1, sb_per = 0;
+    if (part != nullptr) split_plan(total, A.Kp / 256, &ns, &sb_per);
+    if (ns == 1) {
+        kq_gemm_kernel<DT, RT, CT><<<grid, MMA_THREADS, lds, st>>>(w, A, m, n, c, ldc, nrb, ncb, tiles, gp, 0, 0);
+        return hipGetLastError();
+    }
+    const int64_t slice = (int64_t) n * m;
+    kq_gemm_kernel<DT, RT, CT><<<dim3(grid, ns), MMA_THREADS, lds, st>>>(w, A, m, n, part, m, nrb, ncb, tiles, gp,
+                                                                         sb_per, slice);
+    split_reduce_kernel<<<dim3((m + 255) / 256, n), 256, 0, st>>>(part, ns, slice, m, c, ldc);
     return hipGetLastError();
 }
 
+size_t gemm_mma_split_floats(int dt, int k, int m, int n) {
+    if (dt != Q4_K && dt != Q6_K && dt != MXFP4) return 0;
+    const int nrb = (m + 32 * MMA_WAVES - 1) / (32 * MMA_WAVES), ncb = (n + 63) / 64, nsb = (k + 255) / 256;
+    int ns, sb_per;
+    split_plan(nrb * ncb, nsb, &ns, &sb_per);
+    return ns > 1 ? (size_t) ns * n * m : 0;
+}
+
 hipError_t launch_gemm_mma(int dt, const WeightView& w, const GemmAct& A, int k, int m, int n, float* c, int ldc,
-                           hipStream_t st) {
+                           hipStream_t st, float* part) {
     if ((dt != MXFP4 && k % 256) || (w.r0 & 31) || A.NP % 64) return hipErrorNotSupported;
     switch (dt) {
-    case Q4_K: return kq_go<Q4_K, 1, 2>(w, A, m, n, c, ldc, st);
-    case Q6_K: return kq_go<Q6_K, 1, 2>(w, A, m, n, c, ldc, st);
-    case MXFP4: return kq_go<MXFP4, 1, 2>(w, A, m, n, c, ldc, st);
+    case Q4_K: return kq_go<Q4_K, 1, 2>(w, A, m, n, c, ldc, st, Groups{}, part);
+    case Q6_K: return kq_go<Q6_K, 1, 2>(w, A, m, n, c, ldc, st, Groups{}, part);
+    case MXFP4: return kq_go<MXFP4, 1, 2>(w, A, m, n, c, ldc, st, Groups{}, part);
     default: return hipErrorNotSupported;
     }
 }
