@@ -128,7 +128,11 @@ def gpu_leg(args, w: np.ndarray, hip, torch, stream) -> dict:
         if st != JAM.OK:
             raise RuntimeError(hip.last_error())
     host_us = (time.perf_counter() - t0) / calls * 1e6
-    assert np.array_equal(c_h, c[(calls - 1) % COPIES].cpu().numpy()), "host-pointer call disagrees"
+    with torch.cuda.stream(stream):
+        st = hip.mm_device(Segment.of(copies[(calls - 1) % COPIES]), JAM.Q4_K, K, a.data_ptr(), K, ref.data_ptr(),
+                           M, M, N, K)
+    torch.cuda.synchronize()
+    assert st == JAM.OK and np.array_equal(c_h, ref.cpu().numpy()), "host-pointer call disagrees"
     for cp in copies:
         hip.evict(Segment.of(cp))
     return {"event_ms": ev_ms, "wall_s": wall, "host_us": host_us}
