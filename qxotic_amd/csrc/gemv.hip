@@ -196,6 +196,36 @@ JAMHIP_DEV float group_dot(const Group<DT>& w, const int8_t* aq, const float* ad
     }
 }
 
+// Q4_0 F1 decode with 3..7 tokens: the group's nibbles and block scales unpacked once for all the tokens
+// (measured faster for Q4_0 only; the other types unpack per token in group_dot), then per token
+// group_dot's Q4_0 arithmetic.
+struct Q40Codes {
+    uint4 c[16];   // block b: low nibbles c[2b], high nibbles c[2b + 1]
+    float f[8];    // block scales
+};
+
+JAMHIP_DEV void q40_unpack(const Group<Q4_0>& w, Q40Codes& u) {
+#pragma unroll
+    for (int b = 0; b < 8; b++) {
+        u.c[2 * b] = lo_nib(w.q[b]);
+        u.c[2 * b + 1] = hi_nib(w.q[b]);
+        u.f[b] = h2f((word(w.s, b >> 1) >> (16 * (b & 1))) & 0xffffu);
+    }
+}
+
+JAMHIP_DEV float q40_dot_f1(const Q40Codes& u, const int8_t* aq, const float* ad, const int* s16, int nbv) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int b = 0; b < 8; b++) {
+        const int bq = b < nbv ? b : nbv - 1;   // stay inside the token's activations
+        int I = dot16(u.c[2 * b + 1], ld16(aq + 32 * bq + 16), dot16(u.c[2 * b], ld16(aq + 32 * bq), 0));
+        I -= 8 * (s16[2 * bq] + s16[2 * bq + 1]);
+        const float v = (float) I * (u.f[b] * ad[bq]);   // q256 engine (jam_gemm_q256.inc:28-36): fl(sw·da)·I
+        acc += b < nbv ? v : 0.0f;
+    }
+    return acc;
+}
+
 // ------------------------------------------------------------------------------ fused F1 prologue
 // Quantizes NT activation rows into LDS with jam's F1 (quant.h) in the group layout: per token and group
 // 256 int8 codes padded to QS_LDS bytes (conflict-free reads), 8 block scales, 8 block sums, 16 Σq per 16.
@@ -394,14 +424,28 @@ __global__ void __launch_bounds__(64 * MV_WAVES) mv_kernel(WeightView w, ActQ A,
         const int gg = g < Gk ? g : Gk - 1;
         const int nbv = nb - BPG * gg < BPG ? nb - BPG * gg : BPG;
         float* pp = part + (it * 64 + lane) * NT;
-        constexpr int TU = NT > 2 ? 1 : NT;   // keep several tokens' temporaries out of the register file
+        if constexpr (NT <= 2 || FL == 2 || DT != Q4_0) {   // per-token unpacking measured faster for the rest
+            constexpr int TU = NT > 2 ? 1 : NT;   // keep several tokens' temporaries out of the register file
 #pragma unroll TU
-        for (int t = 0; t < NT; t++) {
-            if (t >= ntv) break;
-            const int tt = FUSE ? t : t0 + t;
-            const float p = group_dot<DT, FL>(buf[i], aq + tt * tq + (int64_t) gg * QS, ad + tt * td + 8 * gg,
-                                              as + tt * ts + (FL == 1 ? 8 : 16) * gg, s16 + tt * t16 + 16 * gg, nbv);
-            pp[t] = live ? p : 0.0f;
+            for (int t = 0; t < NT; t++) {
+                if (t >= ntv) break;
+                const int tt = FUSE ? t : t0 + t;
+                const float p = group_dot<DT, FL>(buf[i], aq + tt * tq + (int64_t) gg * QS, ad + tt * td + 8 * gg,
+                                                  as + tt * ts + (FL == 1 ? 8 : 16) * gg, s16 + tt * t16 + 16 * gg,
+                                                  nbv);
+                pp[t] = live ? p : 0.0f;
+            }
+        } else {   // Q4_0 F1, 3..7 tokens: the group's weights unpacked once for all the tokens
+            Q40Codes u;
+            q40_unpack(buf[i], u);
+#pragma unroll 1
+            for (int t = 0; t < NT; t++) {
+                if (t >= ntv) break;
+                const int tt = FUSE ? t : t0 + t;
+                const float p = q40_dot_f1(u, aq + tt * tq + (int64_t) gg * QS, ad + tt * td + 8 * gg,
+                                           s16 + tt * t16 + 16 * gg, nbv);
+                pp[t] = live ? p : 0.0f;
+            }
         }
     }
     __syncthreads();
