@@ -312,6 +312,58 @@ JAMHIP_DEV void f1_store(const APre<HP>& pre, int k, int Gk, int8_t* lq, float* 
     }
 }
 
+// F2 activations staged in LDS (8-token tiles, already quantized by quant_f2_kernel into A): the tile's
+// codes in the fused layout (group g of token t at lq + (t·Gk + g)·QS_LDS), block scales (ld, 8 per group)
+// and per-16 sums (lx, 16 per group), copied once per workgroup so that the dot products read LDS instead
+// of each lane fetching its tokens' activations from L2. As for F1, f2_load's loads go out before the
+// weight stream and f2_store writes LDS after it. Tokens past ntv repeat token ntv - 1; 16-byte pieces
+// past k (a partial last group) re-read the row's last piece and are never read back (group_dot clamps
+// to the group's last valid block). HP = ceil(NT·Gk·16 / 512) code pieces per thread, 2·HP floats.
+template <int HP> struct FPre {
+    uint4 q[HP];
+    float f[2 * HP];
+};
+
+template <int NT, int HP>
+JAMHIP_DEV void f2_load(FPre<HP>& pre, const ActQ& A, int k, int Gk, int t0, int ntv) {
+    const int nb = k >> 5, units = NT * Gk * 16, nf = NT * 3 * nb;
+#pragma unroll
+    for (int i = 0; i < HP; i++) {
+        const int u0 = threadIdx.x + 64 * MV_WAVES * i, u = u0 < units ? u0 : units - 1;
+        const int t = u / (Gk * 16), r = u - t * Gk * 16, tc = t < ntv ? t : ntv - 1;
+        const int off = 256 * (r >> 4) + 16 * (r & 15);
+        pre.q[i] = ld16(A.q + (int64_t) (t0 + tc) * k + (off < k ? off : k - 16));
+    }
+#pragma unroll
+    for (int i = 0; i < 2 * HP; i++) {
+        const int v0 = threadIdx.x + 64 * MV_WAVES * i, v = v0 < nf ? v0 : nf - 1;
+        const int t = v / (3 * nb), r = v - t * 3 * nb, tc = t < ntv ? t : ntv - 1;
+        pre.f[i] = r < nb ? A.d[(int64_t) (t0 + tc) * nb + r] : A.s[(int64_t) (t0 + tc) * 2 * nb + (r - nb)];
+    }
+}
+
+template <int NT, int HP>
+JAMHIP_DEV void f2_store(const FPre<HP>& pre, int k, int Gk, int8_t* lq, float* ld, float* lx) {
+    const int nb = k >> 5, units = NT * Gk * 16, nf = NT * 3 * nb;
+#pragma unroll
+    for (int i = 0; i < HP; i++) {
+        const int u = threadIdx.x + 64 * MV_WAVES * i;
+        if (u < units) {
+            const int t = u / (Gk * 16), r = u - t * Gk * 16;
+            *reinterpret_cast<uint4*>(lq + (t * Gk + (r >> 4)) * QS_LDS + 16 * (r & 15)) = pre.q[i];
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 2 * HP; i++) {
+        const int v = threadIdx.x + 64 * MV_WAVES * i;
+        if (v < nf) {
+            const int t = v / (3 * nb), r = v - t * 3 * nb;
+            if (r < nb) ld[t * 8 * Gk + r] = pre.f[i];
+            else lx[t * 16 * Gk + (r - nb)] = pre.f[i];
+        }
+    }
+}
+
 // ------------------------------------------------------------------------------------------ kernel
 // One workgroup (8 waves) computes one block of rows with straight-line code: the compiler can then count
 // every outstanding load exactly (a branch between a load and its use makes it drain the whole queue).
@@ -371,10 +423,12 @@ __global__ void __launch_bounds__(64 * MV_WAVES) mv_kernel(WeightView w, ActQ A,
     // Only waves that own at least one real half-block of the activations load and quantize them (the
     // others would only write the dummy slot); the condition is wave-uniform. Their loads go first in the
     // load queue and are kept there by the scheduler.
-    const bool pro = FUSE && wave * 64 < NT * 16 * Gk;
-    APre<FUSE ? HP : 1> pre;
-    if constexpr (FUSE)
+    const bool pro = FUSE && FL == 1 && wave * 64 < NT * 16 * Gk;
+    APre<FUSE && FL == 1 ? HP : 1> pre;
+    FPre<FUSE && FL == 2 ? HP : 1> fpre;
+    if constexpr (FUSE && FL == 1)
         if (pro) a_load<NT, HP>(pre, a, lda, k, Gk, ntv);
+    if constexpr (FUSE && FL == 2) f2_load<NT, HP>(fpre, A, k, Gk, t0, ntv);
     __builtin_amdgcn_sched_barrier(0);
 
     // item i of this wave: band q0 + it / J, group slot it % J with it = wave·ITEMS + i (clamped)
@@ -404,15 +458,23 @@ __global__ void __launch_bounds__(64 * MV_WAVES) mv_kernel(WeightView w, ActQ A,
         float* ld = reinterpret_cast<float*>(lq + NT * Gk * QS_LDS);
         float* las = ld + NT * 8 * Gk;
         int* ls16 = reinterpret_cast<int*>(las + NT * 8 * Gk);
-        if (pro) f1_store<NT, HP>(pre, k, Gk, lq, ld, las, ls16, dummy);
         aq = lq;
         ad = ld;
-        as = las;
-        s16 = ls16;
         tq = (int64_t) Gk * QS_LDS;
-        td = ts = 8 * Gk;
-        t16 = 16 * Gk;
+        td = 8 * Gk;
         QS = QS_LDS;
+        if constexpr (FL == 1) {
+            if (pro) f1_store<NT, HP>(pre, k, Gk, lq, ld, las, ls16, dummy);
+            as = las;
+            s16 = ls16;
+            ts = 8 * Gk;
+            t16 = 16 * Gk;
+        } else {   // F2: per-16 sums in the Σq-per-16 region (16 per group and token)
+            float* lx = reinterpret_cast<float*>(ls16);
+            f2_store<NT, HP>(fpre, k, Gk, lq, ld, lx);
+            as = lx;
+            ts = 16 * Gk;
+        }
         __syncthreads();
     }
 
@@ -623,6 +685,15 @@ static hipError_t go_hp(int k, int m, int n, const WeightView& w, const ActQ& A,
 template <int DT, int FL, int NT>
 static hipError_t go(const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m, int n, float* c,
                      int ldc, hipStream_t st) {
+    if constexpr (FL == 2) {   // stage the tile's activations in LDS when they fit
+        const int hp = (NT * ((k / 32 + 7) / 8) * 16 + 64 * MV_WAVES - 1) / (64 * MV_WAVES);
+        if (fuse_lds(NT, k) <= (size_t) kFuseMaxBytes && hp <= 8) {
+            if (hp <= 1) return go_hp<DT, FL, NT, 1>(k, m, n, w, A, a, lda, c, ldc, st);
+            if (hp == 2) return go_hp<DT, FL, NT, 2>(k, m, n, w, A, a, lda, c, ldc, st);
+            if (hp <= 4) return go_hp<DT, FL, NT, 4>(k, m, n, w, A, a, lda, c, ldc, st);
+            return go_hp<DT, FL, NT, 8>(k, m, n, w, A, a, lda, c, ldc, st);
+        }
+    }
     if constexpr (FL == 1) {
         if (a != nullptr) {
             const int hp = fuse_hp(NT, k);
