@@ -27,6 +27,11 @@ COMMON = [
 UNITS = {   # source -> extra flags
     "prep.hip": ["-ffp-contract=off"],
     "gemv.hip": [],
+    "gemv_q4k.hip": [],
+    "gemv_q6k.hip": [],
+    "gemv_q80.hip": [],
+    "gemv_q40.hip": [],
+    "gemv_mxfp4.hip": [],
     "gemm.hip": [],
     "mma.hip": [],
     "moe.hip": [],
@@ -50,7 +55,7 @@ def _compile(src: str, extra: list[str]) -> Path:
 def build(verbose: bool = True) -> Path:
     OBJ.mkdir(exist_ok=True)
     LIB.parent.mkdir(exist_ok=True)
-    with ThreadPoolExecutor(max_workers=min(8, len(UNITS))) as ex:
+    with ThreadPoolExecutor(max_workers=min(os.cpu_count() or 8, len(UNITS), 16)) as ex:
         objs = list(ex.map(lambda kv: _compile(*kv), UNITS.items()))
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]

@@ -1,662 +1,24 @@
-// Weight-streaming matmul for few tokens: the decode GEMV (n < 8, jam's F1 decomposition) and the skinny
-// n >= 8 path (F2 decomposition). HBM-bound: every weight byte is read once per launch with aligned
-// 128-bit loads; int8 dots run on v_dot4_i32_i8; the per-block f32 combine follows the jam kernel named
-// at each dot below.
-//
-// Work split. A lane owns whole 256-element groups of the row-tiled device layout (common.h): the 64 lanes
-// of a wave take 8 consecutive rows (a "band") x 8 groups, so for each chunk index c they read 8 groups x 8
-// rows of 16 bytes, i.e. eight full 128-byte lines, and one group's scales come in one more load. Eight
-// waves share a workgroup, the activation prologue and the LDS in which every lane's per-group partial is
-// parked and each row's partials are summed (see mv_kernel). In the fused F1 variant the workgroup quantizes A into LDS (bit-exact F1) once
-// for all of its rows; its activation loads go out first and its weight stream right behind them.
-#include "common.h"
-#include "launch.h"
-#include "quant.h"
+// Dispatch of the decode / few-token kernels (gemv_impl.h) by weight type; each type's kernels are
+// instantiated in gemv_<type>.hip.
+#include "gemv_impl.h"
 
 namespace jamhip {
 
-// -------------------------------------------------------------------------------------------- weights
-template <int DT> struct Group {
-    uint4 q[group_chunks(DT)];
-    uint4 s;   // the group's scale bytes (Q4_K header; Q8_0/Q4_0 8 x fp16; MXFP4 8 x e8m0; Q6_K d in s.x)
-};
-
-JAMHIP_DEV uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
-
-// Group g of view row `row` (row-tiled layout of common.h: chunk c at +c·512 from chunk 0).
-// Issue order: the chunks in the order the dot products use them (loads retire in issue order) and the
-// scales first, except for Q4_K, whose scales go last (measured faster on the Llama shapes).
-template <int DT> JAMHIP_DEV constexpr int chunk_order(int i) {
-    // Q6_K: the scale chunk, the qh chunks of half 0, ql 0-3, the qh chunks of half 1, ql 4-7
-    return DT != Q6_K ? i : i == 0 ? 12 : i < 3 ? 7 + i : i < 7 ? i - 3 : i < 9 ? i + 3 : i - 5;
-}
-template <int DT>
-JAMHIP_DEV void load_scales(Group<DT>& r, const uint8_t* s) {
-    if constexpr (DT == Q6_K) {
-        r.s.x = *reinterpret_cast<const uint16_t*>(s);
-    } else if constexpr (DT == MXFP4) {
-        const uint2 v = *reinterpret_cast<const uint2*>(s);
-        r.s = make_uint4(v.x, v.y, 0u, 0u);
-    } else {
-        r.s = ld16(s);
-    }
-}
-template <int DT>
-JAMHIP_DEV void load_group(Group<DT>& r, const WeightView& w, int64_t row, int g) {
-    const uint8_t* q = group_q<DT>(w, row, g);
-    const uint8_t* s = group_s<DT>(w, row, g);
-    if constexpr (DT != Q4_K) load_scales<DT>(r, s);
-#pragma unroll
-    for (int i = 0; i < group_chunks(DT); i++) {
-        const int c = chunk_order<DT>(i);
-        r.q[c] = ld16(q + c * CHUNK_STRIDE);
-    }
-    if constexpr (DT == Q4_K) load_scales<DT>(r, s);
-}
-
-
-// ------------------------------------------------------------------------------------- int8 helpers
-JAMHIP_DEV int dot16(const uint4 w, const uint4 a, int c) {
-    c = dot4((int) w.x, (int) a.x, c);
-    c = dot4((int) w.y, (int) a.y, c);
-    c = dot4((int) w.z, (int) a.z, c);
-    return dot4((int) w.w, (int) a.w, c);
-}
-JAMHIP_DEV uint4 and4(uint4 v, uint32_t m) { return make_uint4(v.x & m, v.y & m, v.z & m, v.w & m); }
-JAMHIP_DEV uint4 shr4(uint4 v, int s) { return make_uint4(v.x >> s, v.y >> s, v.z >> s, v.w >> s); }
-JAMHIP_DEV uint4 lo_nib(uint4 v) { return and4(v, 0x0f0f0f0fu); }
-JAMHIP_DEV uint4 hi_nib(uint4 v) { return and4(shr4(v, 4), 0x0f0f0f0fu); }
-JAMHIP_DEV uint32_t word(const uint4& v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
-
-// MXFP4 nibble -> signed int8 code (value x2: 0,1,2,3,4,6,8,12 and negatives; jam_mxfp4.h:14-15),
-// four at a time: v_perm picks the magnitude and its negation from 8-entry tables, bit 3 selects.
-JAMHIP_DEV uint32_t mxfp4_codes(uint32_t nib4) {
-    const uint32_t idx = nib4 & 0x07070707u;
-    const uint32_t pos = __builtin_amdgcn_perm(0x0C080604u, 0x03020100u, idx);
-    const uint32_t neg = __builtin_amdgcn_perm(0xF4F8FAFCu, 0xFDFEFF00u, idx);
-    const uint32_t msk = ((nib4 >> 3) & 0x01010101u) * 0xFFu;
-    return (neg & msk) | (pos & ~msk);
-}
-JAMHIP_DEV uint4 mxfp4_codes4(uint4 n) {
-    return make_uint4(mxfp4_codes(n.x), mxfp4_codes(n.y), mxfp4_codes(n.z), mxfp4_codes(n.w));
-}
-
-// Q4_K 6-bit scale and min of sub-block s (jam/jam-native/src/jam_kquant.h:26-33) from the header words.
-JAMHIP_DEV void q4k_sm(const uint4 h, int s, int& sc, int& mn) {
-    const uint32_t u0 = h.y, u1 = h.z, u2 = h.w;   // scale bytes 0-3, 4-7, 8-11
-    const int sh = 8 * (s & 3);
-    if (s < 4) {
-        sc = (u0 >> sh) & 63;
-        mn = (u1 >> sh) & 63;
-    } else {
-        sc = ((u2 >> sh) & 15) | ((((u0 >> sh) >> 6) & 3) << 4);
-        mn = (((u2 >> sh) >> 4) & 15) | ((((u1 >> sh) >> 6) & 3) << 4);
-    }
-}
-
-JAMHIP_DEV int sbyte(uint32_t w, int b) { return (int) (int8_t) (w >> (8 * b)); }
-
-// Q6_K 6-bit codes of ql chunk c with the matching qh chunk: the low-nibble group and the high one.
-JAMHIP_DEV void q6k_codes(const uint4 ql, const uint4 qh, int jj, uint4& qa, uint4& qb) {
-    const uint4 hia = and4(shr4(qh, 2 * jj), 0x03030303u), hib = and4(shr4(qh, 2 * jj + 4), 0x03030303u);
-    const uint4 lo = lo_nib(ql), hi = hi_nib(ql);
-    qa = make_uint4(lo.x | (hia.x << 4), lo.y | (hia.y << 4), lo.z | (hia.z << 4), lo.w | (hia.w << 4));
-    qb = make_uint4(hi.x | (hib.x << 4), hi.y | (hib.y << 4), hi.z | (hib.z << 4), hi.w | (hib.w << 4));
-}
-
-// -------------------------------------------------------------------------------- per-group partials
-// Activations of one token for one group: aq -> the group's 256 int8 codes, ad -> its 8 block scales,
-// as -> F1: 8 block sums (float Σq) / F2: 16 raw f32 sums Σx per 16, s16 -> F1: 16 int Σq per 16.
-// nbv = blocks of the group inside the call's k (8 but for a row's last group of a 32-element type);
-// blocks past it contribute nothing and read the last valid block's activations.
-template <int DT, int FL>
-JAMHIP_DEV float group_dot(const Group<DT>& w, const int8_t* aq, const float* ad, const float* as, const int* s16,
-                           int nbv) {
-    if constexpr (DT == Q4_K) {
-        const uint4 h = w.s;
-        const float d = h2f(h.x & 0xffffu), dmin = h2f(h.x >> 16);
-        float acc = 0.0f, msum = 0.0f;
-#pragma unroll
-        for (int s = 0; s < 8; s++) {   // sub-block s: chunks 2(s>>1), 2(s>>1)+1, low nibbles if s even
-            const int c0 = 2 * (s >> 1);
-            const uint4 w0 = (s & 1) ? hi_nib(w.q[c0]) : lo_nib(w.q[c0]);
-            const uint4 w1 = (s & 1) ? hi_nib(w.q[c0 + 1]) : lo_nib(w.q[c0 + 1]);
-            const int I = dot16(w1, ld16(aq + 32 * s + 16), dot16(w0, ld16(aq + 32 * s), 0));
-            int sc, mn;
-            q4k_sm(h, s, sc, mn);
-            if constexpr (FL == 1) {
-                // jam_mm_q4k_avx512vnni (jam_kernels_q4k_avx512.c:956-1054):
-                //   Σ_s I_s·fl(fl(ad·sc)·d)  −  dmin·Σ_s mn·fl(asum·ad)
-                acc += (float) I * ((ad[s] * (float) sc) * d);
-                msum += (float) mn * (as[s] * ad[s]);
-            } else {
-                // q4k_block16 (jam_kernels_q4k_avx512.c:76-95): fl(fl(d·sc)·dx)·I − fl(dmin·mn)·fl(xs0+xs1)
-                acc += (float) I * ((d * (float) sc) * ad[s]);
-                msum += (dmin * (float) mn) * (as[2 * s] + as[2 * s + 1]);
-            }
-        }
-        return FL == 1 ? acc - dmin * msum : acc - msum;
-    } else if constexpr (DT == Q6_K) {
-        const float d = h2f(w.s.x & 0xffffu);
-        const uint4 scv = w.q[12];
-        float blk[8];
-#pragma unroll
-        for (int b = 0; b < 8; b++) blk[b] = 0.0f;
-        float off = 0.0f;
-#pragma unroll
-        for (int c = 0; c < 8; c++) {   // ql chunk c: half h, j = jj (low nibbles) and jj+2, l = 16lh..
-            const int h = c >> 2, jj = (c >> 1) & 1, lh = c & 1;
-            uint4 qa, qb;
-            q6k_codes(w.q[c], w.q[8 + 2 * h + lh], jj, qa, qb);
-            const int ta = 8 * h + 2 * jj + lh, tb = ta + 4;   // 16-element groups (= scale index)
-            const int ia = dot16(qa, ld16(aq + 16 * ta), 0), ib = dot16(qb, ld16(aq + 16 * tb), 0);
-            const float sa = d * (float) sbyte(word(scv, ta >> 2), ta & 3);
-            const float sb = d * (float) sbyte(word(scv, tb >> 2), tb & 3);
-            if constexpr (FL == 1) {
-                // jam_mm_q6k_sse3 (jam_kernels_kquant_sse3.c:125-169): ad·(fl(d·sc)·Σ(q6-32)·aq) per 16
-                blk[ta >> 1] += sa * (float) (ia - 32 * s16[ta]);
-                blk[tb >> 1] += sb * (float) (ib - 32 * s16[tb]);
-            } else {
-                // q6k_block16 (jam_kernels_q4k_avx512.c:222-236): fl(fl(d·sc)·dx)·Σq6·xq − fl(d·sc)·fl(32·xs16)
-                blk[ta >> 1] += (float) ia * (sa * ad[ta >> 1]);
-                blk[tb >> 1] += (float) ib * (sb * ad[tb >> 1]);
-                off += sa * (32.0f * as[ta]) + sb * (32.0f * as[tb]);
-            }
-        }
-        float acc = 0.0f;
-#pragma unroll
-        for (int b = 0; b < 8; b++) acc += FL == 1 ? ad[b] * blk[b] : blk[b];
-        return acc - off;
-    } else {
-        float acc = 0.0f;
-#pragma unroll
-        for (int b = 0; b < 8; b++) {
-            const int bb = b < nbv ? b : nbv - 1;   // stay inside the token's activations
-            int I;
-            float sw;
-            if constexpr (DT == Q8_0) {
-                I = dot16(w.q[2 * b + 1], ld16(aq + 32 * bb + 16), dot16(w.q[2 * b], ld16(aq + 32 * bb), 0));
-                sw = h2f((word(w.s, b >> 1) >> (16 * (b & 1))) & 0xffffu);
-            } else if constexpr (DT == Q4_0) {
-                I = dot16(hi_nib(w.q[b]), ld16(aq + 32 * bb + 16), dot16(lo_nib(w.q[b]), ld16(aq + 32 * bb), 0));
-                sw = h2f((word(w.s, b >> 1) >> (16 * (b & 1))) & 0xffffu);
-                if constexpr (FL == 1) I -= 8 * (s16[2 * bb] + s16[2 * bb + 1]);
-            } else {
-                I = dot16(mxfp4_codes4(hi_nib(w.q[b])), ld16(aq + 32 * bb + 16),
-                          dot16(mxfp4_codes4(lo_nib(w.q[b])), ld16(aq + 32 * bb), 0));
-                sw = e8m0_half((word(w.s, b >> 2) >> (8 * (b & 3))) & 0xffu);
-            }
-            // F1 (q256 engine, jam_gemm_q256.inc:28-36) and F2 (q8/q4_0/mxfp4_block16): fl(sw·da)·I;
-            // Q4_0 under F2 also takes − fl(8·d)·fl(xs0+xs1) (jam_kernels_q4k_avx512.c:463-480)
-            float v = (float) I * (sw * ad[bb]);
-            if constexpr (DT == Q4_0 && FL == 2) v -= (8.0f * sw) * (as[2 * bb] + as[2 * bb + 1]);
-            acc += b < nbv ? v : 0.0f;
-        }
-        return acc;
-    }
-}
-
-// Q4_0 F1 decode with 3..7 tokens: the group's nibbles and block scales unpacked once for all the tokens
-// (measured faster for Q4_0 only; the other types unpack per token in group_dot), then per token
-// group_dot's Q4_0 arithmetic.
-struct Q40Codes {
-    uint4 c[16];   // block b: low nibbles c[2b], high nibbles c[2b + 1]
-    float f[8];    // block scales
-};
-
-JAMHIP_DEV void q40_unpack(const Group<Q4_0>& w, Q40Codes& u) {
-#pragma unroll
-    for (int b = 0; b < 8; b++) {
-        u.c[2 * b] = lo_nib(w.q[b]);
-        u.c[2 * b + 1] = hi_nib(w.q[b]);
-        u.f[b] = h2f((word(w.s, b >> 1) >> (16 * (b & 1))) & 0xffffu);
-    }
-}
-
-JAMHIP_DEV float q40_dot_f1(const Q40Codes& u, const int8_t* aq, const float* ad, const int* s16, int nbv) {
-    float acc = 0.0f;
-#pragma unroll
-    for (int b = 0; b < 8; b++) {
-        const int bq = b < nbv ? b : nbv - 1;   // stay inside the token's activations
-        int I = dot16(u.c[2 * b + 1], ld16(aq + 32 * bq + 16), dot16(u.c[2 * b], ld16(aq + 32 * bq), 0));
-        I -= 8 * (s16[2 * bq] + s16[2 * bq + 1]);
-        const float v = (float) I * (u.f[b] * ad[bq]);   // q256 engine (jam_gemm_q256.inc:28-36): fl(sw·da)·I
-        acc += b < nbv ? v : 0.0f;
-    }
-    return acc;
-}
-
-// ------------------------------------------------------------------------------ fused F1 prologue
-// Quantizes NT activation rows into LDS with jam's F1 (quant.h) in the group layout: per token and group
-// 256 int8 codes padded to QS_LDS bytes (conflict-free reads), 8 block scales, 8 block sums, 16 Σq per 16.
-// One thread per 16-element half-block; the halves of a 32-block sit in adjacent lanes, which exchange
-// their |x| maxima and Σq. Elements past k (a partial last group) quantize as zeros.
-constexpr int QS_LDS = 272;
-constexpr int MV_WAVES = 8;   // waves per GEMV workgroup (512 threads)
-
-// The prologue runs in two steps so that its activation loads go out before the weight stream: a_load
-// issues HP unconditional half-block loads per thread (indices clamped; halves past k read as zero),
-// f1_store quantizes them and writes LDS. HP = ceil(NT·16·Gk / 512) half-blocks per thread.
-template <int HP> struct APre { float x[HP][16]; };
-
-template <int NT, int HP>
-JAMHIP_DEV void a_load(APre<HP>& pre, const float* __restrict__ a, int lda, int k, int Gk, int ntv) {
-    // four 16-byte loads per half-block (the launcher checks a and lda for 16-byte alignment); a half past
-    // the token's last element (a partial last group) re-reads the token's last half, zeroed by f1_store
-    // (zeroing here would make the wave wait for these loads before issuing the weight loads)
-    const int halves = 16 * Gk, total = NT * halves, kh = k >> 4;
-#pragma unroll
-    for (int i = 0; i < HP; i++) {
-        const int h0 = threadIdx.x + 64 * MV_WAVES * i, h = h0 < total ? h0 : total - 1;
-        const int j = NT == 1 ? 0 : h / halves, hh = h - j * halves, jr = j < ntv ? j : ntv - 1;   // rows past ntv: clamp
-        const bool in = hh < kh;   // clamp only; the zeroing happens in f1_store
-        const float4* src = reinterpret_cast<const float4*>(a + (int64_t) jr * lda + 16 * (in ? hh : kh - 1));
-#pragma unroll
-        for (int v = 0; v < 4; v++) {
-            const float4 f = src[v];
-            pre.x[i][4 * v + 0] = f.x;
-            pre.x[i][4 * v + 1] = f.y;
-            pre.x[i][4 * v + 2] = f.z;
-            pre.x[i][4 * v + 3] = f.w;
-        }
-    }
-}
-
-template <int NT, int HP>
-JAMHIP_DEV void f1_store(const APre<HP>& pre, int k, int Gk, int8_t* lq, float* ld, float* las, int* ls16, char* dummy) {
-    // branch-free: a thread past the last half-block (its loads were clamped) quantizes anyway and writes to
-    // a dummy LDS slot; pairs stay aligned because the half-block count is even
-    const int halves = 16 * Gk, total = NT * halves;
-#pragma unroll
-    for (int i = 0; i < HP; i++) {
-        const int h0 = threadIdx.x + 64 * MV_WAVES * i;
-        const bool valid = h0 < total;
-        const int h = valid ? h0 : 0;
-        const int j = NT == 1 ? 0 : h / halves, hh = h - j * halves;
-        const bool in = hh < (k >> 4);
-        float x[16];
-#pragma unroll
-        for (int e = 0; e < 16; e++) x[e] = in ? pre.x[i][e] : 0.0f;
-        float am = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 16; e++) am = fmaxf(am, fabsf(x[e]));
-        am = fmaxf(am, __shfl_xor(am, 1));
-        const float db = am / 127.0f;
-        const float id = db > 0.0f ? 1.0f / db : 0.0f;
-        uint32_t pk[4];
-#pragma unroll
-        for (int g = 0; g < 4; g++) {
-            uint32_t v = 0;
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                // lrintf then clamp; a NaN product (non-finite input) lands on -128 like LONG_MIN does
-                const int q = (int) fminf(fmaxf(rintf(x[4 * g + e] * id), -128.0f), 127.0f);
-                v |= (uint32_t) (q & 0xff) << (8 * e);
-            }
-            pk[g] = v;
-        }
-        int s = dot4((int) pk[0], 0x01010101, 0);
-        s = dot4((int) pk[1], 0x01010101, s);
-        s = dot4((int) pk[2], 0x01010101, s);
-        s = dot4((int) pk[3], 0x01010101, s);
-        const int s32 = s + __shfl_xor(s, 1);
-        int8_t* pq = valid ? lq + (int64_t) (j * Gk + (hh >> 4)) * QS_LDS + 16 * (hh & 15) : (int8_t*) dummy;
-        int* p16 = valid ? ls16 + j * halves + hh : (int*) (dummy + 16);
-        const bool first = (hh & 1) == 0;
-        float* pd = valid && first ? ld + j * 8 * Gk + (hh >> 1) : (float*) (dummy + 20);
-        float* ps = valid && first ? las + j * 8 * Gk + (hh >> 1) : (float*) (dummy + 24);
-        *reinterpret_cast<uint4*>(pq) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
-        *p16 = s;
-        *pd = db;
-        *ps = (float) s32;
-    }
-}
-
-// F2 activations staged in LDS (8-token tiles, already quantized by quant_f2_kernel into A): the tile's
-// codes in the fused layout (group g of token t at lq + (t·Gk + g)·QS_LDS), block scales (ld, 8 per group)
-// and per-16 sums (lx, 16 per group), copied once per workgroup so that the dot products read LDS instead
-// of each lane fetching its tokens' activations from L2. As for F1, f2_load's loads go out before the
-// weight stream and f2_store writes LDS after it. Tokens past ntv repeat token ntv - 1; 16-byte pieces
-// past k (a partial last group) re-read the row's last piece and are never read back (group_dot clamps
-// to the group's last valid block). HP = ceil(NT·Gk·16 / 512) code pieces per thread, 2·HP floats.
-template <int HP> struct FPre {
-    uint4 q[HP];
-    float f[2 * HP];
-};
-
-template <int NT, int HP>
-JAMHIP_DEV void f2_load(FPre<HP>& pre, const ActQ& A, int k, int Gk, int t0, int ntv) {
-    const int nb = k >> 5, units = NT * Gk * 16, nf = NT * 3 * nb;
-#pragma unroll
-    for (int i = 0; i < HP; i++) {
-        const int u0 = threadIdx.x + 64 * MV_WAVES * i, u = u0 < units ? u0 : units - 1;
-        const int t = u / (Gk * 16), r = u - t * Gk * 16, tc = t < ntv ? t : ntv - 1;
-        const int off = 256 * (r >> 4) + 16 * (r & 15);
-        pre.q[i] = ld16(A.q + (int64_t) (t0 + tc) * k + (off < k ? off : k - 16));
-    }
-#pragma unroll
-    for (int i = 0; i < 2 * HP; i++) {
-        const int v0 = threadIdx.x + 64 * MV_WAVES * i, v = v0 < nf ? v0 : nf - 1;
-        const int t = v / (3 * nb), r = v - t * 3 * nb, tc = t < ntv ? t : ntv - 1;
-        pre.f[i] = r < nb ? A.d[(int64_t) (t0 + tc) * nb + r] : A.s[(int64_t) (t0 + tc) * 2 * nb + (r - nb)];
-    }
-}
-
-template <int NT, int HP>
-JAMHIP_DEV void f2_store(const FPre<HP>& pre, int k, int Gk, int8_t* lq, float* ld, float* lx) {
-    const int nb = k >> 5, units = NT * Gk * 16, nf = NT * 3 * nb;
-#pragma unroll
-    for (int i = 0; i < HP; i++) {
-        const int u = threadIdx.x + 64 * MV_WAVES * i;
-        if (u < units) {
-            const int t = u / (Gk * 16), r = u - t * Gk * 16;
-            *reinterpret_cast<uint4*>(lq + (t * Gk + (r >> 4)) * QS_LDS + 16 * (r & 15)) = pre.q[i];
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < 2 * HP; i++) {
-        const int v = threadIdx.x + 64 * MV_WAVES * i;
-        if (v < nf) {
-            const int t = v / (3 * nb), r = v - t * 3 * nb;
-            if (r < nb) ld[t * 8 * Gk + r] = pre.f[i];
-            else lx[t * 16 * Gk + (r - nb)] = pre.f[i];
-        }
-    }
-}
-
-// ------------------------------------------------------------------------------------------ kernel
-// One workgroup (8 waves) computes one block of rows with straight-line code: the compiler can then count
-// every outstanding load exactly (a branch between a load and its use makes it drain the whole queue).
-// Lanes: RB consecutive rows (lane % RB) x GS = 64 / RB group slots (lane / RB), so chunk c of an item is
-// GS runs of 16·RB contiguous bytes in the row-tiled layout. An item is a band of RB rows x GS groups; a
-// row band needs J = ceil(Gk / GS) items and a block is QB bands x J items = at most 8·ITEMS items, wave w
-// taking items w·ITEMS .. w·ITEMS+ITEMS-1 (an item past the block re-reads a real group and adds nothing).
-// Order: the activation loads, then every weight load of the wave, then the F1 quantization into LDS
-// (waiting for the activations only), a barrier, the items in order, each lane parking its per-group
-// partial in LDS, and finally each row's J·GS partials summed in a fixed order (deterministic, no
-// atomics, no cross-lane shuffles).
-// FL = 1: F1 activations, NT = n (1..7). HP > 0: quantized into LDS by this workgroup (HP half-blocks
-// per thread); HP = 0: read from A. FL = 2: F2 activations from A; blockIdx.y picks NT tokens, the last
-// group may hold fewer (ntv).
-// GR (grouped matmul): FL = 1 takes expert blockIdx.y if it has 1..7 rows (ntv of them, CSR rows from
-// off[e]); FL = 2 takes the 8-token tile blockIdx.y of map8. The expert's weight rows start at e·gm.
-template <int DT, int FL, int NT, int HP, int RB, int ITEMS, bool GR>
-__global__ void __launch_bounds__(64 * MV_WAVES) mv_kernel(WeightView w, ActQ A, const float* __restrict__ a,
-                                                          int lda, int k, int m, int n, float* __restrict__ c,
-                                                          int ldc, Groups gp) {
-    constexpr int BPG = blocks_per_group(DT), GS = 64 / RB;
-    constexpr bool FUSE = HP > 0;
-    const int lane = threadIdx.x & 63, rr = lane % RB, gs = lane / RB;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int nb = k >> 5;                       // 32-blocks in the call
-    const int Gk = (nb + 7) >> 3;                // groups in the call
-    const int J = (Gk + GS - 1) / GS;            // items per row band
-    const int QB = MV_WAVES * ITEMS / J;         // bands per block (the launcher keeps J <= 8·ITEMS)
-    const int64_t q0 = (int64_t) blockIdx.x * QB;
-    int t0, ntv;
-    if constexpr (GR) {
-        int e, o, ne;
-        if constexpr (FL == 1) {
-            e = blockIdx.y;
-            o = __builtin_amdgcn_readfirstlane(gp.off[e]);
-            ne = __builtin_amdgcn_readfirstlane(gp.off[e + 1]) - o;
-            if (ne <= 0 || ne >= 8) return;   // whole workgroup, before any barrier
-            t0 = o;
-            ntv = ne;
-            a += (int64_t) o * lda;
-        } else {
-            e = __builtin_amdgcn_readfirstlane(gp.map8[blockIdx.y]);
-            if (e < 0) return;
-            const int local = (int) blockIdx.y * 8 - __builtin_amdgcn_readfirstlane(gp.poff8[e]);
-            o = __builtin_amdgcn_readfirstlane(gp.off[e]);
-            ne = __builtin_amdgcn_readfirstlane(gp.off[e + 1]) - o;
-            t0 = o + local;
-            ntv = ne - local < NT ? ne - local : NT;
-        }
-        w.r0 += (int64_t) e * gp.gm;
-        m = gp.gm;
-    } else {
-        t0 = blockIdx.y * NT;
-        ntv = n - t0 < NT ? n - t0 : NT;
-    }
-
-    // Only waves that own at least one real half-block of the activations load and quantize them (the
-    // others would only write the dummy slot); the condition is wave-uniform. Their loads go first in the
-    // load queue and are kept there by the scheduler.
-    const bool pro = FUSE && FL == 1 && wave * 64 < NT * 16 * Gk;
-    APre<FUSE && FL == 1 ? HP : 1> pre;
-    FPre<FUSE && FL == 2 ? HP : 1> fpre;
-    if constexpr (FUSE && FL == 1)
-        if (pro) a_load<NT, HP>(pre, a, lda, k, Gk, ntv);
-    if constexpr (FUSE && FL == 2) f2_load<NT, HP>(fpre, A, k, Gk, t0, ntv);
-    __builtin_amdgcn_sched_barrier(0);
-
-    // item i of this wave: band q0 + it / J, group slot it % J with it = wave·ITEMS + i (clamped)
-    Group<DT> buf[ITEMS];
-#pragma unroll
-    for (int i = 0; i < ITEMS; i++) {
-        const int it = wave * ITEMS + i;
-        int64_t row = RB * (q0 + it / J) + rr;
-        row = row < m ? row : m - 1;
-        int g = GS * (it % J) + gs;
-        g = g < Gk ? g : Gk - 1;
-        load_group<DT>(buf[i], w, row, g);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-
-    extern __shared__ __align__(16) unsigned char smem[];
-    float* part = reinterpret_cast<float*>(smem);   // [8·ITEMS][GS][RB][NT] lane partials
-    const int8_t* aq = A.q;
-    const float* ad = A.d;
-    const float* as = A.s;
-    const int* s16 = A.s16;
-    int64_t tq = k, td = nb, ts = FL == 1 ? nb : 2 * nb, t16 = 2 * nb;
-    int QS = 256;
-    if constexpr (FUSE) {
-        char* dummy = reinterpret_cast<char*>(smem + MV_WAVES * ITEMS * 64 * NT * 4);   // 32 bytes
-        int8_t* lq = reinterpret_cast<int8_t*>(dummy + 32);
-        float* ld = reinterpret_cast<float*>(lq + NT * Gk * QS_LDS);
-        float* las = ld + NT * 8 * Gk;
-        int* ls16 = reinterpret_cast<int*>(las + NT * 8 * Gk);
-        aq = lq;
-        ad = ld;
-        tq = (int64_t) Gk * QS_LDS;
-        td = 8 * Gk;
-        QS = QS_LDS;
-        if constexpr (FL == 1) {
-            if (pro) f1_store<NT, HP>(pre, k, Gk, lq, ld, las, ls16, dummy);
-            as = las;
-            s16 = ls16;
-            ts = 8 * Gk;
-            t16 = 16 * Gk;
-        } else {   // F2: per-16 sums in the Σq-per-16 region (16 per group and token)
-            float* lx = reinterpret_cast<float*>(ls16);
-            f2_store<NT, HP>(fpre, k, Gk, lq, ld, lx);
-            as = lx;
-            ts = 16 * Gk;
-        }
-        __syncthreads();
-    }
-
-#pragma unroll
-    for (int i = 0; i < ITEMS; i++) {
-        const int it = wave * ITEMS + i;
-        const int g = GS * (it % J) + gs;
-        const bool live = g < Gk && it < QB * J && RB * (q0 + it / J) + rr < m;
-        const int gg = g < Gk ? g : Gk - 1;
-        const int nbv = nb - BPG * gg < BPG ? nb - BPG * gg : BPG;
-        float* pp = part + (it * 64 + lane) * NT;
-        if constexpr (NT <= 2 || FL == 2 || DT != Q4_0) {   // per-token unpacking measured faster for the rest
-            constexpr int TU = NT > 2 ? 1 : NT;   // keep several tokens' temporaries out of the register file
-#pragma unroll TU
-            for (int t = 0; t < NT; t++) {
-                if (t >= ntv) break;
-                const int tt = FUSE ? t : t0 + t;
-                const float p = group_dot<DT, FL>(buf[i], aq + tt * tq + (int64_t) gg * QS, ad + tt * td + 8 * gg,
-                                                  as + tt * ts + (FL == 1 ? 8 : 16) * gg, s16 + tt * t16 + 16 * gg,
-                                                  nbv);
-                pp[t] = live ? p : 0.0f;
-            }
-        } else {   // Q4_0 F1, 3..7 tokens: the group's weights unpacked once for all the tokens
-            Q40Codes u;
-            q40_unpack(buf[i], u);
-#pragma unroll 1
-            for (int t = 0; t < NT; t++) {
-                if (t >= ntv) break;
-                const int tt = FUSE ? t : t0 + t;
-                const float p = q40_dot_f1(u, aq + tt * tq + (int64_t) gg * QS, ad + tt * td + 8 * gg,
-                                           s16 + tt * t16 + 16 * gg, nbv);
-                pp[t] = live ? p : 0.0f;
-            }
-        }
-    }
-    __syncthreads();
-    // (band, row, token) of the block: sum its J x GS partials in order; QB·RB·NT can exceed the 512 threads
-    for (int tid = threadIdx.x; tid < QB * RB * NT; tid += 64 * MV_WAVES) {
-        const int q = tid / (RB * NT), r = (tid / NT) % RB, t = tid % NT;
-        float v = 0.0f;
-        for (int j = 0; j < J; j++)
-#pragma unroll
-            for (int s2 = 0; s2 < GS; s2++) v += part[(((q * J + j) * 64) + s2 * RB + r) * NT + t];
-        const int64_t row = RB * (q0 + q) + r;
-        if (row < m && t < ntv) c[(int64_t) (t0 + t) * ldc + row] = v;
-    }
-}
-
-// ----------------------------------------------------------------------------- float-dot tail rows
-// The last m % 16 rows of an n >= 8 call: jam's bands compute them with an exact float dot of the
-// dequantized weight against the f32 activations ("<16-row tail: scalar exact dot",
-// jam_kernels_q4k_avx512.c:185-188 and its siblings). One wave per (row, 8-token group); lane l takes
-// the 32-element chunks l, l+64, ...; products accumulate in f32.
-template <int DT>
-JAMHIP_DEV float deq(const WeightView& w, int64_t row, int elem) {
-    const int64_t g = elem >> 8;
-    const int e = elem & 255;
-    const uint8_t* q = group_q<DT>(w, row, g);
-    const uint8_t* s = group_s<DT>(w, row, g);
-    auto qb = [&](int byte) { return q[(byte >> 4) * CHUNK_STRIDE + (byte & 15)]; };   // group byte
-    auto f16 = [&](const uint8_t* p) { return h2f((uint32_t) p[0] | ((uint32_t) p[1] << 8)); };
-    if constexpr (DT == Q8_0) {
-        return f16(s + 2 * (e >> 5)) * (float) (int8_t) qb(e);
-    } else if constexpr (DT == Q4_0) {
-        const uint8_t b = qb(16 * (e >> 5) + (e & 15));
-        return f16(s + 2 * (e >> 5)) * (float) (((e & 31) < 16 ? b & 15 : b >> 4) - 8);
-    } else if constexpr (DT == MXFP4) {
-        const uint8_t b = qb(16 * (e >> 5) + (e & 15));
-        const uint32_t code = mxfp4_codes((e & 31) < 16 ? b & 15 : b >> 4);
-        return e8m0_half(s[e >> 5]) * (float) (int8_t) (code & 0xff);
-    } else if constexpr (DT == Q4_K) {
-        const int gp = e >> 6, half = (e >> 5) & 1, l = e & 31, sb = 2 * gp + half;
-        const uint8_t b = qb(32 * gp + l);
-        const uint4 h = make_uint4(s[0] | s[1] << 8 | s[2] << 16 | (uint32_t) s[3] << 24,
-                                   s[4] | s[5] << 8 | s[6] << 16 | (uint32_t) s[7] << 24,
-                                   s[8] | s[9] << 8 | s[10] << 16 | (uint32_t) s[11] << 24,
-                                   s[12] | s[13] << 8 | s[14] << 16 | (uint32_t) s[15] << 24);
-        int sc, mn;
-        q4k_sm(h, sb, sc, mn);
-        return f16(s) * (float) sc * (float) (half ? b >> 4 : b & 15) - f16(s + 2) * (float) mn;
-    } else {
-        const int hh = e >> 7, j = (e & 127) >> 5, l = e & 31;
-        const uint8_t qlb = qb(64 * hh + (j & 1) * 32 + l);
-        const int q6 = (j < 2 ? qlb & 15 : qlb >> 4) | (((qb(128 + 32 * hh + l) >> (2 * j)) & 3) << 4);
-        const int sc = (int) (int8_t) qb(192 + 8 * hh + 2 * j + l / 16);
-        return f16(s) * (float) sc * (float) (q6 - 32);
-    }
-}
-
-template <int DT>
-__global__ void __launch_bounds__(64) rows_float_kernel(WeightView w, const float* __restrict__ a, int lda, int k,
-                                                        int r0, int n, float* __restrict__ c, int ldc) {
-    const int64_t row = r0 + blockIdx.x;
-    const int t0 = blockIdx.y * 8, nt = n - t0 < 8 ? n - t0 : 8;
-    const int lane = threadIdx.x;
-    float acc[8];
-#pragma unroll
-    for (int t = 0; t < 8; t++) acc[t] = 0.0f;
-    for (int chunk = lane; chunk < k / 32; chunk += 64) {   // 32 consecutive elements per lane and step
-        for (int e = 32 * chunk; e < 32 * chunk + 32; e++) {
-            const float v = deq<DT>(w, row, e);
-#pragma unroll
-            for (int t = 0; t < 8; t++)
-                if (t < nt) acc[t] += v * a[(int64_t) (t0 + t) * lda + e];
-        }
-    }
-#pragma unroll
-    for (int t = 0; t < 8; t++) {
-        const float v = wave_sum(acc[t]);
-        if (lane == 0 && t < nt) c[(int64_t) (t0 + t) * ldc + row] = v;
-    }
-}
-
-// ---------------------------------------------------------------------------------------- launchers
-// Fused F1 quantization keeps A's codes, scales and sums in LDS: 400 bytes per token and group; its
-// prologue holds up to 4 half-blocks of A per thread in registers.
-constexpr int kFuseMaxBytes = 96 * 1024;
-static size_t fuse_lds(int n, int k) { return (size_t) n * ((k / 32 + 7) / 8) * (QS_LDS + 32 + 32 + 64); }
-static int fuse_hp(int n, int k) { return (n * 16 * ((k / 32 + 7) / 8) + 64 * MV_WAVES - 1) / (64 * MV_WAVES); }
-
-// Work split: bands of RB = 8 rows (x 8 group slots: chunk loads are 128-byte lines; 16-row bands measured
-// slower at every BASELINE shape) and the fewest items per wave that fit a band in one block, 1, 2 or 4
-// for k up to 16384, 32768, 65536. More items per wave only add registers. JAM_HIP_MV_ITEMS overrides
-// (tuning sweeps). Returns false past k = 65536.
-constexpr int MV_RB = 8;
-static bool mv_items(int k, int* items) {
-    const int Gk = (k / 32 + 7) / 8, J = (Gk + 64 / MV_RB - 1) / (64 / MV_RB);
-    const char* vi = getenv("JAM_HIP_MV_ITEMS");
-    int it = vi ? atoi(vi) : 1;
-    const int lo = (J + MV_WAVES - 1) / MV_WAVES;
-    it = it < lo ? lo : it;
-    it = it <= 1 ? 1 : it <= 2 ? 2 : 4;
-    *items = it;
-    return J <= MV_WAVES * it;
-}
-
-template <int DT, int FL, int NT, int HP, int RB, int ITEMS>
-static void launch_shape(int k, int m, int n, const WeightView& w, const ActQ& A, const float* a, int lda, float* c,
-                         int ldc, hipStream_t st) {
-    constexpr int GS = 64 / RB;
-    const int Gk = (k / 32 + 7) / 8, J = (Gk + GS - 1) / GS;
-    const int QB = MV_WAVES * ITEMS / J;
-    const int64_t bands = ((int64_t) m + RB - 1) / RB;
-    const dim3 grid((unsigned) ((bands + QB - 1) / QB), FL == 1 ? 1 : (n + NT - 1) / NT);
-    const size_t lds = (size_t) MV_WAVES * ITEMS * 64 * NT * sizeof(float) + (HP > 0 ? 32 + fuse_lds(NT, k) : 0);
-    mv_kernel<DT, FL, NT, HP, RB, ITEMS, false><<<grid, 64 * MV_WAVES, lds, st>>>(w, A, a, lda, k, m, n, c, ldc,
-                                                                                 Groups{});
-}
-
-template <int DT, int FL, int NT, int HP, int RB, int ITEMS>
-static void launch_shape_grouped(int k, const Groups& g, int ny, const WeightView& w, const ActQ& A, const float* a,
-                                 int lda, float* c, int ldc, hipStream_t st) {
-    constexpr int GS = 64 / RB;
-    const int Gk = (k / 32 + 7) / 8, J = (Gk + GS - 1) / GS;
-    const int QB = MV_WAVES * ITEMS / J;
-    const int64_t bands = ((int64_t) g.gm + RB - 1) / RB;
-    const dim3 grid((unsigned) ((bands + QB - 1) / QB), (unsigned) ny);
-    const size_t lds = (size_t) MV_WAVES * ITEMS * 64 * NT * sizeof(float) + (HP > 0 ? 32 + fuse_lds(NT, k) : 0);
-    mv_kernel<DT, FL, NT, HP, RB, ITEMS, true><<<grid, 64 * MV_WAVES, lds, st>>>(w, A, a, lda, k, g.gm, 0, c, ldc, g);
-}
-
-template <int DT, int FL, int NT, int HP>
-static hipError_t go_grouped(int k, const Groups& g, int ny, const WeightView& w, const ActQ& A, const float* a,
-                             int lda, float* c, int ldc, hipStream_t st) {
-    int items;
-    if (!mv_items(k, &items)) return hipErrorNotSupported;
-    if (items == 1) launch_shape_grouped<DT, FL, NT, HP, MV_RB, 1>(k, g, ny, w, A, a, lda, c, ldc, st);
-    else if (items == 2) launch_shape_grouped<DT, FL, NT, HP, MV_RB, 2>(k, g, ny, w, A, a, lda, c, ldc, st);
-    else launch_shape_grouped<DT, FL, NT, HP, MV_RB, 4>(k, g, ny, w, A, a, lda, c, ldc, st);
-    return hipGetLastError();
-}
-
-template <int DT>
-static hipError_t gemv_grouped_dt(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k,
-                                  const Groups& g, int E, int cap8, float* c, int ldc, hipStream_t st) {
-    if (flavour == 2) return go_grouped<DT, 2, 8, 0>(k, g, cap8, w, A, nullptr, 0, c, ldc, st);
-    if (a == nullptr) return go_grouped<DT, 1, 7, 0>(k, g, E, w, A, nullptr, 0, c, ldc, st);
-    const int hp = fuse_hp(7, k);
-    if (hp <= 1) return go_grouped<DT, 1, 7, 1>(k, g, E, w, A, a, lda, c, ldc, st);
-    if (hp == 2) return go_grouped<DT, 1, 7, 2>(k, g, E, w, A, a, lda, c, ldc, st);
-    return go_grouped<DT, 1, 7, 4>(k, g, E, w, A, a, lda, c, ldc, st);
-}
+extern template hipError_t gemv_dt<Q4_K>(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m, int n, float* c, int ldc, hipStream_t st);
+extern template hipError_t gemv_grouped_dt<Q4_K>(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, const Groups& g, int E, int cap8, float* c, int ldc, hipStream_t st);
+extern template hipError_t rows_float_dt<Q4_K>(const WeightView& w, const float* a, int lda, int k, int r0, int rows, int n, float* c, int ldc, hipStream_t st);
+extern template hipError_t gemv_dt<Q6_K>(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m, int n, float* c, int ldc, hipStream_t st);
+extern template hipError_t gemv_grouped_dt<Q6_K>(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, const Groups& g, int E, int cap8, float* c, int ldc, hipStream_t st);
+extern template hipError_t rows_float_dt<Q6_K>(const WeightView& w, const float* a, int lda, int k, int r0, int rows, int n, float* c, int ldc, hipStream_t st);
+extern template hipError_t gemv_dt<Q8_0>(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m, int n, float* c, int ldc, hipStream_t st);
+extern template hipError_t gemv_grouped_dt<Q8_0>(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, const Groups& g, int E, int cap8, float* c, int ldc, hipStream_t st);
+extern template hipError_t rows_float_dt<Q8_0>(const WeightView& w, const float* a, int lda, int k, int r0, int rows, int n, float* c, int ldc, hipStream_t st);
+extern template hipError_t gemv_dt<Q4_0>(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m, int n, float* c, int ldc, hipStream_t st);
+extern template hipError_t gemv_grouped_dt<Q4_0>(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, const Groups& g, int E, int cap8, float* c, int ldc, hipStream_t st);
+extern template hipError_t rows_float_dt<Q4_0>(const WeightView& w, const float* a, int lda, int k, int r0, int rows, int n, float* c, int ldc, hipStream_t st);
+extern template hipError_t gemv_dt<MXFP4>(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m, int n, float* c, int ldc, hipStream_t st);
+extern template hipError_t gemv_grouped_dt<MXFP4>(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, const Groups& g, int E, int cap8, float* c, int ldc, hipStream_t st);
+extern template hipError_t rows_float_dt<MXFP4>(const WeightView& w, const float* a, int lda, int k, int r0, int rows, int n, float* c, int ldc, hipStream_t st);
 
 hipError_t launch_gemv_grouped(int dt, int flavour, const WeightView& w, const ActQ& A, const float* a, int lda,
                                int k, const Groups& g, int E, int cap8, float* c, int ldc, hipStream_t st) {
@@ -667,56 +29,6 @@ hipError_t launch_gemv_grouped(int dt, int flavour, const WeightView& w, const A
     case Q8_0: return gemv_grouped_dt<Q8_0>(flavour, w, A, a, lda, k, g, E, cap8, c, ldc, st);
     case Q4_0: return gemv_grouped_dt<Q4_0>(flavour, w, A, a, lda, k, g, E, cap8, c, ldc, st);
     case MXFP4: return gemv_grouped_dt<MXFP4>(flavour, w, A, a, lda, k, g, E, cap8, c, ldc, st);
-    default: return hipErrorInvalidValue;
-    }
-}
-
-template <int DT, int FL, int NT, int HP>
-static hipError_t go_hp(int k, int m, int n, const WeightView& w, const ActQ& A, const float* a, int lda, float* c,
-                        int ldc, hipStream_t st) {
-    int items;
-    if (!mv_items(k, &items)) return hipErrorNotSupported;
-    if (items == 1) launch_shape<DT, FL, NT, HP, MV_RB, 1>(k, m, n, w, A, a, lda, c, ldc, st);
-    else if (items == 2) launch_shape<DT, FL, NT, HP, MV_RB, 2>(k, m, n, w, A, a, lda, c, ldc, st);
-    else launch_shape<DT, FL, NT, HP, MV_RB, 4>(k, m, n, w, A, a, lda, c, ldc, st);
-    return hipGetLastError();
-}
-
-template <int DT, int FL, int NT>
-static hipError_t go(const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m, int n, float* c,
-                     int ldc, hipStream_t st) {
-    if constexpr (FL == 2) {   // stage the tile's activations in LDS when they fit
-        const int hp = (NT * ((k / 32 + 7) / 8) * 16 + 64 * MV_WAVES - 1) / (64 * MV_WAVES);
-        if (fuse_lds(NT, k) <= (size_t) kFuseMaxBytes && hp <= 8) {
-            if (hp <= 1) return go_hp<DT, FL, NT, 1>(k, m, n, w, A, a, lda, c, ldc, st);
-            if (hp == 2) return go_hp<DT, FL, NT, 2>(k, m, n, w, A, a, lda, c, ldc, st);
-            if (hp <= 4) return go_hp<DT, FL, NT, 4>(k, m, n, w, A, a, lda, c, ldc, st);
-            return go_hp<DT, FL, NT, 8>(k, m, n, w, A, a, lda, c, ldc, st);
-        }
-    }
-    if constexpr (FL == 1) {
-        if (a != nullptr) {
-            const int hp = fuse_hp(NT, k);
-            if (hp <= 1) return go_hp<DT, FL, NT, 1>(k, m, n, w, A, a, lda, c, ldc, st);
-            if (hp == 2) return go_hp<DT, FL, NT, 2>(k, m, n, w, A, a, lda, c, ldc, st);
-            return go_hp<DT, FL, NT, 4>(k, m, n, w, A, a, lda, c, ldc, st);
-        }
-    }
-    return go_hp<DT, FL, NT, 0>(k, m, n, w, A, a, lda, c, ldc, st);
-}
-
-template <int DT>
-static hipError_t gemv_dt(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m,
-                          int n, float* c, int ldc, hipStream_t st) {
-    if (flavour == 2) return go<DT, 2, 8>(w, A, nullptr, 0, k, m, n, c, ldc, st);
-    switch (n) {
-    case 1: return go<DT, 1, 1>(w, A, a, lda, k, m, n, c, ldc, st);
-    case 2: return go<DT, 1, 2>(w, A, a, lda, k, m, n, c, ldc, st);
-    case 3: return go<DT, 1, 3>(w, A, a, lda, k, m, n, c, ldc, st);
-    case 4: return go<DT, 1, 4>(w, A, a, lda, k, m, n, c, ldc, st);
-    case 5: return go<DT, 1, 5>(w, A, a, lda, k, m, n, c, ldc, st);
-    case 6: return go<DT, 1, 6>(w, A, a, lda, k, m, n, c, ldc, st);
-    case 7: return go<DT, 1, 7>(w, A, a, lda, k, m, n, c, ldc, st);
     default: return hipErrorInvalidValue;
     }
 }
@@ -741,16 +53,14 @@ hipError_t launch_gemv(int dt, int flavour, const WeightView& w, const ActQ& A, 
 hipError_t launch_rows_float(int dt, const WeightView& w, const float* a, int lda, int k, int r0, int rows, int n,
                              float* c, int ldc, hipStream_t st) {
     if (rows <= 0) return hipSuccess;
-    const dim3 grid((unsigned) rows, (unsigned) ((n + 7) / 8));
     switch (dt) {
-    case Q4_K: rows_float_kernel<Q4_K><<<grid, 64, 0, st>>>(w, a, lda, k, r0, n, c, ldc); break;
-    case Q6_K: rows_float_kernel<Q6_K><<<grid, 64, 0, st>>>(w, a, lda, k, r0, n, c, ldc); break;
-    case Q8_0: rows_float_kernel<Q8_0><<<grid, 64, 0, st>>>(w, a, lda, k, r0, n, c, ldc); break;
-    case Q4_0: rows_float_kernel<Q4_0><<<grid, 64, 0, st>>>(w, a, lda, k, r0, n, c, ldc); break;
-    case MXFP4: rows_float_kernel<MXFP4><<<grid, 64, 0, st>>>(w, a, lda, k, r0, n, c, ldc); break;
+    case Q4_K: return rows_float_dt<Q4_K>(w, a, lda, k, r0, rows, n, c, ldc, st);
+    case Q6_K: return rows_float_dt<Q6_K>(w, a, lda, k, r0, rows, n, c, ldc, st);
+    case Q8_0: return rows_float_dt<Q8_0>(w, a, lda, k, r0, rows, n, c, ldc, st);
+    case Q4_0: return rows_float_dt<Q4_0>(w, a, lda, k, r0, rows, n, c, ldc, st);
+    case MXFP4: return rows_float_dt<MXFP4>(w, a, lda, k, r0, rows, n, c, ldc, st);
     default: return hipErrorInvalidValue;
     }
-    return hipGetLastError();
 }
 
 }  // namespace jamhip
