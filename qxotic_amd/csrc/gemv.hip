@@ -4,19 +4,19 @@
 
 namespace jamhip {
 
-extern template hipError_t gemv_dt<Q4_K>(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m, int n, float* c, int ldc, hipStream_t st);
+extern template hipError_t gemv_dt<Q4_K>(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m, int n, float* c, int ldc, hipStream_t st, float* part);
 extern template hipError_t gemv_grouped_dt<Q4_K>(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, const Groups& g, int E, int cap8, float* c, int ldc, hipStream_t st);
 extern template hipError_t rows_float_dt<Q4_K>(const WeightView& w, const float* a, int lda, int k, int r0, int rows, int n, float* c, int ldc, hipStream_t st);
-extern template hipError_t gemv_dt<Q6_K>(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m, int n, float* c, int ldc, hipStream_t st);
+extern template hipError_t gemv_dt<Q6_K>(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m, int n, float* c, int ldc, hipStream_t st, float* part);
 extern template hipError_t gemv_grouped_dt<Q6_K>(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, const Groups& g, int E, int cap8, float* c, int ldc, hipStream_t st);
 extern template hipError_t rows_float_dt<Q6_K>(const WeightView& w, const float* a, int lda, int k, int r0, int rows, int n, float* c, int ldc, hipStream_t st);
-extern template hipError_t gemv_dt<Q8_0>(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m, int n, float* c, int ldc, hipStream_t st);
+extern template hipError_t gemv_dt<Q8_0>(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m, int n, float* c, int ldc, hipStream_t st, float* part);
 extern template hipError_t gemv_grouped_dt<Q8_0>(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, const Groups& g, int E, int cap8, float* c, int ldc, hipStream_t st);
 extern template hipError_t rows_float_dt<Q8_0>(const WeightView& w, const float* a, int lda, int k, int r0, int rows, int n, float* c, int ldc, hipStream_t st);
-extern template hipError_t gemv_dt<Q4_0>(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m, int n, float* c, int ldc, hipStream_t st);
+extern template hipError_t gemv_dt<Q4_0>(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m, int n, float* c, int ldc, hipStream_t st, float* part);
 extern template hipError_t gemv_grouped_dt<Q4_0>(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, const Groups& g, int E, int cap8, float* c, int ldc, hipStream_t st);
 extern template hipError_t rows_float_dt<Q4_0>(const WeightView& w, const float* a, int lda, int k, int r0, int rows, int n, float* c, int ldc, hipStream_t st);
-extern template hipError_t gemv_dt<MXFP4>(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m, int n, float* c, int ldc, hipStream_t st);
+extern template hipError_t gemv_dt<MXFP4>(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m, int n, float* c, int ldc, hipStream_t st, float* part);
 extern template hipError_t gemv_grouped_dt<MXFP4>(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, const Groups& g, int E, int cap8, float* c, int ldc, hipStream_t st);
 extern template hipError_t rows_float_dt<MXFP4>(const WeightView& w, const float* a, int lda, int k, int r0, int rows, int n, float* c, int ldc, hipStream_t st);
 
@@ -33,19 +33,28 @@ hipError_t launch_gemv_grouped(int dt, int flavour, const WeightView& w, const A
     }
 }
 
-bool gemv_fusable(int n, int k, const float* a, int lda) {
-    return n < 8 && fuse_lds(n, k) <= (size_t) kFuseMaxBytes && fuse_hp(n, k) <= 4 &&
+// The fused F1 prologue quantizes one K slice of n tokens per workgroup into LDS (at most 4 half-blocks per
+// thread); ks = the slice length (gemv_slice(k, n) for a launch_gemv call, k for the grouped kernels).
+static bool fusable_slice(int n, int ks, const float* a, int lda) {
+    return n < 8 && fuse_lds(n, ks) <= (size_t) kFuseMaxBytes && fuse_hp(n, ks) <= 4 &&
            (reinterpret_cast<uintptr_t>(a) & 15) == 0 && (lda & 3) == 0;
+}
+bool gemv_fusable(int n, int k, const float* a, int lda) { return fusable_slice(n, gemv_slice(k, n), a, lda); }
+bool gemv_grouped_fusable(int k, const float* a, int lda) { return fusable_slice(7, k, a, lda); }
+
+size_t gemv_split_floats(int k, int m, int n) {
+    const int ks = gemv_slice(k, n);
+    return ks < k ? (size_t) ((k + ks - 1) / ks) * n * m : 0;
 }
 
 hipError_t launch_gemv(int dt, int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m,
-                       int n, float* c, int ldc, hipStream_t st) {
+                       int n, float* c, int ldc, hipStream_t st, float* part) {
     switch (dt) {
-    case Q4_K: return gemv_dt<Q4_K>(flavour, w, A, a, lda, k, m, n, c, ldc, st);
-    case Q6_K: return gemv_dt<Q6_K>(flavour, w, A, a, lda, k, m, n, c, ldc, st);
-    case Q8_0: return gemv_dt<Q8_0>(flavour, w, A, a, lda, k, m, n, c, ldc, st);
-    case Q4_0: return gemv_dt<Q4_0>(flavour, w, A, a, lda, k, m, n, c, ldc, st);
-    case MXFP4: return gemv_dt<MXFP4>(flavour, w, A, a, lda, k, m, n, c, ldc, st);
+    case Q4_K: return gemv_dt<Q4_K>(flavour, w, A, a, lda, k, m, n, c, ldc, st, part);
+    case Q6_K: return gemv_dt<Q6_K>(flavour, w, A, a, lda, k, m, n, c, ldc, st, part);
+    case Q8_0: return gemv_dt<Q8_0>(flavour, w, A, a, lda, k, m, n, c, ldc, st, part);
+    case Q4_0: return gemv_dt<Q4_0>(flavour, w, A, a, lda, k, m, n, c, ldc, st, part);
+    case MXFP4: return gemv_dt<MXFP4>(flavour, w, A, a, lda, k, m, n, c, ldc, st, part);
     default: return hipErrorInvalidValue;
     }
 }

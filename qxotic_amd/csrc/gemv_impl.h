@@ -331,21 +331,23 @@ template <int SP> struct FPre {
     float f[2 * SP];
 };
 
+// k: the row length of A (its stride); elements [k0, k0 + kl) of each token are staged (k0 % 256 == 0).
 template <int NT, int SP>
-JAMHIP_DEV void stage_load(FPre<SP>& pre, const ActQ& A, int k, int Gk, int t0, int ntv) {
-    const int nb = k >> 5, units = NT * Gk * 16, nf = NT * 3 * nb;
+JAMHIP_DEV void stage_load(FPre<SP>& pre, const ActQ& A, int k, int k0, int kl, int Gk, int t0, int ntv) {
+    const int nbf = k >> 5, nb = kl >> 5, units = NT * Gk * 16, nf = NT * 3 * nb;
 #pragma unroll
     for (int i = 0; i < SP; i++) {
         const int u0 = threadIdx.x + 64 * MV_WAVES * i, u = u0 < units ? u0 : units - 1;
         const int t = u / (Gk * 16), r = u - t * Gk * 16, tc = t < ntv ? t : ntv - 1;
         const int off = 256 * (r >> 4) + 16 * (r & 15);
-        pre.q[i] = ld16(A.q + (int64_t) (t0 + tc) * k + (off < k ? off : k - 16));
+        pre.q[i] = ld16(A.q + (int64_t) (t0 + tc) * k + k0 + (off < kl ? off : kl - 16));
     }
 #pragma unroll
     for (int i = 0; i < 2 * SP; i++) {
         const int v0 = threadIdx.x + 64 * MV_WAVES * i, v = v0 < nf ? v0 : nf - 1;
         const int t = v / (3 * nb), r = v - t * 3 * nb, tc = t < ntv ? t : ntv - 1;
-        pre.f[i] = r < nb ? A.d[(int64_t) (t0 + tc) * nb + r] : A.s[(int64_t) (t0 + tc) * 2 * nb + (r - nb)];
+        pre.f[i] = r < nb ? A.d[(int64_t) (t0 + tc) * nbf + (k0 >> 5) + r]
+                          : A.s[(int64_t) (t0 + tc) * 2 * nbf + (k0 >> 4) + (r - nb)];
     }
 }
 
@@ -387,11 +389,20 @@ JAMHIP_DEV void stage_store(const FPre<SP>& pre, int k, int Gk, int8_t* lq, floa
 // group may hold fewer (ntv).
 // GR (grouped matmul): FL = 1 takes expert blockIdx.y if it has 1..7 rows (ntv of them, CSR rows from
 // off[e]); FL = 2 takes the 8-token tile blockIdx.y of map8. The expert's weight rows start at e·gm.
-template <int DT, int FL, int NT, int HP, int RB, int ITEMS, bool GR>
+template <int DT, int FL, int NT, int HP, int RB, int ITEMS, bool GR, bool SK>
 __global__ void __launch_bounds__(64 * MV_WAVES) mv_kernel(WeightView w, ActQ A, const float* __restrict__ a,
                                                           int lda, int k, int m, int n, float* __restrict__ c,
-                                                          int ldc, Groups gp) {
+                                                          int ldc, Groups gp, int ks, int64_t cz) {
     constexpr int BPG = blocks_per_group(DT), GS = 64 / RB;
+    // SK (split K): workgroup column blockIdx.z takes elements [k0, k0 + ks) (ks a multiple of 256; the last
+    // slice may be shorter) and writes its partial result at c + blockIdx.z·cz; J, and so the block shape,
+    // comes from the full slice length, so every slice has the same grid
+    const int k0 = SK ? (int) blockIdx.z * ks : 0, kf = k;
+    if constexpr (SK) {
+        k = kf - k0 < ks ? kf - k0 : ks;
+        c += (int64_t) blockIdx.z * cz;
+        if constexpr (FL == 1 && HP > 0) a += k0;   // the fused prologue's rows (null otherwise)
+    }
     // HP > 0: F1, A quantized into LDS by this workgroup (HP half-blocks per thread); F2, the quantized A
     // staged in LDS (stage_load, HP pieces per thread)
     constexpr bool QF1 = FL == 1 && HP > 0;
@@ -400,9 +411,10 @@ __global__ void __launch_bounds__(64 * MV_WAVES) mv_kernel(WeightView w, ActQ A,
     constexpr bool FUSE = HP > 0;
     const int lane = threadIdx.x & 63, rr = lane % RB, gs = lane / RB;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int nb = k >> 5;                       // 32-blocks in the call
-    const int Gk = (nb + 7) >> 3;                // groups in the call
-    const int J = (Gk + GS - 1) / GS;            // items per row band
+    const int nb = k >> 5;                       // 32-blocks in the slice
+    const int Gk = (nb + 7) >> 3;                // groups in the slice
+    const int J = ((SK ? ((ks >> 5) + 7) / 8 : Gk) + GS - 1) / GS;   // items per row band
+    const int g0 = k0 >> 8;                      // the slice's first group
     const int QB = MV_WAVES * ITEMS / J;         // bands per block (the launcher keeps J <= 8·ITEMS)
     const int64_t q0 = (int64_t) blockIdx.x * QB;
     int t0, ntv;
@@ -440,7 +452,7 @@ __global__ void __launch_bounds__(64 * MV_WAVES) mv_kernel(WeightView w, ActQ A,
     FPre<STG ? SP : 1> fpre;
     if constexpr (QF1)
         if (pro) a_load<NT, QF1 ? HP : 1>(pre, a, lda, k, Gk, ntv);
-    if constexpr (STG) stage_load<NT, SP>(fpre, A, k, Gk, t0, ntv);
+    if constexpr (STG) stage_load<NT, SP>(fpre, A, kf, k0, k, Gk, t0, ntv);
     __builtin_amdgcn_sched_barrier(0);
 
     // item i of this wave: band q0 + it / J, group slot it % J with it = wave·ITEMS + i (clamped)
@@ -452,17 +464,18 @@ __global__ void __launch_bounds__(64 * MV_WAVES) mv_kernel(WeightView w, ActQ A,
         row = row < m ? row : m - 1;
         int g = GS * (it % J) + gs;
         g = g < Gk ? g : Gk - 1;
-        load_group<DT>(buf[i], w, row, g);
+        load_group<DT>(buf[i], w, row, g0 + g);
     }
     __builtin_amdgcn_sched_barrier(0);
 
     extern __shared__ __align__(16) unsigned char smem[];
     float* part = reinterpret_cast<float*>(smem);   // [8·ITEMS][GS][RB][NT] lane partials
-    const int8_t* aq = A.q;
-    const float* ad = A.d;
-    const float* as = A.s;
-    const int* s16 = A.s16;
-    int64_t tq = k, td = nb, ts = FL == 1 ? nb : 2 * nb, t16 = 2 * nb;
+    const int nbf = kf >> 5;                     // strides of A are the full row's
+    const int8_t* aq = A.q + k0;
+    const float* ad = A.d + (k0 >> 5);
+    const float* as = A.s + (FL == 1 ? k0 >> 5 : k0 >> 4);
+    const int* s16 = A.s16 + (k0 >> 4);
+    int64_t tq = kf, td = nbf, ts = FL == 1 ? nbf : 2 * nbf, t16 = 2 * nbf;
     int QS = 256;
     if constexpr (FUSE) {
         char* dummy = reinterpret_cast<char*>(smem + MV_WAVES * ITEMS * 64 * NT * 4);   // 32 bytes
@@ -641,18 +654,33 @@ static bool mv_items(int k, int* items) {
     return J <= MV_WAVES * it;
 }
 
+// Split K: from k = 2·GEMV_SLICE on and for 2 or more tokens, the workgroups of a band take GEMV_SLICE-element
+// slices of k (grid z) so that a block keeps 32-row bands and its slice of every token's activations fits
+// LDS; partials are summed after. One token's activations fit unsplit (measured faster unsplit).
+constexpr int GEMV_SLICE = 4096;
+inline int gemv_slice(int k, int n) { return n >= 2 && k >= 2 * GEMV_SLICE ? GEMV_SLICE : k; }
+
+// ks: elements per K slice (= k unsplit); cz: floats between the slices' partial outputs.
 template <int DT, int FL, int NT, int HP, int RB, int ITEMS>
-static void launch_shape(int k, int m, int n, const WeightView& w, const ActQ& A, const float* a, int lda, float* c,
-                         int ldc, hipStream_t st) {
+static void launch_shape(int k, int ks, int64_t cz, int m, int n, const WeightView& w, const ActQ& A, const float* a,
+                         int lda, float* c, int ldc, hipStream_t st) {
     constexpr int GS = 64 / RB;
-    const int Gk = (k / 32 + 7) / 8, J = (Gk + GS - 1) / GS;
+    const int Gk = (ks / 32 + 7) / 8, J = (Gk + GS - 1) / GS;
     const int QB = MV_WAVES * ITEMS / J;
     const int64_t bands = ((int64_t) m + RB - 1) / RB;
-    const dim3 grid((unsigned) ((bands + QB - 1) / QB), FL == 1 ? 1 : (n + NT - 1) / NT);
-    const size_t lds = (size_t) MV_WAVES * ITEMS * 64 * NT * sizeof(float) + (HP > 0 ? 32 + fuse_lds(NT, k) : 0);
-    lds_allow((const void*) mv_kernel<DT, FL, NT, HP, RB, ITEMS, false>, lds);
-    mv_kernel<DT, FL, NT, HP, RB, ITEMS, false><<<grid, 64 * MV_WAVES, lds, st>>>(w, A, a, lda, k, m, n, c, ldc,
-                                                                                 Groups{});
+    const dim3 grid((unsigned) ((bands + QB - 1) / QB), FL == 1 ? 1 : (n + NT - 1) / NT, (unsigned) ((k + ks - 1) / ks));
+    const size_t lds = (size_t) MV_WAVES * ITEMS * 64 * NT * sizeof(float) + (HP > 0 ? 32 + fuse_lds(NT, ks) : 0);
+    if constexpr (NT >= 2) {   // only calls with 2 or more tokens split K
+        if (ks < k) {
+            lds_allow((const void*) mv_kernel<DT, FL, NT, HP, RB, ITEMS, false, true>, lds);
+            mv_kernel<DT, FL, NT, HP, RB, ITEMS, false, true><<<grid, 64 * MV_WAVES, lds, st>>>(
+                w, A, a, lda, k, m, n, c, ldc, Groups{}, ks, cz);
+            return;
+        }
+    }
+    lds_allow((const void*) mv_kernel<DT, FL, NT, HP, RB, ITEMS, false, false>, lds);
+    mv_kernel<DT, FL, NT, HP, RB, ITEMS, false, false><<<grid, 64 * MV_WAVES, lds, st>>>(w, A, a, lda, k, m, n, c, ldc,
+                                                                                        Groups{}, k, 0);
 }
 
 template <int DT, int FL, int NT, int HP, int RB, int ITEMS>
@@ -664,8 +692,9 @@ static void launch_shape_grouped(int k, const Groups& g, int ny, const WeightVie
     const int64_t bands = ((int64_t) g.gm + RB - 1) / RB;
     const dim3 grid((unsigned) ((bands + QB - 1) / QB), (unsigned) ny);
     const size_t lds = (size_t) MV_WAVES * ITEMS * 64 * NT * sizeof(float) + (HP > 0 ? 32 + fuse_lds(NT, k) : 0);
-    lds_allow((const void*) mv_kernel<DT, FL, NT, HP, RB, ITEMS, true>, lds);
-    mv_kernel<DT, FL, NT, HP, RB, ITEMS, true><<<grid, 64 * MV_WAVES, lds, st>>>(w, A, a, lda, k, g.gm, 0, c, ldc, g);
+    lds_allow((const void*) mv_kernel<DT, FL, NT, HP, RB, ITEMS, true, false>, lds);
+    mv_kernel<DT, FL, NT, HP, RB, ITEMS, true, false><<<grid, 64 * MV_WAVES, lds, st>>>(w, A, a, lda, k, g.gm, 0, c,
+                                                                                       ldc, g, k, 0);
 }
 
 template <int DT, int FL, int NT, int HP>
@@ -692,57 +721,70 @@ hipError_t gemv_grouped_dt(int flavour, const WeightView& w, const ActQ& A, cons
 
 
 template <int DT, int FL, int NT, int HP>
-static hipError_t go_hp(int k, int m, int n, const WeightView& w, const ActQ& A, const float* a, int lda, float* c,
-                        int ldc, hipStream_t st) {
+static hipError_t go_hp(int k, int ks, int64_t cz, int m, int n, const WeightView& w, const ActQ& A, const float* a,
+                        int lda, float* c, int ldc, hipStream_t st) {
     int items;
-    if (!mv_items(k, &items)) return hipErrorNotSupported;
-    if constexpr (FL == 2 && HP > 0) {   // staged activations: one item per wave (k <= 16384)
-        if (items != 1) return go_hp<DT, FL, NT, 0>(k, m, n, w, A, a, lda, c, ldc, st);
-        launch_shape<DT, FL, NT, HP, MV_RB, 1>(k, m, n, w, A, a, lda, c, ldc, st);
+    if (!mv_items(ks, &items)) return hipErrorNotSupported;
+    if constexpr (FL == 2 && HP > 0) {   // staged activations: one item per wave (slices <= 16384)
+        if (items != 1) return go_hp<DT, FL, NT, 0>(k, ks, cz, m, n, w, A, a, lda, c, ldc, st);
+        launch_shape<DT, FL, NT, HP, MV_RB, 1>(k, ks, cz, m, n, w, A, a, lda, c, ldc, st);
         return hipGetLastError();
     }
-    if (items == 1) launch_shape<DT, FL, NT, HP, MV_RB, 1>(k, m, n, w, A, a, lda, c, ldc, st);
-    else if (items == 2) launch_shape<DT, FL, NT, HP, MV_RB, 2>(k, m, n, w, A, a, lda, c, ldc, st);
-    else launch_shape<DT, FL, NT, HP, MV_RB, 4>(k, m, n, w, A, a, lda, c, ldc, st);
+    if (items == 1) launch_shape<DT, FL, NT, HP, MV_RB, 1>(k, ks, cz, m, n, w, A, a, lda, c, ldc, st);
+    else if (items == 2) launch_shape<DT, FL, NT, HP, MV_RB, 2>(k, ks, cz, m, n, w, A, a, lda, c, ldc, st);
+    else launch_shape<DT, FL, NT, HP, MV_RB, 4>(k, ks, cz, m, n, w, A, a, lda, c, ldc, st);
     return hipGetLastError();
 }
 
 template <int DT, int FL, int NT>
-static hipError_t go(const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m, int n, float* c,
-                     int ldc, hipStream_t st) {
+static hipError_t go(const WeightView& w, const ActQ& A, const float* a, int lda, int k, int ks, int64_t cz, int m,
+                     int n, float* c, int ldc, hipStream_t st) {
     if constexpr (FL == 2) {   // stage the tile's activations in LDS when they fit
-        const int hp = (NT * ((k / 32 + 7) / 8) * 16 + 64 * MV_WAVES - 1) / (64 * MV_WAVES);
-        if (fuse_lds(NT, k) <= (size_t) kFuseMaxBytes && hp <= 8) {
-            if (hp <= 2) return go_hp<DT, FL, NT, 2>(k, m, n, w, A, a, lda, c, ldc, st);
-            if (hp <= 4) return go_hp<DT, FL, NT, 4>(k, m, n, w, A, a, lda, c, ldc, st);
-            return go_hp<DT, FL, NT, 8>(k, m, n, w, A, a, lda, c, ldc, st);
+        const int hp = (NT * ((ks / 32 + 7) / 8) * 16 + 64 * MV_WAVES - 1) / (64 * MV_WAVES);
+        if (fuse_lds(NT, ks) <= (size_t) kFuseMaxBytes && hp <= 8) {
+            if (hp <= 2) return go_hp<DT, FL, NT, 2>(k, ks, cz, m, n, w, A, a, lda, c, ldc, st);
+            if (hp <= 4) return go_hp<DT, FL, NT, 4>(k, ks, cz, m, n, w, A, a, lda, c, ldc, st);
+            return go_hp<DT, FL, NT, 8>(k, ks, cz, m, n, w, A, a, lda, c, ldc, st);
         }
     }
     if constexpr (FL == 1) {
         if (a != nullptr) {
-            const int hp = fuse_hp(NT, k);
-            if (hp <= 1) return go_hp<DT, FL, NT, 1>(k, m, n, w, A, a, lda, c, ldc, st);
-            if (hp == 2) return go_hp<DT, FL, NT, 2>(k, m, n, w, A, a, lda, c, ldc, st);
-            return go_hp<DT, FL, NT, 4>(k, m, n, w, A, a, lda, c, ldc, st);
+            const int hp = fuse_hp(NT, ks);
+            if (hp <= 1) return go_hp<DT, FL, NT, 1>(k, ks, cz, m, n, w, A, a, lda, c, ldc, st);
+            if (hp == 2) return go_hp<DT, FL, NT, 2>(k, ks, cz, m, n, w, A, a, lda, c, ldc, st);
+            return go_hp<DT, FL, NT, 4>(k, ks, cz, m, n, w, A, a, lda, c, ldc, st);
         }
     }
-    return go_hp<DT, FL, NT, 0>(k, m, n, w, A, a, lda, c, ldc, st);
+    return go_hp<DT, FL, NT, 0>(k, ks, cz, m, n, w, A, a, lda, c, ldc, st);
 }
 
+// Split calls (gemv_slice(k, n) < k) write each slice's partial result to part ([slices][n][m]) and sum them
+// into c in slice order.
 template <int DT>
 hipError_t gemv_dt(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m,
-                          int n, float* c, int ldc, hipStream_t st) {
-    if (flavour == 2) return go<DT, 2, 8>(w, A, nullptr, 0, k, m, n, c, ldc, st);
-    switch (n) {
-    case 1: return go<DT, 1, 1>(w, A, a, lda, k, m, n, c, ldc, st);
-    case 2: return go<DT, 1, 2>(w, A, a, lda, k, m, n, c, ldc, st);
-    case 3: return go<DT, 1, 3>(w, A, a, lda, k, m, n, c, ldc, st);
-    case 4: return go<DT, 1, 4>(w, A, a, lda, k, m, n, c, ldc, st);
-    case 5: return go<DT, 1, 5>(w, A, a, lda, k, m, n, c, ldc, st);
-    case 6: return go<DT, 1, 6>(w, A, a, lda, k, m, n, c, ldc, st);
-    case 7: return go<DT, 1, 7>(w, A, a, lda, k, m, n, c, ldc, st);
-    default: return hipErrorInvalidValue;
+                          int n, float* c, int ldc, hipStream_t st, float* part) {
+    const int ks = gemv_slice(k, n), ns = (k + ks - 1) / ks;
+    if (ns > 1 && part == nullptr) return hipErrorInvalidValue;
+    const int64_t cz = ns > 1 ? (int64_t) n * m : 0;
+    float* out = ns > 1 ? part : c;
+    const int ldo = ns > 1 ? m : ldc;
+    hipError_t e;
+    if (flavour == 2) {
+        e = go<DT, 2, 8>(w, A, nullptr, 0, k, ks, cz, m, n, out, ldo, st);
+    } else {
+        switch (n) {
+        case 1: e = go<DT, 1, 1>(w, A, a, lda, k, ks, cz, m, n, out, ldo, st); break;
+        case 2: e = go<DT, 1, 2>(w, A, a, lda, k, ks, cz, m, n, out, ldo, st); break;
+        case 3: e = go<DT, 1, 3>(w, A, a, lda, k, ks, cz, m, n, out, ldo, st); break;
+        case 4: e = go<DT, 1, 4>(w, A, a, lda, k, ks, cz, m, n, out, ldo, st); break;
+        case 5: e = go<DT, 1, 5>(w, A, a, lda, k, ks, cz, m, n, out, ldo, st); break;
+        case 6: e = go<DT, 1, 6>(w, A, a, lda, k, ks, cz, m, n, out, ldo, st); break;
+        case 7: e = go<DT, 1, 7>(w, A, a, lda, k, ks, cz, m, n, out, ldo, st); break;
+        default: return hipErrorInvalidValue;
+        }
     }
+    if (e != hipSuccess || ns == 1) return e;
+    return launch_split_reduce(part, ns, cz, m, n, c, ldc, st);
 }
 
 template <int DT>

@@ -181,12 +181,22 @@ static int mma_min_n(int dt) {
 }
 
 // Quantize A (device, f32 [n][lda]) and run the matmul into C (device, [n][ldc]). Decode-sized calls
-// are one fused launch and touch no scratch (safe under stream capture once W is pinned).
+// with k < 8192 are one fused launch and touch no scratch (safe under stream capture once W is pinned);
+// from k = 8192 the decode kernels split K and sum the slices from the context's split buffer.
 jamhip_status compute(jamhip_ctx* ctx, int dt, const WeightView& wv, const float* a, int lda, float* c, int ldc,
                       int m, int n, int k) {
     hipError_t e;
+    float* gpart = nullptr;   // the decode kernels' K-split partials
+    auto decode_part = [&](int rows) -> hipError_t {
+        const size_t pf = gemv_split_floats(k, rows, n);
+        if (pf == 0) return hipSuccess;
+        const hipError_t r = ctx->part.ensure(pf * sizeof(float));
+        gpart = (float*) ctx->part.p;
+        return r;
+    };
     if (gemv_fusable(n, k, a, lda)) {
-        if ((e = launch_gemv(dt, 1, wv, ActQ{}, a, lda, k, m, n, c, ldc, ctx->stream)) != hipSuccess)
+        if ((e = decode_part(m)) != hipSuccess) return hip_fail(ctx, e, "gemv split scratch alloc");
+        if ((e = launch_gemv(dt, 1, wv, ActQ{}, a, lda, k, m, n, c, ldc, ctx->stream, gpart)) != hipSuccess)
             return hip_fail(ctx, e, "gemv launch");
         return JAMHIP_OK;
     }
@@ -224,7 +234,8 @@ jamhip_status compute(jamhip_ctx* ctx, int dt, const WeightView& wv, const float
     if (n < 8) {
         if ((e = launch_quant_f1(a, lda, n, k, q, d, s, s16, ctx->stream)) != hipSuccess)
             return hip_fail(ctx, e, "quant_f1 launch");
-        if ((e = launch_gemv(dt, 1, wv, A, nullptr, 0, k, m, n, c, ldc, ctx->stream)) != hipSuccess)
+        if ((e = decode_part(m)) != hipSuccess) return hip_fail(ctx, e, "gemv split scratch alloc");
+        if ((e = launch_gemv(dt, 1, wv, A, nullptr, 0, k, m, n, c, ldc, ctx->stream, gpart)) != hipSuccess)
             return hip_fail(ctx, e, "gemv launch");
         return JAMHIP_OK;
     }
@@ -232,7 +243,8 @@ jamhip_status compute(jamhip_ctx* ctx, int dt, const WeightView& wv, const float
         if ((e = launch_quant_f2(a, lda, n, k, q, d, s, ctx->stream)) != hipSuccess)
             return hip_fail(ctx, e, "quant_f2 launch");
         e = n >= 32 ? launch_gemm(dt, wv, A, k, m16, n, c, ldc, ctx->stream) : hipErrorNotSupported;
-        if (e == hipErrorNotSupported) e = launch_gemv(dt, 2, wv, A, nullptr, 0, k, m16, n, c, ldc, ctx->stream);
+        if (e == hipErrorNotSupported && (e = decode_part(m16)) == hipSuccess)
+            e = launch_gemv(dt, 2, wv, A, nullptr, 0, k, m16, n, c, ldc, ctx->stream, gpart);
         if (e != hipSuccess) return hip_fail(ctx, e, "matmul launch");
     }
     if ((e = launch_rows_float(dt, wv, a, lda, k, m16, m - m16, n, c, ldc, ctx->stream)) != hipSuccess)
@@ -477,7 +489,7 @@ jamhip_status jamhip_mm_grouped(jamhip_ctx* ctx, const void* w, int wt, int ldw,
         return r;
     };
     // experts with 1..7 rows: jam's F1 decode path, one launch
-    if (gemv_fusable(7, k, a, lda)) {
+    if (gemv_grouped_fusable(k, a, lda)) {
         if ((e = launch_gemv_grouped(wt, 1, wv, ActQ{}, a, lda, k, g, E, cap8, c, ldc, ctx->stream)) != hipSuccess)
             return hip_fail(ctx, e, "grouped: gemv launch");
     } else {

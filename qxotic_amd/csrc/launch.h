@@ -32,15 +32,22 @@ struct Groups {
 
 // flavour 1: n in [1, 7], F1 activations; with `a` non-null the kernel quantizes A itself (requires
 // gemv_fusable(n, k)), else it reads A's quantized copy from `A`. flavour 2: any n >= 1, F2
-// activations from `A`, 8 tokens per grid row.
+// activations from `A`, 8 tokens per grid row. From k = 8192 on, for n >= 2, the kernel splits K into
+// 4096-element slices: `part` must then hold gemv_split_floats(k, m, n) floats (the slices' partial
+// results, summed into c in slice order); gemv_split_floats is 0 otherwise and part may be null.
 bool gemv_fusable(int n, int k, const float* a, int lda);   // a, lda: the f32 activations (16-byte aligned rows)
+size_t gemv_split_floats(int k, int m, int n);
 hipError_t launch_gemv(int dt, int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m,
-                       int n, float* c, int ldc, hipStream_t st);
+                       int n, float* c, int ldc, hipStream_t st, float* part = nullptr);
+// c[t][row] = Σ_s part[s·slice + t·m + row] for s = 0..ns-1 in order (rows < m, tokens < n)
+hipError_t launch_split_reduce(const float* part, int ns, int64_t slice, int m, int n, float* c, int ldc,
+                               hipStream_t st);
 
 // Grouped forms (one launch for all experts). flavour 1: every expert with 1..7 rows, F1, the kernel
-// quantizing its expert's rows itself when `a` is non-null (then gemv_fusable(7, k, a, lda) must hold),
+// quantizing its expert's rows itself when `a` is non-null (then gemv_grouped_fusable(k, a, lda) must hold),
 // else reading them from A (CSR rows). flavour 2: the 8-token tiles of map8 (experts with >= 8 rows), F2
 // activations from A (CSR rows). m here is the rows per expert (g.gm).
+bool gemv_grouped_fusable(int k, const float* a, int lda);
 hipError_t launch_gemv_grouped(int dt, int flavour, const WeightView& w, const ActQ& A, const float* a, int lda,
                                int k, const Groups& g, int E, int cap8, float* c, int ldc, hipStream_t st);
 

@@ -585,6 +585,12 @@ __global__ void __launch_bounds__(256) split_reduce_kernel(const float* __restri
     c[(int64_t) t * ldc + row] = v;
 }
 
+hipError_t launch_split_reduce(const float* part, int ns, int64_t slice, int m, int n, float* c, int ldc,
+                               hipStream_t st) {
+    split_reduce_kernel<<<dim3((m + 255) / 256, n), 256, 0, st>>>(part, ns, slice, m, c, ldc);
+    return hipGetLastError();
+}
+
 // K slices for a grid of `total` workgroups: enough for about two workgroups per CU, whole super-blocks each.
 static void split_plan(int total, int nsb, int* ns, int* sb_per) {
     int want = total >= 384 ? 1 : (512 + total - 1) / total;

@@ -206,6 +206,47 @@ def test_full_size_decode(hip, oracle, dt, m, k, n):
     assert tier1(got, ref, sa).all()
 
 
+@pytest.mark.parametrize("dt", O.QUANT_TYPES)
+def test_split_k_decode(hip, oracle, dt):
+    """From k = 8192 on the decode kernels split K into 4096-element slices and sum the slices' partial
+    results in slice order: a partial last slice (for the 32-element types also a partial last group), F1
+    quantized in the kernel (n < 8), F1 from the quantized copy (rows not 16-byte aligned), F2 tiles (n >= 8
+    where the matrix cores do not take the call), ldc gap untouched, rerun bit-identical."""
+    import torch
+    from qxotic_amd.jam import JAM, Segment
+    be = O.BLOCK[dt][0]
+    m, k = 80, (9024 if be == 32 else 9216)
+    w = oracle.quantize(dt, oracle.normal(0x5A11C0DE ^ 0x5C ^ dt, (m, k), 0.0, 0.02))
+    for n in (1, 4, 7, 8, 13):
+        say(f"split-k {O.NAMES[dt]} m={m} n={n} k={k}")
+        a = oracle.outliers(3000 + n, (n, k))
+        got = run_mm(hip, dt, w, a, m, n, k, ldc=m + 3)
+        assert (got[:, m:] == 0.0).all()
+        ref = oracle.mm_int8(dt, w, a, m, n, k)
+        _, sa = oracle.mm_ref(dt, w, a, m, n, k)
+        ok = tier1(got[:, :m], ref, sa)
+        assert ok.all(), (O.NAMES[dt], n, float(np.max(np.abs(got[:, :m] - ref) / (np.abs(ref) + 1e-30))))
+        assert np.array_equal(bits(run_mm(hip, dt, w, a, m, n, k, ldc=m + 3)), bits(got))
+    # device path with lda = k + 1: the kernel cannot load the rows as 16-byte pieces and reads the F1 copy
+    assert hip.pin(Segment.of(w), dt, k, m) == JAM.OK, hip.last_error()
+    try:
+        n = 3
+        say(f"split-k {O.NAMES[dt]} unaligned rows n={n}")
+        a = oracle.normal(3100, (n, k))
+        a_pad = np.zeros((n, k + 1), np.float32)
+        a_pad[:, :k] = a
+        a_dev = torch.from_numpy(a_pad).cuda()
+        c_dev = torch.zeros((n, m), dtype=torch.float32, device="cuda")
+        st = hip.mm_device(Segment.of(w), dt, k, a_dev.data_ptr(), k + 1, c_dev.data_ptr(), m, m, n, k)
+        assert st == JAM.OK, hip.last_error()
+        hip.synchronize()
+        ref = oracle.mm_int8(dt, w, a, m, n, k)
+        _, sa = oracle.mm_ref(dt, w, a, m, n, k)
+        assert tier1(c_dev.cpu().numpy(), ref, sa).all()
+    finally:
+        assert hip.evict(Segment.of(w)) == JAM.OK
+
+
 # ------------------------------------------------------------------------------------ prefill GEMM
 PREFILL = [(O.Q4_K, 14336, 4096), (O.Q6_K, 4096, 14336)]
 
