@@ -245,7 +245,7 @@ constexpr int MV_WAVES = 8;   // waves per GEMV workgroup (512 threads)
 // f1_store quantizes them and writes LDS. HP = ceil(NT·16·Gk / 512) half-blocks per thread.
 template <int HP> struct APre { float x[HP][16]; };
 
-template <int NT, int HP>
+template <int NT, int HP, int NWV>
 JAMHIP_DEV void a_load(APre<HP>& pre, const float* __restrict__ a, int lda, int k, int Gk, int ntv) {
     // four 16-byte loads per half-block (the launcher checks a and lda for 16-byte alignment); a half past
     // the token's last element (a partial last group) re-reads the token's last half, zeroed by f1_store
@@ -253,7 +253,7 @@ JAMHIP_DEV void a_load(APre<HP>& pre, const float* __restrict__ a, int lda, int 
     const int halves = 16 * Gk, total = NT * halves, kh = k >> 4;
 #pragma unroll
     for (int i = 0; i < HP; i++) {
-        const int h0 = threadIdx.x + 64 * MV_WAVES * i, h = h0 < total ? h0 : total - 1;
+        const int h0 = threadIdx.x + 64 * NWV * i, h = h0 < total ? h0 : total - 1;
         const int j = NT == 1 ? 0 : h / halves, hh = h - j * halves, jr = j < ntv ? j : ntv - 1;   // rows past ntv: clamp
         const bool in = hh < kh;   // clamp only; the zeroing happens in f1_store
         const float4* src = reinterpret_cast<const float4*>(a + (int64_t) jr * lda + 16 * (in ? hh : kh - 1));
@@ -268,14 +268,14 @@ JAMHIP_DEV void a_load(APre<HP>& pre, const float* __restrict__ a, int lda, int 
     }
 }
 
-template <int NT, int HP>
+template <int NT, int HP, int NWV>
 JAMHIP_DEV void f1_store(const APre<HP>& pre, int k, int Gk, int8_t* lq, float* ld, float* las, int* ls16, char* dummy) {
     // branch-free: a thread past the last half-block (its loads were clamped) quantizes anyway and writes to
     // a dummy LDS slot; pairs stay aligned because the half-block count is even
     const int halves = 16 * Gk, total = NT * halves;
 #pragma unroll
     for (int i = 0; i < HP; i++) {
-        const int h0 = threadIdx.x + 64 * MV_WAVES * i;
+        const int h0 = threadIdx.x + 64 * NWV * i;
         const bool valid = h0 < total;
         const int h = valid ? h0 : 0;
         const int j = NT == 1 ? 0 : h / halves, hh = h - j * halves;
@@ -332,31 +332,31 @@ template <int SP> struct FPre {
 };
 
 // k: the row length of A (its stride); elements [k0, k0 + kl) of each token are staged (k0 % 256 == 0).
-template <int NT, int SP>
+template <int NT, int SP, int NWV>
 JAMHIP_DEV void stage_load(FPre<SP>& pre, const ActQ& A, int k, int k0, int kl, int Gk, int t0, int ntv) {
     const int nbf = k >> 5, nb = kl >> 5, units = NT * Gk * 16, nf = NT * 3 * nb;
 #pragma unroll
     for (int i = 0; i < SP; i++) {
-        const int u0 = threadIdx.x + 64 * MV_WAVES * i, u = u0 < units ? u0 : units - 1;
+        const int u0 = threadIdx.x + 64 * NWV * i, u = u0 < units ? u0 : units - 1;
         const int t = u / (Gk * 16), r = u - t * Gk * 16, tc = t < ntv ? t : ntv - 1;
         const int off = 256 * (r >> 4) + 16 * (r & 15);
         pre.q[i] = ld16(A.q + (int64_t) (t0 + tc) * k + k0 + (off < kl ? off : kl - 16));
     }
 #pragma unroll
     for (int i = 0; i < 2 * SP; i++) {
-        const int v0 = threadIdx.x + 64 * MV_WAVES * i, v = v0 < nf ? v0 : nf - 1;
+        const int v0 = threadIdx.x + 64 * NWV * i, v = v0 < nf ? v0 : nf - 1;
         const int t = v / (3 * nb), r = v - t * 3 * nb, tc = t < ntv ? t : ntv - 1;
         pre.f[i] = r < nb ? A.d[(int64_t) (t0 + tc) * nbf + (k0 >> 5) + r]
                           : A.s[(int64_t) (t0 + tc) * 2 * nbf + (k0 >> 4) + (r - nb)];
     }
 }
 
-template <int NT, int SP>
+template <int NT, int SP, int NWV>
 JAMHIP_DEV void stage_store(const FPre<SP>& pre, int k, int Gk, int8_t* lq, float* ld, float* lx) {
     const int nb = k >> 5, units = NT * Gk * 16, nf = NT * 3 * nb;
 #pragma unroll
     for (int i = 0; i < SP; i++) {
-        const int u = threadIdx.x + 64 * MV_WAVES * i;
+        const int u = threadIdx.x + 64 * NWV * i;
         if (u < units) {
             const int t = u / (Gk * 16), r = u - t * Gk * 16;
             *reinterpret_cast<uint4*>(lq + (t * Gk + (r >> 4)) * QS_LDS + 16 * (r & 15)) = pre.q[i];
@@ -364,7 +364,7 @@ JAMHIP_DEV void stage_store(const FPre<SP>& pre, int k, int Gk, int8_t* lq, floa
     }
 #pragma unroll
     for (int i = 0; i < 2 * SP; i++) {
-        const int v = threadIdx.x + 64 * MV_WAVES * i;
+        const int v = threadIdx.x + 64 * NWV * i;
         if (v < nf) {
             const int t = v / (3 * nb), r = v - t * 3 * nb;
             if (r < nb) ld[t * 8 * Gk + r] = pre.f[i];
@@ -389,8 +389,8 @@ JAMHIP_DEV void stage_store(const FPre<SP>& pre, int k, int Gk, int8_t* lq, floa
 // group may hold fewer (ntv).
 // GR (grouped matmul): FL = 1 takes expert blockIdx.y if it has 1..7 rows (ntv of them, CSR rows from
 // off[e]); FL = 2 takes the 8-token tile blockIdx.y of map8. The expert's weight rows start at e·gm.
-template <int DT, int FL, int NT, int HP, int RB, int ITEMS, bool GR, bool SK>
-__global__ void __launch_bounds__(64 * MV_WAVES) mv_kernel(WeightView w, ActQ A, const float* __restrict__ a,
+template <int DT, int FL, int NT, int HP, int RB, int ITEMS, bool GR, bool SK, int NWV>
+__global__ void __launch_bounds__(64 * NWV) mv_kernel(WeightView w, ActQ A, const float* __restrict__ a,
                                                           int lda, int k, int m, int n, float* __restrict__ c,
                                                           int ldc, Groups gp, int ks, int64_t cz) {
     constexpr int BPG = blocks_per_group(DT), GS = 64 / RB;
@@ -415,7 +415,7 @@ __global__ void __launch_bounds__(64 * MV_WAVES) mv_kernel(WeightView w, ActQ A,
     const int Gk = (nb + 7) >> 3;                // groups in the slice
     const int J = ((SK ? ((ks >> 5) + 7) / 8 : Gk) + GS - 1) / GS;   // items per row band
     const int g0 = k0 >> 8;                      // the slice's first group
-    const int QB = MV_WAVES * ITEMS / J;         // bands per block (the launcher keeps J <= 8·ITEMS)
+    const int QB = NWV * ITEMS / J;              // bands per block (the launcher keeps J <= NWV·ITEMS)
     const int64_t q0 = (int64_t) blockIdx.x * QB;
     int t0, ntv;
     if constexpr (GR) {
@@ -451,8 +451,8 @@ __global__ void __launch_bounds__(64 * MV_WAVES) mv_kernel(WeightView w, ActQ A,
     APre<QF1 ? HP : 1> pre;
     FPre<STG ? SP : 1> fpre;
     if constexpr (QF1)
-        if (pro) a_load<NT, QF1 ? HP : 1>(pre, a, lda, k, Gk, ntv);
-    if constexpr (STG) stage_load<NT, SP>(fpre, A, kf, k0, k, Gk, t0, ntv);
+        if (pro) a_load<NT, QF1 ? HP : 1, NWV>(pre, a, lda, k, Gk, ntv);
+    if constexpr (STG) stage_load<NT, SP, NWV>(fpre, A, kf, k0, k, Gk, t0, ntv);
     __builtin_amdgcn_sched_barrier(0);
 
     // item i of this wave: band q0 + it / J, group slot it % J with it = wave·ITEMS + i (clamped)
@@ -478,7 +478,7 @@ __global__ void __launch_bounds__(64 * MV_WAVES) mv_kernel(WeightView w, ActQ A,
     int64_t tq = kf, td = nbf, ts = FL == 1 ? nbf : 2 * nbf, t16 = 2 * nbf;
     int QS = 256;
     if constexpr (FUSE) {
-        char* dummy = reinterpret_cast<char*>(smem + MV_WAVES * ITEMS * 64 * NT * 4);   // 32 bytes
+        char* dummy = reinterpret_cast<char*>(smem + NWV * ITEMS * 64 * NT * 4);   // 32 bytes
         int8_t* lq = reinterpret_cast<int8_t*>(dummy + 32);
         float* ld = reinterpret_cast<float*>(lq + NT * Gk * QS_LDS);
         float* las = ld + NT * 8 * Gk;
@@ -489,9 +489,9 @@ __global__ void __launch_bounds__(64 * MV_WAVES) mv_kernel(WeightView w, ActQ A,
         td = 8 * Gk;
         QS = QS_LDS;
         if constexpr (QF1) {
-            if (pro) f1_store<NT, QF1 ? HP : 1>(pre, k, Gk, lq, ld, las, ls16, dummy);
+            if (pro) f1_store<NT, QF1 ? HP : 1, NWV>(pre, k, Gk, lq, ld, las, ls16, dummy);
         } else {   // F2: per-16 sums in the Σq-per-16 region (16 per group and token)
-            stage_store<NT, SP>(fpre, k, Gk, lq, ld, reinterpret_cast<float*>(ls16));
+            stage_store<NT, SP, NWV>(fpre, k, Gk, lq, ld, reinterpret_cast<float*>(ls16));
         }
         if constexpr (FL == 1) {
             as = las;
@@ -539,7 +539,7 @@ __global__ void __launch_bounds__(64 * MV_WAVES) mv_kernel(WeightView w, ActQ A,
     }
     __syncthreads();
     // (band, row, token) of the block: sum its J x GS partials in order; QB·RB·NT can exceed the 512 threads
-    for (int tid = threadIdx.x; tid < QB * RB * NT; tid += 64 * MV_WAVES) {
+    for (int tid = threadIdx.x; tid < QB * RB * NT; tid += 64 * NWV) {
         const int q = tid / (RB * NT), r = (tid / NT) % RB, t = tid % NT;
         float v = 0.0f;
         for (int j = 0; j < J; j++)
@@ -660,26 +660,27 @@ static bool mv_items(int k, int* items) {
 constexpr int GEMV_SLICE = 4096;
 inline int gemv_slice(int k, int n) { return n >= 2 && k >= 2 * GEMV_SLICE ? GEMV_SLICE : k; }
 
-// ks: elements per K slice (= k unsplit); cz: floats between the slices' partial outputs.
-template <int DT, int FL, int NT, int HP, int RB, int ITEMS>
+// ks: elements per K slice (= k unsplit); cz: floats between the slices' partial outputs; NWV: waves per
+// workgroup.
+template <int DT, int FL, int NT, int HP, int RB, int ITEMS, int NWV = MV_WAVES>
 static void launch_shape(int k, int ks, int64_t cz, int m, int n, const WeightView& w, const ActQ& A, const float* a,
                          int lda, float* c, int ldc, hipStream_t st) {
     constexpr int GS = 64 / RB;
     const int Gk = (ks / 32 + 7) / 8, J = (Gk + GS - 1) / GS;
-    const int QB = MV_WAVES * ITEMS / J;
+    const int QB = NWV * ITEMS / J;
     const int64_t bands = ((int64_t) m + RB - 1) / RB;
     const dim3 grid((unsigned) ((bands + QB - 1) / QB), FL == 1 ? 1 : (n + NT - 1) / NT, (unsigned) ((k + ks - 1) / ks));
-    const size_t lds = (size_t) MV_WAVES * ITEMS * 64 * NT * sizeof(float) + (HP > 0 ? 32 + fuse_lds(NT, ks) : 0);
+    const size_t lds = (size_t) NWV * ITEMS * 64 * NT * sizeof(float) + (HP > 0 ? 32 + fuse_lds(NT, ks) : 0);
     if constexpr (NT >= 2) {   // only calls with 2 or more tokens split K
         if (ks < k) {
-            lds_allow((const void*) mv_kernel<DT, FL, NT, HP, RB, ITEMS, false, true>, lds);
-            mv_kernel<DT, FL, NT, HP, RB, ITEMS, false, true><<<grid, 64 * MV_WAVES, lds, st>>>(
+            lds_allow((const void*) mv_kernel<DT, FL, NT, HP, RB, ITEMS, false, true, NWV>, lds);
+            mv_kernel<DT, FL, NT, HP, RB, ITEMS, false, true, NWV><<<grid, 64 * NWV, lds, st>>>(
                 w, A, a, lda, k, m, n, c, ldc, Groups{}, ks, cz);
             return;
         }
     }
-    lds_allow((const void*) mv_kernel<DT, FL, NT, HP, RB, ITEMS, false, false>, lds);
-    mv_kernel<DT, FL, NT, HP, RB, ITEMS, false, false><<<grid, 64 * MV_WAVES, lds, st>>>(w, A, a, lda, k, m, n, c, ldc,
+    lds_allow((const void*) mv_kernel<DT, FL, NT, HP, RB, ITEMS, false, false, NWV>, lds);
+    mv_kernel<DT, FL, NT, HP, RB, ITEMS, false, false, NWV><<<grid, 64 * NWV, lds, st>>>(w, A, a, lda, k, m, n, c, ldc,
                                                                                         Groups{}, k, 0);
 }
 
@@ -692,9 +693,9 @@ static void launch_shape_grouped(int k, const Groups& g, int ny, const WeightVie
     const int64_t bands = ((int64_t) g.gm + RB - 1) / RB;
     const dim3 grid((unsigned) ((bands + QB - 1) / QB), (unsigned) ny);
     const size_t lds = (size_t) MV_WAVES * ITEMS * 64 * NT * sizeof(float) + (HP > 0 ? 32 + fuse_lds(NT, k) : 0);
-    lds_allow((const void*) mv_kernel<DT, FL, NT, HP, RB, ITEMS, true, false>, lds);
-    mv_kernel<DT, FL, NT, HP, RB, ITEMS, true, false><<<grid, 64 * MV_WAVES, lds, st>>>(w, A, a, lda, k, g.gm, 0, c,
-                                                                                       ldc, g, k, 0);
+    lds_allow((const void*) mv_kernel<DT, FL, NT, HP, RB, ITEMS, true, false, MV_WAVES>, lds);
+    mv_kernel<DT, FL, NT, HP, RB, ITEMS, true, false, MV_WAVES><<<grid, 64 * MV_WAVES, lds, st>>>(w, A, a, lda, k, g.gm,
+                                                                                                 0, c, ldc, g, k, 0);
 }
 
 template <int DT, int FL, int NT, int HP>
@@ -729,6 +730,19 @@ static hipError_t go_hp(int k, int ks, int64_t cz, int m, int n, const WeightVie
         if (items != 1) return go_hp<DT, FL, NT, 0>(k, ks, cz, m, n, w, A, a, lda, c, ldc, st);
         launch_shape<DT, FL, NT, HP, MV_RB, 1>(k, ks, cz, m, n, w, A, a, lda, c, ldc, st);
         return hipGetLastError();
+    }
+    if constexpr (FL == 1 && NT == 1) {
+        // One token whose 8-wave grid would leave CUs idle (fewer than 256 workgroups, e.g. 4096 rows at
+        // k = 4096): 4-wave workgroups of half the rows (measured: Q8_0 4096x4096 5.9 -> 5.4 us; the
+        // 14336-row shapes stay faster with 8 waves)
+        constexpr int GS = 64 / MV_RB;
+        const int Gk = (k / 32 + 7) / 8, J = (Gk + GS - 1) / GS, hp4 = (16 * Gk + 255) / 256;
+        const int64_t bands = ((int64_t) m + MV_RB - 1) / MV_RB;
+        if (items == 1 && ks == k && J <= 4 && (bands + MV_WAVES / J - 1) / (MV_WAVES / J) < 256 &&
+            (HP == 0 || hp4 <= HP)) {
+            launch_shape<DT, FL, NT, HP, MV_RB, 1, 4>(k, ks, cz, m, n, w, A, a, lda, c, ldc, st);
+            return hipGetLastError();
+        }
     }
     if (items == 1) launch_shape<DT, FL, NT, HP, MV_RB, 1>(k, ks, cz, m, n, w, A, a, lda, c, ldc, st);
     else if (items == 2) launch_shape<DT, FL, NT, HP, MV_RB, 2>(k, ks, cz, m, n, w, A, a, lda, c, ldc, st);
