@@ -219,6 +219,21 @@ JAMHIP_DEV void q40_unpack(const Group<Q4_0>& w, Q40Codes& u) {
     }
 }
 
+// F2 (q4_0 block16, jam_kernels_q4k_avx512.c:463-480): fl(sw·dx)·I − fl(8·sw)·fl(xs0+xs1) per block, with
+// I over the raw nibbles (0..15).
+JAMHIP_DEV float q40_dot_f2(const Q40Codes& u, const int8_t* aq, const float* ad, const float* as, int nbv) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int b = 0; b < 8; b++) {
+        const int bq = b < nbv ? b : nbv - 1;   // stay inside the token's activations
+        const int I = dot16(u.c[2 * b + 1], ld16(aq + 32 * bq + 16), dot16(u.c[2 * b], ld16(aq + 32 * bq), 0));
+        float v = (float) I * (u.f[b] * ad[bq]);
+        v -= (8.0f * u.f[b]) * (as[2 * bq] + as[2 * bq + 1]);
+        acc += b < nbv ? v : 0.0f;
+    }
+    return acc;
+}
+
 JAMHIP_DEV float q40_dot_f1(const Q40Codes& u, const int8_t* aq, const float* ad, const int* s16, int nbv) {
     float acc = 0.0f;
 #pragma unroll
@@ -513,7 +528,7 @@ __global__ void __launch_bounds__(64 * NWV) mv_kernel(WeightView w, ActQ A, cons
         const int gg = g < Gk ? g : Gk - 1;
         const int nbv = nb - BPG * gg < BPG ? nb - BPG * gg : BPG;
         float* pp = part + (it * 64 + lane) * NT;
-        if constexpr (NT <= 2 || FL == 2 || DT != Q4_0) {   // per-token unpacking measured faster for the rest
+        if constexpr (NT <= 2 || DT != Q4_0) {   // per-token unpacking measured faster for the rest
             constexpr int TU = NT > 2 ? 1 : NT;   // keep several tokens' temporaries out of the register file
 #pragma unroll TU
             for (int t = 0; t < NT; t++) {
@@ -524,15 +539,20 @@ __global__ void __launch_bounds__(64 * NWV) mv_kernel(WeightView w, ActQ A, cons
                                                   nbv);
                 pp[t] = live ? p : 0.0f;
             }
-        } else {   // Q4_0 F1, 3..7 tokens: the group's weights unpacked once for all the tokens
+        } else {   // Q4_0, 3..8 tokens: the group's weights unpacked once for all the tokens
             Q40Codes u;
             q40_unpack(buf[i], u);
 #pragma unroll 1
             for (int t = 0; t < NT; t++) {
                 if (t >= ntv) break;
                 const int tt = FUSE ? t : t0 + t;
-                const float p = q40_dot_f1(u, aq + tt * tq + (int64_t) gg * QS, ad + tt * td + 8 * gg,
-                                           s16 + tt * t16 + 16 * gg, nbv);
+                float p;
+                if constexpr (FL == 1)
+                    p = q40_dot_f1(u, aq + tt * tq + (int64_t) gg * QS, ad + tt * td + 8 * gg, s16 + tt * t16 + 16 * gg,
+                                   nbv);
+                else
+                    p = q40_dot_f2(u, aq + tt * tq + (int64_t) gg * QS, ad + tt * td + 8 * gg, as + tt * ts + 16 * gg,
+                                   nbv);
                 pp[t] = live ? p : 0.0f;
             }
         }
