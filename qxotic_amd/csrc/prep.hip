@@ -143,7 +143,10 @@ __global__ void __launch_bounds__(256) gemm_prep(const float* __restrict__ a, in
     float* ldb = lsm;
     float* lxs = lsm + (Kp >> 5);
     float* lmx = lxs + (Kp >> 4);
-    const int t = blockIdx.x, nbk = k >> 5, lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nch = Kp >> 8;
+    // workgroup i runs on XCD i % 8: give each XCD a contiguous run of token slots, so that the slots sharing
+    // an output line (the codes, block scales and sums are token-interleaved) are written through one L2
+    const int t = (int) (blockIdx.x % 8) * (NP >> 3) + (int) (blockIdx.x >> 3);
+    const int nbk = k >> 5, lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nch = Kp >> 8;
     const int src = prep_src(t, n, gmap, goff, gpoff);
     const int j = lane & 7;   // lane within the block
     float m2 = 0.0f;
