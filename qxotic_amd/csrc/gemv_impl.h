@@ -768,21 +768,22 @@ static hipError_t go_hp(int k, int ks, int64_t cz, int m, int n, const WeightVie
 // workgroups, e.g. 4096 rows at k = 4096) and k <= 4096 (two items per row band). Measured: Q8_0 4096x4096
 // 5.85 -> 5.43 us, MXFP4 2880x2880 5.42 -> 4.54 us; the 14336-row shapes stay faster with 8 waves, and
 // 2-wave workgroups on the smaller grids were slower still (MXFP4 2880x2880 6.1 us).
-// A row band of 7 items (k = 12288 + 1 .. 14336, e.g. Llama's FFN down projection) takes 7-wave workgroups:
-// with 8, the eighth wave only re-reads the next band's weights.
+// A row band of J items that does not divide 8 (J = 3, 5, 6, 7: k up to 6144, 10240, 12288, 14336, e.g.
+// Llama's FFN down projection at 14336) takes workgroups of J·floor(8 / J) waves: with 8, the spare waves
+// only re-read the next band's weights (measured at k = 14336: Q6_K 4096x14336 12.9 -> 12.1 us).
 static int one_token_waves(int k, int m) {
     int items;
     if (!mv_items(k, &items) || items != 1) return MV_WAVES;
     const int Gk = (k / 32 + 7) / 8, J = (Gk + 64 / MV_RB - 1) / (64 / MV_RB);
     const int64_t bands = ((int64_t) m + MV_RB - 1) / MV_RB;
-    if (J == 7) return 7;
+    if (J == 3 || J == 5 || J == 6 || J == 7) return J * (MV_WAVES / J);
     return J <= 2 && (bands + MV_WAVES / J - 1) / (MV_WAVES / J) < 256 ? 4 : MV_WAVES;
 }
 
 template <int DT, int NWV>
 static hipError_t go_one(const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m, float* c, int ldc,
                          hipStream_t st) {
-    // at most 2 half-blocks per thread in the fused prologue (k <= 4096 with 4 waves, k <= 14336 with 7)
+    // at most 2 half-blocks per thread in the fused prologue (J <= NWV items of 8 groups, 16 half-blocks each)
     const int Gk = (k / 32 + 7) / 8, hp = a != nullptr ? (16 * Gk + 64 * NWV - 1) / (64 * NWV) : 0;
     if (hp == 0) launch_shape<DT, 1, 1, 0, MV_RB, 1, NWV>(k, k, 0, m, 1, w, A, a, lda, c, ldc, st);
     else if (hp == 1) launch_shape<DT, 1, 1, 1, MV_RB, 1, NWV>(k, k, 0, m, 1, w, A, a, lda, c, ldc, st);
@@ -797,6 +798,8 @@ static hipError_t go(const WeightView& w, const ActQ& A, const float* a, int lda
         if (ks == k) {
             const int nw = one_token_waves(k, m);
             if (nw == 4) return go_one<DT, 4>(w, A, a, lda, k, m, c, ldc, st);
+            if (nw == 5) return go_one<DT, 5>(w, A, a, lda, k, m, c, ldc, st);
+            if (nw == 6) return go_one<DT, 6>(w, A, a, lda, k, m, c, ldc, st);
             if (nw == 7) return go_one<DT, 7>(w, A, a, lda, k, m, c, ldc, st);
         }
     }

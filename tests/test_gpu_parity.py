@@ -207,6 +207,21 @@ def test_full_size_decode(hip, oracle, dt, m, k, n):
 
 
 @pytest.mark.parametrize("dt", O.QUANT_TYPES)
+def test_decode_workgroup_shapes(hip, oracle, dt):
+    """One-token decode workgroups sized to the row band: 3, 6 and 7 items of 8 groups per band (k = 5120,
+    11008, 14336: 6, 6 and 7 waves) and small grids (4 waves), beside two tokens on the 8-wave kernel."""
+    for (m, k) in [(72, 5120), (40, 11008), (24, 14336), (200, 4096)]:
+        w = oracle.quantize(dt, oracle.normal(0x5A11C0DE ^ (k + dt), (m, k), 0.0, 0.02))
+        for n in (1, 2):
+            say(f"decode workgroups {O.NAMES[dt]} m={m} n={n} k={k}")
+            a = oracle.outliers(4000 + n, (n, k))
+            got = run_mm(hip, dt, w, a, m, n, k)
+            ref = oracle.mm_int8(dt, w, a, m, n, k)
+            _, sa = oracle.mm_ref(dt, w, a, m, n, k)
+            assert tier1(got, ref, sa).all(), (O.NAMES[dt], m, n, k)
+
+
+@pytest.mark.parametrize("dt", O.QUANT_TYPES)
 def test_split_k_decode(hip, oracle, dt):
     """From k = 8192 on the decode kernels split K into 4096-element slices and sum the slices' partial
     results in slice order: a partial last slice (for the 32-element types also a partial last group), F1
