@@ -73,6 +73,7 @@ struct GemmAct {
     const _Float16* slo;   //   · 2^-e_t, split as f16 high part + f16 remainder
     const float* es;       // [NP] 2^e_t
     int NP, Kp;
+    int K;                 // the call's k (blocks past it are zero)
 };
 int gemm_sums_kind(int dt);   // 0 none, 1 per-32 sums, 2 per-16 sums
 size_t gemm_act_bytes(int dt, int n, int k);

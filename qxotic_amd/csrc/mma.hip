@@ -146,7 +146,9 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
     // split K (sb_per > 0): slice blockIdx.y takes super-blocks [sb_per·y, sb_per·(y + 1)) and writes its
     // partial result to c + y·c_slice (summed by split_reduce_kernel); stages are half super-blocks
     const int st0 = sb_per > 0 ? 2 * sb_per * (int) blockIdx.y : 0;
-    const int nst = sb_per > 0 ? min(2 * nsb, st0 + 2 * sb_per) : 2 * nsb;
+    // stages that hold at least one block of k (MXFP4 pads k to whole groups: k = 2880 needs 23 of 24)
+    const int nstk = min(2 * nsb, (A.K / 32 + 3) / 4);
+    const int nst = sb_per > 0 ? min(nstk, st0 + 2 * sb_per) : nstk;
     int64_t r0t = w.r0 >> 5;                     // the view's first row is tile-aligned (launcher checks)
     int slot0 = 0, crow0 = 0, nvalid = n;        // token slot -> C row: crow0 + (slot - slot0), < nvalid
     if (gp.map64 != nullptr) {                   // grouped: this slot block's expert
@@ -391,7 +393,8 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
                         bfs[bl][j][ks] = *reinterpret_cast<const half8*>(LB + ((2 * bl + ks) * 2 + q) * BN * 16 + (32 * j + r) * 16);
                     dxs[bl][j] = LDX[bl * BN + 32 * j + r];
                 }
-            if (h2 == 1) {   // group end: 2^(e_ref - 128) of the 16 output rows this lane holds
+            const bool gend = h2 == 1 || st == nstk - 1;   // the last group may end after its first half
+            if (gend) {   // group end: 2^(e_ref - 128) of the 16 output rows this lane holds
 #pragma unroll
                 for (int i = 0; i < RT; i++) {
                     const unsigned char* H = buf + S::H_OFF + (wave * RT + i) * 32 * 16;
@@ -436,7 +439,7 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
                                 accs[i][j][e] = fmaf(Dp[pb & 1][i][j][e], dxs[pb][j], accs[i][j][e]);
                 }
             }
-            if (h2 == 1) {   // group end: acc += 2^(e_ref - 128) · accs
+            if (gend) {   // group end: acc += 2^(e_ref - 128) · accs
 #pragma unroll
                 for (int i = 0; i < RT; i++)
 #pragma unroll

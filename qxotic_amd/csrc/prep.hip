@@ -263,7 +263,7 @@ static hipError_t prep_np(int dt, const float* a, int lda, int n, int NP, int k,
     _Float16* slo = (_Float16*) (p + sb);
     p += 2 * sb;
     float* es = (float*) p;
-    *out = GemmAct{bq, dx, shi, slo, es, NP, Kp};
+    *out = GemmAct{bq, dx, shi, slo, es, NP, Kp, k};
     if (NP <= 0) return hipSuccess;
     const int vec = ((reinterpret_cast<uintptr_t>(a) & 15) == 0 && (lda & 3) == 0) ? 1 : 0;
     const size_t lds = ((size_t) (Kp / 32) + (size_t) (Kp / 16) + 4) * sizeof(float);
