@@ -180,6 +180,16 @@ static int mma_min_n(int dt) {
     return x < 8 ? 8 : x;
 }
 
+// Smallest n that takes gemm_kernel (Q8_0 / Q4_0, which mma_path does not cover); below it the F2 decode
+// kernel, whose time grows linearly in n. Measured crossovers: Q8_0 14336x4096 ~60 tokens, Q4_0
+// 14336x4096 ~90, Q4_0 4096x14336 ~320 (gemm_kernel's small grid at k = 14336 takes ~600 us at any n).
+// JAM_HIP_GEMM_MIN_N overrides (tuning).
+static int gemm_min_n(int dt, int k) {
+    const char* v = getenv("JAM_HIP_GEMM_MIN_N");
+    const int x = v ? atoi(v) : k >= 8192 ? 320 : dt == Q8_0 ? 64 : 96;
+    return x < 8 ? 8 : x;
+}
+
 // Quantize A (device, f32 [n][lda]) and run the matmul into C (device, [n][ldc]). Decode-sized calls
 // with k < 8192 are one fused launch and touch no scratch (safe under stream capture once W is pinned);
 // from k = 8192 the decode kernels split K and sum the slices from the context's split buffer.
@@ -242,7 +252,7 @@ jamhip_status compute(jamhip_ctx* ctx, int dt, const WeightView& wv, const float
     if (m16 > 0) {
         if ((e = launch_quant_f2(a, lda, n, k, q, d, s, ctx->stream)) != hipSuccess)
             return hip_fail(ctx, e, "quant_f2 launch");
-        e = n >= 32 ? launch_gemm(dt, wv, A, k, m16, n, c, ldc, ctx->stream) : hipErrorNotSupported;
+        e = n >= gemm_min_n(dt, k) ? launch_gemm(dt, wv, A, k, m16, n, c, ldc, ctx->stream) : hipErrorNotSupported;
         if (e == hipErrorNotSupported && (e = decode_part(m16)) == hipSuccess)
             e = launch_gemv(dt, 2, wv, A, nullptr, 0, k, m16, n, c, ldc, ctx->stream, gpart);
         if (e != hipSuccess) return hip_fail(ctx, e, "matmul launch");
