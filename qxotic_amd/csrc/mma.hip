@@ -78,6 +78,8 @@ JAMHIP_DEV void q4k_scmn(const uint4 h, int s, int& sc, int& mn) {
     }
 }
 
+JAMHIP_DEV uint32_t word(const uint4& v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
+
 JAMHIP_DEV float h2f_bits(uint32_t b) { return (float) __builtin_bit_cast(_Float16, (uint16_t) (b & 0xffffu)); }
 
 // MXFP4: f16 pair (2^d, 2^d) for d = e_block − e_ref <= 0 (exact down to 2^-24, 0 below).
@@ -112,7 +114,7 @@ template <int DT, int RT, int CT> struct Stage {
     static constexpr int TW = MMA_WAVES * RT, BN = 32 * CT;
     static constexpr int NCS = DT == Q6_K ? 7 : 4;           // chunks per stage (Q6_K: 4 ql, 2 qh, scales)
     static constexpr int HB = DT == Q6_K ? 2 : 16;           // header bytes per row (Q6_K: d)
-    static constexpr int SW = DT == Q4_K ? 8 : DT == Q6_K ? 16 : 0;   // sums per token per group
+    static constexpr int SW = DT == Q4_K || DT == Q4_0 ? 8 : DT == Q6_K ? 16 : 0;   // sums per token per group
     static constexpr int A_OFF = 0;
     static constexpr int H_OFF = A_OFF + TW * NCS * 512;
     static constexpr int B_OFF = (H_OFF + TW * 32 * HB + 1023) / 1024 * 1024;
@@ -130,6 +132,7 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
     using S = Stage<DT, RT, CT>;
     constexpr int TW = S::TW, BN = S::BN, NCS = S::NCS;
     extern __shared__ __align__(1024) unsigned char smem[];
+    __shared__ float q40_srow[DT == Q4_0 ? MMA_WAVES * RT * 32 : 1];   // Q4_0: 2^-s of each row of the workgroup
 
     // XCD-aware placement: workgroup id i runs on XCD i % 8; give each XCD a contiguous run of
     // (row block, token block) pairs so a row block's token blocks share one L2.
@@ -219,7 +222,7 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
         if (wave == 2) dma16(dx_src + (int64_t) (4 * st) * A.NP, buf + S::DX_OFF);
         // sums: Q4_K needs them at the super-block's end (odd stage), Q6_K at its start (even stage)
         if constexpr (S::SW > 0) {
-            if ((DT == Q4_K) == (h2 == 1) && (SPC == 2 || wave == 1 || wave == 3))
+            if ((DT == Q4_0 || (DT == Q4_K) == (h2 == 1)) && (SPC == 2 || wave == 1 || wave == 3))
                 dma16(s_src + (int64_t) g * A.NP * SWB, buf + S::S_OFF + s_pl * BN * SWB + s_p * 1024);
         }
     };
@@ -368,6 +371,125 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
                         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(ahi, shi[j], acc[i][j], 0, 0, 0);
                         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(ahi, slo[j], acc[i][j], 0, 0, 0);
                         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(alo, shi[j], acc[i][j], 0, 0, 0);
+                    }
+                }
+            }
+        } else if constexpr (DT == Q4_0) {   // group of 8 blocks; stage h2 = blocks 4h2..4h2+3
+            // The weight operand is d'·nib with d' = d·2^s_r (s_r per row and group: the row's largest block
+            // scale lands in [2^10, 2^11)), split exactly into f16 hi + lo (d'·nib has at most 15 significant
+            // bits). Each block's dot then runs as two MFMAs per K-step, one FMA per output applies dx, and
+            // at the group end −8·Σ_b d'_b·xs_b joins on the matrix cores before the 2^-s_r of each row.
+            const bool gend = h2 == 1 || st == nstk - 1;   // the last group may end after its first half
+            uint4 hdr[RT], chs[RT][4];
+            half8 bfs[4][CT][2];
+            float dxs[4][CT];
+            half4 shi[CT], slo[CT];
+#pragma unroll
+            for (int i = 0; i < RT; i++) {
+                hdr[i] = *reinterpret_cast<const uint4*>(buf + S::H_OFF + ((wave * RT + i) * 32 + r) * 16);
+#pragma unroll
+                for (int bl = 0; bl < 4; bl++)
+                    chs[i][bl] = *reinterpret_cast<const uint4*>(LA + ((wave * RT + i) * NCS + bl) * 512 + 16 * r);
+            }
+#pragma unroll
+            for (int bl = 0; bl < 4; bl++)
+#pragma unroll
+                for (int j = 0; j < CT; j++) {
+#pragma unroll
+                    for (int ks = 0; ks < 2; ks++)
+                        bfs[bl][j][ks] = *reinterpret_cast<const half8*>(LB + ((2 * bl + ks) * 2 + q) * BN * 16 + (32 * j + r) * 16);
+                    dxs[bl][j] = LDX[bl * BN + 32 * j + r];
+                }
+            if (gend) {
+#pragma unroll
+                for (int j = 0; j < CT; j++) {
+                    const unsigned char* SP = buf + S::S_OFF + (32 * j + r) * 16 + 8 * q;
+                    shi[j] = *reinterpret_cast<const half4*>(SP);
+                    slo[j] = *reinterpret_cast<const half4*>(SP + BN * 16);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            if (st + 1 < nst) issue(st + 1, smem + ((st + 1) & 1) * S::BYTES);
+            // s_r of row r from its 8 block scales (f16 exponent fields); 2^-s_r goes to LDS at the group's
+            // first stage for the lanes that hold row r's outputs
+            int sr[RT];
+            // d'_b = d_b·2^s_r of block b of the group, exact in f32 and (above 2^-14) in f16
+            auto dq = [&](int i, int b) { return ldexpf(h2f_bits(word(hdr[i], b >> 1) >> (16 * (b & 1))), sr[i]); };
+#pragma unroll
+            for (int i = 0; i < RT; i++) {
+                const uint32_t e01 = max(hdr[i].x & 0x7C00u, (hdr[i].x >> 16) & 0x7C00u);
+                const uint32_t e23 = max(hdr[i].y & 0x7C00u, (hdr[i].y >> 16) & 0x7C00u);
+                const uint32_t e45 = max(hdr[i].z & 0x7C00u, (hdr[i].z >> 16) & 0x7C00u);
+                const uint32_t e67 = max(hdr[i].w & 0x7C00u, (hdr[i].w >> 16) & 0x7C00u);
+                const int emax = (int) (max(max(e01, e23), max(e45, e67)) >> 10);   // biased exponent, 0..31
+                sr[i] = 25 - emax;
+                if (h2 == 0 && q == 0) q40_srow[(wave * RT + i) * 32 + r] = ldexpf(1.0f, -sr[i]);
+            }
+            floatx16 Dp[2][RT][CT];
+#pragma unroll
+            for (int bl = 0; bl < 5; bl++) {
+                if (bl < 4) {
+                    half8 ah[RT][2], al[RT][2];
+#pragma unroll
+                    for (int i = 0; i < RT; i++) {
+                        const uint4 ch = chs[i][bl];
+                        const float df = dq(i, 4 * h2 + bl);
+                        const _Float16 dh = (_Float16) df;
+                        const half2v d2 = {dh, dh};
+                        // nibble -> exact f16 v: lane half q takes the low (elements 0-15) or high nibbles
+                        const uint32_t mask = q ? vmask_hi : vmask_lo;
+                        const uint32_t mul = q ? 0x2C002C00u : 0x3C003C00u;   // f16 pairs (1/16, 1/16) or (1, 1)
+                        const uint32_t add = q ? 0xD400D400u : 0xE400E400u;   // (-64, -64) or (-1024, -1024)
+                        const half8 v0 = frag8(ch.x, ch.y, mask, mul, add), v1 = frag8(ch.z, ch.w, mask, mul, add);
+#pragma unroll
+                        for (int e = 0; e < 8; e += 2) {
+                            const half2v a0 = {v0[e], v0[e + 1]}, a1 = {v1[e], v1[e + 1]};
+                            const half2v h0 = a0 * d2, h1 = a1 * d2;
+                            const half2v l0 = __builtin_elementwise_fma(a0, d2, -h0), l1 = __builtin_elementwise_fma(a1, d2, -h1);
+                            ah[i][0][e] = h0[0], ah[i][0][e + 1] = h0[1], ah[i][1][e] = h1[0], ah[i][1][e + 1] = h1[1];
+                            al[i][0][e] = l0[0], al[i][0][e + 1] = l0[1], al[i][1][e] = l1[0], al[i][1][e + 1] = l1[1];
+                        }
+                    }
+#pragma unroll
+                    for (int i = 0; i < RT; i++)
+#pragma unroll
+                        for (int j = 0; j < CT; j++) {
+                            floatx16 D = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i][0], bfs[bl][j][0], floatx16{}, 0, 0, 0);
+                            D = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i][0], bfs[bl][j][0], D, 0, 0, 0);
+                            D = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i][1], bfs[bl][j][1], D, 0, 0, 0);
+                            Dp[bl & 1][i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i][1], bfs[bl][j][1], D, 0, 0, 0);
+                        }
+                }
+                if (bl > 0) {
+                    const int pb = bl - 1;
+#pragma unroll
+                    for (int i = 0; i < RT; i++)
+#pragma unroll
+                        for (int j = 0; j < CT; j++)
+#pragma unroll
+                            for (int e = 0; e < 16; e++)
+                                accs[i][j][e] = fmaf(Dp[pb & 1][i][j][e], dxs[pb][j], accs[i][j][e]);
+                }
+            }
+            if (gend) {   // group end: accs −= 8·Σ_b d'_b·xs_b (hi + lo of the sums), then acc += 2^-s · accs
+                if (h2 == 0) __syncthreads();   // 2^-s of this stage's group was written above
+#pragma unroll
+                for (int i = 0; i < RT; i++) {
+                    half4 a8;   // −8·d'_b for blocks 4q..4q+3 of row r (exact: d'_b < 2^11)
+#pragma unroll
+                    for (int e = 0; e < 4; e++) a8[e] = (_Float16) (-8.0f * dq(i, 4 * q + e));
+#pragma unroll
+                    for (int j = 0; j < CT; j++) {
+                        accs[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(a8, shi[j], accs[i][j], 0, 0, 0);
+                        accs[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(a8, slo[j], accs[i][j], 0, 0, 0);
+                    }
+                    const float* SR = q40_srow + (wave * RT + i) * 32;
+#pragma unroll
+                    for (int j = 0; j < CT; j++) {
+#pragma unroll
+                        for (int e = 0; e < 16; e++)
+                            acc[i][j][e] = fmaf(SR[8 * (e >> 2) + 4 * q + (e & 3)], accs[i][j][e], acc[i][j][e]);
+                        accs[i][j] = floatx16{};
                     }
                 }
             }
@@ -631,7 +753,7 @@ static hipError_t kq_go(const WeightView& w, const GemmAct& A, int m, int n, flo
 }
 
 size_t gemm_mma_split_floats(int dt, int k, int m, int n) {
-    if (dt != Q4_K && dt != Q6_K && dt != MXFP4) return 0;
+    if (dt != Q4_K && dt != Q6_K && dt != MXFP4 && dt != Q4_0) return 0;
     const int nrb = (m + 32 * MMA_WAVES - 1) / (32 * MMA_WAVES), ncb = (n + 63) / 64, nsb = (k + 255) / 256;
     int ns, sb_per;
     split_plan(nrb * ncb, nsb, &ns, &sb_per);
@@ -640,9 +762,10 @@ size_t gemm_mma_split_floats(int dt, int k, int m, int n) {
 
 hipError_t launch_gemm_mma(int dt, const WeightView& w, const GemmAct& A, int k, int m, int n, float* c, int ldc,
                            hipStream_t st, float* part) {
-    if ((dt != MXFP4 && k % 256) || (w.r0 & 31) || A.NP % 64) return hipErrorNotSupported;
+    if (((dt == Q4_K || dt == Q6_K) && k % 256) || (w.r0 & 31) || A.NP % 64) return hipErrorNotSupported;
     switch (dt) {
     case Q4_K: return kq_go<Q4_K, 1, 2>(w, A, m, n, c, ldc, st, Groups{}, part);
+    case Q4_0: return kq_go<Q4_0, 1, 2>(w, A, m, n, c, ldc, st, Groups{}, part);
     case Q6_K: return kq_go<Q6_K, 1, 2>(w, A, m, n, c, ldc, st, Groups{}, part);
     case MXFP4: return kq_go<MXFP4, 1, 2>(w, A, m, n, c, ldc, st, Groups{}, part);
     default: return hipErrorNotSupported;
@@ -651,10 +774,12 @@ hipError_t launch_gemm_mma(int dt, const WeightView& w, const GemmAct& A, int k,
 
 hipError_t launch_gemm_mma_grouped(int dt, const WeightView& w, const GemmAct& A, int k, const Groups& g, int cap64,
                                    float* c, int ldc, hipStream_t st) {
-    if ((dt != MXFP4 && k % 256) || (w.r0 & 31) || (g.gm & 31) || A.NP != cap64 * 64) return hipErrorNotSupported;
+    if (((dt == Q4_K || dt == Q6_K) && k % 256) || (w.r0 & 31) || (g.gm & 31) || A.NP != cap64 * 64)
+        return hipErrorNotSupported;
     if (cap64 <= 0) return hipSuccess;
     switch (dt) {
     case Q4_K: return kq_go<Q4_K, 1, 2>(w, A, g.gm, A.NP, c, ldc, st, g);
+    case Q4_0: return kq_go<Q4_0, 1, 2>(w, A, g.gm, A.NP, c, ldc, st, g);
     case Q6_K: return kq_go<Q6_K, 1, 2>(w, A, g.gm, A.NP, c, ldc, st, g);
     case MXFP4: return kq_go<MXFP4, 1, 2>(w, A, g.gm, A.NP, c, ldc, st, g);
     default: return hipErrorNotSupported;
