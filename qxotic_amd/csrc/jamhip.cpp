@@ -165,27 +165,27 @@ bool env_true(const char* name) {
     return v && (!strcmp(v, "1") || !strcasecmp(v, "true") || !strcasecmp(v, "yes"));
 }
 
-// The matrix-core GEMM covers Q4_K, Q6_K (k a multiple of 256), MXFP4 and Q4_0 on 32-row-aligned views
+// The matrix-core GEMM covers Q4_K, Q6_K (k a multiple of 256), MXFP4, Q4_0 and Q8_0 on 32-row-aligned views
 // (launch_gemm_mma), for k up to the activation prep's limit (gemm_prep_fits).
 bool mma_path(int dt, int k, const WeightView& wv) {
     if (env_true("JAM_HIP_NO_MMA")) return false;
-    return (((dt == Q4_K || dt == Q6_K) && k % 256 == 0) || dt == MXFP4 || dt == Q4_0) && (wv.r0 & 31) == 0 &&
-           gemm_prep_fits(k);
+    return (((dt == Q4_K || dt == Q6_K) && k % 256 == 0) || dt == MXFP4 || dt == Q4_0 || dt == Q8_0) &&
+           (wv.r0 & 31) == 0 && gemm_prep_fits(k);
 }
 
 // Smallest n that takes the matrix cores (n >= 8 is F2 either way; small grids split K): measured on the
-// BASELINE shapes, from 8 tokens for Q4_K / Q6_K and 16 for MXFP4 and Q4_0 (Q4_0 n = 16: 32.2 us against
-// the F2 decode kernel's 41.1). JAM_HIP_MMA_MIN_N overrides (tuning).
+// BASELINE shapes, from 8 tokens for Q4_K / Q6_K and 16 for MXFP4, Q4_0 and Q8_0 (14336x4096 n = 16: Q4_0
+// 32.2 us, Q8_0 31.9 us against the F2 decode kernel's 41.1 / 50.4). JAM_HIP_MMA_MIN_N overrides (tuning).
 static int mma_min_n(int dt) {
     const char* v = getenv("JAM_HIP_MMA_MIN_N");
-    const int x = v ? atoi(v) : dt == MXFP4 || dt == Q4_0 ? 16 : 8;
+    const int x = v ? atoi(v) : dt == MXFP4 || dt == Q4_0 || dt == Q8_0 ? 16 : 8;
     return x < 8 ? 8 : x;
 }
 
-// Smallest n that takes gemm_kernel (Q8_0, which mma_path does not cover); below it the F2 decode kernel,
-// whose time grows linearly in n. Measured crossovers: Q8_0 14336x4096 ~60 tokens; at k = 14336
-// gemm_kernel's small grid takes ~600 us at any n (Q4_0 4096x14336, before Q4_0 moved to the matrix
-// cores: ~320).
+// Smallest n that takes gemm_kernel, the fallback when mma_path declines (a view not aligned to 32 rows, k
+// past the prep's limit); below it the F2 decode kernel, whose time grows linearly in n. Measured
+// crossovers: Q8_0 14336x4096 ~60 tokens; at k = 14336 gemm_kernel's small grid takes ~600 us at any n
+// (~320 tokens).
 // JAM_HIP_GEMM_MIN_N overrides (tuning).
 static int gemm_min_n(int dt, int k) {
     const char* v = getenv("JAM_HIP_GEMM_MIN_N");

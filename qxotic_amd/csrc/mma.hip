@@ -112,7 +112,7 @@ JAMHIP_DEV half8 mx_frag(uint32_t w0, uint32_t w1, int q4, uint32_t s2) {   // q
 // block scales [4][BN] f32, sums hi/lo [BN][SW] f16 each.
 template <int DT, int RT, int CT> struct Stage {
     static constexpr int TW = MMA_WAVES * RT, BN = 32 * CT;
-    static constexpr int NCS = DT == Q6_K ? 7 : 4;           // chunks per stage (Q6_K: 4 ql, 2 qh, scales)
+    static constexpr int NCS = DT == Q6_K ? 7 : DT == Q8_0 ? 8 : 4;   // chunks per stage (Q6_K: 4 ql, 2 qh, scales)
     static constexpr int HB = DT == Q6_K ? 2 : 16;           // header bytes per row (Q6_K: d)
     static constexpr int SW = DT == Q4_K || DT == Q4_0 ? 8 : DT == Q6_K ? 16 : 0;   // sums per token per group
     static constexpr int A_OFF = 0;
@@ -132,7 +132,7 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
     using S = Stage<DT, RT, CT>;
     constexpr int TW = S::TW, BN = S::BN, NCS = S::NCS;
     extern __shared__ __align__(1024) unsigned char smem[];
-    __shared__ float q40_srow[DT == Q4_0 ? MMA_WAVES * RT * 32 : 1];   // Q4_0: 2^-s of each row of the workgroup
+    __shared__ float q40_srow[DT == Q4_0 || DT == Q8_0 ? MMA_WAVES * RT * 32 : 1];   // 2^-s of each row
 
     // XCD-aware placement: workgroup id i runs on XCD i % 8; give each XCD a contiguous run of
     // (row block, token block) pairs so a row block's token blocks share one L2.
@@ -195,9 +195,11 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
     auto issue = [&](int st, unsigned char* buf) {
         const int g = st >> 1, h2 = st & 1;
         const uint8_t* ag = a_src + (int64_t) g * (NC * CHUNK_STRIDE);
-        if constexpr (DT != Q6_K) {   // Q4_K chunks 4h2..4h2+3 (sub-block pairs), MXFP4 blocks 4h2..4h2+3
+        if constexpr (DT != Q6_K) {   // Q4_K chunks 4h2..4h2+3 (sub-block pairs), MXFP4 / Q4_0 blocks 4h2..4h2+3,
+                                      // Q8_0 chunks 8h2..8h2+7 (two per block)
 #pragma unroll
-            for (int p = 0; p < 2; p++) dma16(ag + (4 * h2 + 2 * p) * CHUNK_STRIDE, buf + a_dst + 2 * p * 512);
+            for (int p = 0; p < NCS / 2; p++)
+                dma16(ag + (NCS * h2 + 2 * p) * CHUNK_STRIDE, buf + a_dst + 2 * p * 512);
         } else {   // ql chunks 4h2..4h2+3, qh chunks 8+2h2, 9+2h2, the scales chunk 12 (512 B)
 #pragma unroll
             for (int p = 0; p < 2; p++) dma16(ag + (4 * h2 + 2 * p) * CHUNK_STRIDE, buf + a_dst + 2 * p * 512);
@@ -231,9 +233,11 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
     uint32_t vmask_lo, vmask_hi;
     asm volatile("v_mov_b32 %0, 0x000F000F" : "=v"(vmask_lo));
     asm volatile("v_mov_b32 %0, 0x00F000F0" : "=v"(vmask_hi));
-    uint32_t vmask_qh;
+    uint32_t vmask_qh, vmask_b;
     asm volatile("v_mov_b32 %0, 0x00300030" : "=v"(vmask_qh));
+    asm volatile("v_mov_b32 %0, 0x00FF00FF" : "=v"(vmask_b));
     (void) vmask_qh;
+    (void) vmask_b;
 
     floatx16 acc[RT][CT], accs[RT][CT];
 #pragma unroll
@@ -374,11 +378,12 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
                     }
                 }
             }
-        } else if constexpr (DT == Q4_0) {   // group of 8 blocks; stage h2 = blocks 4h2..4h2+3
-            // The weight operand is d'·nib with d' = d·2^s_r (s_r per row and group: the row's largest block
-            // scale lands in [2^10, 2^11)), split exactly into f16 hi + lo (d'·nib has at most 15 significant
-            // bits). Each block's dot then runs as two MFMAs per K-step, one FMA per output applies dx, and
-            // at the group end −8·Σ_b d'_b·xs_b joins on the matrix cores before the 2^-s_r of each row.
+        } else if constexpr (DT == Q4_0 || DT == Q8_0) {   // group of 8 blocks; stage h2 = blocks 4h2..4h2+3
+            // The weight operand is d'·code with d' = d·2^s_r (s_r per row and group: the row's largest block
+            // scale lands in [2^10, 2^11) for Q4_0's nibbles, [2^7, 2^8) for Q8_0's int8, so |d'·code| < 2^15),
+            // split exactly into f16 hi + lo (d'·code has at most 15 significant bits for Q4_0, 19 for Q8_0). Each block's dot then runs as two MFMAs per K-step,
+            // one FMA per output applies dx, and at the group end (Q4_0) −8·Σ_b d'_b·xs_b joins on the matrix
+            // cores before the 2^-s_r of each row.
             const bool gend = h2 == 1 || st == nstk - 1;   // the last group may end after its first half
             uint4 hdr[RT], chs[RT][4];
             half8 bfs[4][CT][2];
@@ -388,8 +393,10 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
             for (int i = 0; i < RT; i++) {
                 hdr[i] = *reinterpret_cast<const uint4*>(buf + S::H_OFF + ((wave * RT + i) * 32 + r) * 16);
 #pragma unroll
-                for (int bl = 0; bl < 4; bl++)
-                    chs[i][bl] = *reinterpret_cast<const uint4*>(LA + ((wave * RT + i) * NCS + bl) * 512 + 16 * r);
+                for (int bl = 0; bl < 4; bl++) {   // Q4_0: block bl's chunk; Q8_0: its half q (elements 16q..)
+                    const int cl = DT == Q8_0 ? 2 * bl + q : bl;
+                    chs[i][bl] = *reinterpret_cast<const uint4*>(LA + ((wave * RT + i) * NCS + cl) * 512 + 16 * r);
+                }
             }
 #pragma unroll
             for (int bl = 0; bl < 4; bl++)
@@ -400,7 +407,7 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
                         bfs[bl][j][ks] = *reinterpret_cast<const half8*>(LB + ((2 * bl + ks) * 2 + q) * BN * 16 + (32 * j + r) * 16);
                     dxs[bl][j] = LDX[bl * BN + 32 * j + r];
                 }
-            if (gend) {
+            if (DT == Q4_0 && gend) {
 #pragma unroll
                 for (int j = 0; j < CT; j++) {
                     const unsigned char* SP = buf + S::S_OFF + (32 * j + r) * 16 + 8 * q;
@@ -422,7 +429,7 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
                 const uint32_t e45 = max(hdr[i].z & 0x7C00u, (hdr[i].z >> 16) & 0x7C00u);
                 const uint32_t e67 = max(hdr[i].w & 0x7C00u, (hdr[i].w >> 16) & 0x7C00u);
                 const int emax = (int) (max(max(e01, e23), max(e45, e67)) >> 10);   // biased exponent, 0..31
-                sr[i] = 25 - emax;
+                sr[i] = (DT == Q8_0 ? 22 : 25) - emax;   // |d'·code| < 2^15 (f16 range)
                 if (h2 == 0 && q == 0) q40_srow[(wave * RT + i) * 32 + r] = ldexpf(1.0f, -sr[i]);
             }
             floatx16 Dp[2][RT][CT];
@@ -436,11 +443,17 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
                         const float df = dq(i, 4 * h2 + bl);
                         const _Float16 dh = (_Float16) df;
                         const half2v d2 = {dh, dh};
-                        // nibble -> exact f16 v: lane half q takes the low (elements 0-15) or high nibbles
-                        const uint32_t mask = q ? vmask_hi : vmask_lo;
-                        const uint32_t mul = q ? 0x2C002C00u : 0x3C003C00u;   // f16 pairs (1/16, 1/16) or (1, 1)
-                        const uint32_t add = q ? 0xD400D400u : 0xE400E400u;   // (-64, -64) or (-1024, -1024)
-                        const half8 v0 = frag8(ch.x, ch.y, mask, mul, add), v1 = frag8(ch.z, ch.w, mask, mul, add);
+                        half8 v0, v1;   // the codes as exact f16
+                        if constexpr (DT == Q4_0) {   // lane half q takes the low (elements 0-15) or high nibbles
+                            const uint32_t mask = q ? vmask_hi : vmask_lo;
+                            const uint32_t mul = q ? 0x2C002C00u : 0x3C003C00u;   // f16 pairs (1/16, 1/16) or (1, 1)
+                            const uint32_t add = q ? 0xD400D400u : 0xE400E400u;   // (-64, -64) or (-1024, -1024)
+                            v0 = frag8(ch.x, ch.y, mask, mul, add);
+                            v1 = frag8(ch.z, ch.w, mask, mul, add);
+                        } else {   // int8 ^ 0x80 = q + 128, as the f16 1024 + q + 128, minus 1152
+                            v0 = frag8(ch.x ^ 0x80808080u, ch.y ^ 0x80808080u, vmask_b, 0x3C003C00u, 0xE480E480u);
+                            v1 = frag8(ch.z ^ 0x80808080u, ch.w ^ 0x80808080u, vmask_b, 0x3C003C00u, 0xE480E480u);
+                        }
 #pragma unroll
                         for (int e = 0; e < 8; e += 2) {
                             const half2v a0 = {v0[e], v0[e + 1]}, a1 = {v1[e], v1[e + 1]};
@@ -471,17 +484,19 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
                                 accs[i][j][e] = fmaf(Dp[pb & 1][i][j][e], dxs[pb][j], accs[i][j][e]);
                 }
             }
-            if (gend) {   // group end: accs −= 8·Σ_b d'_b·xs_b (hi + lo of the sums), then acc += 2^-s · accs
+            if (gend) {   // group end: (Q4_0) accs −= 8·Σ_b d'_b·xs_b (hi + lo of the sums), then acc += 2^-s · accs
                 if (h2 == 0) __syncthreads();   // 2^-s of this stage's group was written above
 #pragma unroll
                 for (int i = 0; i < RT; i++) {
-                    half4 a8;   // −8·d'_b for blocks 4q..4q+3 of row r (exact: d'_b < 2^11)
+                    if constexpr (DT == Q4_0) {
+                        half4 a8;   // −8·d'_b for blocks 4q..4q+3 of row r (exact: d'_b < 2^11)
 #pragma unroll
-                    for (int e = 0; e < 4; e++) a8[e] = (_Float16) (-8.0f * dq(i, 4 * q + e));
+                        for (int e = 0; e < 4; e++) a8[e] = (_Float16) (-8.0f * dq(i, 4 * q + e));
 #pragma unroll
-                    for (int j = 0; j < CT; j++) {
-                        accs[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(a8, shi[j], accs[i][j], 0, 0, 0);
-                        accs[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(a8, slo[j], accs[i][j], 0, 0, 0);
+                        for (int j = 0; j < CT; j++) {
+                            accs[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(a8, shi[j], accs[i][j], 0, 0, 0);
+                            accs[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(a8, slo[j], accs[i][j], 0, 0, 0);
+                        }
                     }
                     const float* SR = q40_srow + (wave * RT + i) * 32;
 #pragma unroll
@@ -753,7 +768,7 @@ static hipError_t kq_go(const WeightView& w, const GemmAct& A, int m, int n, flo
 }
 
 size_t gemm_mma_split_floats(int dt, int k, int m, int n) {
-    if (dt != Q4_K && dt != Q6_K && dt != MXFP4 && dt != Q4_0) return 0;
+    if (dt != Q4_K && dt != Q6_K && dt != MXFP4 && dt != Q4_0 && dt != Q8_0) return 0;
     const int nrb = (m + 32 * MMA_WAVES - 1) / (32 * MMA_WAVES), ncb = (n + 63) / 64, nsb = (k + 255) / 256;
     int ns, sb_per;
     split_plan(nrb * ncb, nsb, &ns, &sb_per);
@@ -766,6 +781,7 @@ hipError_t launch_gemm_mma(int dt, const WeightView& w, const GemmAct& A, int k,
     switch (dt) {
     case Q4_K: return kq_go<Q4_K, 1, 2>(w, A, m, n, c, ldc, st, Groups{}, part);
     case Q4_0: return kq_go<Q4_0, 1, 2>(w, A, m, n, c, ldc, st, Groups{}, part);
+    case Q8_0: return kq_go<Q8_0, 1, 2>(w, A, m, n, c, ldc, st, Groups{}, part);
     case Q6_K: return kq_go<Q6_K, 1, 2>(w, A, m, n, c, ldc, st, Groups{}, part);
     case MXFP4: return kq_go<MXFP4, 1, 2>(w, A, m, n, c, ldc, st, Groups{}, part);
     default: return hipErrorNotSupported;
@@ -780,6 +796,7 @@ hipError_t launch_gemm_mma_grouped(int dt, const WeightView& w, const GemmAct& A
     switch (dt) {
     case Q4_K: return kq_go<Q4_K, 1, 2>(w, A, g.gm, A.NP, c, ldc, st, g);
     case Q4_0: return kq_go<Q4_0, 1, 2>(w, A, g.gm, A.NP, c, ldc, st, g);
+    case Q8_0: return kq_go<Q8_0, 1, 2>(w, A, g.gm, A.NP, c, ldc, st, g);
     case Q6_K: return kq_go<Q6_K, 1, 2>(w, A, g.gm, A.NP, c, ldc, st, g);
     case MXFP4: return kq_go<MXFP4, 1, 2>(w, A, g.gm, A.NP, c, ldc, st, g);
     default: return hipErrorNotSupported;
