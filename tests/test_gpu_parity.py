@@ -221,6 +221,27 @@ def test_decode_workgroup_shapes(hip, oracle, dt):
             assert tier1(got, ref, sa).all(), (O.NAMES[dt], m, n, k)
 
 
+@pytest.mark.parametrize("dt", [O.Q4_0, O.Q8_0])
+def test_matrix_core_block_scale_spread(hip, oracle, dt):
+    """Q4_0 / Q8_0 on the matrix cores fold each block's fp16 scale into the weight operand through a per-row
+    power of two: block scales 2^-20 .. 2^6 apart inside a group, a row whose blocks are all tiny, a
+    zero block, and a partial last group (k = 800) must all meet the tier-1 bound row by row."""
+    m, k, n = 64, 800, 40
+    rng = np.random.default_rng(0x5CA1E ^ dt)
+    x = oracle.normal(0x5CA1E + dt, (m, k), 0.0, 0.02)
+    factor = np.exp2(rng.choice([-20.0, -8.0, 0.0, 6.0], size=(m, k // 32)))
+    factor[5, :] = 2.0 ** -22        # a row of tiny blocks only
+    factor[9, 3] = 0.0               # a zero block
+    w = oracle.quantize(dt, (x * np.repeat(factor, 32, axis=1)).astype(np.float32))
+    a = oracle.outliers(77 + dt, (n, k))
+    say(f"block-scale spread {O.NAMES[dt]} m={m} n={n} k={k}")
+    got = run_mm(hip, dt, w, a, m, n, k)
+    ref = oracle.mm_int8(dt, w, a, m, n, k)
+    _, sa = oracle.mm_ref(dt, w, a, m, n, k)
+    ok = tier1(got, ref, sa)
+    assert ok.all(), (O.NAMES[dt], np.argwhere(~ok)[:4].tolist())
+
+
 @pytest.mark.parametrize("dt", O.QUANT_TYPES)
 def test_split_k_decode(hip, oracle, dt):
     """From k = 8192 on the decode kernels split K into 4096-element slices and sum the slices' partial
