@@ -143,6 +143,47 @@ jamhip_status jamhip_ctx_set_stream(jamhip_ctx* ctx, void* stream);
 void*         jamhip_ctx_stream(const jamhip_ctx* ctx);
 jamhip_status jamhip_ctx_synchronize(jamhip_ctx* ctx);
 
+/* ---- GGUF device weight registry (model load).
+ * Replaces the load step of jinfer's ModelLoader (jinfer/jinfer-kernels/src/main/java/com/qxotic/jinfer/
+ * kernels/ModelLoader.java:35-104: GGUF.read of the header, then one READ_ONLY mapping of the tensor data
+ * region and one view per tensor) for the weights that jam multiplies, and adds what that loader leaves to
+ * the first jam_mm call: the device copy. open parses a GGUF v3 file with the checks of the qxotic reader
+ * (gguf/src/main/java/com/qxotic/format/gguf/impl/ReaderImpl.java:31-380) and maps its data region;
+ * pin uploads and repacks every tensor of a jam weight dtype once, keyed exactly as jamhip_weight_pin
+ * keys it. A tensor of GGUF dims [d0, d1, d2] (d0 contiguous) is pinned as d1·d2 rows of ldw = d0, so an
+ * expert slice of a stacked expert tensor (GptOss.java:673-684) resolves inside it at row e·d1, and
+ * jamhip_mm_grouped takes the stacked tensor itself with m = d1. */
+typedef struct jamhip_gguf jamhip_gguf;
+
+typedef struct {
+    const char* name;      /* valid while the handle is open */
+    int         type;      /* ggml_type id (GGMLType.java:31-277) */
+    int         n_dims;    /* 0..4 */
+    int64_t     dims[4];   /* GGUF order, dims[0] contiguous; unused dims are 1 */
+    int64_t     offset;    /* from the start of the tensor data region */
+    int64_t     bytes;
+    const void* data;      /* inside the handle's read-only mapping; NULL if the region is empty */
+} jamhip_gguf_tensor;
+
+/* NULL on failure, with the reason in err (err_cap bytes, NUL-terminated; err may be NULL). No GPU use. */
+jamhip_gguf*  jamhip_gguf_open(const char* path, char* err, size_t err_cap);
+void          jamhip_gguf_close(jamhip_gguf* g);
+int64_t       jamhip_gguf_tensor_count(const jamhip_gguf* g);
+jamhip_status jamhip_gguf_tensor_at(const jamhip_gguf* g, int64_t i, jamhip_gguf_tensor* out);
+int64_t       jamhip_gguf_find(const jamhip_gguf* g, const char* name);   /* index or -1 */
+int64_t       jamhip_gguf_data_offset(const jamhip_gguf* g);              /* file offset of the data region */
+int           jamhip_gguf_alignment(const jamhip_gguf* g);
+
+/* Pin every Q8_0 / Q4_0 / Q4_K / Q6_K / MXFP4 tensor of g at data_base + offset: data_base is the
+ * caller's own mapping of the same file's data region (the addresses its jam calls will pass), or NULL
+ * for the handle's mapping. Other dtypes are skipped. Stops at the first failure (the status of that
+ * tensor, its name in jamhip_last_error); tensors pinned before it stay pinned. n_pinned / bytes_pinned
+ * (either may be NULL) receive the count and file bytes of the tensors now resident. evict drops the
+ * pins that start at those addresses. */
+jamhip_status jamhip_gguf_pin(jamhip_ctx* ctx, const jamhip_gguf* g, const void* data_base, int64_t* n_pinned,
+                              int64_t* bytes_pinned);
+jamhip_status jamhip_gguf_evict(jamhip_ctx* ctx, const jamhip_gguf* g, const void* data_base, int64_t* n_evicted);
+
 #ifdef __cplusplus
 }
 #endif

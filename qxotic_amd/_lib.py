@@ -30,6 +30,15 @@ SIGNATURES = [
     ("jamhip_ctx_set_stream", _I, [_VP, _VP]),
     ("jamhip_ctx_stream", _VP, [_VP]),
     ("jamhip_ctx_synchronize", _I, [_VP]),
+    ("jamhip_gguf_open", _VP, [C.c_char_p, C.c_char_p, C.c_size_t]),
+    ("jamhip_gguf_close", None, [_VP]),
+    ("jamhip_gguf_tensor_count", _I64, [_VP]),
+    ("jamhip_gguf_tensor_at", _I, [_VP, _I64, _VP]),
+    ("jamhip_gguf_find", _I64, [_VP, C.c_char_p]),
+    ("jamhip_gguf_data_offset", _I64, [_VP]),
+    ("jamhip_gguf_alignment", _I, [_VP]),
+    ("jamhip_gguf_pin", _I, [_VP, _VP, _VP, _VP, _VP]),
+    ("jamhip_gguf_evict", _I, [_VP, _VP, _VP, _VP]),
 ]
 
 

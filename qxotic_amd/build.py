@@ -36,6 +36,7 @@ UNITS = {   # source -> extra flags
     "mma.hip": [],
     "moe.hip": [],
     "jamhip.cpp": ["-x", "hip"],
+    "gguf.cpp": [],
 }
 
 

@@ -4,6 +4,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <atomic>
 #include <cstdio>
 #include <cstdlib>
@@ -13,6 +14,7 @@
 #include <vector>
 
 #include "common.h"
+#include "gguf.h"
 #include "launch.h"
 
 using namespace jamhip;
@@ -56,6 +58,10 @@ bool supported_w(int dt) { return dt == Q8_0 || dt == Q4_0 || dt == Q4_K || dt =
 thread_local std::string g_create_error = "";
 
 }  // namespace
+
+struct jamhip_gguf {
+    GgufFile* f;
+};
 
 struct jamhip_ctx {
     int device = 0;
@@ -109,22 +115,25 @@ jamhip_status validate(jamhip_ctx* ctx, const void* w, int wt, int ldw, const vo
 int64_t row_bytes(int dt, int64_t elems) { return elems / block_elems(dt) * block_bytes(dt); }
 
 // Registry lookup: W inside a pinned range, on a row boundary, same (dtype, ldw), rows [r0, r0+m) held.
+// Pins are kept sorted by host address and never overlap, so the only candidate is the last pin that
+// starts at or below W: one binary search per call.
 bool lookup(jamhip_ctx* ctx, const void* w, int dt, int ldw, int m, WeightView* out) {
     std::lock_guard<std::mutex> lk(ctx->pin_mu);
     const uintptr_t p = reinterpret_cast<uintptr_t>(w);
-    for (const Pin& pin : ctx->pins) {
-        if (pin.dt != dt || pin.ldw != ldw || p < pin.host || p >= pin.host + (uintptr_t) pin.span) continue;
-        const int64_t off = (int64_t) (p - pin.host), rbytes = row_bytes(dt, ldw);
-        if (off % rbytes) continue;
-        const int64_t r0 = off / rbytes;
-        if (r0 + m > pin.rows) continue;
-        out->qs = pin.dev;
-        out->sc = pin.sc;
-        out->G = pin.G;
-        out->r0 = r0;
-        return true;
-    }
-    return false;
+    auto it = std::upper_bound(ctx->pins.begin(), ctx->pins.end(), p,
+                               [](uintptr_t v, const Pin& pin) { return v < pin.host; });
+    if (it == ctx->pins.begin()) return false;
+    const Pin& pin = *(it - 1);
+    if (pin.dt != dt || pin.ldw != ldw || p >= pin.host + (uintptr_t) pin.span) return false;
+    const int64_t off = (int64_t) (p - pin.host), rbytes = row_bytes(dt, ldw);
+    if (off % rbytes) return false;
+    const int64_t r0 = off / rbytes;
+    if (r0 + m > pin.rows) return false;
+    out->qs = pin.dev;
+    out->sc = pin.sc;
+    out->G = pin.G;
+    out->r0 = r0;
+    return true;
 }
 
 // Upload `rows` raw host rows (stride raw_stride bytes, rb blocks used per row) into a device-layout
@@ -265,6 +274,52 @@ jamhip_status compute(jamhip_ctx* ctx, int dt, const WeightView& wv, const float
     return JAMHIP_OK;
 }
 
+// Pin rows [0, m) of the host tensor at w (caller holds the Busy guard, device current). The staging
+// buffer is kept when `keep_staging` (a registry load reuses it for every tensor).
+jamhip_status pin_range(jamhip_ctx* ctx, const void* w, int wt, int ldw, int64_t m, bool keep_staging) {
+    const uintptr_t host = reinterpret_cast<uintptr_t>(w);
+    const int64_t rb = ldw / block_elems(wt), G = groups_of(wt, rb), span = m * row_bytes(wt, ldw);
+    {
+        std::lock_guard<std::mutex> lk(ctx->pin_mu);
+        auto it = std::lower_bound(ctx->pins.begin(), ctx->pins.end(), host,
+                                   [](const Pin& pin, uintptr_t v) { return pin.host < v; });
+        if (it != ctx->pins.end() && it->host == host && it->dt == wt && it->ldw == ldw && it->rows == m)
+            return JAMHIP_OK;   // already pinned
+        const bool hits_next = it != ctx->pins.end() && it->host < host + (uintptr_t) span;
+        const bool hits_prev = it != ctx->pins.begin() && host < (it - 1)->host + (uintptr_t) (it - 1)->span;
+        if (hits_next || hits_prev) return fail(ctx, JAMHIP_EINVAL, "pin: range overlaps a pinned tensor (evict it first)");
+    }
+    const int64_t qsz = align256(tiled_rows(m) * G * group_chunks(wt) * 16), ssz = tiled_rows(m) * G * group_scale_bytes(wt);
+    uint8_t* dev = nullptr;
+    hipError_t e = hipMalloc((void**) &dev, (size_t) (qsz + ssz));
+    if (e != hipSuccess) return hip_fail(ctx, e, "pin: device alloc");
+    uint8_t* sc = dev + qsz;
+    jamhip_status st = upload(ctx, (const uint8_t*) w, wt, row_bytes(wt, ldw), m, rb, G, dev, sc);
+    if (st == JAMHIP_OK && (e = hipStreamSynchronize(ctx->stream)) != hipSuccess) st = hip_fail(ctx, e, "pin: sync");
+    if (st != JAMHIP_OK) {
+        (void) hipFree(dev);
+        return st;
+    }
+    if (!keep_staging) ctx->w_raw.release();   // staging is sized to the tensor; do not hold it
+    std::lock_guard<std::mutex> lk(ctx->pin_mu);
+    auto it = std::lower_bound(ctx->pins.begin(), ctx->pins.end(), host,
+                               [](const Pin& pin, uintptr_t v) { return pin.host < v; });
+    ctx->pins.insert(it, Pin{host, span, wt, ldw, m, G, dev, sc, qsz + ssz});
+    return JAMHIP_OK;
+}
+
+// Drop the pin that starts at host (caller holds the Busy guard, device current); false if none does.
+bool evict_at(jamhip_ctx* ctx, uintptr_t host) {
+    std::lock_guard<std::mutex> lk(ctx->pin_mu);
+    auto it = std::lower_bound(ctx->pins.begin(), ctx->pins.end(), host,
+                               [](const Pin& pin, uintptr_t v) { return pin.host < v; });
+    if (it == ctx->pins.end() || it->host != host) return false;
+    (void) hipStreamSynchronize(ctx->stream);
+    (void) hipFree(it->dev);
+    ctx->pins.erase(it);
+    return true;
+}
+
 }  // namespace
 
 extern "C" {
@@ -377,31 +432,7 @@ jamhip_status jamhip_weight_pin(jamhip_ctx* ctx, const void* w, int wt, int ldw,
     Busy guard(ctx);
     if (!guard.ok) return fail(ctx, JAMHIP_EBUSY, "context busy");
     (void) hipSetDevice(ctx->device);
-    const uintptr_t host = reinterpret_cast<uintptr_t>(w);
-    const int64_t rb = ldw / block_elems(wt), G = groups_of(wt, rb), span = (int64_t) m * row_bytes(wt, ldw);
-    {
-        std::lock_guard<std::mutex> lk(ctx->pin_mu);
-        for (const Pin& p : ctx->pins) {
-            if (p.host == host && p.dt == wt && p.ldw == ldw && p.rows == m) return JAMHIP_OK;   // already pinned
-            if (host < p.host + (uintptr_t) p.span && p.host < host + (uintptr_t) span)
-                return fail(ctx, JAMHIP_EINVAL, "pin: range overlaps a pinned tensor (evict it first)");
-        }
-    }
-    const int64_t qsz = align256(tiled_rows(m) * G * group_chunks(wt) * 16), ssz = tiled_rows(m) * G * group_scale_bytes(wt);
-    uint8_t* dev = nullptr;
-    hipError_t e = hipMalloc((void**) &dev, (size_t) (qsz + ssz));
-    if (e != hipSuccess) return hip_fail(ctx, e, "pin: device alloc");
-    uint8_t* sc = dev + qsz;
-    jamhip_status st = upload(ctx, (const uint8_t*) w, wt, row_bytes(wt, ldw), m, rb, G, dev, sc);
-    if (st == JAMHIP_OK && (e = hipStreamSynchronize(ctx->stream)) != hipSuccess) st = hip_fail(ctx, e, "pin: sync");
-    if (st != JAMHIP_OK) {
-        (void) hipFree(dev);
-        return st;
-    }
-    ctx->w_raw.release();   // staging is sized to the tensor; do not hold it
-    std::lock_guard<std::mutex> lk(ctx->pin_mu);
-    ctx->pins.push_back(Pin{host, span, wt, ldw, m, G, dev, sc, qsz + ssz});
-    return JAMHIP_OK;
+    return pin_range(ctx, w, wt, ldw, m, false);
 }
 
 jamhip_status jamhip_weight_evict(jamhip_ctx* ctx, const void* w) {
@@ -409,16 +440,8 @@ jamhip_status jamhip_weight_evict(jamhip_ctx* ctx, const void* w) {
     Busy guard(ctx);
     if (!guard.ok) return fail(ctx, JAMHIP_EBUSY, "context busy");
     (void) hipSetDevice(ctx->device);
-    std::lock_guard<std::mutex> lk(ctx->pin_mu);
-    for (size_t i = 0; i < ctx->pins.size(); i++) {
-        if (ctx->pins[i].host == reinterpret_cast<uintptr_t>(w)) {
-            (void) hipStreamSynchronize(ctx->stream);
-            (void) hipFree(ctx->pins[i].dev);
-            ctx->pins.erase(ctx->pins.begin() + (long) i);
-            return JAMHIP_OK;
-        }
-    }
-    return fail(ctx, JAMHIP_EINVAL, "evict: no pinned tensor starts at this address");
+    if (!evict_at(ctx, reinterpret_cast<uintptr_t>(w))) return fail(ctx, JAMHIP_EINVAL, "evict: no pinned tensor starts at this address");
+    return JAMHIP_OK;
 }
 
 int64_t jamhip_weight_bytes(const jamhip_ctx* ctx) {
@@ -595,6 +618,105 @@ jamhip_status jamhip_ctx_synchronize(jamhip_ctx* ctx) {
     (void) hipSetDevice(ctx->device);
     hipError_t e = hipStreamSynchronize(ctx->stream);
     return e == hipSuccess ? JAMHIP_OK : hip_fail(ctx, e, "sync");
+}
+
+// ------------------------------------------------------------------ GGUF weight registry
+jamhip_gguf* jamhip_gguf_open(const char* path, char* err, size_t err_cap) {
+    std::string e;
+    GgufFile* f = gguf_read(path, &e);
+    if (err && err_cap) snprintf(err, err_cap, "%s", f ? "" : e.c_str());
+    return f ? new jamhip_gguf{f} : nullptr;
+}
+
+void jamhip_gguf_close(jamhip_gguf* g) {
+    if (!g) return;
+    gguf_free(g->f);
+    delete g;
+}
+
+int64_t jamhip_gguf_tensor_count(const jamhip_gguf* g) { return g ? (int64_t) g->f->tensors.size() : -1; }
+int64_t jamhip_gguf_data_offset(const jamhip_gguf* g) { return g ? g->f->data_offset : -1; }
+int     jamhip_gguf_alignment(const jamhip_gguf* g) { return g ? (int) g->f->alignment : -1; }
+
+jamhip_status jamhip_gguf_tensor_at(const jamhip_gguf* g, int64_t i, jamhip_gguf_tensor* out) {
+    if (!g || !out || i < 0 || i >= (int64_t) g->f->tensors.size()) return JAMHIP_EINVAL;
+    const GgufTensor& t = g->f->tensors[(size_t) i];
+    out->name = t.name.c_str();
+    out->type = t.type;
+    out->n_dims = t.n_dims;
+    for (int d = 0; d < 4; d++) out->dims[d] = t.dims[d];
+    out->offset = t.offset;
+    out->bytes = t.bytes;
+    out->data = g->f->data ? g->f->data + t.offset : nullptr;
+    return JAMHIP_OK;
+}
+
+int64_t jamhip_gguf_find(const jamhip_gguf* g, const char* name) {
+    if (!g || !name) return -1;
+    for (size_t i = 0; i < g->f->tensors.size(); i++)
+        if (g->f->tensors[i].name == name) return (int64_t) i;
+    return -1;
+}
+
+namespace {
+// A tensor the registry pins: a jam weight dtype with data; ldw = dims[0], rows = the other dims' product.
+bool registry_shape(const GgufTensor& t, int* ldw, int64_t* rows) {
+    if (!supported_w(t.type) || t.bytes == 0) return false;
+    *ldw = (int) t.dims[0];
+    *rows = t.bytes / row_bytes(t.type, t.dims[0]);
+    return true;
+}
+}  // namespace
+
+jamhip_status jamhip_gguf_pin(jamhip_ctx* ctx, const jamhip_gguf* g, const void* data_base, int64_t* n_pinned,
+                              int64_t* bytes_pinned) {
+    if (n_pinned) *n_pinned = 0;
+    if (bytes_pinned) *bytes_pinned = 0;
+    if (!ctx) return JAMHIP_EINVAL;
+    if (!g) return fail(ctx, JAMHIP_EINVAL, "gguf pin: null handle");
+    const uint8_t* base = data_base ? static_cast<const uint8_t*>(data_base) : g->f->data;
+    Busy guard(ctx);
+    if (!guard.ok) return fail(ctx, JAMHIP_EBUSY, "context busy");
+    (void) hipSetDevice(ctx->device);
+    jamhip_status st = JAMHIP_OK;
+    for (const GgufTensor& t : g->f->tensors) {
+        int ldw;
+        int64_t rows;
+        if (!registry_shape(t, &ldw, &rows)) continue;
+        if (t.dims[0] % block_elems(t.type)) {
+            st = fail(ctx, JAMHIP_EUNSUPPORTED, "gguf pin: tensor " + t.name + ": row extent is not a whole number of blocks");
+            break;
+        }
+        if (t.dims[0] > (1 << 30) || rows > INT32_MAX) {
+            st = fail(ctx, JAMHIP_EUNSUPPORTED, "gguf pin: tensor " + t.name + " exceeds the kernels' 32-bit extents");
+            break;
+        }
+        if ((st = pin_range(ctx, base + t.offset, t.type, ldw, rows, true)) != JAMHIP_OK) {
+            ctx->err = "gguf pin: tensor " + t.name + ": " + ctx->err;
+            break;
+        }
+        if (n_pinned) ++*n_pinned;
+        if (bytes_pinned) *bytes_pinned += t.bytes;
+    }
+    ctx->w_raw.release();
+    return st;
+}
+
+jamhip_status jamhip_gguf_evict(jamhip_ctx* ctx, const jamhip_gguf* g, const void* data_base, int64_t* n_evicted) {
+    if (n_evicted) *n_evicted = 0;
+    if (!ctx) return JAMHIP_EINVAL;
+    if (!g) return fail(ctx, JAMHIP_EINVAL, "gguf evict: null handle");
+    const uint8_t* base = data_base ? static_cast<const uint8_t*>(data_base) : g->f->data;
+    Busy guard(ctx);
+    if (!guard.ok) return fail(ctx, JAMHIP_EBUSY, "context busy");
+    (void) hipSetDevice(ctx->device);
+    for (const GgufTensor& t : g->f->tensors) {
+        int ldw;
+        int64_t rows;
+        if (registry_shape(t, &ldw, &rows) && evict_at(ctx, reinterpret_cast<uintptr_t>(base + t.offset)) && n_evicted)
+            ++*n_evicted;
+    }
+    return JAMHIP_OK;
 }
 
 }  // extern "C"
