@@ -15,10 +15,12 @@ The same JSON line carries
   * ``prefill``: the metric's second half, M=512 prefill TOPS of Q4_K 14336x4096 and Q6_K 4096x14336
     (activations 99% N(0,1) + 1% outliers at +-20, F2-quantized in the timed calls) against MI355X's dense
     int8 and f16 MFMA peaks;
+  * ``registry``: model load through the GGUF device weight registry (open + pin of a synthetic
+    gpt-oss-20B-shaped file) in GB/s of jam weights made resident;
   * ``cpu_baseline``: the reference's own libjam (oracle/_ref, built from the reference C sources) on the
     same decode workload on this machine's host cores.
 
-    python bench.py [--gpus 1] [--steps 2048] [--warmup 64] [--no-cpu] [--no-prefill] [--no-moe]
+    python bench.py [--gpus 1] [--steps 2048] [--warmup 64] [--no-cpu] [--no-prefill] [--no-moe] [--no-registry]
     profiling runs: --no-graph (plain stream launches) --calibrate-copy (three 256 MiB device copies first,
     the known-size reference for the FETCH_SIZE/WRITE_SIZE scale factors)
 """
@@ -255,6 +257,53 @@ def moe_leg(hip, torch, stream, steps: int = 10) -> dict:
                     "(5760*2880 + 2880*2880)"}
 
 
+def registry_leg(hip, layers: int = 2) -> dict:
+    """Model load through the GGUF device weight registry: a synthetic GGUF holding `layers` gpt-oss-20B
+    layers' jam weights (attention q/k/v/o in Q8_0, stacked gate/up/down experts 32 x 2880 x 2880 in MXFP4,
+    f32 norms and biases), random bytes, freshly written (so page-cache warm). Timed: jamhip_gguf_open +
+    jamhip_gguf_pin (parse, map, H2D of every jam tensor, repack to the device layout) on the wall clock;
+    twice, the second after jamhip_gguf_evict."""
+    import tempfile
+    from qxotic_amd import gguf as G
+    from qxotic_amd.ggml import BY_NAME
+
+    q8, mx, f32 = BY_NAME["Q8_0"], BY_NAME["MXFP4"], BY_NAME["F32"]
+    D, E, HQ, HKV = 2880, 32, 4096, 512
+    rng = np.random.default_rng(0x6E6E)
+    blob = lambda t, rows, cols: rng.integers(0, 256, rows * t.row_bytes(cols), dtype=np.uint8)
+    tensors = []
+    for l in range(layers):
+        p = f"blk.{l}."
+        tensors += [(p + "attn_norm.weight", f32.ggml, (D,), np.ones(D, np.float32)),
+                    (p + "attn_q.weight", q8.ggml, (D, HQ), blob(q8, HQ, D)),
+                    (p + "attn_k.weight", q8.ggml, (D, HKV), blob(q8, HKV, D)),
+                    (p + "attn_v.weight", q8.ggml, (D, HKV), blob(q8, HKV, D)),
+                    (p + "attn_output.weight", q8.ggml, (HQ, D), blob(q8, D, HQ))]
+        for name in ("ffn_gate_exps", "ffn_up_exps", "ffn_down_exps"):
+            tensors += [(p + name + ".weight", mx.ggml, (D, D, E), blob(mx, E * D, D)),
+                        (p + name + ".bias", f32.ggml, (D, E), np.zeros(D * E, np.float32))]
+    with tempfile.TemporaryDirectory() as tmp:
+        path = Path(tmp) / "model.gguf"
+        G.write(path, tensors, [("general.architecture", "string", "gpt-oss")])
+        del tensors
+        size = path.stat().st_size
+        runs = []
+        for _ in range(2):
+            t0 = time.perf_counter()
+            g = G.GGUF(path)
+            st, cnt, nbytes = g.pin(hip)
+            dt = time.perf_counter() - t0
+            assert st == 0, hip.last_error()
+            runs.append(dt)
+            assert g.evict(hip) == cnt
+            g.close()
+    best = min(runs)
+    return {"file_GB": round(size / 1e9, 3), "pinned_tensors": cnt, "pinned_GB": round(nbytes / 1e9, 3),
+            "s": [round(r, 4) for r in runs], "GBs": round(nbytes / best / 1e9, 2),
+            "note": f"{layers} gpt-oss-20B layers' jam weights (Q8_0 attention, 3 stacked 32-expert MXFP4 "
+                    "tensors per layer), page-cache-warm file; open + pin on the wall clock, best of 2"}
+
+
 def cpu_leg(w: np.ndarray, budget_s: float = 4.0) -> dict | None:
     """The reference's own libjam (oracle/_ref), same workload, 32 rotating host copies (1.06 GB, far
     above any L3), one thread per allotted core."""
@@ -303,6 +352,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-moe", action="store_true")
+    ap.add_argument("--no-registry", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true")
     args = ap.parse_args()
@@ -334,6 +384,10 @@ def main() -> int:
     if not args.no_moe:
         log("bench: moe leg")
         moe = moe_leg(hip, torch, stream)
+    reg = None
+    if not args.no_registry:
+        log("bench: registry leg")
+        reg = registry_leg(hip)
     hip.close()
     cpu = None
     if not args.no_cpu:
@@ -354,6 +408,7 @@ def main() -> int:
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles()},
         "prefill": pre,
         "moe": moe,
+        "registry": reg,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
