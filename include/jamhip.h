@@ -138,6 +138,30 @@ jamhip_status jamhip_moe_combine(jamhip_ctx* ctx, const void* y_dev, int ldy, co
                                  const void* route_prob_dev, const void* route_slot_dev, int seq, int topk,
                                  int n_experts, int dim, void* out_dev, int ldo);
 
+/* ---- Fused epilogues (no counterpart in jam: jinfer runs these as separate passes after MatMul.gemm).
+ * mm_device_ex: jamhip_mm_device with the epilogue applied in the matmul's own final store,
+ *   C[j][i] = [C[j][i] +] (dot(W[i,:], A[j,:]) [+ bias[i]])
+ * bias_dev: f32 [m] or NULL (Ops.addRowBiasInPlace, jinfer/jinfer-kernels/src/main/java/com/qxotic/
+ * jinfer/kernels/Ops.java:375-400, as gpt-oss's expert and attention biases, GptOss.java:301-315);
+ * accumulate = 1 adds the result to C in place (Ops.addInPlace, Ops.java:326-360: the residual add after
+ * attention's output projection and the FFN's down projection); 0 overwrites C. The f32 operations and
+ * their order are those of the separate passes. Same validation and status codes as jamhip_mm_device. */
+jamhip_status jamhip_mm_device_ex(jamhip_ctx* ctx,
+                                  const void* w, int wt, int ldw,
+                                  const void* a_dev, int at, int lda,
+                                  void*       c_dev, int ct, int ldc,
+                                  int m, int n, int k,
+                                  const void* bias_dev, int accumulate);
+
+/* Gated activation in place on gate [rows][ldg] (device f32), up [rows][ldu], `cols` per row:
+ * JAMHIP_ACT_SWIGLU      gate = silu(gate)·up                   (Activations.siluMultiply; Ops.java:578-583)
+ * JAMHIP_ACT_SWIGLU_OAI  gate = quickgelu(min(gate, 7))·(clamp(up, ±7) + 1)   (gpt-oss;
+ *                        Activations.clampedSwiglu, Activations.java:183-187)
+ * in the reference's full-scalar arithmetic. Context stream, not synchronized. */
+enum { JAMHIP_ACT_SWIGLU = 1, JAMHIP_ACT_SWIGLU_OAI = 2 };
+jamhip_status jamhip_glu_device(jamhip_ctx* ctx, int act, void* gate_dev, int ldg, const void* up_dev, int ldu,
+                                int rows, int cols);
+
 /* Use `stream` (a hipStream_t; NULL = the context's own) for subsequent work of this context. */
 jamhip_status jamhip_ctx_set_stream(jamhip_ctx* ctx, void* stream);
 void*         jamhip_ctx_stream(const jamhip_ctx* ctx);

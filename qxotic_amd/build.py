@@ -35,6 +35,7 @@ UNITS = {   # source -> extra flags
     "gemm.hip": [],
     "mma.hip": [],
     "moe.hip": [],
+    "epilogue.hip": [],
     "jamhip.cpp": ["-x", "hip"],
     "gguf.cpp": [],
 }

@@ -48,6 +48,21 @@ __host__ __device__ constexpr int64_t groups_of(int dt, int64_t blocks) {
 // rows held by a device copy of m rows (whole 32-row tiles)
 __host__ __device__ constexpr int64_t tiled_rows(int64_t m) { return (m + ROW_TILE - 1) / ROW_TILE * ROW_TILE; }
 
+// Fused epilogue of a matmul's final store: C = [C_old +] (W·A [+ bias[row]]), the bias add first and the
+// residual add second, the f32 operations jinfer runs after MatMul.gemm (Ops.addRowBiasInPlace, then
+// Ops.addInPlace; jinfer/jinfer-kernels/src/main/java/com/qxotic/jinfer/kernels/Ops.java:326-400).
+// Empty (bias null, accumulate 0) = the plain store.
+struct Epi {
+    const float* bias = nullptr;   // [m], indexed by the output row of the call
+    int accumulate = 0;            // 1: add the value already in C (residual add in place)
+};
+
+__device__ inline float epilogue(const Epi& e, float v, int64_t row, const float* dst) {
+    if (e.bias != nullptr) v += e.bias[row];
+    if (e.accumulate) v = *dst + v;
+    return v;
+}
+
 struct WeightView {
     const uint8_t* qs;   // plane 0 of the device copy
     const uint8_t* sc;   // plane 1 of the device copy

@@ -220,7 +220,7 @@ JAMHIP_DEV void stage_x(GemmSmem<DT, BM, BN>& S, const ActQ& A, int n0, int n, i
 
 template <int DT, int BM, int BN>
 __global__ void __launch_bounds__(256) gemm_kernel(WeightView w, ActQ A, int k, int m, int n, float* __restrict__ c,
-                                                   int ldc) {
+                                                   int ldc, Epi ep) {
     __shared__ GemmSmem<DT, BM, BN> S;
     constexpr int RT = BM / 32, CT = BN / 32;   // 16x16 tiles per wave
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -311,26 +311,30 @@ __global__ void __launch_bounds__(256) gemm_kernel(WeightView w, ActQ A, int k, 
             if (tok < n) {
 #pragma unroll
                 for (int i = 0; i < 4; i++)
-                    if (row + i < m) c[(int64_t) tok * ldc + row + i] = acc[rt][ct][i];
+                    if (row + i < m) {
+                        float* dst = c + (int64_t) tok * ldc + row + i;
+                        *dst = epilogue(ep, acc[rt][ct][i], row + i, dst);
+                    }
             }
         }
 }
 
 template <int DT, int BM, int BN>
-static hipError_t gemm_go(const WeightView& w, const ActQ& A, int k, int m, int n, float* c, int ldc, hipStream_t st) {
+static hipError_t gemm_go(const WeightView& w, const ActQ& A, int k, int m, int n, float* c, int ldc, hipStream_t st,
+                          const Epi& ep) {
     const dim3 grid((unsigned) ((m + BM - 1) / BM), (unsigned) ((n + BN - 1) / BN));
-    gemm_kernel<DT, BM, BN><<<grid, 256, 0, st>>>(w, A, k, m, n, c, ldc);
+    gemm_kernel<DT, BM, BN><<<grid, 256, 0, st>>>(w, A, k, m, n, c, ldc, ep);
     return hipGetLastError();
 }
 
 hipError_t launch_gemm(int dt, const WeightView& w, const ActQ& A, int k, int m, int n, float* c, int ldc,
-                       hipStream_t st) {
+                       hipStream_t st, const Epi& ep) {
     switch (dt) {
-    case Q4_K: return gemm_go<Q4_K, 128, 64>(w, A, k, m, n, c, ldc, st);
-    case Q6_K: return gemm_go<Q6_K, 64, 64>(w, A, k, m, n, c, ldc, st);
-    case Q8_0: return gemm_go<Q8_0, 128, 64>(w, A, k, m, n, c, ldc, st);
-    case Q4_0: return gemm_go<Q4_0, 128, 64>(w, A, k, m, n, c, ldc, st);
-    case MXFP4: return gemm_go<MXFP4, 128, 64>(w, A, k, m, n, c, ldc, st);
+    case Q4_K: return gemm_go<Q4_K, 128, 64>(w, A, k, m, n, c, ldc, st, ep);
+    case Q6_K: return gemm_go<Q6_K, 64, 64>(w, A, k, m, n, c, ldc, st, ep);
+    case Q8_0: return gemm_go<Q8_0, 128, 64>(w, A, k, m, n, c, ldc, st, ep);
+    case Q4_0: return gemm_go<Q4_0, 128, 64>(w, A, k, m, n, c, ldc, st, ep);
+    case MXFP4: return gemm_go<MXFP4, 128, 64>(w, A, k, m, n, c, ldc, st, ep);
     default: return hipErrorNotSupported;
     }
 }

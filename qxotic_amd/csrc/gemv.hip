@@ -4,21 +4,21 @@
 
 namespace jamhip {
 
-extern template hipError_t gemv_dt<Q4_K>(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m, int n, float* c, int ldc, hipStream_t st, float* part);
+extern template hipError_t gemv_dt<Q4_K>(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m, int n, float* c, int ldc, hipStream_t st, float* part, const Epi& ep);
 extern template hipError_t gemv_grouped_dt<Q4_K>(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, const Groups& g, int E, int cap8, float* c, int ldc, hipStream_t st);
-extern template hipError_t rows_float_dt<Q4_K>(const WeightView& w, const float* a, int lda, int k, int r0, int rows, int n, float* c, int ldc, hipStream_t st);
-extern template hipError_t gemv_dt<Q6_K>(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m, int n, float* c, int ldc, hipStream_t st, float* part);
+extern template hipError_t rows_float_dt<Q4_K>(const WeightView& w, const float* a, int lda, int k, int r0, int rows, int n, float* c, int ldc, hipStream_t st, const Epi& ep);
+extern template hipError_t gemv_dt<Q6_K>(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m, int n, float* c, int ldc, hipStream_t st, float* part, const Epi& ep);
 extern template hipError_t gemv_grouped_dt<Q6_K>(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, const Groups& g, int E, int cap8, float* c, int ldc, hipStream_t st);
-extern template hipError_t rows_float_dt<Q6_K>(const WeightView& w, const float* a, int lda, int k, int r0, int rows, int n, float* c, int ldc, hipStream_t st);
-extern template hipError_t gemv_dt<Q8_0>(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m, int n, float* c, int ldc, hipStream_t st, float* part);
+extern template hipError_t rows_float_dt<Q6_K>(const WeightView& w, const float* a, int lda, int k, int r0, int rows, int n, float* c, int ldc, hipStream_t st, const Epi& ep);
+extern template hipError_t gemv_dt<Q8_0>(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m, int n, float* c, int ldc, hipStream_t st, float* part, const Epi& ep);
 extern template hipError_t gemv_grouped_dt<Q8_0>(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, const Groups& g, int E, int cap8, float* c, int ldc, hipStream_t st);
-extern template hipError_t rows_float_dt<Q8_0>(const WeightView& w, const float* a, int lda, int k, int r0, int rows, int n, float* c, int ldc, hipStream_t st);
-extern template hipError_t gemv_dt<Q4_0>(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m, int n, float* c, int ldc, hipStream_t st, float* part);
+extern template hipError_t rows_float_dt<Q8_0>(const WeightView& w, const float* a, int lda, int k, int r0, int rows, int n, float* c, int ldc, hipStream_t st, const Epi& ep);
+extern template hipError_t gemv_dt<Q4_0>(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m, int n, float* c, int ldc, hipStream_t st, float* part, const Epi& ep);
 extern template hipError_t gemv_grouped_dt<Q4_0>(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, const Groups& g, int E, int cap8, float* c, int ldc, hipStream_t st);
-extern template hipError_t rows_float_dt<Q4_0>(const WeightView& w, const float* a, int lda, int k, int r0, int rows, int n, float* c, int ldc, hipStream_t st);
-extern template hipError_t gemv_dt<MXFP4>(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m, int n, float* c, int ldc, hipStream_t st, float* part);
+extern template hipError_t rows_float_dt<Q4_0>(const WeightView& w, const float* a, int lda, int k, int r0, int rows, int n, float* c, int ldc, hipStream_t st, const Epi& ep);
+extern template hipError_t gemv_dt<MXFP4>(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m, int n, float* c, int ldc, hipStream_t st, float* part, const Epi& ep);
 extern template hipError_t gemv_grouped_dt<MXFP4>(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, const Groups& g, int E, int cap8, float* c, int ldc, hipStream_t st);
-extern template hipError_t rows_float_dt<MXFP4>(const WeightView& w, const float* a, int lda, int k, int r0, int rows, int n, float* c, int ldc, hipStream_t st);
+extern template hipError_t rows_float_dt<MXFP4>(const WeightView& w, const float* a, int lda, int k, int r0, int rows, int n, float* c, int ldc, hipStream_t st, const Epi& ep);
 
 hipError_t launch_gemv_grouped(int dt, int flavour, const WeightView& w, const ActQ& A, const float* a, int lda,
                                int k, const Groups& g, int E, int cap8, float* c, int ldc, hipStream_t st) {
@@ -48,26 +48,26 @@ size_t gemv_split_floats(int k, int m, int n) {
 }
 
 hipError_t launch_gemv(int dt, int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m,
-                       int n, float* c, int ldc, hipStream_t st, float* part) {
+                       int n, float* c, int ldc, hipStream_t st, float* part, const Epi& ep) {
     switch (dt) {
-    case Q4_K: return gemv_dt<Q4_K>(flavour, w, A, a, lda, k, m, n, c, ldc, st, part);
-    case Q6_K: return gemv_dt<Q6_K>(flavour, w, A, a, lda, k, m, n, c, ldc, st, part);
-    case Q8_0: return gemv_dt<Q8_0>(flavour, w, A, a, lda, k, m, n, c, ldc, st, part);
-    case Q4_0: return gemv_dt<Q4_0>(flavour, w, A, a, lda, k, m, n, c, ldc, st, part);
-    case MXFP4: return gemv_dt<MXFP4>(flavour, w, A, a, lda, k, m, n, c, ldc, st, part);
+    case Q4_K: return gemv_dt<Q4_K>(flavour, w, A, a, lda, k, m, n, c, ldc, st, part, ep);
+    case Q6_K: return gemv_dt<Q6_K>(flavour, w, A, a, lda, k, m, n, c, ldc, st, part, ep);
+    case Q8_0: return gemv_dt<Q8_0>(flavour, w, A, a, lda, k, m, n, c, ldc, st, part, ep);
+    case Q4_0: return gemv_dt<Q4_0>(flavour, w, A, a, lda, k, m, n, c, ldc, st, part, ep);
+    case MXFP4: return gemv_dt<MXFP4>(flavour, w, A, a, lda, k, m, n, c, ldc, st, part, ep);
     default: return hipErrorInvalidValue;
     }
 }
 
 hipError_t launch_rows_float(int dt, const WeightView& w, const float* a, int lda, int k, int r0, int rows, int n,
-                             float* c, int ldc, hipStream_t st) {
+                             float* c, int ldc, hipStream_t st, const Epi& ep) {
     if (rows <= 0) return hipSuccess;
     switch (dt) {
-    case Q4_K: return rows_float_dt<Q4_K>(w, a, lda, k, r0, rows, n, c, ldc, st);
-    case Q6_K: return rows_float_dt<Q6_K>(w, a, lda, k, r0, rows, n, c, ldc, st);
-    case Q8_0: return rows_float_dt<Q8_0>(w, a, lda, k, r0, rows, n, c, ldc, st);
-    case Q4_0: return rows_float_dt<Q4_0>(w, a, lda, k, r0, rows, n, c, ldc, st);
-    case MXFP4: return rows_float_dt<MXFP4>(w, a, lda, k, r0, rows, n, c, ldc, st);
+    case Q4_K: return rows_float_dt<Q4_K>(w, a, lda, k, r0, rows, n, c, ldc, st, ep);
+    case Q6_K: return rows_float_dt<Q6_K>(w, a, lda, k, r0, rows, n, c, ldc, st, ep);
+    case Q8_0: return rows_float_dt<Q8_0>(w, a, lda, k, r0, rows, n, c, ldc, st, ep);
+    case Q4_0: return rows_float_dt<Q4_0>(w, a, lda, k, r0, rows, n, c, ldc, st, ep);
+    case MXFP4: return rows_float_dt<MXFP4>(w, a, lda, k, r0, rows, n, c, ldc, st, ep);
     default: return hipErrorInvalidValue;
     }
 }

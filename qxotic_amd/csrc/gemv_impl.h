@@ -414,7 +414,7 @@ JAMHIP_DEV void stage_store(const FPre<SP>& pre, int k, int Gk, int8_t* lq, floa
 template <int DT, int FL, int NT, int HP, int RB, int ITEMS, bool GR, bool SK, int NWV>
 __global__ void __launch_bounds__(64 * NWV) mv_kernel(WeightView w, ActQ A, const float* __restrict__ a,
                                                           int lda, int k, int m, int n, float* __restrict__ c,
-                                                          int ldc, Groups gp, int ks, int64_t cz) {
+                                                          int ldc, Groups gp, int ks, int64_t cz, Epi ep) {
     constexpr int BPG = blocks_per_group(DT), GS = 64 / RB;
     // SK (split K): workgroup column blockIdx.z takes elements [k0, k0 + ks) (ks a multiple of 256; the last
     // slice may be shorter) and writes its partial result at c + blockIdx.z·cz; J, and so the block shape,
@@ -573,7 +573,10 @@ __global__ void __launch_bounds__(64 * NWV) mv_kernel(WeightView w, ActQ A, cons
 #pragma unroll
             for (int s2 = 0; s2 < GS; s2++) v += part[(((q * J + j) * 64) + s2 * RB + r) * NT + t];
         const int64_t row = RB * (q0 + q) + r;
-        if (row < m && t < ntv) c[(int64_t) (t0 + t) * ldc + row] = v;
+        if (row < m && t < ntv) {
+            float* dst = c + (int64_t) (t0 + t) * ldc + row;
+            *dst = SK ? v : epilogue(ep, v, row, dst);
+        }
     }
 }
 
@@ -620,7 +623,7 @@ JAMHIP_DEV float deq(const WeightView& w, int64_t row, int elem) {
 
 template <int DT>
 __global__ void __launch_bounds__(64) rows_float_kernel(WeightView w, const float* __restrict__ a, int lda, int k,
-                                                        int r0, int n, float* __restrict__ c, int ldc) {
+                                                        int r0, int n, float* __restrict__ c, int ldc, Epi ep) {
     const int64_t row = r0 + blockIdx.x;
     const int t0 = blockIdx.y * 8, nt = n - t0 < 8 ? n - t0 : 8;
     const int lane = threadIdx.x;
@@ -638,7 +641,10 @@ __global__ void __launch_bounds__(64) rows_float_kernel(WeightView w, const floa
 #pragma unroll
     for (int t = 0; t < 8; t++) {
         const float v = wave_sum(acc[t]);
-        if (lane == 0 && t < nt) c[(int64_t) (t0 + t) * ldc + row] = v;
+        if (lane == 0 && t < nt) {
+            float* dst = c + (int64_t) (t0 + t) * ldc + row;
+            *dst = epilogue(ep, v, row, dst);
+        }
     }
 }
 
@@ -691,7 +697,7 @@ inline int gemv_slice(int k, int n) { return n >= 2 && k >= 2 * GEMV_SLICE ? GEM
 // workgroup.
 template <int DT, int FL, int NT, int HP, int RB, int ITEMS, int NWV = MV_WAVES>
 static void launch_shape(int k, int ks, int64_t cz, int m, int n, const WeightView& w, const ActQ& A, const float* a,
-                         int lda, float* c, int ldc, hipStream_t st) {
+                         int lda, float* c, int ldc, hipStream_t st, const Epi& ep) {
     constexpr int GS = 64 / RB;
     const int Gk = (ks / 32 + 7) / 8, J = (Gk + GS - 1) / GS;
     const int QB = NWV * ITEMS / J;
@@ -702,13 +708,13 @@ static void launch_shape(int k, int ks, int64_t cz, int m, int n, const WeightVi
         if (ks < k) {
             lds_allow((const void*) mv_kernel<DT, FL, NT, HP, RB, ITEMS, false, true, NWV>, lds);
             mv_kernel<DT, FL, NT, HP, RB, ITEMS, false, true, NWV><<<grid, 64 * NWV, lds, st>>>(
-                w, A, a, lda, k, m, n, c, ldc, Groups{}, ks, cz);
+                w, A, a, lda, k, m, n, c, ldc, Groups{}, ks, cz, Epi{});
             return;
         }
     }
     lds_allow((const void*) mv_kernel<DT, FL, NT, HP, RB, ITEMS, false, false, NWV>, lds);
     mv_kernel<DT, FL, NT, HP, RB, ITEMS, false, false, NWV><<<grid, 64 * NWV, lds, st>>>(w, A, a, lda, k, m, n, c, ldc,
-                                                                                        Groups{}, k, 0);
+                                                                                        Groups{}, k, 0, ep);
 }
 
 template <int DT, int FL, int NT, int HP, int RB, int ITEMS>
@@ -722,7 +728,7 @@ static void launch_shape_grouped(int k, const Groups& g, int ny, const WeightVie
     const size_t lds = (size_t) MV_WAVES * ITEMS * 64 * NT * sizeof(float) + (HP > 0 ? 32 + fuse_lds(NT, k) : 0);
     lds_allow((const void*) mv_kernel<DT, FL, NT, HP, RB, ITEMS, true, false, MV_WAVES>, lds);
     mv_kernel<DT, FL, NT, HP, RB, ITEMS, true, false, MV_WAVES><<<grid, 64 * MV_WAVES, lds, st>>>(w, A, a, lda, k, g.gm,
-                                                                                                 0, c, ldc, g, k, 0);
+                                                                                                 0, c, ldc, g, k, 0, Epi{});
 }
 
 template <int DT, int FL, int NT, int HP>
@@ -750,17 +756,17 @@ hipError_t gemv_grouped_dt(int flavour, const WeightView& w, const ActQ& A, cons
 
 template <int DT, int FL, int NT, int HP>
 static hipError_t go_hp(int k, int ks, int64_t cz, int m, int n, const WeightView& w, const ActQ& A, const float* a,
-                        int lda, float* c, int ldc, hipStream_t st) {
+                        int lda, float* c, int ldc, hipStream_t st, const Epi& ep) {
     int items;
     if (!mv_items(ks, &items)) return hipErrorNotSupported;
     if constexpr (FL == 2 && HP > 0) {   // staged activations: one item per wave (slices <= 16384)
-        if (items != 1) return go_hp<DT, FL, NT, 0>(k, ks, cz, m, n, w, A, a, lda, c, ldc, st);
-        launch_shape<DT, FL, NT, HP, MV_RB, 1>(k, ks, cz, m, n, w, A, a, lda, c, ldc, st);
+        if (items != 1) return go_hp<DT, FL, NT, 0>(k, ks, cz, m, n, w, A, a, lda, c, ldc, st, ep);
+        launch_shape<DT, FL, NT, HP, MV_RB, 1>(k, ks, cz, m, n, w, A, a, lda, c, ldc, st, ep);
         return hipGetLastError();
     }
-    if (items == 1) launch_shape<DT, FL, NT, HP, MV_RB, 1>(k, ks, cz, m, n, w, A, a, lda, c, ldc, st);
-    else if (items == 2) launch_shape<DT, FL, NT, HP, MV_RB, 2>(k, ks, cz, m, n, w, A, a, lda, c, ldc, st);
-    else launch_shape<DT, FL, NT, HP, MV_RB, 4>(k, ks, cz, m, n, w, A, a, lda, c, ldc, st);
+    if (items == 1) launch_shape<DT, FL, NT, HP, MV_RB, 1>(k, ks, cz, m, n, w, A, a, lda, c, ldc, st, ep);
+    else if (items == 2) launch_shape<DT, FL, NT, HP, MV_RB, 2>(k, ks, cz, m, n, w, A, a, lda, c, ldc, st, ep);
+    else launch_shape<DT, FL, NT, HP, MV_RB, 4>(k, ks, cz, m, n, w, A, a, lda, c, ldc, st, ep);
     return hipGetLastError();
 }
 
@@ -782,80 +788,81 @@ static int one_token_waves(int k, int m) {
 
 template <int DT, int NWV>
 static hipError_t go_one(const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m, float* c, int ldc,
-                         hipStream_t st) {
+                         hipStream_t st, const Epi& ep) {
     // at most 2 half-blocks per thread in the fused prologue (J <= NWV items of 8 groups, 16 half-blocks each)
     const int Gk = (k / 32 + 7) / 8, hp = a != nullptr ? (16 * Gk + 64 * NWV - 1) / (64 * NWV) : 0;
-    if (hp == 0) launch_shape<DT, 1, 1, 0, MV_RB, 1, NWV>(k, k, 0, m, 1, w, A, a, lda, c, ldc, st);
-    else if (hp == 1) launch_shape<DT, 1, 1, 1, MV_RB, 1, NWV>(k, k, 0, m, 1, w, A, a, lda, c, ldc, st);
-    else launch_shape<DT, 1, 1, 2, MV_RB, 1, NWV>(k, k, 0, m, 1, w, A, a, lda, c, ldc, st);
+    if (hp == 0) launch_shape<DT, 1, 1, 0, MV_RB, 1, NWV>(k, k, 0, m, 1, w, A, a, lda, c, ldc, st, ep);
+    else if (hp == 1) launch_shape<DT, 1, 1, 1, MV_RB, 1, NWV>(k, k, 0, m, 1, w, A, a, lda, c, ldc, st, ep);
+    else launch_shape<DT, 1, 1, 2, MV_RB, 1, NWV>(k, k, 0, m, 1, w, A, a, lda, c, ldc, st, ep);
     return hipGetLastError();
 }
 
 template <int DT, int FL, int NT>
 static hipError_t go(const WeightView& w, const ActQ& A, const float* a, int lda, int k, int ks, int64_t cz, int m,
-                     int n, float* c, int ldc, hipStream_t st) {
+                     int n, float* c, int ldc, hipStream_t st, const Epi& ep) {
     if constexpr (FL == 1 && NT == 1) {
         if (ks == k) {
             const int nw = one_token_waves(k, m);
-            if (nw == 4) return go_one<DT, 4>(w, A, a, lda, k, m, c, ldc, st);
-            if (nw == 5) return go_one<DT, 5>(w, A, a, lda, k, m, c, ldc, st);
-            if (nw == 6) return go_one<DT, 6>(w, A, a, lda, k, m, c, ldc, st);
-            if (nw == 7) return go_one<DT, 7>(w, A, a, lda, k, m, c, ldc, st);
+            if (nw == 4) return go_one<DT, 4>(w, A, a, lda, k, m, c, ldc, st, ep);
+            if (nw == 5) return go_one<DT, 5>(w, A, a, lda, k, m, c, ldc, st, ep);
+            if (nw == 6) return go_one<DT, 6>(w, A, a, lda, k, m, c, ldc, st, ep);
+            if (nw == 7) return go_one<DT, 7>(w, A, a, lda, k, m, c, ldc, st, ep);
         }
     }
     if constexpr (FL == 2) {   // stage the tile's activations in LDS when they fit
         const int hp = (NT * ((ks / 32 + 7) / 8) * 16 + 64 * MV_WAVES - 1) / (64 * MV_WAVES);
         if (fuse_lds(NT, ks) <= (size_t) kFuseMaxBytes && hp <= 8) {
-            if (hp <= 2) return go_hp<DT, FL, NT, 2>(k, ks, cz, m, n, w, A, a, lda, c, ldc, st);
-            if (hp <= 4) return go_hp<DT, FL, NT, 4>(k, ks, cz, m, n, w, A, a, lda, c, ldc, st);
-            return go_hp<DT, FL, NT, 8>(k, ks, cz, m, n, w, A, a, lda, c, ldc, st);
+            if (hp <= 2) return go_hp<DT, FL, NT, 2>(k, ks, cz, m, n, w, A, a, lda, c, ldc, st, ep);
+            if (hp <= 4) return go_hp<DT, FL, NT, 4>(k, ks, cz, m, n, w, A, a, lda, c, ldc, st, ep);
+            return go_hp<DT, FL, NT, 8>(k, ks, cz, m, n, w, A, a, lda, c, ldc, st, ep);
         }
     }
     if constexpr (FL == 1) {
         if (a != nullptr) {
             const int hp = fuse_hp(NT, ks);
-            if (hp <= 1) return go_hp<DT, FL, NT, 1>(k, ks, cz, m, n, w, A, a, lda, c, ldc, st);
-            if (hp == 2) return go_hp<DT, FL, NT, 2>(k, ks, cz, m, n, w, A, a, lda, c, ldc, st);
-            return go_hp<DT, FL, NT, 4>(k, ks, cz, m, n, w, A, a, lda, c, ldc, st);
+            if (hp <= 1) return go_hp<DT, FL, NT, 1>(k, ks, cz, m, n, w, A, a, lda, c, ldc, st, ep);
+            if (hp == 2) return go_hp<DT, FL, NT, 2>(k, ks, cz, m, n, w, A, a, lda, c, ldc, st, ep);
+            return go_hp<DT, FL, NT, 4>(k, ks, cz, m, n, w, A, a, lda, c, ldc, st, ep);
         }
     }
-    return go_hp<DT, FL, NT, 0>(k, ks, cz, m, n, w, A, a, lda, c, ldc, st);
+    return go_hp<DT, FL, NT, 0>(k, ks, cz, m, n, w, A, a, lda, c, ldc, st, ep);
 }
 
 // Split calls (gemv_slice(k, n) < k) write each slice's partial result to part ([slices][n][m]) and sum them
 // into c in slice order.
 template <int DT>
 hipError_t gemv_dt(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m,
-                          int n, float* c, int ldc, hipStream_t st, float* part) {
+                          int n, float* c, int ldc, hipStream_t st, float* part, const Epi& ep) {
     const int ks = gemv_slice(k, n), ns = (k + ks - 1) / ks;
     if (ns > 1 && part == nullptr) return hipErrorInvalidValue;
     const int64_t cz = ns > 1 ? (int64_t) n * m : 0;
     float* out = ns > 1 ? part : c;
     const int ldo = ns > 1 ? m : ldc;
+    const Epi eo = ns > 1 ? Epi{} : ep;   // split: the reduce applies the epilogue
     hipError_t e;
     if (flavour == 2) {
-        e = go<DT, 2, 8>(w, A, nullptr, 0, k, ks, cz, m, n, out, ldo, st);
+        e = go<DT, 2, 8>(w, A, nullptr, 0, k, ks, cz, m, n, out, ldo, st, eo);
     } else {
         switch (n) {
-        case 1: e = go<DT, 1, 1>(w, A, a, lda, k, ks, cz, m, n, out, ldo, st); break;
-        case 2: e = go<DT, 1, 2>(w, A, a, lda, k, ks, cz, m, n, out, ldo, st); break;
-        case 3: e = go<DT, 1, 3>(w, A, a, lda, k, ks, cz, m, n, out, ldo, st); break;
-        case 4: e = go<DT, 1, 4>(w, A, a, lda, k, ks, cz, m, n, out, ldo, st); break;
-        case 5: e = go<DT, 1, 5>(w, A, a, lda, k, ks, cz, m, n, out, ldo, st); break;
-        case 6: e = go<DT, 1, 6>(w, A, a, lda, k, ks, cz, m, n, out, ldo, st); break;
-        case 7: e = go<DT, 1, 7>(w, A, a, lda, k, ks, cz, m, n, out, ldo, st); break;
+        case 1: e = go<DT, 1, 1>(w, A, a, lda, k, ks, cz, m, n, out, ldo, st, eo); break;
+        case 2: e = go<DT, 1, 2>(w, A, a, lda, k, ks, cz, m, n, out, ldo, st, eo); break;
+        case 3: e = go<DT, 1, 3>(w, A, a, lda, k, ks, cz, m, n, out, ldo, st, eo); break;
+        case 4: e = go<DT, 1, 4>(w, A, a, lda, k, ks, cz, m, n, out, ldo, st, eo); break;
+        case 5: e = go<DT, 1, 5>(w, A, a, lda, k, ks, cz, m, n, out, ldo, st, eo); break;
+        case 6: e = go<DT, 1, 6>(w, A, a, lda, k, ks, cz, m, n, out, ldo, st, eo); break;
+        case 7: e = go<DT, 1, 7>(w, A, a, lda, k, ks, cz, m, n, out, ldo, st, eo); break;
         default: return hipErrorInvalidValue;
         }
     }
     if (e != hipSuccess || ns == 1) return e;
-    return launch_split_reduce(part, ns, cz, m, n, c, ldc, st);
+    return launch_split_reduce(part, ns, cz, m, n, c, ldc, st, ep);
 }
 
 template <int DT>
 hipError_t rows_float_dt(const WeightView& w, const float* a, int lda, int k, int r0, int rows, int n, float* c, int ldc,
-                         hipStream_t st) {
+                         hipStream_t st, const Epi& ep) {
     const dim3 grid((unsigned) rows, (unsigned) ((n + 7) / 8));
-    rows_float_kernel<DT><<<grid, 64, 0, st>>>(w, a, lda, k, r0, n, c, ldc);
+    rows_float_kernel<DT><<<grid, 64, 0, st>>>(w, a, lda, k, r0, n, c, ldc, ep);
     return hipGetLastError();
 }
 

@@ -206,7 +206,7 @@ static int gemm_min_n(int dt, int k) {
 // with k < 8192 are one fused launch and touch no scratch (safe under stream capture once W is pinned);
 // from k = 8192 the decode kernels split K and sum the slices from the context's split buffer.
 jamhip_status compute(jamhip_ctx* ctx, int dt, const WeightView& wv, const float* a, int lda, float* c, int ldc,
-                      int m, int n, int k) {
+                      int m, int n, int k, const Epi& ep = Epi{}) {
     hipError_t e;
     float* gpart = nullptr;   // the decode kernels' K-split partials
     auto decode_part = [&](int rows) -> hipError_t {
@@ -218,7 +218,7 @@ jamhip_status compute(jamhip_ctx* ctx, int dt, const WeightView& wv, const float
     };
     if (gemv_fusable(n, k, a, lda)) {
         if ((e = decode_part(m)) != hipSuccess) return hip_fail(ctx, e, "gemv split scratch alloc");
-        if ((e = launch_gemv(dt, 1, wv, ActQ{}, a, lda, k, m, n, c, ldc, ctx->stream, gpart)) != hipSuccess)
+        if ((e = launch_gemv(dt, 1, wv, ActQ{}, a, lda, k, m, n, c, ldc, ctx->stream, gpart, ep)) != hipSuccess)
             return hip_fail(ctx, e, "gemv launch");
         return JAMHIP_OK;
     }
@@ -237,9 +237,9 @@ jamhip_status compute(jamhip_ctx* ctx, int dt, const WeightView& wv, const float
                 return hip_fail(ctx, e, "gemm split scratch alloc");
             part = (float*) ctx->part.p;
         }
-        if ((e = launch_gemm_mma(dt, wv, G, k, m16, n, c, ldc, ctx->stream, part)) != hipSuccess)
+        if ((e = launch_gemm_mma(dt, wv, G, k, m16, n, c, ldc, ctx->stream, part, ep)) != hipSuccess)
             return hip_fail(ctx, e, "gemm launch");
-        if ((e = launch_rows_float(dt, wv, a, lda, k, m16, m - m16, n, c, ldc, ctx->stream)) != hipSuccess)
+        if ((e = launch_rows_float(dt, wv, a, lda, k, m16, m - m16, n, c, ldc, ctx->stream, ep)) != hipSuccess)
             return hip_fail(ctx, e, "tail rows launch");
         return JAMHIP_OK;
     }
@@ -257,19 +257,19 @@ jamhip_status compute(jamhip_ctx* ctx, int dt, const WeightView& wv, const float
         if ((e = launch_quant_f1(a, lda, n, k, q, d, s, s16, ctx->stream)) != hipSuccess)
             return hip_fail(ctx, e, "quant_f1 launch");
         if ((e = decode_part(m)) != hipSuccess) return hip_fail(ctx, e, "gemv split scratch alloc");
-        if ((e = launch_gemv(dt, 1, wv, A, nullptr, 0, k, m, n, c, ldc, ctx->stream, gpart)) != hipSuccess)
+        if ((e = launch_gemv(dt, 1, wv, A, nullptr, 0, k, m, n, c, ldc, ctx->stream, gpart, ep)) != hipSuccess)
             return hip_fail(ctx, e, "gemv launch");
         return JAMHIP_OK;
     }
     if (m16 > 0) {
         if ((e = launch_quant_f2(a, lda, n, k, q, d, s, ctx->stream)) != hipSuccess)
             return hip_fail(ctx, e, "quant_f2 launch");
-        e = n >= gemm_min_n(dt, k) ? launch_gemm(dt, wv, A, k, m16, n, c, ldc, ctx->stream) : hipErrorNotSupported;
+        e = n >= gemm_min_n(dt, k) ? launch_gemm(dt, wv, A, k, m16, n, c, ldc, ctx->stream, ep) : hipErrorNotSupported;
         if (e == hipErrorNotSupported && (e = decode_part(m16)) == hipSuccess)
-            e = launch_gemv(dt, 2, wv, A, nullptr, 0, k, m16, n, c, ldc, ctx->stream, gpart);
+            e = launch_gemv(dt, 2, wv, A, nullptr, 0, k, m16, n, c, ldc, ctx->stream, gpart, ep);
         if (e != hipSuccess) return hip_fail(ctx, e, "matmul launch");
     }
-    if ((e = launch_rows_float(dt, wv, a, lda, k, m16, m - m16, n, c, ldc, ctx->stream)) != hipSuccess)
+    if ((e = launch_rows_float(dt, wv, a, lda, k, m16, m - m16, n, c, ldc, ctx->stream, ep)) != hipSuccess)
         return hip_fail(ctx, e, "tail rows launch");
     return JAMHIP_OK;
 }
@@ -422,6 +422,37 @@ jamhip_status jamhip_mm_device(jamhip_ctx* ctx, const void* w, int wt, int ldw, 
     WeightView wv;
     if ((st = resolve_w(ctx, w, wt, ldw, m, k, &wv)) != JAMHIP_OK) return st;
     return compute(ctx, wt, wv, (const float*) a_dev, lda, (float*) c_dev, ldc, m, n, k);
+}
+
+jamhip_status jamhip_mm_device_ex(jamhip_ctx* ctx, const void* w, int wt, int ldw, const void* a_dev, int at, int lda,
+                                  void* c_dev, int ct, int ldc, int m, int n, int k, const void* bias_dev,
+                                  int accumulate) {
+    jamhip_status st = validate(ctx, w, wt, ldw, a_dev, at, lda, c_dev, ct, ldc, m, n, k);
+    if (st != JAMHIP_OK) return st;
+    if (accumulate != 0 && accumulate != 1) return fail(ctx, JAMHIP_EINVAL, "accumulate must be 0 or 1");
+    Busy guard(ctx);
+    if (!guard.ok) return fail(ctx, JAMHIP_EBUSY, "context busy");
+    (void) hipSetDevice(ctx->device);
+    WeightView wv;
+    if ((st = resolve_w(ctx, w, wt, ldw, m, k, &wv)) != JAMHIP_OK) return st;
+    Epi ep;
+    ep.bias = static_cast<const float*>(bias_dev);
+    ep.accumulate = accumulate;
+    return compute(ctx, wt, wv, (const float*) a_dev, lda, (float*) c_dev, ldc, m, n, k, ep);
+}
+
+jamhip_status jamhip_glu_device(jamhip_ctx* ctx, int act, void* gate_dev, int ldg, const void* up_dev, int ldu,
+                                int rows, int cols) {
+    if (!ctx) return JAMHIP_EINVAL;
+    if (!gate_dev || !up_dev) return fail(ctx, JAMHIP_EINVAL, "glu: null operand");
+    if (rows < 0 || cols < 0 || ldg < cols || ldu < cols) return fail(ctx, JAMHIP_EINVAL, "glu: bad extents");
+    if (act != JAMHIP_ACT_SWIGLU && act != JAMHIP_ACT_SWIGLU_OAI)
+        return fail(ctx, JAMHIP_EUNSUPPORTED, "glu: unknown activation");
+    Busy guard(ctx);
+    if (!guard.ok) return fail(ctx, JAMHIP_EBUSY, "context busy");
+    (void) hipSetDevice(ctx->device);
+    const hipError_t e = launch_glu(act, (float*) gate_dev, ldg, (const float*) up_dev, ldu, rows, cols, ctx->stream);
+    return e == hipSuccess ? JAMHIP_OK : hip_fail(ctx, e, "glu launch");
 }
 
 jamhip_status jamhip_weight_pin(jamhip_ctx* ctx, const void* w, int wt, int ldw, int m) {

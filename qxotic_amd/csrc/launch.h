@@ -38,10 +38,10 @@ struct Groups {
 bool gemv_fusable(int n, int k, const float* a, int lda);   // a, lda: the f32 activations (16-byte aligned rows)
 size_t gemv_split_floats(int k, int m, int n);
 hipError_t launch_gemv(int dt, int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m,
-                       int n, float* c, int ldc, hipStream_t st, float* part = nullptr);
+                       int n, float* c, int ldc, hipStream_t st, float* part = nullptr, const Epi& ep = Epi{});
 // c[t][row] = Σ_s part[s·slice + t·m + row] for s = 0..ns-1 in order (rows < m, tokens < n)
 hipError_t launch_split_reduce(const float* part, int ns, int64_t slice, int m, int n, float* c, int ldc,
-                               hipStream_t st);
+                               hipStream_t st, const Epi& ep = Epi{});
 
 // Grouped forms (one launch for all experts). flavour 1: every expert with 1..7 rows, F1, the kernel
 // quantizing its expert's rows itself when `a` is non-null (then gemv_grouped_fusable(k, a, lda) must hold),
@@ -54,11 +54,11 @@ hipError_t launch_gemv_grouped(int dt, int flavour, const WeightView& w, const A
 // Rows [r0, r0 + rows) of an n >= 8 call as jam's bands compute their <16-row tail: an f32 dot of the
 // dequantized weight row with the f32 activations a [n][lda].
 hipError_t launch_rows_float(int dt, const WeightView& w, const float* a, int lda, int k, int r0, int rows, int n,
-                             float* c, int ldc, hipStream_t st);
+                             float* c, int ldc, hipStream_t st, const Epi& ep = Epi{});
 
 // int8-MFMA prefill GEMM (F2 activations), n >= 1; returns hipErrorNotSupported for dtypes it lacks.
 hipError_t launch_gemm(int dt, const WeightView& w, const ActQ& A, int k, int m, int n, float* c, int ldc,
-                       hipStream_t st);
+                       hipStream_t st, const Epi& ep = Epi{});
 
 // Activations of the matrix-core GEMM, written by launch_gemm_prep: jam's F2 quantization of n tokens
 // (bit-exact codes and scales) laid out for the MFMA operand loads. Tokens are padded to NP (a multiple
@@ -87,10 +87,13 @@ hipError_t launch_gemm_prep(int dt, const float* a, int lda, int n, int k, void*
 // summed in a fixed order; part == nullptr: no split).
 size_t gemm_mma_split_floats(int dt, int k, int m, int n);
 hipError_t launch_gemm_mma(int dt, const WeightView& w, const GemmAct& A, int k, int m, int n, float* c, int ldc,
-                           hipStream_t st, float* part = nullptr);
+                           hipStream_t st, float* part = nullptr, const Epi& ep = Epi{});
 hipError_t launch_gemm_mma_grouped(int dt, const WeightView& w, const GemmAct& A, int k, const Groups& g, int cap64,
                                    float* c, int ldc, hipStream_t st);
 size_t gemm_act_bytes_np(int dt, int NP, int k);
+
+// In place on gate [rows][ldg]: act 1 SwiGLU silu(gate)·up, act 2 gpt-oss clamped SwiGLU (epilogue.hip).
+hipError_t launch_glu(int act, float* gate, int ldg, const float* up, int ldu, int rows, int cols, hipStream_t st);
 hipError_t launch_gemm_prep_grouped(int dt, const float* a, int lda, int k, const Groups& g, int cap64,
                                     void* scratch, GemmAct* out, hipStream_t st);
 

@@ -128,7 +128,7 @@ template <int DT, int RT, int CT>
 __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, GemmAct A, int m, int n,
                                                                  float* __restrict__ c, int ldc, int nrb, int ncb,
                                                                  int64_t tiles, Groups gp, int sb_per,
-                                                                 int64_t c_slice) {
+                                                                 int64_t c_slice, Epi ep) {
     using S = Stage<DT, RT, CT>;
     constexpr int TW = S::TW, BN = S::BN, NCS = S::NCS;
     extern __shared__ __align__(1024) unsigned char smem[];
@@ -708,7 +708,10 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
 #pragma unroll
             for (int e = 0; e < 16; e++) {
                 const int64_t row = rowb + 8 * (e >> 2) + (e & 3);
-                if (row < m) ct[row] = acc[i][j][e] * sc;
+                if (row < m) {
+                    const float v = acc[i][j][e] * sc;
+                    ct[row] = sb_per > 0 ? v : epilogue(ep, v, row, ct + row);   // split: the reduce applies it
+                }
             }
         }
     }
@@ -716,18 +719,19 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
 
 // Deterministic sum of the split-K partials: c[t][row] = Σ_s part[s][t][row] in slice order.
 __global__ void __launch_bounds__(256) split_reduce_kernel(const float* __restrict__ part, int ns, int64_t slice,
-                                                          int m, float* __restrict__ c, int ldc) {
+                                                          int m, float* __restrict__ c, int ldc, Epi ep) {
     const int row = blockIdx.x * 256 + threadIdx.x, t = blockIdx.y;
     if (row >= m) return;
     const float* p = part + (int64_t) t * m + row;
     float v = p[0];
     for (int s = 1; s < ns; s++) v += p[(int64_t) s * slice];
-    c[(int64_t) t * ldc + row] = v;
+    float* dst = c + (int64_t) t * ldc + row;
+    *dst = epilogue(ep, v, row, dst);
 }
 
 hipError_t launch_split_reduce(const float* part, int ns, int64_t slice, int m, int n, float* c, int ldc,
-                               hipStream_t st) {
-    split_reduce_kernel<<<dim3((m + 255) / 256, n), 256, 0, st>>>(part, ns, slice, m, c, ldc);
+                               hipStream_t st, const Epi& ep) {
+    split_reduce_kernel<<<dim3((m + 255) / 256, n), 256, 0, st>>>(part, ns, slice, m, c, ldc, ep);
     return hipGetLastError();
 }
 
@@ -741,7 +745,7 @@ static void split_plan(int total, int nsb, int* ns, int* sb_per) {
 
 template <int DT, int RT, int CT>
 static hipError_t kq_go(const WeightView& w, const GemmAct& A, int m, int n, float* c, int ldc, hipStream_t st,
-                        const Groups& gp = Groups{}, float* part = nullptr) {
+                        const Groups& gp = Groups{}, float* part = nullptr, const Epi& ep = Epi{}) {
     using S = Stage<DT, RT, CT>;
     const int nrb = (m + 32 * S::TW - 1) / (32 * S::TW), ncb = A.NP / S::BN;
     const int64_t tiles = (w.r0 + tiled_rows(m)) / 32 - w.r0 / 32;   // tiles of the view that exist
@@ -757,13 +761,13 @@ static hipError_t kq_go(const WeightView& w, const GemmAct& A, int m, int n, flo
     int ns = 1, sb_per = 0;
     if (part != nullptr) split_plan(total, A.Kp / 256, &ns, &sb_per);
     if (ns == 1) {
-        kq_gemm_kernel<DT, RT, CT><<<grid, MMA_THREADS, lds, st>>>(w, A, m, n, c, ldc, nrb, ncb, tiles, gp, 0, 0);
+        kq_gemm_kernel<DT, RT, CT><<<grid, MMA_THREADS, lds, st>>>(w, A, m, n, c, ldc, nrb, ncb, tiles, gp, 0, 0, ep);
         return hipGetLastError();
     }
     const int64_t slice = (int64_t) n * m;
     kq_gemm_kernel<DT, RT, CT><<<dim3(grid, ns), MMA_THREADS, lds, st>>>(w, A, m, n, part, m, nrb, ncb, tiles, gp,
-                                                                         sb_per, slice);
-    split_reduce_kernel<<<dim3((m + 255) / 256, n), 256, 0, st>>>(part, ns, slice, m, c, ldc);
+                                                                         sb_per, slice, Epi{});
+    split_reduce_kernel<<<dim3((m + 255) / 256, n), 256, 0, st>>>(part, ns, slice, m, c, ldc, ep);
     return hipGetLastError();
 }
 
@@ -776,14 +780,14 @@ size_t gemm_mma_split_floats(int dt, int k, int m, int n) {
 }
 
 hipError_t launch_gemm_mma(int dt, const WeightView& w, const GemmAct& A, int k, int m, int n, float* c, int ldc,
-                           hipStream_t st, float* part) {
+                           hipStream_t st, float* part, const Epi& ep) {
     if (((dt == Q4_K || dt == Q6_K) && k % 256) || (w.r0 & 31) || A.NP % 64) return hipErrorNotSupported;
     switch (dt) {
-    case Q4_K: return kq_go<Q4_K, 1, 2>(w, A, m, n, c, ldc, st, Groups{}, part);
-    case Q4_0: return kq_go<Q4_0, 1, 2>(w, A, m, n, c, ldc, st, Groups{}, part);
-    case Q8_0: return kq_go<Q8_0, 1, 2>(w, A, m, n, c, ldc, st, Groups{}, part);
-    case Q6_K: return kq_go<Q6_K, 1, 2>(w, A, m, n, c, ldc, st, Groups{}, part);
-    case MXFP4: return kq_go<MXFP4, 1, 2>(w, A, m, n, c, ldc, st, Groups{}, part);
+    case Q4_K: return kq_go<Q4_K, 1, 2>(w, A, m, n, c, ldc, st, Groups{}, part, ep);
+    case Q4_0: return kq_go<Q4_0, 1, 2>(w, A, m, n, c, ldc, st, Groups{}, part, ep);
+    case Q8_0: return kq_go<Q8_0, 1, 2>(w, A, m, n, c, ldc, st, Groups{}, part, ep);
+    case Q6_K: return kq_go<Q6_K, 1, 2>(w, A, m, n, c, ldc, st, Groups{}, part, ep);
+    case MXFP4: return kq_go<MXFP4, 1, 2>(w, A, m, n, c, ldc, st, Groups{}, part, ep);
     default: return hipErrorNotSupported;
     }
 }

@@ -168,6 +168,18 @@ class HipJAM:
         return lib().jamhip_mm_device(self._ctx, w.address, wt, ldw, a_dev, JAM.F32, lda, c_dev, JAM.F32, ldc,
                                       m, n, k)
 
+    def mm_device_ex(self, w: Segment, wt: int, ldw: int, a_dev: int, lda: int, c_dev: int, ldc: int,
+                     m: int, n: int, k: int, bias_dev: int | None = None, accumulate: bool = False) -> int:
+        """mm_device with the fused epilogue C = [C +] (W·A^T [+ bias]) (jamhip_mm_device_ex)."""
+        return lib().jamhip_mm_device_ex(self._ctx, w.address, wt, ldw, a_dev, JAM.F32, lda, c_dev, JAM.F32, ldc,
+                                         m, n, k, bias_dev, int(accumulate))
+
+    ACT_SWIGLU, ACT_SWIGLU_OAI = 1, 2
+
+    def glu_device(self, act: int, gate_dev: int, ldg: int, up_dev: int, ldu: int, rows: int, cols: int) -> int:
+        """In place on gate: SwiGLU (act 1) or gpt-oss clamped SwiGLU (act 2) (jamhip_glu_device)."""
+        return lib().jamhip_glu_device(self._ctx, act, gate_dev, ldg, up_dev, ldu, rows, cols)
+
     def quantize_device(self, flavour: int, a_dev: int, lda: int, n: int, k: int, q_dev: int, d_dev: int,
                         s_dev: int) -> int:
         return lib().jamhip_quantize_device(self._ctx, flavour, a_dev, lda, n, k, q_dev, d_dev, s_dev)

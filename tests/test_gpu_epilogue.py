@@ -1,0 +1,91 @@
+"""GPU: fused epilogues through the C-ABI.
+
+jamhip_mm_device_ex applies C = [C +] (W·A^T [+ bias]) in the matmul's own final store. Every kernel path
+(decode F1 / F2, K-split decode and its reduce, matrix-core GEMM with and without split K, the fallback
+GEMM, the float-dot tail rows) must give, bit for bit, what the separate passes give in f32 on the plain
+jamhip_mm_device result (oracle/epilogue.py: Ops.addRowBiasInPlace then Ops.addInPlace), and leave the ldc
+gap untouched. jamhip_glu_device must match the full-scalar SwiGLU / gpt-oss clamped SwiGLU within 1 ulp
+(the device exp in double against numpy's)."""
+import sys
+
+import numpy as np
+import pytest
+
+from oracle import epilogue as EP
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+CASES = [   # (m, k, n): decode F1, split-K decode, F2 decode, matrix cores (+ split K), tail rows
+    (104, 1024, 1), (100, 9216, 4), (104, 1024, 8), (100, 1024, 16), (100, 1024, 100), (4096, 4096, 64),
+]
+
+
+@pytest.mark.parametrize("dt", O.QUANT_TYPES)
+@pytest.mark.parametrize("m,k,n", CASES)
+def test_mm_epilogue_bit_exact(hip, oracle, dt, m, k, n):
+    import torch
+    from qxotic_amd.jam import JAM, Segment
+    say(f"epilogue {O.NAMES[dt]} m={m} k={k} n={n}")
+    w = oracle.quantize(dt, oracle.normal(0xE1 + dt + m, (m, k), 0.0, 0.02))
+    a = oracle.outliers(0xE2 + n, (n, k))
+    ldc = m + 3
+    bias = np.random.default_rng(m + n).standard_normal(m).astype(np.float32)
+    c0 = np.random.default_rng(k + n).standard_normal((n, ldc)).astype(np.float32)
+    assert hip.pin(Segment.of(w), dt, k, m) == JAM.OK, hip.last_error()
+    try:
+        a_d = torch.from_numpy(a).cuda()
+        b_d = torch.from_numpy(bias).cuda()
+        plain = torch.zeros((n, ldc), dtype=torch.float32, device="cuda")
+        assert hip.mm_device(Segment.of(w), dt, k, a_d.data_ptr(), k, plain.data_ptr(), ldc, m, n, k) == JAM.OK
+        hip.synchronize()
+        p = plain.cpu().numpy()[:, :m]
+        for bias_on, acc in ((True, False), (False, True), (True, True)):
+            c = torch.from_numpy(c0.copy()).cuda()
+            st = hip.mm_device_ex(Segment.of(w), dt, k, a_d.data_ptr(), k, c.data_ptr(), ldc, m, n, k,
+                                  b_d.data_ptr() if bias_on else None, acc)
+            assert st == JAM.OK, hip.last_error()
+            hip.synchronize()
+            got = c.cpu().numpy()
+            want = EP.add_row_bias(p, bias) if bias_on else p
+            if acc:
+                want = EP.add_in_place(c0[:, :m], want)
+            assert np.array_equal(got[:, :m].view(np.uint32), want.view(np.uint32)), (bias_on, acc)
+            assert np.array_equal(got[:, m:].view(np.uint32), c0[:, m:].view(np.uint32))   # gap untouched
+    finally:
+        hip.evict(Segment.of(w))
+
+
+def test_mm_epilogue_rejects_bad_accumulate(hip, oracle):
+    from qxotic_amd.jam import JAM, Segment
+    w = oracle.quantize(O.Q8_0, oracle.normal(1, (32, 64), 0.0, 0.02))
+    st = hip.mm_device_ex(Segment.of(w), O.Q8_0, 64, 1 << 20, 64, 1 << 20, 32, 32, 1, 64, None, 2)
+    assert st == JAM.EINVAL
+
+
+@pytest.mark.parametrize("act", [1, 2])
+def test_glu(hip, act):
+    import torch
+    rows, cols, ldg, ldu = 7, 3001, 3005, 3003
+    rng = np.random.default_rng(act)
+    g = (rng.standard_normal((rows, ldg)) * 6).astype(np.float32)
+    u = (rng.standard_normal((rows, ldu)) * 6).astype(np.float32)
+    g[0, :8] = [7.0, 7.0001, -7.0, 40.0, -40.0, 0.0, -0.0, 1e-30]
+    u[0, :8] = [7.0, -7.0001, -1.0, 100.0, -100.0, 3.0, 3.0, 1.0]
+    say(f"glu act={act}")
+    g_d = torch.from_numpy(g).cuda()
+    u_d = torch.from_numpy(u).cuda()
+    assert hip.glu_device(act, g_d.data_ptr(), ldg, u_d.data_ptr(), ldu, rows, cols) == 0, hip.last_error()
+    hip.synchronize()
+    got = g_d.cpu().numpy()
+    f = EP.silu_mul if act == 1 else EP.clamped_swiglu
+    want = f(g[:, :cols], u[:, :cols])
+    d = np.abs(got[:, :cols].view(np.int32).astype(np.int64) - want.view(np.int32).astype(np.int64))
+    assert d.max() <= 1, int(d.max())
+    assert np.array_equal(got[:, cols:].view(np.uint32), g[:, cols:].view(np.uint32))   # gap untouched
+    assert np.array_equal(u_d.cpu().numpy(), u)
