@@ -15,12 +15,14 @@ The same JSON line carries
   * ``prefill``: the metric's second half, M=512 prefill TOPS of Q4_K 14336x4096 and Q6_K 4096x14336
     (activations 99% N(0,1) + 1% outliers at +-20, F2-quantized in the timed calls) against MI355X's dense
     int8 and f16 MFMA peaks;
+  * ``epilogue``: a fused bias + residual epilogue against the separate passes (gpt-oss attention output
+    projection at decode);
   * ``registry``: model load through the GGUF device weight registry (open + pin of a synthetic
     gpt-oss-20B-shaped file) in GB/s of jam weights made resident;
   * ``cpu_baseline``: the reference's own libjam (oracle/_ref, built from the reference C sources) on the
     same decode workload on this machine's host cores.
 
-    python bench.py [--gpus 1] [--steps 2048] [--warmup 64] [--no-cpu] [--no-prefill] [--no-moe] [--no-registry]
+    python bench.py [--gpus 1] [--steps 2048] [--warmup 64] [--no-cpu] [--no-prefill] [--no-moe] [--no-epilogue] [--no-registry]
     profiling runs: --no-graph (plain stream launches) --calibrate-copy (three 256 MiB device copies first,
     the known-size reference for the FETCH_SIZE/WRITE_SIZE scale factors)
 """
@@ -257,6 +259,65 @@ def moe_leg(hip, torch, stream, steps: int = 10) -> dict:
                     "(5760*2880 + 2880*2880)"}
 
 
+def epilogue_leg(hip, torch, stream, steps: int = 512) -> dict:
+    """Fused epilogue on gpt-oss-20B's attention output projection at decode (Q8_0 2880x4096, n = 1, with
+    bias, then the residual add): separate = jamhip_mm_device + bias add + residual add (jinfer's order:
+    MatMul.gemm, Ops.addRowBiasInPlace, Ops.addInPlace; 3 launches), fused = jamhip_mm_device_ex (1 launch).
+    Each timed as a captured graph of `steps` steps over 32 rotating weight copies (400 MB)."""
+    from qxotic_amd.jam import JAM, Segment
+
+    m, k, copies = 2880, 4096, 32
+    w = quantized("Q8_0", m, k, 0xA77E)
+    ws = [w.copy() for _ in range(copies)]
+    for x in ws:
+        assert hip.pin(Segment.of(x), JAM.Q8_0, k, m) == JAM.OK, hip.last_error()
+    a = torch.randn((1, k), device="cuda")
+    bias = torch.randn((m,), device="cuda")
+    tmp = torch.empty((1, m), device="cuda")
+    res = {v: torch.randn((1, m), device="cuda") for v in ("separate", "fused")}
+    res["fused"].copy_(res["separate"])
+
+    def step(variant, i):
+        x = Segment.of(ws[i % copies])
+        r = res[variant]
+        if variant == "fused":
+            st = hip.mm_device_ex(x, JAM.Q8_0, k, a.data_ptr(), k, r.data_ptr(), m, m, 1, k, bias.data_ptr(), True)
+        else:
+            st = hip.mm_device(x, JAM.Q8_0, k, a.data_ptr(), k, tmp.data_ptr(), m, m, 1, k)
+            tmp.add_(bias)
+            r.add_(tmp)
+        if st != JAM.OK:
+            raise RuntimeError(hip.last_error())
+
+    out = {}
+    with torch.cuda.stream(stream):
+        for v in ("separate", "fused"):   # one step each from the same residual: identical f32 operations
+            step(v, 0)
+        torch.cuda.synchronize()
+        assert torch.equal(res["separate"], res["fused"]), "fused epilogue disagrees with the separate passes"
+        for v in ("separate", "fused"):
+            for i in range(16):
+                step(v, i)
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                for i in range(steps):
+                    step(v, i)
+            g.replay()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            g.replay()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            out[v] = e0.elapsed_time(e1) * 1e3 / steps
+    for x in ws:
+        hip.evict(Segment.of(x))
+    return {"separate_us": round(out["separate"], 2), "fused_us": round(out["fused"], 2),
+            "saved_us": round(out["separate"] - out["fused"], 2),
+            "note": "gpt-oss-20B attn_output Q8_0 2880x4096, n=1, bias + residual; graph-timed, 32 rotating "
+                    "weight copies; separate = matmul + bias add + residual add (3 launches), fused = 1 launch"}
+
+
 def registry_leg(hip, layers: int = 2) -> dict:
     """Model load through the GGUF device weight registry: a synthetic GGUF holding `layers` gpt-oss-20B
     layers' jam weights (attention q/k/v/o in Q8_0, stacked gate/up/down experts 32 x 2880 x 2880 in MXFP4,
@@ -353,6 +414,7 @@ def main() -> int:
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-moe", action="store_true")
     ap.add_argument("--no-registry", action="store_true")
+    ap.add_argument("--no-epilogue", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true")
     args = ap.parse_args()
@@ -384,6 +446,10 @@ def main() -> int:
     if not args.no_moe:
         log("bench: moe leg")
         moe = moe_leg(hip, torch, stream)
+    epi = None
+    if not args.no_epilogue:
+        log("bench: epilogue leg")
+        epi = epilogue_leg(hip, torch, stream)
     reg = None
     if not args.no_registry:
         log("bench: registry leg")
@@ -408,6 +474,7 @@ def main() -> int:
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles()},
         "prefill": pre,
         "moe": moe,
+        "epilogue": epi,
         "registry": reg,
         "cpu_baseline": cpu,
     }
