@@ -117,6 +117,16 @@ jamhip_status jamhip_mm_grouped(jamhip_ctx* ctx,
                                 void*       c_dev, int ct, int ldc,
                                 int k, int rows_cap, void* offsets_dev);
 
+/* jamhip_mm_grouped with the experts' biases added in the matmul's store: bias_dev is f32 [n_experts][m],
+ * expert e's row i gets bias_dev[e·m + i] (NULL = none), the f32 add of Ops.addRowBiasInPlace on the
+ * expert's rows (gpt-oss's gate / up / down expert biases, GptOss.java:301-315). No counterpart in jam. */
+jamhip_status jamhip_mm_grouped_ex(jamhip_ctx* ctx,
+                                   const void* w, int wt, int ldw, int m, int n_experts,
+                                   const void* counts_dev,
+                                   const void* a_dev, int at, int lda,
+                                   void*       c_dev, int ct, int ldc,
+                                   int k, int rows_cap, void* offsets_dev, const void* bias_dev);
+
 /* Moe.dispatch's CSR build (Moe.java:188-206) from route_expert_dev[seq·topk] (int32 expert of route
  * s·topk + j, Moe.selectTopK's rowTopE): counts_dev[n_experts], offsets_dev[n_experts + 1], and the
  * slot of every route in (s, j) order within its expert: slot_route_dev[slot] = route,

@@ -461,6 +461,7 @@ __global__ void __launch_bounds__(64 * NWV) mv_kernel(WeightView w, ActQ A, cons
         }
         w.r0 += (int64_t) e * gp.gm;
         m = gp.gm;
+        if (gp.bias != nullptr) ep.bias = gp.bias + (int64_t) e * gp.gm;
     } else {
         t0 = blockIdx.y * NT;
         ntv = n - t0 < NT ? n - t0 : NT;

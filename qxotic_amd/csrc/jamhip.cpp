@@ -507,6 +507,13 @@ jamhip_status jamhip_quantize_device(jamhip_ctx* ctx, int flavour, const void* a
 jamhip_status jamhip_mm_grouped(jamhip_ctx* ctx, const void* w, int wt, int ldw, int m, int n_experts,
                                 const void* counts_dev, const void* a_dev, int at, int lda, void* c_dev, int ct,
                                 int ldc, int k, int rows_cap, void* offsets_dev) {
+    return jamhip_mm_grouped_ex(ctx, w, wt, ldw, m, n_experts, counts_dev, a_dev, at, lda, c_dev, ct, ldc, k, rows_cap,
+                                offsets_dev, nullptr);
+}
+
+jamhip_status jamhip_mm_grouped_ex(jamhip_ctx* ctx, const void* w, int wt, int ldw, int m, int n_experts,
+                                   const void* counts_dev, const void* a_dev, int at, int lda, void* c_dev, int ct,
+                                   int ldc, int k, int rows_cap, void* offsets_dev, const void* bias_dev) {
     if (!ctx) return JAMHIP_EINVAL;
     if (!w || !counts_dev || !a_dev || !c_dev) return fail(ctx, JAMHIP_EINVAL, "grouped: null operand");
     if (m <= 0 || k <= 0 || n_experts <= 0 || rows_cap < 0)
@@ -543,7 +550,7 @@ jamhip_status jamhip_mm_grouped(jamhip_ctx* ctx, const void* w, int wt, int ldw,
             hipSuccess)
         return hip_fail(ctx, e, "grouped: offsets copy");
     if (rows_cap == 0) return JAMHIP_OK;
-    const Groups g{off, poff8, map8, poff64, map64, m};
+    const Groups g{off, poff8, map8, poff64, map64, m, static_cast<const float*>(bias_dev)};
     const float* a = (const float*) a_dev;
     float* c = (float*) c_dev;
     // activation scratch for the decode kernels (rows_cap rows; F1 then F2 reuse it in stream order)

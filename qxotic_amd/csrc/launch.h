@@ -28,6 +28,7 @@ struct Groups {
     const int* poff64;
     const int* map64;
     int gm;
+    const float* bias = nullptr;   // per-expert bias [E][gm] added in the store (expert e at bias + e·gm)
 };
 
 // flavour 1: n in [1, 7], F1 activations; with `a` non-null the kernel quantizes A itself (requires

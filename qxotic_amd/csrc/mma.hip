@@ -163,6 +163,7 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
         slot0 = __builtin_amdgcn_readfirstlane(gp.poff64[e]);
         crow0 = __builtin_amdgcn_readfirstlane(gp.off[e]);
         nvalid = __builtin_amdgcn_readfirstlane(gp.off[e + 1]) - crow0;
+        if (gp.bias != nullptr) ep.bias = gp.bias + (int64_t) e * gp.gm;
     }
 
     // ---- global -> LDS copy of one stage. Every wave issues a fixed set of 1 KB pieces: the weight chunks

@@ -192,6 +192,14 @@ class HipJAM:
         return lib().jamhip_mm_grouped(self._ctx, w.address, wt, ldw, m, n_experts, counts_dev, a_dev, JAM.F32, lda,
                                        c_dev, JAM.F32, ldc, k, rows_cap, offsets_dev)
 
+    def mm_grouped_ex(self, w: Segment, wt: int, ldw: int, m: int, n_experts: int, counts_dev: int, a_dev: int,
+                      lda: int, c_dev: int, ldc: int, k: int, rows_cap: int, offsets_dev: int | None = None,
+                      bias_dev: int | None = None) -> int:
+        """mm_grouped with expert e's bias [m] (at bias + e·m) added in the store (jamhip_mm_grouped_ex)."""
+        _require_native(w, "weight W")
+        return lib().jamhip_mm_grouped_ex(self._ctx, w.address, wt, ldw, m, n_experts, counts_dev, a_dev, JAM.F32,
+                                          lda, c_dev, JAM.F32, ldc, k, rows_cap, offsets_dev, bias_dev)
+
     def moe_route(self, route_expert_dev: int, seq: int, topk: int, n_experts: int, counts_dev: int,
                   offsets_dev: int, slot_route_dev: int, route_slot_dev: int) -> int:
         """Moe.dispatch's CSR build on the device (Moe.java:188-206)."""

@@ -89,3 +89,43 @@ def test_glu(hip, act):
     assert d.max() <= 1, int(d.max())
     assert np.array_equal(got[:, cols:].view(np.uint32), g[:, cols:].view(np.uint32))   # gap untouched
     assert np.array_equal(u_d.cpu().numpy(), u)
+
+
+GROUPED_COUNTS = [3, 0, 12, 70, 1, 9, 40]   # F1 experts (1..7 rows), F2 bands (8..15), matrix cores (>= 16)
+
+
+@pytest.mark.parametrize("dt", O.QUANT_TYPES)
+def test_grouped_expert_bias_bit_exact(hip, oracle, dt):
+    """jamhip_mm_grouped_ex: expert e's rows get bias[e·m + i] in the store, bit for bit the f32 add of
+    Ops.addRowBiasInPlace on the plain grouped result; rows past the routed total stay untouched."""
+    import torch
+    from qxotic_amd.jam import JAM, Segment
+    E, m, k = len(GROUPED_COUNTS), 64, 512
+    say(f"grouped bias {O.NAMES[dt]} counts={GROUPED_COUNTS}")
+    w = np.ascontiguousarray(np.concatenate(
+        [oracle.quantize(dt, oracle.normal(0xB1 + 7 * e + dt, (m, k), 0.0, 0.02)) for e in range(E)]))
+    total = sum(GROUPED_COUNTS)
+    cap = total + 4
+    a_d = torch.from_numpy(oracle.outliers(0xB2, (cap, k))).cuda()
+    bias = np.random.default_rng(dt).standard_normal((E, m)).astype(np.float32)
+    b_d = torch.from_numpy(bias).cuda()
+    cnt = torch.tensor(GROUPED_COUNTS, dtype=torch.int32, device="cuda")
+    assert hip.pin(Segment.of(w), dt, k, E * m) == JAM.OK, hip.last_error()
+    try:
+        outs = []
+        for b in (None, b_d.data_ptr()):
+            c = torch.full((cap, m + 1), -5.0, dtype=torch.float32, device="cuda")
+            st = hip.mm_grouped_ex(Segment.of(w), dt, k, m, E, cnt.data_ptr(), a_d.data_ptr(), k, c.data_ptr(),
+                                   m + 1, k, cap, None, b)
+            assert st == JAM.OK, hip.last_error()
+            hip.synchronize()
+            outs.append(c.cpu().numpy())
+        plain, fused = outs
+        o = 0
+        for e, n in enumerate(GROUPED_COUNTS):
+            want = EP.add_row_bias(plain[o:o + n, :m], bias[e])
+            assert np.array_equal(fused[o:o + n, :m].view(np.uint32), want.view(np.uint32)), (e, n)
+            o += n
+        assert (fused[total:] == -5.0).all() and (fused[:, m] == -5.0).all()
+    finally:
+        hip.evict(Segment.of(w))
