@@ -158,7 +158,11 @@ GgufFile* gguf_read(const char* path, std::string* err) {
     if (!r.u32(&g->version)) return bail("");
     if (g->version != 3) return bail("unsupported GGUF version " + std::to_string(g->version) + " (expected 3)");
     if (!r.u64(&n_tensors) || !r.u64(&n_kv)) return bail("");
-    if (n_tensors > (uint64_t) r.size || n_kv > (uint64_t) r.size) return bail("tensor or key count past end of file");
+    // a metadata pair takes at least 13 bytes (key length, type, 1-byte value), a tensor entry at least 24
+    // (name length, n_dims, type, offset): counts the rest of the file cannot hold are rejected before any
+    // table is sized by them
+    if (n_kv > (uint64_t) (r.size - r.pos) / 13 || n_tensors > (uint64_t) (r.size - r.pos) / 24)
+        return bail("tensor or key count past end of file");
     g->n_kv = (int64_t) n_kv;
 
     // metadata: only general.alignment is kept; the registry needs nothing else

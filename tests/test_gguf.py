@@ -113,8 +113,10 @@ BAD = {
     "unknown_type": (lambda: header(1, []) + tensor("t", [32], 99, 0), "GGML type"),
     "partial_block": (lambda: header(1, []) + tensor("t", [100], 12, 0), "whole number of blocks"),
     "past_eof": (lambda: header(1, []) + tensor("t", [64], F32, 0), "past the end"),
-    "truncated_header": (lambda: header(2, []) + tensor("t", [4], F32, 0), "truncated"),
+    "truncated_header": (lambda: header(1, []) + tensor("t", [4, 4], F32, 0)[:-4], "truncated"),
     "truncated_string": (lambda: header(0, [struct.pack("<Q", 1 << 40)]), "past end of file"),
+    "huge_tensor_count": (lambda: header(1 << 40, []) + b"\0" * 64, "count past end of file"),
+    "huge_kv_count": (lambda: header(0, []).replace(struct.pack("<QQ", 0, 0), struct.pack("<QQ", 0, 1 << 40)), "count past end of file"),
 }
 
 
