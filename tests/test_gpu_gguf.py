@@ -1,7 +1,8 @@
 """GPU: the GGUF device weight registry (jamhip_gguf_pin / jamhip_gguf_evict) through the C-ABI.
 
-A file holding a 2-D Q4_K tensor, a stacked MXFP4 expert tensor [k, rows, experts], a Q8_0 tensor with a
-partial row tile and an F32 bias is opened and pinned in one call. Every jam call on a registry address
+A file holding all five jam weight dtypes (2-D Q4_K, Q6_K and Q4_0 tensors, a stacked MXFP4 expert tensor
+[k, rows, experts], a Q8_0 tensor with a partial row tile) beside an F32 bias and an F16 embedding (not
+jam weights: skipped) is opened and pinned in one call. Every jam call on a registry address
 must (1) meet the tier-1 bound against the int8 oracle, (2) equal bit for bit the same call on an unpinned
 heap copy of the same bytes (the staged path runs the same kernels), and (3) read the device copy: when
 the caller's own mapping is pinned and then overwritten, results do not change. Expert slices of the
@@ -49,12 +50,17 @@ def model(oracle, tmp_path_factory):
         "blk.0.ffn_gate_exps.weight": (O.MXFP4, E * ER,
                                        oracle.quantize(O.MXFP4, oracle.normal(0x6602, (E * ER, K), 0.0, 0.02))),
         "blk.0.attn_q.weight": (O.Q8_0, 40, oracle.quantize(O.Q8_0, oracle.normal(0x6603, (40, K), 0.0, 0.02))),
+        "output.weight": (O.Q6_K, 72, oracle.quantize(O.Q6_K, oracle.normal(0x6604, (72, K), 0.0, 0.02))),
+        "blk.0.attn_k.weight": (O.Q4_0, 48, oracle.quantize(O.Q4_0, oracle.normal(0x6605, (48, K), 0.0, 0.02))),
     }
     bias = np.arange(96, dtype=np.float32)
     tensors = [("blk.0.ffn_up.weight", O.Q4_K, (K, 96), w["blk.0.ffn_up.weight"][2]),
                ("blk.0.ffn_up.bias", 0, (96,), bias),
                ("blk.0.ffn_gate_exps.weight", O.MXFP4, (K, ER, E), w["blk.0.ffn_gate_exps.weight"][2]),
-               ("blk.0.attn_q.weight", O.Q8_0, (K, 40), w["blk.0.attn_q.weight"][2])]
+               ("blk.0.attn_q.weight", O.Q8_0, (K, 40), w["blk.0.attn_q.weight"][2]),
+               ("token_embd.weight", 1, (K, 8), np.zeros(8 * K, np.float16)),
+               ("output.weight", O.Q6_K, (K, 72), w["output.weight"][2]),
+               ("blk.0.attn_k.weight", O.Q4_0, (K, 48), w["blk.0.attn_k.weight"][2])]
     path = tmp_path_factory.mktemp("gguf") / "model.gguf"
     G.write(path, tensors, [("general.architecture", "string", "test")], alignment=64)
     return path, w
@@ -68,9 +74,9 @@ def test_registry_pin_lookup_evict(hip, oracle, model):
         say("gguf registry: pin from the handle's mapping")
         st, cnt, nbytes = g.pin(hip)
         assert st == 0, hip.last_error()
-        assert cnt == 3 and nbytes == sum(x[2].nbytes for x in w.values())
+        assert cnt == 5 and nbytes == sum(x[2].nbytes for x in w.values())   # F32 / F16 tensors skipped
         assert hip.pinned_bytes() > before
-        assert g.pin(hip)[:2] == (0, 3)                        # idempotent
+        assert g.pin(hip)[:2] == (0, 5)                        # idempotent
         try:
             for name, (dt, m, wq) in w.items():
                 e = g.tensors[name]
@@ -94,7 +100,7 @@ def test_registry_pin_lookup_evict(hip, oracle, model):
                     sl = np.ascontiguousarray(wq[x * ER:(x + 1) * ER])
                     assert np.array_equal(got.view(np.uint32), mm_heap(hip, sl, O.MXFP4, a, ER, n).view(np.uint32)), (x, n)
         finally:
-            assert g.evict(hip) == 3
+            assert g.evict(hip) == 5
     assert hip.pinned_bytes() == before
 
 
@@ -110,7 +116,7 @@ def test_registry_keys_caller_mapping(hip, oracle, model):
         base = region.ctypes.data
         say("gguf registry: pin the caller's mapping")
         st, cnt, _ = g.pin(hip, base)
-        assert st == 0 and cnt == 3, hip.last_error()
+        assert st == 0 and cnt == 5, hip.last_error()
         try:
             region[:] = 0
             for name, (dt, m, wq) in w.items():
@@ -141,4 +147,23 @@ def test_registry_keys_caller_mapping(hip, oracle, model):
                     assert tier1(got[o:o + n], ref, sa).all(), x
                 o += n
         finally:
-            assert g.evict(hip, base) == 3
+            assert g.evict(hip, base) == 5
+
+
+def test_registry_rejects_partial_row_blocks(hip, tmp_path):
+    """A jam-typed tensor whose row extent is not a whole number of blocks (allowed by GGUF when the total
+    element count is) cannot be a jam weight: pin stops there with EUNSUPPORTED and names the tensor;
+    the tensors pinned before it stay pinned until evicted."""
+    from qxotic_amd import gguf as G
+    from qxotic_amd.jam import JAM
+    ok = np.zeros(2 * 34, np.uint8)                            # Q8_0 [64, 1]
+    bad = np.zeros(3 * 34, np.uint8)                           # Q8_0 [48, 2]: 96 elements, rows of 1.5 blocks
+    path = tmp_path / "bad.gguf"
+    G.write(path, [("a.weight", O.Q8_0, (64, 1), ok), ("b.weight", O.Q8_0, (48, 2), bad)])
+    before = hip.pinned_bytes()
+    with G.GGUF(path) as g:
+        st, cnt, _ = g.pin(hip)
+        assert st == JAM.EUNSUPPORTED and cnt == 1
+        assert "b.weight" in hip.last_error()
+        assert g.evict(hip) == 1
+    assert hip.pinned_bytes() == before
