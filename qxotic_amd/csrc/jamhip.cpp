@@ -182,13 +182,19 @@ bool mma_path(int dt, int k, const WeightView& wv) {
            (wv.r0 & 31) == 0 && gemm_prep_fits(k);
 }
 
-// Smallest n that takes the matrix cores (n >= 8 is F2 either way; small grids split K): measured on the
-// BASELINE shapes, from 8 tokens for Q4_K / Q6_K and 16 for MXFP4, Q4_0 and Q8_0 (14336x4096 n = 16: Q4_0
-// 32.2 us, Q8_0 31.9 us against the F2 decode kernel's 41.1 / 50.4). JAM_HIP_MMA_MIN_N overrides (tuning).
-static int mma_min_n(int dt) {
+// Smallest n that takes the matrix cores (n >= 8 is F2 either way; small grids split K), from a sweep of
+// both paths (graph-timed, rotating weights). The F2 decode kernel reads W once per 8-token tile and wins
+// every shape at one tile (n = 8: Q4_K 14336x4096 21.9 us against 28.4). On weights of up to ~17.8M elements
+// (4096x4096, 5760x2880, 2880x4096) its tiles run side by side on the idle CUs and it wins through n = 16
+// for every dtype (Q8_0 4096x4096 n = 16: 15.2 against 22.9 us) and through n = 32 for Q4_0, Q4_K and
+// Q6_K (Q4_K 4096x4096 n = 32: 21.2 against 26.1). On larger weights the matrix cores win from the second
+// tile (14336x4096 n = 12: Q8_0 32.7 against 43.1 us), except at k > 8192 where they win from n = 16
+// (Q4_0 4096x14336 n = 12: F2 36.3, matrix cores 40.6). JAM_HIP_MMA_MIN_N overrides (tuning).
+static int mma_min_n(int dt, int m, int k) {
     const char* v = getenv("JAM_HIP_MMA_MIN_N");
-    const int x = v ? atoi(v) : dt == MXFP4 || dt == Q4_0 || dt == Q8_0 ? 16 : 8;
-    return x < 8 ? 8 : x;
+    if (v) return atoi(v) < 8 ? 8 : atoi(v);
+    if ((int64_t) m * k <= (int64_t) 17 << 20) return dt == Q4_0 || dt == Q4_K || dt == Q6_K ? 33 : 17;
+    return k > 8192 ? 16 : 9;
 }
 
 // Smallest n that takes gemm_kernel, the fallback when mma_path declines (a view not aligned to 32 rows, k
@@ -225,7 +231,7 @@ jamhip_status compute(jamhip_ctx* ctx, int dt, const WeightView& wv, const float
     // n >= 8: jam's 16-row F2 bands on rows [0, m16); the last m % 16 rows take the band's float-dot tail
     // (jam_kernels_q4k_avx512.c:185-188).
     const int m16 = m - m % 16;
-    if (n >= mma_min_n(dt) && m16 > 0 && mma_path(dt, k, wv)) {
+    if (n >= mma_min_n(dt, m, k) && m16 > 0 && mma_path(dt, k, wv)) {
         GemmAct G;
         if ((e = ctx->gact.ensure(gemm_act_bytes(dt, n, k))) != hipSuccess)
             return hip_fail(ctx, e, "gemm activation scratch alloc");

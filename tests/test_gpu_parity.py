@@ -104,6 +104,26 @@ def test_mm_parity_shapes(hip, oracle, dt):
 
 
 @pytest.mark.parametrize("dt", O.QUANT_TYPES)
+def test_matrix_cores_and_f2_at_few_tokens(hip, oracle, dt, monkeypatch):
+    """Both n >= 8 paths at the token counts where the routing threshold (weight size and k dependent)
+    hands over: JAM_HIP_MMA_MIN_N forces the matrix cores (8) or the F2 decode kernel (huge) on the same
+    inputs; both meet the tier-1 bound."""
+    for (m, k) in SHAPES[:2]:
+        if k % O.BLOCK[dt][0]:
+            continue
+        w = oracle.quantize(dt, oracle.normal(0x7E57 ^ (m * 31 + k + dt), (m, k), 0.0, 0.02))
+        for n in (8, 9, 13, 16, 17, 24, 32):
+            a = oracle.outliers(3000 + n, (n, k))
+            ref = oracle.mm_int8(dt, w, a, m, n, k)
+            _, sa = oracle.mm_ref(dt, w, a, m, n, k)
+            for force in ("8", "100000"):
+                monkeypatch.setenv("JAM_HIP_MMA_MIN_N", force)
+                say(f"few tokens {O.NAMES[dt]} m={m} n={n} k={k} mma_min_n={force}")
+                got = run_mm(hip, dt, w, a, m, n, k)
+                assert tier1(got, ref, sa).all(), (O.NAMES[dt], m, n, k, force)
+
+
+@pytest.mark.parametrize("dt", O.QUANT_TYPES)
 def test_mm_matches_golden_libjam(hip, dt):
     """Against libjam's own outputs committed as fixtures (PRECISION.md bound plus the tier-1 bound
     relative to libjam's own answer)."""
