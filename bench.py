@@ -15,6 +15,8 @@ The same JSON line carries
   * ``prefill``: the metric's second half, M=512 prefill TOPS of Q4_K 14336x4096 and Q6_K 4096x14336
     (activations 99% N(0,1) + 1% outliers at +-20, F2-quantized in the timed calls) against MI355X's dense
     int8 and f16 MFMA peaks;
+  * ``decode_step``: config 3, a whole Llama-3-8B decode step's 225 matmuls (32 layers + output head,
+    4.8 GB of weights) as one graph, in µs per token and HBM fraction;
   * ``epilogue``: a fused bias + residual epilogue against the separate passes (gpt-oss attention output
     projection at decode);
   * ``registry``: model load through the GGUF device weight registry (open + pin of a synthetic
@@ -22,7 +24,7 @@ The same JSON line carries
   * ``cpu_baseline``: the reference's own libjam (oracle/_ref, built from the reference C sources) on the
     same decode workload on this machine's host cores.
 
-    python bench.py [--gpus 1] [--steps 2048] [--warmup 64] [--no-cpu] [--no-prefill] [--no-moe] [--no-epilogue] [--no-registry]
+    python bench.py [--gpus 1] [--steps 2048] [--warmup 64] [--no-cpu] [--no-prefill] [--no-moe] [--no-step] [--no-epilogue] [--no-registry]
     profiling runs: --no-graph (plain stream launches) --calibrate-copy (three 256 MiB device copies first,
     the known-size reference for the FETCH_SIZE/WRITE_SIZE scale factors)
 """
@@ -259,6 +261,80 @@ def moe_leg(hip, torch, stream, steps: int = 10) -> dict:
                     "(5760*2880 + 2880*2880)"}
 
 
+def decode_step_leg(hip, torch, stream, w_gate: np.ndarray, reps: int = 8) -> dict:
+    """Config 3: a Llama-3-8B Q4_K_M-style decode step, matmuls only. Per layer q 4096x4096, k / v
+    1024x4096, o 4096x4096, gate / up 14336x4096 in Q4_K and down 4096x14336 in Q6_K; 32 layers and the
+    128256x4096 Q6_K output head: 4.84 GB of weights, each layer's in its own HBM allocations. One token
+    (n = 1, jam's F1 decode path); every layer reads the same synthetic activations (matmuls only, as the
+    config says). Weight values: one N(0,0.02) quantization per shape, copied into every layer (the
+    kernels' work does not depend on the values). Two schedules of the same bytes:
+      separate  7 calls per layer, as jinfer issues them (225 launches);
+      fused     q|k|v and gate|up as one call each over weights laid out back to back (the way a GGUF file
+                stores a block's tensors), 4 calls per layer (129 launches): the same rows, outputs
+                concatenated.
+    Timed: `reps` replays of one captured graph per schedule, HIP events on the library's stream."""
+    from qxotic_amd.jam import JAM, Segment
+
+    layers, D, KV, FF, V = 32, 4096, 1024, 14336, 128256
+    dd, kv = quantized("Q4_K", D, D, 0xD301), quantized("Q4_K", KV, D, 0xD302)
+    down = quantized("Q6_K", D, FF, 0xD303)
+    blk = quantized("Q6_K", 4096, D, 0xD304)
+    head = np.ascontiguousarray(np.concatenate([blk] * ((V + 4095) // 4096))[:V])
+    plans = {"separate": [], "fused": []}   # (weight, dtype, m, k)
+    for _ in range(layers):
+        plans["separate"] += [(dd.copy(), JAM.Q4_K, D, D), (kv.copy(), JAM.Q4_K, KV, D), (kv.copy(), JAM.Q4_K, KV, D),
+                              (dd.copy(), JAM.Q4_K, D, D), (w_gate.copy(), JAM.Q4_K, FF, D),
+                              (w_gate.copy(), JAM.Q4_K, FF, D), (down.copy(), JAM.Q6_K, D, FF)]
+        plans["fused"] += [(np.concatenate([dd, kv, kv]), JAM.Q4_K, D + 2 * KV, D), (dd.copy(), JAM.Q4_K, D, D),
+                           (np.concatenate([w_gate, w_gate]), JAM.Q4_K, 2 * FF, D), (down.copy(), JAM.Q6_K, D, FF)]
+    for p in plans.values():
+        p.append((head, JAM.Q6_K, V, D))
+    wbytes = sum(x[0].nbytes for x in plans["separate"])
+    assert wbytes == sum(x[0].nbytes for x in plans["fused"])
+    x_d = torch.randn((1, D), device="cuda")
+    h_d = torch.randn((1, FF), device="cuda")
+    out = {}
+    for name, plan in plans.items():
+        for w, dt, m, k in plan:
+            assert hip.pin(Segment.of(w), dt, k, m) == JAM.OK, hip.last_error()
+        outs = {m: torch.empty((1, m), device="cuda") for m in {x[2] for x in plan}}
+
+        def step():
+            for w, dt, m, k in plan:
+                a = h_d if k == FF else x_d
+                st = hip.mm_device(Segment.of(w), dt, k, a.data_ptr(), k, outs[m].data_ptr(), m, m, 1, k)
+                if st != JAM.OK:
+                    raise RuntimeError(hip.last_error())
+
+        with torch.cuda.stream(stream):
+            step()
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                step()
+            g.replay()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(reps):
+                g.replay()
+            e1.record(stream)
+            torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / reps
+        io = sum(4 * (k + m) for _, _, m, k in plan)
+        gbs = (wbytes + io) / (us * 1e-6) / 1e9
+        out[name] = {"us_per_token": round(us, 1), "tokens_per_s": round(1e6 / us, 1), "launches": len(plan),
+                     "GBs": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+        for w, _, _, _ in plan:
+            if w is not head or name == "fused":
+                hip.evict(Segment.of(w))
+        del g
+    out["weights_GB"] = round(wbytes / 1e9, 3)
+    out["note"] = ("config 3: 32 Llama-3-8B layers (q/k/v/o/gate/up Q4_K, down Q6_K) + Q6_K output head, n = 1, "
+                   "matmuls only, one captured graph per schedule; GB/s = weights + activations + outputs")
+    return out
+
+
 def epilogue_leg(hip, torch, stream, steps: int = 512) -> dict:
     """Fused epilogue on gpt-oss-20B's attention output projection at decode (Q8_0 2880x4096, n = 1, with
     bias, then the residual add): separate = jamhip_mm_device + bias add + residual add (jinfer's order:
@@ -415,6 +491,7 @@ def main() -> int:
     ap.add_argument("--no-moe", action="store_true")
     ap.add_argument("--no-registry", action="store_true")
     ap.add_argument("--no-epilogue", action="store_true")
+    ap.add_argument("--no-step", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true")
     args = ap.parse_args()
@@ -446,6 +523,10 @@ def main() -> int:
     if not args.no_moe:
         log("bench: moe leg")
         moe = moe_leg(hip, torch, stream)
+    step = None
+    if not args.no_step:
+        log("bench: decode step leg")
+        step = decode_step_leg(hip, torch, stream, w)
     epi = None
     if not args.no_epilogue:
         log("bench: epilogue leg")
@@ -474,6 +555,7 @@ def main() -> int:
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles()},
         "prefill": pre,
         "moe": moe,
+        "decode_step": step,
         "epilogue": epi,
         "registry": reg,
         "cpu_baseline": cpu,

@@ -210,10 +210,15 @@ int           jamhip_gguf_alignment(const jamhip_gguf* g);
 
 /* Pin every Q8_0 / Q4_0 / Q4_K / Q6_K / MXFP4 tensor of g at data_base + offset: data_base is the
  * caller's own mapping of the same file's data region (the addresses its jam calls will pass), or NULL
- * for the handle's mapping. Other dtypes are skipped. Stops at the first failure (the status of that
- * tensor, its name in jamhip_last_error); tensors pinned before it stay pinned. n_pinned / bytes_pinned
+ * for the handle's mapping. Other dtypes are skipped. Tensors of one dtype and row length stored back to
+ * back (a block's attn_q|attn_k|attn_v, ffn_gate|ffn_up), each starting on a 32-row boundary of the run,
+ * share one device range: every tensor still resolves on its own, and one call with W = the first
+ * tensor's address and m = the rows of several computes them together (their outputs concatenated in
+ * C). Every tensor is checked first (JAMHIP_EUNSUPPORTED, nothing pinned, the tensor's name in
+ * jamhip_last_error, for a row extent that is not whole blocks or exceeds 32-bit extents); a device
+ * failure stops the pinning, and the ranges pinned before it stay pinned. n_pinned / bytes_pinned
  * (either may be NULL) receive the count and file bytes of the tensors now resident. evict drops the
- * pins that start at those addresses. */
+ * file's ranges. */
 jamhip_status jamhip_gguf_pin(jamhip_ctx* ctx, const jamhip_gguf* g, const void* data_base, int64_t* n_pinned,
                               int64_t* bytes_pinned);
 jamhip_status jamhip_gguf_evict(jamhip_ctx* ctx, const jamhip_gguf* g, const void* data_base, int64_t* n_evicted);

@@ -710,6 +710,43 @@ bool registry_shape(const GgufTensor& t, int* ldw, int64_t* rows) {
     *rows = t.bytes / row_bytes(t.type, t.dims[0]);
     return true;
 }
+
+// The registry's device ranges for a file: its jam tensors in offset order, adjacent tensors of one dtype
+// and row length (back to back in the file, every member starting on a 32-row tile) merged into one run,
+// so a call may span them (q|k|v, gate|up) while each tensor still resolves inside the run.
+struct Run {
+    int64_t offset, bytes, rows, members;
+    int type, ldw;
+};
+
+jamhip_status registry_runs(jamhip_ctx* ctx, const GgufFile& f, std::vector<Run>* runs) {
+    std::vector<const GgufTensor*> ts;
+    for (const GgufTensor& t : f.tensors) {
+        int ldw;
+        int64_t rows;
+        if (!registry_shape(t, &ldw, &rows)) continue;
+        if (t.dims[0] % block_elems(t.type))
+            return fail(ctx, JAMHIP_EUNSUPPORTED, "gguf pin: tensor " + t.name + ": row extent is not a whole number of blocks");
+        if (t.dims[0] > (1 << 30) || rows > INT32_MAX)
+            return fail(ctx, JAMHIP_EUNSUPPORTED, "gguf pin: tensor " + t.name + " exceeds the kernels' 32-bit extents");
+        ts.push_back(&t);
+    }
+    std::sort(ts.begin(), ts.end(), [](const GgufTensor* x, const GgufTensor* y) { return x->offset < y->offset; });
+    runs->clear();
+    for (const GgufTensor* t : ts) {
+        const int64_t rows = t->bytes / row_bytes(t->type, t->dims[0]);
+        Run* r = runs->empty() ? nullptr : &runs->back();
+        if (r && r->type == t->type && r->ldw == (int) t->dims[0] && r->offset + r->bytes == t->offset &&
+            r->rows % 32 == 0 && r->rows + rows <= INT32_MAX) {
+            r->bytes += t->bytes;
+            r->rows += rows;
+            r->members++;
+        } else {
+            runs->push_back(Run{t->offset, t->bytes, rows, 1, t->type, (int) t->dims[0]});
+        }
+    }
+    return JAMHIP_OK;
+}
 }  // namespace
 
 jamhip_status jamhip_gguf_pin(jamhip_ctx* ctx, const jamhip_gguf* g, const void* data_base, int64_t* n_pinned,
@@ -722,25 +759,16 @@ jamhip_status jamhip_gguf_pin(jamhip_ctx* ctx, const jamhip_gguf* g, const void*
     Busy guard(ctx);
     if (!guard.ok) return fail(ctx, JAMHIP_EBUSY, "context busy");
     (void) hipSetDevice(ctx->device);
-    jamhip_status st = JAMHIP_OK;
-    for (const GgufTensor& t : g->f->tensors) {
-        int ldw;
-        int64_t rows;
-        if (!registry_shape(t, &ldw, &rows)) continue;
-        if (t.dims[0] % block_elems(t.type)) {
-            st = fail(ctx, JAMHIP_EUNSUPPORTED, "gguf pin: tensor " + t.name + ": row extent is not a whole number of blocks");
+    std::vector<Run> runs;
+    jamhip_status st = registry_runs(ctx, *g->f, &runs);   // every tensor checked before anything is pinned
+    if (st != JAMHIP_OK) return st;
+    for (const Run& r : runs) {
+        if ((st = pin_range(ctx, base + r.offset, r.type, r.ldw, r.rows, true)) != JAMHIP_OK) {
+            ctx->err = "gguf pin: run at data offset " + std::to_string(r.offset) + ": " + ctx->err;
             break;
         }
-        if (t.dims[0] > (1 << 30) || rows > INT32_MAX) {
-            st = fail(ctx, JAMHIP_EUNSUPPORTED, "gguf pin: tensor " + t.name + " exceeds the kernels' 32-bit extents");
-            break;
-        }
-        if ((st = pin_range(ctx, base + t.offset, t.type, ldw, rows, true)) != JAMHIP_OK) {
-            ctx->err = "gguf pin: tensor " + t.name + ": " + ctx->err;
-            break;
-        }
-        if (n_pinned) ++*n_pinned;
-        if (bytes_pinned) *bytes_pinned += t.bytes;
+        if (n_pinned) *n_pinned += r.members;
+        if (bytes_pinned) *bytes_pinned += r.bytes;
     }
     ctx->w_raw.release();
     return st;
@@ -754,12 +782,11 @@ jamhip_status jamhip_gguf_evict(jamhip_ctx* ctx, const jamhip_gguf* g, const voi
     Busy guard(ctx);
     if (!guard.ok) return fail(ctx, JAMHIP_EBUSY, "context busy");
     (void) hipSetDevice(ctx->device);
-    for (const GgufTensor& t : g->f->tensors) {
-        int ldw;
-        int64_t rows;
-        if (registry_shape(t, &ldw, &rows) && evict_at(ctx, reinterpret_cast<uintptr_t>(base + t.offset)) && n_evicted)
-            ++*n_evicted;
-    }
+    std::vector<Run> runs;
+    const jamhip_status st = registry_runs(ctx, *g->f, &runs);
+    if (st != JAMHIP_OK) return st;
+    for (const Run& r : runs)
+        if (evict_at(ctx, reinterpret_cast<uintptr_t>(base + r.offset)) && n_evicted) *n_evicted += r.members;
     return JAMHIP_OK;
 }
 

@@ -152,8 +152,8 @@ def test_registry_keys_caller_mapping(hip, oracle, model):
 
 def test_registry_rejects_partial_row_blocks(hip, tmp_path):
     """A jam-typed tensor whose row extent is not a whole number of blocks (allowed by GGUF when the total
-    element count is) cannot be a jam weight: pin stops there with EUNSUPPORTED and names the tensor;
-    the tensors pinned before it stay pinned until evicted."""
+    element count is) cannot be a jam weight: pin refuses the file with EUNSUPPORTED before pinning
+    anything and names the tensor."""
     from qxotic_amd import gguf as G
     from qxotic_amd.jam import JAM
     ok = np.zeros(2 * 34, np.uint8)                            # Q8_0 [64, 1]
@@ -163,7 +163,50 @@ def test_registry_rejects_partial_row_blocks(hip, tmp_path):
     before = hip.pinned_bytes()
     with G.GGUF(path) as g:
         st, cnt, _ = g.pin(hip)
-        assert st == JAM.EUNSUPPORTED and cnt == 1
+        assert st == JAM.EUNSUPPORTED and cnt == 0
         assert "b.weight" in hip.last_error()
-        assert g.evict(hip) == 1
+    assert hip.pinned_bytes() == before
+
+
+def test_registry_runs_fused_call(hip, oracle, tmp_path):
+    """q|k|v and gate|up stored back to back share one device range: each tensor alone, and one call over
+    the run (W = the first tensor, m = the rows of all), meet the tier-1 bound, the run's rows equal the
+    concatenation of the tensors' own results, and a tensor after a padding gap or of another dtype stays
+    its own range."""
+    from qxotic_amd import gguf as G
+    from qxotic_amd.jam import JAM, Segment
+    q = oracle.quantize(O.Q4_K, oracle.normal(0x7101, (64, K), 0.0, 0.02))
+    kk = oracle.quantize(O.Q4_K, oracle.normal(0x7102, (32, K), 0.0, 0.02))
+    v = oracle.quantize(O.Q4_K, oracle.normal(0x7103, (32, K), 0.0, 0.02))
+    o = oracle.quantize(O.Q8_0, oracle.normal(0x7104, (64, K), 0.0, 0.02))
+    tensors = [("blk.0.attn_q.weight", O.Q4_K, (K, 64), q), ("blk.0.attn_k.weight", O.Q4_K, (K, 32), kk),
+               ("blk.0.attn_v.weight", O.Q4_K, (K, 32), v), ("blk.0.attn_output.weight", O.Q8_0, (K, 64), o)]
+    path = tmp_path / "runs.gguf"
+    G.write(path, tensors)
+    qkv = np.concatenate([q, kk, v])
+    before = hip.pinned_bytes()
+    with G.GGUF(path) as g:
+        e = {n: g.tensors[n] for n, *_ in tensors}
+        assert e["blk.0.attn_k.weight"].offset == e["blk.0.attn_q.weight"].offset + q.nbytes   # back to back
+        st, cnt, _ = g.pin(hip)
+        assert st == 0 and cnt == 4, hip.last_error()
+        try:
+            for n in (1, 4, 16):
+                a = oracle.outliers(0x7200 + n, (n, K))
+                say(f"registry run q|k|v n={n}")
+                fused = mm_at(hip, e["blk.0.attn_q.weight"].address, qkv.nbytes, g, O.Q4_K, a, 128, n)
+                ref = oracle.mm_int8(O.Q4_K, qkv, a, 128, n, K)
+                _, sa = oracle.mm_ref(O.Q4_K, qkv, a, 128, n, K)
+                assert tier1(fused, ref, sa).all(), n
+                parts = [mm_at(hip, e[nm].address, w.nbytes, g, O.Q4_K, a, w.shape[0], n)
+                         for nm, w in (("blk.0.attn_q.weight", q), ("blk.0.attn_k.weight", kk), ("blk.0.attn_v.weight", v))]
+                for got, w in zip(parts, (q, kk, v)):
+                    r = oracle.mm_int8(O.Q4_K, w, a, w.shape[0], n, K)
+                    _, sw = oracle.mm_ref(O.Q4_K, w, a, w.shape[0], n, K)
+                    assert tier1(got, r, sw).all(), n
+                # the output tensor (Q8_0) is a range of its own
+                got = mm_at(hip, e["blk.0.attn_output.weight"].address, o.nbytes, g, O.Q8_0, a, 64, n)
+                assert np.array_equal(got.view(np.uint32), mm_heap(hip, o, O.Q8_0, a, 64, n).view(np.uint32))
+        finally:
+            assert g.evict(hip) == 4
     assert hip.pinned_bytes() == before
