@@ -218,7 +218,9 @@ int           jamhip_gguf_alignment(const jamhip_gguf* g);
  * jamhip_last_error, for a row extent that is not whole blocks or exceeds 32-bit extents); a device
  * failure stops the pinning, and the ranges pinned before it stay pinned. n_pinned / bytes_pinned
  * (either may be NULL) receive the count and file bytes of the tensors now resident. evict drops the
- * file's ranges. */
+ * file's ranges. Pins are keyed by address: evict them before the mapping they were taken from goes
+ * away (jamhip_gguf_close for data_base = NULL, the caller's unmap otherwise), or a later mapping at the
+ * same addresses would be served the old weights. */
 jamhip_status jamhip_gguf_pin(jamhip_ctx* ctx, const jamhip_gguf* g, const void* data_base, int64_t* n_pinned,
                               int64_t* bytes_pinned);
 jamhip_status jamhip_gguf_evict(jamhip_ctx* ctx, const jamhip_gguf* g, const void* data_base, int64_t* n_evicted);
