@@ -673,7 +673,7 @@ static size_t fuse_lds(int n, int k) { return (size_t) n * ((k / 32 + 7) / 8) * 
 static int fuse_hp(int n, int k) { return (n * 16 * ((k / 32 + 7) / 8) + 64 * MV_WAVES - 1) / (64 * MV_WAVES); }
 
 // Work split: bands of RB = 8 rows (x 8 group slots: chunk loads are 128-byte lines; 16-row bands measured
-// slower at every BASELINE shape) and the fewest items per wave that fit a band in one block, 1, 2 or 4
+// slower at every BASELINE shape, 4-row bands 1.5-1.75x slower at k = 14336) and the fewest items per wave that fit a band in one block, 1, 2 or 4
 // for k up to 16384, 32768, 65536. More items per wave only add registers. JAM_HIP_MV_ITEMS overrides
 // (tuning sweeps). Returns false past k = 65536.
 constexpr int MV_RB = 8;
