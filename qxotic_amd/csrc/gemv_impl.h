@@ -267,6 +267,12 @@ constexpr int MV_WAVES = 8;   // waves per GEMV workgroup (512 threads)
 // f1_store quantizes them and writes LDS. HP = ceil(NT·16·Gk / 512) half-blocks per thread.
 template <int HP> struct APre { float x[HP][16]; };
 
+// Half-block i of this thread in the fused F1 prologue: wave w takes the contiguous half-blocks
+// [64·HP·w, 64·HP·(w + 1)), lane l every 64th of them (pairs of a block on adjacent lanes). When a band
+// fills the workgroup (one token, one item per wave, J = NWV, HP = 2) these are exactly the 8 groups the
+// wave's own dot products read, so the prologue needs no workgroup barrier.
+template <int HP> JAMHIP_DEV int pro_half(int i) { return 64 * HP * (int) (threadIdx.x >> 6) + 64 * i + (int) (threadIdx.x & 63); }
+
 template <int NT, int HP, int NWV>
 JAMHIP_DEV void a_load(APre<HP>& pre, const float* __restrict__ a, int lda, int k, int Gk, int ntv) {
     // four 16-byte loads per half-block (the launcher checks a and lda for 16-byte alignment); a half past
@@ -275,7 +281,7 @@ JAMHIP_DEV void a_load(APre<HP>& pre, const float* __restrict__ a, int lda, int 
     const int halves = 16 * Gk, total = NT * halves, kh = k >> 4;
 #pragma unroll
     for (int i = 0; i < HP; i++) {
-        const int h0 = threadIdx.x + 64 * NWV * i, h = h0 < total ? h0 : total - 1;
+        const int h0 = pro_half<HP>(i), h = h0 < total ? h0 : total - 1;
         const int j = NT == 1 ? 0 : h / halves, hh = h - j * halves, jr = j < ntv ? j : ntv - 1;   // rows past ntv: clamp
         const bool in = hh < kh;   // clamp only; the zeroing happens in f1_store
         const float4* src = reinterpret_cast<const float4*>(a + (int64_t) jr * lda + 16 * (in ? hh : kh - 1));
@@ -297,7 +303,7 @@ JAMHIP_DEV void f1_store(const APre<HP>& pre, int k, int Gk, int8_t* lq, float* 
     const int halves = 16 * Gk, total = NT * halves;
 #pragma unroll
     for (int i = 0; i < HP; i++) {
-        const int h0 = threadIdx.x + 64 * NWV * i;
+        const int h0 = pro_half<HP>(i);
         const bool valid = h0 < total;
         const int h = valid ? h0 : 0;
         const int j = NT == 1 ? 0 : h / halves, hh = h - j * halves;
@@ -470,7 +476,7 @@ __global__ void __launch_bounds__(64 * NWV) mv_kernel(WeightView w, ActQ A, cons
     // Only waves that own at least one real half-block of the activations load and quantize them (the
     // others would only write the dummy slot); the condition is wave-uniform. Their loads go first in the
     // load queue and are kept there by the scheduler.
-    const bool pro = QF1 && wave * 64 < NT * 16 * Gk;
+    const bool pro = QF1 && wave * 64 * (QF1 ? HP : 1) < NT * 16 * Gk;
     APre<QF1 ? HP : 1> pre;
     FPre<STG ? SP : 1> fpre;
     if constexpr (QF1)
@@ -516,6 +522,8 @@ __global__ void __launch_bounds__(64 * NWV) mv_kernel(WeightView w, ActQ A, cons
         } else {   // F2: per-16 sums in the Σq-per-16 region (16 per group and token)
             stage_store<NT, SP, NWV>(fpre, k, Gk, lq, ld, reinterpret_cast<float*>(ls16));
         }
+        // a wave that quantized exactly the groups it reads (see pro_half) only waits for its own stores
+        const bool wave_local = QF1 && NT == 1 && ITEMS == 1 && HP == 2 && QB == 1 && J == NWV && Gk == 8 * J;
         if constexpr (FL == 1) {
             as = las;
             s16 = ls16;
@@ -525,7 +533,13 @@ __global__ void __launch_bounds__(64 * NWV) mv_kernel(WeightView w, ActQ A, cons
             as = reinterpret_cast<const float*>(ls16);
             ts = 16 * Gk;
         }
-        __syncthreads();
+        if (wave_local) {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        } else {
+            __syncthreads();
+        }
     }
 
 #pragma unroll
