@@ -50,6 +50,18 @@ def test_hand_assembled_file(tmp_path):
         assert g.find("w") == 0 and g.find("x") == -1
 
 
+def test_writer_matches_hand_assembled_bytes(tmp_path):
+    """qxotic_amd.gguf.write (used by the registry tests and bench.py) emits exactly the hand-assembled
+    image of test_hand_assembled_file: header, key, tensor entry, zero padding to 128, then the data."""
+    q8 = BY_NAME["Q8_0"].ggml
+    payload = bytes(range(136))
+    head = header(1, [kv_u32("general.alignment", 64)]) + tensor("w", [64, 2], q8, 0)
+    want = head + b"\0" * (128 - len(head)) + payload
+    off = G.write(tmp_path / "w.gguf", [("w", q8, (64, 2), np.frombuffer(payload, np.uint8))], alignment=64)
+    assert off == 128
+    assert (tmp_path / "w.gguf").read_bytes() == want
+
+
 def test_default_alignment_and_no_tensors(tmp_path):
     head = header(0, [])                            # 24 bytes, padded to 32
     with G.GGUF(image(tmp_path / "e.gguf", head, 24, b"")) as g:
