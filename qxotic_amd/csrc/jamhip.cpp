@@ -41,6 +41,28 @@ struct DevBuf {
     }
 };
 
+// Pinned host bounce buffer (hipHostMalloc): small copies from it are single DMA transfers, where a
+// pageable source is first staged by the runtime.
+struct HostBuf {
+    void* p = nullptr;
+    size_t cap = 0;
+    hipError_t ensure(size_t bytes) {
+        if (bytes <= cap) return hipSuccess;
+        if (p) (void) hipHostFree(p);
+        p = nullptr;
+        cap = 0;
+        const size_t want = bytes + bytes / 4;
+        hipError_t e = hipHostMalloc(&p, want, hipHostMallocDefault);
+        if (e == hipSuccess) cap = want;
+        return e;
+    }
+    void release() {
+        if (p) (void) hipHostFree(p);
+        p = nullptr;
+        cap = 0;
+    }
+};
+
 struct Pin {
     uintptr_t host;     // registry key: [host, host + span)
     int64_t span;
@@ -73,6 +95,7 @@ struct jamhip_ctx {
     std::mutex pin_mu;
     std::vector<Pin> pins;
     DevBuf act, gact, part, moe, a_stage, c_stage, w_raw, w_stage;
+    HostBuf a_host, c_host;   // jamhip_mm's pinned bounce buffers for A and C
 };
 
 namespace {
@@ -378,6 +401,8 @@ void jamhip_ctx_destroy(jamhip_ctx* ctx) {
     for (Pin& p : ctx->pins) (void) hipFree(p.dev);
     ctx->pins.clear();
     ctx->act.release();
+    ctx->a_host.release();
+    ctx->c_host.release();
     ctx->gact.release();
     ctx->part.release();
     ctx->moe.release();
@@ -403,18 +428,26 @@ jamhip_status jamhip_mm(jamhip_ctx* ctx, const void* w, int wt, int ldw, const v
     WeightView wv;
     if ((st = resolve_w(ctx, w, wt, ldw, m, k, &wv)) != JAMHIP_OK) return st;
     hipError_t e;
-    if ((e = ctx->a_stage.ensure((size_t) n * k * 4)) != hipSuccess) return hip_fail(ctx, e, "A staging alloc");
-    if ((e = ctx->c_stage.ensure((size_t) n * m * 4)) != hipSuccess) return hip_fail(ctx, e, "C staging alloc");
-    if ((e = hipMemcpy2DAsync(ctx->a_stage.p, (size_t) k * 4, a, (size_t) lda * 4, (size_t) k * 4, (size_t) n,
-                              hipMemcpyHostToDevice, ctx->stream)) != hipSuccess)
+    const size_t abytes = (size_t) n * k * 4, cbytes = (size_t) n * m * 4;
+    if ((e = ctx->a_stage.ensure(abytes)) != hipSuccess) return hip_fail(ctx, e, "A staging alloc");
+    if ((e = ctx->c_stage.ensure(cbytes)) != hipSuccess) return hip_fail(ctx, e, "C staging alloc");
+    if ((e = ctx->a_host.ensure(abytes)) != hipSuccess) return hip_fail(ctx, e, "A pinned alloc");
+    if ((e = ctx->c_host.ensure(cbytes)) != hipSuccess) return hip_fail(ctx, e, "C pinned alloc");
+    // A's rows packed into the pinned buffer (lda >= k), then one contiguous transfer
+    const float* af = static_cast<const float*>(a);
+    float* ah = static_cast<float*>(ctx->a_host.p);
+    for (int j = 0; j < n; j++) std::memcpy(ah + (size_t) j * k, af + (size_t) j * lda, (size_t) k * 4);
+    if ((e = hipMemcpyAsync(ctx->a_stage.p, ah, abytes, hipMemcpyHostToDevice, ctx->stream)) != hipSuccess)
         return hip_fail(ctx, e, "A upload");
     if ((st = compute(ctx, wt, wv, (const float*) ctx->a_stage.p, k, (float*) ctx->c_stage.p, m, m, n, k)) != JAMHIP_OK)
         return st;
-    // C columns [m, ldc) stay untouched (jam.h:131-138): a pitched copy of m floats per token.
-    if ((e = hipMemcpy2DAsync(c, (size_t) ldc * 4, ctx->c_stage.p, (size_t) m * 4, (size_t) m * 4, (size_t) n,
-                              hipMemcpyDeviceToHost, ctx->stream)) != hipSuccess)
+    if ((e = hipMemcpyAsync(ctx->c_host.p, ctx->c_stage.p, cbytes, hipMemcpyDeviceToHost, ctx->stream)) != hipSuccess)
         return hip_fail(ctx, e, "C download");
     if ((e = hipStreamSynchronize(ctx->stream)) != hipSuccess) return hip_fail(ctx, e, "stream sync");
+    // C columns [m, ldc) stay untouched (jam.h:131-138): m floats per token row
+    const float* ch = static_cast<const float*>(ctx->c_host.p);
+    float* cf = static_cast<float*>(c);
+    for (int j = 0; j < n; j++) std::memcpy(cf + (size_t) j * ldc, ch + (size_t) j * m, (size_t) m * 4);
     return JAMHIP_OK;
 }
 
