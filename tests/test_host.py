@@ -106,3 +106,17 @@ def test_geometry_and_quantizers_match_oracle(oracle):
     for dt in O.QUANT_TYPES:
         x = oracle.normal(123 + dt, (40, 512), 0.0, 0.02)
         assert np.array_equal(ggml.quantize(O.NAMES[dt], x), oracle.quantize(dt, x)), O.NAMES[dt]
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU: --gpus N > 1 (or a multi-rank launch) exits 2 with a message, before
+    touching any device."""
+    import os
+    import subprocess
+    import sys
+    bench = ROOT / "bench.py"
+    for argv, env in ((["--gpus", "2"], {}), (["--gpus", "1"], {"WORLD_SIZE": "2"})):
+        r = subprocess.run([sys.executable, str(bench), *argv], capture_output=True, text=True, timeout=120,
+                           env={**os.environ, **env})
+        assert r.returncode == 2, (argv, env, r.stderr[-400:])
+        assert "one GPU" in r.stderr and r.stdout == ""
