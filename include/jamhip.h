@@ -22,6 +22,12 @@
  *               rewriting a pinned range.
  *   streams   : a context owns one HIP stream and its scratch: a SERIAL stream, as a jam_ctx is
  *               (jam.h:16-20). A concurrent call on a busy context returns JAMHIP_EBUSY.
+ *   ctx NULL  : every entry point that takes a context uses the process-global one when ctx == NULL, as
+ *               jam_mm(NULL, ...) does (jam.h:128, jam.c:765-768): created on first use on the current
+ *               device, released only by jamhip_global_destroy.
+ *   scratch   : device scratch a context hands to kernels is never freed or moved while the context
+ *               lives (a grown buffer's old allocation is kept until jamhip_ctx_destroy), so a HIP graph
+ *               captured around a call stays valid after later, larger calls.
  */
 
 #include <stddef.h>
@@ -56,10 +62,17 @@ int jamhip_device_available(void);
 jamhip_ctx* jamhip_ctx_create(int device);
 void        jamhip_ctx_destroy(jamhip_ctx* ctx);
 
+/* Destroy the process-global context (the one ctx == NULL selects) with its pins, scratch and stream.
+ * A no-op if it was never created; a later NULL-context call creates it again. Not run automatically:
+ * call it for a clean teardown before unloading the library or at process shutdown. Not safe concurrently
+ * with calls on the global context. Mirrors jam_global_destroy (jam.h:149-155). */
+void        jamhip_global_destroy(void);
+
 /* The device architecture string ("gfx950"); stands in for jam_active_isa/jam_isa_name (jam.h:146,92). */
 const char* jamhip_ctx_arch(const jamhip_ctx* ctx);
 
-/* Last error message of `ctx` (or of the last failed create when ctx == NULL). Never NULL. */
+/* Last error message of `ctx`; for ctx == NULL, of this thread's last failed create or last failed call on
+ * the global context. Never NULL; valid until this thread's next jamhip_last_error call. */
 const char* jamhip_last_error(const jamhip_ctx* ctx);
 
 /* The matmul, host pointers (jam_mm, jam.h:139-143; FFM descriptor NativeJAM.java:225-230).

@@ -2,7 +2,9 @@
 CPU fallback anywhere in this package."""
 from __future__ import annotations
 
+import atexit
 import ctypes as C
+import weakref
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "lib" / "libjamhip.so"
@@ -15,6 +17,7 @@ SIGNATURES = [
     ("jamhip_device_available", _I, []),
     ("jamhip_ctx_create", _VP, [_I]),
     ("jamhip_ctx_destroy", None, [_VP]),
+    ("jamhip_global_destroy", None, []),
     ("jamhip_ctx_arch", C.c_char_p, [_VP]),
     ("jamhip_last_error", C.c_char_p, [_VP]),
     ("jamhip_mm", _I, [_VP, _VP, _I, _I, _VP, _I, _I, _VP, _I, _I, _I, _I, _I]),
@@ -59,6 +62,37 @@ def _adopt_torch_runtime() -> None:
         pass
 
 
+_LIVE: "weakref.WeakSet" = weakref.WeakSet()   # objects holding contexts or mappings: released at exit
+
+
+def register_for_teardown(obj) -> None:
+    """obj.close() runs at interpreter exit, before any runtime finalizer (see on_exit)."""
+    _LIVE.add(obj)
+
+
+def on_exit() -> None:
+    """Deterministic teardown before the interpreter and the HIP runtime finalize: every live HipJAM context
+    is destroyed (its pins, scratch and stream released), then every open GGUF mapping is closed, then the
+    library's process-global context. Registered with atexit when the library is first loaded; objects'
+    __del__ make no native call once this has run."""
+    if on_exit.done or _lib is None:
+        return
+    on_exit.done = True
+    objs = list(_LIVE)
+    for o in sorted(objs, key=lambda o: getattr(o, "TEARDOWN_ORDER", 0)):
+        try:
+            o.close()
+        except Exception:
+            pass
+    try:
+        _lib.jamhip_global_destroy()
+    except Exception:
+        pass
+
+
+on_exit.done = False
+
+
 def lib() -> C.CDLL:
     """The loaded library; raises RuntimeError if it has not been built."""
     global _lib
@@ -72,4 +106,5 @@ def lib() -> C.CDLL:
             fn.restype = res
             fn.argtypes = args
         _lib = L
+        atexit.register(on_exit)
     return _lib

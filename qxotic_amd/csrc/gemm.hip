@@ -327,6 +327,8 @@ static hipError_t gemm_go(const WeightView& w, const ActQ& A, int k, int m, int 
     return hipGetLastError();
 }
 
+bool gemm_covers(int dt) { return dt == Q4_K || dt == Q6_K || dt == Q8_0 || dt == Q4_0 || dt == MXFP4; }
+
 hipError_t launch_gemm(int dt, const WeightView& w, const ActQ& A, int k, int m, int n, float* c, int ldc,
                        hipStream_t st, const Epi& ep) {
     switch (dt) {

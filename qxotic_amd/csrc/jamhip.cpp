@@ -21,25 +21,41 @@ using namespace jamhip;
 
 namespace {
 
-struct DevBuf {
+// Device buffer of a context, grown on demand. For the scratch that kernels of jamhip_mm_device and the
+// grouped / MoE entry points use (RETIRE = true), a grown buffer's old allocation is retired, not freed: a
+// HIP graph captured around an earlier call keeps that address, so every scratch address a context ever
+// handed to a kernel stays valid until jamhip_ctx_destroy (growth is geometric, so the retired total stays
+// below four times the current size). Staging for host copies (RETIRE = false) is freed on growth.
+template <bool RETIRE> struct DevBufT {
     void* p = nullptr;
     size_t cap = 0;
+    std::vector<void*> retired;
     hipError_t ensure(size_t bytes) {
         if (bytes <= cap) return hipSuccess;
-        if (p) (void) hipFree(p);
-        p = nullptr;
-        cap = 0;
         size_t want = bytes + bytes / 4;
-        hipError_t e = hipMalloc(&p, want);
-        if (e == hipSuccess) cap = want;
-        return e;
+        void* q = nullptr;
+        if (!RETIRE && p) {
+            (void) hipFree(p);
+            p = nullptr;
+            cap = 0;
+        }
+        hipError_t e = hipMalloc(&q, want);
+        if (e != hipSuccess) return e;
+        if (p) retired.push_back(p);
+        p = q;
+        cap = want;
+        return hipSuccess;
     }
     void release() {
+        for (void* r : retired) (void) hipFree(r);
+        retired.clear();
         if (p) (void) hipFree(p);
         p = nullptr;
         cap = 0;
     }
 };
+using DevBuf = DevBufT<true>;
+using StageBuf = DevBufT<false>;
 
 // Pinned host bounce buffer (hipHostMalloc): small copies from it are single DMA transfers, where a
 // pageable source is first staged by the runtime.
@@ -77,7 +93,11 @@ constexpr int64_t align256(int64_t v) { return (v + 255) & ~int64_t(255); }
 
 bool supported_w(int dt) { return dt == Q8_0 || dt == Q4_0 || dt == Q4_K || dt == Q6_K || dt == MXFP4; }
 
-thread_local std::string g_create_error = "";
+// Error text of calls with no context of their own: a failed jamhip_ctx_create, or a failed call made with
+// ctx == NULL (the process-global context). Per thread; jamhip_last_error(NULL) returns it.
+thread_local char g_null_error[512] = "";
+
+void set_null_error(const std::string& s) { snprintf(g_null_error, sizeof g_null_error, "%s", s.c_str()); }
 
 }  // namespace
 
@@ -90,19 +110,30 @@ struct jamhip_ctx {
     hipStream_t own = nullptr;
     hipStream_t stream = nullptr;
     std::atomic<int> busy{0};
+    std::mutex err_mu;   // err is written by a failing call while another thread may read or write it
     std::string err;
     char arch[64] = {0};
-    std::mutex pin_mu;
+    mutable std::mutex pin_mu;
     std::vector<Pin> pins;
-    DevBuf act, gact, part, moe, a_stage, c_stage, w_raw, w_stage;
+    int64_t pinned_bytes = 0;   // sum of pins[].bytes, under pin_mu
+    DevBuf act, gact, part, moe;              // kernel scratch (addresses may be captured in graphs)
+    StageBuf a_stage, c_stage, w_raw, w_stage;   // staging of host copies
     HostBuf a_host, c_host;   // jamhip_mm's pinned bounce buffers for A and C
 };
 
 namespace {
 
 jamhip_status fail(jamhip_ctx* ctx, jamhip_status st, const std::string& msg) {
-    if (ctx) ctx->err = msg;
+    if (ctx) {
+        std::lock_guard<std::mutex> lk(ctx->err_mu);
+        ctx->err = msg;
+    }
     return st;
+}
+
+std::string error_of(jamhip_ctx* ctx) {
+    std::lock_guard<std::mutex> lk(ctx->err_mu);
+    return ctx->err;
 }
 
 jamhip_status hip_fail(jamhip_ctx* ctx, hipError_t e, const char* what) {
@@ -231,22 +262,54 @@ static int gemm_min_n(int dt, int k) {
     return x < 8 ? 8 : x;
 }
 
+// Where compute() takes its device scratch: the context's growable buffers, or (the allocation-free entry
+// point) consecutive 256-byte-aligned pieces of one fixed region. Every branch of compute() takes all its
+// pieces before its first launch, so a call that does not fit the fixed region queues nothing.
+struct Scratch {
+    jamhip_ctx* ctx;
+    uint8_t* fixed = nullptr;   // null: the context's DevBufs
+    size_t cap = 0, used = 0;
+    size_t over = 0;            // fixed mode: the bytes a refused piece would have needed in total
+    hipError_t get(DevBuf& b, size_t bytes, void** out) {
+        if (!fixed) {
+            const hipError_t e = b.ensure(bytes);
+            *out = b.p;
+            return e;
+        }
+        const size_t at = (used + 255) & ~(size_t) 255;
+        if (at + bytes > cap) {
+            over = at + bytes;
+            return hipErrorOutOfMemory;
+        }
+        *out = fixed + at;
+        used = at + bytes;
+        return hipSuccess;
+    }
+};
+
+jamhip_status scratch_fail(jamhip_ctx* ctx, const Scratch& sc, hipError_t e, const char* what) {
+    if (sc.fixed && sc.over)
+        return fail(ctx, JAMHIP_EUNSUPPORTED,
+                    std::string(what) + ": the call needs " + std::to_string(sc.over) +
+                        " bytes of scratch, above the static scratch maximum of " + std::to_string(sc.cap) +
+                        " bytes (use jamhip_mm_device)");
+    return hip_fail(ctx, e, what);
+}
+
 // Quantize A (device, f32 [n][lda]) and run the matmul into C (device, [n][ldc]). Decode-sized calls
 // with k < 8192 are one fused launch and touch no scratch (safe under stream capture once W is pinned);
 // from k = 8192 the decode kernels split K and sum the slices from the context's split buffer.
-jamhip_status compute(jamhip_ctx* ctx, int dt, const WeightView& wv, const float* a, int lda, float* c, int ldc,
-                      int m, int n, int k, const Epi& ep = Epi{}) {
+jamhip_status compute(jamhip_ctx* ctx, Scratch& sc, int dt, const WeightView& wv, const float* a, int lda, float* c,
+                      int ldc, int m, int n, int k, const Epi& ep = Epi{}) {
     hipError_t e;
     float* gpart = nullptr;   // the decode kernels' K-split partials
     auto decode_part = [&](int rows) -> hipError_t {
         const size_t pf = gemv_split_floats(k, rows, n);
         if (pf == 0) return hipSuccess;
-        const hipError_t r = ctx->part.ensure(pf * sizeof(float));
-        gpart = (float*) ctx->part.p;
-        return r;
+        return sc.get(ctx->part, pf * sizeof(float), (void**) &gpart);
     };
     if (gemv_fusable(n, k, a, lda)) {
-        if ((e = decode_part(m)) != hipSuccess) return hip_fail(ctx, e, "gemv split scratch alloc");
+        if ((e = decode_part(m)) != hipSuccess) return scratch_fail(ctx, sc, e, "gemv split scratch");
         if ((e = launch_gemv(dt, 1, wv, ActQ{}, a, lda, k, m, n, c, ldc, ctx->stream, gpart, ep)) != hipSuccess)
             return hip_fail(ctx, e, "gemv launch");
         return JAMHIP_OK;
@@ -256,16 +319,15 @@ jamhip_status compute(jamhip_ctx* ctx, int dt, const WeightView& wv, const float
     const int m16 = m - m % 16;
     if (n >= mma_min_n(dt, m, k) && m16 > 0 && mma_path(dt, k, wv)) {
         GemmAct G;
-        if ((e = ctx->gact.ensure(gemm_act_bytes(dt, n, k))) != hipSuccess)
-            return hip_fail(ctx, e, "gemm activation scratch alloc");
-        if ((e = launch_gemm_prep(dt, a, lda, n, k, ctx->gact.p, &G, ctx->stream)) != hipSuccess)
-            return hip_fail(ctx, e, "gemm prep launch");
+        void* gact = nullptr;
         float* part = nullptr;
-        if (const size_t pf = gemm_mma_split_floats(dt, k, m16, n)) {
-            if ((e = ctx->part.ensure(pf * sizeof(float))) != hipSuccess)
-                return hip_fail(ctx, e, "gemm split scratch alloc");
-            part = (float*) ctx->part.p;
-        }
+        if ((e = sc.get(ctx->gact, gemm_act_bytes(dt, n, k), &gact)) != hipSuccess)
+            return scratch_fail(ctx, sc, e, "gemm activation scratch");
+        if (const size_t pf = gemm_mma_split_floats(dt, k, m16, n))
+            if ((e = sc.get(ctx->part, pf * sizeof(float), (void**) &part)) != hipSuccess)
+                return scratch_fail(ctx, sc, e, "gemm split scratch");
+        if ((e = launch_gemm_prep(dt, a, lda, n, k, gact, &G, ctx->stream)) != hipSuccess)
+            return hip_fail(ctx, e, "gemm prep launch");
         if ((e = launch_gemm_mma(dt, wv, G, k, m16, n, c, ldc, ctx->stream, part, ep)) != hipSuccess)
             return hip_fail(ctx, e, "gemm launch");
         if ((e = launch_rows_float(dt, wv, a, lda, k, m16, m - m16, n, c, ldc, ctx->stream, ep)) != hipSuccess)
@@ -274,33 +336,40 @@ jamhip_status compute(jamhip_ctx* ctx, int dt, const WeightView& wv, const float
     }
     const int64_t nb = k / 32;
     const int64_t qb = align256((int64_t) n * k), db = align256(n * nb * 4), sb = align256((int64_t) n * (k / 16) * 4);
-    if ((e = ctx->act.ensure((size_t) (qb + db + 2 * sb))) != hipSuccess)
-        return hip_fail(ctx, e, "activation scratch alloc");
-    uint8_t* base = (uint8_t*) ctx->act.p;
+    uint8_t* base = nullptr;
+    if ((e = sc.get(ctx->act, (size_t) (qb + db + 2 * sb), (void**) &base)) != hipSuccess)
+        return scratch_fail(ctx, sc, e, "activation scratch");
     int8_t* q = (int8_t*) base;
     float* d = (float*) (base + qb);
     float* s = (float*) (base + qb + db);
     int* s16 = (int*) (base + qb + db + sb);
     const ActQ A{q, d, s, s16};
     if (n < 8) {
+        if ((e = decode_part(m)) != hipSuccess) return scratch_fail(ctx, sc, e, "gemv split scratch");
         if ((e = launch_quant_f1(a, lda, n, k, q, d, s, s16, ctx->stream)) != hipSuccess)
             return hip_fail(ctx, e, "quant_f1 launch");
-        if ((e = decode_part(m)) != hipSuccess) return hip_fail(ctx, e, "gemv split scratch alloc");
         if ((e = launch_gemv(dt, 1, wv, A, nullptr, 0, k, m, n, c, ldc, ctx->stream, gpart, ep)) != hipSuccess)
             return hip_fail(ctx, e, "gemv launch");
         return JAMHIP_OK;
     }
     if (m16 > 0) {
+        const bool gemm = n >= gemm_min_n(dt, k) && gemm_covers(dt);
+        if (!gemm && (e = decode_part(m16)) != hipSuccess) return scratch_fail(ctx, sc, e, "gemv split scratch");
         if ((e = launch_quant_f2(a, lda, n, k, q, d, s, ctx->stream)) != hipSuccess)
             return hip_fail(ctx, e, "quant_f2 launch");
-        e = n >= gemm_min_n(dt, k) ? launch_gemm(dt, wv, A, k, m16, n, c, ldc, ctx->stream, ep) : hipErrorNotSupported;
-        if (e == hipErrorNotSupported && (e = decode_part(m16)) == hipSuccess)
-            e = launch_gemv(dt, 2, wv, A, nullptr, 0, k, m16, n, c, ldc, ctx->stream, gpart, ep);
+        e = gemm ? launch_gemm(dt, wv, A, k, m16, n, c, ldc, ctx->stream, ep)
+                 : launch_gemv(dt, 2, wv, A, nullptr, 0, k, m16, n, c, ldc, ctx->stream, gpart, ep);
         if (e != hipSuccess) return hip_fail(ctx, e, "matmul launch");
     }
     if ((e = launch_rows_float(dt, wv, a, lda, k, m16, m - m16, n, c, ldc, ctx->stream, ep)) != hipSuccess)
         return hip_fail(ctx, e, "tail rows launch");
     return JAMHIP_OK;
+}
+
+jamhip_status compute(jamhip_ctx* ctx, int dt, const WeightView& wv, const float* a, int lda, float* c, int ldc,
+                      int m, int n, int k, const Epi& ep = Epi{}) {
+    Scratch sc{ctx};
+    return compute(ctx, sc, dt, wv, a, lda, c, ldc, m, n, k, ep);
 }
 
 // Pin rows [0, m) of the host tensor at w (caller holds the Busy guard, device current). The staging
@@ -334,6 +403,7 @@ jamhip_status pin_range(jamhip_ctx* ctx, const void* w, int wt, int ldw, int64_t
     auto it = std::lower_bound(ctx->pins.begin(), ctx->pins.end(), host,
                                [](const Pin& pin, uintptr_t v) { return pin.host < v; });
     ctx->pins.insert(it, Pin{host, span, wt, ldw, m, G, dev, sc, qsz + ssz});
+    ctx->pinned_bytes += qsz + ssz;
     return JAMHIP_OK;
 }
 
@@ -345,80 +415,26 @@ bool evict_at(jamhip_ctx* ctx, uintptr_t host) {
     if (it == ctx->pins.end() || it->host != host) return false;
     (void) hipStreamSynchronize(ctx->stream);
     (void) hipFree(it->dev);
+    ctx->pinned_bytes -= it->bytes;
     ctx->pins.erase(it);
     return true;
 }
 
 }  // namespace
 
-extern "C" {
+namespace {
 
-int jamhip_device_available(void) {
-    if (env_true("JAM_HIP_DISABLE")) return 0;
-    int n = 0;
-    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return 0;
-    hipDeviceProp_t prop;
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&prop, dev) != hipSuccess) return 0;
-    return strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : 0;
-}
-
-jamhip_ctx* jamhip_ctx_create(int device) {
-    if (env_true("JAM_HIP_DISABLE")) {
-        g_create_error = "disabled by JAM_HIP_DISABLE";
-        return nullptr;
+// Synchronizes the stream when a call returns early after queueing a copy from a pinned bounce buffer, so
+// the next call may reuse or free that buffer.
+struct SyncOnError {
+    jamhip_ctx* ctx;
+    bool armed = false;
+    ~SyncOnError() {
+        if (armed) (void) hipStreamSynchronize(ctx->stream);
     }
-    int dev = device;
-    if (dev < 0 && hipGetDevice(&dev) != hipSuccess) {
-        g_create_error = "no HIP device";
-        return nullptr;
-    }
-    hipDeviceProp_t prop;
-    if (hipSetDevice(dev) != hipSuccess || hipGetDeviceProperties(&prop, dev) != hipSuccess) {
-        g_create_error = "hipSetDevice/hipGetDeviceProperties failed";
-        return nullptr;
-    }
-    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
-        g_create_error = std::string("unsupported device architecture ") + prop.gcnArchName + " (need gfx950)";
-        return nullptr;
-    }
-    auto* ctx = new jamhip_ctx();
-    ctx->device = dev;
-    snprintf(ctx->arch, sizeof ctx->arch, "%s", prop.gcnArchName);
-    if (hipStreamCreate(&ctx->own) != hipSuccess) {
-        g_create_error = "hipStreamCreate failed";
-        delete ctx;
-        return nullptr;
-    }
-    ctx->stream = ctx->own;
-    return ctx;
-}
+};
 
-void jamhip_ctx_destroy(jamhip_ctx* ctx) {
-    if (!ctx) return;
-    (void) hipSetDevice(ctx->device);
-    (void) hipStreamSynchronize(ctx->stream);
-    for (Pin& p : ctx->pins) (void) hipFree(p.dev);
-    ctx->pins.clear();
-    ctx->act.release();
-    ctx->a_host.release();
-    ctx->c_host.release();
-    ctx->gact.release();
-    ctx->part.release();
-    ctx->moe.release();
-    ctx->a_stage.release();
-    ctx->c_stage.release();
-    ctx->w_raw.release();
-    ctx->w_stage.release();
-    if (ctx->own) (void) hipStreamDestroy(ctx->own);
-    delete ctx;
-}
-
-const char* jamhip_ctx_arch(const jamhip_ctx* ctx) { return ctx ? ctx->arch : ""; }
-
-const char* jamhip_last_error(const jamhip_ctx* ctx) { return ctx ? ctx->err.c_str() : g_create_error.c_str(); }
-
-jamhip_status jamhip_mm(jamhip_ctx* ctx, const void* w, int wt, int ldw, const void* a, int at, int lda, void* c,
+jamhip_status mm_impl(jamhip_ctx* ctx, const void* w, int wt, int ldw, const void* a, int at, int lda, void* c,
                         int ct, int ldc, int m, int n, int k) {
     jamhip_status st = validate(ctx, w, wt, ldw, a, at, lda, c, ct, ldc, m, n, k);
     if (st != JAMHIP_OK) return st;
@@ -437,12 +453,15 @@ jamhip_status jamhip_mm(jamhip_ctx* ctx, const void* w, int wt, int ldw, const v
     const float* af = static_cast<const float*>(a);
     float* ah = static_cast<float*>(ctx->a_host.p);
     for (int j = 0; j < n; j++) std::memcpy(ah + (size_t) j * k, af + (size_t) j * lda, (size_t) k * 4);
+    SyncOnError pending{ctx};
     if ((e = hipMemcpyAsync(ctx->a_stage.p, ah, abytes, hipMemcpyHostToDevice, ctx->stream)) != hipSuccess)
         return hip_fail(ctx, e, "A upload");
+    pending.armed = true;
     if ((st = compute(ctx, wt, wv, (const float*) ctx->a_stage.p, k, (float*) ctx->c_stage.p, m, m, n, k)) != JAMHIP_OK)
         return st;
     if ((e = hipMemcpyAsync(ctx->c_host.p, ctx->c_stage.p, cbytes, hipMemcpyDeviceToHost, ctx->stream)) != hipSuccess)
         return hip_fail(ctx, e, "C download");
+    pending.armed = false;
     if ((e = hipStreamSynchronize(ctx->stream)) != hipSuccess) return hip_fail(ctx, e, "stream sync");
     // C columns [m, ldc) stay untouched (jam.h:131-138): m floats per token row
     const float* ch = static_cast<const float*>(ctx->c_host.p);
@@ -451,7 +470,7 @@ jamhip_status jamhip_mm(jamhip_ctx* ctx, const void* w, int wt, int ldw, const v
     return JAMHIP_OK;
 }
 
-jamhip_status jamhip_mm_device(jamhip_ctx* ctx, const void* w, int wt, int ldw, const void* a_dev, int at, int lda,
+jamhip_status mm_device_impl(jamhip_ctx* ctx, const void* w, int wt, int ldw, const void* a_dev, int at, int lda,
                                void* c_dev, int ct, int ldc, int m, int n, int k) {
     jamhip_status st = validate(ctx, w, wt, ldw, a_dev, at, lda, c_dev, ct, ldc, m, n, k);
     if (st != JAMHIP_OK) return st;
@@ -463,7 +482,7 @@ jamhip_status jamhip_mm_device(jamhip_ctx* ctx, const void* w, int wt, int ldw, 
     return compute(ctx, wt, wv, (const float*) a_dev, lda, (float*) c_dev, ldc, m, n, k);
 }
 
-jamhip_status jamhip_mm_device_ex(jamhip_ctx* ctx, const void* w, int wt, int ldw, const void* a_dev, int at, int lda,
+jamhip_status mm_device_ex_impl(jamhip_ctx* ctx, const void* w, int wt, int ldw, const void* a_dev, int at, int lda,
                                   void* c_dev, int ct, int ldc, int m, int n, int k, const void* bias_dev,
                                   int accumulate) {
     jamhip_status st = validate(ctx, w, wt, ldw, a_dev, at, lda, c_dev, ct, ldc, m, n, k);
@@ -480,7 +499,7 @@ jamhip_status jamhip_mm_device_ex(jamhip_ctx* ctx, const void* w, int wt, int ld
     return compute(ctx, wt, wv, (const float*) a_dev, lda, (float*) c_dev, ldc, m, n, k, ep);
 }
 
-jamhip_status jamhip_glu_device(jamhip_ctx* ctx, int act, void* gate_dev, int ldg, const void* up_dev, int ldu,
+jamhip_status glu_device_impl(jamhip_ctx* ctx, int act, void* gate_dev, int ldg, const void* up_dev, int ldu,
                                 int rows, int cols) {
     if (!ctx) return JAMHIP_EINVAL;
     if (!gate_dev || !up_dev) return fail(ctx, JAMHIP_EINVAL, "glu: null operand");
@@ -494,7 +513,7 @@ jamhip_status jamhip_glu_device(jamhip_ctx* ctx, int act, void* gate_dev, int ld
     return e == hipSuccess ? JAMHIP_OK : hip_fail(ctx, e, "glu launch");
 }
 
-jamhip_status jamhip_weight_pin(jamhip_ctx* ctx, const void* w, int wt, int ldw, int m) {
+jamhip_status weight_pin_impl(jamhip_ctx* ctx, const void* w, int wt, int ldw, int m) {
     if (!ctx) return JAMHIP_EINVAL;
     if (!w || m <= 0 || ldw <= 0) return fail(ctx, JAMHIP_EINVAL, "pin: null weight or empty shape");
     if (!supported_w(wt)) return fail(ctx, JAMHIP_EUNSUPPORTED, "pin: weight dtype not supported");
@@ -505,7 +524,7 @@ jamhip_status jamhip_weight_pin(jamhip_ctx* ctx, const void* w, int wt, int ldw,
     return pin_range(ctx, w, wt, ldw, m, false);
 }
 
-jamhip_status jamhip_weight_evict(jamhip_ctx* ctx, const void* w) {
+jamhip_status weight_evict_impl(jamhip_ctx* ctx, const void* w) {
     if (!ctx || !w) return JAMHIP_EINVAL;
     Busy guard(ctx);
     if (!guard.ok) return fail(ctx, JAMHIP_EBUSY, "context busy");
@@ -514,14 +533,8 @@ jamhip_status jamhip_weight_evict(jamhip_ctx* ctx, const void* w) {
     return JAMHIP_OK;
 }
 
-int64_t jamhip_weight_bytes(const jamhip_ctx* ctx) {
-    if (!ctx) return 0;
-    int64_t s = 0;
-    for (const Pin& p : ctx->pins) s += p.bytes;
-    return s;
-}
 
-jamhip_status jamhip_quantize_device(jamhip_ctx* ctx, int flavour, const void* a_dev, int lda, int n, int k,
+jamhip_status quantize_device_impl(jamhip_ctx* ctx, int flavour, const void* a_dev, int lda, int n, int k,
                                      void* q_dev, void* d_dev, void* s_dev) {
     if (!ctx) return JAMHIP_EINVAL;
     if (!a_dev || !q_dev || !d_dev || !s_dev) return fail(ctx, JAMHIP_EINVAL, "quantize: null pointer");
@@ -543,14 +556,7 @@ jamhip_status jamhip_quantize_device(jamhip_ctx* ctx, int flavour, const void* a
     return e == hipSuccess ? JAMHIP_OK : hip_fail(ctx, e, "quantize launch");
 }
 
-jamhip_status jamhip_mm_grouped(jamhip_ctx* ctx, const void* w, int wt, int ldw, int m, int n_experts,
-                                const void* counts_dev, const void* a_dev, int at, int lda, void* c_dev, int ct,
-                                int ldc, int k, int rows_cap, void* offsets_dev) {
-    return jamhip_mm_grouped_ex(ctx, w, wt, ldw, m, n_experts, counts_dev, a_dev, at, lda, c_dev, ct, ldc, k, rows_cap,
-                                offsets_dev, nullptr);
-}
-
-jamhip_status jamhip_mm_grouped_ex(jamhip_ctx* ctx, const void* w, int wt, int ldw, int m, int n_experts,
+jamhip_status mm_grouped_ex_impl(jamhip_ctx* ctx, const void* w, int wt, int ldw, int m, int n_experts,
                                    const void* counts_dev, const void* a_dev, int at, int lda, void* c_dev, int ct,
                                    int ldc, int k, int rows_cap, void* offsets_dev, const void* bias_dev) {
     if (!ctx) return JAMHIP_EINVAL;
@@ -632,7 +638,7 @@ jamhip_status jamhip_mm_grouped_ex(jamhip_ctx* ctx, const void* w, int wt, int l
     return JAMHIP_OK;
 }
 
-jamhip_status jamhip_moe_route(jamhip_ctx* ctx, const void* route_expert_dev, int seq, int topk, int n_experts,
+jamhip_status moe_route_impl(jamhip_ctx* ctx, const void* route_expert_dev, int seq, int topk, int n_experts,
                                void* counts_dev, void* offsets_dev, void* slot_route_dev, void* route_slot_dev) {
     if (!ctx) return JAMHIP_EINVAL;
     if (!route_expert_dev || !counts_dev || !offsets_dev || !slot_route_dev || !route_slot_dev)
@@ -648,7 +654,7 @@ jamhip_status jamhip_moe_route(jamhip_ctx* ctx, const void* route_expert_dev, in
     return e == hipSuccess ? JAMHIP_OK : hip_fail(ctx, e, "route launch");
 }
 
-jamhip_status jamhip_moe_gather(jamhip_ctx* ctx, const void* x_dev, int ldx, const void* slot_route_dev,
+jamhip_status moe_gather_impl(jamhip_ctx* ctx, const void* x_dev, int ldx, const void* slot_route_dev,
                                 const void* offsets_dev, int n_experts, int seq, int topk, int dim, void* g_dev,
                                 int ldg) {
     if (!ctx) return JAMHIP_EINVAL;
@@ -664,7 +670,7 @@ jamhip_status jamhip_moe_gather(jamhip_ctx* ctx, const void* x_dev, int ldx, con
     return e == hipSuccess ? JAMHIP_OK : hip_fail(ctx, e, "gather launch");
 }
 
-jamhip_status jamhip_moe_combine(jamhip_ctx* ctx, const void* y_dev, int ldy, const void* route_expert_dev,
+jamhip_status moe_combine_impl(jamhip_ctx* ctx, const void* y_dev, int ldy, const void* route_expert_dev,
                                  const void* route_prob_dev, const void* route_slot_dev, int seq, int topk,
                                  int n_experts, int dim, void* out_dev, int ldo) {
     if (!ctx) return JAMHIP_EINVAL;
@@ -682,19 +688,248 @@ jamhip_status jamhip_moe_combine(jamhip_ctx* ctx, const void* y_dev, int ldy, co
     return e == hipSuccess ? JAMHIP_OK : hip_fail(ctx, e, "combine launch");
 }
 
-jamhip_status jamhip_ctx_set_stream(jamhip_ctx* ctx, void* stream) {
+jamhip_status ctx_set_stream_impl(jamhip_ctx* ctx, void* stream) {
     if (!ctx) return JAMHIP_EINVAL;
+    Busy guard(ctx);   // the stream is read by every call in flight on this context
+    if (!guard.ok) return fail(ctx, JAMHIP_EBUSY, "context busy");
     ctx->stream = stream ? (hipStream_t) stream : ctx->own;
     return JAMHIP_OK;
 }
 
-void* jamhip_ctx_stream(const jamhip_ctx* ctx) { return ctx ? (void*) ctx->stream : nullptr; }
-
-jamhip_status jamhip_ctx_synchronize(jamhip_ctx* ctx) {
+jamhip_status ctx_synchronize_impl(jamhip_ctx* ctx) {
     if (!ctx) return JAMHIP_EINVAL;
     (void) hipSetDevice(ctx->device);
     hipError_t e = hipStreamSynchronize(ctx->stream);
     return e == hipSuccess ? JAMHIP_OK : hip_fail(ctx, e, "sync");
+}
+
+}  // namespace
+
+namespace {
+
+jamhip_ctx* create_ctx(int device, std::string* err) {
+    if (env_true("JAM_HIP_DISABLE")) {
+        *err = "disabled by JAM_HIP_DISABLE";
+        return nullptr;
+    }
+    int dev = device;
+    if (dev < 0 && hipGetDevice(&dev) != hipSuccess) {
+        *err = "no HIP device";
+        return nullptr;
+    }
+    hipDeviceProp_t prop;
+    if (hipSetDevice(dev) != hipSuccess || hipGetDeviceProperties(&prop, dev) != hipSuccess) {
+        *err = "hipSetDevice/hipGetDeviceProperties failed";
+        return nullptr;
+    }
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        *err = std::string("unsupported device architecture ") + prop.gcnArchName + " (need gfx950)";
+        return nullptr;
+    }
+    auto* ctx = new jamhip_ctx();
+    ctx->device = dev;
+    snprintf(ctx->arch, sizeof ctx->arch, "%s", prop.gcnArchName);
+    if (hipStreamCreate(&ctx->own) != hipSuccess) {
+        *err = "hipStreamCreate failed";
+        delete ctx;
+        return nullptr;
+    }
+    ctx->stream = ctx->own;
+    return ctx;
+}
+
+void destroy_ctx(jamhip_ctx* ctx) {
+    (void) hipSetDevice(ctx->device);
+    (void) hipStreamSynchronize(ctx->stream);
+    for (Pin& p : ctx->pins) (void) hipFree(p.dev);
+    ctx->pins.clear();
+    ctx->act.release();
+    ctx->a_host.release();
+    ctx->c_host.release();
+    ctx->gact.release();
+    ctx->part.release();
+    ctx->moe.release();
+    ctx->a_stage.release();
+    ctx->c_stage.release();
+    ctx->w_raw.release();
+    ctx->w_stage.release();
+    if (ctx->own) (void) hipStreamDestroy(ctx->own);
+    delete ctx;
+}
+
+// The process-global context that ctx == NULL selects (jam.c:420-437, 765-768: created lazily on first use,
+// on the current device; never destroyed implicitly, only by jamhip_global_destroy).
+std::mutex g_global_mu;
+jamhip_ctx* g_global = nullptr;
+
+jamhip_ctx* global_ctx() {
+    std::lock_guard<std::mutex> lk(g_global_mu);
+    if (!g_global) {
+        std::string err;
+        g_global = create_ctx(-1, &err);
+        if (!g_global) set_null_error("global context: " + err);
+    }
+    return g_global;
+}
+
+// Runs f on ctx, or on the process-global context when ctx is NULL; a failure there records its message for
+// jamhip_last_error(NULL).
+template <class F> jamhip_status on_ctx(jamhip_ctx* ctx, F&& f) {
+    if (ctx) return f(ctx);
+    jamhip_ctx* g = global_ctx();
+    if (!g) return JAMHIP_EINVAL;
+    const jamhip_status st = f(g);
+    if (st != JAMHIP_OK) set_null_error(error_of(g));
+    return st;
+}
+
+}  // namespace
+
+extern "C" {
+
+int jamhip_device_available(void) {
+    if (env_true("JAM_HIP_DISABLE")) return 0;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return 0;
+    hipDeviceProp_t prop;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&prop, dev) != hipSuccess) return 0;
+    return strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : 0;
+}
+
+jamhip_ctx* jamhip_ctx_create(int device) {
+    std::string err;
+    jamhip_ctx* ctx = create_ctx(device, &err);
+    if (!ctx) set_null_error(err);
+    return ctx;
+}
+
+void jamhip_ctx_destroy(jamhip_ctx* ctx) {
+    if (ctx) destroy_ctx(ctx);
+}
+
+void jamhip_global_destroy(void) {
+    std::lock_guard<std::mutex> lk(g_global_mu);
+    if (g_global) destroy_ctx(g_global);
+    g_global = nullptr;
+}
+
+const char* jamhip_ctx_arch(const jamhip_ctx* ctx) {
+    if (!ctx) ctx = global_ctx();
+    return ctx ? ctx->arch : "";
+}
+
+const char* jamhip_last_error(const jamhip_ctx* ctx) {
+    if (!ctx) return g_null_error;
+    thread_local std::string copy;   // a stable copy: another thread may overwrite the context's message
+    copy = error_of(const_cast<jamhip_ctx*>(ctx));
+    return copy.c_str();
+}
+
+jamhip_status jamhip_mm(jamhip_ctx* ctx, const void* w, int wt, int ldw, const void* a, int at, int lda, void* c,
+                        int ct, int ldc, int m, int n, int k) {
+    return on_ctx(ctx, [&](jamhip_ctx* x) { return mm_impl(x, w, wt, ldw, a, at, lda, c, ct, ldc, m, n, k); });
+}
+
+jamhip_status jamhip_mm_device(jamhip_ctx* ctx, const void* w, int wt, int ldw, const void* a_dev, int at, int lda,
+                               void* c_dev, int ct, int ldc, int m, int n, int k) {
+    return on_ctx(ctx, [&](jamhip_ctx* x) {
+        return mm_device_impl(x, w, wt, ldw, a_dev, at, lda, c_dev, ct, ldc, m, n, k);
+    });
+}
+
+jamhip_status jamhip_mm_device_ex(jamhip_ctx* ctx, const void* w, int wt, int ldw, const void* a_dev, int at, int lda,
+                                  void* c_dev, int ct, int ldc, int m, int n, int k, const void* bias_dev,
+                                  int accumulate) {
+    return on_ctx(ctx, [&](jamhip_ctx* x) {
+        return mm_device_ex_impl(x, w, wt, ldw, a_dev, at, lda, c_dev, ct, ldc, m, n, k, bias_dev, accumulate);
+    });
+}
+
+jamhip_status jamhip_glu_device(jamhip_ctx* ctx, int act, void* gate_dev, int ldg, const void* up_dev, int ldu,
+                                int rows, int cols) {
+    return on_ctx(ctx, [&](jamhip_ctx* x) { return glu_device_impl(x, act, gate_dev, ldg, up_dev, ldu, rows, cols); });
+}
+
+jamhip_status jamhip_weight_pin(jamhip_ctx* ctx, const void* w, int wt, int ldw, int m) {
+    return on_ctx(ctx, [&](jamhip_ctx* x) { return weight_pin_impl(x, w, wt, ldw, m); });
+}
+
+jamhip_status jamhip_weight_evict(jamhip_ctx* ctx, const void* w) {
+    return on_ctx(ctx, [&](jamhip_ctx* x) { return weight_evict_impl(x, w); });
+}
+
+int64_t jamhip_weight_bytes(const jamhip_ctx* ctx) {
+    if (!ctx) {
+        std::lock_guard<std::mutex> lk(g_global_mu);
+        ctx = g_global;
+        if (!ctx) return 0;
+    }
+    std::lock_guard<std::mutex> lk(ctx->pin_mu);
+    return ctx->pinned_bytes;
+}
+
+jamhip_status jamhip_quantize_device(jamhip_ctx* ctx, int flavour, const void* a_dev, int lda, int n, int k,
+                                     void* q_dev, void* d_dev, void* s_dev) {
+    return on_ctx(ctx, [&](jamhip_ctx* x) {
+        return quantize_device_impl(x, flavour, a_dev, lda, n, k, q_dev, d_dev, s_dev);
+    });
+}
+
+jamhip_status jamhip_mm_grouped(jamhip_ctx* ctx, const void* w, int wt, int ldw, int m, int n_experts,
+                                const void* counts_dev, const void* a_dev, int at, int lda, void* c_dev, int ct,
+                                int ldc, int k, int rows_cap, void* offsets_dev) {
+    return on_ctx(ctx, [&](jamhip_ctx* x) {
+        return mm_grouped_ex_impl(x, w, wt, ldw, m, n_experts, counts_dev, a_dev, at, lda, c_dev, ct, ldc, k, rows_cap,
+                                  offsets_dev, nullptr);
+    });
+}
+
+jamhip_status jamhip_mm_grouped_ex(jamhip_ctx* ctx, const void* w, int wt, int ldw, int m, int n_experts,
+                                   const void* counts_dev, const void* a_dev, int at, int lda, void* c_dev, int ct,
+                                   int ldc, int k, int rows_cap, void* offsets_dev, const void* bias_dev) {
+    return on_ctx(ctx, [&](jamhip_ctx* x) {
+        return mm_grouped_ex_impl(x, w, wt, ldw, m, n_experts, counts_dev, a_dev, at, lda, c_dev, ct, ldc, k, rows_cap,
+                                  offsets_dev, bias_dev);
+    });
+}
+
+jamhip_status jamhip_moe_route(jamhip_ctx* ctx, const void* route_expert_dev, int seq, int topk, int n_experts,
+                               void* counts_dev, void* offsets_dev, void* slot_route_dev, void* route_slot_dev) {
+    return on_ctx(ctx, [&](jamhip_ctx* x) {
+        return moe_route_impl(x, route_expert_dev, seq, topk, n_experts, counts_dev, offsets_dev, slot_route_dev,
+                              route_slot_dev);
+    });
+}
+
+jamhip_status jamhip_moe_gather(jamhip_ctx* ctx, const void* x_dev, int ldx, const void* slot_route_dev,
+                                const void* offsets_dev, int n_experts, int seq, int topk, int dim, void* g_dev,
+                                int ldg) {
+    return on_ctx(ctx, [&](jamhip_ctx* x) {
+        return moe_gather_impl(x, x_dev, ldx, slot_route_dev, offsets_dev, n_experts, seq, topk, dim, g_dev, ldg);
+    });
+}
+
+jamhip_status jamhip_moe_combine(jamhip_ctx* ctx, const void* y_dev, int ldy, const void* route_expert_dev,
+                                 const void* route_prob_dev, const void* route_slot_dev, int seq, int topk,
+                                 int n_experts, int dim, void* out_dev, int ldo) {
+    return on_ctx(ctx, [&](jamhip_ctx* x) {
+        return moe_combine_impl(x, y_dev, ldy, route_expert_dev, route_prob_dev, route_slot_dev, seq, topk, n_experts,
+                                dim, out_dev, ldo);
+    });
+}
+
+jamhip_status jamhip_ctx_set_stream(jamhip_ctx* ctx, void* stream) {
+    return on_ctx(ctx, [&](jamhip_ctx* x) { return ctx_set_stream_impl(x, stream); });
+}
+
+void* jamhip_ctx_stream(const jamhip_ctx* ctx) {
+    if (!ctx) ctx = global_ctx();
+    return ctx ? (void*) ctx->stream : nullptr;
+}
+
+jamhip_status jamhip_ctx_synchronize(jamhip_ctx* ctx) {
+    return on_ctx(ctx, [&](jamhip_ctx* x) { return ctx_synchronize_impl(x); });
 }
 
 // ------------------------------------------------------------------ GGUF weight registry
@@ -737,10 +972,12 @@ int64_t jamhip_gguf_find(const jamhip_gguf* g, const char* name) {
 
 namespace {
 // A tensor the registry pins: a jam weight dtype with data; ldw = dims[0], rows = the other dims' product.
+// A tensor whose row extent dims[0] is not a whole number of blocks (dims[0] below one block included) is
+// taken here too, with rows = 0, so that registry_runs reports it instead of dividing by a zero row size.
 bool registry_shape(const GgufTensor& t, int* ldw, int64_t* rows) {
     if (!supported_w(t.type) || t.bytes == 0) return false;
     *ldw = (int) t.dims[0];
-    *rows = t.bytes / row_bytes(t.type, t.dims[0]);
+    *rows = t.dims[0] % block_elems(t.type) ? 0 : t.bytes / row_bytes(t.type, t.dims[0]);
     return true;
 }
 
@@ -767,7 +1004,7 @@ jamhip_status registry_runs(jamhip_ctx* ctx, const GgufFile& f, std::vector<Run>
     std::sort(ts.begin(), ts.end(), [](const GgufTensor* x, const GgufTensor* y) { return x->offset < y->offset; });
     runs->clear();
     for (const GgufTensor* t : ts) {
-        const int64_t rows = t->bytes / row_bytes(t->type, t->dims[0]);
+        const int64_t rows = t->bytes / row_bytes(t->type, t->dims[0]);   // dims[0] is a block multiple here
         Run* r = runs->empty() ? nullptr : &runs->back();
         if (r && r->type == t->type && r->ldw == (int) t->dims[0] && r->offset + r->bytes == t->offset &&
             r->rows % 32 == 0 && r->rows + rows <= INT32_MAX) {
@@ -782,11 +1019,34 @@ jamhip_status registry_runs(jamhip_ctx* ctx, const GgufFile& f, std::vector<Run>
 }
 }  // namespace
 
+}  // extern "C"
+
+namespace {
+jamhip_status gguf_pin_impl(jamhip_ctx* ctx, const jamhip_gguf* g, const void* data_base, int64_t* n_pinned,
+                            int64_t* bytes_pinned);
+jamhip_status gguf_evict_impl(jamhip_ctx* ctx, const jamhip_gguf* g, const void* data_base, int64_t* n_evicted);
+}  // namespace
+
+extern "C" {
+
 jamhip_status jamhip_gguf_pin(jamhip_ctx* ctx, const jamhip_gguf* g, const void* data_base, int64_t* n_pinned,
                               int64_t* bytes_pinned) {
     if (n_pinned) *n_pinned = 0;
     if (bytes_pinned) *bytes_pinned = 0;
-    if (!ctx) return JAMHIP_EINVAL;
+    return on_ctx(ctx, [&](jamhip_ctx* x) { return gguf_pin_impl(x, g, data_base, n_pinned, bytes_pinned); });
+}
+
+jamhip_status jamhip_gguf_evict(jamhip_ctx* ctx, const jamhip_gguf* g, const void* data_base, int64_t* n_evicted) {
+    if (n_evicted) *n_evicted = 0;
+    return on_ctx(ctx, [&](jamhip_ctx* x) { return gguf_evict_impl(x, g, data_base, n_evicted); });
+}
+
+}  // extern "C"
+
+namespace {
+
+jamhip_status gguf_pin_impl(jamhip_ctx* ctx, const jamhip_gguf* g, const void* data_base, int64_t* n_pinned,
+                            int64_t* bytes_pinned) {
     if (!g) return fail(ctx, JAMHIP_EINVAL, "gguf pin: null handle");
     const uint8_t* base = data_base ? static_cast<const uint8_t*>(data_base) : g->f->data;
     Busy guard(ctx);
@@ -797,7 +1057,7 @@ jamhip_status jamhip_gguf_pin(jamhip_ctx* ctx, const jamhip_gguf* g, const void*
     if (st != JAMHIP_OK) return st;
     for (const Run& r : runs) {
         if ((st = pin_range(ctx, base + r.offset, r.type, r.ldw, r.rows, true)) != JAMHIP_OK) {
-            ctx->err = "gguf pin: run at data offset " + std::to_string(r.offset) + ": " + ctx->err;
+            fail(ctx, st, "gguf pin: run at data offset " + std::to_string(r.offset) + ": " + error_of(ctx));
             break;
         }
         if (n_pinned) *n_pinned += r.members;
@@ -807,9 +1067,7 @@ jamhip_status jamhip_gguf_pin(jamhip_ctx* ctx, const jamhip_gguf* g, const void*
     return st;
 }
 
-jamhip_status jamhip_gguf_evict(jamhip_ctx* ctx, const jamhip_gguf* g, const void* data_base, int64_t* n_evicted) {
-    if (n_evicted) *n_evicted = 0;
-    if (!ctx) return JAMHIP_EINVAL;
+jamhip_status gguf_evict_impl(jamhip_ctx* ctx, const jamhip_gguf* g, const void* data_base, int64_t* n_evicted) {
     if (!g) return fail(ctx, JAMHIP_EINVAL, "gguf evict: null handle");
     const uint8_t* base = data_base ? static_cast<const uint8_t*>(data_base) : g->f->data;
     Busy guard(ctx);
@@ -823,4 +1081,4 @@ jamhip_status jamhip_gguf_evict(jamhip_ctx* ctx, const jamhip_gguf* g, const voi
     return JAMHIP_OK;
 }
 
-}  // extern "C"
+}  // namespace

@@ -57,7 +57,9 @@ hipError_t launch_gemv_grouped(int dt, int flavour, const WeightView& w, const A
 hipError_t launch_rows_float(int dt, const WeightView& w, const float* a, int lda, int k, int r0, int rows, int n,
                              float* c, int ldc, hipStream_t st, const Epi& ep = Epi{});
 
-// int8-MFMA prefill GEMM (F2 activations), n >= 1; returns hipErrorNotSupported for dtypes it lacks.
+// int8-MFMA prefill GEMM (F2 activations), n >= 1; returns hipErrorNotSupported for dtypes it lacks
+// (gemm_covers is false for them).
+bool gemm_covers(int dt);
 hipError_t launch_gemm(int dt, const WeightView& w, const ActQ& A, int k, int m, int n, float* c, int ldc,
                        hipStream_t st, const Epi& ep = Epi{});
 

@@ -11,13 +11,14 @@ from __future__ import annotations
 
 import ctypes as C
 import struct
+import sys
 from dataclasses import dataclass
 from pathlib import Path
 from typing import Any, Iterable, Sequence
 
 import numpy as np
 
-from ._lib import lib
+from ._lib import lib, on_exit, register_for_teardown
 
 MAGIC = 0x46554747
 VERSION = 3
@@ -52,12 +53,15 @@ class TensorEntry:
 class GGUF:
     """A GGUF file opened by the native reader; close() (or a with-block) unmaps it."""
 
+    TEARDOWN_ORDER = 1   # closed at exit after the contexts (which hold device copies, not the mapping)
+
     def __init__(self, path: str | Path):
         L = lib()
         err = C.create_string_buffer(512)
         self._h = L.jamhip_gguf_open(str(path).encode(), err, len(err))
         if not self._h:
             raise GGUFFormatError(err.value.decode(errors="replace"))
+        register_for_teardown(self)
         self.path = str(path)
         self.alignment = L.jamhip_gguf_alignment(self._h)
         self.tensor_data_offset = L.jamhip_gguf_data_offset(self._h)
@@ -81,6 +85,8 @@ class GGUF:
         self.close()
 
     def __del__(self):
+        if sys.is_finalizing() or on_exit.done:   # the exit-time teardown already closed it
+            return
         try:
             self.close()
         except Exception:

@@ -18,6 +18,7 @@ from __future__ import annotations
 
 import ctypes as C
 import os
+import sys
 import threading
 from dataclasses import dataclass
 from typing import Any
@@ -25,7 +26,7 @@ from typing import Any
 import numpy as np
 
 from . import ggml
-from ._lib import lib
+from ._lib import lib, on_exit, register_for_teardown
 
 
 class JAM:
@@ -94,37 +95,63 @@ class _FairLock:
 
 
 class HipJAM:
-    """The MI355X backend behind the JAM contract. One context = one HIP stream (a serial stream)."""
+    """The MI355X backend behind the JAM contract. One context = one HIP stream (a serial stream).
 
-    def __init__(self, device: int = -1):
+    ``HipJAM(device)`` owns a context of its own; ``HipJAM.global_context()`` is bound to the library's
+    process-global context (ctx == NULL, as ``jam_mm(NULL, ...)``, jam/jam-native/include/jam.h:128). A
+    call the GPU answers with EUNSUPPORTED is handed to ``fallback`` (the provider this one shadows) when
+    one is set, so a dtype or shape the kernels do not cover still reaches the CPU backend."""
+
+    def __init__(self, device: int = -1, *, _global: bool = False):
         L = lib()
-        self._ctx = L.jamhip_ctx_create(device)
-        if not self._ctx:
-            raise RuntimeError("jamhip_ctx_create: " + L.jamhip_last_error(None).decode())
+        self._global = _global
+        if _global:
+            self._ctx = None
+        else:
+            self._ctx = L.jamhip_ctx_create(device)
+            if not self._ctx:
+                raise RuntimeError("jamhip_ctx_create: " + L.jamhip_last_error(None).decode())
         self._serial = _config("jam.hip.serial", "true").lower() == "true"
         self._lock = _FairLock() if self._serial else None
+        self.fallback = None
+        self._closed = False
+        register_for_teardown(self)
+
+    @classmethod
+    def global_context(cls) -> "HipJAM":
+        """A backend on the process-global context (created by the library on first use)."""
+        return cls(_global=True)
 
     # -- lifecycle -------------------------------------------------------------------------------
     def close(self):
-        if self._ctx:
-            lib().jamhip_ctx_destroy(self._ctx)
+        """Destroys an owned context (a no-op for the global one: jamhip_global_destroy releases it)."""
+        if not self._closed:
+            self._closed = True
+            if self._ctx:
+                lib().jamhip_ctx_destroy(self._ctx)
             self._ctx = None
 
     def __del__(self):
+        # never call into HIP while the interpreter shuts down: the exit-time teardown (_lib.on_exit) has
+        # already released every context before the runtime's own finalizers run
+        if sys.is_finalizing() or on_exit.done:
+            return
         try:
             self.close()
         except Exception:
             pass
 
     @property
-    def ctx(self) -> int:
+    def ctx(self) -> int | None:
+        if self._closed:
+            raise RuntimeError("HipJAM: context closed")
         return self._ctx
 
     def arch(self) -> str:
-        return lib().jamhip_ctx_arch(self._ctx).decode()
+        return lib().jamhip_ctx_arch(self.ctx).decode()
 
     def last_error(self) -> str:
-        return lib().jamhip_last_error(self._ctx).decode()
+        return lib().jamhip_last_error(self.ctx).decode()
 
     # -- the contract ----------------------------------------------------------------------------
     def mm(self, w: Segment, w_off: int, wt: int, ldw: int, a: Segment, a_off: int, at: int, lda: int,
@@ -137,10 +164,18 @@ class HipJAM:
             _check_segment("weight W", w, w_off, wt, ldw, m, k)
             _check_segment("activation A", a, a_off, at, lda, n, k)
             _check_segment("result R", r, r_off, rt, ldr, n, m)
-        args = (self._ctx, w.address + w_off, wt, ldw, a.address + a_off, at, lda, r.address + r_off, rt, ldr, m, n, k)
+        args = (self.ctx, w.address + w_off, wt, ldw, a.address + a_off, at, lda, r.address + r_off, rt, ldr, m, n, k)
         if self._lock is not None:
             with self._lock:
-                return lib().jamhip_mm(*args)
+                st = self._native_mm(args)
+        else:
+            st = self._native_mm(args)
+        if st == JAM.EUNSUPPORTED and self.fallback is not None:
+            return self.fallback.mm(w, w_off, wt, ldw, a, a_off, at, lda, r, r_off, rt, ldr, m, n, k)
+        return st
+
+    @staticmethod
+    def _native_mm(args) -> int:
         return lib().jamhip_mm(*args)
 
     def mm_contiguous(self, w: Segment, a: Segment, r: Segment, wt: int, m: int, n: int, k: int) -> int:
@@ -154,10 +189,10 @@ class HipJAM:
         if g is not None and m > 0 and ldw > 0 and m * g.row_bytes(ldw) > w.byte_size:
             raise IndexOutOfBoundsError(f"pin: weight segment too small — need {m * g.row_bytes(ldw)} B, "
                                         f"segment is {w.byte_size} B")
-        return lib().jamhip_weight_pin(self._ctx, w.address, wt, ldw, m)
+        return lib().jamhip_weight_pin(self.ctx, w.address, wt, ldw, m)
 
     def evict(self, w: Segment) -> int:
-        return lib().jamhip_weight_evict(self._ctx, w.address)
+        return lib().jamhip_weight_evict(self.ctx, w.address)
 
     def pinned_bytes(self) -> int:
         return lib().jamhip_weight_bytes(self._ctx)
@@ -165,31 +200,31 @@ class HipJAM:
     # -- device-resident path (torch tensors or raw device addresses) ------------------------------
     def mm_device(self, w: Segment, wt: int, ldw: int, a_dev: int, lda: int, c_dev: int, ldc: int,
                   m: int, n: int, k: int) -> int:
-        return lib().jamhip_mm_device(self._ctx, w.address, wt, ldw, a_dev, JAM.F32, lda, c_dev, JAM.F32, ldc,
+        return lib().jamhip_mm_device(self.ctx, w.address, wt, ldw, a_dev, JAM.F32, lda, c_dev, JAM.F32, ldc,
                                       m, n, k)
 
     def mm_device_ex(self, w: Segment, wt: int, ldw: int, a_dev: int, lda: int, c_dev: int, ldc: int,
                      m: int, n: int, k: int, bias_dev: int | None = None, accumulate: bool = False) -> int:
         """mm_device with the fused epilogue C = [C +] (W·A^T [+ bias]) (jamhip_mm_device_ex)."""
-        return lib().jamhip_mm_device_ex(self._ctx, w.address, wt, ldw, a_dev, JAM.F32, lda, c_dev, JAM.F32, ldc,
+        return lib().jamhip_mm_device_ex(self.ctx, w.address, wt, ldw, a_dev, JAM.F32, lda, c_dev, JAM.F32, ldc,
                                          m, n, k, bias_dev, int(accumulate))
 
     ACT_SWIGLU, ACT_SWIGLU_OAI = 1, 2
 
     def glu_device(self, act: int, gate_dev: int, ldg: int, up_dev: int, ldu: int, rows: int, cols: int) -> int:
         """In place on gate: SwiGLU (act 1) or gpt-oss clamped SwiGLU (act 2) (jamhip_glu_device)."""
-        return lib().jamhip_glu_device(self._ctx, act, gate_dev, ldg, up_dev, ldu, rows, cols)
+        return lib().jamhip_glu_device(self.ctx, act, gate_dev, ldg, up_dev, ldu, rows, cols)
 
     def quantize_device(self, flavour: int, a_dev: int, lda: int, n: int, k: int, q_dev: int, d_dev: int,
                         s_dev: int) -> int:
-        return lib().jamhip_quantize_device(self._ctx, flavour, a_dev, lda, n, k, q_dev, d_dev, s_dev)
+        return lib().jamhip_quantize_device(self.ctx, flavour, a_dev, lda, n, k, q_dev, d_dev, s_dev)
 
     # -- mixture of experts (device pointers; jamhip.h) -------------------------------------------
     def mm_grouped(self, w: Segment, wt: int, ldw: int, m: int, n_experts: int, counts_dev: int, a_dev: int,
                    lda: int, c_dev: int, ldc: int, k: int, rows_cap: int, offsets_dev: int | None = None) -> int:
         """One jam matmul per expert over CSR-grouped rows (Moe.dispatch's per-expert MatMul.gemm loop)."""
         _require_native(w, "weight W")
-        return lib().jamhip_mm_grouped(self._ctx, w.address, wt, ldw, m, n_experts, counts_dev, a_dev, JAM.F32, lda,
+        return lib().jamhip_mm_grouped(self.ctx, w.address, wt, ldw, m, n_experts, counts_dev, a_dev, JAM.F32, lda,
                                        c_dev, JAM.F32, ldc, k, rows_cap, offsets_dev)
 
     def mm_grouped_ex(self, w: Segment, wt: int, ldw: int, m: int, n_experts: int, counts_dev: int, a_dev: int,
@@ -197,29 +232,29 @@ class HipJAM:
                       bias_dev: int | None = None) -> int:
         """mm_grouped with expert e's bias [m] (at bias + e·m) added in the store (jamhip_mm_grouped_ex)."""
         _require_native(w, "weight W")
-        return lib().jamhip_mm_grouped_ex(self._ctx, w.address, wt, ldw, m, n_experts, counts_dev, a_dev, JAM.F32,
+        return lib().jamhip_mm_grouped_ex(self.ctx, w.address, wt, ldw, m, n_experts, counts_dev, a_dev, JAM.F32,
                                           lda, c_dev, JAM.F32, ldc, k, rows_cap, offsets_dev, bias_dev)
 
     def moe_route(self, route_expert_dev: int, seq: int, topk: int, n_experts: int, counts_dev: int,
                   offsets_dev: int, slot_route_dev: int, route_slot_dev: int) -> int:
         """Moe.dispatch's CSR build on the device (Moe.java:188-206)."""
-        return lib().jamhip_moe_route(self._ctx, route_expert_dev, seq, topk, n_experts, counts_dev, offsets_dev,
+        return lib().jamhip_moe_route(self.ctx, route_expert_dev, seq, topk, n_experts, counts_dev, offsets_dev,
                                       slot_route_dev, route_slot_dev)
 
     def moe_gather(self, x_dev: int, ldx: int, slot_route_dev: int, offsets_dev: int, n_experts: int, seq: int,
                    topk: int, dim: int, g_dev: int, ldg: int) -> int:
         """Moe.dispatch's gather (Moe.java:214-222)."""
-        return lib().jamhip_moe_gather(self._ctx, x_dev, ldx, slot_route_dev, offsets_dev, n_experts, seq, topk, dim,
+        return lib().jamhip_moe_gather(self.ctx, x_dev, ldx, slot_route_dev, offsets_dev, n_experts, seq, topk, dim,
                                        g_dev, ldg)
 
     def moe_combine(self, y_dev: int, ldy: int, route_expert_dev: int, route_prob_dev: int, route_slot_dev: int,
                     seq: int, topk: int, n_experts: int, dim: int, out_dev: int, ldo: int) -> int:
         """Moe.dispatch's prob-weighted scatter-add (Moe.java:208, 223-231), bit-identical order."""
-        return lib().jamhip_moe_combine(self._ctx, y_dev, ldy, route_expert_dev, route_prob_dev, route_slot_dev, seq,
+        return lib().jamhip_moe_combine(self.ctx, y_dev, ldy, route_expert_dev, route_prob_dev, route_slot_dev, seq,
                                         topk, n_experts, dim, out_dev, ldo)
 
     def set_stream(self, stream: int | None) -> int:
-        return lib().jamhip_ctx_set_stream(self._ctx, stream)
+        return lib().jamhip_ctx_set_stream(self.ctx, stream)
 
     def stream(self) -> int:
         return lib().jamhip_ctx_stream(self._ctx)
@@ -245,13 +280,23 @@ def _check_segment(which: str, seg: Segment, off: int, dt: int, stride: int, row
 
 
 # ------------------------------------------------------------------------------------ discovery
+# Other JAM providers visible to discovery (what ServiceLoader finds on the class path besides this one;
+# jam-native's NativeJAMProvider in a real deployment). register() adds one.
+_REGISTERED: list = []
+
+
+def register(provider) -> None:
+    _REGISTERED.append(provider)
+
+
 class Provider:
     """JAM.Provider (JAM.java:21-38) for the MI355X backend."""
 
     def id(self) -> str:
         """`native` by default: jinfer asks only for ids `native` and `vector` (MatMul.java:1770-1771),
-        so answering to `native` above jam-native's priority puts the GPU under an unedited caller;
-        `JAM_HIP_ID=hip` (jam.hip.id) opts out."""
+        so answering to `native` above jam-native's priority puts the GPU under an unedited caller. The
+        provider it shadows there (jam-native) stays reachable as the fallback of every call the GPU answers
+        with EUNSUPPORTED. `JAM_HIP_ID=hip` (jam.hip.id) moves the GPU to its own id instead."""
         return _config("jam.hip.id", "native")
 
     def priority(self) -> int:
@@ -261,7 +306,17 @@ class Provider:
         return bool(lib().jamhip_device_available())
 
     def create(self) -> HipJAM:
-        return _shared()
+        jam = _shared()
+        if jam.fallback is None:
+            jam.fallback = self.shadowed()
+        return jam
+
+    def shadowed(self):
+        """The backend of the highest-priority other available provider with this provider's id, or None."""
+        for p in providers(_REGISTERED):
+            if p is not self and not isinstance(p, Provider) and p.id() == self.id():
+                return p.create()
+        return None
 
 
 _SHARED: HipJAM | None = None
@@ -269,10 +324,12 @@ _SHARED_LOCK = threading.Lock()
 
 
 def _shared() -> HipJAM:
+    """The provider's instance, on the process-global context (Provider.create may return a shared
+    instance, JAM.java:31-37)."""
     global _SHARED
     with _SHARED_LOCK:
         if _SHARED is None:
-            _SHARED = HipJAM()
+            _SHARED = HipJAM.global_context()
         return _SHARED
 
 
@@ -301,5 +358,5 @@ def addr(x) -> int:
     return x if isinstance(x, int) else int(x.data_ptr())
 
 
-__all__ = ["JAM", "HipJAM", "Provider", "providers", "Segment", "IllegalArgumentError", "IndexOutOfBoundsError",
-           "addr", "C"]
+__all__ = ["JAM", "HipJAM", "Provider", "providers", "register", "Segment", "IllegalArgumentError",
+           "IndexOutOfBoundsError", "addr", "C"]

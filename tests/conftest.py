@@ -71,3 +71,44 @@ def adversarial_activations(k: int = 256) -> np.ndarray:
     rng = np.random.default_rng(1234)
     rows.append(rng.standard_normal(k).astype(np.float32))
     return np.stack(rows)
+
+
+def random_blocks(dt: int, rows: int, k: int, seed: int) -> np.ndarray:
+    """[rows, row_bytes] uint8 of random but valid GGUF blocks (the reference's random-valid-block builders,
+    jam/jam-native/tests/jam_ref.h:160-293): random quant bytes, block scales drawn so the decoded weights
+    are of the N(0, 0.02) order. Much faster than quantizing f32 draws at 100M+ elements."""
+    rng = np.random.default_rng(seed)
+    be, bb = O.BLOCK[dt]
+    nb = k // be
+    blk = rng.integers(0, 256, (rows, nb, bb), dtype=np.uint8)
+
+    def f16(lo, hi, shape):
+        return rng.uniform(lo, hi, shape).astype(np.float16).view(np.uint8).reshape(*shape, 2)
+
+    if dt == O.Q8_0:
+        blk[:, :, 0:2] = f16(1e-4, 3e-4, (rows, nb))
+    elif dt == O.Q4_0:
+        blk[:, :, 0:2] = f16(2e-3, 6e-3, (rows, nb))
+    elif dt == O.MXFP4:
+        blk[:, :, 0] = rng.integers(118, 123, (rows, nb), dtype=np.uint8)
+    elif dt == O.Q4_K:
+        blk[:, :, 0:2] = f16(5e-5, 2e-4, (rows, nb))      # d
+        blk[:, :, 2:4] = f16(1e-4, 5e-4, (rows, nb))      # dmin
+    elif dt == O.Q6_K:
+        blk[:, :, 192:208] = rng.integers(-40, 41, (rows, nb, 16), dtype=np.int8).view(np.uint8)
+        blk[:, :, 208:210] = f16(1e-5, 4e-5, (rows, nb))
+    else:
+        raise ValueError(dt)
+    return np.ascontiguousarray(blk.reshape(rows, nb * bb))
+
+
+def parity_report(label: str, got: np.ndarray, ref: np.ndarray, sa: np.ndarray) -> dict:
+    """The largest relative error (over outputs with |ref| above 1e-3 of the largest) and the largest error
+    in units of sum|w*a|, printed with the case's label; returns both."""
+    err = np.abs(got.astype(np.float64) - ref)
+    big = np.abs(ref) > 1e-3 * np.abs(ref).max()
+    rel = float((err[big] / np.abs(ref[big])).max()) if big.any() else 0.0
+    per_sa = float((err / np.maximum(sa, 1e-30)).max())
+    print(f"parity {label}: max_rel {rel:.3e}  max_err/sumAbs {per_sa:.3e}  outputs {got.size}", file=sys.stderr,
+          flush=True)
+    return {"max_rel": rel, "max_err_per_sumabs": per_sa}

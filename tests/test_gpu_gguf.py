@@ -166,6 +166,18 @@ def test_registry_rejects_partial_row_blocks(hip, tmp_path):
         assert st == JAM.EUNSUPPORTED and cnt == 0
         assert "b.weight" in hip.last_error()
     assert hip.pinned_bytes() == before
+    # a row extent below one block ([16, 2] Q8_0, [128, 2] Q4_K: 32 and 256 elements in all) has a zero row
+    # size; the check runs before any division by it (evict walks the same table)
+    for dt, dims, nbytes in ((O.Q8_0, (16, 2), 34), (O.Q4_K, (128, 2), 144)):
+        path = tmp_path / f"short_{dt}.gguf"
+        G.write(path, [("a.weight", O.Q8_0, (64, 1), ok), ("c.weight", dt, dims, np.zeros(nbytes, np.uint8))])
+        with G.GGUF(path) as g:
+            st, cnt, _ = g.pin(hip)
+            assert st == JAM.EUNSUPPORTED and cnt == 0, (dt, st)
+            assert "c.weight" in hip.last_error()
+            with pytest.raises(RuntimeError):
+                g.evict(hip)
+    assert hip.pinned_bytes() == before
 
 
 def test_registry_runs_fused_call(hip, oracle, tmp_path):

@@ -50,8 +50,11 @@ def _bare_backend():
     from qxotic_amd.jam import HipJAM
     h = object.__new__(HipJAM)   # argument checks run before any native call
     h._ctx = None
+    h._global = False
+    h._closed = False
     h._serial = True
     h._lock = None
+    h.fallback = None
     return h
 
 
@@ -120,3 +123,70 @@ def test_bench_refuses_more_than_one_gpu():
                            env={**os.environ, **env})
         assert r.returncode == 2, (argv, env, r.stderr[-400:])
         assert "one GPU" in r.stderr and r.stdout == ""
+
+
+def test_provider_delegates_unsupported_to_shadowed(monkeypatch):
+    """Answering to id `native` hides jam-native from MatMul.load("native") (MatMul.java:1833-1844); the
+    provider therefore hands every call the GPU answers with EUNSUPPORTED to the provider it shadows (the
+    next available provider with the same id) and returns that provider's status. A provider of another id
+    is never used as the fallback."""
+    from qxotic_amd import jam as J
+
+    calls = []
+
+    class FakeNativeJAM:
+        def mm(self, *args):
+            calls.append(args[2])   # wt
+            return J.JAM.OK
+
+    class FakeProvider:
+        def __init__(self, pid, prio):
+            self.pid, self.prio = pid, prio
+
+        def id(self):
+            return self.pid
+
+        def priority(self):
+            return self.prio
+
+        def is_available(self):
+            return True
+
+        def create(self):
+            return FakeNativeJAM()
+
+    monkeypatch.setattr(J, "_REGISTERED", [FakeProvider("vector", 500), FakeProvider("native", 1000)])
+    monkeypatch.setattr(J, "_SHARED", None)
+    statuses = iter([J.JAM.EUNSUPPORTED, J.JAM.OK, J.JAM.EINVAL])
+    monkeypatch.setattr(J.HipJAM, "_native_mm", staticmethod(lambda args: next(statuses)))
+    jam = J.Provider().create()
+    assert isinstance(jam.fallback, FakeNativeJAM)
+    w = np.zeros((4, 176), np.uint8)
+    a = np.zeros((1, 256), np.float32)
+    r = np.zeros((1, 4), np.float32)
+    args = (J.Segment.of(w), 0, J.JAM.Q5_K, 256, J.Segment.of(a), 0, J.JAM.F32, 256, J.Segment.of(r), 0, J.JAM.F32,
+            4, 4, 1, 256)
+    assert jam.mm(*args) == J.JAM.OK and calls == [J.JAM.Q5_K]     # EUNSUPPORTED -> jam-native ran it
+    assert jam.mm(*args) == J.JAM.OK and calls == [J.JAM.Q5_K]     # the GPU ran it
+    assert jam.mm(*args) == J.JAM.EINVAL and len(calls) == 1       # only EUNSUPPORTED is delegated
+    monkeypatch.setenv("JAM_HIP_ID", "hip")                          # own id: nothing to shadow
+    assert J.Provider().shadowed() is None
+
+
+def test_exit_teardown_runs_without_a_device(tmp_path):
+    """The exit-time teardown (qxotic_amd._lib.on_exit) closes open GGUF mappings and the backend objects and
+    calls jamhip_global_destroy; a process that leaves them open exits with status 0."""
+    import subprocess
+    import sys
+    from qxotic_amd import gguf as G
+    path = tmp_path / "m.gguf"
+    G.write(path, [("w", 8, (32, 2), np.zeros(68, np.uint8))])
+    code = ("import sys; sys.path.insert(0, %r)\n"
+            "from qxotic_amd import gguf as G, _lib\n"
+            "from qxotic_amd.jam import HipJAM\n"
+            "import atexit\n"
+            "atexit.register(lambda: print('closed', g._h is None, h._closed, flush=True))  # runs after on_exit\n"
+            "g = G.GGUF(%r); h = HipJAM.global_context()\n") % (str(ROOT), str(path))
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr[-1000:]
+    assert "closed True True" in r.stdout
