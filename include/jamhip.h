@@ -101,6 +101,22 @@ jamhip_status jamhip_mm_device(jamhip_ctx* ctx,
                                void*       c_dev, int ct, int ldc,
                                int m, int n, int k);
 
+/* jamhip_mm_device that allocates nothing: no hipMalloc, hipFree or other allocating call on its path. No
+ * counterpart in the reference; it is for callers that cannot allocate (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid allocation). W must already be resident (jamhip_weight_pin or the
+ * GGUF registry), else JAMHIP_EUNSUPPORTED. The kernels' scratch (activation codes, the matrix-core operand
+ * layout, split-K partial sums) comes from one static device array of JAMHIP_NOALLOC_SCRATCH_BYTES per GPU,
+ * held by the process until it ends; a call needing more returns JAMHIP_EUNSUPPORTED with the size in
+ * jamhip_last_error and queues nothing (jamhip_mm_device covers it). Every call on one GPU, from any context,
+ * shares that GPU's array: calls that overlap in time on one GPU (two streams, two threads, two contexts)
+ * race on it, so callers serialize them. Same validation, results and status codes as jamhip_mm_device. */
+#define JAMHIP_NOALLOC_SCRATCH_BYTES ((size_t) 64 << 20)   /* 64 MiB: config 4's M = 512 prefill fits */
+jamhip_status jamhip_mm_device_noalloc(jamhip_ctx* ctx,
+                                       const void* w, int wt, int ldw,
+                                       const void* a_dev, int at, int lda,
+                                       void*       c_dev, int ct, int ldc,
+                                       int m, int n, int k);
+
 /* jam's activation quantizers alone (device pointers, context stream, not synchronized); the matmul
  * entry points run the same kernels internally. flavour 1 = F1 (jam_kernels_generic.c:71-94):
  * q[n][k] int8, d[n][k/32], s[n][k/32] = (float)Σq. flavour 2 = F2 (jam_kernels_q4k_avx512.c:25-37):

@@ -25,6 +25,7 @@ SIGNATURES = [
     ("jamhip_weight_evict", _I, [_VP, _VP]),
     ("jamhip_weight_bytes", _I64, [_VP]),
     ("jamhip_mm_device", _I, [_VP, _VP, _I, _I, _VP, _I, _I, _VP, _I, _I, _I, _I, _I]),
+    ("jamhip_mm_device_noalloc", _I, [_VP, _VP, _I, _I, _VP, _I, _I, _VP, _I, _I, _I, _I, _I]),
     ("jamhip_quantize_device", _I, [_VP, _I, _VP, _I, _I, _I, _VP, _VP, _VP]),
     ("jamhip_mm_grouped", _I, [_VP, _VP, _I, _I, _I, _I, _VP, _VP, _I, _I, _VP, _I, _I, _I, _I, _VP]),
     ("jamhip_mm_grouped_ex", _I, [_VP, _VP, _I, _I, _I, _I, _VP, _VP, _I, _I, _VP, _I, _I, _I, _I, _VP, _VP]),

@@ -93,6 +93,40 @@ constexpr int64_t align256(int64_t v) { return (v + 255) & ~int64_t(255); }
 
 bool supported_w(int dt) { return dt == Q8_0 || dt == Q4_0 || dt == Q4_K || dt == Q6_K || dt == MXFP4; }
 
+// Device scratch of jamhip_mm_device_noalloc: one fixed array per GPU, in the code object (no allocation
+// call ever sizes it), shared by every call on that GPU. In host code `scratch` is only a stand-in for the
+// symbol: its device address comes from hipGetSymbolAddress, taken once per device when the first context
+// on that device is created (noalloc_scratch_init) and used everywhere host code refers to the array.
+constexpr size_t NOALLOC_SCRATCH_BYTES = JAMHIP_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
+
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+uint8_t* g_scratch_ptr[MAX_DEVICES] = {};          // device address of `scratch` on each device, once known
+hipError_t g_scratch_err[MAX_DEVICES] = {};
+
+// Takes the address of `scratch` on `device` (which must be current) the first time; later calls return
+// the recorded outcome.
+hipError_t noalloc_scratch_init(int device) {
+    if (device < 0 || device >= MAX_DEVICES) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch_ptr[device] || g_scratch_err[device] != hipSuccess) return g_scratch_err[device];
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr) {
+        g_scratch_err[device] = e != hipSuccess ? e : hipErrorInvalidSymbol;
+        return g_scratch_err[device];
+    }
+    g_scratch_ptr[device] = static_cast<uint8_t*>(ptr);
+    return hipSuccess;
+}
+
+uint8_t* noalloc_scratch(int device) {
+    if (device < 0 || device >= MAX_DEVICES) return nullptr;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    return g_scratch_ptr[device];
+}
+
 // Error text of calls with no context of their own: a failed jamhip_ctx_create, or a failed call made with
 // ctx == NULL (the process-global context). Per thread; jamhip_last_error(NULL) returns it.
 thread_local char g_null_error[512] = "";
@@ -482,6 +516,24 @@ jamhip_status mm_device_impl(jamhip_ctx* ctx, const void* w, int wt, int ldw, co
     return compute(ctx, wt, wv, (const float*) a_dev, lda, (float*) c_dev, ldc, m, n, k);
 }
 
+// jamhip_mm_device with W required resident and every piece of scratch taken from the device's static array:
+// no allocation of any kind on the call's path.
+jamhip_status mm_device_noalloc_impl(jamhip_ctx* ctx, const void* w, int wt, int ldw, const void* a_dev, int at,
+                                     int lda, void* c_dev, int ct, int ldc, int m, int n, int k) {
+    jamhip_status st = validate(ctx, w, wt, ldw, a_dev, at, lda, c_dev, ct, ldc, m, n, k);
+    if (st != JAMHIP_OK) return st;
+    Busy guard(ctx);
+    if (!guard.ok) return fail(ctx, JAMHIP_EBUSY, "context busy");
+    (void) hipSetDevice(ctx->device);
+    uint8_t* base = noalloc_scratch(ctx->device);
+    if (!base) return fail(ctx, JAMHIP_EINVAL, "noalloc: the static scratch array has no device address on this device");
+    WeightView wv;
+    if (!lookup(ctx, w, wt, ldw, m, &wv))
+        return fail(ctx, JAMHIP_EUNSUPPORTED, "noalloc: W is not resident (pin it first: staging it would allocate)");
+    Scratch sc{ctx, base, NOALLOC_SCRATCH_BYTES};
+    return compute(ctx, sc, wt, wv, (const float*) a_dev, lda, (float*) c_dev, ldc, m, n, k);
+}
+
 jamhip_status mm_device_ex_impl(jamhip_ctx* ctx, const void* w, int wt, int ldw, const void* a_dev, int at, int lda,
                                   void* c_dev, int ct, int ldc, int m, int n, int k, const void* bias_dev,
                                   int accumulate) {
@@ -726,6 +778,7 @@ jamhip_ctx* create_ctx(int device, std::string* err) {
         *err = std::string("unsupported device architecture ") + prop.gcnArchName + " (need gfx950)";
         return nullptr;
     }
+    (void) noalloc_scratch_init(dev);   // a failure is reported by jamhip_mm_device_noalloc itself
     auto* ctx = new jamhip_ctx();
     ctx->device = dev;
     snprintf(ctx->arch, sizeof ctx->arch, "%s", prop.gcnArchName);
@@ -835,6 +888,13 @@ jamhip_status jamhip_mm_device(jamhip_ctx* ctx, const void* w, int wt, int ldw, 
                                void* c_dev, int ct, int ldc, int m, int n, int k) {
     return on_ctx(ctx, [&](jamhip_ctx* x) {
         return mm_device_impl(x, w, wt, ldw, a_dev, at, lda, c_dev, ct, ldc, m, n, k);
+    });
+}
+
+jamhip_status jamhip_mm_device_noalloc(jamhip_ctx* ctx, const void* w, int wt, int ldw, const void* a_dev, int at,
+                                       int lda, void* c_dev, int ct, int ldc, int m, int n, int k) {
+    return on_ctx(ctx, [&](jamhip_ctx* x) {
+        return mm_device_noalloc_impl(x, w, wt, ldw, a_dev, at, lda, c_dev, ct, ldc, m, n, k);
     });
 }
 

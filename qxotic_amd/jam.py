@@ -203,6 +203,13 @@ class HipJAM:
         return lib().jamhip_mm_device(self.ctx, w.address, wt, ldw, a_dev, JAM.F32, lda, c_dev, JAM.F32, ldc,
                                       m, n, k)
 
+    def mm_device_noalloc(self, w: Segment, wt: int, ldw: int, a_dev: int, lda: int, c_dev: int, ldc: int,
+                          m: int, n: int, k: int) -> int:
+        """mm_device with no allocation on its path: W pinned, scratch from the GPU's static array
+        (jamhip_mm_device_noalloc)."""
+        return lib().jamhip_mm_device_noalloc(self.ctx, w.address, wt, ldw, a_dev, JAM.F32, lda, c_dev, JAM.F32, ldc,
+                                              m, n, k)
+
     def mm_device_ex(self, w: Segment, wt: int, ldw: int, a_dev: int, lda: int, c_dev: int, ldc: int,
                      m: int, n: int, k: int, bias_dev: int | None = None, accumulate: bool = False) -> int:
         """mm_device with the fused epilogue C = [C +] (W·A^T [+ bias]) (jamhip_mm_device_ex)."""
