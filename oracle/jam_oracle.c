@@ -15,6 +15,8 @@ int jo_block_elems(int dt) {   /* GGMLType.java:15-26 */
     switch (dt) {
     case JO_F32: case JO_F16: case JO_BF16: return 1;
     case JO_Q4_0: case JO_Q8_0: case JO_MXFP4: return 32;
+    case JO_NVFP4: return 64;     /* jam_nvfp4.h:14 */
+    case JO_Q1_0: return 128;     /* jam_q1_0.h:8 */
     case JO_Q4_K: case JO_Q5_K: case JO_Q6_K: return 256;
     default: return 0;
     }
@@ -30,6 +32,8 @@ int jo_block_bytes(int dt) {   /* GGMLType.java:15-26 */
     case JO_Q4_K: return 144;
     case JO_Q5_K: return 176;
     case JO_Q6_K: return 210;
+    case JO_NVFP4: return 36;     /* d[4] UE4M3 + qs[32] */
+    case JO_Q1_0: return 18;      /* fp16 d + 16 sign bytes */
     default: return 0;
     }
 }
@@ -94,6 +98,20 @@ float jo_e8m0_half(uint8_t e) {   /* jam_mxfp4.h:17-24: 0.5 * 2^(e-127) */
 }
 
 static float bf16f(uint16_t h) { uint32_t b = (uint32_t) h << 16; float f; memcpy(&f, &b, 4); return f; }
+
+float jo_ue4m3(uint8_t x) {   /* jam_nvfp4.h:19-25 */
+    if (x == 0 || x == 0x7F) return 0.0f;
+    int e = (x >> 3) & 0xF, m = x & 0x7;
+    return e ? ldexpf(1.0f + (float) m / 8.0f, e - 7) : ldexpf((float) m, -9);
+}
+
+uint16_t jo_float2bf16(float f) {   /* round to nearest even on the 16 dropped bits */
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    if ((x & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((x >> 16) | 0x40u);   /* NaN stays (quiet) NaN */
+    x += 0x7FFFu + ((x >> 16) & 1u);
+    return (uint16_t)(x >> 16);
+}
 
 static const int8_t kMxfp4Codes[16] = { 0, 1, 2, 3, 4, 6, 8, 12, 0, -1, -2, -3, -4, -6, -8, -12 };
 
@@ -183,6 +201,22 @@ void jo_dequant_row_f64(int dt, const uint8_t* w, int k, double* out) {
                 int q = q6k_code(w, e, &s);
                 out[e] = d * (int8_t) w[192 + s] * (q - 32);
             }
+            break;
+        }
+        case JO_NVFP4: {   /* generic.c:128-165: sub-block s byte s*8+j: low nibble elem 16s+j, high 16s+8+j */
+            for (int sb = 0; sb < 4; sb++) {
+                double d = jo_ue4m3(w[sb]);
+                for (int j = 0; j < 8; j++) {
+                    uint8_t b = w[4 + 8 * sb + j];
+                    out[16 * sb + j] = d * kMxfp4Codes[b & 15];
+                    out[16 * sb + 8 + j] = d * kMxfp4Codes[b >> 4];
+                }
+            }
+            break;
+        }
+        case JO_Q1_0: {   /* jam_q1_0.h:16-27: bit j (LSB-first, byte j/8) ? +d : -d */
+            double d = jo_half2float((uint16_t)(w[0] | (w[1] << 8)));
+            for (int e = 0; e < 128; e++) out[e] = ((w[2 + (e >> 3)] >> (e & 7)) & 1) ? d : -d;
             break;
         }
         default: break;
@@ -283,6 +317,80 @@ void jo_quantize_row(int dt, const float* x, int k, uint8_t* out) {
                     out[byte] |= (uint8_t)((s & 1) ? (q << 4) : q);
                 }
             }
+            break;
+        }
+        case JO_F32: memcpy(out, x, 4); break;
+        case JO_F16: put_half(out, x[0]); break;
+        case JO_BF16: { uint16_t h = jo_float2bf16(x[0]); out[0] = (uint8_t) h; out[1] = (uint8_t)(h >> 8); break; }
+        case JO_Q5_K: {   /* as Q4_K with 32 levels: the 5th bit of sub-block 2g/2g+1 in bit 2g/2g+1 of qh[e] */
+            float sub_s[8], sub_m[8], ms = 0.0f, mm = 0.0f;
+            for (int s = 0; s < 8; s++) {
+                float lo = x[32 * s], hi = x[32 * s];
+                for (int e = 1; e < 32; e++) { float v = x[32 * s + e]; lo = v < lo ? v : lo; hi = v > hi ? v : hi; }
+                if (lo > 0.0f) lo = 0.0f;
+                sub_s[s] = (hi - lo) / 31.0f;
+                sub_m[s] = -lo;
+                ms = sub_s[s] > ms ? sub_s[s] : ms;
+                mm = sub_m[s] > mm ? sub_m[s] : mm;
+            }
+            float d = jo_half2float(jo_float2half(ms / 63.0f)), dmin = jo_half2float(jo_float2half(mm / 63.0f));
+            put_half(out, ms / 63.0f);
+            put_half(out + 2, mm / 63.0f);
+            int sc[8], mn[8];
+            for (int s = 0; s < 8; s++) {
+                sc[s] = d > 0.0f ? clampi((int) lrintf(sub_s[s] / d), 0, 63) : 0;
+                mn[s] = dmin > 0.0f ? clampi((int) lrintf(sub_m[s] / dmin), 0, 63) : 0;
+            }
+            uint8_t* b = out + 4;
+            for (int j = 0; j < 4; j++) {
+                b[j] = (uint8_t)((sc[j] & 63) | ((sc[j + 4] >> 4) << 6));
+                b[j + 4] = (uint8_t)((mn[j] & 63) | ((mn[j + 4] >> 4) << 6));
+                b[j + 8] = (uint8_t)((sc[j + 4] & 15) | ((mn[j + 4] & 15) << 4));
+            }
+            for (int s = 0; s < 8; s++) {
+                float ds = d * sc[s], ms_ = dmin * mn[s];
+                for (int e = 0; e < 32; e++) {
+                    int q = ds > 0.0f ? clampi((int) lrintf((x[32 * s + e] + ms_) / ds), 0, 31) : 0;
+                    int g = s / 2;
+                    out[48 + 32 * g + e] |= (uint8_t)((s & 1) ? ((q & 15) << 4) : (q & 15));
+                    out[16 + e] |= (uint8_t)((q >> 4) << s);
+                }
+            }
+            break;
+        }
+        case JO_NVFP4: {   /* per 16: the UE4M3 scale nearest amax/12, then the nearest code of kv = 2·e2m1 */
+            for (int sb = 0; sb < 4; sb++) {
+                const float* v = x + 16 * sb;
+                float target = amax_of(v, 16) / 12.0f, best = 1e30f;
+                int code = 0;
+                for (int c = 1; c < 127; c++) {
+                    float dv = fabsf(jo_ue4m3((uint8_t) c) - target);
+                    if (c != 0x7F && dv < best) { best = dv; code = c; }
+                }
+                if (target == 0.0f) code = 0;
+                out[sb] = (uint8_t) code;
+                float sc = jo_ue4m3((uint8_t) code);
+                for (int j = 0; j < 16; j++) {
+                    int nib = 0;
+                    if (sc > 0.0f) {
+                        float t = v[j] / sc, bd = 1e30f;
+                        for (int c = 0; c < 16; c++) {
+                            float dv = fabsf((float) kMxfp4Codes[c] - t);
+                            if (dv < bd) { bd = dv; nib = c; }
+                        }
+                    }
+                    uint8_t* byte = out + 4 + 8 * sb + (j & 7);
+                    *byte |= (uint8_t)(j < 8 ? nib : nib << 4);
+                }
+            }
+            break;
+        }
+        case JO_Q1_0: {   /* d = mean |x| (fp16), bit = x >= 0 */
+            float s = 0.0f;
+            for (int e = 0; e < 128; e++) s += fabsf(x[e]);
+            put_half(out, s / 128.0f);
+            for (int e = 0; e < 128; e++)
+                if (x[e] >= 0.0f) out[2 + (e >> 3)] |= (uint8_t)(1u << (e & 7));
             break;
         }
         case JO_Q6_K: {   /* 16 sub-blocks of 16: int8 sub-scale under fp16 d, codes q+32 in 0..63 */
@@ -431,6 +539,57 @@ static double row_f1(int dt, const uint8_t* w, const int8_t* aq, const float* ad
         }
         return acc;
     }
+    if (dt == JO_Q5_K) {   /* jam_mm_q5k_sse3 (kquant_sse3.c:70-121): ad·(fl(dl·dot) − fl(ml·asum)) per 32 */
+        for (int B = 0; B < k / 256; B++, w += 176) {
+            float d = h2f_at(w), dmin = h2f_at(w + 2);
+            int sc[8], mn[8];
+            q4k_scales(w + 4, sc, mn);
+            const uint8_t* qh = w + 16;
+            const uint8_t* qs = w + 48;
+            for (int s = 0; s < 8; s++) {
+                int g = s / 2, bi = 8 * B + s, dot = 0;
+                for (int e = 0; e < 32; e++) {
+                    uint8_t q = qs[32 * g + e];
+                    int q5 = ((s & 1) ? (q >> 4) : (q & 15)) | (((qh[e] >> s) & 1) << 4);
+                    dot += q5 * aq[32 * bi + e];
+                }
+                float dl = d * (float) sc[s], ml = dmin * (float) mn[s];
+                float t = dl * (float) dot - ml * as[bi];
+                acc += (double)(ad[bi] * t);
+            }
+        }
+        return acc;
+    }
+    if (dt == JO_NVFP4) {   /* jam_mm_nvfp4_avx512 (avx512bw.c:111-142): Σ_s dot_s·fl(ue4m3(d_s)·ad) per 16 */
+        for (int bb = 0; bb < k / 64; bb++, w += 36) {
+            for (int sb = 0; sb < 4; sb++) {
+                int dot = 0;
+                for (int j = 0; j < 8; j++) {
+                    uint8_t b = w[4 + 8 * sb + j];
+                    dot += kMxfp4Codes[b & 15] * aq[64 * bb + 16 * sb + j] + kMxfp4Codes[b >> 4] * aq[64 * bb + 16 * sb + 8 + j];
+                }
+                float sc = jo_ue4m3(w[sb]) * ad[2 * bb + sb / 2];
+                acc += (double) sc * dot;
+            }
+        }
+        return acc;
+    }
+    if (dt == JO_Q1_0) {   /* jam_mm_q1_0_avx2 (q1_0_avx2.c:45-86): d·Σ_K fma(ad_K, Σ±q, ·) per 128 */
+        for (int bb = 0; bb < k / 128; bb++, w += 18) {
+            float fb = 0.0f;
+            for (int K = 0; K < 4; K++) {
+                int bi = 4 * bb + K, dot = 0;
+                for (int e = 0; e < 32; e++) {
+                    int el = 32 * K + e;
+                    int bit = (w[2 + (el >> 3)] >> (el & 7)) & 1;
+                    dot += bit ? aq[32 * bi + e] : -aq[32 * bi + e];
+                }
+                fb = fmaf(ad[bi], (float) dot, fb);
+            }
+            acc += (double) h2f_at(w) * fb;
+        }
+        return acc;
+    }
     return 0.0;
 }
 
@@ -495,11 +654,56 @@ static double row_f2(int dt, const uint8_t* w, const int8_t* xq, const float* dx
         }
         return acc;
     }
+    if (dt == JO_Q5_K) {   /* q5k_block16 (q4k_avx512.c:798-811): fl(fl(d·sc)·dx)·Σq5·xq − fl(dmin·mn)·fl(xs0+xs1) */
+        for (int B = 0; B < k / 256; B++, w += 176) {
+            float d = h2f_at(w), dmin = h2f_at(w + 2);
+            int sc[8], mn[8];
+            q4k_scales(w + 4, sc, mn);
+            const uint8_t* qh = w + 16;
+            const uint8_t* qs = w + 48;
+            for (int s = 0; s < 8; s++) {
+                int g = s / 2, bi = 8 * B + s, dot = 0;
+                for (int e = 0; e < 32; e++) {
+                    uint8_t q = qs[32 * g + e];
+                    int q5 = ((s & 1) ? (q >> 4) : (q & 15)) | (((qh[e] >> s) & 1) << 4);
+                    dot += q5 * xq[32 * bi + e];
+                }
+                float dw = d * (float) sc[s], mw = dmin * (float) mn[s];
+                acc += (double)(dw * dx[bi]) * dot - (double) mw * (double)(xs[2 * bi] + xs[2 * bi + 1]);
+            }
+        }
+        return acc;
+    }
+    if (dt == JO_Q1_0) {   /* q1_0_block16 (q4k_avx512.c:580-598): fl(d·fl(2·dx))·Σbit·xq − d·fl(xs0+xs1) */
+        for (int bb = 0; bb < k / 128; bb++, w += 18) {
+            float d = h2f_at(w);
+            for (int K = 0; K < 4; K++) {
+                int bi = 4 * bb + K, dot = 0;
+                for (int e = 0; e < 32; e++) {
+                    int el = 32 * K + e;
+                    if ((w[2 + (el >> 3)] >> (el & 7)) & 1) dot += xq[32 * bi + e];
+                }
+                acc += (double)(d * (2.0f * dx[bi])) * dot - (double) d * (double)(xs[2 * bi] + xs[2 * bi + 1]);
+            }
+        }
+        return acc;
+    }
     return 0.0;
 }
 
 static int int8_supported(int dt) {
-    return dt == JO_Q8_0 || dt == JO_Q4_0 || dt == JO_MXFP4 || dt == JO_Q4_K || dt == JO_Q6_K;
+    return dt == JO_Q8_0 || dt == JO_Q4_0 || dt == JO_MXFP4 || dt == JO_Q4_K || dt == JO_Q6_K || dt == JO_Q5_K ||
+           dt == JO_NVFP4 || dt == JO_Q1_0;
+}
+
+/* jam's block-alignment rule per dtype (jam.c:665-685, 752): k on the block for every quantized dtype;
+ * ldw on it too for the 32-element types and Q1_0, while the K-quants and NVFP4 take the row stride as
+ * (ldw / block) blocks. */
+static int aligned(int dt, int ldw, int k) {
+    int be = jo_block_elems(dt);
+    if (k % be) return 0;
+    if (dt == JO_Q4_K || dt == JO_Q5_K || dt == JO_Q6_K || dt == JO_NVFP4) return 1;
+    return ldw % be == 0;
 }
 
 /* Exact float dot of one dequantized weight row with an f32 activation row (double accumulation): the
@@ -516,11 +720,13 @@ static double row_float(int dt, const uint8_t* w, const float* x, int k) {
 
 int jo_mm_int8(int dt, const uint8_t* w, int ldw, const float* a, int lda, float* c, int ldc,
                int m, int n, int k, int flavour) {
-    if (!int8_supported(dt) || k % jo_block_elems(dt) || ldw % jo_block_elems(dt)) return -1;
+    if (!int8_supported(dt) || !aligned(dt, ldw, k)) return -1;
     /* flavour 0 = jam's own routing on an AVX-512-VNNI host (jam.c:469-499, 544-560, 682-730): n < 8 runs
-     * F1 on every row; n >= 8 runs the 16-row F2 bands and leaves the last m % 16 rows to a float dot. */
+     * F1 on every row; n >= 8 runs the 16-row F2 bands and leaves the last m % 16 rows to a float dot.
+     * NVFP4 has no band: run_quant's F1 kernel takes every n (jam.c:662-668). */
     const int jam_rule = flavour == 0;
-    if (flavour == 0) flavour = n < 8 ? 1 : 2;
+    if (dt == JO_NVFP4 && flavour == 2) return -1;
+    if (flavour == 0) flavour = n < 8 || dt == JO_NVFP4 ? 1 : 2;
     const int m_int8 = jam_rule && flavour == 2 ? m - m % 16 : m;
     int nb = k / 32;
     int8_t* q = (int8_t*) malloc((size_t) n * k);
@@ -547,10 +753,34 @@ int jo_mm_int8(int dt, const uint8_t* w, int ldw, const float* a, int lda, float
     return 0;
 }
 
+int jo_bf16_rounds_activations(int n, int k) {   /* jam.c:622-652 on an AVX-512-BF16 host */
+    return (n >= 8 && k % 2 == 0) || k % 32 == 0;
+}
+
+int jo_mm_dense(int dt, const uint8_t* w, int ldw, const float* a, int lda, float* c, int ldc, int m, int n, int k) {
+    if (dt != JO_F32 && dt != JO_F16 && dt != JO_BF16) return -1;
+    const int es = jo_block_bytes(dt), rnd = dt == JO_BF16 && jo_bf16_rounds_activations(n, k);
+    double* row = (double*) malloc(sizeof(double) * (size_t) k);
+    double* x = (double*) malloc(sizeof(double) * (size_t) k);
+    for (int j = 0; j < n; j++) {
+        const float* aj = a + (size_t) j * lda;
+        for (int e = 0; e < k; e++) x[e] = rnd ? bf16f(jo_float2bf16(aj[e])) : aj[e];
+        for (int i = 0; i < m; i++) {
+            jo_dequant_row_f64(dt, w + (int64_t) i * ldw * es, k, row);
+            double s = 0.0;
+            for (int e = 0; e < k; e++) s += row[e] * x[e];
+            c[(size_t) j * ldc + i] = (float) s;
+        }
+    }
+    free(row);
+    free(x);
+    return 0;
+}
+
 int jo_mm_ref(int dt, const uint8_t* w, int ldw, const float* a, int lda, double* c, double* sumabs,
               int ldc, int m, int n, int k) {
     int be = jo_block_elems(dt);
-    if (!be || k % be || ldw % be) return -1;
+    if (!be || k % be || (be > 1 && !aligned(dt, ldw, k))) return -1;
     int64_t wstride = (int64_t)(ldw / be) * jo_block_bytes(dt);
     double* row = (double*) malloc(sizeof(double) * (size_t) k);
     for (int i = 0; i < m; i++) {

@@ -28,7 +28,7 @@ extern "C" {
 
 /* ggml / jam dtype tags (jam/jam-native/include/jam.h:59-77; jam/jam-core/.../JAM.java:74-84). */
 enum { JO_F32 = 0, JO_F16 = 1, JO_Q4_0 = 2, JO_Q8_0 = 8, JO_Q4_K = 12, JO_Q5_K = 13, JO_Q6_K = 14,
-       JO_BF16 = 30, JO_MXFP4 = 39 };
+       JO_BF16 = 30, JO_MXFP4 = 39, JO_NVFP4 = 40, JO_Q1_0 = 41 };
 
 /* Block geometry: elements and bytes per block (jam/jam-core/.../GGMLType.java:15-26). 0 if unknown. */
 int    jo_block_elems(int dtype);
@@ -44,6 +44,13 @@ uint16_t jo_float2half(float f);
 /* E8M0 byte -> 2^(e-128) = 0.5*2^(e-127); e=0 -> 2^-128, e=255 -> +Inf
  * (jam/jam-native/src/kernels/jam_mxfp4.h:17-24). */
 float    jo_e8m0_half(uint8_t e);
+
+/* UE4M3 byte -> float as jam_ue4m3_to_float (jam/jam-native/src/kernels/jam_nvfp4.h:19-25): bit 7 ignored
+ * but 0x00 and 0x7F (exactly) give 0; normal (1 + m/8)·2^(e-7), subnormal m·2^-9. */
+float    jo_ue4m3(uint8_t x);
+/* float -> bf16, round to nearest even (NaN kept quiet); what vcvtne2ps2bf16 does to jam's BF16 activations
+ * (jam_kernels_bf16_avx512bf16.c). */
+uint16_t jo_float2bf16(float f);
 
 /* Decode one weight row of `k` elements (GGUF block layout) to float values
  * (jam_kernels_generic.c:42-321; ScalarJAM.java:95-201). Q4_K/Q6_K/Q5_K values are computed in double
@@ -71,6 +78,15 @@ void jo_quant_f2(const float* x, int k, int8_t* q, float* d, float* xsum16);
  * Returns 0, or -1 for an unsupported dtype/shape. */
 int jo_mm_int8(int dtype, const uint8_t* w, int ldw, const float* a, int lda, float* c, int ldc,
                int m, int n, int k, int flavour);
+
+/* jam's dense paths (F32, F16, BF16 weights; jam.c:596-660) on an AVX-512-BF16 host: F32 and F16 take the
+ * f32 activations as they are; BF16 rounds the activations to bf16 (vcvtne2ps2bf16) whenever jam's bf16
+ * kernels take the call (n >= 8 with k even, or k % 32 == 0) and keeps them f32 otherwise (the dense
+ * convert-and-FMA floor). Products are exact; summed in double. Returns 0, or -1 for another dtype. */
+int jo_mm_dense(int dtype, const uint8_t* w, int ldw, const float* a, int lda, float* c, int ldc, int m, int n,
+                int k);
+/* 1 if jo_mm_dense rounds BF16 activations to bf16 for this (n, k). */
+int jo_bf16_rounds_activations(int n, int k);
 
 /* Float reference: C = Σ dequant(W)·A in double, plus sumabs = Σ|w·a| (QuantWeights.refDot contract,
  * jam/jam-vector/src/test/java/com/qxotic/jam/QuantWeights.java:67-75). Either output may be NULL. */

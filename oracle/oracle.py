@@ -21,12 +21,15 @@ ORACLE_SO = HERE / "_build" / "liboracle.so"
 REF_SO = HERE / "_ref" / "libjam.so"
 
 # ggml / jam dtype tags (jam/jam-native/include/jam.h:59-77)
-F32, F16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, BF16, MXFP4 = 0, 1, 2, 8, 12, 13, 14, 30, 39
+F32, F16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, BF16, MXFP4, NVFP4, Q1_0 = 0, 1, 2, 8, 12, 13, 14, 30, 39, 40, 41
 BLOCK = {F32: (1, 4), F16: (1, 2), BF16: (1, 2), Q4_0: (32, 18), Q8_0: (32, 34), MXFP4: (32, 17),
-         Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210)}
+         Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210), NVFP4: (64, 36), Q1_0: (128, 18)}
 NAMES = {Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K", MXFP4: "MXFP4", Q5_K: "Q5_K",
-         F32: "F32", F16: "F16", BF16: "BF16"}
+         F32: "F32", F16: "F16", BF16: "BF16", NVFP4: "NVFP4", Q1_0: "Q1_0"}
 QUANT_TYPES = (Q8_0, Q4_0, Q4_K, Q6_K, MXFP4)
+NEW_QUANT_TYPES = (Q5_K, NVFP4, Q1_0)          # jam's int8 pipeline, added after the first five
+ALL_QUANT_TYPES = QUANT_TYPES + NEW_QUANT_TYPES
+DENSE_TYPES = (F32, F16, BF16)                 # jam's dense float paths
 
 
 def row_bytes(dt: int, k: int) -> int:
@@ -59,6 +62,11 @@ class Oracle:
         L.jo_mm_int8.restype = i32
         L.jo_mm_ref.argtypes = [i32, vp, i32, vp, i32, vp, vp, i32, i32, i32, i32]
         L.jo_mm_ref.restype = i32
+        L.jo_mm_dense.argtypes = [i32, vp, i32, vp, i32, vp, i32, i32, i32, i32]
+        L.jo_mm_dense.restype = i32
+        L.jo_bf16_rounds_activations.argtypes, L.jo_bf16_rounds_activations.restype = [i32, i32], i32
+        L.jo_ue4m3.argtypes, L.jo_ue4m3.restype = [C.c_uint8], f32
+        L.jo_float2bf16.argtypes, L.jo_float2bf16.restype = [f32], C.c_uint16
         L.jo_fill_normal.argtypes = [u64, vp, C.c_size_t, f32, f32]
         L.jo_fill_outliers.argtypes = [u64, vp, C.c_size_t, f32, f32]
 
@@ -122,6 +130,22 @@ class Oracle:
         if rc:
             raise ValueError("jo_mm_int8: unsupported")
         return c
+
+    def mm_dense(self, dt, w, a, m, n, k, ldw=None) -> np.ndarray:
+        """jam's dense F32 / F16 / BF16 paths, C[n, m] (BF16 rounds the activations where jam does)."""
+        ldw = ldw or k
+        w = np.ascontiguousarray(w, dtype=np.uint8)
+        a = np.ascontiguousarray(a, dtype=np.float32)
+        c = np.zeros((n, m), np.float32)
+        if self.lib.jo_mm_dense(dt, _p(w), ldw, _p(a), a.shape[-1], _p(c), m, m, n, k):
+            raise ValueError("jo_mm_dense: unsupported")
+        return c
+
+    def mm(self, dt, w, a, m, n, k, ldw=None) -> np.ndarray:
+        """jam's own answer for any dtype: the int8 pipeline for quantized weights, the dense paths else."""
+        if dt in DENSE_TYPES:
+            return self.mm_dense(dt, w, a, m, n, k, ldw)
+        return self.mm_int8(dt, w, a, m, n, k, ldw)
 
     def mm_ref(self, dt, w, a, m, n, k, ldw=None):
         """Float reference in double: (C[n, m], sumabs[n, m])."""

@@ -32,6 +32,10 @@ UNITS = {   # source -> extra flags
     "gemv_q80.hip": [],
     "gemv_q40.hip": [],
     "gemv_mxfp4.hip": [],
+    "gemv_q5k.hip": [],
+    "gemv_nvfp4.hip": [],
+    "gemv_q10.hip": [],
+    "dense.hip": [],
     "gemm.hip": [],
     "mma.hip": [],
     "moe.hip": [],

@@ -7,16 +7,21 @@
 namespace jamhip {
 
 // ggml / jam dtype tags (jam/jam-native/include/jam.h:59-77).
-enum Dtype : int { F32 = 0, F16 = 1, Q4_0 = 2, Q8_0 = 8, Q4_K = 12, Q5_K = 13, Q6_K = 14, BF16 = 30, MXFP4 = 39 };
+enum Dtype : int {
+    F32 = 0, F16 = 1, Q4_0 = 2, Q8_0 = 8, Q4_K = 12, Q5_K = 13, Q6_K = 14, BF16 = 30, MXFP4 = 39, NVFP4 = 40, Q1_0 = 41
+};
 
 // GGUF block geometry (jam/jam-core/src/main/java/com/qxotic/jam/GGMLType.java:15-26).
 __host__ __device__ constexpr int block_elems(int dt) {
-    return dt == Q4_K || dt == Q5_K || dt == Q6_K ? 256 : (dt == Q8_0 || dt == Q4_0 || dt == MXFP4) ? 32 : 1;
+    return dt == Q4_K || dt == Q5_K || dt == Q6_K ? 256 : (dt == Q8_0 || dt == Q4_0 || dt == MXFP4) ? 32
+         : dt == NVFP4 ? 64 : dt == Q1_0 ? 128 : 1;
 }
 __host__ __device__ constexpr int block_bytes(int dt) {
     return dt == Q8_0 ? 34 : dt == Q4_0 ? 18 : dt == MXFP4 ? 17 : dt == Q4_K ? 144 : dt == Q5_K ? 176
-         : dt == Q6_K ? 210 : dt == F32 ? 4 : 2;
+         : dt == Q6_K ? 210 : dt == NVFP4 ? 36 : dt == Q1_0 ? 18 : dt == F32 ? 4 : 2;
 }
+// Dense (one element per block) weight types: F32, F16, BF16.
+__host__ __device__ constexpr bool is_dense(int dt) { return dt == F32 || dt == F16 || dt == BF16; }
 
 // Device layout of a pinned weight tensor ("row-tiled groups"). A row of k elements is cut into groups
 // of 256 elements (one super-block, or 8 blocks of 32; a row whose block count is not a multiple of 8
@@ -27,6 +32,9 @@ __host__ __device__ constexpr int block_bytes(int dt) {
 //   Q4_0 : NC 8  chunk c = block c's 16 nibble bytes           | SB 16: the 8 blocks' fp16 d
 //   MXFP4: NC 8  chunk c = block c's 16 nibble bytes           | SB 16: the 8 blocks' e8m0, then their
 //                                                                maximum (the group's reference exponent)
+//   Q5_K : NC 10 chunks 0-7 qs nibble bytes, 8-9 the qh bytes   | SB 16: d, dmin, 12 scale bytes
+//   NVFP4: NC 8  chunk 2j + h = half h of 64-block j's qs       | SB 16: the 4 blocks' 4 UE4M3 scales
+//   Q1_0 : NC 2  chunk j = 128-block j's 16 sign bytes          | SB 4 : the 2 blocks' fp16 d
 // Rows are taken in tiles of 32 (the row count is padded up to a multiple of 32 with zero rows). Plane 0
 // ("qs") holds chunk c of group g of row r at byte ((T·G + g)·NC + c)·512 + (r mod 32)·16 with T = r / 32
 // and G = groups per row: for a fixed (tile, group, chunk) the 32 rows' chunks are 512 contiguous bytes,
@@ -35,10 +43,12 @@ __host__ __device__ constexpr int block_bytes(int dt) {
 // at byte ((T·G + g)·32 + r mod 32)·SB. Every GGUF byte is kept; only the order changes.
 constexpr int ROW_TILE = 32;   // the shifts below assume 32
 __host__ __device__ constexpr int group_chunks(int dt) {
-    return dt == Q4_K ? 8 : dt == Q6_K ? 13 : dt == Q8_0 ? 16 : dt == Q4_0 ? 8 : dt == MXFP4 ? 8 : 0;
+    return dt == Q4_K ? 8 : dt == Q6_K ? 13 : dt == Q8_0 ? 16 : dt == Q4_0 ? 8 : dt == MXFP4 ? 8 : dt == Q5_K ? 10
+         : dt == NVFP4 ? 8 : dt == Q1_0 ? 2 : 0;
 }
 __host__ __device__ constexpr int group_scale_bytes(int dt) {
-    return dt == Q4_K ? 16 : dt == Q6_K ? 2 : dt == Q8_0 ? 16 : dt == Q4_0 ? 16 : dt == MXFP4 ? 16 : 0;
+    return dt == Q4_K ? 16 : dt == Q6_K ? 2 : dt == Q8_0 ? 16 : dt == Q4_0 ? 16 : dt == MXFP4 ? 16 : dt == Q5_K ? 16
+         : dt == NVFP4 ? 16 : dt == Q1_0 ? 4 : 0;
 }
 __host__ __device__ constexpr int blocks_per_group(int dt) { return 256 / block_elems(dt); }
 // groups per row for a row of `blocks` blocks
@@ -47,6 +57,23 @@ __host__ __device__ constexpr int64_t groups_of(int dt, int64_t blocks) {
 }
 // rows held by a device copy of m rows (whole 32-row tiles)
 __host__ __device__ constexpr int64_t tiled_rows(int64_t m) { return (m + ROW_TILE - 1) / ROW_TILE * ROW_TILE; }
+
+// Dense weights are kept row-major on the device, each row padded with zeros to a 256-byte pitch (so every
+// row starts 16-byte aligned for vector loads and the padding reads as zeros); WeightView::G then holds the
+// pitch in bytes. The sizes of a device copy of `rows` rows of `ldw` elements, for any weight type:
+__host__ __device__ constexpr int64_t dense_pitch(int dt, int64_t ldw) { return (ldw * block_bytes(dt) + 255) / 256 * 256; }
+// WeightView::G of such a copy: groups per row (quantized) or the pitch (dense)
+__host__ __device__ constexpr int64_t view_G(int dt, int64_t ldw) {
+    return is_dense(dt) ? dense_pitch(dt, ldw) : groups_of(dt, ldw / block_elems(dt));
+}
+// plane-0 and plane-1 bytes of the copy (plane 0 rounded to 256 bytes; dense types have no plane 1)
+__host__ __device__ constexpr int64_t plane0_bytes(int dt, int64_t rows, int64_t ldw) {
+    return is_dense(dt) ? rows * dense_pitch(dt, ldw)
+                        : (tiled_rows(rows) * view_G(dt, ldw) * group_chunks(dt) * 16 + 255) / 256 * 256;
+}
+__host__ __device__ constexpr int64_t plane1_bytes(int dt, int64_t rows, int64_t ldw) {
+    return is_dense(dt) ? 0 : tiled_rows(rows) * view_G(dt, ldw) * group_scale_bytes(dt);
+}
 
 // Fused epilogue of a matmul's final store: C = [C_old +] (W·A [+ bias[row]]), the bias add first and the
 // residual add second, the f32 operations jinfer runs after MatMul.gemm (Ops.addRowBiasInPlace, then

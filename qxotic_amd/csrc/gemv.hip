@@ -19,6 +19,15 @@ extern template hipError_t rows_float_dt<Q4_0>(const WeightView& w, const float*
 extern template hipError_t gemv_dt<MXFP4>(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m, int n, float* c, int ldc, hipStream_t st, float* part, const Epi& ep);
 extern template hipError_t gemv_grouped_dt<MXFP4>(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, const Groups& g, int E, int cap8, float* c, int ldc, hipStream_t st);
 extern template hipError_t rows_float_dt<MXFP4>(const WeightView& w, const float* a, int lda, int k, int r0, int rows, int n, float* c, int ldc, hipStream_t st, const Epi& ep);
+extern template hipError_t gemv_dt<Q5_K>(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m, int n, float* c, int ldc, hipStream_t st, float* part, const Epi& ep);
+extern template hipError_t gemv_grouped_dt<Q5_K>(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, const Groups& g, int E, int cap8, float* c, int ldc, hipStream_t st);
+extern template hipError_t rows_float_dt<Q5_K>(const WeightView& w, const float* a, int lda, int k, int r0, int rows, int n, float* c, int ldc, hipStream_t st, const Epi& ep);
+extern template hipError_t gemv_dt<NVFP4>(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m, int n, float* c, int ldc, hipStream_t st, float* part, const Epi& ep);
+extern template hipError_t gemv_grouped_dt<NVFP4>(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, const Groups& g, int E, int cap8, float* c, int ldc, hipStream_t st);
+extern template hipError_t rows_float_dt<NVFP4>(const WeightView& w, const float* a, int lda, int k, int r0, int rows, int n, float* c, int ldc, hipStream_t st, const Epi& ep);
+extern template hipError_t gemv_dt<Q1_0>(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m, int n, float* c, int ldc, hipStream_t st, float* part, const Epi& ep);
+extern template hipError_t gemv_grouped_dt<Q1_0>(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, const Groups& g, int E, int cap8, float* c, int ldc, hipStream_t st);
+extern template hipError_t rows_float_dt<Q1_0>(const WeightView& w, const float* a, int lda, int k, int r0, int rows, int n, float* c, int ldc, hipStream_t st, const Epi& ep);
 
 hipError_t launch_gemv_grouped(int dt, int flavour, const WeightView& w, const ActQ& A, const float* a, int lda,
                                int k, const Groups& g, int E, int cap8, float* c, int ldc, hipStream_t st) {
@@ -29,6 +38,9 @@ hipError_t launch_gemv_grouped(int dt, int flavour, const WeightView& w, const A
     case Q8_0: return gemv_grouped_dt<Q8_0>(flavour, w, A, a, lda, k, g, E, cap8, c, ldc, st);
     case Q4_0: return gemv_grouped_dt<Q4_0>(flavour, w, A, a, lda, k, g, E, cap8, c, ldc, st);
     case MXFP4: return gemv_grouped_dt<MXFP4>(flavour, w, A, a, lda, k, g, E, cap8, c, ldc, st);
+    case Q5_K: return gemv_grouped_dt<Q5_K>(flavour, w, A, a, lda, k, g, E, cap8, c, ldc, st);
+    case NVFP4: return gemv_grouped_dt<NVFP4>(flavour, w, A, a, lda, k, g, E, cap8, c, ldc, st);
+    case Q1_0: return gemv_grouped_dt<Q1_0>(flavour, w, A, a, lda, k, g, E, cap8, c, ldc, st);
     default: return hipErrorInvalidValue;
     }
 }
@@ -55,6 +67,9 @@ hipError_t launch_gemv(int dt, int flavour, const WeightView& w, const ActQ& A, 
     case Q8_0: return gemv_dt<Q8_0>(flavour, w, A, a, lda, k, m, n, c, ldc, st, part, ep);
     case Q4_0: return gemv_dt<Q4_0>(flavour, w, A, a, lda, k, m, n, c, ldc, st, part, ep);
     case MXFP4: return gemv_dt<MXFP4>(flavour, w, A, a, lda, k, m, n, c, ldc, st, part, ep);
+    case Q5_K: return gemv_dt<Q5_K>(flavour, w, A, a, lda, k, m, n, c, ldc, st, part, ep);
+    case NVFP4: return gemv_dt<NVFP4>(flavour, w, A, a, lda, k, m, n, c, ldc, st, part, ep);
+    case Q1_0: return gemv_dt<Q1_0>(flavour, w, A, a, lda, k, m, n, c, ldc, st, part, ep);
     default: return hipErrorInvalidValue;
     }
 }
@@ -68,6 +83,9 @@ hipError_t launch_rows_float(int dt, const WeightView& w, const float* a, int ld
     case Q8_0: return rows_float_dt<Q8_0>(w, a, lda, k, r0, rows, n, c, ldc, st, ep);
     case Q4_0: return rows_float_dt<Q4_0>(w, a, lda, k, r0, rows, n, c, ldc, st, ep);
     case MXFP4: return rows_float_dt<MXFP4>(w, a, lda, k, r0, rows, n, c, ldc, st, ep);
+    case Q5_K: return rows_float_dt<Q5_K>(w, a, lda, k, r0, rows, n, c, ldc, st, ep);
+    case NVFP4: return rows_float_dt<NVFP4>(w, a, lda, k, r0, rows, n, c, ldc, st, ep);
+    case Q1_0: return rows_float_dt<Q1_0>(w, a, lda, k, r0, rows, n, c, ldc, st, ep);
     default: return hipErrorInvalidValue;
     }
 }

@@ -47,6 +47,8 @@ template <int DT>
 JAMHIP_DEV void load_scales(Group<DT>& r, const uint8_t* s) {
     if constexpr (DT == Q6_K) {
         r.s.x = *reinterpret_cast<const uint16_t*>(s);
+    } else if constexpr (DT == Q1_0) {
+        r.s.x = *reinterpret_cast<const uint32_t*>(s);
     } else if constexpr (DT == MXFP4) {
         const uint2 v = *reinterpret_cast<const uint2*>(s);
         r.s = make_uint4(v.x, v.y, 0u, 0u);
@@ -109,6 +111,32 @@ JAMHIP_DEV void q4k_sm(const uint4 h, int s, int& sc, int& mn) {
 
 JAMHIP_DEV int sbyte(uint32_t w, int b) { return (int) (int8_t) (w >> (8 * b)); }
 
+// UE4M3 byte -> float as jam_ue4m3_to_float (jam/jam-native/src/kernels/jam_nvfp4.h:19-25): 0x00 and 0x7F give
+// 0, otherwise bit 7 is ignored; normal (1 + m/8)·2^(e-7) built from its bits, subnormal m·2^-9 (exact).
+JAMHIP_DEV float ue4m3(uint32_t x) {
+    const uint32_t e = (x >> 3) & 15u, m = x & 7u;
+    const float normal = __builtin_bit_cast(float, ((e + 120u) << 23) | (m << 20));
+    const float sub = (float) m * 0.001953125f;
+    return (x & 0xffu) == 0u || (x & 0xffu) == 0x7fu ? 0.0f : e ? normal : sub;
+}
+
+// Q1_0: sign bits b0..b3 of a nibble -> the bytes (b0, b1, b2, b3) as 0 / 1 (the products b·2^(7j) land on
+// distinct bits, so the multiply carries nothing into the kept ones).
+JAMHIP_DEV uint32_t bits4_to_bytes(uint32_t b) { return ((b & 15u) * 0x00204081u) & 0x01010101u; }
+
+// Σ bit·q over one 32-element block: its 32 sign bits against its 32 int8 activation codes.
+JAMHIP_DEV int q1_dot01(uint32_t bits, const int8_t* aq) {
+    const uint4 a0 = ld16(aq), a1 = ld16(aq + 16);
+    int I = dot4((int) bits4_to_bytes(bits), (int) a0.x, 0);
+    I = dot4((int) bits4_to_bytes(bits >> 4), (int) a0.y, I);
+    I = dot4((int) bits4_to_bytes(bits >> 8), (int) a0.z, I);
+    I = dot4((int) bits4_to_bytes(bits >> 12), (int) a0.w, I);
+    I = dot4((int) bits4_to_bytes(bits >> 16), (int) a1.x, I);
+    I = dot4((int) bits4_to_bytes(bits >> 20), (int) a1.y, I);
+    I = dot4((int) bits4_to_bytes(bits >> 24), (int) a1.z, I);
+    return dot4((int) bits4_to_bytes(bits >> 28), (int) a1.w, I);
+}
+
 // Q6_K 6-bit codes of ql chunk c with the matching qh chunk: the low-nibble group and the high one.
 JAMHIP_DEV void q6k_codes(const uint4 ql, const uint4 qh, int jj, uint4& qa, uint4& qb) {
     const uint4 hia = and4(shr4(qh, 2 * jj), 0x03030303u), hib = and4(shr4(qh, 2 * jj + 4), 0x03030303u);
@@ -149,6 +177,87 @@ JAMHIP_DEV float group_dot(const Group<DT>& w, const int8_t* aq, const float* ad
             }
         }
         return FL == 1 ? acc - dmin * msum : acc - msum;
+    } else if constexpr (DT == Q5_K) {
+        const uint4 h = w.s;
+        const float d = h2f(h.x & 0xffffu), dmin = h2f(h.x >> 16);
+        float acc = 0.0f, msum = 0.0f;
+#pragma unroll
+        for (int s = 0; s < 8; s++) {   // sub-block s: Q4_K's nibbles plus bit s of qh[l] as bit 4
+            const int c0 = 2 * (s >> 1);
+            const uint4 b0 = make_uint4((w.q[8].x >> s) & 0x01010101u, (w.q[8].y >> s) & 0x01010101u,
+                                        (w.q[8].z >> s) & 0x01010101u, (w.q[8].w >> s) & 0x01010101u);
+            const uint4 b1 = make_uint4((w.q[9].x >> s) & 0x01010101u, (w.q[9].y >> s) & 0x01010101u,
+                                        (w.q[9].z >> s) & 0x01010101u, (w.q[9].w >> s) & 0x01010101u);
+            const uint4 n0 = (s & 1) ? hi_nib(w.q[c0]) : lo_nib(w.q[c0]);
+            const uint4 n1 = (s & 1) ? hi_nib(w.q[c0 + 1]) : lo_nib(w.q[c0 + 1]);
+            const uint4 w0 = make_uint4(n0.x | (b0.x << 4), n0.y | (b0.y << 4), n0.z | (b0.z << 4), n0.w | (b0.w << 4));
+            const uint4 w1 = make_uint4(n1.x | (b1.x << 4), n1.y | (b1.y << 4), n1.z | (b1.z << 4), n1.w | (b1.w << 4));
+            const int I = dot16(w1, ld16(aq + 32 * s + 16), dot16(w0, ld16(aq + 32 * s), 0));
+            int sc, mn;
+            q4k_sm(h, s, sc, mn);
+            const float dl = d * (float) sc, ml = dmin * (float) mn;
+            if constexpr (FL == 1) {
+                // jam_mm_q5k_sse3 (jam_kernels_kquant_sse3.c:70-121): ad·(fl(dl·I) − fl(ml·asum)) per 32
+                acc += ad[s] * (dl * (float) I - ml * as[s]);
+            } else {
+                // q5k_block16 (jam_kernels_q4k_avx512.c:798-811): fl(dl·dx)·I − ml·fl(xs0+xs1)
+                acc += (float) I * (dl * ad[s]);
+                msum += ml * (as[2 * s] + as[2 * s + 1]);
+            }
+        }
+        return acc - msum;
+    } else if constexpr (DT == NVFP4) {
+        // jam_mm_nvfp4_avx512 (jam_kernels_avx512bw.c:111-142; jam's only NVFP4 kernel shape: F1 at every n):
+        // per 16-element sub-block s of 64-block j, Σ code·q times fl(ue4m3(d_s)·ad of its 32-block)
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const bool live = 2 * j < nbv;
+            const int jj = live ? j : nbv / 2 - 1;   // stay inside the token's activations
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                const uint4 ch = w.q[2 * j + (s >> 1)];
+                const uint32_t w0 = word(ch, 2 * (s & 1)), w1 = word(ch, 2 * (s & 1) + 1);
+                const uint4 A = ld16(aq + 64 * jj + 16 * s);
+                int I = dot4((int) mxfp4_codes(w0 & 0x0f0f0f0fu), (int) A.x, 0);
+                I = dot4((int) mxfp4_codes(w1 & 0x0f0f0f0fu), (int) A.y, I);
+                I = dot4((int) mxfp4_codes((w0 >> 4) & 0x0f0f0f0fu), (int) A.z, I);
+                I = dot4((int) mxfp4_codes((w1 >> 4) & 0x0f0f0f0fu), (int) A.w, I);
+                const float sc = ue4m3((word(w.s, j) >> (8 * s)) & 0xffu) * ad[2 * jj + (s >> 1)];
+                acc += live ? (float) I * sc : 0.0f;
+            }
+        }
+        return acc;
+    } else if constexpr (DT == Q1_0) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const bool live = 4 * j < nbv;
+            const int jj = live ? j : nbv / 4 - 1;   // stay inside the token's activations
+            const float d = h2f((w.s.x >> (16 * j)) & 0xffffu);
+            if constexpr (FL == 1) {
+                // jam_mm_q1_0_avx2 (jam_kernels_q1_0_avx2.c:45-86): d · Σ_K fma(ad_K, Σ±q) per 128-block,
+                // Σ±q = 2·Σbit·q − Σq (exact ints)
+                float fb = 0.0f;
+#pragma unroll
+                for (int K = 0; K < 4; K++) {
+                    const int b = 4 * jj + K;
+                    const int I = 2 * q1_dot01(word(w.q[j], K), aq + 32 * b) - (s16[2 * b] + s16[2 * b + 1]);
+                    fb = fmaf(ad[b], (float) I, fb);
+                }
+                acc += live ? d * fb : 0.0f;
+            } else {
+                // q1_0_block16 (jam_kernels_q4k_avx512.c:580-598): fl(d·fl(2·dx))·Σbit·xq − d·fl(xs0+xs1)
+#pragma unroll
+                for (int K = 0; K < 4; K++) {
+                    const int b = 4 * jj + K;
+                    const int I = q1_dot01(word(w.q[j], K), aq + 32 * b);
+                    const float v = (float) I * (d * (2.0f * ad[b])) - d * (as[2 * b] + as[2 * b + 1]);
+                    acc += live ? v : 0.0f;
+                }
+            }
+        }
+        return acc;
     } else if constexpr (DT == Q6_K) {
         const float d = h2f(w.s.x & 0xffffu);
         const uint4 scv = w.q[12];
@@ -421,7 +530,7 @@ template <int DT, int FL, int NT, int HP, int RB, int ITEMS, bool GR, bool SK, i
 __global__ void __launch_bounds__(64 * NWV) mv_kernel(WeightView w, ActQ A, const float* __restrict__ a,
                                                           int lda, int k, int m, int n, float* __restrict__ c,
                                                           int ldc, Groups gp, int ks, int64_t cz, Epi ep) {
-    constexpr int BPG = blocks_per_group(DT), GS = 64 / RB;
+    constexpr int GS = 64 / RB;
     // SK (split K): workgroup column blockIdx.z takes elements [k0, k0 + ks) (ks a multiple of 256; the last
     // slice may be shorter) and writes its partial result at c + blockIdx.z·cz; J, and so the block shape,
     // comes from the full slice length, so every slice has the same grid
@@ -548,7 +657,7 @@ __global__ void __launch_bounds__(64 * NWV) mv_kernel(WeightView w, ActQ A, cons
         const int g = GS * (it % J) + gs;
         const bool live = g < Gk && it < QB * J && RB * (q0 + it / J) + rr < m;
         const int gg = g < Gk ? g : Gk - 1;
-        const int nbv = nb - BPG * gg < BPG ? nb - BPG * gg : BPG;
+        const int nbv = nb - 8 * gg < 8 ? nb - 8 * gg : 8;   // the group's 32-blocks inside the slice
         float* pp = part + (it * 64 + lane) * NT;
         if constexpr (NT <= 2 || DT != Q4_0) {   // per-token unpacking measured faster for the rest
             constexpr int TU = NT > 2 ? 1 : NT;   // keep several tokens' temporaries out of the register file
@@ -617,16 +726,26 @@ JAMHIP_DEV float deq(const WeightView& w, int64_t row, int elem) {
         const uint8_t b = qb(16 * (e >> 5) + (e & 15));
         const uint32_t code = mxfp4_codes((e & 31) < 16 ? b & 15 : b >> 4);
         return e8m0_half(s[e >> 5]) * (float) (int8_t) (code & 0xff);
-    } else if constexpr (DT == Q4_K) {
+    } else if constexpr (DT == NVFP4) {   // 64-block j, sub-block s: byte 8s + (i & 7), high nibble from i = 8
+        const int j = e >> 6, sb = (e >> 4) & 3, i = e & 15;
+        const uint8_t b = qb(32 * j + 8 * sb + (i & 7));
+        const uint32_t code = mxfp4_codes(i < 8 ? b & 15 : b >> 4);
+        return ue4m3(s[4 * j + sb]) * (float) (int8_t) (code & 0xff);
+    } else if constexpr (DT == Q1_0) {
+        const int j = e >> 7, i = e & 127;
+        const float d = f16(s + 2 * j);
+        return (qb(16 * j + (i >> 3)) >> (i & 7)) & 1 ? d : -d;
+    } else if constexpr (DT == Q4_K || DT == Q5_K) {
         const int gp = e >> 6, half = (e >> 5) & 1, l = e & 31, sb = 2 * gp + half;
         const uint8_t b = qb(32 * gp + l);
+        const int hb = DT == Q5_K ? ((qb(128 + l) >> sb) & 1) << 4 : 0;
         const uint4 h = make_uint4(s[0] | s[1] << 8 | s[2] << 16 | (uint32_t) s[3] << 24,
                                    s[4] | s[5] << 8 | s[6] << 16 | (uint32_t) s[7] << 24,
                                    s[8] | s[9] << 8 | s[10] << 16 | (uint32_t) s[11] << 24,
                                    s[12] | s[13] << 8 | s[14] << 16 | (uint32_t) s[15] << 24);
         int sc, mn;
         q4k_sm(h, sb, sc, mn);
-        return f16(s) * (float) sc * (float) (half ? b >> 4 : b & 15) - f16(s + 2) * (float) mn;
+        return f16(s) * (float) sc * (float) ((half ? b >> 4 : b & 15) | hb) - f16(s + 2) * (float) mn;
     } else {
         const int hh = e >> 7, j = (e & 127) >> 5, l = e & 31;
         const uint8_t qlb = qb(64 * hh + (j & 1) * 32 + l);
@@ -717,7 +836,7 @@ static void launch_shape(int k, int ks, int64_t cz, int m, int n, const WeightVi
     const int Gk = (ks / 32 + 7) / 8, J = (Gk + GS - 1) / GS;
     const int QB = NWV * ITEMS / J;
     const int64_t bands = ((int64_t) m + RB - 1) / RB;
-    const dim3 grid((unsigned) ((bands + QB - 1) / QB), FL == 1 ? 1 : (n + NT - 1) / NT, (unsigned) ((k + ks - 1) / ks));
+    const dim3 grid((unsigned) ((bands + QB - 1) / QB), (n + NT - 1) / NT, (unsigned) ((k + ks - 1) / ks));
     const size_t lds = (size_t) NWV * ITEMS * 64 * NT * sizeof(float) + (HP > 0 ? 32 + fuse_lds(NT, ks) : 0);
     if constexpr (NT >= 2) {   // only calls with 2 or more tokens split K
         if (ks < k) {
@@ -857,6 +976,8 @@ hipError_t gemv_dt(int flavour, const WeightView& w, const ActQ& A, const float*
     hipError_t e;
     if (flavour == 2) {
         e = go<DT, 2, 8>(w, A, nullptr, 0, k, ks, cz, m, n, out, ldo, st, eo);
+    } else if (flavour == 3) {   // F1 codes from A, 8-token tiles (any n)
+        e = go<DT, 1, 8>(w, A, nullptr, 0, k, ks, cz, m, n, out, ldo, st, eo);
     } else {
         switch (n) {
         case 1: e = go<DT, 1, 1>(w, A, a, lda, k, ks, cz, m, n, out, ldo, st, eo); break;

@@ -1,5 +1,5 @@
 // The decode / few-token kernels for Q8_0 weights (gemv_impl.h), instantiated in a translation unit of
-// their own so the five weight types compile in parallel.
+// their own so the weight types compile in parallel.
 #include "gemv_impl.h"
 
 namespace jamhip {

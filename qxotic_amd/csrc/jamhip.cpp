@@ -91,7 +91,23 @@ struct Pin {
 
 constexpr int64_t align256(int64_t v) { return (v + 255) & ~int64_t(255); }
 
-bool supported_w(int dt) { return dt == Q8_0 || dt == Q4_0 || dt == Q4_K || dt == Q6_K || dt == MXFP4; }
+// Every weight type of jam's JAM contract (JAM.java:74-84): the int8-pipeline types and the dense ones.
+bool supported_w(int dt) {
+    return dt == Q8_0 || dt == Q4_0 || dt == Q4_K || dt == Q6_K || dt == MXFP4 || dt == Q5_K || dt == NVFP4 ||
+           dt == Q1_0 || dt == F32 || dt == F16 || dt == BF16;
+}
+// The grouped (MoE) matmul covers the types with a grouped kernel.
+bool grouped_w(int dt) { return dt == Q8_0 || dt == Q4_0 || dt == Q4_K || dt == Q6_K || dt == MXFP4; }
+
+// jam's block rule (jam.c:665-685, 752): k on the block for every quantized type; ldw on it too for the
+// 32-element types and Q1_0, while the K-quants and NVFP4 stride rows by (ldw / block) blocks, and the dense
+// types take any k and ldw.
+bool block_aligned(int dt, int ldw, int k) {
+    const int be = block_elems(dt);
+    if (k % be) return false;
+    if (dt == Q4_K || dt == Q5_K || dt == Q6_K || dt == NVFP4 || is_dense(dt)) return true;
+    return ldw % be == 0;
+}
 
 // Device scratch of jamhip_mm_device_noalloc: one fixed array per GPU, in the code object (no allocation
 // call ever sizes it), shared by every call on that GPU. In host code `scratch` is only a stand-in for the
@@ -195,8 +211,7 @@ jamhip_status validate(jamhip_ctx* ctx, const void* w, int wt, int ldw, const vo
     if (ldw < k || lda < k || ldc < m) return fail(ctx, JAMHIP_EINVAL, "stride below extent (ldw<k, lda<k or ldc<m)");
     if (at != F32 || ct != F32) return fail(ctx, JAMHIP_EUNSUPPORTED, "A and C must be F32");
     if (!supported_w(wt)) return fail(ctx, JAMHIP_EUNSUPPORTED, "weight dtype not supported on the GPU backend");
-    const int be = block_elems(wt);
-    if (k % be || ldw % be) return fail(ctx, JAMHIP_EUNSUPPORTED, "k and ldw must be multiples of the block size");
+    if (!block_aligned(wt, ldw, k)) return fail(ctx, JAMHIP_EUNSUPPORTED, "k (and for this dtype ldw) must be a multiple of the block size");
     return JAMHIP_OK;
 }
 
@@ -242,8 +257,8 @@ jamhip_status upload(jamhip_ctx* ctx, const uint8_t* host, int dt, int64_t raw_s
 // Resolve W to a device view: the registry, else a per-call staged copy of rows [0, m), k elements each.
 jamhip_status resolve_w(jamhip_ctx* ctx, const void* w, int dt, int ldw, int m, int k, WeightView* wv) {
     if (lookup(ctx, w, dt, ldw, m, wv)) return JAMHIP_OK;
-    const int64_t rb = k / block_elems(dt), G = groups_of(dt, rb);
-    const int64_t qsz = align256(tiled_rows(m) * G * group_chunks(dt) * 16), ssz = tiled_rows(m) * G * group_scale_bytes(dt);
+    const int64_t rb = k / block_elems(dt), G = view_G(dt, k);
+    const int64_t qsz = plane0_bytes(dt, m, k), ssz = plane1_bytes(dt, m, k);
     hipError_t e = ctx->w_stage.ensure((size_t) (qsz + ssz));
     if (e != hipSuccess) return hip_fail(ctx, e, "weight stage alloc");
     uint8_t* dst = (uint8_t*) ctx->w_stage.p;
@@ -342,6 +357,11 @@ jamhip_status compute(jamhip_ctx* ctx, Scratch& sc, int dt, const WeightView& wv
         if (pf == 0) return hipSuccess;
         return sc.get(ctx->part, pf * sizeof(float), (void**) &gpart);
     };
+    if (is_dense(dt)) {   // jam's dense paths: no activation quantization, no scratch
+        if ((e = launch_dense(dt, wv, a, lda, k, m, n, c, ldc, ctx->stream, ep)) != hipSuccess)
+            return hip_fail(ctx, e, "dense launch");
+        return JAMHIP_OK;
+    }
     if (gemv_fusable(n, k, a, lda)) {
         if ((e = decode_part(m)) != hipSuccess) return scratch_fail(ctx, sc, e, "gemv split scratch");
         if ((e = launch_gemv(dt, 1, wv, ActQ{}, a, lda, k, m, n, c, ldc, ctx->stream, gpart, ep)) != hipSuccess)
@@ -378,11 +398,11 @@ jamhip_status compute(jamhip_ctx* ctx, Scratch& sc, int dt, const WeightView& wv
     float* s = (float*) (base + qb + db);
     int* s16 = (int*) (base + qb + db + sb);
     const ActQ A{q, d, s, s16};
-    if (n < 8) {
+    if (n < 8 || dt == NVFP4) {   // F1 on every row: decode, and NVFP4 at any n (jam.c:662-668)
         if ((e = decode_part(m)) != hipSuccess) return scratch_fail(ctx, sc, e, "gemv split scratch");
         if ((e = launch_quant_f1(a, lda, n, k, q, d, s, s16, ctx->stream)) != hipSuccess)
             return hip_fail(ctx, e, "quant_f1 launch");
-        if ((e = launch_gemv(dt, 1, wv, A, nullptr, 0, k, m, n, c, ldc, ctx->stream, gpart, ep)) != hipSuccess)
+        if ((e = launch_gemv(dt, n < 8 ? 1 : 3, wv, A, nullptr, 0, k, m, n, c, ldc, ctx->stream, gpart, ep)) != hipSuccess)
             return hip_fail(ctx, e, "gemv launch");
         return JAMHIP_OK;
     }
@@ -410,7 +430,7 @@ jamhip_status compute(jamhip_ctx* ctx, int dt, const WeightView& wv, const float
 // buffer is kept when `keep_staging` (a registry load reuses it for every tensor).
 jamhip_status pin_range(jamhip_ctx* ctx, const void* w, int wt, int ldw, int64_t m, bool keep_staging) {
     const uintptr_t host = reinterpret_cast<uintptr_t>(w);
-    const int64_t rb = ldw / block_elems(wt), G = groups_of(wt, rb), span = m * row_bytes(wt, ldw);
+    const int64_t rb = ldw / block_elems(wt), G = view_G(wt, ldw), span = m * row_bytes(wt, ldw);
     {
         std::lock_guard<std::mutex> lk(ctx->pin_mu);
         auto it = std::lower_bound(ctx->pins.begin(), ctx->pins.end(), host,
@@ -421,7 +441,7 @@ jamhip_status pin_range(jamhip_ctx* ctx, const void* w, int wt, int ldw, int64_t
         const bool hits_prev = it != ctx->pins.begin() && host < (it - 1)->host + (uintptr_t) (it - 1)->span;
         if (hits_next || hits_prev) return fail(ctx, JAMHIP_EINVAL, "pin: range overlaps a pinned tensor (evict it first)");
     }
-    const int64_t qsz = align256(tiled_rows(m) * G * group_chunks(wt) * 16), ssz = tiled_rows(m) * G * group_scale_bytes(wt);
+    const int64_t qsz = plane0_bytes(wt, m, ldw), ssz = plane1_bytes(wt, m, ldw);
     uint8_t* dev = nullptr;
     hipError_t e = hipMalloc((void**) &dev, (size_t) (qsz + ssz));
     if (e != hipSuccess) return hip_fail(ctx, e, "pin: device alloc");
@@ -569,7 +589,9 @@ jamhip_status weight_pin_impl(jamhip_ctx* ctx, const void* w, int wt, int ldw, i
     if (!ctx) return JAMHIP_EINVAL;
     if (!w || m <= 0 || ldw <= 0) return fail(ctx, JAMHIP_EINVAL, "pin: null weight or empty shape");
     if (!supported_w(wt)) return fail(ctx, JAMHIP_EUNSUPPORTED, "pin: weight dtype not supported");
-    if (ldw % block_elems(wt)) return fail(ctx, JAMHIP_EUNSUPPORTED, "pin: ldw not a block multiple");
+    const int be = block_elems(wt);   // whole rows of ldw elements: at least one block, on the block where jam needs it
+    if (ldw < be || !block_aligned(wt, ldw, ldw / be * be))
+        return fail(ctx, JAMHIP_EUNSUPPORTED, "pin: ldw not a block multiple");
     Busy guard(ctx);
     if (!guard.ok) return fail(ctx, JAMHIP_EBUSY, "context busy");
     (void) hipSetDevice(ctx->device);
@@ -617,7 +639,7 @@ jamhip_status mm_grouped_ex_impl(jamhip_ctx* ctx, const void* w, int wt, int ldw
         return fail(ctx, JAMHIP_EINVAL, "grouped: m, k, n_experts must be positive and rows_cap >= 0");
     if (ldw < k || lda < k || ldc < m) return fail(ctx, JAMHIP_EINVAL, "grouped: stride below extent");
     if (at != F32 || ct != F32) return fail(ctx, JAMHIP_EUNSUPPORTED, "grouped: A and C must be F32");
-    if (!supported_w(wt)) return fail(ctx, JAMHIP_EUNSUPPORTED, "grouped: weight dtype not supported");
+    if (!grouped_w(wt)) return fail(ctx, JAMHIP_EUNSUPPORTED, "grouped: weight dtype not supported");
     if (k % block_elems(wt) || ldw % block_elems(wt))
         return fail(ctx, JAMHIP_EUNSUPPORTED, "grouped: k and ldw must be multiples of the block size");
     if (m % 16) return fail(ctx, JAMHIP_EUNSUPPORTED, "grouped: m must be a multiple of 16");
@@ -1035,7 +1057,7 @@ namespace {
 // A tensor whose row extent dims[0] is not a whole number of blocks (dims[0] below one block included) is
 // taken here too, with rows = 0, so that registry_runs reports it instead of dividing by a zero row size.
 bool registry_shape(const GgufTensor& t, int* ldw, int64_t* rows) {
-    if (!supported_w(t.type) || t.bytes == 0) return false;
+    if (!supported_w(t.type) || t.bytes == 0 || t.n_dims < 2) return false;   // 1-D: norms, biases
     *ldw = (int) t.dims[0];
     *rows = t.dims[0] % block_elems(t.type) ? 0 : t.bytes / row_bytes(t.type, t.dims[0]);
     return true;

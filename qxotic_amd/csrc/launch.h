@@ -31,7 +31,8 @@ struct Groups {
     const float* bias = nullptr;   // per-expert bias [E][gm] added in the store (expert e at bias + e·gm)
 };
 
-// flavour 1: n in [1, 7], F1 activations; with `a` non-null the kernel quantizes A itself (requires
+// flavour 3: any n, F1 activations read from A in 8-token tiles (NVFP4, whose only jam kernel is F1 at
+// every n). flavour 1: n in [1, 7], F1 activations; with `a` non-null the kernel quantizes A itself (requires
 // gemv_fusable(n, k)), else it reads A's quantized copy from `A`. flavour 2: any n >= 1, F2
 // activations from `A`, 8 tokens per grid row. From k = 8192 on, for n >= 2, the kernel splits K into
 // 4096-element slices: `part` must then hold gemv_split_floats(k, m, n) floats (the slices' partial
@@ -94,6 +95,11 @@ hipError_t launch_gemm_mma(int dt, const WeightView& w, const GemmAct& A, int k,
 hipError_t launch_gemm_mma_grouped(int dt, const WeightView& w, const GemmAct& A, int k, const Groups& g, int cap64,
                                    float* c, int ldc, hipStream_t st);
 size_t gemm_act_bytes_np(int dt, int NP, int k);
+
+// Dense weights (F32, F16, BF16; dense.hip): jam's dense paths, any n, any k (rows padded to a 256-byte pitch,
+// WeightView::G = the pitch).
+hipError_t launch_dense(int dt, const WeightView& w, const float* a, int lda, int k, int m, int n, float* c, int ldc,
+                        hipStream_t st, const Epi& ep = Epi{});
 
 // In place on gate [rows][ldg]: act 1 SwiGLU silu(gate)·up, act 2 gpt-oss clamped SwiGLU (epilogue.hip).
 hipError_t launch_glu(int act, float* gate, int ldg, const float* up, int ldu, int rows, int cols, hipStream_t st);

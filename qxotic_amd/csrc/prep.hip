@@ -60,6 +60,31 @@ __global__ void __launch_bounds__(256) repack_kernel(const uint8_t* __restrict__
         for (int t = 0; t < 16; t++) ds[t] = live ? b[t] : 0;
         for (int c = 0; c < 8; c++)
             for (int t = 0; t < 16; t++) chunk(c)[t] = live ? b[16 + 16 * c + t] : 0;
+    } else if constexpr (DT == Q5_K) {                 // d, dmin, scales @0..15, qh @16..47, qs @48..175
+        const uint8_t* b = row + g * 176;
+        for (int t = 0; t < 16; t++) ds[t] = live ? b[t] : 0;
+        for (int c = 0; c < 8; c++)
+            for (int t = 0; t < 16; t++) chunk(c)[t] = live ? b[48 + 16 * c + t] : 0;
+        for (int c = 0; c < 2; c++)
+            for (int t = 0; t < 16; t++) chunk(8 + c)[t] = live ? b[16 + 16 * c + t] : 0;
+    } else if constexpr (DT == NVFP4) {                // per 64-block: d[4] UE4M3 @0..3, qs @4..35
+        for (int j = 0; j < 4; j++) {
+            const int64_t blk = g * 4 + j;
+            const bool in = live && blk < rb;
+            const uint8_t* b = row + (in ? blk : 0) * 36;
+            for (int t = 0; t < 4; t++) ds[4 * j + t] = in ? b[t] : 0;
+            for (int h = 0; h < 2; h++)
+                for (int t = 0; t < 16; t++) chunk(2 * j + h)[t] = in ? b[4 + 16 * h + t] : 0;
+        }
+    } else if constexpr (DT == Q1_0) {                 // per 128-block: fp16 d @0..1, sign bytes @2..17
+        for (int j = 0; j < 2; j++) {
+            const int64_t blk = g * 2 + j;
+            const bool in = live && blk < rb;
+            const uint8_t* b = row + (in ? blk : 0) * 18;
+            ds[2 * j] = in ? b[0] : 0;
+            ds[2 * j + 1] = in ? b[1] : 0;
+            for (int t = 0; t < 16; t++) chunk(j)[t] = in ? b[2 + t] : 0;
+        }
     } else if constexpr (DT == Q6_K) {                 // ql @0..127, qh @128..191, scales @192..207, d @208
         const uint8_t* b = row + g * 210;
         for (int c = 0; c < 13; c++)
@@ -305,11 +330,35 @@ hipError_t launch_quant_f2(const float* a, int lda, int n, int k, int8_t* q, flo
     return hipGetLastError();
 }
 
+// Dense weights: row r (rb elements of the raw row) to the device copy at pitch G bytes, the rest of the pitch
+// zero. One thread per 16-byte piece of the pitch.
+__global__ void __launch_bounds__(256) repack_dense_kernel(const uint8_t* __restrict__ raw, int64_t raw_stride,
+                                                           int64_t rows, int64_t row_bytes, int64_t G,
+                                                           uint8_t* __restrict__ dst) {
+    const int64_t i = (int64_t) blockIdx.x * 256 + threadIdx.x, per = G / 16;
+    if (i >= rows * per) return;
+    const int64_t r = i / per, o = (i - r * per) * 16;
+    uint8_t v[16];
+    const uint8_t* src = raw + r * raw_stride + o;
+    for (int t = 0; t < 16; t++) v[t] = o + t < row_bytes ? src[t] : 0;
+    uint8_t* d = dst + r * G + o;
+    for (int t = 0; t < 16; t++) d[t] = v[t];
+}
+
 hipError_t launch_repack(int dt, const uint8_t* raw, int64_t raw_stride, int64_t rows, int64_t rb, int64_t G,
                          uint8_t* qs, uint8_t* sc, hipStream_t st) {
+    if (is_dense(dt)) {   // G: the pitch; rb: elements per row
+        const int64_t n = rows * (G / 16);
+        repack_dense_kernel<<<(unsigned) ((n + 255) / 256), 256, 0, st>>>(raw, raw_stride, rows, rb * block_bytes(dt), G,
+                                                                          qs);
+        return hipGetLastError();
+    }
     const int64_t n = tiled_rows(rows) * G;
     const dim3 grid((unsigned) ((n + 255) / 256));
     switch (dt) {
+    case Q5_K: repack_kernel<Q5_K><<<grid, 256, 0, st>>>(raw, raw_stride, rows, rb, G, qs, sc); break;
+    case NVFP4: repack_kernel<NVFP4><<<grid, 256, 0, st>>>(raw, raw_stride, rows, rb, G, qs, sc); break;
+    case Q1_0: repack_kernel<Q1_0><<<grid, 256, 0, st>>>(raw, raw_stride, rows, rb, G, qs, sc); break;
     case Q8_0: repack_kernel<Q8_0><<<grid, 256, 0, st>>>(raw, raw_stride, rows, rb, G, qs, sc); break;
     case Q4_0: repack_kernel<Q4_0><<<grid, 256, 0, st>>>(raw, raw_stride, rows, rb, G, qs, sc); break;
     case MXFP4: repack_kernel<MXFP4><<<grid, 256, 0, st>>>(raw, raw_stride, rows, rb, G, qs, sc); break;

@@ -1,8 +1,8 @@
 """GPU: the GGUF device weight registry (jamhip_gguf_pin / jamhip_gguf_evict) through the C-ABI.
 
-A file holding all five jam weight dtypes (2-D Q4_K, Q6_K and Q4_0 tensors, a stacked MXFP4 expert tensor
-[k, rows, experts], a Q8_0 tensor with a partial row tile) beside an F32 bias and an F16 embedding (not
-jam weights: skipped) is opened and pinned in one call. Every jam call on a registry address
+A file holding five jam weight dtypes (2-D Q4_K, Q6_K and Q4_0 tensors, a stacked MXFP4 expert tensor
+[k, rows, experts], a Q8_0 tensor with a partial row tile) and an F16 token embedding beside a 1-D F32 bias
+(skipped) is opened and pinned in one call. Every jam call on a registry address
 must (1) meet the tier-1 bound against the int8 oracle, (2) equal bit for bit the same call on an unpinned
 heap copy of the same bytes (the staged path runs the same kernels), and (3) read the device copy: when
 the caller's own mapping is pinned and then overwritten, results do not change. Expert slices of the
@@ -74,9 +74,15 @@ def test_registry_pin_lookup_evict(hip, oracle, model):
         say("gguf registry: pin from the handle's mapping")
         st, cnt, nbytes = g.pin(hip)
         assert st == 0, hip.last_error()
-        assert cnt == 5 and nbytes == sum(x[2].nbytes for x in w.values())   # F32 / F16 tensors skipped
+        # every 2-D tensor of a jam weight type is pinned (the F16 token embedding included: tied-embedding
+        # models multiply by it); the 1-D F32 bias is skipped
+        emb = g.tensors["token_embd.weight"]
+        assert cnt == 6 and nbytes == sum(x[2].nbytes for x in w.values()) + emb.byte_size
         assert hip.pinned_bytes() > before
-        assert g.pin(hip)[:2] == (0, 5)                        # idempotent
+        assert g.pin(hip)[:2] == (0, 6)                        # idempotent
+        a = oracle.normal(0x55, (3, K))
+        got = mm_at(hip, emb.address, emb.byte_size, g, O.F16, a, 8, 3)
+        assert np.array_equal(got, np.zeros((3, 8), np.float32))   # the embedding rows are zeros
         try:
             for name, (dt, m, wq) in w.items():
                 e = g.tensors[name]
@@ -100,7 +106,7 @@ def test_registry_pin_lookup_evict(hip, oracle, model):
                     sl = np.ascontiguousarray(wq[x * ER:(x + 1) * ER])
                     assert np.array_equal(got.view(np.uint32), mm_heap(hip, sl, O.MXFP4, a, ER, n).view(np.uint32)), (x, n)
         finally:
-            assert g.evict(hip) == 5
+            assert g.evict(hip) == 6
     assert hip.pinned_bytes() == before
 
 
@@ -116,7 +122,7 @@ def test_registry_keys_caller_mapping(hip, oracle, model):
         base = region.ctypes.data
         say("gguf registry: pin the caller's mapping")
         st, cnt, _ = g.pin(hip, base)
-        assert st == 0 and cnt == 5, hip.last_error()
+        assert st == 0 and cnt == 6, hip.last_error()
         try:
             region[:] = 0
             for name, (dt, m, wq) in w.items():
@@ -147,7 +153,7 @@ def test_registry_keys_caller_mapping(hip, oracle, model):
                     assert tier1(got[o:o + n], ref, sa).all(), x
                 o += n
         finally:
-            assert g.evict(hip, base) == 5
+            assert g.evict(hip, base) == 6
 
 
 def test_registry_rejects_partial_row_blocks(hip, tmp_path):
