@@ -14,8 +14,11 @@
  *               (jam_q8_0_requant, jam_kernels_generic.c:71-94) for n < 8, per-32 "F2" with per-16 f32
  *               sums (quantize_row_q8s, jam_kernels_q4k_avx512.c:25-37) for n >= 8, and each dtype's
  *               per-block combine follows the matching jam kernel's decomposition.
- *   dtypes    : W in {Q8_0, Q4_0, Q4_K, Q6_K, MXFP4}; A and C F32. Anything else -> JAMHIP_EUNSUPPORTED
- *               (jinfer falls through to the next backend, MatMul.java:1822-1828).
+ *   dtypes    : every weight type of jam's JAM contract (JAM.java:74-84): Q8_0, Q4_0, Q4_K, Q5_K, Q6_K,
+ *               MXFP4, NVFP4, Q1_0 through jam's int8 pipeline, F32, F16, BF16 through jam's dense paths
+ *               (BF16 activations rounded to bf16 where jam's bf16 kernels round them, jam.c:622-652); A and C
+ *               F32. JAMHIP_EUNSUPPORTED exactly where jam_mm refuses: another A/C type, k off the block, ldw off
+ *               the block for the 32-element types and Q1_0 (jam.c:662-685, 752).
  *   residency : weights live on the GPU once pinned (jamhip_weight_pin). jamhip_mm on an unpinned W
  *               stages it for that call only (correct, slow). Pinning uploads and repacks once into the
  *               device layout; it is keyed by host address range, so the caller evicts before freeing or
@@ -40,7 +43,7 @@ extern "C" {
 /* dtype tags: numerically jam_dtype / ggml_type (jam/jam-native/include/jam.h:59-77). */
 enum {
     JAMHIP_F32 = 0, JAMHIP_F16 = 1, JAMHIP_Q4_0 = 2, JAMHIP_Q8_0 = 8, JAMHIP_Q4_K = 12,
-    JAMHIP_Q5_K = 13, JAMHIP_Q6_K = 14, JAMHIP_BF16 = 30, JAMHIP_MXFP4 = 39
+    JAMHIP_Q5_K = 13, JAMHIP_Q6_K = 14, JAMHIP_BF16 = 30, JAMHIP_MXFP4 = 39, JAMHIP_NVFP4 = 40, JAMHIP_Q1_0 = 41
 };
 
 /* status: numerically jam_status (jam.h:81-86; JAM.java:87). */
@@ -137,7 +140,8 @@ jamhip_status jamhip_quantize_device(jamhip_ctx* ctx, int flavour, const void* a
  * (CSR order, as Moe.dispatch gathers them); for each expert the result is jam_mm(W_e, A_e, C_e, m,
  * counts[e], k) under jam's routing (F1 below 8 rows, 16-row F2 bands from 8). rows_cap is the number
  * of rows A and C hold: rows past it (a prefix sum beyond rows_cap) are not computed and never read.
- * m must be a multiple of 16 and n_experts <= 1024 (else JAMHIP_EUNSUPPORTED). Replaces the per-expert
+ * W is Q8_0, Q4_0, Q4_K, Q6_K or MXFP4; m must be a multiple of 16 and n_experts <= 1024 (else
+ * JAMHIP_EUNSUPPORTED). Replaces the per-expert
  * MatMul.gemm calls of Moe.dispatch's kernel closure (GptOss.java:295-314). */
 jamhip_status jamhip_mm_grouped(jamhip_ctx* ctx,
                                 const void* w, int wt, int ldw, int m, int n_experts,
@@ -237,9 +241,10 @@ int64_t       jamhip_gguf_find(const jamhip_gguf* g, const char* name);   /* ind
 int64_t       jamhip_gguf_data_offset(const jamhip_gguf* g);              /* file offset of the data region */
 int           jamhip_gguf_alignment(const jamhip_gguf* g);
 
-/* Pin every Q8_0 / Q4_0 / Q4_K / Q6_K / MXFP4 tensor of g at data_base + offset: data_base is the
- * caller's own mapping of the same file's data region (the addresses its jam calls will pass), or NULL
- * for the handle's mapping. Other dtypes are skipped. Tensors of one dtype and row length stored back to
+/* Pin every tensor of g of 2 or more dims and a jam weight type (quantized or F32 / F16 / BF16) at
+ * data_base + offset: data_base is the caller's own mapping of the same file's data region (the addresses its
+ * jam calls will pass), or NULL for the handle's mapping. 1-D tensors (norms, biases) and other types are
+ * skipped. Tensors of one dtype and row length stored back to
  * back (a block's attn_q|attn_k|attn_v, ffn_gate|ffn_up), each starting on a 32-row boundary of the run,
  * share one device range: every tensor still resolves on its own, and one call with W = the first
  * tensor's address and m = the rows of several computes them together (their outputs concatenated in
