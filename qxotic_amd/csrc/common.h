@@ -120,6 +120,19 @@ struct ActQ {
 
 JAMHIP_DEV float h2f(uint32_t bits16) { return (float) __builtin_bit_cast(_Float16, (uint16_t) bits16); }
 
+// v as f16 hi + lo: hi = f16(v), lo = f16(v - hi), about 22 significant bits together. The empty asm makes v
+// an opaque f32 register first: left visible, a product v = x·y has its f16 conversion rewritten into one
+// v_fma_mixlo_f16 (the exact product rounded once), and the compiler may do that for the hi it subtracts but
+// not for the hi it stores; on an f16 tie the two differ by one ulp and hi + lo misses v by that ulp.
+struct F16Pair {
+    _Float16 hi, lo;
+};
+JAMHIP_DEV F16Pair split_f16(float v) {
+    asm volatile("" : "+v"(v));
+    const _Float16 hi = (_Float16) v;
+    return {hi, (_Float16) (v - (float) hi)};
+}
+
 JAMHIP_DEV int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
 template <int CTRL> JAMHIP_DEV float dpp(float v) {

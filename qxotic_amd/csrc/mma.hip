@@ -366,10 +366,9 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
                     for (int e = 0; e < 4; e++) {
                         int sc, mn;
                         q4k_scmn(hdr[i], 4 * q + e, sc, mn);
-                        const float v = -(dmin * (float) mn);
-                        const _Float16 h = (_Float16) v;
-                        ahi[e] = h;
-                        alo[e] = (_Float16) (v - (float) h);
+                        const F16Pair p = split_f16(-(dmin * (float) mn));
+                        ahi[e] = p.hi;
+                        alo[e] = p.lo;
                     }
 #pragma unroll
                     for (int j = 0; j < CT; j++) {

@@ -248,9 +248,9 @@ __global__ void __launch_bounds__(256) gemm_prep(const float* __restrict__ a, in
     const float down = ldexpf(1.0f, -ex);
     if (threadIdx.x == 0) es[t] = ldexpf(1.0f, ex);
     auto put = [&](int64_t o, float v) {
-        const _Float16 h = (_Float16) v;
-        shi[o] = h;
-        slo[o] = (_Float16) (v - (float) h);
+        const F16Pair p = split_f16(v);
+        shi[o] = p.hi;
+        slo[o] = p.lo;
     };
     for (int b = threadIdx.x; b < (Kp >> 5); b += 256) {
         dx[(int64_t) b * NP + t] = ldb[b] * down;
