@@ -144,6 +144,48 @@ def gpu_leg(args, w: np.ndarray, hip, torch, stream) -> dict:
     return {"event_ms": ev_ms, "wall_s": wall, "host_us": host_us}
 
 
+def read_floor_leg(args, hip, torch, stream) -> dict:
+    """The same harness as the decode leg (COPIES rotating buffers, one graph of args.steps launches) around
+    jamhip_read_floor: a plain streaming read of the weight copy's bytes with the decode kernel's load shape,
+    nothing computed or written. Its rate is the practical floor the decode GEMV is measured against."""
+    nbytes = M * (K // 256) * 144
+    bufs = [torch.empty(nbytes, dtype=torch.uint8, device="cuda") for _ in range(COPIES)]
+    for b in bufs:
+        b.random_(0, 255)
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+
+    def step(i):
+        if hip.read_floor(bufs[i % COPIES].data_ptr(), nbytes, sink.data_ptr()) != 0:
+            raise RuntimeError(hip.last_error())
+
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        for i in range(args.warmup):
+            step(i)
+        torch.cuda.synchronize()
+        graph = None
+        if not args.no_graph:
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                for i in range(args.steps):
+                    step(i)
+            graph.replay()
+            torch.cuda.synchronize()
+        e0.record(stream)
+        if graph is not None:
+            graph.replay()
+        else:
+            for i in range(args.steps):
+                step(i)
+        e1.record(stream)
+        torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / args.steps
+    del bufs
+    return {"us": round(us, 3), "GBs": round(nbytes / (us * 1e-6) / 1e9, 1), "bytes": nbytes,
+            "note": "streaming read of the Q4_K weight bytes, decode load shape, same graph harness; no compute, "
+                    "no output"}
+
+
 def prefill_leg(hip, torch, stream, reps: int = 10) -> dict:
     """M=512 prefill on the two BASELINE prefill shapes; each timed call quantizes its activations (F2)."""
     from qxotic_amd.jam import JAM, Segment
@@ -494,6 +536,7 @@ def main() -> int:
     ap.add_argument("--no-step", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true")
+    ap.add_argument("--no-read-floor", action="store_true")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -515,6 +558,11 @@ def main() -> int:
     g = gpu_leg(args, w, hip, torch, stream)
     ms = g["event_ms"] / args.steps
     gbs = STEP_BYTES / (ms * 1e-3) / 1e9
+    floor = None
+    if not args.no_read_floor:
+        log("bench: read floor leg")
+        floor = read_floor_leg(args, hip, torch, stream)
+        floor["decode_frac"] = round(floor["us"] / (ms * 1e3), 4)
     pre = None
     if not args.no_prefill:
         log("bench: prefill leg")
@@ -553,6 +601,7 @@ def main() -> int:
                                       "pinned weights, wall clock; not the metric"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles()},
+        "read_floor": floor,
         "prefill": pre,
         "moe": moe,
         "decode_step": step,

@@ -210,6 +210,12 @@ jamhip_status jamhip_ctx_set_stream(jamhip_ctx* ctx, void* stream);
 void*         jamhip_ctx_stream(const jamhip_ctx* ctx);
 jamhip_status jamhip_ctx_synchronize(jamhip_ctx* ctx);
 
+/* Measurement aid with no counterpart in the reference: a streaming read of `bytes` of device memory at p_dev
+ * (16-byte aligned, bytes a multiple of 16) in the decode kernel's load shape, on the context stream, not
+ * synchronized. It computes nothing; sink_dev (one device word) is written only if the loads xor to a fixed
+ * value. Its time over a weight-sized buffer is the read floor the matmul kernels are measured against. */
+jamhip_status jamhip_read_floor(jamhip_ctx* ctx, const void* p_dev, int64_t bytes, void* sink_dev);
+
 /* ---- GGUF device weight registry (model load).
  * Replaces the load step of jinfer's ModelLoader (jinfer/jinfer-kernels/src/main/java/com/qxotic/jinfer/
  * kernels/ModelLoader.java:35-104: GGUF.read of the header, then one READ_ONLY mapping of the tensor data

@@ -37,6 +37,7 @@ SIGNATURES = [
     ("jamhip_ctx_set_stream", _I, [_VP, _VP]),
     ("jamhip_ctx_stream", _VP, [_VP]),
     ("jamhip_ctx_synchronize", _I, [_VP]),
+    ("jamhip_read_floor", _I, [_VP, _VP, _I64, _VP]),
     ("jamhip_gguf_open", _VP, [C.c_char_p, C.c_char_p, C.c_size_t]),
     ("jamhip_gguf_close", None, [_VP]),
     ("jamhip_gguf_tensor_count", _I64, [_VP]),

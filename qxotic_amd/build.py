@@ -40,6 +40,7 @@ UNITS = {   # source -> extra flags
     "mma.hip": [],
     "moe.hip": [],
     "epilogue.hip": [],
+    "readfloor.hip": [],
     "jamhip.cpp": ["-x", "hip"],
     "gguf.cpp": [],
 }

@@ -585,6 +585,17 @@ jamhip_status glu_device_impl(jamhip_ctx* ctx, int act, void* gate_dev, int ldg,
     return e == hipSuccess ? JAMHIP_OK : hip_fail(ctx, e, "glu launch");
 }
 
+jamhip_status read_floor_impl(jamhip_ctx* ctx, const void* p, int64_t bytes, void* sink) {
+    if (!ctx) return JAMHIP_EINVAL;
+    if (!p || !sink || bytes < 0 || bytes % 16 || (reinterpret_cast<uintptr_t>(p) & 15))
+        return fail(ctx, JAMHIP_EINVAL, "read_floor: null pointer, or bytes / address not 16-byte aligned");
+    Busy guard(ctx);
+    if (!guard.ok) return fail(ctx, JAMHIP_EBUSY, "context busy");
+    (void) hipSetDevice(ctx->device);
+    const hipError_t e = launch_read_floor(p, bytes, (uint32_t*) sink, ctx->stream);
+    return e == hipSuccess ? JAMHIP_OK : hip_fail(ctx, e, "read_floor launch");
+}
+
 jamhip_status weight_pin_impl(jamhip_ctx* ctx, const void* w, int wt, int ldw, int m) {
     if (!ctx) return JAMHIP_EINVAL;
     if (!w || m <= 0 || ldw <= 0) return fail(ctx, JAMHIP_EINVAL, "pin: null weight or empty shape");
@@ -931,6 +942,10 @@ jamhip_status jamhip_mm_device_ex(jamhip_ctx* ctx, const void* w, int wt, int ld
 jamhip_status jamhip_glu_device(jamhip_ctx* ctx, int act, void* gate_dev, int ldg, const void* up_dev, int ldu,
                                 int rows, int cols) {
     return on_ctx(ctx, [&](jamhip_ctx* x) { return glu_device_impl(x, act, gate_dev, ldg, up_dev, ldu, rows, cols); });
+}
+
+jamhip_status jamhip_read_floor(jamhip_ctx* ctx, const void* p_dev, int64_t bytes, void* sink_dev) {
+    return on_ctx(ctx, [&](jamhip_ctx* x) { return read_floor_impl(x, p_dev, bytes, sink_dev); });
 }
 
 jamhip_status jamhip_weight_pin(jamhip_ctx* ctx, const void* w, int wt, int ldw, int m) {

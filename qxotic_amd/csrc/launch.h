@@ -103,6 +103,10 @@ hipError_t launch_dense(int dt, const WeightView& w, const float* a, int lda, in
 
 // In place on gate [rows][ldg]: act 1 SwiGLU silu(gate)·up, act 2 gpt-oss clamped SwiGLU (epilogue.hip).
 hipError_t launch_glu(int act, float* gate, int ldg, const float* up, int ldu, int rows, int cols, hipStream_t st);
+
+// Streaming read of `bytes` (a multiple of 16; 16-byte aligned p) with the decode kernel's load shape, nothing
+// written but a word at `sink` if the loads xor to a fixed value (readfloor.hip).
+hipError_t launch_read_floor(const void* p, int64_t bytes, uint32_t* sink, hipStream_t st);
 hipError_t launch_gemm_prep_grouped(int dt, const float* a, int lda, int k, const Groups& g, int cap64,
                                     void* scratch, GemmAct* out, hipStream_t st);
 

@@ -222,6 +222,10 @@ class HipJAM:
         """In place on gate: SwiGLU (act 1) or gpt-oss clamped SwiGLU (act 2) (jamhip_glu_device)."""
         return lib().jamhip_glu_device(self.ctx, act, gate_dev, ldg, up_dev, ldu, rows, cols)
 
+    def read_floor(self, p_dev: int, nbytes: int, sink_dev: int) -> int:
+        """Streaming read of nbytes at p_dev in the decode kernel's load shape (jamhip_read_floor)."""
+        return lib().jamhip_read_floor(self.ctx, p_dev, nbytes, sink_dev)
+
     def quantize_device(self, flavour: int, a_dev: int, lda: int, n: int, k: int, q_dev: int, d_dev: int,
                         s_dev: int) -> int:
         return lib().jamhip_quantize_device(self.ctx, flavour, a_dev, lda, n, k, q_dev, d_dev, s_dev)

@@ -273,3 +273,20 @@ def test_exit_with_open_contexts_and_mappings(tmp_path):
     r = subprocess.run([sys.executable, str(script), str(ROOT)], capture_output=True, text=True, timeout=300)
     assert r.returncode == 0, (r.returncode, r.stderr[-2000:])
     assert "left open" in r.stdout
+
+
+def test_read_floor_entry_point(hip):
+    """jamhip_read_floor (measurement aid) reads a device buffer and returns OK; unaligned sizes or addresses and
+    null pointers are EINVAL, with the reason in the error text."""
+    import torch
+    from qxotic_amd.jam import JAM
+    buf = torch.randint(0, 255, (1 << 20,), dtype=torch.uint8, device="cuda")
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+    assert hip.read_floor(buf.data_ptr(), buf.numel(), sink.data_ptr()) == JAM.OK, hip.last_error()
+    assert hip.read_floor(buf.data_ptr(), 0, sink.data_ptr()) == JAM.OK
+    assert hip.synchronize() == JAM.OK
+    assert hip.read_floor(buf.data_ptr(), 1000, sink.data_ptr()) == JAM.EINVAL
+    assert "aligned" in hip.last_error()
+    assert hip.read_floor(buf.data_ptr() + 8, 1024, sink.data_ptr()) == JAM.EINVAL
+    assert hip.read_floor(0, 1024, sink.data_ptr()) == JAM.EINVAL
+    assert hip.read_floor(buf.data_ptr(), 1024, 0) == JAM.EINVAL
