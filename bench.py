@@ -514,6 +514,66 @@ def cpu_leg(w: np.ndarray, budget_s: float = 4.0) -> dict | None:
                       f"{calls} calls over {COPIES} rotating host copies in {dt:.1f} s"}
 
 
+def cpu_gemm_leg(budget_s: float = 4.0) -> dict | None:
+    """libjam (oracle/_ref) at the GEMM shapes, one thread per allotted core, on bounded row samples of the
+    same weights (jam_bench.c:77-90 times M x N x K the same way): config 4's Q4_K 14336x4096 and Q6_K
+    4096x14336 at M = 512 (F2 bands, jam.c:489-499), and config 5's 32 MXFP4 experts with their routed
+    counts (gate_up 5760x2880 and down 2880x2880 per expert, jam's per-expert calls as Moe.dispatch makes
+    them). Each sample is repeated for `budget_s` seconds; ops = 2·rows·n·k per call."""
+    try:
+        from oracle import oracle as O
+    except Exception as e:   # pragma: no cover
+        log(f"cpu gemm baseline unavailable: {e}")
+        return None
+    if not O.ref_available():
+        return None
+    threads = O.default_threads()
+    ref = O.RefJam(nthreads=threads)
+    out = {}
+
+    def timed(calls_fn):
+        calls_fn()                              # warm
+        t0, reps = time.perf_counter(), 0
+        while time.perf_counter() - t0 < budget_s:
+            calls_fn()
+            reps += 1
+        return reps, time.perf_counter() - t0
+
+    n = 512
+    for name, dt, m, k, rows in (("Q4_K", O.Q4_K, 14336, 4096, 1024), ("Q6_K", O.Q6_K, 4096, 14336, 512)):
+        w = quantized(name, rows, k, 0x5EED ^ dt)        # the GPU leg's distribution, a row sample
+        a = np.random.default_rng(11).standard_normal((n, k)).astype(np.float32)
+        c = np.zeros((n, rows), np.float32)
+        reps, dt_s = timed(lambda: ref.mm(dt, w, a, rows, n, k, out=c))
+        tops = reps * 2.0 * rows * n * k / dt_s / 1e12
+        out[f"{name} {m}x{k} M=512"] = {"TOPS": round(tops, 3), "sample": f"rows 0..{rows - 1} of {m}, "
+                                        f"{reps} calls in {dt_s:.1f} s"}
+    E, D, FF, frac = 32, 2880, 5760, 8
+    counts = [388, 268, 191, 124, 112, 115, 76, 67, 61, 57, 52, 50, 44, 42, 27, 39, 28, 30, 26, 25, 26, 18, 19,
+              19, 19, 30, 15, 20, 14, 21, 11, 14]   # the GPU leg's Zipf(1.1) top-4 routing of 512 tokens
+    gu = quantized("MXFP4", FF // frac, D, 0xC0F5)
+    dn = quantized("MXFP4", D // frac, D, 0xD0F5)
+    xs = [np.random.default_rng(e).standard_normal((c_, D)).astype(np.float32) for e, c_ in enumerate(counts)]
+    cg = [np.zeros((c_, FF // frac), np.float32) for c_ in counts]
+    cd = [np.zeros((c_, D // frac), np.float32) for c_ in counts]
+
+    def layer():
+        for e in range(E):
+            ref.mm(O.MXFP4, gu, xs[e], FF // frac, counts[e], D, out=cg[e])
+            ref.mm(O.MXFP4, dn, xs[e], D // frac, counts[e], D, out=cd[e])
+    reps, dt_s = timed(layer)
+    ops = 2.0 * sum(counts) * (FF // frac + D // frac) * D
+    out["MoE config 5 layer"] = {"TOPS": round(reps * ops / dt_s / 1e12, 3),
+                                 "us_per_layer_scaled": round(dt_s / reps * frac * 1e6, 1),
+                                 "sample": f"1/{frac} of every expert's rows (gate_up {FF // frac}, down {D // frac}) "
+                                           f"at the routed counts, 64 jam_mm calls per layer, {reps} layers in "
+                                           f"{dt_s:.1f} s; us_per_layer_scaled = x{frac}"}
+    ref.close()
+    out.update({"cores": threads, "kind": "reference", "unit": "TOPS",
+                "note": "libjam jam_mm (reference C sources, isa avx512_vnni dispatch), int8 ops counted as 2*M*N*K"})
+    return out
+
+
 def traffic_from_profiles() -> int | None:
     """HBM bytes per GEMV launch, measured by rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE (calibrated)."""
     try:
@@ -584,10 +644,13 @@ def main() -> int:
         log("bench: registry leg")
         reg = registry_leg(hip)
     hip.close()
-    cpu = None
+    cpu = cpu_gemm = None
     if not args.no_cpu:
         log("bench: cpu baseline")
         cpu = cpu_leg(w)
+        if not (args.no_prefill and args.no_moe):
+            log("bench: cpu gemm baseline")
+            cpu_gemm = cpu_gemm_leg()
     out = {
         "metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms, 6), "higher_is_better": True, "scaling": "weak",
@@ -608,6 +671,7 @@ def main() -> int:
         "epilogue": epi,
         "registry": reg,
         "cpu_baseline": cpu,
+        "cpu_baseline_gemm": cpu_gemm,
     }
     print(json.dumps(out), flush=True)
     return 0
