@@ -70,7 +70,7 @@ hipError_t launch_gemm(int dt, const WeightView& w, const ActQ& A, int k, int m,
 // its largest activation sum lies in [2^13, 2^14): the GEMM accumulates in units of 2^-e_t (the block
 // scales and sums below are pre-multiplied by it, exactly) and multiplies by 2^e_t on the way out.
 struct GemmAct {
-    const _Float16* b;     // [Kp/16][NP][16] activation codes; kstep k16 = 2·block + ks, slot 8q + i holds
+    const _Float16* b;     // [Kp/16][2][NP][8] activation codes; kstep k16 = 2·block + ks, half q, slot i holds
                            // element 32·block + 16q + 8ks + perm8(i)
     const float* dx;       // [Kp/32][NP] block scale d · 2^-e_t
     const _Float16* shi;   // per-32 sums (Q4_K, Q4_0) [Kp/256][NP][8] or per-16 sums (Q6_K) [Kp/256][NP][16],

@@ -18,8 +18,9 @@
 // Operands. With the 32-row tiles of the device layout, the A fragment of lane (r, q) (row r = lane % 32,
 // q = lane / 32) for K-step ks of a block is the low or high nibbles of bytes 8ks..8ks+7 of one 16-byte
 // chunk, turned into f16 pairs from bytes (0,2), (1,3), (4,6), (5,7) by mask-and-or with 0x6400 (1024 + v)
-// and one packed FMA with the scale (which removes the 1024). The activation codes are stored in that
-// same order (GemmAct::b), so no shuffle is needed on either side.
+// and one packed FMA with the scale (which removes the 1024). MXFP4 instead converts each byte's two nibbles
+// (elements e, e + 16) with the hardware e2m1 conversion. The activation codes are stored in the matching
+// order (GemmAct::b), so no shuffle is needed on either side.
 //
 // Tiling. A workgroup of 4 waves owns 4·RT row tiles (32 rows each, wave w the RT tiles w·RT..) x CT token
 // tiles (32 tokens each) and walks k in stages of 128 elements (half a super-block). Each stage's weight
@@ -29,6 +30,8 @@
 // weight tile is read from HBM into that XCD's L2 once.
 #include "common.h"
 #include "launch.h"
+
+#include <atomic>
 
 namespace jamhip {
 
@@ -82,29 +85,17 @@ JAMHIP_DEV uint32_t word(const uint4& v, int i) { return i == 0 ? v.x : i == 1 ?
 
 JAMHIP_DEV float h2f_bits(uint32_t b) { return (float) __builtin_bit_cast(_Float16, (uint16_t) (b & 0xffffu)); }
 
-// MXFP4: f16 pair (2^d, 2^d) for d = e_block − e_ref <= 0 (exact down to 2^-24, 0 below).
-JAMHIP_DEV uint32_t mx_scale2(int d) {
-    const uint32_t b = d >= -14 ? (uint32_t) (d + 15) << 10 : d >= -24 ? 1u << (d + 24) : 0u;
-    return b | (b << 16);
-}
-
-// MXFP4: 8 f16 of one K-step from two words of a block's nibble bytes; lane half q takes the low (q = 0,
-// elements 0-15) or high (elements 16-31) nibbles. The e2m1 value x2 (jam_mxfp4.h:14-15: 0,1,2,3,4,6,8,12,
-// sign in bit 3) is looked up as its f16 high byte with v_perm, the sign bit moved in, then scaled by s2.
-JAMHIP_DEV uint32_t mx_pair(uint32_t x, uint32_t hb, uint32_t sel, uint32_t sgnmask, int sgnshift, uint32_t s2) {
-    const uint32_t v = __builtin_amdgcn_perm(hb, 0u, sel) | ((x & sgnmask) << sgnshift);
-    const half2v r = __builtin_bit_cast(half2v, v) * __builtin_bit_cast(half2v, s2);
-    return __builtin_bit_cast(uint32_t, r);
-}
-JAMHIP_DEV half8 mx_frag(uint32_t w0, uint32_t w1, int q4, uint32_t s2) {   // q4 = 4·q
-    const uint32_t x0 = (w0 >> q4) & 0x0F0F0F0Fu, x1 = (w1 >> q4) & 0x0F0F0F0Fu;
-    const uint32_t h0 = __builtin_amdgcn_perm(0x4A484644u, 0x42403C00u, x0 & 0x07070707u);
-    const uint32_t h1 = __builtin_amdgcn_perm(0x4A484644u, 0x42403C00u, x1 & 0x07070707u);
-    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-    return __builtin_bit_cast(half8, u32x4{mx_pair(x0, h0, 0x060C040Cu, 0x00080008u, 12, s2),
-                                           mx_pair(x0, h0, 0x070C050Cu, 0x08000800u, 4, s2),
-                                           mx_pair(x1, h1, 0x060C040Cu, 0x00080008u, 12, s2),
-                                           mx_pair(x1, h1, 0x070C050Cu, 0x08000800u, 4, s2)});
+// MXFP4: 8 f16 of one K-step from one word (4 bytes) of a block's nibble bytes, by the hardware e2m1
+// conversion: byte u gives the pair (e2m1(low nibble), e2m1(high nibble))·scale, elements e and e + 16 of the
+// block (the activation codes are stored in the same order, GemmAct). scale = 2^(e_block − e_ref + 1) turns
+// e2m1 into jam's doubled value x2 (jam_mxfp4.h:14-15: 0,1,2,3,4,6,8,12) times 2^(e_block − e_ref).
+JAMHIP_DEV half8 mx_frag(uint32_t w, float scale) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const h2 p0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, scale, 0);
+    const h2 p1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, scale, 1);
+    const h2 p2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, scale, 2);
+    const h2 p3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, scale, 3);
+    return half8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
 }
 
 // ------------------------------------------------------------------------------------ stage layout
@@ -184,8 +175,8 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
         const int64_t T = T0 + (lane >> 2) < tiles ? T0 + (lane >> 2) : tiles - 1;
         h_src = w.sc + ((r0t + T) * G * 32 + 8 * (lane & 3)) * 2;
     }
-    // GemmAct::b holds 16 f16 (32 bytes) per (K-step, token slot)
-    const uint8_t* b_src = reinterpret_cast<const uint8_t*>(A.b) + ((int64_t) (2 * wave) * A.NP + n0) * 32 + 32 * lane;
+    // GemmAct::b holds 8 f16 (16 bytes) per (K-step, half, token slot), the two halves of a K-step in planes
+    const uint8_t* b_src = reinterpret_cast<const uint8_t*>(A.b) + (int64_t) (2 * wave) * A.NP * 32 + n0 * 16 + 16 * lane;
     const int64_t b_kstep = (int64_t) A.NP * 32;                                  // bytes per K-step
     const float* dx_src = A.dx + (int64_t) (lane >> 4) * A.NP + n0 + 4 * (lane & 15);
     constexpr int SWB = S::SW * 2;                                                // sum bytes per token per plane
@@ -207,15 +198,15 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
             dma16(ag + (8 + 2 * h2) * CHUNK_STRIDE, buf + a_dst + 4 * 512);
             if (lane < 32) dma16(ag + 12 * CHUNK_STRIDE, buf + a_dst + 6 * 512);
         }
-        // activation codes: K-steps 8·st + 2·wave, +1; in LDS each K-step's two 8-element halves are split into
-        // planes [kk][half][BN tokens][16 B] so a fragment read is 512 contiguous bytes per half-wave
-        // (conflict-free); the copy gathers the halves from the token-interleaved global layout
+        // activation codes: K-steps 8·st + 2·wave, +1; in LDS, as in GemmAct, each K-step's two 8-element halves
+        // are planes [kk][half][BN tokens][16 B] so a fragment read is 512 contiguous bytes per half-wave
+        // (conflict-free) and each piece copied is 1 KB contiguous
         const uint8_t* bs = b_src + (int64_t) (8 * st) * b_kstep;
 #pragma unroll
         for (int kl = 0; kl < 2; kl++)
 #pragma unroll
             for (int p = 0; p < 2; p++)
-                dma16(bs + kl * b_kstep + 16 * p, buf + S::B_OFF + (2 * (2 * wave + kl) + p) * 1024);
+                dma16(bs + kl * b_kstep + p * (b_kstep / 2), buf + S::B_OFF + (2 * (2 * wave + kl) + p) * 1024);
         if constexpr (DT != Q6_K) {
             if (wave < 2) dma16(h_src + (int64_t) g * 32 * 16, buf + S::H_OFF + wave * 1024);
         } else {
@@ -553,9 +544,11 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
                         const int b = 4 * h2 + bl;
                         const int eb = (int) (((b < 4 ? hdr[i].x : hdr[i].y) >> (8 * (b & 3))) & 0xffu);
                         const int er = (int) (hdr[i].z & 0xffu);
-                        const uint32_t s2 = mx_scale2(eb - er);
-                        af[i][0] = mx_frag(ch.x, ch.y, 4 * q, s2);
-                        af[i][1] = mx_frag(ch.z, ch.w, 4 * q, s2);
+                        const int ex = eb - er + 128;   // biased exponent of 2^(eb - er + 1); below 2^-126: 0
+                        const float scale = ex > 0 ? __builtin_bit_cast(float, (uint32_t) ex << 23) : 0.0f;
+                        // lane half q takes bytes 8q..8q+7 of the block: K-step 0 word 2q, K-step 1 word 2q + 1
+                        af[i][0] = mx_frag(q ? ch.z : ch.x, scale);
+                        af[i][1] = mx_frag(q ? ch.w : ch.y, scale);
                     }
 #pragma unroll
                     for (int i = 0; i < RT; i++)
@@ -751,12 +744,12 @@ static hipError_t kq_go(const WeightView& w, const GemmAct& A, int m, int n, flo
     const int64_t tiles = (w.r0 + tiled_rows(m)) / 32 - w.r0 / 32;   // tiles of the view that exist
     const int total = nrb * ncb, grid = (total + 7) / 8 * 8;
     const size_t lds = 2 * (size_t) S::BYTES;
-    static bool attr = false;
-    if (!attr) {
+    static std::atomic<bool> attr{false};   // threads racing here both set the same value
+    if (!attr.load(std::memory_order_acquire)) {
         hipError_t e = hipFuncSetAttribute((const void*) kq_gemm_kernel<DT, RT, CT>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int) lds);
         if (e != hipSuccess) return e;
-        attr = true;
+        attr.store(true, std::memory_order_release);
     }
     int ns = 1, sb_per = 0;
     if (part != nullptr) split_plan(total, A.Kp / 256, &ns, &sb_per);

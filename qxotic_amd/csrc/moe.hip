@@ -5,6 +5,8 @@
 #include "common.h"
 #include "launch.h"
 
+#include <atomic>
+
 namespace jamhip {
 
 constexpr int MOE_THREADS = 1024;
@@ -277,13 +279,13 @@ hipError_t launch_moe_route(const int* route_expert, int R, int E, int* counts, 
                             int* route_slot, hipStream_t st) {
     if (E < 1 || E > MOE_THREADS) return hipErrorNotSupported;
     const size_t lds = (size_t) (ROUTE_WAVES + 1) * E * sizeof(int);
-    static bool attr = false;
-    if (!attr) {
+    static std::atomic<bool> attr{false};   // threads racing here both set the same value
+    if (!attr.load(std::memory_order_acquire)) {
         const hipError_t e = hipFuncSetAttribute((const void*) moe_route_kernel,
                                                  hipFuncAttributeMaxDynamicSharedMemorySize,
                                                  (ROUTE_WAVES + 1) * MOE_THREADS * (int) sizeof(int));
         if (e != hipSuccess) return e;
-        attr = true;
+        attr.store(true, std::memory_order_release);
     }
     moe_route_kernel<<<1, MOE_THREADS, lds, st>>>(route_expert, R, E, counts, off, slot_route, route_slot);
     return hipGetLastError();

@@ -4,6 +4,8 @@
 #include "launch.h"
 #include "quant.h"
 
+#include <atomic>
+
 namespace jamhip {
 
 // One lane per activation element; a 32-lane half-wave owns one 32-element block (quant.h).
@@ -158,7 +160,9 @@ constexpr int PREP_MAX_KP = 65536;   // LDS: Kp/32 + Kp/16 floats per slot
 // q = sat8(rne(x·inv)) with NaN/overflow -> -128, and the per-16 sums in _mm512_reduce_add_ps's pairing
 // (distance 8, 4, 2, 1): distances 8 and 4 cross lanes (xor 2, xor 1: DPP quad permutes), 2 and 1 stay in
 // the lane.
-template <int SK>
+// MXO: the MXFP4 element order (the GEMM converts a weight byte's two nibbles, elements e and e + 16 of the
+// block, into one f16 pair): K-step 2·block + ks, half q, slot i holds element 8q + 4ks + i/2 + 16·(i % 2).
+template <int SK, bool MXO>
 __global__ void __launch_bounds__(256) gemm_prep(const float* __restrict__ a, int lda, int n, int k, int Kp, int NP,
                                                  _Float16* __restrict__ bq, float* __restrict__ dx,
                                                  _Float16* __restrict__ shi, _Float16* __restrict__ slo,
@@ -211,10 +215,22 @@ __global__ void __launch_bounds__(256) gemm_prep(const float* __restrict__ a, in
                 const float p = x[u] * inv;
                 qv[u] = !(p > -2147483648.0f && p < 2147483648.0f) ? -128 : (int) fminf(fmaxf(rintf(p), -128.0f), 127.0f);
             }
-            // codes: elements 4j..4j+3 -> K-step (j >> 1) & 1, half j >> 2, slots 4(j & 1) + {0, 2, 1, 3}
             typedef _Float16 half4 __attribute__((ext_vector_type(4)));
-            const half4 hv = {(_Float16) qv[0], (_Float16) qv[2], (_Float16) qv[1], (_Float16) qv[3]};
-            *reinterpret_cast<half4*>(bq + ((int64_t) (2 * b + ((j >> 1) & 1)) * NP + t) * 16 + 8 * (j >> 2) + 4 * (j & 1)) = hv;
+            if constexpr (!MXO) {
+                // codes: elements 4j..4j+3 -> K-step (j >> 1) & 1, half j >> 2, slots 4(j & 1) + {0, 2, 1, 3} of the
+                // (K-step, half) plane's 8 per token
+                const half4 hv = {(_Float16) qv[0], (_Float16) qv[2], (_Float16) qv[1], (_Float16) qv[3]};
+                *reinterpret_cast<half4*>(bq + ((int64_t) (2 * (2 * b + ((j >> 1) & 1)) + (j >> 2)) * NP + t) * 8 + 4 * (j & 1)) = hv;
+            } else {
+                // elements 4j + u -> K-step j & 1, half (j & 3) >> 1, slot 2u + (j >> 2): lanes j and j ^ 4 interleave
+                // their codes; lane j < 4 stores slots 0-3, lane j + 4 slots 4-7
+                int ov[4];
+#pragma unroll
+                for (int u = 0; u < 4; u++) ov[u] = __shfl_xor(qv[u], 4);
+                const half4 hv = j < 4 ? half4{(_Float16) qv[0], (_Float16) ov[0], (_Float16) qv[1], (_Float16) ov[1]}
+                                       : half4{(_Float16) ov[2], (_Float16) qv[2], (_Float16) ov[3], (_Float16) qv[3]};
+                *reinterpret_cast<half4*>(bq + ((int64_t) (2 * (2 * b + (j & 1)) + ((j & 3) >> 1)) * NP + t) * 8 + 4 * (j >> 2)) = hv;
+            }
             // per-16 sums: distance 8 (xor 2), distance 4 (xor 1), then in-lane distance 2 and 1
             float s[4];
 #pragma unroll
@@ -292,17 +308,21 @@ static hipError_t prep_np(int dt, const float* a, int lda, int n, int NP, int k,
     if (NP <= 0) return hipSuccess;
     const int vec = ((reinterpret_cast<uintptr_t>(a) & 15) == 0 && (lda & 3) == 0) ? 1 : 0;
     const size_t lds = ((size_t) (Kp / 32) + (size_t) (Kp / 16) + 4) * sizeof(float);
-    static bool attr[3] = {false, false, false};
-    const void* fn = sk == 1 ? (const void*) gemm_prep<1> : sk == 2 ? (const void*) gemm_prep<2> : (const void*) gemm_prep<0>;
-    if (!attr[sk]) {
+    const int kind = dt == MXFP4 ? 3 : sk;
+    const void* fn = kind == 1 ? (const void*) gemm_prep<1, false> : kind == 2 ? (const void*) gemm_prep<2, false>
+                   : kind == 3 ? (const void*) gemm_prep<0, true> : (const void*) gemm_prep<0, false>;
+    // the LDS limit is raised once per kernel; threads racing here both set the same value
+    static std::atomic<bool> attr[4];
+    if (!attr[kind].load(std::memory_order_acquire)) {
         const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
                                                  (int) ((PREP_MAX_KP / 32 + PREP_MAX_KP / 16 + 4) * sizeof(float)));
         if (e != hipSuccess) return e;
-        attr[sk] = true;
+        attr[kind].store(true, std::memory_order_release);
     }
-    if (sk == 1) gemm_prep<1><<<NP, 256, lds, st>>>(a, lda, n, k, Kp, NP, bq, dx, shi, slo, es, gmap, goff, gpoff, vec);
-    else if (sk == 2) gemm_prep<2><<<NP, 256, lds, st>>>(a, lda, n, k, Kp, NP, bq, dx, shi, slo, es, gmap, goff, gpoff, vec);
-    else gemm_prep<0><<<NP, 256, lds, st>>>(a, lda, n, k, Kp, NP, bq, dx, shi, slo, es, gmap, goff, gpoff, vec);
+    if (kind == 1) gemm_prep<1, false><<<NP, 256, lds, st>>>(a, lda, n, k, Kp, NP, bq, dx, shi, slo, es, gmap, goff, gpoff, vec);
+    else if (kind == 2) gemm_prep<2, false><<<NP, 256, lds, st>>>(a, lda, n, k, Kp, NP, bq, dx, shi, slo, es, gmap, goff, gpoff, vec);
+    else if (kind == 3) gemm_prep<0, true><<<NP, 256, lds, st>>>(a, lda, n, k, Kp, NP, bq, dx, shi, slo, es, gmap, goff, gpoff, vec);
+    else gemm_prep<0, false><<<NP, 256, lds, st>>>(a, lda, n, k, Kp, NP, bq, dx, shi, slo, es, gmap, goff, gpoff, vec);
     return hipGetLastError();
 }
 
