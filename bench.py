@@ -134,6 +134,23 @@ def gpu_leg(args, w: np.ndarray, hip, torch, stream) -> dict:
         if st != JAM.OK:
             raise RuntimeError(hip.last_error())
     host_us = (time.perf_counter() - t0) / calls * 1e6
+    # the same call on a weight nobody pinned: staged every call (autopin off), then with autopin (pinned on
+    # its second sighting, the first staged) -- the residency an unedited jinfer gets
+    fresh = w.copy()
+    t0 = time.perf_counter()
+    for i in range(8):
+        hip.mm_contiguous(Segment.of(fresh), Segment.of(a_h), Segment.of(c_h), JAM.Q4_K, M, N, K)
+    staged_us = (time.perf_counter() - t0) / 8 * 1e6
+    assert hip.set_autopin(2) == JAM.OK
+    for i in range(2):
+        hip.mm_contiguous(Segment.of(fresh), Segment.of(a_h), Segment.of(c_h), JAM.Q4_K, M, N, K)
+    t0 = time.perf_counter()
+    for i in range(calls):
+        hip.mm_contiguous(Segment.of(fresh), Segment.of(a_h), Segment.of(c_h), JAM.Q4_K, M, N, K)
+    auto_us = (time.perf_counter() - t0) / calls * 1e6
+    ap = hip.autopin_stats()
+    assert ap["pins"] >= 1 and ap["hits"] >= calls, ap
+    assert hip.set_autopin(0) == JAM.OK and hip.evict(Segment.of(fresh)) == JAM.OK
     with torch.cuda.stream(stream):
         st = hip.mm_device(Segment.of(copies[(calls - 1) % COPIES]), JAM.Q4_K, K, a.data_ptr(), K, ref.data_ptr(),
                            M, M, N, K)
@@ -141,7 +158,7 @@ def gpu_leg(args, w: np.ndarray, hip, torch, stream) -> dict:
     assert st == JAM.OK and np.array_equal(c_h, ref.cpu().numpy()), "host-pointer call disagrees"
     for cp in copies:
         hip.evict(Segment.of(cp))
-    return {"event_ms": ev_ms, "wall_s": wall, "host_us": host_us}
+    return {"event_ms": ev_ms, "wall_s": wall, "host_us": host_us, "staged_us": staged_us, "auto_us": auto_us}
 
 
 def read_floor_leg(args, hip, torch, stream) -> dict:
@@ -661,7 +678,10 @@ def main() -> int:
                    "graph_launches": 0 if args.no_graph else args.steps, "wall_s": round(g["wall_s"], 4)},
         "host_pointer_call": {"us": round(g["host_us"], 2), "GBs": round(STEP_BYTES / (g["host_us"] * 1e-6) / 1e9, 1),
                               "note": "jamhip_mm with host A and C (16 KiB H2D + 56 KiB D2H + sync per call), "
-                                      "pinned weights, wall clock; not the metric"},
+                                      "pinned weights, wall clock; not the metric",
+                              "unpinned_staged_us": round(g["staged_us"], 2), "unpinned_autopin_us": round(g["auto_us"], 2),
+                              "autopin_note": "the same call on a weight nobody pinned: staged every call, then with "
+                                              "jamhip_ctx_set_autopin(2) (pinned on its 2nd call, spot-checked each call)"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles()},
         "read_floor": floor,

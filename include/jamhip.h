@@ -95,6 +95,24 @@ jamhip_status jamhip_weight_evict(jamhip_ctx* ctx, const void* w);
 /* Bytes of device memory held by pinned weights. */
 int64_t       jamhip_weight_bytes(const jamhip_ctx* ctx);
 
+/* Autopin: residency for callers that never pin (no counterpart in jam; it stands in for the host-address
+ * registry the SPI lacks, since JAM.mm carries no weight identity and jinfer passes the same mmap'd
+ * address of a tensor on every call, MatMul.java:1783-1830, ModelLoader.java:70-104). Off by default.
+ * With sightings = N >= 1, jamhip_mm pins a whole contiguous W (ldw == k, rows [0, m)) that no pin holds on
+ * its N-th call with the same (address, dtype, ldw, m), taking a 64-bit hash of every 4 KiB page of the
+ * host range; later calls read the device copy after hashing two of its pages again (one rotating, one
+ * scattered, so repeated calls sweep the range). A mismatch means the caller rewrote the range in place
+ * (an arena reused for another tensor): the pin is evicted and the call stages W. A rewrite that leaves
+ * both checked pages unchanged is not seen on that call; callers that rewrite weights evict them
+ * (jamhip_weight_evict) or keep autopin off. max_bytes caps the device bytes autopin holds (0: no cap; a
+ * range over the cap stays staged). Applies to jamhip_mm only (the device-pointer entry points read pins
+ * made explicitly, so a captured graph never refers to a copy that a check could evict). Env at context
+ * creation: JAM_HIP_AUTOPIN=N, JAM_HIP_AUTOPIN_MAX_BYTES. */
+jamhip_status jamhip_ctx_set_autopin(jamhip_ctx* ctx, int sightings, int64_t max_bytes);
+/* out4 = {ranges autopinned, calls served from an autopin, calls staged while autopin was on, pins evicted
+ * by a failed check}, since the context was created. */
+jamhip_status jamhip_ctx_autopin_stats(const jamhip_ctx* ctx, int64_t* out4);
+
 /* Device-resident variant of jamhip_mm: W is a pinned host address (the registry key); A and C are
  * device pointers; the work is queued on the context stream and NOT synchronized. Same validation and
  * status codes as jamhip_mm. For callers that keep activations on the GPU (graph capture, benches). */

@@ -87,6 +87,18 @@ struct Pin {
     uint8_t* dev;       // plane 0
     uint8_t* sc;        // plane 1
     int64_t bytes;      // device bytes held
+    // autopin only (pinned by jamhip_mm on a repeat sighting): a hash of every 4 KiB page of the host range
+    // taken at pin time, and the count of per-call spot checks made against it
+    std::vector<uint64_t> pages;
+    uint64_t checks = 0;
+};
+
+// A host weight range seen by jamhip_mm while not resident (the autopin candidates).
+struct Sight {
+    uintptr_t host;
+    int dt, ldw;
+    int64_t rows;
+    int count;
 };
 
 constexpr int64_t align256(int64_t v) { return (v + 255) & ~int64_t(255); }
@@ -169,6 +181,12 @@ struct jamhip_ctx {
     DevBuf act, gact, part, moe;              // kernel scratch (addresses may be captured in graphs)
     StageBuf a_stage, c_stage, w_raw, w_stage;   // staging of host copies
     HostBuf a_host, c_host;   // jamhip_mm's pinned bounce buffers for A and C
+    // autopin (jamhip_ctx_set_autopin): pin a host weight range on its `autopin`-th sighting, 0 = off
+    int autopin = 0;
+    int64_t autopin_cap = 0;        // bytes autopin may hold on the device (0: no limit)
+    int64_t autopin_bytes = 0;      // held by autopins now, under pin_mu
+    std::vector<Sight> sights;      // under pin_mu, at most AUTOPIN_SIGHTS entries
+    int64_t ap_stats[4] = {0, 0, 0, 0};   // pins made, calls served by an autopin, staged calls, invalidations
 };
 
 namespace {
@@ -470,8 +488,109 @@ bool evict_at(jamhip_ctx* ctx, uintptr_t host) {
     (void) hipStreamSynchronize(ctx->stream);
     (void) hipFree(it->dev);
     ctx->pinned_bytes -= it->bytes;
+    if (!it->pages.empty()) ctx->autopin_bytes -= it->bytes;
     ctx->pins.erase(it);
     return true;
+}
+
+// ---- autopin: residency for callers that never pin (an unedited jinfer passes the same mmap'd address for
+// a tensor on every call, MatMul.java:1783-1830). A range is pinned on its N-th sighting; from then on each
+// call spot-checks two 4 KiB pages of the host range against the hashes taken at pin time (a rotating page
+// and a scattered one, so repeated calls sweep the whole range), and a mismatch (the caller rewrote the
+// range in place, e.g. an arena reused for another tensor) evicts the pin and stages the call.
+constexpr int64_t AUTOPIN_PAGE = 4096;
+constexpr size_t AUTOPIN_SIGHTS = 4096;
+
+// 64-bit hash of `bytes` host bytes (a multiply-xorshift over 8-byte words, then the tail bytes).
+uint64_t page_hash(const uint8_t* p, int64_t bytes) {
+    uint64_t h = 0x243F6A8885A308D3ull ^ (uint64_t) bytes;
+    int64_t i = 0;
+    for (; i + 8 <= bytes; i += 8) {
+        uint64_t w;
+        std::memcpy(&w, p + i, 8);
+        h = (h ^ w) * 0x9E3779B97F4A7C15ull;
+        h ^= h >> 29;
+    }
+    for (; i < bytes; i++) h = (h ^ p[i]) * 0x100000001B3ull;
+    return h;
+}
+
+std::vector<uint64_t> range_hashes(const uint8_t* p, int64_t span) {
+    std::vector<uint64_t> v((size_t) ((span + AUTOPIN_PAGE - 1) / AUTOPIN_PAGE));
+    for (size_t i = 0; i < v.size(); i++)
+        v[i] = page_hash(p + (int64_t) i * AUTOPIN_PAGE, std::min(AUTOPIN_PAGE, span - (int64_t) i * AUTOPIN_PAGE));
+    return v;
+}
+
+// The autopin (if any) that serves W: true with its device view after the spot check passes; a failed check
+// evicts it (the call then stages).
+bool autopin_lookup(jamhip_ctx* ctx, const void* w, int dt, int ldw, int m, WeightView* out) {
+    uintptr_t host = 0;
+    {
+        std::lock_guard<std::mutex> lk(ctx->pin_mu);
+        const uintptr_t p = reinterpret_cast<uintptr_t>(w);
+        auto it = std::upper_bound(ctx->pins.begin(), ctx->pins.end(), p,
+                                   [](uintptr_t v, const Pin& pin) { return v < pin.host; });
+        if (it == ctx->pins.begin()) return false;
+        Pin& pin = *(it - 1);
+        if (pin.pages.empty() || pin.host != p || pin.dt != dt || pin.ldw != ldw || pin.rows < m) return false;
+        const uint64_t np = pin.pages.size(), c = pin.checks++;
+        const uint64_t pg[2] = {c % np, (c * 2654435761ull + 1) % np};
+        bool same = true;
+        for (uint64_t i : pg) {
+            const int64_t at = (int64_t) i * AUTOPIN_PAGE;
+            same = same && page_hash((const uint8_t*) pin.host + at, std::min(AUTOPIN_PAGE, pin.span - at)) == pin.pages[i];
+        }
+        if (same) {
+            out->qs = pin.dev;
+            out->sc = pin.sc;
+            out->G = pin.G;
+            out->r0 = 0;
+            ctx->ap_stats[1]++;
+            return true;
+        }
+        host = pin.host;
+        ctx->ap_stats[3]++;
+    }
+    evict_at(ctx, host);
+    return false;
+}
+
+// Count a sighting of a non-resident W; on the autopin-th, pin it (a failed pin, e.g. out of device memory or
+// over the cap, leaves the call staged). Only whole contiguous matrices are taken (ldw == k), so the bytes
+// pinned and hashed are exactly the bytes the call reads.
+void autopin_sight(jamhip_ctx* ctx, const void* w, int dt, int ldw, int m, int k) {
+    if (ctx->autopin <= 0 || ldw != k) return;
+    const uintptr_t host = reinterpret_cast<uintptr_t>(w);
+    const int64_t span = (int64_t) m * row_bytes(dt, ldw);
+    bool pin_now = false;
+    {
+        std::lock_guard<std::mutex> lk(ctx->pin_mu);
+        auto it = std::find_if(ctx->sights.begin(), ctx->sights.end(), [&](const Sight& s) {
+            return s.host == host && s.dt == dt && s.ldw == ldw && s.rows == m;
+        });
+        if (it == ctx->sights.end()) {
+            if (ctx->sights.size() >= AUTOPIN_SIGHTS) ctx->sights.erase(ctx->sights.begin(), ctx->sights.begin() + AUTOPIN_SIGHTS / 2);
+            ctx->sights.push_back(Sight{host, dt, ldw, m, 0});
+            it = ctx->sights.end() - 1;
+        }
+        if (++it->count >= ctx->autopin) {
+            const int64_t dev_bytes = plane0_bytes(dt, m, ldw) + plane1_bytes(dt, m, ldw);
+            pin_now = ctx->autopin_cap <= 0 || ctx->autopin_bytes + dev_bytes <= ctx->autopin_cap;
+            ctx->sights.erase(it);
+        }
+    }
+    if (!pin_now) return;
+    std::vector<uint64_t> pages = range_hashes((const uint8_t*) w, span);
+    if (pin_range(ctx, w, dt, ldw, m, true) != JAMHIP_OK) return;   // overlap, allocation: stay staged
+    std::lock_guard<std::mutex> lk(ctx->pin_mu);
+    auto it = std::lower_bound(ctx->pins.begin(), ctx->pins.end(), host,
+                               [](const Pin& pin, uintptr_t v) { return pin.host < v; });
+    if (it != ctx->pins.end() && it->host == host && it->pages.empty()) {
+        it->pages = std::move(pages);
+        ctx->autopin_bytes += it->bytes;
+        ctx->ap_stats[0]++;
+    }
 }
 
 }  // namespace
@@ -496,6 +615,16 @@ jamhip_status mm_impl(jamhip_ctx* ctx, const void* w, int wt, int ldw, const voi
     if (!guard.ok) return fail(ctx, JAMHIP_EBUSY, "context busy");
     (void) hipSetDevice(ctx->device);
     WeightView wv;
+    if (ctx->autopin > 0 && !autopin_lookup(ctx, w, wt, ldw, m, &wv)) {
+        WeightView probe;
+        if (!lookup(ctx, w, wt, ldw, m, &probe)) {   // not resident by any pin: count the sighting
+            autopin_sight(ctx, w, wt, ldw, m, k);
+            if (!autopin_lookup(ctx, w, wt, ldw, m, &wv)) {
+                std::lock_guard<std::mutex> lk(ctx->pin_mu);
+                ctx->ap_stats[2]++;
+            }
+        }
+    }
     if ((st = resolve_w(ctx, w, wt, ldw, m, k, &wv)) != JAMHIP_OK) return st;
     hipError_t e;
     const size_t abytes = (size_t) n * k * 4, cbytes = (size_t) n * m * 4;
@@ -607,6 +736,18 @@ jamhip_status weight_pin_impl(jamhip_ctx* ctx, const void* w, int wt, int ldw, i
     if (!guard.ok) return fail(ctx, JAMHIP_EBUSY, "context busy");
     (void) hipSetDevice(ctx->device);
     return pin_range(ctx, w, wt, ldw, m, false);
+}
+
+jamhip_status set_autopin_impl(jamhip_ctx* ctx, int sightings, int64_t max_bytes) {
+    if (!ctx) return JAMHIP_EINVAL;
+    if (sightings < 0 || max_bytes < 0) return fail(ctx, JAMHIP_EINVAL, "autopin: sightings and max_bytes must be >= 0");
+    Busy guard(ctx);
+    if (!guard.ok) return fail(ctx, JAMHIP_EBUSY, "context busy");
+    std::lock_guard<std::mutex> lk(ctx->pin_mu);
+    ctx->autopin = sightings;
+    ctx->autopin_cap = max_bytes;
+    if (sightings == 0) ctx->sights.clear();
+    return JAMHIP_OK;
 }
 
 jamhip_status weight_evict_impl(jamhip_ctx* ctx, const void* w) {
@@ -821,6 +962,8 @@ jamhip_ctx* create_ctx(int device, std::string* err) {
         return nullptr;
     }
     ctx->stream = ctx->own;
+    if (const char* v = getenv("JAM_HIP_AUTOPIN")) ctx->autopin = atoi(v) > 0 ? atoi(v) : 0;
+    if (const char* v = getenv("JAM_HIP_AUTOPIN_MAX_BYTES")) ctx->autopin_cap = atoll(v) > 0 ? atoll(v) : 0;
     return ctx;
 }
 
@@ -946,6 +1089,18 @@ jamhip_status jamhip_glu_device(jamhip_ctx* ctx, int act, void* gate_dev, int ld
 
 jamhip_status jamhip_read_floor(jamhip_ctx* ctx, const void* p_dev, int64_t bytes, void* sink_dev) {
     return on_ctx(ctx, [&](jamhip_ctx* x) { return read_floor_impl(x, p_dev, bytes, sink_dev); });
+}
+
+jamhip_status jamhip_ctx_set_autopin(jamhip_ctx* ctx, int sightings, int64_t max_bytes) {
+    return on_ctx(ctx, [&](jamhip_ctx* x) { return set_autopin_impl(x, sightings, max_bytes); });
+}
+
+jamhip_status jamhip_ctx_autopin_stats(const jamhip_ctx* ctx, int64_t* out4) {
+    jamhip_ctx* x = ctx ? const_cast<jamhip_ctx*>(ctx) : global_ctx();
+    if (!x || !out4) return JAMHIP_EINVAL;
+    std::lock_guard<std::mutex> lk(x->pin_mu);
+    for (int i = 0; i < 4; i++) out4[i] = x->ap_stats[i];
+    return JAMHIP_OK;
 }
 
 jamhip_status jamhip_weight_pin(jamhip_ctx* ctx, const void* w, int wt, int ldw, int m) {

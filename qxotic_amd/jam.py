@@ -197,6 +197,18 @@ class HipJAM:
     def pinned_bytes(self) -> int:
         return lib().jamhip_weight_bytes(self._ctx)
 
+    def set_autopin(self, sightings: int, max_bytes: int = 0) -> int:
+        """Pin a whole W on its `sightings`-th jamhip_mm call (0 = off), content-checked per call
+        (jamhip_ctx_set_autopin)."""
+        return lib().jamhip_ctx_set_autopin(self.ctx, sightings, max_bytes)
+
+    def autopin_stats(self) -> dict:
+        """{pins, hits, staged, invalidated} since the context was created (jamhip_ctx_autopin_stats)."""
+        out = (C.c_int64 * 4)()
+        if lib().jamhip_ctx_autopin_stats(self.ctx, out) != 0:
+            raise RuntimeError("autopin stats: " + self.last_error())
+        return dict(zip(("pins", "hits", "staged", "invalidated"), list(out)))
+
     # -- device-resident path (torch tensors or raw device addresses) ------------------------------
     def mm_device(self, w: Segment, wt: int, ldw: int, a_dev: int, lda: int, c_dev: int, ldc: int,
                   m: int, n: int, k: int) -> int:
