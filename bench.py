@@ -305,16 +305,38 @@ def moe_leg(hip, torch, stream, steps: int = 10) -> dict:
     us = e0.elapsed_time(e1) * 1e3 / steps
     assert np.array_equal(counts.cpu().numpy(), counts_h), "device routing counts disagree with the host's"
     assert bool(torch.isfinite(out).all()), "moe output not finite"
+    ops = 2.0 * R * (FF * D + D * D)
+    # the opt-in native-MX mode (not jam's activation semantics): the same layer with the experts' matrix-core
+    # calls on the scaled fp4 x fp8 MFMA, MX-FP8 activations hi + lo (mode 1) or hi only (mode 2)
+    native = {}
+    for mode in (1, 2):
+        assert hip.set_mx_native(mode) == JAM.OK
+        with torch.cuda.stream(stream):
+            for i in range(3):
+                layer(i)
+            torch.cuda.synchronize()
+            e0.record(stream)
+            for i in range(steps):
+                layer(i)
+            e1.record(stream)
+            torch.cuda.synchronize()
+        assert hip.set_mx_native(0) == JAM.OK
+        assert bool(torch.isfinite(out).all()), "moe output not finite"
+        u = e0.elapsed_time(e1) * 1e3 / steps
+        native[f"mode{mode}"] = {"us_per_layer": round(u, 1), "TOPS": round(ops / (u * 1e-6) / 1e12, 2),
+                                 "frac_fp4_peak": round(ops / (u * 1e-6) / 1e12 / 10070.0, 4)}
+    native["note"] = ("opt-in jamhip_ctx_set_mx_native: MXFP4 weights as fp4 on v_mfma_scale_f32_32x32x64_f8f6f4, "
+                      "activations MX-FP8 hi + lo (mode 1, ~8 bits) or hi only (mode 2, ~4 bits); not jam's "
+                      "int8 activation semantics")
     for xx in wg + wd:
         hip.evict(Segment.of(xx))
-    ops = 2.0 * R * (FF * D + D * D)
     wbytes = E * (FF + D) * (D // 32) * 17
     tops = ops / (us * 1e-6) / 1e12
     gbs = wbytes / (us * 1e-6) / 1e9
     return {"us_per_layer": round(us, 1), "TOPS": round(tops, 2), "weights_GBs": round(gbs, 1),
             "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
             "frac_fp4_peak": round(tops / 10070.0, 4), "routed_rows": R,
-            "counts": counts_h.tolist(),
+            "counts": counts_h.tolist(), "mx_native": native,
             "note": "32 experts x (5760x2880 + 2880x2880) MXFP4 (423 MB, 2 rotating copies; experts cycle through "
                     "2 distinct N(0,0.02) quantizations), 512 tokens top-4 Zipf(1.1); ops = 2*routed_rows*"
                     "(5760*2880 + 2880*2880)"}

@@ -113,6 +113,19 @@ jamhip_status jamhip_ctx_set_autopin(jamhip_ctx* ctx, int sightings, int64_t max
  * by a failed check}, since the context was created. */
 jamhip_status jamhip_ctx_autopin_stats(const jamhip_ctx* ctx, int64_t* out4);
 
+/* Native-MX mode for MXFP4 weights (no counterpart in jam; off by default). The MXFP4 calls this library
+ * runs on the matrix cores (from the same size-dependent token count as the int8 path, 9 to 17 tokens, and
+ * every jamhip_mm_grouped expert with 8 or more rows) then feed the weights to v_mfma_scale_f32_32x32x64_f8f6f4 as their own fp4 codes and the
+ * activations as MX-FP8: per 32-element block E = the smallest exponent with max|x|·2^-E <= 448,
+ * hi = e4m3(x·2^-E) (round to nearest even) with scale 2^E, lo = e4m3((x·2^-E - hi)·16) with scale 2^(E-4);
+ * mode 1 multiplies hi and lo (about 8 significant bits per activation), mode 2 hi only (about 4). The
+ * weights keep jam's exact values; the activations are NOT jam's int8 F2 codes, so results differ from
+ * jam's by up to its own quantization error (tests bound mode 1 against the f64 product of the unquantized
+ * activations at 5e-3·Σ|w·a|; measured 6e-5, jam's int8 path 2.3e-3). The hardware's scaled block dot
+ * itself rounds (steps of about 2^-16 at unit magnitude, measured). Non-finite activations give unspecified (finite-bounded) results. Decode
+ * calls (fewer tokens) keep jam's semantics. Env at context creation: JAM_HIP_MX_NATIVE=1|2. */
+jamhip_status jamhip_ctx_set_mx_native(jamhip_ctx* ctx, int mode);
+
 /* Device-resident variant of jamhip_mm: W is a pinned host address (the registry key); A and C are
  * device pointers; the work is queued on the context stream and NOT synchronized. Same validation and
  * status codes as jamhip_mm. For callers that keep activations on the GPU (graph capture, benches). */

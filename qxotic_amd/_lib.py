@@ -26,6 +26,7 @@ SIGNATURES = [
     ("jamhip_weight_bytes", _I64, [_VP]),
     ("jamhip_ctx_set_autopin", _I, [_VP, _I, _I64]),
     ("jamhip_ctx_autopin_stats", _I, [_VP, _VP]),
+    ("jamhip_ctx_set_mx_native", _I, [_VP, _I]),
     ("jamhip_mm_device", _I, [_VP, _VP, _I, _I, _VP, _I, _I, _VP, _I, _I, _I, _I, _I]),
     ("jamhip_mm_device_noalloc", _I, [_VP, _VP, _I, _I, _VP, _I, _I, _VP, _I, _I, _I, _I, _I]),
     ("jamhip_quantize_device", _I, [_VP, _I, _VP, _I, _I, _I, _VP, _VP, _VP]),

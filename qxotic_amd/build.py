@@ -38,6 +38,7 @@ UNITS = {   # source -> extra flags
     "dense.hip": [],
     "gemm.hip": [],
     "mma.hip": [],
+    "mxn.hip": [],
     "moe.hip": [],
     "epilogue.hip": [],
     "readfloor.hip": [],

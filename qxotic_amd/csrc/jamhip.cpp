@@ -187,6 +187,7 @@ struct jamhip_ctx {
     int64_t autopin_bytes = 0;      // held by autopins now, under pin_mu
     std::vector<Sight> sights;      // under pin_mu, at most AUTOPIN_SIGHTS entries
     int64_t ap_stats[4] = {0, 0, 0, 0};   // pins made, calls served by an autopin, staged calls, invalidations
+    int mx_native = 0;   // MXFP4 matrix-core calls: 0 jam's int8 semantics, 1 / 2 the native-MX path (mxn.hip)
 };
 
 namespace {
@@ -389,6 +390,18 @@ jamhip_status compute(jamhip_ctx* ctx, Scratch& sc, int dt, const WeightView& wv
     // n >= 8: jam's 16-row F2 bands on rows [0, m16); the last m % 16 rows take the band's float-dot tail
     // (jam_kernels_q4k_avx512.c:185-188).
     const int m16 = m - m % 16;
+    if (dt == MXFP4 && ctx->mx_native && n >= mma_min_n(dt, m, k) && mma_path(dt, k, wv)) {
+        // opt-in native MX (not jam's activation semantics): every row on the scaled fp4 x fp8 MFMA
+        MxAct X;
+        void* gact = nullptr;
+        if ((e = sc.get(ctx->gact, mx_act_bytes_np((n + 63) / 64 * 64, k), &gact)) != hipSuccess)
+            return scratch_fail(ctx, sc, e, "mx activation scratch");
+        if ((e = launch_mx_prep(a, lda, n, k, ctx->mx_native, gact, &X, ctx->stream)) != hipSuccess)
+            return hip_fail(ctx, e, "mx prep launch");
+        if ((e = launch_mx_gemm(ctx->mx_native, wv, X, m, n, c, ldc, ctx->stream, ep)) != hipSuccess)
+            return hip_fail(ctx, e, "mx gemm launch");
+        return JAMHIP_OK;
+    }
     if (n >= mma_min_n(dt, m, k) && m16 > 0 && mma_path(dt, k, wv)) {
         GemmAct G;
         void* gact = nullptr;
@@ -750,6 +763,15 @@ jamhip_status set_autopin_impl(jamhip_ctx* ctx, int sightings, int64_t max_bytes
     return JAMHIP_OK;
 }
 
+jamhip_status set_mx_native_impl(jamhip_ctx* ctx, int mode) {
+    if (!ctx) return JAMHIP_EINVAL;
+    if (mode < 0 || mode > 2) return fail(ctx, JAMHIP_EINVAL, "mx_native: mode must be 0, 1 or 2");
+    Busy guard(ctx);
+    if (!guard.ok) return fail(ctx, JAMHIP_EBUSY, "context busy");
+    ctx->mx_native = mode;
+    return JAMHIP_OK;
+}
+
 jamhip_status weight_evict_impl(jamhip_ctx* ctx, const void* w) {
     if (!ctx || !w) return JAMHIP_EINVAL;
     Busy guard(ctx);
@@ -846,7 +868,14 @@ jamhip_status mm_grouped_ex_impl(jamhip_ctx* ctx, const void* w, int wt, int ldw
             return hip_fail(ctx, e, "grouped: gemv launch");
     }
     // experts with >= 8 rows: jam's F2 bands (m % 16 == 0: no float-dot tail rows)
-    if (mma_path(wt, k, wv) && m % 32 == 0) {
+    if (wt == MXFP4 && ctx->mx_native && mma_path(wt, k, wv) && m % 32 == 0) {   // opt-in native MX
+        MxAct X;
+        if ((e = ctx->gact.ensure(mx_act_bytes_np(cap64 * 64, k))) != hipSuccess)
+            return hip_fail(ctx, e, "grouped: mx activation scratch alloc");
+        if ((e = launch_mx_prep_grouped(a, lda, k, ctx->mx_native, g, cap64, ctx->gact.p, &X, ctx->stream)) != hipSuccess ||
+            (e = launch_mx_gemm_grouped(ctx->mx_native, wv, X, g, cap64, c, ldc, ctx->stream)) != hipSuccess)
+            return hip_fail(ctx, e, "grouped: mx gemm launch");
+    } else if (mma_path(wt, k, wv) && m % 32 == 0) {
         GemmAct G;
         if ((e = ctx->gact.ensure(gemm_act_bytes_np(wt, cap64 * 64, k))) != hipSuccess)
             return hip_fail(ctx, e, "grouped: gemm activation scratch alloc");
@@ -964,6 +993,7 @@ jamhip_ctx* create_ctx(int device, std::string* err) {
     ctx->stream = ctx->own;
     if (const char* v = getenv("JAM_HIP_AUTOPIN")) ctx->autopin = atoi(v) > 0 ? atoi(v) : 0;
     if (const char* v = getenv("JAM_HIP_AUTOPIN_MAX_BYTES")) ctx->autopin_cap = atoll(v) > 0 ? atoll(v) : 0;
+    if (const char* v = getenv("JAM_HIP_MX_NATIVE")) ctx->mx_native = atoi(v) == 1 || atoi(v) == 2 ? atoi(v) : 0;
     return ctx;
 }
 
@@ -1093,6 +1123,10 @@ jamhip_status jamhip_read_floor(jamhip_ctx* ctx, const void* p_dev, int64_t byte
 
 jamhip_status jamhip_ctx_set_autopin(jamhip_ctx* ctx, int sightings, int64_t max_bytes) {
     return on_ctx(ctx, [&](jamhip_ctx* x) { return set_autopin_impl(x, sightings, max_bytes); });
+}
+
+jamhip_status jamhip_ctx_set_mx_native(jamhip_ctx* ctx, int mode) {
+    return on_ctx(ctx, [&](jamhip_ctx* x) { return set_mx_native_impl(x, mode); });
 }
 
 jamhip_status jamhip_ctx_autopin_stats(const jamhip_ctx* ctx, int64_t* out4) {

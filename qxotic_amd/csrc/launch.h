@@ -96,6 +96,24 @@ hipError_t launch_gemm_mma_grouped(int dt, const WeightView& w, const GemmAct& A
                                    float* c, int ldc, hipStream_t st);
 size_t gemm_act_bytes_np(int dt, int NP, int k);
 
+// Opt-in native-MX path for MXFP4 (mxn.hip): activations as MX-FP8 hi + lo codes (mode 1) or hi only
+// (mode 2) in the scaled MFMA's B operand order, one e8m0 scale per 32-block for each part.
+struct MxAct {
+    const uint8_t* hi;    // [Kp/64][2][NP][32] e4m3 codes (64-K step, lane half, token slot, byte)
+    const uint8_t* lo;
+    const uint8_t* shi;   // [Kp/32][NP] e8m0 scale of each block's hi codes
+    const uint8_t* slo;
+    int NP, Kp, K;
+};
+size_t mx_act_bytes_np(int NP, int k);
+hipError_t launch_mx_prep(const float* a, int lda, int n, int k, int mode, void* scratch, MxAct* out, hipStream_t st);
+hipError_t launch_mx_prep_grouped(const float* a, int lda, int k, int mode, const Groups& g, int cap64, void* scratch,
+                                  MxAct* out, hipStream_t st);
+hipError_t launch_mx_gemm(int mode, const WeightView& w, const MxAct& A, int m, int n, float* c, int ldc, hipStream_t st,
+                          const Epi& ep = Epi{});
+hipError_t launch_mx_gemm_grouped(int mode, const WeightView& w, const MxAct& A, const Groups& g, int cap64, float* c,
+                                  int ldc, hipStream_t st);
+
 // Dense weights (F32, F16, BF16; dense.hip): jam's dense paths, any n, any k (rows padded to a 256-byte pitch,
 // WeightView::G = the pitch).
 hipError_t launch_dense(int dt, const WeightView& w, const float* a, int lda, int k, int m, int n, float* c, int ldc,

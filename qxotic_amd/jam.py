@@ -202,6 +202,11 @@ class HipJAM:
         (jamhip_ctx_set_autopin)."""
         return lib().jamhip_ctx_set_autopin(self.ctx, sightings, max_bytes)
 
+    def set_mx_native(self, mode: int) -> int:
+        """MXFP4 matrix-core calls on the native MX path: 0 off (jam semantics), 1 MX-FP8 hi + lo activations,
+        2 hi only (jamhip_ctx_set_mx_native)."""
+        return lib().jamhip_ctx_set_mx_native(self.ctx, mode)
+
     def autopin_stats(self) -> dict:
         """{pins, hits, staged, invalidated} since the context was created (jamhip_ctx_autopin_stats)."""
         out = (C.c_int64 * 4)()
