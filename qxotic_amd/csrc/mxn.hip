@@ -69,15 +69,20 @@ JAMHIP_DEV int slot_source(int t, int n, const int* gmap, const int* goff, const
 }  // namespace mxn
 
 // One workgroup of 256 threads per token slot; a half-wave (32 lanes) per 32-element block, one element per
-// lane: the block maximum by shuffles, E, the hi / lo codes in the MFMA B order, the two scale bytes.
+// lane: the block maximum by shuffles, E, the hi / lo codes in the MFMA B order, the two scale bytes. The
+// codes of 8 blocks (4 K-steps x 2 halves x 32 bytes per plane) are assembled in LDS and written as 16-byte
+// pieces. A padding slot (past n, or past its expert's rows) is left unwritten: its token column is computed
+// but never stored. Mode 2 writes no lo plane (the GEMM reads none).
 __global__ void __launch_bounds__(256) mxn_prep_kernel(const float* __restrict__ a, int lda, int n, int k, int Kp,
                                                        int NP, int mode, uint8_t* __restrict__ hi,
                                                        uint8_t* __restrict__ lo, uint8_t* __restrict__ shi,
                                                        uint8_t* __restrict__ slo, const int* __restrict__ gmap,
                                                        const int* __restrict__ goff, const int* __restrict__ gpoff) {
     using namespace mxn;
+    __shared__ __align__(16) uint8_t lh[256], ll[256];  // 8 blocks' codes: [4 steps][2 halves][32 bytes]
     const int t = blockIdx.x;
     const int src = slot_source(t, n, gmap, goff, gpoff);
+    if (src < 0) return;
     const int e = threadIdx.x & 31;                     // element within the block
     for (int b = threadIdx.x >> 5; b < Kp / 32; b += 8) {
         const int col = 32 * b + e;
@@ -99,13 +104,23 @@ __global__ void __launch_bounds__(256) mxn_prep_kernel(const float* __restrict__
         const uint32_t cl = lo_ok ? e4m3((v - e4m3_value(ch)) * 16.0f) : 0u;
         // B order: K-step s = b / 2, bytes 16·(b % 2) + j of lane half q, element 8q + j/2 + 16·(j % 2)
         const int q = (e & 15) >> 3, j = 2 * ((e & 15) - 8 * q) + (e >> 4);
-        const int64_t at = (((int64_t) (b >> 1) * 2 + q) * NP + t) * 32 + 16 * (b & 1) + j;
-        hi[at] = (uint8_t) ch;
-        lo[at] = (uint8_t) cl;
+        const int bl = b & 7;                            // block within the 8 of this pass
+        const int li = ((bl >> 1) * 2 + q) * 32 + 16 * (bl & 1) + j;
+        lh[li] = (uint8_t) ch;
+        ll[li] = (uint8_t) cl;
         if (e == 0) {
             shi[(int64_t) b * NP + t] = (uint8_t) (E + 127);
-            slo[(int64_t) b * NP + t] = lo_ok ? (uint8_t) (E - 4 + 127) : (uint8_t) 0;
+            if (mode == 1) slo[(int64_t) b * NP + t] = lo_ok ? (uint8_t) (E - 4 + 127) : (uint8_t) 0;
         }
+        __syncthreads();
+        // 16 pieces of 16 bytes per plane: piece p = (step s, half q, 16-byte half h) of this pass's 4 steps
+        if (threadIdx.x < (mode == 1 ? 32 : 16)) {
+            const int pl = threadIdx.x >> 4, p = threadIdx.x & 15, s = p >> 2, qq = (p >> 1) & 1, h = p & 1;
+            const int step = (b - bl) / 2 + s;
+            uint8_t* dst = (pl ? lo : hi) + (((int64_t) step * 2 + qq) * NP + t) * 32 + 16 * h;
+            *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>((pl ? ll : lh) + (s * 2 + qq) * 32 + 16 * h);
+        }
+        __syncthreads();
     }
 }
 
@@ -164,16 +179,18 @@ __global__ void __launch_bounds__(256, 2) mxn_gemm_kernel(WeightView w, MxAct A,
         const uint8_t* ag = a_src + (int64_t) g * (NC * CHUNK_STRIDE) + (4 * h2) * CHUNK_STRIDE;
         dma16(ag, buf + A_OFF + wave * 2048);
         dma16(ag + 2 * CHUNK_STRIDE, buf + A_OFF + wave * 2048 + 1024);
+        if (MODE == 1 || wave < 2) {   // mode 2 has no lo plane
 #pragma unroll
-        for (int p = 0; p < 2; p++) {
-            const int sq = 2 * (wave & 1) + p;         // (step, half) = (sq >> 1, sq & 1)
+            for (int p = 0; p < 2; p++) {
+                const int sq = 2 * (wave & 1) + p;     // (step, half) = (sq >> 1, sq & 1)
 #pragma unroll
-            for (int th = 0; th < 2; th++)
-                dma16(bplane + (int64_t) (2 * st + (sq >> 1)) * bstep + ((int64_t) (sq & 1) * A.NP + n0 + 32 * th) * 32 + 16 * lane,
-                      buf + boff + (sq * 64 + 32 * th) * 32);
+                for (int th = 0; th < 2; th++)
+                    dma16(bplane + (int64_t) (2 * st + (sq >> 1)) * bstep + ((int64_t) (sq & 1) * A.NP + n0 + 32 * th) * 32 + 16 * lane,
+                          buf + boff + (sq * 64 + 32 * th) * 32);
+            }
         }
         if (wave < 2) dma16(h_src + (int64_t) g * 32 * 16, buf + H_OFF + wave * 1024);
-        if (wave >= 2 && lane < 16) {   // scales: 4 blocks x 64 tokens, one byte each
+        if ((wave == 2 || (wave == 3 && MODE == 1)) && lane < 16) {   // scales: 4 blocks x 64 tokens, a byte each
             const uint8_t* s = (wave == 2 ? A.shi : A.slo) + (int64_t) (4 * st + (lane >> 2)) * A.NP + n0 + 16 * (lane & 3);
             dma16(s, buf + (wave == 2 ? SH_OFF : SL_OFF));
         }

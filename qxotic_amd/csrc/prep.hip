@@ -177,6 +177,9 @@ __global__ void __launch_bounds__(256) gemm_prep(const float* __restrict__ a, in
     const int t = (int) (blockIdx.x % 8) * (NP >> 3) + (int) (blockIdx.x >> 3);
     const int nbk = k >> 5, lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nch = Kp >> 8;
     const int src = prep_src(t, n, gmap, goff, gpoff);
+    // a padding slot (past n, or past its expert's rows) is left unwritten: the GEMM's token column for it is
+    // computed but never stored, and no other column reads it
+    if (src < 0) return;
     const int j = lane & 7;   // lane within the block
     float m2 = 0.0f;
     // batches of 4 chunks per wave: the batch's loads go out together, then the chunks are quantized
