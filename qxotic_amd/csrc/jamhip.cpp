@@ -178,7 +178,7 @@ struct jamhip_ctx {
     mutable std::mutex pin_mu;
     std::vector<Pin> pins;
     int64_t pinned_bytes = 0;   // sum of pins[].bytes, under pin_mu
-    DevBuf act, gact, part, moe;              // kernel scratch (addresses may be captured in graphs)
+    DevBuf act, gact, part, moe, route;       // kernel scratch (addresses may be captured in graphs)
     StageBuf a_stage, c_stage, w_raw, w_stage;   // staging of host copies
     HostBuf a_host, c_host;   // jamhip_mm's pinned bounce buffers for A and C
     // autopin (jamhip_ctx_set_autopin): pin a host weight range on its `autopin`-th sighting, 0 = off
@@ -904,8 +904,13 @@ jamhip_status moe_route_impl(jamhip_ctx* ctx, const void* route_expert_dev, int 
     Busy guard(ctx);
     if (!guard.ok) return fail(ctx, JAMHIP_EBUSY, "context busy");
     (void) hipSetDevice(ctx->device);
+    int* scratch = nullptr;
+    if (const size_t ni = moe_route_scratch_ints(seq * topk, n_experts)) {   // chunk counts of the spread kernel
+        if (ctx->route.ensure(ni * sizeof(int)) == hipSuccess) scratch = (int*) ctx->route.p;
+    }
     const hipError_t e = launch_moe_route((const int*) route_expert_dev, seq * topk, n_experts, (int*) counts_dev,
-                                          (int*) offsets_dev, (int*) slot_route_dev, (int*) route_slot_dev, ctx->stream);
+                                          (int*) offsets_dev, (int*) slot_route_dev, (int*) route_slot_dev, ctx->stream,
+                                          scratch);
     return e == hipSuccess ? JAMHIP_OK : hip_fail(ctx, e, "route launch");
 }
 
@@ -1008,6 +1013,7 @@ void destroy_ctx(jamhip_ctx* ctx) {
     ctx->gact.release();
     ctx->part.release();
     ctx->moe.release();
+    ctx->route.release();
     ctx->a_stage.release();
     ctx->c_stage.release();
     ctx->w_raw.release();

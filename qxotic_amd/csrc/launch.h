@@ -131,8 +131,11 @@ hipError_t launch_gemm_prep_grouped(int dt, const float* a, int lda, int k, cons
 // MoE bookkeeping (moe.hip)
 hipError_t launch_moe_offsets(const int* counts, int E, int rows_cap, int* off, int* poff64, int* poff8, int* map64,
                               int cap64, int* map8, int cap8, hipStream_t st);
+// scratch: moe_route_scratch_ints(R, E) ints of device memory for the chunked form (R > 256 routes, E <= 256),
+// or null for the single-workgroup kernel; both give the same slots.
+size_t moe_route_scratch_ints(int R, int E);
 hipError_t launch_moe_route(const int* route_expert, int R, int E, int* counts, int* off, int* slot_route,
-                            int* route_slot, hipStream_t st);
+                            int* route_slot, hipStream_t st, int* scratch = nullptr);
 hipError_t launch_moe_gather(const float* x, int ldx, const int* slot_route, const int* off, int E, int R, int topk,
                              int dim, float* g, int ldg, hipStream_t st);
 hipError_t launch_moe_combine(const float* y, int ldy, const int* route_expert, const float* route_prob,

@@ -175,6 +175,84 @@ __global__ void __launch_bounds__(MOE_THREADS) moe_route_kernel(const int* __res
     }
 }
 
+// The same CSR build spread over chunks of 256 routes, for E <= 256 (two launches, still no atomics):
+// moe_route_count_kernel writes each chunk's per-expert counts; moe_route_slot_kernel gives every chunk the
+// totals, the experts' offsets (exclusive scan of the totals) and the counts of the chunks before it, so each
+// route's slot is off[e] + (earlier chunks' routes of e) + (earlier waves' of the chunk) + (its rank in the
+// wave): the same slots as the single-workgroup kernel.
+constexpr int RCH = 256, RCH_WAVES = RCH / 64;
+JAMHIP_DEV void chunk_wave_counts(int e, int E, int* wcnt, int* rank) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint64_t below = (1ull << lane) - 1ull;
+    for (int x = 0; x < E; x++) {
+        const uint64_t m = __ballot(e == x);
+        if (e == x) *rank = __popcll(m & below);
+        if (lane == 0) wcnt[wave * E + x] = __popcll(m);
+    }
+}
+__global__ void __launch_bounds__(RCH) moe_route_count_kernel(const int* __restrict__ route_expert, int R, int E,
+                                                             int* __restrict__ ccnt) {
+    __shared__ int wcnt[RCH_WAVES * 256];
+    const int r = blockIdx.x * RCH + threadIdx.x;
+    const int e = r < R ? route_expert[r] : -1;
+    int rank = 0;
+    chunk_wave_counts(e, E, wcnt, &rank);
+    __syncthreads();
+    if (threadIdx.x < E) {
+        int s = 0;
+        for (int w = 0; w < RCH_WAVES; w++) s += wcnt[w * E + threadIdx.x];
+        ccnt[(int64_t) blockIdx.x * E + threadIdx.x] = s;
+    }
+}
+__global__ void __launch_bounds__(RCH) moe_route_slot_kernel(const int* __restrict__ route_expert, int R, int E,
+                                                            const int* __restrict__ ccnt, int nch,
+                                                            int* __restrict__ counts, int* __restrict__ off,
+                                                            int* __restrict__ slot_route, int* __restrict__ route_slot) {
+    __shared__ int wcnt[RCH_WAVES * 256], base[256], scan[RCH];
+    const int t = threadIdx.x, wave = t >> 6;
+    int total = 0, before = 0;
+    if (t < E)
+        for (int c = 0; c < nch; c++) {
+            const int v = ccnt[(int64_t) c * E + t];
+            total += v;
+            before += c < (int) blockIdx.x ? v : 0;
+        }
+    // exclusive scan of the totals over the experts (Hillis-Steele in LDS)
+    scan[t] = t < E ? total : 0;
+    __syncthreads();
+    for (int o = 1; o < RCH; o <<= 1) {
+        const int x = t >= o ? scan[t - o] : 0;
+        __syncthreads();
+        scan[t] += x;
+        __syncthreads();
+    }
+    const int oe = scan[t] - (t < E ? total : 0);
+    if (t < E) {
+        base[t] = oe + before;
+        if (blockIdx.x == 0) {
+            counts[t] = total;
+            off[t] = oe;
+            if (t == E - 1) off[E] = oe + total;
+        }
+    }
+    const int r = blockIdx.x * RCH + t;
+    const int e = r < R ? route_expert[r] : -1;
+    int rank = 0;
+    chunk_wave_counts(e, E, wcnt, &rank);
+    __syncthreads();
+    if (r < R) {
+        if (e >= 0 && e < E) {
+            int pre = 0;
+            for (int w = 0; w < wave; w++) pre += wcnt[w * E + e];
+            const int slot = base[e] + pre + rank;
+            slot_route[slot] = r;
+            route_slot[r] = slot;
+        } else {
+            route_slot[r] = -1;
+        }
+    }
+}
+
 // Moe.dispatch's gather (Moe.java:214-222): g[slot] = x[slot_route[slot] / topk] (dim floats per row).
 // Slots past off[E] (routes with an expert id outside [0, E) leave them unassigned) are not written. V4:
 // rows copied as float4 (the launcher checks 16-byte alignment of both rows and dim % 4 == 0).
@@ -275,9 +353,17 @@ hipError_t launch_moe_offsets(const int* counts, int E, int rows_cap, int* off, 
     return hipGetLastError();
 }
 
+size_t moe_route_scratch_ints(int R, int E) { return E <= 256 && R > RCH ? (size_t) ((R + RCH - 1) / RCH) * E : 0; }
+
 hipError_t launch_moe_route(const int* route_expert, int R, int E, int* counts, int* off, int* slot_route,
-                            int* route_slot, hipStream_t st) {
+                            int* route_slot, hipStream_t st, int* scratch) {
     if (E < 1 || E > MOE_THREADS) return hipErrorNotSupported;
+    if (scratch != nullptr && moe_route_scratch_ints(R, E) > 0) {   // chunked: R > 256 routes, E <= 256
+        const int nch = (R + RCH - 1) / RCH;
+        moe_route_count_kernel<<<nch, RCH, 0, st>>>(route_expert, R, E, scratch);
+        moe_route_slot_kernel<<<nch, RCH, 0, st>>>(route_expert, R, E, scratch, nch, counts, off, slot_route, route_slot);
+        return hipGetLastError();
+    }
     const size_t lds = (size_t) (ROUTE_WAVES + 1) * E * sizeof(int);
     static std::atomic<bool> attr{false};   // threads racing here both set the same value
     if (!attr.load(std::memory_order_acquire)) {

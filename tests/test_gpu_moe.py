@@ -32,12 +32,16 @@ def dev(x):
 
 def test_route_gather_combine_bit_exact(hip):
     import torch
-    # up to 64 experts; the last case takes five 1024-route chunks (4400 routes)
-    for seed, seq, topk, E in ((1, 37, 4, 8), (2, 300, 2, 32), (3, 5, 1, 3), (4, 700, 4, 32), (5, 1100, 4, 64)):
+    # more than 256 routes with at most 256 experts take the chunked two-kernel routing, the rest the
+    # single-workgroup kernel (chunks of 1024: the last case takes five); both must give Moe.dispatch's slots
+    for seed, seq, topk, E in ((1, 37, 4, 8), (2, 300, 2, 32), (3, 5, 1, 3), (4, 700, 4, 32), (5, 1100, 4, 64),
+                               (6, 300, 4, 16), (7, 200, 2, 300), (8, 512, 4, 256)):
         say(f"moe route seq={seq} topk={topk} E={E}")
         re = routes(seed, seq, topk, E)
         if seed == 3:
             re[2] = E + 5                        # an id outside [0, E) takes no slot
+        if seed == 6:                            # the same in the chunked form, in two different chunks
+            re[7], re[1000] = -1, E + 3
         R = seq * topk
         counts = torch.zeros(E, dtype=torch.int32, device="cuda")
         off = torch.zeros(E + 1, dtype=torch.int32, device="cuda")
@@ -57,7 +61,8 @@ def test_route_gather_combine_bit_exact(hip):
         dim = 96
         x = np.random.default_rng(seed + 10).standard_normal((seq, dim)).astype(np.float32)
         g = torch.zeros((R, dim + 3), dtype=torch.float32, device="cuda")
-        assert hip.moe_gather(dev(x).data_ptr(), dim, slot_route.data_ptr(), off.data_ptr(), E, seq, topk, dim,
+        x_dv = dev(x)   # held until the kernels that read it have run
+        assert hip.moe_gather(x_dv.data_ptr(), dim, slot_route.data_ptr(), off.data_ptr(), E, seq, topk, dim,
                               g.data_ptr(), dim + 3) == 0, hip.last_error()
         hip.synchronize()
         assert np.array_equal(g.cpu().numpy()[:total, :dim], M.gather(x, sr_o, total, topk))
@@ -65,7 +70,9 @@ def test_route_gather_combine_bit_exact(hip):
         y = np.random.default_rng(seed + 20).standard_normal((R, dim)).astype(np.float32)
         prob = np.random.default_rng(seed + 30).random(R).astype(np.float32)
         out = torch.full((seq, dim + 1), 7.0, dtype=torch.float32, device="cuda")
-        assert hip.moe_combine(dev(y).data_ptr(), dim, re_d.data_ptr(), dev(prob).data_ptr(), route_slot.data_ptr(),
+        y_dv = dev(y)   # held until the kernels that read it have run
+        prob_dv = dev(prob)   # held until the kernels that read it have run
+        assert hip.moe_combine(y_dv.data_ptr(), dim, re_d.data_ptr(), prob_dv.data_ptr(), route_slot.data_ptr(),
                                seq, topk, E, dim, out.data_ptr(), dim + 1) == 0, hip.last_error()
         hip.synchronize()
         want = M.combine(y, re, prob, rs_o, seq, topk, E)
@@ -75,10 +82,13 @@ def test_route_gather_combine_bit_exact(hip):
 
         # contiguous 16-byte-aligned rows (the four-wide copy and fma paths)
         g4 = torch.zeros((R, dim), dtype=torch.float32, device="cuda")
-        assert hip.moe_gather(dev(x).data_ptr(), dim, slot_route.data_ptr(), off.data_ptr(), E, seq, topk, dim,
+        x_dv = dev(x)   # held until the kernels that read it have run
+        assert hip.moe_gather(x_dv.data_ptr(), dim, slot_route.data_ptr(), off.data_ptr(), E, seq, topk, dim,
                               g4.data_ptr(), dim) == 0, hip.last_error()
         out4 = torch.zeros((seq, dim), dtype=torch.float32, device="cuda")
-        assert hip.moe_combine(dev(y).data_ptr(), dim, re_d.data_ptr(), dev(prob).data_ptr(), route_slot.data_ptr(),
+        y_dv = dev(y)   # held until the kernels that read it have run
+        prob_dv = dev(prob)   # held until the kernels that read it have run
+        assert hip.moe_combine(y_dv.data_ptr(), dim, re_d.data_ptr(), prob_dv.data_ptr(), route_slot.data_ptr(),
                                seq, topk, E, dim, out4.data_ptr(), dim) == 0, hip.last_error()
         hip.synchronize()
         assert np.array_equal(g4.cpu().numpy()[:total], M.gather(x, sr_o, total, topk))
@@ -150,8 +160,11 @@ def test_mm_grouped_counts_past_rows_cap(hip, oracle):
     try:
         c = torch.full((rows_cap, m), -3.0, dtype=torch.float32, device="cuda")
         off = torch.zeros(E + 1, dtype=torch.int32, device="cuda")
-        assert hip.mm_grouped(Segment.of(w), dt, k, m, E, dev(np.array(counts, np.int32)).data_ptr(),
-                              dev(a).data_ptr(), k, c.data_ptr(), m, k, rows_cap, off.data_ptr()) == JAM.OK
+        a_dv = dev(a)   # held until the kernels that read it have run
+        counts_dv = dev(np.array(counts, np.int32))
+        torch.cuda.synchronize()   # torch's fills run on its own stream
+        assert hip.mm_grouped(Segment.of(w), dt, k, m, E, counts_dv.data_ptr(),
+                              a_dv.data_ptr(), k, c.data_ptr(), m, k, rows_cap, off.data_ptr()) == JAM.OK
         hip.synchronize()
         assert off.cpu().numpy().tolist() == [0, 10, 45, 45]
         ref = M.mm_grouped(oracle, dt, w_e, a, [10, 35, 0], m, k)
