@@ -31,6 +31,37 @@ struct Groups {
     const float* bias = nullptr;   // per-expert bias [E][gm] added in the store (expert e at bias + e·gm)
 };
 
+// Matrix-core GEMM workgroup -> linear tile; workgroup b runs on XCD b % 8. Ungrouped: each XCD takes one
+// contiguous run of tiles (a row block's token blocks share its L2). Grouped: runs of GCH consecutive
+// expert-major tiles are dealt to the XCDs in turn, so each XCD gets a share of every expert (their tiles
+// differ in cost: an expert's last slot block may be half empty) while a run keeps its weight rows and
+// activation slots in one L2. tile_grid is the launch size that covers every tile.
+constexpr int GCH = 16;
+JAMHIP_DEV int tile_of_block(bool grouped, int total) {
+    const int b = (int) blockIdx.x, x = b % 8, i = b / 8;
+    if (grouped) return ((i / GCH) * 8 + x) * GCH + i % GCH;
+    return x * ((total + 7) / 8) + i;
+}
+inline int tile_grid(bool grouped, int total) {
+    return grouped ? (total + 8 * GCH - 1) / (8 * GCH) * (8 * GCH) : (total + 7) / 8 * 8;
+}
+
+// Grouped matrix-core GEMMs: linear workgroup `lin` of nrb row blocks x the 64-slot blocks -> (row block,
+// slot block) in expert-major order. Expert e's slot blocks [cbs, cbs + ns) own the linear range
+// [nrb·cbs, nrb·(cbs + ns)), row block-major inside it, so workgroups placed next to each other (one XCD
+// takes a contiguous run) share the expert's weight rows and its activation slots stay in that XCD's L2.
+// Returns the expert, or -1 for a slot block past the last expert's.
+JAMHIP_DEV int grouped_tile(const Groups& gp, int lin, int nrb, int* rb, int* cb) {
+    const int e = __builtin_amdgcn_readfirstlane(gp.map64[lin / nrb]);
+    if (e < 0) return -1;
+    const int p = __builtin_amdgcn_readfirstlane(gp.poff64[e]), cbs = p / 64;
+    const int ns = (__builtin_amdgcn_readfirstlane(gp.poff64[e + 1]) - p) / 64;   // >= 1: e owns slot block lin / nrb
+    const int l = lin - nrb * cbs;
+    *rb = l / ns;
+    *cb = cbs + l % ns;
+    return e;
+}
+
 // flavour 3: any n, F1 activations read from A in 8-token tiles (NVFP4, whose only jam kernel is F1 at
 // every n). flavour 1: n in [1, 7], F1 activations; with `a` non-null the kernel quantizes A itself (requires
 // gemv_fusable(n, k)), else it reads A's quantized copy from `A`. flavour 2: any n >= 1, F2

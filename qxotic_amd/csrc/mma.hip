@@ -32,6 +32,7 @@
 #include "launch.h"
 
 #include <atomic>
+#include <type_traits>
 
 namespace jamhip {
 
@@ -125,12 +126,12 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
     extern __shared__ __align__(1024) unsigned char smem[];
     __shared__ float q40_srow[DT == Q4_0 || DT == Q8_0 ? MMA_WAVES * RT * 32 : 1];   // 2^-s of each row
 
-    // XCD-aware placement: workgroup id i runs on XCD i % 8; give each XCD a contiguous run of
-    // (row block, token block) pairs so a row block's token blocks share one L2.
-    const int total = nrb * ncb, per = (total + 7) / 8;
-    const int lin = (int) (blockIdx.x % 8) * per + (int) (blockIdx.x / 8);
+    // XCD-aware placement (tile_of_block); grouped calls take their tiles in expert-major order
+    const int total = nrb * ncb;
+    const int lin = tile_of_block(gp.map64 != nullptr, total);
     if (lin >= total) return;
-    const int rb = lin / ncb, cb = lin % ncb;
+    int rb = lin / ncb, cb = lin % ncb;
+    if (gp.map64 != nullptr && grouped_tile(gp, lin, nrb, &rb, &cb) < 0) return;   // before any barrier
     const int64_t T0 = (int64_t) rb * TW;        // first row tile of the workgroup
     const int n0 = cb * BN;                      // first token slot of GemmAct
 
@@ -156,6 +157,9 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
         nvalid = __builtin_amdgcn_readfirstlane(gp.off[e + 1]) - crow0;
         if (gp.bias != nullptr) ep.bias = gp.bias + (int64_t) e * gp.gm;
     }
+    // valid tokens of this slot block all in its first 32 slots: the second token tile is neither copied
+    // nor computed (its columns are never stored)
+    const bool half = CT == 2 && nvalid - (n0 - slot0) <= 32;
 
     // ---- global -> LDS copy of one stage. Every wave issues a fixed set of 1 KB pieces: the weight chunks
     // of its own row tile, the activation codes of K-steps 2·wave and 2·wave + 1, and one of the small
@@ -202,11 +206,13 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
         // are planes [kk][half][BN tokens][16 B] so a fragment read is 512 contiguous bytes per half-wave
         // (conflict-free) and each piece copied is 1 KB contiguous
         const uint8_t* bs = b_src + (int64_t) (8 * st) * b_kstep;
+        if (!half || lane < 32) {   // lane l copies token slot n0 + l
 #pragma unroll
-        for (int kl = 0; kl < 2; kl++)
+            for (int kl = 0; kl < 2; kl++)
 #pragma unroll
-            for (int p = 0; p < 2; p++)
-                dma16(bs + kl * b_kstep + p * (b_kstep / 2), buf + S::B_OFF + (2 * (2 * wave + kl) + p) * 1024);
+                for (int p = 0; p < 2; p++)
+                    dma16(bs + kl * b_kstep + p * (b_kstep / 2), buf + S::B_OFF + (2 * (2 * wave + kl) + p) * 1024);
+        }
         if constexpr (DT != Q6_K) {
             if (wave < 2) dma16(h_src + (int64_t) g * 32 * 16, buf + S::H_OFF + wave * 1024);
         } else {
@@ -241,452 +247,461 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
 
-    for (int st = st0; st < nst; st++) {
-        unsigned char* buf = smem + (st & 1) * S::BYTES;
-        // each type issues the next stage's copy itself, after its last LDS read of this stage: the compiler
-        // makes any LDS read that follows a global -> LDS copy wait for that copy
-        const int h2 = st & 1;
-        const unsigned char* LA = buf + S::A_OFF;
-        const unsigned char* LB = buf + S::B_OFF;
-        const float* LDX = reinterpret_cast<const float*>(buf + S::DX_OFF);
+    // the stage loop for CA active token tiles: a slot block whose valid tokens all fall in its first
+    // 32 (an expert's or the call's last block) runs only the first tile's fragments and products
+    auto run = [&](auto ca) {
+        constexpr int CA = decltype(ca)::value;
+        for (int st = st0; st < nst; st++) {
+            unsigned char* buf = smem + (st & 1) * S::BYTES;
+            // each type issues the next stage's copy itself, after its last LDS read of this stage: the compiler
+            // makes any LDS read that follows a global -> LDS copy wait for that copy
+            const int h2 = st & 1;
+            const unsigned char* LA = buf + S::A_OFF;
+            const unsigned char* LB = buf + S::B_OFF;
+            const float* LDX = reinterpret_cast<const float*>(buf + S::DX_OFF);
 
-        if constexpr (DT == Q4_K) {   // accs starts at zero and is cleared where it is consumed
-            uint4 hdr[RT];
-            uint32_t scs[RT];   // the stage's 4 sub-block scales (6-bit), one per byte
-#pragma unroll
-            for (int i = 0; i < RT; i++) {
-                hdr[i] = *reinterpret_cast<const uint4*>(buf + S::H_OFF + ((wave * RT + i) * 32 + r) * 16);
-                // jam_kquant.h:26-33: sub-blocks 0-3 scale = byte & 63; 4-7 = low nibble of bytes 8-11 with
-                // the top 2 bits of bytes 0-3
-                scs[i] = h2 == 0 ? hdr[i].y & 0x3F3F3F3Fu
-                                 : (hdr[i].w & 0x0F0F0F0Fu) | ((hdr[i].y >> 2) & 0x30303030u);
-            }
-            // every LDS read of the stage up front (the wave then works down an in-order queue)
-            uint4 chs[2][RT];
-            half8 bfs[4][CT][2];
-            float dxs[4][CT];
-#pragma unroll
-            for (int gpl = 0; gpl < 2; gpl++)
-#pragma unroll
-                for (int i = 0; i < RT; i++)
-                    chs[gpl][i] = *reinterpret_cast<const uint4*>(LA + ((wave * RT + i) * NCS + 2 * gpl + q) * 512 + 16 * r);
-#pragma unroll
-            for (int bl = 0; bl < 4; bl++)
-#pragma unroll
-                for (int j = 0; j < CT; j++) {
-#pragma unroll
-                    for (int ks = 0; ks < 2; ks++)
-                        bfs[bl][j][ks] = *reinterpret_cast<const half8*>(LB + ((2 * bl + ks) * 2 + q) * BN * 16 + (32 * j + r) * 16);
-                    dxs[bl][j] = LDX[bl * BN + 32 * j + r];
-                }
-            // super-block end (odd stage): d of the 16 output rows this lane holds, and the sums' fragments
-            float dds[RT][16];
-            half4 shi[CT], slo[CT];
-            if (h2 == 1) {
-#pragma unroll
+            if constexpr (DT == Q4_K) {   // accs starts at zero and is cleared where it is consumed
+                uint4 hdr[RT];
+                uint32_t scs[RT];   // the stage's 4 sub-block scales (6-bit), one per byte
+    #pragma unroll
                 for (int i = 0; i < RT; i++) {
-                    const unsigned char* H = buf + S::H_OFF + (wave * RT + i) * 32 * 16;
-#pragma unroll
-                    for (int e = 0; e < 16; e++)
-                        dds[i][e] = h2f_bits(*reinterpret_cast<const uint16_t*>(H + (8 * (e >> 2) + 4 * q + (e & 3)) * 16));
+                    hdr[i] = *reinterpret_cast<const uint4*>(buf + S::H_OFF + ((wave * RT + i) * 32 + r) * 16);
+                    // jam_kquant.h:26-33: sub-blocks 0-3 scale = byte & 63; 4-7 = low nibble of bytes 8-11 with
+                    // the top 2 bits of bytes 0-3
+                    scs[i] = h2 == 0 ? hdr[i].y & 0x3F3F3F3Fu
+                                     : (hdr[i].w & 0x0F0F0F0Fu) | ((hdr[i].y >> 2) & 0x30303030u);
                 }
-#pragma unroll
-                for (int j = 0; j < CT; j++) {
-                    const unsigned char* SP = buf + S::S_OFF + (32 * j + r) * 16 + 8 * q;
-                    shi[j] = *reinterpret_cast<const half4*>(SP);
-                    slo[j] = *reinterpret_cast<const half4*>(SP + BN * 16);
-                }
-            }
-            __builtin_amdgcn_sched_barrier(0);   // keep the reads ahead of the compute
-            // this stage's LDS reads are all issued: start copying the next stage into the other buffer
-            if (st + 1 < nst) issue(st + 1, smem + ((st + 1) & 1) * S::BYTES);
-            // Software pipeline over the stage's 4 blocks: block bl's products go out on the matrix cores into
-            // D[bl & 1] before block bl-1's scale FMAs, which then run while the matrix cores work.
-            floatx16 Dp[2][RT][CT];
-#pragma unroll
-            for (int bl = 0; bl < 5; bl++) {
-                if (bl < 4) {
-                    const uint4* ch = chs[bl >> 1];
-                    const int sub = bl & 1;
-                    half8 af[RT][2];
-#pragma unroll
-                    for (int i = 0; i < RT; i++) {
-                        // lo nibble: (1024 + v)·sc − 1024·sc; hi nibble (bits 4-7): (1024 + 16v)·sc/16 − 64·sc
-                        const uint32_t sc = (scs[i] >> (8 * bl)) & 0xffu;
-                        const uint32_t dup = sc | (sc << 16) | 0x64006400u;   // f16 pair (1024 + sc, 1024 + sc)
-                        const half2v one = __builtin_bit_cast(half2v, dup) - __builtin_bit_cast(half2v, 0x64006400u);
-                        const half2v mulv = sub ? one * (_Float16) 0.0625f : one;
-                        const half2v addv = one * (sub ? (_Float16) -64.0f : (_Float16) -1024.0f);
-                        const uint32_t mul = __builtin_bit_cast(uint32_t, mulv), add = __builtin_bit_cast(uint32_t, addv);
-                        const uint32_t mask = sub ? vmask_hi : vmask_lo;
-                        af[i][0] = frag8(ch[i].x, ch[i].y, mask, mul, add);
-                        af[i][1] = frag8(ch[i].z, ch[i].w, mask, mul, add);
-                    }
-#pragma unroll
+                // every LDS read of the stage up front (the wave then works down an in-order queue)
+                uint4 chs[2][RT];
+                half8 bfs[4][CT][2];
+                float dxs[4][CT];
+    #pragma unroll
+                for (int gpl = 0; gpl < 2; gpl++)
+    #pragma unroll
                     for (int i = 0; i < RT; i++)
-#pragma unroll
-                        for (int j = 0; j < CT; j++) {
-                            floatx16 D = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i][0], bfs[bl][j][0], floatx16{}, 0, 0, 0);
-                            Dp[bl & 1][i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i][1], bfs[bl][j][1], D, 0, 0, 0);
-                        }
-                }
-                if (bl > 0) {
-                    const int pb = bl - 1;
-#pragma unroll
-                    for (int i = 0; i < RT; i++)
-#pragma unroll
-                        for (int j = 0; j < CT; j++)
-#pragma unroll
-                            for (int e = 0; e < 16; e++)
-                                accs[i][j][e] = fmaf(Dp[pb & 1][i][j][e], dxs[pb][j], accs[i][j][e]);
-                }
-            }
-            if (h2 == 1) {   // super-block end: d, then the mins on the matrix cores
-#pragma unroll
-                for (int i = 0; i < RT; i++) {
-#pragma unroll
-                    for (int j = 0; j < CT; j++) {
-#pragma unroll
-                        for (int e = 0; e < 16; e++) acc[i][j][e] = fmaf(dds[i][e], accs[i][j][e], acc[i][j][e]);
-                        accs[i][j] = floatx16{};
-                    }
-                    // A' = −dmin·mn_s for sub-blocks 4q..4q+3 of row r, split hi + lo
-                    const float dmin = h2f_bits(hdr[i].x >> 16);
-                    half4 ahi, alo;
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        int sc, mn;
-                        q4k_scmn(hdr[i], 4 * q + e, sc, mn);
-                        const F16Pair p = split_f16(-(dmin * (float) mn));
-                        ahi[e] = p.hi;
-                        alo[e] = p.lo;
-                    }
-#pragma unroll
-                    for (int j = 0; j < CT; j++) {
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(ahi, shi[j], acc[i][j], 0, 0, 0);
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(ahi, slo[j], acc[i][j], 0, 0, 0);
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(alo, shi[j], acc[i][j], 0, 0, 0);
-                    }
-                }
-            }
-        } else if constexpr (DT == Q4_0 || DT == Q8_0) {   // group of 8 blocks; stage h2 = blocks 4h2..4h2+3
-            // The weight operand is d'·code with d' = d·2^s_r (s_r per row and group: the row's largest block
-            // scale lands in [2^10, 2^11) for Q4_0's nibbles, [2^7, 2^8) for Q8_0's int8, so |d'·code| < 2^15),
-            // split exactly into f16 hi + lo (d'·code has at most 15 significant bits for Q4_0, 19 for Q8_0). Each block's dot then runs as two MFMAs per K-step,
-            // one FMA per output applies dx, and at the group end (Q4_0) −8·Σ_b d'_b·xs_b joins on the matrix
-            // cores before the 2^-s_r of each row.
-            const bool gend = h2 == 1 || st == nstk - 1;   // the last group may end after its first half
-            uint4 hdr[RT], chs[RT][4];
-            half8 bfs[4][CT][2];
-            float dxs[4][CT];
-            half4 shi[CT], slo[CT];
-#pragma unroll
-            for (int i = 0; i < RT; i++) {
-                hdr[i] = *reinterpret_cast<const uint4*>(buf + S::H_OFF + ((wave * RT + i) * 32 + r) * 16);
-#pragma unroll
-                for (int bl = 0; bl < 4; bl++) {   // Q4_0: block bl's chunk; Q8_0: its half q (elements 16q..)
-                    const int cl = DT == Q8_0 ? 2 * bl + q : bl;
-                    chs[i][bl] = *reinterpret_cast<const uint4*>(LA + ((wave * RT + i) * NCS + cl) * 512 + 16 * r);
-                }
-            }
-#pragma unroll
-            for (int bl = 0; bl < 4; bl++)
-#pragma unroll
-                for (int j = 0; j < CT; j++) {
-#pragma unroll
-                    for (int ks = 0; ks < 2; ks++)
-                        bfs[bl][j][ks] = *reinterpret_cast<const half8*>(LB + ((2 * bl + ks) * 2 + q) * BN * 16 + (32 * j + r) * 16);
-                    dxs[bl][j] = LDX[bl * BN + 32 * j + r];
-                }
-            if (DT == Q4_0 && gend) {
-#pragma unroll
-                for (int j = 0; j < CT; j++) {
-                    const unsigned char* SP = buf + S::S_OFF + (32 * j + r) * 16 + 8 * q;
-                    shi[j] = *reinterpret_cast<const half4*>(SP);
-                    slo[j] = *reinterpret_cast<const half4*>(SP + BN * 16);
-                }
-            }
-            __builtin_amdgcn_sched_barrier(0);
-            if (st + 1 < nst) issue(st + 1, smem + ((st + 1) & 1) * S::BYTES);
-            // s_r of row r from its 8 block scales (f16 exponent fields); 2^-s_r goes to LDS at the group's
-            // first stage for the lanes that hold row r's outputs
-            int sr[RT];
-            // d'_b = d_b·2^s_r of block b of the group, exact in f32 and (above 2^-14) in f16
-            auto dq = [&](int i, int b) { return ldexpf(h2f_bits(word(hdr[i], b >> 1) >> (16 * (b & 1))), sr[i]); };
-#pragma unroll
-            for (int i = 0; i < RT; i++) {
-                const uint32_t e01 = max(hdr[i].x & 0x7C00u, (hdr[i].x >> 16) & 0x7C00u);
-                const uint32_t e23 = max(hdr[i].y & 0x7C00u, (hdr[i].y >> 16) & 0x7C00u);
-                const uint32_t e45 = max(hdr[i].z & 0x7C00u, (hdr[i].z >> 16) & 0x7C00u);
-                const uint32_t e67 = max(hdr[i].w & 0x7C00u, (hdr[i].w >> 16) & 0x7C00u);
-                const int emax = (int) (max(max(e01, e23), max(e45, e67)) >> 10);   // biased exponent, 0..31
-                sr[i] = (DT == Q8_0 ? 22 : 25) - emax;   // |d'·code| < 2^15 (f16 range)
-                if (h2 == 0 && q == 0) q40_srow[(wave * RT + i) * 32 + r] = ldexpf(1.0f, -sr[i]);
-            }
-            floatx16 Dp[2][RT][CT];
-#pragma unroll
-            for (int bl = 0; bl < 5; bl++) {
-                if (bl < 4) {
-                    half8 ah[RT][2], al[RT][2];
-#pragma unroll
-                    for (int i = 0; i < RT; i++) {
-                        const uint4 ch = chs[i][bl];
-                        const float df = dq(i, 4 * h2 + bl);
-                        const _Float16 dh = (_Float16) df;
-                        const half2v d2 = {dh, dh};
-                        half8 v0, v1;   // the codes as exact f16
-                        if constexpr (DT == Q4_0) {   // lane half q takes the low (elements 0-15) or high nibbles
-                            const uint32_t mask = q ? vmask_hi : vmask_lo;
-                            const uint32_t mul = q ? 0x2C002C00u : 0x3C003C00u;   // f16 pairs (1/16, 1/16) or (1, 1)
-                            const uint32_t add = q ? 0xD400D400u : 0xE400E400u;   // (-64, -64) or (-1024, -1024)
-                            v0 = frag8(ch.x, ch.y, mask, mul, add);
-                            v1 = frag8(ch.z, ch.w, mask, mul, add);
-                        } else {   // int8 ^ 0x80 = q + 128, as the f16 1024 + q + 128, minus 1152
-                            v0 = frag8(ch.x ^ 0x80808080u, ch.y ^ 0x80808080u, vmask_b, 0x3C003C00u, 0xE480E480u);
-                            v1 = frag8(ch.z ^ 0x80808080u, ch.w ^ 0x80808080u, vmask_b, 0x3C003C00u, 0xE480E480u);
-                        }
-#pragma unroll
-                        for (int e = 0; e < 8; e += 2) {
-                            const half2v a0 = {v0[e], v0[e + 1]}, a1 = {v1[e], v1[e + 1]};
-                            const half2v h0 = a0 * d2, h1 = a1 * d2;
-                            const half2v l0 = __builtin_elementwise_fma(a0, d2, -h0), l1 = __builtin_elementwise_fma(a1, d2, -h1);
-                            ah[i][0][e] = h0[0], ah[i][0][e + 1] = h0[1], ah[i][1][e] = h1[0], ah[i][1][e + 1] = h1[1];
-                            al[i][0][e] = l0[0], al[i][0][e + 1] = l0[1], al[i][1][e] = l1[0], al[i][1][e + 1] = l1[1];
-                        }
-                    }
-#pragma unroll
-                    for (int i = 0; i < RT; i++)
-#pragma unroll
-                        for (int j = 0; j < CT; j++) {
-                            floatx16 D = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i][0], bfs[bl][j][0], floatx16{}, 0, 0, 0);
-                            D = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i][0], bfs[bl][j][0], D, 0, 0, 0);
-                            D = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i][1], bfs[bl][j][1], D, 0, 0, 0);
-                            Dp[bl & 1][i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i][1], bfs[bl][j][1], D, 0, 0, 0);
-                        }
-                }
-                if (bl > 0) {
-                    const int pb = bl - 1;
-#pragma unroll
-                    for (int i = 0; i < RT; i++)
-#pragma unroll
-                        for (int j = 0; j < CT; j++)
-#pragma unroll
-                            for (int e = 0; e < 16; e++)
-                                accs[i][j][e] = fmaf(Dp[pb & 1][i][j][e], dxs[pb][j], accs[i][j][e]);
-                }
-            }
-            if (gend) {   // group end: (Q4_0) accs −= 8·Σ_b d'_b·xs_b (hi + lo of the sums), then acc += 2^-s · accs
-                if (h2 == 0) __syncthreads();   // 2^-s of this stage's group was written above
-#pragma unroll
-                for (int i = 0; i < RT; i++) {
-                    if constexpr (DT == Q4_0) {
-                        half4 a8;   // −8·d'_b for blocks 4q..4q+3 of row r (exact: d'_b < 2^11)
-#pragma unroll
-                        for (int e = 0; e < 4; e++) a8[e] = (_Float16) (-8.0f * dq(i, 4 * q + e));
-#pragma unroll
-                        for (int j = 0; j < CT; j++) {
-                            accs[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(a8, shi[j], accs[i][j], 0, 0, 0);
-                            accs[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(a8, slo[j], accs[i][j], 0, 0, 0);
-                        }
-                    }
-                    const float* SR = q40_srow + (wave * RT + i) * 32;
-#pragma unroll
-                    for (int j = 0; j < CT; j++) {
-#pragma unroll
-                        for (int e = 0; e < 16; e++)
-                            acc[i][j][e] = fmaf(SR[8 * (e >> 2) + 4 * q + (e & 3)], accs[i][j][e], acc[i][j][e]);
-                        accs[i][j] = floatx16{};
-                    }
-                }
-            }
-        } else if constexpr (DT == MXFP4) {   // group of 8 blocks; stage h2 = blocks 4h2..4h2+3
-            // every LDS read of the stage up front, then the next stage's copy, then the compute
-            uint4 hdr[RT], chs[RT][4];
-            half8 bfs[4][CT][2];
-            float dxs[4][CT];
-            float sg[RT][16];
-#pragma unroll
-            for (int i = 0; i < RT; i++) {
-                hdr[i] = *reinterpret_cast<const uint4*>(buf + S::H_OFF + ((wave * RT + i) * 32 + r) * 16);
-#pragma unroll
+                        chs[gpl][i] = *reinterpret_cast<const uint4*>(LA + ((wave * RT + i) * NCS + 2 * gpl + q) * 512 + 16 * r);
+    #pragma unroll
                 for (int bl = 0; bl < 4; bl++)
-                    chs[i][bl] = *reinterpret_cast<const uint4*>(LA + ((wave * RT + i) * NCS + bl) * 512 + 16 * r);
-            }
-#pragma unroll
-            for (int bl = 0; bl < 4; bl++)
-#pragma unroll
-                for (int j = 0; j < CT; j++) {
-#pragma unroll
-                    for (int ks = 0; ks < 2; ks++)
-                        bfs[bl][j][ks] = *reinterpret_cast<const half8*>(LB + ((2 * bl + ks) * 2 + q) * BN * 16 + (32 * j + r) * 16);
-                    dxs[bl][j] = LDX[bl * BN + 32 * j + r];
-                }
-            const bool gend = h2 == 1 || st == nstk - 1;   // the last group may end after its first half
-            if (gend) {   // group end: 2^(e_ref - 128) of the 16 output rows this lane holds
-#pragma unroll
-                for (int i = 0; i < RT; i++) {
-                    const unsigned char* H = buf + S::H_OFF + (wave * RT + i) * 32 * 16;
-#pragma unroll
-                    for (int e = 0; e < 16; e++) sg[i][e] = e8m0_half(H[(8 * (e >> 2) + 4 * q + (e & 3)) * 16 + 8]);
-                }
-            }
-            __builtin_amdgcn_sched_barrier(0);
-            if (st + 1 < nst) issue(st + 1, smem + ((st + 1) & 1) * S::BYTES);
-            // software pipeline: block bl's products go out before block bl-1's scale FMAs
-            floatx16 Dp[2][RT][CT];
-#pragma unroll
-            for (int bl = 0; bl < 5; bl++) {
-                if (bl < 4) {
-                    half8 af[RT][2];
-#pragma unroll
-                    for (int i = 0; i < RT; i++) {
-                        const uint4 ch = chs[i][bl];
-                        const int b = 4 * h2 + bl;
-                        const int eb = (int) (((b < 4 ? hdr[i].x : hdr[i].y) >> (8 * (b & 3))) & 0xffu);
-                        const int er = (int) (hdr[i].z & 0xffu);
-                        const int ex = eb - er + 128;   // biased exponent of 2^(eb - er + 1); below 2^-126: 0
-                        const float scale = ex > 0 ? __builtin_bit_cast(float, (uint32_t) ex << 23) : 0.0f;
-                        // lane half q takes bytes 8q..8q+7 of the block: K-step 0 word 2q, K-step 1 word 2q + 1
-                        af[i][0] = mx_frag(q ? ch.z : ch.x, scale);
-                        af[i][1] = mx_frag(q ? ch.w : ch.y, scale);
+    #pragma unroll
+                    for (int j = 0; j < CA; j++) {
+    #pragma unroll
+                        for (int ks = 0; ks < 2; ks++)
+                            bfs[bl][j][ks] = *reinterpret_cast<const half8*>(LB + ((2 * bl + ks) * 2 + q) * BN * 16 + (32 * j + r) * 16);
+                        dxs[bl][j] = LDX[bl * BN + 32 * j + r];
                     }
-#pragma unroll
+                // super-block end (odd stage): d of the 16 output rows this lane holds, and the sums' fragments
+                float dds[RT][16];
+                half4 shi[CT], slo[CT];
+                if (h2 == 1) {
+    #pragma unroll
+                    for (int i = 0; i < RT; i++) {
+                        const unsigned char* H = buf + S::H_OFF + (wave * RT + i) * 32 * 16;
+    #pragma unroll
+                        for (int e = 0; e < 16; e++)
+                            dds[i][e] = h2f_bits(*reinterpret_cast<const uint16_t*>(H + (8 * (e >> 2) + 4 * q + (e & 3)) * 16));
+                    }
+    #pragma unroll
+                    for (int j = 0; j < CA; j++) {
+                        const unsigned char* SP = buf + S::S_OFF + (32 * j + r) * 16 + 8 * q;
+                        shi[j] = *reinterpret_cast<const half4*>(SP);
+                        slo[j] = *reinterpret_cast<const half4*>(SP + BN * 16);
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);   // keep the reads ahead of the compute
+                // this stage's LDS reads are all issued: start copying the next stage into the other buffer
+                if (st + 1 < nst) issue(st + 1, smem + ((st + 1) & 1) * S::BYTES);
+                // Software pipeline over the stage's 4 blocks: block bl's products go out on the matrix cores into
+                // D[bl & 1] before block bl-1's scale FMAs, which then run while the matrix cores work.
+                floatx16 Dp[2][RT][CT];
+    #pragma unroll
+                for (int bl = 0; bl < 5; bl++) {
+                    if (bl < 4) {
+                        const uint4* ch = chs[bl >> 1];
+                        const int sub = bl & 1;
+                        half8 af[RT][2];
+    #pragma unroll
+                        for (int i = 0; i < RT; i++) {
+                            // lo nibble: (1024 + v)·sc − 1024·sc; hi nibble (bits 4-7): (1024 + 16v)·sc/16 − 64·sc
+                            const uint32_t sc = (scs[i] >> (8 * bl)) & 0xffu;
+                            const uint32_t dup = sc | (sc << 16) | 0x64006400u;   // f16 pair (1024 + sc, 1024 + sc)
+                            const half2v one = __builtin_bit_cast(half2v, dup) - __builtin_bit_cast(half2v, 0x64006400u);
+                            const half2v mulv = sub ? one * (_Float16) 0.0625f : one;
+                            const half2v addv = one * (sub ? (_Float16) -64.0f : (_Float16) -1024.0f);
+                            const uint32_t mul = __builtin_bit_cast(uint32_t, mulv), add = __builtin_bit_cast(uint32_t, addv);
+                            const uint32_t mask = sub ? vmask_hi : vmask_lo;
+                            af[i][0] = frag8(ch[i].x, ch[i].y, mask, mul, add);
+                            af[i][1] = frag8(ch[i].z, ch[i].w, mask, mul, add);
+                        }
+    #pragma unroll
+                        for (int i = 0; i < RT; i++)
+    #pragma unroll
+                            for (int j = 0; j < CA; j++) {
+                                floatx16 D = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i][0], bfs[bl][j][0], floatx16{}, 0, 0, 0);
+                                Dp[bl & 1][i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i][1], bfs[bl][j][1], D, 0, 0, 0);
+                            }
+                    }
+                    if (bl > 0) {
+                        const int pb = bl - 1;
+    #pragma unroll
+                        for (int i = 0; i < RT; i++)
+    #pragma unroll
+                            for (int j = 0; j < CA; j++)
+    #pragma unroll
+                                for (int e = 0; e < 16; e++)
+                                    accs[i][j][e] = fmaf(Dp[pb & 1][i][j][e], dxs[pb][j], accs[i][j][e]);
+                    }
+                }
+                if (h2 == 1) {   // super-block end: d, then the mins on the matrix cores
+    #pragma unroll
+                    for (int i = 0; i < RT; i++) {
+    #pragma unroll
+                        for (int j = 0; j < CA; j++) {
+    #pragma unroll
+                            for (int e = 0; e < 16; e++) acc[i][j][e] = fmaf(dds[i][e], accs[i][j][e], acc[i][j][e]);
+                            accs[i][j] = floatx16{};
+                        }
+                        // A' = −dmin·mn_s for sub-blocks 4q..4q+3 of row r, split hi + lo
+                        const float dmin = h2f_bits(hdr[i].x >> 16);
+                        half4 ahi, alo;
+    #pragma unroll
+                        for (int e = 0; e < 4; e++) {
+                            int sc, mn;
+                            q4k_scmn(hdr[i], 4 * q + e, sc, mn);
+                            const F16Pair p = split_f16(-(dmin * (float) mn));
+                            ahi[e] = p.hi;
+                            alo[e] = p.lo;
+                        }
+    #pragma unroll
+                        for (int j = 0; j < CA; j++) {
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(ahi, shi[j], acc[i][j], 0, 0, 0);
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(ahi, slo[j], acc[i][j], 0, 0, 0);
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(alo, shi[j], acc[i][j], 0, 0, 0);
+                        }
+                    }
+                }
+            } else if constexpr (DT == Q4_0 || DT == Q8_0) {   // group of 8 blocks; stage h2 = blocks 4h2..4h2+3
+                // The weight operand is d'·code with d' = d·2^s_r (s_r per row and group: the row's largest block
+                // scale lands in [2^10, 2^11) for Q4_0's nibbles, [2^7, 2^8) for Q8_0's int8, so |d'·code| < 2^15),
+                // split exactly into f16 hi + lo (d'·code has at most 15 significant bits for Q4_0, 19 for Q8_0). Each block's dot then runs as two MFMAs per K-step,
+                // one FMA per output applies dx, and at the group end (Q4_0) −8·Σ_b d'_b·xs_b joins on the matrix
+                // cores before the 2^-s_r of each row.
+                const bool gend = h2 == 1 || st == nstk - 1;   // the last group may end after its first half
+                uint4 hdr[RT], chs[RT][4];
+                half8 bfs[4][CT][2];
+                float dxs[4][CT];
+                half4 shi[CT], slo[CT];
+    #pragma unroll
+                for (int i = 0; i < RT; i++) {
+                    hdr[i] = *reinterpret_cast<const uint4*>(buf + S::H_OFF + ((wave * RT + i) * 32 + r) * 16);
+    #pragma unroll
+                    for (int bl = 0; bl < 4; bl++) {   // Q4_0: block bl's chunk; Q8_0: its half q (elements 16q..)
+                        const int cl = DT == Q8_0 ? 2 * bl + q : bl;
+                        chs[i][bl] = *reinterpret_cast<const uint4*>(LA + ((wave * RT + i) * NCS + cl) * 512 + 16 * r);
+                    }
+                }
+    #pragma unroll
+                for (int bl = 0; bl < 4; bl++)
+    #pragma unroll
+                    for (int j = 0; j < CA; j++) {
+    #pragma unroll
+                        for (int ks = 0; ks < 2; ks++)
+                            bfs[bl][j][ks] = *reinterpret_cast<const half8*>(LB + ((2 * bl + ks) * 2 + q) * BN * 16 + (32 * j + r) * 16);
+                        dxs[bl][j] = LDX[bl * BN + 32 * j + r];
+                    }
+                if (DT == Q4_0 && gend) {
+    #pragma unroll
+                    for (int j = 0; j < CA; j++) {
+                        const unsigned char* SP = buf + S::S_OFF + (32 * j + r) * 16 + 8 * q;
+                        shi[j] = *reinterpret_cast<const half4*>(SP);
+                        slo[j] = *reinterpret_cast<const half4*>(SP + BN * 16);
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                if (st + 1 < nst) issue(st + 1, smem + ((st + 1) & 1) * S::BYTES);
+                // s_r of row r from its 8 block scales (f16 exponent fields); 2^-s_r goes to LDS at the group's
+                // first stage for the lanes that hold row r's outputs
+                int sr[RT];
+                // d'_b = d_b·2^s_r of block b of the group, exact in f32 and (above 2^-14) in f16
+                auto dq = [&](int i, int b) { return ldexpf(h2f_bits(word(hdr[i], b >> 1) >> (16 * (b & 1))), sr[i]); };
+    #pragma unroll
+                for (int i = 0; i < RT; i++) {
+                    const uint32_t e01 = max(hdr[i].x & 0x7C00u, (hdr[i].x >> 16) & 0x7C00u);
+                    const uint32_t e23 = max(hdr[i].y & 0x7C00u, (hdr[i].y >> 16) & 0x7C00u);
+                    const uint32_t e45 = max(hdr[i].z & 0x7C00u, (hdr[i].z >> 16) & 0x7C00u);
+                    const uint32_t e67 = max(hdr[i].w & 0x7C00u, (hdr[i].w >> 16) & 0x7C00u);
+                    const int emax = (int) (max(max(e01, e23), max(e45, e67)) >> 10);   // biased exponent, 0..31
+                    sr[i] = (DT == Q8_0 ? 22 : 25) - emax;   // |d'·code| < 2^15 (f16 range)
+                    if (h2 == 0 && q == 0) q40_srow[(wave * RT + i) * 32 + r] = ldexpf(1.0f, -sr[i]);
+                }
+                floatx16 Dp[2][RT][CT];
+    #pragma unroll
+                for (int bl = 0; bl < 5; bl++) {
+                    if (bl < 4) {
+                        half8 ah[RT][2], al[RT][2];
+    #pragma unroll
+                        for (int i = 0; i < RT; i++) {
+                            const uint4 ch = chs[i][bl];
+                            const float df = dq(i, 4 * h2 + bl);
+                            const _Float16 dh = (_Float16) df;
+                            const half2v d2 = {dh, dh};
+                            half8 v0, v1;   // the codes as exact f16
+                            if constexpr (DT == Q4_0) {   // lane half q takes the low (elements 0-15) or high nibbles
+                                const uint32_t mask = q ? vmask_hi : vmask_lo;
+                                const uint32_t mul = q ? 0x2C002C00u : 0x3C003C00u;   // f16 pairs (1/16, 1/16) or (1, 1)
+                                const uint32_t add = q ? 0xD400D400u : 0xE400E400u;   // (-64, -64) or (-1024, -1024)
+                                v0 = frag8(ch.x, ch.y, mask, mul, add);
+                                v1 = frag8(ch.z, ch.w, mask, mul, add);
+                            } else {   // int8 ^ 0x80 = q + 128, as the f16 1024 + q + 128, minus 1152
+                                v0 = frag8(ch.x ^ 0x80808080u, ch.y ^ 0x80808080u, vmask_b, 0x3C003C00u, 0xE480E480u);
+                                v1 = frag8(ch.z ^ 0x80808080u, ch.w ^ 0x80808080u, vmask_b, 0x3C003C00u, 0xE480E480u);
+                            }
+    #pragma unroll
+                            for (int e = 0; e < 8; e += 2) {
+                                const half2v a0 = {v0[e], v0[e + 1]}, a1 = {v1[e], v1[e + 1]};
+                                const half2v h0 = a0 * d2, h1 = a1 * d2;
+                                const half2v l0 = __builtin_elementwise_fma(a0, d2, -h0), l1 = __builtin_elementwise_fma(a1, d2, -h1);
+                                ah[i][0][e] = h0[0], ah[i][0][e + 1] = h0[1], ah[i][1][e] = h1[0], ah[i][1][e + 1] = h1[1];
+                                al[i][0][e] = l0[0], al[i][0][e + 1] = l0[1], al[i][1][e] = l1[0], al[i][1][e + 1] = l1[1];
+                            }
+                        }
+    #pragma unroll
+                        for (int i = 0; i < RT; i++)
+    #pragma unroll
+                            for (int j = 0; j < CA; j++) {
+                                floatx16 D = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i][0], bfs[bl][j][0], floatx16{}, 0, 0, 0);
+                                D = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i][0], bfs[bl][j][0], D, 0, 0, 0);
+                                D = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i][1], bfs[bl][j][1], D, 0, 0, 0);
+                                Dp[bl & 1][i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i][1], bfs[bl][j][1], D, 0, 0, 0);
+                            }
+                    }
+                    if (bl > 0) {
+                        const int pb = bl - 1;
+    #pragma unroll
+                        for (int i = 0; i < RT; i++)
+    #pragma unroll
+                            for (int j = 0; j < CA; j++)
+    #pragma unroll
+                                for (int e = 0; e < 16; e++)
+                                    accs[i][j][e] = fmaf(Dp[pb & 1][i][j][e], dxs[pb][j], accs[i][j][e]);
+                    }
+                }
+                if (gend) {   // group end: (Q4_0) accs −= 8·Σ_b d'_b·xs_b (hi + lo of the sums), then acc += 2^-s · accs
+                    if (h2 == 0) __syncthreads();   // 2^-s of this stage's group was written above
+    #pragma unroll
+                    for (int i = 0; i < RT; i++) {
+                        if constexpr (DT == Q4_0) {
+                            half4 a8;   // −8·d'_b for blocks 4q..4q+3 of row r (exact: d'_b < 2^11)
+    #pragma unroll
+                            for (int e = 0; e < 4; e++) a8[e] = (_Float16) (-8.0f * dq(i, 4 * q + e));
+    #pragma unroll
+                            for (int j = 0; j < CA; j++) {
+                                accs[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(a8, shi[j], accs[i][j], 0, 0, 0);
+                                accs[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(a8, slo[j], accs[i][j], 0, 0, 0);
+                            }
+                        }
+                        const float* SR = q40_srow + (wave * RT + i) * 32;
+    #pragma unroll
+                        for (int j = 0; j < CA; j++) {
+    #pragma unroll
+                            for (int e = 0; e < 16; e++)
+                                acc[i][j][e] = fmaf(SR[8 * (e >> 2) + 4 * q + (e & 3)], accs[i][j][e], acc[i][j][e]);
+                            accs[i][j] = floatx16{};
+                        }
+                    }
+                }
+            } else if constexpr (DT == MXFP4) {   // group of 8 blocks; stage h2 = blocks 4h2..4h2+3
+                // every LDS read of the stage up front, then the next stage's copy, then the compute
+                uint4 hdr[RT], chs[RT][4];
+                half8 bfs[4][CT][2];
+                float dxs[4][CT];
+                float sg[RT][16];
+    #pragma unroll
+                for (int i = 0; i < RT; i++) {
+                    hdr[i] = *reinterpret_cast<const uint4*>(buf + S::H_OFF + ((wave * RT + i) * 32 + r) * 16);
+    #pragma unroll
+                    for (int bl = 0; bl < 4; bl++)
+                        chs[i][bl] = *reinterpret_cast<const uint4*>(LA + ((wave * RT + i) * NCS + bl) * 512 + 16 * r);
+                }
+    #pragma unroll
+                for (int bl = 0; bl < 4; bl++)
+    #pragma unroll
+                    for (int j = 0; j < CA; j++) {
+    #pragma unroll
+                        for (int ks = 0; ks < 2; ks++)
+                            bfs[bl][j][ks] = *reinterpret_cast<const half8*>(LB + ((2 * bl + ks) * 2 + q) * BN * 16 + (32 * j + r) * 16);
+                        dxs[bl][j] = LDX[bl * BN + 32 * j + r];
+                    }
+                const bool gend = h2 == 1 || st == nstk - 1;   // the last group may end after its first half
+                if (gend) {   // group end: 2^(e_ref - 128) of the 16 output rows this lane holds
+    #pragma unroll
+                    for (int i = 0; i < RT; i++) {
+                        const unsigned char* H = buf + S::H_OFF + (wave * RT + i) * 32 * 16;
+    #pragma unroll
+                        for (int e = 0; e < 16; e++) sg[i][e] = e8m0_half(H[(8 * (e >> 2) + 4 * q + (e & 3)) * 16 + 8]);
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                if (st + 1 < nst) issue(st + 1, smem + ((st + 1) & 1) * S::BYTES);
+                // software pipeline: block bl's products go out before block bl-1's scale FMAs
+                floatx16 Dp[2][RT][CT];
+    #pragma unroll
+                for (int bl = 0; bl < 5; bl++) {
+                    if (bl < 4) {
+                        half8 af[RT][2];
+    #pragma unroll
+                        for (int i = 0; i < RT; i++) {
+                            const uint4 ch = chs[i][bl];
+                            const int b = 4 * h2 + bl;
+                            const int eb = (int) (((b < 4 ? hdr[i].x : hdr[i].y) >> (8 * (b & 3))) & 0xffu);
+                            const int er = (int) (hdr[i].z & 0xffu);
+                            const int ex = eb - er + 128;   // biased exponent of 2^(eb - er + 1); below 2^-126: 0
+                            const float scale = ex > 0 ? __builtin_bit_cast(float, (uint32_t) ex << 23) : 0.0f;
+                            // lane half q takes bytes 8q..8q+7 of the block: K-step 0 word 2q, K-step 1 word 2q + 1
+                            af[i][0] = mx_frag(q ? ch.z : ch.x, scale);
+                            af[i][1] = mx_frag(q ? ch.w : ch.y, scale);
+                        }
+    #pragma unroll
+                        for (int i = 0; i < RT; i++)
+    #pragma unroll
+                            for (int j = 0; j < CA; j++) {
+                                floatx16 D = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i][0], bfs[bl][j][0], floatx16{}, 0, 0, 0);
+                                Dp[bl & 1][i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i][1], bfs[bl][j][1], D, 0, 0, 0);
+                            }
+                    }
+                    if (bl > 0) {
+                        const int pb = bl - 1;
+    #pragma unroll
+                        for (int i = 0; i < RT; i++)
+    #pragma unroll
+                            for (int j = 0; j < CA; j++)
+    #pragma unroll
+                                for (int e = 0; e < 16; e++)
+                                    accs[i][j][e] = fmaf(Dp[pb & 1][i][j][e], dxs[pb][j], accs[i][j][e]);
+                    }
+                }
+                if (gend) {   // group end: acc += 2^(e_ref - 128) · accs
+    #pragma unroll
                     for (int i = 0; i < RT; i++)
-#pragma unroll
-                        for (int j = 0; j < CT; j++) {
-                            floatx16 D = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i][0], bfs[bl][j][0], floatx16{}, 0, 0, 0);
-                            Dp[bl & 1][i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i][1], bfs[bl][j][1], D, 0, 0, 0);
+    #pragma unroll
+                        for (int j = 0; j < CA; j++) {
+    #pragma unroll
+                            for (int e = 0; e < 16; e++) acc[i][j][e] = fmaf(sg[i][e], accs[i][j][e], acc[i][j][e]);
+                            accs[i][j] = floatx16{};
                         }
                 }
-                if (bl > 0) {
-                    const int pb = bl - 1;
-#pragma unroll
+            } else {   // Q6_K: stage h2 = half h of the super-block, blocks j = 0..3 (elements 128h + 32j + l)
+                // every LDS read of the stage up front, then the next stage's copy, then the compute
+                uint4 ql[RT][2], qh[RT];
+                int8_t scl[RT][4];
+                uint2 sco[RT];             // h2 = 0: the 8 scales of row r's 16-groups 8q..8q+7 (offset term)
+                half8 bhi[CT], blo[CT];    // h2 = 0: the sums' fragments
+                half8 bfs[4][CT][2];
+                float dxs[4][CT];
+    #pragma unroll
+                for (int i = 0; i < RT; i++) {
+                    const unsigned char* T = LA + (wave * RT + i) * NCS * 512 + 16 * r;
+                    ql[i][0] = *reinterpret_cast<const uint4*>(T + (0 + q) * 512);
+                    ql[i][1] = *reinterpret_cast<const uint4*>(T + (2 + q) * 512);
+                    qh[i] = *reinterpret_cast<const uint4*>(T + (4 + q) * 512);
+                    const int8_t* sc16 = reinterpret_cast<const int8_t*>(T + 6 * 512);
+    #pragma unroll
+                    for (int jb = 0; jb < 4; jb++) scl[i][jb] = sc16[8 * h2 + 2 * jb + q];
+                    if (h2 == 0) sco[i] = *reinterpret_cast<const uint2*>(sc16 + 8 * q);
+                }
+                if (h2 == 0) {
+    #pragma unroll
+                    for (int j = 0; j < CA; j++) {
+                        const unsigned char* SP = buf + S::S_OFF + (32 * j + r) * 32 + 16 * q;
+                        bhi[j] = *reinterpret_cast<const half8*>(SP);
+                        blo[j] = *reinterpret_cast<const half8*>(SP + BN * 32);
+                    }
+                }
+    #pragma unroll
+                for (int jb = 0; jb < 4; jb++)
+    #pragma unroll
+                    for (int j = 0; j < CA; j++) {
+    #pragma unroll
+                        for (int ks = 0; ks < 2; ks++)
+                            bfs[jb][j][ks] = *reinterpret_cast<const half8*>(LB + ((2 * jb + ks) * 2 + q) * BN * 16 + (32 * j + r) * 16);
+                        dxs[jb][j] = LDX[jb * BN + 32 * j + r];
+                    }
+                if (h2 == 0) {
+                    // accs = −8·Σ_t sc_t·xs_t (the −32 offset, in units of 1/4), one 32x32x16 step hi + lo
+    #pragma unroll
+                    for (int i = 0; i < RT; i++) {
+                        half8 ao;
+    #pragma unroll
+                        for (int e = 0; e < 8; e++)
+                            ao[e] = (_Float16) (-8.0f * (float) (int8_t) (((e < 4 ? sco[i].x : sco[i].y) >> (8 * (e & 3))) & 0xffu));
+    #pragma unroll
+                        for (int j = 0; j < CA; j++) {
+                            accs[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ao, bhi[j], floatx16{}, 0, 0, 0);
+                            accs[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ao, blo[j], accs[i][j], 0, 0, 0);
+                        }
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                if (st + 1 < nst) issue(st + 1, smem + ((st + 1) & 1) * S::BYTES);
+    #pragma unroll
+                for (int jb = 0; jb < 4; jb++) {
+                    half8 a1[RT][2], a2[RT][2];
+    #pragma unroll
+                    for (int i = 0; i < RT; i++) {
+                        const float sc = (float) scl[i][jb];
+                        // ql nibble: lo (1024 + v)·sc/4 − 256·sc; hi (1024 + 16v)·sc/64 − 16·sc
+                        const bool hi = jb >= 2;
+                        const float fm = hi ? sc * 0.015625f : sc * 0.25f, fa = hi ? -16.0f * sc : -256.0f * sc;
+                        const uint32_t mul1 = pack2((_Float16) fm, (_Float16) fm), add1 = pack2((_Float16) fa, (_Float16) fa);
+                        const uint4 L = ql[i][jb & 1];
+                        const uint32_t m1 = hi ? vmask_hi : vmask_lo;
+                        a1[i][0] = frag8(L.x, L.y, m1, mul1, add1);
+                        a1[i][1] = frag8(L.z, L.w, m1, mul1, add1);
+                        // qh bits 2jb..2jb+1 moved to bits 4-5: (1024 + 16v)·sc/4 − 256·sc = 4·sc·v = sc·(16v)/4
+                        const float fm2 = sc * 0.25f, fa2 = -256.0f * sc;
+                        const uint32_t mul2 = pack2((_Float16) fm2, (_Float16) fm2), add2 = pack2((_Float16) fa2, (_Float16) fa2);
+                        const uint4 Q = qh[i];
+                        const int sh = 2 * jb;   // bits 2jb..2jb+1 -> 4..5
+                        auto mv = [&](uint32_t x) { return sh <= 4 ? x << (4 - sh) : x >> (sh - 4); };
+                        a2[i][0] = frag8(mv(Q.x), mv(Q.y), vmask_qh, mul2, add2);
+                        a2[i][1] = frag8(mv(Q.z), mv(Q.w), vmask_qh, mul2, add2);
+                    }
+    #pragma unroll
                     for (int i = 0; i < RT; i++)
-#pragma unroll
-                        for (int j = 0; j < CT; j++)
-#pragma unroll
-                            for (int e = 0; e < 16; e++)
-                                accs[i][j][e] = fmaf(Dp[pb & 1][i][j][e], dxs[pb][j], accs[i][j][e]);
+    #pragma unroll
+                        for (int j = 0; j < CA; j++) {
+                            floatx16 D = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1[i][0], bfs[jb][j][0], floatx16{}, 0, 0, 0);
+                            D = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1[i][1], bfs[jb][j][1], D, 0, 0, 0);
+                            D = __builtin_amdgcn_mfma_f32_32x32x16_f16(a2[i][0], bfs[jb][j][0], D, 0, 0, 0);
+                            D = __builtin_amdgcn_mfma_f32_32x32x16_f16(a2[i][1], bfs[jb][j][1], D, 0, 0, 0);
+    #pragma unroll
+                            for (int e = 0; e < 16; e++) accs[i][j][e] = fmaf(D[e], dxs[jb][j], accs[i][j][e]);
+                        }
                 }
-            }
-            if (gend) {   // group end: acc += 2^(e_ref - 128) · accs
-#pragma unroll
-                for (int i = 0; i < RT; i++)
-#pragma unroll
-                    for (int j = 0; j < CT; j++) {
-#pragma unroll
-                        for (int e = 0; e < 16; e++) acc[i][j][e] = fmaf(sg[i][e], accs[i][j][e], acc[i][j][e]);
-                        accs[i][j] = floatx16{};
-                    }
-            }
-        } else {   // Q6_K: stage h2 = half h of the super-block, blocks j = 0..3 (elements 128h + 32j + l)
-            // every LDS read of the stage up front, then the next stage's copy, then the compute
-            uint4 ql[RT][2], qh[RT];
-            int8_t scl[RT][4];
-            uint2 sco[RT];             // h2 = 0: the 8 scales of row r's 16-groups 8q..8q+7 (offset term)
-            half8 bhi[CT], blo[CT];    // h2 = 0: the sums' fragments
-            half8 bfs[4][CT][2];
-            float dxs[4][CT];
-#pragma unroll
-            for (int i = 0; i < RT; i++) {
-                const unsigned char* T = LA + (wave * RT + i) * NCS * 512 + 16 * r;
-                ql[i][0] = *reinterpret_cast<const uint4*>(T + (0 + q) * 512);
-                ql[i][1] = *reinterpret_cast<const uint4*>(T + (2 + q) * 512);
-                qh[i] = *reinterpret_cast<const uint4*>(T + (4 + q) * 512);
-                const int8_t* sc16 = reinterpret_cast<const int8_t*>(T + 6 * 512);
-#pragma unroll
-                for (int jb = 0; jb < 4; jb++) scl[i][jb] = sc16[8 * h2 + 2 * jb + q];
-                if (h2 == 0) sco[i] = *reinterpret_cast<const uint2*>(sc16 + 8 * q);
-            }
-            if (h2 == 0) {
-#pragma unroll
-                for (int j = 0; j < CT; j++) {
-                    const unsigned char* SP = buf + S::S_OFF + (32 * j + r) * 32 + 16 * q;
-                    bhi[j] = *reinterpret_cast<const half8*>(SP);
-                    blo[j] = *reinterpret_cast<const half8*>(SP + BN * 32);
-                }
-            }
-#pragma unroll
-            for (int jb = 0; jb < 4; jb++)
-#pragma unroll
-                for (int j = 0; j < CT; j++) {
-#pragma unroll
-                    for (int ks = 0; ks < 2; ks++)
-                        bfs[jb][j][ks] = *reinterpret_cast<const half8*>(LB + ((2 * jb + ks) * 2 + q) * BN * 16 + (32 * j + r) * 16);
-                    dxs[jb][j] = LDX[jb * BN + 32 * j + r];
-                }
-            if (h2 == 0) {
-                // accs = −8·Σ_t sc_t·xs_t (the −32 offset, in units of 1/4), one 32x32x16 step hi + lo
-#pragma unroll
-                for (int i = 0; i < RT; i++) {
-                    half8 ao;
-#pragma unroll
-                    for (int e = 0; e < 8; e++)
-                        ao[e] = (_Float16) (-8.0f * (float) (int8_t) (((e < 4 ? sco[i].x : sco[i].y) >> (8 * (e & 3))) & 0xffu));
-#pragma unroll
-                    for (int j = 0; j < CT; j++) {
-                        accs[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ao, bhi[j], floatx16{}, 0, 0, 0);
-                        accs[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ao, blo[j], accs[i][j], 0, 0, 0);
+                if (h2 == 1) {   // super-block end: acc += 4d · accs (d read here: the next copy has had the stage)
+    #pragma unroll
+                    for (int i = 0; i < RT; i++) {
+                        const unsigned char* H = buf + S::H_OFF + (wave * RT + i) * 32 * 2;
+                        float dd[16];
+    #pragma unroll
+                        for (int e = 0; e < 16; e++) {
+                            const int row = 8 * (e >> 2) + 4 * q + (e & 3);
+                            dd[e] = 4.0f * h2f_bits(*reinterpret_cast<const uint16_t*>(H + row * 2));
+                        }
+    #pragma unroll
+                        for (int j = 0; j < CA; j++)
+    #pragma unroll
+                            for (int e = 0; e < 16; e++) acc[i][j][e] = fmaf(dd[e], accs[i][j][e], acc[i][j][e]);
                     }
                 }
             }
-            __builtin_amdgcn_sched_barrier(0);
-            if (st + 1 < nst) issue(st + 1, smem + ((st + 1) & 1) * S::BYTES);
-#pragma unroll
-            for (int jb = 0; jb < 4; jb++) {
-                half8 a1[RT][2], a2[RT][2];
-#pragma unroll
-                for (int i = 0; i < RT; i++) {
-                    const float sc = (float) scl[i][jb];
-                    // ql nibble: lo (1024 + v)·sc/4 − 256·sc; hi (1024 + 16v)·sc/64 − 16·sc
-                    const bool hi = jb >= 2;
-                    const float fm = hi ? sc * 0.015625f : sc * 0.25f, fa = hi ? -16.0f * sc : -256.0f * sc;
-                    const uint32_t mul1 = pack2((_Float16) fm, (_Float16) fm), add1 = pack2((_Float16) fa, (_Float16) fa);
-                    const uint4 L = ql[i][jb & 1];
-                    const uint32_t m1 = hi ? vmask_hi : vmask_lo;
-                    a1[i][0] = frag8(L.x, L.y, m1, mul1, add1);
-                    a1[i][1] = frag8(L.z, L.w, m1, mul1, add1);
-                    // qh bits 2jb..2jb+1 moved to bits 4-5: (1024 + 16v)·sc/4 − 256·sc = 4·sc·v = sc·(16v)/4
-                    const float fm2 = sc * 0.25f, fa2 = -256.0f * sc;
-                    const uint32_t mul2 = pack2((_Float16) fm2, (_Float16) fm2), add2 = pack2((_Float16) fa2, (_Float16) fa2);
-                    const uint4 Q = qh[i];
-                    const int sh = 2 * jb;   // bits 2jb..2jb+1 -> 4..5
-                    auto mv = [&](uint32_t x) { return sh <= 4 ? x << (4 - sh) : x >> (sh - 4); };
-                    a2[i][0] = frag8(mv(Q.x), mv(Q.y), vmask_qh, mul2, add2);
-                    a2[i][1] = frag8(mv(Q.z), mv(Q.w), vmask_qh, mul2, add2);
-                }
-#pragma unroll
-                for (int i = 0; i < RT; i++)
-#pragma unroll
-                    for (int j = 0; j < CT; j++) {
-                        floatx16 D = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1[i][0], bfs[jb][j][0], floatx16{}, 0, 0, 0);
-                        D = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1[i][1], bfs[jb][j][1], D, 0, 0, 0);
-                        D = __builtin_amdgcn_mfma_f32_32x32x16_f16(a2[i][0], bfs[jb][j][0], D, 0, 0, 0);
-                        D = __builtin_amdgcn_mfma_f32_32x32x16_f16(a2[i][1], bfs[jb][j][1], D, 0, 0, 0);
-#pragma unroll
-                        for (int e = 0; e < 16; e++) accs[i][j][e] = fmaf(D[e], dxs[jb][j], accs[i][j][e]);
-                    }
-            }
-            if (h2 == 1) {   // super-block end: acc += 4d · accs (d read here: the next copy has had the stage)
-#pragma unroll
-                for (int i = 0; i < RT; i++) {
-                    const unsigned char* H = buf + S::H_OFF + (wave * RT + i) * 32 * 2;
-                    float dd[16];
-#pragma unroll
-                    for (int e = 0; e < 16; e++) {
-                        const int row = 8 * (e >> 2) + 4 * q + (e & 3);
-                        dd[e] = 4.0f * h2f_bits(*reinterpret_cast<const uint16_t*>(H + row * 2));
-                    }
-#pragma unroll
-                    for (int j = 0; j < CT; j++)
-#pragma unroll
-                        for (int e = 0; e < 16; e++) acc[i][j][e] = fmaf(dd[e], accs[i][j][e], acc[i][j][e]);
-                }
-            }
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
         }
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
-    }
+    };
+    if (CT == 2 && half)
+        run(std::integral_constant<int, 1>{});
+    else
+        run(std::integral_constant<int, CT>{});
 
     // epilogue: lane holds token n0 + 32j + r, rows 8·(e/4) + 4q + e%4 of each tile; scale back by 2^e_t
 #pragma unroll
@@ -742,7 +757,7 @@ static hipError_t kq_go(const WeightView& w, const GemmAct& A, int m, int n, flo
     using S = Stage<DT, RT, CT>;
     const int nrb = (m + 32 * S::TW - 1) / (32 * S::TW), ncb = A.NP / S::BN;
     const int64_t tiles = (w.r0 + tiled_rows(m)) / 32 - w.r0 / 32;   // tiles of the view that exist
-    const int total = nrb * ncb, grid = (total + 7) / 8 * 8;
+    const int total = nrb * ncb, grid = tile_grid(gp.map64 != nullptr, total);
     const size_t lds = 2 * (size_t) S::BYTES;
     static std::atomic<bool> attr{false};   // threads racing here both set the same value
     if (!attr.load(std::memory_order_acquire)) {

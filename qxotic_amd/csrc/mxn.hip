@@ -142,10 +142,11 @@ __global__ void __launch_bounds__(256, 2) mxn_gemm_kernel(WeightView w, MxAct A,
                                                           int ldc, int nrb, int ncb, int64_t tiles, Groups gp, Epi ep) {
     using namespace mxn;
     __shared__ __align__(1024) unsigned char smem[2 * STAGE];
-    const int total = nrb * ncb, per = (total + 7) / 8;
-    const int lin = (int) (blockIdx.x % 8) * per + (int) (blockIdx.x / 8);   // XCD-aware: runs of row blocks
+    const int total = nrb * ncb;
+    const int lin = tile_of_block(gp.map64 != nullptr, total);
     if (lin >= total) return;
-    const int rb = lin / ncb, cb = lin % ncb;
+    int rb = lin / ncb, cb = lin % ncb;
+    if (gp.map64 != nullptr && grouped_tile(gp, lin, nrb, &rb, &cb) < 0) return;
     const int64_t T0 = (int64_t) rb * 4;
     const int n0 = cb * 64;
     const int lane = threadIdx.x & 63, r = lane & 31, q = lane >> 5;
@@ -284,7 +285,7 @@ static hipError_t mx_go(int mode, const WeightView& w, const MxAct& A, int m, in
     if ((w.r0 & 31) || A.NP % 64) return hipErrorNotSupported;
     const int nrb = (m + 127) / 128, ncb = A.NP / 64;
     const int64_t tiles = (w.r0 + tiled_rows(m)) / 32 - w.r0 / 32;
-    const int grid = (nrb * ncb + 7) / 8 * 8;
+    const int grid = tile_grid(gp.map64 != nullptr, nrb * ncb);
     if (mode == 1) mxn_gemm_kernel<1><<<grid, 256, 0, st>>>(w, A, m, n, c, ldc, nrb, ncb, tiles, gp, ep);
     else mxn_gemm_kernel<2><<<grid, 256, 0, st>>>(w, A, m, n, c, ldc, nrb, ncb, tiles, gp, ep);
     return hipGetLastError();
