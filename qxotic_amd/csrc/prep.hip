@@ -135,9 +135,11 @@ JAMHIP_DEV int perm8(int j) { return j == 1 ? 2 : j == 2 ? 1 : j == 5 ? 6 : j ==
 
 int gemm_sums_kind(int dt) { return dt == Q4_K || dt == Q4_0 ? 1 : dt == Q6_K ? 2 : 0; }
 
-// One workgroup per token slot (4 waves, a wave per 256-element chunk at a time): jam's F2 quantization of
-// the slot's activation row (f2_lane, bit-exact), the codes scattered into the fragment order of
-// GemmAct::b, the block scales and per-16 sums parked in LDS together with the row's largest |sum| (SK 1:
+// One workgroup per token slot (256 threads, a thread per 16-element half of a block, 128 blocks per round):
+// jam's F2 quantization of the slot's activation row (f2_lane's arithmetic, bit-exact; the block's two
+// halves sit in adjacent lanes, which exchange their maxima), each half's codes stored as two 16-byte
+// pieces of GemmAct::b's fragment order, the block scales and per-16 sums parked in LDS together with the
+// row's largest |sum| (SK 1:
 // per-32 xs0 + xs1, jam's fl(xs0 + xs1); SK 2: per-16; SK 0: none); then the slot's power of two from that
 // maximum and the scaled block scales and sums.
 // Grouped form (gmap non-null): slot t belongs to expert gmap[t / 64] (-1: padding) and holds that
@@ -155,11 +157,10 @@ template <int CTRL> JAMHIP_DEV float dppf(float v) {
 }
 constexpr int PREP_MAX_KP = 65536;   // LDS: Kp/32 + Kp/16 floats per slot
 
-// Per chunk: each lane holds 4 consecutive elements of one block (8 lanes per block, a wave = one
-// 256-element chunk). F2 exactly as f2_lane: the block max over the 8 lanes, d = max/127, inv = 127/max,
-// q = sat8(rne(x·inv)) with NaN/overflow -> -128, and the per-16 sums in _mm512_reduce_add_ps's pairing
-// (distance 8, 4, 2, 1): distances 8 and 4 cross lanes (xor 2, xor 1: DPP quad permutes), 2 and 1 stay in
-// the lane.
+// F2 exactly as f2_lane: the block max over both halves, d = max/127, inv = 127/max, q = sat8(rne(x·inv))
+// with NaN/overflow -> -128, and the per-16 sums in _mm512_reduce_add_ps's pairing (distance 8, 4, 2, 1),
+// all inside the lane. A lane holds elements 16h..16h+15 of its block (half h), or for MXO elements
+// 8h..8h+7 and 16+8h..16+8h+7: exactly the two (K-step, half) planes it stores.
 // MXO: the MXFP4 element order (the GEMM converts a weight byte's two nibbles, elements e and e + 16 of the
 // block, into one f16 pair): K-step 2·block + ks, half q, slot i holds element 8q + 4ks + i/2 + 16·(i % 2).
 template <int SK, bool MXO>
@@ -175,77 +176,86 @@ __global__ void __launch_bounds__(256) gemm_prep(const float* __restrict__ a, in
     // workgroup i runs on XCD i % 8: give each XCD a contiguous run of token slots, so that the slots sharing
     // an output line (the codes, block scales and sums are token-interleaved) are written through one L2
     const int t = (int) (blockIdx.x % 8) * (NP >> 3) + (int) (blockIdx.x >> 3);
-    const int nbk = k >> 5, lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nch = Kp >> 8;
+    const int nbk = k >> 5, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int src = prep_src(t, n, gmap, goff, gpoff);
     // a padding slot (past n, or past its expert's rows) is left unwritten: the GEMM's token column for it is
     // computed but never stored, and no other column reads it
     if (src < 0) return;
-    const int j = lane & 7;   // lane within the block
+    const int hh = lane & 1;   // which half of its block the lane holds
     float m2 = 0.0f;
-    // batches of 4 chunks per wave: the batch's loads go out together, then the chunks are quantized
-    for (int c0 = wave; c0 < nch; c0 += 16) {
-        float xb[4][4];
+    typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+    // one 16-element half of one block per lane (lanes 2b', 2b' + 1 hold a block): 128 blocks per round of the
+    // workgroup, two rounds' loads in flight; blocks past k (up to Kp) quantize zeros
+    const int nbp = Kp >> 5;
+    const float* row = a + (int64_t) src * lda;
+    for (int r0 = threadIdx.x >> 1; r0 < nbp; r0 += 256) {
+        float xr[2][16];
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const int b = 8 * (c0 + 4 * u) + (lane >> 3);
+        for (int u = 0; u < 2; u++) {
+            const int b = r0 + 128 * u;
 #pragma unroll
-            for (int v = 0; v < 4; v++) xb[u][v] = 0.0f;
-            if (src >= 0 && b < nbk) {
-                const float* p = a + (int64_t) src * lda + 32 * b + 4 * j;
+            for (int i = 0; i < 16; i++) xr[u][i] = 0.0f;
+            if (b < nbk) {
+                // MXO: elements 8hh..8hh+7 and 16+8hh..16+8hh+7 (the order the GEMM pairs them in); else 16hh..16hh+15
+                const float* p0 = row + 32 * b + (MXO ? 8 * hh : 16 * hh);
+                const float* p1 = p0 + (MXO ? 16 : 8);
                 if (vec) {   // a and lda 16-byte aligned (the launcher checks)
-                    const float4 v = *reinterpret_cast<const float4*>(p);
-                    xb[u][0] = v.x, xb[u][1] = v.y, xb[u][2] = v.z, xb[u][3] = v.w;
+#pragma unroll
+                    for (int v = 0; v < 2; v++) {
+                        const float4 f0 = *reinterpret_cast<const float4*>(p0 + 4 * v);
+                        const float4 f1 = *reinterpret_cast<const float4*>(p1 + 4 * v);
+                        xr[u][4 * v + 0] = f0.x, xr[u][4 * v + 1] = f0.y, xr[u][4 * v + 2] = f0.z, xr[u][4 * v + 3] = f0.w;
+                        xr[u][8 + 4 * v + 0] = f1.x, xr[u][8 + 4 * v + 1] = f1.y, xr[u][8 + 4 * v + 2] = f1.z,
+                                         xr[u][8 + 4 * v + 3] = f1.w;
+                    }
                 } else {
-                    xb[u][0] = p[0], xb[u][1] = p[1], xb[u][2] = p[2], xb[u][3] = p[3];
+#pragma unroll
+                    for (int i = 0; i < 8; i++) xr[u][i] = p0[i], xr[u][8 + i] = p1[i];
                 }
             }
         }
 #pragma unroll
-        for (int cb = 0; cb < 4; cb++) {
-            const int ch = c0 + 4 * cb;
-            if (ch >= nch) break;   // wave-uniform
-            const int b = 8 * ch + (lane >> 3);
-            const float* x = xb[cb];
-            float mx = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
-            mx = fmaxf(mx, __shfl_xor(mx, 4));
-            mx = fmaxf(mx, dppf<0x4E>(mx));   // lane ^ 2
-            mx = fmaxf(mx, dppf<0xB1>(mx));   // lane ^ 1
+        for (int u = 0; u < 2; u++) {
+            const int b = r0 + 128 * u;
+            if (b >= nbp) break;   // lane pairs stay together: b is the same for both lanes of a block
+            const float* x = xr[u];
+            float mx = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 16; i++) mx = fmaxf(mx, fabsf(x[i]));
+            mx = fmaxf(mx, dppf<0xB1>(mx));   // the block's other half (lane ^ 1)
             const float db = mx / 127.0f;
             const float inv = mx > 0.0f ? 127.0f / mx : 0.0f;
-            int qv[4];
+            float qf[16];
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const float p = x[u] * inv;
-                qv[u] = !(p > -2147483648.0f && p < 2147483648.0f) ? -128 : (int) fminf(fmaxf(rintf(p), -128.0f), 127.0f);
+            for (int i = 0; i < 16; i++) {
+                const float p = x[i] * inv;
+                qf[i] = !(p > -2147483648.0f && p < 2147483648.0f) ? -128.0f : fminf(fmaxf(rintf(p), -128.0f), 127.0f);
             }
-            typedef _Float16 half4 __attribute__((ext_vector_type(4)));
-            if constexpr (!MXO) {
-                // codes: elements 4j..4j+3 -> K-step (j >> 1) & 1, half j >> 2, slots 4(j & 1) + {0, 2, 1, 3} of the
-                // (K-step, half) plane's 8 per token
-                const half4 hv = {(_Float16) qv[0], (_Float16) qv[2], (_Float16) qv[1], (_Float16) qv[3]};
-                *reinterpret_cast<half4*>(bq + ((int64_t) (2 * (2 * b + ((j >> 1) & 1)) + (j >> 2)) * NP + t) * 8 + 4 * (j & 1)) = hv;
-            } else {
-                // elements 4j + u -> K-step j & 1, half (j & 3) >> 1, slot 2u + (j >> 2): lanes j and j ^ 4 interleave
-                // their codes; lane j < 4 stores slots 0-3, lane j + 4 slots 4-7
-                int ov[4];
+            // the lane's two (K-step, half) planes: 8 f16 (16 bytes) each at the slot
 #pragma unroll
-                for (int u = 0; u < 4; u++) ov[u] = __shfl_xor(qv[u], 4);
-                const half4 hv = j < 4 ? half4{(_Float16) qv[0], (_Float16) ov[0], (_Float16) qv[1], (_Float16) ov[1]}
-                                       : half4{(_Float16) ov[2], (_Float16) qv[2], (_Float16) ov[3], (_Float16) qv[3]};
-                *reinterpret_cast<half4*>(bq + ((int64_t) (2 * (2 * b + (j & 1)) + ((j & 3) >> 1)) * NP + t) * 8 + 4 * (j >> 2)) = hv;
+            for (int ks = 0; ks < 2; ks++) {
+                half8 hv;
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    if constexpr (!MXO) hv[perm8(i)] = (_Float16) qf[8 * ks + i];   // elements 16hh + 8ks + i
+                    else hv[2 * (i & 3) + (i >> 2)] = (_Float16) qf[8 * (i >> 2) + 4 * ks + (i & 3)];
+                }
+                *reinterpret_cast<half8*>(bq + ((int64_t) (2 * (2 * b + ks) + hh) * NP + t) * 8) = hv;
             }
-            // per-16 sums: distance 8 (xor 2), distance 4 (xor 1), then in-lane distance 2 and 1
-            float s[4];
-#pragma unroll
-            for (int u = 0; u < 4; u++) s[u] = dppf<0x4E>(x[u]) + x[u];
-#pragma unroll
-            for (int u = 0; u < 4; u++) s[u] = dppf<0xB1>(s[u]) + s[u];
-            const float xs16 = (s[0] + s[2]) + (s[1] + s[3]);
-            if (j == 0) ldb[b] = db;
-            if ((j & 3) == 0) lxs[2 * b + (j >> 2)] = xs16;
+            if (hh == 0) ldb[b] = db;
             if constexpr (SK != 0) {
-                const float other = __shfl_xor(xs16, 4);   // the block's other half
-                m2 = fmaxf(m2, SK == 1 ? fabsf((j < 4) ? xs16 + other : other + xs16) : fabsf(xs16));
+                // per-16 sum in _mm512_reduce_add_ps's pairing: distance 8, 4, 2, 1
+                float s8[8];
+#pragma unroll
+                for (int i = 0; i < 8; i++) s8[i] = x[i] + x[i + 8];
+#pragma unroll
+                for (int i = 0; i < 4; i++) s8[i] = s8[i] + s8[i + 4];
+                s8[0] = s8[0] + s8[2];
+                s8[1] = s8[1] + s8[3];
+                const float xs16 = s8[0] + s8[1];
+                lxs[2 * b + hh] = xs16;
+                const float other = dppf<0xB1>(xs16);   // the block's other half
+                m2 = fmaxf(m2, SK == 1 ? fabsf(hh == 0 ? xs16 + other : other + xs16) : fabsf(xs16));
             }
         }
     }
