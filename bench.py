@@ -699,8 +699,8 @@ def main() -> int:
                    "weights": "N(0,0.02) quantized to Q4_K", "activations": "N(0,1) f32",
                    "graph_launches": 0 if args.no_graph else args.steps, "wall_s": round(g["wall_s"], 4)},
         "host_pointer_call": {"us": round(g["host_us"], 2), "GBs": round(STEP_BYTES / (g["host_us"] * 1e-6) / 1e9, 1),
-                              "note": "jamhip_mm with host A and C (16 KiB H2D + 56 KiB D2H + sync per call), "
-                                      "pinned weights, wall clock; not the metric",
+                              "note": "jamhip_mm with host A and C (16 KiB upload, 56 KiB of C stored by the kernel "
+                                      "into pinned host memory, sync per call), pinned weights, wall clock; not the metric",
                               "unpinned_staged_us": round(g["staged_us"], 2), "unpinned_autopin_us": round(g["auto_us"], 2),
                               "autopin_note": "the same call on a weight nobody pinned: staged every call, then with "
                                               "jamhip_ctx_set_autopin(2) (pinned on its 2nd call, spot-checked each call)"},

@@ -620,6 +620,10 @@ struct SyncOnError {
     }
 };
 
+// Largest A / C (bytes) that jamhip_mm moves by the shader cores: A uploaded by a copy kernel, C stored by the
+// matmul kernels straight into the pinned bounce buffer.
+constexpr size_t kDirectCBytes = 1 << 20;
+
 jamhip_status mm_impl(jamhip_ctx* ctx, const void* w, int wt, int ldw, const void* a, int at, int lda, void* c,
                         int ct, int ldc, int m, int n, int k) {
     jamhip_status st = validate(ctx, w, wt, ldw, a, at, lda, c, ct, ldc, m, n, k);
@@ -650,12 +654,21 @@ jamhip_status mm_impl(jamhip_ctx* ctx, const void* w, int wt, int ldw, const voi
     float* ah = static_cast<float*>(ctx->a_host.p);
     for (int j = 0; j < n; j++) std::memcpy(ah + (size_t) j * k, af + (size_t) j * lda, (size_t) k * 4);
     SyncOnError pending{ctx};
-    if ((e = hipMemcpyAsync(ctx->a_stage.p, ah, abytes, hipMemcpyHostToDevice, ctx->stream)) != hipSuccess)
-        return hip_fail(ctx, e, "A upload");
+    // a small A goes up by a copy kernel reading the pinned buffer (lower latency than the runtime's copy)
+    if (abytes <= kDirectCBytes && abytes % 16 == 0)
+        e = launch_stage_copy(ah, ctx->a_stage.p, abytes, ctx->stream);
+    else
+        e = hipMemcpyAsync(ctx->a_stage.p, ah, abytes, hipMemcpyHostToDevice, ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "A upload");
     pending.armed = true;
-    if ((st = compute(ctx, wt, wv, (const float*) ctx->a_stage.p, k, (float*) ctx->c_stage.p, m, m, n, k)) != JAMHIP_OK)
-        return st;
-    if ((e = hipMemcpyAsync(ctx->c_host.p, ctx->c_stage.p, cbytes, hipMemcpyDeviceToHost, ctx->stream)) != hipSuccess)
+    // A small C (decode: m floats per token) is stored by the kernels straight into the pinned buffer, which
+    // the device addresses directly: no separate device-to-host copy. A large one goes through device memory
+    // and one copy.
+    const bool direct_c = cbytes <= kDirectCBytes;
+    float* cdst = static_cast<float*>(direct_c ? ctx->c_host.p : ctx->c_stage.p);
+    if ((st = compute(ctx, wt, wv, (const float*) ctx->a_stage.p, k, cdst, m, m, n, k)) != JAMHIP_OK) return st;
+    if (!direct_c &&
+        (e = hipMemcpyAsync(ctx->c_host.p, ctx->c_stage.p, cbytes, hipMemcpyDeviceToHost, ctx->stream)) != hipSuccess)
         return hip_fail(ctx, e, "C download");
     pending.armed = false;
     if ((e = hipStreamSynchronize(ctx->stream)) != hipSuccess) return hip_fail(ctx, e, "stream sync");

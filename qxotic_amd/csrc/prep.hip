@@ -349,6 +349,23 @@ hipError_t launch_gemm_prep_grouped(int dt, const float* a, int lda, int k, cons
     return prep_np(dt, a, lda, 0, cap64 * 64, k, scratch, out, g.map64, g.off, g.poff64, st);
 }
 
+// Host-to-device staging of jamhip_mm's activations by the shader cores: the pinned host buffer is read over
+// the bus 16 bytes per thread (a handful of workgroups for a decode vector) and written to device memory.
+__global__ void __launch_bounds__(256) stage_copy_kernel(const uint4* __restrict__ src, uint4* __restrict__ dst,
+                                                         int64_t n16) {
+    for (int64_t i = (int64_t) blockIdx.x * 256 + threadIdx.x; i < n16; i += (int64_t) gridDim.x * 256) dst[i] = src[i];
+}
+
+hipError_t launch_stage_copy(const void* src, void* dst, size_t bytes, hipStream_t st) {
+    const int64_t n16 = (int64_t) (bytes / 16);
+    if (bytes % 16 || (reinterpret_cast<uintptr_t>(src) & 15) || (reinterpret_cast<uintptr_t>(dst) & 15))
+        return hipErrorInvalidValue;
+    if (n16 == 0) return hipSuccess;
+    const int64_t blocks = (n16 + 255) / 256;
+    stage_copy_kernel<<<(unsigned) (blocks < 64 ? blocks : 64), 256, 0, st>>>((const uint4*) src, (uint4*) dst, n16);
+    return hipGetLastError();
+}
+
 hipError_t launch_quant_f1(const float* a, int lda, int n, int k, int8_t* q, float* d, float* asum, int* s16,
                            hipStream_t st) {
     dim3 grid((k + 255) / 256, n);
