@@ -848,6 +848,24 @@ jamhip_status mm_grouped_ex_impl(jamhip_ctx* ctx, const void* w, int wt, int ldw
     int* poff8 = poff64 + (E + 1);
     int* map64 = poff8 + (E + 1);
     int* map8 = map64 + cap64;
+    const float* a = (const float*) a_dev;
+    float* c = (float*) c_dev;
+    // Matrix-core path with at least 8 rows per expert on average: one prep launch builds the offsets and the
+    // slot map from the device counts and quantizes every expert's rows (F1 for experts of 1..7 rows, whose
+    // 64-slot blocks then take the GEMM's single-token-tile form), so neither the offsets kernel nor the F1
+    // decode launch runs. Sparser calls keep the F1 decode kernel for their small experts.
+    if (rows_cap >= 8 * E && E <= PREP_FUSED_MAX_E && mma_path(wt, k, wv) && m % 32 == 0 &&
+        !(wt == MXFP4 && ctx->mx_native)) {
+        const PrepGroups pg{(const int*) counts_dev, E, rows_cap, off, poff64, map64, cap64, (int*) offsets_dev};
+        const Groups g{off, poff8, map8, poff64, map64, m, static_cast<const float*>(bias_dev)};
+        GemmAct G;
+        if ((e = ctx->gact.ensure(gemm_act_bytes_np(wt, cap64 * 64, k))) != hipSuccess)
+            return hip_fail(ctx, e, "grouped: gemm activation scratch alloc");
+        if ((e = launch_gemm_prep_grouped_fused(wt, a, lda, k, pg, ctx->gact.p, &G, ctx->stream)) != hipSuccess ||
+            (e = launch_gemm_mma_grouped(wt, wv, G, k, g, cap64, c, ldc, ctx->stream)) != hipSuccess)
+            return hip_fail(ctx, e, "grouped: gemm launch");
+        return JAMHIP_OK;
+    }
     if ((e = launch_moe_offsets((const int*) counts_dev, E, rows_cap, off, poff64, poff8, map64, cap64, map8, cap8,
                                 ctx->stream)) != hipSuccess)
         return hip_fail(ctx, e, "grouped: offsets launch");
@@ -857,8 +875,6 @@ jamhip_status mm_grouped_ex_impl(jamhip_ctx* ctx, const void* w, int wt, int ldw
         return hip_fail(ctx, e, "grouped: offsets copy");
     if (rows_cap == 0) return JAMHIP_OK;
     const Groups g{off, poff8, map8, poff64, map64, m, static_cast<const float*>(bias_dev)};
-    const float* a = (const float*) a_dev;
-    float* c = (float*) c_dev;
     // activation scratch for the decode kernels (rows_cap rows; F1 then F2 reuse it in stream order)
     const int64_t nb = k / 32, n = rows_cap;
     const int64_t qb = align256(n * k), db = align256(n * nb * 4), sb = align256(n * (k / 16) * 4);

@@ -159,6 +159,19 @@ hipError_t launch_glu(int act, float* gate, int ldg, const float* up, int ldu, i
 // Streaming read of `bytes` (a multiple of 16; 16-byte aligned p) with the decode kernel's load shape, nothing
 // written but a word at `sink` if the loads xor to a fixed value (readfloor.hip).
 hipError_t launch_read_floor(const void* p, int64_t bytes, uint32_t* sink, hipStream_t st);
+// The grouped prep that builds its own slot map (one launch instead of offsets + F1 decode + prep; E <= 256):
+// every expert with rows gets 64-token slots (experts with 1..7 rows quantized with jam's F1, the rest with
+// F2), and workgroup 0 writes the CSR offsets (off, and off_out if non-null), poff64 and map64 for the GEMM.
+struct PrepGroups {
+    const int* counts;
+    int E, rows_cap;
+    int *off, *poff64, *map64;
+    int cap64;
+    int* off_out;
+};
+constexpr int PREP_FUSED_MAX_E = 256;
+hipError_t launch_gemm_prep_grouped_fused(int dt, const float* a, int lda, int k, const PrepGroups& pg,
+                                          void* scratch, GemmAct* out, hipStream_t st);
 hipError_t launch_gemm_prep_grouped(int dt, const float* a, int lda, int k, const Groups& g, int cap64,
                                     void* scratch, GemmAct* out, hipStream_t st);
 

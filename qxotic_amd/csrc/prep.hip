@@ -157,6 +157,82 @@ template <int CTRL> JAMHIP_DEV float dppf(float v) {
 }
 constexpr int PREP_MAX_KP = 65536;   // LDS: Kp/32 + Kp/16 floats per slot
 
+// Exclusive scans of (x, y) over the lanes of the first wave (wide false) or of the 256 lanes of the
+// workgroup (wide true: every thread must call it; two barriers); lane e holds expert e; *tot = the sums.
+JAMHIP_DEV int2 block_scan2(int x, int y, int2* tot, int2* sm, bool wide) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int sx = x, sy = y;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int ux = __shfl_up(sx, o), uy = __shfl_up(sy, o);
+        if (lane >= o) sx += ux, sy += uy;
+    }
+    if (!wide) {
+        *tot = make_int2(__shfl(sx, 63), __shfl(sy, 63));
+        return make_int2(sx - x, sy - y);
+    }
+    if (lane == 63) sm[wave] = make_int2(sx, sy);
+    __syncthreads();
+    int bx = 0, by = 0, tx = 0, ty = 0;
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+        const int2 v = sm[w];
+        if (w < wave) bx += v.x, by += v.y;
+        tx += v.x, ty += v.y;
+    }
+    __syncthreads();   // sm is reused by the next scan
+    *tot = make_int2(tx, ty);
+    return make_int2(bx + sx - x, by + sy - y);
+}
+
+// Token slot t of the fused grouped prep, from the expert counts on the device. Expert e keeps c_e rows: its
+// count, clamped so that the experts' rows fit rows_cap in expert order (rows past rows_cap are dropped, as
+// by launch_moe_offsets); its C rows start at oc_e (exclusive scan of c), and an expert with rows owns
+// roundup(c_e, 64) token slots from p_e (exclusive scan). Returns slot t's source row, oc_e + (t - p_e) when
+// t - p_e < c_e, else -1 (padding, or past every expert). *f1: the owner has 1..7 rows, below jam's F2 band
+// gate n >= JAM_VNNI_MIN_SEQ = 8 (jam.c:492, 570; jam_kquant.h:23). With pub set, also writes off[0..E] (and off_out), poff64[0..E] and map64[0..cap64) (the
+// owner of each 64-slot block, -1 past the last). Every thread of the workgroup must call it.
+JAMHIP_DEV int fused_slot(const PrepGroups& pg, int t, bool pub, bool* f1) {
+    __shared__ int2 sm[4];
+    __shared__ int own[2];   // slot t's source row and its expert's row count
+    const bool wide = pg.E > 64;   // up to 64 experts: the first wave alone, no barrier until the last
+    if (wide || threadIdx.x < 64) {
+        const int e = threadIdx.x, nt = wide ? 256 : 64;
+        const bool in = e < pg.E;
+        // min(count, rows_cap) changes no clamped count and keeps the scan within E·rows_cap
+        const int c0 = in ? min(max(pg.counts[e], 0), pg.rows_cap) : 0;
+        int2 tot;
+        const int o = block_scan2(c0, 0, &tot, sm, wide).x;
+        const int c = in ? max(0, min(c0, pg.rows_cap - o)) : 0;
+        const int a64 = (c + 63) / 64 * 64;
+        if (threadIdx.x == 0) own[0] = -1, own[1] = 0;
+        // ordered before the owner's stores below: by the scan's barriers, or within the one wave
+        const int2 s = block_scan2(c, a64, &tot, sm, wide);
+        const int oc = s.x, p64 = s.y;
+        if (a64 > 0 && t >= p64 && t < p64 + a64) {
+            own[0] = t - p64 < c ? oc + (t - p64) : -1;
+            own[1] = c;
+        }
+        if (pub) {
+            if (in) {
+                pg.off[e] = oc;
+                pg.poff64[e] = p64;
+                if (pg.off_out != nullptr) pg.off_out[e] = oc;
+                for (int i = p64 / 64; i < (p64 + a64) / 64 && i < pg.cap64; i++) pg.map64[i] = e;
+            }
+            if (e == 0) {
+                pg.off[pg.E] = tot.x;
+                pg.poff64[pg.E] = tot.y;
+                if (pg.off_out != nullptr) pg.off_out[pg.E] = tot.x;
+            }
+            for (int i = tot.y / 64 + e; i < pg.cap64; i += nt) pg.map64[i] = -1;
+        }
+    }
+    __syncthreads();
+    *f1 = own[1] < 8;
+    return own[0];
+}
+
 // F2 exactly as f2_lane: the block max over both halves, d = max/127, inv = 127/max, q = sat8(rne(x·inv))
 // with NaN/overflow -> -128, and the per-16 sums in _mm512_reduce_add_ps's pairing (distance 8, 4, 2, 1),
 // all inside the lane. A lane holds elements 16h..16h+15 of its block (half h), or for MXO elements
@@ -168,7 +244,8 @@ __global__ void __launch_bounds__(256) gemm_prep(const float* __restrict__ a, in
                                                  _Float16* __restrict__ bq, float* __restrict__ dx,
                                                  _Float16* __restrict__ shi, _Float16* __restrict__ slo,
                                                  float* __restrict__ es, const int* __restrict__ gmap,
-                                                 const int* __restrict__ goff, const int* __restrict__ gpoff, int vec) {
+                                                 const int* __restrict__ goff, const int* __restrict__ gpoff, int vec,
+                                                 PrepGroups pg) {
     extern __shared__ float lsm[];   // [Kp/32] block scales, [Kp/16] per-16 sums, [4] wave maxima
     float* ldb = lsm;
     float* lxs = lsm + (Kp >> 5);
@@ -177,7 +254,9 @@ __global__ void __launch_bounds__(256) gemm_prep(const float* __restrict__ a, in
     // an output line (the codes, block scales and sums are token-interleaved) are written through one L2
     const int t = (int) (blockIdx.x % 8) * (NP >> 3) + (int) (blockIdx.x >> 3);
     const int nbk = k >> 5, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int src = prep_src(t, n, gmap, goff, gpoff);
+    // fused grouped mode (counts on the device): F1 codes for an expert of 1..7 rows, else F2
+    bool f1 = false;
+    const int src = pg.counts != nullptr ? fused_slot(pg, t, blockIdx.x == 0, &f1) : prep_src(t, n, gmap, goff, gpoff);
     // a padding slot (past n, or past its expert's rows) is left unwritten: the GEMM's token column for it is
     // computed but never stored, and no other column reads it
     if (src < 0) return;
@@ -224,12 +303,21 @@ __global__ void __launch_bounds__(256) gemm_prep(const float* __restrict__ a, in
             for (int i = 0; i < 16; i++) mx = fmaxf(mx, fabsf(x[i]));
             mx = fmaxf(mx, dppf<0xB1>(mx));   // the block's other half (lane ^ 1)
             const float db = mx / 127.0f;
-            const float inv = mx > 0.0f ? 127.0f / mx : 0.0f;
             float qf[16];
+            if (f1) {
+                // F1 (jam_q8_0_requant, jam_kernels_generic.c:71-94): id = 1/d, q = clamp(rint(x·id)); a NaN
+                // product lands on -128 like LONG_MIN does
+                const float id = db > 0.0f ? 1.0f / db : 0.0f;
 #pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const float p = x[i] * inv;
-                qf[i] = !(p > -2147483648.0f && p < 2147483648.0f) ? -128.0f : fminf(fmaxf(rintf(p), -128.0f), 127.0f);
+                for (int i = 0; i < 16; i++) qf[i] = fminf(fmaxf(rintf(x[i] * id), -128.0f), 127.0f);
+            } else {
+                const float inv = mx > 0.0f ? 127.0f / mx : 0.0f;
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const float p = x[i] * inv;
+                    qf[i] = !(p > -2147483648.0f && p < 2147483648.0f) ? -128.0f
+                                                                        : fminf(fmaxf(rintf(p), -128.0f), 127.0f);
+                }
             }
             // the lane's two (K-step, half) planes: 8 f16 (16 bytes) each at the slot
 #pragma unroll
@@ -243,7 +331,17 @@ __global__ void __launch_bounds__(256) gemm_prep(const float* __restrict__ a, in
                 *reinterpret_cast<half8*>(bq + ((int64_t) (2 * (2 * b + ks) + hh) * NP + t) * 8) = hv;
             }
             if (hh == 0) ldb[b] = db;
-            if constexpr (SK != 0) {
+            if (SK != 0 && f1) {
+                // F1's offset terms take the integer code sums times d (Q4_K and Q4_0 fl(asum·ad) per 32, Q6_K's
+                // −32 per 16): the sums slot holds Σq·d, the 32-sum in the block's first half
+                float s16 = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 16; i++) s16 += qf[i];   // exact: |Σ| <= 2048
+                const float s32 = s16 + dppf<0xB1>(s16);
+                const float xs = SK == 1 ? s32 * db : s16 * db;
+                lxs[2 * b + hh] = SK == 1 && hh == 1 ? 0.0f : xs;
+                m2 = fmaxf(m2, fabsf(xs));
+            } else if constexpr (SK != 0) {
                 // per-16 sum in _mm512_reduce_add_ps's pairing: distance 8, 4, 2, 1
                 float s8[8];
 #pragma unroll
@@ -304,7 +402,8 @@ size_t gemm_act_bytes(int dt, int n, int k) { return gemm_act_bytes_np(dt, (n + 
 bool gemm_prep_fits(int k) { return (k + 255) / 256 * 256 <= PREP_MAX_KP; }
 
 static hipError_t prep_np(int dt, const float* a, int lda, int n, int NP, int k, void* scratch, GemmAct* out,
-                          const int* gmap, const int* goff, const int* gpoff, hipStream_t st) {
+                          const int* gmap, const int* goff, const int* gpoff, hipStream_t st,
+                          const PrepGroups& pg = PrepGroups{}) {
     const int Kp = (k + 255) / 256 * 256, sk = gemm_sums_kind(dt);
     if (Kp > PREP_MAX_KP) return hipErrorNotSupported;
     uint8_t* p = (uint8_t*) scratch;
@@ -332,10 +431,10 @@ static hipError_t prep_np(int dt, const float* a, int lda, int n, int NP, int k,
         if (e != hipSuccess) return e;
         attr[kind].store(true, std::memory_order_release);
     }
-    if (kind == 1) gemm_prep<1, false><<<NP, 256, lds, st>>>(a, lda, n, k, Kp, NP, bq, dx, shi, slo, es, gmap, goff, gpoff, vec);
-    else if (kind == 2) gemm_prep<2, false><<<NP, 256, lds, st>>>(a, lda, n, k, Kp, NP, bq, dx, shi, slo, es, gmap, goff, gpoff, vec);
-    else if (kind == 3) gemm_prep<0, true><<<NP, 256, lds, st>>>(a, lda, n, k, Kp, NP, bq, dx, shi, slo, es, gmap, goff, gpoff, vec);
-    else gemm_prep<0, false><<<NP, 256, lds, st>>>(a, lda, n, k, Kp, NP, bq, dx, shi, slo, es, gmap, goff, gpoff, vec);
+    if (kind == 1) gemm_prep<1, false><<<NP, 256, lds, st>>>(a, lda, n, k, Kp, NP, bq, dx, shi, slo, es, gmap, goff, gpoff, vec, pg);
+    else if (kind == 2) gemm_prep<2, false><<<NP, 256, lds, st>>>(a, lda, n, k, Kp, NP, bq, dx, shi, slo, es, gmap, goff, gpoff, vec, pg);
+    else if (kind == 3) gemm_prep<0, true><<<NP, 256, lds, st>>>(a, lda, n, k, Kp, NP, bq, dx, shi, slo, es, gmap, goff, gpoff, vec, pg);
+    else gemm_prep<0, false><<<NP, 256, lds, st>>>(a, lda, n, k, Kp, NP, bq, dx, shi, slo, es, gmap, goff, gpoff, vec, pg);
     return hipGetLastError();
 }
 
@@ -347,6 +446,13 @@ hipError_t launch_gemm_prep(int dt, const float* a, int lda, int n, int k, void*
 hipError_t launch_gemm_prep_grouped(int dt, const float* a, int lda, int k, const Groups& g, int cap64,
                                     void* scratch, GemmAct* out, hipStream_t st) {
     return prep_np(dt, a, lda, 0, cap64 * 64, k, scratch, out, g.map64, g.off, g.poff64, st);
+}
+
+hipError_t launch_gemm_prep_grouped_fused(int dt, const float* a, int lda, int k, const PrepGroups& pg,
+                                          void* scratch, GemmAct* out, hipStream_t st) {
+    if (pg.counts == nullptr || pg.E < 1 || pg.E > PREP_FUSED_MAX_E || pg.rows_cap < 0 || pg.cap64 < 1)
+        return hipErrorInvalidValue;
+    return prep_np(dt, a, lda, 0, pg.cap64 * 64, k, scratch, out, nullptr, nullptr, nullptr, st, pg);
 }
 
 // Host-to-device staging of jamhip_mm's activations by the shader cores: the pinned host buffer is read over

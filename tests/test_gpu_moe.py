@@ -95,17 +95,23 @@ def test_route_gather_combine_bit_exact(hip):
         assert np.array_equal(out4.cpu().numpy().view(np.uint32), want.view(np.uint32))
 
 
-# (dtype, m rows per expert, k): m % 32 == 0 takes the matrix cores for Q4_K / Q6_K / MXFP4 (k % 256 for the
-# K-quants; MXFP4 pads k to 256); m = 48 and Q8_0 / Q4_0 take the decode kernels' F2 tiles.
+# (dtype, m rows per expert, k): m % 32 == 0 takes the matrix cores (k % 256 for the K-quants; MXFP4 pads k
+# to 256); m = 48 takes the decode kernels' F2 tiles.
 GROUPED = [(O.MXFP4, 64, 576), (O.MXFP4, 48, 320), (O.Q4_K, 96, 512), (O.Q6_K, 64, 256), (O.Q8_0, 64, 320),
            (O.Q4_0, 48, 256)]
+# Expert row counts. DENSE (rows_cap >= 8 per expert) takes the one-launch prep on the matrix-core shapes, its
+# 1..7-row experts quantized with F1 inside the GEMM's slots; SPARSE (fewer rows than 8 per expert) keeps the
+# offsets kernel and the F1 decode kernel for its small experts.
 COUNTS = [0, 1, 7, 8, 9, 33, 64, 70, 3]
+SPARSE = [0, 1, 0, 0, 9, 0, 2, 0, 0, 0, 0, 0, 33, 0]
 
 
+@pytest.mark.parametrize("counts", [COUNTS, SPARSE], ids=["dense", "sparse"])
 @pytest.mark.parametrize("dt,m,k", GROUPED)
-def test_mm_grouped_parity(hip, oracle, dt, m, k):
+def test_mm_grouped_parity(hip, oracle, dt, m, k, counts):
     import torch
     from qxotic_amd.jam import JAM, Segment
+    COUNTS = counts
     E = len(COUNTS)
     say(f"grouped {O.NAMES[dt]} m={m} k={k} counts={COUNTS}")
     w_e = [oracle.quantize(dt, oracle.normal(0x5A11C0DE ^ (100 * e + dt), (m, k), 0.0, 0.02)) for e in range(E)]
@@ -171,6 +177,53 @@ def test_mm_grouped_counts_past_rows_cap(hip, oracle):
         got = c.cpu().numpy()
         _, sa = oracle.mm_ref(dt, w_e[1], np.ascontiguousarray(a[10:45]), m, 35, k)
         assert (np.abs(got[10:45] - ref[10:45]) <= 1e-3 * np.abs(ref[10:45]) + 1e-5 * sa).all()
+    finally:
+        hip.evict(Segment.of(w))
+
+
+def test_mm_grouped_many_experts(hip, oracle):
+    """More than 64 experts (the slot map spans the prep workgroup's four waves), small and large experts mixed,
+    and counts past rows_cap: offsets are the clamped prefix sums, every kept row meets the bound."""
+    import torch
+    from qxotic_amd.jam import JAM, Segment
+    dt, m, k, E = O.Q4_K, 32, 256, 150
+    rng = np.random.default_rng(4242)
+    counts = rng.integers(0, 16, E)
+    counts[rng.permutation(E)[:30]] = 0
+    counts[[3, 77, 140]] = [170, 130, 66]            # several 64-slot blocks each
+    counts[[5, 6, 90, 149]] = [1, 7, 2, 5]           # F1 experts (the last one loses its rows)
+    total = int(counts.sum())
+    rows_cap = total - 9                             # the last experts lose rows
+    assert rows_cap >= 8 * E
+    kept, o = [], 0
+    for n in counts:
+        kept.append(max(0, min(int(n), rows_cap - o)))
+        o += int(n)
+    say(f"grouped many experts E={E} total={total} rows_cap={rows_cap}")
+    w_e = [oracle.quantize(dt, oracle.normal(7000 + e, (m, k), 0.0, 0.02)) for e in range(E)]
+    w = np.ascontiguousarray(np.concatenate(w_e, axis=0))
+    a = oracle.outliers(78, (rows_cap, k))
+    assert hip.pin(Segment.of(w), dt, k, E * m) == JAM.OK, hip.last_error()
+    try:
+        c = torch.full((rows_cap, m), -3.0, dtype=torch.float32, device="cuda")
+        off = torch.zeros(E + 1, dtype=torch.int32, device="cuda")
+        a_dv = dev(a)   # held until the kernels that read it have run
+        counts_dv = dev(counts.astype(np.int32))
+        torch.cuda.synchronize()   # torch's fills run on its own stream
+        assert hip.mm_grouped(Segment.of(w), dt, k, m, E, counts_dv.data_ptr(), a_dv.data_ptr(), k, c.data_ptr(), m,
+                              k, rows_cap, off.data_ptr()) == JAM.OK, hip.last_error()
+        hip.synchronize()
+        assert off.cpu().numpy().tolist() == [0] + np.cumsum(kept).tolist()
+        ref = M.mm_grouped(oracle, dt, w_e, a, kept, m, k)
+        got = c.cpu().numpy()
+        o = 0
+        for e, n in enumerate(kept):
+            if n:
+                _, sa = oracle.mm_ref(dt, w_e[e], np.ascontiguousarray(a[o:o + n]), m, n, k)
+                r = ref[o:o + n]
+                ok = np.abs(got[o:o + n] - r) <= 1e-3 * np.abs(r) + 1e-5 * sa
+                assert ok.all(), (e, n, float(np.max(np.abs(got[o:o + n] - r))))
+            o += n
     finally:
         hip.evict(Segment.of(w))
 
