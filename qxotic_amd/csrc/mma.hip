@@ -120,20 +120,30 @@ template <int DT, int RT, int CT>
 __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, GemmAct A, int m, int n,
                                                                  float* __restrict__ c, int ldc, int nrb, int ncb,
                                                                  int64_t tiles, Groups gp, int sb_per,
-                                                                 int64_t c_slice, Epi ep) {
+                                                                 int64_t c_slice, Epi ep, int xsplit) {
     using S = Stage<DT, RT, CT>;
     constexpr int TW = S::TW, BN = S::BN, NCS = S::NCS;
     extern __shared__ __align__(1024) unsigned char smem[];
     __shared__ float q40_srow[DT == Q4_0 || DT == Q8_0 ? MMA_WAVES * RT * 32 : 1];   // 2^-s of each row
 
     // XCD-aware placement (tile_of_block); grouped calls take their tiles in expert-major order
+    // xsplit > 0 (ungrouped): the last xsplit tiles of each XCD's run are split into two workgroups of 32
+    // tokens each (sub 0 and 1), dispatched after the run's whole tiles, so that a last partial round of whole
+    // tiles becomes one of half tiles
     const int total = nrb * ncb;
-    const int lin = tile_of_block(gp.map64 != nullptr, total);
+    int lin, sub = -1;
+    if (xsplit > 0) {
+        const int T8 = (total + 7) / 8, x = (int) blockIdx.x % 8, i = (int) blockIdx.x / 8, nf = T8 - xsplit;
+        lin = x * T8 + (i < nf ? i : nf + (i - nf) / 2);
+        if (i >= nf) sub = (i - nf) & 1;
+    } else {
+        lin = tile_of_block(gp.map64 != nullptr, total);
+    }
     if (lin >= total) return;
     int rb = lin / ncb, cb = lin % ncb;
     if (gp.map64 != nullptr && grouped_tile(gp, lin, nrb, &rb, &cb) < 0) return;   // before any barrier
     const int64_t T0 = (int64_t) rb * TW;        // first row tile of the workgroup
-    const int n0 = cb * BN;                      // first token slot of GemmAct
+    const int n0 = cb * BN + (sub > 0 ? 32 : 0); // first token slot of GemmAct
 
     const int lane = threadIdx.x & 63, r = lane & 31, q = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -157,9 +167,9 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
         nvalid = __builtin_amdgcn_readfirstlane(gp.off[e + 1]) - crow0;
         if (gp.bias != nullptr) ep.bias = gp.bias + (int64_t) e * gp.gm;
     }
-    // valid tokens of this slot block all in its first 32 slots: the second token tile is neither copied
-    // nor computed (its columns are never stored)
-    const bool half = CT == 2 && nvalid - (n0 - slot0) <= 32;
+    // valid tokens of this slot block all in its first 32 slots, or one half of a split tile: the second token
+    // tile is neither copied nor computed nor stored
+    const bool half = CT == 2 && (sub >= 0 || nvalid - (n0 - slot0) <= 32);
 
     // ---- global -> LDS copy of one stage. Every wave issues a fixed set of 1 KB pieces: the weight chunks
     // of its own row tile, the activation codes of K-steps 2·wave and 2·wave + 1, and one of the small
@@ -218,11 +228,14 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
         } else {
             if (wave == 0 && h2 == 1 && lane < 4 * TW) dma16(h_src + (int64_t) g * 32 * 2, buf + S::H_OFF);
         }
-        // block scales: 4 blocks x BN tokens (f32)
-        if (wave == 2) dma16(dx_src + (int64_t) (4 * st) * A.NP, buf + S::DX_OFF);
-        // sums: Q4_K needs them at the super-block's end (odd stage), Q6_K at its start (even stage)
+        // block scales: 4 blocks x BN tokens (f32; lane l: block l / 16, tokens 4·(l % 16)..); a half tile
+        // copies its 32 tokens only (the second half of the call's last slot block has no slots past it)
+        if (wave == 2 && (!half || (lane & 15) < 8)) dma16(dx_src + (int64_t) (4 * st) * A.NP, buf + S::DX_OFF);
+        // sums: Q4_K needs them at the super-block's end (odd stage), Q6_K at its start (even stage); a plane's
+        // piece p holds tokens 32p.. (two pieces) or a token per lane (one piece)
         if constexpr (S::SW > 0) {
-            if ((DT == Q4_0 || (DT == Q4_K) == (h2 == 1)) && (SPC == 2 || wave == 1 || wave == 3))
+            if ((DT == Q4_0 || (DT == Q4_K) == (h2 == 1)) && (SPC == 2 || wave == 1 || wave == 3) &&
+                (!half || (SPC == 2 ? s_p == 0 : lane < 32)))
                 dma16(s_src + (int64_t) g * A.NP * SWB, buf + S::S_OFF + s_pl * BN * SWB + s_p * 1024);
         }
     };
@@ -707,7 +720,7 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
 #pragma unroll
     for (int j = 0; j < CT; j++) {
         const int t = n0 + 32 * j + r, tl = t - slot0;
-        if (tl >= nvalid) continue;
+        if (tl >= nvalid || (half && j > 0)) continue;
         const float sc = A.es[t];
         float* ct = c + (int64_t) blockIdx.y * c_slice + (int64_t) (crow0 + tl) * ldc;
 #pragma unroll
@@ -751,6 +764,24 @@ static void split_plan(int total, int nsb, int* ns, int* sb_per) {
     *ns = want > 1 ? (nsb + *sb_per - 1) / *sb_per : 1;
 }
 
+// Workgroups of two resident per CU take about the same CU time whether a CU holds one or two, so a call
+// takes ceil(tiles per CU) tile times: Q4_K 14336x4096 at n = 448, 512 and 576 (784, 896 and 1008 tiles)
+// all ran 128 us. Each XCD takes a contiguous run of T8 = ceil(tiles / 8) tiles over its CUs; when that
+// leaves r <= CUs / 2 tiles for a last partial round, those r tiles run as 2r half tiles (32 tokens) instead,
+// one per CU. Returns r, or 0 for no split.
+static int tail_split(int total) {
+    static std::atomic<int> cus[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    int n = cus[dev].load(std::memory_order_relaxed);
+    if (n == 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 8) return 0;
+        cus[dev].store(n, std::memory_order_relaxed);
+    }
+    const int cu8 = n / 8, T8 = (total + 7) / 8, r = T8 % cu8;
+    return r > 0 && 2 * r <= cu8 ? r : 0;
+}
+
 template <int DT, int RT, int CT>
 static hipError_t kq_go(const WeightView& w, const GemmAct& A, int m, int n, float* c, int ldc, hipStream_t st,
                         const Groups& gp = Groups{}, float* part = nullptr, const Epi& ep = Epi{}) {
@@ -769,12 +800,14 @@ static hipError_t kq_go(const WeightView& w, const GemmAct& A, int m, int n, flo
     int ns = 1, sb_per = 0;
     if (part != nullptr) split_plan(total, A.Kp / 256, &ns, &sb_per);
     if (ns == 1) {
-        kq_gemm_kernel<DT, RT, CT><<<grid, MMA_THREADS, lds, st>>>(w, A, m, n, c, ldc, nrb, ncb, tiles, gp, 0, 0, ep);
+        const int xs = gp.map64 == nullptr ? tail_split(total) : 0;
+        kq_gemm_kernel<DT, RT, CT><<<grid + 8 * xs, MMA_THREADS, lds, st>>>(w, A, m, n, c, ldc, nrb, ncb, tiles, gp, 0,
+                                                                            0, ep, xs);
         return hipGetLastError();
     }
     const int64_t slice = (int64_t) n * m;
     kq_gemm_kernel<DT, RT, CT><<<dim3(grid, ns), MMA_THREADS, lds, st>>>(w, A, m, n, part, m, nrb, ncb, tiles, gp,
-                                                                         sb_per, slice, Epi{});
+                                                                         sb_per, slice, Epi{}, 0);
     split_reduce_kernel<<<dim3((m + 255) / 256, n), 256, 0, st>>>(part, ns, slice, m, c, ldc, ep);
     return hipGetLastError();
 }

@@ -344,6 +344,29 @@ def test_prefill_ragged_shapes(hip, oracle, dt):
         assert tier1(got, ref, sa).all(), (O.NAMES[dt], m, n, k)
 
 
+@pytest.mark.parametrize("dt", [O.Q4_K, O.Q6_K, O.MXFP4, O.Q8_0, O.Q4_0])
+def test_prefill_tail_split_tiles(hip, oracle, dt):
+    """Grids whose last partial round of tiles runs as half tiles: 1024 rows x 65 slot blocks give 65 tiles per
+    XCD, one of them split into two 32-token workgroups. Every token's result equals that of the n = 4096 grid
+    (64 tiles per XCD, none split) bit for bit, and a row sample meets tier 1. n = 4150 leaves the second half
+    of the last slot block partly valid, n = 4110 leaves it empty."""
+    m, k = 1024, 256
+    w = oracle.quantize(dt, oracle.normal(0x7A11 ^ dt, (m, k), 0.0, 0.02))
+    a = oracle.outliers(0x7A12, (4150, k))
+    base = run_mm(hip, dt, w, np.ascontiguousarray(a[:4096]), m, 4096, k)
+    rows = np.sort(np.random.default_rng(dt + 7).choice(m, 48, replace=False))
+    ws = np.ascontiguousarray(w[rows])
+    for n in (4150, 4110):
+        say(f"tail split {O.NAMES[dt]} m={m} n={n} k={k}")
+        an = np.ascontiguousarray(a[:n])
+        got = run_mm(hip, dt, w, an, m, n, k)
+        assert np.array_equal(bits(got[:4096]), bits(base)), (O.NAMES[dt], n)
+        ref = oracle.mm_int8(dt, ws, an, len(rows), n, k)
+        _, sa = oracle.mm_ref(dt, ws, an, len(rows), n, k)
+        ok = tier1(got[:, rows], ref, sa)
+        assert ok.all(), (O.NAMES[dt], n, int((~ok).sum()))
+
+
 @pytest.mark.parametrize("dt", O.QUANT_TYPES)
 def test_prefill_error_floor(hip, oracle, dt):
     """The GEMM stays at its arithmetic's error floor, far inside tier 1: max |gpu - oracle| / sum|w*a| <= 2e-6
