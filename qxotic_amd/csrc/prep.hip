@@ -156,6 +156,7 @@ template <int CTRL> JAMHIP_DEV float dppf(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
 }
 constexpr int PREP_MAX_KP = 65536;   // LDS: Kp/32 + Kp/16 floats per slot
+constexpr int PREP_GRID = 1024;      // a multiple of 8 (XCDs)
 
 // Exclusive scans of (x, y) over the lanes of the first wave (wide false) or of the 256 lanes of the
 // workgroup (wide true: every thread must call it; two barriers); lane e holds expert e; *tot = the sums.
@@ -185,17 +186,20 @@ JAMHIP_DEV int2 block_scan2(int x, int y, int2* tot, int2* sm, bool wide) {
     return make_int2(bx + sx - x, by + sy - y);
 }
 
-// Token slot t of the fused grouped prep, from the expert counts on the device. Expert e keeps c_e rows: its
-// count, clamped so that the experts' rows fit rows_cap in expert order (rows past rows_cap are dropped, as
-// by launch_moe_offsets); its C rows start at oc_e (exclusive scan of c), and an expert with rows owns
-// roundup(c_e, 64) token slots from p_e (exclusive scan). Returns slot t's source row, oc_e + (t - p_e) when
-// t - p_e < c_e, else -1 (padding, or past every expert). *f1: the owner has 1..7 rows, below jam's F2 band
-// gate n >= JAM_VNNI_MIN_SEQ = 8 (jam.c:492, 570; jam_kquant.h:23). With pub set, also writes off[0..E] (and off_out), poff64[0..E] and map64[0..cap64) (the
-// owner of each 64-slot block, -1 past the last). Every thread of the workgroup must call it.
-JAMHIP_DEV int fused_slot(const PrepGroups& pg, int t, bool pub, bool* f1) {
+// The fused grouped prep's expert table, from the expert counts on the device (one expert per thread: the
+// first wave for up to 64 experts, else the workgroup). Expert e keeps c_e rows: its count, clamped so that
+// the experts' rows fit rows_cap in expert order (rows past rows_cap are dropped, as by launch_moe_offsets);
+// its C rows start at oc_e (exclusive scan of c), and an expert with rows owns roundup(c_e, 64) token slots
+// from p_e (exclusive scan), so the slots [0, P) are all owned. Returns P. With pub set, also writes
+// off[0..E] (and off_out), poff64[0..E] and map64[0..cap64) (the owner of each 64-slot block, -1 past the
+// last). Every thread of the workgroup must call it.
+struct SlotOwner {
+    int oc = 0, c = 0, p64 = 0, a64 = 0;
+};
+JAMHIP_DEV int fused_scan(const PrepGroups& pg, bool pub, SlotOwner* so) {
     __shared__ int2 sm[4];
-    __shared__ int own[2];   // slot t's source row and its expert's row count
-    const bool wide = pg.E > 64;   // up to 64 experts: the first wave alone, no barrier until the last
+    __shared__ int ptot;
+    const bool wide = pg.E > 64;   // up to 64 experts: the first wave alone
     if (wide || threadIdx.x < 64) {
         const int e = threadIdx.x, nt = wide ? 256 : 64;
         const bool in = e < pg.E;
@@ -205,14 +209,10 @@ JAMHIP_DEV int fused_slot(const PrepGroups& pg, int t, bool pub, bool* f1) {
         const int o = block_scan2(c0, 0, &tot, sm, wide).x;
         const int c = in ? max(0, min(c0, pg.rows_cap - o)) : 0;
         const int a64 = (c + 63) / 64 * 64;
-        if (threadIdx.x == 0) own[0] = -1, own[1] = 0;
-        // ordered before the owner's stores below: by the scan's barriers, or within the one wave
         const int2 s = block_scan2(c, a64, &tot, sm, wide);
         const int oc = s.x, p64 = s.y;
-        if (a64 > 0 && t >= p64 && t < p64 + a64) {
-            own[0] = t - p64 < c ? oc + (t - p64) : -1;
-            own[1] = c;
-        }
+        so->oc = oc, so->c = c, so->p64 = p64, so->a64 = a64;
+        if (threadIdx.x == 0) ptot = tot.y;
         if (pub) {
             if (in) {
                 pg.off[e] = oc;
@@ -229,8 +229,7 @@ JAMHIP_DEV int fused_slot(const PrepGroups& pg, int t, bool pub, bool* f1) {
         }
     }
     __syncthreads();
-    *f1 = own[1] < 8;
-    return own[0];
+    return ptot;
 }
 
 // F2 exactly as f2_lane: the block max over both halves, d = max/127, inv = 127/max, q = sat8(rne(x·inv))
@@ -247,146 +246,169 @@ __global__ void __launch_bounds__(256) gemm_prep(const float* __restrict__ a, in
                                                  const int* __restrict__ goff, const int* __restrict__ gpoff, int vec,
                                                  PrepGroups pg) {
     extern __shared__ float lsm[];   // [Kp/32] block scales, [Kp/16] per-16 sums, [4] wave maxima
+    __shared__ int own[2];           // fused grouped mode: the slot's source row and its expert's row count
     float* ldb = lsm;
     float* lxs = lsm + (Kp >> 5);
     float* lmx = lxs + (Kp >> 4);
-    // workgroup i runs on XCD i % 8: give each XCD a contiguous run of token slots, so that the slots sharing
-    // an output line (the codes, block scales and sums are token-interleaved) are written through one L2
-    const int t = (int) (blockIdx.x % 8) * (NP >> 3) + (int) (blockIdx.x >> 3);
     const int nbk = k >> 5, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    // fused grouped mode (counts on the device): F1 codes for an expert of 1..7 rows, else F2
-    bool f1 = false;
-    const int src = pg.counts != nullptr ? fused_slot(pg, t, blockIdx.x == 0, &f1) : prep_src(t, n, gmap, goff, gpoff);
-    // a padding slot (past n, or past its expert's rows) is left unwritten: the GEMM's token column for it is
-    // computed but never stored, and no other column reads it
-    if (src < 0) return;
-    const int hh = lane & 1;   // which half of its block the lane holds
-    float m2 = 0.0f;
-    typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-    // one 16-element half of one block per lane (lanes 2b', 2b' + 1 hold a block): 128 blocks per round of the
-    // workgroup, two rounds' loads in flight; blocks past k (up to Kp) quantize zeros
-    const int nbp = Kp >> 5;
-    const float* row = a + (int64_t) src * lda;
-    for (int r0 = threadIdx.x >> 1; r0 < nbp; r0 += 256) {
-        float xr[2][16];
+    // the slots that can hold rows: [0, n) dense, [0, P) fused grouped (P from the counts), all NP otherwise
+    SlotOwner so;
+    const int P = pg.counts != nullptr ? fused_scan(pg, blockIdx.x == 0, &so) : gmap != nullptr ? NP : n;
+    // workgroup i runs on XCD i % 8: each XCD takes a contiguous run of P8 slots (a multiple of 8), its
+    // workgroups the run's slots in turn, so that the slots sharing an output line (the codes, block scales and
+    // sums are token-interleaved) are written through one L2
+    const int x = (int) (blockIdx.x % 8), nw = (int) (gridDim.x >> 3), P8 = ((P + 7) / 8 + 7) & ~7;
+    const int t_end = min((x + 1) * P8, P);
+    for (int t = x * P8 + (int) (blockIdx.x >> 3); t < t_end; t += nw) {
+        // fused grouped mode (counts on the device): F1 codes for an expert of 1..7 rows, else F2
+        bool f1 = false;
+        int src;
+        if (pg.counts != nullptr) {
+            if (so.a64 > 0 && t >= so.p64 && t < so.p64 + so.a64) {   // exactly one owner for t < P
+                own[0] = t - so.p64 < so.c ? so.oc + (t - so.p64) : -1;
+                own[1] = so.c;
+            }
+            __syncthreads();
+            src = own[0];
+            f1 = own[1] < 8;
+        } else {
+            src = prep_src(t, n, gmap, goff, gpoff);
+        }
+        // a padding slot (past n, or past its expert's rows) is left unwritten: the GEMM's token column for it
+        // is computed but never stored, and no other column reads it
+        if (src >= 0) {
+            const int hh = lane & 1;   // which half of its block the lane holds
+            float m2 = 0.0f;
+            typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+            // one 16-element half of one block per lane (lanes 2b', 2b' + 1 hold a block): 128 blocks per round
+            // of the workgroup, two rounds' loads in flight; blocks past k (up to Kp) quantize zeros
+            const int nbp = Kp >> 5;
+            const float* row = a + (int64_t) src * lda;
+            for (int r0 = threadIdx.x >> 1; r0 < nbp; r0 += 256) {
+                float xr[2][16];
 #pragma unroll
-        for (int u = 0; u < 2; u++) {
-            const int b = r0 + 128 * u;
+                for (int u = 0; u < 2; u++) {
+                    const int b = r0 + 128 * u;
 #pragma unroll
-            for (int i = 0; i < 16; i++) xr[u][i] = 0.0f;
-            if (b < nbk) {
-                // MXO: elements 8hh..8hh+7 and 16+8hh..16+8hh+7 (the order the GEMM pairs them in); else 16hh..16hh+15
-                const float* p0 = row + 32 * b + (MXO ? 8 * hh : 16 * hh);
-                const float* p1 = p0 + (MXO ? 16 : 8);
-                if (vec) {   // a and lda 16-byte aligned (the launcher checks)
+                    for (int i = 0; i < 16; i++) xr[u][i] = 0.0f;
+                    if (b < nbk) {
+                        // MXO: elements 8hh..8hh+7 and 16+8hh..16+8hh+7 (the order the GEMM pairs them in); else
+                        // 16hh..16hh+15
+                        const float* p0 = row + 32 * b + (MXO ? 8 * hh : 16 * hh);
+                        const float* p1 = p0 + (MXO ? 16 : 8);
+                        if (vec) {   // a and lda 16-byte aligned (the launcher checks)
 #pragma unroll
-                    for (int v = 0; v < 2; v++) {
-                        const float4 f0 = *reinterpret_cast<const float4*>(p0 + 4 * v);
-                        const float4 f1 = *reinterpret_cast<const float4*>(p1 + 4 * v);
-                        xr[u][4 * v + 0] = f0.x, xr[u][4 * v + 1] = f0.y, xr[u][4 * v + 2] = f0.z, xr[u][4 * v + 3] = f0.w;
-                        xr[u][8 + 4 * v + 0] = f1.x, xr[u][8 + 4 * v + 1] = f1.y, xr[u][8 + 4 * v + 2] = f1.z,
-                                         xr[u][8 + 4 * v + 3] = f1.w;
+                            for (int v = 0; v < 2; v++) {
+                                const float4 f0 = *reinterpret_cast<const float4*>(p0 + 4 * v);
+                                const float4 f1 = *reinterpret_cast<const float4*>(p1 + 4 * v);
+                                xr[u][4 * v + 0] = f0.x, xr[u][4 * v + 1] = f0.y;
+                                xr[u][4 * v + 2] = f0.z, xr[u][4 * v + 3] = f0.w;
+                                xr[u][8 + 4 * v + 0] = f1.x, xr[u][8 + 4 * v + 1] = f1.y;
+                                xr[u][8 + 4 * v + 2] = f1.z, xr[u][8 + 4 * v + 3] = f1.w;
+                            }
+                        } else {
+#pragma unroll
+                            for (int i = 0; i < 8; i++) xr[u][i] = p0[i], xr[u][8 + i] = p1[i];
+                        }
                     }
-                } else {
+                }
 #pragma unroll
-                    for (int i = 0; i < 8; i++) xr[u][i] = p0[i], xr[u][8 + i] = p1[i];
+                for (int u = 0; u < 2; u++) {
+                    const int b = r0 + 128 * u;
+                    if (b >= nbp) break;   // lane pairs stay together: b is the same for both lanes of a block
+                    const float* x = xr[u];
+                    float mx = 0.0f;
+#pragma unroll
+                    for (int i = 0; i < 16; i++) mx = fmaxf(mx, fabsf(x[i]));
+                    mx = fmaxf(mx, dppf<0xB1>(mx));   // the block's other half (lane ^ 1)
+                    const float db = mx / 127.0f;
+                    float qf[16];
+                    if (f1) {
+                        // F1 (jam_q8_0_requant, jam_kernels_generic.c:71-94): id = 1/d, q = clamp(rint(x·id));
+                        // a NaN product lands on -128 like LONG_MIN does
+                        const float id = db > 0.0f ? 1.0f / db : 0.0f;
+#pragma unroll
+                        for (int i = 0; i < 16; i++) qf[i] = fminf(fmaxf(rintf(x[i] * id), -128.0f), 127.0f);
+                    } else {
+                        const float inv = mx > 0.0f ? 127.0f / mx : 0.0f;
+#pragma unroll
+                        for (int i = 0; i < 16; i++) {
+                            const float p = x[i] * inv;
+                            const bool ok = p > -2147483648.0f && p < 2147483648.0f;
+                            qf[i] = ok ? fminf(fmaxf(rintf(p), -128.0f), 127.0f) : -128.0f;
+                        }
+                    }
+                    // the lane's two (K-step, half) planes: 8 f16 (16 bytes) each at the slot
+#pragma unroll
+                    for (int ks = 0; ks < 2; ks++) {
+                        half8 hv;
+#pragma unroll
+                        for (int i = 0; i < 8; i++) {
+                            if constexpr (!MXO) hv[perm8(i)] = (_Float16) qf[8 * ks + i];   // elements 16hh + 8ks + i
+                            else hv[2 * (i & 3) + (i >> 2)] = (_Float16) qf[8 * (i >> 2) + 4 * ks + (i & 3)];
+                        }
+                        *reinterpret_cast<half8*>(bq + ((int64_t) (2 * (2 * b + ks) + hh) * NP + t) * 8) = hv;
+                    }
+                    if (hh == 0) ldb[b] = db;
+                    if (SK != 0 && f1) {
+                        // F1's offset terms take the integer code sums times d (Q4_K and Q4_0 fl(asum·ad) per
+                        // 32, Q6_K's −32 per 16): the sums slot holds Σq·d, the 32-sum in the block's first half
+                        float s16 = 0.0f;
+#pragma unroll
+                        for (int i = 0; i < 16; i++) s16 += qf[i];   // exact: |Σ| <= 2048
+                        const float s32 = s16 + dppf<0xB1>(s16);
+                        const float xs = SK == 1 ? s32 * db : s16 * db;
+                        lxs[2 * b + hh] = SK == 1 && hh == 1 ? 0.0f : xs;
+                        m2 = fmaxf(m2, fabsf(xs));
+                    } else if constexpr (SK != 0) {
+                        // per-16 sum in _mm512_reduce_add_ps's pairing: distance 8, 4, 2, 1
+                        float s8[8];
+#pragma unroll
+                        for (int i = 0; i < 8; i++) s8[i] = x[i] + x[i + 8];
+#pragma unroll
+                        for (int i = 0; i < 4; i++) s8[i] = s8[i] + s8[i + 4];
+                        s8[0] = s8[0] + s8[2];
+                        s8[1] = s8[1] + s8[3];
+                        const float xs16 = s8[0] + s8[1];
+                        lxs[2 * b + hh] = xs16;
+                        const float other = dppf<0xB1>(xs16);   // the block's other half
+                        m2 = fmaxf(m2, SK == 1 ? fabsf(hh == 0 ? xs16 + other : other + xs16) : fabsf(xs16));
+                    }
+                }
+            }
+            if constexpr (SK != 0) {
+#pragma unroll
+                for (int o = 32; o > 0; o >>= 1) m2 = fmaxf(m2, __shfl_xor(m2, o));
+                if (lane == 0) lmx[wave] = m2;
+            }
+            __syncthreads();
+            // the slot's power of two: the largest |sum| lands in [2^13, 2^14); zero or non-finite sums keep 2^0
+            int ex = 0;
+            if constexpr (SK != 0) {
+                const float mx = fmaxf(fmaxf(lmx[0], lmx[1]), fmaxf(lmx[2], lmx[3]));
+                if (mx > 0.0f && mx <= 3.0e38f) {
+                    frexpf(mx, &ex);
+                    ex -= 14;
+                }
+            }
+            const float down = ldexpf(1.0f, -ex);
+            if (threadIdx.x == 0) es[t] = ldexpf(1.0f, ex);
+            auto put = [&](int64_t o, float v) {
+                const F16Pair p = split_f16(v);
+                shi[o] = p.hi;
+                slo[o] = p.lo;
+            };
+            for (int b = threadIdx.x; b < (Kp >> 5); b += 256) {
+                dx[(int64_t) b * NP + t] = ldb[b] * down;
+                const float x0 = lxs[2 * b], x1 = lxs[2 * b + 1];
+                if constexpr (SK == 1) put(((int64_t) (b >> 3) * NP + t) * 8 + (b & 7), (x0 + x1) * down);
+                if constexpr (SK == 2) {
+                    put(((int64_t) (b >> 3) * NP + t) * 16 + 2 * (b & 7), x0 * down);
+                    put(((int64_t) (b >> 3) * NP + t) * 16 + 2 * (b & 7) + 1, x1 * down);
                 }
             }
         }
-#pragma unroll
-        for (int u = 0; u < 2; u++) {
-            const int b = r0 + 128 * u;
-            if (b >= nbp) break;   // lane pairs stay together: b is the same for both lanes of a block
-            const float* x = xr[u];
-            float mx = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 16; i++) mx = fmaxf(mx, fabsf(x[i]));
-            mx = fmaxf(mx, dppf<0xB1>(mx));   // the block's other half (lane ^ 1)
-            const float db = mx / 127.0f;
-            float qf[16];
-            if (f1) {
-                // F1 (jam_q8_0_requant, jam_kernels_generic.c:71-94): id = 1/d, q = clamp(rint(x·id)); a NaN
-                // product lands on -128 like LONG_MIN does
-                const float id = db > 0.0f ? 1.0f / db : 0.0f;
-#pragma unroll
-                for (int i = 0; i < 16; i++) qf[i] = fminf(fmaxf(rintf(x[i] * id), -128.0f), 127.0f);
-            } else {
-                const float inv = mx > 0.0f ? 127.0f / mx : 0.0f;
-#pragma unroll
-                for (int i = 0; i < 16; i++) {
-                    const float p = x[i] * inv;
-                    qf[i] = !(p > -2147483648.0f && p < 2147483648.0f) ? -128.0f
-                                                                        : fminf(fmaxf(rintf(p), -128.0f), 127.0f);
-                }
-            }
-            // the lane's two (K-step, half) planes: 8 f16 (16 bytes) each at the slot
-#pragma unroll
-            for (int ks = 0; ks < 2; ks++) {
-                half8 hv;
-#pragma unroll
-                for (int i = 0; i < 8; i++) {
-                    if constexpr (!MXO) hv[perm8(i)] = (_Float16) qf[8 * ks + i];   // elements 16hh + 8ks + i
-                    else hv[2 * (i & 3) + (i >> 2)] = (_Float16) qf[8 * (i >> 2) + 4 * ks + (i & 3)];
-                }
-                *reinterpret_cast<half8*>(bq + ((int64_t) (2 * (2 * b + ks) + hh) * NP + t) * 8) = hv;
-            }
-            if (hh == 0) ldb[b] = db;
-            if (SK != 0 && f1) {
-                // F1's offset terms take the integer code sums times d (Q4_K and Q4_0 fl(asum·ad) per 32, Q6_K's
-                // −32 per 16): the sums slot holds Σq·d, the 32-sum in the block's first half
-                float s16 = 0.0f;
-#pragma unroll
-                for (int i = 0; i < 16; i++) s16 += qf[i];   // exact: |Σ| <= 2048
-                const float s32 = s16 + dppf<0xB1>(s16);
-                const float xs = SK == 1 ? s32 * db : s16 * db;
-                lxs[2 * b + hh] = SK == 1 && hh == 1 ? 0.0f : xs;
-                m2 = fmaxf(m2, fabsf(xs));
-            } else if constexpr (SK != 0) {
-                // per-16 sum in _mm512_reduce_add_ps's pairing: distance 8, 4, 2, 1
-                float s8[8];
-#pragma unroll
-                for (int i = 0; i < 8; i++) s8[i] = x[i] + x[i + 8];
-#pragma unroll
-                for (int i = 0; i < 4; i++) s8[i] = s8[i] + s8[i + 4];
-                s8[0] = s8[0] + s8[2];
-                s8[1] = s8[1] + s8[3];
-                const float xs16 = s8[0] + s8[1];
-                lxs[2 * b + hh] = xs16;
-                const float other = dppf<0xB1>(xs16);   // the block's other half
-                m2 = fmaxf(m2, SK == 1 ? fabsf(hh == 0 ? xs16 + other : other + xs16) : fabsf(xs16));
-            }
-        }
-    }
-    if constexpr (SK != 0) {
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) m2 = fmaxf(m2, __shfl_xor(m2, o));
-        if (lane == 0) lmx[wave] = m2;
-    }
-    __syncthreads();
-    // the slot's power of two: the largest |sum| lands in [2^13, 2^14); zero or non-finite sums keep 2^0
-    int ex = 0;
-    if constexpr (SK != 0) {
-        const float mx = fmaxf(fmaxf(lmx[0], lmx[1]), fmaxf(lmx[2], lmx[3]));
-        if (mx > 0.0f && mx <= 3.0e38f) {
-            frexpf(mx, &ex);
-            ex -= 14;
-        }
-    }
-    const float down = ldexpf(1.0f, -ex);
-    if (threadIdx.x == 0) es[t] = ldexpf(1.0f, ex);
-    auto put = [&](int64_t o, float v) {
-        const F16Pair p = split_f16(v);
-        shi[o] = p.hi;
-        slo[o] = p.lo;
-    };
-    for (int b = threadIdx.x; b < (Kp >> 5); b += 256) {
-        dx[(int64_t) b * NP + t] = ldb[b] * down;
-        const float x0 = lxs[2 * b], x1 = lxs[2 * b + 1];
-        if constexpr (SK == 1) put(((int64_t) (b >> 3) * NP + t) * 8 + (b & 7), (x0 + x1) * down);
-        if constexpr (SK == 2) {
-            put(((int64_t) (b >> 3) * NP + t) * 16 + 2 * (b & 7), x0 * down);
-            put(((int64_t) (b >> 3) * NP + t) * 16 + 2 * (b & 7) + 1, x1 * down);
-        }
+        __syncthreads();   // the LDS (and own) is the next slot's
     }
 }
 
@@ -421,6 +443,8 @@ static hipError_t prep_np(int dt, const float* a, int lda, int n, int NP, int k,
     const int vec = ((reinterpret_cast<uintptr_t>(a) & 15) == 0 && (lda & 3) == 0) ? 1 : 0;
     const size_t lds = ((size_t) (Kp / 32) + (size_t) (Kp / 16) + 4) * sizeof(float);
     const int kind = dt == MXFP4 ? 3 : sk;
+    // at most PREP_GRID workgroups (all resident), each looping over its XCD's slots
+    const unsigned grid = (unsigned) (NP < PREP_GRID ? NP : PREP_GRID);
     const void* fn = kind == 1 ? (const void*) gemm_prep<1, false> : kind == 2 ? (const void*) gemm_prep<2, false>
                    : kind == 3 ? (const void*) gemm_prep<0, true> : (const void*) gemm_prep<0, false>;
     // the LDS limit is raised once per kernel; threads racing here both set the same value
@@ -431,10 +455,10 @@ static hipError_t prep_np(int dt, const float* a, int lda, int n, int NP, int k,
         if (e != hipSuccess) return e;
         attr[kind].store(true, std::memory_order_release);
     }
-    if (kind == 1) gemm_prep<1, false><<<NP, 256, lds, st>>>(a, lda, n, k, Kp, NP, bq, dx, shi, slo, es, gmap, goff, gpoff, vec, pg);
-    else if (kind == 2) gemm_prep<2, false><<<NP, 256, lds, st>>>(a, lda, n, k, Kp, NP, bq, dx, shi, slo, es, gmap, goff, gpoff, vec, pg);
-    else if (kind == 3) gemm_prep<0, true><<<NP, 256, lds, st>>>(a, lda, n, k, Kp, NP, bq, dx, shi, slo, es, gmap, goff, gpoff, vec, pg);
-    else gemm_prep<0, false><<<NP, 256, lds, st>>>(a, lda, n, k, Kp, NP, bq, dx, shi, slo, es, gmap, goff, gpoff, vec, pg);
+    if (kind == 1) gemm_prep<1, false><<<grid, 256, lds, st>>>(a, lda, n, k, Kp, NP, bq, dx, shi, slo, es, gmap, goff, gpoff, vec, pg);
+    else if (kind == 2) gemm_prep<2, false><<<grid, 256, lds, st>>>(a, lda, n, k, Kp, NP, bq, dx, shi, slo, es, gmap, goff, gpoff, vec, pg);
+    else if (kind == 3) gemm_prep<0, true><<<grid, 256, lds, st>>>(a, lda, n, k, Kp, NP, bq, dx, shi, slo, es, gmap, goff, gpoff, vec, pg);
+    else gemm_prep<0, false><<<grid, 256, lds, st>>>(a, lda, n, k, Kp, NP, bq, dx, shi, slo, es, gmap, goff, gpoff, vec, pg);
     return hipGetLastError();
 }
 

@@ -21,8 +21,10 @@ def say(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-CASES = [   # (m, k, n): decode F1, split-K decode, F2 decode, matrix cores (+ split K), tail rows
+CASES = [   # (m, k, n): decode F1, split-K decode, F2 decode, matrix cores (+ split K), tail rows, and matrix
+    # cores whose last round runs as half tiles (1024 x 4150: 65 tiles per XCD)
     (104, 1024, 1), (100, 9216, 4), (104, 1024, 8), (100, 1024, 16), (100, 1024, 100), (4096, 4096, 64),
+    (1024, 256, 4150),
 ]
 
 
