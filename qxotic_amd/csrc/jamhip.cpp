@@ -1016,6 +1016,7 @@ jamhip_ctx* create_ctx(int device, std::string* err) {
         return nullptr;
     }
     (void) noalloc_scratch_init(dev);   // a failure is reported by jamhip_mm_device_noalloc itself
+    gemm_tail_prime(dev);
     auto* ctx = new jamhip_ctx();
     ctx->device = dev;
     snprintf(ctx->arch, sizeof ctx->arch, "%s", prop.gcnArchName);

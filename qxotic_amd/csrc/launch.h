@@ -115,7 +115,9 @@ size_t gemm_act_bytes(int dt, int n, int k);
 bool gemm_prep_fits(int k);
 // jamhip_mm's activation upload by a copy kernel (bytes and both pointers 16-byte aligned; src device-visible
 // pinned host memory); hipErrorInvalidValue otherwise
-hipError_t launch_stage_copy(const void* src, void* dst, size_t bytes, hipStream_t st);   // the activation prep holds a slot's block scales and sums in LDS
+hipError_t launch_stage_copy(const void* src, void* dst, size_t bytes, hipStream_t st);
+// Caches device dev's CU count for the matrix-core GEMM's last-round balancing (called at context creation).
+void gemm_tail_prime(int dev);   // the activation prep holds a slot's block scales and sums in LDS
 hipError_t launch_gemm_prep(int dt, const float* a, int lda, int n, int k, void* scratch, GemmAct* out,
                             hipStream_t st);
 // Matrix-core GEMM over GemmAct (f16 MFMA on exact integer operands); hipErrorNotSupported for dtypes it

@@ -769,15 +769,18 @@ static void split_plan(int total, int nsb, int* ns, int* sb_per) {
 // all ran 128 us. Each XCD takes a contiguous run of T8 = ceil(tiles / 8) tiles over its CUs; when that
 // leaves r <= CUs / 2 tiles for a last partial round, those r tiles run as 2r half tiles (32 tokens) instead,
 // one per CU. Returns r, or 0 for no split.
+// CUs per device, filled by gemm_tail_prime at context creation (before any caller can be capturing a graph)
+static std::atomic<int> g_cus[64];
+void gemm_tail_prime(int dev) {
+    int n = 0;
+    if (dev >= 0 && dev < 64 && hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
+        g_cus[dev].store(n, std::memory_order_relaxed);
+}
 static int tail_split(int total) {
-    static std::atomic<int> cus[64];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-    int n = cus[dev].load(std::memory_order_relaxed);
-    if (n == 0) {
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 8) return 0;
-        cus[dev].store(n, std::memory_order_relaxed);
-    }
+    const int n = g_cus[dev].load(std::memory_order_relaxed);
+    if (n < 8) return 0;   // not primed: no split
     const int cu8 = n / 8, T8 = (total + 7) / 8, r = T8 % cu8;
     return r > 0 && 2 * r <= cu8 ? r : 0;
 }

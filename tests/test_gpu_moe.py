@@ -181,20 +181,23 @@ def test_mm_grouped_counts_past_rows_cap(hip, oracle):
         hip.evict(Segment.of(w))
 
 
-def test_mm_grouped_many_experts(hip, oracle):
-    """More than 64 experts (the slot map spans the prep workgroup's four waves), small and large experts mixed,
-    and counts past rows_cap: offsets are the clamped prefix sums, every kept row meets the bound."""
+@pytest.mark.parametrize("E", [150, 300])
+def test_mm_grouped_many_experts(hip, oracle, E):
+    """More than 64 experts, small and large experts mixed, and counts past rows_cap: offsets are the clamped
+    prefix sums, every kept row meets the bound. 150 experts take the one-launch prep (its expert table spans
+    the workgroup's four waves); 300 experts (more than the prep's 256) the offsets kernel and the F1 decode
+    kernel for the small experts."""
     import torch
     from qxotic_amd.jam import JAM, Segment
-    dt, m, k, E = O.Q4_K, 32, 256, 150
+    dt, m, k = O.Q4_K, 32, 256
     rng = np.random.default_rng(4242)
     counts = rng.integers(0, 16, E)
     counts[rng.permutation(E)[:30]] = 0
     counts[[3, 77, 140]] = [170, 130, 66]            # several 64-slot blocks each
-    counts[[5, 6, 90, 149]] = [1, 7, 2, 5]           # F1 experts (the last one loses its rows)
+    counts[[5, 6, 90, 149]] = [1, 7, 2, 5]           # F1 experts (E = 150: the last one loses its rows)
     total = int(counts.sum())
     rows_cap = total - 9                             # the last experts lose rows
-    assert rows_cap >= 8 * E
+    assert (rows_cap >= 8 * E) == (E <= 256)
     kept, o = [], 0
     for n in counts:
         kept.append(max(0, min(int(n), rows_cap - o)))
