@@ -135,13 +135,13 @@ JAMHIP_DEV int perm8(int j) { return j == 1 ? 2 : j == 2 ? 1 : j == 5 ? 6 : j ==
 
 int gemm_sums_kind(int dt) { return dt == Q4_K || dt == Q4_0 ? 1 : dt == Q6_K ? 2 : 0; }
 
-// One workgroup per token slot (256 threads, a thread per 16-element half of a block, 128 blocks per round):
-// jam's F2 quantization of the slot's activation row (f2_lane's arithmetic, bit-exact; the block's two
-// halves sit in adjacent lanes, which exchange their maxima), each half's codes stored as two 16-byte
+// A workgroup takes one token slot at a time (256 threads, a thread per 16-element half of a block, 128
+// blocks per round; at most PREP_GRID workgroups, each looping over its XCD's share of the slots that hold
+// rows): jam's F2 quantization of the slot's activation row (f2_lane's arithmetic, bit-exact; the block's
+// two halves sit in adjacent lanes, which exchange their maxima), each half's codes stored as two 16-byte
 // pieces of GemmAct::b's fragment order, the block scales and per-16 sums parked in LDS together with the
-// row's largest |sum| (SK 1:
-// per-32 xs0 + xs1, jam's fl(xs0 + xs1); SK 2: per-16; SK 0: none); then the slot's power of two from that
-// maximum and the scaled block scales and sums.
+// row's largest |sum| (SK 1: per-32 xs0 + xs1, jam's fl(xs0 + xs1); SK 2: per-16; SK 0: none); then the
+// slot's power of two from that maximum and the scaled block scales and sums.
 // Grouped form (gmap non-null): slot t belongs to expert gmap[t / 64] (-1: padding) and holds that
 // expert's row t - gpoff[e] (CSR row goff[e] + t - gpoff[e]) while that is below its row count.
 JAMHIP_DEV int prep_src(int t, int n, const int* gmap, const int* goff, const int* gpoff) {
