@@ -125,7 +125,7 @@ static void q4k_scales(const uint8_t* b, int sc[8], int mn[8]) {
     }
 }
 
-/* Q6_K element -> (6-bit code, int8 scale index) (jam_kernels_generic.c:217-252; SURVEY App. A). */
+/* Q6_K element -> (6-bit code, int8 scale index) (jam_kernels_generic.c:217-252). */
 static int q6k_code(const uint8_t* blk, int e, int* sidx) {
     int h = e / 128, j = (e % 128) / 32, l = e % 32;
     uint8_t qlb = blk[64 * h + (j & 1) * 32 + l];
