@@ -171,8 +171,8 @@ jamhip_status jamhip_quantize_device(jamhip_ctx* ctx, int flavour, const void* a
  * (CSR order, as Moe.dispatch gathers them); for each expert the result is jam_mm(W_e, A_e, C_e, m,
  * counts[e], k) under jam's routing (F1 below 8 rows, 16-row F2 bands from 8). rows_cap is the number
  * of rows A and C hold: rows past it (a prefix sum beyond rows_cap) are not computed and never read.
- * W is Q8_0, Q4_0, Q4_K, Q6_K or MXFP4; m must be a multiple of 16 and n_experts <= 1024 (else
- * JAMHIP_EUNSUPPORTED). Replaces the per-expert
+ * W is Q8_0, Q4_0, Q4_K, Q6_K or MXFP4; m must be a multiple of 16, n_experts <= 1024 and
+ * n_experts·rows_cap below 2^31 (else JAMHIP_EUNSUPPORTED). Replaces the per-expert
  * MatMul.gemm calls of Moe.dispatch's kernel closure (GptOss.java:295-314). */
 jamhip_status jamhip_mm_grouped(jamhip_ctx* ctx,
                                 const void* w, int wt, int ldw, int m, int n_experts,

@@ -832,6 +832,9 @@ jamhip_status mm_grouped_ex_impl(jamhip_ctx* ctx, const void* w, int wt, int ldw
     if (m % 16) return fail(ctx, JAMHIP_EUNSUPPORTED, "grouped: m must be a multiple of 16");
     if (n_experts > 1024) return fail(ctx, JAMHIP_EUNSUPPORTED, "grouped: at most 1024 experts");
     if ((int64_t) m * n_experts > INT32_MAX) return fail(ctx, JAMHIP_EUNSUPPORTED, "grouped: too many rows");
+    // the device prefix sums of the (rows_cap-clamped) counts stay below n_experts·rows_cap
+    if ((int64_t) rows_cap * n_experts >= INT32_MAX)
+        return fail(ctx, JAMHIP_EUNSUPPORTED, "grouped: n_experts·rows_cap must be below 2^31");
     Busy guard(ctx);
     if (!guard.ok) return fail(ctx, JAMHIP_EBUSY, "context busy");
     (void) hipSetDevice(ctx->device);

@@ -37,7 +37,7 @@ __global__ void __launch_bounds__(MOE_THREADS) moe_offsets_kernel(const int* __r
                                                                  int cap64, int* __restrict__ map8, int cap8) {
     __shared__ int tmp[MOE_THREADS];
     const int e = threadIdx.x;
-    const int c0 = e < E ? max(counts[e], 0) : 0;
+    const int c0 = e < E ? min(max(counts[e], 0), rows_cap) : 0;   // changes no clamped count; no overflow
     const int o = block_exclusive_scan(c0, tmp);
     const int c = e < E ? max(0, min(c0, rows_cap - o)) : 0;   // rows past rows_cap are dropped
     const int oc = block_exclusive_scan(c, tmp);
@@ -79,7 +79,7 @@ __global__ void __launch_bounds__(64) moe_offsets_wave_kernel(const int* __restr
                                                              int* __restrict__ poff8, int* __restrict__ map64,
                                                              int cap64, int* __restrict__ map8, int cap8) {
     const int e = threadIdx.x;
-    const int c0 = e < E ? max(counts[e], 0) : 0;
+    const int c0 = e < E ? min(max(counts[e], 0), rows_cap) : 0;   // changes no clamped count; no overflow
     const int o = wave_exclusive_scan(c0);
     const int c = e < E ? max(0, min(c0, rows_cap - o)) : 0;   // rows past rows_cap are dropped
     const int oc = wave_exclusive_scan(c);

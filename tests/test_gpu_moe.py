@@ -242,6 +242,7 @@ def test_grouped_status_codes(hip):
                                        kw.get("cap", 4), None)
     assert call(m=24) == JAM.EUNSUPPORTED           # m % 16
     assert call(E=2000) == JAM.EUNSUPPORTED         # more than 1024 experts
+    assert call(E=1024, cap=1 << 21) == JAM.EUNSUPPORTED   # n_experts·rows_cap = 2^31: the prefix sums overflow
     assert call(ldc=16) == JAM.EINVAL               # ldc < m
     assert call(cap=-1) == JAM.EINVAL
     assert call(dt=JAM.F16) == JAM.EUNSUPPORTED
