@@ -899,6 +899,8 @@ jamhip_status mm_grouped_ex_impl(jamhip_ctx* ctx, const void* w, int wt, int ldw
             (e = launch_gemv_grouped(wt, 1, wv, A, nullptr, 0, k, g, E, cap8, c, ldc, ctx->stream)) != hipSuccess)
             return hip_fail(ctx, e, "grouped: gemv launch");
     }
+    // fewer than 8 rows in all (decode-time MoE): no expert reaches the F2 bands, nothing more to launch
+    if (rows_cap < 8) return JAMHIP_OK;
     // experts with >= 8 rows: jam's F2 bands (m % 16 == 0: no float-dot tail rows)
     if (wt == MXFP4 && ctx->mx_native && mma_path(wt, k, wv) && m % 32 == 0) {   // opt-in native MX
         MxAct X;

@@ -181,6 +181,46 @@ def test_mm_grouped_counts_past_rows_cap(hip, oracle):
         hip.evict(Segment.of(w))
 
 
+@pytest.mark.parametrize("dt", [O.MXFP4, O.Q4_K])
+def test_mm_grouped_decode_sized(hip, oracle, dt):
+    """Decode-time MoE: fewer than 8 rows in all (one token, top-4 and a ragged cap), so every expert takes
+    jam's F1 and only the F1 decode launch runs; rows and the ldc gap past the counts stay untouched."""
+    import torch
+    from qxotic_amd.jam import JAM, Segment
+    m, k = 64, 512
+    for counts, rows_cap in (([1, 0, 1, 0, 1, 1], 4), ([0, 3, 0, 2, 0, 0, 1], 7)):
+        E = len(counts)
+        say(f"grouped decode-sized {O.NAMES[dt]} counts={counts} rows_cap={rows_cap}")
+        w_e = [oracle.quantize(dt, oracle.normal(0xDEC0 + 31 * e + dt, (m, k), 0.0, 0.02)) for e in range(E)]
+        w = np.ascontiguousarray(np.concatenate(w_e, axis=0))
+        a = oracle.outliers(0xDEC1 + E, (rows_cap, k))
+        assert hip.pin(Segment.of(w), dt, k, E * m) == JAM.OK, hip.last_error()
+        try:
+            c = torch.full((rows_cap + 1, m + 2), -3.0, dtype=torch.float32, device="cuda")
+            off = torch.zeros(E + 1, dtype=torch.int32, device="cuda")
+            a_dv = dev(a)   # held until the kernels that read it have run
+            counts_dv = dev(np.array(counts, np.int32))
+            torch.cuda.synchronize()   # torch's fills run on its own stream
+            assert hip.mm_grouped(Segment.of(w), dt, k, m, E, counts_dv.data_ptr(), a_dv.data_ptr(), k, c.data_ptr(),
+                                  m + 2, k, rows_cap, off.data_ptr()) == JAM.OK, hip.last_error()
+            hip.synchronize()
+            total = sum(counts)
+            assert off.cpu().numpy().tolist() == [0] + np.cumsum(counts).tolist()
+            got = c.cpu().numpy()
+            ref = M.mm_grouped(oracle, dt, w_e, a, counts, m, k)
+            o = 0
+            for e, n in enumerate(counts):
+                if n:
+                    _, sa = oracle.mm_ref(dt, w_e[e], np.ascontiguousarray(a[o:o + n]), m, n, k)
+                    r = ref[o:o + n]
+                    assert (np.abs(got[o:o + n, :m] - r) <= 1e-3 * np.abs(r) + 1e-5 * sa).all(), (e, n)
+                o += n
+            assert (got[:, m:] == -3.0).all()
+            assert (got[total:] == -3.0).all()
+        finally:
+            hip.evict(Segment.of(w))
+
+
 @pytest.mark.parametrize("E", [150, 300])
 def test_mm_grouped_many_experts(hip, oracle, E):
     """More than 64 experts, small and large experts mixed, and counts past rows_cap: offsets are the clamped
