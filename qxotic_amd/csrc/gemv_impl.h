@@ -386,8 +386,9 @@ template <int NT, int HP, int NWV>
 JAMHIP_DEV void a_load(APre<HP>& pre, const float* __restrict__ a, int lda, int k, int Gk, int ntv) {
     // four 16-byte loads per half-block (the launcher checks a and lda for 16-byte alignment); a half past
     // the token's last element (a partial last group) re-reads the token's last half, zeroed by f1_store
-    // (zeroing here would make the wave wait for these loads before issuing the weight loads)
-    const int halves = 16 * Gk, total = NT * halves, kh = k >> 4;
+    // (zeroing here would make the wave wait for these loads before issuing the weight loads). Only the
+    // ntv tokens present are quantized (a grouped call's expert may hold fewer rows than NT).
+    const int halves = 16 * Gk, total = (NT == 1 ? 1 : ntv) * halves, kh = k >> 4;
 #pragma unroll
     for (int i = 0; i < HP; i++) {
         const int h0 = pro_half<HP>(i), h = h0 < total ? h0 : total - 1;
@@ -406,10 +407,11 @@ JAMHIP_DEV void a_load(APre<HP>& pre, const float* __restrict__ a, int lda, int 
 }
 
 template <int NT, int HP, int NWV>
-JAMHIP_DEV void f1_store(const APre<HP>& pre, int k, int Gk, int8_t* lq, float* ld, float* las, int* ls16, char* dummy) {
+JAMHIP_DEV void f1_store(const APre<HP>& pre, int k, int Gk, int ntv, int8_t* lq, float* ld, float* las, int* ls16,
+                         char* dummy) {
     // branch-free: a thread past the last half-block (its loads were clamped) quantizes anyway and writes to
     // a dummy LDS slot; pairs stay aligned because the half-block count is even
-    const int halves = 16 * Gk, total = NT * halves;
+    const int halves = 16 * Gk, total = (NT == 1 ? 1 : ntv) * halves;
 #pragma unroll
     for (int i = 0; i < HP; i++) {
         const int h0 = pro_half<HP>(i);
@@ -585,7 +587,7 @@ __global__ void __launch_bounds__(64 * NWV) mv_kernel(WeightView w, ActQ A, cons
     // Only waves that own at least one real half-block of the activations load and quantize them (the
     // others would only write the dummy slot); the condition is wave-uniform. Their loads go first in the
     // load queue and are kept there by the scheduler.
-    const bool pro = QF1 && wave * 64 * (QF1 ? HP : 1) < NT * 16 * Gk;
+    const bool pro = QF1 && wave * 64 * (QF1 ? HP : 1) < (NT == 1 ? 1 : ntv) * 16 * Gk;
     APre<QF1 ? HP : 1> pre;
     FPre<STG ? SP : 1> fpre;
     if constexpr (QF1)
@@ -627,7 +629,7 @@ __global__ void __launch_bounds__(64 * NWV) mv_kernel(WeightView w, ActQ A, cons
         td = 8 * Gk;
         QS = QS_LDS;
         if constexpr (QF1) {
-            if (pro) f1_store<NT, QF1 ? HP : 1, NWV>(pre, k, Gk, lq, ld, las, ls16, dummy);
+            if (pro) f1_store<NT, QF1 ? HP : 1, NWV>(pre, k, Gk, ntv, lq, ld, las, ls16, dummy);
         } else {   // F2: per-16 sums in the Σq-per-16 region (16 per group and token)
             stage_store<NT, SP, NWV>(fpre, k, Gk, lq, ld, reinterpret_cast<float*>(ls16));
         }
