@@ -253,6 +253,39 @@ __global__ void __launch_bounds__(RCH) moe_route_slot_kernel(const int* __restri
     }
 }
 
+// The same CSR build for at most 64 routes and 64 experts (decode-time MoE) in one wave, with no barrier:
+// lane l holds route l (expert e_l) and expert l's count. One ballot per expert gives the count (popcount)
+// and each route its rank among the earlier routes of its expert (popcount below its lane); a wave scan of
+// the counts gives off, so route l's slot is off[e_l] + rank: Moe.dispatch's cursor order.
+__global__ void __launch_bounds__(64) moe_route_wave_kernel(const int* __restrict__ route_expert, int R, int E,
+                                                           int* __restrict__ counts, int* __restrict__ off,
+                                                           int* __restrict__ slot_route, int* __restrict__ route_slot) {
+    const int lane = threadIdx.x;
+    const uint64_t below = (1ull << lane) - 1ull;
+    const int e = lane < R ? route_expert[lane] : -1;
+    int cnt = 0, rank = 0;
+    for (int x = 0; x < E; x++) {
+        const uint64_t m = __ballot(e == x);
+        if (lane == x) cnt = __popcll(m);
+        if (e == x) rank = __popcll(m & below);
+    }
+    const int o = wave_exclusive_scan(cnt);   // lanes past E hold count 0
+    if (lane < E) {
+        counts[lane] = cnt;
+        off[lane] = o;
+        if (lane == E - 1) off[E] = o + cnt;
+    }
+    const int oe = __shfl(o, e >= 0 && e < E ? e : 0);
+    if (lane < R) {
+        if (e >= 0 && e < E) {
+            slot_route[oe + rank] = lane;
+            route_slot[lane] = oe + rank;
+        } else {
+            route_slot[lane] = -1;
+        }
+    }
+}
+
 // Moe.dispatch's gather (Moe.java:214-222): g[slot] = x[slot_route[slot] / topk] (dim floats per row).
 // Slots past off[E] (routes with an expert id outside [0, E) leave them unassigned) are not written. V4:
 // rows copied as float4 (the launcher checks 16-byte alignment of both rows and dim % 4 == 0).
@@ -358,6 +391,10 @@ size_t moe_route_scratch_ints(int R, int E) { return E <= 256 && R > RCH ? (size
 hipError_t launch_moe_route(const int* route_expert, int R, int E, int* counts, int* off, int* slot_route,
                             int* route_slot, hipStream_t st, int* scratch) {
     if (E < 1 || E > MOE_THREADS) return hipErrorNotSupported;
+    if (R <= 64 && E <= 64) {   // one wave
+        moe_route_wave_kernel<<<1, 64, 0, st>>>(route_expert, R, E, counts, off, slot_route, route_slot);
+        return hipGetLastError();
+    }
     if (scratch != nullptr && moe_route_scratch_ints(R, E) > 0) {   // chunked: R > 256 routes, E <= 256
         const int nch = (R + RCH - 1) / RCH;
         moe_route_count_kernel<<<nch, RCH, 0, st>>>(route_expert, R, E, scratch);

@@ -32,14 +32,18 @@ def dev(x):
 
 def test_route_gather_combine_bit_exact(hip):
     import torch
-    # more than 256 routes with at most 256 experts take the chunked two-kernel routing, the rest the
-    # single-workgroup kernel (chunks of 1024: the last case takes five); both must give Moe.dispatch's slots
+    # more than 256 routes with at most 256 experts take the chunked two-kernel routing, up to 64 routes over
+    # up to 64 experts the one-wave kernel, the rest the single-workgroup kernel (chunks of 1024: the last
+    # case takes five); all must give Moe.dispatch's slots
     for seed, seq, topk, E in ((1, 37, 4, 8), (2, 300, 2, 32), (3, 5, 1, 3), (4, 700, 4, 32), (5, 1100, 4, 64),
-                               (6, 300, 4, 16), (7, 200, 2, 300), (8, 512, 4, 256)):
+                               (6, 300, 4, 16), (7, 200, 2, 300), (8, 512, 4, 256), (9, 16, 4, 64), (10, 1, 4, 32),
+                               (11, 8, 2, 80)):
         say(f"moe route seq={seq} topk={topk} E={E}")
         re = routes(seed, seq, topk, E)
         if seed == 3:
             re[2] = E + 5                        # an id outside [0, E) takes no slot
+        if seed == 9:
+            re[5], re[63] = -1, E                # the same in the one-wave kernel (its last lane too)
         if seed == 6:                            # the same in the chunked form, in two different chunks
             re[7], re[1000] = -1, E + 3
         R = seq * topk
