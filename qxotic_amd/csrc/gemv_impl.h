@@ -560,7 +560,8 @@ __global__ void __launch_bounds__(64 * NWV) mv_kernel(WeightView w, ActQ A, cons
     if constexpr (GR) {
         int e, o, ne;
         if constexpr (FL == 1) {
-            e = blockIdx.y;
+            e = gp.small != nullptr ? __builtin_amdgcn_readfirstlane(gp.small[blockIdx.y]) : (int) blockIdx.y;
+            if (e < 0) return;   // whole workgroup, before any barrier
             o = __builtin_amdgcn_readfirstlane(gp.off[e]);
             ne = __builtin_amdgcn_readfirstlane(gp.off[e + 1]) - o;
             if (ne <= 0 || ne >= 8) return;   // whole workgroup, before any barrier

@@ -29,6 +29,9 @@ struct Groups {
     const int* map64;
     int gm;
     const float* bias = nullptr;   // per-expert bias [E][gm] added in the store (expert e at bias + e·gm)
+    // the experts with 1..7 rows in expert order, -1 past the last (launch_moe_offsets): the F1 grouped kernel's
+    // workgroup column y takes expert small[y] (null: expert y)
+    const int* small = nullptr;
 };
 
 // Matrix-core GEMM workgroup -> linear tile; workgroup b runs on XCD b % 8. Ungrouped: each XCD takes one
@@ -178,8 +181,10 @@ hipError_t launch_gemm_prep_grouped(int dt, const float* a, int lda, int k, cons
                                     void* scratch, GemmAct* out, hipStream_t st);
 
 // MoE bookkeeping (moe.hip)
+// small[0..nsmall): the experts with 1..7 rows in expert order, -1 past the last; nsmall >= min(E, rows_cap)
+// (at most that many experts hold rows).
 hipError_t launch_moe_offsets(const int* counts, int E, int rows_cap, int* off, int* poff64, int* poff8, int* map64,
-                              int cap64, int* map8, int cap8, hipStream_t st);
+                              int cap64, int* map8, int cap8, int* small, int nsmall, hipStream_t st);
 // scratch: moe_route_scratch_ints(R, E) ints of device memory for the chunked form (R > 256 routes, E <= 256),
 // or null for the single-workgroup kernel; both give the same slots.
 size_t moe_route_scratch_ints(int R, int E);
