@@ -564,7 +564,7 @@ __global__ void __launch_bounds__(64 * NWV) mv_kernel(WeightView w, ActQ A, cons
             if (e < 0) return;   // whole workgroup, before any barrier
             o = __builtin_amdgcn_readfirstlane(gp.off[e]);
             ne = __builtin_amdgcn_readfirstlane(gp.off[e + 1]) - o;
-            if (ne <= 0 || ne >= 8) return;   // whole workgroup, before any barrier
+            if (ne <= 0 || ne > NT) return;   // whole workgroup, before any barrier
             t0 = o;
             ntv = ne;
             a += (int64_t) o * lda;
@@ -883,6 +883,13 @@ template <int DT>
 hipError_t gemv_grouped_dt(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k,
                                   const Groups& g, int E, int cap8, float* c, int ldc, hipStream_t st) {
     if (flavour == 2) return go_grouped<DT, 2, 8, 0>(k, g, cap8, w, A, nullptr, 0, c, ldc, st);
+    if (flavour == 0) {   // one-row experts: one token's registers, LDS and prologue
+        if (a == nullptr) return go_grouped<DT, 1, 1, 0>(k, g, E, w, A, nullptr, 0, c, ldc, st);
+        const int hp = fuse_hp(1, k);
+        if (hp <= 1) return go_grouped<DT, 1, 1, 1>(k, g, E, w, A, a, lda, c, ldc, st);
+        if (hp == 2) return go_grouped<DT, 1, 1, 2>(k, g, E, w, A, a, lda, c, ldc, st);
+        return go_grouped<DT, 1, 1, 4>(k, g, E, w, A, a, lda, c, ldc, st);
+    }
     if (a == nullptr) return go_grouped<DT, 1, 7, 0>(k, g, E, w, A, nullptr, 0, c, ldc, st);
     const int hp = fuse_hp(7, k);
     if (hp <= 1) return go_grouped<DT, 1, 7, 1>(k, g, E, w, A, a, lda, c, ldc, st);

@@ -844,15 +844,17 @@ jamhip_status mm_grouped_ex_impl(jamhip_ctx* ctx, const void* w, int wt, int ldw
     const int E = n_experts;
     const int cap64 = (int) (((int64_t) rows_cap + 63 * E + 63) / 64), cap8 = (int) (((int64_t) rows_cap + 7 * E + 7) / 8);
     hipError_t e;
-    if ((e = ctx->moe.ensure((size_t) (3 * (E + 1) + cap64 + cap8 + E) * sizeof(int))) != hipSuccess)
+    if ((e = ctx->moe.ensure((size_t) (3 * (E + 1) + cap64 + cap8 + 2 * E) * sizeof(int))) != hipSuccess)
         return hip_fail(ctx, e, "grouped: scratch alloc");
     int* off = (int*) ctx->moe.p;
     int* poff64 = off + (E + 1);
     int* poff8 = poff64 + (E + 1);
     int* map64 = poff8 + (E + 1);
     int* map8 = map64 + cap64;
-    int* small = map8 + cap8;   // the experts with 1..7 rows (the F1 kernel's workgroup columns)
-    const int nsmall = E < rows_cap ? E : rows_cap;   // at most rows_cap experts hold rows
+    // the F1 decode kernels' workgroup columns: the experts with one row (at most rows_cap of them), then
+    // those with 2..7 rows (at most rows_cap / 2)
+    int* small = map8 + cap8;
+    const int n1 = E < rows_cap ? E : rows_cap, n2 = E < rows_cap / 2 ? E : rows_cap / 2;
     const float* a = (const float*) a_dev;
     float* c = (float*) c_dev;
     // Matrix-core path with at least 8 rows per expert on average: one prep launch builds the offsets and the
@@ -872,7 +874,7 @@ jamhip_status mm_grouped_ex_impl(jamhip_ctx* ctx, const void* w, int wt, int ldw
         return JAMHIP_OK;
     }
     if ((e = launch_moe_offsets((const int*) counts_dev, E, rows_cap, off, poff64, poff8, map64, cap64, map8, cap8,
-                                small, nsmall > 0 ? nsmall : 1, ctx->stream)) != hipSuccess)
+                                small, n1, n2, ctx->stream)) != hipSuccess)
         return hip_fail(ctx, e, "grouped: offsets launch");
     if (offsets_dev &&
         (e = hipMemcpyAsync(offsets_dev, off, (size_t) (E + 1) * sizeof(int), hipMemcpyDeviceToDevice, ctx->stream)) !=
@@ -889,21 +891,25 @@ jamhip_status mm_grouped_ex_impl(jamhip_ctx* ctx, const void* w, int wt, int ldw
         *A = ActQ{(int8_t*) base, (float*) (base + qb), (float*) (base + qb + db), (int*) (base + qb + db + sb)};
         return r;
     };
-    // experts with 1..7 rows: jam's F1 decode path, one launch, a workgroup column per listed expert (at most
-    // min(E, rows_cap) of them)
-    Groups g1 = g;
+    // experts with 1..7 rows: jam's F1 decode path, a workgroup column per listed expert: one launch of the
+    // one-token kernel over the experts with one row (decode: every expert), one of the seven-token kernel
+    // over those with 2..7 (none can exist below rows_cap = 2)
+    Groups g1 = g, g2 = g;
     g1.small = small;
-    if (gemv_grouped_fusable(k, a, lda)) {
-        if ((e = launch_gemv_grouped(wt, 1, wv, ActQ{}, a, lda, k, g1, nsmall, cap8, c, ldc, ctx->stream)) != hipSuccess)
-            return hip_fail(ctx, e, "grouped: gemv launch");
-    } else {
-        ActQ A;
+    g2.small = small + n1;
+    const bool fuse = gemv_grouped_fusable(k, a, lda);
+    ActQ A{};
+    if (!fuse) {
         if ((e = actq(&A)) != hipSuccess) return hip_fail(ctx, e, "grouped: activation scratch alloc");
         if ((e = launch_quant_f1(a, lda, rows_cap, k, (int8_t*) A.q, (float*) A.d, (float*) A.s, (int*) A.s16,
-                                 ctx->stream)) != hipSuccess ||
-            (e = launch_gemv_grouped(wt, 1, wv, A, nullptr, 0, k, g1, nsmall, cap8, c, ldc, ctx->stream)) != hipSuccess)
-            return hip_fail(ctx, e, "grouped: gemv launch");
+                                 ctx->stream)) != hipSuccess)
+            return hip_fail(ctx, e, "grouped: quantize launch");
     }
+    const float* af = fuse ? a : nullptr;
+    const int laf = fuse ? lda : 0;
+    if ((e = launch_gemv_grouped(wt, 0, wv, A, af, laf, k, g1, n1, cap8, c, ldc, ctx->stream)) != hipSuccess ||
+        (n2 > 0 && (e = launch_gemv_grouped(wt, 1, wv, A, af, laf, k, g2, n2, cap8, c, ldc, ctx->stream)) != hipSuccess))
+        return hip_fail(ctx, e, "grouped: gemv launch");
     // fewer than 8 rows in all (decode-time MoE): no expert reaches the F2 bands, nothing more to launch
     if (rows_cap < 8) return JAMHIP_OK;
     // experts with >= 8 rows: jam's F2 bands (m % 16 == 0: no float-dot tail rows)

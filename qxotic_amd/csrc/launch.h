@@ -29,8 +29,8 @@ struct Groups {
     const int* map64;
     int gm;
     const float* bias = nullptr;   // per-expert bias [E][gm] added in the store (expert e at bias + e·gm)
-    // the experts with 1..7 rows in expert order, -1 past the last (launch_moe_offsets): the F1 grouped kernel's
-    // workgroup column y takes expert small[y] (null: expert y)
+    // an expert list in expert order, -1 past its last (launch_moe_offsets): the F1 grouped kernel's workgroup
+    // column y takes expert small[y] (null: expert y)
     const int* small = nullptr;
 };
 
@@ -79,10 +79,12 @@ hipError_t launch_gemv(int dt, int flavour, const WeightView& w, const ActQ& A, 
 hipError_t launch_split_reduce(const float* part, int ns, int64_t slice, int m, int n, float* c, int ldc,
                                hipStream_t st, const Epi& ep = Epi{});
 
-// Grouped forms (one launch for all experts). flavour 1: every expert with 1..7 rows, F1, the kernel
-// quantizing its expert's rows itself when `a` is non-null (then gemv_grouped_fusable(k, a, lda) must hold),
-// else reading them from A (CSR rows). flavour 2: the 8-token tiles of map8 (experts with >= 8 rows), F2
-// activations from A (CSR rows). m here is the rows per expert (g.gm).
+// Grouped forms (one launch for all experts). flavour 0 / 1: F1 over the experts of g.small (E workgroup
+// columns) holding exactly one row / 2..7 rows (one-token / seven-token kernels; experts with other counts
+// are skipped), the kernel quantizing its expert's rows itself when `a` is non-null (then
+// gemv_grouped_fusable(k, a, lda) must hold), else reading them from A (CSR rows). flavour 2: the 8-token
+// tiles of map8 (experts with >= 8 rows), F2 activations from A (CSR rows). m here is the rows per expert
+// (g.gm).
 bool gemv_grouped_fusable(int k, const float* a, int lda);
 hipError_t launch_gemv_grouped(int dt, int flavour, const WeightView& w, const ActQ& A, const float* a, int lda,
                                int k, const Groups& g, int E, int cap8, float* c, int ldc, hipStream_t st);
@@ -181,10 +183,11 @@ hipError_t launch_gemm_prep_grouped(int dt, const float* a, int lda, int k, cons
                                     void* scratch, GemmAct* out, hipStream_t st);
 
 // MoE bookkeeping (moe.hip)
-// small[0..nsmall): the experts with 1..7 rows in expert order, -1 past the last; nsmall >= min(E, rows_cap)
-// (at most that many experts hold rows).
+// small[0..n1): the experts with exactly one row, small[n1..n1 + n2): those with 2..7 rows, each list in expert
+// order and -1 past its last; n1 >= min(E, rows_cap), n2 >= min(E, rows_cap / 2) (at most that many experts can
+// hold one row / two or more).
 hipError_t launch_moe_offsets(const int* counts, int E, int rows_cap, int* off, int* poff64, int* poff8, int* map64,
-                              int cap64, int* map8, int cap8, int* small, int nsmall, hipStream_t st);
+                              int cap64, int* map8, int cap8, int* small, int n1, int n2, hipStream_t st);
 // scratch: moe_route_scratch_ints(R, E) ints of device memory for the chunked form (R > 256 routes, E <= 256),
 // or null for the single-workgroup kernel; both give the same slots.
 size_t moe_route_scratch_ints(int R, int E);

@@ -30,12 +30,14 @@ JAMHIP_DEV int block_exclusive_scan(int v, int* tmp) {
 // counts[E] (device, clamped to >= 0 and so that the total stays within rows_cap) -> off[E+1] (CSR row
 // offsets), and for the experts with at least 8 rows (jam's band threshold, jam_kquant.h:23) the token
 // slots of the matrix-core activation layout (poff64: each expert padded to 64 slots) and of the 8-token
-// decode tiles (poff8), with the tile -> expert maps map64[cap64] / map8[cap8] (-1 = no expert).
+// decode tiles (poff8), with the tile -> expert maps map64[cap64] / map8[cap8] (-1 = no expert), and the F1
+// decode kernels' expert lists: small[0..n1) the experts with exactly one row, small[n1..n1 + n2) those with
+// 2..7 rows, each in expert order and -1 past its last.
 __global__ void __launch_bounds__(MOE_THREADS) moe_offsets_kernel(const int* __restrict__ counts, int E, int rows_cap,
                                                                  int* __restrict__ off, int* __restrict__ poff64,
                                                                  int* __restrict__ poff8, int* __restrict__ map64,
                                                                  int cap64, int* __restrict__ map8, int cap8,
-                                                                 int* __restrict__ small, int nsmall) {
+                                                                 int* __restrict__ small, int n1, int n2) {
     __shared__ int tmp[MOE_THREADS];
     const int e = threadIdx.x;
     const int c0 = e < E ? min(max(counts[e], 0), rows_cap) : 0;   // changes no clamped count; no overflow
@@ -45,12 +47,14 @@ __global__ void __launch_bounds__(MOE_THREADS) moe_offsets_kernel(const int* __r
     const int big = c >= 8;
     const int p64 = block_exclusive_scan(big ? (c + 63) / 64 * 64 : 0, tmp);
     const int p8 = block_exclusive_scan(big ? (c + 7) / 8 * 8 : 0, tmp);
-    const int sm = c >= 1 && c <= 7, rs = block_exclusive_scan(sm, tmp);   // the F1 experts' list
+    const int s1 = c == 1, r1 = block_exclusive_scan(s1, tmp);               // the F1 lists
+    const int s2 = c >= 2 && c <= 7, r2 = block_exclusive_scan(s2, tmp);
     for (int i = e; i < cap64; i += MOE_THREADS) map64[i] = -1;
     for (int i = e; i < cap8; i += MOE_THREADS) map8[i] = -1;
-    for (int i = e; i < nsmall; i += MOE_THREADS) small[i] = -1;
+    for (int i = e; i < n1 + n2; i += MOE_THREADS) small[i] = -1;
     __syncthreads();
-    if (sm) small[rs] = e;   // rs < nsmall: each listed expert holds a row
+    if (s1) small[r1] = e;        // r1 < n1: each listed expert holds a row
+    if (s2) small[n1 + r2] = e;   // r2 < n2: each listed expert holds two or more
     if (e < E) {
         off[e] = oc;
         poff64[e] = p64;
@@ -82,7 +86,7 @@ __global__ void __launch_bounds__(64) moe_offsets_wave_kernel(const int* __restr
                                                              int* __restrict__ off, int* __restrict__ poff64,
                                                              int* __restrict__ poff8, int* __restrict__ map64,
                                                              int cap64, int* __restrict__ map8, int cap8,
-                                                             int* __restrict__ small, int nsmall) {
+                                                             int* __restrict__ small, int n1, int n2) {
     const int e = threadIdx.x;
     const int c0 = e < E ? min(max(counts[e], 0), rows_cap) : 0;   // changes no clamped count; no overflow
     const int o = wave_exclusive_scan(c0);
@@ -92,12 +96,14 @@ __global__ void __launch_bounds__(64) moe_offsets_wave_kernel(const int* __restr
     const int a64 = big ? (c + 63) / 64 * 64 : 0, a8 = big ? (c + 7) / 8 * 8 : 0;
     const int p64 = wave_exclusive_scan(a64);
     const int p8 = wave_exclusive_scan(a8);
-    const int sm = c >= 1 && c <= 7, rs = wave_exclusive_scan(sm);   // the F1 experts' list
+    const int s1 = c == 1, r1 = wave_exclusive_scan(s1);               // the F1 lists
+    const int s2 = c >= 2 && c <= 7, r2 = wave_exclusive_scan(s2);
     for (int i = e; i < cap64; i += 64) map64[i] = -1;
     for (int i = e; i < cap8; i += 64) map8[i] = -1;
-    for (int i = e; i < nsmall; i += 64) small[i] = -1;
+    for (int i = e; i < n1 + n2; i += 64) small[i] = -1;
     __syncthreads();
-    if (sm) small[rs] = e;   // rs < nsmall: each listed expert holds a row
+    if (s1) small[r1] = e;        // r1 < n1: each listed expert holds a row
+    if (s2) small[n1 + r2] = e;   // r2 < n2: each listed expert holds two or more
     if (e < E) {
         off[e] = oc;
         poff64[e] = p64;
@@ -385,15 +391,16 @@ __global__ void __launch_bounds__(256) moe_combine_kernel(const float* __restric
 }
 
 hipError_t launch_moe_offsets(const int* counts, int E, int rows_cap, int* off, int* poff64, int* poff8, int* map64,
-                              int cap64, int* map8, int cap8, int* small, int nsmall, hipStream_t st) {
+                              int cap64, int* map8, int cap8, int* small, int n1, int n2, hipStream_t st) {
     if (E < 1 || E > MOE_THREADS) return hipErrorNotSupported;
-    if (nsmall < (E < rows_cap ? E : rows_cap)) return hipErrorInvalidValue;
+    if (rows_cap < 0 || n1 < (E < rows_cap ? E : rows_cap) || n2 < (E < rows_cap / 2 ? E : rows_cap / 2))
+        return hipErrorInvalidValue;
     if (E <= 64)
         moe_offsets_wave_kernel<<<1, 64, 0, st>>>(counts, E, rows_cap, off, poff64, poff8, map64, cap64, map8, cap8,
-                                                  small, nsmall);
+                                                  small, n1, n2);
     else
         moe_offsets_kernel<<<1, MOE_THREADS, 0, st>>>(counts, E, rows_cap, off, poff64, poff8, map64, cap64, map8, cap8,
-                                                      small, nsmall);
+                                                      small, n1, n2);
     return hipGetLastError();
 }
 
