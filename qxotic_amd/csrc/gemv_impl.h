@@ -318,6 +318,39 @@ JAMHIP_DEV float group_dot(const Group<DT>& w, const int8_t* aq, const float* ad
     }
 }
 
+// MXFP4 F1 dot of one group against f16 activation pairs (QS_F16 layout of the fused prologue): byte u of a
+// block's 16 code bytes converts, by the hardware e2m1 conversion scaled by 2 (jam's doubled codes,
+// jam_mxfp4.h:14-15), to the codes of elements u and u + 16, which v_dot2 multiplies with the pair
+// (q_u, q_{u+16}). Products and partial sums are integers below 2^16, exact in f32, so a block's sum is jam's
+// integer I exactly; then fl(sw·da)·I as in group_dot. Half the VALU work of the int8 form (a byte's two
+// codes in two instructions instead of a table lookup per four nibbles and a v_dot4).
+JAMHIP_DEV float mx_dot_f16(const Group<MXFP4>& w, const int8_t* a2, const float* ad, int nbv) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    float acc = 0.0f;
+#pragma unroll
+    for (int b = 0; b < 8; b++) {
+        const int bb = b < nbv ? b : nbv - 1;   // stay inside the token's activations
+        float I = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint4 A = ld16(a2 + 64 * bb + 16 * j);   // pairs 4j .. 4j + 3
+            const uint32_t wj = word(w.q[b], j);          // code bytes 4j .. 4j + 3
+            I = __builtin_amdgcn_fdot2(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(wj, 2.0f, 0),
+                                       __builtin_bit_cast(h2, A.x), I, false);
+            I = __builtin_amdgcn_fdot2(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(wj, 2.0f, 1),
+                                       __builtin_bit_cast(h2, A.y), I, false);
+            I = __builtin_amdgcn_fdot2(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(wj, 2.0f, 2),
+                                       __builtin_bit_cast(h2, A.z), I, false);
+            I = __builtin_amdgcn_fdot2(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(wj, 2.0f, 3),
+                                       __builtin_bit_cast(h2, A.w), I, false);
+        }
+        const float sw = e8m0_half((word(w.s, b >> 2) >> (8 * (b & 3))) & 0xffu);
+        const float v = I * (sw * ad[bb]);
+        acc += b < nbv ? v : 0.0f;
+    }
+    return acc;
+}
+
 // Q4_0 F1 decode with 3..7 tokens: the group's nibbles and block scales unpacked once for all the tokens
 // (measured faster for Q4_0 only; the other types unpack per token in group_dot), then per token
 // group_dot's Q4_0 arithmetic.
@@ -369,6 +402,13 @@ JAMHIP_DEV float q40_dot_f1(const Q40Codes& u, const int8_t* aq, const float* ad
 // One thread per 16-element half-block; the halves of a 32-block sit in adjacent lanes, which exchange
 // their |x| maxima and Σq. Elements past k (a partial last group) quantize as zeros.
 constexpr int QS_LDS = 272;
+// MXFP4 with one token (fused prologue): the codes go to LDS as f16 pairs (q_i, q_{i+16}) of each 32-block,
+// the order in which the e2m1 conversion returns a weight byte's two codes (mx_dot_f16): 512 bytes per group,
+// padded to QS_F16.
+constexpr int QS_F16 = 528;
+template <int DT, int FL, int NT, int HP> constexpr bool f16_pairs() {
+    return DT == MXFP4 && FL == 1 && NT == 1 && HP > 0;
+}
 constexpr int MV_WAVES = 8;   // waves per GEMV workgroup (512 threads)
 
 // The prologue runs in two steps so that its activation loads go out before the weight stream: a_load
@@ -406,7 +446,7 @@ JAMHIP_DEV void a_load(APre<HP>& pre, const float* __restrict__ a, int lda, int 
     }
 }
 
-template <int NT, int HP, int NWV>
+template <int NT, int HP, int NWV, bool F16P = false>
 JAMHIP_DEV void f1_store(const APre<HP>& pre, int k, int Gk, int ntv, int8_t* lq, float* ld, float* las, int* ls16,
                          char* dummy) {
     // branch-free: a thread past the last half-block (its loads were clamped) quantizes anyway and writes to
@@ -428,6 +468,24 @@ JAMHIP_DEV void f1_store(const APre<HP>& pre, int k, int Gk, int ntv, int8_t* lq
         am = fmaxf(am, __shfl_xor(am, 1));
         const float db = am / 127.0f;
         const float id = db > 0.0f ? 1.0f / db : 0.0f;
+        if constexpr (F16P) {
+            // element e of this half is f16 number (hh & 1) of pair slot e of its block (the codes are
+            // integers in [-128, 127], exact in f16 whatever the rounding); MXFP4 reads no sums
+            if (valid) {
+                uint16_t* p2 = reinterpret_cast<uint16_t*>(lq + (int64_t) (hh >> 4) * QS_F16 + 64 * ((hh >> 1) & 7) +
+                                                           2 * (hh & 1));
+#pragma unroll
+                for (int e = 0; e < 16; e += 2) {
+                    const float q0 = fminf(fmaxf(rintf(x[e] * id), -128.0f), 127.0f);
+                    const float q1 = fminf(fmaxf(rintf(x[e + 1] * id), -128.0f), 127.0f);
+                    const uint32_t v = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(q0, q1));
+                    p2[2 * e] = (uint16_t) (v & 0xffffu);
+                    p2[2 * e + 2] = (uint16_t) (v >> 16);
+                }
+                if ((hh & 1) == 0) ld[hh >> 1] = db;
+            }
+            continue;
+        }
         uint32_t pk[4];
 #pragma unroll
         for (int g = 0; g < 4; g++) {
@@ -619,18 +677,20 @@ __global__ void __launch_bounds__(64 * NWV) mv_kernel(WeightView w, ActQ A, cons
     int64_t tq = kf, td = nbf, ts = FL == 1 ? nbf : 2 * nbf, t16 = 2 * nbf;
     int QS = 256;
     if constexpr (FUSE) {
+        constexpr bool F16P = f16_pairs<DT, FL, NT, HP>();
+        constexpr int QSB = F16P ? QS_F16 : QS_LDS;
         char* dummy = reinterpret_cast<char*>(smem + NWV * ITEMS * 64 * NT * 4);   // 32 bytes
         int8_t* lq = reinterpret_cast<int8_t*>(dummy + 32);
-        float* ld = reinterpret_cast<float*>(lq + NT * Gk * QS_LDS);
+        float* ld = reinterpret_cast<float*>(lq + NT * Gk * QSB);
         float* las = ld + NT * 8 * Gk;
         int* ls16 = reinterpret_cast<int*>(las + NT * 8 * Gk);
         aq = lq;
         ad = ld;
-        tq = (int64_t) Gk * QS_LDS;
+        tq = (int64_t) Gk * QSB;
         td = 8 * Gk;
-        QS = QS_LDS;
+        QS = QSB;
         if constexpr (QF1) {
-            if (pro) f1_store<NT, QF1 ? HP : 1, NWV>(pre, k, Gk, ntv, lq, ld, las, ls16, dummy);
+            if (pro) f1_store<NT, QF1 ? HP : 1, NWV, F16P>(pre, k, Gk, ntv, lq, ld, las, ls16, dummy);
         } else {   // F2: per-16 sums in the Σq-per-16 region (16 per group and token)
             stage_store<NT, SP, NWV>(fpre, k, Gk, lq, ld, reinterpret_cast<float*>(ls16));
         }
@@ -668,9 +728,12 @@ __global__ void __launch_bounds__(64 * NWV) mv_kernel(WeightView w, ActQ A, cons
             for (int t = 0; t < NT; t++) {
                 if (t >= ntv) break;
                 const int tt = FUSE ? t : t0 + t;
-                const float p = group_dot<DT, FL>(buf[i], aq + tt * tq + (int64_t) gg * QS, ad + tt * td + 8 * gg,
-                                                  as + tt * ts + (FL == 1 ? 8 : 16) * gg, s16 + tt * t16 + 16 * gg,
-                                                  nbv);
+                float p;
+                if constexpr (f16_pairs<DT, FL, NT, HP>())
+                    p = mx_dot_f16(buf[i], aq + (int64_t) gg * QS, ad + 8 * gg, nbv);
+                else
+                    p = group_dot<DT, FL>(buf[i], aq + tt * tq + (int64_t) gg * QS, ad + tt * td + 8 * gg,
+                                          as + tt * ts + (FL == 1 ? 8 : 16) * gg, s16 + tt * t16 + 16 * gg, nbv);
                 pp[t] = live ? p : 0.0f;
             }
         } else {   // Q4_0, 3..8 tokens: the group's weights unpacked once for all the tokens
@@ -805,7 +868,9 @@ static void lds_allow(const void* fn, size_t bytes) {
     (void) hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int) bytes);
     done.emplace_back(fn, bytes);
 }
-static size_t fuse_lds(int n, int k) { return (size_t) n * ((k / 32 + 7) / 8) * (QS_LDS + 32 + 32 + 64); }
+static size_t fuse_lds(int n, int k, bool f16p = false) {
+    return (size_t) n * ((k / 32 + 7) / 8) * ((f16p ? QS_F16 : QS_LDS) + 32 + 32 + 64);
+}
 static int fuse_hp(int n, int k) { return (n * 16 * ((k / 32 + 7) / 8) + 64 * MV_WAVES - 1) / (64 * MV_WAVES); }
 
 // Work split: bands of RB = 8 rows (x 8 group slots: chunk loads are 128-byte lines; 16-row bands measured
@@ -840,7 +905,8 @@ static void launch_shape(int k, int ks, int64_t cz, int m, int n, const WeightVi
     const int QB = NWV * ITEMS / J;
     const int64_t bands = ((int64_t) m + RB - 1) / RB;
     const dim3 grid((unsigned) ((bands + QB - 1) / QB), (n + NT - 1) / NT, (unsigned) ((k + ks - 1) / ks));
-    const size_t lds = (size_t) NWV * ITEMS * 64 * NT * sizeof(float) + (HP > 0 ? 32 + fuse_lds(NT, ks) : 0);
+    const size_t lds = (size_t) NWV * ITEMS * 64 * NT * sizeof(float) +
+                       (HP > 0 ? 32 + fuse_lds(NT, ks, f16_pairs<DT, FL, NT, HP>()) : 0);
     if constexpr (NT >= 2) {   // only calls with 2 or more tokens split K
         if (ks < k) {
             lds_allow((const void*) mv_kernel<DT, FL, NT, HP, RB, ITEMS, false, true, NWV>, lds);
@@ -862,7 +928,8 @@ static void launch_shape_grouped(int k, const Groups& g, int ny, const WeightVie
     const int QB = MV_WAVES * ITEMS / J;
     const int64_t bands = ((int64_t) g.gm + RB - 1) / RB;
     const dim3 grid((unsigned) ((bands + QB - 1) / QB), (unsigned) ny);
-    const size_t lds = (size_t) MV_WAVES * ITEMS * 64 * NT * sizeof(float) + (HP > 0 ? 32 + fuse_lds(NT, k) : 0);
+    const size_t lds = (size_t) MV_WAVES * ITEMS * 64 * NT * sizeof(float) +
+                       (HP > 0 ? 32 + fuse_lds(NT, k, f16_pairs<DT, FL, NT, HP>()) : 0);
     lds_allow((const void*) mv_kernel<DT, FL, NT, HP, RB, ITEMS, true, false, MV_WAVES>, lds);
     mv_kernel<DT, FL, NT, HP, RB, ITEMS, true, false, MV_WAVES><<<grid, 64 * MV_WAVES, lds, st>>>(w, A, a, lda, k, g.gm,
                                                                                                  0, c, ldc, g, k, 0, Epi{});
