@@ -305,33 +305,35 @@ def test_split_k_decode(hip, oracle, dt):
 
 @pytest.mark.parametrize("dt", O.QUANT_TYPES)
 def test_decode_fused_prologue_matches_quantized_copy(hip, oracle, dt):
-    """One token: rows the kernel can load as 16-byte pieces are quantized in each workgroup's prologue (MXFP4:
-    into f16 pairs for the hardware e2m1 conversion and v_dot2), rows that are not (lda = k + 1) come from the
-    F1 copy through the int8 dot products. Both give jam's integer block sums, so the outputs are
-    bit-identical: a partial last group, the k = 14336 one-band workgroups and a small 4-wave grid."""
+    """1..7 tokens: rows the kernel can load as 16-byte pieces are quantized in each workgroup's prologue (MXFP4
+    with one token: into f16 pairs for the hardware e2m1 conversion and v_dot2), rows that are not
+    (lda = k + 1) come from the F1 copy through the int8 dot products. Both give jam's integer block sums, so the outputs are
+    bit-identical: a partial last group, the k = 14336 one-band workgroups (split K from two tokens on) and a
+    small 4-wave grid."""
     import torch
     from qxotic_amd.jam import JAM, Segment
     be = O.BLOCK[dt][0]
     for (m, k) in [(200, 2880 if be == 32 else 2816), (96, 14336), (520, 4096)]:
-        say(f"fused vs copy {O.NAMES[dt]} m={m} k={k}")
         w = oracle.quantize(dt, oracle.normal(0x5A11C0DE ^ 0xF1 ^ dt ^ k, (m, k), 0.0, 0.02))
-        a = oracle.outliers(3200 + k, (1, k))
         assert hip.pin(Segment.of(w), dt, k, m) == JAM.OK, hip.last_error()
         try:
-            outs = []
-            for lda in (k, k + 1):
-                a_pad = np.zeros((1, lda), np.float32)
-                a_pad[:, :k] = a
-                a_dev = torch.from_numpy(a_pad).cuda()
-                c_dev = torch.zeros((1, m), dtype=torch.float32, device="cuda")
-                st = hip.mm_device(Segment.of(w), dt, k, a_dev.data_ptr(), lda, c_dev.data_ptr(), m, m, 1, k)
-                assert st == JAM.OK, hip.last_error()
-                hip.synchronize()
-                outs.append(c_dev.cpu().numpy())
-            assert np.array_equal(bits(outs[0]), bits(outs[1])), (O.NAMES[dt], m, k)
-            ref = oracle.mm_int8(dt, w, a, m, 1, k)
-            _, sa = oracle.mm_ref(dt, w, a, m, 1, k)
-            assert tier1(outs[0], ref, sa).all()
+            for n in (1, 3, 7):
+                say(f"fused vs copy {O.NAMES[dt]} m={m} n={n} k={k}")
+                a = oracle.outliers(3200 + k + n, (n, k))
+                outs = []
+                for lda in (k, k + 1):
+                    a_pad = np.zeros((n, lda), np.float32)
+                    a_pad[:, :k] = a
+                    a_dev = torch.from_numpy(a_pad).cuda()
+                    c_dev = torch.zeros((n, m), dtype=torch.float32, device="cuda")
+                    st = hip.mm_device(Segment.of(w), dt, k, a_dev.data_ptr(), lda, c_dev.data_ptr(), m, m, n, k)
+                    assert st == JAM.OK, hip.last_error()
+                    hip.synchronize()
+                    outs.append(c_dev.cpu().numpy())
+                assert np.array_equal(bits(outs[0]), bits(outs[1])), (O.NAMES[dt], m, n, k)
+                ref = oracle.mm_int8(dt, w, a, m, n, k)
+                _, sa = oracle.mm_ref(dt, w, a, m, n, k)
+                assert tier1(outs[0], ref, sa).all()
         finally:
             assert hip.evict(Segment.of(w)) == JAM.OK
 
