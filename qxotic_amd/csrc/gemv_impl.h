@@ -351,6 +351,38 @@ JAMHIP_DEV float mx_dot_f16(const Group<MXFP4>& w, const int8_t* a2, const float
     return acc;
 }
 
+// NVFP4 F1 dot (jam_mm_nvfp4_avx512, jam_kernels_avx512bw.c:111-142) against f16 activation pairs: byte u of a
+// 16-element sub-block's 8 code bytes holds elements u (low nibble) and u + 8, which the e2m1 conversion
+// (scaled by 2) returns as one pair for v_dot2 with (q_u, q_{u+8}); the sub-block sums are jam's integer I
+// exactly (integers below 2^15), then fl(ue4m3(d_s)·ad)·I as in group_dot.
+JAMHIP_DEV float nv_dot_f16(const Group<NVFP4>& w, const int8_t* a2, const float* ad, int nbv) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const bool live = 2 * j < nbv;
+        const int jj = live ? j : nbv / 2 - 1;   // stay inside the token's activations
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            const uint4 ch = w.q[2 * j + (s >> 1)];
+            const uint32_t w0 = word(ch, 2 * (s & 1)), w1 = word(ch, 2 * (s & 1) + 1);
+            const uint4 P0 = ld16(a2 + 32 * (4 * jj + s)), P1 = ld16(a2 + 32 * (4 * jj + s) + 16);
+            float I = 0.0f;
+            I = __builtin_amdgcn_fdot2(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w0, 2.0f, 0), __builtin_bit_cast(h2, P0.x), I, false);
+            I = __builtin_amdgcn_fdot2(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w0, 2.0f, 1), __builtin_bit_cast(h2, P0.y), I, false);
+            I = __builtin_amdgcn_fdot2(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w0, 2.0f, 2), __builtin_bit_cast(h2, P0.z), I, false);
+            I = __builtin_amdgcn_fdot2(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w0, 2.0f, 3), __builtin_bit_cast(h2, P0.w), I, false);
+            I = __builtin_amdgcn_fdot2(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w1, 2.0f, 0), __builtin_bit_cast(h2, P1.x), I, false);
+            I = __builtin_amdgcn_fdot2(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w1, 2.0f, 1), __builtin_bit_cast(h2, P1.y), I, false);
+            I = __builtin_amdgcn_fdot2(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w1, 2.0f, 2), __builtin_bit_cast(h2, P1.z), I, false);
+            I = __builtin_amdgcn_fdot2(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w1, 2.0f, 3), __builtin_bit_cast(h2, P1.w), I, false);
+            const float sc = ue4m3((word(w.s, j) >> (8 * s)) & 0xffu) * ad[2 * jj + (s >> 1)];
+            acc += live ? I * sc : 0.0f;
+        }
+    }
+    return acc;
+}
+
 // Q4_0 F1 decode with 3..7 tokens: the group's nibbles and block scales unpacked once for all the tokens
 // (measured faster for Q4_0 only; the other types unpack per token in group_dot), then per token
 // group_dot's Q4_0 arithmetic.
@@ -402,12 +434,13 @@ JAMHIP_DEV float q40_dot_f1(const Q40Codes& u, const int8_t* aq, const float* ad
 // One thread per 16-element half-block; the halves of a 32-block sit in adjacent lanes, which exchange
 // their |x| maxima and Σq. Elements past k (a partial last group) quantize as zeros.
 constexpr int QS_LDS = 272;
-// MXFP4 with one token (fused prologue): the codes go to LDS as f16 pairs (q_i, q_{i+16}) of each 32-block,
-// the order in which the e2m1 conversion returns a weight byte's two codes (mx_dot_f16): 512 bytes per group,
-// padded to QS_F16.
+// The e2m1 types with one token (fused prologue): the codes go to LDS as f16 pairs in the order in which the
+// e2m1 conversion returns a weight byte's two codes: (q_i, q_{i+16}) of each 32-block for MXFP4 (mode 1,
+// mx_dot_f16), (q_i, q_{i+8}) of each 16-element sub-block for NVFP4 (mode 2, nv_dot_f16); 512 bytes per
+// group, padded to QS_F16. Mode 0: int8 codes.
 constexpr int QS_F16 = 528;
-template <int DT, int FL, int NT, int HP> constexpr bool f16_pairs() {
-    return DT == MXFP4 && FL == 1 && NT == 1 && HP > 0;
+template <int DT, int FL, int NT, int HP> constexpr int f16_pairs() {
+    return FL == 1 && NT == 1 && HP > 0 ? (DT == MXFP4 ? 1 : DT == NVFP4 ? 2 : 0) : 0;
 }
 constexpr int MV_WAVES = 8;   // waves per GEMV workgroup (512 threads)
 
@@ -446,7 +479,7 @@ JAMHIP_DEV void a_load(APre<HP>& pre, const float* __restrict__ a, int lda, int 
     }
 }
 
-template <int NT, int HP, int NWV, bool F16P = false>
+template <int NT, int HP, int NWV, int F16P = 0>
 JAMHIP_DEV void f1_store(const APre<HP>& pre, int k, int Gk, int ntv, int8_t* lq, float* ld, float* las, int* ls16,
                          char* dummy) {
     // branch-free: a thread past the last half-block (its loads were clamped) quantizes anyway and writes to
@@ -468,7 +501,24 @@ JAMHIP_DEV void f1_store(const APre<HP>& pre, int k, int Gk, int ntv, int8_t* lq
         am = fmaxf(am, __shfl_xor(am, 1));
         const float db = am / 127.0f;
         const float id = db > 0.0f ? 1.0f / db : 0.0f;
-        if constexpr (F16P) {
+        if constexpr (F16P == 2) {
+            // pair slot u of this half (an NVFP4 sub-block) is (q_u, q_{u+8}), both this thread's; exact in f16
+            if (valid) {
+                uint32_t sp[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    const float q0 = fminf(fmaxf(rintf(x[u] * id), -128.0f), 127.0f);
+                    const float q1 = fminf(fmaxf(rintf(x[u + 8] * id), -128.0f), 127.0f);
+                    sp[u] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(q0, q1));
+                }
+                uint4* p4 = reinterpret_cast<uint4*>(lq + (int64_t) (hh >> 4) * QS_F16 + 32 * (hh & 15));
+                p4[0] = make_uint4(sp[0], sp[1], sp[2], sp[3]);
+                p4[1] = make_uint4(sp[4], sp[5], sp[6], sp[7]);
+                if ((hh & 1) == 0) ld[hh >> 1] = db;
+            }
+            continue;
+        }
+        if constexpr (F16P == 1) {
             // element e of this half is f16 number (hh & 1) of pair slot e of its block (the codes are
             // integers in [-128, 127], exact in f16 whatever the rounding); MXFP4 reads no sums
             if (valid) {
@@ -677,7 +727,7 @@ __global__ void __launch_bounds__(64 * NWV) mv_kernel(WeightView w, ActQ A, cons
     int64_t tq = kf, td = nbf, ts = FL == 1 ? nbf : 2 * nbf, t16 = 2 * nbf;
     int QS = 256;
     if constexpr (FUSE) {
-        constexpr bool F16P = f16_pairs<DT, FL, NT, HP>();
+        constexpr int F16P = f16_pairs<DT, FL, NT, HP>();
         constexpr int QSB = F16P ? QS_F16 : QS_LDS;
         char* dummy = reinterpret_cast<char*>(smem + NWV * ITEMS * 64 * NT * 4);   // 32 bytes
         int8_t* lq = reinterpret_cast<int8_t*>(dummy + 32);
@@ -729,8 +779,10 @@ __global__ void __launch_bounds__(64 * NWV) mv_kernel(WeightView w, ActQ A, cons
                 if (t >= ntv) break;
                 const int tt = FUSE ? t : t0 + t;
                 float p;
-                if constexpr (f16_pairs<DT, FL, NT, HP>())
+                if constexpr (f16_pairs<DT, FL, NT, HP>() == 1)
                     p = mx_dot_f16(buf[i], aq + (int64_t) gg * QS, ad + 8 * gg, nbv);
+                else if constexpr (f16_pairs<DT, FL, NT, HP>() == 2)
+                    p = nv_dot_f16(buf[i], aq + (int64_t) gg * QS, ad + 8 * gg, nbv);
                 else
                     p = group_dot<DT, FL>(buf[i], aq + tt * tq + (int64_t) gg * QS, ad + tt * td + 8 * gg,
                                           as + tt * ts + (FL == 1 ? 8 : 16) * gg, s16 + tt * t16 + 16 * gg, nbv);

@@ -303,17 +303,17 @@ def test_split_k_decode(hip, oracle, dt):
         assert hip.evict(Segment.of(w)) == JAM.OK
 
 
-@pytest.mark.parametrize("dt", O.QUANT_TYPES)
+@pytest.mark.parametrize("dt", O.ALL_QUANT_TYPES)
 def test_decode_fused_prologue_matches_quantized_copy(hip, oracle, dt):
     """1..7 tokens: rows the kernel can load as 16-byte pieces are quantized in each workgroup's prologue (MXFP4
-    with one token: into f16 pairs for the hardware e2m1 conversion and v_dot2), rows that are not
+    and NVFP4 with one token: into f16 pairs for the hardware e2m1 conversion and v_dot2), rows that are not
     (lda = k + 1) come from the F1 copy through the int8 dot products. Both give jam's integer block sums, so the outputs are
     bit-identical: a partial last group, the k = 14336 one-band workgroups (split K from two tokens on) and a
     small 4-wave grid."""
     import torch
     from qxotic_amd.jam import JAM, Segment
     be = O.BLOCK[dt][0]
-    for (m, k) in [(200, 2880 if be == 32 else 2816), (96, 14336), (520, 4096)]:
+    for (m, k) in [(200, 2880 if 2880 % be == 0 else 2816), (96, 14336), (520, 4096)]:
         w = oracle.quantize(dt, oracle.normal(0x5A11C0DE ^ 0xF1 ^ dt ^ k, (m, k), 0.0, 0.02))
         assert hip.pin(Segment.of(w), dt, k, m) == JAM.OK, hip.last_error()
         try:
