@@ -327,7 +327,8 @@ __global__ void __launch_bounds__(256) moe_gather_kernel(const float* __restrict
 // which the expert loop reaches them — so the result is bit-identical and needs no atomics. The row's
 // routes are loaded once into LDS; one thread drops the ones without a slot and sorts the rest (stable
 // insertion sort on the expert id) into (slot, prob) lists; then every thread runs the fma chain for its
-// columns (four at a time when V4: rows 16-byte aligned, dim % 4 == 0).
+// columns (four at a time when V4: rows 16-byte aligned, dim % 4 == 0). Workgroup column blockIdx.y takes
+// every gridDim.y-th 256-column piece (few tokens: several workgroups per token, one piece each).
 template <bool V4>
 __global__ void __launch_bounds__(256) moe_combine_kernel(const float* __restrict__ y, int ldy,
                                                          const int* __restrict__ route_expert,
@@ -369,7 +370,7 @@ __global__ void __launch_bounds__(256) moe_combine_kernel(const float* __restric
     const int nv = l_n;
     float* o = out + (int64_t) s * ldo;
     if constexpr (V4) {
-        for (int i = threadIdx.x; i < dim / 4; i += 256) {
+        for (int i = threadIdx.x + 256 * blockIdx.y; i < dim / 4; i += 256 * gridDim.y) {
             float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             for (int j = 0; j < nv; j++) {
                 const float p = l_prob[j];
@@ -382,7 +383,7 @@ __global__ void __launch_bounds__(256) moe_combine_kernel(const float* __restric
             reinterpret_cast<float4*>(o)[i] = acc;
         }
     } else {
-        for (int i = threadIdx.x; i < dim; i += 256) {
+        for (int i = threadIdx.x + 256 * blockIdx.y; i < dim; i += 256 * gridDim.y) {
             float acc = 0.0f;
             for (int j = 0; j < nv; j++) acc = fmaf(l_prob[j], y[(int64_t) l_slot[j] * ldy + i], acc);
             o[i] = acc;
@@ -451,12 +452,16 @@ hipError_t launch_moe_combine(const float* y, int ldy, const int* route_expert, 
                               hipStream_t st) {
     if (topk > 16) return hipErrorNotSupported;
     if (seq <= 0) return hipSuccess;
-    if (rows16(y, ldy, dim) && rows16(out, ldo, dim))
-        moe_combine_kernel<true><<<seq, 256, 0, st>>>(y, ldy, route_expert, route_prob, route_slot, seq, topk, E, dim,
-                                                      out, ldo);
-    else
-        moe_combine_kernel<false><<<seq, 256, 0, st>>>(y, ldy, route_expert, route_prob, route_slot, seq, topk, E, dim,
+    const bool v4 = rows16(y, ldy, dim) && rows16(out, ldo, dim);
+    // below 256 tokens a token's columns are split over up to 64 workgroups of 256 threads (one piece each)
+    const int pieces = ((v4 ? dim / 4 : dim) + 255) / 256;
+    const dim3 grid((unsigned) seq, (unsigned) (seq >= 256 ? 1 : pieces < 64 ? (pieces > 0 ? pieces : 1) : 64));
+    if (v4)
+        moe_combine_kernel<true><<<grid, 256, 0, st>>>(y, ldy, route_expert, route_prob, route_slot, seq, topk, E, dim,
                                                        out, ldo);
+    else
+        moe_combine_kernel<false><<<grid, 256, 0, st>>>(y, ldy, route_expert, route_prob, route_slot, seq, topk, E, dim,
+                                                        out, ldo);
     return hipGetLastError();
 }
 
