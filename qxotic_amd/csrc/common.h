@@ -95,6 +95,11 @@ struct WeightView {
     const uint8_t* sc;   // plane 1 of the device copy
     int64_t G;           // groups per row of the device layout
     int64_t r0;          // device-copy row of the view's row 0
+    // Host-side routing facts, unused by the kernels: whether every group's block scales fold exactly into
+    // the matrix-core GEMM's f16 operands (repack_kernel), and for a copy staged by the current call the
+    // device flag the repack left, read only when a call would take the matrix cores.
+    int fold_ok = 1;
+    const int* fold_flag = nullptr;
 };
 
 // Plane-0 address of chunk 0 of group g of view row `row` (chunk c at +c·512), and its plane-1 address.

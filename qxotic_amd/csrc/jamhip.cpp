@@ -91,6 +91,7 @@ struct Pin {
     // taken at pin time, and the count of per-call spot checks made against it
     std::vector<uint64_t> pages;
     uint64_t checks = 0;
+    int fold_ok = 1;    // the repack's check: block scales fold exactly into the matrix-core operands
 };
 
 // A host weight range seen by jamhip_mm while not resident (the autopin candidates).
@@ -179,6 +180,7 @@ struct jamhip_ctx {
     std::vector<Pin> pins;
     int64_t pinned_bytes = 0;   // sum of pins[].bytes, under pin_mu
     DevBuf act, gact, part, moe, route;       // kernel scratch (addresses may be captured in graphs)
+    DevBuf fold;                              // the repack's fold flag (one int)
     StageBuf a_stage, c_stage, w_raw, w_stage;   // staging of host copies
     HostBuf a_host, c_host;   // jamhip_mm's pinned bounce buffers for A and C
     // autopin (jamhip_ctx_set_autopin): pin a host weight range on its `autopin`-th sighting, 0 = off
@@ -238,14 +240,19 @@ int64_t row_bytes(int dt, int64_t elems) { return elems / block_elems(dt) * bloc
 
 // Registry lookup: W inside a pinned range, on a row boundary, same (dtype, ldw), rows [r0, r0+m) held.
 // Pins are kept sorted by host address and never overlap, so the only candidate is the last pin that
-// starts at or below W: one binary search per call.
-bool lookup(jamhip_ctx* ctx, const void* w, int dt, int ldw, int m, WeightView* out) {
+// starts at or below W: one binary search per call. An autopin (a pin with page hashes) serves only
+// jamhip_mm calls that start at its first byte, after their spot check (autopin_lookup): every other
+// lookup passes explicit_only and does not see it, so a device entry point (whose launches a graph may
+// capture) never refers to a copy that a failed check could free, and a call at a row offset into an
+// autopinned range is staged rather than served without a check.
+bool lookup(jamhip_ctx* ctx, const void* w, int dt, int ldw, int m, WeightView* out, bool explicit_only = true) {
     std::lock_guard<std::mutex> lk(ctx->pin_mu);
     const uintptr_t p = reinterpret_cast<uintptr_t>(w);
     auto it = std::upper_bound(ctx->pins.begin(), ctx->pins.end(), p,
                                [](uintptr_t v, const Pin& pin) { return v < pin.host; });
     if (it == ctx->pins.begin()) return false;
     const Pin& pin = *(it - 1);
+    if (explicit_only && !pin.pages.empty()) return false;
     if (pin.dt != dt || pin.ldw != ldw || p >= pin.host + (uintptr_t) pin.span) return false;
     const int64_t off = (int64_t) (p - pin.host), rbytes = row_bytes(dt, ldw);
     if (off % rbytes) return false;
@@ -255,39 +262,62 @@ bool lookup(jamhip_ctx* ctx, const void* w, int dt, int ldw, int m, WeightView* 
     out->sc = pin.sc;
     out->G = pin.G;
     out->r0 = r0;
+    out->fold_ok = pin.fold_ok;
+    out->fold_flag = nullptr;
     return true;
 }
 
 // Upload `rows` raw host rows (stride raw_stride bytes, rb blocks used per row) into a device-layout
 // buffer of G groups per row at dst (plane 0) / dst_sc (plane 1) via a staging copy and the repack kernel.
+// The repack also leaves the fold flag (launch_repack) in ctx->fold for Q8_0 / Q4_0 / MXFP4; *flag gets its
+// device address then (null otherwise).
 jamhip_status upload(jamhip_ctx* ctx, const uint8_t* host, int dt, int64_t raw_stride, int64_t rows, int64_t rb,
-                     int64_t G, uint8_t* dst, uint8_t* dst_sc) {
+                     int64_t G, uint8_t* dst, uint8_t* dst_sc, const int** flag) {
     const int64_t span = (rows - 1) * raw_stride + rb * block_bytes(dt);
     hipError_t e;
     if ((e = ctx->w_raw.ensure((size_t) span)) != hipSuccess) return hip_fail(ctx, e, "weight staging alloc");
+    int* fl = nullptr;
+    if (dt == Q8_0 || dt == Q4_0 || dt == MXFP4) {
+        if ((e = ctx->fold.ensure(sizeof(int))) != hipSuccess) return hip_fail(ctx, e, "fold flag alloc");
+        fl = (int*) ctx->fold.p;
+    }
     if ((e = hipMemcpyAsync(ctx->w_raw.p, host, (size_t) span, hipMemcpyHostToDevice, ctx->stream)) != hipSuccess)
         return hip_fail(ctx, e, "weight upload");
-    if ((e = launch_repack(dt, (const uint8_t*) ctx->w_raw.p, raw_stride, rows, rb, G, dst, dst_sc, ctx->stream)) !=
+    if ((e = launch_repack(dt, (const uint8_t*) ctx->w_raw.p, raw_stride, rows, rb, G, dst, dst_sc, ctx->stream, fl)) !=
         hipSuccess)
         return hip_fail(ctx, e, "weight repack");
+    *flag = fl;
+    return JAMHIP_OK;
+}
+
+// Reads a fold flag the repack left (stream-ordered, then a synchronize): 1 when every group folds exactly.
+jamhip_status read_fold(jamhip_ctx* ctx, const int* flag, int* fold_ok) {
+    int v = 0;
+    hipError_t e = hipMemcpyAsync(&v, flag, sizeof v, hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "fold flag read");
+    *fold_ok = v == 0;
     return JAMHIP_OK;
 }
 
 // Resolve W to a device view: the registry, else a per-call staged copy of rows [0, m), k elements each.
 jamhip_status resolve_w(jamhip_ctx* ctx, const void* w, int dt, int ldw, int m, int k, WeightView* wv) {
-    if (lookup(ctx, w, dt, ldw, m, wv)) return JAMHIP_OK;
+    if (lookup(ctx, w, dt, ldw, m, wv, true)) return JAMHIP_OK;
     const int64_t rb = k / block_elems(dt), G = view_G(dt, k);
     const int64_t qsz = plane0_bytes(dt, m, k), ssz = plane1_bytes(dt, m, k);
     hipError_t e = ctx->w_stage.ensure((size_t) (qsz + ssz));
     if (e != hipSuccess) return hip_fail(ctx, e, "weight stage alloc");
     uint8_t* dst = (uint8_t*) ctx->w_stage.p;
     uint8_t* dsc = dst + qsz;
-    jamhip_status st = upload(ctx, (const uint8_t*) w, dt, row_bytes(dt, ldw), m, rb, G, dst, dsc);
+    const int* flag = nullptr;
+    jamhip_status st = upload(ctx, (const uint8_t*) w, dt, row_bytes(dt, ldw), m, rb, G, dst, dsc, &flag);
     if (st != JAMHIP_OK) return st;
     wv->qs = dst;
     wv->sc = dsc;
     wv->G = G;
     wv->r0 = 0;
+    wv->fold_ok = 1;
+    wv->fold_flag = flag;
     return JAMHIP_OK;
 }
 
@@ -302,6 +332,20 @@ bool mma_path(int dt, int k, const WeightView& wv) {
     if (env_true("JAM_HIP_NO_MMA")) return false;
     return (((dt == Q4_K || dt == Q6_K) && k % 256 == 0) || dt == MXFP4 || dt == Q4_0 || dt == Q8_0) &&
            (wv.r0 & 31) == 0 && gemm_prep_fits(k);
+}
+
+// mma_path for jam's semantics: also every group of W must fold its block scales exactly (Q8_0, Q4_0, MXFP4;
+// repack_kernel). A copy staged by this call has its flag read here, once (a synchronize), and only when the
+// call would otherwise take the matrix cores.
+bool mma_exact(jamhip_ctx* ctx, int dt, int k, WeightView& wv) {
+    if (!mma_path(dt, k, wv)) return false;
+    if (wv.fold_flag != nullptr) {
+        int ok = 0;
+        if (read_fold(ctx, wv.fold_flag, &ok) != JAMHIP_OK) ok = 0;   // unknown: the exact kernels
+        wv.fold_ok = ok;
+        wv.fold_flag = nullptr;
+    }
+    return wv.fold_ok != 0;
 }
 
 // Smallest n that takes the matrix cores (n >= 8 is F2 either way; small grids split K), from a sweep of
@@ -367,7 +411,7 @@ jamhip_status scratch_fail(jamhip_ctx* ctx, const Scratch& sc, hipError_t e, con
 // Quantize A (device, f32 [n][lda]) and run the matmul into C (device, [n][ldc]). Decode-sized calls
 // with k < 8192 are one fused launch and touch no scratch (safe under stream capture once W is pinned);
 // from k = 8192 the decode kernels split K and sum the slices from the context's split buffer.
-jamhip_status compute(jamhip_ctx* ctx, Scratch& sc, int dt, const WeightView& wv, const float* a, int lda, float* c,
+jamhip_status compute(jamhip_ctx* ctx, Scratch& sc, int dt, WeightView wv, const float* a, int lda, float* c,
                       int ldc, int m, int n, int k, const Epi& ep = Epi{}) {
     hipError_t e;
     float* gpart = nullptr;   // the decode kernels' K-split partials
@@ -402,7 +446,7 @@ jamhip_status compute(jamhip_ctx* ctx, Scratch& sc, int dt, const WeightView& wv
             return hip_fail(ctx, e, "mx gemm launch");
         return JAMHIP_OK;
     }
-    if (n >= mma_min_n(dt, m, k) && m16 > 0 && mma_path(dt, k, wv)) {
+    if (n >= mma_min_n(dt, m, k) && m16 > 0 && mma_exact(ctx, dt, k, wv)) {
         GemmAct G;
         void* gact = nullptr;
         float* part = nullptr;
@@ -457,41 +501,6 @@ jamhip_status compute(jamhip_ctx* ctx, int dt, const WeightView& wv, const float
     return compute(ctx, sc, dt, wv, a, lda, c, ldc, m, n, k, ep);
 }
 
-// Pin rows [0, m) of the host tensor at w (caller holds the Busy guard, device current). The staging
-// buffer is kept when `keep_staging` (a registry load reuses it for every tensor).
-jamhip_status pin_range(jamhip_ctx* ctx, const void* w, int wt, int ldw, int64_t m, bool keep_staging) {
-    const uintptr_t host = reinterpret_cast<uintptr_t>(w);
-    const int64_t rb = ldw / block_elems(wt), G = view_G(wt, ldw), span = m * row_bytes(wt, ldw);
-    {
-        std::lock_guard<std::mutex> lk(ctx->pin_mu);
-        auto it = std::lower_bound(ctx->pins.begin(), ctx->pins.end(), host,
-                                   [](const Pin& pin, uintptr_t v) { return pin.host < v; });
-        if (it != ctx->pins.end() && it->host == host && it->dt == wt && it->ldw == ldw && it->rows == m)
-            return JAMHIP_OK;   // already pinned
-        const bool hits_next = it != ctx->pins.end() && it->host < host + (uintptr_t) span;
-        const bool hits_prev = it != ctx->pins.begin() && host < (it - 1)->host + (uintptr_t) (it - 1)->span;
-        if (hits_next || hits_prev) return fail(ctx, JAMHIP_EINVAL, "pin: range overlaps a pinned tensor (evict it first)");
-    }
-    const int64_t qsz = plane0_bytes(wt, m, ldw), ssz = plane1_bytes(wt, m, ldw);
-    uint8_t* dev = nullptr;
-    hipError_t e = hipMalloc((void**) &dev, (size_t) (qsz + ssz));
-    if (e != hipSuccess) return hip_fail(ctx, e, "pin: device alloc");
-    uint8_t* sc = dev + qsz;
-    jamhip_status st = upload(ctx, (const uint8_t*) w, wt, row_bytes(wt, ldw), m, rb, G, dev, sc);
-    if (st == JAMHIP_OK && (e = hipStreamSynchronize(ctx->stream)) != hipSuccess) st = hip_fail(ctx, e, "pin: sync");
-    if (st != JAMHIP_OK) {
-        (void) hipFree(dev);
-        return st;
-    }
-    if (!keep_staging) ctx->w_raw.release();   // staging is sized to the tensor; do not hold it
-    std::lock_guard<std::mutex> lk(ctx->pin_mu);
-    auto it = std::lower_bound(ctx->pins.begin(), ctx->pins.end(), host,
-                               [](const Pin& pin, uintptr_t v) { return pin.host < v; });
-    ctx->pins.insert(it, Pin{host, span, wt, ldw, m, G, dev, sc, qsz + ssz});
-    ctx->pinned_bytes += qsz + ssz;
-    return JAMHIP_OK;
-}
-
 // Drop the pin that starts at host (caller holds the Busy guard, device current); false if none does.
 bool evict_at(jamhip_ctx* ctx, uintptr_t host) {
     std::lock_guard<std::mutex> lk(ctx->pin_mu);
@@ -504,6 +513,57 @@ bool evict_at(jamhip_ctx* ctx, uintptr_t host) {
     if (!it->pages.empty()) ctx->autopin_bytes -= it->bytes;
     ctx->pins.erase(it);
     return true;
+}
+
+// Pin rows [0, m) of the host tensor at w (caller holds the Busy guard, device current). The staging
+// buffer is kept when `keep_staging` (a registry load reuses it for every tensor). An explicit pin (the
+// caller's jamhip_weight_pin or a registry load, not autopin) takes over autopins in its way: they are
+// evicted and the range is copied afresh (an autopin's copy is only spot-checked, so it may predate the bytes
+// the caller is pinning); an overlapping explicit pin is an error.
+jamhip_status pin_range(jamhip_ctx* ctx, const void* w, int wt, int ldw, int64_t m, bool keep_staging,
+                        bool explicit_pin) {
+    const uintptr_t host = reinterpret_cast<uintptr_t>(w);
+    const int64_t rb = ldw / block_elems(wt), G = view_G(wt, ldw), span = m * row_bytes(wt, ldw);
+    std::vector<uintptr_t> drop;   // autopins overlapping [host, host + span)
+    {
+        std::lock_guard<std::mutex> lk(ctx->pin_mu);
+        auto it = std::lower_bound(ctx->pins.begin(), ctx->pins.end(), host,
+                                   [](const Pin& pin, uintptr_t v) { return pin.host < v; });
+        if (it != ctx->pins.end() && it->host == host && it->dt == wt && it->ldw == ldw && it->rows == m &&
+            it->pages.empty() == explicit_pin)
+            return JAMHIP_OK;   // already pinned
+        auto first = it;
+        if (first != ctx->pins.begin() && host < (first - 1)->host + (uintptr_t) (first - 1)->span) --first;
+        for (auto p = first; p != ctx->pins.end() && p->host < host + (uintptr_t) span; ++p) {
+            if (!explicit_pin || p->pages.empty())
+                return fail(ctx, JAMHIP_EINVAL, "pin: range overlaps a pinned tensor (evict it first)");
+            drop.push_back(p->host);
+        }
+    }
+    for (uintptr_t h : drop) evict_at(ctx, h);
+    const int64_t qsz = plane0_bytes(wt, m, ldw), ssz = plane1_bytes(wt, m, ldw);
+    uint8_t* dev = nullptr;
+    hipError_t e = hipMalloc((void**) &dev, (size_t) (qsz + ssz));
+    if (e != hipSuccess) return hip_fail(ctx, e, "pin: device alloc");
+    uint8_t* sc = dev + qsz;
+    const int* flag = nullptr;
+    int fold_ok = 1;
+    jamhip_status st = upload(ctx, (const uint8_t*) w, wt, row_bytes(wt, ldw), m, rb, G, dev, sc, &flag);
+    if (st == JAMHIP_OK && (e = hipStreamSynchronize(ctx->stream)) != hipSuccess) st = hip_fail(ctx, e, "pin: sync");
+    if (st == JAMHIP_OK && flag) st = read_fold(ctx, flag, &fold_ok);
+    if (st != JAMHIP_OK) {
+        (void) hipFree(dev);
+        return st;
+    }
+    if (!keep_staging) ctx->w_raw.release();   // staging is sized to the tensor; do not hold it
+    std::lock_guard<std::mutex> lk(ctx->pin_mu);
+    auto it = std::lower_bound(ctx->pins.begin(), ctx->pins.end(), host,
+                               [](const Pin& pin, uintptr_t v) { return pin.host < v; });
+    Pin pin{host, span, wt, ldw, m, G, dev, sc, qsz + ssz};
+    pin.fold_ok = fold_ok;
+    ctx->pins.insert(it, std::move(pin));
+    ctx->pinned_bytes += qsz + ssz;
+    return JAMHIP_OK;
 }
 
 // ---- autopin: residency for callers that never pin (an unedited jinfer passes the same mmap'd address for
@@ -559,6 +619,8 @@ bool autopin_lookup(jamhip_ctx* ctx, const void* w, int dt, int ldw, int m, Weig
             out->sc = pin.sc;
             out->G = pin.G;
             out->r0 = 0;
+            out->fold_ok = pin.fold_ok;
+            out->fold_flag = nullptr;
             ctx->ap_stats[1]++;
             return true;
         }
@@ -595,7 +657,7 @@ void autopin_sight(jamhip_ctx* ctx, const void* w, int dt, int ldw, int m, int k
     }
     if (!pin_now) return;
     std::vector<uint64_t> pages = range_hashes((const uint8_t*) w, span);
-    if (pin_range(ctx, w, dt, ldw, m, true) != JAMHIP_OK) return;   // overlap, allocation: stay staged
+    if (pin_range(ctx, w, dt, ldw, m, true, false) != JAMHIP_OK) return;   // overlap, allocation: stay staged
     std::lock_guard<std::mutex> lk(ctx->pin_mu);
     auto it = std::lower_bound(ctx->pins.begin(), ctx->pins.end(), host,
                                [](const Pin& pin, uintptr_t v) { return pin.host < v; });
@@ -632,17 +694,19 @@ jamhip_status mm_impl(jamhip_ctx* ctx, const void* w, int wt, int ldw, const voi
     if (!guard.ok) return fail(ctx, JAMHIP_EBUSY, "context busy");
     (void) hipSetDevice(ctx->device);
     WeightView wv;
-    if (ctx->autopin > 0 && !autopin_lookup(ctx, w, wt, ldw, m, &wv)) {
+    bool served = false;   // by an autopin whose spot check passed
+    if (ctx->autopin > 0 && !(served = autopin_lookup(ctx, w, wt, ldw, m, &wv))) {
         WeightView probe;
-        if (!lookup(ctx, w, wt, ldw, m, &probe)) {   // not resident by any pin: count the sighting
+        if (!lookup(ctx, w, wt, ldw, m, &probe)) {   // not resident by an explicit pin: count the sighting
             autopin_sight(ctx, w, wt, ldw, m, k);
-            if (!autopin_lookup(ctx, w, wt, ldw, m, &wv)) {
+            if (!(served = autopin_lookup(ctx, w, wt, ldw, m, &wv))) {
                 std::lock_guard<std::mutex> lk(ctx->pin_mu);
                 ctx->ap_stats[2]++;
             }
         }
     }
-    if ((st = resolve_w(ctx, w, wt, ldw, m, k, &wv)) != JAMHIP_OK) return st;
+    // an explicit pin, else a staged copy (an autopinned range is never served without its check)
+    if (!served && (st = resolve_w(ctx, w, wt, ldw, m, k, &wv)) != JAMHIP_OK) return st;
     hipError_t e;
     const size_t abytes = (size_t) n * k * 4, cbytes = (size_t) n * m * 4;
     if ((e = ctx->a_stage.ensure(abytes)) != hipSuccess) return hip_fail(ctx, e, "A staging alloc");
@@ -761,7 +825,7 @@ jamhip_status weight_pin_impl(jamhip_ctx* ctx, const void* w, int wt, int ldw, i
     Busy guard(ctx);
     if (!guard.ok) return fail(ctx, JAMHIP_EBUSY, "context busy");
     (void) hipSetDevice(ctx->device);
-    return pin_range(ctx, w, wt, ldw, m, false);
+    return pin_range(ctx, w, wt, ldw, m, false, true);
 }
 
 jamhip_status set_autopin_impl(jamhip_ctx* ctx, int sightings, int64_t max_bytes) {
@@ -861,8 +925,8 @@ jamhip_status mm_grouped_ex_impl(jamhip_ctx* ctx, const void* w, int wt, int ldw
     // slot map from the device counts and quantizes every expert's rows (F1 for experts of 1..7 rows, whose
     // 64-slot blocks then take the GEMM's single-token-tile form), so neither the offsets kernel nor the F1
     // decode launch runs. Sparser calls keep the F1 decode kernel for their small experts.
-    if (rows_cap >= 8 * E && E <= PREP_FUSED_MAX_E && mma_path(wt, k, wv) && m % 32 == 0 &&
-        !(wt == MXFP4 && ctx->mx_native)) {
+    if (rows_cap >= 8 * E && E <= PREP_FUSED_MAX_E && m % 32 == 0 && !(wt == MXFP4 && ctx->mx_native) &&
+        mma_exact(ctx, wt, k, wv)) {
         const PrepGroups pg{(const int*) counts_dev, E, rows_cap, off, poff64, map64, cap64, (int*) offsets_dev};
         const Groups g{off, poff8, map8, poff64, map64, m, static_cast<const float*>(bias_dev)};
         GemmAct G;
@@ -920,7 +984,7 @@ jamhip_status mm_grouped_ex_impl(jamhip_ctx* ctx, const void* w, int wt, int ldw
         if ((e = launch_mx_prep_grouped(a, lda, k, ctx->mx_native, g, cap64, ctx->gact.p, &X, ctx->stream)) != hipSuccess ||
             (e = launch_mx_gemm_grouped(ctx->mx_native, wv, X, g, cap64, c, ldc, ctx->stream)) != hipSuccess)
             return hip_fail(ctx, e, "grouped: mx gemm launch");
-    } else if (mma_path(wt, k, wv) && m % 32 == 0) {
+    } else if (m % 32 == 0 && mma_exact(ctx, wt, k, wv)) {
         GemmAct G;
         if ((e = ctx->gact.ensure(gemm_act_bytes_np(wt, cap64 * 64, k))) != hipSuccess)
             return hip_fail(ctx, e, "grouped: gemm activation scratch alloc");
@@ -1394,7 +1458,7 @@ jamhip_status gguf_pin_impl(jamhip_ctx* ctx, const jamhip_gguf* g, const void* d
     jamhip_status st = registry_runs(ctx, *g->f, &runs);   // every tensor checked before anything is pinned
     if (st != JAMHIP_OK) return st;
     for (const Run& r : runs) {
-        if ((st = pin_range(ctx, base + r.offset, r.type, r.ldw, r.rows, true)) != JAMHIP_OK) {
+        if ((st = pin_range(ctx, base + r.offset, r.type, r.ldw, r.rows, true, true)) != JAMHIP_OK) {
             fail(ctx, st, "gguf pin: run at data offset " + std::to_string(r.offset) + ": " + error_of(ctx));
             break;
         }

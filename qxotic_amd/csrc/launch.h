@@ -14,9 +14,11 @@ hipError_t launch_quant_f1(const float* a, int lda, int n, int k, int8_t* q, flo
 // F2: q [n][k] int8, d [n][k/32], xs [n][k/16] (raw f32 Σx).
 hipError_t launch_quant_f2(const float* a, int lda, int n, int k, int8_t* q, float* d, float* xs, hipStream_t st);
 
-// raw GGUF rows (rb blocks each, stride raw_stride bytes) -> the device layout with G groups per row
+// raw GGUF rows (rb blocks each, stride raw_stride bytes) -> the device layout with G groups per row. For
+// Q8_0, Q4_0 and MXFP4 with a non-null flag (device int), *flag ends 1 if some group's block scales cannot
+// be folded exactly into the matrix-core GEMM's f16 operands (prep.hip, repack_kernel), else 0.
 hipError_t launch_repack(int dt, const uint8_t* raw, int64_t raw_stride, int64_t rows, int64_t rb, int64_t G,
-                         uint8_t* qs, uint8_t* sc, hipStream_t st);
+                         uint8_t* qs, uint8_t* sc, hipStream_t st, int* flag = nullptr);
 
 // Expert grouping of a grouped matmul (moe.hip): CSR row offsets off[E+1] of the experts' rows in A and
 // C, the 8-token tile map (poff8, map8) and the 64-token slot map (poff64, map64) of the experts with at

@@ -44,10 +44,23 @@ __global__ void __launch_bounds__(256) quant_f2_kernel(const float* __restrict__
 // common.h. One thread per (tile, group, row of the tile), consecutive threads on consecutive rows so each
 // chunk store of 32 threads fills 512 contiguous bytes; a group past the row's last block, and every row
 // past `rows` in the last tile, is zero-filled. Runs once per pinned tensor.
+//
+// Q8_0, Q4_0 and MXFP4 groups are also checked for the matrix-core GEMM (mma.hip), which folds each block's
+// scale into an f16 weight operand relative to a per-row, per-group reference: MXFP4 codes times
+// 2^(e_b - e_ref + 1), Q4_0 / Q8_0 codes times d_b·2^s_r with s_r set by the group's largest fp16 exponent.
+// That is exact while every folded operand is a normal f16 (>= 2^-14). A block whose products are zero
+// whatever its scale (MXFP4: every code 0 or -0; Q8_0: every q 0) must not set the reference, or a large
+// scale on it would push its neighbours below f16's range: such a block's scale is stored as 0 (MXFP4 e=0,
+// Q8_0 d=0; its terms are zero on every path either way) and the reference comes from the other blocks. A
+// Q4_0 block always counts (jam's n >= 8 term -fl(8d)·fl(xs0+xs1) does not vanish with the codes). A group
+// whose blocks still span more than the f16 range below its reference (MXFP4 e_b < e_ref - 14; Q8_0
+// |d_b| < 2^(F - 36), Q4_0 |d_b| < 2^(F - 39), F the largest fp16 exponent field), or that holds a non-finite
+// scale (MXFP4 e = 255, which jam decodes as +Inf; an fp16 Inf/NaN), sets *flag: the host then keeps the
+// tensor off the matrix cores, on kernels that apply every block scale in f32 as jam does.
 template <int DT>
 __global__ void __launch_bounds__(256) repack_kernel(const uint8_t* __restrict__ raw, int64_t raw_stride,
                                                      int64_t rows, int64_t rb, int64_t G, uint8_t* __restrict__ qs,
-                                                     uint8_t* __restrict__ sc) {
+                                                     uint8_t* __restrict__ sc, int* __restrict__ flag) {
     constexpr int NC = group_chunks(DT), SB = group_scale_bytes(DT), BPG = blocks_per_group(DT);
     const int64_t i = (int64_t) blockIdx.x * 256 + threadIdx.x;
     if (i >= tiled_rows(rows) * G) return;
@@ -94,6 +107,7 @@ __global__ void __launch_bounds__(256) repack_kernel(const uint8_t* __restrict__
         ds[0] = live ? b[208] : 0;
         ds[1] = live ? b[209] : 0;
     } else {
+        bool nz[BPG];   // the block has a code whose product is not zero
         for (int j = 0; j < BPG; j++) {
             const int64_t blk = g * BPG + j;
             uint8_t q[32] = {0}, s[2] = {0, 0};   // a block past the row end, or a padding row, stays zero
@@ -103,6 +117,9 @@ __global__ void __launch_bounds__(256) repack_kernel(const uint8_t* __restrict__
                 for (int t = 0; t < sbytes; t++) s[t] = b[t];
                 for (int t = 0; t < qbytes; t++) q[t] = b[sbytes + t];
             }
+            uint8_t any = 0;   // Q8_0: any q != 0; MXFP4: any nibble other than +-0 (codes 0 and 8)
+            for (int t = 0; t < 32; t++) any |= DT == MXFP4 ? (uint8_t) (q[t] & 0x77) : q[t];
+            nz[j] = any != 0;
             if constexpr (DT == Q8_0) {                // d fp16 @0, q @2..33
                 ds[2 * j] = s[0];
                 ds[2 * j + 1] = s[1];
@@ -119,14 +136,44 @@ __global__ void __launch_bounds__(256) repack_kernel(const uint8_t* __restrict__
                 for (int t = 0; t < 16; t++) chunk(j)[t] = q[t];
             }
         }
-        if constexpr (DT == MXFP4) {                   // byte 8: the group's largest exponent; 9..15 zero
-            uint8_t mx = 0;
-            for (int j = 0; j < BPG; j++) mx = ds[j] > mx ? ds[j] : mx;
-            ds[8] = mx;
+        bool bad = false;   // the matrix cores' folding would not be exact for this row's group
+        if constexpr (DT == MXFP4) {   // byte 8: the reference exponent (largest of the counted blocks); 9..15 zero
+            uint8_t er = 0;
+            for (int j = 0; j < BPG; j++) {
+                if (!nz[j] && ds[j] != 255) ds[j] = 0;
+                er = ds[j] > er ? ds[j] : er;
+                bad |= ds[j] == 255;
+            }
+            for (int j = 0; j < BPG; j++) bad |= nz[j] && (int) ds[j] + 14 < (int) er;
+            ds[8] = er;
             for (int t = 9; t < 16; t++) ds[t] = 0;
+        } else {
+            uint32_t hs[BPG];
+            int F = 0;   // largest fp16 exponent field of the group
+            for (int j = 0; j < BPG; j++) {
+                hs[j] = (uint32_t) ds[2 * j] | ((uint32_t) ds[2 * j + 1] << 8);
+                if (DT == Q8_0 && !nz[j] && (hs[j] & 0x7C00u) != 0x7C00u) {
+                    ds[2 * j] = ds[2 * j + 1] = 0;
+                    hs[j] = 0;
+                }
+                const int f = (int) ((hs[j] >> 10) & 31);
+                F = f > F ? f : F;
+            }
+            if (F == 31) {
+                bad = true;
+            } else {
+                const float lim = ldexpf(1.0f, F - (DT == Q8_0 ? 36 : 39));
+                for (int j = 0; j < BPG; j++) {
+                    const float v = h2f(hs[j] & 0x7FFFu);
+                    bad |= v != 0.0f && v < lim;
+                }
+            }
         }
+        if (bad && flag != nullptr) atomicOr(flag, 1);
     }
 }
+
+__global__ void flag_clear_kernel(int* flag) { *flag = 0; }
 
 // ------------------------------------------------------------------------- matrix-core GEMM activations
 // Position of element j of an 8-element run inside an A-operand fragment (its own inverse): the weight
@@ -526,24 +573,25 @@ __global__ void __launch_bounds__(256) repack_dense_kernel(const uint8_t* __rest
 }
 
 hipError_t launch_repack(int dt, const uint8_t* raw, int64_t raw_stride, int64_t rows, int64_t rb, int64_t G,
-                         uint8_t* qs, uint8_t* sc, hipStream_t st) {
+                         uint8_t* qs, uint8_t* sc, hipStream_t st, int* flag) {
     if (is_dense(dt)) {   // G: the pitch; rb: elements per row
         const int64_t n = rows * (G / 16);
         repack_dense_kernel<<<(unsigned) ((n + 255) / 256), 256, 0, st>>>(raw, raw_stride, rows, rb * block_bytes(dt), G,
                                                                           qs);
         return hipGetLastError();
     }
+    if (flag != nullptr && (dt == Q8_0 || dt == Q4_0 || dt == MXFP4)) flag_clear_kernel<<<1, 1, 0, st>>>(flag);
     const int64_t n = tiled_rows(rows) * G;
     const dim3 grid((unsigned) ((n + 255) / 256));
     switch (dt) {
-    case Q5_K: repack_kernel<Q5_K><<<grid, 256, 0, st>>>(raw, raw_stride, rows, rb, G, qs, sc); break;
-    case NVFP4: repack_kernel<NVFP4><<<grid, 256, 0, st>>>(raw, raw_stride, rows, rb, G, qs, sc); break;
-    case Q1_0: repack_kernel<Q1_0><<<grid, 256, 0, st>>>(raw, raw_stride, rows, rb, G, qs, sc); break;
-    case Q8_0: repack_kernel<Q8_0><<<grid, 256, 0, st>>>(raw, raw_stride, rows, rb, G, qs, sc); break;
-    case Q4_0: repack_kernel<Q4_0><<<grid, 256, 0, st>>>(raw, raw_stride, rows, rb, G, qs, sc); break;
-    case MXFP4: repack_kernel<MXFP4><<<grid, 256, 0, st>>>(raw, raw_stride, rows, rb, G, qs, sc); break;
-    case Q6_K: repack_kernel<Q6_K><<<grid, 256, 0, st>>>(raw, raw_stride, rows, rb, G, qs, sc); break;
-    case Q4_K: repack_kernel<Q4_K><<<grid, 256, 0, st>>>(raw, raw_stride, rows, rb, G, qs, sc); break;
+    case Q5_K: repack_kernel<Q5_K><<<grid, 256, 0, st>>>(raw, raw_stride, rows, rb, G, qs, sc, nullptr); break;
+    case NVFP4: repack_kernel<NVFP4><<<grid, 256, 0, st>>>(raw, raw_stride, rows, rb, G, qs, sc, nullptr); break;
+    case Q1_0: repack_kernel<Q1_0><<<grid, 256, 0, st>>>(raw, raw_stride, rows, rb, G, qs, sc, nullptr); break;
+    case Q8_0: repack_kernel<Q8_0><<<grid, 256, 0, st>>>(raw, raw_stride, rows, rb, G, qs, sc, flag); break;
+    case Q4_0: repack_kernel<Q4_0><<<grid, 256, 0, st>>>(raw, raw_stride, rows, rb, G, qs, sc, flag); break;
+    case MXFP4: repack_kernel<MXFP4><<<grid, 256, 0, st>>>(raw, raw_stride, rows, rb, G, qs, sc, flag); break;
+    case Q6_K: repack_kernel<Q6_K><<<grid, 256, 0, st>>>(raw, raw_stride, rows, rb, G, qs, sc, nullptr); break;
+    case Q4_K: repack_kernel<Q4_K><<<grid, 256, 0, st>>>(raw, raw_stride, rows, rb, G, qs, sc, nullptr); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

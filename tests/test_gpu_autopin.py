@@ -149,3 +149,88 @@ def test_autopin_limits(ctxs, oracle):
     assert auto.autopin_stats()["pins"] == 1 and auto.pinned_bytes() > 0
     assert auto.evict(Segment.of(w)) == 0
     assert auto.pinned_bytes() == 0
+
+
+def test_device_entry_points_never_serve_an_autopin(ctxs, oracle):
+    """An autopin serves only jamhip_mm calls that pass its spot check. jamhip_mm_device (whose launches a
+    caller may capture in a graph) stages W instead: after an in-place rewrite of an autopinned range it
+    returns the new bytes' result, and the noalloc entry point (which cannot stage) declines."""
+    import torch
+    from qxotic_amd.jam import JAM, Segment
+    auto, plain = ctxs
+    m, k, n = 64, 1024, 2
+    assert auto.set_autopin(1) == 0
+    w = oracle.quantize(O.Q4_K, oracle.normal(41, (m, k), 0.0, 0.02))
+    other = oracle.quantize(O.Q4_K, oracle.normal(42, (m, k), 0.0, 0.02))
+    a = oracle.normal(43, (n, k))
+    mm(auto, O.Q4_K, w, a, m, n, k)
+    assert auto.autopin_stats()["pins"] == 1
+    w[...] = other
+    a_d = torch.from_numpy(a).cuda()
+    c_d = torch.zeros((n, m), dtype=torch.float32, device="cuda")
+    assert auto.mm_device(Segment.of(w), O.Q4_K, k, a_d.data_ptr(), k, c_d.data_ptr(), m, m, n, k) == JAM.OK
+    auto.synchronize()
+    assert np.array_equal(bits(c_d.cpu().numpy()), bits(mm(plain, O.Q4_K, other, a, m, n, k)))
+    assert auto.mm_device_noalloc(Segment.of(w), O.Q4_K, k, a_d.data_ptr(), k, c_d.data_ptr(), m, m, n,
+                                  k) == JAM.EUNSUPPORTED
+    assert auto.autopin_stats()["invalidated"] == 0   # the device entry points never looked at the autopin
+
+
+def test_offset_call_into_an_autopin_is_staged(ctxs, oracle):
+    """A jamhip_mm call at a row offset inside an autopinned range is not served from the autopin (no spot
+    check covers it): after an in-place rewrite it returns the new bytes' result."""
+    auto, plain = ctxs
+    m, k, n = 64, 1024, 1
+    assert auto.set_autopin(1) == 0
+    w = oracle.quantize(O.Q4_K, oracle.normal(51, (2 * m, k), 0.0, 0.02))
+    other = oracle.quantize(O.Q4_K, oracle.normal(52, (2 * m, k), 0.0, 0.02))
+    a = oracle.normal(53, (n, k))
+    mm(auto, O.Q4_K, w, a, 2 * m, n, k)
+    assert auto.autopin_stats()["pins"] == 1
+    w[...] = other
+    from qxotic_amd.jam import JAM, Segment
+    c = np.zeros((n, m), np.float32)
+    st = auto.mm(Segment.of(w), m * O.row_bytes(O.Q4_K, k), O.Q4_K, k, Segment.of(a), 0, JAM.F32, k, Segment.of(c),
+                 0, JAM.F32, m, m, n, k)
+    assert st == JAM.OK, auto.last_error()
+    want = mm(plain, O.Q4_K, np.ascontiguousarray(other[m:]), a, m, n, k)
+    assert np.array_equal(bits(c), bits(want))
+
+
+def test_explicit_pin_takes_over_an_autopin(ctxs, oracle):
+    """jamhip_weight_pin on an autopinned range (the same extent, or one overlapping it) succeeds: the autopin
+    is dropped and the range copied afresh, so the pin holds the bytes at pin time even if the autopin's copy
+    predates them. The pin then serves device calls, and stays after further rewrites (an explicit pin is the
+    caller's promise)."""
+    import torch
+    from qxotic_amd.jam import JAM, Segment
+    auto, plain = ctxs
+    m, k, n = 64, 1024, 1
+    assert auto.set_autopin(1) == 0
+    w = oracle.quantize(O.Q4_K, oracle.normal(61, (2 * m, k), 0.0, 0.02))
+    snap = oracle.quantize(O.Q4_K, oracle.normal(62, (2 * m, k), 0.0, 0.02))
+    a = oracle.normal(63, (n, k))
+    mm(auto, O.Q4_K, w, a, m, n, k)            # autopin of rows [0, m)
+    assert auto.autopin_stats()["pins"] == 1
+    w[...] = snap                              # rewritten in place, not yet spot-checked
+    assert auto.pin(Segment.of(w), O.Q4_K, k, 2 * m) == JAM.OK, auto.last_error()   # overlaps the autopin
+    a_d = torch.from_numpy(a).cuda()
+    c_d = torch.zeros((n, 2 * m), dtype=torch.float32, device="cuda")
+    w[...] = 0                                 # the pin keeps the bytes it copied
+    assert auto.mm_device(Segment.of(w), O.Q4_K, k, a_d.data_ptr(), k, c_d.data_ptr(), 2 * m, 2 * m, n,
+                          k) == JAM.OK
+    auto.synchronize()
+    assert np.array_equal(bits(c_d.cpu().numpy()), bits(mm(plain, O.Q4_K, snap, a, 2 * m, n, k)))
+    assert auto.evict(Segment.of(w)) == JAM.OK
+    assert auto.pinned_bytes() == 0
+    # the same extent as the autopin
+    w[...] = snap
+    mm(auto, O.Q4_K, w, a, 2 * m, n, k)
+    assert auto.autopin_stats()["pins"] == 2
+    assert auto.pin(Segment.of(w), O.Q4_K, k, 2 * m) == JAM.OK, auto.last_error()
+    w[...] = 0
+    assert auto.mm_device(Segment.of(w), O.Q4_K, k, a_d.data_ptr(), k, c_d.data_ptr(), 2 * m, 2 * m, n,
+                          k) == JAM.OK
+    auto.synchronize()
+    assert np.array_equal(bits(c_d.cpu().numpy()), bits(mm(plain, O.Q4_K, snap, a, 2 * m, n, k)))
+    assert auto.evict(Segment.of(w)) == JAM.OK

@@ -290,3 +290,45 @@ def test_grouped_status_codes(hip):
     assert call(ldc=16) == JAM.EINVAL               # ldc < m
     assert call(cap=-1) == JAM.EINVAL
     assert call(dt=JAM.F16) == JAM.EUNSUPPORTED
+
+
+@pytest.mark.parametrize("dt", [O.MXFP4, O.Q4_K])
+def test_mm_grouped_decode_unfused(hip, oracle, dt):
+    """The grouped F1 decode kernels reading the quantized copy instead of quantizing in their prologue: k past
+    the fused prologue's reach (k = 5120, 14336) and rows not 16-byte aligned (lda = k + 1), with one-row and
+    2..7-row experts (the one-token and seven-token launches). Tier 1 on every expert, the ldc gap and the rows
+    past the counts untouched."""
+    import torch
+    from qxotic_amd.jam import JAM, Segment
+    m = 32
+    for k, lda in ((5120, 5120), (14336, 14336), (2816, 2817)):
+        counts, rows_cap = [1, 0, 3, 1, 0, 2], 7
+        E = len(counts)
+        say(f"grouped unfused {O.NAMES[dt]} k={k} lda={lda} counts={counts}")
+        w_e = [oracle.quantize(dt, oracle.normal(0xF1D0 + 13 * e + dt + k, (m, k), 0.0, 0.02)) for e in range(E)]
+        w = np.ascontiguousarray(np.concatenate(w_e, axis=0))
+        a = oracle.outliers(0xF1D1 + k, (rows_cap, k))
+        a_pad = np.zeros((rows_cap, lda), np.float32)
+        a_pad[:, :k] = a
+        assert hip.pin(Segment.of(w), dt, k, E * m) == JAM.OK, hip.last_error()
+        try:
+            c = torch.full((rows_cap + 1, m + 2), -3.0, dtype=torch.float32, device="cuda")
+            a_dv = dev(a_pad)
+            counts_dv = dev(np.array(counts, np.int32))
+            torch.cuda.synchronize()
+            assert hip.mm_grouped(Segment.of(w), dt, k, m, E, counts_dv.data_ptr(), a_dv.data_ptr(), lda,
+                                  c.data_ptr(), m + 2, k, rows_cap, None) == JAM.OK, hip.last_error()
+            hip.synchronize()
+            got = c.cpu().numpy()
+            ref = M.mm_grouped(oracle, dt, w_e, a, counts, m, k)
+            o = 0
+            for e, n in enumerate(counts):
+                if n:
+                    _, sa = oracle.mm_ref(dt, w_e[e], np.ascontiguousarray(a[o:o + n]), m, n, k)
+                    r = ref[o:o + n]
+                    assert (np.abs(got[o:o + n, :m] - r) <= 1e-3 * np.abs(r) + 1e-5 * sa).all(), (k, e, n)
+                o += n
+            assert (got[:, m:] == -3.0).all()
+            assert (got[sum(counts):] == -3.0).all()
+        finally:
+            hip.evict(Segment.of(w))

@@ -419,3 +419,51 @@ def test_prefill_error_floor(hip, oracle, dt):
     rel = np.abs(got - ref) / sa
     worst = np.unravel_index(int(np.argmax(rel)), rel.shape)
     assert rel.max() <= 2e-6, (O.NAMES[dt], float(rel.max()), worst)
+
+
+@pytest.mark.parametrize("dt", O.ALL_QUANT_TYPES)
+def test_pinned_column_slice(hip, oracle, dt, monkeypatch):
+    """A pinned tensor read with ldw > k (the first k elements of each ldw-element row, jam.c:551): the device
+    copy holds whole rows, the kernels read its first k / 256 groups. Decode (F1, in-kernel and from the
+    quantized copy), the F2 decode kernel, the matrix cores and the grouped matmul give the staged call's bits
+    (staging copies only the k columns), and tier 1 against the oracle."""
+    import torch
+    from qxotic_amd.jam import JAM, Segment
+    be = O.BLOCK[dt][0]
+    m, k = 64, 768 if be < 256 else 512
+    ldw = k + 256
+    w = oracle.quantize(dt, oracle.normal(0x51CE ^ dt, (m, ldw), 0.0, 0.02))
+    assert hip.pin(Segment.of(w), dt, ldw, m) == JAM.OK, hip.last_error()
+    try:
+        for n, force in ((1, None), (3, None), (12, "100000"), (40, "8")):
+            monkeypatch.delenv("JAM_HIP_MMA_MIN_N", raising=False)
+            if force:
+                monkeypatch.setenv("JAM_HIP_MMA_MIN_N", force)
+            say(f"pinned column slice {O.NAMES[dt]} m={m} k={k} ldw={ldw} n={n}")
+            a = oracle.outliers(0x51CF + n, (n, k))
+            got = run_mm(hip, dt, w, a, m, n, k, ldw=ldw)
+            ref = oracle.mm_int8(dt, w, a, m, n, k, ldw=ldw)
+            _, sa = oracle.mm_ref(dt, w, a, m, n, k, ldw=ldw)
+            assert tier1(got, ref, sa).all(), (O.NAMES[dt], n)
+            staged = run_mm(hip, dt, np.ascontiguousarray(w[:, :O.row_bytes(dt, k)]), a, m, n, k)
+            assert np.array_equal(bits(got), bits(staged)), (O.NAMES[dt], n)
+        monkeypatch.delenv("JAM_HIP_MMA_MIN_N", raising=False)
+        if dt in O.QUANT_TYPES:   # grouped: two experts of 32 rows of the pinned tensor, ldw > k
+            counts = [20, 2]
+            a = oracle.outliers(0x51D0, (22, k))
+            a_d = torch.from_numpy(a).cuda()
+            c = torch.zeros((22, 32), dtype=torch.float32, device="cuda")
+            cnt = torch.from_numpy(np.array(counts, np.int32)).cuda()
+            say(f"pinned column slice grouped {O.NAMES[dt]}")
+            assert hip.mm_grouped(Segment.of(w), dt, ldw, 32, 2, cnt.data_ptr(), a_d.data_ptr(), k, c.data_ptr(), 32,
+                                  k, 22, None) == JAM.OK, hip.last_error()
+            hip.synchronize()
+            got = c.cpu().numpy()
+            for e, (o, nr) in enumerate(((0, 20), (20, 2))):
+                we = np.ascontiguousarray(w[32 * e:32 * e + 32])
+                ae = np.ascontiguousarray(a[o:o + nr])
+                ref = oracle.mm_int8(dt, we, ae, 32, nr, k, ldw=ldw)
+                _, sa = oracle.mm_ref(dt, we, ae, 32, nr, k, ldw=ldw)
+                assert tier1(got[o:o + nr], ref, sa).all(), (O.NAMES[dt], e)
+    finally:
+        assert hip.evict(Segment.of(w)) == JAM.OK
