@@ -203,6 +203,63 @@ def read_floor_leg(args, hip, torch, stream) -> dict:
                     "no output"}
 
 
+def shapes_leg(hip, torch, stream, steps: int = 512) -> dict:
+    """The other BASELINE decode shapes, in the headline's harness: config 1 (Q8_0 4096x4096, M = 1), config 2
+    (Q4_0 14336x4096 and 4096x14336, M in {1, 4, 8}) and config 3's down projection (Q6_K 4096x14336, M = 1).
+    Each shape rotates over enough pinned copies to pass 1 GB (beyond the 256 MB Infinity Cache) inside one
+    captured graph of `steps` launches on the library's stream, timed with HIP events; GB/s counts each
+    operand once (jam_bench.c:46-75)."""
+    from qxotic_amd.jam import JAM, Segment
+
+    out = {}
+    for label, name, dt, m, k, ns in (("config1", "Q8_0", JAM.Q8_0, 4096, 4096, (1,)),
+                                      ("config2", "Q4_0", JAM.Q4_0, 14336, 4096, (1, 4, 8)),
+                                      ("config2", "Q4_0", JAM.Q4_0, 4096, 14336, (1, 4, 8)),
+                                      ("config3 down", "Q6_K", JAM.Q6_K, 4096, 14336, (1,))):
+        w = quantized(name, m, k, 0x5A11C0DE ^ dt ^ m)
+        ncp = max(32, -(-1_070_000_000 // w.nbytes))
+        copies = [w.copy() for _ in range(ncp)]
+        for cp in copies:
+            assert hip.pin(Segment.of(cp), dt, k, m) == JAM.OK, hip.last_error()
+        for n in ns:
+            a = torch.randn((n, k), dtype=torch.float32, device="cuda")
+            c = torch.empty((ncp, n, m), dtype=torch.float32, device="cuda")
+
+            def step(i):
+                if hip.mm_device(Segment.of(copies[i % ncp]), dt, k, a.data_ptr(), k, c[i % ncp].data_ptr(), m, m, n,
+                                 k) != JAM.OK:
+                    raise RuntimeError(hip.last_error())
+
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            with torch.cuda.stream(stream):
+                for i in range(ncp):
+                    step(i)
+                torch.cuda.synchronize()
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph, stream=stream):
+                    for i in range(steps):
+                        step(i)
+                graph.replay()
+                torch.cuda.synchronize()
+                e0.record(stream)
+                graph.replay()
+                e1.record(stream)
+                torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / steps
+            nbytes = w.nbytes + n * k * 4 + n * m * 4
+            gbs = nbytes / (us * 1e-6) / 1e9
+            out[f"{label} {name} {m}x{k} M={n}"] = {"us": round(us, 3), "GBs": round(gbs, 1),
+                                                    "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "bytes": nbytes,
+                                                    "copies": ncp}
+            del graph, a, c
+        for cp in copies:
+            hip.evict(Segment.of(cp))
+        del copies
+    out["note"] = ("graph-timed like the headline: one captured graph of %d launches over >= 1.07 GB of rotating "
+                   "pinned copies; bytes = W + A + C once" % steps)
+    return out
+
+
 def prefill_leg(hip, torch, stream, reps: int = 10) -> dict:
     """M=512 prefill on the two BASELINE prefill shapes; each timed call quantizes its activations (F2)."""
     from qxotic_amd.jam import JAM, Segment
@@ -231,13 +288,22 @@ def prefill_leg(hip, torch, stream, reps: int = 10) -> dict:
         us = e0.elapsed_time(e1) * 1e3 / reps
         tops = 2.0 * m * n * k / (us * 1e-6) / 1e12
         assert bool(torch.isfinite(c).all()), "prefill output not finite"
+        # the host-pointer entry point on the same call (jamhip_mm: 8 / 28 MiB of A up, C down, synchronized)
+        c_h = np.empty((n, m), np.float32)
+        hip.mm_contiguous(Segment.of(w), Segment.of(x), Segment.of(c_h), dt, m, n, k)
+        t0 = time.perf_counter()
+        for _ in range(5):
+            assert hip.mm_contiguous(Segment.of(w), Segment.of(x), Segment.of(c_h), dt, m, n, k) == JAM.OK
+        host_us = (time.perf_counter() - t0) / 5 * 1e6
         out[f"{name} {m}x{k} M=512"] = {"us": round(us, 2), "TOPS": round(tops, 2),
                                         "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
-                                        "frac_f16_peak": round(tops / F16_PEAK_TFLOPS, 4)}
+                                        "frac_f16_peak": round(tops / F16_PEAK_TFLOPS, 4),
+                                        "host_pointer_us": round(host_us, 1)}
         hip.evict(Segment.of(w))
         del a, c
     out["note"] = ("jam's F2 quantization + int8 products computed exactly on f16 MFMA (integer operands "
-                   "<= 2048); peaks are MI355X dense int8 5.0 POP/s and f16 2.5 PFLOP/s")
+                   "<= 2048); peaks are MI355X dense int8 5.0 POP/s and f16 2.5 PFLOP/s; host_pointer_us = the "
+                   "same call through jamhip_mm with host A and C (PCIe both ways, synchronized), wall clock")
     return out
 
 
@@ -366,6 +432,38 @@ def moe_leg(hip, torch, stream, steps: int = 10) -> dict:
               "note": "1 token top-4 (a random expert set per layer), route + gather + two grouped calls + combine "
                       "in stream order, median of 3 runs of 200 layers; weights = 4 experts' gate_up + down "
                       "(52.9 MB)"}
+    # the same layer the way an unedited jinfer runs it through the host-pointer entry point: Moe.dispatch's host
+    # loop (Moe.java:178-232) gathering each expert's rows, one jamhip_mm per expert and matrix on a row view of
+    # the pinned stacked tensors (GptOss.java:677-717), the probability-weighted scatter on the host
+    rb = (D // 32) * 17
+    re_h, x_h, hid_h, prob_h = sel.ravel(), x.cpu().numpy(), hid.cpu().numpy(), prob.cpu().numpy()
+    by_e = np.argsort(re_h, kind="stable")
+    off_h = np.concatenate([[0], np.cumsum(counts_h)])
+    hb = [np.empty((int(c_), FF), np.float32) for c_ in counts_h]
+    yb = [np.empty((int(c_), D), np.float32) for c_ in counts_h]
+
+    def host_layer():
+        acc = np.zeros((SEQ, D), np.float32)
+        for e in range(E):
+            r = by_e[off_h[e]:off_h[e + 1]]
+            ne = len(r)
+            if ne == 0:
+                continue
+            xe, he = np.ascontiguousarray(x_h[r // TOPK]), np.ascontiguousarray(hid_h[r])
+            ok = hip.mm(Segment.of(wg[0]), e * FF * rb, JAM.MXFP4, D, Segment.of(xe), 0, JAM.F32, D, Segment.of(hb[e]),
+                        0, JAM.F32, FF, FF, ne, D) == JAM.OK
+            ok &= hip.mm(Segment.of(wd[0]), e * D * rb, JAM.MXFP4, D, Segment.of(he), 0, JAM.F32, D, Segment.of(yb[e]),
+                         0, JAM.F32, D, D, ne, D) == JAM.OK
+            if not ok:
+                raise RuntimeError(hip.last_error())
+            acc[r // TOPK] += prob_h[r, None] * yb[e]
+        return acc
+
+    host_layer()
+    t0 = time.perf_counter()
+    for _ in range(3):
+        host_layer()
+    host_us = (time.perf_counter() - t0) / 3 * 1e6
     for xx in wg + wd:
         hip.evict(Segment.of(xx))
     wbytes = E * (FF + D) * (D // 32) * 17
@@ -375,6 +473,10 @@ def moe_leg(hip, torch, stream, steps: int = 10) -> dict:
             "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
             "frac_fp4_peak": round(tops / 10070.0, 4), "routed_rows": R,
             "counts": counts_h.tolist(), "mx_native": native, "decode": decode,
+            "host_pointer_layer_us": round(host_us, 1),
+            "host_pointer_note": "the layer as 64 jamhip_mm calls with host A and C (one per expert and matrix, on row "
+                                 "views of the pinned stacked experts) plus the host-side gather and weighted scatter, "
+                                 "wall clock, mean of 3",
             "note": "32 experts x (5760x2880 + 2880x2880) MXFP4 (423 MB, 2 rotating copies; experts cycle through "
                     "2 distinct N(0,0.02) quantizations), 512 tokens top-4 Zipf(1.1); ops = 2*routed_rows*"
                     "(5760*2880 + 2880*2880)"}
@@ -444,13 +546,29 @@ def decode_step_leg(hip, torch, stream, w_gate: np.ndarray, reps: int = 8) -> di
         gbs = (wbytes + io) / (us * 1e-6) / 1e9
         out[name] = {"us_per_token": round(us, 1), "tokens_per_s": round(1e6 / us, 1), "launches": len(plan),
                      "GBs": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+        if name == "separate":   # the same 225 calls through jamhip_mm with host A and C, as an unedited jinfer
+            a_h, h_h = x_d.cpu().numpy(), h_d.cpu().numpy()
+            outs_h = {m: np.empty((1, m), np.float32) for m in outs}
+
+            def host_step():
+                for w, dt, m, k in plan:
+                    if hip.mm_contiguous(Segment.of(w), Segment.of(h_h if k == FF else a_h), Segment.of(outs_h[m]), dt,
+                                         m, 1, k) != JAM.OK:
+                        raise RuntimeError(hip.last_error())
+
+            host_step()
+            t0 = time.perf_counter()
+            for _ in range(3):
+                host_step()
+            out[name]["host_pointer_us_per_token"] = round((time.perf_counter() - t0) / 3 * 1e6, 1)
         for w, _, _, _ in plan:
             if w is not head or name == "fused":
                 hip.evict(Segment.of(w))
         del g
     out["weights_GB"] = round(wbytes / 1e9, 3)
     out["note"] = ("config 3: 32 Llama-3-8B layers (q/k/v/o/gate/up Q4_K, down Q6_K) + Q6_K output head, n = 1, "
-                   "matmuls only, one captured graph per schedule; GB/s = weights + activations + outputs")
+                   "matmuls only, one captured graph per schedule; GB/s = weights + activations + outputs; "
+                   "host_pointer_us_per_token = the 225 calls through jamhip_mm with host A and C, wall clock")
     return out
 
 
@@ -674,6 +792,7 @@ def main() -> int:
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true")
     ap.add_argument("--no-read-floor", action="store_true")
+    ap.add_argument("--no-shapes", action="store_true")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -700,6 +819,10 @@ def main() -> int:
         log("bench: read floor leg")
         floor = read_floor_leg(args, hip, torch, stream)
         floor["decode_frac"] = round(floor["us"] / (ms * 1e3), 4)
+    shapes = None
+    if not args.no_shapes:
+        log("bench: decode shapes leg (configs 1, 2 and the Q6_K down projection)")
+        shapes = shapes_leg(hip, torch, stream)
     pre = None
     if not args.no_prefill:
         log("bench: prefill leg")
@@ -745,12 +868,14 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles()},
         "read_floor": floor,
+        "decode_shapes": shapes,
         "prefill": pre,
         "moe": moe,
         "decode_step": step,
         "epilogue": epi,
         "registry": reg,
         "cpu_baseline": cpu,
+        "jam_vector": "not run: no JDK 25 (jdk.incubator.vector) on the GPU box or in the build image",
         "cpu_baseline_gemm": cpu_gemm,
     }
     print(json.dumps(out), flush=True)

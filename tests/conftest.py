@@ -1,3 +1,5 @@
+import json
+import os
 import subprocess
 import sys
 from pathlib import Path
@@ -111,4 +113,9 @@ def parity_report(label: str, got: np.ndarray, ref: np.ndarray, sa: np.ndarray) 
     per_sa = float((err / np.maximum(sa, 1e-30)).max())
     print(f"parity {label}: max_rel {rel:.3e}  max_err/sumAbs {per_sa:.3e}  outputs {got.size}", file=sys.stderr,
           flush=True)
-    return {"max_rel": rel, "max_err_per_sumabs": per_sa}
+    out = {"max_rel": rel, "max_err_per_sumabs": per_sa}
+    log = os.environ.get("JAM_PARITY_LOG")   # a JSON line per case, for the committed per-config summary
+    if log:
+        with open(log, "a") as f:
+            f.write(json.dumps({"case": label, "outputs": int(got.size), **out}) + "\n")
+    return out

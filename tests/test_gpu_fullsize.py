@@ -12,6 +12,8 @@
 Bound: tier 1, |gpu - oracle| <= 1e-3*|oracle| + 1e-5*sum|w*a| (same int8 semantics, f32 order differs). Each
 case prints its largest relative error (parity_report).
 """
+import json
+import os
 import sys
 
 import numpy as np
@@ -202,6 +204,11 @@ def test_config5_gptoss_moe_layer(hip, oracle):
             worst["max_err_per_sumabs"] = max(worst["max_err_per_sumabs"], float((err / sa).max()))
         say(f"parity config5 {name} (32 experts, 96 sampled rows each): max_rel {worst['max_rel']:.3e}  "
             f"max_err/sumAbs {worst['max_err_per_sumabs']:.3e}")
+        log = os.environ.get("JAM_PARITY_LOG")
+        if log:
+            with open(log, "a") as f:
+                f.write(json.dumps({"case": f"config5 MoE grouped {name} MXFP4 (32 experts, 96 sampled rows each)",
+                                    "outputs": int(R * 96), **worst}) + "\n")
 
 
 # ---------------------------------------------------------------------------------- fallback GEMM

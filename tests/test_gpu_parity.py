@@ -10,7 +10,7 @@ import sys
 import numpy as np
 import pytest
 
-from conftest import adversarial_activations
+from conftest import adversarial_activations, parity_report
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -223,6 +223,8 @@ def test_full_size_decode(hip, oracle, dt, m, k, n):
     got = run_mm(hip, dt, w, a, m, n, k)
     ref = oracle.mm_int8(dt, w, a, m, n, k)
     _, sa = oracle.mm_ref(dt, w, a, m, n, k)
+    cfg = {(O.Q8_0, 4096, 4096): "config1 ", (O.Q4_K, 14336, 4096): "config3 ", (O.Q6_K, 4096, 14336): "config3 "}
+    parity_report(f"{cfg.get((dt, m, k), '')}{O.NAMES[dt]} {m}x{k} M={n}", got, ref, sa)
     assert tier1(got, ref, sa).all()
 
 
@@ -358,6 +360,7 @@ def test_prefill_full_size(hip, oracle, dt, m, k):
     ws = np.ascontiguousarray(w[rows])
     ref = oracle.mm_int8(dt, ws, a, len(rows), n, k)
     _, sa = oracle.mm_ref(dt, ws, a, len(rows), n, k)
+    parity_report(f"config4 {O.NAMES[dt]} {m}x{k} M={n} (192 sampled rows)", got[:, rows], ref, sa)
     ok = tier1(got[:, rows], ref, sa)
     assert ok.all(), (int((~ok).sum()), float(np.max(np.abs(got[:, rows] - ref) / (np.abs(ref) + 1e-30))))
 
