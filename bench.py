@@ -310,9 +310,10 @@ def prefill_leg(hip, torch, stream, reps: int = 10) -> dict:
 def moe_leg(hip, torch, stream, steps: int = 10) -> dict:
     """Config 5: a gpt-oss-20B-shaped MoE layer on the device: 32 experts with an MXFP4 gate_up 5760x2880
     and down 2880x2880, 512 tokens routed top-4 by Zipf(1.1) popularity (Gumbel-top-k on log p_e,
-    p_e ~ e^-1.1). One step = jamhip_moe_route + _gather + grouped gate_up + grouped down + _combine
+    p_e ~ e^-1.1). One step = jamhip_moe_select_topk + _route + _gather + grouped gate_up + grouped down + _combine
     (the down projection reads a synthetic 2880-wide hidden of the routed rows; the activation between
-    the two matmuls is not part of jam's path)."""
+    the two matmuls is not part of jam's path). The layer starts from the router's logits on the device:
+    jamhip_moe_select_topk (Moe.selectTopK + gpt-oss's softmax over the selected logits) gives the routes."""
     from qxotic_amd.jam import JAM, Segment
 
     E, TOPK, SEQ, D, FF = 32, 4, 512, 2880, 5760
@@ -328,10 +329,13 @@ def moe_leg(hip, torch, stream, steps: int = 10) -> dict:
         assert hip.pin(Segment.of(x), JAM.MXFP4, D, E * D) == JAM.OK, hip.last_error()
     rng = np.random.default_rng(0x5A11C0DE ^ 5)
     logp = -1.1 * np.log(np.arange(1, E + 1))
-    sel = np.argsort(-(logp[None, :] + rng.gumbel(size=(SEQ, E))), axis=1)[:, :TOPK].astype(np.int32)
+    logits_h = (logp[None, :] + rng.gumbel(size=(SEQ, E))).astype(np.float32)   # router logits: Zipf(1.1) top-4
+    sel = np.argsort(-logits_h, axis=1, kind="stable")[:, :TOPK].astype(np.int32)
     counts_h = np.bincount(sel.ravel(), minlength=E)
     R = SEQ * TOPK
     dev = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to("cuda")
+    logits0 = dev(logits_h)
+    logits = torch.empty_like(logits0)
     re = dev(sel.ravel())
     prob = dev(rng.random(R).astype(np.float32))
     x = dev(rng.standard_normal((SEQ, D)).astype(np.float32))
@@ -345,8 +349,11 @@ def moe_leg(hip, torch, stream, steps: int = 10) -> dict:
 
     def layer(i):
         cg, cd = wg[i % copies], wd[i % copies]
-        ok = hip.moe_route(re.data_ptr(), SEQ, TOPK, E, counts.data_ptr(), off.data_ptr(), slot_route.data_ptr(),
-                           route_slot.data_ptr()) == JAM.OK
+        logits.copy_(logits0)   # the router's output (selectTopK consumes it)
+        ok = hip.moe_select_topk(logits.data_ptr(), None, SEQ, E, E, TOPK, hip.TOPK_SOFTMAX, re.data_ptr(),
+                                 prob.data_ptr()) == JAM.OK
+        ok &= hip.moe_route(re.data_ptr(), SEQ, TOPK, E, counts.data_ptr(), off.data_ptr(), slot_route.data_ptr(),
+                            route_slot.data_ptr()) == JAM.OK
         ok &= hip.moe_gather(x.data_ptr(), D, slot_route.data_ptr(), off.data_ptr(), E, SEQ, TOPK, D, g.data_ptr(),
                              D) == JAM.OK
         ok &= hip.mm_grouped(Segment.of(cg), JAM.MXFP4, D, FF, E, counts.data_ptr(), g.data_ptr(), D, h.data_ptr(),
@@ -378,6 +385,7 @@ def moe_leg(hip, torch, stream, steps: int = 10) -> dict:
 
     us = timed()
     assert np.array_equal(counts.cpu().numpy(), counts_h), "device routing counts disagree with the host's"
+    assert np.array_equal(re.cpu().numpy(), sel.ravel()), "device top-k disagrees with the host's"
     assert bool(torch.isfinite(out).all()), "moe output not finite"
     ops = 2.0 * R * (FF * D + D * D)
     # the opt-in native-MX mode (not jam's activation semantics): the same layer with the experts' matrix-core

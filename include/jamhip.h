@@ -212,6 +212,30 @@ jamhip_status jamhip_moe_combine(jamhip_ctx* ctx, const void* y_dev, int ldy, co
                                  const void* route_prob_dev, const void* route_slot_dev, int seq, int topk,
                                  int n_experts, int dim, void* out_dev, int ldo);
 
+/* Router top-k on the device, replacing jinfer's host-side Moe.selectTopK (jinfer/jinfer-kernels/src/main/
+ * java/com/qxotic/jinfer/kernels/Moe.java:76-127) and the weight step that follows it:
+ *   for each row s, topk passes: best = the first expert with the row's largest selection score (strict >;
+ *   NaN never wins; a row with nothing above -Inf picks expert 0), route_expert[s*topk + k] = best,
+ *   p = weights[s][best] (the selection array itself when weights_dev is NULL, read before the mask),
+ *   selection[s][best] = -Inf (the selection array is consumed in place, as in jinfer);
+ *   counts_dev (int [n_experts], may be NULL) is zeroed, then counts[best]++ per route;
+ * then per row, by mode:
+ *   JAMHIP_TOPK_RAW        route_prob = p                                   (Moe.selectTopK)
+ *   JAMHIP_TOPK_SOFTMAX    softmax over the topk selected values, times weights_scale   (gpt-oss:
+ *                          GptOss.java:320-345; f32 order of the Java code, exp in double rounded to f32)
+ *   JAMHIP_TOPK_NORMALIZE  p / sum of the row's topk p                      (Moe.normalizeTopP, :146-152)
+ * and, with expert_scale_dev (f32 [n_experts]) non-NULL, route_prob *= expert_scale[best] (Moe.dispatch's
+ * expertScale fold, Moe.java:187-203). selection and weights are f32 [rows][ld], ld >= n_experts;
+ * 1 <= n_experts <= 1024, 1 <= topk <= 16. route_expert / route_prob feed jamhip_moe_route and
+ * jamhip_moe_combine directly. */
+#define JAMHIP_TOPK_RAW 0
+#define JAMHIP_TOPK_SOFTMAX 1
+#define JAMHIP_TOPK_NORMALIZE 2
+jamhip_status jamhip_moe_select_topk(jamhip_ctx* ctx, void* selection_dev, const void* weights_dev, int rows,
+                                     int n_experts, int ld, int topk, int mode, float weights_scale,
+                                     const void* expert_scale_dev, void* route_expert_dev, void* route_prob_dev,
+                                     void* counts_dev);
+
 /* ---- Fused epilogues (no counterpart in jam: jinfer runs these as separate passes after MatMul.gemm).
  * mm_device_ex: jamhip_mm_device with the epilogue applied in the matmul's own final store,
  *   C[j][i] = [C[j][i] +] (dot(W[i,:], A[j,:]) [+ bias[i]])

@@ -8,7 +8,13 @@ Follows ``jinfer/jinfer-kernels/src/main/java/com/qxotic/jinfer/kernels/Moe.java
 * ``combine``       -- Moe.java:208 and 223-231: ``out`` zero-filled, then the experts in ascending order
   add ``prob · y`` to their rows with ``Ops.saxpyInPlace``'s fused multiply-add (Ops.java:688-725);
 * ``mm_grouped``    -- the per-expert ``MatMul.gemm`` calls of the dispatch closure (GptOss.java:295-314),
-  each one jam matmul of the expert's rows, through the int8 oracle (jo_mm_int8, jam's own routing).
+  each one jam matmul of the expert's rows, through the int8 oracle (jo_mm_int8, jam's own routing);
+* ``select_topk``   -- ``Moe.selectTopK`` (Moe.java:76-127: k argmax passes per row, the first maximum winning
+  by strict ``>``, each winner masked to -Infinity in the selection array; combine weights from a second
+  array in the two-source form; counts re-zeroed then filled), followed by one of the weight steps callers
+  run on ``rowTopP``: gpt-oss's softmax over the k selected logits times ``expertWeightsScale``
+  (GptOss.java:320-345) or ``Moe.normalizeTopP`` (Moe.java:146-152), and ``Moe.dispatch``'s fold of a
+  per-expert ``expertScale`` into the combine weight (Moe.java:187-203).
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s cpu_baseline leg may import this module.
 """
@@ -74,3 +80,55 @@ def mm_grouped(oracle, dt: int, w_experts: list, a: np.ndarray, counts, m: int, 
             out[o:o + n] = oracle.mm_int8(dt, w_experts[e], np.ascontiguousarray(a[o:o + n]), m, n, k)
         o += n
     return out
+
+
+TOPK_RAW, TOPK_SOFTMAX, TOPK_NORMALIZE = 0, 1, 2
+
+
+def select_topk(selection: np.ndarray, topk: int, weights: np.ndarray | None = None, mode: int = TOPK_RAW,
+                weights_scale: float = 1.0, expert_scale: np.ndarray | None = None):
+    """(route_expert[rows*topk] int, route_prob[rows*topk] f32, counts[E] int, selection after masking).
+    ``selection`` [rows][E] f32 is copied, not changed; the returned copy carries the -Inf masks jinfer
+    leaves in its array."""
+    sel = np.array(selection, np.float32, copy=True)
+    w = sel if weights is None else np.asarray(weights, np.float32)
+    rows, E = sel.shape
+    re = np.zeros(rows * topk, np.int64)
+    rp = np.zeros(rows * topk, np.float32)
+    counts = np.zeros(E, np.int64)
+    for s in range(rows):
+        for ki in range(topk):
+            best, best_val = 0, np.float32(-np.inf)
+            for e in range(E):
+                v = sel[s, e]
+                if v > best_val:   # NaN compares false: never taken, as in Java
+                    best_val, best = v, e
+            re[s * topk + ki] = best
+            rp[s * topk + ki] = w[s, best]   # read before the mask (one-source form: the same array)
+            sel[s, best] = np.float32(-np.inf)
+            counts[best] += 1
+        base = s * topk
+        p = rp[base:base + topk]
+        if mode == TOPK_SOFTMAX:           # GptOss.selectExperts: softmax over the raw selected logits
+            mx = np.float32(-np.inf)
+            for v in p:
+                mx = np.float32(np.nan) if (np.isnan(mx) or np.isnan(v)) else max(mx, v)   # Math.max
+            total = np.float32(0.0)
+            vals = np.zeros(topk, np.float32)
+            for i in range(topk):
+                vals[i] = np.float32(np.exp(np.float64(np.float32(p[i] - mx))))      # (float) Math.exp(double)
+                total = np.float32(total + vals[i])
+            inv = np.float32(0.0) if total == 0 else np.float32(np.float32(1.0) / total)
+            for i in range(topk):
+                p[i] = np.float32(np.float32(vals[i] * inv) * np.float32(weights_scale))
+        elif mode == TOPK_NORMALIZE:       # Moe.normalizeTopP
+            total = np.float32(0.0)
+            for i in range(topk):
+                total = np.float32(total + p[i])
+            for i in range(topk):
+                p[i] = np.float32(p[i] / total)
+        if expert_scale is not None:       # Moe.dispatch: probByExpert = rowTopP * expertScale[e]
+            for i in range(topk):
+                p[i] = np.float32(p[i] * np.float32(expert_scale[re[base + i]]))
+        rp[base:base + topk] = p
+    return re, rp, counts, sel

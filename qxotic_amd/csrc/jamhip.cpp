@@ -1057,6 +1057,25 @@ jamhip_status moe_combine_impl(jamhip_ctx* ctx, const void* y_dev, int ldy, cons
     return e == hipSuccess ? JAMHIP_OK : hip_fail(ctx, e, "combine launch");
 }
 
+jamhip_status moe_topk_impl(jamhip_ctx* ctx, void* sel, const void* wts, int rows, int E, int ld, int topk, int mode,
+                            float wscale, const void* escale, void* route_expert, void* route_prob, void* counts) {
+    if (!ctx) return JAMHIP_EINVAL;
+    if (!sel || !route_expert || !route_prob) return fail(ctx, JAMHIP_EINVAL, "topk: null pointer");
+    if (rows <= 0 || E <= 0 || topk <= 0 || ld < E) return fail(ctx, JAMHIP_EINVAL, "topk: bad shape");
+    if (mode != JAMHIP_TOPK_RAW && mode != JAMHIP_TOPK_SOFTMAX && mode != JAMHIP_TOPK_NORMALIZE)
+        return fail(ctx, JAMHIP_EINVAL, "topk: mode must be JAMHIP_TOPK_RAW, _SOFTMAX or _NORMALIZE");
+    if (E > 1024) return fail(ctx, JAMHIP_EUNSUPPORTED, "topk: at most 1024 experts");
+    if (topk > MOE_TOPK_MAX) return fail(ctx, JAMHIP_EUNSUPPORTED, "topk: topk above 16");
+    if ((int64_t) rows * topk > INT32_MAX) return fail(ctx, JAMHIP_EUNSUPPORTED, "topk: too many routes");
+    Busy guard(ctx);
+    if (!guard.ok) return fail(ctx, JAMHIP_EBUSY, "context busy");
+    (void) hipSetDevice(ctx->device);
+    const hipError_t e = launch_moe_topk((float*) sel, (const float*) wts, rows, E, ld, topk, mode, wscale,
+                                         (const float*) escale, (int*) route_expert, (float*) route_prob, (int*) counts,
+                                         ctx->stream);
+    return e == hipSuccess ? JAMHIP_OK : hip_fail(ctx, e, "topk launch");
+}
+
 jamhip_status ctx_set_stream_impl(jamhip_ctx* ctx, void* stream) {
     if (!ctx) return JAMHIP_EINVAL;
     Busy guard(ctx);   // the stream is read by every call in flight on this context
@@ -1318,6 +1337,16 @@ jamhip_status jamhip_moe_combine(jamhip_ctx* ctx, const void* y_dev, int ldy, co
     return on_ctx(ctx, [&](jamhip_ctx* x) {
         return moe_combine_impl(x, y_dev, ldy, route_expert_dev, route_prob_dev, route_slot_dev, seq, topk, n_experts,
                                 dim, out_dev, ldo);
+    });
+}
+
+jamhip_status jamhip_moe_select_topk(jamhip_ctx* ctx, void* selection_dev, const void* weights_dev, int rows,
+                                     int n_experts, int ld, int topk, int mode, float weights_scale,
+                                     const void* expert_scale_dev, void* route_expert_dev, void* route_prob_dev,
+                                     void* counts_dev) {
+    return on_ctx(ctx, [&](jamhip_ctx* x) {
+        return moe_topk_impl(x, selection_dev, weights_dev, rows, n_experts, ld, topk, mode, weights_scale,
+                             expert_scale_dev, route_expert_dev, route_prob_dev, counts_dev);
     });
 }
 

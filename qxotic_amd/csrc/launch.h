@@ -197,6 +197,13 @@ hipError_t launch_moe_route(const int* route_expert, int R, int E, int* counts, 
                             int* route_slot, hipStream_t st, int* scratch = nullptr);
 hipError_t launch_moe_gather(const float* x, int ldx, const int* slot_route, const int* off, int E, int R, int topk,
                              int dim, float* g, int ldg, hipStream_t st);
+// Router top-k (Moe.selectTopK + the caller's weight step): sel [rows][ld] scores, consumed (winners masked to
+// -Inf); wts the combine weights (null: sel itself); mode MOE_TOPK_RAW / _SOFTMAX / _NORMALIZE; escale [E] per
+// expert (nullable); outputs route_expert / route_prob [rows][topk], counts [E] (nullable, zeroed then filled).
+constexpr int MOE_TOPK_MAX = 16;
+constexpr int MOE_TOPK_RAW = 0, MOE_TOPK_SOFTMAX = 1, MOE_TOPK_NORMALIZE = 2;
+hipError_t launch_moe_topk(float* sel, const float* wts, int rows, int E, int ld, int topk, int mode, float wscale,
+                           const float* escale, int* route_expert, float* route_prob, int* counts, hipStream_t st);
 hipError_t launch_moe_combine(const float* y, int ldy, const int* route_expert, const float* route_prob,
                               const int* route_slot, int seq, int topk, int E, int dim, float* out, int ldo,
                               hipStream_t st);

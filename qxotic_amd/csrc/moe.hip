@@ -1,7 +1,8 @@
 // Device side of jinfer's CSR-grouped MoE dispatch (jinfer/jinfer-kernels/.../Moe.java:178-232) and the
 // bookkeeping of the grouped matmul: per-expert counts -> CSR offsets (device prefix sum), the route ->
 // slot assignment in dispatch's order, the row gather, and the prob-weighted combine in dispatch's
-// expert order. Everything is deterministic: no atomics, every sum in a fixed order.
+// expert order; and Moe.selectTopK's router top-k. Everything is deterministic: every sum in a fixed order, the
+// only atomics integer counts.
 #include "common.h"
 #include "launch.h"
 
@@ -444,6 +445,132 @@ hipError_t launch_moe_gather(const float* x, int ldx, const int* slot_route, con
         moe_gather_kernel<true><<<R, 256, 0, st>>>(x, ldx, slot_route, off, E, topk, dim, g, ldg);
     else
         moe_gather_kernel<false><<<R, 256, 0, st>>>(x, ldx, slot_route, off, E, topk, dim, g, ldg);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------------------------------------ top-k
+// jinfer's Moe.selectTopK (Moe.java:76-127), one wave per router row, the row's scores in registers (EPL per
+// lane, expert e in lane e % 64, slot e / 64). Each of the k passes takes the lane's first strict maximum in
+// ascending expert order, then the wave's largest value with the lowest expert on ties: the first maximum, as
+// the Java loop's strict `>` keeps it; NaN never wins, and a row with nothing above -Inf picks expert 0 (the
+// loop's initial best). The winner's owner lane reads its combine weight (from the registers in the
+// one-source form, so a masked entry reads as -Inf exactly as in the Java array; from `wts` in the two-source
+// form) and masks the score to -Inf in registers and in `sel`, which the call consumes like jinfer does.
+// Lane 0 then runs the row's weight step sequentially in jinfer's f32 order: gpt-oss's softmax over the k
+// selected logits times expertWeightsScale (GptOss.java:320-345: Math.max with NaN propagation, the exp in
+// double rounded to f32, a sequential f32 sum, 1/sum or 0), or Moe.normalizeTopP (Moe.java:146-152), then
+// Moe.dispatch's expertScale fold (Moe.java:187-203), and writes the row's routes in (token, k) order. counts
+// (zeroed by the launcher) take one atomic add per route.
+template <int EPL>
+__global__ void __launch_bounds__(256) moe_topk_kernel(float* __restrict__ sel, const float* wts, int rows, int E,
+                                                       int ld, int topk, int mode, float wscale,
+                                                       const float* __restrict__ escale, int* __restrict__ route_expert,
+                                                       float* __restrict__ route_prob, int* __restrict__ counts) {
+    __shared__ float sp[4][MOE_TOPK_MAX];
+    __shared__ int se[4][MOE_TOPK_MAX];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int row = blockIdx.x * 4 + wv;
+    if (row >= rows) return;   // the whole wave
+    float* srow = sel + (int64_t) row * ld;
+    const bool one = wts == sel;
+    float v[EPL];
+#pragma unroll
+    for (int j = 0; j < EPL; j++) {
+        const int e = lane + 64 * j;
+        v[j] = e < E ? srow[e] : -INFINITY;
+    }
+    for (int ki = 0; ki < topk; ki++) {
+        float bv = -INFINITY;
+        int bi = INT_MAX;
+#pragma unroll
+        for (int j = 0; j < EPL; j++)
+            if (v[j] > bv) {
+                bv = v[j];
+                bi = lane + 64 * j;
+            }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) {
+            const float ov = __shfl_xor(bv, o);
+            const int oi = __shfl_xor(bi, o);
+            if (ov > bv || (ov == bv && oi < bi)) {
+                bv = ov;
+                bi = oi;
+            }
+        }
+        const int best = bi == INT_MAX ? 0 : bi;
+        float pw = 0.0f;
+        if (lane == (best & 63)) {
+#pragma unroll
+            for (int j = 0; j < EPL; j++)
+                if (j == (best >> 6)) {
+                    pw = one ? v[j] : wts[(int64_t) row * ld + best];
+                    v[j] = -INFINITY;
+                }
+            srow[best] = -INFINITY;
+            sp[wv][ki] = pw;
+            se[wv][ki] = best;
+            if (counts != nullptr) atomicAdd(&counts[best], 1);
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (lane != 0) return;
+    // loops unrolled over the maximum with a guard, so p stays in registers; each runs i = 0, 1, ... in order
+    float p[MOE_TOPK_MAX];
+#pragma unroll
+    for (int i = 0; i < MOE_TOPK_MAX; i++) p[i] = i < topk ? sp[wv][i] : 0.0f;
+    if (mode == MOE_TOPK_SOFTMAX) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < MOE_TOPK_MAX; i++)
+            if (i < topk) mx = (isnan(mx) || isnan(p[i])) ? __builtin_nanf("") : fmaxf(mx, p[i]);
+        float total = 0.0f;
+#pragma unroll
+        for (int i = 0; i < MOE_TOPK_MAX; i++)
+            if (i < topk) {
+                p[i] = (float) exp((double) __fsub_rn(p[i], mx));
+                total = __fadd_rn(total, p[i]);
+            }
+        const float inv = total == 0.0f ? 0.0f : __fdiv_rn(1.0f, total);
+#pragma unroll
+        for (int i = 0; i < MOE_TOPK_MAX; i++) p[i] = __fmul_rn(__fmul_rn(p[i], inv), wscale);
+    } else if (mode == MOE_TOPK_NORMALIZE) {
+        float total = 0.0f;
+#pragma unroll
+        for (int i = 0; i < MOE_TOPK_MAX; i++)
+            if (i < topk) total = __fadd_rn(total, p[i]);
+#pragma unroll
+        for (int i = 0; i < MOE_TOPK_MAX; i++) p[i] = __fdiv_rn(p[i], total);
+    }
+#pragma unroll
+    for (int i = 0; i < MOE_TOPK_MAX; i++)
+        if (i < topk) {
+            const int e = se[wv][i];
+            route_expert[(int64_t) row * topk + i] = e;
+            route_prob[(int64_t) row * topk + i] = escale != nullptr ? __fmul_rn(p[i], escale[e]) : p[i];
+        }
+}
+
+__global__ void moe_fill_int_kernel(int* __restrict__ p, int n, int v) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = v;
+}
+
+hipError_t launch_moe_topk(float* sel, const float* wts, int rows, int E, int ld, int topk, int mode, float wscale,
+                           const float* escale, int* route_expert, float* route_prob, int* counts, hipStream_t st) {
+    if (E < 1 || E > 1024 || topk < 1 || topk > MOE_TOPK_MAX || rows < 0 || ld < E) return hipErrorInvalidValue;
+    if (counts != nullptr) moe_fill_int_kernel<<<(E + 255) / 256, 256, 0, st>>>(counts, E, 0);
+    if (rows == 0) return hipGetLastError();
+    const dim3 grid((unsigned) ((rows + 3) / 4));
+#define JAMHIP_TOPK(EPL) moe_topk_kernel<EPL><<<grid, 256, 0, st>>>(sel, wts ? wts : sel, rows, E, ld, topk, mode, \
+                                                                     wscale, escale, route_expert, route_prob, counts)
+    if (E <= 64) JAMHIP_TOPK(1);
+    else if (E <= 128) JAMHIP_TOPK(2);
+    else if (E <= 256) JAMHIP_TOPK(4);
+    else if (E <= 512) JAMHIP_TOPK(8);
+    else JAMHIP_TOPK(16);
+#undef JAMHIP_TOPK
     return hipGetLastError();
 }
 

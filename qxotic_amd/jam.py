@@ -275,6 +275,19 @@ class HipJAM:
         return lib().jamhip_moe_gather(self.ctx, x_dev, ldx, slot_route_dev, offsets_dev, n_experts, seq, topk, dim,
                                        g_dev, ldg)
 
+    TOPK_RAW, TOPK_SOFTMAX, TOPK_NORMALIZE = 0, 1, 2
+
+    def moe_select_topk(self, selection_dev: int, weights_dev: int | None, rows: int, n_experts: int, ld: int,
+                        topk: int, mode: int, route_expert_dev: int, route_prob_dev: int,
+                        counts_dev: int | None = None, weights_scale: float = 1.0,
+                        expert_scale_dev: int | None = None) -> int:
+        """Moe.selectTopK on the device (selection consumed: winners masked to -Inf), then the row's weight
+        step by mode: raw, gpt-oss's softmax over the selected logits x weights_scale, or normalizeTopP; the
+        optional per-expert expertScale fold (jamhip_moe_select_topk)."""
+        return lib().jamhip_moe_select_topk(self.ctx, selection_dev, weights_dev, rows, n_experts, ld, topk, mode,
+                                            weights_scale, expert_scale_dev, route_expert_dev, route_prob_dev,
+                                            counts_dev)
+
     def moe_combine(self, y_dev: int, ldy: int, route_expert_dev: int, route_prob_dev: int, route_slot_dev: int,
                     seq: int, topk: int, n_experts: int, dim: int, out_dev: int, ldo: int) -> int:
         """Moe.dispatch's prob-weighted scatter-add (Moe.java:208, 223-231), bit-identical order."""

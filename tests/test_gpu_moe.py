@@ -332,3 +332,86 @@ def test_mm_grouped_decode_unfused(hip, oracle, dt):
             assert (got[sum(counts):] == -3.0).all()
         finally:
             hip.evict(Segment.of(w))
+
+
+def _topk_case(hip, sel, topk, mode, weights=None, wscale=1.0, escale=None, ld=None):
+    import torch
+    rows, E = sel.shape
+    ld = ld or E
+    s_pad = np.full((rows, ld), 5.5, np.float32)
+    s_pad[:, :E] = sel
+    sd = dev(s_pad)
+    wd = None
+    if weights is not None:
+        w_pad = np.zeros((rows, ld), np.float32)
+        w_pad[:, :E] = weights
+        wd = dev(w_pad)
+    ed = dev(np.asarray(escale, np.float32)) if escale is not None else None
+    re = torch.full((rows * topk,), -7, dtype=torch.int32, device="cuda")
+    rp = torch.zeros(rows * topk, dtype=torch.float32, device="cuda")
+    cnt = torch.full((E,), 99, dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()
+    st = hip.moe_select_topk(sd.data_ptr(), None if wd is None else wd.data_ptr(), rows, E, ld, topk, mode,
+                             re.data_ptr(), rp.data_ptr(), cnt.data_ptr(), wscale,
+                             None if ed is None else ed.data_ptr())
+    assert st == 0, hip.last_error()
+    hip.synchronize()
+    got_sel = sd.cpu().numpy()
+    assert (got_sel[:, E:] == 5.5).all()          # the row stride's gap is untouched
+    return re.cpu().numpy(), rp.cpu().numpy(), cnt.cpu().numpy(), got_sel[:, :E]
+
+
+def _topk_check(got, sel, topk, **kw):
+    re, rp, cnt, masked = got
+    re_o, rp_o, cnt_o, masked_o = M.select_topk(sel, topk, **kw)
+    assert np.array_equal(re, re_o)
+    assert np.array_equal(rp.view(np.uint32), rp_o.view(np.uint32)), np.flatnonzero(rp.view(np.uint32) != rp_o.view(np.uint32))[:5]
+    assert np.array_equal(cnt, cnt_o)
+    assert np.array_equal(masked.view(np.uint32), masked_o.view(np.uint32))
+
+
+def test_select_topk_bit_exact(hip):
+    """jamhip_moe_select_topk against oracle/moe.py's select_topk (Moe.selectTopK, gpt-oss's softmax over the
+    selected logits, normalizeTopP, the expertScale fold), bit for bit: routes, weights, counts and the
+    consumed selection array. Config 5's router (512 tokens x 32 experts, top-4, Zipf(1.1) popularity by
+    Gumbel-top-k on log p_e), one- and two-source forms, a row stride above E, and hand-made edge rows
+    (ties, all -Inf, NaN); E = 16 with k = 16 (every expert), E = 300 and 1024 (more scores per lane)."""
+    rng = np.random.default_rng(0x5A11C0DE ^ 5)
+    E, SEQ, TOPK = 32, 512, 4
+    logp = -1.1 * np.log(np.arange(1, E + 1))
+    logits = (logp[None, :] + rng.gumbel(size=(SEQ, E))).astype(np.float32)
+    logits[0, 3] = logits[0, 7] = np.float32(50.0)          # a tie: expert 3 first
+    logits[1] = -np.inf                                     # nothing above -Inf: expert 0 each pass
+    logits[2, :5] = np.nan                                  # NaN never wins
+    logits[3] = np.float32(0.25)                            # all equal
+    w = rng.random((SEQ, E)).astype(np.float32)
+    scale = (0.5 + rng.random(E)).astype(np.float32)
+    for mode in (M.TOPK_RAW, M.TOPK_SOFTMAX, M.TOPK_NORMALIZE):
+        say(f"topk config5 mode={mode}")
+        _topk_check(_topk_case(hip, logits, TOPK, mode), logits, TOPK, mode=mode)
+        _topk_check(_topk_case(hip, logits, TOPK, mode, weights=w, wscale=0.75, escale=scale, ld=E + 3), logits,
+                    TOPK, weights=w, mode=mode, weights_scale=0.75, expert_scale=scale)
+    re, _, cnt, _ = _topk_case(hip, logits, TOPK, M.TOPK_SOFTMAX)
+    c_o, _, _, _ = M.dispatch_csr(re, E)
+    assert np.array_equal(cnt, c_o)                        # the counts jamhip_moe_route builds from the routes
+    for E2, k2, seq in ((16, 16, 40), (300, 8, 70), (1024, 16, 9)):
+        say(f"topk E={E2} k={k2}")
+        sel = rng.standard_normal((seq, E2)).astype(np.float32)
+        sel[0, E2 - 1] = np.float32(9.0)                  # the last lane's last score
+        for mode in (M.TOPK_RAW, M.TOPK_SOFTMAX):
+            _topk_check(_topk_case(hip, sel, k2, mode), sel, k2, mode=mode)
+
+
+def test_select_topk_status_codes(hip):
+    import torch
+    f = torch.zeros((8, 64), dtype=torch.float32, device="cuda")
+    i = torch.zeros(64, dtype=torch.int32, device="cuda")
+    call = lambda **kw: hip.moe_select_topk(f.data_ptr(), None, kw.get("rows", 4), kw.get("E", 8), kw.get("ld", 8),
+                                            kw.get("k", 2), kw.get("mode", 0), i.data_ptr(), f.data_ptr(), None)
+    assert call() == 0
+    assert call(ld=7) == 1                      # EINVAL: ld < E
+    assert call(mode=3) == 1
+    assert call(k=0) == 1
+    assert call(k=17) == 2                      # EUNSUPPORTED: topk above 16
+    assert call(E=2000, ld=2000) == 2
+    hip.synchronize()
