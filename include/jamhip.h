@@ -260,6 +260,17 @@ enum { JAMHIP_ACT_SWIGLU = 1, JAMHIP_ACT_SWIGLU_OAI = 2 };
 jamhip_status jamhip_glu_device(jamhip_ctx* ctx, int act, void* gate_dev, int ldg, const void* up_dev, int ldu,
                                 int rows, int cols);
 
+/* jamhip_glu_device in the arithmetic jinfer runs by default, its Vector API loops (jdk.incubator.vector on;
+ * `lanes` = the float species length, 8 on AVX2 hosts, 16 on AVX-512): per row, elements [0, cols - cols %
+ * lanes) take the vector body with njuffa's rational tanh (Ops.tanhApprox, Ops.java:620-663):
+ *   JAMHIP_ACT_SWIGLU      g·(tanh(g/2)·0.5 + 0.5)·u                      (Ops.java:540-563)
+ *   JAMHIP_ACT_SWIGLU_OAI  min(g,7)·0.5·(1 + tanh(0.851·min(g,7)))·(clamp(u,±7) + 1)   (Activations.java:209-224)
+ * and the rest the loop's scalar tail (SwiGLU: the full-scalar double formula, Ops.java:566-575; gpt-oss:
+ * clampedSwigluApprox, Activations.java:189-194). f32 operations rounded where the Java code rounds, fma fused.
+ * lanes = 0 is jamhip_glu_device. */
+jamhip_status jamhip_glu_device_vector(jamhip_ctx* ctx, int act, void* gate_dev, int ldg, const void* up_dev,
+                                       int ldu, int rows, int cols, int lanes);
+
 /* Use `stream` (a hipStream_t; NULL = the context's own) for subsequent work of this context. */
 jamhip_status jamhip_ctx_set_stream(jamhip_ctx* ctx, void* stream);
 void*         jamhip_ctx_stream(const jamhip_ctx* ctx);

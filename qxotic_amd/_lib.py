@@ -38,6 +38,7 @@ SIGNATURES = [
     ("jamhip_moe_select_topk", _I, [_VP, _VP, _VP, _I, _I, _I, _I, _I, C.c_float, _VP, _VP, _VP, _VP]),
     ("jamhip_mm_device_ex", _I, [_VP, _VP, _I, _I, _VP, _I, _I, _VP, _I, _I, _I, _I, _I, _VP, _I]),
     ("jamhip_glu_device", _I, [_VP, _I, _VP, _I, _VP, _I, _I, _I]),
+    ("jamhip_glu_device_vector", _I, [_VP, _I, _VP, _I, _VP, _I, _I, _I, _I]),
     ("jamhip_ctx_set_stream", _I, [_VP, _VP]),
     ("jamhip_ctx_stream", _VP, [_VP]),
     ("jamhip_ctx_synchronize", _I, [_VP]),

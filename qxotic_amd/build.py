@@ -1,8 +1,9 @@
 """Build libjamhip.so (gfx950) in-tree with hipcc: ``python -m qxotic_amd.build``.
 
 Every translation unit is compiled for gfx950 only, with packed-FP32 instructions disabled; the
-activation quantizers additionally compile with -ffp-contract=off so their f32 products round exactly
-where jam's do.
+activation quantizers, the MoE routing (top-k weights) and the gated activations additionally compile with
+-ffp-contract=off so their f32 products round exactly where jam's and jinfer's do (a product is never fused
+into a following add unless the reference writes an fma).
 """
 from __future__ import annotations
 
@@ -39,8 +40,8 @@ UNITS = {   # source -> extra flags
     "gemm.hip": [],
     "mma.hip": [],
     "mxn.hip": [],
-    "moe.hip": [],
-    "epilogue.hip": [],
+    "moe.hip": ["-ffp-contract=off"],
+    "epilogue.hip": ["-ffp-contract=off"],
     "readfloor.hip": [],
     "jamhip.cpp": ["-x", "hip"],
     "gguf.cpp": [],

@@ -791,7 +791,7 @@ jamhip_status mm_device_ex_impl(jamhip_ctx* ctx, const void* w, int wt, int ldw,
 }
 
 jamhip_status glu_device_impl(jamhip_ctx* ctx, int act, void* gate_dev, int ldg, const void* up_dev, int ldu,
-                                int rows, int cols) {
+                                int rows, int cols, int lanes = 0) {
     if (!ctx) return JAMHIP_EINVAL;
     if (!gate_dev || !up_dev) return fail(ctx, JAMHIP_EINVAL, "glu: null operand");
     if (rows < 0 || cols < 0 || ldg < cols || ldu < cols) return fail(ctx, JAMHIP_EINVAL, "glu: bad extents");
@@ -800,7 +800,9 @@ jamhip_status glu_device_impl(jamhip_ctx* ctx, int act, void* gate_dev, int ldg,
     Busy guard(ctx);
     if (!guard.ok) return fail(ctx, JAMHIP_EBUSY, "context busy");
     (void) hipSetDevice(ctx->device);
-    const hipError_t e = launch_glu(act, (float*) gate_dev, ldg, (const float*) up_dev, ldu, rows, cols, ctx->stream);
+    if (lanes < 0) return fail(ctx, JAMHIP_EINVAL, "glu: lanes must be >= 0");
+    const hipError_t e = launch_glu(act, (float*) gate_dev, ldg, (const float*) up_dev, ldu, rows, cols, ctx->stream,
+                                    lanes);
     return e == hipSuccess ? JAMHIP_OK : hip_fail(ctx, e, "glu launch");
 }
 
@@ -1250,6 +1252,13 @@ jamhip_status jamhip_mm_device_ex(jamhip_ctx* ctx, const void* w, int wt, int ld
 jamhip_status jamhip_glu_device(jamhip_ctx* ctx, int act, void* gate_dev, int ldg, const void* up_dev, int ldu,
                                 int rows, int cols) {
     return on_ctx(ctx, [&](jamhip_ctx* x) { return glu_device_impl(x, act, gate_dev, ldg, up_dev, ldu, rows, cols); });
+}
+
+jamhip_status jamhip_glu_device_vector(jamhip_ctx* ctx, int act, void* gate_dev, int ldg, const void* up_dev,
+                                       int ldu, int rows, int cols, int lanes) {
+    return on_ctx(ctx, [&](jamhip_ctx* x) {
+        return glu_device_impl(x, act, gate_dev, ldg, up_dev, ldu, rows, cols, lanes);
+    });
 }
 
 jamhip_status jamhip_read_floor(jamhip_ctx* ctx, const void* p_dev, int64_t bytes, void* sink_dev) {

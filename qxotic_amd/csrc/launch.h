@@ -162,8 +162,10 @@ hipError_t launch_mx_gemm_grouped(int mode, const WeightView& w, const MxAct& A,
 hipError_t launch_dense(int dt, const WeightView& w, const float* a, int lda, int k, int m, int n, float* c, int ldc,
                         hipStream_t st, const Epi& ep = Epi{});
 
-// In place on gate [rows][ldg]: act 1 SwiGLU silu(gate)·up, act 2 gpt-oss clamped SwiGLU (epilogue.hip).
-hipError_t launch_glu(int act, float* gate, int ldg, const float* up, int ldu, int rows, int cols, hipStream_t st);
+// In place on gate [rows][ldg]: act 1 SwiGLU silu(gate)·up, act 2 gpt-oss clamped SwiGLU (epilogue.hip); lanes 0
+// the full-scalar arithmetic, lanes > 0 jinfer's Vector API arithmetic with a species of `lanes` floats.
+hipError_t launch_glu(int act, float* gate, int ldg, const float* up, int ldu, int rows, int cols, hipStream_t st,
+                      int lanes = 0);
 
 // Streaming read of `bytes` (a multiple of 16; 16-byte aligned p) with the decode kernel's load shape, nothing
 // written but a word at `sink` if the loads xor to a fixed value (readfloor.hip).

@@ -239,6 +239,12 @@ class HipJAM:
         """In place on gate: SwiGLU (act 1) or gpt-oss clamped SwiGLU (act 2) (jamhip_glu_device)."""
         return lib().jamhip_glu_device(self.ctx, act, gate_dev, ldg, up_dev, ldu, rows, cols)
 
+    def glu_device_vector(self, act: int, gate_dev: int, ldg: int, up_dev: int, ldu: int, rows: int, cols: int,
+                          lanes: int) -> int:
+        """glu_device in jinfer's default Vector API arithmetic (rational tanh) with a `lanes`-float species
+        (jamhip_glu_device_vector)."""
+        return lib().jamhip_glu_device_vector(self.ctx, act, gate_dev, ldg, up_dev, ldu, rows, cols, lanes)
+
     def read_floor(self, p_dev: int, nbytes: int, sink_dev: int) -> int:
         """Streaming read of nbytes at p_dev in the decode kernel's load shape (jamhip_read_floor)."""
         return lib().jamhip_read_floor(self.ctx, p_dev, nbytes, sink_dev)

@@ -131,3 +131,37 @@ def test_grouped_expert_bias_bit_exact(hip, oracle, dt):
         assert (fused[total:] == -5.0).all() and (fused[:, m] == -5.0).all()
     finally:
         hip.evict(Segment.of(w))
+
+
+@pytest.mark.parametrize("act", [1, 2])
+@pytest.mark.parametrize("lanes", [8, 16])
+def test_glu_vector(hip, act, lanes):
+    """jamhip_glu_device_vector: jinfer's default Vector API arithmetic (njuffa's rational tanh in f32 with
+    fused multiply-adds) against oracle/epilogue.py, bit for bit on the vector body; the elements past each
+    row's loop bound take the scalar tail (SwiGLU: the double formula, within 1 ulp, the double exp differing
+    by implementation; gpt-oss: clampedSwigluApprox, bit for bit). Clamp edges, +-0, NaN, the row gap."""
+    import torch
+    rows, cols, ldg, ldu = 5, 2885, 2889, 2887          # 2885 = 180*16 + 5 = 360*8 + 5
+    rng = np.random.default_rng(act * 100 + lanes)
+    g = (rng.standard_normal((rows, ldg)) * 6).astype(np.float32)
+    u = (rng.standard_normal((rows, ldu)) * 6).astype(np.float32)
+    g[0, :9] = [7.0, 7.0001, -7.0, 40.0, -40.0, 0.0, -0.0, 1e-30, np.nan]
+    u[0, :9] = [7.0, -7.0001, -1.0, 100.0, -100.0, 3.0, 3.0, 1.0, 2.0]
+    g[1, cols - 3:cols] = [11.5, -0.25, 6.0]            # the scalar tail
+    say(f"glu vector act={act} lanes={lanes}")
+    g_d = torch.from_numpy(g).cuda()
+    u_d = torch.from_numpy(u).cuda()
+    assert hip.glu_device_vector(act, g_d.data_ptr(), ldg, u_d.data_ptr(), ldu, rows, cols, lanes) == 0, \
+        hip.last_error()
+    hip.synchronize()
+    got = g_d.cpu().numpy()[:, :cols]
+    f = EP.silu_mul_vector if act == 1 else EP.clamped_swiglu_vector
+    want = f(g[:, :cols], u[:, :cols], lanes)
+    bound = cols - cols % lanes
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    got, want = np.where(np.isnan(got), 0, got), np.where(np.isnan(want), 0, want)   # NaN payloads may differ
+    assert np.array_equal(got[:, :bound].view(np.uint32), want[:, :bound].view(np.uint32))
+    d = np.abs(got[:, bound:].view(np.int32).astype(np.int64) - want[:, bound:].view(np.int32).astype(np.int64))
+    assert d.max() <= (1 if act == 1 else 0), int(d.max())
+    assert np.array_equal(g_d.cpu().numpy()[:, cols:].view(np.uint32), g[:, cols:].view(np.uint32))
+    assert hip.glu_device_vector(act, g_d.data_ptr(), ldg, u_d.data_ptr(), ldu, rows, cols, -1) == 1   # EINVAL
