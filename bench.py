@@ -64,6 +64,31 @@ def quantized(name: str, m: int, k: int, seed: int) -> np.ndarray:
     return ggml.quantize(name, x)
 
 
+def synthetic(name: str, m: int, k: int, seed: int) -> np.ndarray:
+    """[m, row_bytes] weights for the types qxotic_amd.ggml does not quantize: Q5_K, NVFP4 and Q1_0 as random
+    valid blocks (random quant bytes; block scales drawn so the decoded values are of the N(0, 0.02) order),
+    F16 / BF16 as N(0, 0.02) draws rounded to the type. The kernels' work does not depend on the values."""
+    rng = np.random.default_rng(seed)
+    if name in ("F16", "BF16"):
+        x = rng.normal(0.0, 0.02, (m, k)).astype(np.float32)
+        if name == "F16":
+            return np.ascontiguousarray(x.astype(np.float16).view(np.uint8))
+        u = x.view(np.uint32)
+        return np.ascontiguousarray(((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16).view(np.uint8))
+    be, bb = {"Q5_K": (256, 176), "NVFP4": (64, 36), "Q1_0": (128, 18)}[name]
+    nb = k // be
+    blk = rng.integers(0, 256, (m, nb, bb), dtype=np.uint8)
+    f16 = lambda lo, hi: rng.uniform(lo, hi, (m, nb)).astype(np.float16).view(np.uint8).reshape(m, nb, 2)
+    if name == "Q5_K":
+        blk[:, :, 0:2] = f16(2e-5, 8e-5)          # d
+        blk[:, :, 2:4] = f16(1e-4, 5e-4)          # dmin
+    elif name == "NVFP4":
+        blk[:, :, 0:4] = rng.integers(0x20, 0x30, (m, nb, 4), dtype=np.uint8)   # UE4M3 sub-block scales
+    else:
+        blk[:, :, 0:2] = f16(0.01, 0.03)
+    return np.ascontiguousarray(blk.reshape(m, nb * bb))
+
+
 def calibrate_copy(torch) -> None:
     """Three device-to-device copies of 256 MiB: 256 MiB read + 256 MiB written per dispatch."""
     src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
@@ -215,8 +240,14 @@ def shapes_leg(hip, torch, stream, steps: int = 512) -> dict:
     for label, name, dt, m, k, ns in (("config1", "Q8_0", JAM.Q8_0, 4096, 4096, (1,)),
                                       ("config2", "Q4_0", JAM.Q4_0, 14336, 4096, (1, 4, 8)),
                                       ("config2", "Q4_0", JAM.Q4_0, 4096, 14336, (1, 4, 8)),
-                                      ("config3 down", "Q6_K", JAM.Q6_K, 4096, 14336, (1,))):
-        w = quantized(name, m, k, 0x5A11C0DE ^ dt ^ m)
+                                      ("config3 down", "Q6_K", JAM.Q6_K, 4096, 14336, (1,)),
+                                      ("dtype", "Q5_K", JAM.Q5_K, 14336, 4096, (1,)),
+                                      ("dtype", "NVFP4", JAM.NVFP4, 14336, 4096, (1,)),
+                                      ("dtype", "Q1_0", JAM.Q1_0, 14336, 4096, (1,)),
+                                      ("dtype", "F16", JAM.F16, 14336, 4096, (1,)),
+                                      ("dtype", "BF16", JAM.BF16, 14336, 4096, (1,))):
+        w = (quantized(name, m, k, 0x5A11C0DE ^ dt ^ m) if name in ("Q8_0", "Q4_0", "Q6_K")
+             else synthetic(name, m, k, 0x5A11C0DE ^ dt ^ m))
         ncp = max(32, -(-1_070_000_000 // w.nbytes))
         copies = [w.copy() for _ in range(ncp)]
         for cp in copies:
@@ -256,18 +287,25 @@ def shapes_leg(hip, torch, stream, steps: int = 512) -> dict:
             hip.evict(Segment.of(cp))
         del copies
     out["note"] = ("graph-timed like the headline: one captured graph of %d launches over >= 1.07 GB of rotating "
-                   "pinned copies; bytes = W + A + C once" % steps)
+                   "pinned copies; bytes = W + A + C once; 'dtype' rows: jam's other weight types (random valid "
+                   "blocks / N(0,0.02) rounded)" % steps)
     return out
 
 
 def prefill_leg(hip, torch, stream, reps: int = 10) -> dict:
-    """M=512 prefill on the two BASELINE prefill shapes; each timed call quantizes its activations (F2)."""
+    """M=512 prefill on the two BASELINE prefill shapes (config 4), then jam's other weight types at 14336x4096;
+    each timed call quantizes its activations (F2; NVFP4: F1, jam's only path for it)."""
     from qxotic_amd.jam import JAM, Segment
 
     out = {}
     n = 512
-    for name, dt, m, k in (("Q4_K", JAM.Q4_K, 14336, 4096), ("Q6_K", JAM.Q6_K, 4096, 14336)):
-        w = quantized(name, m, k, 0x5EED ^ dt)
+    for name, dt, m, k in (("Q4_K", JAM.Q4_K, 14336, 4096), ("Q6_K", JAM.Q6_K, 4096, 14336),
+                           ("Q5_K", JAM.Q5_K, 14336, 4096), ("Q4_0", JAM.Q4_0, 14336, 4096),
+                           ("Q8_0", JAM.Q8_0, 14336, 4096), ("MXFP4", JAM.MXFP4, 14336, 4096),
+                           ("NVFP4", JAM.NVFP4, 14336, 4096), ("Q1_0", JAM.Q1_0, 14336, 4096),
+                           ("F16", JAM.F16, 14336, 4096)):
+        w = (quantized(name, m, k, 0x5EED ^ dt) if name in ("Q4_K", "Q6_K", "Q4_0", "Q8_0", "MXFP4")
+             else synthetic(name, m, k, 0x5EED ^ dt))
         assert hip.pin(Segment.of(w), dt, k, m) == JAM.OK, hip.last_error()
         rng = np.random.default_rng(11)
         x = rng.standard_normal((n, k)).astype(np.float32)
@@ -289,16 +327,18 @@ def prefill_leg(hip, torch, stream, reps: int = 10) -> dict:
         tops = 2.0 * m * n * k / (us * 1e-6) / 1e12
         assert bool(torch.isfinite(c).all()), "prefill output not finite"
         # the host-pointer entry point on the same call (jamhip_mm: 8 / 28 MiB of A up, C down, synchronized)
-        c_h = np.empty((n, m), np.float32)
-        hip.mm_contiguous(Segment.of(w), Segment.of(x), Segment.of(c_h), dt, m, n, k)
-        t0 = time.perf_counter()
-        for _ in range(5):
-            assert hip.mm_contiguous(Segment.of(w), Segment.of(x), Segment.of(c_h), dt, m, n, k) == JAM.OK
-        host_us = (time.perf_counter() - t0) / 5 * 1e6
+        host_us = None
+        if name in ("Q4_K", "Q6_K"):
+            c_h = np.empty((n, m), np.float32)
+            hip.mm_contiguous(Segment.of(w), Segment.of(x), Segment.of(c_h), dt, m, n, k)
+            t0 = time.perf_counter()
+            for _ in range(5):
+                assert hip.mm_contiguous(Segment.of(w), Segment.of(x), Segment.of(c_h), dt, m, n, k) == JAM.OK
+            host_us = round((time.perf_counter() - t0) / 5 * 1e6, 1)
         out[f"{name} {m}x{k} M=512"] = {"us": round(us, 2), "TOPS": round(tops, 2),
                                         "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
                                         "frac_f16_peak": round(tops / F16_PEAK_TFLOPS, 4),
-                                        "host_pointer_us": round(host_us, 1)}
+                                        "host_pointer_us": host_us}
         hip.evict(Segment.of(w))
         del a, c
     out["note"] = ("jam's F2 quantization + int8 products computed exactly on f16 MFMA (integer operands "

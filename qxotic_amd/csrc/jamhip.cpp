@@ -326,11 +326,11 @@ bool env_true(const char* name) {
     return v && (!strcmp(v, "1") || !strcasecmp(v, "true") || !strcasecmp(v, "yes"));
 }
 
-// The matrix-core GEMM covers Q4_K, Q6_K (k a multiple of 256), MXFP4, Q4_0 and Q8_0 on 32-row-aligned views
-// (launch_gemm_mma), for k up to the activation prep's limit (gemm_prep_fits).
+// The matrix-core GEMM covers Q4_K, Q5_K, Q6_K (k a multiple of 256), MXFP4, Q4_0 and Q8_0 on 32-row-aligned
+// views (launch_gemm_mma), for k up to the activation prep's limit (gemm_prep_fits).
 bool mma_path(int dt, int k, const WeightView& wv) {
     if (env_true("JAM_HIP_NO_MMA")) return false;
-    return (((dt == Q4_K || dt == Q6_K) && k % 256 == 0) || dt == MXFP4 || dt == Q4_0 || dt == Q8_0) &&
+    return (((dt == Q4_K || dt == Q5_K || dt == Q6_K) && k % 256 == 0) || dt == MXFP4 || dt == Q4_0 || dt == Q8_0) &&
            (wv.r0 & 31) == 0 && gemm_prep_fits(k);
 }
 
@@ -359,7 +359,7 @@ bool mma_exact(jamhip_ctx* ctx, int dt, int k, WeightView& wv) {
 static int mma_min_n(int dt, int m, int k) {
     const char* v = getenv("JAM_HIP_MMA_MIN_N");
     if (v) return atoi(v) < 8 ? 8 : atoi(v);
-    if ((int64_t) m * k <= (int64_t) 17 << 20) return dt == Q4_0 || dt == Q4_K || dt == Q6_K ? 33 : 17;
+    if ((int64_t) m * k <= (int64_t) 17 << 20) return dt == Q4_0 || dt == Q4_K || dt == Q5_K || dt == Q6_K ? 33 : 17;
     return k > 8192 ? 16 : 9;
 }
 

@@ -1,9 +1,10 @@
-// Matrix-core prefill GEMM for Q4_K, Q6_K and MXFP4 weights: C[n][m] = W[m][k] · A[n][k]^T with jam's
+// Matrix-core prefill GEMM for Q4_K, Q5_K, Q6_K, MXFP4, Q4_0 and Q8_0 weights: C[n][m] = W[m][k] · A[n][k]^T with jam's
 // F2 semantics (the n >= 8 bands of jam_kernels_q4k_avx512.c), activations from launch_gemm_prep.
 //
 // Arithmetic. Each 32-element block's integer dot runs on v_mfma_f32_32x32x16_f16 with integer operands
 // that f16 holds exactly: the activation codes (int8) and the weight codes with their integer sub-scale
-// folded in (Q4_K sc·nib <= 945; Q6_K sc·q6 / 4 in two planes, sc·(q6 & 15) / 4 and sc·(q6 & 48) / 4).
+// folded in (Q4_K sc·nib <= 945, Q5_K sc·q5 <= 1953; Q6_K sc·q6 / 4 in two planes, sc·(q6 & 15) / 4 and
+// sc·(q6 & 48) / 4).
 // Every product and every 32-term sum is an exact f32 integer (a quarter-integer for Q6_K), so the MFMA
 // returns the block's exact dot; one f32 FMA per output then applies the block's activation scale, and
 // the super-block scale d is applied once per 256 elements. The super-block's other term runs on the
@@ -69,6 +70,25 @@ JAMHIP_DEV half8 frag8(uint32_t w0, uint32_t w1, uint32_t mask, uint32_t mul, ui
     return __builtin_bit_cast(half8, u32x4{p0, p1, p2, p3});
 }
 
+// Q5_K: frag8 of a nibble word pair with the 5th bit of each element merged in. Bit b (the stage's block) of
+// each qh byte (h0 / h1: the qh bytes of the nibble bytes of w0 / w1) goes to bit 4 of the lo-nibble field
+// (value nib + 16·bit, b even) or to bit 8 for the hi-nibble field (16·(nib + 16·bit), b odd), so
+// 0x6400 | field is the f16 1024 + v5 or 1024 + 16·v5 that mul / add turn into sc·v5 (<= 1953, exact).
+JAMHIP_DEV half8 frag8q5(uint32_t w0, uint32_t w1, uint32_t h0, uint32_t h1, int b, uint32_t mask, uint32_t mul,
+                         uint32_t add) {
+    const uint32_t m = 0x64006400u;
+    const bool hi = b & 1;
+    const uint32_t hm = hi ? 0x01000100u : 0x00100010u;
+    // bytes (0, 2): bit b -> bit 4 (lo) / 8 (hi); bytes (1, 3) (the word shifted down by 8): bit 8 + b -> the same
+    const int up = hi ? 8 - b : 4 - b, dn = hi ? b : b + 4;
+    const uint32_t e0 = ((h0 << up) & hm) | m, e1 = ((h0 >> dn) & hm) | m;
+    const uint32_t e2 = ((h1 << up) & hm) | m, e3 = ((h1 >> dn) & hm) | m;
+    const uint32_t p0 = pkfma((w0 & mask) | e0, mul, add), p1 = pkfma(((w0 >> 8) & mask) | e1, mul, add);
+    const uint32_t p2 = pkfma((w1 & mask) | e2, mul, add), p3 = pkfma(((w1 >> 8) & mask) | e3, mul, add);
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    return __builtin_bit_cast(half8, u32x4{p0, p1, p2, p3});
+}
+
 // Q4_K 6-bit scale and min of sub-block s (jam/jam-native/src/jam_kquant.h:26-33); h = the 16-byte header.
 JAMHIP_DEV void q4k_scmn(const uint4 h, int s, int& sc, int& mn) {
     const uint32_t u0 = h.y, u1 = h.z, u2 = h.w;
@@ -104,9 +124,10 @@ JAMHIP_DEV half8 mx_frag(uint32_t w, float scale) {
 // block scales [4][BN] f32, sums hi/lo [BN][SW] f16 each.
 template <int DT, int RT, int CT> struct Stage {
     static constexpr int TW = MMA_WAVES * RT, BN = 32 * CT;
-    static constexpr int NCS = DT == Q6_K ? 7 : DT == Q8_0 ? 8 : 4;   // chunks per stage (Q6_K: 4 ql, 2 qh, scales)
+    // chunks per stage (Q6_K: 4 ql, 2 qh, scales; Q5_K: 4 nibble chunks, then the super-block's 2 qh chunks)
+    static constexpr int NCS = DT == Q6_K ? 7 : DT == Q8_0 ? 8 : DT == Q5_K ? 6 : 4;
     static constexpr int HB = DT == Q6_K ? 2 : 16;           // header bytes per row (Q6_K: d)
-    static constexpr int SW = DT == Q4_K || DT == Q4_0 ? 8 : DT == Q6_K ? 16 : 0;   // sums per token per group
+    static constexpr int SW = DT == Q4_K || DT == Q5_K || DT == Q4_0 ? 8 : DT == Q6_K ? 16 : 0;   // sums per token per group
     static constexpr int A_OFF = 0;
     static constexpr int H_OFF = A_OFF + TW * NCS * 512;
     static constexpr int B_OFF = (H_OFF + TW * 32 * HB + 1023) / 1024 * 1024;
@@ -201,8 +222,12 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
     auto issue = [&](int st, unsigned char* buf) {
         const int g = st >> 1, h2 = st & 1;
         const uint8_t* ag = a_src + (int64_t) g * (NC * CHUNK_STRIDE);
-        if constexpr (DT != Q6_K) {   // Q4_K chunks 4h2..4h2+3 (sub-block pairs), MXFP4 / Q4_0 blocks 4h2..4h2+3,
-                                      // Q8_0 chunks 8h2..8h2+7 (two per block)
+        if constexpr (DT == Q5_K) {   // nibble chunks 4h2..4h2+3 as Q4_K, then the qh chunks 8, 9
+#pragma unroll
+            for (int p = 0; p < 2; p++) dma16(ag + (4 * h2 + 2 * p) * CHUNK_STRIDE, buf + a_dst + 2 * p * 512);
+            dma16(ag + 8 * CHUNK_STRIDE, buf + a_dst + 4 * 512);
+        } else if constexpr (DT != Q6_K) {   // Q4_K chunks 4h2..4h2+3 (sub-block pairs), MXFP4 / Q4_0 blocks
+                                             // 4h2..4h2+3, Q8_0 chunks 8h2..8h2+7 (two per block)
 #pragma unroll
             for (int p = 0; p < NCS / 2; p++)
                 dma16(ag + (NCS * h2 + 2 * p) * CHUNK_STRIDE, buf + a_dst + 2 * p * 512);
@@ -234,7 +259,7 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
         // sums: Q4_K needs them at the super-block's end (odd stage), Q6_K at its start (even stage); a plane's
         // piece p holds tokens 32p.. (two pieces) or a token per lane (one piece)
         if constexpr (S::SW > 0) {
-            if ((DT == Q4_0 || (DT == Q4_K) == (h2 == 1)) && (SPC == 2 || wave == 1 || wave == 3) &&
+            if ((DT == Q4_0 || (DT == Q4_K || DT == Q5_K) == (h2 == 1)) && (SPC == 2 || wave == 1 || wave == 3) &&
                 (!half || (SPC == 2 ? s_p == 0 : lane < 32)))
                 dma16(s_src + (int64_t) g * A.NP * SWB, buf + S::S_OFF + s_pl * BN * SWB + s_p * 1024);
         }
@@ -273,7 +298,7 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
             const unsigned char* LB = buf + S::B_OFF;
             const float* LDX = reinterpret_cast<const float*>(buf + S::DX_OFF);
 
-            if constexpr (DT == Q4_K) {   // accs starts at zero and is cleared where it is consumed
+            if constexpr (DT == Q4_K || DT == Q5_K) {   // accs starts at zero and is cleared where it is consumed
                 uint4 hdr[RT];
                 uint32_t scs[RT];   // the stage's 4 sub-block scales (6-bit), one per byte
     #pragma unroll
@@ -286,6 +311,8 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
                 }
                 // every LDS read of the stage up front (the wave then works down an in-order queue)
                 uint4 chs[2][RT];
+                uint4 qhs[RT];   // Q5_K: the qh bytes of this lane's 16 elements (bit s = sub-block s), shifted so
+                                 // that bit bl is the stage's block bl
                 half8 bfs[4][CT][2];
                 float dxs[4][CT];
     #pragma unroll
@@ -293,6 +320,14 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
     #pragma unroll
                     for (int i = 0; i < RT; i++)
                         chs[gpl][i] = *reinterpret_cast<const uint4*>(LA + ((wave * RT + i) * NCS + 2 * gpl + q) * 512 + 16 * r);
+                if constexpr (DT == Q5_K) {
+    #pragma unroll
+                    for (int i = 0; i < RT; i++) {
+                        const uint4 h = *reinterpret_cast<const uint4*>(LA + ((wave * RT + i) * NCS + 4 + q) * 512 + 16 * r);
+                        const int sh = 4 * h2;
+                        qhs[i] = make_uint4(h.x >> sh, h.y >> sh, h.z >> sh, h.w >> sh);
+                    }
+                }
     #pragma unroll
                 for (int bl = 0; bl < 4; bl++)
     #pragma unroll
@@ -342,8 +377,13 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
                             const half2v addv = one * (sub ? (_Float16) -64.0f : (_Float16) -1024.0f);
                             const uint32_t mul = __builtin_bit_cast(uint32_t, mulv), add = __builtin_bit_cast(uint32_t, addv);
                             const uint32_t mask = sub ? vmask_hi : vmask_lo;
-                            af[i][0] = frag8(ch[i].x, ch[i].y, mask, mul, add);
-                            af[i][1] = frag8(ch[i].z, ch[i].w, mask, mul, add);
+                            if constexpr (DT == Q5_K) {   // the 5th bit (qh bit bl of each byte) at bit 4 (lo) or 8 (hi)
+                                af[i][0] = frag8q5(ch[i].x, ch[i].y, qhs[i].x, qhs[i].y, bl, mask, mul, add);
+                                af[i][1] = frag8q5(ch[i].z, ch[i].w, qhs[i].z, qhs[i].w, bl, mask, mul, add);
+                            } else {
+                                af[i][0] = frag8(ch[i].x, ch[i].y, mask, mul, add);
+                                af[i][1] = frag8(ch[i].z, ch[i].w, mask, mul, add);
+                            }
                         }
     #pragma unroll
                         for (int i = 0; i < RT; i++)
@@ -816,7 +856,7 @@ static hipError_t kq_go(const WeightView& w, const GemmAct& A, int m, int n, flo
 }
 
 size_t gemm_mma_split_floats(int dt, int k, int m, int n) {
-    if (dt != Q4_K && dt != Q6_K && dt != MXFP4 && dt != Q4_0 && dt != Q8_0) return 0;
+    if (dt != Q4_K && dt != Q5_K && dt != Q6_K && dt != MXFP4 && dt != Q4_0 && dt != Q8_0) return 0;
     const int nrb = (m + 32 * MMA_WAVES - 1) / (32 * MMA_WAVES), ncb = (n + 63) / 64, nsb = (k + 255) / 256;
     int ns, sb_per;
     split_plan(nrb * ncb, nsb, &ns, &sb_per);
@@ -825,9 +865,10 @@ size_t gemm_mma_split_floats(int dt, int k, int m, int n) {
 
 hipError_t launch_gemm_mma(int dt, const WeightView& w, const GemmAct& A, int k, int m, int n, float* c, int ldc,
                            hipStream_t st, float* part, const Epi& ep) {
-    if (((dt == Q4_K || dt == Q6_K) && k % 256) || (w.r0 & 31) || A.NP % 64) return hipErrorNotSupported;
+    if (((dt == Q4_K || dt == Q5_K || dt == Q6_K) && k % 256) || (w.r0 & 31) || A.NP % 64) return hipErrorNotSupported;
     switch (dt) {
     case Q4_K: return kq_go<Q4_K, 1, 2>(w, A, m, n, c, ldc, st, Groups{}, part, ep);
+    case Q5_K: return kq_go<Q5_K, 1, 2>(w, A, m, n, c, ldc, st, Groups{}, part, ep);
     case Q4_0: return kq_go<Q4_0, 1, 2>(w, A, m, n, c, ldc, st, Groups{}, part, ep);
     case Q8_0: return kq_go<Q8_0, 1, 2>(w, A, m, n, c, ldc, st, Groups{}, part, ep);
     case Q6_K: return kq_go<Q6_K, 1, 2>(w, A, m, n, c, ldc, st, Groups{}, part, ep);

@@ -180,7 +180,7 @@ __global__ void flag_clear_kernel(int* flag) { *flag = 0; }
 // dequantization builds f16 pairs from bytes (0,2), (1,3), (4,6), (5,7) of two 32-bit words.
 JAMHIP_DEV int perm8(int j) { return j == 1 ? 2 : j == 2 ? 1 : j == 5 ? 6 : j == 6 ? 5 : j; }
 
-int gemm_sums_kind(int dt) { return dt == Q4_K || dt == Q4_0 ? 1 : dt == Q6_K ? 2 : 0; }
+int gemm_sums_kind(int dt) { return dt == Q4_K || dt == Q5_K || dt == Q4_0 ? 1 : dt == Q6_K ? 2 : 0; }
 
 // A workgroup takes one token slot at a time (256 threads, a thread per 16-element half of a block, 128
 // blocks per round; at most PREP_GRID workgroups, each looping over its XCD's share of the slots that hold

@@ -16,6 +16,7 @@ from oracle import oracle as O
 pytestmark = pytest.mark.gpu
 
 SHAPES = [(104, 1024), (100, 512), (70, 256), (64, 768)]   # JamBackendParityTest.java:204-252
+MMA_TYPES = O.QUANT_TYPES + (O.Q5_K,)                       # the types the matrix-core GEMM covers
 NS = [1, 2, 3, 4, 7, 8, 13, 16, 17, 32, 33, 64, 100]
 
 
@@ -103,7 +104,7 @@ def test_mm_parity_shapes(hip, oracle, dt):
             assert (np.abs(got - fref) <= 1e-2 * sa + 1e-3).all(), (O.NAMES[dt], m, n, k)
 
 
-@pytest.mark.parametrize("dt", O.QUANT_TYPES)
+@pytest.mark.parametrize("dt", MMA_TYPES)
 def test_matrix_cores_and_f2_at_few_tokens(hip, oracle, dt, monkeypatch):
     """Both n >= 8 paths at the token counts where the routing threshold (weight size and k dependent)
     hands over: JAM_HIP_MMA_MIN_N forces the matrix cores (8) or the F2 decode kernel (huge) on the same
@@ -341,7 +342,7 @@ def test_decode_fused_prologue_matches_quantized_copy(hip, oracle, dt):
 
 
 # ------------------------------------------------------------------------------------ prefill GEMM
-PREFILL = [(O.Q4_K, 14336, 4096), (O.Q6_K, 4096, 14336)]
+PREFILL = [(O.Q4_K, 14336, 4096), (O.Q6_K, 4096, 14336), (O.Q5_K, 14336, 4096)]
 
 
 @pytest.mark.parametrize("dt,m,k", PREFILL)
@@ -365,7 +366,7 @@ def test_prefill_full_size(hip, oracle, dt, m, k):
     assert ok.all(), (int((~ok).sum()), float(np.max(np.abs(got[:, rows] - ref) / (np.abs(ref) + 1e-30))))
 
 
-@pytest.mark.parametrize("dt", O.QUANT_TYPES)
+@pytest.mark.parametrize("dt", MMA_TYPES)
 def test_prefill_ragged_shapes(hip, oracle, dt):
     """GEMM edge tiles: m not a multiple of the row tile (and of 16: float-dot tail), n not a multiple of the
     token tile, k with a partial 256-element chunk for the 32-element block types."""
@@ -382,7 +383,7 @@ def test_prefill_ragged_shapes(hip, oracle, dt):
         assert tier1(got, ref, sa).all(), (O.NAMES[dt], m, n, k)
 
 
-@pytest.mark.parametrize("dt", [O.Q4_K, O.Q6_K, O.MXFP4, O.Q8_0, O.Q4_0])
+@pytest.mark.parametrize("dt", [O.Q4_K, O.Q5_K, O.Q6_K, O.MXFP4, O.Q8_0, O.Q4_0])
 def test_prefill_tail_split_tiles(hip, oracle, dt):
     """Grids whose last partial round of tiles runs as half tiles: 1024 rows x 65 slot blocks give 65 tiles per
     XCD, one of them split into two 32-token workgroups. Every token's result equals that of the n = 4096 grid
@@ -405,7 +406,7 @@ def test_prefill_tail_split_tiles(hip, oracle, dt):
         assert ok.all(), (O.NAMES[dt], n, int((~ok).sum()))
 
 
-@pytest.mark.parametrize("dt", O.QUANT_TYPES)
+@pytest.mark.parametrize("dt", MMA_TYPES)
 def test_prefill_error_floor(hip, oracle, dt):
     """The GEMM stays at its arithmetic's error floor, far inside tier 1: max |gpu - oracle| / sum|w*a| <= 2e-6
     over 160 tokens of N(0,1) activations with a per-token offset in [-1, 1] (an offset token's super-block
