@@ -162,4 +162,13 @@ JAMHIP_DEV float e8m0_half(uint32_t e) {
     return 0.5f * __builtin_bit_cast(float, bits);
 }
 
+// UE4M3 byte -> float as jam_ue4m3_to_float (jam/jam-native/src/kernels/jam_nvfp4.h:19-25): 0x00 and 0x7F give
+// 0, otherwise bit 7 is ignored; normal (1 + m/8)·2^(e-7) built from its bits, subnormal m·2^-9 (exact).
+JAMHIP_DEV float ue4m3(uint32_t x) {
+    const uint32_t e = (x >> 3) & 15u, m = x & 7u;
+    const float normal = __builtin_bit_cast(float, ((e + 120u) << 23) | (m << 20));
+    const float sub = (float) m * 0.001953125f;
+    return (x & 0xffu) == 0u || (x & 0xffu) == 0x7fu ? 0.0f : e ? normal : sub;
+}
+
 }  // namespace jamhip

@@ -111,14 +111,6 @@ JAMHIP_DEV void q4k_sm(const uint4 h, int s, int& sc, int& mn) {
 
 JAMHIP_DEV int sbyte(uint32_t w, int b) { return (int) (int8_t) (w >> (8 * b)); }
 
-// UE4M3 byte -> float as jam_ue4m3_to_float (jam/jam-native/src/kernels/jam_nvfp4.h:19-25): 0x00 and 0x7F give
-// 0, otherwise bit 7 is ignored; normal (1 + m/8)·2^(e-7) built from its bits, subnormal m·2^-9 (exact).
-JAMHIP_DEV float ue4m3(uint32_t x) {
-    const uint32_t e = (x >> 3) & 15u, m = x & 7u;
-    const float normal = __builtin_bit_cast(float, ((e + 120u) << 23) | (m << 20));
-    const float sub = (float) m * 0.001953125f;
-    return (x & 0xffu) == 0u || (x & 0xffu) == 0x7fu ? 0.0f : e ? normal : sub;
-}
 
 // Q1_0: sign bits b0..b3 of a nibble -> the bytes (b0, b1, b2, b3) as 0 / 1 (the products b·2^(7j) land on
 // distinct bits, so the multiply carries nothing into the kept ones).

@@ -326,11 +326,12 @@ bool env_true(const char* name) {
     return v && (!strcmp(v, "1") || !strcasecmp(v, "true") || !strcasecmp(v, "yes"));
 }
 
-// The matrix-core GEMM covers Q4_K, Q5_K, Q6_K (k a multiple of 256), MXFP4, Q4_0 and Q8_0 on 32-row-aligned
-// views (launch_gemm_mma), for k up to the activation prep's limit (gemm_prep_fits).
+// The matrix-core GEMM covers Q4_K, Q5_K, Q6_K (k a multiple of 256), MXFP4, NVFP4, Q4_0 and Q8_0 on
+// 32-row-aligned views (launch_gemm_mma), for k up to the activation prep's limit (gemm_prep_fits).
 bool mma_path(int dt, int k, const WeightView& wv) {
     if (env_true("JAM_HIP_NO_MMA")) return false;
-    return (((dt == Q4_K || dt == Q5_K || dt == Q6_K) && k % 256 == 0) || dt == MXFP4 || dt == Q4_0 || dt == Q8_0) &&
+    return (((dt == Q4_K || dt == Q5_K || dt == Q6_K) && k % 256 == 0) || dt == MXFP4 || dt == NVFP4 || dt == Q4_0 ||
+            dt == Q8_0) &&
            (wv.r0 & 31) == 0 && gemm_prep_fits(k);
 }
 
@@ -446,20 +447,23 @@ jamhip_status compute(jamhip_ctx* ctx, Scratch& sc, int dt, WeightView wv, const
             return hip_fail(ctx, e, "mx gemm launch");
         return JAMHIP_OK;
     }
-    if (n >= mma_min_n(dt, m, k) && m16 > 0 && mma_exact(ctx, dt, k, wv)) {
+    // NVFP4 has no 16-row band in jam (F1 on every row at every n, jam.c:662-668): all m rows on the matrix cores
+    const int mm_rows = dt == NVFP4 ? m : m16;
+    if (n >= mma_min_n(dt, m, k) && mm_rows > 0 && mma_exact(ctx, dt, k, wv)) {
         GemmAct G;
         void* gact = nullptr;
         float* part = nullptr;
         if ((e = sc.get(ctx->gact, gemm_act_bytes(dt, n, k), &gact)) != hipSuccess)
             return scratch_fail(ctx, sc, e, "gemm activation scratch");
-        if (const size_t pf = gemm_mma_split_floats(dt, k, m16, n))
+        if (const size_t pf = gemm_mma_split_floats(dt, k, mm_rows, n))
             if ((e = sc.get(ctx->part, pf * sizeof(float), (void**) &part)) != hipSuccess)
                 return scratch_fail(ctx, sc, e, "gemm split scratch");
         if ((e = launch_gemm_prep(dt, a, lda, n, k, gact, &G, ctx->stream)) != hipSuccess)
             return hip_fail(ctx, e, "gemm prep launch");
-        if ((e = launch_gemm_mma(dt, wv, G, k, m16, n, c, ldc, ctx->stream, part, ep)) != hipSuccess)
+        if ((e = launch_gemm_mma(dt, wv, G, k, mm_rows, n, c, ldc, ctx->stream, part, ep)) != hipSuccess)
             return hip_fail(ctx, e, "gemm launch");
-        if ((e = launch_rows_float(dt, wv, a, lda, k, m16, m - m16, n, c, ldc, ctx->stream, ep)) != hipSuccess)
+        if (mm_rows < m &&
+            (e = launch_rows_float(dt, wv, a, lda, k, m16, m - m16, n, c, ldc, ctx->stream, ep)) != hipSuccess)
             return hip_fail(ctx, e, "tail rows launch");
         return JAMHIP_OK;
     }

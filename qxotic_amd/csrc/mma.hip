@@ -119,6 +119,19 @@ JAMHIP_DEV half8 mx_frag(uint32_t w, float scale) {
     return half8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
 }
 
+// NVFP4: 8 f16 of one K-step from one word (bytes 4q..4q+3 of a 16-element sub-block): byte u's two codes are
+// elements u and u + 8 (jam_kernels_generic.c:128-131), converted with scale 2 (jam's integer codes kv, 0..12)
+// and multiplied by the sub-block's scale d: slots 2j, 2j + 1 = elements 4q + j, 4q + j + 8 (GemmAct order 2).
+JAMHIP_DEV half8 nv_frag(uint32_t w, _Float16 d) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const h2 dd = {d, d};
+    const h2 p0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 2.0f, 0) * dd;
+    const h2 p1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 2.0f, 1) * dd;
+    const h2 p2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 2.0f, 2) * dd;
+    const h2 p3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 2.0f, 3) * dd;
+    return half8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+}
+
 // ------------------------------------------------------------------------------------ stage layout
 // Per stage buffer (bytes): A chunks [TW][NCS][32][16], header [TW][32][HB], codes [8][BN][32],
 // block scales [4][BN] f32, sums hi/lo [BN][SW] f16 each.
@@ -642,6 +655,69 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
                             accs[i][j] = floatx16{};
                         }
                 }
+            } else if constexpr (DT == NVFP4) {
+                // stage h2 = 64-blocks 2h2, 2h2 + 1; its chunk bl holds 16-element sub-blocks S = 8h2 + 2bl + ks
+                // (ks = 0, 1: the 32-block bl's two K-steps), 8 bytes each, byte u = elements u and u + 8. Lane half q
+                // takes bytes 4q..4q+3 of a sub-block: the hardware e2m1 conversion (scale 2: jam's codes kv) gives
+                // the pairs (u, u + 8), and one packed multiply applies the sub-block's UE4M3 scale d (kv·d has at
+                // most 6 significant bits and lies in [2^-10, 5760]: exact in f16). jam's F1 activation scale of the
+                // 32-block then comes in with one FMA per output, straight into acc (no group scale).
+                uint4 hdr[RT], chs[RT][4];
+                half8 bfs[4][CT][2];
+                float dxs[4][CT];
+    #pragma unroll
+                for (int i = 0; i < RT; i++) {
+                    hdr[i] = *reinterpret_cast<const uint4*>(buf + S::H_OFF + ((wave * RT + i) * 32 + r) * 16);
+    #pragma unroll
+                    for (int bl = 0; bl < 4; bl++)
+                        chs[i][bl] = *reinterpret_cast<const uint4*>(LA + ((wave * RT + i) * NCS + bl) * 512 + 16 * r);
+                }
+    #pragma unroll
+                for (int bl = 0; bl < 4; bl++)
+    #pragma unroll
+                    for (int j = 0; j < CA; j++) {
+    #pragma unroll
+                        for (int ks = 0; ks < 2; ks++)
+                            bfs[bl][j][ks] = *reinterpret_cast<const half8*>(LB + ((2 * bl + ks) * 2 + q) * BN * 16 + (32 * j + r) * 16);
+                        dxs[bl][j] = LDX[bl * BN + 32 * j + r];
+                    }
+                __builtin_amdgcn_sched_barrier(0);
+                if (st + 1 < nst) issue(st + 1, smem + ((st + 1) & 1) * S::BYTES);
+                floatx16 Dp[2][RT][CT];
+    #pragma unroll
+                for (int bl = 0; bl < 5; bl++) {
+                    if (bl < 4) {
+                        half8 af[RT][2];
+    #pragma unroll
+                        for (int i = 0; i < RT; i++) {
+                            const uint4 ch = chs[i][bl];
+    #pragma unroll
+                            for (int ks = 0; ks < 2; ks++) {
+                                const int sb = 8 * h2 + 2 * bl + ks;   // the sub-block's scale byte in the header
+                                const uint32_t sbyte = (word(hdr[i], sb >> 2) >> (8 * (sb & 3))) & 0xffu;
+                                const _Float16 d = (_Float16) ue4m3(sbyte);
+                                af[i][ks] = nv_frag(ks ? (q ? ch.w : ch.z) : (q ? ch.y : ch.x), d);
+                            }
+                        }
+    #pragma unroll
+                        for (int i = 0; i < RT; i++)
+    #pragma unroll
+                            for (int j = 0; j < CA; j++) {
+                                floatx16 D = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i][0], bfs[bl][j][0], floatx16{}, 0, 0, 0);
+                                Dp[bl & 1][i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i][1], bfs[bl][j][1], D, 0, 0, 0);
+                            }
+                    }
+                    if (bl > 0) {
+                        const int pb = bl - 1;
+    #pragma unroll
+                        for (int i = 0; i < RT; i++)
+    #pragma unroll
+                            for (int j = 0; j < CA; j++)
+    #pragma unroll
+                                for (int e = 0; e < 16; e++)
+                                    acc[i][j][e] = fmaf(Dp[pb & 1][i][j][e], dxs[pb][j], acc[i][j][e]);
+                    }
+                }
             } else {   // Q6_K: stage h2 = half h of the super-block, blocks j = 0..3 (elements 128h + 32j + l)
                 // every LDS read of the stage up front, then the next stage's copy, then the compute
                 uint4 ql[RT][2], qh[RT];
@@ -856,7 +932,7 @@ static hipError_t kq_go(const WeightView& w, const GemmAct& A, int m, int n, flo
 }
 
 size_t gemm_mma_split_floats(int dt, int k, int m, int n) {
-    if (dt != Q4_K && dt != Q5_K && dt != Q6_K && dt != MXFP4 && dt != Q4_0 && dt != Q8_0) return 0;
+    if (dt != Q4_K && dt != Q5_K && dt != Q6_K && dt != MXFP4 && dt != Q4_0 && dt != Q8_0 && dt != NVFP4) return 0;
     const int nrb = (m + 32 * MMA_WAVES - 1) / (32 * MMA_WAVES), ncb = (n + 63) / 64, nsb = (k + 255) / 256;
     int ns, sb_per;
     split_plan(nrb * ncb, nsb, &ns, &sb_per);
@@ -869,6 +945,7 @@ hipError_t launch_gemm_mma(int dt, const WeightView& w, const GemmAct& A, int k,
     switch (dt) {
     case Q4_K: return kq_go<Q4_K, 1, 2>(w, A, m, n, c, ldc, st, Groups{}, part, ep);
     case Q5_K: return kq_go<Q5_K, 1, 2>(w, A, m, n, c, ldc, st, Groups{}, part, ep);
+    case NVFP4: return kq_go<NVFP4, 1, 2>(w, A, m, n, c, ldc, st, Groups{}, part, ep);
     case Q4_0: return kq_go<Q4_0, 1, 2>(w, A, m, n, c, ldc, st, Groups{}, part, ep);
     case Q8_0: return kq_go<Q8_0, 1, 2>(w, A, m, n, c, ldc, st, Groups{}, part, ep);
     case Q6_K: return kq_go<Q6_K, 1, 2>(w, A, m, n, c, ldc, st, Groups{}, part, ep);

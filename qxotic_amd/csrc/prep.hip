@@ -285,13 +285,18 @@ JAMHIP_DEV int fused_scan(const PrepGroups& pg, bool pub, SlotOwner* so) {
 // 8h..8h+7 and 16+8h..16+8h+7: exactly the two (K-step, half) planes it stores.
 // MXO: the MXFP4 element order (the GEMM converts a weight byte's two nibbles, elements e and e + 16 of the
 // block, into one f16 pair): K-step 2·block + ks, half q, slot i holds element 8q + 4ks + i/2 + 16·(i % 2).
-template <int SK, bool MXO>
+// ORD: the element order of the codes inside a K-step, matching the weight operand the GEMM builds:
+//   0  elements 16q + 8ks + perm8(i)            (nibble / byte fields, Q4_K, Q5_K, Q6_K, Q4_0, Q8_0, Q1_0)
+//   1  pairs (e, e + 16) of the 32-block         (MXFP4: a weight byte's two e2m1 codes)
+//   2  pairs (u, u + 8) of each 16-element sub-block, K-step ks = sub-block ks of the block (NVFP4)
+// f1all: jam's F1 quantization for every slot (NVFP4, whose only jam path is F1 at every n, jam.c:662-668).
+template <int SK, int ORD>
 __global__ void __launch_bounds__(256) gemm_prep(const float* __restrict__ a, int lda, int n, int k, int Kp, int NP,
                                                  _Float16* __restrict__ bq, float* __restrict__ dx,
                                                  _Float16* __restrict__ shi, _Float16* __restrict__ slo,
                                                  float* __restrict__ es, const int* __restrict__ gmap,
                                                  const int* __restrict__ goff, const int* __restrict__ gpoff, int vec,
-                                                 PrepGroups pg) {
+                                                 PrepGroups pg, int f1all) {
     extern __shared__ float lsm[];   // [Kp/32] block scales, [Kp/16] per-16 sums, [4] wave maxima
     __shared__ int own[2];           // fused grouped mode: the slot's source row and its expert's row count
     float* ldb = lsm;
@@ -308,7 +313,7 @@ __global__ void __launch_bounds__(256) gemm_prep(const float* __restrict__ a, in
     const int t_end = min((x + 1) * P8, P);
     for (int t = x * P8 + (int) (blockIdx.x >> 3); t < t_end; t += nw) {
         // fused grouped mode (counts on the device): F1 codes for an expert of 1..7 rows, else F2
-        bool f1 = false;
+        bool f1 = f1all != 0;
         int src;
         if (pg.counts != nullptr) {
             if (so.a64 > 0 && t >= so.p64 && t < so.p64 + so.a64) {   // exactly one owner for t < P
@@ -317,7 +322,7 @@ __global__ void __launch_bounds__(256) gemm_prep(const float* __restrict__ a, in
             }
             __syncthreads();
             src = own[0];
-            f1 = own[1] < 8;
+            f1 = f1 || own[1] < 8;
         } else {
             src = prep_src(t, n, gmap, goff, gpoff);
         }
@@ -338,9 +343,22 @@ __global__ void __launch_bounds__(256) gemm_prep(const float* __restrict__ a, in
                     const int b = r0 + 128 * u;
 #pragma unroll
                     for (int i = 0; i < 16; i++) xr[u][i] = 0.0f;
-                    if (b < nbk) {
-                        // MXO: elements 8hh..8hh+7 and 16+8hh..16+8hh+7 (the order the GEMM pairs them in); else
+                    if (b < nbk && ORD == 2) {   // elements 4hh.., 8+4hh.., 16+4hh.., 24+4hh.. (4 each)
+                        const float* p0 = row + 32 * b + 4 * hh;
+#pragma unroll
+                        for (int v = 0; v < 4; v++) {
+                            if (vec) {
+                                const float4 f = *reinterpret_cast<const float4*>(p0 + 8 * v);
+                                xr[u][4 * v + 0] = f.x, xr[u][4 * v + 1] = f.y, xr[u][4 * v + 2] = f.z, xr[u][4 * v + 3] = f.w;
+                            } else {
+#pragma unroll
+                                for (int i = 0; i < 4; i++) xr[u][4 * v + i] = p0[8 * v + i];
+                            }
+                        }
+                    } else if (b < nbk) {
+                        // ORD 1: elements 8hh..8hh+7 and 16+8hh..16+8hh+7 (the order the GEMM pairs them in); else
                         // 16hh..16hh+15
+                        constexpr bool MXO = ORD == 1;
                         const float* p0 = row + 32 * b + (MXO ? 8 * hh : 16 * hh);
                         const float* p1 = p0 + (MXO ? 16 : 8);
                         if (vec) {   // a and lda 16-byte aligned (the launcher checks)
@@ -391,8 +409,10 @@ __global__ void __launch_bounds__(256) gemm_prep(const float* __restrict__ a, in
                         half8 hv;
 #pragma unroll
                         for (int i = 0; i < 8; i++) {
-                            if constexpr (!MXO) hv[perm8(i)] = (_Float16) qf[8 * ks + i];   // elements 16hh + 8ks + i
-                            else hv[2 * (i & 3) + (i >> 2)] = (_Float16) qf[8 * (i >> 2) + 4 * ks + (i & 3)];
+                            if constexpr (ORD == 0) hv[perm8(i)] = (_Float16) qf[8 * ks + i];   // elements 16hh + 8ks + i
+                            else if constexpr (ORD == 1) hv[2 * (i & 3) + (i >> 2)] = (_Float16) qf[8 * (i >> 2) + 4 * ks + (i & 3)];
+                            // ORD 2: slot 2j = element 16ks + 4hh + j, slot 2j + 1 = element 16ks + 4hh + 8 + j
+                            else hv[2 * (i & 3) + (i >> 2)] = (_Float16) qf[8 * ks + 4 * (i >> 2) + (i & 3)];
                         }
                         *reinterpret_cast<half8*>(bq + ((int64_t) (2 * (2 * b + ks) + hh) * NP + t) * 8) = hv;
                     }
@@ -489,23 +509,29 @@ static hipError_t prep_np(int dt, const float* a, int lda, int n, int NP, int k,
     if (NP <= 0) return hipSuccess;
     const int vec = ((reinterpret_cast<uintptr_t>(a) & 15) == 0 && (lda & 3) == 0) ? 1 : 0;
     const size_t lds = ((size_t) (Kp / 32) + (size_t) (Kp / 16) + 4) * sizeof(float);
-    const int kind = dt == MXFP4 ? 3 : sk;
+    const int kind = dt == MXFP4 ? 3 : dt == NVFP4 ? 4 : sk;
+    const int f1all = dt == NVFP4;
     // at most PREP_GRID workgroups (all resident), each looping over its XCD's slots
     const unsigned grid = (unsigned) (NP < PREP_GRID ? NP : PREP_GRID);
-    const void* fn = kind == 1 ? (const void*) gemm_prep<1, false> : kind == 2 ? (const void*) gemm_prep<2, false>
-                   : kind == 3 ? (const void*) gemm_prep<0, true> : (const void*) gemm_prep<0, false>;
+    const void* fn = kind == 1 ? (const void*) gemm_prep<1, 0> : kind == 2 ? (const void*) gemm_prep<2, 0>
+                   : kind == 3 ? (const void*) gemm_prep<0, 1> : kind == 4 ? (const void*) gemm_prep<0, 2>
+                   : (const void*) gemm_prep<0, 0>;
     // the LDS limit is raised once per kernel; threads racing here both set the same value
-    static std::atomic<bool> attr[4];
+    static std::atomic<bool> attr[5];
     if (!attr[kind].load(std::memory_order_acquire)) {
         const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
                                                  (int) ((PREP_MAX_KP / 32 + PREP_MAX_KP / 16 + 4) * sizeof(float)));
         if (e != hipSuccess) return e;
         attr[kind].store(true, std::memory_order_release);
     }
-    if (kind == 1) gemm_prep<1, false><<<grid, 256, lds, st>>>(a, lda, n, k, Kp, NP, bq, dx, shi, slo, es, gmap, goff, gpoff, vec, pg);
-    else if (kind == 2) gemm_prep<2, false><<<grid, 256, lds, st>>>(a, lda, n, k, Kp, NP, bq, dx, shi, slo, es, gmap, goff, gpoff, vec, pg);
-    else if (kind == 3) gemm_prep<0, true><<<grid, 256, lds, st>>>(a, lda, n, k, Kp, NP, bq, dx, shi, slo, es, gmap, goff, gpoff, vec, pg);
-    else gemm_prep<0, false><<<grid, 256, lds, st>>>(a, lda, n, k, Kp, NP, bq, dx, shi, slo, es, gmap, goff, gpoff, vec, pg);
+#define JAMHIP_PREP(SK, ORD) gemm_prep<SK, ORD><<<grid, 256, lds, st>>>(a, lda, n, k, Kp, NP, bq, dx, shi, slo, es, gmap, \
+                                                                   goff, gpoff, vec, pg, f1all)
+    if (kind == 1) JAMHIP_PREP(1, 0);
+    else if (kind == 2) JAMHIP_PREP(2, 0);
+    else if (kind == 3) JAMHIP_PREP(0, 1);
+    else if (kind == 4) JAMHIP_PREP(0, 2);
+    else JAMHIP_PREP(0, 0);
+#undef JAMHIP_PREP
     return hipGetLastError();
 }
 
