@@ -269,7 +269,7 @@ bool lookup(jamhip_ctx* ctx, const void* w, int dt, int ldw, int m, WeightView* 
 
 // Upload `rows` raw host rows (stride raw_stride bytes, rb blocks used per row) into a device-layout
 // buffer of G groups per row at dst (plane 0) / dst_sc (plane 1) via a staging copy and the repack kernel.
-// The repack also leaves the fold flag (launch_repack) in ctx->fold for Q8_0 / Q4_0 / MXFP4; *flag gets its
+// The repack also leaves the fold flag (launch_repack) in ctx->fold for Q8_0 / Q4_0 / MXFP4 / Q1_0; *flag gets its
 // device address then (null otherwise).
 jamhip_status upload(jamhip_ctx* ctx, const uint8_t* host, int dt, int64_t raw_stride, int64_t rows, int64_t rb,
                      int64_t G, uint8_t* dst, uint8_t* dst_sc, const int** flag) {
@@ -277,7 +277,7 @@ jamhip_status upload(jamhip_ctx* ctx, const uint8_t* host, int dt, int64_t raw_s
     hipError_t e;
     if ((e = ctx->w_raw.ensure((size_t) span)) != hipSuccess) return hip_fail(ctx, e, "weight staging alloc");
     int* fl = nullptr;
-    if (dt == Q8_0 || dt == Q4_0 || dt == MXFP4) {
+    if (dt == Q8_0 || dt == Q4_0 || dt == MXFP4 || dt == Q1_0) {
         if ((e = ctx->fold.ensure(sizeof(int))) != hipSuccess) return hip_fail(ctx, e, "fold flag alloc");
         fl = (int*) ctx->fold.p;
     }
@@ -326,18 +326,18 @@ bool env_true(const char* name) {
     return v && (!strcmp(v, "1") || !strcasecmp(v, "true") || !strcasecmp(v, "yes"));
 }
 
-// The matrix-core GEMM covers Q4_K, Q5_K, Q6_K (k a multiple of 256), MXFP4, NVFP4, Q4_0 and Q8_0 on
+// The matrix-core GEMM covers Q4_K, Q5_K, Q6_K (k a multiple of 256), MXFP4, NVFP4, Q4_0, Q8_0 and Q1_0 on
 // 32-row-aligned views (launch_gemm_mma), for k up to the activation prep's limit (gemm_prep_fits).
 bool mma_path(int dt, int k, const WeightView& wv) {
     if (env_true("JAM_HIP_NO_MMA")) return false;
     return (((dt == Q4_K || dt == Q5_K || dt == Q6_K) && k % 256 == 0) || dt == MXFP4 || dt == NVFP4 || dt == Q4_0 ||
-            dt == Q8_0) &&
+            dt == Q8_0 || dt == Q1_0) &&
            (wv.r0 & 31) == 0 && gemm_prep_fits(k);
 }
 
-// mma_path for jam's semantics: also every group of W must fold its block scales exactly (Q8_0, Q4_0, MXFP4;
-// repack_kernel). A copy staged by this call has its flag read here, once (a synchronize), and only when the
-// call would otherwise take the matrix cores.
+// mma_path for jam's semantics: also every group of W must fold its block scales exactly (Q8_0, Q4_0, MXFP4,
+// Q1_0; repack_kernel). A copy staged by this call has its flag read here, once (a synchronize), and only
+// when the call would otherwise take the matrix cores.
 bool mma_exact(jamhip_ctx* ctx, int dt, int k, WeightView& wv) {
     if (!mma_path(dt, k, wv)) return false;
     if (wv.fold_flag != nullptr) {
@@ -360,7 +360,7 @@ bool mma_exact(jamhip_ctx* ctx, int dt, int k, WeightView& wv) {
 static int mma_min_n(int dt, int m, int k) {
     const char* v = getenv("JAM_HIP_MMA_MIN_N");
     if (v) return atoi(v) < 8 ? 8 : atoi(v);
-    if ((int64_t) m * k <= (int64_t) 17 << 20) return dt == Q4_0 || dt == Q4_K || dt == Q5_K || dt == Q6_K ? 33 : 17;
+    if ((int64_t) m * k <= (int64_t) 17 << 20) return dt == Q4_0 || dt == Q4_K || dt == Q5_K || dt == Q6_K || dt == Q1_0 ? 33 : 17;
     return k > 8192 ? 16 : 9;
 }
 

@@ -119,6 +119,15 @@ JAMHIP_DEV half8 mx_frag(uint32_t w, float scale) {
     return half8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
 }
 
+// Q1_0: 8 f16 of one K-step from one byte of sign bits, bit j = element j of the run, each as 2^-14 (the
+// smallest normal f16, bit 10) or 0, in the frag8 pair order (bits 0,2), (1,3), (4,6), (5,7): with x = B | B << 14
+// bit j sits at j and j + 14, so x << (10 - j0) puts bits j0 and j0 + 2 at bits 10 and 26.
+JAMHIP_DEV half8 q1_frag(uint32_t b) {
+    const uint32_t x = b | (b << 14), m = 0x04000400u;
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    return __builtin_bit_cast(half8, u32x4{(x << 10) & m, (x << 9) & m, (x << 6) & m, (x << 5) & m});
+}
+
 // NVFP4: 8 f16 of one K-step from one word (bytes 4q..4q+3 of a 16-element sub-block): byte u's two codes are
 // elements u and u + 8 (jam_kernels_generic.c:128-131), converted with scale 2 (jam's integer codes kv, 0..12)
 // and multiplied by the sub-block's scale d: slots 2j, 2j + 1 = elements 4q + j, 4q + j + 8 (GemmAct order 2).
@@ -137,10 +146,11 @@ JAMHIP_DEV half8 nv_frag(uint32_t w, _Float16 d) {
 // block scales [4][BN] f32, sums hi/lo [BN][SW] f16 each.
 template <int DT, int RT, int CT> struct Stage {
     static constexpr int TW = MMA_WAVES * RT, BN = 32 * CT;
-    // chunks per stage (Q6_K: 4 ql, 2 qh, scales; Q5_K: 4 nibble chunks, then the super-block's 2 qh chunks)
-    static constexpr int NCS = DT == Q6_K ? 7 : DT == Q8_0 ? 8 : DT == Q5_K ? 6 : 4;
-    static constexpr int HB = DT == Q6_K ? 2 : 16;           // header bytes per row (Q6_K: d)
-    static constexpr int SW = DT == Q4_K || DT == Q5_K || DT == Q4_0 ? 8 : DT == Q6_K ? 16 : 0;   // sums per token per group
+    // chunks per stage (Q6_K: 4 ql, 2 qh, scales; Q5_K: 4 nibble chunks, then the super-block's 2 qh chunks;
+    // Q1_0: the 128-block's 16 sign bytes)
+    static constexpr int NCS = DT == Q6_K ? 7 : DT == Q8_0 ? 8 : DT == Q5_K ? 6 : DT == Q1_0 ? 1 : 4;
+    static constexpr int HB = DT == Q6_K ? 2 : DT == Q1_0 ? 4 : 16;   // header bytes per row (Q6_K: d; Q1_0: 2 d)
+    static constexpr int SW = DT == Q4_K || DT == Q5_K || DT == Q4_0 || DT == Q1_0 ? 8 : DT == Q6_K ? 16 : 0;   // sums per token per group
     static constexpr int A_OFF = 0;
     static constexpr int H_OFF = A_OFF + TW * NCS * 512;
     static constexpr int B_OFF = (H_OFF + TW * 32 * HB + 1023) / 1024 * 1024;
@@ -216,7 +226,10 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
     const int a_dst = S::A_OFF + wave * NCS * 512;
     // headers: Q4_K / MXFP4 16 B per row, tiles 2·wave + q (waves 0, 1); Q6_K d, 8 rows per lane (wave 0)
     const uint8_t* h_src;
-    if constexpr (DT != Q6_K) {
+    if constexpr (DT == Q1_0) {   // 4 B per row: lanes 0..31 of wave 0 copy 16 B each, tile lane / 8
+        const int64_t T = T0 + (lane >> 3) < tiles ? T0 + (lane >> 3) : tiles - 1;
+        h_src = w.sc + (r0t + T) * G * 128 + (lane & 7) * 16;
+    } else if constexpr (DT != Q6_K) {
         const int64_t T = T0 + 2 * (wave & 1) + q < tiles ? T0 + 2 * (wave & 1) + q : tiles - 1;
         h_src = w.sc + ((r0t + T) * G * 32 + r) * 16;
     } else {
@@ -235,7 +248,9 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
     auto issue = [&](int st, unsigned char* buf) {
         const int g = st >> 1, h2 = st & 1;
         const uint8_t* ag = a_src + (int64_t) g * (NC * CHUNK_STRIDE);
-        if constexpr (DT == Q5_K) {   // nibble chunks 4h2..4h2+3 as Q4_K, then the qh chunks 8, 9
+        if constexpr (DT == Q1_0) {   // chunk h2 (512 B: lanes 0..31)
+            if (lane < 32) dma16(ag + h2 * CHUNK_STRIDE, buf + a_dst);
+        } else if constexpr (DT == Q5_K) {   // nibble chunks 4h2..4h2+3 as Q4_K, then the qh chunks 8, 9
 #pragma unroll
             for (int p = 0; p < 2; p++) dma16(ag + (4 * h2 + 2 * p) * CHUNK_STRIDE, buf + a_dst + 2 * p * 512);
             dma16(ag + 8 * CHUNK_STRIDE, buf + a_dst + 4 * 512);
@@ -261,7 +276,9 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
                 for (int p = 0; p < 2; p++)
                     dma16(bs + kl * b_kstep + p * (b_kstep / 2), buf + S::B_OFF + (2 * (2 * wave + kl) + p) * 1024);
         }
-        if constexpr (DT != Q6_K) {
+        if constexpr (DT == Q1_0) {
+            if (wave == 0 && lane < 32) dma16(h_src + (int64_t) g * 128, buf + S::H_OFF);
+        } else if constexpr (DT != Q6_K) {
             if (wave < 2) dma16(h_src + (int64_t) g * 32 * 16, buf + S::H_OFF + wave * 1024);
         } else {
             if (wave == 0 && h2 == 1 && lane < 4 * TW) dma16(h_src + (int64_t) g * 32 * 2, buf + S::H_OFF);
@@ -272,7 +289,7 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
         // sums: Q4_K needs them at the super-block's end (odd stage), Q6_K at its start (even stage); a plane's
         // piece p holds tokens 32p.. (two pieces) or a token per lane (one piece)
         if constexpr (S::SW > 0) {
-            if ((DT == Q4_0 || (DT == Q4_K || DT == Q5_K) == (h2 == 1)) && (SPC == 2 || wave == 1 || wave == 3) &&
+            if ((DT == Q4_0 || DT == Q1_0 || (DT == Q4_K || DT == Q5_K) == (h2 == 1)) && (SPC == 2 || wave == 1 || wave == 3) &&
                 (!half || (SPC == 2 ? s_p == 0 : lane < 32)))
                 dma16(s_src + (int64_t) g * A.NP * SWB, buf + S::S_OFF + s_pl * BN * SWB + s_p * 1024);
         }
@@ -655,6 +672,98 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
                             accs[i][j] = floatx16{};
                         }
                 }
+            } else if constexpr (DT == Q1_0) {
+                // stage h2 = 128-block h2 of the group (one chunk of sign bits, d = the row's fp16 d[h2]). jam's F2
+                // decomposition per 32-block (q1_0_block16, jam_kernels_q4k_avx512.c:580-598): fl(d·fl(2·dx))·
+                // Σbit·xq − d·fl(xs0 + xs1). The bits go to the matrix cores as the f16 2^-14 (normal) or 0, so a
+                // block's MFMA result is 2^-14·Σbit·xq exactly; one FMA per output applies 2·dx into accs,
+                // 2^14·d comes in once per stage, and the −d·sums term runs on the matrix cores at the
+                // group's end (A' = −d of each block's 128-block against the sums' hi and lo parts).
+                const bool gend = h2 == 1 || st == nstk - 1;
+                uint32_t dh[RT];   // row r's two fp16 d
+                uint4 chs[RT];
+                half8 bfs[4][CT][2];
+                float dxs[4][CT];
+                half4 shi[CT], slo[CT];
+    #pragma unroll
+                for (int i = 0; i < RT; i++) {
+                    dh[i] = *reinterpret_cast<const uint32_t*>(buf + S::H_OFF + (wave * RT + i) * 128 + r * 4);
+                    chs[i] = *reinterpret_cast<const uint4*>(LA + (wave * RT + i) * NCS * 512 + 16 * r);
+                }
+    #pragma unroll
+                for (int bl = 0; bl < 4; bl++)
+    #pragma unroll
+                    for (int j = 0; j < CA; j++) {
+    #pragma unroll
+                        for (int ks = 0; ks < 2; ks++)
+                            bfs[bl][j][ks] = *reinterpret_cast<const half8*>(LB + ((2 * bl + ks) * 2 + q) * BN * 16 + (32 * j + r) * 16);
+                        dxs[bl][j] = LDX[bl * BN + 32 * j + r] * 2.0f;   // 2·dx, exact
+                    }
+                float dds[RT][16];   // 2^14·d[h2] of the 16 output rows this lane holds (exact, finite)
+    #pragma unroll
+                for (int i = 0; i < RT; i++) {
+                    const unsigned char* H = buf + S::H_OFF + (wave * RT + i) * 128 + 2 * h2;
+    #pragma unroll
+                    for (int e = 0; e < 16; e++)
+                        dds[i][e] = 16384.0f * h2f_bits(*reinterpret_cast<const uint16_t*>(H + (8 * (e >> 2) + 4 * q + (e & 3)) * 4));
+                }
+                if (gend) {
+    #pragma unroll
+                    for (int j = 0; j < CA; j++) {
+                        const unsigned char* SP = buf + S::S_OFF + (32 * j + r) * 16 + 8 * q;
+                        shi[j] = *reinterpret_cast<const half4*>(SP);
+                        slo[j] = *reinterpret_cast<const half4*>(SP + BN * 16);
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                if (st + 1 < nst) issue(st + 1, smem + ((st + 1) & 1) * S::BYTES);
+                floatx16 Dp[2][RT][CT];
+    #pragma unroll
+                for (int bl = 0; bl < 5; bl++) {
+                    if (bl < 4) {
+                        half8 af[RT][2];
+    #pragma unroll
+                        for (int i = 0; i < RT; i++)
+    #pragma unroll
+                            for (int ks = 0; ks < 2; ks++)   // elements 16q + 8ks + j: byte 4bl + 2q + ks, bit j
+                                af[i][ks] = q1_frag((word(chs[i], bl) >> (8 * (2 * q + ks))) & 0xffu);
+    #pragma unroll
+                        for (int i = 0; i < RT; i++)
+    #pragma unroll
+                            for (int j = 0; j < CA; j++) {
+                                floatx16 D = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i][0], bfs[bl][j][0], floatx16{}, 0, 0, 0);
+                                Dp[bl & 1][i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i][1], bfs[bl][j][1], D, 0, 0, 0);
+                            }
+                    }
+                    if (bl > 0) {
+                        const int pb = bl - 1;
+    #pragma unroll
+                        for (int i = 0; i < RT; i++)
+    #pragma unroll
+                            for (int j = 0; j < CA; j++)
+    #pragma unroll
+                                for (int e = 0; e < 16; e++)
+                                    accs[i][j][e] = fmaf(Dp[pb & 1][i][j][e], dxs[pb][j], accs[i][j][e]);
+                    }
+                }
+    #pragma unroll
+                for (int i = 0; i < RT; i++) {   // stage end: acc += d·accs; group end: acc −= Σ_b d_b·sums_b
+    #pragma unroll
+                    for (int j = 0; j < CA; j++) {
+    #pragma unroll
+                        for (int e = 0; e < 16; e++) acc[i][j][e] = fmaf(dds[i][e], accs[i][j][e], acc[i][j][e]);
+                        accs[i][j] = floatx16{};
+                    }
+                    if (gend) {
+                        const _Float16 nd = -__builtin_bit_cast(_Float16, (uint16_t) (dh[i] >> (16 * q)));
+                        const half4 a8 = {nd, nd, nd, nd};   // blocks 4q..4q+3 of the group: 128-block q
+    #pragma unroll
+                        for (int j = 0; j < CA; j++) {
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(a8, shi[j], acc[i][j], 0, 0, 0);
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(a8, slo[j], acc[i][j], 0, 0, 0);
+                        }
+                    }
+                }
             } else if constexpr (DT == NVFP4) {
                 // stage h2 = 64-blocks 2h2, 2h2 + 1; its chunk bl holds 16-element sub-blocks S = 8h2 + 2bl + ks
                 // (ks = 0, 1: the 32-block bl's two K-steps), 8 bytes each, byte u = elements u and u + 8. Lane half q
@@ -932,7 +1041,8 @@ static hipError_t kq_go(const WeightView& w, const GemmAct& A, int m, int n, flo
 }
 
 size_t gemm_mma_split_floats(int dt, int k, int m, int n) {
-    if (dt != Q4_K && dt != Q5_K && dt != Q6_K && dt != MXFP4 && dt != Q4_0 && dt != Q8_0 && dt != NVFP4) return 0;
+    if (dt != Q4_K && dt != Q5_K && dt != Q6_K && dt != MXFP4 && dt != Q4_0 && dt != Q8_0 && dt != NVFP4 && dt != Q1_0)
+        return 0;
     const int nrb = (m + 32 * MMA_WAVES - 1) / (32 * MMA_WAVES), ncb = (n + 63) / 64, nsb = (k + 255) / 256;
     int ns, sb_per;
     split_plan(nrb * ncb, nsb, &ns, &sb_per);
@@ -946,6 +1056,7 @@ hipError_t launch_gemm_mma(int dt, const WeightView& w, const GemmAct& A, int k,
     case Q4_K: return kq_go<Q4_K, 1, 2>(w, A, m, n, c, ldc, st, Groups{}, part, ep);
     case Q5_K: return kq_go<Q5_K, 1, 2>(w, A, m, n, c, ldc, st, Groups{}, part, ep);
     case NVFP4: return kq_go<NVFP4, 1, 2>(w, A, m, n, c, ldc, st, Groups{}, part, ep);
+    case Q1_0: return kq_go<Q1_0, 1, 2>(w, A, m, n, c, ldc, st, Groups{}, part, ep);
     case Q4_0: return kq_go<Q4_0, 1, 2>(w, A, m, n, c, ldc, st, Groups{}, part, ep);
     case Q8_0: return kq_go<Q8_0, 1, 2>(w, A, m, n, c, ldc, st, Groups{}, part, ep);
     case Q6_K: return kq_go<Q6_K, 1, 2>(w, A, m, n, c, ldc, st, Groups{}, part, ep);

@@ -99,6 +99,9 @@ __global__ void __launch_bounds__(256) repack_kernel(const uint8_t* __restrict__
             ds[2 * j] = in ? b[0] : 0;
             ds[2 * j + 1] = in ? b[1] : 0;
             for (int t = 0; t < 16; t++) chunk(j)[t] = in ? b[2 + t] : 0;
+            // a non-finite d keeps the tensor off the matrix cores, whose per-stage order of d's products
+            // would turn jam's per-block Inf/NaN pattern into a different one
+            if (flag != nullptr && (ds[2 * j + 1] & 0x7C) == 0x7C) atomicOr(flag, 1);
         }
     } else if constexpr (DT == Q6_K) {                 // ql @0..127, qh @128..191, scales @192..207, d @208
         const uint8_t* b = row + g * 210;
@@ -180,7 +183,7 @@ __global__ void flag_clear_kernel(int* flag) { *flag = 0; }
 // dequantization builds f16 pairs from bytes (0,2), (1,3), (4,6), (5,7) of two 32-bit words.
 JAMHIP_DEV int perm8(int j) { return j == 1 ? 2 : j == 2 ? 1 : j == 5 ? 6 : j == 6 ? 5 : j; }
 
-int gemm_sums_kind(int dt) { return dt == Q4_K || dt == Q5_K || dt == Q4_0 ? 1 : dt == Q6_K ? 2 : 0; }
+int gemm_sums_kind(int dt) { return dt == Q4_K || dt == Q5_K || dt == Q4_0 || dt == Q1_0 ? 1 : dt == Q6_K ? 2 : 0; }
 
 // A workgroup takes one token slot at a time (256 threads, a thread per 16-element half of a block, 128
 // blocks per round; at most PREP_GRID workgroups, each looping over its XCD's share of the slots that hold
@@ -606,13 +609,13 @@ hipError_t launch_repack(int dt, const uint8_t* raw, int64_t raw_stride, int64_t
                                                                           qs);
         return hipGetLastError();
     }
-    if (flag != nullptr && (dt == Q8_0 || dt == Q4_0 || dt == MXFP4)) flag_clear_kernel<<<1, 1, 0, st>>>(flag);
+    if (flag != nullptr && (dt == Q8_0 || dt == Q4_0 || dt == MXFP4 || dt == Q1_0)) flag_clear_kernel<<<1, 1, 0, st>>>(flag);
     const int64_t n = tiled_rows(rows) * G;
     const dim3 grid((unsigned) ((n + 255) / 256));
     switch (dt) {
     case Q5_K: repack_kernel<Q5_K><<<grid, 256, 0, st>>>(raw, raw_stride, rows, rb, G, qs, sc, nullptr); break;
     case NVFP4: repack_kernel<NVFP4><<<grid, 256, 0, st>>>(raw, raw_stride, rows, rb, G, qs, sc, nullptr); break;
-    case Q1_0: repack_kernel<Q1_0><<<grid, 256, 0, st>>>(raw, raw_stride, rows, rb, G, qs, sc, nullptr); break;
+    case Q1_0: repack_kernel<Q1_0><<<grid, 256, 0, st>>>(raw, raw_stride, rows, rb, G, qs, sc, flag); break;
     case Q8_0: repack_kernel<Q8_0><<<grid, 256, 0, st>>>(raw, raw_stride, rows, rb, G, qs, sc, flag); break;
     case Q4_0: repack_kernel<Q4_0><<<grid, 256, 0, st>>>(raw, raw_stride, rows, rb, G, qs, sc, flag); break;
     case MXFP4: repack_kernel<MXFP4><<<grid, 256, 0, st>>>(raw, raw_stride, rows, rb, G, qs, sc, flag); break;

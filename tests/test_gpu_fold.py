@@ -1,4 +1,4 @@
-"""GPU: block-scale edges of Q8_0 / Q4_0 / MXFP4 on every path, and jam's Q8_0 saturation suites.
+"""GPU: block-scale edges of Q8_0 / Q4_0 / MXFP4 / Q1_0 on every path, and jam's Q8_0 saturation suites.
 
 The matrix-core GEMM folds each block's scale into an f16 weight operand relative to a per-group reference
 (qxotic_amd/csrc/mma.hip); the repack (qxotic_amd/csrc/prep.hip, repack_kernel) keeps blocks whose products
@@ -360,3 +360,67 @@ def test_adversarial_suite(hip, oracle, dt, k, monkeypatch):
         got = mm_host(hip, dt, w, B, m, n, k)
         assert np.isfinite(got).all()
         assert (got[0] == 0.0).all()
+
+
+def q1_block(d_bits, rng):
+    """One Q1_0 block (18 bytes): the fp16 d, then 128 random sign bits (jam_q1_0.h)."""
+    return np.concatenate([np.array([d_bits & 0xFF, d_bits >> 8], np.uint8), rng.integers(0, 256, 16, np.uint8)])
+
+
+def test_q1_0_scales_every_path(hip, oracle, monkeypatch):
+    """Q1_0 (one fp16 d per 128 elements, each element +d or -d): d subnormal, at the smallest normal, at the
+    fp16 maximum, zero and negative beside ordinary d in one row. The matrix cores apply 2^14·d in f32 once
+    per block and -d as an f16 operand of the sums term, so every finite d takes them and stays at the error
+    floor; a non-finite d (+-Inf, NaN) flags the tensor, which then gives the F2 decode kernel's bits and is
+    non-finite where jam's result is. Decode (n = 1, 3), the F2 decode kernel (n = 12) and the matrix cores
+    (n = 40), staged and pinned."""
+    from qxotic_amd.jam import JAM, Segment
+    m, k = 64, 512
+    special = [0x0001, 0x03FF, 0x0400, 0x7BFF, 0x0000, 0x8001, 0xFBFF, 0x8400]
+    nonfinite = [0x7C00, 0xFC00, 0x7E00]
+    for flagged in (False, True):
+        rng = np.random.default_rng(0x0110 + flagged)
+        rows = []
+        for r in range(m):
+            ds = [int(np.float16(rng.uniform(0.01, 0.03) * rng.choice([-1, 1])).view(np.uint16)) for _ in range(4)]
+            if r < 2 * len(special):
+                ds[r % 4] = special[r % len(special)]
+            if flagged and r < len(nonfinite):
+                ds[1] = nonfinite[r]
+            rows.append(np.concatenate([q1_block(d, rng) for d in ds]))
+        w = np.ascontiguousarray(np.stack(rows))
+        tag = f"Q1_0 {'with non-finite d' if flagged else 'finite d'}"
+        for n, force in ((1, None), (3, None), (12, "100000"), (40, "8")):
+            for an, a in activation_sets(oracle, n, k, 0x1F0 + n).items():
+                say(f"q1_0 scales {tag} n={n} mma_min_n={force} acts={an}")
+                if force:
+                    monkeypatch.setenv("JAM_HIP_MMA_MIN_N", force)
+                else:
+                    monkeypatch.delenv("JAM_HIP_MMA_MIN_N", raising=False)
+                with np.errstate(all="ignore"):
+                    ref = oracle.mm_int8(O.Q1_0, w, a, m, n, k)
+                    _, sa = oracle.mm_ref(O.Q1_0, w, a, m, n, k)
+                got = mm_host(hip, O.Q1_0, w, a, m, n, k)
+                check(got, ref, sa, (tag, n, an), None if flagged or n != 40 else list(range(m)))
+                if n == 40 and an == "A":
+                    monkeypatch.setenv("JAM_HIP_NO_MMA", "1")
+                    f2 = mm_host(hip, O.Q1_0, w, a, m, n, k)
+                    monkeypatch.delenv("JAM_HIP_NO_MMA")
+                    assert np.array_equal(bits(got), bits(f2)) == flagged, (tag, "routing")
+        assert hip.pin(Segment.of(w), O.Q1_0, k, m) == JAM.OK, hip.last_error()
+        try:
+            monkeypatch.setenv("JAM_HIP_MMA_MIN_N", "8")
+            a = oracle.normal(0x1F7, (40, k))
+            say(f"q1_0 scales {tag} pinned n=40")
+            got = mm_host(hip, O.Q1_0, w, a, m, 40, k)
+            with np.errstate(all="ignore"):
+                ref = oracle.mm_int8(O.Q1_0, w, a, m, 40, k)
+                _, sa = oracle.mm_ref(O.Q1_0, w, a, m, 40, k)
+            check(got, ref, sa, (tag, "pinned"), None if flagged else list(range(m)))
+            monkeypatch.setenv("JAM_HIP_NO_MMA", "1")
+            f2 = mm_host(hip, O.Q1_0, w, a, m, 40, k)
+            monkeypatch.delenv("JAM_HIP_NO_MMA")
+            assert np.array_equal(bits(got), bits(f2)) == flagged, (tag, "pinned routing")
+        finally:
+            monkeypatch.delenv("JAM_HIP_MMA_MIN_N", raising=False)
+            assert hip.evict(Segment.of(w)) == JAM.OK

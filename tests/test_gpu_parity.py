@@ -16,7 +16,7 @@ from oracle import oracle as O
 pytestmark = pytest.mark.gpu
 
 SHAPES = [(104, 1024), (100, 512), (70, 256), (64, 768)]   # JamBackendParityTest.java:204-252
-MMA_TYPES = O.QUANT_TYPES + (O.Q5_K, O.NVFP4)               # the types the matrix-core GEMM covers
+MMA_TYPES = O.QUANT_TYPES + (O.Q5_K, O.NVFP4, O.Q1_0)       # the types the matrix-core GEMM covers
 NS = [1, 2, 3, 4, 7, 8, 13, 16, 17, 32, 33, 64, 100]
 
 
@@ -342,7 +342,8 @@ def test_decode_fused_prologue_matches_quantized_copy(hip, oracle, dt):
 
 
 # ------------------------------------------------------------------------------------ prefill GEMM
-PREFILL = [(O.Q4_K, 14336, 4096), (O.Q6_K, 4096, 14336), (O.Q5_K, 14336, 4096), (O.NVFP4, 14336, 4096)]
+PREFILL = [(O.Q4_K, 14336, 4096), (O.Q6_K, 4096, 14336), (O.Q5_K, 14336, 4096), (O.NVFP4, 14336, 4096),
+           (O.Q1_0, 14336, 4096)]
 
 
 @pytest.mark.parametrize("dt,m,k", PREFILL)
@@ -383,7 +384,7 @@ def test_prefill_ragged_shapes(hip, oracle, dt):
         assert tier1(got, ref, sa).all(), (O.NAMES[dt], m, n, k)
 
 
-@pytest.mark.parametrize("dt", [O.Q4_K, O.Q5_K, O.Q6_K, O.MXFP4, O.NVFP4, O.Q8_0, O.Q4_0])
+@pytest.mark.parametrize("dt", [O.Q4_K, O.Q5_K, O.Q6_K, O.MXFP4, O.NVFP4, O.Q8_0, O.Q4_0, O.Q1_0])
 def test_prefill_tail_split_tiles(hip, oracle, dt):
     """Grids whose last partial round of tiles runs as half tiles: 1024 rows x 65 slot blocks give 65 tiles per
     XCD, one of them split into two 32-token workgroups. Every token's result equals that of the n = 4096 grid
