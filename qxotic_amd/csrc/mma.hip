@@ -830,7 +830,7 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
             } else {   // Q6_K: stage h2 = half h of the super-block, blocks j = 0..3 (elements 128h + 32j + l)
                 // every LDS read of the stage up front, then the next stage's copy, then the compute
                 uint4 ql[RT][2], qh[RT];
-                int8_t scl[RT][4];
+                int scl[RT][4];
                 uint2 sco[RT];             // h2 = 0: the 8 scales of row r's 16-groups 8q..8q+7 (offset term)
                 half8 bhi[CT], blo[CT];    // h2 = 0: the sums' fragments
                 half8 bfs[4][CT][2];
@@ -841,10 +841,16 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
                     ql[i][0] = *reinterpret_cast<const uint4*>(T + (0 + q) * 512);
                     ql[i][1] = *reinterpret_cast<const uint4*>(T + (2 + q) * 512);
                     qh[i] = *reinterpret_cast<const uint4*>(T + (4 + q) * 512);
-                    const int8_t* sc16 = reinterpret_cast<const int8_t*>(T + 6 * 512);
+                    // the row's 16 int8 scales in one 16-byte read (the 32 rows' reads are 512 contiguous bytes;
+                    // byte reads at a 16-byte stride would conflict 4 ways), then the bytes this stage needs:
+                    // scale 8h2 + 2jb + q (word 2h2 + jb/2, byte 2(jb % 2) + q) and, at h2 = 0, words 2q, 2q + 1
+                    const uint4 sv = *reinterpret_cast<const uint4*>(T + 6 * 512);
     #pragma unroll
-                    for (int jb = 0; jb < 4; jb++) scl[i][jb] = sc16[8 * h2 + 2 * jb + q];
-                    if (h2 == 0) sco[i] = *reinterpret_cast<const uint2*>(sc16 + 8 * q);
+                    for (int jb = 0; jb < 4; jb++) {
+                        const uint32_t wv = jb < 2 ? (h2 ? sv.z : sv.x) : (h2 ? sv.w : sv.y);
+                        scl[i][jb] = __builtin_amdgcn_sbfe(wv, 8 * (2 * (jb & 1) + q), 8);
+                    }
+                    sco[i] = q ? make_uint2(sv.z, sv.w) : make_uint2(sv.x, sv.y);
                 }
                 if (h2 == 0) {
     #pragma unroll
