@@ -421,7 +421,19 @@ jamhip_status compute(jamhip_ctx* ctx, Scratch& sc, int dt, WeightView wv, const
         if (pf == 0) return hipSuccess;
         return sc.get(ctx->part, pf * sizeof(float), (void**) &gpart);
     };
-    if (is_dense(dt)) {   // jam's dense paths: no activation quantization, no scratch
+    if (is_dense(dt)) {   // jam's dense paths: no activation quantization
+        if (dense_mma_planes(dt, n, k) > 0) {   // the staged matrix-core GEMM: operand-ordered activations
+            void* dact = nullptr;
+            float* part = nullptr;
+            if ((e = sc.get(ctx->gact, dense_act_bytes(dt, n, k), &dact)) != hipSuccess)
+                return scratch_fail(ctx, sc, e, "dense activation scratch");
+            if (const size_t pf = dense_mma_split_floats(dt, k, m, n))
+                if ((e = sc.get(ctx->part, pf * sizeof(float), (void**) &part)) != hipSuccess)
+                    return scratch_fail(ctx, sc, e, "dense split scratch");
+            if ((e = launch_dense_mma(dt, wv, a, lda, k, m, n, c, ldc, dact, part, ctx->stream, ep)) != hipSuccess)
+                return hip_fail(ctx, e, "dense gemm launch");
+            return JAMHIP_OK;
+        }
         if ((e = launch_dense(dt, wv, a, lda, k, m, n, c, ldc, ctx->stream, ep)) != hipSuccess)
             return hip_fail(ctx, e, "dense launch");
         return JAMHIP_OK;

@@ -161,6 +161,17 @@ hipError_t launch_mx_gemm_grouped(int mode, const WeightView& w, const MxAct& A,
 // WeightView::G = the pitch).
 hipError_t launch_dense(int dt, const WeightView& w, const float* a, int lda, int k, int m, int n, float* c, int ldc,
                         hipStream_t st, const Epi& ep = Epi{});
+// From DENSE_MMA_MIN_N tokens (from 2 where the staged GEMV's activation tile would not fit LDS) F16, and BF16
+// where jam rounds the activations to bf16, take the staged matrix-core GEMM instead
+// (dense_mma_planes(dt, n, k) > 0): scratch of dense_act_bytes(dt, n, k) bytes for
+// the operand-ordered activations, and dense_mma_split_floats(dt, k, m, n) floats of split-K partials
+// (nullptr when that is 0).
+constexpr int DENSE_MMA_MIN_N = 9;
+int dense_mma_planes(int dt, int n, int k);
+size_t dense_act_bytes(int dt, int n, int k);
+size_t dense_mma_split_floats(int dt, int k, int m, int n);
+hipError_t launch_dense_mma(int dt, const WeightView& w, const float* a, int lda, int k, int m, int n, float* c,
+                            int ldc, void* scratch, float* part, hipStream_t st, const Epi& ep = Epi{});
 
 // In place on gate [rows][ldg]: act 1 SwiGLU silu(gate)·up, act 2 gpt-oss clamped SwiGLU (epilogue.hip); lanes 0
 // the full-scalar arithmetic, lanes > 0 jinfer's Vector API arithmetic with a species of `lanes` floats.

@@ -117,7 +117,8 @@ def test_pinned_matches_staged_and_slices(hip, oracle, dt):
 
 FULL = [(O.Q5_K, 14336, 4096, 1), (O.Q5_K, 4096, 14336, 8), (O.NVFP4, 4096, 4096, 1), (O.NVFP4, 4096, 4096, 16),
         (O.Q1_0, 4096, 4096, 1), (O.Q1_0, 4096, 4096, 16), (O.BF16, 4096, 4096, 1), (O.BF16, 4096, 4096, 64),
-        (O.F16, 4096, 4096, 4), (O.F32, 2048, 2880, 33)]
+        (O.F16, 4096, 4096, 4), (O.F32, 2048, 2880, 33), (O.F16, 14336, 4096, 512), (O.BF16, 4096, 14336, 2),
+        (O.F16, 14336, 4096, 8)]
 
 
 @pytest.mark.parametrize("dt,m,k,n", FULL)
