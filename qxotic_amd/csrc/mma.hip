@@ -594,7 +594,8 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
                 }
             } else if constexpr (DT == MXFP4) {   // group of 8 blocks; stage h2 = blocks 4h2..4h2+3
                 // every LDS read of the stage up front, then the next stage's copy, then the compute
-                uint4 hdr[RT], chs[RT][4];
+                uint4 hdr[RT];
+                uint2 chs[RT][4];   // lane half q: bytes 8q..8q+7 of each block (K-step 0 word 2q, K-step 1 word 2q + 1)
                 half8 bfs[4][CT][2];
                 float dxs[4][CT];
                 float sg[RT][16];
@@ -603,7 +604,7 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
                     hdr[i] = *reinterpret_cast<const uint4*>(buf + S::H_OFF + ((wave * RT + i) * 32 + r) * 16);
     #pragma unroll
                     for (int bl = 0; bl < 4; bl++)
-                        chs[i][bl] = *reinterpret_cast<const uint4*>(LA + ((wave * RT + i) * NCS + bl) * 512 + 16 * r);
+                        chs[i][bl] = *reinterpret_cast<const uint2*>(LA + ((wave * RT + i) * NCS + bl) * 512 + 16 * r + 8 * q);
                 }
     #pragma unroll
                 for (int bl = 0; bl < 4; bl++)
@@ -615,12 +616,13 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
                         dxs[bl][j] = LDX[bl * BN + 32 * j + r];
                     }
                 const bool gend = h2 == 1 || st == nstk - 1;   // the last group may end after its first half
-                if (gend) {   // group end: 2^(e_ref - 128) of the 16 output rows this lane holds
+                if (gend) {   // group end: 2^(e_ref - 128) of the 16 output rows this lane holds (header bytes 12..15)
     #pragma unroll
                     for (int i = 0; i < RT; i++) {
-                        const unsigned char* H = buf + S::H_OFF + (wave * RT + i) * 32 * 16;
+                        const unsigned char* H = buf + S::H_OFF + (wave * RT + i) * 32 * 16 + 12;
     #pragma unroll
-                        for (int e = 0; e < 16; e++) sg[i][e] = e8m0_half(H[(8 * (e >> 2) + 4 * q + (e & 3)) * 16 + 8]);
+                        for (int e = 0; e < 16; e++)
+                            sg[i][e] = *reinterpret_cast<const float*>(H + (8 * (e >> 2) + 4 * q + (e & 3)) * 16);
                     }
                 }
                 __builtin_amdgcn_sched_barrier(0);
@@ -633,15 +635,15 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
                         half8 af[RT][2];
     #pragma unroll
                         for (int i = 0; i < RT; i++) {
-                            const uint4 ch = chs[i][bl];
-                            const int b = 4 * h2 + bl;
-                            const int eb = (int) (((b < 4 ? hdr[i].x : hdr[i].y) >> (8 * (b & 3))) & 0xffu);
+                            const uint2 ch = chs[i][bl];
+                            const int eb = (int) (((h2 ? hdr[i].y : hdr[i].x) >> (8 * bl)) & 0xffu);
                             const int er = (int) (hdr[i].z & 0xffu);
-                            const int ex = eb - er + 128;   // biased exponent of 2^(eb - er + 1); below 2^-126: 0
-                            const float scale = ex > 0 ? __builtin_bit_cast(float, (uint32_t) ex << 23) : 0.0f;
-                            // lane half q takes bytes 8q..8q+7 of the block: K-step 0 word 2q, K-step 1 word 2q + 1
-                            af[i][0] = mx_frag(q ? ch.z : ch.x, scale);
-                            af[i][1] = mx_frag(q ? ch.w : ch.y, scale);
+                            // f32 bits of 2^(eb - er + 1): (eb - er)·2^23 + bits(2.0); a scale below 2^-126 (only a
+                            // zero-code block stored as e = 0 under a reference >= 128) comes out <= 0 and becomes 0
+                            const int sb = (eb - er) * (1 << 23) + 0x40000000;
+                            const float scale = __builtin_bit_cast(float, max(sb, 0));
+                            af[i][0] = mx_frag(ch.x, scale);
+                            af[i][1] = mx_frag(ch.y, scale);
                         }
     #pragma unroll
                         for (int i = 0; i < RT; i++)

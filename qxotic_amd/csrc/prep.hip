@@ -140,7 +140,8 @@ __global__ void __launch_bounds__(256) repack_kernel(const uint8_t* __restrict__
             }
         }
         bool bad = false;   // the matrix cores' folding would not be exact for this row's group
-        if constexpr (DT == MXFP4) {   // byte 8: the reference exponent (largest of the counted blocks); 9..15 zero
+        if constexpr (DT == MXFP4) {   // byte 8: the reference exponent (largest of the counted blocks); 9..11
+                                       // zero; 12..15: the f32 2^(e_ref - 128) that the matrix cores apply per group
             uint8_t er = 0;
             for (int j = 0; j < BPG; j++) {
                 if (!nz[j] && ds[j] != 255) ds[j] = 0;
@@ -149,7 +150,9 @@ __global__ void __launch_bounds__(256) repack_kernel(const uint8_t* __restrict__
             }
             for (int j = 0; j < BPG; j++) bad |= nz[j] && (int) ds[j] + 14 < (int) er;
             ds[8] = er;
-            for (int t = 9; t < 16; t++) ds[t] = 0;
+            for (int t = 9; t < 12; t++) ds[t] = 0;
+            const uint32_t f = __builtin_bit_cast(uint32_t, e8m0_half(er));
+            for (int t = 0; t < 4; t++) ds[12 + t] = (uint8_t) (f >> (8 * t));
         } else {
             uint32_t hs[BPG];
             int F = 0;   // largest fp16 exponent field of the group

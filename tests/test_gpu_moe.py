@@ -185,28 +185,34 @@ def test_mm_grouped_counts_past_rows_cap(hip, oracle):
         hip.evict(Segment.of(w))
 
 
+@pytest.mark.parametrize("k,pad", [(512, 0), (5120, 0), (512, 1)])
 @pytest.mark.parametrize("dt", [O.MXFP4, O.Q4_K])
-def test_mm_grouped_decode_sized(hip, oracle, dt):
+def test_mm_grouped_decode_sized(hip, oracle, dt, k, pad):
     """Decode-time MoE: fewer than 8 rows in all (one token, top-4 and a ragged cap), so every expert takes
-    jam's F1 and only the F1 decode launch runs; rows and the ldc gap past the counts stay untouched."""
+    jam's F1 and only the F1 decode launch runs; rows and the ldc gap past the counts stay untouched.
+    k = 512 with lda = k quantizes the activations inside the decode kernels; k = 5120 (too long for the
+    seven-token kernel's fused prologue) and lda = k + 1 (rows not 16-byte aligned) quantize them in a
+    separate launch and the kernels read the codes at each expert's CSR offset."""
     import torch
     from qxotic_amd.jam import JAM, Segment
-    m, k = 64, 512
+    m, lda = 64, k + pad
     for counts, rows_cap in (([1, 0, 1, 0, 1, 1], 4), ([0, 3, 0, 2, 0, 0, 1], 7)):
         E = len(counts)
-        say(f"grouped decode-sized {O.NAMES[dt]} counts={counts} rows_cap={rows_cap}")
+        say(f"grouped decode-sized {O.NAMES[dt]} k={k} lda={lda} counts={counts} rows_cap={rows_cap}")
         w_e = [oracle.quantize(dt, oracle.normal(0xDEC0 + 31 * e + dt, (m, k), 0.0, 0.02)) for e in range(E)]
         w = np.ascontiguousarray(np.concatenate(w_e, axis=0))
-        a = oracle.outliers(0xDEC1 + E, (rows_cap, k))
+        a = oracle.outliers(0xDEC1 + E + k, (rows_cap, k))
+        a_pad = np.full((rows_cap, lda), np.nan, np.float32)   # the gap past k is never read
+        a_pad[:, :k] = a
         assert hip.pin(Segment.of(w), dt, k, E * m) == JAM.OK, hip.last_error()
         try:
             c = torch.full((rows_cap + 1, m + 2), -3.0, dtype=torch.float32, device="cuda")
             off = torch.zeros(E + 1, dtype=torch.int32, device="cuda")
-            a_dv = dev(a)   # held until the kernels that read it have run
+            a_dv = dev(a_pad)   # held until the kernels that read it have run
             counts_dv = dev(np.array(counts, np.int32))
             torch.cuda.synchronize()   # torch's fills run on its own stream
-            assert hip.mm_grouped(Segment.of(w), dt, k, m, E, counts_dv.data_ptr(), a_dv.data_ptr(), k, c.data_ptr(),
-                                  m + 2, k, rows_cap, off.data_ptr()) == JAM.OK, hip.last_error()
+            assert hip.mm_grouped(Segment.of(w), dt, k, m, E, counts_dv.data_ptr(), a_dv.data_ptr(), lda,
+                                  c.data_ptr(), m + 2, k, rows_cap, off.data_ptr()) == JAM.OK, hip.last_error()
             hip.synchronize()
             total = sum(counts)
             assert off.cpu().numpy().tolist() == [0] + np.cumsum(counts).tolist()
