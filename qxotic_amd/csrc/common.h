@@ -90,6 +90,44 @@ __device__ inline float epilogue(const Epi& e, float v, int64_t row, const float
     return v;
 }
 
+// One lane's column of a 32x32 MFMA accumulator tile (16 values v[e]): C row `ct`, rows rowb + 8·(e/4) + e%4
+// (rowb = the tile's first row + 4·(lane / 32)), each times `scale` and through the epilogue unless `raw`
+// (split-K partials). Four consecutive rows go out as one 16-byte store where all four are below m and
+// ct + rowb is 16-byte aligned; the values and their order of operations are the scalar path's.
+template <typename V>
+__device__ inline void store_column(float* ct, int64_t rowb, int64_t m, const V& v, float scale, const Epi& ep,
+                                    bool raw) {
+    const bool al = (reinterpret_cast<uintptr_t>(ct + rowb) & 15) == 0;
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+        const int64_t r0 = rowb + 8 * g;
+        if (al && r0 + 3 < m) {
+            float x[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) x[i] = v[4 * g + i] * scale;
+            if (!raw) {
+                if (ep.bias != nullptr)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) x[i] += ep.bias[r0 + i];
+                if (ep.accumulate) {
+                    const float4 o = *reinterpret_cast<const float4*>(ct + r0);
+                    x[0] = o.x + x[0], x[1] = o.y + x[1], x[2] = o.z + x[2], x[3] = o.w + x[3];
+                }
+            }
+            *reinterpret_cast<float4*>(ct + r0) = make_float4(x[0], x[1], x[2], x[3]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int64_t row = r0 + i;
+                if (row < m) {
+                    const float val = v[4 * g + i] * scale;
+                    ct[row] = raw ? val : epilogue(ep, val, row, ct + row);
+                }
+            }
+        }
+    }
+}
+
 struct WeightView {
     const uint8_t* qs;   // plane 0 of the device copy
     const uint8_t* sc;   // plane 1 of the device copy

@@ -296,19 +296,8 @@ __global__ void __launch_bounds__(64 * DM_WAVES) dense_mfma_kernel(WeightView w,
             }
         }
     }
-#pragma unroll
-    for (int e = 0; e < 16; e++) {
-        const int64_t row = row0 + 8 * (e >> 2) + 4 * q + (e & 3);
-        if (row >= m) continue;
-        if (vA) {
-            float* dst = c + (int64_t) tA * ldc + row;
-            *dst = epilogue(ep, accA[e], row, dst);
-        }
-        if (vB) {
-            float* dst = c + (int64_t) tB * ldc + row;
-            *dst = epilogue(ep, accB[e], row, dst);
-        }
-    }
+    if (vA) store_column(c + (int64_t) tA * ldc, row0 + 4 * q, m, accA, 1.0f, ep, false);
+    if (vB) store_column(c + (int64_t) tB * ldc, row0 + 4 * q, m, accB, 1.0f, ep, false);
 }
 
 // ------------------------------------------------------------------------- staged matrix-core GEMM (n >= 9)
@@ -491,14 +480,7 @@ __global__ void __launch_bounds__(256, 2) dense_mma_kernel(WeightView w, const u
         const int t = n0 + 32 * j + r;
         if (t >= n) continue;
         const float sc = es[t];
-        float* ct = c + (int64_t) t * ldc;
-#pragma unroll
-        for (int e = 0; e < 16; e++) {
-            const int64_t row = row0 + 8 * (e >> 2) + 4 * q + (e & 3);
-            if (row >= m) continue;
-            const float v = acc[j][e] * sc;
-            ct[row] = st_per > 0 ? v : epilogue(ep, v, row, ct + row);
-        }
+        store_column(c + (int64_t) t * ldc, row0 + 4 * q, m, acc[j], sc, ep, st_per > 0);
     }
 }
 

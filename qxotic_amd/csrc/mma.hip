@@ -957,17 +957,8 @@ __global__ void __launch_bounds__(MMA_THREADS, 2) kq_gemm_kernel(WeightView w, G
         const float sc = A.es[t];
         float* ct = c + (int64_t) blockIdx.y * c_slice + (int64_t) (crow0 + tl) * ldc;
 #pragma unroll
-        for (int i = 0; i < RT; i++) {
-            const int64_t rowb = (T0 + wave * RT + i) * 32 + 4 * q;
-#pragma unroll
-            for (int e = 0; e < 16; e++) {
-                const int64_t row = rowb + 8 * (e >> 2) + (e & 3);
-                if (row < m) {
-                    const float v = acc[i][j][e] * sc;
-                    ct[row] = sb_per > 0 ? v : epilogue(ep, v, row, ct + row);   // split: the reduce applies it
-                }
-            }
-        }
+        for (int i = 0; i < RT; i++)   // split K: the reduce applies the epilogue
+            store_column(ct, (T0 + wave * RT + i) * 32 + 4 * q, m, acc[i][j], sc, ep, sb_per > 0);
     }
 }
 

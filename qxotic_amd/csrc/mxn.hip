@@ -24,6 +24,7 @@
 #include "launch.h"
 
 #include <atomic>
+#include <type_traits>
 
 namespace jamhip {
 
@@ -125,34 +126,52 @@ __global__ void __launch_bounds__(256) mxn_prep_kernel(const float* __restrict__
 }
 
 // ------------------------------------------------------------------------------------------- GEMM
-// Workgroup: 4 waves x 32 rows (wave w: row tile w) x 64 tokens (2 token tiles per wave); stages of 128 K (two
-// 64-K MFMA steps) copied global -> LDS, double-buffered. Stage buffer: weight chunks [4 tiles][4 blocks][32 rows]
-// [16 B], header [4 tiles][32 rows][16 B], B hi / lo [2 steps][2 halves][64 tokens][32 B] each, scales hi / lo
-// [4 blocks][64 tokens] bytes each.
+// Workgroup: 8 waves x 32 rows (wave w: row tile w) x 64 tokens (2 token tiles per wave), one per CU; K in stages
+// of 256 (one MXFP4 group, four 64-K MFMA steps). The kernel does no per-block VALU work, so the matrix cores
+// wait only on memory, and every operand goes global -> LDS (global_load_lds) two stages ahead into a ring of
+// three stage buffers. Each buffer is its own LDS object, and every copy in flight is such a copy, so the
+// compiler's wait before a buffer's reads covers only the copies into that buffer. Stage buffer:
+//   weights  [8 waves][4 steps][64 lanes][16 B]   (lane (r, q) of step kk: block 2kk + q of row r)
+//   headers  [8 waves][32 rows][8 B]              (the rows' block exponents, header bytes 0..7)
+//   codes    [4 steps][2 halves][2 planes][64 tokens][16 B] (waves 2kk, 2kk + 1 copy step kk's two halves;
+//                                                  plane p = bytes 16p..16p+15 of a token's 32, so a lane
+//                                                  fragment read is 1 KB contiguous over the wave: no bank
+//                                                  conflicts)
+//   scales   [8 waves][256 B]                     (waves 0 / 1: blocks 0-3 / 4-7 x 64 tokens; the other
+//                                                  waves copy the same bytes, so every wave issues the same)
+// Eight copies per wave and stage. The stage barrier is a plain s_barrier after an explicit wait for the wave's
+// own copies of the stage (a workgroup fence would wait for every copy in flight). Past the end of K the copies
+// re-read the last stage, so every stage issues the same; stages past the end run on zero weights. PLANE selects
+// the hi (0) or lo (1) codes and scales: mode 2 is one launch over hi, mode 1 a second launch over lo that adds
+// its products into C (the first launch applied the call's epilogue).
 namespace mxn {
-constexpr int A_OFF = 0, H_OFF = 8192, BH_OFF = 10240, BL_OFF = 18432, SH_OFF = 26624, SL_OFF = 26880;
-constexpr int STAGE = 27648;
-JAMHIP_DEV void dma16(const void* g, void* lds_base) {
-    __builtin_amdgcn_global_load_lds(g, (lds_void*) lds_base, 16, 0, 0);
+constexpr int MW = 8;                                           // waves per workgroup
+constexpr int OA = 0, OH = OA + MW * 4096, OB = OH + MW * 256, OS = OB + 16384, BSTAGE = OS + MW * 256;
+constexpr int UNROLL = 6;                                       // stages per loop trip (two turns of the ring)
+// s_waitcnt with only vmcnt set (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8)
+template <int N> JAMHIP_DEV void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 }  // namespace mxn
 
-template <int MODE>
-__global__ void __launch_bounds__(256, 2) mxn_gemm_kernel(WeightView w, MxAct A, int m, int n, float* __restrict__ c,
-                                                          int ldc, int nrb, int ncb, int64_t tiles, Groups gp, Epi ep) {
+template <int PLANE>
+__global__ void __launch_bounds__(64 * mxn::MW, 1) mxn_gemm_kernel(WeightView w, MxAct A, int m, int n,
+                                                                   float* __restrict__ c, int ldc, int nrb, int ncb,
+                                                                   int64_t tiles, Groups gp, Epi ep) {
     using namespace mxn;
-    __shared__ __align__(1024) unsigned char smem[2 * STAGE];
+    __shared__ __align__(1024) unsigned char sb0[BSTAGE], sb1[BSTAGE], sb2[BSTAGE];
     const int total = nrb * ncb;
     const int lin = tile_of_block(gp.map64 != nullptr, total);
     if (lin >= total) return;
     int rb = lin / ncb, cb = lin % ncb;
     if (gp.map64 != nullptr && grouped_tile(gp, lin, nrb, &rb, &cb) < 0) return;
-    const int64_t T0 = (int64_t) rb * 4;
+    const int64_t T0 = (int64_t) rb * MW;
     const int n0 = cb * 64;
     const int lane = threadIdx.x & 63, r = lane & 31, q = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int G = (int) w.G;
-    const int nst = (A.K / 32 + 3) / 4;                 // stages holding at least one block of k
+    const int nsg = A.Kp / 256;                         // stages (groups of K)
     int64_t r0t = w.r0 >> 5;
     int slot0 = 0, crow0 = 0, nvalid = n;
     if (gp.map64 != nullptr) {                          // grouped: this slot block's expert
@@ -168,86 +187,93 @@ __global__ void __launch_bounds__(256, 2) mxn_gemm_kernel(WeightView w, MxAct A,
     }
     constexpr int NC = group_chunks(MXFP4);
     const int64_t Tw = T0 + wave < tiles ? T0 + wave : tiles - 1;
-    const uint8_t* a_src = w.qs + (r0t + Tw) * G * (NC * CHUNK_STRIDE) + 16 * lane;
-    const int64_t Th = T0 + 2 * (wave & 1) + q < tiles ? T0 + 2 * (wave & 1) + q : tiles - 1;
-    const uint8_t* h_src = w.sc + ((r0t + Th) * G * 32 + r) * 16;
-    const int64_t bstep = (int64_t) 2 * A.NP * 32;      // bytes per 64-K step (both halves)
-    // B pieces (1 KB = 32 tokens x 32 B): wave w takes plane w >> 1 (hi, lo) and (step, half) pairs 2(w&1), +1
-    const uint8_t* bplane = (wave >> 1) ? A.lo : A.hi;
-    const int boff = (wave >> 1) ? BL_OFF : BH_OFF;
-    auto issue = [&](int st, unsigned char* buf) {
-        const int g = st >> 1, h2 = st & 1;
-        const uint8_t* ag = a_src + (int64_t) g * (NC * CHUNK_STRIDE) + (4 * h2) * CHUNK_STRIDE;
-        dma16(ag, buf + A_OFF + wave * 2048);
-        dma16(ag + 2 * CHUNK_STRIDE, buf + A_OFF + wave * 2048 + 1024);
-        if (MODE == 1 || wave < 2) {   // mode 2 has no lo plane
-#pragma unroll
-            for (int p = 0; p < 2; p++) {
-                const int sq = 2 * (wave & 1) + p;     // (step, half) = (sq >> 1, sq & 1)
-#pragma unroll
-                for (int th = 0; th < 2; th++)
-                    dma16(bplane + (int64_t) (2 * st + (sq >> 1)) * bstep + ((int64_t) (sq & 1) * A.NP + n0 + 32 * th) * 32 + 16 * lane,
-                          buf + boff + (sq * 64 + 32 * th) * 32);
-            }
-        }
-        if (wave < 2) dma16(h_src + (int64_t) g * 32 * 16, buf + H_OFF + wave * 1024);
-        if ((wave == 2 || (wave == 3 && MODE == 1)) && lane < 16) {   // scales: 4 blocks x 64 tokens, a byte each
-            const uint8_t* s = (wave == 2 ? A.shi : A.slo) + (int64_t) (4 * st + (lane >> 2)) * A.NP + n0 + 16 * (lane & 3);
-            dma16(s, buf + (wave == 2 ? SH_OFF : SL_OFF));
-        }
-    };
+    const uint8_t* a_src = w.qs + (r0t + Tw) * G * (NC * CHUNK_STRIDE) + 16 * lane;                // + g·4096
+    const uint8_t* h_src = w.sc + ((r0t + Tw) * G * 32 + (lane >> 1)) * 16 + 4 * (lane & 1);   // + g·512
+    const int64_t sstep = (int64_t) A.NP * 32;          // bytes per (64-K step, half) plane
+    const int bstep = wave >> 1, bhalf = wave & 1;      // the code piece pair this wave copies
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
     floatx16 acc[2] = {floatx16{}, floatx16{}};
-    issue(0, smem);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    for (int st = 0; st < nst; st++) {
-        unsigned char* buf = smem + (st & 1) * STAGE;
-        const int h2 = st & 1;
-        v8i av[2], bh[2][2], bl[2][2];
-        int sa[2], sbh[2][2], sbl[2][2];
+    auto ring = [&](int i) -> unsigned char* { return i == 0 ? sb0 : i == 1 ? sb1 : sb2; };
+    {
+        const uint8_t* codes = PLANE ? A.lo : A.hi;
+        const uint8_t* scales = PLANE ? A.slo : A.shi;
+        auto issue = [&](int s, unsigned char* buf) {
+            const int64_t g = min(s, nsg - 1);
+            const uint8_t* ag = a_src + g * (NC * CHUNK_STRIDE);
 #pragma unroll
-        for (int kk = 0; kk < 2; kk++) {
-            const uint4 x = *reinterpret_cast<const uint4*>(buf + A_OFF + (wave * 4 + 2 * kk + q) * 512 + 16 * r);
-            av[kk] = v8i{(int) x.x, (int) x.y, (int) x.z, (int) x.w, 0, 0, 0, 0};
-            sa[kk] = buf[H_OFF + (wave * 32 + r) * 16 + 4 * h2 + 2 * kk + q];
+            for (int kk = 0; kk < 4; kk++)   // chunks 2kk, 2kk + 1: 1 KB contiguous
+                __builtin_amdgcn_global_load_lds(ag + kk * 2 * CHUNK_STRIDE, (lds_void*) (buf + OA + (wave * 4 + kk) * 1024),
+                                                 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(h_src + g * 512, (lds_void*) (buf + OH + wave * 256), 4, 0, 0);
+            const int64_t st = 4 * g + bstep;
 #pragma unroll
-            for (int j = 0; j < 2; j++) {
-                const int bo = ((2 * kk + q) * 64 + 32 * j + r) * 32;
-                bh[kk][j] = *reinterpret_cast<const v8i*>(buf + BH_OFF + bo);
-                sbh[kk][j] = buf[SH_OFF + (2 * kk + q) * 64 + 32 * j + r];
-                if (MODE == 1) {
-                    bl[kk][j] = *reinterpret_cast<const v8i*>(buf + BL_OFF + bo);
-                    sbl[kk][j] = buf[SL_OFF + (2 * kk + q) * 64 + 32 * j + r];
+            for (int pp = 0; pp < 2; pp++)   // lane l: token l's bytes 16pp..16pp+15
+                __builtin_amdgcn_global_load_lds(codes + (2 * st + bhalf) * sstep + (int64_t) (n0 + lane) * 32 + 16 * pp,
+                                                 (lds_void*) (buf + OB + ((2 * bstep + bhalf) * 2 + pp) * 1024), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(scales + (8 * g + 4 * (wave & 1) + (lane >> 4)) * A.NP + n0 + 4 * (lane & 15),
+                                             (lds_void*) (buf + OS + wave * 256), 4, 0, 0);
+        };
+        issue(0, ring(0));
+        issue(1, ring(1));
+        auto stage = [&](auto U, int s) {
+            constexpr int u = decltype(U)::value;
+            const unsigned char* buf = ring(u % 3);
+            // stage s's eight copies were issued two stages ago and stage s + 1's eight follow them; then every
+            // wave's copies are in, and every wave is done reading the buffer that the next issue overwrites
+            wait_vm<8>();
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            issue(s + 2, ring((u + 2) % 3));
+            // the stage's operands, read up front as 16-byte loads (a 32-byte LDS load is split without the
+            // alias information that keeps the compiler from waiting for every copy in flight)
+            u32x4 av[4];
+            v8i bq[4][2];
+            int sq[4][2];
+            const uint2 hx = *reinterpret_cast<const uint2*>(buf + OH + wave * 256 + 8 * r);
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) {
+                av[kk] = *reinterpret_cast<const u32x4*>(buf + OA + (wave * 4 + kk) * 1024 + 16 * lane);
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    const u32x4 b0 = *reinterpret_cast<const u32x4*>(buf + OB + ((2 * kk + q) * 128 + 32 * j + r) * 16);
+                    const u32x4 b1 = *reinterpret_cast<const u32x4*>(buf + OB + ((2 * kk + q) * 128 + 64 + 32 * j + r) * 16);
+                    bq[kk][j] = v8i{(int) b0.x, (int) b0.y, (int) b0.z, (int) b0.w, (int) b1.x, (int) b1.y, (int) b1.z,
+                                    (int) b1.w};
+                    // block 2kk + q: wave (2kk + q) / 4's slot, row (2kk + q) % 4 of 64 tokens
+                    sq[kk][j] = buf[OS + ((2 * kk + q) >> 2) * 256 + ((2 * kk + q) & 3) * 64 + 32 * j + r];
                 }
             }
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        if (st + 1 < nst) issue(st + 1, smem + ((st + 1) & 1) * STAGE);
+            __builtin_amdgcn_sched_barrier(0);
+            const bool live = s < nsg;   // past the end of K: zero weights, exactly zero products
 #pragma unroll
-        for (int kk = 0; kk < 2; kk++)
+            for (int kk = 0; kk < 4; kk++) {
+                const u32x4 x = live ? av[kk] : u32x4{0u, 0u, 0u, 0u};
+                const v8i a8 = v8i{(int) x.x, (int) x.y, (int) x.z, (int) x.w, 0, 0, 0, 0};
+                const int sa = (int) (((kk < 2 ? hx.x : hx.y) >> (8 * (2 * (kk & 1) + q))) & 0xffu);
 #pragma unroll
-            for (int j = 0; j < 2; j++) {
-                acc[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av[kk], bh[kk][j], acc[j], 4, 0, 0, sa[kk], 0,
-                                                                         sbh[kk][j]);
-                if (MODE == 1)
-                    acc[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av[kk], bl[kk][j], acc[j], 4, 0, 0, sa[kk],
-                                                                             0, sbl[kk][j]);
+                for (int j = 0; j < 2; j++)
+                    acc[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a8, bq[kk][j], acc[j], 4, 0, 0, sa, 0,
+                                                                             sq[kk][j]);
             }
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        for (int s = 0; s < nsg; s += UNROLL) {
+            stage(std::integral_constant<int, 0>{}, s);
+            stage(std::integral_constant<int, 1>{}, s + 1);
+            stage(std::integral_constant<int, 2>{}, s + 2);
+            if (s + 3 < nsg) {
+                stage(std::integral_constant<int, 3>{}, s + 3);
+                stage(std::integral_constant<int, 4>{}, s + 4);
+                stage(std::integral_constant<int, 5>{}, s + 5);
+            }
+        }
     }
+    wait_vm<0>();   // no copy may still be writing this workgroup's LDS when it exits
     // epilogue: lane holds token n0 + 32j + r, rows 8·(e/4) + 4q + e%4 of the wave's tile
 #pragma unroll
     for (int j = 0; j < 2; j++) {
         const int t = n0 + 32 * j + r, tl = t - slot0;
         if (tl >= nvalid) continue;
-        float* ct = c + (int64_t) (crow0 + tl) * ldc;
-        const int64_t rowb = (T0 + wave) * 32 + 4 * q;
-#pragma unroll
-        for (int e = 0; e < 16; e++) {
-            const int64_t row = rowb + 8 * (e >> 2) + (e & 3);
-            if (row < m) ct[row] = epilogue(ep, acc[j][e], row, ct + row);
-        }
+        store_column(c + (int64_t) (crow0 + tl) * ldc, (T0 + wave) * 32 + 4 * q, m, acc[j], 1.0f, ep, false);
     }
 }
 
@@ -283,11 +309,15 @@ hipError_t launch_mx_prep_grouped(const float* a, int lda, int k, int mode, cons
 static hipError_t mx_go(int mode, const WeightView& w, const MxAct& A, int m, int n, float* c, int ldc, const Groups& gp,
                         const Epi& ep, hipStream_t st) {
     if ((w.r0 & 31) || A.NP % 64) return hipErrorNotSupported;
-    const int nrb = (m + 127) / 128, ncb = A.NP / 64;
+    const int nrb = (m + 32 * mxn::MW - 1) / (32 * mxn::MW), ncb = A.NP / 64;
     const int64_t tiles = (w.r0 + tiled_rows(m)) / 32 - w.r0 / 32;
     const int grid = tile_grid(gp.map64 != nullptr, nrb * ncb);
-    if (mode == 1) mxn_gemm_kernel<1><<<grid, 256, 0, st>>>(w, A, m, n, c, ldc, nrb, ncb, tiles, gp, ep);
-    else mxn_gemm_kernel<2><<<grid, 256, 0, st>>>(w, A, m, n, c, ldc, nrb, ncb, tiles, gp, ep);
+    mxn_gemm_kernel<0><<<grid, 64 * mxn::MW, 0, st>>>(w, A, m, n, c, ldc, nrb, ncb, tiles, gp, ep);
+    if (mode == 1) {   // the lo codes' products, added into C behind the first launch
+        Epi add;
+        add.accumulate = 1;
+        mxn_gemm_kernel<1><<<grid, 64 * mxn::MW, 0, st>>>(w, A, m, n, c, ldc, nrb, ncb, tiles, gp, add);
+    }
     return hipGetLastError();
 }
 
