@@ -347,7 +347,7 @@ def prefill_leg(hip, torch, stream, reps: int = 10) -> dict:
     return out
 
 
-def moe_leg(hip, torch, stream, steps: int = 10) -> dict:
+def moe_leg(hip, torch, stream, steps: int = 10, no_graph: bool = False) -> dict:
     """Config 5: a gpt-oss-20B-shaped MoE layer on the device: 32 experts with an MXFP4 gate_up 5760x2880
     and down 2880x2880, 512 tokens routed top-4 by Zipf(1.1) popularity (Gumbel-top-k on log p_e,
     p_e ~ e^-1.1). One step = jamhip_moe_select_topk + _route + _gather + grouped gate_up + grouped down + _combine
@@ -407,23 +407,42 @@ def moe_leg(hip, torch, stream, steps: int = 10) -> dict:
 
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
-    def timed() -> float:
-        """Median over 3 runs of `steps` layers (one run varies by 2-3% between runs on one box)."""
-        runs = []
+    def timed(fn=layer, n=steps, warm=3) -> tuple:
+        """(graph, stream) µs per layer: the median of 3 replays of one captured graph of `n` layers (the layer's
+        launches are all device-side: routing, offsets and slot maps come from device counts), and the median
+        of 3 runs of `n` layers launched on the stream (one run varies by 2-3% between runs on one box). The
+        stream runs come first and allocate every scratch buffer the capture then reuses."""
+        runs, gruns = [], []
         with torch.cuda.stream(stream):
-            for i in range(3):
-                layer(i)
+            for i in range(warm):
+                fn(i)
             torch.cuda.synchronize()
             for _ in range(3):
                 e0.record(stream)
-                for i in range(steps):
-                    layer(i)
+                for i in range(n):
+                    fn(i)
                 e1.record(stream)
                 torch.cuda.synchronize()
-                runs.append(e0.elapsed_time(e1) * 1e3 / steps)
-        return sorted(runs)[1]
+                runs.append(e0.elapsed_time(e1) * 1e3 / n)
+        if no_graph:
+            return sorted(runs)[1], sorted(runs)[1]
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            for i in range(n):
+                fn(i)
+        with torch.cuda.stream(stream):
+            g.replay()   # warm replay
+            torch.cuda.synchronize()
+            for _ in range(3):
+                e0.record(stream)
+                g.replay()
+                e1.record(stream)
+                torch.cuda.synchronize()
+                gruns.append(e0.elapsed_time(e1) * 1e3 / n)
+        del g
+        return sorted(gruns)[1], sorted(runs)[1]
 
-    us = timed()
+    us, us_stream = timed()
     assert np.array_equal(counts.cpu().numpy(), counts_h), "device routing counts disagree with the host's"
     assert np.array_equal(re.cpu().numpy(), sel.ravel()), "device top-k disagrees with the host's"
     assert bool(torch.isfinite(out).all()), "moe output not finite"
@@ -433,10 +452,11 @@ def moe_leg(hip, torch, stream, steps: int = 10) -> dict:
     native = {}
     for mode in (1, 2):
         assert hip.set_mx_native(mode) == JAM.OK
-        u = timed()
+        u, u_stream = timed()
         assert hip.set_mx_native(0) == JAM.OK
         assert bool(torch.isfinite(out).all()), "moe output not finite"
-        native[f"mode{mode}"] = {"us_per_layer": round(u, 1), "TOPS": round(ops / (u * 1e-6) / 1e12, 2),
+        native[f"mode{mode}"] = {"us_per_layer": round(u, 1), "us_per_layer_stream": round(u_stream, 1),
+                                 "TOPS": round(ops / (u * 1e-6) / 1e12, 2),
                                  "frac_fp4_peak": round(ops / (u * 1e-6) / 1e12 / 10070.0, 4)}
     native["note"] = ("opt-in jamhip_ctx_set_mx_native: MXFP4 weights as fp4 on v_mfma_scale_f32_32x32x64_f8f6f4, "
                       "activations MX-FP8 hi + lo (mode 1, ~8 bits) or hi only (mode 2, ~4 bits); not jam's "
@@ -461,25 +481,14 @@ def moe_leg(hip, torch, stream, steps: int = 10) -> dict:
         if not ok:
             raise RuntimeError(hip.last_error())
 
-    dec_runs = []
-    with torch.cuda.stream(stream):
-        for i in range(8):
-            dec_layer(i)
-        torch.cuda.synchronize()
-        for _ in range(3):
-            e0.record(stream)
-            for i in range(NDEC):
-                dec_layer(i)
-            e1.record(stream)
-            torch.cuda.synchronize()
-            dec_runs.append(e0.elapsed_time(e1) * 1e3 / NDEC)
+    dus, dus_stream = timed(dec_layer, NDEC, 8)
     assert bool(torch.isfinite(out[:1]).all()), "decode moe output not finite"
-    dus = sorted(dec_runs)[1]
     dbytes = TOPK * (FF + D) * (D // 32) * 17
-    decode = {"us_per_layer": round(dus, 1), "weights_GBs": round(dbytes / (dus * 1e-6) / 1e9, 1),
-              "note": "1 token top-4 (a random expert set per layer), route + gather + two grouped calls + combine "
-                      "in stream order, median of 3 runs of 200 layers; weights = 4 experts' gate_up + down "
-                      "(52.9 MB)"}
+    decode = {"us_per_layer": round(dus, 1), "us_per_layer_stream": round(dus_stream, 1),
+              "weights_GBs": round(dbytes / (dus * 1e-6) / 1e9, 1),
+              "note": "1 token top-4 (a random expert set per layer), route + gather + two grouped calls + combine, "
+                      "one captured graph of 200 layers (median of 3 replays; us_per_layer_stream: the same 200 "
+                      "layers launched on the stream); weights = 4 experts' gate_up + down (52.9 MB)"}
     # the same layer the way an unedited jinfer runs it through the host-pointer entry point: Moe.dispatch's host
     # loop (Moe.java:178-232) gathering each expert's rows, one jamhip_mm per expert and matrix on a row view of
     # the pinned stacked tensors (GptOss.java:677-717), the probability-weighted scatter on the host
@@ -517,7 +526,8 @@ def moe_leg(hip, torch, stream, steps: int = 10) -> dict:
     wbytes = E * (FF + D) * (D // 32) * 17
     tops = ops / (us * 1e-6) / 1e12
     gbs = wbytes / (us * 1e-6) / 1e9
-    return {"us_per_layer": round(us, 1), "TOPS": round(tops, 2), "weights_GBs": round(gbs, 1),
+    return {"us_per_layer": round(us, 1), "us_per_layer_stream": round(us_stream, 1), "TOPS": round(tops, 2),
+            "weights_GBs": round(gbs, 1),
             "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
             "frac_fp4_peak": round(tops / 10070.0, 4), "routed_rows": R,
             "counts": counts_h.tolist(), "mx_native": native, "decode": decode,
@@ -527,7 +537,8 @@ def moe_leg(hip, torch, stream, steps: int = 10) -> dict:
                                  "wall clock, mean of 3",
             "note": "32 experts x (5760x2880 + 2880x2880) MXFP4 (423 MB, 2 rotating copies; experts cycle through "
                     "2 distinct N(0,0.02) quantizations), 512 tokens top-4 Zipf(1.1); ops = 2*routed_rows*"
-                    "(5760*2880 + 2880*2880)"}
+                    "(5760*2880 + 2880*2880); us_per_layer: one captured graph of the timed layers, median of 3 "
+                    "replays; us_per_layer_stream: the same layers launched on the stream"}
 
 
 def decode_step_leg(hip, torch, stream, w_gate: np.ndarray, reps: int = 8) -> dict:
@@ -878,7 +889,7 @@ def main() -> int:
     moe = None
     if not args.no_moe:
         log("bench: moe leg")
-        moe = moe_leg(hip, torch, stream)
+        moe = moe_leg(hip, torch, stream, no_graph=args.no_graph)
     step = None
     if not args.no_step:
         log("bench: decode step leg")

@@ -69,59 +69,80 @@ JAMHIP_DEV int slot_source(int t, int n, const int* gmap, const int* goff, const
 
 }  // namespace mxn
 
-// One workgroup of 256 threads per token slot; a half-wave (32 lanes) per 32-element block, one element per
-// lane: the block maximum by shuffles, E, the hi / lo codes in the MFMA B order, the two scale bytes. The
-// codes of 8 blocks (4 K-steps x 2 halves x 32 bytes per plane) are assembled in LDS and written as 16-byte
-// pieces. A padding slot (past n, or past its expert's rows) is left unwritten: its token column is computed
-// but never stored. Mode 2 writes no lo plane (the GEMM reads none).
+// One workgroup of 256 threads per token slot, eight lanes per 32-element block (lane s of a group: elements
+// 4s..4s+3), 32 blocks per round; the row's loads for up to four rounds are issued before any is used, and no
+// step waits on another lane group, so a slot costs about one load latency. Per block: the maximum by shuffles
+// within the group, E, the hi / lo codes. The MFMA B order puts elements 8q..8q+7 and 8q+16..8q+23 of a block,
+// interleaved, in the 16 bytes of lane half q: lane s < 4 interleaves its four codes with those of lane s + 4
+// and stores the 8 bytes. A padding slot (past n, or past its expert's rows) is left unwritten: its token column
+// is computed but never stored. Mode 2 writes no lo plane (the GEMM reads none).
 __global__ void __launch_bounds__(256) mxn_prep_kernel(const float* __restrict__ a, int lda, int n, int k, int Kp,
                                                        int NP, int mode, uint8_t* __restrict__ hi,
                                                        uint8_t* __restrict__ lo, uint8_t* __restrict__ shi,
                                                        uint8_t* __restrict__ slo, const int* __restrict__ gmap,
-                                                       const int* __restrict__ goff, const int* __restrict__ gpoff) {
+                                                       const int* __restrict__ goff, const int* __restrict__ gpoff,
+                                                       int vec) {
     using namespace mxn;
-    __shared__ __align__(16) uint8_t lh[256], ll[256];  // 8 blocks' codes: [4 steps][2 halves][32 bytes]
     const int t = blockIdx.x;
     const int src = slot_source(t, n, gmap, goff, gpoff);
     if (src < 0) return;
-    const int e = threadIdx.x & 31;                     // element within the block
-    for (int b = threadIdx.x >> 5; b < Kp / 32; b += 8) {
-        const int col = 32 * b + e;
-        const float x = src >= 0 && col < k ? a[(int64_t) src * lda + col] : 0.0f;
-        float amax = fabsf(x);
+    const float* row = a + (int64_t) src * lda;
+    const int sub = threadIdx.x & 7, nb = Kp / 32;
+    constexpr int RQ = 4;   // rounds in flight
+    for (int r0 = 0; r0 < nb; r0 += 32 * RQ) {
+        float x[RQ][4];
 #pragma unroll
-        for (int o = 16; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 32));
-        int E = -127;
-        if (amax > 0.0f) {
-            int ee;
-            const float f = frexpf(amax / 448.0f, &ee);   // amax / 448 = f · 2^ee
-            E = f == 0.5f ? ee - 1 : ee;
-            if (ldexpf(amax, -E) > 448.0f) E += 1;        // rounding in amax / 448
-            E = max(-127, min(127, E));
+        for (int u = 0; u < RQ; u++) {
+            const int b = r0 + 32 * u + (threadIdx.x >> 3), col = 32 * b + 4 * sub;
+            if (b < nb && vec && col + 3 < k) {   // a and lda 16-byte aligned (the launcher checks)
+                const float4 f = *reinterpret_cast<const float4*>(row + col);
+                x[u][0] = f.x, x[u][1] = f.y, x[u][2] = f.z, x[u][3] = f.w;
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; i++) x[u][i] = b < nb && col + i < k ? row[col + i] : 0.0f;
+            }
         }
-        const float v = ldexpf(x, -E);
-        const uint32_t ch = e4m3(v);
-        const bool lo_ok = mode == 1 && E - 4 >= -127;
-        const uint32_t cl = lo_ok ? e4m3((v - e4m3_value(ch)) * 16.0f) : 0u;
-        // B order: K-step s = b / 2, bytes 16·(b % 2) + j of lane half q, element 8q + j/2 + 16·(j % 2)
-        const int q = (e & 15) >> 3, j = 2 * ((e & 15) - 8 * q) + (e >> 4);
-        const int bl = b & 7;                            // block within the 8 of this pass
-        const int li = ((bl >> 1) * 2 + q) * 32 + 16 * (bl & 1) + j;
-        lh[li] = (uint8_t) ch;
-        ll[li] = (uint8_t) cl;
-        if (e == 0) {
-            shi[(int64_t) b * NP + t] = (uint8_t) (E + 127);
-            if (mode == 1) slo[(int64_t) b * NP + t] = lo_ok ? (uint8_t) (E - 4 + 127) : (uint8_t) 0;
+#pragma unroll
+        for (int u = 0; u < RQ; u++) {
+            const int b = r0 + 32 * u + (threadIdx.x >> 3);
+            if (r0 + 32 * u >= nb) break;   // uniform: no block of this round exists
+            float amax = fmaxf(fmaxf(fabsf(x[u][0]), fabsf(x[u][1])), fmaxf(fabsf(x[u][2]), fabsf(x[u][3])));
+#pragma unroll
+            for (int o = 4; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 8));
+            int E = -127;
+            if (amax > 0.0f) {
+                int ee;
+                const float f = frexpf(amax / 448.0f, &ee);   // amax / 448 = f · 2^ee
+                E = f == 0.5f ? ee - 1 : ee;
+                if (ldexpf(amax, -E) > 448.0f) E += 1;        // rounding in amax / 448
+                E = max(-127, min(127, E));
+            }
+            const bool lo_ok = mode == 1 && E - 4 >= -127;
+            uint32_t ch = 0, cl = 0;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float v = ldexpf(x[u][i], -E);
+                const uint32_t c = e4m3(v);
+                ch |= c << (8 * i);
+                if (lo_ok) cl |= e4m3((v - e4m3_value(c)) * 16.0f) << (8 * i);
+            }
+            const uint32_t ph = __shfl_xor(ch, 4, 8), pl = __shfl_xor(cl, 4, 8);
+            if (b < nb && sub < 4) {
+                // bytes: own0, partner0, own1, partner1, ... (elements e, e + 16 of the block)
+                auto mix = [](uint32_t o, uint32_t p) {
+                    const uint32_t lo16 = (o & 0xffu) | ((p & 0xffu) << 8) | ((o & 0xff00u) << 8) | ((p & 0xff00u) << 16);
+                    const uint32_t hi16 = ((o >> 16) & 0xffu) | (((p >> 16) & 0xffu) << 8) | ((o >> 24) << 16) | ((p >> 24) << 24);
+                    return make_uint2(lo16, hi16);
+                };
+                const int64_t off = ((int64_t) ((b >> 1) * 2 + (sub >> 1)) * NP + t) * 32 + 16 * (b & 1) + 8 * (sub & 1);
+                *reinterpret_cast<uint2*>(hi + off) = mix(ch, ph);
+                if (mode == 1) *reinterpret_cast<uint2*>(lo + off) = mix(cl, pl);
+                if (sub == 0) {
+                    shi[(int64_t) b * NP + t] = (uint8_t) (E + 127);
+                    if (mode == 1) slo[(int64_t) b * NP + t] = lo_ok ? (uint8_t) (E - 4 + 127) : (uint8_t) 0;
+                }
+            }
         }
-        __syncthreads();
-        // 16 pieces of 16 bytes per plane: piece p = (step s, half q, 16-byte half h) of this pass's 4 steps
-        if (threadIdx.x < (mode == 1 ? 32 : 16)) {
-            const int pl = threadIdx.x >> 4, p = threadIdx.x & 15, s = p >> 2, qq = (p >> 1) & 1, h = p & 1;
-            const int step = (b - bl) / 2 + s;
-            uint8_t* dst = (pl ? lo : hi) + (((int64_t) step * 2 + qq) * NP + t) * 32 + 16 * h;
-            *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>((pl ? ll : lh) + (s * 2 + qq) * 32 + 16 * h);
-        }
-        __syncthreads();
     }
 }
 
@@ -294,7 +315,8 @@ static hipError_t mx_prep_np(const float* a, int lda, int n, int NP, int k, int 
     uint8_t* slo = shi + a256((int64_t) (Kp / 32) * NP);
     *out = MxAct{hi, lo, shi, slo, NP, Kp, k};
     if (NP <= 0) return hipSuccess;
-    mxn_prep_kernel<<<NP, 256, 0, st>>>(a, lda, n, k, Kp, NP, mode, hi, lo, shi, slo, gmap, goff, gpoff);
+    const int vec = (reinterpret_cast<uintptr_t>(a) & 15) == 0 && (lda & 3) == 0;
+    mxn_prep_kernel<<<NP, 256, 0, st>>>(a, lda, n, k, Kp, NP, mode, hi, lo, shi, slo, gmap, goff, gpoff, vec);
     return hipGetLastError();
 }
 
