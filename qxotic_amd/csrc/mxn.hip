@@ -34,31 +34,6 @@ typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) void lds_void;
 
-// OCP e4m3 (E4M3FN) code of v, |v| <= 448, round to nearest even (no NaN or saturation arises in range).
-JAMHIP_DEV uint32_t e4m3(float v) {
-    const uint32_t sgn = v < 0.0f ? 0x80u : 0u;
-    const float a = fabsf(v);
-    if (a < 0.015625f) {                          // below 2^-6: subnormal codes, step 2^-9 (8 -> 0x08, normal)
-        const uint32_t q = (uint32_t) rintf(a * 512.0f);
-        return sgn | q;
-    }
-    int e;
-    (void) frexpf(a, &e);                         // a = f · 2^e, f in [0.5, 1): exponent of a is e - 1
-    const int ex = e - 1;
-    uint32_t mt = (uint32_t) rintf(ldexpf(a, 3 - ex));   // in [8, 16]
-    int be = ex + 7;
-    if (mt == 16) {
-        mt = 8;
-        be += 1;
-    }
-    return sgn | ((uint32_t) be << 3) | (mt - 8);
-}
-JAMHIP_DEV float e4m3_value(uint32_t c) {
-    const uint32_t be = (c >> 3) & 15, mt = c & 7;
-    const float mag = be == 0 ? (float) mt * 0.001953125f : ldexpf((float) (8 + mt), (int) be - 10);
-    return (c & 0x80u) ? -mag : mag;
-}
-
 JAMHIP_DEV int slot_source(int t, int n, const int* gmap, const int* goff, const int* gpoff) {
     if (gmap == nullptr) return t < n ? t : -1;
     const int ex = gmap[t >> 6];
@@ -118,13 +93,22 @@ __global__ void __launch_bounds__(256) mxn_prep_kernel(const float* __restrict__
                 E = max(-127, min(127, E));
             }
             const bool lo_ok = mode == 1 && E - 4 >= -127;
-            uint32_t ch = 0, cl = 0;
+            // x·2^-E is exact (|v| <= 448); the hardware conversion gives the nearest OCP e4m3 code, ties to the
+            // even code; + 0.0f turns a -0 into +0 (code 0x00, not 0x80)
+            float v[4];
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float v = ldexpf(x[u][i], -E);
-                const uint32_t c = e4m3(v);
-                ch |= c << (8 * i);
-                if (lo_ok) cl |= e4m3((v - e4m3_value(c)) * 16.0f) << (8 * i);
+            for (int i = 0; i < 4; i++) v[i] = ldexpf(x[u][i], -E) + 0.0f;
+            uint32_t ch = (uint32_t) __builtin_amdgcn_cvt_pk_fp8_f32(v[0], v[1], 0, false);
+            ch = (uint32_t) __builtin_amdgcn_cvt_pk_fp8_f32(v[2], v[3], (int) ch, true);
+            uint32_t cl = 0;
+            if (lo_ok) {
+                const float hv[4] = {__builtin_amdgcn_cvt_f32_fp8((int) ch, 0), __builtin_amdgcn_cvt_f32_fp8((int) ch, 1),
+                                     __builtin_amdgcn_cvt_f32_fp8((int) ch, 2), __builtin_amdgcn_cvt_f32_fp8((int) ch, 3)};
+                float rr[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) rr[i] = (v[i] - hv[i]) * 16.0f + 0.0f;
+                cl = (uint32_t) __builtin_amdgcn_cvt_pk_fp8_f32(rr[0], rr[1], 0, false);
+                cl = (uint32_t) __builtin_amdgcn_cvt_pk_fp8_f32(rr[2], rr[3], (int) cl, true);
             }
             const uint32_t ph = __shfl_xor(ch, 4, 8), pl = __shfl_xor(cl, 4, 8);
             if (b < nb && sub < 4) {
