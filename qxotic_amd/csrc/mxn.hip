@@ -131,28 +131,38 @@ __global__ void __launch_bounds__(256) mxn_prep_kernel(const float* __restrict__
 }
 
 // ------------------------------------------------------------------------------------------- GEMM
-// Workgroup: 8 waves x 32 rows (wave w: row tile w) x 64 tokens (2 token tiles per wave), one per CU; K in stages
-// of 256 (one MXFP4 group, four 64-K MFMA steps). The kernel does no per-block VALU work, so the matrix cores
-// wait only on memory, and every operand goes global -> LDS (global_load_lds) two stages ahead into a ring of
-// three stage buffers. Each buffer is its own LDS object, and every copy in flight is such a copy, so the
-// compiler's wait before a buffer's reads covers only the copies into that buffer. Stage buffer:
-//   weights  [8 waves][4 steps][64 lanes][16 B]   (lane (r, q) of step kk: block 2kk + q of row r)
-//   headers  [8 waves][32 rows][8 B]              (the rows' block exponents, header bytes 0..7)
-//   codes    [4 steps][2 halves][2 planes][64 tokens][16 B] (waves 2kk, 2kk + 1 copy step kk's two halves;
-//                                                  plane p = bytes 16p..16p+15 of a token's 32, so a lane
-//                                                  fragment read is 1 KB contiguous over the wave: no bank
-//                                                  conflicts)
-//   scales   [8 waves][256 B]                     (waves 0 / 1: blocks 0-3 / 4-7 x 64 tokens; the other
-//                                                  waves copy the same bytes, so every wave issues the same)
-// Eight copies per wave and stage. The stage barrier is a plain s_barrier after an explicit wait for the wave's
-// own copies of the stage (a workgroup fence would wait for every copy in flight). Past the end of K the copies
-// re-read the last stage, so every stage issues the same; stages past the end run on zero weights. PLANE selects
-// the hi (0) or lo (1) codes and scales: mode 2 is one launch over hi, mode 1 a second launch over lo that adds
-// its products into C (the first launch applied the call's epilogue).
+// Workgroup: MW waves x 32 rows (wave w: row tile w) x 64 tokens (2 token tiles per wave), 8 / MW per CU; K in
+// stages of KS 64-K MFMA steps. The kernel does no per-block VALU work, so the matrix cores wait only on memory,
+// and every operand goes global -> LDS (global_load_lds) RB - 1 stages ahead into a ring of RB stage buffers.
+// Each buffer is its own LDS object, and every copy in flight is such a copy, so the compiler's wait before a
+// buffer's reads covers only the copies into that buffer. Stage buffer:
+//   weights  [MW waves][KS steps][64 lanes][16 B]     (lane (r, q) of step kk: block 2kk + q of row r)
+//   headers  [MW waves][256 B]                        (the rows' exponents of the stage's 2·KS blocks)
+//   codes    [KS steps][2 halves][2 planes][64 tokens][16 B] (plane p = bytes 16p..16p+15 of a token's 32, so a
+//                                                      fragment read is 1 KB contiguous over the wave: no bank
+//                                                      conflicts; piece i = (step, half, plane) is copied by
+//                                                      wave i / (4·KS / MW))
+//   scales   [MW waves][256 B]                        (piece i: blocks 4i..4i+3 x 64 tokens, copied by the
+//                                                      waves w with w % (KS / 2) == i into their own slot)
+// Every wave issues the same copies each stage (KS + 4·KS / MW + 2), so the wait for a stage's own copies is one
+// fixed count of later copies; the stage barrier is then a plain s_barrier (a workgroup fence would wait for
+// every copy in flight). Past the end of K the copies re-read the last stage. PLANE selects the hi (0) or lo (1)
+// codes and scales: mode 2 is one launch over hi, mode 1 a second launch over lo that adds its products into C
+// (the first launch applied the call's epilogue).
 namespace mxn {
-constexpr int MW = 8;                                           // waves per workgroup
-constexpr int OA = 0, OH = OA + MW * 4096, OB = OH + MW * 256, OS = OB + 16384, BSTAGE = OS + MW * 256;
-constexpr int UNROLL = 6;                                       // stages per loop trip (two turns of the ring)
+// 4 waves, 256-K stages, two buffers: two workgroups per CU, each a stage ahead (measured against 8 waves with 3
+// buffers, 128-K stages with 3-5 buffers and 2-wave workgroups: fastest at n = 512 and 2048)
+#ifndef JAMHIP_MXN_KS
+#define JAMHIP_MXN_MW 4
+#define JAMHIP_MXN_KS 4
+#define JAMHIP_MXN_RB 2
+#endif
+constexpr int MW = JAMHIP_MXN_MW, KS = JAMHIP_MXN_KS, RB = JAMHIP_MXN_RB;   // waves, steps per stage, buffers
+constexpr int WPC = 8 / MW;                             // workgroups per CU
+constexpr int PPW = 4 * KS / MW;                        // code pieces per wave and stage
+constexpr int NPW = KS + PPW + 2;                       // copies per wave and stage
+constexpr int OA = 0, OH = OA + MW * KS * 1024, OB = OH + MW * 256, OS = OB + 4 * KS * 1024, BSTAGE = OS + MW * 256;
+static_assert(WPC * RB * BSTAGE <= 160 * 1024 && (KS == 2 || KS == 4) && PPW >= 1 && RB >= 2 && RB <= 6, "ring");
 // s_waitcnt with only vmcnt set (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8)
 template <int N> JAMHIP_DEV void wait_vm() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
@@ -161,11 +171,12 @@ template <int N> JAMHIP_DEV void wait_vm() {
 }  // namespace mxn
 
 template <int PLANE>
-__global__ void __launch_bounds__(64 * mxn::MW, 1) mxn_gemm_kernel(WeightView w, MxAct A, int m, int n,
+__global__ void __launch_bounds__(64 * mxn::MW, mxn::WPC) mxn_gemm_kernel(WeightView w, MxAct A, int m, int n,
                                                                    float* __restrict__ c, int ldc, int nrb, int ncb,
                                                                    int64_t tiles, Groups gp, Epi ep) {
     using namespace mxn;
-    __shared__ __align__(1024) unsigned char sb0[BSTAGE], sb1[BSTAGE], sb2[BSTAGE];
+    __shared__ __align__(1024) unsigned char sb0[BSTAGE], sb1[BSTAGE], sb2[RB > 2 ? BSTAGE : 1], sb3[RB > 3 ? BSTAGE : 1],
+        sb4[RB > 4 ? BSTAGE : 1], sb5[RB > 5 ? BSTAGE : 1];
     const int total = nrb * ncb;
     const int lin = tile_of_block(gp.map64 != nullptr, total);
     if (lin >= total) return;
@@ -176,7 +187,7 @@ __global__ void __launch_bounds__(64 * mxn::MW, 1) mxn_gemm_kernel(WeightView w,
     const int lane = threadIdx.x & 63, r = lane & 31, q = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int G = (int) w.G;
-    const int nsg = A.Kp / 256;                         // stages (groups of K)
+    const int nsg = A.Kp / (64 * KS);                   // stages
     int64_t r0t = w.r0 >> 5;
     int slot0 = 0, crow0 = 0, nvalid = n;
     if (gp.map64 != nullptr) {                          // grouped: this slot block's expert
@@ -192,83 +203,100 @@ __global__ void __launch_bounds__(64 * mxn::MW, 1) mxn_gemm_kernel(WeightView w,
     }
     constexpr int NC = group_chunks(MXFP4);
     const int64_t Tw = T0 + wave < tiles ? T0 + wave : tiles - 1;
-    const uint8_t* a_src = w.qs + (r0t + Tw) * G * (NC * CHUNK_STRIDE) + 16 * lane;                // + g·4096
-    const uint8_t* h_src = w.sc + ((r0t + Tw) * G * 32 + (lane >> 1)) * 16 + 4 * (lane & 1);   // + g·512
+    const uint8_t* a_src = w.qs + (r0t + Tw) * G * (NC * CHUNK_STRIDE) + 16 * lane;   // + group · 4096
+    // headers: KS == 4, lane l copies word l % 2 of row l / 2's exponents; KS == 2, lane l word h of row l % 32
+    const uint8_t* h_src = KS == 4 ? w.sc + ((r0t + Tw) * G * 32 + (lane >> 1)) * 16 + 4 * (lane & 1)
+                                   : w.sc + ((r0t + Tw) * G * 32 + r) * 16;
     const int64_t sstep = (int64_t) A.NP * 32;          // bytes per (64-K step, half) plane
-    const int bstep = wave >> 1, bhalf = wave & 1;      // the code piece pair this wave copies
     typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
     floatx16 acc[2] = {floatx16{}, floatx16{}};
-    auto ring = [&](int i) -> unsigned char* { return i == 0 ? sb0 : i == 1 ? sb1 : sb2; };
-    {
-        const uint8_t* codes = PLANE ? A.lo : A.hi;
-        const uint8_t* scales = PLANE ? A.slo : A.shi;
-        auto issue = [&](int s, unsigned char* buf) {
-            const int64_t g = min(s, nsg - 1);
-            const uint8_t* ag = a_src + g * (NC * CHUNK_STRIDE);
+    auto ring = [&](int i) -> unsigned char* {
+        return i == 0 ? sb0 : i == 1 ? sb1 : i == 2 ? sb2 : i == 3 ? sb3 : i == 4 ? sb4 : sb5;
+    };
+    const uint8_t* codes = PLANE ? A.lo : A.hi;
+    const uint8_t* scales = PLANE ? A.slo : A.shi;
+    auto issue = [&](int s, unsigned char* buf) {
+        const int64_t gs = (int64_t) min(s, nsg - 1) * KS;   // the stage's first 64-K step
+        const int64_t g = gs / 4, k4 = gs % 4;                // its group, and step within the group
+        const uint8_t* ag = a_src + g * (NC * CHUNK_STRIDE) + k4 * 2 * CHUNK_STRIDE;
 #pragma unroll
-            for (int kk = 0; kk < 4; kk++)   // chunks 2kk, 2kk + 1: 1 KB contiguous
-                __builtin_amdgcn_global_load_lds(ag + kk * 2 * CHUNK_STRIDE, (lds_void*) (buf + OA + (wave * 4 + kk) * 1024),
-                                                 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(h_src + g * 512, (lds_void*) (buf + OH + wave * 256), 4, 0, 0);
-            const int64_t st = 4 * g + bstep;
+        for (int kk = 0; kk < KS; kk++)   // chunks 2kk, 2kk + 1 of the stage: 1 KB contiguous
+            __builtin_amdgcn_global_load_lds(ag + kk * 2 * CHUNK_STRIDE, (lds_void*) (buf + OA + (wave * KS + kk) * 1024),
+                                             16, 0, 0);
+        __builtin_amdgcn_global_load_lds(h_src + g * 512 + (KS == 2 ? 4 * (k4 >> 1) : 0), (lds_void*) (buf + OH + wave * 256),
+                                         4, 0, 0);
 #pragma unroll
-            for (int pp = 0; pp < 2; pp++)   // lane l: token l's bytes 16pp..16pp+15
-                __builtin_amdgcn_global_load_lds(codes + (2 * st + bhalf) * sstep + (int64_t) (n0 + lane) * 32 + 16 * pp,
-                                                 (lds_void*) (buf + OB + ((2 * bstep + bhalf) * 2 + pp) * 1024), 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(scales + (8 * g + 4 * (wave & 1) + (lane >> 4)) * A.NP + n0 + 4 * (lane & 15),
-                                             (lds_void*) (buf + OS + wave * 256), 4, 0, 0);
-        };
-        issue(0, ring(0));
-        issue(1, ring(1));
-        auto stage = [&](auto U, int s) {
-            constexpr int u = decltype(U)::value;
-            const unsigned char* buf = ring(u % 3);
-            // stage s's eight copies were issued two stages ago and stage s + 1's eight follow them; then every
-            // wave's copies are in, and every wave is done reading the buffer that the next issue overwrites
-            wait_vm<8>();
-            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-            issue(s + 2, ring((u + 2) % 3));
-            // the stage's operands, read up front as 16-byte loads (a 32-byte LDS load is split without the
-            // alias information that keeps the compiler from waiting for every copy in flight)
-            u32x4 av[4];
-            v8i bq[4][2];
-            int sq[4][2];
-            const uint2 hx = *reinterpret_cast<const uint2*>(buf + OH + wave * 256 + 8 * r);
+        for (int i = 0; i < PPW; i++) {
+            const int pc = wave * PPW + i, st = pc >> 2, half = (pc >> 1) & 1, pl = pc & 1;
+            __builtin_amdgcn_global_load_lds(codes + (2 * (gs + st) + half) * sstep + (int64_t) (n0 + lane) * 32 + 16 * pl,
+                                             (lds_void*) (buf + OB + pc * 1024), 16, 0, 0);
+        }
+        const int sp = wave % (KS / 2);
+        __builtin_amdgcn_global_load_lds(scales + (2 * gs + 4 * sp + (lane >> 4)) * A.NP + n0 + 4 * (lane & 15),
+                                         (lds_void*) (buf + OS + wave * 256), 4, 0, 0);
+    };
 #pragma unroll
-            for (int kk = 0; kk < 4; kk++) {
-                av[kk] = *reinterpret_cast<const u32x4*>(buf + OA + (wave * 4 + kk) * 1024 + 16 * lane);
+    for (int s = 0; s < RB - 1; s++) issue(s, ring(s));
+    auto stage = [&](auto U, int s) {
+        constexpr int u = decltype(U)::value;
+        const unsigned char* buf = ring(u);
+        // stage s's copies were issued RB - 1 stages ago and RB - 2 stages' copies follow them; then every wave's
+        // copies are in, and every wave is done reading the buffer that the next issue overwrites
+        wait_vm<(RB - 2) * NPW>();
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        issue(s + RB - 1, ring((u + RB - 1) % RB));
+        // the stage's operands, read up front as 16-byte loads (a 32-byte LDS load is split without the alias
+        // information that keeps the compiler from waiting for every copy in flight)
+        u32x4 av[KS];
+        v8i bq[KS][2];
+        int sq[KS][2];
+        const uint2 hx = KS == 4 ? *reinterpret_cast<const uint2*>(buf + OH + wave * 256 + 8 * r)
+                                 : make_uint2(*reinterpret_cast<const uint32_t*>(buf + OH + wave * 256 + 4 * r), 0u);
 #pragma unroll
-                for (int j = 0; j < 2; j++) {
-                    const u32x4 b0 = *reinterpret_cast<const u32x4*>(buf + OB + ((2 * kk + q) * 128 + 32 * j + r) * 16);
-                    const u32x4 b1 = *reinterpret_cast<const u32x4*>(buf + OB + ((2 * kk + q) * 128 + 64 + 32 * j + r) * 16);
-                    bq[kk][j] = v8i{(int) b0.x, (int) b0.y, (int) b0.z, (int) b0.w, (int) b1.x, (int) b1.y, (int) b1.z,
-                                    (int) b1.w};
-                    // block 2kk + q: wave (2kk + q) / 4's slot, row (2kk + q) % 4 of 64 tokens
-                    sq[kk][j] = buf[OS + ((2 * kk + q) >> 2) * 256 + ((2 * kk + q) & 3) * 64 + 32 * j + r];
+        for (int kk = 0; kk < KS; kk++) {
+            av[kk] = *reinterpret_cast<const u32x4*>(buf + OA + (wave * KS + kk) * 1024 + 16 * lane);
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const u32x4 b0 = *reinterpret_cast<const u32x4*>(buf + OB + ((2 * kk + q) * 128 + 32 * j + r) * 16);
+                const u32x4 b1 = *reinterpret_cast<const u32x4*>(buf + OB + ((2 * kk + q) * 128 + 64 + 32 * j + r) * 16);
+                bq[kk][j] = v8i{(int) b0.x, (int) b0.y, (int) b0.z, (int) b0.w, (int) b1.x, (int) b1.y, (int) b1.z,
+                                (int) b1.w};
+                // block 2kk + q of the stage: scale piece (2kk + q) / 4, row (2kk + q) % 4 of 64 tokens
+                sq[kk][j] = buf[OS + ((2 * kk + q) >> 2) * 256 + ((2 * kk + q) & 3) * 64 + 32 * j + r];
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int kk = 0; kk < KS; kk++) {
+            const u32x4 x = av[kk];
+            const v8i a8 = v8i{(int) x.x, (int) x.y, (int) x.z, (int) x.w, 0, 0, 0, 0};
+            const int sa = (int) (((kk < 2 ? hx.x : hx.y) >> (8 * (2 * (kk & 1) + q))) & 0xffu);
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+                acc[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a8, bq[kk][j], acc[j], 4, 0, 0, sa, 0,
+                                                                         sq[kk][j]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // one turn of the ring per loop trip; a stage past the end of K is skipped (uniform over the workgroup)
+    for (int s = 0; s < nsg; s += RB) {
+        stage(std::integral_constant<int, 0>{}, s);
+        if (s + 1 < nsg) {
+            stage(std::integral_constant<int, 1 % RB>{}, s + 1);
+            if (RB > 2 && s + 2 < nsg) {
+                stage(std::integral_constant<int, 2 % RB>{}, s + 2);
+                if constexpr (RB > 3) {
+                    if (s + 3 < nsg) {
+                        stage(std::integral_constant<int, 3 % RB>{}, s + 3);
+                        if constexpr (RB > 4) {
+                            if (s + 4 < nsg) {
+                                stage(std::integral_constant<int, 4 % RB>{}, s + 4);
+                                if constexpr (RB > 5)
+                                    if (s + 5 < nsg) stage(std::integral_constant<int, 5 % RB>{}, s + 5);
+                            }
+                        }
+                    }
                 }
-            }
-            __builtin_amdgcn_sched_barrier(0);
-            const bool live = s < nsg;   // past the end of K: zero weights, exactly zero products
-#pragma unroll
-            for (int kk = 0; kk < 4; kk++) {
-                const u32x4 x = live ? av[kk] : u32x4{0u, 0u, 0u, 0u};
-                const v8i a8 = v8i{(int) x.x, (int) x.y, (int) x.z, (int) x.w, 0, 0, 0, 0};
-                const int sa = (int) (((kk < 2 ? hx.x : hx.y) >> (8 * (2 * (kk & 1) + q))) & 0xffu);
-#pragma unroll
-                for (int j = 0; j < 2; j++)
-                    acc[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a8, bq[kk][j], acc[j], 4, 0, 0, sa, 0,
-                                                                             sq[kk][j]);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-        };
-        for (int s = 0; s < nsg; s += UNROLL) {
-            stage(std::integral_constant<int, 0>{}, s);
-            stage(std::integral_constant<int, 1>{}, s + 1);
-            stage(std::integral_constant<int, 2>{}, s + 2);
-            if (s + 3 < nsg) {
-                stage(std::integral_constant<int, 3>{}, s + 3);
-                stage(std::integral_constant<int, 4>{}, s + 4);
-                stage(std::integral_constant<int, 5>{}, s + 5);
             }
         }
     }
