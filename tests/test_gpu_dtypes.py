@@ -165,3 +165,26 @@ def test_status_codes_follow_jam(hip, oracle):
     assert st(O.Q1_0, 256, 128) == JAM.OK
     for dt in O.DENSE_TYPES:
         assert st(dt, 7, 7) == JAM.OK and st(dt, 9, 5) == JAM.OK
+
+
+def test_nvfp4_every_scale_code(hip, oracle):
+    """All 256 UE4M3 scale bytes in the weights of every NVFP4 path: one-token decode, the 2..7-token F1 kernel,
+    F1 bands, and the matrix cores (n >= 9). jam reads 0x00 and 0x7F as 0 and otherwise ignores bit 7, so 0x80
+    reads 0 but 0xFF reads 480 (e = 15, m = 7): a decoder that masks bit 7 first and then treats 0x7F as zero
+    gets 0xFF wrong, and this case catches it."""
+    m, k = 64, 256   # 16 sub-blocks per row: 1024 scale bytes, each code 4 times
+    w = oracle.quantize(O.NVFP4, oracle.normal(0x5CA1E, (m, k), 0.0, 0.02)).reshape(m, -1).copy()
+    codes = np.arange(m * 16, dtype=np.uint32) % 256
+    for r in range(m):
+        for j in range(k // 64):
+            w[r, 36 * j:36 * j + 4] = codes[16 * r + 4 * j:16 * r + 4 * j + 4]
+    w = np.ascontiguousarray(w)
+    for n in (1, 3, 7, 8, 16, 64):
+        say(f"nvfp4 every scale code n={n}")
+        a = oracle.outliers(0x5CA + n, (n, k))
+        got = run_mm(hip, O.NVFP4, w, a, m, n, k)
+        ref = oracle.mm(O.NVFP4, w, a, m, n, k)
+        _, sa = oracle.mm_ref(O.NVFP4, w, a, m, n, k)
+        assert np.isfinite(got).all()
+        ok = tier1(got, ref, sa)
+        assert ok.all(), (n, int((~ok).sum()))
