@@ -188,13 +188,14 @@ JAMHIP_DEV int perm8(int j) { return j == 1 ? 2 : j == 2 ? 1 : j == 5 ? 6 : j ==
 
 int gemm_sums_kind(int dt) { return dt == Q4_K || dt == Q5_K || dt == Q4_0 || dt == Q1_0 ? 1 : dt == Q6_K ? 2 : 0; }
 
-// A workgroup takes one token slot at a time (256 threads, a thread per 16-element half of a block, 128
-// blocks per round; at most PREP_GRID workgroups, each looping over its XCD's share of the slots that hold
-// rows): jam's F2 quantization of the slot's activation row (f2_lane's arithmetic, bit-exact; the block's
-// two halves sit in adjacent lanes, which exchange their maxima), each half's codes stored as two 16-byte
-// pieces of GemmAct::b's fragment order, the block scales and per-16 sums parked in LDS together with the
-// row's largest |sum| (SK 1: per-32 xs0 + xs1, jam's fl(xs0 + xs1); SK 2: per-16; SK 0: none); then the
-// slot's power of two from that maximum and the scaled block scales and sums.
+// A workgroup takes a group of SG token slots at a time (256 threads, a thread per 16-element half of a block
+// of one slot, 128 / SG blocks per round; at most PREP_GRID workgroups, each looping over its XCD's share of
+// the groups): jam's F2 quantization of the slots' activation rows (f2_lane's arithmetic, bit-exact; a block's
+// two halves sit SG lanes apart and exchange their maxima), each half's codes stored as two 16-byte pieces of
+// GemmAct::b's fragment order (with SG = 8 the eight slots of a group fill whole 128-byte lines), the block
+// scales and per-16 sums parked in LDS together with each row's largest |sum| (SK 1: per-32 xs0 + xs1, jam's
+// fl(xs0 + xs1); SK 2: per-16; SK 0: none); then each slot's power of two from that maximum and the scaled
+// block scales and sums.
 // Grouped form (gmap non-null): slot t belongs to expert gmap[t / 64] (-1: padding) and holds that
 // expert's row t - gpoff[e] (CSR row goff[e] + t - gpoff[e]) while that is below its row count.
 JAMHIP_DEV int prep_src(int t, int n, const int* gmap, const int* goff, const int* gpoff) {
@@ -208,7 +209,14 @@ JAMHIP_DEV int prep_src(int t, int n, const int* gmap, const int* goff, const in
 template <int CTRL> JAMHIP_DEV float dppf(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
 }
+// lane ^ SG's value (the other half of the thread's block in gemm_prep)
+template <int SG> JAMHIP_DEV float pair_other(float v) {
+    if constexpr (SG == 1) return dppf<0xB1>(v);         // quad_perm [1, 0, 3, 2]
+    else if constexpr (SG == 8) return dppf<0x128>(v);   // row_ror:8 inside 16-lane rows
+    else return __shfl_xor(v, SG);
+}
 constexpr int PREP_MAX_KP = 65536;   // LDS: Kp/32 + Kp/16 floats per slot
+constexpr int PREP_SG_KP = 16384;    // groups of 8 slots up to this Kp (48 KB of LDS)
 constexpr int PREP_GRID = 1024;      // a multiple of 8 (XCDs)
 
 // Exclusive scans of (x, y) over the lanes of the first wave (wide false) or of the 256 lanes of the
@@ -296,60 +304,74 @@ JAMHIP_DEV int fused_scan(const PrepGroups& pg, bool pub, SlotOwner* so) {
 //   1  pairs (e, e + 16) of the 32-block         (MXFP4: a weight byte's two e2m1 codes)
 //   2  pairs (u, u + 8) of each 16-element sub-block, K-step ks = sub-block ks of the block (NVFP4)
 // f1all: jam's F1 quantization for every slot (NVFP4, whose only jam path is F1 at every n, jam.c:662-668).
-template <int SK, int ORD>
+template <int SK, int ORD, int SG>
 __global__ void __launch_bounds__(256) gemm_prep(const float* __restrict__ a, int lda, int n, int k, int Kp, int NP,
                                                  _Float16* __restrict__ bq, float* __restrict__ dx,
                                                  _Float16* __restrict__ shi, _Float16* __restrict__ slo,
                                                  float* __restrict__ es, const int* __restrict__ gmap,
                                                  const int* __restrict__ goff, const int* __restrict__ gpoff, int vec,
                                                  PrepGroups pg, int f1all) {
-    extern __shared__ float lsm[];   // [Kp/32] block scales, [Kp/16] per-16 sums, [4] wave maxima
-    __shared__ int own[2];           // fused grouped mode: the slot's source row and its expert's row count
-    float* ldb = lsm;
-    float* lxs = lsm + (Kp >> 5);
-    float* lmx = lxs + (Kp >> 4);
+    // LDS: per slot of the group [Kp/32] block scales and [Kp/16] per-16 sums, then [4][SG] wave maxima
+    extern __shared__ float lsm[];
+    __shared__ int own[2 * SG];      // fused grouped mode: each slot's source row and its expert's row count
+    const int nbp = Kp >> 5;
+    float* lmx = lsm + SG * 3 * nbp;
     const int nbk = k >> 5, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int s = lane % SG;          // the thread's slot in the group
+    float* ldb = lsm + s * 3 * nbp;   // its block scales and sums
+    float* lxs = ldb + nbp;
     // the slots that can hold rows: [0, n) dense, [0, P) fused grouped (P from the counts), all NP otherwise
     SlotOwner so;
     const int P = pg.counts != nullptr ? fused_scan(pg, blockIdx.x == 0, &so) : gmap != nullptr ? NP : n;
-    // workgroup i runs on XCD i % 8: each XCD takes a contiguous run of P8 slots (a multiple of 8), its
-    // workgroups the run's slots in turn, so that the slots sharing an output line (the codes, block scales and
-    // sums are token-interleaved) are written through one L2
-    const int x = (int) (blockIdx.x % 8), nw = (int) (gridDim.x >> 3), P8 = ((P + 7) / 8 + 7) & ~7;
-    const int t_end = min((x + 1) * P8, P);
-    for (int t = x * P8 + (int) (blockIdx.x >> 3); t < t_end; t += nw) {
+    // workgroup i runs on XCD i % 8: each XCD takes a contiguous run of the groups of SG slots (a multiple of
+    // 8 slots), its workgroups the run's groups in turn, so that slots sharing an output line (the codes, block
+    // scales and sums are token-interleaved) are written through one L2
+    const int G = (P + SG - 1) / SG, rnd = 8 / SG;
+    const int x = (int) (blockIdx.x % 8), nw = (int) (gridDim.x >> 3), PG8 = ((G + 7) / 8 + rnd - 1) / rnd * rnd;
+    const int g_end = min((x + 1) * PG8, G);
+    for (int g = x * PG8 + (int) (blockIdx.x >> 3); g < g_end; g += nw) {
+        const int t0 = g * SG, t = t0 + s;
         // fused grouped mode (counts on the device): F1 codes for an expert of 1..7 rows, else F2
-        bool f1 = f1all != 0;
-        int src;
+        int src, cnt = 8;
         if (pg.counts != nullptr) {
-            if (so.a64 > 0 && t >= so.p64 && t < so.p64 + so.a64) {   // exactly one owner for t < P
-                own[0] = t - so.p64 < so.c ? so.oc + (t - so.p64) : -1;
-                own[1] = so.c;
+#pragma unroll
+            for (int i = 0; i < SG; i++) {
+                const int ti = t0 + i;
+                if (so.a64 > 0 && ti >= so.p64 && ti < so.p64 + so.a64) {   // exactly one owner for ti < P
+                    own[2 * i] = ti - so.p64 < so.c ? so.oc + (ti - so.p64) : -1;
+                    own[2 * i + 1] = so.c;
+                }
             }
             __syncthreads();
-            src = own[0];
-            f1 = f1 || own[1] < 8;
+            src = t < P ? own[2 * s] : -1;
+            cnt = own[2 * s + 1];
         } else {
             src = prep_src(t, n, gmap, goff, gpoff);
         }
-        // a padding slot (past n, or past its expert's rows) is left unwritten: the GEMM's token column for it
-        // is computed but never stored, and no other column reads it
-        if (src >= 0) {
-            const int hh = lane & 1;   // which half of its block the lane holds
+        const bool f1 = f1all != 0 || (pg.counts != nullptr && cnt < 8);
+        // one slot: its padding leaves it unwritten (the GEMM's token column for it is computed but never stored,
+        // and no other column reads it); in a group of 8 every slot is written, a padding slot as a zero row, so
+        // that each store covers whole 128-byte lines, and a group of padding slots only is skipped
+        bool any = src >= 0;
+        if (SG > 1) any = __syncthreads_or(any);
+        if (any) {
+            const int hh = (lane / SG) & 1;   // which half of its block the thread holds
             float m2 = 0.0f;
             typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-            // one 16-element half of one block per lane (lanes 2b', 2b' + 1 hold a block): 128 blocks per round
-            // of the workgroup, two rounds' loads in flight; blocks past k (up to Kp) quantize zeros
-            const int nbp = Kp >> 5;
-            const float* row = a + (int64_t) src * lda;
-            for (int r0 = threadIdx.x >> 1; r0 < nbp; r0 += 256) {
-                float xr[2][16];
+            // one 16-element half of one block per thread (the threads of slot s, 256 / SG of them, hold
+            // consecutive halves; a block's two halves sit SG lanes apart): 128 / SG blocks per round of the
+            // workgroup, two rounds' loads in flight (more measured no faster); blocks past k (up to Kp)
+            // quantize zeros
+            constexpr int BPR = 128 / SG, NU = 2;
+            const float* row = a + (int64_t) (src >= 0 ? src : 0) * lda;
+            for (int r0 = threadIdx.x / (2 * SG); r0 < nbp; r0 += NU * BPR) {
+                float xr[NU][16];
 #pragma unroll
-                for (int u = 0; u < 2; u++) {
-                    const int b = r0 + 128 * u;
+                for (int u = 0; u < NU; u++) {
+                    const int b = r0 + BPR * u;
 #pragma unroll
                     for (int i = 0; i < 16; i++) xr[u][i] = 0.0f;
-                    if (b < nbk && ORD == 2) {   // elements 4hh.., 8+4hh.., 16+4hh.., 24+4hh.. (4 each)
+                    if (b < nbk && src >= 0 && ORD == 2) {   // elements 4hh.., 8+4hh.., 16+4hh.., 24+4hh.. (4 each)
                         const float* p0 = row + 32 * b + 4 * hh;
 #pragma unroll
                         for (int v = 0; v < 4; v++) {
@@ -361,7 +383,7 @@ __global__ void __launch_bounds__(256) gemm_prep(const float* __restrict__ a, in
                                 for (int i = 0; i < 4; i++) xr[u][4 * v + i] = p0[8 * v + i];
                             }
                         }
-                    } else if (b < nbk) {
+                    } else if (b < nbk && src >= 0) {
                         // ORD 1: elements 8hh..8hh+7 and 16+8hh..16+8hh+7 (the order the GEMM pairs them in); else
                         // 16hh..16hh+15
                         constexpr bool MXO = ORD == 1;
@@ -384,14 +406,14 @@ __global__ void __launch_bounds__(256) gemm_prep(const float* __restrict__ a, in
                     }
                 }
 #pragma unroll
-                for (int u = 0; u < 2; u++) {
-                    const int b = r0 + 128 * u;
-                    if (b >= nbp) break;   // lane pairs stay together: b is the same for both lanes of a block
+                for (int u = 0; u < NU; u++) {
+                    const int b = r0 + BPR * u;
+                    if (b >= nbp) break;   // the two halves of a block stay together: b is the same for both
                     const float* x = xr[u];
                     float mx = 0.0f;
 #pragma unroll
                     for (int i = 0; i < 16; i++) mx = fmaxf(mx, fabsf(x[i]));
-                    mx = fmaxf(mx, dppf<0xB1>(mx));   // the block's other half (lane ^ 1)
+                    mx = fmaxf(mx, pair_other<SG>(mx));   // the block's other half
                     const float db = mx / 127.0f;
                     float qf[16];
                     if (f1) {
@@ -409,7 +431,7 @@ __global__ void __launch_bounds__(256) gemm_prep(const float* __restrict__ a, in
                             qf[i] = ok ? fminf(fmaxf(rintf(p), -128.0f), 127.0f) : -128.0f;
                         }
                     }
-                    // the lane's two (K-step, half) planes: 8 f16 (16 bytes) each at the slot
+                    // the thread's two (K-step, half) planes: 8 f16 (16 bytes) each at the slot
 #pragma unroll
                     for (int ks = 0; ks < 2; ks++) {
                         half8 hv;
@@ -429,7 +451,7 @@ __global__ void __launch_bounds__(256) gemm_prep(const float* __restrict__ a, in
                         float s16 = 0.0f;
 #pragma unroll
                         for (int i = 0; i < 16; i++) s16 += qf[i];   // exact: |Σ| <= 2048
-                        const float s32 = s16 + dppf<0xB1>(s16);
+                        const float s32 = s16 + pair_other<SG>(s16);
                         const float xs = SK == 1 ? s32 * db : s16 * db;
                         lxs[2 * b + hh] = SK == 1 && hh == 1 ? 0.0f : xs;
                         m2 = fmaxf(m2, fabsf(xs));
@@ -444,44 +466,54 @@ __global__ void __launch_bounds__(256) gemm_prep(const float* __restrict__ a, in
                         s8[1] = s8[1] + s8[3];
                         const float xs16 = s8[0] + s8[1];
                         lxs[2 * b + hh] = xs16;
-                        const float other = dppf<0xB1>(xs16);   // the block's other half
+                        const float other = pair_other<SG>(xs16);   // the block's other half
                         m2 = fmaxf(m2, SK == 1 ? fabsf(hh == 0 ? xs16 + other : other + xs16) : fabsf(xs16));
                     }
                 }
             }
-            if constexpr (SK != 0) {
+            if constexpr (SK != 0) {   // each slot's largest |sum| over its threads (lanes s, s + SG, ...)
 #pragma unroll
-                for (int o = 32; o > 0; o >>= 1) m2 = fmaxf(m2, __shfl_xor(m2, o));
-                if (lane == 0) lmx[wave] = m2;
+                for (int o = 32; o >= SG; o >>= 1) m2 = fmaxf(m2, __shfl_xor(m2, o));
+                if (lane < SG) lmx[wave * SG + lane] = m2;
             }
             __syncthreads();
-            // the slot's power of two: the largest |sum| lands in [2^13, 2^14); zero or non-finite sums keep 2^0
-            int ex = 0;
-            if constexpr (SK != 0) {
-                const float mx = fmaxf(fmaxf(lmx[0], lmx[1]), fmaxf(lmx[2], lmx[3]));
-                if (mx > 0.0f && mx <= 3.0e38f) {
-                    frexpf(mx, &ex);
-                    ex -= 14;
+            // a slot's power of two: the largest |sum| lands in [2^13, 2^14); zero or non-finite sums keep 2^0
+            auto slot_exp = [&](int sl) {
+                int ex = 0;
+                if constexpr (SK != 0) {
+                    const float mx = fmaxf(fmaxf(lmx[sl], lmx[SG + sl]), fmaxf(lmx[2 * SG + sl], lmx[3 * SG + sl]));
+                    if (mx > 0.0f && mx <= 3.0e38f) {
+                        frexpf(mx, &ex);
+                        ex -= 14;
+                    }
                 }
-            }
-            const float down = ldexpf(1.0f, -ex);
-            if (threadIdx.x == 0) es[t] = ldexpf(1.0f, ex);
+                return ex;
+            };
+            if (threadIdx.x < SG && (SG > 1 || src >= 0)) es[t0 + threadIdx.x] = ldexpf(1.0f, slot_exp(threadIdx.x));
             auto put = [&](int64_t o, float v) {
                 const F16Pair p = split_f16(v);
                 shi[o] = p.hi;
                 slo[o] = p.lo;
             };
-            for (int b = threadIdx.x; b < (Kp >> 5); b += 256) {
-                dx[(int64_t) b * NP + t] = ldb[b] * down;
-                const float x0 = lxs[2 * b], x1 = lxs[2 * b + 1];
-                if constexpr (SK == 1) put(((int64_t) (b >> 3) * NP + t) * 8 + (b & 7), (x0 + x1) * down);
-                if constexpr (SK == 2) {
-                    put(((int64_t) (b >> 3) * NP + t) * 16 + 2 * (b & 7), x0 * down);
-                    put(((int64_t) (b >> 3) * NP + t) * 16 + 2 * (b & 7) + 1, x1 * down);
+            // block scales and sums of the group's slots, consecutive threads on consecutive slots (dx) or on
+            // consecutive entries of a slot's 8 / 16 sums (shi, slo)
+            for (int i = threadIdx.x; i < nbp * SG; i += 256) {
+                const int sl = i % SG, b = i / SG;
+                dx[(int64_t) b * NP + t0 + sl] = lsm[sl * 3 * nbp + b] * ldexpf(1.0f, -slot_exp(sl));
+            }
+            if constexpr (SK != 0) {
+                constexpr int NS = SK == 1 ? 8 : 16;   // sums per slot and group of 8 blocks
+                for (int i = threadIdx.x; i < (nbp / 8) * SG * NS; i += 256) {
+                    const int c = i % NS, sl = (i / NS) % SG, gb = i / (NS * SG);
+                    const float* xs = lsm + sl * 3 * nbp + nbp;
+                    const float down = ldexpf(1.0f, -slot_exp(sl));
+                    const int64_t o = ((int64_t) gb * NP + t0 + sl) * NS + c;
+                    if constexpr (SK == 1) put(o, (xs[2 * (8 * gb + c)] + xs[2 * (8 * gb + c) + 1]) * down);
+                    else put(o, xs[2 * (8 * gb) + c] * down);
                 }
             }
         }
-        __syncthreads();   // the LDS (and own) is the next slot's
+        __syncthreads();   // the LDS (and own) is the next group's
     }
 }
 
@@ -514,29 +546,41 @@ static hipError_t prep_np(int dt, const float* a, int lda, int n, int NP, int k,
     *out = GemmAct{bq, dx, shi, slo, es, NP, Kp, k};
     if (NP <= 0) return hipSuccess;
     const int vec = ((reinterpret_cast<uintptr_t>(a) & 15) == 0 && (lda & 3) == 0) ? 1 : 0;
-    const size_t lds = ((size_t) (Kp / 32) + (size_t) (Kp / 16) + 4) * sizeof(float);
     const int kind = dt == MXFP4 ? 3 : dt == NVFP4 ? 4 : sk;
     const int f1all = dt == NVFP4;
-    // at most PREP_GRID workgroups (all resident), each looping over its XCD's slots
-    const unsigned grid = (unsigned) (NP < PREP_GRID ? NP : PREP_GRID);
-    const void* fn = kind == 1 ? (const void*) gemm_prep<1, 0> : kind == 2 ? (const void*) gemm_prep<2, 0>
-                   : kind == 3 ? (const void*) gemm_prep<0, 1> : kind == 4 ? (const void*) gemm_prep<0, 2>
-                   : (const void*) gemm_prep<0, 0>;
+    // groups of 8 slots (every code store a whole 128-byte line) when that still gives a workgroup per CU
+    const int sg = NP >= 8 * 256 && Kp <= PREP_SG_KP ? 8 : 1;
+    const size_t lds = ((size_t) sg * 3 * (Kp / 32) + 4 * sg) * sizeof(float);
+    // at most PREP_GRID workgroups (all resident), each looping over its XCD's groups
+    const int ng = NP / sg;
+    const unsigned grid = (unsigned) (ng < PREP_GRID ? ng : PREP_GRID);
+    const void* fn;
+#define JAMHIP_PREP_FN(SG) \
+    fn = kind == 1 ? (const void*) gemm_prep<1, 0, SG> : kind == 2 ? (const void*) gemm_prep<2, 0, SG> \
+       : kind == 3 ? (const void*) gemm_prep<0, 1, SG> : kind == 4 ? (const void*) gemm_prep<0, 2, SG> \
+       : (const void*) gemm_prep<0, 0, SG>
+    if (sg == 8) JAMHIP_PREP_FN(8);
+    else JAMHIP_PREP_FN(1);
+#undef JAMHIP_PREP_FN
     // the LDS limit is raised once per kernel; threads racing here both set the same value
-    static std::atomic<bool> attr[5];
-    if (!attr[kind].load(std::memory_order_acquire)) {
-        const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                 (int) ((PREP_MAX_KP / 32 + PREP_MAX_KP / 16 + 4) * sizeof(float)));
+    static std::atomic<bool> attr[2][5];
+    if (!attr[sg == 8][kind].load(std::memory_order_acquire)) {
+        const size_t mx = sg == 8 ? (size_t) 8 * 3 * (PREP_SG_KP / 32) + 32 : (size_t) 3 * (PREP_MAX_KP / 32) + 4;
+        const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int) (mx * sizeof(float)));
         if (e != hipSuccess) return e;
-        attr[kind].store(true, std::memory_order_release);
+        attr[sg == 8][kind].store(true, std::memory_order_release);
     }
-#define JAMHIP_PREP(SK, ORD) gemm_prep<SK, ORD><<<grid, 256, lds, st>>>(a, lda, n, k, Kp, NP, bq, dx, shi, slo, es, gmap, \
-                                                                   goff, gpoff, vec, pg, f1all)
-    if (kind == 1) JAMHIP_PREP(1, 0);
-    else if (kind == 2) JAMHIP_PREP(2, 0);
-    else if (kind == 3) JAMHIP_PREP(0, 1);
-    else if (kind == 4) JAMHIP_PREP(0, 2);
-    else JAMHIP_PREP(0, 0);
+#define JAMHIP_PREP(SK, ORD, SG) gemm_prep<SK, ORD, SG><<<grid, 256, lds, st>>>(a, lda, n, k, Kp, NP, bq, dx, shi, slo, es, \
+                                                                           gmap, goff, gpoff, vec, pg, f1all)
+#define JAMHIP_PREP_SG(SG)                      \
+    if (kind == 1) JAMHIP_PREP(1, 0, SG);       \
+    else if (kind == 2) JAMHIP_PREP(2, 0, SG);  \
+    else if (kind == 3) JAMHIP_PREP(0, 1, SG);  \
+    else if (kind == 4) JAMHIP_PREP(0, 2, SG);  \
+    else JAMHIP_PREP(0, 0, SG)
+    if (sg == 8) { JAMHIP_PREP_SG(8); }
+    else { JAMHIP_PREP_SG(1); }
+#undef JAMHIP_PREP_SG
 #undef JAMHIP_PREP
     return hipGetLastError();
 }
