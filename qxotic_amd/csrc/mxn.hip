@@ -201,6 +201,9 @@ __global__ void __launch_bounds__(64 * mxn::MW, mxn::WPC) mxn_gemm_kernel(Weight
         nvalid = __builtin_amdgcn_readfirstlane(gp.off[e + 1]) - crow0;
         if (gp.bias != nullptr) ep.bias = gp.bias + (int64_t) e * gp.gm;
     }
+    // valid tokens of this slot block all in its first 32 slots: the second token tile is neither copied nor
+    // computed (its epilogue stores nothing either)
+    const bool half = nvalid - (n0 - slot0) <= 32;
     constexpr int NC = group_chunks(MXFP4);
     const int64_t Tw = T0 + wave < tiles ? T0 + wave : tiles - 1;
     const uint8_t* a_src = w.qs + (r0t + Tw) * G * (NC * CHUNK_STRIDE) + 16 * lane;   // + group · 4096
@@ -227,9 +230,10 @@ __global__ void __launch_bounds__(64 * mxn::MW, mxn::WPC) mxn_gemm_kernel(Weight
                                          4, 0, 0);
 #pragma unroll
         for (int i = 0; i < PPW; i++) {
-            const int pc = wave * PPW + i, st = pc >> 2, half = (pc >> 1) & 1, pl = pc & 1;
-            __builtin_amdgcn_global_load_lds(codes + (2 * (gs + st) + half) * sstep + (int64_t) (n0 + lane) * 32 + 16 * pl,
-                                             (lds_void*) (buf + OB + pc * 1024), 16, 0, 0);
+            const int pc = wave * PPW + i, st = pc >> 2, hf = (pc >> 1) & 1, pl = pc & 1;
+            if (!half || lane < 32)
+                __builtin_amdgcn_global_load_lds(codes + (2 * (gs + st) + hf) * sstep + (int64_t) (n0 + lane) * 32 + 16 * pl,
+                                                 (lds_void*) (buf + OB + pc * 1024), 16, 0, 0);
         }
         const int sp = wave % (KS / 2);
         __builtin_amdgcn_global_load_lds(scales + (2 * gs + 4 * sp + (lane >> 4)) * A.NP + n0 + 4 * (lane & 15),
@@ -271,10 +275,10 @@ __global__ void __launch_bounds__(64 * mxn::MW, mxn::WPC) mxn_gemm_kernel(Weight
             const u32x4 x = av[kk];
             const v8i a8 = v8i{(int) x.x, (int) x.y, (int) x.z, (int) x.w, 0, 0, 0, 0};
             const int sa = (int) (((kk < 2 ? hx.x : hx.y) >> (8 * (2 * (kk & 1) + q))) & 0xffu);
-#pragma unroll
-            for (int j = 0; j < 2; j++)
-                acc[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a8, bq[kk][j], acc[j], 4, 0, 0, sa, 0,
-                                                                         sq[kk][j]);
+            acc[0] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a8, bq[kk][0], acc[0], 4, 0, 0, sa, 0, sq[kk][0]);
+            if (!half)
+                acc[1] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a8, bq[kk][1], acc[1], 4, 0, 0, sa, 0,
+                                                                         sq[kk][1]);
         }
         __builtin_amdgcn_sched_barrier(0);
     };
