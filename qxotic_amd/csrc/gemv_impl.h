@@ -935,9 +935,12 @@ static bool mv_items(int k, int* items) {
 
 // Split K: from k = 2·GEMV_SLICE on and for 2 or more tokens, the workgroups of a band take GEMV_SLICE-element
 // slices of k (grid z) so that a block keeps 32-row bands and its slice of every token's activations fits
-// LDS; partials are summed after. One token's activations fit unsplit (measured faster unsplit).
-constexpr int GEMV_SLICE = 4096;
-inline int gemv_slice(int k, int n) { return n >= 2 && k >= 2 * GEMV_SLICE ? GEMV_SLICE : k; }
+// LDS; partials are summed after. One token's activations fit unsplit (measured faster unsplit) up to
+// k = 65536, the most a row band holds (mv_items); past that one token takes slices of GEMV_SLICE1.
+constexpr int GEMV_SLICE = 4096, GEMV_SLICE1 = 32768, GEMV_K1_MAX = 65536;
+inline int gemv_slice(int k, int n) {
+    return n >= 2 && k >= 2 * GEMV_SLICE ? GEMV_SLICE : n == 1 && k > GEMV_K1_MAX ? GEMV_SLICE1 : k;
+}
 
 // ks: elements per K slice (= k unsplit); cz: floats between the slices' partial outputs; NWV: waves per
 // workgroup.
@@ -951,7 +954,7 @@ static void launch_shape(int k, int ks, int64_t cz, int m, int n, const WeightVi
     const dim3 grid((unsigned) ((bands + QB - 1) / QB), (n + NT - 1) / NT, (unsigned) ((k + ks - 1) / ks));
     const size_t lds = (size_t) NWV * ITEMS * 64 * NT * sizeof(float) +
                        (HP > 0 ? 32 + fuse_lds(NT, ks, f16_pairs<DT, FL, NT, HP>()) : 0);
-    if constexpr (NT >= 2) {   // only calls with 2 or more tokens split K
+    {   // split K (2 or more tokens from k = 8192, one token past k = 65536)
         if (ks < k) {
             lds_allow((const void*) mv_kernel<DT, FL, NT, HP, RB, ITEMS, false, true, NWV>, lds);
             mv_kernel<DT, FL, NT, HP, RB, ITEMS, false, true, NWV><<<grid, 64 * NWV, lds, st>>>(

@@ -411,7 +411,8 @@ jamhip_status scratch_fail(jamhip_ctx* ctx, const Scratch& sc, hipError_t e, con
 
 // Quantize A (device, f32 [n][lda]) and run the matmul into C (device, [n][ldc]). Decode-sized calls
 // with k < 8192 are one fused launch and touch no scratch (safe under stream capture once W is pinned);
-// from k = 8192 the decode kernels split K and sum the slices from the context's split buffer.
+// from k = 8192 (one token: past k = 65536) the decode kernels split K and sum the slices from the context's
+// split buffer.
 jamhip_status compute(jamhip_ctx* ctx, Scratch& sc, int dt, WeightView wv, const float* a, int lda, float* c,
                       int ldc, int m, int n, int k, const Epi& ep = Epi{}) {
     hipError_t e;

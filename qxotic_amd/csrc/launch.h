@@ -71,8 +71,9 @@ JAMHIP_DEV int grouped_tile(const Groups& gp, int lin, int nrb, int* rb, int* cb
 // every n). flavour 1: n in [1, 7], F1 activations; with `a` non-null the kernel quantizes A itself (requires
 // gemv_fusable(n, k)), else it reads A's quantized copy from `A`. flavour 2: any n >= 1, F2
 // activations from `A`, 8 tokens per grid row. From k = 8192 on, for n >= 2, the kernel splits K into
-// 4096-element slices: `part` must then hold gemv_split_floats(k, m, n) floats (the slices' partial
-// results, summed into c in slice order); gemv_split_floats is 0 otherwise and part may be null.
+// 4096-element slices, and past k = 65536 for n = 1 into 32768-element slices: `part` must then hold
+// gemv_split_floats(k, m, n) floats (the slices' partial results, summed into c in slice order);
+// gemv_split_floats is 0 otherwise and part may be null.
 bool gemv_fusable(int n, int k, const float* a, int lda);   // a, lda: the f32 activations (16-byte aligned rows)
 size_t gemv_split_floats(int k, int m, int n);
 hipError_t launch_gemv(int dt, int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k, int m,

@@ -307,6 +307,45 @@ def test_split_k_decode(hip, oracle, dt):
 
 
 @pytest.mark.parametrize("dt", O.ALL_QUANT_TYPES)
+def test_past_k_65536(hip, oracle, dt):
+    """jam takes any k. One token past k = 65536 (the most one row band holds) splits K into 32768-element
+    slices summed in slice order; 2..7 tokens take 4096-element slices, 8 and more the F2 path the matrix cores
+    decline to (their prep holds k <= 65536). A partial last slice (for the types with blocks below 256 also a
+    partial last group), F1 quantized in the kernel and, with rows that are not 16-byte aligned, read from the
+    quantized copy; ldc gap untouched, rerun bit-identical."""
+    import torch
+    from qxotic_amd.jam import JAM, Segment
+    be = O.BLOCK[dt][0]
+    m, k = 48, 65536 + 8192 + (be if be < 256 else 256)
+    w = oracle.quantize(dt, oracle.normal(0x5A11C0DE ^ 0x6B ^ dt, (m, k), 0.0, 0.02))
+    for n in (1, 3, 8, 17):
+        a = oracle.outliers(3200 + 16 * dt + n, (n, k))
+        say(f"past k 65536: {O.NAMES[dt]} m={m} n={n} k={k}")
+        got = run_mm(hip, dt, w, a, m, n, k, ldc=m + 3)
+        assert (got[:, m:] == 0.0).all()
+        ref = oracle.mm_int8(dt, w, a, m, n, k)
+        _, sa = oracle.mm_ref(dt, w, a, m, n, k)
+        ok = tier1(got[:, :m], ref, sa)
+        assert ok.all(), (O.NAMES[dt], n, float(np.max(np.abs(got[:, :m] - ref) / (np.abs(ref) + 1e-30))))
+        assert np.array_equal(bits(run_mm(hip, dt, w, a, m, n, k, ldc=m + 3)), bits(got))
+    a = oracle.outliers(3200 + 16 * dt + 1, (1, k))
+    ref = oracle.mm_int8(dt, w, a, m, 1, k)
+    _, sa = oracle.mm_ref(dt, w, a, m, 1, k)
+    assert hip.pin(Segment.of(w), dt, k, m) == JAM.OK, hip.last_error()
+    try:
+        a_pad = np.zeros((1, k + 1), np.float32)
+        a_pad[:, :k] = a
+        a_dev = torch.from_numpy(a_pad).cuda()
+        c_dev = torch.zeros((1, m), dtype=torch.float32, device="cuda")
+        st = hip.mm_device(Segment.of(w), dt, k, a_dev.data_ptr(), k + 1, c_dev.data_ptr(), m, m, 1, k)
+        assert st == JAM.OK, hip.last_error()
+        hip.synchronize()
+        assert tier1(c_dev.cpu().numpy(), ref, sa).all()
+    finally:
+        assert hip.evict(Segment.of(w)) == JAM.OK
+
+
+@pytest.mark.parametrize("dt", O.ALL_QUANT_TYPES)
 def test_decode_fused_prologue_matches_quantized_copy(hip, oracle, dt):
     """1..7 tokens: rows the kernel can load as 16-byte pieces are quantized in each workgroup's prologue (MXFP4
     and NVFP4 with one token: into f16 pairs for the hardware e2m1 conversion and v_dot2), rows that are not
