@@ -1028,20 +1028,32 @@ static hipError_t go_hp(int k, int ks, int64_t cz, int m, int n, const WeightVie
     return hipGetLastError();
 }
 
-// Waves per workgroup for one token: 8, or 4 when the 8-wave grid would leave CUs idle (fewer than 256
-// workgroups, e.g. 4096 rows at k = 4096) and k <= 4096 (two items per row band). Measured: Q8_0 4096x4096
-// 5.85 -> 5.43 us, MXFP4 2880x2880 5.42 -> 4.54 us; the 14336-row shapes stay faster with 8 waves, and
-// 2-wave workgroups on the smaller grids were slower still (MXFP4 2880x2880 6.1 us).
-// A row band of J items that does not divide 8 (J = 3, 5, 6, 7: k up to 6144, 10240, 12288, 14336, e.g.
-// Llama's FFN down projection at 14336) takes workgroups of J·floor(8 / J) waves: with 8, the spare waves
-// only re-read the next band's weights (measured at k = 14336: Q6_K 4096x14336 12.9 -> 12.1 us).
+// Waves per workgroup for one token. A row band of J items that does not divide 8 (J = 3, 5, 6, 7: k up to
+// 6144, 10240, 12288, 14336, e.g. Llama's FFN down projection at 14336) takes workgroups of J·floor(8 / J)
+// waves: with 8, the spare waves only re-read the next band's weights (measured at k = 14336: Q6_K 4096x14336
+// 12.9 -> 12.1 us). With one or two items per band (k <= 4096) a workgroup of 4 or 8 waves holds 4 / J or
+// 8 / J bands; the one whose last partial round of workgroups over the CUs is fuller (workgroups / CUs over
+// its ceiling) wins, and on a tie 8 waves, unless both fill every round (then 4). Q4_K at k = 4096, graph-timed
+// (4 / 8 waves, us): 4096 rows 4.04 / 4.37, 6144 5.30 / 4.88, 10240 6.53 / 6.85, 14336 7.99 / 7.46, 20480
+// 9.94 / 10.32, 28672 12.59 / 13.25, 57344 22.2 / 23.7; MXFP4 5760x2880 5.66 / 5.48; 12, 14 and 16 waves
+// and 2 items per wave were slower everywhere. JAM_HIP_MV_WAVES overrides (tuning sweeps).
 static int one_token_waves(int k, int m) {
     int items;
     if (!mv_items(k, &items) || items != 1) return MV_WAVES;
     const int Gk = (k / 32 + 7) / 8, J = (Gk + 64 / MV_RB - 1) / (64 / MV_RB);
     const int64_t bands = ((int64_t) m + MV_RB - 1) / MV_RB;
+    if (const char* v = getenv("JAM_HIP_MV_WAVES")) {
+        const int x = atoi(v);
+        if (x >= 4 && x <= 8 && x % J == 0) return x;
+    }
     if (J == 3 || J == 5 || J == 6 || J == 7) return J * (MV_WAVES / J);
-    return J <= 2 && (bands + MV_WAVES / J - 1) / (MV_WAVES / J) < 256 ? 4 : MV_WAVES;
+    if (J > 2) return MV_WAVES;
+    const int64_t cus = device_cus() >= 8 ? device_cus() : 256;
+    const int64_t w4 = (bands + 4 / J - 1) / (4 / J), w8 = (bands + 8 / J - 1) / (8 / J);
+    const int64_t r4 = (w4 + cus - 1) / cus, r8 = (w8 + cus - 1) / cus;   // rounds
+    // fullness w / (r·cus), compared without division
+    if (w4 * r8 != w8 * r4) return w4 * r8 > w8 * r4 ? 4 : 8;
+    return w4 == r4 * cus && w8 == r8 * cus ? 4 : 8;
 }
 
 template <int DT, int NWV>

@@ -125,7 +125,9 @@ bool gemm_prep_fits(int k);
 // pinned host memory); hipErrorInvalidValue otherwise
 hipError_t launch_stage_copy(const void* src, void* dst, size_t bytes, hipStream_t st);
 // Caches device dev's CU count for the matrix-core GEMM's last-round balancing (called at context creation).
-void gemm_tail_prime(int dev);   // the activation prep holds a slot's block scales and sums in LDS
+void gemm_tail_prime(int dev);
+int device_cus();   // CUs of the current device (gemm_tail_prime's record; 0 before it)
+   // the activation prep holds a slot's block scales and sums in LDS
 hipError_t launch_gemm_prep(int dt, const float* a, int lda, int n, int k, void* scratch, GemmAct* out,
                             hipStream_t st);
 // Matrix-core GEMM over GemmAct (f16 MFMA on exact integer operands); hipErrorNotSupported for dtypes it

@@ -1000,6 +1000,11 @@ void gemm_tail_prime(int dev) {
     if (dev >= 0 && dev < 64 && hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
         g_cus[dev].store(n, std::memory_order_relaxed);
 }
+int device_cus() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    return g_cus[dev].load(std::memory_order_relaxed);
+}
 static int tail_split(int total) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
