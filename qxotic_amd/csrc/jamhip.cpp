@@ -944,6 +944,21 @@ jamhip_status mm_grouped_ex_impl(jamhip_ctx* ctx, const void* w, int wt, int ldw
     // slot map from the device counts and quantizes every expert's rows (F1 for experts of 1..7 rows, whose
     // 64-slot blocks then take the GEMM's single-token-tile form), so neither the offsets kernel nor the F1
     // decode launch runs. Sparser calls keep the F1 decode kernel for their small experts.
+    // Native-MX mode, the same density: one prep launch (expert table from the counts, MX-FP8 codes of every
+    // expert's rows) and the native GEMM over every expert, those with fewer than 8 rows included.
+    if (rows_cap >= 8 * E && E <= PREP_FUSED_MAX_E && m % 32 == 0 && wt == MXFP4 && ctx->mx_native &&
+        mma_path(wt, k, wv)) {
+        const PrepGroups pg{(const int*) counts_dev, E, rows_cap, off, poff64, map64, cap64, (int*) offsets_dev};
+        const Groups g{off, poff8, map8, poff64, map64, m, static_cast<const float*>(bias_dev)};
+        MxAct X;
+        if ((e = ctx->gact.ensure(mx_act_bytes_np(cap64 * 64, k))) != hipSuccess)
+            return hip_fail(ctx, e, "grouped: mx activation scratch alloc");
+        if ((e = launch_mx_prep_grouped_fused(a, lda, k, ctx->mx_native, pg, ctx->gact.p, &X, ctx->stream)) !=
+                hipSuccess ||
+            (e = launch_mx_gemm_grouped(ctx->mx_native, wv, X, g, cap64, c, ldc, ctx->stream)) != hipSuccess)
+            return hip_fail(ctx, e, "grouped: mx gemm launch");
+        return JAMHIP_OK;
+    }
     if (rows_cap >= 8 * E && E <= PREP_FUSED_MAX_E && m % 32 == 0 && !(wt == MXFP4 && ctx->mx_native) &&
         mma_exact(ctx, wt, k, wv)) {
         const PrepGroups pg{(const int*) counts_dev, E, rows_cap, off, poff64, map64, cap64, (int*) offsets_dev};

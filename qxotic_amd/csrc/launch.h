@@ -193,12 +193,19 @@ struct PrepGroups {
     int *off, *poff64, *map64;
     int cap64;
     int* off_out;
+    // gathered input: CSR row r of A is row rows[r] / rdiv of the activations (null: row r)
+    const int* rows = nullptr;
+    int rdiv = 1;
 };
 constexpr int PREP_FUSED_MAX_E = 256;
 hipError_t launch_gemm_prep_grouped_fused(int dt, const float* a, int lda, int k, const PrepGroups& pg,
                                           void* scratch, GemmAct* out, hipStream_t st);
 hipError_t launch_gemm_prep_grouped(int dt, const float* a, int lda, int k, const Groups& g, int cap64,
                                     void* scratch, GemmAct* out, hipStream_t st);
+// The native-MX prep (mxn.hip) for a grouped call that derives its expert table from the device counts in
+// the same way: also writes pg's offsets, 64-slot offsets and slot map.
+hipError_t launch_mx_prep_grouped_fused(const float* a, int lda, int k, int mode, const PrepGroups& pg, void* scratch,
+                                        MxAct* out, hipStream_t st);
 
 // MoE bookkeeping (moe.hip)
 // small[0..n1): the experts with exactly one row, small[n1..n1 + n2): those with 2..7 rows, each list in expert

@@ -22,6 +22,7 @@
 // are used as stored, and the activation codes are written in that element order.
 #include "common.h"
 #include "launch.h"
+#include "groups.h"
 
 #include <atomic>
 #include <type_traits>
@@ -44,86 +45,105 @@ JAMHIP_DEV int slot_source(int t, int n, const int* gmap, const int* goff, const
 
 }  // namespace mxn
 
-// One workgroup of 256 threads per token slot, eight lanes per 32-element block (lane s of a group: elements
+// A workgroup of 256 threads per token slot, eight lanes per 32-element block (lane s of a group: elements
 // 4s..4s+3), 32 blocks per round; the row's loads for up to four rounds are issued before any is used, and no
 // step waits on another lane group, so a slot costs about one load latency. Per block: the maximum by shuffles
 // within the group, E, the hi / lo codes. The MFMA B order puts elements 8q..8q+7 and 8q+16..8q+23 of a block,
 // interleaved, in the 16 bytes of lane half q: lane s < 4 interleaves its four codes with those of lane s + 4
 // and stores the 8 bytes. A padding slot (past n, or past its expert's rows) is left unwritten: its token column
 // is computed but never stored. Mode 2 writes no lo plane (the GEMM reads none).
+// Fused grouped mode (pg.counts set): every workgroup derives the expert table from the device counts
+// (fused_scan; workgroup 0 also publishes the offsets and the slot map the GEMM reads), then takes its XCD's
+// share of the slots [0, P) in turn, as gemm_prep does; otherwise workgroup t takes slot t.
 __global__ void __launch_bounds__(256) mxn_prep_kernel(const float* __restrict__ a, int lda, int n, int k, int Kp,
                                                        int NP, int mode, uint8_t* __restrict__ hi,
                                                        uint8_t* __restrict__ lo, uint8_t* __restrict__ shi,
                                                        uint8_t* __restrict__ slo, const int* __restrict__ gmap,
                                                        const int* __restrict__ goff, const int* __restrict__ gpoff,
-                                                       int vec) {
+                                                       int vec, PrepGroups pg) {
     using namespace mxn;
-    const int t = blockIdx.x;
-    const int src = slot_source(t, n, gmap, goff, gpoff);
-    if (src < 0) return;
-    const float* row = a + (int64_t) src * lda;
-    const int sub = threadIdx.x & 7, nb = Kp / 32;
-    constexpr int RQ = 4;   // rounds in flight
-    for (int r0 = 0; r0 < nb; r0 += 32 * RQ) {
-        float x[RQ][4];
-#pragma unroll
-        for (int u = 0; u < RQ; u++) {
-            const int b = r0 + 32 * u + (threadIdx.x >> 3), col = 32 * b + 4 * sub;
-            if (b < nb && vec && col + 3 < k) {   // a and lda 16-byte aligned (the launcher checks)
-                const float4 f = *reinterpret_cast<const float4*>(row + col);
-                x[u][0] = f.x, x[u][1] = f.y, x[u][2] = f.z, x[u][3] = f.w;
-            } else {
-#pragma unroll
-                for (int i = 0; i < 4; i++) x[u][i] = b < nb && col + i < k ? row[col + i] : 0.0f;
-            }
+    __shared__ int own;
+    SlotOwner so;
+    const bool fused = pg.counts != nullptr;
+    const int P = fused ? fused_scan(pg, blockIdx.x == 0, &so) : NP;
+    const int x8 = (int) (blockIdx.x % 8), nw = (int) (gridDim.x >> 3), P8 = ((P + 7) / 8 + 7) & ~7;
+    const int t_first = fused ? x8 * P8 + (int) (blockIdx.x >> 3) : (int) blockIdx.x;
+    const int t_end = fused ? min((x8 + 1) * P8, P) : (int) blockIdx.x + 1;
+    for (int t = t_first; t < t_end; t += fused ? nw : 1) {
+        int src;
+        if (fused) {
+            slot_owner_store(pg, so, t, &own, nullptr);
+            __syncthreads();
+            src = own;
+            __syncthreads();   // own is the next slot's
+        } else {
+            src = slot_source(t, n, gmap, goff, gpoff);
         }
+        if (src < 0) continue;   // uniform over the workgroup
+        const float* row = a + (int64_t) src * lda;
+        const int sub = threadIdx.x & 7, nb = Kp / 32;
+        constexpr int RQ = 4;   // rounds in flight
+        for (int r0 = 0; r0 < nb; r0 += 32 * RQ) {
+            float x[RQ][4];
 #pragma unroll
-        for (int u = 0; u < RQ; u++) {
-            const int b = r0 + 32 * u + (threadIdx.x >> 3);
-            if (r0 + 32 * u >= nb) break;   // uniform: no block of this round exists
-            float amax = fmaxf(fmaxf(fabsf(x[u][0]), fabsf(x[u][1])), fmaxf(fabsf(x[u][2]), fabsf(x[u][3])));
+            for (int u = 0; u < RQ; u++) {
+                const int b = r0 + 32 * u + (threadIdx.x >> 3), col = 32 * b + 4 * sub;
+                if (b < nb && vec && col + 3 < k) {   // a and lda 16-byte aligned (the launcher checks)
+                    const float4 f = *reinterpret_cast<const float4*>(row + col);
+                    x[u][0] = f.x, x[u][1] = f.y, x[u][2] = f.z, x[u][3] = f.w;
+                } else {
 #pragma unroll
-            for (int o = 4; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 8));
-            int E = -127;
-            if (amax > 0.0f) {
-                int ee;
-                const float f = frexpf(amax / 448.0f, &ee);   // amax / 448 = f · 2^ee
-                E = f == 0.5f ? ee - 1 : ee;
-                if (ldexpf(amax, -E) > 448.0f) E += 1;        // rounding in amax / 448
-                E = max(-127, min(127, E));
+                    for (int i = 0; i < 4; i++) x[u][i] = b < nb && col + i < k ? row[col + i] : 0.0f;
+                }
             }
-            const bool lo_ok = mode == 1 && E - 4 >= -127;
-            // x·2^-E is exact (|v| <= 448); the hardware conversion gives the nearest OCP e4m3 code, ties to the
-            // even code; + 0.0f turns a -0 into +0 (code 0x00, not 0x80)
-            float v[4];
 #pragma unroll
-            for (int i = 0; i < 4; i++) v[i] = ldexpf(x[u][i], -E) + 0.0f;
-            uint32_t ch = (uint32_t) __builtin_amdgcn_cvt_pk_fp8_f32(v[0], v[1], 0, false);
-            ch = (uint32_t) __builtin_amdgcn_cvt_pk_fp8_f32(v[2], v[3], (int) ch, true);
-            uint32_t cl = 0;
-            if (lo_ok) {
-                const float hv[4] = {__builtin_amdgcn_cvt_f32_fp8((int) ch, 0), __builtin_amdgcn_cvt_f32_fp8((int) ch, 1),
-                                     __builtin_amdgcn_cvt_f32_fp8((int) ch, 2), __builtin_amdgcn_cvt_f32_fp8((int) ch, 3)};
-                float rr[4];
+            for (int u = 0; u < RQ; u++) {
+                const int b = r0 + 32 * u + (threadIdx.x >> 3);
+                if (r0 + 32 * u >= nb) break;   // uniform: no block of this round exists
+                float amax = fmaxf(fmaxf(fabsf(x[u][0]), fabsf(x[u][1])), fmaxf(fabsf(x[u][2]), fabsf(x[u][3])));
 #pragma unroll
-                for (int i = 0; i < 4; i++) rr[i] = (v[i] - hv[i]) * 16.0f + 0.0f;
-                cl = (uint32_t) __builtin_amdgcn_cvt_pk_fp8_f32(rr[0], rr[1], 0, false);
-                cl = (uint32_t) __builtin_amdgcn_cvt_pk_fp8_f32(rr[2], rr[3], (int) cl, true);
-            }
-            const uint32_t ph = __shfl_xor(ch, 4, 8), pl = __shfl_xor(cl, 4, 8);
-            if (b < nb && sub < 4) {
-                // bytes: own0, partner0, own1, partner1, ... (elements e, e + 16 of the block)
-                auto mix = [](uint32_t o, uint32_t p) {
-                    const uint32_t lo16 = (o & 0xffu) | ((p & 0xffu) << 8) | ((o & 0xff00u) << 8) | ((p & 0xff00u) << 16);
-                    const uint32_t hi16 = ((o >> 16) & 0xffu) | (((p >> 16) & 0xffu) << 8) | ((o >> 24) << 16) | ((p >> 24) << 24);
-                    return make_uint2(lo16, hi16);
-                };
-                const int64_t off = ((int64_t) ((b >> 1) * 2 + (sub >> 1)) * NP + t) * 32 + 16 * (b & 1) + 8 * (sub & 1);
-                *reinterpret_cast<uint2*>(hi + off) = mix(ch, ph);
-                if (mode == 1) *reinterpret_cast<uint2*>(lo + off) = mix(cl, pl);
-                if (sub == 0) {
-                    shi[(int64_t) b * NP + t] = (uint8_t) (E + 127);
-                    if (mode == 1) slo[(int64_t) b * NP + t] = lo_ok ? (uint8_t) (E - 4 + 127) : (uint8_t) 0;
+                for (int o = 4; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 8));
+                int E = -127;
+                if (amax > 0.0f) {
+                    int ee;
+                    const float f = frexpf(amax / 448.0f, &ee);   // amax / 448 = f · 2^ee
+                    E = f == 0.5f ? ee - 1 : ee;
+                    if (ldexpf(amax, -E) > 448.0f) E += 1;        // rounding in amax / 448
+                    E = max(-127, min(127, E));
+                }
+                const bool lo_ok = mode == 1 && E - 4 >= -127;
+                // x·2^-E is exact (|v| <= 448); the hardware conversion gives the nearest OCP e4m3 code, ties to the
+                // even code; + 0.0f turns a -0 into +0 (code 0x00, not 0x80)
+                float v[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) v[i] = ldexpf(x[u][i], -E) + 0.0f;
+                uint32_t ch = (uint32_t) __builtin_amdgcn_cvt_pk_fp8_f32(v[0], v[1], 0, false);
+                ch = (uint32_t) __builtin_amdgcn_cvt_pk_fp8_f32(v[2], v[3], (int) ch, true);
+                uint32_t cl = 0;
+                if (lo_ok) {
+                    const float hv[4] = {__builtin_amdgcn_cvt_f32_fp8((int) ch, 0), __builtin_amdgcn_cvt_f32_fp8((int) ch, 1),
+                                         __builtin_amdgcn_cvt_f32_fp8((int) ch, 2), __builtin_amdgcn_cvt_f32_fp8((int) ch, 3)};
+                    float rr[4];
+#pragma unroll
+                    for (int i = 0; i < 4; i++) rr[i] = (v[i] - hv[i]) * 16.0f + 0.0f;
+                    cl = (uint32_t) __builtin_amdgcn_cvt_pk_fp8_f32(rr[0], rr[1], 0, false);
+                    cl = (uint32_t) __builtin_amdgcn_cvt_pk_fp8_f32(rr[2], rr[3], (int) cl, true);
+                }
+                const uint32_t ph = __shfl_xor(ch, 4, 8), pl = __shfl_xor(cl, 4, 8);
+                if (b < nb && sub < 4) {
+                    // bytes: own0, partner0, own1, partner1, ... (elements e, e + 16 of the block)
+                    auto mix = [](uint32_t o, uint32_t p) {
+                        const uint32_t lo16 = (o & 0xffu) | ((p & 0xffu) << 8) | ((o & 0xff00u) << 8) | ((p & 0xff00u) << 16);
+                        const uint32_t hi16 = ((o >> 16) & 0xffu) | (((p >> 16) & 0xffu) << 8) | ((o >> 24) << 16) | ((p >> 24) << 24);
+                        return make_uint2(lo16, hi16);
+                    };
+                    const int64_t off = ((int64_t) ((b >> 1) * 2 + (sub >> 1)) * NP + t) * 32 + 16 * (b & 1) + 8 * (sub & 1);
+                    *reinterpret_cast<uint2*>(hi + off) = mix(ch, ph);
+                    if (mode == 1) *reinterpret_cast<uint2*>(lo + off) = mix(cl, pl);
+                    if (sub == 0) {
+                        shi[(int64_t) b * NP + t] = (uint8_t) (E + 127);
+                        if (mode == 1) slo[(int64_t) b * NP + t] = lo_ok ? (uint8_t) (E - 4 + 127) : (uint8_t) 0;
+                    }
                 }
             }
         }
@@ -322,7 +342,8 @@ size_t mx_act_bytes_np(int NP, int k) {
 }
 
 static hipError_t mx_prep_np(const float* a, int lda, int n, int NP, int k, int mode, void* scratch, MxAct* out,
-                             const int* gmap, const int* goff, const int* gpoff, hipStream_t st) {
+                             const int* gmap, const int* goff, const int* gpoff, hipStream_t st,
+                             const PrepGroups& pg = PrepGroups{}) {
     const int Kp = (k + 255) / 256 * 256;
     uint8_t* p = (uint8_t*) scratch;
     uint8_t* hi = p;
@@ -332,7 +353,9 @@ static hipError_t mx_prep_np(const float* a, int lda, int n, int NP, int k, int 
     *out = MxAct{hi, lo, shi, slo, NP, Kp, k};
     if (NP <= 0) return hipSuccess;
     const int vec = (reinterpret_cast<uintptr_t>(a) & 15) == 0 && (lda & 3) == 0;
-    mxn_prep_kernel<<<NP, 256, 0, st>>>(a, lda, n, k, Kp, NP, mode, hi, lo, shi, slo, gmap, goff, gpoff, vec);
+    // fused grouped mode: at most 1024 workgroups (all resident), each looping over its XCD's slots
+    const int grid = pg.counts != nullptr ? (NP < 1024 ? (NP + 7) / 8 * 8 : 1024) : NP;
+    mxn_prep_kernel<<<grid, 256, 0, st>>>(a, lda, n, k, Kp, NP, mode, hi, lo, shi, slo, gmap, goff, gpoff, vec, pg);
     return hipGetLastError();
 }
 
@@ -342,6 +365,12 @@ hipError_t launch_mx_prep(const float* a, int lda, int n, int k, int mode, void*
 hipError_t launch_mx_prep_grouped(const float* a, int lda, int k, int mode, const Groups& g, int cap64, void* scratch,
                                   MxAct* out, hipStream_t st) {
     return mx_prep_np(a, lda, 0, cap64 * 64, k, mode, scratch, out, g.map64, g.off, g.poff64, st);
+}
+hipError_t launch_mx_prep_grouped_fused(const float* a, int lda, int k, int mode, const PrepGroups& pg, void* scratch,
+                                        MxAct* out, hipStream_t st) {
+    if (pg.counts == nullptr || pg.E < 1 || pg.E > PREP_FUSED_MAX_E || pg.rows_cap < 0 || pg.cap64 < 1)
+        return hipErrorInvalidValue;
+    return mx_prep_np(a, lda, 0, pg.cap64 * 64, k, mode, scratch, out, nullptr, nullptr, nullptr, st, pg);
 }
 
 static hipError_t mx_go(int mode, const WeightView& w, const MxAct& A, int m, int n, float* c, int ldc, const Groups& gp,

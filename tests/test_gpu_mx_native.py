@@ -83,36 +83,42 @@ def test_mx_native_keeps_decode_semantics(hip, oracle):
 
 
 @pytest.mark.parametrize("mode", [1, 2])
-def test_mx_native_grouped(hip, oracle, mode):
-    """jamhip_mm_grouped under the mode: experts with >= 8 rows on the native path (each against the
-    restatement), experts below 8 rows on jam's F1 path, rows past the prefix untouched."""
+@pytest.mark.parametrize("E", [7, 24])
+def test_mx_native_grouped(hip, oracle, mode, E):
+    """jamhip_mm_grouped under the mode. With rows_cap >= 8·n_experts (E = 7: 135 rows) one fused prep derives
+    the expert table from the device counts and every expert runs on the native path, those below 8 rows
+    included; sparser calls (E = 24) keep jam's F1 path for experts below 8 rows. Each native expert against
+    the restatement, each F1 expert against the int8 oracle, rows past the prefix untouched."""
     import torch
     from qxotic_amd.jam import JAM, Segment
-    E, m, k = 7, 64, 576
-    counts = np.array([3, 0, 12, 70, 1, 9, 40], np.int32)
+    m, k = 64, 576
+    counts = np.zeros(E, np.int32)
+    counts[:7] = [3, 0, 12, 70, 1, 9, 40]
     R = int(counts.sum())
     w = oracle.quantize(O.MXFP4, oracle.normal(27, (E * m, k), 0.0, 0.02))
     a = acts(28, R, k)
     dev = lambda x: torch.from_numpy(np.ascontiguousarray(x)).cuda()
     counts_d, a_d = dev(counts), dev(a)
     c = torch.full((R, m), 7.0, dtype=torch.float32, device="cuda")
+    offs = torch.full((E + 1,), -5, dtype=torch.int32, device="cuda")
     torch.cuda.synchronize()   # the inputs are written on torch's stream; the library runs on its own
     assert hip.set_mx_native(mode) == 0
     try:
         st = hip.mm_grouped(Segment.of(w), JAM.MXFP4, k, m, E, counts_d.data_ptr(), a_d.data_ptr(), k,
-                            c.data_ptr(), m, k, R)
+                            c.data_ptr(), m, k, R, offs.data_ptr())
         torch.cuda.synchronize()
     finally:
         hip.set_mx_native(0)
     assert st == JAM.OK, hip.last_error()
     got = c.cpu().numpy()
     off = np.concatenate([[0], np.cumsum(counts)])
+    assert np.array_equal(offs.cpu().numpy(), off)
     for e in range(E):
         rows = slice(off[e], off[e + 1])
         if counts[e] == 0:
             continue
         we = w[e * m:(e + 1) * m]
-        if counts[e] >= 8:
+        if counts[e] >= 8 or R >= 8 * E:
             ref, sref = X.mm(oracle.dequant(O.MXFP4, we, k, f64=True), a[rows], mode)
             assert (np.abs(got[rows] - ref) <= TOL_MFMA * sref + 1e-30).all(), f"expert {e}"
         else:
