@@ -114,8 +114,8 @@ jamhip_status jamhip_ctx_set_autopin(jamhip_ctx* ctx, int sightings, int64_t max
 jamhip_status jamhip_ctx_autopin_stats(const jamhip_ctx* ctx, int64_t* out4);
 
 /* Native-MX mode for MXFP4 weights (no counterpart in jam; off by default). The MXFP4 calls this library
- * runs on the matrix cores (from the same size-dependent token count as the int8 path, 9 to 17 tokens, and
- * every jamhip_mm_grouped expert with 8 or more rows) then feed the weights to v_mfma_scale_f32_32x32x64_f8f6f4 as their own fp4 codes and the
+ * runs on the matrix cores (from the same size-dependent token count as the int8 path, 9 to 17 tokens; in
+ * jamhip_mm_grouped every expert when rows_cap >= 8·n_experts, else the experts with 8 or more rows) then feed the weights to v_mfma_scale_f32_32x32x64_f8f6f4 as their own fp4 codes and the
  * activations as MX-FP8: per 32-element block E = the smallest exponent with max|x|·2^-E <= 448,
  * hi = e4m3(x·2^-E) (round to nearest even) with scale 2^E, lo = e4m3((x·2^-E - hi)·16) with scale 2^(E-4);
  * mode 1 multiplies hi and lo (about 8 significant bits per activation), mode 2 hi only (about 4). The
