@@ -442,10 +442,31 @@ def moe_leg(hip, torch, stream, steps: int = 10, no_graph: bool = False) -> dict
         del g
         return sorted(gruns)[1], sorted(runs)[1]
 
+    def layer_gf(i):
+        # the same layer with the gather folded into the gate_up call (jamhip_mm_grouped_gather): its activation
+        # prep reads each routed row from x through slot_route; bit-identical results (tests/test_gpu_moe.py)
+        cg, cd = wg[i % copies], wd[i % copies]
+        logits.copy_(logits0)
+        ok = hip.moe_select_topk(logits.data_ptr(), None, SEQ, E, E, TOPK, hip.TOPK_SOFTMAX, re.data_ptr(),
+                                 prob.data_ptr()) == JAM.OK
+        ok &= hip.moe_route(re.data_ptr(), SEQ, TOPK, E, counts.data_ptr(), off.data_ptr(), slot_route.data_ptr(),
+                            route_slot.data_ptr()) == JAM.OK
+        ok &= hip.mm_grouped_gather(Segment.of(cg), JAM.MXFP4, D, FF, E, counts.data_ptr(), x.data_ptr(), D,
+                                    slot_route.data_ptr(), TOPK, h.data_ptr(), FF, D, R, None) == JAM.OK
+        ok &= hip.mm_grouped(Segment.of(cd), JAM.MXFP4, D, D, E, counts.data_ptr(), hid.data_ptr(), D, y.data_ptr(),
+                             D, D, R, None) == JAM.OK
+        ok &= hip.moe_combine(y.data_ptr(), D, re.data_ptr(), prob.data_ptr(), route_slot.data_ptr(), SEQ, TOPK, E, D,
+                              out.data_ptr(), D) == JAM.OK
+        if not ok:
+            raise RuntimeError(hip.last_error())
+
     us, us_stream = timed()
     assert np.array_equal(counts.cpu().numpy(), counts_h), "device routing counts disagree with the host's"
     assert np.array_equal(re.cpu().numpy(), sel.ravel()), "device top-k disagrees with the host's"
     assert bool(torch.isfinite(out).all()), "moe output not finite"
+    out_ref = out.clone()
+    us_gf, _ = timed(layer_gf)
+    assert torch.equal(out, out_ref), "the gather-folded layer differs from jam's path"
     ops = 2.0 * R * (FF * D + D * D)
     # the opt-in native-MX mode (not jam's activation semantics): the same layer with the experts' matrix-core
     # calls on the scaled fp4 x fp8 MFMA, MX-FP8 activations hi + lo (mode 1) or hi only (mode 2)
@@ -453,9 +474,11 @@ def moe_leg(hip, torch, stream, steps: int = 10, no_graph: bool = False) -> dict
     for mode in (1, 2):
         assert hip.set_mx_native(mode) == JAM.OK
         u, u_stream = timed()
+        u_gf, _ = timed(layer_gf)
         assert hip.set_mx_native(0) == JAM.OK
         assert bool(torch.isfinite(out).all()), "moe output not finite"
         native[f"mode{mode}"] = {"us_per_layer": round(u, 1), "us_per_layer_stream": round(u_stream, 1),
+                                 "us_per_layer_gather_folded": round(u_gf, 1),
                                  "TOPS": round(ops / (u * 1e-6) / 1e12, 2),
                                  "frac_fp4_peak": round(ops / (u * 1e-6) / 1e12 / 10070.0, 4)}
     native["note"] = ("opt-in jamhip_ctx_set_mx_native: MXFP4 weights as fp4 on v_mfma_scale_f32_32x32x64_f8f6f4, "
@@ -527,6 +550,7 @@ def moe_leg(hip, torch, stream, steps: int = 10, no_graph: bool = False) -> dict
     tops = ops / (us * 1e-6) / 1e12
     gbs = wbytes / (us * 1e-6) / 1e9
     return {"us_per_layer": round(us, 1), "us_per_layer_stream": round(us_stream, 1), "TOPS": round(tops, 2),
+            "us_per_layer_gather_folded": round(us_gf, 1),
             "weights_GBs": round(gbs, 1),
             "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
             "frac_fp4_peak": round(tops / 10070.0, 4), "routed_rows": R,
@@ -538,7 +562,9 @@ def moe_leg(hip, torch, stream, steps: int = 10, no_graph: bool = False) -> dict
             "note": "32 experts x (5760x2880 + 2880x2880) MXFP4 (423 MB, 2 rotating copies; experts cycle through "
                     "2 distinct N(0,0.02) quantizations), 512 tokens top-4 Zipf(1.1); ops = 2*routed_rows*"
                     "(5760*2880 + 2880*2880); us_per_layer: one captured graph of the timed layers, median of 3 "
-                    "replays; us_per_layer_stream: the same layers launched on the stream"}
+                    "replays; us_per_layer_stream: the same layers launched on the stream; "
+                    "us_per_layer_gather_folded: the same layer with jamhip_moe_gather folded into the gate_up call "
+                    "(jamhip_mm_grouped_gather, bit-identical output)"}
 
 
 def decode_step_leg(hip, torch, stream, w_gate: np.ndarray, reps: int = 8) -> dict:

@@ -191,6 +191,19 @@ jamhip_status jamhip_mm_grouped_ex(jamhip_ctx* ctx,
                                    void*       c_dev, int ct, int ldc,
                                    int k, int rows_cap, void* offsets_dev, const void* bias_dev);
 
+/* jamhip_moe_gather and jamhip_mm_grouped_ex in one call: A is not materialised; CSR row r of A is row
+ * slot_route_dev[r] / topk of x_dev [seq][ldx] (slot_route_dev as jamhip_moe_route writes it for the same
+ * counts), read by the activation quantization itself where the call takes the matrix cores with at least
+ * 8·n_experts rows of capacity (other paths gather into context scratch first). Results bit-identical to
+ * the two calls. No counterpart in jam: it replaces Moe.dispatch's gather (Moe.java:214-222) followed by
+ * the grouped matmul (GptOss.java:295-314), for the gate and up projections that read the gathered rows. */
+jamhip_status jamhip_mm_grouped_gather(jamhip_ctx* ctx,
+                                       const void* w, int wt, int ldw, int m, int n_experts,
+                                       const void* counts_dev,
+                                       const void* x_dev, int at, int ldx, const void* slot_route_dev, int topk,
+                                       void*       c_dev, int ct, int ldc,
+                                       int k, int rows_cap, void* offsets_dev, const void* bias_dev);
+
 /* Moe.dispatch's CSR build (Moe.java:188-206) from route_expert_dev[seq·topk] (int32 expert of route
  * s·topk + j, Moe.selectTopK's rowTopE): counts_dev[n_experts], offsets_dev[n_experts + 1], and the
  * slot of every route in (s, j) order within its expert: slot_route_dev[slot] = route,

@@ -32,6 +32,7 @@ SIGNATURES = [
     ("jamhip_quantize_device", _I, [_VP, _I, _VP, _I, _I, _I, _VP, _VP, _VP]),
     ("jamhip_mm_grouped", _I, [_VP, _VP, _I, _I, _I, _I, _VP, _VP, _I, _I, _VP, _I, _I, _I, _I, _VP]),
     ("jamhip_mm_grouped_ex", _I, [_VP, _VP, _I, _I, _I, _I, _VP, _VP, _I, _I, _VP, _I, _I, _I, _I, _VP, _VP]),
+    ("jamhip_mm_grouped_gather", _I, [_VP, _VP, _I, _I, _I, _I, _VP, _VP, _I, _I, _VP, _I, _VP, _I, _I, _I, _I, _VP, _VP]),
     ("jamhip_moe_route", _I, [_VP, _VP, _I, _I, _I, _VP, _VP, _VP, _VP]),
     ("jamhip_moe_gather", _I, [_VP, _VP, _I, _VP, _VP, _I, _I, _I, _I, _VP, _I]),
     ("jamhip_moe_combine", _I, [_VP, _VP, _I, _VP, _VP, _VP, _I, _I, _I, _I, _VP, _I]),

@@ -179,7 +179,7 @@ struct jamhip_ctx {
     mutable std::mutex pin_mu;
     std::vector<Pin> pins;
     int64_t pinned_bytes = 0;   // sum of pins[].bytes, under pin_mu
-    DevBuf act, gact, part, moe, route;       // kernel scratch (addresses may be captured in graphs)
+    DevBuf act, gact, part, moe, route, gath; // kernel scratch (addresses may be captured in graphs)
     DevBuf fold;                              // the repack's fold flag (one int)
     StageBuf a_stage, c_stage, w_raw, w_stage;   // staging of host copies
     HostBuf a_host, c_host;   // jamhip_mm's pinned bounce buffers for A and C
@@ -900,11 +900,15 @@ jamhip_status quantize_device_impl(jamhip_ctx* ctx, int flavour, const void* a_d
     return e == hipSuccess ? JAMHIP_OK : hip_fail(ctx, e, "quantize launch");
 }
 
+// x_rows (gathered input): CSR row r of A is row x_rows[r] / rdiv of a_dev (jamhip_moe_gather folded in); the
+// fused preps read it there, the other paths gather the rows into scratch first.
 jamhip_status mm_grouped_ex_impl(jamhip_ctx* ctx, const void* w, int wt, int ldw, int m, int n_experts,
                                    const void* counts_dev, const void* a_dev, int at, int lda, void* c_dev, int ct,
-                                   int ldc, int k, int rows_cap, void* offsets_dev, const void* bias_dev) {
+                                   int ldc, int k, int rows_cap, void* offsets_dev, const void* bias_dev,
+                                   const int* x_rows = nullptr, int rdiv = 1) {
     if (!ctx) return JAMHIP_EINVAL;
     if (!w || !counts_dev || !a_dev || !c_dev) return fail(ctx, JAMHIP_EINVAL, "grouped: null operand");
+    if (rdiv < 1) return fail(ctx, JAMHIP_EINVAL, "grouped gather: topk must be positive");
     if (m <= 0 || k <= 0 || n_experts <= 0 || rows_cap < 0)
         return fail(ctx, JAMHIP_EINVAL, "grouped: m, k, n_experts must be positive and rows_cap >= 0");
     if (ldw < k || lda < k || ldc < m) return fail(ctx, JAMHIP_EINVAL, "grouped: stride below extent");
@@ -948,7 +952,8 @@ jamhip_status mm_grouped_ex_impl(jamhip_ctx* ctx, const void* w, int wt, int ldw
     // expert's rows) and the native GEMM over every expert, those with fewer than 8 rows included.
     if (rows_cap >= 8 * E && E <= PREP_FUSED_MAX_E && m % 32 == 0 && wt == MXFP4 && ctx->mx_native &&
         mma_path(wt, k, wv)) {
-        const PrepGroups pg{(const int*) counts_dev, E, rows_cap, off, poff64, map64, cap64, (int*) offsets_dev};
+        const PrepGroups pg{(const int*) counts_dev, E, rows_cap, off, poff64, map64, cap64, (int*) offsets_dev,
+                            x_rows, rdiv};
         const Groups g{off, poff8, map8, poff64, map64, m, static_cast<const float*>(bias_dev)};
         MxAct X;
         if ((e = ctx->gact.ensure(mx_act_bytes_np(cap64 * 64, k))) != hipSuccess)
@@ -961,7 +966,8 @@ jamhip_status mm_grouped_ex_impl(jamhip_ctx* ctx, const void* w, int wt, int ldw
     }
     if (rows_cap >= 8 * E && E <= PREP_FUSED_MAX_E && m % 32 == 0 && !(wt == MXFP4 && ctx->mx_native) &&
         mma_exact(ctx, wt, k, wv)) {
-        const PrepGroups pg{(const int*) counts_dev, E, rows_cap, off, poff64, map64, cap64, (int*) offsets_dev};
+        const PrepGroups pg{(const int*) counts_dev, E, rows_cap, off, poff64, map64, cap64, (int*) offsets_dev,
+                            x_rows, rdiv};
         const Groups g{off, poff8, map8, poff64, map64, m, static_cast<const float*>(bias_dev)};
         GemmAct G;
         if ((e = ctx->gact.ensure(gemm_act_bytes_np(wt, cap64 * 64, k))) != hipSuccess)
@@ -979,6 +985,15 @@ jamhip_status mm_grouped_ex_impl(jamhip_ctx* ctx, const void* w, int wt, int ldw
             hipSuccess)
         return hip_fail(ctx, e, "grouped: offsets copy");
     if (rows_cap == 0) return JAMHIP_OK;
+    if (x_rows != nullptr) {   // the gathered rows, in CSR order, for the kernels below
+        if ((e = ctx->gath.ensure((size_t) rows_cap * k * sizeof(float))) != hipSuccess)
+            return hip_fail(ctx, e, "grouped gather: scratch alloc");
+        if ((e = launch_moe_gather(a, lda, x_rows, off, E, rows_cap, rdiv, k, (float*) ctx->gath.p, k, ctx->stream)) !=
+            hipSuccess)
+            return hip_fail(ctx, e, "grouped gather: gather launch");
+        a = (const float*) ctx->gath.p;
+        lda = k;
+    }
     const Groups g{off, poff8, map8, poff64, map64, m, static_cast<const float*>(bias_dev)};
     // activation scratch for the decode kernels (rows_cap rows; F1 then F2 reuse it in stream order)
     const int64_t nb = k / 32, n = rows_cap;
@@ -1177,6 +1192,7 @@ void destroy_ctx(jamhip_ctx* ctx) {
     ctx->part.release();
     ctx->moe.release();
     ctx->route.release();
+    ctx->gath.release();
     ctx->a_stage.release();
     ctx->c_stage.release();
     ctx->w_raw.release();
@@ -1353,6 +1369,17 @@ jamhip_status jamhip_mm_grouped_ex(jamhip_ctx* ctx, const void* w, int wt, int l
     return on_ctx(ctx, [&](jamhip_ctx* x) {
         return mm_grouped_ex_impl(x, w, wt, ldw, m, n_experts, counts_dev, a_dev, at, lda, c_dev, ct, ldc, k, rows_cap,
                                   offsets_dev, bias_dev);
+    });
+}
+
+jamhip_status jamhip_mm_grouped_gather(jamhip_ctx* ctx, const void* w, int wt, int ldw, int m, int n_experts,
+                                       const void* counts_dev, const void* x_dev, int at, int ldx,
+                                       const void* slot_route_dev, int topk, void* c_dev, int ct, int ldc, int k,
+                                       int rows_cap, void* offsets_dev, const void* bias_dev) {
+    return on_ctx(ctx, [&](jamhip_ctx* x) {
+        if (!slot_route_dev) return fail(x, JAMHIP_EINVAL, "grouped gather: null slot_route");
+        return mm_grouped_ex_impl(x, w, wt, ldw, m, n_experts, counts_dev, x_dev, at, ldx, c_dev, ct, ldc, k, rows_cap,
+                                  offsets_dev, bias_dev, static_cast<const int*>(slot_route_dev), topk);
     });
 }
 

@@ -269,6 +269,16 @@ class HipJAM:
         return lib().jamhip_mm_grouped_ex(self.ctx, w.address, wt, ldw, m, n_experts, counts_dev, a_dev, JAM.F32,
                                           lda, c_dev, JAM.F32, ldc, k, rows_cap, offsets_dev, bias_dev)
 
+    def mm_grouped_gather(self, w: Segment, wt: int, ldw: int, m: int, n_experts: int, counts_dev: int, x_dev: int,
+                          ldx: int, slot_route_dev: int, topk: int, c_dev: int, ldc: int, k: int, rows_cap: int,
+                          offsets_dev: int | None = None, bias_dev: int | None = None) -> int:
+        """moe_gather + mm_grouped_ex in one call: CSR row r of A is row slot_route[r] // topk of x
+        (jamhip_mm_grouped_gather)."""
+        _require_native(w, "weight W")
+        return lib().jamhip_mm_grouped_gather(self.ctx, w.address, wt, ldw, m, n_experts, counts_dev, x_dev, JAM.F32,
+                                              ldx, slot_route_dev, topk, c_dev, JAM.F32, ldc, k, rows_cap, offsets_dev,
+                                              bias_dev)
+
     def moe_route(self, route_expert_dev: int, seq: int, topk: int, n_experts: int, counts_dev: int,
                   offsets_dev: int, slot_route_dev: int, route_slot_dev: int) -> int:
         """Moe.dispatch's CSR build on the device (Moe.java:188-206)."""

@@ -156,6 +156,59 @@ def test_mm_grouped_parity(hip, oracle, dt, m, k, counts):
         hip.evict(Segment.of(w))
 
 
+@pytest.mark.parametrize("native", [0, 2])
+@pytest.mark.parametrize("seq,topk,E", [(200, 4, 8), (24, 4, 32), (2, 4, 16)], ids=["dense", "mid", "sparse"])
+@pytest.mark.parametrize("dt,m,k", [(O.MXFP4, 64, 576), (O.Q4_K, 96, 512), (O.MXFP4, 48, 320)])
+def test_mm_grouped_gather_matches_two_calls(hip, oracle, dt, m, k, seq, topk, E, native):
+    """jamhip_mm_grouped_gather (CSR row r of A = row slot_route[r] / topk of x) is bit-identical to
+    jamhip_moe_gather followed by jamhip_mm_grouped_ex, offsets included: the fused preps reading x themselves
+    (dense: rows_cap >= 8 per expert on the matrix cores, jam's path and native MX mode 2) and the paths that
+    gather into scratch first (mid: F1 decode + matrix cores; sparse: F1 decode only; m = 48: F2 tiles); x
+    with a row pitch above k, expert biases on the dense case."""
+    import torch
+    from qxotic_amd.jam import JAM, Segment
+    if native and dt != O.MXFP4:
+        pytest.skip("native MX mode is MXFP4 only")
+    say(f"grouped gather {O.NAMES[dt]} m={m} k={k} seq={seq} topk={topk} E={E} native={native}")
+    R = seq * topk
+    re = routes(0xC0DE + seq + E, seq, topk, E)
+    w = oracle.quantize(dt, oracle.normal(0x5A11C0DE ^ (31 * E + dt), (E * m, k), 0.0, 0.02))
+    ldx = k + 4
+    x = np.zeros((seq, ldx), np.float32)
+    x[:, :k] = oracle.outliers(91 + seq, (seq, k))
+    bias = oracle.normal(93, (E, m)) if seq == 200 else None
+    i32 = lambda n: torch.zeros(n, dtype=torch.int32, device="cuda")
+    counts, off, slot_route, route_slot = i32(E), i32(E + 1), i32(R), i32(R)
+    re_d, x_d = dev(re), dev(x)
+    b_d = dev(bias) if bias is not None else None
+    g = torch.zeros((R, k), dtype=torch.float32, device="cuda")
+    ca = torch.full((R, m + 1), -3.0, dtype=torch.float32, device="cuda")
+    cb = torch.full((R, m + 1), -3.0, dtype=torch.float32, device="cuda")
+    offa, offb = i32(E + 1), i32(E + 1)
+    torch.cuda.synchronize()   # the inputs are written on torch's stream; the library runs on its own
+    assert hip.pin(Segment.of(w), dt, k, E * m) == JAM.OK, hip.last_error()
+    assert hip.set_mx_native(native) == JAM.OK
+    try:
+        assert hip.moe_route(re_d.data_ptr(), seq, topk, E, counts.data_ptr(), off.data_ptr(), slot_route.data_ptr(),
+                             route_slot.data_ptr()) == JAM.OK, hip.last_error()
+        assert hip.moe_gather(x_d.data_ptr(), ldx, slot_route.data_ptr(), off.data_ptr(), E, seq, topk, k,
+                              g.data_ptr(), k) == JAM.OK, hip.last_error()
+        bp = b_d.data_ptr() if b_d is not None else None
+        assert hip.mm_grouped_ex(Segment.of(w), dt, k, m, E, counts.data_ptr(), g.data_ptr(), k, ca.data_ptr(), m + 1,
+                                 k, R, offa.data_ptr(), bp) == JAM.OK, hip.last_error()
+        assert hip.mm_grouped_gather(Segment.of(w), dt, k, m, E, counts.data_ptr(), x_d.data_ptr(), ldx,
+                                     slot_route.data_ptr(), topk, cb.data_ptr(), m + 1, k, R, offb.data_ptr(),
+                                     bp) == JAM.OK, hip.last_error()
+        hip.synchronize()
+        got_a, got_b = ca.cpu().numpy(), cb.cpu().numpy()
+        assert np.array_equal(offa.cpu().numpy(), offb.cpu().numpy())
+        assert (got_a[:, m:] == -3.0).all() and (got_b[:, m:] == -3.0).all()
+        assert np.array_equal(got_a.view(np.uint32), got_b.view(np.uint32))
+    finally:
+        hip.set_mx_native(0)
+        assert hip.evict(Segment.of(w)) == JAM.OK
+
+
 def test_mm_grouped_counts_past_rows_cap(hip, oracle):
     """Counts whose sum exceeds rows_cap: the rows past rows_cap are neither read nor written."""
     import torch
@@ -296,6 +349,10 @@ def test_grouped_status_codes(hip):
     assert call(ldc=16) == JAM.EINVAL               # ldc < m
     assert call(cap=-1) == JAM.EINVAL
     assert call(dt=JAM.F16) == JAM.EUNSUPPORTED
+    gcall = lambda sr, topk: hip.mm_grouped_gather(Segment.of(w), JAM.MXFP4, 256, 32, 2, z.data_ptr(), f.data_ptr(),
+                                                   256, sr, topk, f.data_ptr(), 32, 256, 4, None, None)
+    assert gcall(None, 4) == JAM.EINVAL              # no slot_route
+    assert gcall(z.data_ptr(), 0) == JAM.EINVAL      # topk < 1
 
 
 @pytest.mark.parametrize("dt", [O.MXFP4, O.Q4_K])
