@@ -219,19 +219,12 @@ __global__ void __launch_bounds__(RCH) moe_route_count_kernel(const int* __restr
         ccnt[(int64_t) blockIdx.x * E + threadIdx.x] = s;
     }
 }
-__global__ void __launch_bounds__(RCH) moe_route_slot_kernel(const int* __restrict__ route_expert, int R, int E,
-                                                            const int* __restrict__ ccnt, int nch,
-                                                            int* __restrict__ counts, int* __restrict__ off,
-                                                            int* __restrict__ slot_route, int* __restrict__ route_slot) {
+// Chunk blockIdx.x's slots from expert e's total (thread e) and its routes in the chunks before this one.
+JAMHIP_DEV void chunk_slots(const int* __restrict__ route_expert, int R, int E, int total, int before,
+                            int* __restrict__ counts, int* __restrict__ off, int* __restrict__ slot_route,
+                            int* __restrict__ route_slot) {
     __shared__ int wcnt[RCH_WAVES * 256], base[256], scan[RCH];
     const int t = threadIdx.x, wave = t >> 6;
-    int total = 0, before = 0;
-    if (t < E)
-        for (int c = 0; c < nch; c++) {
-            const int v = ccnt[(int64_t) c * E + t];
-            total += v;
-            before += c < (int) blockIdx.x ? v : 0;
-        }
     // exclusive scan of the totals over the experts (Hillis-Steele in LDS)
     scan[t] = t < E ? total : 0;
     __syncthreads();
@@ -266,6 +259,40 @@ __global__ void __launch_bounds__(RCH) moe_route_slot_kernel(const int* __restri
             route_slot[r] = -1;
         }
     }
+}
+__global__ void __launch_bounds__(RCH) moe_route_slot_kernel(const int* __restrict__ route_expert, int R, int E,
+                                                            const int* __restrict__ ccnt, int nch,
+                                                            int* __restrict__ counts, int* __restrict__ off,
+                                                            int* __restrict__ slot_route, int* __restrict__ route_slot) {
+    int total = 0, before = 0;
+    if (threadIdx.x < E)
+        for (int c = 0; c < nch; c++) {
+            const int v = ccnt[(int64_t) c * E + threadIdx.x];
+            total += v;
+            before += c < (int) blockIdx.x ? v : 0;
+        }
+    chunk_slots(route_expert, R, E, total, before, counts, off, slot_route, route_slot);
+}
+// One launch for up to ROUTE_FUSED_MAX routes: every chunk's workgroup counts all routes itself (integer LDS
+// atomics: the totals, and the routes before its chunk), then takes its chunk's slots as above.
+constexpr int ROUTE_FUSED_MAX = 16384;
+__global__ void __launch_bounds__(RCH) moe_route_fused_kernel(const int* __restrict__ route_expert, int R, int E,
+                                                             int* __restrict__ counts, int* __restrict__ off,
+                                                             int* __restrict__ slot_route, int* __restrict__ route_slot) {
+    __shared__ int tot[256], bef[256];
+    const int t = threadIdx.x, lim = (int) blockIdx.x * RCH;
+    tot[t] = 0;
+    bef[t] = 0;
+    __syncthreads();
+    for (int r = t; r < R; r += RCH) {
+        const int e = route_expert[r];
+        if (e >= 0 && e < E) {
+            atomicAdd(&tot[e], 1);
+            if (r < lim) atomicAdd(&bef[e], 1);
+        }
+    }
+    __syncthreads();
+    chunk_slots(route_expert, R, E, t < E ? tot[t] : 0, t < E ? bef[t] : 0, counts, off, slot_route, route_slot);
 }
 
 // The same CSR build for at most 64 routes and 64 experts (decode-time MoE) in one wave, with no barrier:
@@ -413,6 +440,11 @@ hipError_t launch_moe_route(const int* route_expert, int R, int E, int* counts, 
     if (E < 1 || E > MOE_THREADS) return hipErrorNotSupported;
     if (R <= 64 && E <= 64) {   // one wave
         moe_route_wave_kernel<<<1, 64, 0, st>>>(route_expert, R, E, counts, off, slot_route, route_slot);
+        return hipGetLastError();
+    }
+    if (R > RCH && R <= ROUTE_FUSED_MAX && E <= 256) {   // chunked, one launch
+        moe_route_fused_kernel<<<(R + RCH - 1) / RCH, RCH, 0, st>>>(route_expert, R, E, counts, off, slot_route,
+                                                                    route_slot);
         return hipGetLastError();
     }
     if (scratch != nullptr && moe_route_scratch_ints(R, E) > 0) {   // chunked: R > 256 routes, E <= 256

@@ -32,12 +32,13 @@ def dev(x):
 
 def test_route_gather_combine_bit_exact(hip):
     import torch
-    # more than 256 routes with at most 256 experts take the chunked two-kernel routing, up to 64 routes over
-    # up to 64 experts the one-wave kernel, the rest the single-workgroup kernel (chunks of 1024: the last
-    # case takes five); all must give Moe.dispatch's slots
+    # 257..16384 routes with at most 256 experts take the chunked one-launch routing (each chunk counts every
+    # route itself), more the chunked two-kernel routing, up to 64 routes over up to 64 experts the one-wave
+    # kernel, the rest the single-workgroup kernel (chunks of 1024: the last case takes five); all must give
+    # Moe.dispatch's slots
     for seed, seq, topk, E in ((1, 37, 4, 8), (2, 300, 2, 32), (3, 5, 1, 3), (4, 700, 4, 32), (5, 1100, 4, 64),
                                (6, 300, 4, 16), (7, 200, 2, 300), (8, 512, 4, 256), (9, 16, 4, 64), (10, 1, 4, 32),
-                               (11, 8, 2, 80)):
+                               (11, 8, 2, 80), (12, 4200, 4, 32), (13, 4100, 4, 48)):
         say(f"moe route seq={seq} topk={topk} E={E}")
         re = routes(seed, seq, topk, E)
         if seed == 3:
@@ -46,6 +47,8 @@ def test_route_gather_combine_bit_exact(hip):
             re[5], re[63] = -1, E                # the same in the one-wave kernel (its last lane too)
         if seed == 6:                            # the same in the chunked form, in two different chunks
             re[7], re[1000] = -1, E + 3
+        if seed == 12:                           # and in the two-kernel form
+            re[9], re[16000] = -2, E
         R = seq * topk
         counts = torch.zeros(E, dtype=torch.int32, device="cuda")
         off = torch.zeros(E + 1, dtype=torch.int32, device="cuda")
