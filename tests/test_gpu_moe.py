@@ -431,7 +431,10 @@ def _topk_check(got, sel, topk, **kw):
     re, rp, cnt, masked = got
     re_o, rp_o, cnt_o, masked_o = M.select_topk(sel, topk, **kw)
     assert np.array_equal(re, re_o)
-    assert np.array_equal(rp.view(np.uint32), rp_o.view(np.uint32)), np.flatnonzero(rp.view(np.uint32) != rp_o.view(np.uint32))[:5]
+    # bit for bit, NaN payloads aside (a NaN weight reaching the softmax makes the row's weights NaN, whose payload
+    # neither Java nor IEEE arithmetic pins)
+    same = (rp.view(np.uint32) == rp_o.view(np.uint32)) | (np.isnan(rp) & np.isnan(rp_o))
+    assert same.all(), np.flatnonzero(~same)[:5]
     assert np.array_equal(cnt, cnt_o)
     assert np.array_equal(masked.view(np.uint32), masked_o.view(np.uint32))
 
@@ -450,6 +453,15 @@ def test_select_topk_bit_exact(hip):
     logits[1] = -np.inf                                     # nothing above -Inf: expert 0 each pass
     logits[2, :5] = np.nan                                  # NaN never wins
     logits[3] = np.float32(0.25)                            # all equal
+    logits[4] = -np.inf                                     # two scores above -Inf, NaN at expert 0: passes 3
+    logits[4, 0], logits[4, 9], logits[4, 20] = np.nan, 1.0, 2.0   # and 4 fall back to expert 0 (NaN, then -Inf)
+    logits[5] = -np.inf                                     # expert 0 wins first, then only the fallback
+    logits[5, 0] = 3.0
+    logits[6, 1], logits[6, 2] = np.float32(-0.0), np.float32(0.0)  # -0 == +0: a tie, the lower expert first
+    logits[6, 5:] = -1.0
+    logits[6, 0] = -1.0
+    logits[6, 3:5] = -1.0
+    logits[7, 30], logits[7, 31] = np.inf, np.inf           # +Inf wins, ties by expert
     w = rng.random((SEQ, E)).astype(np.float32)
     scale = (0.5 + rng.random(E)).astype(np.float32)
     for mode in (M.TOPK_RAW, M.TOPK_SOFTMAX, M.TOPK_NORMALIZE):
