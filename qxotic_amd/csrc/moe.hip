@@ -225,16 +225,22 @@ JAMHIP_DEV void chunk_slots(const int* __restrict__ route_expert, int R, int E, 
                             int* __restrict__ route_slot) {
     __shared__ int wcnt[RCH_WAVES * 256], base[256], scan[RCH];
     const int t = threadIdx.x, wave = t >> 6;
-    // exclusive scan of the totals over the experts (Hillis-Steele in LDS)
-    scan[t] = t < E ? total : 0;
-    __syncthreads();
-    for (int o = 1; o < RCH; o <<= 1) {
-        const int x = t >= o ? scan[t - o] : 0;
+    // exclusive scan of the totals over the experts: one wave's shuffles for up to 64 experts (no barrier),
+    // else Hillis-Steele in LDS
+    int oe = 0;
+    if (E <= 64) {
+        if (t < 64) oe = wave_exclusive_scan(t < E ? total : 0);
+    } else {
+        scan[t] = t < E ? total : 0;
         __syncthreads();
-        scan[t] += x;
-        __syncthreads();
+        for (int o = 1; o < RCH; o <<= 1) {
+            const int x = t >= o ? scan[t - o] : 0;
+            __syncthreads();
+            scan[t] += x;
+            __syncthreads();
+        }
+        oe = scan[t] - (t < E ? total : 0);
     }
-    const int oe = scan[t] - (t < E ? total : 0);
     if (t < E) {
         base[t] = oe + before;
         if (blockIdx.x == 0) {
@@ -548,23 +554,31 @@ __global__ void __launch_bounds__(256) moe_topk_kernel(float* __restrict__ sel, 
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // softmax: lane i < topk takes the exp of the i-th logit (the double exp is the long part), then lane 0 runs
+    // the rest in order
+    if (mode == MOE_TOPK_SOFTMAX && lane < topk) {
+        float mx = -INFINITY;
+        for (int i = 0; i < topk; i++) {
+            const float q = sp[wv][i];
+            mx = (isnan(mx) || isnan(q)) ? __builtin_nanf("") : fmaxf(mx, q);
+        }
+        const float ex = (float) exp((double) __fsub_rn(sp[wv][lane], mx));
+        __builtin_amdgcn_wave_barrier();   // every lane has read sp before lane i overwrites entry i
+        sp[wv][lane] = ex;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     if (lane != 0) return;
     // loops unrolled over the maximum with a guard, so p stays in registers; each runs i = 0, 1, ... in order
     float p[MOE_TOPK_MAX];
 #pragma unroll
     for (int i = 0; i < MOE_TOPK_MAX; i++) p[i] = i < topk ? sp[wv][i] : 0.0f;
     if (mode == MOE_TOPK_SOFTMAX) {
-        float mx = -INFINITY;
-#pragma unroll
-        for (int i = 0; i < MOE_TOPK_MAX; i++)
-            if (i < topk) mx = (isnan(mx) || isnan(p[i])) ? __builtin_nanf("") : fmaxf(mx, p[i]);
         float total = 0.0f;
 #pragma unroll
         for (int i = 0; i < MOE_TOPK_MAX; i++)
-            if (i < topk) {
-                p[i] = (float) exp((double) __fsub_rn(p[i], mx));
-                total = __fadd_rn(total, p[i]);
-            }
+            if (i < topk) total = __fadd_rn(total, p[i]);   // p[i] = exp(logit_i - max), from lane i
         const float inv = total == 0.0f ? 0.0f : __fdiv_rn(1.0f, total);
 #pragma unroll
         for (int i = 0; i < MOE_TOPK_MAX; i++) p[i] = __fmul_rn(__fmul_rn(p[i], inv), wscale);
