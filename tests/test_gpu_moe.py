@@ -159,10 +159,10 @@ def test_mm_grouped_parity(hip, oracle, dt, m, k, counts):
         hip.evict(Segment.of(w))
 
 
-@pytest.mark.parametrize("native", [0, 2])
 @pytest.mark.parametrize("seq,topk,E", [(200, 4, 8), (24, 4, 32), (2, 4, 16)], ids=["dense", "mid", "sparse"])
-@pytest.mark.parametrize("dt,m,k", [(O.MXFP4, 64, 576), (O.Q4_K, 96, 512), (O.MXFP4, 48, 320)])
-def test_mm_grouped_gather_matches_two_calls(hip, oracle, dt, m, k, seq, topk, E, native):
+@pytest.mark.parametrize("dt,m,k,native", [(O.MXFP4, 64, 576, 0), (O.MXFP4, 64, 576, 2), (O.Q4_K, 96, 512, 0),
+                                           (O.MXFP4, 48, 320, 0), (O.MXFP4, 48, 320, 2)])
+def test_mm_grouped_gather_matches_two_calls(hip, oracle, dt, m, k, native, seq, topk, E):
     """jamhip_mm_grouped_gather (CSR row r of A = row slot_route[r] / topk of x) is bit-identical to
     jamhip_moe_gather followed by jamhip_mm_grouped_ex, offsets included: the fused preps reading x themselves
     (dense: rows_cap >= 8 per expert on the matrix cores, jam's path and native MX mode 2) and the paths that
@@ -170,8 +170,6 @@ def test_mm_grouped_gather_matches_two_calls(hip, oracle, dt, m, k, seq, topk, E
     with a row pitch above k, expert biases on the dense case."""
     import torch
     from qxotic_amd.jam import JAM, Segment
-    if native and dt != O.MXFP4:
-        pytest.skip("native MX mode is MXFP4 only")
     say(f"grouped gather {O.NAMES[dt]} m={m} k={k} seq={seq} topk={topk} E={E} native={native}")
     R = seq * topk
     re = routes(0xC0DE + seq + E, seq, topk, E)
