@@ -6,6 +6,8 @@
 #include "common.h"
 #include "launch.h"
 
+#include <type_traits>
+
 #include <atomic>
 
 namespace jamhip {
@@ -526,16 +528,30 @@ __global__ void __launch_bounds__(256) moe_topk_kernel(float* __restrict__ sel, 
                 bv = v[j];
                 bi = lane + 64 * j;
             }
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) {
-            const float ov = __shfl_xor(bv, o);
-            const int oi = __shfl_xor(bi, o);
+        // the wave's largest value, lowest expert on ties, by DPP steps (quad swaps, then rotations by 4 and 8
+        // inside each 16-lane row, then each row's result passed on by row_bcast:15 / :31): lane 63 holds it
+        auto take = [&](float ov, int oi) {
             if (ov > bv || (ov == bv && oi < bi)) {
                 bv = ov;
                 bi = oi;
             }
-        }
-        const int best = bi == INT_MAX ? 0 : bi;
+        };
+        auto dpp_step = [&](auto C, auto RM) {
+            constexpr int ctrl = decltype(C)::value, row_mask = decltype(RM)::value;
+            const int vb = __builtin_bit_cast(int, bv);
+            const float ov = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(vb, vb, ctrl, row_mask, 0xF, false));
+            const int oi = __builtin_amdgcn_update_dpp(bi, bi, ctrl, row_mask, 0xF, false);
+            take(ov, oi);
+        };
+        using I = std::integral_constant<int, 0xF>;
+        dpp_step(std::integral_constant<int, 0xB1>{}, I{});               // quad_perm [1, 0, 3, 2]
+        dpp_step(std::integral_constant<int, 0x4E>{}, I{});               // quad_perm [2, 3, 0, 1]
+        dpp_step(std::integral_constant<int, 0x124>{}, I{});              // row_ror:4
+        dpp_step(std::integral_constant<int, 0x128>{}, I{});              // row_ror:8
+        dpp_step(std::integral_constant<int, 0x142>{}, std::integral_constant<int, 0xA>{});   // row_bcast:15
+        dpp_step(std::integral_constant<int, 0x143>{}, std::integral_constant<int, 0xC>{});   // row_bcast:31
+        bi = __builtin_amdgcn_readlane(bi, 63);
+        const int best = bi == INT_MAX || bi < 0 || bi >= E ? 0 : bi;
         float pw = 0.0f;
         if (lane == (best & 63)) {
 #pragma unroll
