@@ -69,83 +69,112 @@ __global__ void __launch_bounds__(256) mxn_prep_kernel(const float* __restrict__
     const int x8 = (int) (blockIdx.x % 8), nw = (int) (gridDim.x >> 3), P8 = ((P + 7) / 8 + 7) & ~7;
     const int t_first = fused ? x8 * P8 + (int) (blockIdx.x >> 3) : (int) blockIdx.x;
     const int t_end = fused ? min((x8 + 1) * P8, P) : (int) blockIdx.x + 1;
-    for (int t = t_first; t < t_end; t += fused ? nw : 1) {
-        int src;
-        if (fused) {
-            slot_owner_store(pg, so, t, &own, nullptr);
-            __syncthreads();
-            src = own;
-            __syncthreads();   // own is the next slot's
-        } else {
-            src = slot_source(t, n, gmap, goff, gpoff);
+    const int sub = threadIdx.x & 7, nb = Kp / 32;
+    constexpr int RQ = 4;   // rounds in flight
+    // slot t's source row (-1: padding); in fused mode the owner thread passes it through LDS (every thread calls)
+    auto resolve = [&](int t) -> int {
+        if (!fused) return slot_source(t, n, gmap, goff, gpoff);
+        slot_owner_store(pg, so, t, &own, nullptr);
+        __syncthreads();
+        const int r = own;
+        __syncthreads();   // own is the next slot's
+        return r;
+    };
+    // the loads of pass r0 of row src (blocks r0 .. r0 + 32·RQ - 1, eight lanes per block; zeros past k)
+    auto load = [&](int src, int r0, float (&x)[RQ][4]) {
+        const float* row = a + (int64_t) (src >= 0 ? src : 0) * lda;
+#pragma unroll
+        for (int u = 0; u < RQ; u++) {
+            const int b = r0 + 32 * u + (threadIdx.x >> 3), col = 32 * b + 4 * sub;
+            if (src >= 0 && b < nb && vec && col + 3 < k) {   // a and lda 16-byte aligned (the launcher checks)
+                const float4 f = *reinterpret_cast<const float4*>(row + col);
+                x[u][0] = f.x, x[u][1] = f.y, x[u][2] = f.z, x[u][3] = f.w;
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; i++) x[u][i] = src >= 0 && b < nb && col + i < k ? row[col + i] : 0.0f;
+            }
         }
+    };
+    // the codes, scales and stores of pass r0 of slot t
+    auto code = [&](int t, int r0, float (&x)[RQ][4]) {
+#pragma unroll
+        for (int u = 0; u < RQ; u++) {
+            const int b = r0 + 32 * u + (threadIdx.x >> 3);
+            if (r0 + 32 * u >= nb) break;   // uniform: no block of this round exists
+            float amax = fmaxf(fmaxf(fabsf(x[u][0]), fabsf(x[u][1])), fmaxf(fabsf(x[u][2]), fabsf(x[u][3])));
+#pragma unroll
+            for (int o = 4; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 8));
+            int E = -127;
+            if (amax > 0.0f) {
+                int ee;
+                const float f = frexpf(amax / 448.0f, &ee);   // amax / 448 = f · 2^ee
+                E = f == 0.5f ? ee - 1 : ee;
+                if (ldexpf(amax, -E) > 448.0f) E += 1;        // rounding in amax / 448
+                E = max(-127, min(127, E));
+            }
+            const bool lo_ok = mode == 1 && E - 4 >= -127;
+            // x·2^-E is exact (|v| <= 448); the hardware conversion gives the nearest OCP e4m3 code, ties to the
+            // even code; + 0.0f turns a -0 into +0 (code 0x00, not 0x80)
+            float v[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) v[i] = ldexpf(x[u][i], -E) + 0.0f;
+            uint32_t ch = (uint32_t) __builtin_amdgcn_cvt_pk_fp8_f32(v[0], v[1], 0, false);
+            ch = (uint32_t) __builtin_amdgcn_cvt_pk_fp8_f32(v[2], v[3], (int) ch, true);
+            uint32_t cl = 0;
+            if (lo_ok) {
+                const float hv[4] = {__builtin_amdgcn_cvt_f32_fp8((int) ch, 0), __builtin_amdgcn_cvt_f32_fp8((int) ch, 1),
+                                     __builtin_amdgcn_cvt_f32_fp8((int) ch, 2), __builtin_amdgcn_cvt_f32_fp8((int) ch, 3)};
+                float rr[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) rr[i] = (v[i] - hv[i]) * 16.0f + 0.0f;
+                cl = (uint32_t) __builtin_amdgcn_cvt_pk_fp8_f32(rr[0], rr[1], 0, false);
+                cl = (uint32_t) __builtin_amdgcn_cvt_pk_fp8_f32(rr[2], rr[3], (int) cl, true);
+            }
+            const uint32_t ph = __shfl_xor(ch, 4, 8), pl = __shfl_xor(cl, 4, 8);
+            if (b < nb && sub < 4) {
+                // bytes: own0, partner0, own1, partner1, ... (elements e, e + 16 of the block)
+                auto mix = [](uint32_t o, uint32_t p) {
+                    const uint32_t lo16 = (o & 0xffu) | ((p & 0xffu) << 8) | ((o & 0xff00u) << 8) | ((p & 0xff00u) << 16);
+                    const uint32_t hi16 = ((o >> 16) & 0xffu) | (((p >> 16) & 0xffu) << 8) | ((o >> 24) << 16) | ((p >> 24) << 24);
+                    return make_uint2(lo16, hi16);
+                };
+                const int64_t off = ((int64_t) ((b >> 1) * 2 + (sub >> 1)) * NP + t) * 32 + 16 * (b & 1) + 8 * (sub & 1);
+                *reinterpret_cast<uint2*>(hi + off) = mix(ch, ph);
+                if (mode == 1) *reinterpret_cast<uint2*>(lo + off) = mix(cl, pl);
+                if (sub == 0) {
+                    shi[(int64_t) b * NP + t] = (uint8_t) (E + 127);
+                    if (mode == 1) slo[(int64_t) b * NP + t] = lo_ok ? (uint8_t) (E - 4 + 127) : (uint8_t) 0;
+                }
+            }
+        }
+    };
+    const int step = fused ? nw : 1;
+    if (nb <= 32 * RQ) {
+        // one pass per slot: the next slot's loads are issued before this slot's codes are computed
+        float xa[RQ][4], xb[RQ][4];
+        int t = t_first, src = t < t_end ? resolve(t) : -1;
+        if (t < t_end && src >= 0) load(src, 0, xa);
+        while (t < t_end) {
+            const int tn = t + step;
+            const int srcn = tn < t_end ? resolve(tn) : -1;   // uniform: every thread resolves
+            if (srcn >= 0) load(srcn, 0, xb);
+            if (src >= 0) code(t, 0, xa);
+#pragma unroll
+            for (int u = 0; u < RQ; u++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) xa[u][i] = xb[u][i];
+            t = tn;
+            src = srcn;
+        }
+        return;
+    }
+    for (int t = t_first; t < t_end; t += step) {
+        const int src = resolve(t);
         if (src < 0) continue;   // uniform over the workgroup
-        const float* row = a + (int64_t) src * lda;
-        const int sub = threadIdx.x & 7, nb = Kp / 32;
-        constexpr int RQ = 4;   // rounds in flight
         for (int r0 = 0; r0 < nb; r0 += 32 * RQ) {
             float x[RQ][4];
-#pragma unroll
-            for (int u = 0; u < RQ; u++) {
-                const int b = r0 + 32 * u + (threadIdx.x >> 3), col = 32 * b + 4 * sub;
-                if (b < nb && vec && col + 3 < k) {   // a and lda 16-byte aligned (the launcher checks)
-                    const float4 f = *reinterpret_cast<const float4*>(row + col);
-                    x[u][0] = f.x, x[u][1] = f.y, x[u][2] = f.z, x[u][3] = f.w;
-                } else {
-#pragma unroll
-                    for (int i = 0; i < 4; i++) x[u][i] = b < nb && col + i < k ? row[col + i] : 0.0f;
-                }
-            }
-#pragma unroll
-            for (int u = 0; u < RQ; u++) {
-                const int b = r0 + 32 * u + (threadIdx.x >> 3);
-                if (r0 + 32 * u >= nb) break;   // uniform: no block of this round exists
-                float amax = fmaxf(fmaxf(fabsf(x[u][0]), fabsf(x[u][1])), fmaxf(fabsf(x[u][2]), fabsf(x[u][3])));
-#pragma unroll
-                for (int o = 4; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 8));
-                int E = -127;
-                if (amax > 0.0f) {
-                    int ee;
-                    const float f = frexpf(amax / 448.0f, &ee);   // amax / 448 = f · 2^ee
-                    E = f == 0.5f ? ee - 1 : ee;
-                    if (ldexpf(amax, -E) > 448.0f) E += 1;        // rounding in amax / 448
-                    E = max(-127, min(127, E));
-                }
-                const bool lo_ok = mode == 1 && E - 4 >= -127;
-                // x·2^-E is exact (|v| <= 448); the hardware conversion gives the nearest OCP e4m3 code, ties to the
-                // even code; + 0.0f turns a -0 into +0 (code 0x00, not 0x80)
-                float v[4];
-#pragma unroll
-                for (int i = 0; i < 4; i++) v[i] = ldexpf(x[u][i], -E) + 0.0f;
-                uint32_t ch = (uint32_t) __builtin_amdgcn_cvt_pk_fp8_f32(v[0], v[1], 0, false);
-                ch = (uint32_t) __builtin_amdgcn_cvt_pk_fp8_f32(v[2], v[3], (int) ch, true);
-                uint32_t cl = 0;
-                if (lo_ok) {
-                    const float hv[4] = {__builtin_amdgcn_cvt_f32_fp8((int) ch, 0), __builtin_amdgcn_cvt_f32_fp8((int) ch, 1),
-                                         __builtin_amdgcn_cvt_f32_fp8((int) ch, 2), __builtin_amdgcn_cvt_f32_fp8((int) ch, 3)};
-                    float rr[4];
-#pragma unroll
-                    for (int i = 0; i < 4; i++) rr[i] = (v[i] - hv[i]) * 16.0f + 0.0f;
-                    cl = (uint32_t) __builtin_amdgcn_cvt_pk_fp8_f32(rr[0], rr[1], 0, false);
-                    cl = (uint32_t) __builtin_amdgcn_cvt_pk_fp8_f32(rr[2], rr[3], (int) cl, true);
-                }
-                const uint32_t ph = __shfl_xor(ch, 4, 8), pl = __shfl_xor(cl, 4, 8);
-                if (b < nb && sub < 4) {
-                    // bytes: own0, partner0, own1, partner1, ... (elements e, e + 16 of the block)
-                    auto mix = [](uint32_t o, uint32_t p) {
-                        const uint32_t lo16 = (o & 0xffu) | ((p & 0xffu) << 8) | ((o & 0xff00u) << 8) | ((p & 0xff00u) << 16);
-                        const uint32_t hi16 = ((o >> 16) & 0xffu) | (((p >> 16) & 0xffu) << 8) | ((o >> 24) << 16) | ((p >> 24) << 24);
-                        return make_uint2(lo16, hi16);
-                    };
-                    const int64_t off = ((int64_t) ((b >> 1) * 2 + (sub >> 1)) * NP + t) * 32 + 16 * (b & 1) + 8 * (sub & 1);
-                    *reinterpret_cast<uint2*>(hi + off) = mix(ch, ph);
-                    if (mode == 1) *reinterpret_cast<uint2*>(lo + off) = mix(cl, pl);
-                    if (sub == 0) {
-                        shi[(int64_t) b * NP + t] = (uint8_t) (E + 127);
-                        if (mode == 1) slo[(int64_t) b * NP + t] = lo_ok ? (uint8_t) (E - 4 + 127) : (uint8_t) 0;
-                    }
-                }
-            }
+            load(src, r0, x);
+            code(t, r0, x);
         }
     }
 }
