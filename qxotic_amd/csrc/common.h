@@ -177,6 +177,9 @@ JAMHIP_DEV F16Pair split_f16(float v) {
 }
 
 JAMHIP_DEV int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+// The value of lane ^ 1 through DPP (quad_perm [1, 0, 3, 2]): no LDS round trip; both lanes of the pair active.
+JAMHIP_DEV int xor1_i(int v) { return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, true); }
+JAMHIP_DEV float xor1_f(float v) { return __builtin_bit_cast(float, xor1_i(__builtin_bit_cast(int, v))); }
 
 template <int CTRL> JAMHIP_DEV float dpp(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));

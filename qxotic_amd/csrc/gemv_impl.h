@@ -490,7 +490,7 @@ JAMHIP_DEV void f1_store(const APre<HP>& pre, int k, int Gk, int ntv, int8_t* lq
         float am = 0.0f;
 #pragma unroll
         for (int e = 0; e < 16; e++) am = fmaxf(am, fabsf(x[e]));
-        am = fmaxf(am, __shfl_xor(am, 1));
+        am = fmaxf(am, xor1_f(am));
         const float db = am / 127.0f;
         const float id = db > 0.0f ? 1.0f / db : 0.0f;
         if constexpr (F16P == 2) {
@@ -544,7 +544,7 @@ JAMHIP_DEV void f1_store(const APre<HP>& pre, int k, int Gk, int ntv, int8_t* lq
         s = dot4((int) pk[1], 0x01010101, s);
         s = dot4((int) pk[2], 0x01010101, s);
         s = dot4((int) pk[3], 0x01010101, s);
-        const int s32 = s + __shfl_xor(s, 1);
+        const int s32 = s + xor1_i(s);
         int8_t* pq = valid ? lq + (int64_t) (j * Gk + (hh >> 4)) * QS_LDS + 16 * (hh & 15) : (int8_t*) dummy;
         int* p16 = valid ? ls16 + j * halves + hh : (int*) (dummy + 16);
         const bool first = (hh & 1) == 0;
@@ -710,7 +710,7 @@ __global__ void __launch_bounds__(64 * NWV) mv_kernel(WeightView w, ActQ A, cons
     __builtin_amdgcn_sched_barrier(0);
 
     extern __shared__ __align__(16) unsigned char smem[];
-    float* part = reinterpret_cast<float*>(smem);   // [8·ITEMS][GS][RB][NT] lane partials
+    float* part = reinterpret_cast<float*>(smem);   // lane partials: [8·ITEMS][GS][RB][NT], one token [8·ITEMS][RB][GS]
     const int nbf = kf >> 5;                     // strides of A are the full row's
     const int8_t* aq = A.q + k0;
     const float* ad = A.d + (k0 >> 5);
@@ -763,7 +763,8 @@ __global__ void __launch_bounds__(64 * NWV) mv_kernel(WeightView w, ActQ A, cons
         const bool live = g < Gk && it < QB * J && RB * (q0 + it / J) + rr < m;
         const int gg = g < Gk ? g : Gk - 1;
         const int nbv = nb - 8 * gg < 8 ? nb - 8 * gg : 8;   // the group's 32-blocks inside the slice
-        float* pp = part + (it * 64 + lane) * NT;
+        // one token: a row's GS partials of an item are contiguous (read back as 16-byte pieces)
+        float* pp = part + (NT == 1 ? it * 64 + rr * GS + gs : (it * 64 + lane) * NT);
         if constexpr (NT <= 2 || DT != Q4_0) {   // per-token unpacking measured faster for the rest
             constexpr int TU = NT > 2 ? 1 : NT;   // keep several tokens' temporaries out of the register file
 #pragma unroll TU
@@ -803,9 +804,24 @@ __global__ void __launch_bounds__(64 * NWV) mv_kernel(WeightView w, ActQ A, cons
     for (int tid = threadIdx.x; tid < QB * RB * NT; tid += 64 * NWV) {
         const int q = tid / (RB * NT), r = (tid / NT) % RB, t = tid % NT;
         float v = 0.0f;
-        for (int j = 0; j < J; j++)
+        if constexpr (NT == 1 && GS % 4 == 0) {
+            const float4* src = reinterpret_cast<const float4*>(part + q * J * 64 + r * GS);
+#pragma unroll 2
+            for (int j = 0; j < J; j++) {
 #pragma unroll
-            for (int s2 = 0; s2 < GS; s2++) v += part[(((q * J + j) * 64) + s2 * RB + r) * NT + t];
+                for (int s4 = 0; s4 < GS / 4; s4++) {
+                    const float4 f = src[j * 16 + s4];
+                    v += f.x;
+                    v += f.y;
+                    v += f.z;
+                    v += f.w;
+                }
+            }
+        } else {
+            for (int j = 0; j < J; j++)
+#pragma unroll
+                for (int s2 = 0; s2 < GS; s2++) v += part[(((q * J + j) * 64) + s2 * RB + r) * NT + t];
+        }
         const int64_t row = RB * (q0 + q) + r;
         if (row < m && t < ntv) {
             float* dst = c + (int64_t) (t0 + t) * ldc + row;
