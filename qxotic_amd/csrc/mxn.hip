@@ -100,7 +100,7 @@ __global__ void __launch_bounds__(256) mxn_prep_kernel(const float* __restrict__
 #pragma unroll
         for (int u = 0; u < RQ; u++) {
             const int b = r0 + 32 * u + (threadIdx.x >> 3);
-            if (r0 + 32 * u >= nb) break;   // uniform: no block of this round exists
+            if (r0 + 32 * u >= nb) break;   // uniform: no block of this load step exists
             float amax = fmaxf(fmaxf(fabsf(x[u][0]), fabsf(x[u][1])), fmaxf(fabsf(x[u][2]), fabsf(x[u][3])));
 #pragma unroll
             for (int o = 4; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 8));

@@ -156,7 +156,7 @@ def rand_nibs(rng, nonzero=True):
     return nib
 
 
-# ------------------------------------------------------------------------- the verdict's edge cases
+# ------------------------------------------------------------------------- the scale-folding edge cases
 def mx_cases():
     rng = np.random.default_rng(7)
     cases = {}
