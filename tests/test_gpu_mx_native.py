@@ -42,7 +42,7 @@ def run(hip, w, a, m, n, k):
 
 
 @pytest.mark.parametrize("mode", [1, 2])
-@pytest.mark.parametrize("m,k,n", [(128, 2880, 64), (256, 1024, 100), (512, 2880, 37), (96, 4096, 512)])
+@pytest.mark.parametrize("m,k,n", [(128, 2880, 64), (256, 1024, 100), (512, 2880, 37), (96, 4096, 512), (64, 6176, 40)])
 def test_mx_native_matches_restatement(hip, oracle, mode, m, k, n):
     say(f"mx native mode={mode} m={m} k={k} n={n}")
     w = oracle.quantize(O.MXFP4, oracle.normal(7 + m, (m, k), 0.0, 0.02))
@@ -125,3 +125,42 @@ def test_mx_native_grouped(hip, oracle, mode, E):
             ref = oracle.mm_int8(O.MXFP4, we, a[rows], m, int(counts[e]), k)
             _, sa = oracle.mm_ref(O.MXFP4, we, a[rows], m, int(counts[e]), k)
             assert (np.abs(got[rows] - ref) <= 1e-3 * np.abs(ref) + 1e-5 * sa).all(), f"expert {e}"
+
+
+@pytest.mark.parametrize("mode,k", [(2, 2880), (1, 6176)])
+def test_mx_native_grouped_many_slots(hip, oracle, mode, k):
+    """The fused grouped prep with more real slots than its 1024 workgroups (1530 rows over 6 experts, one
+    empty and one of a single row), so that workgroups loop over several slots with the next slot's loads
+    issued ahead; k = 6176 (193 blocks) takes two passes per row, the second one partial. Every expert against
+    the restatement, the offsets and rows past the prefix untouched."""
+    import torch
+    from qxotic_amd.jam import JAM, Segment
+    say(f"mx native grouped many slots mode={mode} k={k}")
+    m, E = 32, 6
+    counts = np.array([700, 0, 1, 300, 9, 520], np.int32)
+    R = int(counts.sum())
+    w = oracle.quantize(O.MXFP4, oracle.normal(37 + k, (E * m, k), 0.0, 0.02))
+    a = acts(38 + k, R, k)
+    dev = lambda x: torch.from_numpy(np.ascontiguousarray(x)).cuda()
+    counts_d, a_d = dev(counts), dev(a)
+    c = torch.full((R + 3, m), 7.0, dtype=torch.float32, device="cuda")
+    offs = torch.full((E + 1,), -5, dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()
+    assert hip.set_mx_native(mode) == 0
+    try:
+        st = hip.mm_grouped(Segment.of(w), JAM.MXFP4, k, m, E, counts_d.data_ptr(), a_d.data_ptr(), k,
+                            c.data_ptr(), m, k, R, offs.data_ptr())
+        torch.cuda.synchronize()
+    finally:
+        hip.set_mx_native(0)
+    assert st == JAM.OK, hip.last_error()
+    got = c.cpu().numpy()
+    off = np.concatenate([[0], np.cumsum(counts)])
+    assert np.array_equal(offs.cpu().numpy(), off)
+    assert (got[R:] == 7.0).all()
+    for e in range(E):
+        if counts[e] == 0:
+            continue
+        rows = slice(off[e], off[e + 1])
+        ref, sref = X.mm(oracle.dequant(O.MXFP4, w[e * m:(e + 1) * m], k, f64=True), a[rows], mode)
+        assert (np.abs(got[rows] - ref) <= TOL_MFMA * sref + 1e-30).all(), f"expert {e}"
