@@ -197,6 +197,18 @@ JAMHIP_DEV float wave_sum(float v) {
     return (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
 }
 
+// Exclusive prefix sum over the 64 lanes of a wave (lane l gets the sum of lanes below it).
+JAMHIP_DEV int wave_exclusive_scan(int v) {
+    const int lane = threadIdx.x & 63;
+    int x = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(x, o);
+        if (lane >= o) x += y;
+    }
+    return x - v;
+}
+
 // E8M0 -> 2^(e-128) (jam/jam-native/src/kernels/jam_mxfp4.h:17-24): e=0 -> 2^-128, e=255 -> +Inf.
 JAMHIP_DEV float e8m0_half(uint32_t e) {
     uint32_t bits = e == 0 ? 0x00400000u : (e << 23);

@@ -660,10 +660,25 @@ __global__ void __launch_bounds__(64 * NWV) mv_kernel(WeightView w, ActQ A, cons
     if constexpr (GR) {
         int e, o, ne;
         if constexpr (FL == 1) {
-            e = gp.small != nullptr ? __builtin_amdgcn_readfirstlane(gp.small[blockIdx.y]) : (int) blockIdx.y;
-            if (e < 0) return;   // whole workgroup, before any barrier
-            o = __builtin_amdgcn_readfirstlane(gp.off[e]);
-            ne = __builtin_amdgcn_readfirstlane(gp.off[e + 1]) - o;
+            if (gp.counts != nullptr) {
+                // every wave: lane l holds expert l's clamped count (rows past rows_cap dropped) and its row
+                // offset; column y takes the y-th expert, in expert order, with 1 (NT = 1) or 2..7 rows
+                const int l = (int) (threadIdx.x & 63);
+                const int c0 = l < gp.n_experts ? min(max(gp.counts[l], 0), gp.rows_cap) : 0;
+                const int c = max(0, min(c0, gp.rows_cap - wave_exclusive_scan(c0)));
+                const int oc = wave_exclusive_scan(c);
+                uint64_t sel = __ballot(NT == 1 ? c == 1 : c >= 2 && c <= 7);
+                for (int i = 0; i < (int) blockIdx.y && sel != 0; i++) sel &= sel - 1;
+                if (sel == 0) return;   // whole workgroup, before any barrier
+                e = __builtin_ctzll(sel);
+                o = __builtin_amdgcn_readlane(oc, e);
+                ne = __builtin_amdgcn_readlane(c, e);
+            } else {
+                e = gp.small != nullptr ? __builtin_amdgcn_readfirstlane(gp.small[blockIdx.y]) : (int) blockIdx.y;
+                if (e < 0) return;   // whole workgroup, before any barrier
+                o = __builtin_amdgcn_readfirstlane(gp.off[e]);
+                ne = __builtin_amdgcn_readfirstlane(gp.off[e + 1]) - o;
+            }
             if (ne <= 0 || ne > NT) return;   // whole workgroup, before any barrier
             t0 = o;
             ntv = ne;

@@ -977,8 +977,11 @@ jamhip_status mm_grouped_ex_impl(jamhip_ctx* ctx, const void* w, int wt, int ldw
             return hip_fail(ctx, e, "grouped: gemm launch");
         return JAMHIP_OK;
     }
-    if ((e = launch_moe_offsets((const int*) counts_dev, E, rows_cap, off, poff64, poff8, map64, cap64, map8, cap8,
-                                small, n1, n2, ctx->stream)) != hipSuccess)
+    // Decode-sized calls (fewer than 8 rows in all, at most 64 experts, no offsets asked for, no gather): the F1
+    // kernels find their experts and rows from the counts themselves, so the offsets kernel does not run.
+    const bool derive = rows_cap < 8 && E <= 64 && offsets_dev == nullptr && x_rows == nullptr;
+    if (!derive && (e = launch_moe_offsets((const int*) counts_dev, E, rows_cap, off, poff64, poff8, map64, cap64,
+                                           map8, cap8, small, n1, n2, ctx->stream)) != hipSuccess)
         return hip_fail(ctx, e, "grouped: offsets launch");
     if (offsets_dev &&
         (e = hipMemcpyAsync(offsets_dev, off, (size_t) (E + 1) * sizeof(int), hipMemcpyDeviceToDevice, ctx->stream)) !=
@@ -1008,8 +1011,14 @@ jamhip_status mm_grouped_ex_impl(jamhip_ctx* ctx, const void* w, int wt, int ldw
     // one-token kernel over the experts with one row (decode: every expert), one of the seven-token kernel
     // over those with 2..7 (none can exist below rows_cap = 2)
     Groups g1 = g, g2 = g;
-    g1.small = small;
-    g2.small = small + n1;
+    if (derive) {
+        g1.counts = g2.counts = (const int*) counts_dev;
+        g1.n_experts = g2.n_experts = E;
+        g1.rows_cap = g2.rows_cap = rows_cap;
+    } else {
+        g1.small = small;
+        g2.small = small + n1;
+    }
     const bool fuse = gemv_grouped_fusable(k, a, lda);
     ActQ A{};
     if (!fuse) {

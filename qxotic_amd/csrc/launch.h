@@ -34,6 +34,10 @@ struct Groups {
     // an expert list in expert order, -1 past its last (launch_moe_offsets): the F1 grouped kernel's workgroup
     // column y takes expert small[y] (null: expert y)
     const int* small = nullptr;
+    // or, when counts is set (at most 64 experts, fewer than 8 rows in all): the F1 grouped kernel finds its
+    // expert and rows from the device counts itself, with launch_moe_offsets' clamps to rows_cap
+    const int* counts = nullptr;
+    int n_experts = 0, rows_cap = 0;
 };
 
 // Matrix-core GEMM workgroup -> linear tile; workgroup b runs on XCD b % 8. Ungrouped: each XCD takes one

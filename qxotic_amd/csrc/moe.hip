@@ -75,16 +75,6 @@ __global__ void __launch_bounds__(MOE_THREADS) moe_offsets_kernel(const int* __r
 }
 
 // The same for E <= 64 in a single wave: the four exclusive scans are wave scans (shuffles, no barriers).
-JAMHIP_DEV int wave_exclusive_scan(int v) {
-    const int lane = threadIdx.x & 63;
-    int x = v;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const int y = __shfl_up(x, o);
-        if (lane >= o) x += y;
-    }
-    return x - v;
-}
 __global__ void __launch_bounds__(64) moe_offsets_wave_kernel(const int* __restrict__ counts, int E, int rows_cap,
                                                              int* __restrict__ off, int* __restrict__ poff64,
                                                              int* __restrict__ poff8, int* __restrict__ map64,

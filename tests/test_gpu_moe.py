@@ -357,6 +357,58 @@ def test_grouped_status_codes(hip):
 
 
 @pytest.mark.parametrize("dt", [O.MXFP4, O.Q4_K])
+def test_mm_grouped_decode_counts_derived(hip, oracle, dt):
+    """Decode-sized calls without an offsets output: the F1 kernels find their experts and rows from the device
+    counts (no offsets launch, at most 64 experts). Each case is run with and without the offsets output (the
+    offsets-kernel path); both must give bit-identical C, equal to the oracle on the kept rows, with the
+    counts clamped as the offsets kernel clamps them (rows past rows_cap dropped, an expert cut short), 64
+    experts (the most a wave holds) and 70 (past it: the offsets kernel runs either way)."""
+    import torch
+    from qxotic_amd.jam import JAM, Segment
+    m, k = 32, 512
+    c64 = np.zeros(64, np.int64)
+    c64[[3, 17, 40, 63]] = [1, 2, 1, 3]
+    c70 = np.zeros(70, np.int64)
+    c70[[2, 65, 69]] = [2, 1, 1]
+    for counts, rows_cap in (([2, 0, 5, 1], 5), ([1, 1, 0, 9], 4), (c64.tolist(), 7), (c70.tolist(), 4)):
+        E = len(counts)
+        c0 = np.clip(np.array(counts), 0, rows_cap)
+        o = np.concatenate([[0], np.cumsum(c0)[:-1]])
+        kept = np.maximum(0, np.minimum(c0, rows_cap - o)).tolist()
+        say(f"grouped decode derived {O.NAMES[dt]} E={E} rows_cap={rows_cap} kept={[x for x in kept if x]}")
+        w_e = [oracle.quantize(dt, oracle.normal(0xDE71 + 7 * e + dt, (m, k), 0.0, 0.02)) for e in range(E)]
+        w = np.ascontiguousarray(np.concatenate(w_e, axis=0))
+        a = oracle.outliers(0xDE72 + E + rows_cap, (rows_cap, k))
+        assert hip.pin(Segment.of(w), dt, k, E * m) == JAM.OK, hip.last_error()
+        try:
+            a_dv = dev(a)
+            counts_dv = dev(np.array(counts, np.int32))
+            outs = []
+            for with_off in (False, True):
+                c = torch.full((rows_cap + 1, m + 2), -3.0, dtype=torch.float32, device="cuda")
+                off = torch.zeros(E + 1, dtype=torch.int32, device="cuda")
+                torch.cuda.synchronize()
+                assert hip.mm_grouped(Segment.of(w), dt, k, m, E, counts_dv.data_ptr(), a_dv.data_ptr(), k,
+                                      c.data_ptr(), m + 2, k, rows_cap,
+                                      off.data_ptr() if with_off else None) == JAM.OK, hip.last_error()
+                hip.synchronize()
+                outs.append(c.cpu().numpy())
+            assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+            got = outs[0]
+            ref = M.mm_grouped(oracle, dt, w_e, a, kept, m, k)
+            r0 = 0
+            for e, n in enumerate(kept):
+                if n:
+                    _, sa = oracle.mm_ref(dt, w_e[e], np.ascontiguousarray(a[r0:r0 + n]), m, n, k)
+                    r = ref[r0:r0 + n]
+                    assert (np.abs(got[r0:r0 + n, :m] - r) <= 1e-3 * np.abs(r) + 1e-5 * sa).all(), (e, n)
+                r0 += n
+            assert (got[r0:] == -3.0).all() and (got[:, m:] == -3.0).all()
+        finally:
+            hip.evict(Segment.of(w))
+
+
+@pytest.mark.parametrize("dt", [O.MXFP4, O.Q4_K])
 def test_mm_grouped_decode_unfused(hip, oracle, dt):
     """The grouped F1 decode kernels reading the quantized copy instead of quantizing in their prologue: k past
     the fused prologue's reach (k = 5120, 14336) and rows not 16-byte aligned (lda = k + 1), with one-row and
