@@ -628,221 +628,39 @@ JAMHIP_DEV void stage_store(const FPre<SP>& pre, int k, int Gk, int8_t* lq, floa
 // group may hold fewer (ntv).
 // GR (grouped matmul): FL = 1 takes expert blockIdx.y if it has 1..7 rows (ntv of them, CSR rows from
 // off[e]); FL = 2 takes the 8-token tile blockIdx.y of map8. The expert's weight rows start at e·gm.
+// The kernel body; by is the workgroup's column (a column of one flavour's range in mv_pair_kernel).
+template <int DT, int FL, int NT, int HP, int RB, int ITEMS, bool GR, bool SK, int NWV>
+__device__ __attribute__((always_inline)) inline void mv_body(WeightView w, ActQ A, const float* __restrict__ a,
+                                                              int lda, int k, int m, int n, float* __restrict__ c,
+                                                              int ldc, Groups gp, int ks, int64_t cz, Epi ep,
+                                                              unsigned by) {
+#define MV_COL by
+#include "gemv_body.inc"
+#undef MV_COL
+}
+
 template <int DT, int FL, int NT, int HP, int RB, int ITEMS, bool GR, bool SK, int NWV>
 __global__ void __launch_bounds__(64 * NWV) mv_kernel(WeightView w, ActQ A, const float* __restrict__ a,
                                                           int lda, int k, int m, int n, float* __restrict__ c,
                                                           int ldc, Groups gp, int ks, int64_t cz, Epi ep) {
-    constexpr int GS = 64 / RB;
-    // SK (split K): workgroup column blockIdx.z takes elements [k0, k0 + ks) (ks a multiple of 256; the last
-    // slice may be shorter) and writes its partial result at c + blockIdx.z·cz; J, and so the block shape,
-    // comes from the full slice length, so every slice has the same grid
-    const int k0 = SK ? (int) blockIdx.z * ks : 0, kf = k;
-    if constexpr (SK) {
-        k = kf - k0 < ks ? kf - k0 : ks;
-        c += (int64_t) blockIdx.z * cz;
-        if constexpr (FL == 1 && HP > 0) a += k0;   // the fused prologue's rows (null otherwise)
-    }
-    // HP > 0: F1, A quantized into LDS by this workgroup (HP half-blocks per thread); F2, the quantized A
-    // staged in LDS (stage_load, HP pieces per thread)
-    constexpr bool QF1 = FL == 1 && HP > 0;
-    constexpr bool STG = FL == 2 && HP > 0;
-    constexpr int SP = HP;
-    constexpr bool FUSE = HP > 0;
-    const int lane = threadIdx.x & 63, rr = lane % RB, gs = lane / RB;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int nb = k >> 5;                       // 32-blocks in the slice
-    const int Gk = (nb + 7) >> 3;                // groups in the slice
-    const int J = ((SK ? ((ks >> 5) + 7) / 8 : Gk) + GS - 1) / GS;   // items per row band
-    const int g0 = k0 >> 8;                      // the slice's first group
-    const int QB = NWV * ITEMS / J;              // bands per block (the launcher keeps J <= NWV·ITEMS)
-    const int64_t q0 = (int64_t) blockIdx.x * QB;
-    int t0, ntv;
-    if constexpr (GR) {
-        int e, o, ne;
-        if constexpr (FL == 1) {
-            if (gp.counts != nullptr) {
-                // every wave: lane l holds expert l's clamped count (rows past rows_cap dropped) and its row
-                // offset; column y takes the y-th expert, in expert order, with 1 (NT = 1) or 2..7 rows
-                const int l = (int) (threadIdx.x & 63);
-                const int c0 = l < gp.n_experts ? min(max(gp.counts[l], 0), gp.rows_cap) : 0;
-                const int c = max(0, min(c0, gp.rows_cap - wave_exclusive_scan(c0)));
-                const int oc = wave_exclusive_scan(c);
-                uint64_t sel = __ballot(NT == 1 ? c == 1 : c >= 2 && c <= 7);
-                for (int i = 0; i < (int) blockIdx.y && sel != 0; i++) sel &= sel - 1;
-                if (sel == 0) return;   // whole workgroup, before any barrier
-                e = __builtin_ctzll(sel);
-                o = __builtin_amdgcn_readlane(oc, e);
-                ne = __builtin_amdgcn_readlane(c, e);
-            } else {
-                e = gp.small != nullptr ? __builtin_amdgcn_readfirstlane(gp.small[blockIdx.y]) : (int) blockIdx.y;
-                if (e < 0) return;   // whole workgroup, before any barrier
-                o = __builtin_amdgcn_readfirstlane(gp.off[e]);
-                ne = __builtin_amdgcn_readfirstlane(gp.off[e + 1]) - o;
-            }
-            if (ne <= 0 || ne > NT) return;   // whole workgroup, before any barrier
-            t0 = o;
-            ntv = ne;
-            a += (int64_t) o * lda;
-        } else {
-            e = __builtin_amdgcn_readfirstlane(gp.map8[blockIdx.y]);
-            if (e < 0) return;
-            const int local = (int) blockIdx.y * 8 - __builtin_amdgcn_readfirstlane(gp.poff8[e]);
-            o = __builtin_amdgcn_readfirstlane(gp.off[e]);
-            ne = __builtin_amdgcn_readfirstlane(gp.off[e + 1]) - o;
-            t0 = o + local;
-            ntv = ne - local < NT ? ne - local : NT;
-        }
-        w.r0 += (int64_t) e * gp.gm;
-        m = gp.gm;
-        if (gp.bias != nullptr) ep.bias = gp.bias + (int64_t) e * gp.gm;
-    } else {
-        t0 = blockIdx.y * NT;
-        ntv = n - t0 < NT ? n - t0 : NT;
-    }
+#define MV_COL blockIdx.y
+#include "gemv_body.inc"
+#undef MV_COL
+}
 
-    // Only waves that own at least one real half-block of the activations load and quantize them (the
-    // others would only write the dummy slot); the condition is wave-uniform. Their loads go first in the
-    // load queue and are kept there by the scheduler.
-    const bool pro = QF1 && wave * 64 * (QF1 ? HP : 1) < (NT == 1 ? 1 : ntv) * 16 * Gk;
-    APre<QF1 ? HP : 1> pre;
-    FPre<STG ? SP : 1> fpre;
-    if constexpr (QF1)
-        if (pro) a_load<NT, QF1 ? HP : 1, NWV>(pre, a, lda, k, Gk, ntv);
-    if constexpr (STG) stage_load<NT, SP, NWV>(fpre, A, kf, k0, k, Gk, t0, ntv);
-    __builtin_amdgcn_sched_barrier(0);
-
-    // item i of this wave: band q0 + it / J, group slot it % J with it = wave·ITEMS + i (clamped)
-    Group<DT> buf[ITEMS];
-#pragma unroll
-    for (int i = 0; i < ITEMS; i++) {
-        const int it = wave * ITEMS + i;
-        int64_t row = RB * (q0 + it / J) + rr;
-        row = row < m ? row : m - 1;
-        int g = GS * (it % J) + gs;
-        g = g < Gk ? g : Gk - 1;
-        load_group<DT>(buf[i], w, row, g0 + g);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-
-    extern __shared__ __align__(16) unsigned char smem[];
-    float* part = reinterpret_cast<float*>(smem);   // lane partials: [8·ITEMS][GS][RB][NT], one token [8·ITEMS][RB][GS]
-    const int nbf = kf >> 5;                     // strides of A are the full row's
-    const int8_t* aq = A.q + k0;
-    const float* ad = A.d + (k0 >> 5);
-    const float* as = A.s + (FL == 1 ? k0 >> 5 : k0 >> 4);
-    const int* s16 = A.s16 + (k0 >> 4);
-    int64_t tq = kf, td = nbf, ts = FL == 1 ? nbf : 2 * nbf, t16 = 2 * nbf;
-    int QS = 256;
-    if constexpr (FUSE) {
-        constexpr int F16P = f16_pairs<DT, FL, NT, HP>();
-        constexpr int QSB = F16P ? QS_F16 : QS_LDS;
-        char* dummy = reinterpret_cast<char*>(smem + NWV * ITEMS * 64 * NT * 4);   // 32 bytes
-        int8_t* lq = reinterpret_cast<int8_t*>(dummy + 32);
-        float* ld = reinterpret_cast<float*>(lq + NT * Gk * QSB);
-        float* las = ld + NT * 8 * Gk;
-        int* ls16 = reinterpret_cast<int*>(las + NT * 8 * Gk);
-        aq = lq;
-        ad = ld;
-        tq = (int64_t) Gk * QSB;
-        td = 8 * Gk;
-        QS = QSB;
-        if constexpr (QF1) {
-            if (pro) f1_store<NT, QF1 ? HP : 1, NWV, F16P>(pre, k, Gk, ntv, lq, ld, las, ls16, dummy);
-        } else {   // F2: per-16 sums in the Σq-per-16 region (16 per group and token)
-            stage_store<NT, SP, NWV>(fpre, k, Gk, lq, ld, reinterpret_cast<float*>(ls16));
-        }
-        // a wave that quantized exactly the groups it reads (see pro_half) only waits for its own stores
-        const bool wave_local = QF1 && NT == 1 && ITEMS == 1 && HP == 2 && QB == 1 && J == NWV && Gk == 8 * J;
-        if constexpr (FL == 1) {
-            as = las;
-            s16 = ls16;
-            ts = 8 * Gk;
-            t16 = 16 * Gk;
-        } else {
-            as = reinterpret_cast<const float*>(ls16);
-            ts = 16 * Gk;
-        }
-        if (wave_local) {
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        } else {
-            __syncthreads();
-        }
-    }
-
-#pragma unroll
-    for (int i = 0; i < ITEMS; i++) {
-        const int it = wave * ITEMS + i;
-        const int g = GS * (it % J) + gs;
-        const bool live = g < Gk && it < QB * J && RB * (q0 + it / J) + rr < m;
-        const int gg = g < Gk ? g : Gk - 1;
-        const int nbv = nb - 8 * gg < 8 ? nb - 8 * gg : 8;   // the group's 32-blocks inside the slice
-        // one token: a row's GS partials of an item are contiguous (read back as 16-byte pieces)
-        float* pp = part + (NT == 1 ? it * 64 + rr * GS + gs : (it * 64 + lane) * NT);
-        if constexpr (NT <= 2 || DT != Q4_0) {   // per-token unpacking measured faster for the rest
-            constexpr int TU = NT > 2 ? 1 : NT;   // keep several tokens' temporaries out of the register file
-#pragma unroll TU
-            for (int t = 0; t < NT; t++) {
-                if (t >= ntv) break;
-                const int tt = FUSE ? t : t0 + t;
-                float p;
-                if constexpr (f16_pairs<DT, FL, NT, HP>() == 1)
-                    p = mx_dot_f16(buf[i], aq + (int64_t) gg * QS, ad + 8 * gg, nbv);
-                else if constexpr (f16_pairs<DT, FL, NT, HP>() == 2)
-                    p = nv_dot_f16(buf[i], aq + (int64_t) gg * QS, ad + 8 * gg, nbv);
-                else
-                    p = group_dot<DT, FL>(buf[i], aq + tt * tq + (int64_t) gg * QS, ad + tt * td + 8 * gg,
-                                          as + tt * ts + (FL == 1 ? 8 : 16) * gg, s16 + tt * t16 + 16 * gg, nbv);
-                pp[t] = live ? p : 0.0f;
-            }
-        } else {   // Q4_0, 3..8 tokens: the group's weights unpacked once for all the tokens
-            Q40Codes u;
-            q40_unpack(buf[i], u);
-#pragma unroll 1
-            for (int t = 0; t < NT; t++) {
-                if (t >= ntv) break;
-                const int tt = FUSE ? t : t0 + t;
-                float p;
-                if constexpr (FL == 1)
-                    p = q40_dot_f1(u, aq + tt * tq + (int64_t) gg * QS, ad + tt * td + 8 * gg, s16 + tt * t16 + 16 * gg,
-                                   nbv);
-                else
-                    p = q40_dot_f2(u, aq + tt * tq + (int64_t) gg * QS, ad + tt * td + 8 * gg, as + tt * ts + 16 * gg,
-                                   nbv);
-                pp[t] = live ? p : 0.0f;
-            }
-        }
-    }
-    __syncthreads();
-    // (band, row, token) of the block: sum its J x GS partials in order; QB·RB·NT can exceed the 512 threads
-    for (int tid = threadIdx.x; tid < QB * RB * NT; tid += 64 * NWV) {
-        const int q = tid / (RB * NT), r = (tid / NT) % RB, t = tid % NT;
-        float v = 0.0f;
-        if constexpr (NT == 1 && GS % 4 == 0) {
-            const float4* src = reinterpret_cast<const float4*>(part + q * J * 64 + r * GS);
-#pragma unroll 2
-            for (int j = 0; j < J; j++) {
-#pragma unroll
-                for (int s4 = 0; s4 < GS / 4; s4++) {
-                    const float4 f = src[j * 16 + s4];
-                    v += f.x;
-                    v += f.y;
-                    v += f.z;
-                    v += f.w;
-                }
-            }
-        } else {
-            for (int j = 0; j < J; j++)
-#pragma unroll
-                for (int s2 = 0; s2 < GS; s2++) v += part[(((q * J + j) * 64) + s2 * RB + r) * NT + t];
-        }
-        const int64_t row = RB * (q0 + q) + r;
-        if (row < m && t < ntv) {
-            float* dst = c + (int64_t) (t0 + t) * ldc + row;
-            *dst = SK ? v : epilogue(ep, v, row, dst);
-        }
-    }
+// Both F1 grouped flavours in one launch (decode-sized calls whose experts come from the counts): columns
+// [0, n1) run the one-token body over the experts with one row, the rest the seven-token body over those
+// with 2..7 rows.
+template <int DT, int HP1, int HP7, int RB, int ITEMS>
+__global__ void __launch_bounds__(64 * MV_WAVES) mv_pair_kernel(WeightView w, ActQ A, const float* __restrict__ a,
+                                                                 int lda, int k, float* __restrict__ c, int ldc,
+                                                                 Groups gp, int n1) {
+    const int y = (int) blockIdx.y;
+    if (y < n1)
+        mv_body<DT, 1, 1, HP1, RB, ITEMS, true, false, MV_WAVES>(w, A, a, lda, k, gp.gm, 0, c, ldc, gp, k, 0, Epi{}, (unsigned) y);
+    else
+        mv_body<DT, 1, 7, HP7, RB, ITEMS, true, false, MV_WAVES>(w, A, a, lda, k, gp.gm, 0, c, ldc, gp, k, 0, Epi{},
+                                                                 (unsigned) (y - n1));
 }
 
 // ----------------------------------------------------------------------------- float-dot tail rows
@@ -1024,10 +842,48 @@ static hipError_t go_grouped(int k, const Groups& g, int ny, const WeightView& w
     return hipGetLastError();
 }
 
+template <int DT, int HP1, int HP7, int RB, int ITEMS>
+static void launch_pair(int k, const Groups& g, int n1, int n2, const WeightView& w, const ActQ& A, const float* a,
+                        int lda, float* c, int ldc, hipStream_t st) {
+    constexpr int GS = 64 / RB;
+    const int Gk = (k / 32 + 7) / 8, J = (Gk + GS - 1) / GS;
+    const int QB = MV_WAVES * ITEMS / J;
+    const int64_t bands = ((int64_t) g.gm + RB - 1) / RB;
+    const dim3 grid((unsigned) ((bands + QB - 1) / QB), (unsigned) (n1 + n2));
+    const size_t l1 = (size_t) MV_WAVES * ITEMS * 64 * sizeof(float) +
+                      (HP1 > 0 ? 32 + fuse_lds(1, k, f16_pairs<DT, 1, 1, HP1>()) : 0);
+    const size_t l7 = (size_t) MV_WAVES * ITEMS * 64 * 7 * sizeof(float) +
+                      (HP7 > 0 ? 32 + fuse_lds(7, k, f16_pairs<DT, 1, 7, HP7>()) : 0);
+    const size_t lds = l1 > l7 ? l1 : l7;
+    lds_allow((const void*) mv_pair_kernel<DT, HP1, HP7, RB, ITEMS>, lds);
+    mv_pair_kernel<DT, HP1, HP7, RB, ITEMS><<<grid, 64 * MV_WAVES, lds, st>>>(w, A, a, lda, k, c, ldc, g, n1);
+}
+
+template <int DT, int HP1, int HP7>
+static hipError_t go_pair(int k, const Groups& g, int n1, int n2, const WeightView& w, const ActQ& A, const float* a,
+                          int lda, float* c, int ldc, hipStream_t st) {
+    int items;
+    if (!mv_items(k, &items)) return hipErrorNotSupported;
+    if (items == 1) launch_pair<DT, HP1, HP7, MV_RB, 1>(k, g, n1, n2, w, A, a, lda, c, ldc, st);
+    else if (items == 2) launch_pair<DT, HP1, HP7, MV_RB, 2>(k, g, n1, n2, w, A, a, lda, c, ldc, st);
+    else launch_pair<DT, HP1, HP7, MV_RB, 4>(k, g, n1, n2, w, A, a, lda, c, ldc, st);
+    return hipGetLastError();
+}
+
 template <int DT>
 hipError_t gemv_grouped_dt(int flavour, const WeightView& w, const ActQ& A, const float* a, int lda, int k,
                                   const Groups& g, int E, int cap8, float* c, int ldc, hipStream_t st) {
     if (flavour == 2) return go_grouped<DT, 2, 8, 0>(k, g, cap8, w, A, nullptr, 0, c, ldc, st);
+    if (flavour == 3) {   // both F1 flavours in one launch, experts from g.counts: E = n1 columns, cap8 = n2
+        if (a == nullptr) return go_pair<DT, 0, 0>(k, g, E, cap8, w, A, nullptr, 0, c, ldc, st);
+        const int h1 = fuse_hp(1, k), h7 = fuse_hp(7, k);
+        if (h7 <= 1) return go_pair<DT, 1, 1>(k, g, E, cap8, w, A, a, lda, c, ldc, st);
+        if (h7 == 2) return h1 <= 1 ? go_pair<DT, 1, 2>(k, g, E, cap8, w, A, a, lda, c, ldc, st)
+                                    : go_pair<DT, 2, 2>(k, g, E, cap8, w, A, a, lda, c, ldc, st);
+        return h1 <= 1 ? go_pair<DT, 1, 4>(k, g, E, cap8, w, A, a, lda, c, ldc, st)
+                       : h1 == 2 ? go_pair<DT, 2, 4>(k, g, E, cap8, w, A, a, lda, c, ldc, st)
+                                 : go_pair<DT, 4, 4>(k, g, E, cap8, w, A, a, lda, c, ldc, st);
+    }
     if (flavour == 0) {   // one-row experts: one token's registers, LDS and prologue
         if (a == nullptr) return go_grouped<DT, 1, 1, 0>(k, g, E, w, A, nullptr, 0, c, ldc, st);
         const int hp = fuse_hp(1, k);

@@ -1029,8 +1029,12 @@ jamhip_status mm_grouped_ex_impl(jamhip_ctx* ctx, const void* w, int wt, int ldw
     }
     const float* af = fuse ? a : nullptr;
     const int laf = fuse ? lda : 0;
-    if ((e = launch_gemv_grouped(wt, 0, wv, A, af, laf, k, g1, n1, cap8, c, ldc, ctx->stream)) != hipSuccess ||
-        (n2 > 0 && (e = launch_gemv_grouped(wt, 1, wv, A, af, laf, k, g2, n2, cap8, c, ldc, ctx->stream)) != hipSuccess))
+    if (derive) {   // both flavours in one launch (n1 one-token columns, then n2 seven-token columns)
+        if ((e = launch_gemv_grouped(wt, 3, wv, A, af, laf, k, g1, n1, n2, c, ldc, ctx->stream)) != hipSuccess)
+            return hip_fail(ctx, e, "grouped: gemv launch");
+    } else if ((e = launch_gemv_grouped(wt, 0, wv, A, af, laf, k, g1, n1, cap8, c, ldc, ctx->stream)) != hipSuccess ||
+               (n2 > 0 &&
+                (e = launch_gemv_grouped(wt, 1, wv, A, af, laf, k, g2, n2, cap8, c, ldc, ctx->stream)) != hipSuccess))
         return hip_fail(ctx, e, "grouped: gemv launch");
     // fewer than 8 rows in all (decode-time MoE): no expert reaches the F2 bands, nothing more to launch
     if (rows_cap < 8) return JAMHIP_OK;

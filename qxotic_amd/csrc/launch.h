@@ -90,8 +90,9 @@ hipError_t launch_split_reduce(const float* part, int ns, int64_t slice, int m, 
 // columns) holding exactly one row / 2..7 rows (one-token / seven-token kernels; experts with other counts
 // are skipped), the kernel quantizing its expert's rows itself when `a` is non-null (then
 // gemv_grouped_fusable(k, a, lda) must hold), else reading them from A (CSR rows). flavour 2: the 8-token
-// tiles of map8 (experts with >= 8 rows), F2 activations from A (CSR rows). m here is the rows per expert
-// (g.gm).
+// tiles of map8 (experts with >= 8 rows), F2 activations from A (CSR rows). flavour 3: flavours 0 and 1 in
+// one launch with the experts taken from g.counts (E = the one-token columns, cap8 = the seven-token
+// columns). m here is the rows per expert (g.gm).
 bool gemv_grouped_fusable(int k, const float* a, int lda);
 hipError_t launch_gemv_grouped(int dt, int flavour, const WeightView& w, const ActQ& A, const float* a, int lda,
                                int k, const Groups& g, int E, int cap8, float* c, int ldc, hipStream_t st);
