@@ -506,12 +506,37 @@ def moe_leg(hip, torch, stream, steps: int = 10, no_graph: bool = False) -> dict
 
     dus, dus_stream = timed(dec_layer, NDEC, 8)
     assert bool(torch.isfinite(out[:1]).all()), "decode moe output not finite"
+    ref_h = h.clone()
+
+    def dec_layer_gf(i):   # the gather folded into the gate_up call (jamhip_mm_grouped_gather)
+        cg, cd, rd = wg[i % copies], wd[i % copies], res[i % NL]
+        ok = hip.moe_route(rd.data_ptr(), 1, TOPK, E, counts.data_ptr(), off.data_ptr(), slot_route.data_ptr(),
+                           route_slot.data_ptr()) == JAM.OK
+        ok &= hip.mm_grouped_gather(Segment.of(cg), JAM.MXFP4, D, FF, E, counts.data_ptr(), x.data_ptr(), D,
+                                    slot_route.data_ptr(), TOPK, h.data_ptr(), FF, D, TOPK) == JAM.OK
+        ok &= hip.mm_grouped(Segment.of(cd), JAM.MXFP4, D, D, E, counts.data_ptr(), hid.data_ptr(), D, y.data_ptr(),
+                             D, D, TOPK, None) == JAM.OK
+        ok &= hip.moe_combine(y.data_ptr(), D, rd.data_ptr(), prob.data_ptr(), route_slot.data_ptr(), 1, TOPK, E, D,
+                              out.data_ptr(), D) == JAM.OK
+        if not ok:
+            raise RuntimeError(hip.last_error())
+
+    dus_gf, _ = timed(dec_layer_gf, NDEC, 8)
+    dec_layer(NDEC - 1)
+    torch.cuda.synchronize()
+    ref_h.copy_(h)
+    dec_layer_gf(NDEC - 1)
+    torch.cuda.synchronize()
+    assert torch.equal(ref_h.view(torch.int32), h.view(torch.int32)), "decode gather-folded gate_up differs"
     dbytes = TOPK * (FF + D) * (D // 32) * 17
     decode = {"us_per_layer": round(dus, 1), "us_per_layer_stream": round(dus_stream, 1),
+              "us_per_layer_gather_folded": round(dus_gf, 1),
               "weights_GBs": round(dbytes / (dus * 1e-6) / 1e9, 1),
               "note": "1 token top-4 (a random expert set per layer), route + gather + two grouped calls + combine, "
                       "one captured graph of 200 layers (median of 3 replays; us_per_layer_stream: the same 200 "
-                      "layers launched on the stream); weights = 4 experts' gate_up + down (52.9 MB)"}
+                      "layers launched on the stream; us_per_layer_gather_folded: gate_up through "
+                      "jamhip_mm_grouped_gather, no gather launch, bit-identical); weights = 4 experts' gate_up + down "
+                      "(52.9 MB)"}
     # the same layer the way an unedited jinfer runs it through the host-pointer entry point: Moe.dispatch's host
     # loop (Moe.java:178-232) gathering each expert's rows, one jamhip_mm per expert and matrix on a row view of
     # the pinned stacked tensors (GptOss.java:677-717), the probability-weighted scatter on the host

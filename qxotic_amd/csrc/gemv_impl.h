@@ -447,8 +447,10 @@ template <int HP> struct APre { float x[HP][16]; };
 // wave's own dot products read, so the prologue needs no workgroup barrier.
 template <int HP> JAMHIP_DEV int pro_half(int i) { return 64 * HP * (int) (threadIdx.x >> 6) + 64 * i + (int) (threadIdx.x & 63); }
 
-template <int NT, int HP, int NWV>
-JAMHIP_DEV void a_load(APre<HP>& pre, const float* __restrict__ a, int lda, int k, int Gk, int ntv) {
+template <int NT, int HP, int NWV, bool GATHER = false>
+JAMHIP_DEV void a_load(APre<HP>& pre, const float* __restrict__ a, int lda, int k, int Gk, int ntv,
+                       const int* __restrict__ rows = nullptr, int rdiv = 1) {
+    // GATHER: token j's row is a[rows[j] / rdiv] (a grouped call with the gather folded in)
     // four 16-byte loads per half-block (the launcher checks a and lda for 16-byte alignment); a half past
     // the token's last element (a partial last group) re-reads the token's last half, zeroed by f1_store
     // (zeroing here would make the wave wait for these loads before issuing the weight loads). Only the
@@ -459,7 +461,8 @@ JAMHIP_DEV void a_load(APre<HP>& pre, const float* __restrict__ a, int lda, int 
         const int h0 = pro_half<HP>(i), h = h0 < total ? h0 : total - 1;
         const int j = NT == 1 ? 0 : h / halves, hh = h - j * halves, jr = j < ntv ? j : ntv - 1;   // rows past ntv: clamp
         const bool in = hh < kh;   // clamp only; the zeroing happens in f1_store
-        const float4* src = reinterpret_cast<const float4*>(a + (int64_t) jr * lda + 16 * (in ? hh : kh - 1));
+        const int64_t rj = GATHER ? (int64_t) (rows[jr] / rdiv) : (int64_t) jr;
+        const float4* src = reinterpret_cast<const float4*>(a + rj * lda + 16 * (in ? hh : kh - 1));
 #pragma unroll
         for (int v = 0; v < 4; v++) {
             const float4 f = src[v];

@@ -977,9 +977,11 @@ jamhip_status mm_grouped_ex_impl(jamhip_ctx* ctx, const void* w, int wt, int ldw
             return hip_fail(ctx, e, "grouped: gemm launch");
         return JAMHIP_OK;
     }
-    // Decode-sized calls (fewer than 8 rows in all, at most 64 experts, no offsets asked for, no gather): the F1
-    // kernels find their experts and rows from the counts themselves, so the offsets kernel does not run.
-    const bool derive = rows_cap < 8 && E <= 64 && offsets_dev == nullptr && x_rows == nullptr;
+    // Decode-sized calls (fewer than 8 rows in all, at most 64 experts, no offsets asked for; a gather only where
+    // the fused prologue reads the routed rows itself): the F1 kernels find their experts and rows from the
+    // counts, so neither the offsets kernel nor the gather runs.
+    const bool derive = rows_cap < 8 && E <= 64 && offsets_dev == nullptr &&
+                        (x_rows == nullptr || gemv_grouped_fusable(k, a, lda));   // a gather folds into the prologue
     if (!derive && (e = launch_moe_offsets((const int*) counts_dev, E, rows_cap, off, poff64, poff8, map64, cap64,
                                            map8, cap8, small, n1, n2, ctx->stream)) != hipSuccess)
         return hip_fail(ctx, e, "grouped: offsets launch");
@@ -988,7 +990,7 @@ jamhip_status mm_grouped_ex_impl(jamhip_ctx* ctx, const void* w, int wt, int ldw
             hipSuccess)
         return hip_fail(ctx, e, "grouped: offsets copy");
     if (rows_cap == 0) return JAMHIP_OK;
-    if (x_rows != nullptr) {   // the gathered rows, in CSR order, for the kernels below
+    if (x_rows != nullptr && !derive) {   // the gathered rows, in CSR order, for the kernels below
         if ((e = ctx->gath.ensure((size_t) rows_cap * k * sizeof(float))) != hipSuccess)
             return hip_fail(ctx, e, "grouped gather: scratch alloc");
         if ((e = launch_moe_gather(a, lda, x_rows, off, E, rows_cap, rdiv, k, (float*) ctx->gath.p, k, ctx->stream)) !=
@@ -1015,6 +1017,8 @@ jamhip_status mm_grouped_ex_impl(jamhip_ctx* ctx, const void* w, int wt, int ldw
         g1.counts = g2.counts = (const int*) counts_dev;
         g1.n_experts = g2.n_experts = E;
         g1.rows_cap = g2.rows_cap = rows_cap;
+        g1.rows = g2.rows = x_rows;   // null without a gather
+        g1.rdiv = g2.rdiv = rdiv;
     } else {
         g1.small = small;
         g2.small = small + n1;

@@ -38,6 +38,9 @@ struct Groups {
     // expert and rows from the device counts itself, with launch_moe_offsets' clamps to rows_cap
     const int* counts = nullptr;
     int n_experts = 0, rows_cap = 0;
+    // the gather folded in (F1 grouped kernels with the fused prologue): slot t's row is a[rows[t] / rdiv]
+    const int* rows = nullptr;
+    int rdiv = 1;
 };
 
 // Matrix-core GEMM workgroup -> linear tile; workgroup b runs on XCD b % 8. Ungrouped: each XCD takes one

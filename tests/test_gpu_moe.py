@@ -543,3 +543,51 @@ def test_select_topk_status_codes(hip):
     assert call(k=17) == 2                      # EUNSUPPORTED: topk above 16
     assert call(E=2000, ld=2000) == 2
     hip.synchronize()
+
+
+@pytest.mark.parametrize("dt", [O.MXFP4, O.Q4_K])
+def test_decode_sized_gather_folded(hip, oracle, dt):
+    """Decode-sized grouped calls with the gather folded in: the fused F1 prologue reads each slot's token row
+    through slot_route / topk itself (one-token and seven-token bodies: 3 tokens top-2 give experts of 1, 2 and
+    3 rows; 1 token top-4 gives four 1-row experts). Bit-identical to jamhip_moe_gather + jamhip_mm_grouped."""
+    import torch
+    from qxotic_amd.jam import JAM, Segment
+    m, k, E = 32, 512, 6
+    w_e = [oracle.quantize(dt, oracle.normal(0x6A7E + 5 * e + dt, (m, k), 0.0, 0.02)) for e in range(E)]
+    w = np.ascontiguousarray(np.concatenate(w_e, axis=0))
+    assert hip.pin(Segment.of(w), dt, k, E * m) == JAM.OK, hip.last_error()
+    try:
+        for re, topk in (([[1, 3], [3, 5], [1, 3]], 2), ([[4, 0, 2, 5]], 4)):
+            seq, R = len(re), len(re) * topk
+            say(f"decode-sized gather folded {O.NAMES[dt]} seq={seq} topk={topk}")
+            x = oracle.outliers(0x6A7F + seq, (seq, k))
+            i32 = lambda n: torch.zeros(n, dtype=torch.int32, device="cuda")
+            counts, off, slot_route, route_slot = i32(E), i32(E + 1), i32(R), i32(R)
+            re_d, x_d = dev(np.array(re, np.int32).ravel()), dev(x)
+            g = torch.zeros((R, k), dtype=torch.float32, device="cuda")
+            ca = torch.full((R + 1, m), -3.0, dtype=torch.float32, device="cuda")
+            cb = torch.full((R + 1, m), -3.0, dtype=torch.float32, device="cuda")
+            torch.cuda.synchronize()
+            assert hip.moe_route(re_d.data_ptr(), seq, topk, E, counts.data_ptr(), off.data_ptr(),
+                                 slot_route.data_ptr(), route_slot.data_ptr()) == JAM.OK, hip.last_error()
+            assert hip.moe_gather(x_d.data_ptr(), k, slot_route.data_ptr(), off.data_ptr(), E, seq, topk, k,
+                                  g.data_ptr(), k) == JAM.OK, hip.last_error()
+            assert hip.mm_grouped(Segment.of(w), dt, k, m, E, counts.data_ptr(), g.data_ptr(), k, ca.data_ptr(), m, k,
+                                  R) == JAM.OK, hip.last_error()
+            assert hip.mm_grouped_gather(Segment.of(w), dt, k, m, E, counts.data_ptr(), x_d.data_ptr(), k,
+                                         slot_route.data_ptr(), topk, cb.data_ptr(), m, k, R) == JAM.OK, hip.last_error()
+            hip.synchronize()
+            a_, b_ = ca.cpu().numpy(), cb.cpu().numpy()
+            assert np.array_equal(a_.view(np.uint32), b_.view(np.uint32))
+            assert (b_[R:] == -3.0).all()
+            cnt, ga = counts.cpu().numpy(), g.cpu().numpy()
+            o = 0
+            for e in range(E):
+                n = int(cnt[e])
+                if n:
+                    ref = oracle.mm_int8(dt, w_e[e], np.ascontiguousarray(ga[o:o + n]), m, n, k)
+                    _, sa = oracle.mm_ref(dt, w_e[e], np.ascontiguousarray(ga[o:o + n]), m, n, k)
+                    assert (np.abs(b_[o:o + n] - ref) <= 1e-3 * np.abs(ref) + 1e-5 * sa).all(), (e, n)
+                o += n
+    finally:
+        hip.evict(Segment.of(w))
